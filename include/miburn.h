@@ -1,0 +1,252 @@
+/*
+ * miburn.h -- the C ABI of the MI355X (gfx950) Burn-backend engine.
+ *
+ * One entry point per method of the reference's `Engine` trait that the hot
+ * path uses (crates/burn-tt/src/server.rs:42-788): the device engine that the
+ * Burn backend's server thread drives.  A Rust `-sys` crate binds these names
+ * one for one; the C++ and Python hosts in this repository bind them too.
+ *
+ * Conventions (mirroring the trait):
+ *  - A buffer is a row-major `[rows, cols]` matrix of one element kind, named
+ *    by a `mi_id` (the trait's `BufferId = u64`, server.rs:862).  Ids are
+ *    process-unique and never reused (server.rs:2421-2446).  Rank-N tensors
+ *    fold to `[prod(leading dims), last dim]` on the host, as the reference's
+ *    `stored_dims` does (crates/burn-tt/src/tensor.rs:905-908).
+ *  - Every call returns an `int` status: 0 on success, a negative `MI_E_*`
+ *    code otherwise, with a message in `mi_last_error`.  A call that fails
+ *    argument checks creates nothing.
+ *  - Work is stream-ordered and asynchronous on the context's one HIP
+ *    stream: an op returns its result id at once.  A failure found by a
+ *    kernel (an index out of range) is recorded and returned by the next
+ *    waiting call (`mi_sync`, a download), and the first such failure sticks
+ *    -- the trait's deferred `Ids.failed` (server.rs:2951-2991, 2390-2425).
+ *  - A context is used by one thread at a time (the reference serialises its
+ *    engine behind one server thread, server.rs:2886-2914); the library
+ *    takes a per-context lock so concurrent callers are serialised, not
+ *    undefined.
+ */
+#ifndef MIBURN_H
+#define MIBURN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mi_ctx mi_ctx;
+typedef uint64_t mi_id;
+
+/* Element kinds: the trait's `Elem` (server.rs:862 ff.).  I32 and Bool are
+ * 32-bit words (a Bool is 0 or 1), BF16 two-byte slots. */
+enum mi_elem { MI_F32 = 0, MI_I32 = 1, MI_BOOL = 2, MI_BF16 = 3 };
+
+/* Status codes.  `MI_E_DOMAIN` is the reference's DOMAIN error for an index
+ * out of range (crates/burn-tt/src/ops.rs:995-1000). */
+enum mi_status {
+  MI_OK = 0,
+  MI_E_ARG = -1,         /* bad argument: shape, kind, elem mismatch */
+  MI_E_ID = -2,          /* unknown or freed id (a stale tensor) */
+  MI_E_HIP = -3,         /* HIP runtime failure */
+  MI_E_OOM = -4,         /* device or pinned memory exhausted */
+  MI_E_DOMAIN = -5,      /* an index out of range, found by a kernel */
+  MI_E_UNSUPPORTED = -6, /* an op this engine does not run */
+  MI_E_STICKY = -7       /* an earlier asynchronous failure, not yet cleared */
+};
+
+/* ---- context: server.rs `attach` / `KmdEngine` (server.rs:2738, 4071) ---- */
+int mi_ctx_create(int device, mi_ctx **out);
+int mi_ctx_destroy(mi_ctx *ctx);
+/* The last message of this context (or of the process for a NULL ctx). */
+const char *mi_last_error(const mi_ctx *ctx);
+/* Wait for all submitted work; return the first asynchronous failure and
+ * clear it (`Backend::sync`, crates/burn-tt/src/lib.rs:218-226). */
+int mi_sync(mi_ctx *ctx);
+/* The HIP stream (`hipStream_t`) work is submitted on, for callers that
+ * order their own work with it. */
+int mi_stream(mi_ctx *ctx, void **stream);
+
+/* ---- storage: Engine::upload / upload_bits / upload_bf16 / download* /
+ *      free / metadata (server.rs:91-174) ---- */
+int mi_upload(mi_ctx *ctx, const float *values, int64_t rows, int64_t cols,
+              mi_id *out);
+int mi_upload_bits(mi_ctx *ctx, const uint32_t *bits, int64_t rows,
+                   int64_t cols, int elem, mi_id *out);
+int mi_upload_bf16(mi_ctx *ctx, const uint16_t *bits, int64_t rows,
+                   int64_t cols, mi_id *out);
+/* Read back `rows * cols` datums; `n` is the capacity of `out` in datums. */
+int mi_download(mi_ctx *ctx, mi_id id, float *out, int64_t n);
+int mi_download_bits(mi_ctx *ctx, mi_id id, uint32_t *out, int64_t n);
+int mi_download_bf16(mi_ctx *ctx, mi_id id, uint16_t *out, int64_t n);
+int mi_free(mi_ctx *ctx, mi_id id);
+int mi_metadata(mi_ctx *ctx, mi_id id, int64_t *rows, int64_t *cols,
+                int *elem);
+/* A fresh `[rows, cols]` buffer of `elem` filled with the 32-bit pattern
+ * `bits` (the low 16 bits for BF16): Engine::zeros_dram (server.rs:285). */
+int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits,
+            mi_id *out);
+
+/* ---- products: Engine::matmul_dram / matmul_dram_bf16 (server.rs:178-204)
+ * `op(A) @ op(B)`: `a` is `[m, k]` or, transposed, `[k, m]`; `b` is `[k, n]`
+ * or, transposed, `[n, k]`.  F32 or BF16 operands (either mix); BF16
+ * operands are multiplied exactly and accumulated in F32.  The result is F32,
+ * or BF16 rounded once, ties to even, when `out_elem` is MI_BF16. */
+int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
+              int b_transposed, int out_elem, mi_id *out);
+/* Engine::matmul_dram_batched (server.rs:229): `batch` products of one shape
+ * over stacked operands.  `a` holds `batch_a` matrices stacked by rows
+ * (`[batch_a * m, k]`, or `[batch_a * k, m]` transposed), `b` likewise; a
+ * stack of one is broadcast to every product.  The result stacks the
+ * products by rows: `[batch * m, n]`. */
+int mi_matmul_batched(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
+                      int b_transposed, int64_t batch, int64_t m, int64_t k,
+                      int64_t n, int out_elem, mi_id *out);
+
+/* ---- element-wise: Engine::eltwise_op_as (server.rs:519) ----
+ * `kind` is one of the MI_K_* ids below (the reference's op ids,
+ * crates/tt-kernels/src/kind.rs:11-27 and sfpu/ops.rs:24-250).  `b` and `c`
+ * are 0 when the op takes fewer operands.  Each operand is `[rows, cols]`,
+ * or broadcasts a `[1, cols]` row, a `[rows, 1]` column or a `[1, 1]` value
+ * over the output, which takes the largest extent of each axis.  F32 and BF16
+ * inputs are read as F32; the result is F32 (BF16 rounded once when
+ * `out_elem` is MI_BF16), or Bool for a comparison. */
+int mi_eltwise(mi_ctx *ctx, uint32_t kind, float scalar, float scalar2,
+               mi_id a, mi_id b, mi_id c, int out_elem, mi_id *out);
+
+/* Element-wise op ids (the reference's numbering). */
+enum mi_kind {
+  MI_K_ADD = 1, MI_K_SUB = 2, MI_K_MUL = 3, MI_K_MUL_SCALAR = 4,
+  MI_K_RELU = 5, MI_K_RELU_BACKWARD = 6, MI_K_ADD_ROW = 7,
+  MI_K_ADD_SCALAR = 11,
+  MI_K_RECIP = 0x100, MI_K_DIV = 0x101, MI_K_DIV_SCALAR = 0x102,
+  MI_K_EXP = 0x103, MI_K_LOG = 0x104,
+  MI_K_BOOL_NOT = 0x105, MI_K_BOOL_AND = 0x106, MI_K_BOOL_OR = 0x107,
+  MI_K_BOOL_XOR = 0x108,
+  MI_K_NEG = 0x109, MI_K_ABS = 0x10a, MI_K_SIGN = 0x10b,
+  MI_K_CLAMP = 0x10c, MI_K_CLAMP_MIN = 0x10d, MI_K_CLAMP_MAX = 0x10e,
+  MI_K_LEAKY_RELU = 0x10f, MI_K_HARD_SIGMOID = 0x110,
+  MI_K_EQ = 0x111, MI_K_NE = 0x112, MI_K_GT = 0x113, MI_K_GE = 0x114,
+  MI_K_LT = 0x115, MI_K_LE = 0x116,
+  MI_K_EQ_S = 0x117, MI_K_NE_S = 0x118, MI_K_GT_S = 0x119, MI_K_GE_S = 0x11a,
+  MI_K_LT_S = 0x11b, MI_K_LE_S = 0x11c,
+  MI_K_IS_NAN = 0x11d, MI_K_IS_INF = 0x11e,
+  MI_K_MASK_FILL = 0x11f, MI_K_MASK_WHERE = 0x120,
+  MI_K_FILL = 0x122, MI_K_SQRT = 0x123, MI_K_RSQRT = 0x124,
+  MI_K_LOG1P = 0x125, MI_K_POW = 0x126, MI_K_POW_S = 0x127,
+  MI_K_I32_TO_F32 = 0x129, MI_K_EXPM1 = 0x12a,
+  MI_K_SIGMOID = 0x12b, MI_K_SIGMOID_BACKWARD = 0x12c,
+  MI_K_TANH = 0x12d, MI_K_ERF = 0x12e,
+  MI_K_GELU = 0x12f, MI_K_GELU_BACKWARD = 0x130,
+  MI_K_SIN = 0x138, MI_K_COS = 0x139,
+  MI_K_BOOL_TO_F32 = 0x13f,
+  MI_K_ADD_RELU = 0x1f0, MI_K_SILU = 0x1f1, MI_K_SILU_MUL = 0x1f2,
+  MI_K_SUB_EXP = 0x1f3, MI_K_MUL_ADD = 0x1f4, MI_K_SCALE_MASK_FILL = 0x1f5,
+  /* Fused kinds of this engine, numbered above the reference's. */
+  MI_K_RSQRT_ABS_ADD = 0x200 /* 1 / sqrt(|a| + scalar) */
+};
+
+/* ---- reductions: Engine::reduce (server.rs:404), Engine::full_reduce ----
+ * `axis` MI_AXIS_ROWS reduces over rows (Burn dim 0): `[r, c] -> [1, c]`;
+ * MI_AXIS_COLS over columns (dim 1): `[r, c] -> [r, 1]`.  MI_R_MEAN is the
+ * sum divided by the count.  F32 or BF16 in, F32 out. */
+enum mi_reduce_op { MI_R_SUM = 0, MI_R_MAX = 1, MI_R_MEAN = 2, MI_R_MIN = 3 };
+enum mi_axis { MI_AXIS_ROWS = 0, MI_AXIS_COLS = 1 };
+int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out);
+/* The whole buffer to `[1, 1]` (float_sum / float_mean, ops.rs:3246-3400). */
+int mi_reduce_all(mi_ctx *ctx, mi_id a, int op, mi_id *out);
+
+/* ---- softmax: Engine::softmax_rows (server.rs:428) and the
+ * softmax/log_softmax composition (ops.rs:5133-5166) ----
+ * Over each row: `softmax(scale * x)` with entries where `mask` (a Bool
+ * `[mask_rows, cols]`, row `r % mask_rows` read for row `r`; 0 for none) is
+ * true set to -inf first.  With a mask the max is clamped below at -FLT_MAX
+ * and the sum at FLT_MIN, so a fully masked row gives zeros (ops.rs:
+ * 4572-4590).  `log` selects `(x - max) - ln(sum)` instead. */
+int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, int log,
+                    int out_elem, mi_id *out);
+
+/* ---- RMSNorm: Engine::rms_norm_as (server.rs:449) ----
+ * `a / sqrt(mean(a * a) + eps) * gamma` over each row; `gamma` a `[1, cols]`
+ * row or 0. */
+int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem,
+                mi_id *out);
+/* LayerNorm over each row, `(a - mean) / sqrt(var + eps) * gamma + beta`
+ * (Burn's `LayerNorm`, biased variance); gamma/beta `[1, cols]` or 0. */
+int mi_layer_norm(mi_ctx *ctx, mi_id a, mi_id gamma, mi_id beta, float eps,
+                  mi_id *out);
+
+/* ---- indexing (ops.rs:1001-1240) ---- */
+/* Engine::argmax_row (server.rs:477) over every row: `[r, c] -> [r, 1]` I32,
+ * the first maximum, a NaN ranking above every number. */
+int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out);
+/* Engine::select_rows (server.rs:300): `out[i, :] = table[idx[i], :]`, raw
+ * bits; `idx` an I32 buffer of any dims, read in row-major order.  An index
+ * outside `[0, table rows)` is an MI_E_DOMAIN failure. */
+int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out);
+/* Engine::pick_columns (server.rs:349): `out[r] = x[r, idx[r]]`, raw bits,
+ * `[r, 1]`. */
+int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out);
+/* The gather's backward (ops.rs:1043-1100): a copy of `x` with `v[r]` added
+ * at `[r, idx[r]]`. */
+int mi_scatter_add_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id v,
+                           mi_id *out);
+/* Engine::select_add_rows (server.rs:358): a copy of `t` with row `i` of
+ * `value` added to row `idx[i]`, duplicates folded in index order. */
+int mi_select_add_rows(mi_ctx *ctx, mi_id t, mi_id idx, mi_id value,
+                       mi_id *out);
+
+/* ---- layout: Engine::repack / copy_blocks (server.rs:269-284) ----
+ * A new `[rows, cols]` buffer whose element `(i, j)` is
+ * `src[offset + i * row_stride + j * col_stride]` (strides in elements):
+ * transposes, head splits and slices as one strided copy. */
+int mi_copy_strided(mi_ctx *ctx, mi_id src, int64_t rows, int64_t cols,
+                    int64_t offset, int64_t row_stride, int64_t col_stride,
+                    mi_id *out);
+/* A strided copy over a 4-D index space `[d0, d1, d2, d3]` (row-major
+ * output of `d0*d1*d2` rows by `d3` columns), source strides s0..s3: a
+ * `swap_dims`/`permute` materialised in one pass. */
+int mi_copy_strided4(mi_ctx *ctx, mi_id src, const int64_t dims[4],
+                     int64_t offset, const int64_t strides[4], mi_id *out);
+/* Write `src` into `dst` (in place) at rows `[row0, row0 + src rows)`,
+ * columns `[col0, col0 + src cols)`: a `slice_assign` (KV-cache writes). */
+int mi_assign_block(mi_ctx *ctx, mi_id dst, mi_id src, int64_t row0,
+                    int64_t col0);
+/* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
+ * a NaN; and I32 -> F32 (`as f32`). */
+int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);
+
+/* ---- random: Engine::random_dram (server.rs:768) with the draw's 64-bit
+ * base (crates/burn-tt/src/random.rs:42-56) ---- */
+enum mi_draw {
+  MI_DRAW_UNIT = 0,    /* [0, 1) */
+  MI_DRAW_UNIFORM = 1, /* [p1, p2) */
+  MI_DRAW_NORMAL = 2,  /* N(p1, p2^2) */
+  MI_DRAW_BERNOULLI = 3, /* 1 with probability p1, as F32 */
+  MI_DRAW_INT_RANGE = 4  /* integers in [p1, p2), I32 */
+};
+int mi_random(mi_ctx *ctx, int64_t rows, int64_t cols, int draw, float p1,
+              float p2, uint64_t base, mi_id *out);
+
+/* ---- timing on the context's stream (bench support; the reference's
+ * session profiler, session.rs:9811-9830) ---- */
+int mi_event_record(mi_ctx *ctx, int slot); /* slot in [0, 16) */
+int mi_event_elapsed_ms(mi_ctx *ctx, int from, int to, float *ms);
+
+/* ---- the op report (crates/burn-tt/src/report.rs:29-51) ---- */
+typedef struct mi_report {
+  uint64_t ops;            /* kernels submitted */
+  uint64_t uploads;        /* host-to-device copies */
+  uint64_t downloads;      /* device-to-host copies */
+  uint64_t bytes_up;       /* host-to-device bytes */
+  uint64_t bytes_down;     /* device-to-host bytes */
+  uint64_t live_buffers;   /* ids not yet freed */
+  uint64_t device_bytes;   /* bytes held by live buffers */
+  uint64_t cached_bytes;   /* bytes held by the allocator's free lists */
+} mi_report;
+int mi_get_report(mi_ctx *ctx, mi_report *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIBURN_H */

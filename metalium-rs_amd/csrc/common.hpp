@@ -1,0 +1,133 @@
+// Shared definitions of the MI355X engine: the context (device, stream,
+// buffer table, caching allocator, sticky error), element helpers and the
+// launch-check helpers every kernel file uses.
+//
+// The context restates the reference's device server state -- the buffer
+// table `DramBuffers` (crates/burn-tt/src/server.rs:868), the id counter that
+// never reuses an id (server.rs:2421-2446) and the first recorded failure
+// (server.rs:2390-2425) -- for a GPU driven through one HIP stream instead of
+// a server thread.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/miburn.h"
+
+namespace mi {
+
+// ---------------------------------------------------------------- elements
+inline size_t elem_size(int elem) { return elem == MI_BF16 ? 2 : 4; }
+inline bool elem_valid(int elem) { return elem >= MI_F32 && elem <= MI_BF16; }
+inline bool elem_float(int elem) { return elem == MI_F32 || elem == MI_BF16; }
+const char *elem_name(int elem);
+
+// BF16 <-> F32 on the device.  Narrowing rounds to nearest, ties to even, and
+// keeps a NaN a (quiet) NaN; widening is exact.
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// ------------------------------------------------------------------ buffers
+struct Buffer {
+  void *ptr = nullptr;
+  size_t bytes = 0;  // bytes the allocator handed out (>= datum bytes)
+  int64_t rows = 0, cols = 0;
+  int elem = MI_F32;
+  int64_t numel() const { return rows * cols; }
+};
+
+// Device error flags a kernel may raise; read back at the next wait.
+enum DeviceFlag : uint32_t { FLAG_INDEX_RANGE = 1u };
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex mu;
+
+  std::unordered_map<mi_id, Buffer> bufs;
+  // Caching allocator: exact rounded size -> free blocks.  One stream orders
+  // every use, so a block freed by the host is safe to hand out to the next
+  // op on the same stream.
+  std::map<size_t, std::vector<void *>> free_blocks;
+  size_t cached_bytes = 0, live_bytes = 0;
+
+  // Pinned staging ring for host transfers.
+  static constexpr int kStageSlots = 4;
+  static constexpr size_t kStageBytes = size_t(32) << 20;
+  void *stage[kStageSlots] = {};
+  hipEvent_t stage_done[kStageSlots] = {};
+  bool stage_pending[kStageSlots] = {};
+  int stage_next = 0;
+
+  uint32_t *dev_flags = nullptr;  // DeviceFlag bits, device memory
+
+  hipEvent_t events[16] = {};
+  std::string last_error;
+  int sticky = MI_OK;  // first asynchronous failure not yet reported
+  std::string sticky_msg;
+
+  mi_report report{};
+
+  // Scratch for multi-pass kernels (reductions' partials), grown on demand.
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+};
+
+// Status with a formatted message stored on the context.
+int fail(Ctx *ctx, int code, const char *fmt, ...);
+// Record a launch failure (hipGetLastError) for `what`; returns its status.
+int check_launch(Ctx *ctx, const char *what);
+
+// Buffer table.
+Buffer *lookup(Ctx *ctx, mi_id id);
+mi_id insert(Ctx *ctx, const Buffer &b);
+// A new buffer of `rows x cols` of `elem`; returns its id or 0 (status set).
+int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id,
+               Buffer **out);
+void *device_alloc(Ctx *ctx, size_t bytes, size_t *got);
+void device_release(Ctx *ctx, void *p, size_t bytes);
+void *scratch(Ctx *ctx, size_t bytes);
+
+// Kernel-side flag word for the context.
+inline uint32_t *flags(Ctx *ctx) { return ctx->dev_flags; }
+
+// Grid sizing: blocks to cover `n` items at `per_block`, capped.
+inline unsigned grid_for(int64_t n, int64_t per_block, int64_t cap = 1 << 20) {
+  int64_t g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g);
+}
+
+}  // namespace mi
+
+struct mi_ctx : mi::Ctx {};
+
+// Take the context's lock and validate it.
+#define MI_ENTER(ctx)                                                  \
+  if ((ctx) == nullptr) return MI_E_ARG;                               \
+  std::lock_guard<std::recursive_mutex> mi_guard_((ctx)->mu)
+
+// Look up id `id` into `Buffer *var`, failing with MI_E_ID.
+#define MI_BUF(ctx, var, id)                                           \
+  mi::Buffer *var = mi::lookup((ctx), (id));                           \
+  if (var == nullptr)                                                  \
+    return mi::fail((ctx), MI_E_ID, "unknown or freed buffer id %llu", \
+                    (unsigned long long)(id))

@@ -1,0 +1,524 @@
+// Element-wise ops, casts, fills and strided copies.
+//
+// Reference: the SFPU element-wise family -- op ids and meanings in
+// crates/tt-kernels/src/kind.rs:11-27 and crates/tt-kernels/src/sfpu/ops.rs:24-250,
+// entered through Engine::eltwise_op_as (crates/burn-tt/src/server.rs:519) and
+// the routing `device_op_as` (crates/burn-tt/src/ops.rs:1770) with its row,
+// column and scalar broadcasts (ops.rs:1830-1872); casts Engine::cast_float
+// (server.rs:128); layout copies Engine::repack / copy_blocks (server.rs:269-284).
+//
+// MI355X design: one grid-stride kernel per op id, HBM-bound.  The fast form
+// reads F32 operands as float4 (16-byte lanes, fully coalesced: a wavefront
+// moves 1 KiB per access), with each operand full, a broadcast row, a
+// broadcast column or a single value; anything else (BF16/Bool/I32 inputs,
+// ragged widths) takes the scalar form with per-operand strides.  Each op is
+// computed in F32 with IEEE round-to-nearest arithmetic and the HIP device
+// library's expf/logf/erff/tanhf.
+#include "common.hpp"
+
+namespace mi {
+
+// Operand addressing: element (i, j) of the output reads p[i * rs + j * cs].
+struct Opnd {
+  const void *p;
+  int64_t rs, cs;
+  int elem;
+  int mode;  // fast form: 0 full, 1 row broadcast, 2 column broadcast, 3 value
+};
+
+__device__ __forceinline__ float load_elem(const Opnd &o, int64_t idx) {
+  switch (o.elem) {
+    case MI_F32: return static_cast<const float *>(o.p)[idx];
+    case MI_BF16: return bf16_bits_to_f32(static_cast<const uint16_t *>(o.p)[idx]);
+    case MI_I32: return static_cast<float>(static_cast<const int32_t *>(o.p)[idx]);
+    default: return static_cast<float>(static_cast<const uint32_t *>(o.p)[idx]);  // Bool 0/1
+  }
+}
+
+__device__ __forceinline__ float sigmoid2(float x) {
+  // Two branches, so neither exponential overflows for large |x|.
+  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+  float e = expf(x);
+  return e / (1.0f + e);
+}
+
+__device__ __forceinline__ float clamp_min_flex(float a, float s) {
+  if (isnan(s)) return a;
+  return a > s ? a : s;  // a NaN `a` gives the scalar, equal values the scalar
+}
+__device__ __forceinline__ float clamp_max_flex(float a, float s) {
+  if (isnan(s)) return a;
+  return a < s ? a : s;
+}
+
+// The op for id K on one element; `a`, `b`, `c` the operands (0 if absent).
+template <uint32_t K>
+__device__ __forceinline__ float op(float a, float b, float c, float s1, float s2) {
+  constexpr float kInvSqrt2 = 0.70710678118654752440f;
+  constexpr float kInvSqrt2Pi = 0.39894228040143267794f;
+  if constexpr (K == MI_K_ADD || K == MI_K_ADD_ROW) return a + b;
+  else if constexpr (K == MI_K_SUB) return a - b;
+  else if constexpr (K == MI_K_MUL) return a * b;
+  else if constexpr (K == MI_K_MUL_SCALAR) return a * s1;
+  else if constexpr (K == MI_K_ADD_SCALAR) return a + s1;
+  else if constexpr (K == MI_K_RELU) return a > 0.0f ? a : 0.0f;
+  else if constexpr (K == MI_K_RELU_BACKWARD) return a > 0.0f ? b : 0.0f;
+  else if constexpr (K == MI_K_RECIP) return 1.0f / a;
+  else if constexpr (K == MI_K_DIV) return a / b;
+  else if constexpr (K == MI_K_DIV_SCALAR) return a / s1;
+  else if constexpr (K == MI_K_EXP) return expf(a);
+  else if constexpr (K == MI_K_LOG) return logf(a);
+  else if constexpr (K == MI_K_BOOL_NOT) return a == 0.0f ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_BOOL_AND) return (a != 0.0f && b != 0.0f) ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_BOOL_OR) return (a != 0.0f || b != 0.0f) ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_BOOL_XOR) return ((a != 0.0f) != (b != 0.0f)) ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_NEG) return __uint_as_float(__float_as_uint(a) ^ 0x80000000u);
+  else if constexpr (K == MI_K_ABS) return __uint_as_float(__float_as_uint(a) & 0x7fffffffu);
+  else if constexpr (K == MI_K_SIGN) return isnan(a) ? a : (a > 0.0f ? 1.0f : (a < 0.0f ? -1.0f : 0.0f));
+  else if constexpr (K == MI_K_CLAMP) return isnan(a) ? a : (a < s1 ? s1 : (a > s2 ? s2 : a));
+  else if constexpr (K == MI_K_CLAMP_MIN) return clamp_min_flex(a, s1);
+  else if constexpr (K == MI_K_CLAMP_MAX) return clamp_max_flex(a, s1);
+  else if constexpr (K == MI_K_LEAKY_RELU) return a >= 0.0f ? a : s1 * a;
+  else if constexpr (K == MI_K_HARD_SIGMOID) {
+    float t = __fadd_rn(__fmul_rn(s1, a), s2);
+    return isnan(t) ? t : (t < 0.0f ? 0.0f : (t > 1.0f ? 1.0f : t));
+  }
+  else if constexpr (K == MI_K_EQ) return a == b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_NE) return a != b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_GT) return a > b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_GE) return a >= b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_LT) return a < b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_LE) return a <= b ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_EQ_S) return a == s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_NE_S) return a != s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_GT_S) return a > s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_GE_S) return a >= s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_LT_S) return a < s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_LE_S) return a <= s1 ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_IS_NAN) return isnan(a) ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_IS_INF) return isinf(a) ? 1.0f : 0.0f;
+  else if constexpr (K == MI_K_MASK_FILL) return b != 0.0f ? s1 : a;
+  else if constexpr (K == MI_K_MASK_WHERE) return b != 0.0f ? c : a;
+  else if constexpr (K == MI_K_FILL) return s1;
+  else if constexpr (K == MI_K_SQRT) return __fsqrt_rn(a);
+  else if constexpr (K == MI_K_RSQRT) return __fdiv_rn(1.0f, __fsqrt_rn(a));
+  else if constexpr (K == MI_K_LOG1P) return log1pf(a);
+  else if constexpr (K == MI_K_POW) return powf(a, b);
+  else if constexpr (K == MI_K_POW_S) return powf(a, s1);
+  else if constexpr (K == MI_K_I32_TO_F32 || K == MI_K_BOOL_TO_F32) return a;
+  else if constexpr (K == MI_K_EXPM1) return expm1f(a);
+  else if constexpr (K == MI_K_SIGMOID) return sigmoid2(a);
+  else if constexpr (K == MI_K_SIGMOID_BACKWARD) return (b * a) * (1.0f - a);
+  else if constexpr (K == MI_K_TANH) return tanhf(a);
+  else if constexpr (K == MI_K_ERF) return erff(a);
+  else if constexpr (K == MI_K_GELU) return 0.5f * a * (1.0f + erff(a * kInvSqrt2));
+  else if constexpr (K == MI_K_GELU_BACKWARD) {
+    float cdf = 0.5f * (1.0f + erff(a * kInvSqrt2));
+    float pdf = kInvSqrt2Pi * expf(-0.5f * a * a);
+    return b * (cdf + a * pdf);
+  }
+  else if constexpr (K == MI_K_SIN) return sinf(a);
+  else if constexpr (K == MI_K_COS) return cosf(a);
+  else if constexpr (K == MI_K_ADD_RELU) { float t = a + b; return t > 0.0f ? t : 0.0f; }
+  else if constexpr (K == MI_K_SILU) return a * sigmoid2(a);
+  else if constexpr (K == MI_K_SILU_MUL) return (a * sigmoid2(a)) * b;
+  else if constexpr (K == MI_K_SUB_EXP) return expf(a - b);
+  else if constexpr (K == MI_K_MUL_ADD) return __fadd_rn(c, __fmul_rn(a, b));
+  else if constexpr (K == MI_K_SCALE_MASK_FILL) return b != 0.0f ? s2 : a * s1;
+  else if constexpr (K == MI_K_RSQRT_ABS_ADD) return __fdiv_rn(1.0f, __fsqrt_rn(fabsf(a) + s1));
+  else return __builtin_nanf("");
+}
+
+__device__ __forceinline__ void store_elem(void *out, int out_elem, int64_t idx, float v) {
+  if (out_elem == MI_F32) static_cast<float *>(out)[idx] = v;
+  else if (out_elem == MI_BF16) static_cast<uint16_t *>(out)[idx] = f32_to_bf16_bits(v);
+  else static_cast<uint32_t *>(out)[idx] = v != 0.0f ? 1u : 0u;  // Bool
+}
+
+// Fast form: F32 operands, the output width a multiple of 4, four lanes of
+// one row per thread per step.
+__device__ __forceinline__ float4 load4(const Opnd &o, int64_t flat, int64_t cols) {
+  const float *p = static_cast<const float *>(o.p);
+  switch (o.mode) {
+    case 0: return *reinterpret_cast<const float4 *>(p + flat);
+    case 1: return *reinterpret_cast<const float4 *>(p + (flat % cols));
+    case 2: { float v = p[flat / cols]; return make_float4(v, v, v, v); }
+    default: { float v = p[0]; return make_float4(v, v, v, v); }
+  }
+}
+
+template <uint32_t K, int NIN>
+__global__ void __launch_bounds__(256) ew_vec4(Opnd a, Opnd b, Opnd c, float s1, float s2,
+                                               void *out, int out_elem, int64_t n4, int64_t cols) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < n4; v += stride) {
+    const int64_t flat = v * 4;
+    float4 x = load4(a, flat, cols);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f), z = y;
+    if constexpr (NIN >= 2) y = load4(b, flat, cols);
+    if constexpr (NIN >= 3) z = load4(c, flat, cols);
+    float4 r;
+    r.x = op<K>(x.x, y.x, z.x, s1, s2);
+    r.y = op<K>(x.y, y.y, z.y, s1, s2);
+    r.z = op<K>(x.z, y.z, z.z, s1, s2);
+    r.w = op<K>(x.w, y.w, z.w, s1, s2);
+    if (out_elem == MI_F32) {
+      *reinterpret_cast<float4 *>(static_cast<float *>(out) + flat) = r;
+    } else if (out_elem == MI_BF16) {
+      uint2 h;
+      h.x = uint32_t(f32_to_bf16_bits(r.x)) | (uint32_t(f32_to_bf16_bits(r.y)) << 16);
+      h.y = uint32_t(f32_to_bf16_bits(r.z)) | (uint32_t(f32_to_bf16_bits(r.w)) << 16);
+      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = h;
+    } else {
+      uint4 m = make_uint4(r.x != 0.f, r.y != 0.f, r.z != 0.f, r.w != 0.f);
+      *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(out) + flat) = m;
+    }
+  }
+}
+
+template <uint32_t K, int NIN>
+__global__ void __launch_bounds__(256) ew_generic(Opnd a, Opnd b, Opnd c, float s1, float s2,
+                                                  void *out, int out_elem, int64_t n, int64_t cols) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int64_t i = e / cols, j = e - i * cols;
+    float x = load_elem(a, i * a.rs + j * a.cs);
+    float y = 0.f, z = 0.f;
+    if constexpr (NIN >= 2) y = load_elem(b, i * b.rs + j * b.cs);
+    if constexpr (NIN >= 3) z = load_elem(c, i * c.rs + j * c.cs);
+    store_elem(out, out_elem, e, op<K>(x, y, z, s1, s2));
+  }
+}
+
+// Operand count and output class of each op id; 0 operands = unknown id.
+struct KindInfo { int nin; bool bool_out; bool bool_in; };
+
+static KindInfo kind_info(uint32_t k) {
+  switch (k) {
+    case MI_K_ADD: case MI_K_SUB: case MI_K_MUL: case MI_K_ADD_ROW: case MI_K_RELU_BACKWARD:
+    case MI_K_DIV: case MI_K_POW: case MI_K_SIGMOID_BACKWARD: case MI_K_GELU_BACKWARD:
+    case MI_K_ADD_RELU: case MI_K_SILU_MUL: case MI_K_SUB_EXP:
+      return {2, false, false};
+    case MI_K_MASK_FILL: case MI_K_SCALE_MASK_FILL:
+      return {2, false, false};
+    case MI_K_MUL_ADD: case MI_K_MASK_WHERE:
+      return {3, false, false};
+    case MI_K_EQ: case MI_K_NE: case MI_K_GT: case MI_K_GE: case MI_K_LT: case MI_K_LE:
+      return {2, true, false};
+    case MI_K_BOOL_AND: case MI_K_BOOL_OR: case MI_K_BOOL_XOR:
+      return {2, true, true};
+    case MI_K_BOOL_NOT:
+      return {1, true, true};
+    case MI_K_EQ_S: case MI_K_NE_S: case MI_K_GT_S: case MI_K_GE_S: case MI_K_LT_S: case MI_K_LE_S:
+    case MI_K_IS_NAN: case MI_K_IS_INF:
+      return {1, true, false};
+    case MI_K_MUL_SCALAR: case MI_K_ADD_SCALAR: case MI_K_RELU: case MI_K_RECIP: case MI_K_DIV_SCALAR:
+    case MI_K_EXP: case MI_K_LOG: case MI_K_NEG: case MI_K_ABS: case MI_K_SIGN: case MI_K_CLAMP:
+    case MI_K_CLAMP_MIN: case MI_K_CLAMP_MAX: case MI_K_LEAKY_RELU: case MI_K_HARD_SIGMOID:
+    case MI_K_FILL: case MI_K_SQRT: case MI_K_RSQRT: case MI_K_LOG1P: case MI_K_POW_S:
+    case MI_K_I32_TO_F32: case MI_K_BOOL_TO_F32: case MI_K_EXPM1: case MI_K_SIGMOID: case MI_K_TANH:
+    case MI_K_ERF: case MI_K_GELU: case MI_K_SIN: case MI_K_COS: case MI_K_SILU: case MI_K_RSQRT_ABS_ADD:
+      return {1, false, false};
+    default:
+      return {0, false, false};
+  }
+}
+
+#define MI_KIND_LIST(X)                                                                         \
+  X(MI_K_ADD) X(MI_K_SUB) X(MI_K_MUL) X(MI_K_MUL_SCALAR) X(MI_K_RELU) X(MI_K_RELU_BACKWARD)      \
+  X(MI_K_ADD_ROW) X(MI_K_ADD_SCALAR) X(MI_K_RECIP) X(MI_K_DIV) X(MI_K_DIV_SCALAR) X(MI_K_EXP)   \
+  X(MI_K_LOG) X(MI_K_BOOL_NOT) X(MI_K_BOOL_AND) X(MI_K_BOOL_OR) X(MI_K_BOOL_XOR) X(MI_K_NEG)    \
+  X(MI_K_ABS) X(MI_K_SIGN) X(MI_K_CLAMP) X(MI_K_CLAMP_MIN) X(MI_K_CLAMP_MAX) X(MI_K_LEAKY_RELU) \
+  X(MI_K_HARD_SIGMOID) X(MI_K_EQ) X(MI_K_NE) X(MI_K_GT) X(MI_K_GE) X(MI_K_LT) X(MI_K_LE)        \
+  X(MI_K_EQ_S) X(MI_K_NE_S) X(MI_K_GT_S) X(MI_K_GE_S) X(MI_K_LT_S) X(MI_K_LE_S) X(MI_K_IS_NAN)  \
+  X(MI_K_IS_INF) X(MI_K_MASK_FILL) X(MI_K_MASK_WHERE) X(MI_K_FILL) X(MI_K_SQRT) X(MI_K_RSQRT)   \
+  X(MI_K_LOG1P) X(MI_K_POW) X(MI_K_POW_S) X(MI_K_I32_TO_F32) X(MI_K_EXPM1) X(MI_K_SIGMOID)      \
+  X(MI_K_SIGMOID_BACKWARD) X(MI_K_TANH) X(MI_K_ERF) X(MI_K_GELU) X(MI_K_GELU_BACKWARD)          \
+  X(MI_K_SIN) X(MI_K_COS) X(MI_K_BOOL_TO_F32) X(MI_K_ADD_RELU) X(MI_K_SILU) X(MI_K_SILU_MUL)    \
+  X(MI_K_SUB_EXP) X(MI_K_MUL_ADD) X(MI_K_SCALE_MASK_FILL) X(MI_K_RSQRT_ABS_ADD)
+
+template <uint32_t K>
+static void launch_kind(bool fast, int nin, const Opnd &a, const Opnd &b, const Opnd &c, float s1,
+                        float s2, void *out, int out_elem, int64_t n, int64_t cols, hipStream_t st) {
+  const int threads = 256;
+  if (fast) {
+    const int64_t n4 = n / 4;
+    unsigned g = grid_for(n4, threads * 4, 256 * 32);
+    if (nin == 1) ew_vec4<K, 1><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+    else if (nin == 2) ew_vec4<K, 2><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+    else ew_vec4<K, 3><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+  } else {
+    unsigned g = grid_for(n, threads * 4, 256 * 32);
+    if (nin == 1) ew_generic<K, 1><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n, cols);
+    else if (nin == 2) ew_generic<K, 2><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n, cols);
+    else ew_generic<K, 3><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n, cols);
+  }
+}
+
+// Describe operand `x` against output dims; false if it does not broadcast.
+static bool describe(const Buffer *x, int64_t R, int64_t C, Opnd *o) {
+  o->p = x->ptr;
+  o->elem = x->elem;
+  const bool full_r = x->rows == R, full_c = x->cols == C;
+  if (!(full_r || x->rows == 1) || !(full_c || x->cols == 1)) return false;
+  o->rs = (x->rows == 1 && R != 1) ? 0 : x->cols;
+  o->cs = (x->cols == 1 && C != 1) ? 0 : 1;
+  if (x->rows == R && x->cols == C) o->mode = 0;
+  else if (x->rows == 1 && x->cols == C) o->mode = 1;
+  else if (x->rows == R && x->cols == 1) o->mode = 2;
+  else o->mode = 3;
+  if (x->rows == 1 && x->cols == 1) o->mode = 3;
+  return true;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_eltwise(mi_ctx *ctx, uint32_t kind, float scalar, float scalar2, mi_id a, mi_id b,
+                          mi_id c, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  KindInfo info = kind_info(kind);
+  if (info.nin == 0) return fail(ctx, MI_E_UNSUPPORTED, "element-wise op id %#x is not supported", kind);
+  const Buffer *ops[3] = {nullptr, nullptr, nullptr};
+  mi_id ids[3] = {a, b, c};
+  for (int i = 0; i < 3; ++i) {
+    if (i < info.nin) {
+      ops[i] = lookup(ctx, ids[i]);
+      if (!ops[i]) return fail(ctx, MI_E_ID, "op %#x: operand %d: unknown buffer id %llu", kind, i, (unsigned long long)ids[i]);
+    } else if (ids[i] != 0) {
+      return fail(ctx, MI_E_ARG, "op %#x takes %d operand(s)", kind, info.nin);
+    }
+  }
+  int64_t R = 1, C = 1;
+  for (int i = 0; i < info.nin; ++i) {
+    R = std::max(R, ops[i]->rows);
+    C = std::max(C, ops[i]->cols);
+    if (ops[i]->rows == 0) R = 0;
+    if (ops[i]->cols == 0) C = 0;
+  }
+  Opnd od[3] = {};
+  for (int i = 0; i < info.nin; ++i) {
+    if (!describe(ops[i], R, C, &od[i]))
+      return fail(ctx, MI_E_ARG, "op %#x: operand %d [%lld, %lld] does not broadcast to [%lld, %lld]", kind, i,
+                  (long long)ops[i]->rows, (long long)ops[i]->cols, (long long)R, (long long)C);
+  }
+  // Element kinds: the mask operand of MASK_FILL/MASK_WHERE/SCALE_MASK_FILL is Bool;
+  // Bool ops take Bool; everything else takes F32/BF16 (I32 for I32_TO_F32).
+  for (int i = 0; i < info.nin; ++i) {
+    int e = ops[i]->elem;
+    bool mask_slot = (i == 1) && (kind == MI_K_MASK_FILL || kind == MI_K_MASK_WHERE || kind == MI_K_SCALE_MASK_FILL);
+    bool ok;
+    if (info.bool_in) ok = e == MI_BOOL;
+    else if (mask_slot) ok = e == MI_BOOL;
+    else if (kind == MI_K_I32_TO_F32) ok = e == MI_I32;
+    else if (kind == MI_K_BOOL_TO_F32) ok = e == MI_BOOL;
+    else ok = elem_float(e);
+    if (!ok) return fail(ctx, MI_E_ARG, "op %#x: operand %d is %s", kind, i, elem_name(e));
+  }
+  int oe = info.bool_out ? MI_BOOL : out_elem;
+  if (!info.bool_out && oe != MI_F32 && oe != MI_BF16)
+    return fail(ctx, MI_E_ARG, "op %#x: result kind %s", kind, elem_name(oe));
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, C, oe, &id, &ob);
+  if (s) return s;
+  const int64_t n = R * C;
+  if (n > 0) {
+    bool fast = (C % 4 == 0);
+    for (int i = 0; i < info.nin; ++i) {
+      if (ops[i]->elem != MI_F32) fast = false;
+      // A value of one element per row must be 4-aligned to be read as float4 only in mode 0/1.
+    }
+    switch (kind) {
+#define MI_CASE(K) case K: launch_kind<K>(fast, info.nin, od[0], od[1], od[2], scalar, scalar2, ob->ptr, oe, n, C, ctx->stream); break;
+      MI_KIND_LIST(MI_CASE)
+#undef MI_CASE
+      default: break;
+    }
+    s = check_launch(ctx, "eltwise");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+// ------------------------------------------------------------------ fills
+namespace mi {
+__global__ void fill32(uint32_t *p, int64_t n, uint32_t bits) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = bits;
+}
+__global__ void fill16(uint16_t *p, int64_t n, uint16_t bits) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = bits;
+}
+}  // namespace mi
+
+extern "C" int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  mi_id id; Buffer *b;
+  int s = new_buffer(ctx, rows, cols, elem, &id, &b);
+  if (s) return s;
+  int64_t n = rows * cols;
+  if (n > 0) {
+    unsigned g = grid_for(n, 256 * 4, 256 * 32);
+    if (elem == MI_BF16) fill16<<<g, 256, 0, ctx->stream>>>(static_cast<uint16_t *>(b->ptr), n, uint16_t(bits));
+    else fill32<<<g, 256, 0, ctx->stream>>>(static_cast<uint32_t *>(b->ptr), n, bits);
+    s = check_launch(ctx, "fill");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+// ------------------------------------------------------------------ casts
+namespace mi {
+__global__ void cast_kernel(const void *src, int se, void *dst, int de, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float v;
+    if (se == MI_F32) v = static_cast<const float *>(src)[i];
+    else if (se == MI_BF16) v = bf16_bits_to_f32(static_cast<const uint16_t *>(src)[i]);
+    else if (se == MI_I32) v = static_cast<float>(static_cast<const int32_t *>(src)[i]);
+    else v = static_cast<float>(static_cast<const uint32_t *>(src)[i]);
+    if (de == MI_F32) static_cast<float *>(dst)[i] = v;
+    else if (de == MI_BF16) static_cast<uint16_t *>(dst)[i] = f32_to_bf16_bits(v);
+    else if (de == MI_BOOL) static_cast<uint32_t *>(dst)[i] = v != 0.0f ? 1u : 0u;
+    else {
+      // F32 -> I32 truncates toward zero, saturating (Rust's `as i32`); a NaN gives 0.
+      int32_t r;
+      if (isnan(v)) r = 0;
+      else if (v >= 2147483648.0f) r = 2147483647;
+      else if (v < -2147483648.0f) r = -2147483647 - 1;
+      else r = static_cast<int32_t>(v);
+      static_cast<int32_t *>(dst)[i] = r;
+    }
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, src, a);
+  if (!elem_valid(out_elem)) return fail(ctx, MI_E_ARG, "cast to unknown kind %d", out_elem);
+  int64_t rows = src->rows, cols = src->cols;
+  int se = src->elem;
+  const void *sp = src->ptr;
+  mi_id id; Buffer *b;
+  int s = new_buffer(ctx, rows, cols, out_elem, &id, &b);
+  if (s) return s;
+  int64_t n = rows * cols;
+  if (n > 0) {
+    if (se == out_elem) {
+      (void)hipMemcpyAsync(b->ptr, sp, n * elem_size(se), hipMemcpyDeviceToDevice, ctx->stream);
+    } else {
+      cast_kernel<<<grid_for(n, 256 * 4, 256 * 32), 256, 0, ctx->stream>>>(sp, se, b->ptr, out_elem, n);
+    }
+    s = check_launch(ctx, "cast");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+// --------------------------------------------------------- strided copies
+namespace mi {
+template <typename T>
+__global__ void copy4_kernel(const T *src, T *dst, int64_t d1, int64_t d2, int64_t d3, int64_t n, int64_t off,
+                             int64_t s0, int64_t s1, int64_t s2, int64_t s3) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    int64_t i3 = e % d3, r = e / d3;
+    int64_t i2 = r % d2; r /= d2;
+    int64_t i1 = r % d1, i0 = r / d1;
+    dst[e] = src[off + i0 * s0 + i1 * s1 + i2 * s2 + i3 * s3];
+  }
+}
+
+static int copy4(Ctx *ctx, mi_id srcid, const int64_t dims[4], int64_t offset, const int64_t strides[4], mi_id *out) {
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, src, srcid);
+  int64_t n = 1;
+  for (int i = 0; i < 4; ++i) {
+    if (dims[i] < 0) return fail(ctx, MI_E_ARG, "negative copy extent");
+    n *= dims[i];
+  }
+  // Bounds of the addressed range: every element read lies in the source.
+  if (n > 0) {
+    int64_t lo = offset, hi = offset;
+    for (int i = 0; i < 4; ++i) {
+      int64_t span = (dims[i] - 1) * strides[i];
+      if (span < 0) lo += span; else hi += span;
+    }
+    if (lo < 0 || hi >= src->numel())
+      return fail(ctx, MI_E_ARG, "strided copy reads [%lld, %lld] of a %lld-element buffer", (long long)lo,
+                  (long long)hi, (long long)src->numel());
+  }
+  const void *sp = src->ptr;
+  int se = src->elem;
+  mi_id id; Buffer *b;
+  int s = new_buffer(ctx, dims[0] * dims[1] * dims[2], dims[3], se, &id, &b);
+  if (s) return s;
+  if (n > 0) {
+    unsigned g = grid_for(n, 256 * 4, 256 * 32);
+    if (se == MI_BF16)
+      copy4_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(sp), static_cast<uint16_t *>(b->ptr),
+                                                        dims[1], dims[2], dims[3], n, offset, strides[0], strides[1], strides[2], strides[3]);
+    else
+      copy4_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(sp), static_cast<uint32_t *>(b->ptr),
+                                                        dims[1], dims[2], dims[3], n, offset, strides[0], strides[1], strides[2], strides[3]);
+    s = check_launch(ctx, "copy_strided");
+    if (s) { mi_free(static_cast<mi_ctx *>(ctx), id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+template <typename T>
+__global__ void assign_kernel(T *dst, int64_t dcols, const T *src, int64_t rows, int64_t cols, int64_t r0, int64_t c0) {
+  const int64_t n = rows * cols;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    int64_t i = e / cols, j = e - i * cols;
+    dst[(r0 + i) * dcols + c0 + j] = src[e];
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_copy_strided(mi_ctx *ctx, mi_id src, int64_t rows, int64_t cols, int64_t offset, int64_t row_stride,
+                               int64_t col_stride, mi_id *out) {
+  MI_ENTER(ctx);
+  int64_t dims[4] = {1, 1, rows, cols};
+  int64_t strides[4] = {0, 0, row_stride, col_stride};
+  return copy4(ctx, src, dims, offset, strides, out);
+}
+
+extern "C" int mi_copy_strided4(mi_ctx *ctx, mi_id src, const int64_t dims[4], int64_t offset, const int64_t strides[4],
+                                mi_id *out) {
+  MI_ENTER(ctx);
+  if (!dims || !strides) return fail(ctx, MI_E_ARG, "null dims or strides");
+  return copy4(ctx, src, dims, offset, strides, out);
+}
+
+extern "C" int mi_assign_block(mi_ctx *ctx, mi_id dst, mi_id src, int64_t row0, int64_t col0) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, d, dst);
+  MI_BUF(ctx, s, src);
+  if (d->elem != s->elem) return fail(ctx, MI_E_ARG, "assign of %s into %s", elem_name(s->elem), elem_name(d->elem));
+  if (row0 < 0 || col0 < 0 || row0 + s->rows > d->rows || col0 + s->cols > d->cols)
+    return fail(ctx, MI_E_ARG, "block [%lld, %lld] at (%lld, %lld) outside [%lld, %lld]", (long long)s->rows,
+                (long long)s->cols, (long long)row0, (long long)col0, (long long)d->rows, (long long)d->cols);
+  int64_t n = s->numel();
+  if (n == 0) return MI_OK;
+  unsigned g = grid_for(n, 256 * 4, 256 * 32);
+  if (d->elem == MI_BF16)
+    assign_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<uint16_t *>(d->ptr), d->cols,
+                                                       static_cast<const uint16_t *>(s->ptr), s->rows, s->cols, row0, col0);
+  else
+    assign_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<uint32_t *>(d->ptr), d->cols,
+                                                       static_cast<const uint32_t *>(s->ptr), s->rows, s->cols, row0, col0);
+  return check_launch(ctx, "assign_block");
+}

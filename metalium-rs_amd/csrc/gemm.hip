@@ -1,0 +1,500 @@
+// Matrix products on the gfx950 matrix cores (MFMA).
+//
+// Reference: Engine::matmul_dram / matmul_dram_bf16 / matmul_dram_batched
+// (crates/burn-tt/src/server.rs:178-239) over Session::matmul_dram_as and
+// matmul_dram_batched (crates/tt-kernels/src/session.rs:8990, 9415); the routing
+// `float_matmul` / `batched_matmul` (crates/burn-tt/src/ops.rs:2833-3052), where
+// a transposed operand is a view, not a copy; BF16 products accumulated in F32
+// and rounded once (crates/burn-tt/src/ops/rounded.rs:75-120).
+//
+// MI355X design
+//  * One kernel template for both precisions.  BF16 x BF16 runs
+//    v_mfma_f32_32x32x16_bf16 (each lane supplies 8 consecutive k of one row
+//    of A and one column of B); anything with an F32 operand runs
+//    v_mfma_f32_32x32x2f32 in full F32 (BF16 operands widen exactly).
+//  * Operand tiles live in LDS as [rows][k] with 128-byte rows (64 BF16 or 32
+//    F32 of k) and a 16-byte-chunk XOR swizzle (chunk c of row r stored at
+//    c ^ (r & 7)), so the MFMA fragment reads (one 16-byte chunk per lane, 32
+//    consecutive rows per half-wave) and the tile writes are conflict-free.
+//  * An operand whose k is contiguous in HBM (A as [m, k], a transposed B as
+//    [n, k]) is copied chunk by chunk; one whose m/n is contiguous (A
+//    transposed, B as [k, n]) is read as 8x8 (BF16) or 4x4 (F32) blocks and
+//    transposed in registers before its LDS write.  Transposed operands are
+//    never materialised.
+//  * Two LDS stages: the next k-tile's global loads are issued before the
+//    current tile's MFMAs, written to the other stage after them, one barrier
+//    per k-tile.
+//  * Tile order is XCD-aware: MI355X deals workgroups round-robin over its 8
+//    XCDs (each with its own L2), so consecutive workgroup ids are remapped
+//    so that each XCD owns a compact group of output tiles sharing A rows and
+//    B columns.
+//  * Shapes that are not multiples of the tile take a guarded variant
+//    (zero-filled loads, masked stores) of the same kernel.
+#include "common.hpp"
+
+namespace mi {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Element types: uint16_t carries BF16 bits, float is F32.
+template <typename T> struct Elt;
+template <> struct Elt<uint16_t> { static constexpr int CH = 8; };  // elements per 16-byte chunk
+template <> struct Elt<float> { static constexpr int CH = 4; };
+
+__device__ __forceinline__ float to_f32(uint16_t h) { return bf16_bits_to_f32(h); }
+__device__ __forceinline__ float to_f32(float f) { return f; }
+
+// Convert one element of the source type S to the MFMA operand type T.
+template <typename T, typename S> __device__ __forceinline__ T conv(S v);
+template <> __device__ __forceinline__ uint16_t conv<uint16_t, uint16_t>(uint16_t v) { return v; }
+template <> __device__ __forceinline__ float conv<float, float>(float v) { return v; }
+template <> __device__ __forceinline__ float conv<float, uint16_t>(uint16_t v) { return bf16_bits_to_f32(v); }
+
+// A 16-byte chunk of T.
+union Chunk {
+  uint4 u;
+  uint16_t h[8];
+  float f[4];
+};
+
+// Load CH consecutive elements of S starting at p and convert to one chunk of T.
+template <typename T, typename S>
+__device__ __forceinline__ Chunk load_chunk(const S *p) {
+  Chunk c;
+  if constexpr (sizeof(S) == sizeof(T)) {
+    c.u = *reinterpret_cast<const uint4 *>(p);
+  } else {  // BF16 source widened to F32: 4 elements = 8 bytes
+    uint2 v = *reinterpret_cast<const uint2 *>(p);
+    c.f[0] = __uint_as_float(v.x << 16);
+    c.f[1] = __uint_as_float(v.x & 0xffff0000u);
+    c.f[2] = __uint_as_float(v.y << 16);
+    c.f[3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+  return c;
+}
+
+// Guarded form: element e of the chunk read only if e < valid and the chunk is in range.
+template <typename T, typename S>
+__device__ __forceinline__ Chunk load_chunk_guard(const S *p, int valid) {
+  constexpr int CH = Elt<T>::CH;
+  Chunk c;
+  c.u = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    if (e < valid) {
+      if constexpr (sizeof(T) == 2) c.h[e] = conv<T, S>(p[e]);
+      else c.f[e] = conv<T, S>(p[e]);
+    }
+  }
+  return c;
+}
+
+// Swizzled LDS byte offset of chunk c of row r (128-byte rows).
+__device__ __forceinline__ int lds_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+// Per-operand tile loader.  ROWS = tile rows (m or n); the k extent is 128
+// bytes of T.  KCONTIG: source element (r, k) at src[r * ld + k]; otherwise at
+// src[k * ld + r].
+template <typename T, typename S, int ROWS, int NT, bool KCONTIG, bool GUARD>
+struct TileLoader {
+  static constexpr int CH = Elt<T>::CH;
+  static constexpr int BK = 128 / sizeof(T);
+  static constexpr int KCH = BK / CH;  // 8 chunks per LDS row
+  static_assert(KCH == 8, "128-byte LDS rows");
+  // KCONTIG: chunks per thread; else CHxCH blocks per thread (CH chunks each).
+  // A thread whose index runs past the tile's last chunk or block idles.
+  static constexpr int TOTAL_CHUNKS = ROWS * KCH;
+  static constexpr int TOTAL_BLKS = (ROWS / CH) * KCH;
+  static constexpr int NCHUNK = (TOTAL_CHUNKS + NT - 1) / NT;
+  static constexpr int NBLK = (TOTAL_BLKS + NT - 1) / NT;
+  static constexpr bool CHUNK_EVEN = TOTAL_CHUNKS % NT == 0;
+  static constexpr bool BLK_EVEN = TOTAL_BLKS % NT == 0;
+  static constexpr int NREG = KCONTIG ? NCHUNK : NBLK * CH;
+  static_assert(ROWS % CH == 0, "tile rows a multiple of the chunk");
+  Chunk reg[NREG];
+
+  // Load the k-tile starting at k0 for tile rows starting at r0.
+  __device__ __forceinline__ void load(const S *src, int64_t ld, int64_t r0, int64_t k0, int64_t rows_total,
+                                       int64_t k_total, int tid) {
+    if constexpr (KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < NCHUNK; ++i) {
+        const int q = tid + i * NT;
+        if (!CHUNK_EVEN && q >= TOTAL_CHUNKS) break;
+        const int r = q / KCH, c = q % KCH;
+        const int64_t gr = r0 + r, gk = k0 + c * CH;
+        const S *p = src + gr * ld + gk;
+        if constexpr (GUARD) {
+          int valid = (gr < rows_total) ? static_cast<int>(k_total - gk) : 0;
+          valid = valid < 0 ? 0 : (valid > CH ? CH : valid);
+          // Vector path only when the whole chunk is in range and aligned.
+          if (valid == CH && ((reinterpret_cast<uintptr_t>(p) & (sizeof(S) * CH - 1)) == 0))
+            reg[i] = load_chunk<T, S>(p);
+          else
+            reg[i] = load_chunk_guard<T, S>(p, valid);
+        } else {
+          reg[i] = load_chunk<T, S>(p);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) {
+        const int q = tid + b * NT;
+        if (!BLK_EVEN && q >= TOTAL_BLKS) break;
+        const int kb = q % KCH, rb = q / KCH;
+        Chunk in[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const int64_t gk = k0 + kb * CH + i, gr = r0 + rb * CH;
+          const S *p = src + gk * ld + gr;
+          if constexpr (GUARD) {
+            int valid = (gk < k_total) ? static_cast<int>(rows_total - gr) : 0;
+            valid = valid < 0 ? 0 : (valid > CH ? CH : valid);
+            if (valid == CH && ((reinterpret_cast<uintptr_t>(p) & (sizeof(S) * CH - 1)) == 0))
+              in[i] = load_chunk<T, S>(p);
+            else
+              in[i] = load_chunk_guard<T, S>(p, valid);
+          } else {
+            in[i] = load_chunk<T, S>(p);
+          }
+        }
+        // Transpose the CH x CH block: out[j] holds k = 0..CH-1 of row j.
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          Chunk o;
+          if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const uint32_t lo = reinterpret_cast<const uint32_t *>(&in[2 * m].u)[j >> 1];
+              const uint32_t hi = reinterpret_cast<const uint32_t *>(&in[2 * m + 1].u)[j >> 1];
+              reinterpret_cast<uint32_t *>(&o.u)[m] =
+                  (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) o.f[m] = in[m].f[j];
+          }
+          reg[b * CH + j] = o;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(char *lds, int tid) const {
+    if constexpr (KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < NCHUNK; ++i) {
+        const int q = tid + i * NT;
+        if (!CHUNK_EVEN && q >= TOTAL_CHUNKS) break;
+        const int r = q / KCH, c = q % KCH;
+        *reinterpret_cast<uint4 *>(lds + lds_off(r, c)) = reg[i].u;
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NBLK; ++b) {
+        const int q = tid + b * NT;
+        if (!BLK_EVEN && q >= TOTAL_BLKS) break;
+        const int kb = q % KCH, rb = q / KCH;
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+          *reinterpret_cast<uint4 *>(lds + lds_off(rb * CH + j, kb)) = reg[b * CH + j].u;
+      }
+    }
+  }
+};
+
+struct GemmArgs {
+  const void *a;
+  const void *b;
+  void *c;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sa, sb, sc;  // batch strides in elements (0 = broadcast)
+  int tiles_m, tiles_n;
+};
+
+// Map a linear workgroup id to an output tile (tm, tn), grouping the tiles
+// each XCD receives.  Workgroup w runs on XCD w % 8.
+__device__ __forceinline__ void tile_of(int w, int tiles_m, int tiles_n, int *tm, int *tn) {
+  const int total = tiles_m * tiles_n;
+  int t = w;
+  if ((total & 7) == 0) t = (w & 7) * (total >> 3) + (w >> 3);
+  // Within the XCD-ordered sequence, walk groups of GROUP_M tile rows.
+  constexpr int GROUP_M = 4;
+  const int group_size = GROUP_M * tiles_n;
+  const int g = t / group_size;
+  const int first_m = g * GROUP_M;
+  const int gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  const int in_g = t - g * group_size;
+  *tm = first_m + in_g % gm;
+  *tn = in_g / gm;
+}
+
+template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC,
+          bool GUARD>
+__global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 128 / sizeof(T);
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA tiles per wave
+  static_assert(TM >= 1 && TN >= 1, "wave tile");
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t z = blockIdx.y;
+  const SA *A = static_cast<const SA *>(g.a) + z * g.sa;
+  const SB *B = static_cast<const SB *>(g.b) + z * g.sb;
+  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+
+  TileLoader<T, SA, BM, NT, AK, GUARD> la;
+  TileLoader<T, SB, BN, NT, BKC, GUARD> lb;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t ktiles = (g.K + BK - 1) / BK;
+  la.load(A, g.lda, m0, 0, g.M, g.K, tid);
+  lb.load(B, g.ldb, n0, 0, g.N, g.K, tid);
+  la.store(smem, tid);
+  lb.store(smem + A_BYTES, tid);
+  __syncthreads();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      la.load(A, g.lda, m0, (kt + 1) * BK, g.M, g.K, tid);
+      lb.load(B, g.ldb, n0, (kt + 1) * BK, g.N, g.K, tid);
+    }
+    const char *a_s = smem + cur * STAGE;
+    const char *b_s = a_s + A_BYTES;
+    // Four pairs of 16-byte chunks per 128-byte row; the half-waves take the
+    // two chunks of a pair.
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int c = 2 * p + lhalf;
+      Chunk fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i].u = *reinterpret_cast<const uint4 *>(a_s + lds_off(wm * WTM + i * 32 + lrow, c));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j].u = *reinterpret_cast<const uint4 *>(b_s + lds_off(wn * WTN + j * 32 + lrow, c));
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i].u),
+                                                                __builtin_bit_cast(bf16x8, fb[j].u), acc[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].f[e], fb[j].f[e], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (more) {
+      la.store(smem + (cur ^ 1) * STAGE, tid);
+      lb.store(smem + (cur ^ 1) * STAGE + A_BYTES, tid);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        if (!GUARD || (row < g.M && col < g.N)) {
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
+          else C[row * g.ldc + col] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------- launching
+struct Plan {
+  int64_t M, N, K, batch;
+  bool ta, tb;
+  int ea, eb, eo;  // element kinds
+  const void *a, *b;
+  void *c;
+  int64_t sa, sb, sc;
+};
+
+template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD>
+static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int SMEM = 2 * (BM + BN) * 128;
+  auto kern = gemm_kernel<T, SA, SB, TO, BM, BN, WM, WN, AK, BKC, GUARD>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  GemmArgs g;
+  g.a = p.a; g.b = p.b; g.c = p.c;
+  g.M = p.M; g.N = p.N; g.K = p.K;
+  g.lda = p.ta ? p.M : p.K;  // A is [m, k] or [k, m]
+  g.ldb = p.tb ? p.K : p.N;  // B is [k, n] or [n, k]
+  g.ldc = p.N;
+  g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
+  g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
+  kern<<<grid, NT, SMEM, st>>>(g);
+  return hipGetLastError();
+}
+
+// Operand orientation: A k-contiguous unless transposed; B k-contiguous when transposed.
+template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool GUARD>
+static hipError_t launch_orient(const Plan &p, hipStream_t st) {
+  const bool ak = !p.ta, bk = p.tb;
+  if (ak && bk) return launch_cfg<T, SA, SB, TO, BM, BN, WM, WN, true, true, GUARD>(p, st);
+  if (ak && !bk) return launch_cfg<T, SA, SB, TO, BM, BN, WM, WN, true, false, GUARD>(p, st);
+  if (!ak && bk) return launch_cfg<T, SA, SB, TO, BM, BN, WM, WN, false, true, GUARD>(p, st);
+  return launch_cfg<T, SA, SB, TO, BM, BN, WM, WN, false, false, GUARD>(p, st);
+}
+
+// Every operand pointer, leading dimension and batch stride a multiple of the
+// 16-byte chunk, and the shape a multiple of the tile: the unguarded kernel.
+static bool tiles_exactly(const Plan &p, int bm, int bn, int bk, int64_t align_elems) {
+  if (p.M % bm || p.N % bn || p.K % bk) return false;
+  const int64_t lda = p.ta ? p.M : p.K, ldb = p.tb ? p.K : p.N;
+  if (lda % align_elems || ldb % align_elems) return false;
+  if (p.sa % align_elems || p.sb % align_elems) return false;
+  return true;
+}
+
+template <typename TO>
+static hipError_t run_bf16(const Plan &p, hipStream_t st) {
+  using T = uint16_t;
+  const int64_t tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * p.batch;
+  if (tiles256 >= 128 && tiles_exactly(p, 256, 256, 64, 8))
+    return launch_orient<T, T, T, TO, 256, 256, 2, 2, false>(p, st);
+  if (tiles_exactly(p, 128, 128, 64, 8))
+    return launch_orient<T, T, T, TO, 128, 128, 2, 2, false>(p, st);
+  if (tiles_exactly(p, 64, 64, 64, 8))
+    return launch_orient<T, T, T, TO, 64, 64, 2, 2, false>(p, st);
+  return launch_orient<T, T, T, TO, 64, 64, 2, 2, true>(p, st);
+}
+
+template <typename SA, typename SB, typename TO>
+static hipError_t run_f32(const Plan &p, hipStream_t st) {
+  using T = float;
+  const int64_t al = (sizeof(SA) == 2 || sizeof(SB) == 2) ? 4 : 4;
+  const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
+  if (tiles128 >= 128 && tiles_exactly(p, 128, 128, 32, al))
+    return launch_orient<T, SA, SB, TO, 128, 128, 2, 2, false>(p, st);
+  if (tiles_exactly(p, 64, 64, 32, al))
+    return launch_orient<T, SA, SB, TO, 64, 64, 2, 2, false>(p, st);
+  return launch_orient<T, SA, SB, TO, 64, 64, 2, 2, true>(p, st);
+}
+
+static hipError_t run_plan(const Plan &p, hipStream_t st) {
+  const bool bf = p.eo == MI_BF16;
+  if (p.ea == MI_BF16 && p.eb == MI_BF16)
+    return bf ? run_bf16<uint16_t>(p, st) : run_bf16<float>(p, st);
+  if (p.ea == MI_F32 && p.eb == MI_F32)
+    return bf ? run_f32<float, float, uint16_t>(p, st) : run_f32<float, float, float>(p, st);
+  if (p.ea == MI_F32 && p.eb == MI_BF16)
+    return bf ? run_f32<float, uint16_t, uint16_t>(p, st) : run_f32<float, uint16_t, float>(p, st);
+  return bf ? run_f32<uint16_t, float, uint16_t>(p, st) : run_f32<uint16_t, float, float>(p, st);
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t batch, int64_t m, int64_t k,
+                         int64_t n, bool batched, int out_elem, mi_id *out) {
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, A, a);
+  MI_BUF(ctx, B, b);
+  if (!elem_float(A->elem) || !elem_float(B->elem))
+    return fail(ctx, MI_E_ARG, "matmul of %s and %s", elem_name(A->elem), elem_name(B->elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "matmul result kind %s", elem_name(out_elem));
+  Plan p;
+  p.ta = ta != 0; p.tb = tb != 0;
+  p.ea = A->elem; p.eb = B->elem; p.eo = out_elem;
+  p.a = A->ptr; p.b = B->ptr;
+  if (!batched) {
+    p.M = ta ? A->cols : A->rows;
+    p.K = ta ? A->rows : A->cols;
+    const int64_t kb = tb ? B->cols : B->rows;
+    p.N = tb ? B->rows : B->cols;
+    if (kb != p.K)
+      return fail(ctx, MI_E_ARG, "matmul: op(A) is [%lld, %lld], op(B) is [%lld, %lld]", (long long)p.M, (long long)p.K,
+                  (long long)kb, (long long)p.N);
+    p.batch = 1; p.sa = p.sb = p.sc = 0;
+  } else {
+    if (batch < 1 || m < 0 || k < 0 || n < 0) return fail(ctx, MI_E_ARG, "batched matmul dims");
+    p.M = m; p.K = k; p.N = n; p.batch = batch;
+    const int64_t a_item = m * k, b_item = k * n;
+    const int64_t a_rows = ta ? k : m, a_cols = ta ? m : k;
+    const int64_t b_rows = tb ? n : k, b_cols = tb ? k : n;
+    if (A->cols != a_cols || (A->rows != a_rows && A->rows != a_rows * batch))
+      return fail(ctx, MI_E_ARG, "batched matmul: A is [%lld, %lld], items [%lld, %lld] x %lld", (long long)A->rows,
+                  (long long)A->cols, (long long)a_rows, (long long)a_cols, (long long)batch);
+    if (B->cols != b_cols || (B->rows != b_rows && B->rows != b_rows * batch))
+      return fail(ctx, MI_E_ARG, "batched matmul: B is [%lld, %lld], items [%lld, %lld] x %lld", (long long)B->rows,
+                  (long long)B->cols, (long long)b_rows, (long long)b_cols, (long long)batch);
+    p.sa = (A->rows == a_rows && batch > 1) ? 0 : a_item;
+    p.sb = (B->rows == b_rows && batch > 1) ? 0 : b_item;
+    p.sc = m * n;
+  }
+  if (p.batch > 65535) return fail(ctx, MI_E_ARG, "batched matmul: batch %lld above 65535", (long long)p.batch);
+  mi_id id; Buffer *cb;
+  int s = new_buffer(ctx, p.batch * p.M, p.N, out_elem, &id, &cb);
+  if (s) return s;
+  p.c = cb->ptr;
+  if (p.M > 0 && p.N > 0) {
+    if (p.K == 0) {
+      (void)hipMemsetAsync(cb->ptr, 0, p.batch * p.M * p.N * elem_size(out_elem), ctx->stream);
+    } else {
+      hipError_t e = run_plan(p, ctx->stream);
+      if (e != hipSuccess) {
+        mi_free(ctx, id);
+        return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
+      }
+    }
+    s = check_launch(ctx, "matmul");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, false, out_elem, out);
+}
+
+extern "C" int mi_matmul_batched(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int64_t batch,
+                                 int64_t m, int64_t k, int64_t n, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  return matmul_common(ctx, a, a_transposed, b, b_transposed, batch, m, k, n, true, out_elem, out);
+}

@@ -1,0 +1,283 @@
+// Indexing: row select (embedding), column pick (cross-entropy gather) and
+// its scatter-add backward, row select-add (embedding backward), row argmax.
+//
+// Reference: Engine::select_rows / pick_columns / select_add_rows / argmax_row
+// (crates/burn-tt/src/server.rs:300, 349, 358, 477); their routing
+// `select_rows_native`, `pick_columns_native`, `scatter_add_columns_native`
+// (crates/burn-tt/src/ops.rs:1001-1240); duplicates folded in index order
+// (crates/burn-tt/src/ops/index.rs:27-30); argmax's first maximum with NaN
+// above every number (crates/tt-models/src/generate.rs:176-183,
+// crates/burn-tt/src/ops.rs:2389-2490).
+//
+// Every copy here moves raw bits, so results are bit-exact.  An index outside
+// its range sets the context's device flag (reported as MI_E_DOMAIN at the
+// next wait) and the element is written as zero bits, never read out of
+// bounds.
+#include "common.hpp"
+
+#include <hipcub/device/device_radix_sort.hpp>
+
+namespace mi {
+
+// ---------------------------------------------------------- select_rows
+// A block of 256 threads copies rows: each wave one output row per step,
+// 16-byte lanes when the row width allows.
+template <typename V>
+__global__ void __launch_bounds__(256) select_rows_kernel(const V *table, int64_t vrows, int64_t vcols,
+                                                          const int32_t *idx, int64_t n, V *out,
+                                                          uint32_t *flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t waves = (static_cast<int64_t>(gridDim.x) * blockDim.x) >> 6;
+  for (int64_t i = wave; i < n; i += waves) {
+    const int32_t r = idx[i];
+    V *dst = out + i * vcols;
+    if (r < 0 || r >= vrows) {
+      if (lane == 0) atomicOr(flags, FLAG_INDEX_RANGE);
+      for (int64_t j = lane; j < vcols; j += 64) dst[j] = V{};
+      continue;
+    }
+    const V *src = table + static_cast<int64_t>(r) * vcols;
+    for (int64_t j = lane; j < vcols; j += 64) dst[j] = src[j];
+  }
+}
+
+// ---------------------------------------------------------- pick_columns
+__global__ void pick_columns_kernel(const uint32_t *x, int64_t rows, int64_t cols, const int32_t *idx,
+                                    uint32_t *out, uint32_t *flags) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int32_t c = idx[r];
+  if (c < 0 || c >= cols) { atomicOr(flags, FLAG_INDEX_RANGE); out[r] = 0; return; }
+  out[r] = x[r * cols + c];
+}
+
+__global__ void scatter_add_columns_kernel(float *out, int64_t rows, int64_t cols, const int32_t *idx,
+                                           const float *v, uint32_t *flags) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int32_t c = idx[r];
+  if (c < 0 || c >= cols) { atomicOr(flags, FLAG_INDEX_RANGE); return; }
+  out[r * cols + c] = out[r * cols + c] + v[r];
+}
+
+// ------------------------------------------------------- select_add_rows
+// After a stable sort of (index, position) pairs, each run of one index is a
+// segment; one wave per segment start adds the segment's value rows into the
+// destination row in position order, so duplicates fold in index order.
+__global__ void iota_kernel(int32_t *p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = static_cast<int32_t>(i);
+}
+
+__global__ void __launch_bounds__(256) select_add_segments(float *out, int64_t vrows, int64_t cols,
+                                                           const int32_t *keys, const int32_t *pos, int64_t n,
+                                                           const float *value, uint32_t *flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t p = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (p >= n) return;
+  const int32_t key = keys[p];
+  if (p > 0 && keys[p - 1] == key) return;  // not a segment start
+  if (key < 0 || key >= vrows) {
+    if (lane == 0) atomicOr(flags, FLAG_INDEX_RANGE);
+    return;
+  }
+  int64_t end = p + 1;
+  while (end < n && keys[end] == key) ++end;
+  float *dst = out + static_cast<int64_t>(key) * cols;
+  for (int64_t j = lane; j < cols; j += 64) {
+    float acc = dst[j];
+    for (int64_t q = p; q < end; ++q) acc = acc + value[static_cast<int64_t>(pos[q]) * cols + j];
+    dst[j] = acc;
+  }
+}
+
+// --------------------------------------------------------------- argmax
+struct ArgBest { float v; int32_t i; };
+__device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
+  const bool an = isnan(a.v), bn = isnan(b.v);
+  if (an || bn) {
+    if (an && bn) return a.i <= b.i ? a : b;
+    return an ? a : b;
+  }
+  if (a.v > b.v) return a;
+  if (b.v > a.v) return b;
+  return a.i <= b.i ? a : b;
+}
+
+__global__ void __launch_bounds__(256) argmax_rows_kernel(const void *x, int elem, int64_t rows, int64_t cols,
+                                                          int32_t *out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  ArgBest best{-INFINITY, INT32_MAX};
+  for (int64_t j = lane; j < cols; j += 64) {
+    float v = elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[base + j])
+                              : static_cast<const float *>(x)[base + j];
+    best = better(best, ArgBest{v, static_cast<int32_t>(j)});
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ArgBest other{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)};
+    best = better(best, other);
+  }
+  if (lane == 0) out[row] = best.i == INT32_MAX ? 0 : best.i;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, t, table);
+  MI_BUF(ctx, ix, idx);
+  if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "select_rows indices are %s, not I32", elem_name(ix->elem));
+  const int64_t n = ix->numel(), V = t->rows, D = t->cols;
+  const void *tp = t->ptr;
+  const int32_t *ip = static_cast<const int32_t *>(ix->ptr);
+  const int te = t->elem;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, n, D, te, &id, &ob);
+  if (s) return s;
+  if (n > 0 && D > 0) {
+    const size_t row_bytes = static_cast<size_t>(D) * elem_size(te);
+    const unsigned g = grid_for(n, 4, 256 * 64);
+    if (row_bytes % 16 == 0)
+      select_rows_kernel<uint4><<<g, 256, 0, ctx->stream>>>(static_cast<const uint4 *>(tp), V, row_bytes / 16, ip, n,
+                                                            static_cast<uint4 *>(ob->ptr), flags(ctx));
+    else if (row_bytes % 4 == 0)
+      select_rows_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(tp), V, row_bytes / 4, ip, n,
+                                                               static_cast<uint32_t *>(ob->ptr), flags(ctx));
+    else
+      select_rows_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(tp), V, row_bytes / 2, ip, n,
+                                                               static_cast<uint16_t *>(ob->ptr), flags(ctx));
+    s = check_launch(ctx, "select_rows");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, ix, idx);
+  if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "pick_columns indices are %s, not I32", elem_name(ix->elem));
+  if (elem_size(xb->elem) != 4) return fail(ctx, MI_E_ARG, "pick_columns of a %s buffer", elem_name(xb->elem));
+  if (ix->numel() != xb->rows) return fail(ctx, MI_E_ARG, "pick_columns: %lld indices for %lld rows", (long long)ix->numel(), (long long)xb->rows);
+  const int64_t R = xb->rows, C = xb->cols;
+  const void *xp = xb->ptr;
+  const int32_t *ip = static_cast<const int32_t *>(ix->ptr);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, 1, xb->elem, &id, &ob);
+  if (s) return s;
+  if (R > 0) {
+    pick_columns_kernel<<<grid_for(R, 256, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(xp), R, C, ip,
+                                                                            static_cast<uint32_t *>(ob->ptr), flags(ctx));
+    s = check_launch(ctx, "pick_columns");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_scatter_add_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id v, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, ix, idx);
+  MI_BUF(ctx, vb, v);
+  if (xb->elem != MI_F32 || vb->elem != MI_F32) return fail(ctx, MI_E_ARG, "scatter_add_columns takes F32 values");
+  if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "scatter_add_columns indices are %s, not I32", elem_name(ix->elem));
+  if (ix->numel() != xb->rows || vb->numel() != xb->rows)
+    return fail(ctx, MI_E_ARG, "scatter_add_columns: %lld indices, %lld values for %lld rows", (long long)ix->numel(),
+                (long long)vb->numel(), (long long)xb->rows);
+  const int64_t R = xb->rows, C = xb->cols;
+  const void *xp = xb->ptr;
+  const int32_t *ip = static_cast<const int32_t *>(ix->ptr);
+  const float *vp = static_cast<const float *>(vb->ptr);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, C, MI_F32, &id, &ob);
+  if (s) return s;
+  if (R * C > 0) {
+    (void)hipMemcpyAsync(ob->ptr, xp, R * C * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+    scatter_add_columns_kernel<<<grid_for(R, 256, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<float *>(ob->ptr), R, C, ip,
+                                                                                   vp, flags(ctx));
+    s = check_launch(ctx, "scatter_add_columns");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_select_add_rows(mi_ctx *ctx, mi_id t, mi_id idx, mi_id value, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, tb, t);
+  MI_BUF(ctx, ix, idx);
+  MI_BUF(ctx, vb, value);
+  if (tb->elem != MI_F32 || vb->elem != MI_F32) return fail(ctx, MI_E_ARG, "select_add_rows takes F32 values");
+  if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "select_add_rows indices are %s, not I32", elem_name(ix->elem));
+  const int64_t n = ix->numel(), V = tb->rows, D = tb->cols;
+  if (vb->rows != n || vb->cols != D)
+    return fail(ctx, MI_E_ARG, "select_add_rows: value [%lld, %lld] for %lld indices of width %lld", (long long)vb->rows,
+                (long long)vb->cols, (long long)n, (long long)D);
+  if (n > INT32_MAX) return fail(ctx, MI_E_ARG, "select_add_rows: too many indices");
+  const void *tp = tb->ptr;
+  const int32_t *ip = static_cast<const int32_t *>(ix->ptr);
+  const float *vp = static_cast<const float *>(vb->ptr);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, V, D, MI_F32, &id, &ob);
+  if (s) return s;
+  if (V * D > 0) (void)hipMemcpyAsync(ob->ptr, tp, V * D * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+  if (n > 0 && D > 0) {
+    const int ni = static_cast<int>(n);
+    size_t temp_bytes = 0;
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, static_cast<const int32_t *>(nullptr),
+                                       static_cast<int32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                                       static_cast<int32_t *>(nullptr), ni, 0, 32, ctx->stream);
+    const size_t arr = (static_cast<size_t>(n) * 4 + 255) & ~size_t(255);
+    char *sc = static_cast<char *>(scratch(ctx, 3 * arr + temp_bytes + 256));
+    if (!sc) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "select_add_rows scratch"); }
+    int32_t *pos_in = reinterpret_cast<int32_t *>(sc);
+    int32_t *keys_out = reinterpret_cast<int32_t *>(sc + arr);
+    int32_t *pos_out = reinterpret_cast<int32_t *>(sc + 2 * arr);
+    void *temp = sc + 3 * arr;
+    iota_kernel<<<grid_for(n, 256, INT32_MAX), 256, 0, ctx->stream>>>(pos_in, n);
+    // Keys as unsigned bits keep negative (invalid) indices grouped; the
+    // segment kernel flags them.
+    (void)hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, ip, keys_out, pos_in, pos_out, ni, 0, 32, ctx->stream);
+    select_add_segments<<<grid_for(n, 4, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<float *>(ob->ptr), V, D, keys_out,
+                                                                           pos_out, n, vp, flags(ctx));
+  }
+  s = check_launch(ctx, "select_add_rows");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, a);
+  if (!elem_float(xb->elem)) return fail(ctx, MI_E_ARG, "argmax of a %s buffer", elem_name(xb->elem));
+  if (xb->cols == 0) return fail(ctx, MI_E_ARG, "argmax of an empty row");
+  if (xb->cols > (int64_t(1) << 31) - 1) return fail(ctx, MI_E_ARG, "argmax row too long");
+  const int64_t R = xb->rows, C = xb->cols;
+  const void *xp = xb->ptr;
+  const int xe = xb->elem;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, 1, MI_I32, &id, &ob);
+  if (s) return s;
+  if (R > 0) {
+    argmax_rows_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, R, C, static_cast<int32_t *>(ob->ptr));
+    s = check_launch(ctx, "argmax_rows");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}

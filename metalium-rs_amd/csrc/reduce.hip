@@ -1,0 +1,540 @@
+// Reductions over one axis and over a whole buffer, fused row softmax /
+// log-softmax (with attention's scale and mask), RMSNorm and LayerNorm.
+//
+// Reference: Engine::reduce (crates/burn-tt/src/server.rs:404) and
+// Session::reduce_then (crates/tt-kernels/src/session.rs:8487) with the order
+// contract of crates/tt-kernels/src/sfpu/reduce.rs:1-38; full sums
+// (crates/burn-tt/src/ops.rs:3246-3400); mean = sum / count (ops.rs:3456-3469);
+// softmax / log_softmax (ops.rs:5133-5166) and attention's clamped softmax
+// (ops.rs:4572-4590); Engine::softmax_rows (server.rs:428); Engine::rms_norm
+// (server.rs:438, crates/burn-tt/src/ops/norm.rs:39-283).
+//
+// MI355X design.  Row-wise work (over columns) gives each row to one 64-lane
+// wavefront: lanes stride the row with coalesced loads, keep it in registers
+// when it fits (softmax reads its row from HBM once and writes it once), and
+// fold across lanes with a fixed butterfly, so results are deterministic.
+// Column sums (over rows) split the rows over a 2-D grid, each block summing a
+// strip of 256 columns as float4 lanes, and a second pass adds the strips'
+// partials in strip order -- deterministic, and enough blocks to fill 256 CUs.
+#include "common.hpp"
+
+#include <cfloat>
+
+namespace mi {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float max_nan(float a, float b) {
+  // NaN ranks above every number, so it propagates.
+  if (isnan(a)) return a;
+  if (isnan(b)) return b;
+  return b > a ? b : a;
+}
+__device__ __forceinline__ float min_nan(float a, float b) {
+  if (isnan(a)) return a;
+  if (isnan(b)) return b;
+  return b < a ? b : a;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max_nan(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min_nan(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float ld(const void *p, int elem, int64_t i) {
+  return elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]) : static_cast<const float *>(p)[i];
+}
+__device__ __forceinline__ void st(void *p, int elem, int64_t i, float v) {
+  if (elem == MI_BF16) static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+  else static_cast<float *>(p)[i] = v;
+}
+
+// ------------------------------------------------ reduce over columns (dim 1)
+// One wavefront per row; four rows per 256-thread block.
+__global__ void __launch_bounds__(256) reduce_cols_kernel(const void *x, int elem, float *out, int64_t rows,
+                                                          int64_t cols, int op) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  if (elem == MI_F32 && (cols % 4) == 0) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+    const int64_t n4 = cols / 4;
+    for (int64_t j = lane; j < n4; j += 64) {
+      float4 v = p[j];
+      if (op == MI_R_MAX) acc = max_nan(max_nan(max_nan(max_nan(acc, v.x), v.y), v.z), v.w);
+      else if (op == MI_R_MIN) acc = min_nan(min_nan(min_nan(min_nan(acc, v.x), v.y), v.z), v.w);
+      else acc += (v.x + v.y) + (v.z + v.w);
+    }
+  } else {
+    for (int64_t j = lane; j < cols; j += 64) {
+      float v = ld(x, elem, base + j);
+      if (op == MI_R_MAX) acc = max_nan(acc, v);
+      else if (op == MI_R_MIN) acc = min_nan(acc, v);
+      else acc += v;
+    }
+  }
+  if (op == MI_R_MAX) acc = wave_max(acc);
+  else if (op == MI_R_MIN) acc = wave_min(acc);
+  else acc = wave_sum(acc);
+  if (lane == 0) out[row] = (op == MI_R_MEAN) ? acc / static_cast<float>(cols) : acc;
+}
+
+// --------------------------------------------------- reduce over rows (dim 0)
+// Block (256 threads) = 4 waves; a wave's 64 lanes cover 256 columns as
+// float4 (or 64 columns as scalars).  Wave w adds rows r0 + w, r0 + w + 4, ...
+// of the block's row strip; the 4 waves then fold in order through LDS.
+template <bool VEC>
+__global__ void __launch_bounds__(256) reduce_rows_part(const void *x, int elem, float *part, int64_t rows,
+                                                        int64_t cols, int64_t rows_per_split, int op) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int CW = VEC ? 256 : 64;  // columns per block
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CW;
+  const int64_t split = blockIdx.y;
+  const int64_t r_begin = split * rows_per_split;
+  const int64_t r_end = r_begin + rows_per_split < rows ? r_begin + rows_per_split : rows;
+  const float init = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  float4 acc = make_float4(init, init, init, init);
+  __shared__ float4 red[4][64];
+  if (VEC) {
+    const int64_t c = c0 + lane * 4;
+    if (c < cols) {
+      const float *p = static_cast<const float *>(x);
+      for (int64_t r = r_begin + w; r < r_end; r += 4) {
+        float4 v = *reinterpret_cast<const float4 *>(p + r * cols + c);
+        if (op == MI_R_MAX) { acc.x = max_nan(acc.x, v.x); acc.y = max_nan(acc.y, v.y); acc.z = max_nan(acc.z, v.z); acc.w = max_nan(acc.w, v.w); }
+        else if (op == MI_R_MIN) { acc.x = min_nan(acc.x, v.x); acc.y = min_nan(acc.y, v.y); acc.z = min_nan(acc.z, v.z); acc.w = min_nan(acc.w, v.w); }
+        else { acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w; }
+      }
+    }
+  } else {
+    const int64_t c = c0 + lane;
+    if (c < cols) {
+      for (int64_t r = r_begin + w; r < r_end; r += 4) {
+        float v = ld(x, elem, r * cols + c);
+        if (op == MI_R_MAX) acc.x = max_nan(acc.x, v);
+        else if (op == MI_R_MIN) acc.x = min_nan(acc.x, v);
+        else acc.x += v;
+      }
+    }
+  }
+  red[w][lane] = acc;
+  __syncthreads();
+  if (w == 0) {
+    float4 s = red[0][lane];
+    for (int k = 1; k < 4; ++k) {
+      float4 v = red[k][lane];
+      if (op == MI_R_MAX) { s.x = max_nan(s.x, v.x); s.y = max_nan(s.y, v.y); s.z = max_nan(s.z, v.z); s.w = max_nan(s.w, v.w); }
+      else if (op == MI_R_MIN) { s.x = min_nan(s.x, v.x); s.y = min_nan(s.y, v.y); s.z = min_nan(s.z, v.z); s.w = min_nan(s.w, v.w); }
+      else { s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w; }
+    }
+    float *dst = part + split * cols;
+    if (VEC) {
+      const int64_t c = c0 + lane * 4;
+      if (c < cols) *reinterpret_cast<float4 *>(dst + c) = s;
+    } else {
+      const int64_t c = c0 + lane;
+      if (c < cols) dst[c] = s.x;
+    }
+  }
+}
+
+__global__ void reduce_rows_final(const float *part, float *out, int64_t splits, int64_t cols, int64_t rows, int op) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float s = part[c];
+  for (int64_t k = 1; k < splits; ++k) {
+    float v = part[k * cols + c];
+    if (op == MI_R_MAX) s = max_nan(s, v);
+    else if (op == MI_R_MIN) s = min_nan(s, v);
+    else s += v;
+  }
+  out[c] = (op == MI_R_MEAN) ? s / static_cast<float>(rows) : s;
+}
+
+// ---------------------------------------------------------- full reduction
+__global__ void __launch_bounds__(256) reduce_all_part(const void *x, int elem, float *part, int64_t n, int op) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float v = ld(x, elem, i);
+    if (op == MI_R_MAX) acc = max_nan(acc, v);
+    else if (op == MI_R_MIN) acc = min_nan(acc, v);
+    else acc += v;
+  }
+  __shared__ float red[4];
+  if (op == MI_R_MAX) acc = wave_max(acc);
+  else if (op == MI_R_MIN) acc = wave_min(acc);
+  else acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = red[0];
+    for (int k = 1; k < 4; ++k) s = (op == MI_R_MAX) ? max_nan(s, red[k]) : (op == MI_R_MIN ? min_nan(s, red[k]) : s + red[k]);
+    part[blockIdx.x] = s;
+  }
+}
+
+__global__ void reduce_all_final(const float *part, int parts, float *out, int64_t n, int op) {
+  // One wave folds the block partials in a fixed order.
+  const int lane = threadIdx.x;
+  float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  for (int i = lane; i < parts; i += 64) {
+    float v = part[i];
+    if (op == MI_R_MAX) acc = max_nan(acc, v);
+    else if (op == MI_R_MIN) acc = min_nan(acc, v);
+    else acc += v;
+  }
+  if (op == MI_R_MAX) acc = wave_max(acc);
+  else if (op == MI_R_MIN) acc = wave_min(acc);
+  else acc = wave_sum(acc);
+  if (lane == 0) out[0] = (op == MI_R_MEAN) ? acc / static_cast<float>(n) : acc;
+}
+
+// ------------------------------------------------------------ row softmax
+// One wavefront per row, the row in registers: lane l holds columns
+// l + 64 t (t < T).  `mask` Bool rows read as row % mask_rows.
+template <int T>
+__global__ void __launch_bounds__(256) softmax_kernel(const void *x, int elem, const uint32_t *mask, int64_t mask_rows,
+                                                      float scale, int log_mode, void *out, int out_elem,
+                                                      int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  const uint32_t *mrow = mask ? mask + (row % mask_rows) * cols : nullptr;
+  float v[T];
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    float a = -INFINITY;
+    if (j < cols) {
+      a = ld(x, elem, base + j);
+      if (scale != 1.0f) a = a * scale;
+      if (mrow && mrow[j]) a = -INFINITY;
+    }
+    v[t] = a;
+    m = max_nan(m, a);
+  }
+  m = wave_max(m);
+  if (mrow) m = m > -FLT_MAX ? m : (isnan(m) ? m : -FLT_MAX);
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    float sh = v[t] - m;
+    float e = (j < cols) ? expf(sh) : 0.0f;
+    if (log_mode) v[t] = sh; else v[t] = e;
+    s += e;
+  }
+  s = wave_sum(s);
+  if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
+  const float ls = log_mode ? logf(s) : 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] / s);
+  }
+}
+
+// Rows too long for registers: three passes over the row (from L2).
+__global__ void __launch_bounds__(256) softmax_long_kernel(const void *x, int elem, const uint32_t *mask, int64_t mask_rows,
+                                                           float scale, int log_mode, void *out, int out_elem,
+                                                           int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  const uint32_t *mrow = mask ? mask + (row % mask_rows) * cols : nullptr;
+  auto val = [&](int64_t j) {
+    float a = ld(x, elem, base + j);
+    if (scale != 1.0f) a = a * scale;
+    if (mrow && mrow[j]) a = -INFINITY;
+    return a;
+  };
+  float m = -INFINITY;
+  for (int64_t j = lane; j < cols; j += 64) m = max_nan(m, val(j));
+  m = wave_max(m);
+  if (mrow) m = m > -FLT_MAX ? m : (isnan(m) ? m : -FLT_MAX);
+  float s = 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) s += expf(val(j) - m);
+  s = wave_sum(s);
+  if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
+  const float ls = log_mode ? logf(s) : 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) {
+    float sh = val(j) - m;
+    st(out, out_elem, base + j, log_mode ? sh - ls : expf(sh) / s);
+  }
+}
+
+// ------------------------------------------------------- RMSNorm, LayerNorm
+template <int T>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, const void *gamma, int gelem, float eps,
+                                                       void *out, int out_elem, int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float v[T];
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    v[t] = j < cols ? ld(x, elem, base + j) : 0.0f;
+    ss += v[t] * v[t];
+  }
+  ss = wave_sum(ss);
+  const float rms = __fsqrt_rn(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < cols) {
+      float y = v[t] / rms;
+      if (gamma) y = y * ld(gamma, gelem, j);
+      st(out, out_elem, base + j, y);
+    }
+  }
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) layer_norm_kernel(const float *x, const float *gamma, const float *beta, float eps,
+                                                         float *out, int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float v[T];
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    v[t] = j < cols ? x[base + j] : 0.0f;
+    s += v[t];
+  }
+  const float mean = wave_sum(s) / static_cast<float>(cols);
+  float q = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    float d = j < cols ? v[t] - mean : 0.0f;
+    q += d * d;
+  }
+  const float var = wave_sum(q) / static_cast<float>(cols);
+  const float den = __fsqrt_rn(var + eps);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < cols) {
+      float y = (v[t] - mean) / den;
+      if (gamma) y = y * gamma[j];
+      if (beta) y = y + beta[j];
+      out[base + j] = y;
+    }
+  }
+}
+
+// Register-row kernels: the smallest T (columns per lane) covering `cols`.
+static int pick_t(int64_t cols) {
+  const int ts[] = {1, 2, 4, 8, 16, 32, 64, 128};
+  for (int t : ts)
+    if (cols <= 64 * t) return t;
+  return 0;  // too long: a multi-pass kernel
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, x, a);
+  if (op < MI_R_SUM || op > MI_R_MIN) return fail(ctx, MI_E_ARG, "reduce op %d", op);
+  if (!elem_float(x->elem)) return fail(ctx, MI_E_ARG, "reduce of a %s buffer", elem_name(x->elem));
+  if (axis != MI_AXIS_ROWS && axis != MI_AXIS_COLS) return fail(ctx, MI_E_ARG, "reduce axis %d", axis);
+  const int64_t R = x->rows, C = x->cols;
+  const void *xp = x->ptr;
+  const int xe = x->elem;
+  if ((axis == MI_AXIS_COLS ? C : R) == 0 && op != MI_R_SUM)
+    return fail(ctx, MI_E_ARG, "reduce of an empty axis");
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, axis == MI_AXIS_COLS ? R : 1, axis == MI_AXIS_COLS ? 1 : C, MI_F32, &id, &ob);
+  if (s) return s;
+  float *o = static_cast<float *>(ob->ptr);
+  if (axis == MI_AXIS_COLS) {
+    if (R > 0) {
+      if (C == 0) (void)hipMemsetAsync(o, 0, R * sizeof(float), ctx->stream);
+      else reduce_cols_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, o, R, C, op);
+    }
+  } else if (C > 0) {
+    if (R == 0) {
+      (void)hipMemsetAsync(o, 0, C * sizeof(float), ctx->stream);
+    } else {
+      const bool vec = (xe == MI_F32) && (C % 4 == 0);
+      const int64_t cw = vec ? 256 : 64;
+      const int64_t tiles = (C + cw - 1) / cw;
+      int64_t splits = (2048 + tiles - 1) / tiles;
+      int64_t max_splits = (R + 15) / 16;
+      if (splits > max_splits) splits = max_splits;
+      if (splits < 1) splits = 1;
+      const int64_t rps = (R + splits - 1) / splits;
+      splits = (R + rps - 1) / rps;
+      float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(splits * C) * sizeof(float)));
+      if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "reduce scratch"); }
+      dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
+      if (vec) reduce_rows_part<true><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
+      else reduce_rows_part<false><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
+      reduce_rows_final<<<grid_for(C, 256, INT32_MAX), 256, 0, ctx->stream>>>(part, o, splits, C, R, op);
+    }
+  }
+  s = check_launch(ctx, "reduce");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_reduce_all(mi_ctx *ctx, mi_id a, int op, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, x, a);
+  if (op < MI_R_SUM || op > MI_R_MIN) return fail(ctx, MI_E_ARG, "reduce op %d", op);
+  if (!elem_float(x->elem)) return fail(ctx, MI_E_ARG, "reduce of a %s buffer", elem_name(x->elem));
+  const int64_t n = x->numel();
+  if (n == 0 && op != MI_R_SUM) return fail(ctx, MI_E_ARG, "reduce of an empty buffer");
+  const void *xp = x->ptr;
+  const int xe = x->elem;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, 1, 1, MI_F32, &id, &ob);
+  if (s) return s;
+  const int parts = static_cast<int>(grid_for(n, 256 * 8, 2048));
+  float *part = static_cast<float *>(scratch(ctx, parts * sizeof(float)));
+  if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "reduce scratch"); }
+  reduce_all_part<<<parts, 256, 0, ctx->stream>>>(xp, xe, part, n, op);
+  reduce_all_final<<<1, 64, 0, ctx->stream>>>(part, parts, static_cast<float *>(ob->ptr), n, op);
+  s = check_launch(ctx, "reduce_all");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, int log, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  if (!elem_float(xb->elem)) return fail(ctx, MI_E_ARG, "softmax of a %s buffer", elem_name(xb->elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "softmax result kind %s", elem_name(out_elem));
+  const uint32_t *mp = nullptr;
+  int64_t mrows = 1;
+  if (mask) {
+    MI_BUF(ctx, mb, mask);
+    if (mb->elem != MI_BOOL) return fail(ctx, MI_E_ARG, "softmax mask is %s", elem_name(mb->elem));
+    if (mb->cols != xb->cols || mb->rows == 0 || (xb->rows % mb->rows) != 0)
+      return fail(ctx, MI_E_ARG, "softmax mask [%lld, %lld] for [%lld, %lld]", (long long)mb->rows, (long long)mb->cols,
+                  (long long)xb->rows, (long long)xb->cols);
+    mp = static_cast<const uint32_t *>(mb->ptr);
+    mrows = mb->rows;
+  }
+  const int64_t R = xb->rows, C = xb->cols;
+  const void *xp = xb->ptr;
+  const int xe = xb->elem;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, C, out_elem, &id, &ob);
+  if (s) return s;
+  if (R > 0 && C > 0) {
+    unsigned g = grid_for(R, 4, INT32_MAX);
+    int t = pick_t(C);
+    switch (t) {
+#define MI_SM(T) case T: softmax_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, R, C); break;
+      MI_SM(1) MI_SM(2) MI_SM(4) MI_SM(8) MI_SM(16) MI_SM(32) MI_SM(64) MI_SM(128)
+#undef MI_SM
+      default: softmax_long_kernel<<<g, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, R, C);
+    }
+  }
+  s = check_launch(ctx, "softmax_rows");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, a);
+  if (!elem_float(xb->elem)) return fail(ctx, MI_E_ARG, "rms_norm of a %s buffer", elem_name(xb->elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "rms_norm result kind %s", elem_name(out_elem));
+  const void *gp = nullptr;
+  int ge = MI_F32;
+  if (gamma) {
+    MI_BUF(ctx, gb, gamma);
+    if (!elem_float(gb->elem) || gb->numel() != xb->cols) return fail(ctx, MI_E_ARG, "rms_norm gamma must be [1, %lld] float", (long long)xb->cols);
+    gp = gb->ptr; ge = gb->elem;
+  }
+  const int64_t R = xb->rows, C = xb->cols;
+  int t = pick_t(C);
+  if (t == 0) return fail(ctx, MI_E_UNSUPPORTED, "rms_norm rows longer than 8192");
+  const void *xp = xb->ptr;
+  const int xe = xb->elem;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, C, out_elem, &id, &ob);
+  if (s) return s;
+  if (R > 0 && C > 0) {
+    unsigned g = grid_for(R, 4, INT32_MAX);
+    switch (t) {
+#define MI_RN(T) case T: rms_norm_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, gp, ge, eps, ob->ptr, out_elem, R, C); break;
+      MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16) MI_RN(32) MI_RN(64) MI_RN(128)
+#undef MI_RN
+    }
+  }
+  s = check_launch(ctx, "rms_norm");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_layer_norm(mi_ctx *ctx, mi_id a, mi_id gamma, mi_id beta, float eps, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, a);
+  if (xb->elem != MI_F32) return fail(ctx, MI_E_ARG, "layer_norm of a %s buffer", elem_name(xb->elem));
+  const float *gp = nullptr, *bp = nullptr;
+  if (gamma) {
+    MI_BUF(ctx, gb, gamma);
+    if (gb->elem != MI_F32 || gb->numel() != xb->cols) return fail(ctx, MI_E_ARG, "layer_norm gamma must be [1, %lld] F32", (long long)xb->cols);
+    gp = static_cast<const float *>(gb->ptr);
+  }
+  if (beta) {
+    MI_BUF(ctx, bb, beta);
+    if (bb->elem != MI_F32 || bb->numel() != xb->cols) return fail(ctx, MI_E_ARG, "layer_norm beta must be [1, %lld] F32", (long long)xb->cols);
+    bp = static_cast<const float *>(bb->ptr);
+  }
+  const int64_t R = xb->rows, C = xb->cols;
+  int t = pick_t(C);
+  if (t == 0) return fail(ctx, MI_E_UNSUPPORTED, "layer_norm rows longer than 8192");
+  const float *xp = static_cast<const float *>(xb->ptr);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, C, MI_F32, &id, &ob);
+  if (s) return s;
+  if (R > 0 && C > 0) {
+    unsigned g = grid_for(R, 4, INT32_MAX);
+    float *o = static_cast<float *>(ob->ptr);
+    switch (t) {
+#define MI_LN(T) case T: layer_norm_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, gp, bp, eps, o, R, C); break;
+      MI_LN(1) MI_LN(2) MI_LN(4) MI_LN(8) MI_LN(16) MI_LN(32) MI_LN(64) MI_LN(128)
+#undef MI_LN
+    }
+  }
+  s = check_launch(ctx, "layer_norm");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}

@@ -1,0 +1,328 @@
+"""Python host binding of the MI355X engine (libmiburn.so, include/miburn.h).
+
+`Engine` mirrors the reference's device-engine trait, method for method: the
+`Engine` of crates/burn-tt/src/server.rs:42-788 (upload / download / free,
+matmul_dram, matmul_dram_batched, eltwise_op_as, reduce, softmax_rows,
+rms_norm, argmax_row, select_rows, pick_columns, select_add_rows,
+random_dram, cast_float).  Buffers are row-major `[rows, cols]` matrices named
+by integer ids, as the trait's `BufferId`.  Errors raise `MiError` carrying the
+C status; asynchronous failures (an index out of range found by a kernel)
+surface at the next `sync()` or download, as the reference defers them to its
+next wait (server.rs:2951-2991).
+
+The shared library is the only implementation: importing this module on a
+machine where libmiburn.so is missing raises, and there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmiburn.so")
+
+F32, I32, BOOL, BF16 = 0, 1, 2, 3
+_NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}
+
+AXIS_ROWS, AXIS_COLS = 0, 1
+R_SUM, R_MAX, R_MEAN, R_MIN = 0, 1, 2, 3
+DRAW_UNIT, DRAW_UNIFORM, DRAW_NORMAL, DRAW_BERNOULLI, DRAW_INT_RANGE = 0, 1, 2, 3, 4
+
+# Element-wise op ids (the reference's numbering, crates/tt-kernels/src/kind.rs,
+# crates/tt-kernels/src/sfpu/ops.rs:24-250).
+K = dict(
+    ADD=1, SUB=2, MUL=3, MUL_SCALAR=4, RELU=5, RELU_BACKWARD=6, ADD_ROW=7, ADD_SCALAR=11,
+    RECIP=0x100, DIV=0x101, DIV_SCALAR=0x102, EXP=0x103, LOG=0x104,
+    BOOL_NOT=0x105, BOOL_AND=0x106, BOOL_OR=0x107, BOOL_XOR=0x108,
+    NEG=0x109, ABS=0x10A, SIGN=0x10B, CLAMP=0x10C, CLAMP_MIN=0x10D, CLAMP_MAX=0x10E,
+    LEAKY_RELU=0x10F, HARD_SIGMOID=0x110,
+    EQ=0x111, NE=0x112, GT=0x113, GE=0x114, LT=0x115, LE=0x116,
+    EQ_S=0x117, NE_S=0x118, GT_S=0x119, GE_S=0x11A, LT_S=0x11B, LE_S=0x11C,
+    IS_NAN=0x11D, IS_INF=0x11E, MASK_FILL=0x11F, MASK_WHERE=0x120, FILL=0x122,
+    SQRT=0x123, RSQRT=0x124, LOG1P=0x125, POW=0x126, POW_S=0x127, I32_TO_F32=0x129,
+    EXPM1=0x12A, SIGMOID=0x12B, SIGMOID_BACKWARD=0x12C, TANH=0x12D, ERF=0x12E,
+    GELU=0x12F, GELU_BACKWARD=0x130, SIN=0x138, COS=0x139, BOOL_TO_F32=0x13F,
+    ADD_RELU=0x1F0, SILU=0x1F1, SILU_MUL=0x1F2, SUB_EXP=0x1F3, MUL_ADD=0x1F4,
+    SCALE_MASK_FILL=0x1F5, RSQRT_ABS_ADD=0x200,
+)
+
+STATUS = {0: "OK", -1: "ARG", -2: "ID", -3: "HIP", -4: "OOM", -5: "DOMAIN", -6: "UNSUPPORTED",
+          -7: "STICKY"}
+
+
+class MiError(RuntimeError):
+    """A failed engine call: `status` is the C code, `kind` its name."""
+
+    def __init__(self, status: int, msg: str):
+        self.status = status
+        self.kind = STATUS.get(status, str(status))
+        super().__init__(f"{self.kind}: {msg}")
+
+
+class Report(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "ops", "uploads", "downloads", "bytes_up", "bytes_down", "live_buffers", "device_bytes",
+        "cached_bytes")]
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built: run `make -C metalium-rs_amd` (or "
+                          "__graft_entry__.build()); there is no fallback implementation")
+    lib = ctypes.CDLL(LIB_PATH)
+    P = ctypes.c_void_p
+    I64 = ctypes.c_int64
+    U64 = ctypes.c_uint64
+    Ip = ctypes.POINTER(U64)
+    c_int, c_float, c_u32 = ctypes.c_int, ctypes.c_float, ctypes.c_uint32
+    sigs = {
+        "mi_ctx_create": [c_int, ctypes.POINTER(P)],
+        "mi_ctx_destroy": [P],
+        "mi_sync": [P],
+        "mi_stream": [P, ctypes.POINTER(P)],
+        "mi_upload": [P, P, I64, I64, Ip],
+        "mi_upload_bits": [P, P, I64, I64, c_int, Ip],
+        "mi_upload_bf16": [P, P, I64, I64, Ip],
+        "mi_download": [P, U64, P, I64],
+        "mi_download_bits": [P, U64, P, I64],
+        "mi_download_bf16": [P, U64, P, I64],
+        "mi_free": [P, U64],
+        "mi_metadata": [P, U64, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(c_int)],
+        "mi_fill": [P, I64, I64, c_int, c_u32, Ip],
+        "mi_matmul": [P, U64, c_int, U64, c_int, c_int, Ip],
+        "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
+        "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
+        "mi_reduce": [P, U64, c_int, c_int, Ip],
+        "mi_reduce_all": [P, U64, c_int, Ip],
+        "mi_softmax_rows": [P, U64, U64, c_float, c_int, c_int, Ip],
+        "mi_rms_norm": [P, U64, U64, c_float, c_int, Ip],
+        "mi_layer_norm": [P, U64, U64, U64, c_float, Ip],
+        "mi_argmax_rows": [P, U64, Ip],
+        "mi_select_rows": [P, U64, U64, Ip],
+        "mi_pick_columns": [P, U64, U64, Ip],
+        "mi_scatter_add_columns": [P, U64, U64, U64, Ip],
+        "mi_select_add_rows": [P, U64, U64, U64, Ip],
+        "mi_copy_strided": [P, U64, I64, I64, I64, I64, I64, Ip],
+        "mi_copy_strided4": [P, U64, ctypes.POINTER(I64), I64, ctypes.POINTER(I64), Ip],
+        "mi_assign_block": [P, U64, U64, I64, I64],
+        "mi_cast": [P, U64, c_int, Ip],
+        "mi_random": [P, I64, I64, c_int, c_float, c_float, U64, Ip],
+        "mi_event_record": [P, c_int],
+        "mi_event_elapsed_ms": [P, c_int, c_int, ctypes.POINTER(c_float)],
+        "mi_get_report": [P, ctypes.POINTER(Report)],
+    }
+    for name, args in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = c_int
+    lib.mi_last_error.argtypes = [P]
+    lib.mi_last_error.restype = ctypes.c_char_p
+    return lib
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+class Engine:
+    """One device context: the reference's `KmdEngine` (server.rs:4071) for an MI355X."""
+
+    def __init__(self, device: int = 0):
+        self._lib = lib()
+        ctx = ctypes.c_void_p()
+        st = self._lib.mi_ctx_create(device, ctypes.byref(ctx))
+        if st != 0:
+            raise MiError(st, self._lib.mi_last_error(None).decode())
+        self.ctx = ctx
+
+    # -- plumbing --------------------------------------------------------
+    def close(self) -> None:
+        if self.ctx:
+            self._lib.mi_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int) -> None:
+        if st != 0:
+            raise MiError(st, self._lib.mi_last_error(self.ctx).decode())
+
+    def _out(self, fn, *args) -> int:
+        out = ctypes.c_uint64()
+        self._check(fn(self.ctx, *args, ctypes.byref(out)))
+        return out.value
+
+    # -- storage (server.rs:91-174) ----------------------------------------
+    def upload(self, x: np.ndarray) -> int:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        r, c = _dims(x)
+        return self._out(self._lib.mi_upload, x.ctypes.data, r, c)
+
+    def upload_bits(self, x: np.ndarray, elem: int) -> int:
+        x = np.ascontiguousarray(x)
+        if x.dtype.itemsize != 4:
+            raise ValueError("upload_bits takes 32-bit datums")
+        r, c = _dims(x)
+        return self._out(self._lib.mi_upload_bits, x.ctypes.data, r, c, elem)
+
+    def upload_i32(self, x: np.ndarray) -> int:
+        return self.upload_bits(np.ascontiguousarray(x, dtype=np.int32), I32)
+
+    def upload_bool(self, x: np.ndarray) -> int:
+        return self.upload_bits(np.ascontiguousarray(x, dtype=np.uint32), BOOL)
+
+    def upload_bf16(self, bits: np.ndarray) -> int:
+        bits = np.ascontiguousarray(bits, dtype=np.uint16)
+        r, c = _dims(bits)
+        return self._out(self._lib.mi_upload_bf16, bits.ctypes.data, r, c)
+
+    def metadata(self, id_: int) -> Tuple[int, int, int]:
+        r, c, e = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+        self._check(self._lib.mi_metadata(self.ctx, id_, ctypes.byref(r), ctypes.byref(c), ctypes.byref(e)))
+        return r.value, c.value, e.value
+
+    def download(self, id_: int) -> np.ndarray:
+        r, c, e = self.metadata(id_)
+        out = np.empty((r, c), dtype=_NP[e])
+        if e == F32:
+            self._check(self._lib.mi_download(self.ctx, id_, out.ctypes.data, out.size))
+        elif e == BF16:
+            self._check(self._lib.mi_download_bf16(self.ctx, id_, out.ctypes.data, out.size))
+        else:
+            self._check(self._lib.mi_download_bits(self.ctx, id_, out.ctypes.data, out.size))
+        return out
+
+    def free(self, id_: int) -> None:
+        self._check(self._lib.mi_free(self.ctx, id_))
+
+    def fill(self, rows: int, cols: int, elem: int, bits: int) -> int:
+        return self._out(self._lib.mi_fill, rows, cols, elem, bits)
+
+    def sync(self) -> None:
+        self._check(self._lib.mi_sync(self.ctx))
+
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        self._check(self._lib.mi_stream(self.ctx, ctypes.byref(s)))
+        return s.value or 0
+
+    # -- ops ---------------------------------------------------------------
+    def matmul_dram(self, a: int, a_t: bool, b: int, b_t: bool, out_elem: int = F32) -> int:
+        return self._out(self._lib.mi_matmul, a, int(a_t), b, int(b_t), out_elem)
+
+    def matmul_dram_bf16(self, a: int, a_t: bool, b: int, b_t: bool) -> int:
+        return self.matmul_dram(a, a_t, b, b_t, BF16)
+
+    def matmul_dram_batched(self, a: int, a_t: bool, b: int, b_t: bool, batch: int, m: int, k: int, n: int,
+                            out_elem: int = F32) -> int:
+        return self._out(self._lib.mi_matmul_batched, a, int(a_t), b, int(b_t), batch, m, k, n, out_elem)
+
+    def eltwise_op_as(self, kind, a: int, b: int = 0, c: int = 0, scalar: float = 0.0, scalar2: float = 0.0,
+                      out_elem: int = F32) -> int:
+        k = K[kind] if isinstance(kind, str) else int(kind)
+        return self._out(self._lib.mi_eltwise, k, scalar, scalar2, a, b, c, out_elem)
+
+    def reduce(self, a: int, op: int, axis: int) -> int:
+        return self._out(self._lib.mi_reduce, a, op, axis)
+
+    def reduce_all(self, a: int, op: int) -> int:
+        return self._out(self._lib.mi_reduce_all, a, op)
+
+    def softmax_rows(self, x: int, mask: int = 0, scale: float = 1.0, log: bool = False,
+                     out_elem: int = F32) -> int:
+        return self._out(self._lib.mi_softmax_rows, x, mask, scale, int(log), out_elem)
+
+    def rms_norm(self, a: int, gamma: int = 0, eps: float = 1e-5, out_elem: int = F32) -> int:
+        return self._out(self._lib.mi_rms_norm, a, gamma, eps, out_elem)
+
+    def layer_norm(self, a: int, gamma: int = 0, beta: int = 0, eps: float = 1e-5) -> int:
+        return self._out(self._lib.mi_layer_norm, a, gamma, beta, eps)
+
+    def argmax_row(self, a: int) -> int:
+        return self._out(self._lib.mi_argmax_rows, a)
+
+    def select_rows(self, table: int, idx: int) -> int:
+        return self._out(self._lib.mi_select_rows, table, idx)
+
+    def pick_columns(self, x: int, idx: int) -> int:
+        return self._out(self._lib.mi_pick_columns, x, idx)
+
+    def scatter_add_columns(self, x: int, idx: int, v: int) -> int:
+        return self._out(self._lib.mi_scatter_add_columns, x, idx, v)
+
+    def select_add_rows(self, t: int, idx: int, value: int) -> int:
+        return self._out(self._lib.mi_select_add_rows, t, idx, value)
+
+    def copy_strided(self, src: int, rows: int, cols: int, offset: int, row_stride: int, col_stride: int) -> int:
+        return self._out(self._lib.mi_copy_strided, src, rows, cols, offset, row_stride, col_stride)
+
+    def copy_strided4(self, src: int, dims: Sequence[int], offset: int, strides: Sequence[int]) -> int:
+        d = (ctypes.c_int64 * 4)(*dims)
+        s = (ctypes.c_int64 * 4)(*strides)
+        return self._out(self._lib.mi_copy_strided4, src, d, offset, s)
+
+    def assign_block(self, dst: int, src: int, row0: int, col0: int) -> None:
+        self._check(self._lib.mi_assign_block(self.ctx, dst, src, row0, col0))
+
+    def cast_float(self, a: int, out_elem: int) -> int:
+        return self._out(self._lib.mi_cast, a, out_elem)
+
+    def random_dram(self, rows: int, cols: int, draw: int, p1: float = 0.0, p2: float = 1.0,
+                    base: int = 0) -> int:
+        return self._out(self._lib.mi_random, rows, cols, draw, p1, p2, base & (2**64 - 1))
+
+    # -- timing and report ---------------------------------------------------
+    def event_record(self, slot: int) -> None:
+        self._check(self._lib.mi_event_record(self.ctx, slot))
+
+    def event_elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        self._check(self._lib.mi_event_elapsed_ms(self.ctx, a, b, ctypes.byref(ms)))
+        return ms.value
+
+    def report(self) -> dict:
+        r = Report()
+        self._check(self._lib.mi_get_report(self.ctx, ctypes.byref(r)))
+        return {n: getattr(r, n) for n, _ in Report._fields_}
+
+
+def _dims(x: np.ndarray) -> Tuple[int, int]:
+    """`[rows, cols]` of an array, rank N folded to `[prod(leading), last]`
+    (crates/burn-tt/src/tensor.rs:905-908)."""
+    if x.ndim == 0:
+        return 1, 1
+    if x.ndim == 1:
+        return 1, x.shape[0]
+    return int(np.prod(x.shape[:-1])), x.shape[-1]
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """F32 -> BF16 bits, ties to even, NaN kept a NaN (host-side conversion for uploads)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)

@@ -1,0 +1,20 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "metalium-rs_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libmiburn.so on the device)")
+
+
+@pytest.fixture(scope="session")
+def engine():
+    import miburn
+    eng = miburn.Engine(0)
+    yield eng
+    eng.close()

@@ -1,0 +1,552 @@
+"""Device parity: every engine op through the C ABI against the CPU oracle on
+the same seeded inputs.
+
+Bars: indexing, gather, argmax, casts and copies
+bit-exact; F32 element-wise ops and reductions within rel 1e-5; BF16-input
+products within rel 2e-2 of the F32 oracle and, against the oracle fed the
+same BF16 values, within the F32 accumulation bound.
+"""
+import numpy as np
+import pytest
+
+import miburn
+import oracle_lib as orc
+from miburn import AXIS_COLS, AXIS_ROWS, BF16, BOOL, F32, I32, K, R_MAX, R_MEAN, R_MIN, R_SUM
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(20240611)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a).view(np.uint32)
+    b = np.ascontiguousarray(b).view(np.uint32)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    bad = np.flatnonzero(a.ravel() != b.ravel())
+    assert bad.size == 0, f"{bad.size} datums differ, first at {bad[0]}: {a.ravel()[bad[0]]:#x} vs {b.ravel()[bad[0]]:#x}"
+
+
+def close(got, want, rtol=1e-5, atol=0.0):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"NaN positions differ: {np.flatnonzero(gn != wn)[:5]}"
+    g, w = got[~gn], want[~wn]
+    inf = np.isinf(w)
+    assert np.array_equal(g[inf], w[inf]), "infinities differ"
+    g, w = g[~inf].astype(np.float64), w[~inf].astype(np.float64)
+    err = np.abs(g - w)
+    lim = rtol * np.abs(w) + atol
+    worst = np.argmax(err - lim) if err.size else 0
+    assert np.all(err <= lim), f"max excess at {worst}: got {g[worst]!r} want {w[worst]!r} (tol {lim[worst]:.3g})"
+
+
+# --------------------------------------------------------------- element-wise
+EXACT_UNARY = ["NEG", "ABS", "RELU", "SIGN", "SQRT"]
+APPROX_UNARY = ["EXP", "LOG", "RECIP", "RSQRT", "SIGMOID", "TANH", "ERF", "GELU", "SILU", "LOG1P", "EXPM1",
+                "SIN", "COS"]
+
+
+def unary_input(kind, shape):
+    x = rnd(*shape)
+    if kind in ("LOG", "RSQRT", "SQRT"):
+        x = np.abs(x) + np.float32(1e-3)
+    if kind == "LOG1P":
+        x = np.abs(x)
+    return x
+
+
+@pytest.mark.parametrize("kind", EXACT_UNARY + APPROX_UNARY)
+@pytest.mark.parametrize("shape", [(64, 256), (37, 13)])
+def test_unary(engine, kind, shape):
+    x = unary_input(kind, shape)
+    a = engine.upload(x)
+    y = engine.eltwise_op_as(kind, a)
+    got = engine.download(y)
+    want = orc.eltwise(K[kind], x)
+    if kind in EXACT_UNARY:
+        same_bits(got, want)
+    else:
+        close(got, want, rtol=1e-5, atol=1e-7)
+    engine.free(a)
+    engine.free(y)
+
+
+@pytest.mark.parametrize("kind", ["ADD", "SUB", "MUL", "DIV", "RELU_BACKWARD", "ADD_RELU"])
+@pytest.mark.parametrize("bshape", ["full", "row", "col", "one"])
+def test_binary_broadcast_exact(engine, kind, bshape):
+    R, C = 48, 96
+    x = rnd(R, C)
+    y = {"full": rnd(R, C), "row": rnd(1, C), "col": rnd(R, 1), "one": rnd(1, 1)}[bshape]
+    if kind == "DIV":
+        y = np.where(np.abs(y) < 0.1, np.float32(0.5), y).astype(np.float32)
+    a, b = engine.upload(x), engine.upload(y)
+    got = engine.download(engine.eltwise_op_as(kind, a, b))
+    same_bits(got, orc.eltwise(K[kind], x, y))
+
+
+@pytest.mark.parametrize("kind", ["SIGMOID_BACKWARD", "GELU_BACKWARD", "SILU_MUL", "SUB_EXP", "POW"])
+def test_binary_approx(engine, kind):
+    R, C = 40, 200
+    x, y = rnd(R, C), rnd(R, C)
+    if kind == "POW":
+        x = np.abs(x) + np.float32(0.1)
+    if kind == "SIGMOID_BACKWARD":
+        x = 1.0 / (1.0 + np.exp(-x)).astype(np.float32)
+    a, b = engine.upload(x), engine.upload(y)
+    got = engine.download(engine.eltwise_op_as(kind, a, b))
+    close(got, orc.eltwise(K[kind], x, y), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("kind,s1,s2", [("MUL_SCALAR", -1.75, 0.0), ("ADD_SCALAR", 2.7, 0.0),
+                                        ("ADD_SCALAR", -0.0, 0.0), ("DIV_SCALAR", 3.0, 0.0),
+                                        ("CLAMP", -0.5, 0.75), ("CLAMP_MIN", 0.25, 0.0), ("CLAMP_MAX", -0.1, 0.0),
+                                        ("LEAKY_RELU", 0.01, 0.0), ("HARD_SIGMOID", 0.2, 0.5), ("FILL", 1.5, 0.0),
+                                        ("POW_S", 2.0, 0.0)])
+def test_scalar_ops_exact(engine, kind, s1, s2):
+    x = rnd(33, 64)
+    a = engine.upload(x)
+    got = engine.download(engine.eltwise_op_as(kind, a, scalar=s1, scalar2=s2))
+    want = orc.eltwise(K[kind], x, s1=s1, s2=s2)
+    if kind == "POW_S":
+        close(got, want, rtol=1e-6)
+    else:
+        same_bits(got, want)
+
+
+def test_rsqrt_abs_add_fused(engine):
+    x = rnd(128, 128)
+    a = engine.upload(x)
+    got = engine.download(engine.eltwise_op_as("RSQRT_ABS_ADD", a, scalar=1e-6))
+    close(got, orc.eltwise(K["RSQRT_ABS_ADD"], x, s1=1e-6), rtol=1e-5)
+
+
+@pytest.mark.parametrize("kind", ["EQ", "NE", "GT", "GE", "LT", "LE"])
+def test_compare(engine, kind):
+    x = rnd(16, 40)
+    y = x.copy()
+    y[::2] = rnd(8, 40)
+    y[0, 0], x[0, 0] = np.nan, 1.0
+    x[1, 1], y[1, 1] = -0.0, 0.0
+    a, b = engine.upload(x), engine.upload(y)
+    out = engine.eltwise_op_as(kind, a, b)
+    assert engine.metadata(out)[2] == BOOL
+    got = engine.download(out)
+    same_bits(got, orc.eltwise(K[kind], x, y).astype(np.uint32))
+
+
+def test_mask_fill_and_where(engine):
+    x, z = rnd(24, 80), rnd(24, 80)
+    m = (RNG.random((24, 80)) < 0.3).astype(np.uint32)
+    mrow = (RNG.random((1, 80)) < 0.5).astype(np.uint32)
+    a, c = engine.upload(x), engine.upload(z)
+    mb, mr = engine.upload_bool(m), engine.upload_bool(mrow)
+    same_bits(engine.download(engine.eltwise_op_as("MASK_FILL", a, mb, scalar=-np.inf)),
+              orc.eltwise(K["MASK_FILL"], x, m, s1=-np.inf))
+    same_bits(engine.download(engine.eltwise_op_as("MASK_FILL", a, mr, scalar=7.0)),
+              orc.eltwise(K["MASK_FILL"], x, mrow, s1=7.0))
+    same_bits(engine.download(engine.eltwise_op_as("MASK_WHERE", a, mb, c)),
+              orc.eltwise(K["MASK_WHERE"], x, m, z))
+    same_bits(engine.download(engine.eltwise_op_as("SCALE_MASK_FILL", a, mr, scalar=0.125, scalar2=-np.inf)),
+              orc.eltwise(K["SCALE_MASK_FILL"], x, mrow, s1=0.125, s2=-np.inf))
+
+
+def test_mul_add_ternary(engine):
+    x, y, z = rnd(30, 64), rnd(30, 64), rnd(30, 64)
+    a, b, c = engine.upload(x), engine.upload(y), engine.upload(z)
+    same_bits(engine.download(engine.eltwise_op_as("MUL_ADD", a, b, c)), orc.eltwise(K["MUL_ADD"], x, y, z))
+
+
+def test_special_values_relu_and_neg(engine):
+    x = np.array([[0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.0]], np.float32)
+    a = engine.upload(x)
+    same_bits(engine.download(engine.eltwise_op_as("RELU", a)), orc.eltwise(K["RELU"], x))
+    same_bits(engine.download(engine.eltwise_op_as("NEG", a)), orc.eltwise(K["NEG"], x))
+    same_bits(engine.download(engine.eltwise_op_as("ABS", a)), orc.eltwise(K["ABS"], x))
+
+
+def test_bf16_in_and_out(engine):
+    x = rnd(64, 128)
+    xb = orc.to_bf16(x)
+    a = engine.upload_bf16(xb)
+    y = engine.eltwise_op_as("GELU", a, out_elem=BF16)
+    assert engine.metadata(y)[2] == BF16
+    got = miburn.bf16_to_f32(engine.download(y))
+    want = orc.from_bf16(orc.to_bf16(orc.eltwise(K["GELU"], orc.from_bf16(xb))))
+    # One rounding to BF16 of values within 1e-5 of each other: at most one BF16 ulp apart.
+    close(got, want, rtol=2 ** -7, atol=1e-30)
+
+
+def test_large_vector_path(engine):
+    x, y = rnd(1024, 4096), rnd(1, 4096)
+    a, b = engine.upload(x), engine.upload(y)
+    same_bits(engine.download(engine.eltwise_op_as("ADD", a, b)), x + y)
+    close(engine.download(engine.eltwise_op_as("EXP", a)), orc.eltwise(K["EXP"], x), rtol=1e-5)
+
+
+# ------------------------------------------------------------------ reductions
+def reduce_tol(x, axis):
+    # Normwise: rel 1e-5 of the sum of magnitudes along the reduced axis.
+    return 1e-5 * np.abs(x.astype(np.float64)).sum(axis=1 - axis if axis in (0, 1) else None, keepdims=True)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 3), (64, 10), (130, 1000), (1000, 130), (2048, 512), (5, 9000)])
+@pytest.mark.parametrize("axis", [AXIS_ROWS, AXIS_COLS])
+def test_sum_mean(engine, shape, axis):
+    x = rnd(*shape)
+    a = engine.upload(x)
+    n = shape[0] if axis == AXIS_ROWS else shape[1]
+    absx = np.abs(x.astype(np.float64)).sum(axis=0 if axis == AXIS_ROWS else 1)
+    absx = absx.reshape((1, -1) if axis == AXIS_ROWS else (-1, 1))
+    for op in (R_SUM, R_MEAN):
+        got = engine.download(engine.reduce(a, op, axis))
+        want = orc.reduce(x, op, axis)
+        scale = absx if op == R_SUM else absx / n
+        assert got.shape == want.shape
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("shape", [(3, 5), (64, 10), (300, 700)])
+@pytest.mark.parametrize("axis", [AXIS_ROWS, AXIS_COLS])
+def test_max_min_exact(engine, shape, axis):
+    x = rnd(*shape)
+    x[0, 0] = np.nan
+    a = engine.upload(x)
+    for op in (R_MAX, R_MIN):
+        same_bits(engine.download(engine.reduce(a, op, axis)), orc.reduce(x, op, axis))
+
+
+def test_reduce_all(engine):
+    x = rnd(333, 777)
+    a = engine.upload(x)
+    tol = 1e-5 * np.abs(x.astype(np.float64)).sum()
+    got = engine.download(engine.reduce_all(a, R_SUM))[0, 0]
+    assert abs(float(got) - float(orc.reduce_all(x, R_SUM))) <= tol
+    got = engine.download(engine.reduce_all(a, R_MEAN))[0, 0]
+    assert abs(float(got) - float(orc.reduce_all(x, R_MEAN))) <= tol / x.size
+    same_bits(engine.download(engine.reduce_all(a, R_MAX)).ravel(), np.array([orc.reduce_all(x, R_MAX)]))
+
+
+def test_bf16_reduce(engine):
+    x = orc.to_bf16(rnd(100, 300))
+    a = engine.upload_bf16(x)
+    xf = orc.from_bf16(x)
+    got = engine.download(engine.reduce(a, R_SUM, AXIS_COLS))
+    tol = 1e-5 * np.abs(xf.astype(np.float64)).sum(axis=1, keepdims=True)
+    assert np.all(np.abs(got - orc.reduce(xf, R_SUM, AXIS_COLS)) <= tol)
+
+
+# --------------------------------------------------------------------- softmax
+@pytest.mark.parametrize("cols", [1, 10, 64, 128, 640, 1000, 8192, 9000])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax(engine, cols, log):
+    x = rnd(17, cols, scale=3.0)
+    a = engine.upload(x)
+    got = engine.download(engine.softmax_rows(a, log=log))
+    want = orc.softmax_rows(x, log=log)
+    close(got, want, rtol=1e-5, atol=1e-6 if log else 1e-12)
+    if not log:
+        assert np.allclose(got.sum(axis=1), 1.0, atol=cols * 6e-8 + 1e-6)
+
+
+def test_softmax_masked_scaled(engine):
+    R, C = 36, 200
+    x = rnd(R, C)
+    mask = (RNG.random((12, C)) < 0.4).astype(np.uint32)
+    mask[3, :] = 1  # a fully masked row gives zeros
+    a, m = engine.upload(x), engine.upload_bool(mask)
+    got = engine.download(engine.softmax_rows(a, m, scale=0.125))
+    want = orc.softmax_rows(x, mask=mask, scale=0.125)
+    close(got, want, rtol=1e-5, atol=1e-12)
+    assert np.all(got[3] == 0.0) and np.all(got[15] == 0.0)
+
+
+def test_softmax_shift_invariance(engine):
+    x = rnd(8, 512)
+    a, b = engine.upload(x), engine.upload(x + np.float32(4.0))
+    close(engine.download(engine.softmax_rows(a)), engine.download(engine.softmax_rows(b)), rtol=5e-6, atol=1e-12)
+
+
+# ----------------------------------------------------------------------- norms
+@pytest.mark.parametrize("cols", [64, 576, 1000])
+def test_rms_norm(engine, cols):
+    x, g = rnd(50, cols), rnd(1, cols)
+    a, gb = engine.upload(x), engine.upload(g)
+    close(engine.download(engine.rms_norm(a, gb, 1e-5)), orc.rms_norm(x, g, 1e-5), rtol=1e-5, atol=1e-7)
+    close(engine.download(engine.rms_norm(a, 0, 1e-5)), orc.rms_norm(x, None, 1e-5), rtol=1e-5, atol=1e-7)
+
+
+def test_layer_norm(engine):
+    x, g, b = rnd(64, 256), rnd(1, 256), rnd(1, 256)
+    ids = [engine.upload(v) for v in (x, g, b)]
+    close(engine.download(engine.layer_norm(*ids, eps=1e-5)), orc.layer_norm(x, g, b, 1e-5), rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------ products
+def mm_tol(a, b, ta, tb, rel):
+    aa = np.abs(a.T if ta else a).astype(np.float64)
+    bb = np.abs(b.T if tb else b).astype(np.float64)
+    return rel * (aa @ bb)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("mnk", [(64, 128, 784), (64, 10, 128), (100, 70, 33), (256, 256, 256), (1, 576, 1536),
+                                 (513, 129, 77)])
+def test_matmul_f32(engine, ta, tb, mnk):
+    m, n, k = mnk
+    a = rnd(k, m) if ta else rnd(m, k)
+    b = rnd(n, k) if tb else rnd(k, n)
+    ia, ib = engine.upload(a), engine.upload(b)
+    got = engine.download(engine.matmul_dram(ia, ta, ib, tb))
+    want = orc.matmul(a, b, ta, tb)
+    assert got.shape == (m, n)
+    assert np.all(np.abs(got - want) <= mm_tol(a, b, ta, tb, 1e-5) + 1e-30)
+
+
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("mnk", [(512, 512, 512), (256, 512, 192), (128, 64, 64), (100, 70, 33), (1, 576, 1536),
+                                 (2048, 256, 1024)])
+def test_matmul_bf16(engine, ta, tb, mnk):
+    m, n, k = mnk
+    a = rnd(k, m) if ta else rnd(m, k)
+    b = rnd(n, k) if tb else rnd(k, n)
+    ab, bb = orc.to_bf16(a), orc.to_bf16(b)
+    ia, ib = engine.upload_bf16(ab), engine.upload_bf16(bb)
+    got = engine.download(engine.matmul_dram(ia, ta, ib, tb))
+    af, bf = orc.from_bf16(ab), orc.from_bf16(bb)
+    # Against the oracle fed the same BF16 values: exact products, F32 accumulation.
+    assert np.all(np.abs(got - orc.matmul(af, bf, ta, tb)) <= mm_tol(af, bf, ta, tb, 1e-5) + 1e-30)
+    # Against the unrounded F32 product: the north star's rel 2e-2 (normwise).
+    assert np.all(np.abs(got - orc.matmul(a, b, ta, tb)) <= mm_tol(a, b, ta, tb, 2e-2))
+
+
+def test_matmul_bf16_out(engine):
+    a, b = rnd(256, 128), rnd(128, 384)
+    ab, bb = orc.to_bf16(a), orc.to_bf16(b)
+    out = engine.matmul_dram(engine.upload_bf16(ab), False, engine.upload_bf16(bb), False, BF16)
+    got = miburn.bf16_to_f32(engine.download(out))
+    want = orc.from_bf16(orc.to_bf16(orc.matmul(orc.from_bf16(ab), orc.from_bf16(bb))))
+    close(got, want, rtol=2 ** -7, atol=1e-30)
+
+
+def test_matmul_mixed_f32_bf16(engine):
+    a, b = rnd(64, 96), orc.to_bf16(rnd(96, 48))
+    got = engine.download(engine.matmul_dram(engine.upload(a), False, engine.upload_bf16(b), False))
+    bf = orc.from_bf16(b)
+    assert np.all(np.abs(got - orc.matmul(a, bf)) <= mm_tol(a, bf, False, False, 1e-5) + 1e-30)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_matmul_integer_exact_big(engine, dtype):
+    """The reference's step11 trick: small-integer operands make every
+    summation order exact, so the device must equal the float64 product bit
+    for bit -- at the 256x256-tile kernel's size (128 tiles)."""
+    n = 2048 if dtype == "bf16" else 1024
+    a = RNG.integers(-4, 5, (n, n)).astype(np.float32)
+    b = RNG.integers(-4, 5, (n, n)).astype(np.float32)
+    if dtype == "bf16":
+        ia, ib = engine.upload_bf16(orc.to_bf16(a)), engine.upload_bf16(orc.to_bf16(b))
+    else:
+        ia, ib = engine.upload(a), engine.upload(b)
+    for ta, tb in ((False, False), (False, True), (True, False), (True, True)):
+        got = engine.download(engine.matmul_dram(ia, ta, ib, tb))
+        want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+        same_bits(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("bcast", ["none", "a", "b"])
+def test_matmul_batched(engine, bcast):
+    batch, m, k, n = 6, 64, 48, 80
+    a = rnd(1 if bcast == "a" else batch, m, k)
+    b = rnd(1 if bcast == "b" else batch, k, n)
+    ia, ib = engine.upload(a.reshape(-1, k)), engine.upload(b.reshape(-1, n))
+    got = engine.download(engine.matmul_dram_batched(ia, False, ib, False, batch, m, k, n)).reshape(batch, m, n)
+    for z in range(batch):
+        az, bz = a[0 if bcast == "a" else z], b[0 if bcast == "b" else z]
+        assert np.all(np.abs(got[z] - orc.matmul(az, bz)) <= mm_tol(az, bz, False, False, 1e-5) + 1e-30)
+
+
+def test_matmul_batched_bf16_transposed(engine):
+    batch, m, k, n = 16, 128, 64, 128
+    a = orc.to_bf16(rnd(batch, m, k))
+    b = orc.to_bf16(rnd(batch, n, k))  # B transposed: items [n, k]
+    got = engine.download(engine.matmul_dram_batched(engine.upload_bf16(a.reshape(-1, k)), False,
+                                                     engine.upload_bf16(b.reshape(-1, k)), True, batch, m, k, n))
+    got = got.reshape(batch, m, n)
+    af, bf = orc.from_bf16(a), orc.from_bf16(b)
+    for z in range(batch):
+        want = orc.matmul(af[z], bf[z], False, True)
+        assert np.all(np.abs(got[z] - want) <= mm_tol(af[z], bf[z], False, True, 1e-5) + 1e-30)
+
+
+def test_matmul_shape_error(engine):
+    ia, ib = engine.upload(rnd(4, 5)), engine.upload(rnd(6, 7))
+    with pytest.raises(miburn.MiError) as e:
+        engine.matmul_dram(ia, False, ib, False)
+    assert e.value.kind == "ARG"
+
+
+# -------------------------------------------------------------------- indexing
+def special_table(rows, cols):
+    t = rnd(rows, cols)
+    flat = t.ravel()
+    flat[:6] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40]
+    bits = t.view(np.uint32).copy()
+    bits.ravel()[6] = 0x7FC0BEEF  # a NaN payload
+    return bits
+
+
+def test_select_rows_bits(engine):
+    V, D = 1000, 576
+    bits = special_table(V, D)
+    idx = RNG.integers(0, V, (3, 700)).astype(np.int32)
+    idx[0, 0] = 0
+    t = engine.upload_bits(bits, F32)
+    out = engine.select_rows(t, engine.upload_i32(idx))
+    same_bits(engine.download(out).view(np.uint32), orc.select_rows(bits, idx))
+
+
+@pytest.mark.parametrize("D", [576, 13, 2])
+def test_select_rows_widths(engine, D):
+    bits = RNG.integers(0, 2**32, (77, D), dtype=np.uint64).astype(np.uint32)
+    idx = RNG.integers(0, 77, 300).astype(np.int32)
+    got = engine.download(engine.select_rows(engine.upload_bits(bits, I32), engine.upload_i32(idx)))
+    same_bits(got.view(np.uint32), orc.select_rows(bits, idx))
+
+
+def test_select_rows_bf16(engine):
+    bits = RNG.integers(0, 2**16, (50, 64), dtype=np.uint32).astype(np.uint16)
+    idx = RNG.integers(0, 50, 99).astype(np.int32)
+    got = engine.download(engine.select_rows(engine.upload_bf16(bits), engine.upload_i32(idx)))
+    assert np.array_equal(got, bits[idx])
+
+
+def test_select_rows_out_of_range_is_domain(engine):
+    engine.sync()
+    t = engine.upload(rnd(10, 8))
+    idx = engine.upload_i32(np.array([1, 2, 10], np.int32))
+    engine.select_rows(t, idx)  # submitted: the failure is deferred
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()  # reported once, then cleared
+
+
+def test_pick_and_scatter_add_columns(engine):
+    R, C = 2048, 8192 // 8
+    bits = special_table(R, C)
+    idx = RNG.integers(0, C, R).astype(np.int32)
+    x = engine.upload_bits(bits, F32)
+    ix = engine.upload_i32(idx.reshape(R, 1))
+    same_bits(engine.download(engine.pick_columns(x, ix)).view(np.uint32), orc.pick_columns(bits, idx))
+    xf = rnd(R, C)
+    v = rnd(R, 1)
+    got = engine.download(engine.scatter_add_columns(engine.upload(xf), ix, engine.upload(v)))
+    same_bits(got, orc.scatter_add_columns(xf, idx, v))
+
+
+def test_select_add_rows_duplicates_in_order(engine):
+    V, D, n = 300, 64, 2048
+    t = rnd(V, D)
+    idx = RNG.integers(0, 40, n).astype(np.int32)  # many duplicates
+    val = rnd(n, D)
+    got = engine.download(engine.select_add_rows(engine.upload(t), engine.upload_i32(idx), engine.upload(val)))
+    same_bits(got, orc.select_add_rows(t, idx, val))
+
+
+def test_argmax_first_and_nan(engine):
+    x = rnd(40, 49152 // 16)
+    x[1, 5] = x[1, 9] = 100.0  # tie: the first wins
+    x[2, 7] = np.nan  # NaN above every number
+    x[2, 3] = np.inf
+    x[3, :] = 0.0
+    x[3, 4] = -0.0
+    got = engine.download(engine.argmax_row(engine.upload(x)))
+    assert np.array_equal(got, orc.argmax_rows(x))
+    assert got[1, 0] == 5 and got[2, 0] == 7 and got[3, 0] == 0
+
+
+def test_argmax_vocab_rows(engine):
+    x = rnd(32, 49152)
+    assert np.array_equal(engine.download(engine.argmax_row(engine.upload(x))), orc.argmax_rows(x))
+
+
+# ------------------------------------------------------------- casts, copies
+def test_cast_roundtrip_bits(engine):
+    x = rnd(64, 100)
+    x.ravel()[:5] = [np.nan, np.inf, -0.0, 1e-40, 3.0000002]
+    a = engine.upload(x)
+    h = engine.cast_float(a, BF16)
+    assert np.array_equal(engine.download(h), orc.to_bf16(x))
+    same_bits(engine.download(engine.cast_float(h, F32)), orc.from_bf16(orc.to_bf16(x)))
+
+
+def test_cast_i32_to_f32(engine):
+    v = np.array([[0, -1, 2**24 + 1, -(2**31), 2**31 - 1]], np.int32)
+    got = engine.download(engine.cast_float(engine.upload_i32(v), F32))
+    same_bits(got, v.astype(np.float32))
+
+
+def test_copy_strided_transpose_keeps_negative_zero(engine):
+    # essentials.rs:33-56: owned storage keeps -0.0 through transpose + reshape.
+    x = rnd(12, 20)
+    x[3, 4] = -0.0
+    a = engine.upload(x)
+    t = engine.copy_strided(a, 20, 12, 0, 1, 20)
+    same_bits(engine.download(t), np.ascontiguousarray(x.T))
+
+
+def test_copy_strided4_head_split(engine):
+    B, T, H, Dh = 4, 16, 4, 8
+    x = rnd(B * T, H * Dh)
+    a = engine.upload(x)
+    # [B, T, H, Dh] -> [B, H, T, Dh]
+    dims, strides = (B, H, T, Dh), (T * H * Dh, Dh, H * Dh, 1)
+    got = engine.download(engine.copy_strided4(a, dims, 0, strides))
+    same_bits(got, orc.copy_strided4(x, dims, 0, strides).view(np.float32))
+    same_bits(got, x.reshape(B, T, H, Dh).transpose(0, 2, 1, 3).reshape(-1, Dh))
+
+
+def test_assign_block(engine):
+    cache = np.zeros((64, 32), np.float32)
+    blk = rnd(5, 32)
+    c = engine.upload(cache)
+    engine.assign_block(c, engine.upload(blk), 10, 0)
+    cache[10:15] = blk
+    same_bits(engine.download(c), cache)
+
+
+# --------------------------------------------------------------------- random
+def test_random_is_seeded_and_distributed(engine):
+    a = engine.download(engine.random_dram(512, 512, miburn.DRAW_UNIT, base=7))
+    b = engine.download(engine.random_dram(512, 512, miburn.DRAW_UNIT, base=7))
+    c = engine.download(engine.random_dram(512, 512, miburn.DRAW_UNIT, base=8))
+    same_bits(a, b)
+    assert not np.array_equal(a, c)
+    assert a.min() >= 0.0 and a.max() < 1.0 and abs(a.mean() - 0.5) < 0.01
+    n = engine.download(engine.random_dram(1024, 1024, miburn.DRAW_NORMAL, 0.0, 0.02, base=3))
+    assert abs(n.mean()) < 1e-3 and abs(n.std() - 0.02) < 5e-4
+    u = engine.download(engine.random_dram(256, 256, miburn.DRAW_UNIFORM, -0.125, 0.125, base=5))
+    assert u.min() >= -0.125 and u.max() < 0.125
+    i = engine.download(engine.random_dram(100, 1000, miburn.DRAW_INT_RANGE, 0, 10, base=9))
+    assert i.dtype == np.int32 and i.min() == 0 and i.max() == 9
+
+
+# --------------------------------------------------------------------- errors
+def test_stale_id_and_report(engine):
+    a = engine.upload(rnd(4, 4))
+    engine.free(a)
+    with pytest.raises(miburn.MiError) as e:
+        engine.download(a)
+    assert e.value.kind == "ID"
+    with pytest.raises(miburn.MiError):
+        engine.eltwise_op_as("EXP", a)
+    r = engine.report()
+    assert r["uploads"] > 0 and r["ops"] > 0
