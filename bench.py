@@ -13,7 +13,9 @@ against MI355X's dense BF16 peak), and the CPU baseline (the oracle's F32
 product timed on this host's cores on a bounded 1024^3 sample).
 
 Flags: --gpus N (only 1: this build runs on one GPU), --steps K, --warmup W,
---n (cube size, default 4096), --dtype bf16|f32, --no-cpu.
+--n (cube size, default 4096), --dtype bf16|f32, --no-cpu.  `--suite` instead
+prints one JSON line per kernel of the HBM-bound suite (BASELINE.json
+configs[2]) and the matmul sweep, each against its roofline.
 """
 from __future__ import annotations
 
@@ -56,6 +58,88 @@ def cpu_baseline(n: int = 1024) -> dict:
             "sample": f"oracle F32 product {n}^3 (k-ascending F32 accumulation, OpenMP rows), {reps} reps in {el:.2f} s"}
 
 
+def _time_op(eng, fn, reps: int, warm: int = 3) -> float:
+    """Average device time (ms) of `fn` (which returns an id to free), from
+    HIP events on the engine's stream."""
+    for _ in range(warm):
+        eng.free(fn())
+    eng.sync()
+    eng.event_record(2)
+    ids = [fn() for _ in range(reps)]
+    eng.event_record(3)
+    ms = eng.event_elapsed_ms(2, 3) / reps
+    for i in ids:
+        eng.free(i)
+    return ms
+
+
+def suite(steps: int) -> int:
+    """HBM-bound kernels on [8192, 8192] F32 and the
+    matmul cube sweep: one JSON line per kernel."""
+    import miburn
+    eng = miburn.Engine(0)
+    R = C = 8192
+    n = R * C
+    x = eng.random_dram(R, C, miburn.DRAW_NORMAL, 0.0, 1.0, base=21)
+    y = eng.random_dram(R, C, miburn.DRAW_NORMAL, 0.0, 1.0, base=22)
+    reps = max(5, steps // 10)
+    lines = []
+
+    def hbm(name, fn, nbytes):
+        ms = _time_op(eng, fn, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        lines.append({"kernel": name, "config": "f32 [8192, 8192]" if "gather" not in name else
+                      "table [49152, 576] f32, 65536 ids", "ms": round(ms, 5), "bytes": nbytes,
+                      "achieved_GBs": round(gbs, 1), "peak_GBs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4)})
+
+    hbm("add", lambda: eng.eltwise_op_as("ADD", x, y), 12 * n)
+    hbm("mul", lambda: eng.eltwise_op_as("MUL", x, y), 12 * n)
+    for k in ("EXP", "GELU", "SILU"):
+        hbm(k.lower(), lambda k=k: eng.eltwise_op_as(k, x), 8 * n)
+    hbm("rsqrt(|x|+1e-6) fused", lambda: eng.eltwise_op_as("RSQRT_ABS_ADD", x, scalar=1e-6), 8 * n)
+    hbm("row softmax", lambda: eng.softmax_rows(x), 8 * n)
+    hbm("row sum (dim 1)", lambda: eng.reduce(x, miburn.R_SUM, miburn.AXIS_COLS), 4 * n + 4 * R)
+    hbm("row mean (dim 1)", lambda: eng.reduce(x, miburn.R_MEAN, miburn.AXIS_COLS), 4 * n + 4 * R)
+    hbm("column sum (dim 0)", lambda: eng.reduce(x, miburn.R_SUM, miburn.AXIS_ROWS), 4 * n + 4 * C)
+    hbm("column mean (dim 0)", lambda: eng.reduce(x, miburn.R_MEAN, miburn.AXIS_ROWS), 4 * n + 4 * C)
+    eng.free(x)
+    eng.free(y)
+    table = eng.random_dram(49152, 576, miburn.DRAW_NORMAL, 0.0, 1.0, base=23)
+    ids = eng.random_dram(1, 65536, miburn.DRAW_INT_RANGE, 0, 49152, base=24)
+    hbm("embedding gather", lambda: eng.select_rows(table, ids), 2 * 65536 * 576 * 4 + 65536 * 4)
+    for line in lines:
+        print(json.dumps(line), flush=True)
+
+    for dt in ("bf16", "f32"):
+        for m in (512, 1024, 2048, 4096, 8192):
+            a = eng.random_dram(m, m, miburn.DRAW_NORMAL, 0.0, 1.0, base=31)
+            b = eng.random_dram(m, m, miburn.DRAW_NORMAL, 0.0, 1.0, base=32)
+            if dt == "bf16":
+                a2, b2 = eng.cast_float(a, miburn.BF16), eng.cast_float(b, miburn.BF16)
+                eng.free(a)
+                eng.free(b)
+                a, b = a2, b2
+            r = max(3, min(reps, int(2e12 / (2 * m ** 3)) + 3))
+            ms = _time_op(eng, lambda: eng.matmul_dram(a, False, b, False), r)
+            tf = 2 * m ** 3 / (ms * 1e-3) / 1e12
+            print(json.dumps({"kernel": f"matmul {dt}", "config": f"{m}^3 NN", "ms": round(ms, 5),
+                              "achieved_TFLOPs": round(tf, 1), "peak_TFLOPs": PEAK_TFLOPS[dt],
+                              "frac": round(tf / PEAK_TFLOPS[dt], 4)}), flush=True)
+            eng.free(a)
+            eng.free(b)
+        a = eng.random_dram(16 * 512, 512, miburn.DRAW_NORMAL, 0.0, 1.0, base=33)
+        b = eng.random_dram(16 * 512, 512, miburn.DRAW_NORMAL, 0.0, 1.0, base=34)
+        if dt == "bf16":
+            a, b = eng.cast_float(a, miburn.BF16), eng.cast_float(b, miburn.BF16)
+        ms = _time_op(eng, lambda: eng.matmul_dram_batched(a, False, b, False, 16, 512, 512, 512), reps)
+        tf = 16 * 2 * 512 ** 3 / (ms * 1e-3) / 1e12
+        print(json.dumps({"kernel": f"batched matmul {dt}", "config": "[16,512,512]x[16,512,512]",
+                          "ms": round(ms, 5), "achieved_TFLOPs": round(tf, 1), "peak_TFLOPs": PEAK_TFLOPS[dt],
+                          "frac": round(tf / PEAK_TFLOPS[dt], 4)}), flush=True)
+    eng.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -64,11 +148,14 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--suite", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(sharding is described in DESIGN.md, not run)", file=sys.stderr)
         return 2
+    if args.suite:
+        return suite(args.steps)
 
     import miburn
     eng = miburn.Engine(0)

@@ -100,7 +100,9 @@ __device__ __forceinline__ float op(float a, float b, float c, float s1, float s
   else if constexpr (K == MI_K_MASK_FILL) return b != 0.0f ? s1 : a;
   else if constexpr (K == MI_K_MASK_WHERE) return b != 0.0f ? c : a;
   else if constexpr (K == MI_K_FILL) return s1;
-  else if constexpr (K == MI_K_SQRT) return __fsqrt_rn(a);
+  // Correctly rounded: the F64 root of an F32 rounded to F32 (double rounding
+  // is innocuous for sqrt when 53 >= 2 * 24 + 2, Figueroa 1995).
+  else if constexpr (K == MI_K_SQRT) return static_cast<float>(__dsqrt_rn(static_cast<double>(a)));
   else if constexpr (K == MI_K_RSQRT) return __fdiv_rn(1.0f, __fsqrt_rn(a));
   else if constexpr (K == MI_K_LOG1P) return log1pf(a);
   else if constexpr (K == MI_K_POW) return powf(a, b);

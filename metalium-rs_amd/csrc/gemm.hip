@@ -114,7 +114,10 @@ struct TileLoader {
   static_assert(ROWS % CH == 0, "tile rows a multiple of the chunk");
   Chunk reg[NREG];
 
-  // Load the k-tile starting at k0 for tile rows starting at r0.
+  // Issue the global loads of the k-tile starting at k0 for tile rows
+  // starting at r0.  The chunks stay raw in registers; a transposition (if
+  // any) waits for `store`, so the loads' latency overlaps the MFMAs issued
+  // between the two calls.
   __device__ __forceinline__ void load(const S *src, int64_t ld, int64_t r0, int64_t k0, int64_t rows_total,
                                        int64_t k_total, int tid) {
     if constexpr (KCONTIG) {
@@ -143,44 +146,28 @@ struct TileLoader {
         const int q = tid + b * NT;
         if (!BLK_EVEN && q >= TOTAL_BLKS) break;
         const int kb = q % KCH, rb = q / KCH;
-        Chunk in[CH];
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
           const int64_t gk = k0 + kb * CH + i, gr = r0 + rb * CH;
           const S *p = src + gk * ld + gr;
+          Chunk &in = reg[b * CH + i];
           if constexpr (GUARD) {
             int valid = (gk < k_total) ? static_cast<int>(rows_total - gr) : 0;
             valid = valid < 0 ? 0 : (valid > CH ? CH : valid);
             if (valid == CH && ((reinterpret_cast<uintptr_t>(p) & (sizeof(S) * CH - 1)) == 0))
-              in[i] = load_chunk<T, S>(p);
+              in = load_chunk<T, S>(p);
             else
-              in[i] = load_chunk_guard<T, S>(p, valid);
+              in = load_chunk_guard<T, S>(p, valid);
           } else {
-            in[i] = load_chunk<T, S>(p);
+            in = load_chunk<T, S>(p);
           }
-        }
-        // Transpose the CH x CH block: out[j] holds k = 0..CH-1 of row j.
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          Chunk o;
-          if constexpr (sizeof(T) == 2) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-              const uint32_t lo = reinterpret_cast<const uint32_t *>(&in[2 * m].u)[j >> 1];
-              const uint32_t hi = reinterpret_cast<const uint32_t *>(&in[2 * m + 1].u)[j >> 1];
-              reinterpret_cast<uint32_t *>(&o.u)[m] =
-                  (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-            }
-          } else {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) o.f[m] = in[m].f[j];
-          }
-          reg[b * CH + j] = o;
         }
       }
     }
   }
 
+  // Write the loaded k-tile to LDS (transposing CH x CH blocks of an m/n-
+  // contiguous operand so that every LDS row holds k-contiguous chunks).
   __device__ __forceinline__ void store(char *lds, int tid) const {
     if constexpr (KCONTIG) {
 #pragma unroll
@@ -196,9 +183,25 @@ struct TileLoader {
         const int q = tid + b * NT;
         if (!BLK_EVEN && q >= TOTAL_BLKS) break;
         const int kb = q % KCH, rb = q / KCH;
+        const Chunk *in = &reg[b * CH];
+        // out[j] holds k = 0..CH-1 of row j.
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
-          *reinterpret_cast<uint4 *>(lds + lds_off(rb * CH + j, kb)) = reg[b * CH + j].u;
+        for (int j = 0; j < CH; ++j) {
+          Chunk o;
+          if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const uint32_t lo = reinterpret_cast<const uint32_t *>(&in[2 * m].u)[j >> 1];
+              const uint32_t hi = reinterpret_cast<const uint32_t *>(&in[2 * m + 1].u)[j >> 1];
+              reinterpret_cast<uint32_t *>(&o.u)[m] =
+                  (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) o.f[m] = in[m].f[j];
+          }
+          *reinterpret_cast<uint4 *>(lds + lds_off(rb * CH + j, kb)) = o.u;
+        }
       }
     }
   }
@@ -232,7 +235,7 @@ __device__ __forceinline__ void tile_of(int w, int tiles_m, int tiles_n, int *tm
 }
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC,
-          bool GUARD>
+          bool GUARD, int STORE_AT = 3>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   constexpr int NT = WM * WN * 64;
   constexpr int BK = 128 / sizeof(T);
@@ -273,6 +276,36 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   __syncthreads();
 
   const int lrow = lane & 31, lhalf = lane >> 5;
+  // Fragment registers, double-buffered over the four chunk pairs of a
+  // k-tile: the reads for pair p + 1 are issued before the MFMAs of pair p.
+  Chunk fa[2][TM], fb[2][TN];
+  auto read_frags = [&](const char *a_s, const char *b_s, int p, int buf) {
+    const int c = 2 * p + lhalf;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i].u = *reinterpret_cast<const uint4 *>(a_s + lds_off(wm * WTM + i * 32 + lrow, c));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[buf][j].u = *reinterpret_cast<const uint4 *>(b_s + lds_off(wn * WTN + j * 32 + lrow, c));
+  };
+  auto mfmas = [&](int buf) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[buf][i].u),
+                                                              __builtin_bit_cast(bf16x8, fb[buf][j].u), acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[buf][i].f[e], fb[buf][j].f[e], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  read_frags(smem, smem + A_BYTES, 0, 0);
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < ktiles;
@@ -282,38 +315,20 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
     }
     const char *a_s = smem + cur * STAGE;
     const char *b_s = a_s + A_BYTES;
-    // Four pairs of 16-byte chunks per 128-byte row; the half-waves take the
-    // two chunks of a pair.
+    char *nxt = smem + (cur ^ 1) * STAGE;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const int c = 2 * p + lhalf;
-      Chunk fa[TM], fb[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i].u = *reinterpret_cast<const uint4 *>(a_s + lds_off(wm * WTM + i * 32 + lrow, c));
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j].u = *reinterpret_cast<const uint4 *>(b_s + lds_off(wn * WTN + j * 32 + lrow, c));
-      if constexpr (sizeof(T) == 2) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i].u),
-                                                                __builtin_bit_cast(bf16x8, fb[j].u), acc[i][j], 0, 0, 0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].f[e], fb[j].f[e], acc[i][j], 0, 0, 0);
+      if (p < 3) read_frags(a_s, b_s, p + 1, (p + 1) & 1);
+      mfmas(p & 1);
+      // The other stage was last read before the previous barrier: the next
+      // tile may be written into it while this one is still being consumed.
+      if (p == STORE_AT && more) {
+        la.store(nxt, tid);
+        lb.store(nxt + A_BYTES, tid);
       }
     }
-    if (more) {
-      la.store(smem + (cur ^ 1) * STAGE, tid);
-      lb.store(smem + (cur ^ 1) * STAGE + A_BYTES, tid);
-    }
     __syncthreads();
+    if (more) read_frags(nxt, nxt + A_BYTES, 0, 0);
   }
 
   // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
@@ -344,11 +359,12 @@ struct Plan {
   int64_t sa, sb, sc;
 };
 
-template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD>
+template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
+          int STORE_AT = 3>
 static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   constexpr int NT = WM * WN * 64;
   constexpr int SMEM = 2 * (BM + BN) * 128;
-  auto kern = gemm_kernel<T, SA, SB, TO, BM, BN, WM, WN, AK, BKC, GUARD>;
+  auto kern = gemm_kernel<T, SA, SB, TO, BM, BN, WM, WN, AK, BKC, GUARD, STORE_AT>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
