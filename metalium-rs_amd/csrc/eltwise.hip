@@ -149,31 +149,55 @@ __device__ __forceinline__ float4 load4(const Opnd &o, int64_t flat, int64_t col
   }
 }
 
+// Each thread owns EW_UNROLL float4 lanes spaced a block apart, issuing all
+// its loads before any arithmetic so that several 16-byte reads per lane are
+// in flight.
+constexpr int EW_UNROLL = 4;
+
+__device__ __forceinline__ void store4(void *out, int out_elem, int64_t flat, float4 r) {
+  if (out_elem == MI_F32) {
+    *reinterpret_cast<float4 *>(static_cast<float *>(out) + flat) = r;
+  } else if (out_elem == MI_BF16) {
+    uint2 h;
+    h.x = uint32_t(f32_to_bf16_bits(r.x)) | (uint32_t(f32_to_bf16_bits(r.y)) << 16);
+    h.y = uint32_t(f32_to_bf16_bits(r.z)) | (uint32_t(f32_to_bf16_bits(r.w)) << 16);
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = h;
+  } else {
+    uint4 m = make_uint4(r.x != 0.f, r.y != 0.f, r.z != 0.f, r.w != 0.f);
+    *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(out) + flat) = m;
+  }
+}
+
 template <uint32_t K, int NIN>
 __global__ void __launch_bounds__(256) ew_vec4(Opnd a, Opnd b, Opnd c, float s1, float s2,
                                                void *out, int out_elem, int64_t n4, int64_t cols) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < n4; v += stride) {
-    const int64_t flat = v * 4;
-    float4 x = load4(a, flat, cols);
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f), z = y;
-    if constexpr (NIN >= 2) y = load4(b, flat, cols);
-    if constexpr (NIN >= 3) z = load4(c, flat, cols);
-    float4 r;
-    r.x = op<K>(x.x, y.x, z.x, s1, s2);
-    r.y = op<K>(x.y, y.y, z.y, s1, s2);
-    r.z = op<K>(x.z, y.z, z.z, s1, s2);
-    r.w = op<K>(x.w, y.w, z.w, s1, s2);
-    if (out_elem == MI_F32) {
-      *reinterpret_cast<float4 *>(static_cast<float *>(out) + flat) = r;
-    } else if (out_elem == MI_BF16) {
-      uint2 h;
-      h.x = uint32_t(f32_to_bf16_bits(r.x)) | (uint32_t(f32_to_bf16_bits(r.y)) << 16);
-      h.y = uint32_t(f32_to_bf16_bits(r.z)) | (uint32_t(f32_to_bf16_bits(r.w)) << 16);
-      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = h;
-    } else {
-      uint4 m = make_uint4(r.x != 0.f, r.y != 0.f, r.z != 0.f, r.w != 0.f);
-      *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(out) + flat) = m;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * EW_UNROLL) + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * (256 * EW_UNROLL);
+  for (int64_t v0 = base; v0 < n4; v0 += stride) {
+    float4 x[EW_UNROLL], y[EW_UNROLL], z[EW_UNROLL];
+#pragma unroll
+    for (int u = 0; u < EW_UNROLL; ++u) {
+      const int64_t v = v0 + u * 256;
+      if (v < n4) {
+        x[u] = load4(a, v * 4, cols);
+        if constexpr (NIN >= 2) y[u] = load4(b, v * 4, cols);
+        if constexpr (NIN >= 3) z[u] = load4(c, v * 4, cols);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < EW_UNROLL; ++u) {
+      const int64_t v = v0 + u * 256;
+      if (v < n4) {
+        float4 yy = make_float4(0.f, 0.f, 0.f, 0.f), zz = yy;
+        if constexpr (NIN >= 2) yy = y[u];
+        if constexpr (NIN >= 3) zz = z[u];
+        float4 r;
+        r.x = op<K>(x[u].x, yy.x, zz.x, s1, s2);
+        r.y = op<K>(x[u].y, yy.y, zz.y, s1, s2);
+        r.z = op<K>(x[u].z, yy.z, zz.z, s1, s2);
+        r.w = op<K>(x[u].w, yy.w, zz.w, s1, s2);
+        store4(out, out_elem, v * 4, r);
+      }
     }
   }
 }
@@ -245,7 +269,7 @@ static void launch_kind(bool fast, int nin, const Opnd &a, const Opnd &b, const 
   const int threads = 256;
   if (fast) {
     const int64_t n4 = n / 4;
-    unsigned g = grid_for(n4, threads * 4, 256 * 32);
+    unsigned g = grid_for(n4, threads * EW_UNROLL, 256 * 64);
     if (nin == 1) ew_vec4<K, 1><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
     else if (nin == 2) ew_vec4<K, 2><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
     else ew_vec4<K, 3><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);

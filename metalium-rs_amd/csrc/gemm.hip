@@ -349,6 +349,261 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   }
 }
 
+// ------------------------------------------- BF16: HBM -> LDS direct path
+// The BF16 kernel for exactly tiled shapes.  Operand tiles move from HBM to
+// LDS with `global_load_lds_dwordx4` (each lane's 16 bytes land at
+// base + 16 * lane), so no staging registers and no LDS store instructions
+// are spent on them, and the next k-tile streams in while the current one is
+// multiplied.  An operand whose k is contiguous keeps the swizzled 128-byte
+// rows above; one whose m/n is contiguous is stored as it lies, [k][rows], and
+// its MFMA fragments are read with `ds_read_b64_tr_b16`, which hands lane j of
+// each 16-lane group element j % 4 of the 8 bytes that lane 4 t + j / 4 of the
+// group addressed (t = 0..3): lane i addressing row k0 + i / 4, columns
+// n0 + 4 (i % 4) .. + 3 gives lane j the four k of column n0 + j.  Chunk c of
+// row k of such a tile is stored at chunk c ^ (4 (k % 4)), so the 16 rows x 64
+// bytes a transposed fragment read touches cover all 64 banks.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+template <int ROWS, bool KCONTIG, int BK>
+struct DmaOperand {
+  static constexpr int BYTES = ROWS * BK * 2;  // tile bytes (ROWS x BK BF16)
+  static constexpr int BLOCKS = BYTES / 1024;
+  static constexpr int READS = KCONTIG ? 1 : 2;  // LDS reads per fragment
+  // k-contiguous tiles: RB-byte rows of CPR 16-byte chunks, chunk c of row r
+  // stored at c ^ swz(r) -- for 128-byte rows r & 7, for 64-byte rows
+  // (r / 4) & 3 -- so 32 rows at one logical chunk spread over all banks.
+  static constexpr int RB = KCONTIG ? 2 * BK : 2 * ROWS;
+  static constexpr int CPR = RB / 16;
+  static constexpr int RPB = 1024 / RB;  // rows per 1 KiB block
+  static_assert(BK == 32 || BK == 64, "k tile");
+  static_assert(KCONTIG || ROWS >= 128, "transposed-read swizzle needs rows of 16+ chunks");
+  __device__ __forceinline__ static int swz(int r) {
+    if constexpr (BK == 64) return r & 7;
+    else return (r >> 2) & 3;
+  }
+
+  // Issue this wave's share of the tile's 1 KiB blocks.  Each address is a
+  // wave-uniform block base (SGPRs) plus one 32-bit per-lane byte offset.
+  // The instruction is written out (with M0, its LDS base, set just before)
+  // rather than left to the compiler, which would otherwise wait for every
+  // DMA still in flight before any later LDS read; the kernel counts its own
+  // DMA instead (wait_vmcnt before each barrier, and 0 before it ends).
+  template <int NW>
+  __device__ __forceinline__ static void load(const uint16_t *src, int64_t ld, int64_t r0, int64_t k0, char *lds,
+                                              int wave, int lane) {
+    static_assert(BLOCKS % NW == 0, "blocks per wave");
+    const int lr = (lane * 16) / RB;          // row of this lane within its block
+    const int pch = ((lane * 16) % RB) >> 4;  // physical chunk it fills
+    uint32_t voff;
+    int64_t base_off, ustep;  // bytes
+    if constexpr (KCONTIG) {
+      // Block b covers rows RPB b .. RPB b + RPB - 1 (RPB a multiple of 8 or
+      // 16), so swz(row) = swz(lr).
+      const int c = pch ^ swz(lr);
+      voff = static_cast<uint32_t>((lr * ld + c * 8) * 2);
+      base_off = ((r0 + RPB * wave) * ld + k0) * 2;
+    } else {
+      // k row of this lane: RPB b + lr; RPB * NW is a multiple of 4, so
+      // k % 4 = (RPB wave + lr) % 4 for every block this wave loads.
+      const int kq = (RPB * wave + lr) & 3;
+      const int c = pch ^ (4 * kq);
+      voff = static_cast<uint32_t>((lr * ld + c * 8) * 2);
+      base_off = ((k0 + RPB * wave) * ld + r0) * 2;
+    }
+    ustep = static_cast<int64_t>(RPB) * NW * ld * 2;
+    const char *base = reinterpret_cast<const char *>(src) + base_off;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(lds)));
+#pragma unroll
+    for (int i = 0; i < BLOCKS / NW; ++i) {
+      const int b = i * NW + wave;
+      const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds0 + b * 1024);
+      const char *gb = reinterpret_cast<const char *>(
+          __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>(base + i * ustep))) & 0xffffffffu |
+          (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(
+               static_cast<int>(reinterpret_cast<uintptr_t>(base + i * ustep) >> 32)))
+           << 32));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :
+                   : "s"(m0v), "v"(voff), "s"(gb)
+                   : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+  }
+
+  // The 8 BF16 of lane `lane` for the 32-row fragment at `row0`, k step p.
+  __device__ __forceinline__ static uint4 frag(const char *lds, int row0, int p, int lane) {
+    if constexpr (KCONTIG) {
+      const int r = row0 + (lane & 31);
+      const int c = 2 * p + (lane >> 5);
+      return *reinterpret_cast<const uint4 *>(lds + r * RB + ((c ^ swz(r)) << 4));
+    } else {
+      const int i = lane & 15;
+      const int nhalf = (lane >> 4) & 1, kg = lane >> 5;
+      const int n = row0 + 16 * nhalf + 4 * (i & 3);
+      const int kbase = p * 16 + kg * 8 + (i >> 2);
+      uint4 out;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = kbase + 4 * h;
+        const int pch = (n >> 3) ^ (4 * (k & 3));
+        const char *addr = lds + k * RB + pch * 16 + ((n & 7) >> 2) * 8;
+        v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(addr));
+        if (h == 0) { out.x = __builtin_bit_cast(uint2, v).x; out.y = __builtin_bit_cast(uint2, v).y; }
+        else { out.z = __builtin_bit_cast(uint2, v).x; out.w = __builtin_bit_cast(uint2, v).y; }
+      }
+      return out;
+    }
+  }
+};
+
+// Scheduling directive for one k step: MF MFMAs, each followed by its share
+// of the NR LDS reads of the next step (compile-time group sizes).
+template <int Q, int MF, int NR>
+__device__ __forceinline__ void interleave_mfma_reads() {
+  if constexpr (Q < MF) {
+    constexpr int per = (NR + MF - 1) / MF;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (Q * per < NR) __builtin_amdgcn_sched_group_barrier(0x100, (NR - Q * per) < per ? (NR - Q * per) : per, 0);
+    interleave_mfma_reads<Q + 1, MF, NR>();
+  }
+}
+
+// `s_waitcnt vmcnt(N)`, the other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One k-tile of the direct path on stage `cur` (a static LDS array, so that
+// the compiler's LDS alias scopes keep the other stages' in-flight DMA from
+// forcing a wait before these reads), refilling stage `nxt` -- the stage read
+// one tile ago -- with the tile at k_next.
+template <typename OA, typename OB, int BK, int NW, int TM, int TN, int WTM, int WTN, int INFLIGHT>
+__device__ __forceinline__ void dma_tile(f32x16 (&acc)[TM][TN], const char *cur, char *nxt, const uint16_t *A,
+                                         const uint16_t *B, const GemmArgs &g, int64_t m0, int64_t n0, int64_t k_next,
+                                         int wm, int wn, int wave, int lane) {
+  constexpr int PER_TILE = (OA::BLOCKS + OB::BLOCKS) / NW;  // this thread's DMA instructions per tile
+  constexpr int STEPS = BK / 16;                            // MFMA k steps per tile
+  // This thread's DMA of the current tile has landed (the INFLIGHT younger
+  // tiles' may still be in flight); the barrier makes every thread's visible
+  // and ends every wave's reads of the stage about to be refilled.
+  // A bare s_barrier: a __syncthreads() fence would wait for every DMA in
+  // flight, including the younger tiles'.  LDS reads need no fence: the
+  // wave's own reads have all returned (lgkmcnt 0) before it arrives.
+  wait_vmcnt<INFLIGHT * PER_TILE>();
+  __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00 | (0 << 8));  // lgkmcnt(0) (vmcnt field at its maximum)
+  __builtin_amdgcn_s_barrier();
+  OA::template load<NW>(A, g.lda, m0, k_next, nxt, wave, lane);
+  OB::template load<NW>(B, g.ldb, n0, k_next, nxt + OA::BYTES, wave, lane);
+  const char *a_s = cur, *b_s = cur + OA::BYTES;
+  uint4 fa[2][TM], fb[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = OA::frag(a_s, wm * WTM + i * 32, 0, lane);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[0][j] = OB::frag(b_s, wn * WTN + j * 32, 0, lane);
+  constexpr int MF = TM * TN;
+  constexpr int NR = TM * OA::READS + TN * OB::READS;  // LDS reads per k step
+#pragma unroll
+  for (int p = 0; p < STEPS; ++p) {
+    const int cb = p & 1;
+    if (p + 1 < STEPS) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[cb ^ 1][i] = OA::frag(a_s, wm * WTM + i * 32, p + 1, lane);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[cb ^ 1][j] = OB::frag(b_s, wn * WTN + j * 32, p + 1, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[cb][i]),
+                                                            __builtin_bit_cast(bf16x8, fb[cb][j]), acc[i][j], 0, 0, 0);
+    if (p + 1 < STEPS) interleave_mfma_reads<0, MF, NR>();
+  }
+}
+
+// The static LDS stage S of NS (unused stages collapse to 16 bytes).
+#define MI_DMA_STAGES(STAGE, NS)                                                            \
+  __shared__ __attribute__((aligned(1024))) char st0[STAGE];                                 \
+  __shared__ __attribute__((aligned(1024))) char st1[STAGE];                                 \
+  __shared__ __attribute__((aligned(1024))) char st2[(NS) > 2 ? (STAGE) : 16];               \
+  __shared__ __attribute__((aligned(1024))) char st3[(NS) > 3 ? (STAGE) : 16];               \
+  __shared__ __attribute__((aligned(1024))) char st4[(NS) > 4 ? (STAGE) : 16];               \
+  char *const stages[5] = {st0, st1, st2, st3, st4};
+
+template <typename TO, int BM, int BN, int BK, int NS, bool AK, bool BKC, int WM = 2, int WN = 2>
+__global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  using OA = DmaOperand<BM, AK, BK>;
+  using OB = DmaOperand<BN, BKC, BK>;
+  constexpr int STAGE = OA::BYTES + OB::BYTES;
+  static_assert(NS >= 2 && NS <= 5, "stages");
+  static_assert(NS * STAGE <= 160 * 1024, "LDS");
+  MI_DMA_STAGES(STAGE, NS)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t z = blockIdx.y;
+  const uint16_t *A = static_cast<const uint16_t *>(g.a) + z * g.sa;
+  const uint16_t *B = static_cast<const uint16_t *>(g.b) + z * g.sb;
+  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t ktiles = g.K / BK;
+  // Tiles past the last reload the last into a stage nobody reads again, so
+  // every thread issues the same number of DMA instructions per tile and the
+  // counted waits stay exact.
+  auto kclamp = [&](int64_t t) { return (t < ktiles ? t : ktiles - 1) * BK; };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+    OA::template load<NW>(A, g.lda, m0, kclamp(s), stages[s], wave, lane);
+    OB::template load<NW>(B, g.ldb, n0, kclamp(s), stages[s] + OA::BYTES, wave, lane);
+  }
+  for (int64_t kt = 0; kt < ktiles; kt += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s == 0 || kt + s < ktiles)
+        dma_tile<OA, OB, BK, NW, TM, TN, WTM, WTN, NS - 2>(acc, stages[s], stages[(s + NS - 1) % NS], A, B, g, m0, n0,
+                                                       kclamp(kt + s + NS - 1), wm, wn, wave, lane);
+    }
+  }
+  // No DMA may still be writing this workgroup's LDS when its waves end.
+  wait_vmcnt<0>();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
+        else C[row * g.ldc + col] = acc[i][j][r];
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------- launching
 struct Plan {
   int64_t M, N, K, batch;
@@ -385,6 +640,32 @@ static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename TO, int BM, int BN, int BK, int NS, bool AK, bool BKC, int WM = 2, int WN = 2>
+static hipError_t launch_dma_cfg(const Plan &p, hipStream_t st) {
+  auto kern = gemm_dma_kernel<TO, BM, BN, BK, NS, AK, BKC, WM, WN>;
+  GemmArgs g;
+  g.a = p.a; g.b = p.b; g.c = p.c;
+  g.M = p.M; g.N = p.N; g.K = p.K;
+  g.lda = p.ta ? p.M : p.K;
+  g.ldb = p.tb ? p.K : p.N;
+  g.ldc = p.N;
+  g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.tiles_m = static_cast<int>(p.M / BM);
+  g.tiles_n = static_cast<int>(p.N / BN);
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
+  kern<<<grid, WM * WN * 64, 0, st>>>(g);
+  return hipGetLastError();
+}
+
+template <typename TO, int BM, int BN, int BK, int NS, int WM = 2, int WN = 2>
+static hipError_t launch_dma(const Plan &p, hipStream_t st) {
+  const bool ak = !p.ta, bk = p.tb;
+  if (ak && bk) return launch_dma_cfg<TO, BM, BN, BK, NS, true, true, WM, WN>(p, st);
+  if (ak && !bk) return launch_dma_cfg<TO, BM, BN, BK, NS, true, false, WM, WN>(p, st);
+  if (!ak && bk) return launch_dma_cfg<TO, BM, BN, BK, NS, false, true, WM, WN>(p, st);
+  return launch_dma_cfg<TO, BM, BN, BK, NS, false, false, WM, WN>(p, st);
+}
+
 // Operand orientation: A k-contiguous unless transposed; B k-contiguous when transposed.
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool GUARD>
 static hipError_t launch_orient(const Plan &p, hipStream_t st) {
@@ -408,11 +689,15 @@ static bool tiles_exactly(const Plan &p, int bm, int bn, int bk, int64_t align_e
 template <typename TO>
 static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   using T = uint16_t;
-  const int64_t tiles256 = ((p.M + 255) / 256) * ((p.N + 255) / 256) * p.batch;
-  if (tiles256 >= 128 && tiles_exactly(p, 256, 256, 64, 8))
-    return launch_orient<T, T, T, TO, 256, 256, 2, 2, false>(p, st);
-  if (tiles_exactly(p, 128, 128, 64, 8))
-    return launch_orient<T, T, T, TO, 128, 128, 2, 2, false>(p, st);
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.batch; };
+  // Exactly tiled shapes take the direct HBM -> LDS kernel: 256 x 256 tiles
+  // (8 waves, each 128 x 64 or 64 x 128, two k-tiles of 64 in LDS) when they
+  // give most of the 256 CUs a tile, else 128 x 128 tiles (4 waves, four
+  // stages).
+  if (tiles_exactly(p, 256, 256, 64, 8) && tiles(256, 256) >= 192)
+    return p.tb ? launch_dma<TO, 256, 256, 64, 2, 4, 2>(p, st) : launch_dma<TO, 256, 256, 64, 2, 2, 4>(p, st);
+  if (tiles_exactly(p, 128, 128, 64, 8) && tiles(128, 128) >= 96)
+    return launch_dma<TO, 128, 128, 64, 4>(p, st);
   if (tiles_exactly(p, 64, 64, 64, 8))
     return launch_orient<T, T, T, TO, 64, 64, 2, 2, false>(p, st);
   return launch_orient<T, T, T, TO, 64, 64, 2, 2, true>(p, st);

@@ -109,6 +109,7 @@ __global__ void __launch_bounds__(256) reduce_rows_part(const void *x, int elem,
     const int64_t c = c0 + lane * 4;
     if (c < cols) {
       const float *p = static_cast<const float *>(x);
+#pragma unroll 8
       for (int64_t r = r_begin + w; r < r_end; r += 4) {
         float4 v = *reinterpret_cast<const float4 *>(p + r * cols + c);
         if (op == MI_R_MAX) { acc.x = max_nan(acc.x, v.x); acc.y = max_nan(acc.y, v.y); acc.z = max_nan(acc.z, v.z); acc.w = max_nan(acc.w, v.w); }
@@ -244,6 +245,102 @@ __global__ void __launch_bounds__(256) softmax_kernel(const void *x, int elem, c
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
     if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] / s);
+  }
+}
+
+// Long rows: one 256-thread block per row, the row in registers (thread t
+// holds float4 lanes t + 256 u, u < VPT, or scalars t + 256 u, u < 4 VPT),
+// cross-wave folds through LDS.
+__device__ __forceinline__ float block_max(float v, float *red) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = max_nan(max_nan(red[0], red[1]), max_nan(red[2], red[3]));
+  __syncthreads();
+  return m;
+}
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return s;
+}
+
+template <int VPT, bool VEC>
+__global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
+                                                            int64_t mask_rows, float scale, int log_mode, void *out,
+                                                            int out_elem, int64_t cols) {
+  constexpr int T = 4 * VPT;  // elements per thread
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * cols;
+  const uint32_t *mrow = mask ? mask + (row % mask_rows) * cols : nullptr;
+  const int tid = threadIdx.x;
+  float v[T];
+  auto col_of = [&](int t) -> int64_t {
+    return VEC ? (static_cast<int64_t>(tid + 256 * (t >> 2)) * 4 + (t & 3)) : static_cast<int64_t>(tid + 256 * t);
+  };
+  if constexpr (VEC) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int64_t j4 = tid + 256 * u;
+      float4 q = (j4 * 4 < cols) ? p[j4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      v[4 * u] = q.x; v[4 * u + 1] = q.y; v[4 * u + 2] = q.z; v[4 * u + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = col_of(t);
+      v[t] = j < cols ? ld(x, elem, base + j) : -INFINITY;
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = col_of(t);
+    if (j < cols) {
+      if (scale != 1.0f) v[t] = v[t] * scale;
+      if (mrow && mrow[j]) v[t] = -INFINITY;
+    }
+    m = max_nan(m, v[t]);
+  }
+  m = block_max(m, red);
+  if (mrow) m = m > -FLT_MAX ? m : (isnan(m) ? m : -FLT_MAX);
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = col_of(t);
+    const float sh = v[t] - m;
+    const float e = j < cols ? expf(sh) : 0.0f;
+    v[t] = log_mode ? sh : e;
+    s += e;
+  }
+  s = block_sum(s, red);
+  if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
+  const float ls = log_mode ? logf(s) : 0.0f;
+  if (VEC && out_elem == MI_F32) {
+    float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + base);
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int64_t j4 = tid + 256 * u;
+      if (j4 * 4 < cols) {
+        float4 r;
+        r.x = log_mode ? v[4 * u] - ls : v[4 * u] / s;
+        r.y = log_mode ? v[4 * u + 1] - ls : v[4 * u + 1] / s;
+        r.z = log_mode ? v[4 * u + 2] - ls : v[4 * u + 2] / s;
+        r.w = log_mode ? v[4 * u + 3] - ls : v[4 * u + 3] / s;
+        o[j4] = r;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = col_of(t);
+      if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] / s);
+    }
   }
 }
 
@@ -453,11 +550,27 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
   if (R > 0 && C > 0) {
     unsigned g = grid_for(R, 4, INT32_MAX);
     int t = pick_t(C);
-    switch (t) {
+    const bool vec = (xe == MI_F32) && (C % 4 == 0);
+    if (t != 0 && t <= 16) {
+      // Up to 1024 columns: a wavefront per row.
+      switch (t) {
 #define MI_SM(T) case T: softmax_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, R, C); break;
-      MI_SM(1) MI_SM(2) MI_SM(4) MI_SM(8) MI_SM(16) MI_SM(32) MI_SM(64) MI_SM(128)
+        MI_SM(1) MI_SM(2) MI_SM(4) MI_SM(8) MI_SM(16)
 #undef MI_SM
-      default: softmax_long_kernel<<<g, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, R, C);
+      }
+    } else if (C <= 16384) {
+      // A block per row: the smallest VPT with 1024 * VPT >= C.
+      int vpt = 1;
+      while (1024 * vpt < C) vpt *= 2;
+      const unsigned rows = static_cast<unsigned>(R);
+      switch (vpt) {
+#define MI_SB(V) case V: if (vec) softmax_block_kernel<V, true><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+                         else softmax_block_kernel<V, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); break;
+        MI_SB(1) MI_SB(2) MI_SB(4) MI_SB(8) MI_SB(16)
+#undef MI_SB
+      }
+    } else {
+      softmax_long_kernel<<<g, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, R, C);
     }
   }
   s = check_launch(ctx, "softmax_rows");

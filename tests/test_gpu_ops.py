@@ -242,7 +242,7 @@ def test_bf16_reduce(engine):
 
 
 # --------------------------------------------------------------------- softmax
-@pytest.mark.parametrize("cols", [1, 10, 64, 128, 640, 1000, 8192, 9000])
+@pytest.mark.parametrize("cols", [1, 10, 64, 128, 640, 1000, 1030, 8192, 9000, 20000])
 @pytest.mark.parametrize("log", [False, True])
 def test_softmax(engine, cols, log):
     x = rnd(17, cols, scale=3.0)
@@ -345,12 +345,12 @@ def test_matmul_mixed_f32_bf16(engine):
     assert np.all(np.abs(got - orc.matmul(a, bf)) <= mm_tol(a, bf, False, False, 1e-5) + 1e-30)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_matmul_integer_exact_big(engine, dtype):
+@pytest.mark.parametrize("dtype,n", [("f32", 1024), ("bf16", 1024), ("bf16", 2048), ("bf16", 4096)])
+def test_matmul_integer_exact_big(engine, dtype, n):
     """The reference's step11 trick: small-integer operands make every
     summation order exact, so the device must equal the float64 product bit
-    for bit -- at the 256x256-tile kernel's size (128 tiles)."""
-    n = 2048 if dtype == "bf16" else 1024
+    for bit -- for each kernel the shape selects (bf16: 64x64 tiles at 1024,
+    128x128 direct-to-LDS at 2048, 256x256 direct-to-LDS at 4096)."""
     a = RNG.integers(-4, 5, (n, n)).astype(np.float32)
     b = RNG.integers(-4, 5, (n, n)).astype(np.float32)
     if dtype == "bf16":
@@ -386,6 +386,32 @@ def test_matmul_batched_bf16_transposed(engine):
     for z in range(batch):
         want = orc.matmul(af[z], bf[z], False, True)
         assert np.all(np.abs(got[z] - want) <= mm_tol(af[z], bf[z], False, True, 1e-5) + 1e-30)
+
+
+@pytest.mark.parametrize("tb", [False, True])
+def test_matmul_batched_bf16_integer_exact_256_tiles(engine, tb):
+    """12 items of 1024^2 give 192 tiles of 256x256: the direct kernel's
+    batched path, exact with small-integer operands."""
+    batch, m, k, n = 12, 1024, 1024, 1024
+    a = RNG.integers(-3, 4, (batch, m, k)).astype(np.float32)
+    b = RNG.integers(-3, 4, (batch, n, k) if tb else (batch, k, n)).astype(np.float32)
+    ia = engine.upload_bf16(orc.to_bf16(a.reshape(-1, k)))
+    ib = engine.upload_bf16(orc.to_bf16(b.reshape(-1, b.shape[-1])))
+    got = engine.download(engine.matmul_dram_batched(ia, False, ib, tb, batch, m, k, n)).reshape(batch, m, n)
+    bb = b.transpose(0, 2, 1) if tb else b
+    want = np.matmul(a.astype(np.float64), bb.astype(np.float64)).astype(np.float32)
+    same_bits(got, want)
+
+
+def test_matmul_bf16_out_direct_kernel(engine):
+    a, b = rnd(4096, 512), rnd(512, 4096)
+    ab, bb = orc.to_bf16(a), orc.to_bf16(b)
+    out = engine.matmul_dram(engine.upload_bf16(ab), False, engine.upload_bf16(bb), False, BF16)
+    got = miburn.bf16_to_f32(engine.download(out))
+    af, bf = orc.from_bf16(ab), orc.from_bf16(bb)
+    want = af.astype(np.float64) @ bf.astype(np.float64)
+    tol = 2.0 ** -8 * np.abs(want) + 1e-5 * (np.abs(af).astype(np.float64) @ np.abs(bf).astype(np.float64))
+    assert np.all(np.abs(got - want) <= tol)
 
 
 def test_matmul_shape_error(engine):
