@@ -299,9 +299,11 @@ void or_softmax_rows(const float *x, int64_t R, int64_t C, const uint32_t *mask,
     for (int64_t j = 0; j < C; ++j) s += exp((double)(v[j] - m));
     float sf = (float)s;
     if (mr && !(sf > FLT_MIN) && !isnan(sf)) sf = FLT_MIN;
+    /* log_softmax's ln(sum) is an F32 tensor, subtracted in F32. */
+    const float ls = (float)log((double)sf);
     for (int64_t j = 0; j < C; ++j) {
       float sh = v[j] - m;
-      out[i * C + j] = log_mode ? (float)((double)sh - log((double)sf)) : (float)(exp((double)sh) / (double)sf);
+      out[i * C + j] = log_mode ? sh - ls : (float)(exp((double)sh) / (double)sf);
     }
   }
   free(v);

@@ -1,0 +1,265 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each check is chosen so a plausible slip in the oracle fails it: golden
+vectors computed independently in float64 numpy/scipy (tests/golden/
+make_golden.py), exact answers from small-integer products (the reference's
+step11 trick), the reference's portable known answers (signed zero through a
+transpose, crates/burn-tt/tests/essentials.rs:33-56; gather of +-0/inf/NaN
+payloads, crates/tt-tests/tests/step61_burn_gather.rs:1-13; argmax's first
+maximum and NaN rule, crates/tt-models/src/generate.rs:176-183), closed forms
+and invariants (softmax rows sum to one and ignore a shift; mean = sum / n),
+and brute-force loops on tiny inputs.  No GPU is needed.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from miburn import AXIS_COLS, AXIS_ROWS, K, R_MAX, R_MEAN, R_SUM
+
+G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_v1.npz"))
+ULP = 2.0 ** -23
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def assert_bits(a, b):
+    a, b = bits(a).ravel(), bits(b).ravel()
+    assert a.size == b.size, (a.size, b.size)
+    assert np.array_equal(a, b), np.flatnonzero(a != b)[:5]
+
+
+def assert_ulps(got, want, n_ulp):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape
+    tol = n_ulp * ULP * np.abs(want) + 1e-38
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), (np.flatnonzero(bad)[:5], got.ravel()[bad.ravel()][:3], want.ravel()[bad.ravel()][:3])
+
+
+# ------------------------------------------------------------ element-wise
+@pytest.mark.parametrize("kind,key,src,n_ulp", [
+    ("EXP", "ew_exp", "ew_x", 1), ("TANH", "ew_tanh", "ew_x", 1), ("ERF", "ew_erf", "ew_x", 1),
+    ("GELU", "ew_gelu", "ew_x", 1), ("SIGMOID", "ew_sigmoid", "ew_x", 1), ("SILU", "ew_silu", "ew_x", 2),
+    ("LOG", "ew_log", "ew_pos", 1), ("SQRT", "ew_sqrt", "ew_pos", 0), ("RSQRT", "ew_rsqrt", "ew_pos", 1),
+])
+def test_unary_against_float64_golden(kind, key, src, n_ulp):
+    got = orc.eltwise(K[kind], G[src]).ravel()
+    if n_ulp == 0:
+        assert_bits(got, G[key])
+    else:
+        assert_ulps(got, G[key], n_ulp)
+
+
+def test_gelu_backward_golden():
+    got = orc.eltwise(K["GELU_BACKWARD"], G["ew_x"], G["ew_g"]).ravel()
+    want = G["ew_gelu_bwd"].astype(np.float64)
+    # Cancellation near x = -0.75 makes the value small: bound by the terms' size.
+    scale = np.abs(G["ew_g"]).astype(np.float64) * 1.5
+    assert np.all(np.abs(got - want) <= 4 * ULP * (np.abs(want) + scale))
+
+
+@pytest.mark.parametrize("kind,key", [("ADD", "sp_add"), ("SUB", "sp_sub"), ("MUL", "sp_mul"), ("DIV", "sp_div"),
+                                      ("RELU_BACKWARD", "sp_relu_bwd"), ("GT", "sp_gt"), ("EQ", "sp_eq")])
+def test_exact_binary_with_special_values(kind, key):
+    assert_bits(orc.eltwise(K[kind], G["sp_a"], G["sp_b"]).ravel(), G[key])
+
+
+def test_relu_special_values():
+    # kind.rs:19-22: a positive datum passes; zeros, negatives and NaN give +0.
+    assert_bits(orc.eltwise(K["RELU"], G["sp_a"]).ravel(), G["sp_relu"])
+    x = np.array([-0.0, np.nan, -np.inf, 1e-45], np.float32)
+    assert_bits(orc.eltwise(K["RELU"], x).ravel(), np.array([0.0, 0.0, 0.0, 1e-45], np.float32))
+
+
+def test_broadcast_row_column_value():
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    row = np.array([[10, 20, 30, 40]], np.float32)
+    col = np.array([[100], [200], [300]], np.float32)
+    assert_bits(orc.eltwise(K["ADD"], a, row), a + row)
+    assert_bits(orc.eltwise(K["ADD"], a, col), a + col)
+    assert_bits(orc.eltwise(K["SUB"], a, np.float32([[1.5]])), a - np.float32(1.5))
+    # The broadcast operand may be the first.
+    assert_bits(orc.eltwise(K["SUB"], row, a), row - a)
+
+
+def test_fused_kinds_equal_their_compositions():
+    x, y, z = G["ew_x"][:512], G["ew_g"][:512], G["ew_x"][512:1024]
+    sig = orc.eltwise(K["SIGMOID"], x)
+    assert_bits(orc.eltwise(K["SILU"], x), orc.eltwise(K["MUL"], x, sig))
+    assert_bits(orc.eltwise(K["SILU_MUL"], x, y), orc.eltwise(K["MUL"], orc.eltwise(K["SILU"], x), y))
+    assert_bits(orc.eltwise(K["ADD_RELU"], x, y), orc.eltwise(K["RELU"], orc.eltwise(K["ADD"], x, y)))
+    assert_bits(orc.eltwise(K["MUL_ADD"], x, y, z), orc.eltwise(K["ADD"], z, orc.eltwise(K["MUL"], x, y)))
+    assert_bits(orc.eltwise(K["SUB_EXP"], x, y), orc.eltwise(K["EXP"], orc.eltwise(K["SUB"], x, y)))
+
+
+def test_scalar_forms_and_clamps():
+    x = np.array([-2.0, -0.0, 0.0, 0.5, 3.0, np.nan], np.float32)
+    assert_bits(orc.eltwise(K["ADD_SCALAR"], x, s1=-1.25), x + np.float32(-1.25))
+    assert_bits(orc.eltwise(K["MUL_SCALAR"], x, s1=3.0), x * np.float32(3.0))
+    # Flex's clamp_min is f32::max: a NaN datum gives the scalar, equal values the scalar.
+    assert_bits(orc.eltwise(K["CLAMP_MIN"], x, s1=0.0), np.array([0, 0, 0, 0.5, 3, 0], np.float32))
+    assert_bits(orc.eltwise(K["CLAMP_MAX"], x, s1=0.0), np.array([-2, 0, 0, 0, 0, 0], np.float32))
+    c = orc.eltwise(K["CLAMP"], x, s1=-1.0, s2=1.0).ravel()
+    assert_bits(c[:5], np.array([-1, -0.0, 0, 0.5, 1], np.float32))
+    assert np.isnan(c[5])
+
+
+def test_mask_fill_and_where():
+    a = np.array([[1, 2, 3, 4]], np.float32)
+    m = np.array([[0, 1, 0, 1]], np.float32)
+    assert_bits(orc.eltwise(K["MASK_FILL"], a, m, s1=-np.inf), np.array([[1, -np.inf, 3, -np.inf]], np.float32))
+    c = np.array([[9, 8, 7, 6]], np.float32)
+    assert_bits(orc.eltwise(K["MASK_WHERE"], a, m, c), np.array([[1, 8, 3, 6]], np.float32))
+
+
+# ---------------------------------------------------------------- products
+@pytest.mark.parametrize("ta", [False, True])
+@pytest.mark.parametrize("tb", [False, True])
+def test_integer_product_exact_every_orientation(ta, tb):
+    a, b = G["mm_ai"], G["mm_bi"]
+    got = orc.matmul(a.T.copy() if ta else a, b.T.copy() if tb else b, ta, tb)
+    assert_bits(got, G["mm_ci"])
+
+
+def test_float_product_against_float64():
+    got = orc.matmul(G["mm_a"], G["mm_b"])
+    assert_bits(got, G["mm_c"])  # double accumulation rounded once == float64 numpy
+
+
+def test_product_brute_force_tiny():
+    a = np.array([[1.5, -2.0, 0.25], [3.0, 0.5, -1.0]], np.float32)
+    b = np.array([[2.0, 1.0], [0.5, -4.0], [8.0, 0.0]], np.float32)
+    want = np.array([[sum(float(a[i, k]) * float(b[k, j]) for k in range(3)) for j in range(2)] for i in range(2)],
+                    np.float32)
+    assert_bits(orc.matmul(a, b), want)
+    # A non-square, non-symmetric pair catches a transposed operand.
+    assert orc.matmul(a, b).shape == (2, 2)
+    assert_bits(orc.matmul(b.T.copy(), a.T.copy()), want.T.copy())
+
+
+def test_f32acc_product_is_the_k_ascending_sum():
+    a, b = G["mm_a"], G["mm_b"]
+    got = orc.matmul_f32acc(a, b)
+    want = np.zeros((a.shape[0], b.shape[1]), np.float32)
+    for k in range(a.shape[1]):
+        want = (want + a[:, k:k + 1] * b[k:k + 1, :]).astype(np.float32)
+    assert_bits(got, want)
+
+
+def test_bf16_casts():
+    x = np.array([1.0, 1.00390625, 1.005859375, -0.0, np.inf, np.nan, 3.0e38, 1e-40], np.float32)
+    h = orc.to_bf16(x)
+    # ties to even: 1 + 2^-8 (a tie) -> 1.0; 1 + 1.5 * 2^-8 -> 1 + 2^-7
+    assert h[0] == 0x3F80 and h[1] == 0x3F80 and h[2] == 0x3F81
+    assert h[3] == 0x8000 and h[4] == 0x7F80 and (h[5] & 0x7F80) == 0x7F80 and (h[5] & 0x7F) != 0
+    assert_bits(orc.from_bf16(h)[:5], np.array([1.0, 1.0, 1.0078125, -0.0, np.inf], np.float32))
+
+
+# -------------------------------------------------------------- reductions
+def test_reductions_against_float64():
+    x = G["red_x"]
+    assert_bits(orc.reduce(x, R_SUM, AXIS_ROWS), G["red_sum0"])
+    assert_bits(orc.reduce(x, R_SUM, AXIS_COLS), G["red_sum1"])
+    assert_bits(orc.reduce(x, R_MAX, AXIS_ROWS), G["red_max0"])
+    assert_bits(orc.reduce(x, R_MAX, AXIS_COLS), G["red_max1"])
+    assert_bits(np.array([orc.reduce_all(x, R_MEAN)]), G["red_mean_all"])
+
+
+def test_mean_is_sum_over_count():
+    x = G["red_x"]
+    s = orc.reduce(x, R_SUM, AXIS_COLS)
+    assert_bits(orc.reduce(x, R_MEAN, AXIS_COLS), (s / np.float32(x.shape[1])).astype(np.float32))
+
+
+def test_max_propagates_nan_and_sum_keeps_exact_values():
+    x = np.array([[1.0, np.nan, 3.0], [-1.0, -2.0, -0.5]], np.float32)
+    m = orc.reduce(x, R_MAX, AXIS_COLS).ravel()
+    assert np.isnan(m[0]) and m[1] == -0.5
+    y = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
+    assert orc.reduce(y, R_SUM, AXIS_COLS)[0, 0] == 10.0
+
+
+# ------------------------------------------------------------------ softmax
+def test_softmax_against_float64():
+    assert_ulps(orc.softmax_rows(G["sm_x"]), G["sm_softmax"], 1)
+    assert_bits(orc.softmax_rows(G["sm_x"], log=True), G["sm_log_softmax"])
+
+
+def test_softmax_invariants():
+    x = G["sm_x"]
+    p = orc.softmax_rows(x)
+    assert np.allclose(p.sum(axis=1), 1.0, atol=x.shape[1] * ULP * 2)
+    # A row shift leaves softmax unchanged (to rounding) -- a missing max
+    # shift overflows on row 0, whose entries exceed 80.
+    assert np.all(np.isfinite(p))
+    assert np.allclose(orc.softmax_rows(x - np.float32(7.0)), p, rtol=1e-5, atol=1e-30)
+
+
+def test_attention_softmax_clamps():
+    x = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], np.float32)
+    mask = np.array([[0, 1, 0], [1, 1, 1]], np.uint32)
+    p = orc.softmax_rows(x, mask=mask)
+    assert p[0, 1] == 0.0 and np.isclose(p[0, 0] + p[0, 2], 1.0)
+    assert np.all(p[1] == 0.0)  # fully masked: zeros, not NaN
+    q = orc.softmax_rows(x, scale=0.5)
+    assert_ulps(q, orc.softmax_rows(x * np.float32(0.5)), 0)
+
+
+# -------------------------------------------------------------------- norms
+def test_norms_against_float64():
+    assert_ulps(orc.rms_norm(G["nm_x"], G["nm_gamma"], 1e-5), G["nm_rms"], 1)
+    assert_ulps(orc.layer_norm(G["nm_x"], G["nm_gamma"], G["nm_beta"], 1e-5), G["nm_ln"], 1)
+
+
+# ----------------------------------------------------------------- indexing
+def test_select_and_pick_move_raw_bits():
+    t = G["ix_table"]
+    assert_bits(orc.select_rows(t, G["ix_idx"]).view(np.float32), G["ix_select"])
+    assert_bits(orc.pick_columns(t, G["ix_cols"]).view(np.float32), G["ix_pick"])
+    # step61: a NaN payload survives the copy.
+    tb = t.view(np.uint32).copy()
+    tb[0, 0] = 0x7FC0BEEF
+    assert orc.select_rows(tb, np.array([0], np.int32))[0, 0] == 0x7FC0BEEF
+
+
+def test_index_out_of_range_is_an_error():
+    t = G["ix_table"]
+    assert orc.select_rows(t, np.array([0, 50], np.int32)) is None
+    assert orc.select_rows(t, np.array([-1], np.int32)) is None
+    assert orc.pick_columns(t, np.full(50, 12, np.int32)) is None
+
+
+def test_argmax_first_maximum_and_nan():
+    assert np.array_equal(orc.argmax_rows(G["am_x"]), G["am_idx"])
+
+
+def test_scatter_add_columns_brute_force():
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    idx = np.array([3, 0, 3], np.int32)
+    v = np.array([0.5, -1.0, 10.0], np.float32)
+    want = x.copy()
+    for r in range(3):
+        want[r, idx[r]] += v[r]
+    assert_bits(orc.scatter_add_columns(x, idx, v), want)
+
+
+def test_select_add_rows_folds_duplicates_in_index_order():
+    t = G["red_x"][:10, :8].copy()
+    idx = np.array([3, 1, 3, 3, 9, 1], np.int32)
+    val = G["red_x"][10:16, :8].copy()
+    want = t.copy()
+    for i, r in enumerate(idx):  # sequential f32 adds, in index order
+        want[r] = (want[r] + val[i]).astype(np.float32)
+    assert_bits(orc.select_add_rows(t, idx, val), want)
+
+
+def test_copy_strided_transpose_keeps_negative_zero():
+    # essentials.rs:33-45: [[-0.0, 2.5], [3.0, 4.0]].transpose().reshape([4, 1]) == [-0.0, 3.0, 2.5, 4.0]
+    x = np.array([[-0.0, 2.5], [3.0, 4.0]], np.float32)
+    got = orc.copy_strided4(x, (1, 1, 2, 2), 0, (0, 0, 1, 2)).view(np.float32).reshape(4)
+    assert_bits(got, np.array([-0.0, 3.0, 2.5, 4.0], np.float32))
