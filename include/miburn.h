@@ -82,6 +82,10 @@ int mi_download_bf16(mi_ctx *ctx, mi_id id, uint16_t *out, int64_t n);
 int mi_free(mi_ctx *ctx, mi_id id);
 int mi_metadata(mi_ctx *ctx, mi_id id, int64_t *rows, int64_t *cols,
                 int *elem);
+/* Change a buffer's `[rows, cols]` in place, the element count kept: the
+ * reference's free `float_reshape` over the same storage
+ * (crates/burn-tt/src/views.rs:1-30, tensor.rs:905-908). */
+int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols);
 /* A fresh `[rows, cols]` buffer of `elem` filled with the 32-bit pattern
  * `bits` (the low 16 bits for BF16): Engine::zeros_dram (server.rs:285). */
 int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits,
@@ -102,6 +106,18 @@ int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
 int mi_matmul_batched(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
                       int b_transposed, int64_t batch, int64_t m, int64_t k,
                       int64_t n, int out_elem, mi_id *out);
+
+/* Engine::matmul_dram_batched with explicit items (server.rs:229: the items
+ * are blocks of resident buffers): product i multiplies the block of `a` at
+ * element a_offset + i * a_stride by the block of `b` at b_offset +
+ * i * b_stride, each block read with its buffer's row pitch (its cols), e.g.
+ * the first ctx rows of a KV-cache slot.  A stride of 0 broadcasts one
+ * block.  Result `[batch * m, n]`. */
+int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
+                     int b_transposed, int64_t batch, int64_t m, int64_t k,
+                     int64_t n, int64_t a_offset, int64_t a_stride,
+                     int64_t b_offset, int64_t b_stride, int out_elem,
+                     mi_id *out);
 
 /* ---- element-wise: Engine::eltwise_op_as (server.rs:519) ----
  * `kind` is one of the MI_K_* ids below (the reference's op ids,
@@ -212,6 +228,21 @@ int mi_copy_strided4(mi_ctx *ctx, mi_id src, const int64_t dims[4],
  * columns `[col0, col0 + src cols)`: a `slice_assign` (KV-cache writes). */
 int mi_assign_block(mi_ctx *ctx, mi_id dst, mi_id src, int64_t row0,
                     int64_t col0);
+/* A strided 4-D copy into an existing buffer (in place): element
+ * (i0, i1, i2, i3) of `dims` goes from src[src_offset + sum i * src_strides]
+ * to dst[dst_offset + sum i * dst_strides]; both ranges are bounds-checked.
+ * KV-cache appends (crates/tt-models/src/llama.rs:415-435: `slice_assign`
+ * into the cache) and Engine::scatter_rows_into (server.rs:389). */
+int mi_copy_into4(mi_ctx *ctx, mi_id dst, int64_t dst_offset,
+                  const int64_t dst_strides[4], mi_id src, int64_t src_offset,
+                  const int64_t src_strides[4], const int64_t dims[4]);
+/* Engine::rope_blocks (server.rs:566; crates/burn-tt/src/ops/rope.rs:27-240):
+ * rows of `x` ([rows, d] F32) laid out (sequence, position, head) -- row r
+ * at position pos0 + (r / heads) % seq -- become x * cos + rotate(x) * sin,
+ * rotate swapping the halves; `cos`/`sin` are [positions, d] tables with
+ * sin's first half negated (crates/tt-models/src/rope.rs:6-60). */
+int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table,
+            int64_t heads, int64_t seq, int64_t pos0, mi_id *out);
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);

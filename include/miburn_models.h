@@ -1,0 +1,81 @@
+/*
+ * miburn_models.h -- the model harnesses that drive the engine: the callers
+ * on either side of the hot path (the reference's crates/tt-mnist and
+ * crates/tt-models), written once over the engine's C ABI (miburn.h).
+ * They are not part of the engine boundary; tests and bench.py reach them
+ * through these entry points.
+ */
+#ifndef MIBURN_MODELS_H
+#define MIBURN_MODELS_H
+
+#include <stdint.h>
+
+#include "miburn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Llama / SmolLM2 decoder (crates/tt-models/src/llama.rs:40-71,
+ * 140-520, 1030-1178): pre-norm GQA attention with RoPE, SwiGLU MLP, RMSNorm,
+ * tied embedding head, BF16 weights and F32 activations. ---- */
+typedef struct mi_llama_config {
+  int32_t vocab, hidden, layers, heads, kv_heads, head_dim, intermediate;
+  float rope_theta, eps;
+  int32_t max_ctx, max_batch;
+} mi_llama_config;
+
+typedef struct mi_llama mi_llama;
+
+/* Random init: every weight N(0, init_std^2) drawn on the device from `seed`
+ * and stored BF16; RMSNorm gains 1. */
+int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed,
+                    float init_std, mi_llama **out);
+int mi_llama_destroy(mi_llama *m);
+/* The id of a weight (for checks): which = 0 embedding table [vocab, hidden]
+ * (layer ignored), 1 final norm; per layer 2 attention norm, 3 q [q_dim,
+ * hidden], 4 k [kv_dim, hidden], 5 v, 6 o [hidden, q_dim], 7 mlp norm,
+ * 8 gate [inter, hidden], 9 up, 10 down [hidden, inter].  Projection
+ * weights are stored [out, in] (the product reads them transposed). */
+int mi_llama_param(mi_llama *m, int layer, int which, mi_id *out);
+/* Empty the KV cache. */
+int mi_llama_reset(mi_llama *m);
+/* Feed `t` tokens per sequence (ids [batch, t], row-major) at the cache's
+ * current length; return the logits of every position ([batch * t, vocab],
+ * all_positions != 0) or of each sequence's last ([batch, vocab]). */
+int mi_llama_forward(mi_llama *m, const int32_t *ids, int32_t batch,
+                     int32_t t, int32_t all_positions, mi_id *logits);
+/* Greedy generation (llama.rs:1136-1178): prefill the prompts, then decode
+ * n_new tokens per sequence, each the argmax of the last logits.  `out`
+ * receives [batch, n_new] ids; the times (ms, device-synchronised) of the
+ * prefill and of all decode steps are returned if the pointers are set. */
+int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch,
+                      int32_t t_prompt, int32_t n_new, int32_t *out,
+                      double *prefill_ms, double *decode_ms);
+
+/* Last error message of the model layer. */
+const char *mi_models_last_error(void);
+
+/* ---- MLP d_in -> hidden -> d_out, ReLU, softmax cross-entropy, SGD (the
+ * reference's MNIST gate, crates/tt-tests/tests/step12_mnist.rs:57-114):
+ * Burn `Linear` layers, weight [d_in, d_out], initialised U(-k, k),
+ * k = 1/sqrt(d_in), from the gate's 64-bit LCG seeded `lcg_seed`. ---- */
+typedef struct mi_mlp mi_mlp;
+int mi_mlp_create(mi_ctx *ctx, int32_t d_in, int32_t hidden, int32_t d_out,
+                  uint64_t lcg_seed, mi_mlp **out);
+int mi_mlp_destroy(mi_mlp *m);
+/* which: 0 w1 [d_in, hidden], 1 b1 [1, hidden], 2 w2 [hidden, d_out], 3 b2. */
+int mi_mlp_param(mi_mlp *m, int which, mi_id *out);
+/* One step on resident x [B, d_in] F32 and labels (B I32): forward, loss,
+ * backward, SGD update; the loss [1, 1] is a new id the caller frees. */
+int mi_mlp_train_step(mi_mlp *m, mi_id x, mi_id labels, float lr, mi_id *loss);
+/* `steps` steps on device-drawn data (x ~ U[0, 1), labels uniform in
+ * [0, d_out)); per-step losses and the wall time of all steps (ms, synced). */
+int mi_mlp_train_synthetic(mi_mlp *m, int32_t batch, int32_t steps, float lr,
+                           uint64_t data_seed, float *losses, double *ms);
+const char *mi_mlp_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIBURN_MODELS_H */

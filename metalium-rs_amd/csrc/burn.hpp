@@ -1,0 +1,288 @@
+// Host-side tensor layer over the engine's C ABI: the shape of the
+// reference's Burn backend surface (`FloatTensorOps` / `IntTensorOps`,
+// crates/burn-tt/src/generated/ops.rs:78, 2423) for the model harnesses.
+//
+// A Tensor is a shared handle on one engine buffer plus its logical shape;
+// dropping the last handle frees the buffer (crates/burn-tt/src/tensor.rs:
+// 188-192).  Rank-N shapes fold to `[prod(leading), last]`
+// (tensor.rs:905-908).  A failed engine call throws `burn::Error` carrying the
+// engine's status and message; model entry points catch it at the C boundary.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/miburn.h"
+
+namespace burn {
+
+struct Error : std::runtime_error {
+  int status;
+  Error(int st, const std::string &m) : std::runtime_error(m), status(st) {}
+};
+
+inline void check(mi_ctx *ctx, int st, const char *what) {
+  if (st != MI_OK) throw Error(st, std::string(what) + ": " + mi_last_error(ctx));
+}
+
+struct Buf {
+  mi_ctx *ctx;
+  mi_id id;
+  Buf(mi_ctx *c, mi_id i) : ctx(c), id(i) {}
+  ~Buf() { mi_free(ctx, id); }
+  Buf(const Buf &) = delete;
+  Buf &operator=(const Buf &) = delete;
+};
+
+class Tensor {
+ public:
+  Tensor() = default;
+  Tensor(mi_ctx *ctx, mi_id id, std::vector<int64_t> shape) : buf_(std::make_shared<Buf>(ctx, id)), shape_(std::move(shape)) {}
+
+  mi_id id() const { return buf_ ? buf_->id : 0; }
+  // The id with the engine buffer's [rows, cols] set to this tensor's folded
+  // shape (handles sharing storage may fold it differently): pass this to
+  // every op.
+  mi_id use() const {
+    check(ctx(), mi_reshape(ctx(), id(), rows(), cols()), "shape");
+    return id();
+  }
+  mi_ctx *ctx() const { return buf_->ctx; }
+  const std::vector<int64_t> &shape() const { return shape_; }
+  int64_t dim(int i) const { return shape_[i < 0 ? shape_.size() + i : i]; }
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t d : shape_) n *= d;
+    return n;
+  }
+  int64_t cols() const { return shape_.empty() ? 1 : shape_.back(); }
+  int64_t rows() const { return cols() == 0 ? 0 : numel() / cols(); }
+  bool defined() const { return static_cast<bool>(buf_); }
+
+  // float_reshape: a new logical shape over the same storage (free).  The
+  // engine buffer takes the folded [rows, cols] of the new shape.
+  Tensor reshape(std::vector<int64_t> shape) const {
+    Tensor t = *this;
+    t.shape_ = std::move(shape);
+    check(ctx(), mi_reshape(ctx(), id(), t.rows(), t.cols()), "reshape");
+    return t;
+  }
+
+ private:
+  std::shared_ptr<Buf> buf_;
+  std::vector<int64_t> shape_;
+};
+
+// Wrap a fresh engine id with a logical shape.
+inline Tensor wrap(mi_ctx *ctx, mi_id id, std::vector<int64_t> shape) {
+  Tensor t(ctx, id, std::move(shape));
+  check(ctx, mi_reshape(ctx, id, t.rows(), t.cols()), "shape");
+  return t;
+}
+
+// ------------------------------------------------------------------ ops
+// Names follow Burn's trait methods; each is one engine call.
+
+inline Tensor float_from_data(mi_ctx *ctx, const float *v, std::vector<int64_t> shape) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_upload(ctx, v, cols ? n / cols : 0, cols, &id), "float_from_data");
+  return Tensor(ctx, id, std::move(shape));
+}
+
+inline Tensor int_from_data(mi_ctx *ctx, const int32_t *v, std::vector<int64_t> shape) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_upload_bits(ctx, reinterpret_cast<const uint32_t *>(v), cols ? n / cols : 0, cols, MI_I32, &id),
+        "int_from_data");
+  return Tensor(ctx, id, std::move(shape));
+}
+
+inline Tensor bool_from_data(mi_ctx *ctx, const uint32_t *v, std::vector<int64_t> shape) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_upload_bits(ctx, v, cols ? n / cols : 0, cols, MI_BOOL, &id), "bool_from_data");
+  return Tensor(ctx, id, std::move(shape));
+}
+
+inline std::vector<float> float_into_data(const Tensor &t) {
+  std::vector<float> v(static_cast<size_t>(t.numel()));
+  check(t.ctx(), mi_download(t.ctx(), t.use(), v.data(), t.numel()), "float_into_data");
+  return v;
+}
+
+inline std::vector<int32_t> int_into_data(const Tensor &t) {
+  std::vector<int32_t> v(static_cast<size_t>(t.numel()));
+  check(t.ctx(), mi_download_bits(t.ctx(), t.use(), reinterpret_cast<uint32_t *>(v.data()), t.numel()),
+        "int_into_data");
+  return v;
+}
+
+inline Tensor random(mi_ctx *ctx, std::vector<int64_t> shape, int draw, float p1, float p2, uint64_t base) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_random(ctx, cols ? n / cols : 0, cols, draw, p1, p2, base, &id), "float_random");
+  return Tensor(ctx, id, std::move(shape));
+}
+
+inline Tensor fill(mi_ctx *ctx, std::vector<int64_t> shape, int elem, uint32_t bits) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_fill(ctx, cols ? n / cols : 0, cols, elem, bits, &id), "fill");
+  return Tensor(ctx, id, std::move(shape));
+}
+
+inline Tensor float_cast(const Tensor &a, int elem) {
+  mi_id id;
+  check(a.ctx(), mi_cast(a.ctx(), a.use(), elem, &id), "float_cast");
+  return Tensor(a.ctx(), id, a.shape());
+}
+
+// Element-wise op by the reference's op id; the result takes a's shape
+// unless b (broadcast) is larger.
+inline Tensor eltwise(uint32_t kind, const Tensor &a, const Tensor *b = nullptr, const Tensor *c = nullptr,
+                      float s1 = 0.0f, float s2 = 0.0f, int out_elem = MI_F32) {
+  mi_id id;
+  check(a.ctx(), mi_eltwise(a.ctx(), kind, s1, s2, a.use(), b ? b->use() : 0, c ? c->use() : 0, out_elem, &id),
+        "eltwise");
+  std::vector<int64_t> shape = a.shape();
+  if (b && b->numel() > a.numel()) shape = b->shape();
+  return Tensor(a.ctx(), id, shape);
+}
+inline Tensor float_add(const Tensor &a, const Tensor &b) { return eltwise(MI_K_ADD, a, &b); }
+inline Tensor float_sub(const Tensor &a, const Tensor &b) { return eltwise(MI_K_SUB, a, &b); }
+inline Tensor float_mul(const Tensor &a, const Tensor &b) { return eltwise(MI_K_MUL, a, &b); }
+inline Tensor float_mul_scalar(const Tensor &a, float s) { return eltwise(MI_K_MUL_SCALAR, a, nullptr, nullptr, s); }
+inline Tensor float_add_scalar(const Tensor &a, float s) { return eltwise(MI_K_ADD_SCALAR, a, nullptr, nullptr, s); }
+inline Tensor relu(const Tensor &a) { return eltwise(MI_K_RELU, a); }
+inline Tensor relu_backward(const Tensor &out, const Tensor &grad) { return eltwise(MI_K_RELU_BACKWARD, out, &grad); }
+inline Tensor gelu(const Tensor &a) { return eltwise(MI_K_GELU, a); }
+inline Tensor gelu_backward(const Tensor &x, const Tensor &grad) { return eltwise(MI_K_GELU_BACKWARD, x, &grad); }
+inline Tensor float_exp(const Tensor &a) { return eltwise(MI_K_EXP, a); }
+inline Tensor float_neg(const Tensor &a) { return eltwise(MI_K_NEG, a); }
+// silu(gate) * up in one pass (crates/burn-tt/src/ops.rs:2622-2651).
+inline Tensor silu_mul(const Tensor &gate, const Tensor &up) { return eltwise(MI_K_SILU_MUL, gate, &up); }
+
+// float_matmul over the folded matrices: a [.., k] (or, transposed, its
+// stored [k, m]) times b [k, n] (or [n, k] transposed).
+inline Tensor float_matmul(const Tensor &a, bool ta, const Tensor &b, bool tb, int out_elem = MI_F32) {
+  mi_id id;
+  check(a.ctx(), mi_matmul(a.ctx(), a.use(), ta, b.use(), tb, out_elem, &id), "float_matmul");
+  const int64_t m = ta ? a.cols() : a.rows();
+  const int64_t n = tb ? b.rows() : b.cols();
+  std::vector<int64_t> shape;
+  if (!ta && a.shape().size() > 2) {
+    shape.assign(a.shape().begin(), a.shape().end() - 1);
+    shape.push_back(n);
+  } else {
+    shape = {m, n};
+  }
+  return Tensor(a.ctx(), id, shape);
+}
+
+// Products over item blocks of resident buffers (batched_matmul,
+// crates/burn-tt/src/ops.rs:2981-3052): result [batch * m, n].
+inline Tensor matmul_blocks(const Tensor &a, bool ta, const Tensor &b, bool tb, int64_t batch, int64_t m, int64_t k,
+                            int64_t n, int64_t a_off, int64_t a_stride, int64_t b_off, int64_t b_stride) {
+  mi_id id;
+  check(a.ctx(), mi_matmul_blocks(a.ctx(), a.use(), ta, b.use(), tb, batch, m, k, n, a_off, a_stride, b_off, b_stride,
+                                  MI_F32, &id), "matmul_blocks");
+  return Tensor(a.ctx(), id, {batch * m, n});
+}
+
+inline Tensor reduce(const Tensor &a, int op, int axis) {
+  mi_id id;
+  check(a.ctx(), mi_reduce(a.ctx(), a.use(), op, axis, &id), "reduce");
+  return Tensor(a.ctx(), id, axis == MI_AXIS_COLS ? std::vector<int64_t>{a.rows(), 1} : std::vector<int64_t>{1, a.cols()});
+}
+inline Tensor reduce_all(const Tensor &a, int op) {
+  mi_id id;
+  check(a.ctx(), mi_reduce_all(a.ctx(), a.use(), op, &id), "reduce_all");
+  return Tensor(a.ctx(), id, {1, 1});
+}
+
+inline Tensor softmax_rows(const Tensor &x, const Tensor *mask, float scale, bool log) {
+  mi_id id;
+  check(x.ctx(), mi_softmax_rows(x.ctx(), x.use(), mask ? mask->use() : 0, scale, log, MI_F32, &id), "softmax_rows");
+  return Tensor(x.ctx(), id, x.shape());
+}
+
+inline Tensor rms_norm(const Tensor &x, const Tensor &gamma, float eps) {
+  mi_id id;
+  check(x.ctx(), mi_rms_norm(x.ctx(), x.use(), gamma.use(), eps, MI_F32, &id), "rms_norm");
+  return Tensor(x.ctx(), id, x.shape());
+}
+
+inline Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, float eps) {
+  mi_id id;
+  check(x.ctx(), mi_layer_norm(x.ctx(), x.use(), gamma.use(), beta.use(), eps, &id), "layer_norm");
+  return Tensor(x.ctx(), id, x.shape());
+}
+
+inline Tensor argmax_rows(const Tensor &x) {
+  mi_id id;
+  check(x.ctx(), mi_argmax_rows(x.ctx(), x.use(), &id), "float_argmax");
+  return Tensor(x.ctx(), id, {x.rows(), 1});
+}
+
+// embedding: rows of the table for every index, [.., d].
+inline Tensor select_rows(const Tensor &table, const Tensor &idx) {
+  mi_id id;
+  check(table.ctx(), mi_select_rows(table.ctx(), table.use(), idx.use(), &id), "select_rows");
+  std::vector<int64_t> shape = idx.shape();
+  if (shape.size() >= 2 && shape.back() == 1) shape.pop_back();
+  shape.push_back(table.cols());
+  return Tensor(table.ctx(), id, shape);
+}
+
+inline Tensor pick_columns(const Tensor &x, const Tensor &idx) {
+  mi_id id;
+  check(x.ctx(), mi_pick_columns(x.ctx(), x.use(), idx.use(), &id), "pick_columns");
+  return Tensor(x.ctx(), id, {x.rows(), 1});
+}
+
+inline Tensor scatter_add_columns(const Tensor &x, const Tensor &idx, const Tensor &v) {
+  mi_id id;
+  check(x.ctx(), mi_scatter_add_columns(x.ctx(), x.use(), idx.use(), v.use(), &id), "scatter_add_columns");
+  return Tensor(x.ctx(), id, x.shape());
+}
+
+inline Tensor select_add_rows(const Tensor &t, const Tensor &idx, const Tensor &v) {
+  mi_id id;
+  check(t.ctx(), mi_select_add_rows(t.ctx(), t.use(), idx.use(), v.use(), &id), "select_add_rows");
+  return Tensor(t.ctx(), id, t.shape());
+}
+
+// A strided 4-D gather into a new [d0 * d1 * d2, d3] tensor (swap_dims,
+// head split/merge materialised).
+inline Tensor copy4(const Tensor &src, const int64_t dims[4], int64_t off, const int64_t st[4]) {
+  mi_id id;
+  check(src.ctx(), mi_copy_strided4(src.ctx(), src.use(), dims, off, st, &id), "copy_strided4");
+  return Tensor(src.ctx(), id, {dims[0] * dims[1] * dims[2], dims[3]});
+}
+
+inline void copy_into4(const Tensor &dst, int64_t doff, const int64_t dst_st[4], const Tensor &src, int64_t soff,
+                       const int64_t src_st[4], const int64_t dims[4]) {
+  check(dst.ctx(), mi_copy_into4(dst.ctx(), dst.use(), doff, dst_st, src.use(), soff, src_st, dims), "copy_into4");
+}
+
+inline Tensor rope(const Tensor &x, const Tensor &cos, const Tensor &sin, int64_t heads, int64_t seq, int64_t pos0) {
+  mi_id id;
+  check(x.ctx(), mi_rope(x.ctx(), x.use(), cos.use(), sin.use(), heads, seq, pos0, &id), "rope");
+  return Tensor(x.ctx(), id, x.shape());
+}
+
+}  // namespace burn

@@ -548,3 +548,102 @@ extern "C" int mi_assign_block(mi_ctx *ctx, mi_id dst, mi_id src, int64_t row0, 
                                                        static_cast<const uint32_t *>(s->ptr), s->rows, s->cols, row0, col0);
   return check_launch(ctx, "assign_block");
 }
+
+// ------------------------------------------------- strided copy into a buffer
+namespace mi {
+template <typename T>
+__global__ void copy_into4_kernel(T *dst, const T *src, int64_t d1, int64_t d2, int64_t d3, int64_t n, int64_t doff,
+                                  int64_t ds0, int64_t ds1, int64_t ds2, int64_t ds3, int64_t soff, int64_t ss0,
+                                  int64_t ss1, int64_t ss2, int64_t ss3) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    int64_t i3 = e % d3, r = e / d3;
+    int64_t i2 = r % d2; r /= d2;
+    int64_t i1 = r % d1, i0 = r / d1;
+    dst[doff + i0 * ds0 + i1 * ds1 + i2 * ds2 + i3 * ds3] = src[soff + i0 * ss0 + i1 * ss1 + i2 * ss2 + i3 * ss3];
+  }
+}
+
+// [lo, hi] element range a 4-D strided index space addresses.
+static void span4(const int64_t dims[4], int64_t off, const int64_t st[4], int64_t *lo, int64_t *hi) {
+  *lo = off; *hi = off;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t span = (dims[i] - 1) * st[i];
+    if (span < 0) *lo += span; else *hi += span;
+  }
+}
+
+// RoPE on rows of [rows, d] laid out (sequence, position, head): row r is at
+// position pos0 + (r / heads) % seq.  out = x cos + rotate(x) sin, rotate
+// swapping the two halves and `sin`'s first half stored negated, two
+// roundings (crates/tt-models/src/rope.rs:6-60; ops/rope.rs:27-240).
+__global__ void rope_kernel(const float *x, const float *cosp, const float *sinp, float *out, int64_t rows, int64_t d,
+                            int64_t heads, int64_t seq, int64_t pos0) {
+  const int64_t n = rows * d;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t half = d / 2;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int64_t r = e / d, j = e - r * d;
+    const int64_t pos = pos0 + (r / heads) % seq;
+    const float xv = x[e];
+    const float rv = x[r * d + (j < half ? j + half : j - half)];
+    const float c = __fmul_rn(xv, cosp[pos * d + j]);
+    out[e] = __fadd_rn(c, __fmul_rn(rv, sinp[pos * d + j]));
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_copy_into4(mi_ctx *ctx, mi_id dst, int64_t dst_offset, const int64_t dst_strides[4], mi_id src,
+                             int64_t src_offset, const int64_t src_strides[4], const int64_t dims[4]) {
+  MI_ENTER(ctx);
+  if (!dst_strides || !src_strides || !dims) return fail(ctx, MI_E_ARG, "null dims or strides");
+  MI_BUF(ctx, d, dst);
+  MI_BUF(ctx, sb, src);
+  if (elem_size(d->elem) != elem_size(sb->elem)) return fail(ctx, MI_E_ARG, "copy of %s into %s", elem_name(sb->elem), elem_name(d->elem));
+  int64_t n = 1;
+  for (int i = 0; i < 4; ++i) {
+    if (dims[i] < 0) return fail(ctx, MI_E_ARG, "negative copy extent");
+    n *= dims[i];
+  }
+  if (n == 0) return MI_OK;
+  int64_t lo, hi;
+  span4(dims, dst_offset, dst_strides, &lo, &hi);
+  if (lo < 0 || hi >= d->numel()) return fail(ctx, MI_E_ARG, "copy writes [%lld, %lld] of a %lld-element buffer", (long long)lo, (long long)hi, (long long)d->numel());
+  span4(dims, src_offset, src_strides, &lo, &hi);
+  if (lo < 0 || hi >= sb->numel()) return fail(ctx, MI_E_ARG, "copy reads [%lld, %lld] of a %lld-element buffer", (long long)lo, (long long)hi, (long long)sb->numel());
+  const unsigned g = grid_for(n, 256 * 4, 256 * 32);
+  if (elem_size(d->elem) == 2)
+    copy_into4_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<uint16_t *>(d->ptr), static_cast<const uint16_t *>(sb->ptr),
+        dims[1], dims[2], dims[3], n, dst_offset, dst_strides[0], dst_strides[1], dst_strides[2], dst_strides[3],
+        src_offset, src_strides[0], src_strides[1], src_strides[2], src_strides[3]);
+  else
+    copy_into4_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<uint32_t *>(d->ptr), static_cast<const uint32_t *>(sb->ptr),
+        dims[1], dims[2], dims[3], n, dst_offset, dst_strides[0], dst_strides[1], dst_strides[2], dst_strides[3],
+        src_offset, src_strides[0], src_strides[1], src_strides[2], src_strides[3]);
+  return check_launch(ctx, "copy_into4");
+}
+
+extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, int64_t heads, int64_t seq, int64_t pos0,
+                       mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, cb, cos_table);
+  MI_BUF(ctx, sb, sin_table);
+  if (xb->elem != MI_F32 || cb->elem != MI_F32 || sb->elem != MI_F32) return fail(ctx, MI_E_ARG, "rope takes F32");
+  const int64_t R = xb->rows, D = xb->cols;
+  if (D % 2 || cb->cols != D || sb->cols != D || cb->rows != sb->rows) return fail(ctx, MI_E_ARG, "rope tables [%lld, %lld] for width %lld", (long long)cb->rows, (long long)cb->cols, (long long)D);
+  if (heads < 1 || seq < 1 || R % (heads * seq) != 0) return fail(ctx, MI_E_ARG, "rope: %lld rows are not sequences of %lld positions x %lld heads", (long long)R, (long long)seq, (long long)heads);
+  if (pos0 < 0 || pos0 + seq > cb->rows) return fail(ctx, MI_E_ARG, "rope positions [%lld, %lld) beyond the %lld-row table", (long long)pos0, (long long)(pos0 + seq), (long long)cb->rows);
+  const float *xp = static_cast<const float *>(xb->ptr), *cp = static_cast<const float *>(cb->ptr), *sp = static_cast<const float *>(sb->ptr);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, D, MI_F32, &id, &ob);
+  if (s) return s;
+  if (R * D > 0) {
+    rope_kernel<<<grid_for(R * D, 256 * 4, 256 * 32), 256, 0, ctx->stream>>>(xp, cp, sp, static_cast<float *>(ob->ptr), R, D, heads, seq, pos0);
+    s = check_launch(ctx, "rope");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}

@@ -215,6 +215,7 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;
   int64_t sa, sb, sc;  // batch strides in elements (0 = broadcast)
   int tiles_m, tiles_n;
+  int64_t kc;          // split-K: k per slice (blockIdx.z), 0 for none
 };
 
 // Map a linear workgroup id to an output tile (tm, tn), grouping the tiles
@@ -256,6 +257,16 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   const SA *A = static_cast<const SA *>(g.a) + z * g.sa;
   const SB *B = static_cast<const SB *>(g.b) + z * g.sb;
   TO *C = static_cast<TO *>(g.c) + z * g.sc;
+  int64_t Kz = g.K;
+  if (g.kc > 0) {
+    // Split-K slice blockIdx.z: k in [ks, ks + Kz), its partial product
+    // written to slice z of an [S, M, N] buffer.
+    const int64_t ks = static_cast<int64_t>(blockIdx.z) * g.kc;
+    Kz = g.K - ks < g.kc ? g.K - ks : g.kc;
+    A += AK ? ks : ks * g.lda;
+    B += BKC ? ks : ks * g.ldb;
+    C += static_cast<int64_t>(blockIdx.z) * g.M * g.ldc;
+  }
 
   TileLoader<T, SA, BM, NT, AK, GUARD> la;
   TileLoader<T, SB, BN, NT, BKC, GUARD> lb;
@@ -268,9 +279,9 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int64_t ktiles = (g.K + BK - 1) / BK;
-  la.load(A, g.lda, m0, 0, g.M, g.K, tid);
-  lb.load(B, g.ldb, n0, 0, g.N, g.K, tid);
+  const int64_t ktiles = (Kz + BK - 1) / BK;
+  la.load(A, g.lda, m0, 0, g.M, Kz, tid);
+  lb.load(B, g.ldb, n0, 0, g.N, Kz, tid);
   la.store(smem, tid);
   lb.store(smem + A_BYTES, tid);
   __syncthreads();
@@ -310,8 +321,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
     const int cur = kt & 1;
     const bool more = kt + 1 < ktiles;
     if (more) {
-      la.load(A, g.lda, m0, (kt + 1) * BK, g.M, g.K, tid);
-      lb.load(B, g.ldb, n0, (kt + 1) * BK, g.N, g.K, tid);
+      la.load(A, g.lda, m0, (kt + 1) * BK, g.M, Kz, tid);
+      lb.load(B, g.ldb, n0, (kt + 1) * BK, g.N, Kz, tid);
     }
     const char *a_s = smem + cur * STAGE;
     const char *b_s = a_s + A_BYTES;
@@ -604,6 +615,98 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------- small-M products
+// Decode-shaped products (M <= 8 rows of F32 activations against a
+// k-contiguous weight, B stored [n, k]): the weight streams from HBM once,
+// 16 bytes per lane per step, each wavefront owning GEMV_NR outputs for all
+// M rows; lanes stride k and fold with a butterfly.  HBM-bound on the weight.
+constexpr int GEMV_NR = 2;
+
+__device__ __forceinline__ float gemv_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int M, typename SB, typename TO>
+__global__ void __launch_bounds__(256) gemv_kernel(const float *A, int64_t lda, const SB *B, int64_t ldb, TO *C,
+                                                   int64_t ldc, int64_t N, int64_t K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n0 = wave * GEMV_NR;
+  if (n0 >= N) return;
+  float acc[M][GEMV_NR];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < GEMV_NR; ++r) acc[m][r] = 0.0f;
+  for (int64_t k = static_cast<int64_t>(lane) * 8; k < K; k += 512) {
+    float w[GEMV_NR][8];
+#pragma unroll
+    for (int r = 0; r < GEMV_NR; ++r) {
+      if (n0 + r < N) {
+        const SB *row = B + (n0 + r) * ldb + k;
+        if constexpr (sizeof(SB) == 2) {
+          const uint4 q = *reinterpret_cast<const uint4 *>(row);
+          const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[r][2 * e] = __uint_as_float(u[e] << 16);
+            w[r][2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+          }
+        } else {
+          const float4 q0 = *reinterpret_cast<const float4 *>(row);
+          const float4 q1 = *reinterpret_cast<const float4 *>(row + 4);
+          w[r][0] = q0.x; w[r][1] = q0.y; w[r][2] = q0.z; w[r][3] = q0.w;
+          w[r][4] = q1.x; w[r][5] = q1.y; w[r][6] = q1.z; w[r][7] = q1.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[r][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float4 a0 = *reinterpret_cast<const float4 *>(A + m * lda + k);
+      const float4 a1 = *reinterpret_cast<const float4 *>(A + m * lda + k + 4);
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int r = 0; r < GEMV_NR; ++r) {
+        float t = acc[m][r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t += av[e] * w[r][e];
+        acc[m][r] = t;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < GEMV_NR; ++r) acc[m][r] = gemv_wave_sum(acc[m][r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < GEMV_NR; ++r) {
+        if (n0 + r < N) {
+          if constexpr (sizeof(TO) == 2) C[m * ldc + n0 + r] = f32_to_bf16_bits(acc[m][r]);
+          else C[m * ldc + n0 + r] = acc[m][r];
+        }
+      }
+  }
+}
+
+// Split-K: the S partial products [S, M, N] added in slice order.
+template <typename TO>
+__global__ void splitk_reduce(const float *part, int S, int64_t mn, TO *C) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= mn) return;
+  float s = part[i];
+  for (int z = 1; z < S; ++z) s += part[z * mn + i];
+  if constexpr (sizeof(TO) == 2) C[i] = f32_to_bf16_bits(s);
+  else C[i] = s;
+}
+
 // ----------------------------------------------------------- launching
 struct Plan {
   int64_t M, N, K, batch;
@@ -612,6 +715,9 @@ struct Plan {
   const void *a, *b;
   void *c;
   int64_t sa, sb, sc;
+  int64_t lda, ldb;   // row pitch of each operand's storage
+  int64_t kc = 0;     // split-K slice length (register kernel only)
+  int splits = 1;
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -629,13 +735,15 @@ static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   GemmArgs g;
   g.a = p.a; g.b = p.b; g.c = p.c;
   g.M = p.M; g.N = p.N; g.K = p.K;
-  g.lda = p.ta ? p.M : p.K;  // A is [m, k] or [k, m]
-  g.ldb = p.tb ? p.K : p.N;  // B is [k, n] or [n, k]
+  g.lda = p.lda;  // A is [m, k] or [k, m]
+  g.ldb = p.ldb;  // B is [k, n] or [n, k]
   g.ldc = p.N;
   g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.kc = p.kc;
   g.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
-  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch),
+            static_cast<unsigned>(p.splits));
   kern<<<grid, NT, SMEM, st>>>(g);
   return hipGetLastError();
 }
@@ -646,10 +754,11 @@ static hipError_t launch_dma_cfg(const Plan &p, hipStream_t st) {
   GemmArgs g;
   g.a = p.a; g.b = p.b; g.c = p.c;
   g.M = p.M; g.N = p.N; g.K = p.K;
-  g.lda = p.ta ? p.M : p.K;
-  g.ldb = p.tb ? p.K : p.N;
+  g.lda = p.lda;
+  g.ldb = p.ldb;
   g.ldc = p.N;
   g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.kc = 0;
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>(p.N / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
@@ -680,9 +789,10 @@ static hipError_t launch_orient(const Plan &p, hipStream_t st) {
 // 16-byte chunk, and the shape a multiple of the tile: the unguarded kernel.
 static bool tiles_exactly(const Plan &p, int bm, int bn, int bk, int64_t align_elems) {
   if (p.M % bm || p.N % bn || p.K % bk) return false;
-  const int64_t lda = p.ta ? p.M : p.K, ldb = p.tb ? p.K : p.N;
+  const int64_t lda = p.lda, ldb = p.ldb;
   if (lda % align_elems || ldb % align_elems) return false;
   if (p.sa % align_elems || p.sb % align_elems) return false;
+  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.b) & 15)) return false;
   return true;
 }
 
@@ -730,8 +840,101 @@ static hipError_t run_plan(const Plan &p, hipStream_t st) {
 
 using namespace mi;
 
+namespace mi {
+
+template <int M>
+static void launch_gemv_m(const Plan &p, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>((p.N + 4 * GEMV_NR - 1) / (4 * GEMV_NR));
+  const float *A = static_cast<const float *>(p.a);
+  if (p.eb == MI_BF16) {
+    const uint16_t *B = static_cast<const uint16_t *>(p.b);
+    if (p.eo == MI_BF16) gemv_kernel<M, uint16_t, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.N, p.N, p.K);
+    else gemv_kernel<M, uint16_t, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.N, p.N, p.K);
+  } else {
+    const float *B = static_cast<const float *>(p.b);
+    if (p.eo == MI_BF16) gemv_kernel<M, float, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.N, p.N, p.K);
+    else gemv_kernel<M, float, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.N, p.N, p.K);
+  }
+}
+
+// The GEMV applies: a few F32 rows against a k-contiguous F32 or BF16
+// weight, 16-byte aligned rows.
+static bool gemv_fits(const Plan &p) {
+  if (p.batch != 1 || p.M < 1 || p.M > 8 || !p.tb || p.ta || p.ea != MI_F32) return false;
+  if (p.K % 8 || p.lda % 4 || p.ldb % 8) return false;
+  if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.b) & 15)) return false;
+  return true;
+}
+
+static void launch_gemv(const Plan &p, hipStream_t st) {
+  // One instantiation per row count: a kernel never touches a row past M.
+  switch (p.M) {
+    case 1: launch_gemv_m<1>(p, st); break;
+    case 2: launch_gemv_m<2>(p, st); break;
+    case 3: launch_gemv_m<3>(p, st); break;
+    case 4: launch_gemv_m<4>(p, st); break;
+    case 5: launch_gemv_m<5>(p, st); break;
+    case 6: launch_gemv_m<6>(p, st); break;
+    case 7: launch_gemv_m<7>(p, st); break;
+    default: launch_gemv_m<8>(p, st); break;  // gemv_fits admits M <= 8 only
+  }
+}
+
+// Split-K for few output tiles over a long k: enough (tile, slice) pairs to
+// give most CUs work, each slice at least 256 deep.
+static int splitk_slices(const Plan &p) {
+  if (p.batch != 1) return 1;
+  const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+  if (tiles >= 128 || p.K < 512) return 1;
+  int64_t s = (192 + tiles - 1) / tiles;
+  const int64_t smax = p.K / 256;
+  if (s > smax) s = smax;
+  if (s > 64) s = 64;
+  return s < 2 ? 1 : static_cast<int>(s);
+}
+
+template <typename T, typename SA, typename SB>
+static hipError_t run_splitk_kernels(const Plan &p, hipStream_t st) {
+  return launch_orient<T, SA, SB, float, 64, 64, 2, 2, true>(p, st);
+}
+
+static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
+  const int S = p.splits;
+  const int64_t align = 64;  // slice boundaries on k-tile boundaries of both precisions
+  p.kc = ((p.K + S - 1) / S + align - 1) / align * align;
+  p.splits = static_cast<int>((p.K + p.kc - 1) / p.kc);
+  void *final_c = p.c;
+  const int eo = p.eo;
+  p.c = part;
+  p.eo = MI_F32;
+  hipError_t e;
+  if (p.ea == MI_BF16 && p.eb == MI_BF16) e = run_splitk_kernels<uint16_t, uint16_t, uint16_t>(p, st);
+  else if (p.ea == MI_F32 && p.eb == MI_F32) e = run_splitk_kernels<float, float, float>(p, st);
+  else if (p.ea == MI_F32) e = run_splitk_kernels<float, float, uint16_t>(p, st);
+  else e = run_splitk_kernels<float, uint16_t, float>(p, st);
+  if (e != hipSuccess) return e;
+  const int64_t mn = p.M * p.N;
+  const unsigned g = static_cast<unsigned>((mn + 255) / 256);
+  if (eo == MI_BF16) splitk_reduce<uint16_t><<<g, 256, 0, st>>>(part, p.splits, mn, static_cast<uint16_t *>(final_c));
+  else splitk_reduce<float><<<g, 256, 0, st>>>(part, p.splits, mn, static_cast<float *>(final_c));
+  return hipGetLastError();
+}
+
+// Check that `rows x cols` items at off + i * stride (row pitch ld) lie in x.
+static bool items_in(const Buffer *x, int64_t batch, int64_t rows, int64_t cols, int64_t off, int64_t stride,
+                     int64_t ld) {
+  if (rows == 0 || cols == 0) return true;
+  if (off < 0 || cols > ld || ld != x->cols) return false;
+  const int64_t last = off + (batch - 1) * (stride > 0 ? stride : 0) + (rows - 1) * ld + cols - 1;
+  return last < x->numel() && (stride >= 0);
+}
+
+}  // namespace mi
+
 static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t batch, int64_t m, int64_t k,
-                         int64_t n, bool batched, int out_elem, mi_id *out) {
+                         int64_t n, int mode, const int64_t *blk, int out_elem, mi_id *out) {
+  // mode 0: plain; 1: stacked batch; 2: explicit item offsets/strides (blk =
+  // {a_off, a_stride, b_off, b_stride}), items read with the operand's row pitch.
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, A, a);
   MI_BUF(ctx, B, b);
@@ -742,7 +945,7 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   p.ta = ta != 0; p.tb = tb != 0;
   p.ea = A->elem; p.eb = B->elem; p.eo = out_elem;
   p.a = A->ptr; p.b = B->ptr;
-  if (!batched) {
+  if (mode == 0) {
     p.M = ta ? A->cols : A->rows;
     p.K = ta ? A->rows : A->cols;
     const int64_t kb = tb ? B->cols : B->rows;
@@ -751,7 +954,8 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
       return fail(ctx, MI_E_ARG, "matmul: op(A) is [%lld, %lld], op(B) is [%lld, %lld]", (long long)p.M, (long long)p.K,
                   (long long)kb, (long long)p.N);
     p.batch = 1; p.sa = p.sb = p.sc = 0;
-  } else {
+    p.lda = A->cols; p.ldb = B->cols;
+  } else if (mode == 1) {
     if (batch < 1 || m < 0 || k < 0 || n < 0) return fail(ctx, MI_E_ARG, "batched matmul dims");
     p.M = m; p.K = k; p.N = n; p.batch = batch;
     const int64_t a_item = m * k, b_item = k * n;
@@ -766,6 +970,25 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
     p.sa = (A->rows == a_rows && batch > 1) ? 0 : a_item;
     p.sb = (B->rows == b_rows && batch > 1) ? 0 : b_item;
     p.sc = m * n;
+    p.lda = a_cols; p.ldb = b_cols;
+  } else {
+    if (batch < 1 || m < 0 || k < 0 || n < 0 || !blk) return fail(ctx, MI_E_ARG, "block matmul dims");
+    p.M = m; p.K = k; p.N = n; p.batch = batch;
+    const int64_t a_rows = ta ? k : m, a_cols = ta ? m : k;
+    const int64_t b_rows = tb ? n : k, b_cols = tb ? k : n;
+    p.lda = A->cols; p.ldb = B->cols;
+    if (!items_in(A, batch, a_rows, a_cols, blk[0], blk[1], p.lda))
+      return fail(ctx, MI_E_ARG, "block matmul: A items [%lld, %lld] at %lld + i * %lld exceed [%lld, %lld]",
+                  (long long)a_rows, (long long)a_cols, (long long)blk[0], (long long)blk[1], (long long)A->rows,
+                  (long long)A->cols);
+    if (!items_in(B, batch, b_rows, b_cols, blk[2], blk[3], p.ldb))
+      return fail(ctx, MI_E_ARG, "block matmul: B items [%lld, %lld] at %lld + i * %lld exceed [%lld, %lld]",
+                  (long long)b_rows, (long long)b_cols, (long long)blk[2], (long long)blk[3], (long long)B->rows,
+                  (long long)B->cols);
+    const size_t ea = elem_size(A->elem), eb = elem_size(B->elem);
+    p.a = static_cast<const char *>(A->ptr) + blk[0] * ea;
+    p.b = static_cast<const char *>(B->ptr) + blk[2] * eb;
+    p.sa = blk[1]; p.sb = blk[3]; p.sc = m * n;
   }
   if (p.batch > 65535) return fail(ctx, MI_E_ARG, "batched matmul: batch %lld above 65535", (long long)p.batch);
   mi_id id; Buffer *cb;
@@ -773,14 +996,23 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   if (s) return s;
   p.c = cb->ptr;
   if (p.M > 0 && p.N > 0) {
+    hipError_t e = hipSuccess;
     if (p.K == 0) {
-      (void)hipMemsetAsync(cb->ptr, 0, p.batch * p.M * p.N * elem_size(out_elem), ctx->stream);
+      e = hipMemsetAsync(cb->ptr, 0, p.batch * p.M * p.N * elem_size(out_elem), ctx->stream);
+    } else if (gemv_fits(p)) {
+      launch_gemv(p, ctx->stream);
+      e = hipGetLastError();
+    } else if ((p.splits = splitk_slices(p)) > 1) {
+      float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(p.splits) * p.M * p.N * sizeof(float)));
+      if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "split-K scratch"); }
+      e = run_splitk(p, part, ctx->stream);
     } else {
-      hipError_t e = run_plan(p, ctx->stream);
-      if (e != hipSuccess) {
-        mi_free(ctx, id);
-        return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
-      }
+      p.splits = 1;
+      e = run_plan(p, ctx->stream);
+    }
+    if (e != hipSuccess) {
+      mi_free(ctx, id);
+      return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
     }
     s = check_launch(ctx, "matmul");
     if (s) { mi_free(ctx, id); return s; }
@@ -791,11 +1023,19 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
 
 extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
-  return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, false, out_elem, out);
+  return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out);
+}
+
+extern "C" int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int64_t batch,
+                                int64_t m, int64_t k, int64_t n, int64_t a_offset, int64_t a_stride, int64_t b_offset,
+                                int64_t b_stride, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  const int64_t blk[4] = {a_offset, a_stride, b_offset, b_stride};
+  return matmul_common(ctx, a, a_transposed, b, b_transposed, batch, m, k, n, 2, blk, out_elem, out);
 }
 
 extern "C" int mi_matmul_batched(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int64_t batch,
                                  int64_t m, int64_t k, int64_t n, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
-  return matmul_common(ctx, a, a_transposed, b, b_transposed, batch, m, k, n, true, out_elem, out);
+  return matmul_common(ctx, a, a_transposed, b, b_transposed, batch, m, k, n, 1, nullptr, out_elem, out);
 }

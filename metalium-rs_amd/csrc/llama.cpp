@@ -1,0 +1,294 @@
+// The Llama / SmolLM2 decoder harness over the engine.
+//
+// Reference: crates/tt-models/src/llama.rs -- the config (40-71), a layer's
+// pre-norm attention and SwiGLU MLP (140-520), the tied head on the last
+// position (1030-1090), greedy generation (1136-1178); the KV cache written
+// by slice_assign (415-435) and grouped-query attention (437-455);
+// crates/tt-models/src/rope.rs:1-140 for the rotary tables.
+//
+// Layout on the device.  Activations are F32 [batch * t, hidden], row
+// (sequence, position).  Projection weights are BF16 stored [out, in], so
+// every product reads its weight k-contiguous: the decode GEMV streams each
+// weight row once; prefill runs the MFMA kernels.  The KV cache of a layer is
+// F32 [batch * kv_heads * max_ctx, head_dim], item (sequence, kv head), so the
+// attention of a query group is one product over a block of the cache:
+// queries regrouped to [batch * kv_heads, t * group, head_dim] (row
+// t * group + g) multiply the first ctx rows of their cache item.
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/miburn_models.h"
+#include "burn.hpp"
+
+namespace {
+
+thread_local std::string g_model_error;
+
+using burn::Tensor;
+
+struct Layer {
+  Tensor attn_norm, wq, wk, wv, wo, mlp_norm, wgate, wup, wdown;
+  Tensor cache_k, cache_v;
+};
+
+}  // namespace
+
+struct mi_llama {
+  mi_ctx *ctx;
+  mi_llama_config cfg;
+  Tensor embed, final_norm;
+  std::vector<Layer> layers;
+  Tensor rope_cos, rope_sin;  // [max_ctx, head_dim]
+  int64_t len = 0;            // positions in the cache
+  int64_t cache_batch = 0;    // sequences the cache holds
+};
+
+namespace {
+
+int fail_model(const std::exception &e) {
+  g_model_error = e.what();
+  if (auto *be = dynamic_cast<const burn::Error *>(&e)) return be->status;
+  return MI_E_ARG;
+}
+
+Tensor weight(mi_ctx *ctx, int64_t rows, int64_t cols, float stdv, uint64_t base) {
+  Tensor w = burn::random(ctx, {rows, cols}, MI_DRAW_NORMAL, 0.0f, stdv, base);
+  return burn::float_cast(w, MI_BF16);
+}
+
+Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
+
+// The forward of `t` positions per sequence at cache length m->len; returns
+// the final-norm hidden states [batch * t, hidden].
+Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t) {
+  mi_ctx *ctx = m->ctx;
+  const mi_llama_config &c = m->cfg;
+  const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim, G = H / KVH;
+  const int64_t pos0 = m->len, ctxlen = pos0 + t, maxc = c.max_ctx;
+  const int64_t rows = batch * t;
+
+  Tensor idx = burn::int_from_data(ctx, ids, {rows});
+  Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
+  x = x.reshape({rows, c.hidden});
+
+  // Causal mask for t > 1, rows (position, group) of one item: row
+  // p * G + g attends to cache columns <= pos0 + p (bottom-right aligned).
+  Tensor mask;
+  if (t > 1) {
+    std::vector<uint32_t> mk(static_cast<size_t>(t * G * ctxlen));
+    for (int64_t p = 0; p < t; ++p)
+      for (int64_t g = 0; g < G; ++g)
+        for (int64_t j = 0; j < ctxlen; ++j) mk[(p * G + g) * ctxlen + j] = j > pos0 + p ? 1u : 0u;
+    mask = burn::bool_from_data(ctx, mk.data(), {t * G, ctxlen});
+  }
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+
+  for (Layer &L : m->layers) {
+    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps);
+    Tensor q = burn::float_matmul(xn, false, L.wq, true).reshape({rows * H, D});
+    Tensor k = burn::float_matmul(xn, false, L.wk, true).reshape({rows * KVH, D});
+    Tensor v = burn::float_matmul(xn, false, L.wv, true).reshape({rows * KVH, D});
+    q = burn::rope(q, m->rope_cos, m->rope_sin, H, t, pos0);
+    k = burn::rope(k, m->rope_cos, m->rope_sin, KVH, t, pos0);
+    // Append k, v at positions pos0.. of each (sequence, kv head) item.
+    {
+      const int64_t dims[4] = {batch, KVH, t, D};
+      const int64_t dst[4] = {KVH * maxc * D, maxc * D, D, 1};
+      const int64_t src[4] = {t * KVH * D, D, KVH * D, 1};
+      burn::copy_into4(L.cache_k, pos0 * D, dst, k, 0, src, dims);
+      burn::copy_into4(L.cache_v, pos0 * D, dst, v, 0, src, dims);
+    }
+    // Queries regrouped per kv head: [batch * KVH * t, G * D] = rows (p, g).
+    Tensor qg;
+    {
+      const int64_t dims[4] = {batch, KVH, t, G * D};
+      const int64_t st[4] = {t * H * D, G * D, H * D, 1};
+      qg = burn::copy4(q, dims, 0, st).reshape({batch * KVH * t * G, D});
+    }
+    Tensor scores = burn::matmul_blocks(qg, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
+                                        maxc * D);
+    Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
+    Tensor o = burn::matmul_blocks(p, false, L.cache_v, false, batch * KVH, t * G, ctxlen, D, 0, t * G * ctxlen, 0,
+                                   maxc * D);
+    // Back to rows (sequence, position), heads in order h = j * G + g.
+    Tensor oh;
+    {
+      const int64_t dims[4] = {batch, t, KVH, G * D};
+      const int64_t st[4] = {KVH * t * G * D, G * D, t * G * D, 1};
+      oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
+    }
+    x = burn::float_add(x, burn::float_matmul(oh, false, L.wo, true));
+    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps);
+    Tensor gate = burn::float_matmul(hn, false, L.wgate, true);
+    Tensor up = burn::float_matmul(hn, false, L.wup, true);
+    x = burn::float_add(x, burn::float_matmul(burn::silu_mul(gate, up), false, L.wdown, true));
+  }
+  m->len = ctxlen;
+  return burn::rms_norm(x, m->final_norm, c.eps);
+}
+
+// The tied head over the last position of each sequence: [batch, vocab].
+Tensor head_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
+  const int64_t dims[4] = {1, 1, batch, m->cfg.hidden};
+  const int64_t st[4] = {0, 0, t * m->cfg.hidden, 1};
+  Tensor last = burn::copy4(hidden, dims, (t - 1) * m->cfg.hidden, st);
+  return burn::float_matmul(last, false, m->embed, true);
+}
+
+void ensure_cache(mi_llama *m, int64_t batch) {
+  if (m->len == 0 && m->cache_batch != batch) {
+    const mi_llama_config &c = m->cfg;
+    for (Layer &L : m->layers) {
+      L.cache_k = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, MI_F32, 0);
+      L.cache_v = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, MI_F32, 0);
+    }
+    m->cache_batch = batch;
+  }
+  if (batch != m->cache_batch) throw burn::Error(MI_E_ARG, "batch differs from the cache's; reset first");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mi_models_last_error(void) { return g_model_error.c_str(); }
+
+int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, float init_std, mi_llama **out) {
+  if (!ctx || !cfg || !out) return MI_E_ARG;
+  const mi_llama_config &c = *cfg;
+  if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 2 || c.layers < 0 || c.max_ctx <= 0 ||
+      c.max_batch <= 0) {
+    g_model_error = "invalid llama config";
+    return MI_E_ARG;
+  }
+  mi_llama *m = new mi_llama();
+  try {
+    m->ctx = ctx;
+    m->cfg = c;
+    uint64_t base = seed * 1000003ull;
+    auto next = [&]() { return base++; };
+    const int64_t qd = static_cast<int64_t>(c.heads) * c.head_dim, kvd = static_cast<int64_t>(c.kv_heads) * c.head_dim;
+    m->embed = weight(ctx, c.vocab, c.hidden, init_std, next());
+    m->final_norm = ones(ctx, c.hidden);
+    m->layers.resize(c.layers);
+    for (Layer &L : m->layers) {
+      L.attn_norm = ones(ctx, c.hidden);
+      L.wq = weight(ctx, qd, c.hidden, init_std, next());
+      L.wk = weight(ctx, kvd, c.hidden, init_std, next());
+      L.wv = weight(ctx, kvd, c.hidden, init_std, next());
+      L.wo = weight(ctx, c.hidden, qd, init_std, next());
+      L.mlp_norm = ones(ctx, c.hidden);
+      L.wgate = weight(ctx, c.intermediate, c.hidden, init_std, next());
+      L.wup = weight(ctx, c.intermediate, c.hidden, init_std, next());
+      L.wdown = weight(ctx, c.hidden, c.intermediate, init_std, next());
+    }
+    // Rotary tables (rope.rs:14-60): angle = position * theta^(-2i / d), the
+    // first half repeated as the second, sin's first half negated.
+    const int64_t D = c.head_dim, half = D / 2;
+    std::vector<float> cs(static_cast<size_t>(c.max_ctx * D)), sn(cs.size());
+    for (int64_t p = 0; p < c.max_ctx; ++p)
+      for (int64_t i = 0; i < half; ++i) {
+        const float freq = static_cast<float>(std::pow(static_cast<double>(c.rope_theta), -2.0 * i / D));
+        const float ang = static_cast<float>(p) * freq;
+        const float co = static_cast<float>(std::cos(static_cast<double>(ang)));
+        const float si = static_cast<float>(std::sin(static_cast<double>(ang)));
+        cs[p * D + i] = co;
+        cs[p * D + half + i] = co;
+        sn[p * D + i] = -si;
+        sn[p * D + half + i] = si;
+      }
+    m->rope_cos = burn::float_from_data(ctx, cs.data(), {c.max_ctx, D});
+    m->rope_sin = burn::float_from_data(ctx, sn.data(), {c.max_ctx, D});
+  } catch (const std::exception &e) {
+    delete m;
+    return fail_model(e);
+  }
+  *out = m;
+  return MI_OK;
+}
+
+int mi_llama_destroy(mi_llama *m) {
+  delete m;
+  return MI_OK;
+}
+
+int mi_llama_param(mi_llama *m, int layer, int which, mi_id *out) {
+  if (!m || !out) return MI_E_ARG;
+  const Tensor *t = nullptr;
+  if (which == 0) t = &m->embed;
+  else if (which == 1) t = &m->final_norm;
+  else if (layer >= 0 && layer < static_cast<int>(m->layers.size())) {
+    Layer &L = m->layers[layer];
+    const Tensor *w[] = {&L.attn_norm, &L.wq, &L.wk, &L.wv, &L.wo, &L.mlp_norm, &L.wgate, &L.wup, &L.wdown};
+    if (which >= 2 && which <= 10) t = w[which - 2];
+  }
+  if (!t) {
+    g_model_error = "no such parameter";
+    return MI_E_ARG;
+  }
+  try {
+    t->use();
+  } catch (const std::exception &e) {
+    return fail_model(e);
+  }
+  *out = t->id();
+  return MI_OK;
+}
+
+int mi_llama_reset(mi_llama *m) {
+  if (!m) return MI_E_ARG;
+  m->len = 0;
+  return MI_OK;
+}
+
+int mi_llama_forward(mi_llama *m, const int32_t *ids, int32_t batch, int32_t t, int32_t all_positions,
+                     mi_id *logits) {
+  if (!m || !ids || !logits || batch <= 0 || t <= 0) return MI_E_ARG;
+  try {
+    if (batch > m->cfg.max_batch || m->len + t > m->cfg.max_ctx) throw burn::Error(MI_E_ARG, "batch or context too large");
+    ensure_cache(m, batch);
+    Tensor h = forward_hidden(m, ids, batch, t);
+    Tensor out = all_positions ? burn::float_matmul(h, false, m->embed, true) : head_last(m, h, batch, t);
+    // Hand the buffer to the caller: it owns (and frees) the id.
+    mi_id id;
+    burn::check(m->ctx, mi_cast(m->ctx, out.use(), MI_F32, &id), "logits");
+    *logits = id;
+  } catch (const std::exception &e) {
+    return fail_model(e);
+  }
+  return MI_OK;
+}
+
+int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t t_prompt, int32_t n_new,
+                      int32_t *out, double *prefill_ms, double *decode_ms) {
+  if (!m || !prompt || !out || batch <= 0 || t_prompt <= 0 || n_new < 0) return MI_E_ARG;
+  using clock = std::chrono::steady_clock;
+  try {
+    if (batch > m->cfg.max_batch || t_prompt + n_new > m->cfg.max_ctx) throw burn::Error(MI_E_ARG, "batch or context too large");
+    m->len = 0;
+    ensure_cache(m, batch);
+    burn::check(m->ctx, mi_sync(m->ctx), "sync");
+    auto t0 = clock::now();
+    Tensor h = forward_hidden(m, prompt, batch, t_prompt);
+    Tensor next = burn::argmax_rows(head_last(m, h, batch, t_prompt));
+    std::vector<int32_t> tok = burn::int_into_data(next);  // waits for the prefill
+    auto t1 = clock::now();
+    for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
+    for (int32_t s = 1; s < n_new; ++s) {
+      Tensor hs = forward_hidden(m, tok.data(), batch, 1);
+      tok = burn::int_into_data(burn::argmax_rows(head_last(m, hs, batch, 1)));
+      for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
+    }
+    auto t2 = clock::now();
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+  } catch (const std::exception &e) {
+    return fail_model(e);
+  }
+  return MI_OK;
+}
+
+}  // extern "C"

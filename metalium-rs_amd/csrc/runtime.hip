@@ -349,6 +349,17 @@ int mi_metadata(mi_ctx *ctx, mi_id id, int64_t *rows, int64_t *cols, int *elem) 
   return MI_OK;
 }
 
+int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, b, id);
+  if (rows < 0 || cols < 0 || rows * cols != b->numel())
+    return fail(ctx, MI_E_ARG, "reshape of [%lld, %lld] to [%lld, %lld]", (long long)b->rows, (long long)b->cols,
+                (long long)rows, (long long)cols);
+  b->rows = rows;
+  b->cols = cols;
+  return MI_OK;
+}
+
 int mi_event_record(mi_ctx *ctx, int slot) {
   MI_ENTER(ctx);
   if (slot < 0 || slot >= 16) return fail(ctx, MI_E_ARG, "event slot %d", slot);

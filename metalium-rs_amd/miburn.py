@@ -92,8 +92,12 @@ def _load() -> ctypes.CDLL:
         "mi_free": [P, U64],
         "mi_metadata": [P, U64, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(c_int)],
         "mi_fill": [P, I64, I64, c_int, c_u32, Ip],
+        "mi_reshape": [P, U64, I64, I64],
         "mi_matmul": [P, U64, c_int, U64, c_int, c_int, Ip],
         "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
+        "mi_matmul_blocks": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, I64, I64, c_int, Ip],
+        "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
+        "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
         "mi_reduce": [P, U64, c_int, c_int, Ip],
         "mi_reduce_all": [P, U64, c_int, Ip],
@@ -214,6 +218,9 @@ class Engine:
     def free(self, id_: int) -> None:
         self._check(self._lib.mi_free(self.ctx, id_))
 
+    def reshape(self, id_: int, rows: int, cols: int) -> None:
+        self._check(self._lib.mi_reshape(self.ctx, id_, rows, cols))
+
     def fill(self, rows: int, cols: int, elem: int, bits: int) -> int:
         return self._out(self._lib.mi_fill, rows, cols, elem, bits)
 
@@ -235,6 +242,20 @@ class Engine:
     def matmul_dram_batched(self, a: int, a_t: bool, b: int, b_t: bool, batch: int, m: int, k: int, n: int,
                             out_elem: int = F32) -> int:
         return self._out(self._lib.mi_matmul_batched, a, int(a_t), b, int(b_t), batch, m, k, n, out_elem)
+
+    def matmul_blocks(self, a: int, a_t: bool, b: int, b_t: bool, batch: int, m: int, k: int, n: int,
+                      a_offset: int, a_stride: int, b_offset: int, b_stride: int, out_elem: int = F32) -> int:
+        return self._out(self._lib.mi_matmul_blocks, a, int(a_t), b, int(b_t), batch, m, k, n, a_offset, a_stride,
+                         b_offset, b_stride, out_elem)
+
+    def copy_into4(self, dst: int, dst_offset: int, dst_strides, src: int, src_offset: int, src_strides,
+                   dims) -> None:
+        A4 = ctypes.c_int64 * 4
+        self._check(self._lib.mi_copy_into4(self.ctx, dst, dst_offset, A4(*dst_strides), src, src_offset,
+                                            A4(*src_strides), A4(*dims)))
+
+    def rope(self, x: int, cos: int, sin: int, heads: int, seq: int, pos0: int) -> int:
+        return self._out(self._lib.mi_rope, x, cos, sin, heads, seq, pos0)
 
     def eltwise_op_as(self, kind, a: int, b: int = 0, c: int = 0, scalar: float = 0.0, scalar2: float = 0.0,
                       out_elem: int = F32) -> int:
@@ -326,3 +347,157 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------- models
+class LlamaConfig(ctypes.Structure):
+    """mi_llama_config (include/miburn_models.h)."""
+    _fields_ = [("vocab", ctypes.c_int32), ("hidden", ctypes.c_int32), ("layers", ctypes.c_int32),
+                ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("intermediate", ctypes.c_int32), ("rope_theta", ctypes.c_float), ("eps", ctypes.c_float),
+                ("max_ctx", ctypes.c_int32), ("max_batch", ctypes.c_int32)]
+
+
+# SmolLM2-135M's shape (crates/tt-models/src/llama.rs:60-71).
+SMOLLM2_135M = dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, head_dim=64, intermediate=1536,
+                    rope_theta=100000.0, eps=1e-5)
+
+LLAMA_PARAMS = {"embed": 0, "final_norm": 1, "attn_norm": 2, "wq": 3, "wk": 4, "wv": 5, "wo": 6, "mlp_norm": 7,
+                "wgate": 8, "wup": 9, "wdown": 10}
+
+
+def _models_lib():
+    L = lib()
+    if getattr(L, "_models_bound", False):
+        return L
+    P, I32, U64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64
+    L.mi_llama_create.argtypes = [P, ctypes.POINTER(LlamaConfig), U64, ctypes.c_float, ctypes.POINTER(P)]
+    L.mi_llama_destroy.argtypes = [P]
+    L.mi_llama_param.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.POINTER(U64)]
+    L.mi_llama_reset.argtypes = [P]
+    L.mi_llama_forward.argtypes = [P, P, I32, I32, I32, ctypes.POINTER(U64)]
+    L.mi_llama_generate.argtypes = [P, P, I32, I32, I32, P, ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_double)]
+    for f in (L.mi_llama_create, L.mi_llama_destroy, L.mi_llama_param, L.mi_llama_reset, L.mi_llama_forward,
+              L.mi_llama_generate):
+        f.restype = ctypes.c_int
+    L.mi_models_last_error.argtypes = []
+    L.mi_models_last_error.restype = ctypes.c_char_p
+    L._models_bound = True
+    return L
+
+
+class Llama:
+    """The SmolLM2-shaped decoder harness (crates/tt-models/src/llama.rs) on an Engine."""
+
+    def __init__(self, eng: Engine, cfg: dict, max_ctx: int, max_batch: int, seed: int = 0, init_std: float = 0.02):
+        self.eng = eng
+        self.L = _models_lib()
+        c = LlamaConfig(**{k: cfg[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim",
+                                               "intermediate")},
+                        rope_theta=cfg["rope_theta"], eps=cfg["eps"], max_ctx=max_ctx, max_batch=max_batch)
+        self.cfg = dict(cfg, max_ctx=max_ctx, max_batch=max_batch)
+        h = ctypes.c_void_p()
+        self._check(self.L.mi_llama_create(eng.ctx, ctypes.byref(c), seed, init_std, ctypes.byref(h)))
+        self.h = h
+
+    def _check(self, st):
+        if st != 0:
+            raise MiError(st, self.L.mi_models_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.mi_llama_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def param(self, name: str, layer: int = 0) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_llama_param(self.h, layer, LLAMA_PARAMS[name], ctypes.byref(out)))
+        return out.value
+
+    def reset(self):
+        self._check(self.L.mi_llama_reset(self.h))
+
+    def forward(self, ids: np.ndarray, all_positions: bool = False) -> int:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        b, t = ids.shape
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_llama_forward(self.h, ids.ctypes.data, b, t, int(all_positions), ctypes.byref(out)))
+        return out.value
+
+    def generate(self, prompt: np.ndarray, n_new: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        b, t = prompt.shape
+        out = np.zeros((b, n_new), np.int32)
+        pf, dc = ctypes.c_double(), ctypes.c_double()
+        self._check(self.L.mi_llama_generate(self.h, prompt.ctypes.data, b, t, n_new, out.ctypes.data,
+                                             ctypes.byref(pf), ctypes.byref(dc)))
+        return out, pf.value, dc.value
+
+
+class Mlp:
+    """The MLP training harness (crates/tt-tests/tests/step12_mnist.rs) on an Engine."""
+
+    def __init__(self, eng: Engine, d_in: int = 784, hidden: int = 128, d_out: int = 10, lcg_seed: int = 0x3A15):
+        self.eng = eng
+        L = lib()
+        if not getattr(L, "_mlp_bound", False):
+            P, I32, U64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64
+            L.mi_mlp_create.argtypes = [P, I32, I32, I32, U64, ctypes.POINTER(P)]
+            L.mi_mlp_destroy.argtypes = [P]
+            L.mi_mlp_param.argtypes = [P, ctypes.c_int, ctypes.POINTER(U64)]
+            L.mi_mlp_train_step.argtypes = [P, U64, U64, ctypes.c_float, ctypes.POINTER(U64)]
+            L.mi_mlp_train_synthetic.argtypes = [P, I32, I32, ctypes.c_float, U64, P, ctypes.POINTER(ctypes.c_double)]
+            for f in (L.mi_mlp_create, L.mi_mlp_destroy, L.mi_mlp_param, L.mi_mlp_train_step,
+                      L.mi_mlp_train_synthetic):
+                f.restype = ctypes.c_int
+            L.mi_mlp_last_error.restype = ctypes.c_char_p
+            L._mlp_bound = True
+        self.L = L
+        h = ctypes.c_void_p()
+        self._check(L.mi_mlp_create(eng.ctx, d_in, hidden, d_out, lcg_seed, ctypes.byref(h)))
+        self.h = h
+        self.d_out = d_out
+
+    def _check(self, st):
+        if st != 0:
+            raise MiError(st, self.L.mi_mlp_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.mi_mlp_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def param(self, which: int) -> np.ndarray:
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_mlp_param(self.h, which, ctypes.byref(out)))
+        return self.eng.download(out.value)
+
+    def train_step(self, x: np.ndarray, labels: np.ndarray, lr: float) -> float:
+        xi = self.eng.upload(x)
+        li = self.eng.upload_i32(np.ascontiguousarray(labels, np.int32).reshape(-1, 1))
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_mlp_train_step(self.h, xi, li, lr, ctypes.byref(out)))
+        loss = float(self.eng.download(out.value)[0, 0])
+        for i in (xi, li, out.value):
+            self.eng.free(i)
+        return loss
+
+    def train_synthetic(self, batch: int, steps: int, lr: float, data_seed: int = 0):
+        losses = np.zeros(steps, np.float32)
+        ms = ctypes.c_double()
+        self._check(self.L.mi_mlp_train_synthetic(self.h, batch, steps, lr, data_seed, losses.ctypes.data,
+                                                  ctypes.byref(ms)))
+        return losses, ms.value
