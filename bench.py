@@ -12,8 +12,13 @@ from HIP events recorded on the engine's own stream around the timed steps,
 against MI355X's dense BF16 peak), and the CPU baseline (the oracle's F32
 product timed on this host's cores on a bounded 1024^3 sample).
 
+The same line carries BASELINE.json's other measured configs: `decoder`, the
+SmolLM2-135M-shaped decoder (config 5) at batch 1 and 32 -- prefill 512 tokens,
+greedy-decode 128, tokens/s -- and `mlp_train`, the MLP training step
+(config 1), ms/step over 100 steps.
+
 Flags: --gpus N (only 1: this build runs on one GPU), --steps K, --warmup W,
---n (cube size, default 4096), --dtype bf16|f32, --no-cpu.  `--suite` instead
+--n (cube size, default 4096), --dtype bf16|f32, --no-cpu, --no-models.  `--suite` instead
 prints one JSON line per kernel of the HBM-bound suite (BASELINE.json
 configs[2]) and the matmul sweep, each against its roofline.
 """
@@ -140,6 +145,34 @@ def suite(steps: int) -> int:
     return 0
 
 
+def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128) -> dict:
+    """the SmolLM2-135M-shaped decoder (random N(0, 0.02)
+    BF16 weights), prefill `prompt` random tokens per sequence, then greedy
+    decode `new` tokens; tokens/s of the prefill and of the decode steps."""
+    import miburn
+    m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt + new, max_batch=batch, seed=5)
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, 49152, (batch, prompt)).astype(np.int32)
+    m.generate(ids[:, :32], 4)  # warm the kernels
+    out, pf_ms, dc_ms = m.generate(ids, new)
+    m.close()
+    return {"batch": batch, "prompt": prompt, "new_tokens": new,
+            "prefill_ms": round(pf_ms, 2), "prefill_tokens_per_s": round(batch * prompt / (pf_ms / 1e3), 1),
+            "decode_ms_per_step": round(dc_ms / max(new - 1, 1), 3),
+            "decode_tokens_per_s": round(batch * (new - 1) / (dc_ms / 1e3), 1)}
+
+
+def mlp_bench(eng, steps: int = 100) -> dict:
+    """MLP 784->128->10 training, batch 64, SGD lr 0.01."""
+    import miburn
+    m = miburn.Mlp(eng)
+    m.train_synthetic(64, 5, 0.01, data_seed=2)
+    losses, ms = m.train_synthetic(64, steps, 0.01, data_seed=3)
+    m.close()
+    return {"steps": steps, "ms_per_step": round(ms / steps, 4), "first_loss": round(float(losses[0]), 5),
+            "last_loss": round(float(losses[-1]), 5)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +182,7 @@ def main() -> int:
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true")
+    ap.add_argument("--no-models", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -213,6 +247,9 @@ def main() -> int:
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+    if not args.no_models:
+        line["decoder"] = [decoder_bench(eng, 1), decoder_bench(eng, 32)]
+        line["mlp_train"] = mlp_bench(eng)
     print(json.dumps(line), flush=True)
     eng.close()
     return 0
