@@ -183,6 +183,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true")
     ap.add_argument("--no-models", action="store_true")
+    ap.add_argument("--only", choices=["decoder", "mlp"],
+                    help="run one model harness alone (for profiling) and print its JSON")
+    ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -193,6 +196,11 @@ def main() -> int:
 
     import miburn
     eng = miburn.Engine(0)
+    if args.only:
+        out = decoder_bench(eng, args.batch) if args.only == "decoder" else mlp_bench(eng)
+        print(json.dumps({"harness": args.only, **out}), flush=True)
+        eng.close()
+        return 0
     n = args.n
     draw = miburn.DRAW_NORMAL
     a32 = eng.random_dram(n, n, draw, 0.0, 1.0, base=11)

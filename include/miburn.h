@@ -243,6 +243,20 @@ int mi_copy_into4(mi_ctx *ctx, mi_id dst, int64_t dst_offset,
  * sin's first half negated (crates/tt-models/src/rope.rs:6-60). */
 int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table,
             int64_t heads, int64_t seq, int64_t pos0, mi_id *out);
+/* Engine::attention_rows (server.rs:255-265; crates/tt-kernels/src/
+ * attention.rs:1-20; the composition of crates/burn-tt/src/ops.rs:4520-4595):
+ * causal grouped-query attention of `t` new positions per sequence against a
+ * KV cache.  q: [batch * t, heads * d] F32, rows (sequence, position), head h
+ * reading kv head h / (heads / kv_heads).  k_cache, v_cache: F32
+ * [batch * kv_heads * max_ctx, d], item (sequence, kv head), the new
+ * positions already written at pos0 .. pos0 + t - 1.  Query position p sees
+ * cache positions 0 .. pos0 + p.  out: [batch * t, heads * d] =
+ * softmax(scale * q k^T) v per head (max clamped at -FLT_MAX, sum at
+ * FLT_MIN).  d in {16, 32, 64, 128}; at most 8 query heads per kv head. */
+int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
+                      int64_t batch, int64_t t, int64_t heads,
+                      int64_t kv_heads, int64_t pos0, float scale,
+                      mi_id *out);
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);

@@ -1,0 +1,302 @@
+// Attention of a few query rows against a KV cache, as one operation.
+//
+// Reference: Engine::attention_rows (crates/burn-tt/src/server.rs:255-265;
+// crates/tt-kernels/src/attention.rs:1-20) -- per key/value head, the
+// composition of ops.rs:4520-4595: scores = Q K^T, scaled, masked to -inf
+// above the causal diagonal, max clamped below at -FLT_MAX, exp(x - max), sum
+// clamped below at FLT_MIN, divide, then P V.
+//
+// MI355X design.  The cache of one (sequence, kv head) item is F32 [max_ctx,
+// D], position-major, so a key or value row is one contiguous D-float read.
+// A block of 256 threads (4 wavefronts) takes one (item, query position,
+// key chunk); the group's G query heads share every key and value row read.
+// D/4 lanes read a row as float4s (a wavefront covers 64/(D/4) rows per
+// access, coalesced), dot products fold over those lanes with xor shuffles,
+// the scores [G, chunk] stay in LDS, each softmax row is one wavefront's, and
+// the value product accumulates per lane and folds across lanes and waves in
+// a fixed order.
+//
+// Decode has only batch * kv_heads query groups -- 3 for SmolLM2 at batch 1,
+// far too few blocks for 256 CUs -- so the keys are split into chunks across
+// blocks (split-K over the context): each chunk writes its own max, exp-sum
+// and unnormalised P V to scratch, and a combine pass rescales them by
+// exp(max_s - max) and divides.  One chunk writes the normalised result
+// directly, the composition's exact formula order.
+#include "common.hpp"
+#include "wave.hpp"
+
+#include <cfloat>
+
+namespace mi {
+
+constexpr int ATT_MAX_GROUP = 8;       // query heads per kv head
+constexpr int64_t ATT_MAX_CHUNK = 1024;
+constexpr int64_t ATT_MIN_CHUNK = 64;
+constexpr int64_t ATT_TARGET_BLOCKS = 512;
+
+// scores[g] = q[g] . k for one key row per lane group, folded over the row's
+// D/4 lanes.
+template <int G, int LPR>
+__device__ __forceinline__ void dots(const float4 (&qv)[G], float4 kv, float (&part)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) part[g] = (qv[g].x * kv.x + qv[g].y * kv.y) + (qv[g].z * kv.z + qv[g].w * kv.w);
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g) part[g] += __shfl_xor(part[g], o, 64);
+}
+
+// One (item, position, chunk).  DIRECT: the only chunk -- write normalised
+// rows of `out`.  Else write part[(item * S + s)] = {m[G], l[G], o[G][D]}.
+template <int D, int G>
+__global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, const float *kc, const float *vc,
+                                                              float *out, float *part, int64_t T, int64_t H,
+                                                              int64_t KVH, int64_t pos0, int64_t maxc, int64_t chunk,
+                                                              float scale, int direct) {
+  constexpr int LPR = D / 4;     // lanes per row
+  constexpr int KPW = 64 / LPR;  // rows per wavefront access
+  constexpr int U = 4;           // accesses in flight per wavefront
+  constexpr int STEP = 4 * KPW;  // rows per block access
+  extern __shared__ float sm[];
+  const int s = blockIdx.y;
+  const int64_t item = blockIdx.x;  // (sequence, kv head, position), position fastest
+  const int64_t p = item % T, bj = item / T;
+  const int64_t j = bj % KVH, b = bj / KVH;
+  const int64_t n = pos0 + p + 1;  // causal: cache positions 0 .. pos0 + p
+  const int64_t lo = static_cast<int64_t>(s) * chunk;
+  const int64_t len = n > lo ? (n - lo < chunk ? n - lo : chunk) : 0;
+  const float *K = kc + ((bj)*maxc + lo) * D;
+  const float *V = vc + ((bj)*maxc + lo) * D;
+  float *scores = sm;                     // [G][chunk]
+  float *red = sm + G * chunk;            // [4][G][D]
+  float *stat = red + 4 * G * D;          // [G] max, [G] sum
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sl = lane % LPR, kk = lane / LPR;
+  const float *qrow = q + (b * T + p) * H * D + j * G * D;
+  float4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const float4 *>(qrow + g * D + 4 * sl);
+
+  // Scores, U accesses in flight per wavefront.
+  for (int64_t c0 = static_cast<int64_t>(wave) * KPW + kk; c0 < len + kk; c0 += STEP * U) {
+    float4 kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      kv[u] = c < len ? *reinterpret_cast<const float4 *>(K + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      float pr[G];
+      dots<G, LPR>(qv, kv[u], pr);
+      if (sl == 0 && c < len)
+#pragma unroll
+        for (int g = 0; g < G; ++g) scores[g * chunk + c] = pr[g] * scale;
+    }
+  }
+  __syncthreads();
+
+  // Softmax statistics of each row (one wavefront per row).
+  for (int g = wave; g < G; g += 4) {
+    float *row = scores + g * chunk;
+    float m = -INFINITY;
+    for (int64_t c = lane; c < len; c += 64) m = max_nan(m, row[c]);
+    m = wave_max(m);
+    m = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
+    float sum = 0.0f;
+    for (int64_t c = lane; c < len; c += 64) {
+      const float e = expf(row[c] - m);
+      row[c] = e;
+      sum += e;
+    }
+    sum = wave_sum(sum);
+    if (direct) {
+      sum = isnan(sum) ? sum : (sum > FLT_MIN ? sum : FLT_MIN);
+      for (int64_t c = lane; c < len; c += 64) row[c] = row[c] / sum;
+    }
+    if (lane == 0) {
+      stat[g] = m;
+      stat[G + g] = sum;
+    }
+  }
+  __syncthreads();
+
+  // P V.
+  float4 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t c0 = static_cast<int64_t>(wave) * KPW + kk; c0 < len + kk; c0 += STEP * U) {
+    float4 vv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      if (c < len) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pg = scores[g * chunk + c];
+          acc[g].x += pg * vv[u].x;
+          acc[g].y += pg * vv[u].y;
+          acc[g].z += pg * vv[u].z;
+          acc[g].w += pg * vv[u].w;
+        }
+      }
+    }
+  }
+  // Fold the row groups of a wavefront (lanes with equal sl), then the waves.
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      acc[g].x += __shfl_xor(acc[g].x, o, 64);
+      acc[g].y += __shfl_xor(acc[g].y, o, 64);
+      acc[g].z += __shfl_xor(acc[g].z, o, 64);
+      acc[g].w += __shfl_xor(acc[g].w, o, 64);
+    }
+  if (kk == 0)
+#pragma unroll
+    for (int g = 0; g < G; ++g) *reinterpret_cast<float4 *>(red + (wave * G + g) * D + 4 * sl) = acc[g];
+  __syncthreads();
+  float *dst;
+  if (direct) {
+    dst = out + (b * T + p) * H * D + j * G * D;
+  } else {
+    float *pb = part + (item * gridDim.y + s) * static_cast<int64_t>(G * (D + 2));
+    if (tid < 2 * G) pb[tid] = stat[tid];
+    dst = pb + 2 * G;
+  }
+  for (int e = tid; e < G * D; e += 256) {
+    const int g = e / D, d = e % D;
+    dst[e] = ((red[g * D + d] + red[(G + g) * D + d]) + red[(2 * G + g) * D + d]) + red[(3 * G + g) * D + d];
+  }
+}
+
+// Combine the chunks of one (item, position): out = sum_s w_s o_s / sum_s w_s
+// l_s with w_s = exp(m_s - max_s m_s), the sum clamped below at FLT_MIN.
+template <int D, int G>
+__global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, float *out, int64_t T, int64_t H,
+                                                                int64_t KVH, int S) {
+  const int64_t item = blockIdx.x;
+  const int64_t p = item % T, bj = item / T;
+  const int64_t j = bj % KVH, b = bj / KVH;
+  const float *pb = part + item * S * static_cast<int64_t>(G * (D + 2));
+  float *dst = out + (b * T + p) * H * D + j * G * D;
+  for (int e = threadIdx.x; e < G * D; e += 256) {
+    const int g = e / D;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = max_nan(M, pb[s * G * (D + 2) + g]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float *ps = pb + s * G * (D + 2);
+      const float w = expf(ps[g] - M);
+      den += w * ps[G + g];
+      num += w * ps[2 * G + e];
+    }
+    den = isnan(den) ? den : (den > FLT_MIN ? den : FLT_MIN);
+    dst[e] = num / den;
+  }
+}
+
+template <int D, int G>
+void launch_attention(hipStream_t st, const float *q, const float *k, const float *v, float *out, float *part,
+                      int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
+                      int64_t chunk, float scale) {
+  const size_t smem = static_cast<size_t>(G * chunk + 4 * G * D + 2 * G) * sizeof(float);
+  attention_chunk_kernel<D, G><<<dim3(static_cast<unsigned>(items), static_cast<unsigned>(S)), 256, smem, st>>>(
+      q, k, v, out, part, T, H, KVH, pos0, maxc, chunk, scale, S == 1);
+  if (S > 1)
+    attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, 0, st>>>(part, out, T, H, KVH, S);
+}
+
+template <int D>
+bool dispatch_group(int64_t G, hipStream_t st, const float *q, const float *k, const float *v, float *out,
+                    float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
+                    int64_t chunk, float scale) {
+  switch (G) {
+#define MI_ATT_G(g)                                                                                   \
+  case g:                                                                                             \
+    launch_attention<D, g>(st, q, k, v, out, part, items, S, T, H, KVH, pos0, maxc, chunk, scale); \
+    return true;
+    MI_ATT_G(1) MI_ATT_G(2) MI_ATT_G(3) MI_ATT_G(4) MI_ATT_G(5) MI_ATT_G(6) MI_ATT_G(7) MI_ATT_G(8)
+#undef MI_ATT_G
+    default:
+      return false;
+  }
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
+                                 int64_t heads, int64_t kv_heads, int64_t pos0, float scale, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, qb, q);
+  MI_BUF(ctx, kb, k_cache);
+  MI_BUF(ctx, vb, v_cache);
+  if (qb->elem != MI_F32 || kb->elem != MI_F32 || vb->elem != MI_F32)
+    return fail(ctx, MI_E_ARG, "attention_rows takes F32 queries and caches");
+  if (batch < 1 || t < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return fail(ctx, MI_E_ARG, "attention_rows: batch %lld, t %lld, heads %lld, kv heads %lld", (long long)batch,
+                (long long)t, (long long)heads, (long long)kv_heads);
+  const int64_t D = kb->cols, G = heads / kv_heads;
+  if (G > ATT_MAX_GROUP)
+    return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: %lld query heads per kv head (at most %d)", (long long)G,
+                ATT_MAX_GROUP);
+  if (D != 16 && D != 32 && D != 64 && D != 128)
+    return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: head width %lld (16, 32, 64 or 128)", (long long)D);
+  if (qb->rows != batch * t || qb->cols != heads * D)
+    return fail(ctx, MI_E_ARG, "attention_rows: q is [%lld, %lld], want [%lld, %lld]", (long long)qb->rows,
+                (long long)qb->cols, (long long)(batch * t), (long long)(heads * D));
+  if (vb->cols != D || vb->rows != kb->rows || kb->rows % (batch * kv_heads))
+    return fail(ctx, MI_E_ARG, "attention_rows: caches must both be [batch * kv_heads * max_ctx, %lld]", (long long)D);
+  const int64_t maxc = kb->rows / (batch * kv_heads);
+  if (pos0 < 0 || pos0 + t > maxc)
+    return fail(ctx, MI_E_ARG, "attention_rows: positions %lld..%lld beyond the cache's %lld", (long long)pos0,
+                (long long)(pos0 + t), (long long)maxc);
+  // Chunks: at least enough that none exceeds ATT_MAX_CHUNK keys, more (down
+  // to ATT_MIN_CHUNK keys each) until the grid has ATT_TARGET_BLOCKS blocks.
+  const int64_t items = batch * kv_heads * t, nmax = pos0 + t;
+  int64_t S = (nmax + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
+  const int64_t want = (ATT_TARGET_BLOCKS + items - 1) / items;
+  const int64_t cap = (nmax + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
+  if (want > S) S = want < cap ? want : cap;
+  if (S < 1) S = 1;
+  // Chunks are a multiple of 4 keys, so the LDS fold area after the scores
+  // stays 16-byte aligned for its float4 stores.
+  const int64_t chunk = ((nmax + S - 1) / S + 3) / 4 * 4;
+  S = (nmax + chunk - 1) / chunk;
+  if (items > INT32_MAX || S > 65535) return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: grid too large");
+  float *part = nullptr;
+  if (S > 1) {
+    part = static_cast<float *>(scratch(ctx, static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float)));
+    if (!part) return fail(ctx, MI_E_OOM, "attention_rows scratch");
+  }
+  mi_id id;
+  Buffer *ob;
+  int s = new_buffer(ctx, batch * t, heads * D, MI_F32, &id, &ob);
+  if (s) return s;
+  const float *qp = static_cast<const float *>(qb->ptr), *kp = static_cast<const float *>(kb->ptr),
+              *vp = static_cast<const float *>(vb->ptr);
+  float *op = static_cast<float *>(ob->ptr);
+  const int Si = static_cast<int>(S);
+  switch (D) {
+    case 16: dispatch_group<16>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
+    case 32: dispatch_group<32>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
+    case 64: dispatch_group<64>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
+    default: dispatch_group<128>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
+  }
+  s = check_launch(ctx, "attention_rows");
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *out = id;
+  return MI_OK;
+}

@@ -285,4 +285,13 @@ inline Tensor rope(const Tensor &x, const Tensor &cos, const Tensor &sin, int64_
   return Tensor(x.ctx(), id, x.shape());
 }
 
+inline Tensor attention_rows(const Tensor &q, const Tensor &k_cache, const Tensor &v_cache, int64_t batch, int64_t t,
+                             int64_t heads, int64_t kv_heads, int64_t pos0, float scale) {
+  mi_id id;
+  check(q.ctx(), mi_attention_rows(q.ctx(), q.use(), k_cache.use(), v_cache.use(), batch, t, heads, kv_heads, pos0,
+                                   scale, &id),
+        "attention_rows");
+  return Tensor(q.ctx(), id, {q.rows(), q.cols()});
+}
+
 }  // namespace burn

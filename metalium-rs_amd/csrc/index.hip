@@ -125,6 +125,34 @@ __global__ void __launch_bounds__(256) argmax_rows_kernel(const void *x, int ele
   if (lane == 0) out[row] = best.i == INT32_MAX ? 0 : best.i;
 }
 
+// Long rows (a vocabulary's logits): one 256-thread block per row, each
+// thread a strided share, folded by the same (value, index) rule in a fixed
+// order through LDS.
+__global__ void __launch_bounds__(256) argmax_block_kernel(const void *x, int elem, int64_t cols, int32_t *out) {
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * cols;
+  ArgBest best{-INFINITY, INT32_MAX};
+  for (int64_t j = threadIdx.x; j < cols; j += 256) {
+    float v = elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[base + j])
+                              : static_cast<const float *>(x)[base + j];
+    best = better(best, ArgBest{v, static_cast<int32_t>(j)});
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ArgBest other{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)};
+    best = better(best, other);
+  }
+  __shared__ float rv[4];
+  __shared__ int32_t ri[4];
+  if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = best.v; ri[threadIdx.x >> 6] = best.i; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgBest b{rv[0], ri[0]};
+    for (int w = 1; w < 4; ++w) b = better(b, ArgBest{rv[w], ri[w]});
+    out[row] = b.i == INT32_MAX ? 0 : b.i;
+  }
+}
+
 }  // namespace mi
 
 using namespace mi;
@@ -274,7 +302,10 @@ extern "C" int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out) {
   int s = new_buffer(ctx, R, 1, MI_I32, &id, &ob);
   if (s) return s;
   if (R > 0) {
-    argmax_rows_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, R, C, static_cast<int32_t *>(ob->ptr));
+    if (C > 2048 && R <= INT32_MAX)
+      argmax_block_kernel<<<static_cast<unsigned>(R), 256, 0, ctx->stream>>>(xp, xe, C, static_cast<int32_t *>(ob->ptr));
+    else
+      argmax_rows_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, R, C, static_cast<int32_t *>(ob->ptr));
     s = check_launch(ctx, "argmax_rows");
     if (s) { mi_free(ctx, id); return s; }
   }

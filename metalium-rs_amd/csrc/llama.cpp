@@ -59,6 +59,9 @@ Tensor weight(mi_ctx *ctx, int64_t rows, int64_t cols, float stdv, uint64_t base
   return burn::float_cast(w, MI_BF16);
 }
 
+// Largest number of new positions per sequence that take the fused attention.
+constexpr int64_t kFusedAttentionMaxT = 16;
+
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
 // The forward of `t` positions per sequence at cache length m->len; returns
@@ -74,10 +77,13 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
   Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
   x = x.reshape({rows, c.hidden});
 
-  // Causal mask for t > 1, rows (position, group) of one item: row
-  // p * G + g attends to cache columns <= pos0 + p (bottom-right aligned).
+  // A few new positions (decode) take the fused attention kernel; a long
+  // prefill takes the product composition, whose MFMA products pay off there.
+  const bool fused = t <= kFusedAttentionMaxT && (D == 16 || D == 32 || D == 64 || D == 128) && G <= 8;
+  // The composition's causal mask for t > 1, rows (position, group) of one
+  // item: row p * G + g attends to cache columns <= pos0 + p.
   Tensor mask;
-  if (t > 1) {
+  if (t > 1 && !fused) {
     std::vector<uint32_t> mk(static_cast<size_t>(t * G * ctxlen));
     for (int64_t p = 0; p < t; ++p)
       for (int64_t g = 0; g < G; ++g)
@@ -101,24 +107,28 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
       burn::copy_into4(L.cache_k, pos0 * D, dst, k, 0, src, dims);
       burn::copy_into4(L.cache_v, pos0 * D, dst, v, 0, src, dims);
     }
-    // Queries regrouped per kv head: [batch * KVH * t, G * D] = rows (p, g).
-    Tensor qg;
-    {
-      const int64_t dims[4] = {batch, KVH, t, G * D};
-      const int64_t st[4] = {t * H * D, G * D, H * D, 1};
-      qg = burn::copy4(q, dims, 0, st).reshape({batch * KVH * t * G, D});
-    }
-    Tensor scores = burn::matmul_blocks(qg, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
-                                        maxc * D);
-    Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
-    Tensor o = burn::matmul_blocks(p, false, L.cache_v, false, batch * KVH, t * G, ctxlen, D, 0, t * G * ctxlen, 0,
-                                   maxc * D);
-    // Back to rows (sequence, position), heads in order h = j * G + g.
     Tensor oh;
-    {
-      const int64_t dims[4] = {batch, t, KVH, G * D};
-      const int64_t st[4] = {KVH * t * G * D, G * D, t * G * D, 1};
-      oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
+    if (fused) {
+      oh = burn::attention_rows(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0, scale);
+    } else {
+      // Queries regrouped per kv head: [batch * KVH * t, G * D] = rows (p, g).
+      Tensor qg;
+      {
+        const int64_t dims[4] = {batch, KVH, t, G * D};
+        const int64_t st[4] = {t * H * D, G * D, H * D, 1};
+        qg = burn::copy4(q, dims, 0, st).reshape({batch * KVH * t * G, D});
+      }
+      Tensor scores = burn::matmul_blocks(qg, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
+                                          maxc * D);
+      Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
+      Tensor o = burn::matmul_blocks(p, false, L.cache_v, false, batch * KVH, t * G, ctxlen, D, 0, t * G * ctxlen, 0,
+                                     maxc * D);
+      // Back to rows (sequence, position), heads in order h = j * G + g.
+      {
+        const int64_t dims[4] = {batch, t, KVH, G * D};
+        const int64_t st[4] = {KVH * t * G * D, G * D, t * G * D, 1};
+        oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
+      }
     }
     x = burn::float_add(x, burn::float_matmul(oh, false, L.wo, true));
     Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps);

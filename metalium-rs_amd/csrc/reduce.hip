@@ -17,37 +17,11 @@
 // strip of 256 columns as float4 lanes, and a second pass adds the strips'
 // partials in strip order -- deterministic, and enough blocks to fill 256 CUs.
 #include "common.hpp"
+#include "wave.hpp"
 
 #include <cfloat>
 
 namespace mi {
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float max_nan(float a, float b) {
-  // NaN ranks above every number, so it propagates.
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  return b > a ? b : a;
-}
-__device__ __forceinline__ float min_nan(float a, float b) {
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  return b < a ? b : a;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max_nan(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = min_nan(v, __shfl_xor(v, o, 64));
-  return v;
-}
 
 __device__ __forceinline__ float ld(const void *p, int elem, int64_t i) {
   return elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]) : static_cast<const float *>(p)[i];

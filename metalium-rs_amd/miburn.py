@@ -98,6 +98,7 @@ def _load() -> ctypes.CDLL:
         "mi_matmul_blocks": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, I64, I64, c_int, Ip],
         "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
+        "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
         "mi_reduce": [P, U64, c_int, c_int, Ip],
         "mi_reduce_all": [P, U64, c_int, Ip],
@@ -256,6 +257,12 @@ class Engine:
 
     def rope(self, x: int, cos: int, sin: int, heads: int, seq: int, pos0: int) -> int:
         return self._out(self._lib.mi_rope, x, cos, sin, heads, seq, pos0)
+
+    def attention_rows(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int, kv_heads: int,
+                       pos0: int, scale: float) -> int:
+        """Engine::attention_rows (server.rs:255-265): causal GQA of `t` new
+        positions against the first pos0 + t rows of each cache item."""
+        return self._out(self._lib.mi_attention_rows, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, scale)
 
     def eltwise_op_as(self, kind, a: int, b: int = 0, c: int = 0, scalar: float = 0.0, scalar2: float = 0.0,
                       out_elem: int = F32) -> int:

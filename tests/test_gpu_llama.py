@@ -90,12 +90,13 @@ def close_logits(got, want, rel=2e-3):
     assert np.abs(got - want).max() <= rel * scale, (np.abs(got - want).max(), scale)
 
 
-def test_prefill_logits_all_positions(engine, tiny):
+@pytest.mark.parametrize("t", [12, 24])  # fused attention kernel; product composition (over 16 positions)
+def test_prefill_logits_all_positions(engine, tiny, t):
     m, W = tiny
     rng = np.random.default_rng(5)
-    ids = rng.integers(0, TINY["vocab"], (2, 12)).astype(np.int32)
+    ids = rng.integers(0, TINY["vocab"], (2, t)).astype(np.int32)
     m.reset()
-    got = engine.download(m.forward(ids, all_positions=True)).reshape(2, 12, -1)
+    got = engine.download(m.forward(ids, all_positions=True)).reshape(2, t, -1)
     close_logits(got, ref_logits(W, TINY, ids))
 
 

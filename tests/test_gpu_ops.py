@@ -489,8 +489,9 @@ def test_select_add_rows_duplicates_in_order(engine):
     same_bits(got, orc.select_add_rows(t, idx, val))
 
 
-def test_argmax_first_and_nan(engine):
-    x = rnd(40, 49152 // 16)
+@pytest.mark.parametrize("cols", [3072, 1000])  # block-per-row and wave-per-row kernels
+def test_argmax_first_and_nan(engine, cols):
+    x = rnd(40, cols)
     x[1, 5] = x[1, 9] = 100.0  # tie: the first wins
     x[2, 7] = np.nan  # NaN above every number
     x[2, 3] = np.inf
@@ -504,6 +505,72 @@ def test_argmax_first_and_nan(engine):
 def test_argmax_vocab_rows(engine):
     x = rnd(32, 49152)
     assert np.array_equal(engine.download(engine.argmax_row(engine.upload(x))), orc.argmax_rows(x))
+
+
+def test_argmax_bf16_long_rows(engine):
+    x = rnd(8, 49152)
+    x[2, 40000] = x[2, 40001] = 50.0
+    xb = orc.to_bf16(x)  # ties from the rounding: the first wins
+    got = engine.download(engine.argmax_row(engine.upload_bf16(xb)))
+    assert np.array_equal(got, orc.argmax_rows(orc.from_bf16(xb)))
+    assert got[2, 0] == 40000
+
+
+# ------------------------------------------------------------------ attention
+def attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale):
+    """float64 causal GQA over the cache (crates/burn-tt/src/ops.rs:4520-4595)."""
+    D = kc.shape[1]
+    G = heads // kvh
+    maxc = kc.shape[0] // (batch * kvh)
+    K = kc.reshape(batch, kvh, maxc, D).astype(np.float64)
+    V = vc.reshape(batch, kvh, maxc, D).astype(np.float64)
+    Q = q.reshape(batch, t, heads, D).astype(np.float64)
+    out = np.zeros((batch, t, heads, D))
+    for b in range(batch):
+        for p in range(t):
+            n = pos0 + p + 1
+            for h in range(heads):
+                s = K[b, h // G, :n] @ Q[b, p, h] * scale
+                w = np.exp(s - s.max())
+                out[b, p, h] = (w / w.sum()) @ V[b, h // G, :n]
+    return out.reshape(batch * t, heads * D)
+
+
+@pytest.mark.parametrize("batch,t,heads,kvh,D,pos0,maxc", [
+    (1, 1, 9, 3, 64, 639, 640),      # SmolLM2 decode at a long context: many key chunks
+    (1, 1, 9, 3, 64, 0, 640),        # first position: one key
+    (32, 1, 9, 3, 64, 200, 640),     # batch 32 decode
+    (2, 5, 4, 2, 16, 7, 64),         # several new positions, causal inside the chunk
+    (3, 16, 8, 1, 128, 30, 64),      # 8 query heads per kv head
+    (2, 3, 4, 4, 32, 2000, 2304),    # no grouping, context over one chunk's limit
+    (1, 2, 6, 2, 64, 0, 8),          # whole cache, one chunk, direct write
+])
+def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
+    q = rnd(batch * t, heads * D)
+    kc = rnd(batch * kvh * maxc, D)
+    vc = rnd(batch * kvh * maxc, D)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    got = engine.download(engine.attention_rows(engine.upload(q), engine.upload(kc), engine.upload(vc), batch, t,
+                                                heads, kvh, pos0, scale))
+    want = attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale)
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
+
+
+def test_attention_rows_errors(engine):
+    q = engine.upload(rnd(2, 10 * 64))
+    k = engine.upload(rnd(2 * 1 * 16, 64))
+    for args, kind in [((2, 1, 10, 1, 0), "UNSUPPORTED"),  # 10 query heads per kv head
+                       ((2, 1, 10, 2, 16), "ARG"),          # cache holds 8 positions per item, not 17
+                       ((2, 1, 10, 3, 0), "ARG")]:          # heads not a multiple of kv heads
+        with pytest.raises(miburn.MiError) as e:
+            engine.attention_rows(q, k, k, *args[:4], args[4], 0.125)
+        assert e.value.kind == kind, (args, e.value)
+    q48 = engine.upload(rnd(1, 2 * 48))
+    k48 = engine.upload(rnd(4, 48))
+    with pytest.raises(miburn.MiError) as e:
+        engine.attention_rows(q48, k48, k48, 1, 1, 2, 1, 0, 0.125)
+    assert e.value.kind == "UNSUPPORTED"
 
 
 # ------------------------------------------------------------- casts, copies
