@@ -173,6 +173,25 @@ def mlp_bench(eng, steps: int = 100) -> dict:
             "last_loss": round(float(losses[-1]), 5)}
 
 
+def transformer_bench(eng, steps: int = 20) -> dict:
+    """4 layers, d_model 256, 4 heads, FFN 1024 GELU,
+    LayerNorm, vocab 8192, seq 128, batch 16, fp32; uniform random tokens and
+    targets; forward, cross-entropy, backward and SGD each step."""
+    import miburn
+    cfg = miburn.TRANSFORMER_CONFIG4
+    B, S = 16, 128
+    R, d, F, V, H = B * S, cfg["d_model"], cfg["d_ff"], cfg["vocab"], cfg["heads"]
+    fwd = cfg["layers"] * (4 * 2 * R * d * d + 2 * 2 * R * d * F + 2 * 2 * B * H * S * S * (d // H)) + 2 * R * d * V
+    m = miburn.Transformer(eng, cfg, seed=0)
+    m.train_synthetic(B, S, 2, 0.05, data_seed=1)  # warm the kernels and the allocator
+    losses, ms = m.train_synthetic(B, S, steps, 0.05, data_seed=2)
+    m.close()
+    step_ms = ms / steps
+    return {"steps": steps, "batch": B, "seq": S, "ms_per_step": round(step_ms, 3),
+            "flop_per_step": 3 * fwd, "tflops": round(3 * fwd / (step_ms * 1e-3) / 1e12, 2),
+            "first_loss": round(float(losses[0]), 4), "last_loss": round(float(losses[-1]), 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,7 +202,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true")
     ap.add_argument("--no-models", action="store_true")
-    ap.add_argument("--only", choices=["decoder", "mlp"],
+    ap.add_argument("--only", choices=["decoder", "mlp", "transformer"],
                     help="run one model harness alone (for profiling) and print its JSON")
     ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
     args = ap.parse_args()
@@ -197,7 +216,8 @@ def main() -> int:
     import miburn
     eng = miburn.Engine(0)
     if args.only:
-        out = decoder_bench(eng, args.batch) if args.only == "decoder" else mlp_bench(eng)
+        out = {"decoder": lambda: decoder_bench(eng, args.batch), "mlp": lambda: mlp_bench(eng),
+               "transformer": lambda: transformer_bench(eng)}[args.only]()
         print(json.dumps({"harness": args.only, **out}), flush=True)
         eng.close()
         return 0
@@ -258,6 +278,7 @@ def main() -> int:
     if not args.no_models:
         line["decoder"] = [decoder_bench(eng, 1), decoder_bench(eng, 32)]
         line["mlp_train"] = mlp_bench(eng)
+        line["transformer_train"] = transformer_bench(eng)
     print(json.dumps(line), flush=True)
     eng.close()
     return 0

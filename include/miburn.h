@@ -192,6 +192,32 @@ int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem,
 int mi_layer_norm(mi_ctx *ctx, mi_id a, mi_id gamma, mi_id beta, float eps,
                   mi_id *out);
 
+/* ---- backward rows for the training harnesses.  No Engine counterpart:
+ * Burn's autodiff composes these gradients from the forward's primitive ops
+ * (burn-nn LayerNorm; softmax's exp / sum / divide, ops.rs:5133-5166); the
+ * fused forms are this engine's, for the transformer training step. ---- */
+/* LayerNorm's gradient: with xh = (x - mean) / sqrt(var + eps) and
+ * g = dy * gamma, dx = (g - mean(g) - xh * mean(g * xh)) / sqrt(var + eps)
+ * (+ residual_grad if not 0), dgamma = sum_rows(dy * xh), dbeta =
+ * sum_rows(dy) ([1, cols] each).  x, dy F32 [rows, cols], cols <= 1024;
+ * gamma [1, cols] or 0.  Three new ids. */
+int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id dy,
+                           mi_id residual_grad, float eps, mi_id *dx,
+                           mi_id *dgamma, mi_id *dbeta);
+/* Softmax's gradient over rows, p = softmax(scale * x):
+ * ds = scale * p * (dp - sum_row(p * dp)).  F32 [rows, cols]. */
+int mi_softmax_backward(mi_ctx *ctx, mi_id p, mi_id dp, float scale,
+                        mi_id *out);
+
+/* The optimizer step `param <- param - grad * lr` (burn-optim `Sgd`, no
+ * momentum or decay; the reference applies it per parameter, and its traced
+ * training step writes the weights in place, crates/burn-tt/src/trace.rs:
+ * 989-1010) for `count` parameters in place, in one launch per 48.  params[i]
+ * and grads[i] are F32 buffers of equal element count (grads[i] may have any
+ * [rows, cols] folding); the same bits as the two-op form. */
+int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params,
+                  const mi_id *grads, float lr);
+
 /* ---- indexing (ops.rs:1001-1240) ---- */
 /* Engine::argmax_row (server.rs:477) over every row: `[r, c] -> [r, 1]` I32,
  * the first maximum, a NaN ranking above every number. */

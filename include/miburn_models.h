@@ -75,6 +75,42 @@ int mi_mlp_train_synthetic(mi_mlp *m, int32_t batch, int32_t steps, float lr,
                            uint64_t data_seed, float *losses, double *ms);
 const char *mi_mlp_last_error(void);
 
+/* ---- Transformer training (the reference's TinyTransformer,
+ * crates/tt-mnist/src/transformer.rs:36-166, trained by
+ * crates/tt-tests/tests/step59_burn_transformer.rs): Embedding, pre-norm
+ * encoder layers (LayerNorm, multi-head self-attention without a mask,
+ * LayerNorm, Linear-GELU-Linear), Linear head, cross-entropy, SGD; F32.
+ * Burn's default init drawn on the device from `seed`: embedding N(0, 1),
+ * Linear weight [d_in, d_out] and bias U(-1/sqrt(d_in), 1/sqrt(d_in)),
+ * LayerNorm gamma 1, beta 0. ---- */
+typedef struct mi_transformer_config {
+  int32_t vocab, d_model, heads, d_ff, layers;
+  float eps;
+} mi_transformer_config;
+
+typedef struct mi_transformer mi_transformer;
+int mi_transformer_create(mi_ctx *ctx, const mi_transformer_config *cfg,
+                          uint64_t seed, mi_transformer **out);
+int mi_transformer_destroy(mi_transformer *m);
+/* layer < 0: which 0 embedding [vocab, d], 1 head weight [d, vocab], 2 head
+ * bias [1, vocab].  layer >= 0: which 0 ln1 gamma, 1 ln1 beta, 2 wq, 3 bq,
+ * 4 wk, 5 bk, 6 wv, 7 bv, 8 wo, 9 bo (weights [d, d], biases [1, d]),
+ * 10 ln2 gamma, 11 ln2 beta, 12 w1 [d, d_ff], 13 b1, 14 w2 [d_ff, d], 15 b2. */
+int mi_transformer_param(mi_transformer *m, int layer, int which, mi_id *out);
+/* One step on resident tokens and targets (batch * seq I32 each, row-major
+ * [batch, seq]): forward, mean cross-entropy over all positions, backward,
+ * SGD with rate lr.  The loss [1, 1] is a new id the caller frees. */
+int mi_transformer_train_step(mi_transformer *m, mi_id tokens, mi_id targets,
+                              int32_t batch, int32_t seq, float lr,
+                              mi_id *loss);
+/* `steps` steps on device-drawn tokens and targets, each uniform in
+ * [0, vocab); per-step losses and the wall time of all steps (ms, synced). */
+int mi_transformer_train_synthetic(mi_transformer *m, int32_t batch,
+                                   int32_t seq, int32_t steps, float lr,
+                                   uint64_t data_seed, float *losses,
+                                   double *ms);
+const char *mi_transformer_last_error(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -232,6 +232,38 @@ inline Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &bet
   return Tensor(x.ctx(), id, x.shape());
 }
 
+struct NormGrads {
+  Tensor dx, dgamma, dbeta;
+};
+// LayerNorm's gradient (fused); `residual` (may be undefined) is added to dx.
+inline NormGrads layer_norm_backward(const Tensor &x, const Tensor &gamma, const Tensor &dy, const Tensor &residual,
+                                     float eps) {
+  mi_id ids[3];
+  check(x.ctx(), mi_layer_norm_backward(x.ctx(), x.use(), gamma.use(), dy.use(), residual.defined() ? residual.use() : 0,
+                                        eps, &ids[0], &ids[1], &ids[2]),
+        "layer_norm_backward");
+  return {Tensor(x.ctx(), ids[0], x.shape()), Tensor(x.ctx(), ids[1], {1, x.cols()}),
+          Tensor(x.ctx(), ids[2], {1, x.cols()})};
+}
+
+// Softmax's gradient over rows: scale * p * (dp - rowsum(p * dp)).
+inline Tensor softmax_backward(const Tensor &p, const Tensor &dp, float scale) {
+  mi_id id;
+  check(p.ctx(), mi_softmax_backward(p.ctx(), p.use(), dp.use(), scale, &id), "softmax_backward");
+  return Tensor(p.ctx(), id, p.shape());
+}
+
+// Sgd's step in place over (parameter, gradient) pairs, one launch.
+inline void sgd_update(mi_ctx *ctx, const std::vector<const Tensor *> &params, const std::vector<Tensor> &grads,
+                       float lr) {
+  std::vector<mi_id> p, g;
+  for (size_t i = 0; i < params.size(); ++i) {
+    p.push_back(params[i]->use());
+    g.push_back(grads[i].use());
+  }
+  check(ctx, mi_sgd_update(ctx, static_cast<int64_t>(p.size()), p.data(), g.data(), lr), "sgd_update");
+}
+
 inline Tensor argmax_rows(const Tensor &x) {
   mi_id id;
   check(x.ctx(), mi_argmax_rows(x.ctx(), x.use(), &id), "float_argmax");

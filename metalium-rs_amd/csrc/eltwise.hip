@@ -647,3 +647,86 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
   *out = id;
   return MI_OK;
 }
+
+// ------------------------------------------------------------- SGD update
+// The optimizer's `param - grad * lr` (burn-optim `Sgd` without momentum or
+// decay) for many parameters in one launch, in place.  Each parameter gets a
+// run of blocks; a block finds its parameter by a scan of the (at most
+// SGD_MAX_PARAMS) block offsets in the kernel argument, then updates 4 float4
+// per thread.  Bits equal the two-op form: grad * lr rounded, then subtracted.
+namespace mi {
+constexpr int SGD_MAX_PARAMS = 48;
+constexpr int SGD_BLOCK_ELEMS = 256 * 16;
+
+struct SgdList {
+  float *p[SGD_MAX_PARAMS];
+  const float *g[SGD_MAX_PARAMS];
+  int64_t n[SGD_MAX_PARAMS];
+  int64_t first_block[SGD_MAX_PARAMS + 1];
+  int count;
+};
+
+__global__ void __launch_bounds__(256) sgd_kernel(SgdList L, float lr) {
+  int i = 0;
+  while (i + 1 < L.count && static_cast<int64_t>(blockIdx.x) >= L.first_block[i + 1]) ++i;
+  float *p = L.p[i];
+  const float *g = L.g[i];
+  const int64_t n = L.n[i];
+  const int64_t base = (static_cast<int64_t>(blockIdx.x) - L.first_block[i]) * SGD_BLOCK_ELEMS;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t e = base + (static_cast<int64_t>(u) * 256 + threadIdx.x) * 4;
+    if (e + 3 < n) {
+      float4 pv = *reinterpret_cast<const float4 *>(p + e);
+      const float4 gv = *reinterpret_cast<const float4 *>(g + e);
+      pv.x = __fsub_rn(pv.x, __fmul_rn(gv.x, lr));
+      pv.y = __fsub_rn(pv.y, __fmul_rn(gv.y, lr));
+      pv.z = __fsub_rn(pv.z, __fmul_rn(gv.z, lr));
+      pv.w = __fsub_rn(pv.w, __fmul_rn(gv.w, lr));
+      *reinterpret_cast<float4 *>(p + e) = pv;
+    } else {
+      for (int64_t k = e; k < n && k < e + 4; ++k) p[k] = __fsub_rn(p[k], __fmul_rn(g[k], lr));
+    }
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params, const mi_id *grads, float lr) {
+  MI_ENTER(ctx);
+  if (count < 0 || (count > 0 && (!params || !grads))) return fail(ctx, MI_E_ARG, "sgd_update: null lists");
+  SgdList L;
+  L.count = 0;
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (L.count == 0) return MI_OK;
+    L.first_block[L.count] = blocks;
+    sgd_kernel<<<static_cast<unsigned>(blocks), 256, 0, ctx->stream>>>(L, lr);
+    L.count = 0;
+    blocks = 0;
+    return check_launch(ctx, "sgd_update");
+  };
+  for (int64_t i = 0; i < count; ++i) {
+    const Buffer *pb = lookup(ctx, params[i]);
+    const Buffer *gb = lookup(ctx, grads[i]);
+    if (!pb || !gb) return fail(ctx, MI_E_ID, "sgd_update: unknown id in entry %lld", (long long)i);
+    if (pb->elem != MI_F32 || gb->elem != MI_F32) return fail(ctx, MI_E_ARG, "sgd_update: entry %lld is not F32", (long long)i);
+    const int64_t n = pb->rows * pb->cols;
+    if (gb->rows * gb->cols != n)
+      return fail(ctx, MI_E_ARG, "sgd_update: entry %lld: %lld parameters, %lld gradients", (long long)i, (long long)n,
+                  (long long)(gb->rows * gb->cols));
+    if (params[i] == grads[i]) return fail(ctx, MI_E_ARG, "sgd_update: entry %lld updates a buffer by itself", (long long)i);
+    if (n == 0) continue;
+    const int64_t nb = (n + SGD_BLOCK_ELEMS - 1) / SGD_BLOCK_ELEMS;
+    if (L.count == SGD_MAX_PARAMS || blocks + nb > INT32_MAX) {
+      int s = flush();
+      if (s) return s;
+    }
+    L.p[L.count] = static_cast<float *>(pb->ptr);
+    L.g[L.count] = static_cast<const float *>(gb->ptr);
+    L.n[L.count] = n;
+    L.first_block[L.count] = blocks;
+    ++L.count;
+    blocks += nb;
+  }
+  return flush();
+}

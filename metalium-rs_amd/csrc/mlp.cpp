@@ -76,12 +76,8 @@ Tensor step(mi_mlp *m, const Tensor &x, const Tensor &labels, float lr) {
   Tensor da1 = burn::relu_backward(h, dh);
   Tensor dw1 = burn::float_matmul(x, true, da1, false);
   Tensor db1 = burn::reduce(da1, MI_R_SUM, MI_AXIS_ROWS);
-  // SGD.
-  auto sgd = [&](Tensor &p, const Tensor &grad) { p = burn::float_sub(p, burn::float_mul_scalar(grad, lr)); };
-  sgd(m->w1, dw1);
-  sgd(m->b1, db1);
-  sgd(m->w2, dw2);
-  sgd(m->b2, db2);
+  // SGD, in place, one launch.
+  burn::sgd_update(m->ctx, {&m->w1, &m->b1, &m->w2, &m->b2}, {dw1, db1, dw2, db2}, lr);
   return loss;
 }
 

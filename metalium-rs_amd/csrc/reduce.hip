@@ -14,8 +14,10 @@
 // when it fits (softmax reads its row from HBM once and writes it once), and
 // fold across lanes with a fixed butterfly, so results are deterministic.
 // Column sums (over rows) split the rows over a 2-D grid, each block summing a
-// strip of 256 columns as float4 lanes, and a second pass adds the strips'
-// partials in strip order -- deterministic, and enough blocks to fill 256 CUs.
+// strip of 256 columns over a range of rows as float4 lanes, and a second
+// pass folds the row ranges' partials in a fixed order (16 interleaved
+// chains, then in chain order) -- deterministic, and enough blocks to fill
+// 256 CUs.
 #include "common.hpp"
 #include "wave.hpp"
 
@@ -123,17 +125,41 @@ __global__ void __launch_bounds__(256) reduce_rows_part(const void *x, int elem,
   }
 }
 
-__global__ void reduce_rows_final(const float *part, float *out, int64_t splits, int64_t cols, int64_t rows, int op) {
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  float s = part[c];
-  for (int64_t k = 1; k < splits; ++k) {
-    float v = part[k * cols + c];
-    if (op == MI_R_MAX) s = max_nan(s, v);
-    else if (op == MI_R_MIN) s = min_nan(s, v);
-    else s += v;
+// Fold the partial rows [nb, n] of a split reduction into [1, n].  A block of
+// 16 wavefronts takes 64 columns; wavefront w folds partial rows w, w + 16,
+// ... (four loads in flight), and the 16 results fold in wave order through
+// LDS -- a fixed order, so the result is deterministic.  Columns below
+// `split_at` go to out0, the rest to out1 (two reductions in one pass).
+__global__ void __launch_bounds__(1024) fold_partials_kernel(const float *part, int64_t nb, int64_t n, int op,
+                                                             float div, float *out0, int64_t split_at, float *out1) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  auto fold = [op](float a, float b) {
+    if (op == MI_R_MAX) return max_nan(a, b);
+    if (op == MI_R_MIN) return min_nan(a, b);
+    return a + b;
+  };
+  float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  if (c < n) {
+    int64_t k = w;
+    for (; k + 48 < nb; k += 64) {
+      const float v0 = part[k * n + c], v1 = part[(k + 16) * n + c];
+      const float v2 = part[(k + 32) * n + c], v3 = part[(k + 48) * n + c];
+      acc = fold(fold(fold(fold(acc, v0), v1), v2), v3);
+    }
+    for (; k < nb; k += 16) acc = fold(acc, part[k * n + c]);
   }
-  out[c] = (op == MI_R_MEAN) ? s / static_cast<float>(rows) : s;
+  red[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && c < n) {
+    float s = red[0][lane];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) s = fold(s, red[k][lane]);
+    if (op == MI_R_MEAN) s = s / div;
+    if (c < split_at) out0[c] = s;
+    else out1[c - split_at] = s;
+  }
 }
 
 // ---------------------------------------------------------- full reduction
@@ -465,7 +491,8 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
       dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
       if (vec) reduce_rows_part<true><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
       else reduce_rows_part<false><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
-      reduce_rows_final<<<grid_for(C, 256, INT32_MAX), 256, 0, ctx->stream>>>(part, o, splits, C, R, op);
+      fold_partials_kernel<<<static_cast<unsigned>((C + 63) / 64), 1024, 0, ctx->stream>>>(
+          part, splits, C, op, static_cast<float>(R), o, C, nullptr);
     }
   }
   s = check_launch(ctx, "reduce");
@@ -621,6 +648,184 @@ extern "C" int mi_layer_norm(mi_ctx *ctx, mi_id a, mi_id gamma, mi_id beta, floa
     }
   }
   s = check_launch(ctx, "layer_norm");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+namespace mi {
+
+// ------------------------------------------------------------ backward rows
+// LayerNorm's backward, fused (Burn's autodiff composes it from the forward's
+// primitive ops -- mean, subtract, square, mean, sqrt, divide, scale, shift):
+// with xh = (x - mean) / den, den = sqrt(var + eps) and g = dy * gamma,
+//   dx = (g - mean(g) - xh * mean(g * xh)) / den   (+ an incoming residual
+//   gradient, added in the same pass),
+//   dgamma = sum over rows of dy * xh,  dbeta = sum over rows of dy.
+// One wavefront per row with the row in registers (T columns per lane);
+// each block of 4 waves takes LNB_ROWS rows and writes its column partials
+// of dgamma and dbeta; a second pass folds the blocks' partials.
+constexpr int LNB_ROWS = 16;
+
+template <int T>
+__global__ void __launch_bounds__(256) layer_norm_backward_kernel(const float *x, const float *gamma, const float *dy,
+                                                                  const float *dres, float eps, float *dx,
+                                                                  float *part, int64_t rows, int64_t cols) {
+  __shared__ float red[4][2][64 * T];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float pg[T], pb[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) pg[t] = pb[t] = 0.0f;
+  for (int r = wave; r < LNB_ROWS; r += 4) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * LNB_ROWS + r;
+    if (row >= rows) break;
+    const int64_t base = row * cols;
+    float v[T], g[T], d[T];
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = lane + 64 * t;
+      v[t] = j < cols ? x[base + j] : 0.0f;
+      d[t] = j < cols ? dy[base + j] : 0.0f;
+      g[t] = j < cols ? d[t] * (gamma ? gamma[j] : 1.0f) : 0.0f;
+      s += v[t];
+    }
+    const float inv_n = 1.0f / static_cast<float>(cols);
+    const float mean = wave_sum(s) / static_cast<float>(cols);
+    float q = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = lane + 64 * t;
+      const float c = j < cols ? v[t] - mean : 0.0f;
+      q += c * c;
+    }
+    const float den = __fsqrt_rn(wave_sum(q) / static_cast<float>(cols) + eps);
+    float sg = 0.0f, sgx = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      v[t] = (v[t] - mean) / den;  // xh
+      sg += g[t];
+      sgx += g[t] * v[t];
+    }
+    const float mg = wave_sum(sg) * inv_n, mgx = wave_sum(sgx) * inv_n;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = lane + 64 * t;
+      if (j < cols) {
+        float o = (g[t] - mg - v[t] * mgx) / den;
+        if (dres) o = o + dres[base + j];
+        dx[base + j] = o;
+        pg[t] += d[t] * v[t];
+        pb[t] += d[t];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    red[wave][0][lane + 64 * t] = pg[t];
+    red[wave][1][lane + 64 * t] = pb[t];
+  }
+  __syncthreads();
+  float *pp = part + static_cast<int64_t>(blockIdx.x) * 2 * cols;
+  for (int64_t j = threadIdx.x; j < 2 * cols; j += 256) {
+    const int w = j < cols ? 0 : 1;
+    const int64_t c = j < cols ? j : j - cols;
+    pp[j] = ((red[0][w][c] + red[1][w][c]) + red[2][w][c]) + red[3][w][c];
+  }
+}
+
+// Softmax's backward over rows (Burn composes it from the forward's ops):
+// ds = scale * p * (dp - sum_row(p * dp)).  One wavefront per row; the row
+// is read twice, the second time from cache.
+__global__ void __launch_bounds__(256) softmax_backward_kernel(const float *p, const float *dp, float scale, float *ds,
+                                                               int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float s = 0.0f;
+  for (int64_t j = lane; j < cols; j += 64) s += p[base + j] * dp[base + j];
+  s = wave_sum(s);
+  for (int64_t j = lane; j < cols; j += 64) ds[base + j] = scale * (p[base + j] * (dp[base + j] - s));
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id dy, mi_id residual_grad, float eps,
+                                      mi_id *dx, mi_id *dgamma, mi_id *dbeta) {
+  MI_ENTER(ctx);
+  if (!dx || !dgamma || !dbeta) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, db, dy);
+  const Buffer *gb = nullptr, *rb = nullptr;
+  if (gamma) { gb = lookup(ctx, gamma); if (!gb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)gamma); }
+  if (residual_grad) {
+    rb = lookup(ctx, residual_grad);
+    if (!rb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)residual_grad);
+  }
+  const int64_t R = xb->rows, C = xb->cols;
+  if (xb->elem != MI_F32 || db->elem != MI_F32 || db->rows != R || db->cols != C)
+    return fail(ctx, MI_E_ARG, "layer_norm_backward: x and dy must be F32 of one shape");
+  if (gb && (gb->elem != MI_F32 || gb->rows * gb->cols != C)) return fail(ctx, MI_E_ARG, "layer_norm_backward: gamma");
+  if (rb && (rb->elem != MI_F32 || rb->rows != R || rb->cols != C))
+    return fail(ctx, MI_E_ARG, "layer_norm_backward: residual gradient shape");
+  const int t = pick_t(C);
+  if (t == 0 || t > 16) return fail(ctx, MI_E_UNSUPPORTED, "layer_norm_backward: %lld columns (at most 1024)", (long long)C);
+  const int64_t nb = (R + LNB_ROWS - 1) / LNB_ROWS;
+  if (nb > INT32_MAX) return fail(ctx, MI_E_UNSUPPORTED, "layer_norm_backward: too many rows");
+  float *part = nullptr;
+  if (R > 0) {
+    part = static_cast<float *>(scratch(ctx, static_cast<size_t>(nb * 2 * C) * sizeof(float)));
+    if (!part) return fail(ctx, MI_E_OOM, "layer_norm_backward scratch");
+  }
+  mi_id ids[3];
+  Buffer *bx, *bg, *bb;
+  int s = new_buffer(ctx, R, C, MI_F32, &ids[0], &bx);
+  if (s) return s;
+  s = new_buffer(ctx, 1, C, MI_F32, &ids[1], &bg);
+  if (s) { mi_free(ctx, ids[0]); return s; }
+  s = new_buffer(ctx, 1, C, MI_F32, &ids[2], &bb);
+  if (s) { mi_free(ctx, ids[0]); mi_free(ctx, ids[1]); return s; }
+  if (R == 0) {
+    (void)hipMemsetAsync(bg->ptr, 0, C * sizeof(float), ctx->stream);
+    (void)hipMemsetAsync(bb->ptr, 0, C * sizeof(float), ctx->stream);
+  } else {
+    const float *xp = static_cast<const float *>(xb->ptr), *dp = static_cast<const float *>(db->ptr);
+    const float *gp = gb ? static_cast<const float *>(gb->ptr) : nullptr;
+    const float *rp = rb ? static_cast<const float *>(rb->ptr) : nullptr;
+    float *o = static_cast<float *>(bx->ptr);
+    const unsigned g = static_cast<unsigned>(nb);
+    switch (t) {
+#define MI_LNB(T) case T: layer_norm_backward_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, gp, dp, rp, eps, o, part, R, C); break;
+      MI_LNB(1) MI_LNB(2) MI_LNB(4) MI_LNB(8) MI_LNB(16)
+#undef MI_LNB
+    }
+    fold_partials_kernel<<<static_cast<unsigned>((2 * C + 63) / 64), 1024, 0, ctx->stream>>>(
+        part, nb, 2 * C, MI_R_SUM, 1.0f, static_cast<float *>(bg->ptr), C, static_cast<float *>(bb->ptr));
+  }
+  s = check_launch(ctx, "layer_norm_backward");
+  if (s) { for (mi_id i : ids) mi_free(ctx, i); return s; }
+  *dx = ids[0]; *dgamma = ids[1]; *dbeta = ids[2];
+  return MI_OK;
+}
+
+extern "C" int mi_softmax_backward(mi_ctx *ctx, mi_id p, mi_id dp, float scale, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, pb, p);
+  MI_BUF(ctx, db, dp);
+  if (pb->elem != MI_F32 || db->elem != MI_F32 || pb->rows != db->rows || pb->cols != db->cols)
+    return fail(ctx, MI_E_ARG, "softmax_backward: p and dp must be F32 of one shape");
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, pb->rows, pb->cols, MI_F32, &id, &ob);
+  if (s) return s;
+  if (pb->rows > 0 && pb->cols > 0)
+    softmax_backward_kernel<<<grid_for(pb->rows, 4, INT32_MAX), 256, 0, ctx->stream>>>(
+        static_cast<const float *>(pb->ptr), static_cast<const float *>(db->ptr), scale, static_cast<float *>(ob->ptr),
+        pb->rows, pb->cols);
+  s = check_launch(ctx, "softmax_backward");
   if (s) { mi_free(ctx, id); return s; }
   *out = id;
   return MI_OK;

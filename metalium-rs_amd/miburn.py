@@ -16,6 +16,7 @@ machine where libmiburn.so is missing raises, and there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import weakref
 import os
 from typing import Optional, Sequence, Tuple
 
@@ -105,6 +106,9 @@ def _load() -> ctypes.CDLL:
         "mi_softmax_rows": [P, U64, U64, c_float, c_int, c_int, Ip],
         "mi_rms_norm": [P, U64, U64, c_float, c_int, Ip],
         "mi_layer_norm": [P, U64, U64, U64, c_float, Ip],
+        "mi_layer_norm_backward": [P, U64, U64, U64, U64, c_float, Ip, Ip, Ip],
+        "mi_softmax_backward": [P, U64, U64, c_float, Ip],
+        "mi_sgd_update": [P, I64, ctypes.POINTER(U64), ctypes.POINTER(U64), c_float],
         "mi_argmax_rows": [P, U64, Ip],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_pick_columns": [P, U64, U64, Ip],
@@ -142,6 +146,7 @@ class Engine:
     """One device context: the reference's `KmdEngine` (server.rs:4071) for an MI355X."""
 
     def __init__(self, device: int = 0):
+        self._children = weakref.WeakSet()  # model harnesses to close before the context
         self._lib = lib()
         ctx = ctypes.c_void_p()
         st = self._lib.mi_ctx_create(device, ctypes.byref(ctx))
@@ -151,7 +156,11 @@ class Engine:
 
     # -- plumbing --------------------------------------------------------
     def close(self) -> None:
+        """Destroy the context; the model harnesses built on it are closed
+        first (their buffers belong to the context)."""
         if self.ctx:
+            for child in list(self._children):
+                child.close()
             self._lib.mi_ctx_destroy(self.ctx)
             self.ctx = None
 
@@ -285,6 +294,23 @@ class Engine:
     def layer_norm(self, a: int, gamma: int = 0, beta: int = 0, eps: float = 1e-5) -> int:
         return self._out(self._lib.mi_layer_norm, a, gamma, beta, eps)
 
+    def layer_norm_backward(self, x: int, gamma: int, dy: int, residual_grad: int = 0, eps: float = 1e-5):
+        """LayerNorm's gradient, fused: (dx, dgamma, dbeta) ids."""
+        outs = [ctypes.c_uint64() for _ in range(3)]
+        self._check(self._lib.mi_layer_norm_backward(self.ctx, x, gamma, dy, residual_grad, eps,
+                                                     *[ctypes.byref(o) for o in outs]))
+        return tuple(o.value for o in outs)
+
+    def sgd_update(self, params, grads, lr: float) -> None:
+        """In place: params[i] <- params[i] - grads[i] * lr."""
+        n = len(params)
+        pa = (ctypes.c_uint64 * max(n, 1))(*params)
+        ga = (ctypes.c_uint64 * max(n, 1))(*grads)
+        self._check(self._lib.mi_sgd_update(self.ctx, n, pa, ga, lr))
+
+    def softmax_backward(self, p: int, dp: int, scale: float = 1.0) -> int:
+        return self._out(self._lib.mi_softmax_backward, p, dp, scale)
+
     def argmax_row(self, a: int) -> int:
         return self._out(self._lib.mi_argmax_rows, a)
 
@@ -407,6 +433,7 @@ class Llama:
         h = ctypes.c_void_p()
         self._check(self.L.mi_llama_create(eng.ctx, ctypes.byref(c), seed, init_std, ctypes.byref(h)))
         self.h = h
+        eng._children.add(self)
 
     def _check(self, st):
         if st != 0:
@@ -470,6 +497,7 @@ class Mlp:
         h = ctypes.c_void_p()
         self._check(L.mi_mlp_create(eng.ctx, d_in, hidden, d_out, lcg_seed, ctypes.byref(h)))
         self.h = h
+        eng._children.add(self)
         self.d_out = d_out
 
     def _check(self, st):
@@ -507,4 +535,86 @@ class Mlp:
         ms = ctypes.c_double()
         self._check(self.L.mi_mlp_train_synthetic(self.h, batch, steps, lr, data_seed, losses.ctypes.data,
                                                   ctypes.byref(ms)))
+        return losses, ms.value
+
+
+class TransformerConfig(ctypes.Structure):
+    _fields_ = [("vocab", ctypes.c_int32), ("d_model", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("d_ff", ctypes.c_int32), ("layers", ctypes.c_int32), ("eps", ctypes.c_float)]
+
+
+# BASELINE config 4's shape.
+TRANSFORMER_CONFIG4 = dict(vocab=8192, d_model=256, heads=4, d_ff=1024, layers=4, eps=1e-5)
+TRANSFORMER_LAYER_PARAMS = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "ln2_g", "ln2_b",
+                            "w1", "b1", "w2", "b2")
+
+
+class Transformer:
+    """The transformer training harness (crates/tt-mnist/src/transformer.rs:36-166;
+    step59_burn_transformer.rs) on an Engine."""
+
+    def __init__(self, eng: Engine, cfg: dict, seed: int = 0):
+        self.eng = eng
+        L = lib()
+        if not getattr(L, "_tf_bound", False):
+            P, I32, U64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64
+            L.mi_transformer_create.argtypes = [P, ctypes.POINTER(TransformerConfig), U64, ctypes.POINTER(P)]
+            L.mi_transformer_destroy.argtypes = [P]
+            L.mi_transformer_param.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.POINTER(U64)]
+            L.mi_transformer_train_step.argtypes = [P, U64, U64, I32, I32, ctypes.c_float, ctypes.POINTER(U64)]
+            L.mi_transformer_train_synthetic.argtypes = [P, I32, I32, I32, ctypes.c_float, U64, P,
+                                                         ctypes.POINTER(ctypes.c_double)]
+            for f in (L.mi_transformer_create, L.mi_transformer_destroy, L.mi_transformer_param,
+                      L.mi_transformer_train_step, L.mi_transformer_train_synthetic):
+                f.restype = ctypes.c_int
+            L.mi_transformer_last_error.restype = ctypes.c_char_p
+            L._tf_bound = True
+        self.L = L
+        self.cfg = dict(cfg)
+        c = TransformerConfig(vocab=cfg["vocab"], d_model=cfg["d_model"], heads=cfg["heads"], d_ff=cfg["d_ff"],
+                              layers=cfg["layers"], eps=cfg.get("eps", 1e-5))
+        h = ctypes.c_void_p()
+        self._check(L.mi_transformer_create(eng.ctx, ctypes.byref(c), seed, ctypes.byref(h)))
+        self.h = h
+        eng._children.add(self)
+
+    def _check(self, st):
+        if st != 0:
+            raise MiError(st, self.L.mi_transformer_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.mi_transformer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def param(self, name: str, layer: int = -1) -> np.ndarray:
+        which = ("embed", "head_w", "head_b").index(name) if layer < 0 else TRANSFORMER_LAYER_PARAMS.index(name)
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_transformer_param(self.h, layer, which, ctypes.byref(out)))
+        return self.eng.download(out.value)
+
+    def train_step(self, tokens: np.ndarray, targets: np.ndarray, lr: float) -> float:
+        """One step on host tokens / targets [batch, seq]."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        b, s = tokens.shape
+        ti = self.eng.upload_i32(tokens.reshape(-1, 1))
+        yi = self.eng.upload_i32(np.ascontiguousarray(targets, np.int32).reshape(-1, 1))
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_transformer_train_step(self.h, ti, yi, b, s, lr, ctypes.byref(out)))
+        loss = float(self.eng.download(out.value)[0, 0])
+        for i in (ti, yi, out.value):
+            self.eng.free(i)
+        return loss
+
+    def train_synthetic(self, batch: int, seq: int, steps: int, lr: float, data_seed: int = 0):
+        losses = np.zeros(steps, np.float32)
+        ms = ctypes.c_double()
+        self._check(self.L.mi_transformer_train_synthetic(self.h, batch, seq, steps, lr, data_seed,
+                                                          losses.ctypes.data, ctypes.byref(ms)))
         return losses, ms.value

@@ -346,6 +346,60 @@ void or_layer_norm(const float *x, int64_t R, int64_t C, const float *gamma, con
   }
 }
 
+/* LayerNorm's gradient (the chain rule through or_layer_norm's formula;
+ * Burn's autodiff reaches it through the forward's primitive ops,
+ * burn-nn LayerNorm): xh = (x - mean) / den, g = dy * gamma,
+ * dx = (g - mean(g) - xh * mean(g * xh)) / den (+ dres), dgamma = sum_rows(dy
+ * xh), dbeta = sum_rows(dy).  double throughout, rounded once. */
+void or_layer_norm_backward(const float *x, int64_t R, int64_t C, const float *gamma, const float *dy,
+                            const float *dres, float eps, float *dx, float *dgamma, float *dbeta) {
+  double *xh = (double *)malloc((size_t)(C > 0 ? C : 1) * sizeof(double));
+  double *ag = (double *)calloc((size_t)(C > 0 ? C : 1), sizeof(double));
+  double *ab = (double *)calloc((size_t)(C > 0 ? C : 1), sizeof(double));
+  for (int64_t i = 0; i < R; ++i) {
+    const float *xr = x + i * C, *dr = dy + i * C;
+    double s = 0.0;
+    for (int64_t j = 0; j < C; ++j) s += xr[j];
+    const double mean = s / (double)C;
+    double q = 0.0;
+    for (int64_t j = 0; j < C; ++j) q += (xr[j] - mean) * (xr[j] - mean);
+    const double den = sqrt(q / (double)C + (double)eps);
+    double sg = 0.0, sgx = 0.0;
+    for (int64_t j = 0; j < C; ++j) {
+      xh[j] = (xr[j] - mean) / den;
+      const double g = (double)dr[j] * (gamma ? gamma[j] : 1.0);
+      sg += g;
+      sgx += g * xh[j];
+      ag[j] += (double)dr[j] * xh[j];
+      ab[j] += dr[j];
+    }
+    for (int64_t j = 0; j < C; ++j) {
+      const double g = (double)dr[j] * (gamma ? gamma[j] : 1.0);
+      double o = (g - sg / (double)C - xh[j] * sgx / (double)C) / den;
+      if (dres) o += dres[i * C + j];
+      dx[i * C + j] = (float)o;
+    }
+  }
+  for (int64_t j = 0; j < C; ++j) {
+    dgamma[j] = (float)ag[j];
+    dbeta[j] = (float)ab[j];
+  }
+  free(xh);
+  free(ag);
+  free(ab);
+}
+
+/* Softmax's gradient through p = softmax(scale x): ds = scale p (dp -
+ * sum_row(p dp)), double, rounded once. */
+void or_softmax_backward(const float *p, const float *dp, int64_t R, int64_t C, float scale, float *ds) {
+  for (int64_t i = 0; i < R; ++i) {
+    double s = 0.0;
+    for (int64_t j = 0; j < C; ++j) s += (double)p[i * C + j] * dp[i * C + j];
+    for (int64_t j = 0; j < C; ++j)
+      ds[i * C + j] = (float)((double)scale * p[i * C + j] * ((double)dp[i * C + j] - s));
+  }
+}
+
 /* ---------------------------------------------------------------- indexing */
 /* argmax over each row: the first maximum, NaN above every number
  * (generate.rs:176-183; ops.rs:2389-2440). */

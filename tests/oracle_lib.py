@@ -35,6 +35,8 @@ def lib():
         L.or_softmax_rows.argtypes = [P, I64, I64, P, I64, F, I, P]
         L.or_rms_norm.argtypes = [P, I64, I64, P, F, P]
         L.or_layer_norm.argtypes = [P, I64, I64, P, P, F, P]
+        L.or_layer_norm_backward.argtypes = [P, I64, I64, P, P, P, F, P, P, P]
+        L.or_softmax_backward.argtypes = [P, P, I64, I64, F, P]
         L.or_argmax_rows.argtypes = [P, I64, I64, P]
         L.or_select_rows.argtypes = [P, I64, I64, P, I64, P]
         L.or_pick_columns.argtypes = [P, I64, I64, P, P]
@@ -127,6 +129,25 @@ def layer_norm(x, gamma=None, beta=None, eps=1e-5):
     b = f32(beta).ravel() if beta is not None else None
     out = np.empty_like(x)
     lib().or_layer_norm(_p(x), x.shape[0], x.shape[1], _p(g), _p(b), eps, _p(out))
+    return out
+
+
+def layer_norm_backward(x, gamma, dy, dres=None, eps=1e-5):
+    x, dy = _2d(x), _2d(dy)
+    R, C = x.shape
+    g = f32(gamma).ravel() if gamma is not None else None
+    r = _2d(dres) if dres is not None else None
+    dx = np.empty_like(x)
+    dg = np.empty((1, C), np.float32)
+    db = np.empty((1, C), np.float32)
+    lib().or_layer_norm_backward(_p(x), R, C, _p(g), _p(dy), _p(r), eps, _p(dx), _p(dg), _p(db))
+    return dx, dg, db
+
+
+def softmax_backward(p, dp, scale=1.0):
+    p, dp = _2d(p), _2d(dp)
+    out = np.empty_like(p)
+    lib().or_softmax_backward(_p(p), _p(dp), p.shape[0], p.shape[1], scale, _p(out))
     return out
 
 

@@ -287,6 +287,49 @@ def test_layer_norm(engine):
     close(engine.download(engine.layer_norm(*ids, eps=1e-5)), orc.layer_norm(x, g, b, 1e-5), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("rows,cols", [(2048, 256), (37, 1000), (5, 64)])
+@pytest.mark.parametrize("res", [False, True])
+def test_layer_norm_backward(engine, rows, cols, res):
+    x = rnd(rows, cols, scale=2.0) + np.float32(0.3)
+    g, dy = rnd(1, cols) + np.float32(1.0), rnd(rows, cols)
+    dres = rnd(rows, cols) if res else None
+    ids = engine.layer_norm_backward(engine.upload(x), engine.upload(g), engine.upload(dy),
+                                     engine.upload(dres) if res else 0, 1e-5)
+    dx, dg, db = (engine.download(i) for i in ids)
+    wx, wg, wb = orc.layer_norm_backward(x, g, dy, dres, 1e-5)
+    # Cancellation inside dx and sums over all rows for dgamma / dbeta: bound
+    # the error by the magnitudes of the terms.
+    den = np.sqrt(x.astype(np.float64).var(1, keepdims=True) + 1e-5)
+    close(dx, wx, rtol=1e-5, atol=2e-6 * np.abs(dy * g / den).max())
+    xh = (x - x.astype(np.float64).mean(1, keepdims=True)) / den
+    close(dg, wg, rtol=1e-5, atol=2e-7 * np.abs(dy * xh).sum(0).max())
+    close(db, wb, rtol=1e-5, atol=2e-7 * np.abs(dy).sum(0).max())
+
+
+def test_softmax_backward(engine):
+    x, dp = rnd(512, 128, scale=2.0), rnd(512, 128)
+    p = orc.softmax_rows(x, scale=0.125)
+    got = engine.download(engine.softmax_backward(engine.upload(p), engine.upload(dp), 0.125))
+    want = orc.softmax_backward(p, dp, 0.125)
+    close(got, want, rtol=1e-5, atol=1e-6 * 0.125 * np.abs(p * dp).sum(1, keepdims=True).max())
+
+
+def test_sgd_update_in_place_bits(engine):
+    sizes = [(256, 256), (1, 256), (1, 7), (33, 5), (1024, 1024)] * 11  # 55 parameters: two launches
+    ps = [rnd(*s) for s in sizes]
+    gs = [rnd(*s) for s in sizes]
+    pid = [engine.upload(p) for p in ps]
+    gid = [engine.upload(g.reshape(-1, 1) if i % 3 == 0 else g) for i, g in enumerate(gs)]  # any folding
+    lr = np.float32(0.05)
+    engine.sgd_update(pid, gid, float(lr))
+    for i, (p, g) in enumerate(zip(ps, gs)):
+        same_bits(engine.download(pid[i]), (p - g * lr).astype(np.float32))
+    with pytest.raises(miburn.MiError):
+        engine.sgd_update([pid[0]], [pid[0]], 0.1)
+    with pytest.raises(miburn.MiError):
+        engine.sgd_update([pid[0]], [gid[1]], 0.1)  # 65536 parameters, 256 gradients
+
+
 # ------------------------------------------------------------------ products
 def mm_tol(a, b, ta, tb, rel):
     aa = np.abs(a.T if ta else a).astype(np.float64)

@@ -263,3 +263,56 @@ def test_copy_strided_transpose_keeps_negative_zero():
     x = np.array([[-0.0, 2.5], [3.0, 4.0]], np.float32)
     got = orc.copy_strided4(x, (1, 1, 2, 2), 0, (0, 0, 1, 2)).view(np.float32).reshape(4)
     assert_bits(got, np.array([-0.0, 3.0, 2.5, 4.0], np.float32))
+
+
+# ----------------------------------------------------------- backward rows
+# The fused backward restatements are pinned by central differences of the
+# oracle's own forward functions (a derivative fixed by the forward, not a
+# retyped formula): a dropped mean term, a wrong sign or a missing 1/den fails.
+def _fd(f, x, h=1e-2):
+    g = np.zeros(x.size)
+    for i in range(x.size):
+        xp, xm = x.copy(), x.copy()
+        xp.flat[i] += h
+        xm.flat[i] -= h
+        g[i] = (f(xp) - f(xm)) / (2 * h)
+    return g.reshape(x.shape)
+
+
+def test_layer_norm_backward_matches_finite_differences():
+    rng = np.random.default_rng(41)
+    R, C = 3, 7
+    x = (rng.standard_normal((R, C)) * 2 + 0.5).astype(np.float32)
+    gam = (rng.standard_normal((1, C)) + 1).astype(np.float32)
+    bet = rng.standard_normal((1, C)).astype(np.float32)
+    dy = rng.standard_normal((R, C)).astype(np.float32)
+    dres = rng.standard_normal((R, C)).astype(np.float32)
+
+    def loss(xv, g=gam, b=bet):
+        return float(np.sum(dy.astype(np.float64) * orc.layer_norm(xv.astype(np.float32), g, b)))
+
+    dx, dg, db = orc.layer_norm_backward(x, gam, dy, dres)
+    fx = _fd(lambda v: loss(v), x.astype(np.float64))
+    fg = _fd(lambda v: loss(x, g=v.astype(np.float32)), gam.astype(np.float64))
+    fb = _fd(lambda v: loss(x, b=v.astype(np.float32)), bet.astype(np.float64))
+    assert np.allclose(dx - dres, fx, atol=2e-3, rtol=2e-3)
+    assert np.allclose(dg, fg, atol=2e-3, rtol=2e-3)
+    assert np.allclose(db, fb, atol=2e-3, rtol=2e-3)
+    # Without gamma: the unit gain.
+    dx1, _, _ = orc.layer_norm_backward(x, None, dy)
+    dx2, _, _ = orc.layer_norm_backward(x, np.ones((1, C), np.float32), dy)
+    assert np.array_equal(dx1, dx2)
+
+
+def test_softmax_backward_matches_finite_differences():
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((4, 9)).astype(np.float32)
+    dp = rng.standard_normal((4, 9)).astype(np.float32)
+    scale = 0.37
+    p = orc.softmax_rows(x, scale=scale)
+    ds = orc.softmax_backward(p, dp, scale)
+    f = _fd(lambda v: float(np.sum(dp.astype(np.float64) * orc.softmax_rows(v.astype(np.float32), scale=scale))),
+            x.astype(np.float64))
+    assert np.allclose(ds, f, atol=1e-3, rtol=1e-3)
+    # Rows of the gradient sum to zero (softmax is shift-invariant).
+    assert np.abs(ds.astype(np.float64).sum(1)).max() < 1e-6
