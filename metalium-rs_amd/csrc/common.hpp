@@ -44,6 +44,54 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Streaming (non-temporal) 16-byte accesses: the line is not kept in the
+// caches.  On an MI355X a stream of them moves ~80% of the 8 TB/s peak
+// against ~70% for ordinary accesses; they suit operands far larger than the
+// caches that no later kernel re-reads soon.  NT = false gives the ordinary
+// access, so one kernel body serves both.
+typedef float mi_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mi_u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+__device__ __forceinline__ float4 ld4(const float *p) {
+  if constexpr (NT) {
+    const mi_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const mi_f32x4 *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const float4 *>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void st4(float *p, float4 v) {
+  if constexpr (NT) {
+    const mi_f32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<mi_f32x4 *>(p));
+  } else {
+    *reinterpret_cast<float4 *>(p) = v;
+  }
+}
+template <bool NT>
+__device__ __forceinline__ uint4 ldu4(const void *p) {
+  if constexpr (NT) {
+    const mi_u32x4 v = __builtin_nontemporal_load(static_cast<const mi_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *static_cast<const uint4 *>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void stu4(void *p, uint4 v) {
+  if constexpr (NT) {
+    const mi_u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, static_cast<mi_u32x4 *>(p));
+  } else {
+    *static_cast<uint4 *>(p) = v;
+  }
+}
+// Host side: stream an operation's accesses when it moves at least this many
+// bytes -- beyond what the 256 MB last-level cache would keep for the next
+// kernel to re-read.
+constexpr int64_t kStreamBytes = int64_t(128) << 20;
+
 // ------------------------------------------------------------------ buffers
 struct Buffer {
   void *ptr = nullptr;

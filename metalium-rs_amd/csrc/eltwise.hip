@@ -139,10 +139,11 @@ __device__ __forceinline__ void store_elem(void *out, int out_elem, int64_t idx,
 
 // Fast form: F32 operands, the output width a multiple of 4, four lanes of
 // one row per thread per step.
+template <bool NT>
 __device__ __forceinline__ float4 load4(const Opnd &o, int64_t flat, int64_t cols) {
   const float *p = static_cast<const float *>(o.p);
   switch (o.mode) {
-    case 0: return *reinterpret_cast<const float4 *>(p + flat);
+    case 0: return ld4<NT>(p + flat);
     case 1: return *reinterpret_cast<const float4 *>(p + (flat % cols));
     case 2: { float v = p[flat / cols]; return make_float4(v, v, v, v); }
     default: { float v = p[0]; return make_float4(v, v, v, v); }
@@ -154,9 +155,10 @@ __device__ __forceinline__ float4 load4(const Opnd &o, int64_t flat, int64_t col
 // in flight.
 constexpr int EW_UNROLL = 4;
 
+template <bool NT>
 __device__ __forceinline__ void store4(void *out, int out_elem, int64_t flat, float4 r) {
   if (out_elem == MI_F32) {
-    *reinterpret_cast<float4 *>(static_cast<float *>(out) + flat) = r;
+    st4<NT>(static_cast<float *>(out) + flat, r);
   } else if (out_elem == MI_BF16) {
     uint2 h;
     h.x = uint32_t(f32_to_bf16_bits(r.x)) | (uint32_t(f32_to_bf16_bits(r.y)) << 16);
@@ -164,11 +166,11 @@ __device__ __forceinline__ void store4(void *out, int out_elem, int64_t flat, fl
     *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = h;
   } else {
     uint4 m = make_uint4(r.x != 0.f, r.y != 0.f, r.z != 0.f, r.w != 0.f);
-    *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(out) + flat) = m;
+    stu4<NT>(static_cast<uint32_t *>(out) + flat, m);
   }
 }
 
-template <uint32_t K, int NIN>
+template <uint32_t K, int NIN, bool NT>
 __global__ void __launch_bounds__(256) ew_vec4(Opnd a, Opnd b, Opnd c, float s1, float s2,
                                                void *out, int out_elem, int64_t n4, int64_t cols) {
   const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * EW_UNROLL) + threadIdx.x;
@@ -179,9 +181,9 @@ __global__ void __launch_bounds__(256) ew_vec4(Opnd a, Opnd b, Opnd c, float s1,
     for (int u = 0; u < EW_UNROLL; ++u) {
       const int64_t v = v0 + u * 256;
       if (v < n4) {
-        x[u] = load4(a, v * 4, cols);
-        if constexpr (NIN >= 2) y[u] = load4(b, v * 4, cols);
-        if constexpr (NIN >= 3) z[u] = load4(c, v * 4, cols);
+        x[u] = load4<NT>(a, v * 4, cols);
+        if constexpr (NIN >= 2) y[u] = load4<NT>(b, v * 4, cols);
+        if constexpr (NIN >= 3) z[u] = load4<NT>(c, v * 4, cols);
       }
     }
 #pragma unroll
@@ -196,7 +198,7 @@ __global__ void __launch_bounds__(256) ew_vec4(Opnd a, Opnd b, Opnd c, float s1,
         r.y = op<K>(x[u].y, yy.y, zz.y, s1, s2);
         r.z = op<K>(x[u].z, yy.z, zz.z, s1, s2);
         r.w = op<K>(x[u].w, yy.w, zz.w, s1, s2);
-        store4(out, out_elem, v * 4, r);
+        store4<NT>(out, out_elem, v * 4, r);
       }
     }
   }
@@ -270,9 +272,18 @@ static void launch_kind(bool fast, int nin, const Opnd &a, const Opnd &b, const 
   if (fast) {
     const int64_t n4 = n / 4;
     unsigned g = grid_for(n4, threads * EW_UNROLL, 256 * 64);
-    if (nin == 1) ew_vec4<K, 1><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
-    else if (nin == 2) ew_vec4<K, 2><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
-    else ew_vec4<K, 3><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+    // Stream the accesses when the operation moves more than the last-level
+    // cache holds (inputs and output counted at 4 bytes an element).
+    const bool nt = n * 4 * (nin + 1) >= kStreamBytes;
+    if (nt) {
+      if (nin == 1) ew_vec4<K, 1, true><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+      else if (nin == 2) ew_vec4<K, 2, true><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+      else ew_vec4<K, 3, true><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+    } else {
+      if (nin == 1) ew_vec4<K, 1, false><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+      else if (nin == 2) ew_vec4<K, 2, false><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+      else ew_vec4<K, 3, false><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n4, cols);
+    }
   } else {
     unsigned g = grid_for(n, threads * 4, 256 * 32);
     if (nin == 1) ew_generic<K, 1><<<g, threads, 0, st>>>(a, b, c, s1, s2, out, out_elem, n, cols);

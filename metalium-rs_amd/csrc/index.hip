@@ -22,7 +22,7 @@ namespace mi {
 // ---------------------------------------------------------- select_rows
 // A block of 256 threads copies rows: each wave one output row per step,
 // 16-byte lanes when the row width allows.
-template <typename V>
+template <typename V, bool NT>
 __global__ void __launch_bounds__(256) select_rows_kernel(const V *table, int64_t vrows, int64_t vcols,
                                                           const int32_t *idx, int64_t n, V *out,
                                                           uint32_t *flags) {
@@ -38,7 +38,20 @@ __global__ void __launch_bounds__(256) select_rows_kernel(const V *table, int64_
       continue;
     }
     const V *src = table + static_cast<int64_t>(r) * vcols;
-    for (int64_t j = lane; j < vcols; j += 64) dst[j] = src[j];
+    // Up to four loads per lane in flight before the stores.
+    for (int64_t j0 = lane; j0 < vcols; j0 += 256) {
+      V v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (j0 + 64 * u < vcols) v[u] = src[j0 + 64 * u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (j0 + 64 * u < vcols) {
+          if constexpr (NT && sizeof(V) == 16) stu4<true>(dst + j0 + 64 * u, v[u]);
+          else dst[j0 + 64 * u] = v[u];
+        }
+      }
+    }
   }
 }
 
@@ -173,15 +186,23 @@ extern "C" int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out) {
   if (n > 0 && D > 0) {
     const size_t row_bytes = static_cast<size_t>(D) * elem_size(te);
     const unsigned g = grid_for(n, 4, 256 * 64);
-    if (row_bytes % 16 == 0)
-      select_rows_kernel<uint4><<<g, 256, 0, ctx->stream>>>(static_cast<const uint4 *>(tp), V, row_bytes / 16, ip, n,
-                                                            static_cast<uint4 *>(ob->ptr), flags(ctx));
+    // The gathered rows are streamed out when the result outgrows the
+    // last-level cache; the table is read through the caches (ids repeat).
+    const bool nt = n * row_bytes >= kStreamBytes;
+    if (row_bytes % 16 == 0 && nt)
+      select_rows_kernel<uint4, true><<<g, 256, 0, ctx->stream>>>(static_cast<const uint4 *>(tp), V, row_bytes / 16, ip,
+                                                                  n, static_cast<uint4 *>(ob->ptr), flags(ctx));
+    else if (row_bytes % 16 == 0)
+      select_rows_kernel<uint4, false><<<g, 256, 0, ctx->stream>>>(static_cast<const uint4 *>(tp), V, row_bytes / 16, ip,
+                                                                   n, static_cast<uint4 *>(ob->ptr), flags(ctx));
     else if (row_bytes % 4 == 0)
-      select_rows_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(tp), V, row_bytes / 4, ip, n,
-                                                               static_cast<uint32_t *>(ob->ptr), flags(ctx));
+      select_rows_kernel<uint32_t, false><<<g, 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(tp), V,
+                                                                      row_bytes / 4, ip, n,
+                                                                      static_cast<uint32_t *>(ob->ptr), flags(ctx));
     else
-      select_rows_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(tp), V, row_bytes / 2, ip, n,
-                                                               static_cast<uint16_t *>(ob->ptr), flags(ctx));
+      select_rows_kernel<uint16_t, false><<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(tp), V,
+                                                                      row_bytes / 2, ip, n,
+                                                                      static_cast<uint16_t *>(ob->ptr), flags(ctx));
     s = check_launch(ctx, "select_rows");
     if (s) { mi_free(ctx, id); return s; }
   }

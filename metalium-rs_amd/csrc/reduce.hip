@@ -35,6 +35,7 @@ __device__ __forceinline__ void st(void *p, int elem, int64_t i, float v) {
 
 // ------------------------------------------------ reduce over columns (dim 1)
 // One wavefront per row; four rows per 256-thread block.
+template <bool NT>
 __global__ void __launch_bounds__(256) reduce_cols_kernel(const void *x, int elem, float *out, int64_t rows,
                                                           int64_t cols, int op) {
   const int lane = threadIdx.x & 63;
@@ -43,14 +44,22 @@ __global__ void __launch_bounds__(256) reduce_cols_kernel(const void *x, int ele
   const int64_t base = row * cols;
   float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
   if (elem == MI_F32 && (cols % 4) == 0) {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + base);
+    const float *p = static_cast<const float *>(x) + base;
     const int64_t n4 = cols / 4;
-    for (int64_t j = lane; j < n4; j += 64) {
-      float4 v = p[j];
-      if (op == MI_R_MAX) acc = max_nan(max_nan(max_nan(max_nan(acc, v.x), v.y), v.z), v.w);
-      else if (op == MI_R_MIN) acc = min_nan(min_nan(min_nan(min_nan(acc, v.x), v.y), v.z), v.w);
-      else acc += (v.x + v.y) + (v.z + v.w);
+    auto fold = [op](float a, float4 v) {
+      if (op == MI_R_MAX) return max_nan(max_nan(max_nan(max_nan(a, v.x), v.y), v.z), v.w);
+      if (op == MI_R_MIN) return min_nan(min_nan(min_nan(min_nan(a, v.x), v.y), v.z), v.w);
+      return a + ((v.x + v.y) + (v.z + v.w));
+    };
+    int64_t j = lane;
+    // Four float4 per lane in flight, streamed when the input is large.
+    for (; j + 192 < n4; j += 256) {
+      float4 v0, v1, v2, v3;
+      if (NT) { v0 = ld4<true>(p + 4 * j); v1 = ld4<true>(p + 4 * (j + 64)); v2 = ld4<true>(p + 4 * (j + 128)); v3 = ld4<true>(p + 4 * (j + 192)); }
+      else { v0 = ld4<false>(p + 4 * j); v1 = ld4<false>(p + 4 * (j + 64)); v2 = ld4<false>(p + 4 * (j + 128)); v3 = ld4<false>(p + 4 * (j + 192)); }
+      acc = fold(fold(fold(fold(acc, v0), v1), v2), v3);
     }
+    for (; j < n4; j += 64) acc = fold(acc, ld4<false>(p + 4 * j));
   } else {
     for (int64_t j = lane; j < cols; j += 64) {
       float v = ld(x, elem, base + j);
@@ -123,6 +132,38 @@ __global__ void __launch_bounds__(256) reduce_rows_part(const void *x, int elem,
       if (c < cols) dst[c] = s.x;
     }
   }
+}
+
+// Wide rows (F32, at least 1024 columns, a multiple of 4): a block's 256
+// threads cover 1024 contiguous columns as float4, so each row step reads 4 KB
+// in one run; thread t folds its four columns over the block's row range in
+// row order, eight rows' loads in flight at a time (streamed when large).
+template <bool NT>
+__global__ void __launch_bounds__(256) reduce_rows_wide(const float *x, float *part, int64_t rows, int64_t cols,
+                                                        int64_t rows_per_split, int op) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 1024 + threadIdx.x * 4;
+  const int64_t split = blockIdx.y;
+  const int64_t r_begin = split * rows_per_split;
+  const int64_t r_end = r_begin + rows_per_split < rows ? r_begin + rows_per_split : rows;
+  if (c >= cols) return;
+  const float init = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  float4 acc = make_float4(init, init, init, init);
+  auto fold = [op](float4 &a, float4 v) {
+    if (op == MI_R_MAX) { a.x = max_nan(a.x, v.x); a.y = max_nan(a.y, v.y); a.z = max_nan(a.z, v.z); a.w = max_nan(a.w, v.w); }
+    else if (op == MI_R_MIN) { a.x = min_nan(a.x, v.x); a.y = min_nan(a.y, v.y); a.z = min_nan(a.z, v.z); a.w = min_nan(a.w, v.w); }
+    else { a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w; }
+  };
+  const float *p = x + c;
+  int64_t r = r_begin;
+  for (; r + 8 <= r_end; r += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = ld4<NT>(p + (r + u) * cols);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) fold(acc, v[u]);
+  }
+  for (; r < r_end; ++r) fold(acc, ld4<NT>(p + r * cols));
+  *reinterpret_cast<float4 *>(part + split * cols + c) = acc;
 }
 
 // Fold the partial rows [nb, n] of a split reduction into [1, n].  A block of
@@ -268,7 +309,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return s;
 }
 
-template <int VPT, bool VEC>
+template <int VPT, bool VEC, bool NT>
 __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
                                                             int64_t mask_rows, float scale, int log_mode, void *out,
                                                             int out_elem, int64_t cols) {
@@ -287,7 +328,8 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
       const int64_t j4 = tid + 256 * u;
-      float4 q = (j4 * 4 < cols) ? p[j4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      float4 q = (j4 * 4 < cols) ? ld4<NT>(reinterpret_cast<const float *>(p + j4))
+                                 : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
       v[4 * u] = q.x; v[4 * u + 1] = q.y; v[4 * u + 2] = q.z; v[4 * u + 3] = q.w;
     }
   } else {
@@ -332,7 +374,7 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
         r.y = log_mode ? v[4 * u + 1] - ls : v[4 * u + 1] / s;
         r.z = log_mode ? v[4 * u + 2] - ls : v[4 * u + 2] / s;
         r.w = log_mode ? v[4 * u + 3] - ls : v[4 * u + 3] / s;
-        o[j4] = r;
+        st4<NT>(reinterpret_cast<float *>(o + j4), r);
       }
     }
   } else {
@@ -471,16 +513,24 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
   if (axis == MI_AXIS_COLS) {
     if (R > 0) {
       if (C == 0) (void)hipMemsetAsync(o, 0, R * sizeof(float), ctx->stream);
-      else reduce_cols_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, o, R, C, op);
+      else if (R * C * 4 >= kStreamBytes)
+        reduce_cols_kernel<true><<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, o, R, C, op);
+      else
+        reduce_cols_kernel<false><<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, o, R, C, op);
     }
   } else if (C > 0) {
     if (R == 0) {
       (void)hipMemsetAsync(o, 0, C * sizeof(float), ctx->stream);
     } else {
       const bool vec = (xe == MI_F32) && (C % 4 == 0);
-      const int64_t cw = vec ? 256 : 64;
+      const bool wide = vec && C >= 1024;
+      const int64_t cw = wide ? 1024 : (vec ? 256 : 64);
       const int64_t tiles = (C + cw - 1) / cw;
-      int64_t splits = (2048 + tiles - 1) / tiles;
+      // About 2048 blocks (512 for the wide kernel, whose blocks read 4 KB a
+      // row step and fold 8 rows at a time: fewer, longer row ranges keep
+      // the partials -- written and re-read by the fold -- small).
+      const int64_t target = wide ? 512 : 2048;
+      int64_t splits = (target + tiles - 1) / tiles;
       int64_t max_splits = (R + 15) / 16;
       if (splits > max_splits) splits = max_splits;
       if (splits < 1) splits = 1;
@@ -489,7 +539,10 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
       float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(splits * C) * sizeof(float)));
       if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "reduce scratch"); }
       dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
-      if (vec) reduce_rows_part<true><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
+      const float *xf = static_cast<const float *>(xp);
+      if (wide && R * C * 4 >= kStreamBytes) reduce_rows_wide<true><<<grid, 256, 0, ctx->stream>>>(xf, part, R, C, rps, op);
+      else if (wide) reduce_rows_wide<false><<<grid, 256, 0, ctx->stream>>>(xf, part, R, C, rps, op);
+      else if (vec) reduce_rows_part<true><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
       else reduce_rows_part<false><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
       fold_partials_kernel<<<static_cast<unsigned>((C + 63) / 64), 1024, 0, ctx->stream>>>(
           part, splits, C, op, static_cast<float>(R), o, C, nullptr);
@@ -564,9 +617,12 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
       int vpt = 1;
       while (1024 * vpt < C) vpt *= 2;
       const unsigned rows = static_cast<unsigned>(R);
+      // Stream rows the size of the last-level cache and beyond.
+      const bool nt = vec && R * C * 8 >= kStreamBytes;
       switch (vpt) {
-#define MI_SB(V) case V: if (vec) softmax_block_kernel<V, true><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
-                         else softmax_block_kernel<V, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); break;
+#define MI_SB(V) case V: if (nt) softmax_block_kernel<V, true, true><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+                         else if (vec) softmax_block_kernel<V, true, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+                         else softmax_block_kernel<V, false, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); break;
         MI_SB(1) MI_SB(2) MI_SB(4) MI_SB(8) MI_SB(16)
 #undef MI_SB
       }
