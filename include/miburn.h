@@ -283,6 +283,26 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
                       int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, int64_t pos0, float scale,
                       mi_id *out);
+/* ---- fused decode projections: the fused q|k|v and gate|up matrices of
+ * crates/tt-models/src/llama.rs:655-672 (`Llama::fused`) composed with the
+ * ops around them in a decode step -- Engine::rms_norm_as (server.rs:449),
+ * rope_blocks (server.rs:566), the KV-cache slice_assign (llama.rs:415-435),
+ * the residual add and silu_mul (crates/burn-tt/src/ops.rs:2622-2651).  x is
+ * [M, K] F32 with 1 <= M <= 8 (one row per sequence), K a multiple of 8; w is
+ * BF16 [N, K] (each output row's weights k-contiguous, as the projections are
+ * stored); gamma a [1, K] F32 RMSNorm gain or 0 for no norm. ---- */
+/* out = residual + rmsnorm(x) w^T ([M, N]; residual [M, N] or 0), or with
+ * silu_mul != 0 and w = [gate; up] ([2 I, K]): out = silu(g) * u, [M, I]. */
+int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w,
+                   mi_id residual, int silu_mul, mi_id *out);
+/* w_qkv = [wq; wk; wv] ([(heads + 2 kv_heads) * d, K]): q = rope(rmsnorm(x)
+ * wq^T) returned [M, heads * d]; k = rope(.. wk^T) and v = .. wv^T written
+ * into the caches ([M * kv_heads * max_ctx, d] F32, item (row, kv head)) at
+ * position `pos`; the rotary tables as mi_rope's, read at row `pos`. */
+int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
+                     mi_id w_qkv, mi_id cos_table, mi_id sin_table,
+                     int64_t heads, int64_t kv_heads, int64_t pos,
+                     mi_id k_cache, mi_id v_cache, mi_id *q_out);
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);

@@ -32,11 +32,13 @@ typedef struct mi_llama mi_llama;
 int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed,
                     float init_std, mi_llama **out);
 int mi_llama_destroy(mi_llama *m);
-/* The id of a weight (for checks): which = 0 embedding table [vocab, hidden]
- * (layer ignored), 1 final norm; per layer 2 attention norm, 3 q [q_dim,
- * hidden], 4 k [kv_dim, hidden], 5 v, 6 o [hidden, q_dim], 7 mlp norm,
- * 8 gate [inter, hidden], 9 up, 10 down [hidden, inter].  Projection
- * weights are stored [out, in] (the product reads them transposed). */
+/* A copy of a weight (for checks), a new id the caller frees: which = 0
+ * embedding table [vocab, hidden] (layer ignored), 1 final norm; per layer
+ * 2 attention norm, 3 q [q_dim, hidden], 4 k [kv_dim, hidden], 5 v, 6 o
+ * [hidden, q_dim], 7 mlp norm, 8 gate [inter, hidden], 9 up, 10 down
+ * [hidden, inter].  Projection weights are stored [out, in] (the product
+ * reads them transposed); q|k|v and gate|up are row blocks of one fused
+ * matrix each. */
 int mi_llama_param(mi_llama *m, int layer, int which, mi_id *out);
 /* Empty the KV cache. */
 int mi_llama_reset(mi_llama *m);

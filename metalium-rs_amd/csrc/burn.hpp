@@ -326,4 +326,25 @@ inline Tensor attention_rows(const Tensor &q, const Tensor &k_cache, const Tenso
   return Tensor(q.ctx(), id, {q.rows(), q.cols()});
 }
 
+// Fused decode projections (one row per sequence, at most 8 rows).
+inline Tensor norm_matvec(const Tensor &x, const Tensor *gamma, float eps, const Tensor &w, const Tensor *residual,
+                          bool silu_mul) {
+  mi_id id;
+  check(x.ctx(), mi_norm_matvec(x.ctx(), x.use(), gamma ? gamma->use() : 0, eps, w.use(),
+                                residual ? residual->use() : 0, silu_mul, &id),
+        "norm_matvec");
+  const int64_t n = silu_mul ? w.rows() / 2 : w.rows();
+  return Tensor(x.ctx(), id, {x.rows(), n});
+}
+
+inline Tensor norm_qkv_rope(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv, const Tensor &cos,
+                            const Tensor &sin, int64_t heads, int64_t kv_heads, int64_t pos, const Tensor &k_cache,
+                            const Tensor &v_cache) {
+  mi_id id;
+  check(x.ctx(), mi_norm_qkv_rope(x.ctx(), x.use(), gamma.use(), eps, w_qkv.use(), cos.use(), sin.use(), heads,
+                                  kv_heads, pos, k_cache.use(), v_cache.use(), &id),
+        "norm_qkv_rope");
+  return Tensor(x.ctx(), id, {x.rows(), heads * k_cache.cols()});
+}
+
 }  // namespace burn

@@ -1,0 +1,336 @@
+// Fused decode projections: a few activation rows (one per sequence) times a
+// BF16 weight, with the neighbouring element-wise work folded in so that a
+// decoder layer's step is six launches instead of eighteen.
+//
+// Reference: the fused projections of crates/tt-models/src/llama.rs:655-672
+// (`Llama::fused`: each layer's q|k|v and gate|up weights one matrix each,
+// every output column keeping its own accumulation) composed with the ops the
+// decode step runs around them -- Engine::rms_norm_as (crates/burn-tt/src/
+// server.rs:449; ops/norm.rs:39-283), Engine::rope_blocks (server.rs:566;
+// ops/rope.rs:27-240), the KV-cache `slice_assign` (llama.rs:415-435), the
+// residual add, and silu(gate) * up (ops.rs:2622-2651).
+//
+// MI355X design.  Decode reads every weight once per step: the kernels are
+// HBM-latency-bound GEMVs.  A wavefront owns two output rows of the weight
+// and all M (<= 8) activation rows; each lane streams 16 bytes (8 BF16) of
+// both weight rows per step, so a 576-wide row is read by the wavefront in two
+// coalesced passes.  The activation rows (a few KB) are re-read from cache by
+// every wavefront; when a gain is given each wavefront first folds its rows'
+// sum of squares and normalises on the fly (x / rms * gamma, the norm
+// kernel's formula), so the normalised rows never touch HBM.  The two rows a
+// wavefront owns are chosen so that the epilogue is local: a RoPE pair
+// (i, i + d/2) of one head, or a gate row and its up row.
+#include "common.hpp"
+#include "wave.hpp"
+
+namespace mi {
+
+enum DecodeMode { DM_PLAIN = 0, DM_SILU_MUL = 1, DM_QKV = 2 };
+constexpr int DECODE_MAX_M = 8;
+
+struct DecodeArgs {
+  const float *x;  // [M, K] F32, rows ldx apart
+  int64_t ldx, K;
+  const float *gamma;  // [1, K] RMSNorm gain, or null for no norm
+  float eps;
+  const uint16_t *w;  // [N, K] BF16, k-contiguous
+  int64_t N, npairs;
+  // DM_PLAIN: pair p = rows (2p, 2p + 1), out [M, N] (+ resid [M, N]).
+  // DM_SILU_MUL: pair p = rows (p, p + inter), out [M, inter].
+  const float *resid;
+  float *out;
+  int64_t ldo, inter;
+  // DM_QKV: pair p = rows (h d + i, h d + i + d / 2) of head h = p / (d / 2)
+  // over heads q 0..H-1, k H..H+KVH-1, v H+KVH..H+2KVH-1; q to `out`, k and v
+  // into the caches at position pos of item (row m, kv head).
+  int d, H, KVH;
+  int64_t pos, maxc;
+  const float *cos, *sin;
+  float *kc, *vc;
+};
+
+__device__ __forceinline__ void bf16x8(uint4 q, float (&w)[8]) {
+  const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w[2 * e] = __uint_as_float(u[e] << 16);
+    w[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ float silu2(float a) {
+  // a * sigmoid(a), the sigmoid in the two-branch form of the element-wise op.
+  const float s = a >= 0.0f ? 1.0f / (1.0f + expf(-a)) : expf(a) / (1.0f + expf(a));
+  return a * s;
+}
+
+template <int M, int MODE>
+__global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  if (p >= g.npairs) return;  // whole wavefronts
+  int64_t r0, r1;
+  int64_t head = 0, hi = 0;
+  if constexpr (MODE == DM_PLAIN) {
+    r0 = 2 * p;
+    r1 = 2 * p + 1;
+  } else if constexpr (MODE == DM_SILU_MUL) {
+    r0 = p;
+    r1 = p + g.inter;
+  } else {
+    const int half = g.d / 2;
+    head = p / half;
+    hi = p % half;
+    r0 = head * g.d + hi;
+    r1 = r0 + half;
+  }
+  const bool has1 = r1 < g.N;
+
+  // RMSNorm of the activation rows: sqrt(mean(x x) + eps).
+  float rms[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) rms[m] = 1.0f;
+  if (g.gamma) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float ss = 0.0f;
+      for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
+        const float4 a0 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
+        const float4 a1 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k + 4);
+        ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w;
+        ss += a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+      }
+      ss = wave_sum(ss);
+      rms[m] = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
+    }
+  }
+
+  float acc[M][2];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
+  for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
+    float w0[8], w1[8];
+    bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
+    if (has1) bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k), w1);
+    else
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w1[e] = 0.0f;
+    float gm[8];
+    if (g.gamma) {
+      const float4 g0 = *reinterpret_cast<const float4 *>(g.gamma + k);
+      const float4 g1 = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
+      gm[0] = g0.x; gm[1] = g0.y; gm[2] = g0.z; gm[3] = g0.w;
+      gm[4] = g1.x; gm[5] = g1.y; gm[6] = g1.z; gm[7] = g1.w;
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float4 a0 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
+      const float4 a1 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k + 4);
+      float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      if (g.gamma)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[e] = (av[e] / rms[m]) * gm[e];
+      float t0 = acc[m][0], t1 = acc[m][1];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        t0 += av[e] * w0[e];
+        t1 += av[e] * w1[e];
+      }
+      acc[m][0] = t0;
+      acc[m][1] = t1;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    acc[m][0] = wave_sum(acc[m][0]);
+    acc[m][1] = wave_sum(acc[m][1]);
+  }
+  // Lane m writes activation row m's outputs.
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if (lane != m) continue;
+    const float y0 = acc[m][0], y1 = acc[m][1];
+    if constexpr (MODE == DM_PLAIN) {
+      float *o = g.out + m * g.ldo;
+      o[r0] = g.resid ? __fadd_rn(g.resid[m * g.ldo + r0], y0) : y0;
+      if (has1) o[r1] = g.resid ? __fadd_rn(g.resid[m * g.ldo + r1], y1) : y1;
+    } else if constexpr (MODE == DM_SILU_MUL) {
+      g.out[m * g.ldo + r0] = silu2(y0) * y1;
+    } else {
+      const int64_t half = g.d / 2;
+      if (head < g.H + g.KVH) {
+        const float *cs = g.cos + g.pos * g.d, *sn = g.sin + g.pos * g.d;
+        const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
+        const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
+        if (head < g.H) {
+          float *o = g.out + m * g.ldo + head * g.d;
+          o[hi] = o0;
+          o[hi + half] = o1;
+        } else {
+          float *o = g.kc + ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d;
+          o[hi] = o0;
+          o[hi + half] = o1;
+        }
+      } else {
+        float *o = g.vc + ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d;
+        o[hi] = y0;
+        o[hi + half] = y1;
+      }
+    }
+  }
+}
+
+template <int MODE>
+static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
+  switch (M) {
+#define MI_DEC(m) case m: decode_matvec_kernel<m, MODE><<<grid, 256, 0, st>>>(g); break;
+    MI_DEC(1) MI_DEC(2) MI_DEC(3) MI_DEC(4) MI_DEC(5) MI_DEC(6) MI_DEC(7) MI_DEC(8)
+#undef MI_DEC
+  }
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Shared checks: x [M <= 8, K] F32, w [N, K] BF16, K % 8 == 0, gamma [1, K].
+static int check_common(mi_ctx *ctx, const Buffer *xb, const Buffer *wb, const Buffer *gb, const char *what) {
+  if (xb->elem != MI_F32) return fail(ctx, MI_E_ARG, "%s: activations are %s, not F32", what, elem_name(xb->elem));
+  if (wb->elem != MI_BF16) return fail(ctx, MI_E_ARG, "%s: weight is %s, not BF16", what, elem_name(wb->elem));
+  if (xb->rows < 1 || xb->rows > DECODE_MAX_M)
+    return fail(ctx, MI_E_UNSUPPORTED, "%s: %lld activation rows (1 to %d)", what, (long long)xb->rows, DECODE_MAX_M);
+  if (wb->cols != xb->cols) return fail(ctx, MI_E_ARG, "%s: weight is [%lld, %lld], activations [%lld, %lld]", what,
+                                        (long long)wb->rows, (long long)wb->cols, (long long)xb->rows, (long long)xb->cols);
+  if (xb->cols % 8) return fail(ctx, MI_E_UNSUPPORTED, "%s: width %lld is not a multiple of 8", what, (long long)xb->cols);
+  if (gb && (gb->elem != MI_F32 || gb->rows * gb->cols != xb->cols))
+    return fail(ctx, MI_E_ARG, "%s: gain must be [1, %lld] F32", what, (long long)xb->cols);
+  if (!aligned16(xb->ptr) || !aligned16(wb->ptr) || (gb && !aligned16(gb->ptr)))
+    return fail(ctx, MI_E_ARG, "%s: buffers must be 16-byte aligned", what);
+  return MI_OK;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w, mi_id residual, int silu_mul,
+                              mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, wb, w);
+  const Buffer *gb = nullptr, *rb = nullptr;
+  if (gamma) {
+    gb = lookup(ctx, gamma);
+    if (!gb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)gamma);
+  }
+  if (residual) {
+    rb = lookup(ctx, residual);
+    if (!rb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)residual);
+  }
+  int s = check_common(ctx, xb, wb, gb, "norm_matvec");
+  if (s) return s;
+  const int64_t M = xb->rows, K = xb->cols, N = wb->rows;
+  if (silu_mul && (N % 2 || rb))
+    return fail(ctx, MI_E_ARG, "norm_matvec: silu_mul takes a [2 * inter, K] weight and no residual");
+  const int64_t ncols = silu_mul ? N / 2 : N;
+  if (rb && (rb->elem != MI_F32 || rb->rows != M || rb->cols != N))
+    return fail(ctx, MI_E_ARG, "norm_matvec: residual must be [%lld, %lld] F32", (long long)M, (long long)N);
+  mi_id id;
+  Buffer *ob;
+  s = new_buffer(ctx, M, ncols, MI_F32, &id, &ob);
+  if (s) return s;
+  if (ncols > 0) {
+    DecodeArgs g{};
+    g.x = static_cast<const float *>(xb->ptr);
+    g.ldx = K;
+    g.K = K;
+    g.gamma = gb ? static_cast<const float *>(gb->ptr) : nullptr;
+    g.eps = eps;
+    g.w = static_cast<const uint16_t *>(wb->ptr);
+    g.N = N;
+    g.resid = rb ? static_cast<const float *>(rb->ptr) : nullptr;
+    g.out = static_cast<float *>(ob->ptr);
+    g.ldo = ncols;
+    if (silu_mul) {
+      g.inter = ncols;
+      g.npairs = ncols;
+      launch_decode<DM_SILU_MUL>(M, g, ctx->stream);
+    } else {
+      g.npairs = (N + 1) / 2;
+      launch_decode<DM_PLAIN>(M, g, ctx->stream);
+    }
+  }
+  s = check_launch(ctx, "norm_matvec");
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                mi_id sin_table, int64_t heads, int64_t kv_heads, int64_t pos, mi_id k_cache,
+                                mi_id v_cache, mi_id *q_out) {
+  MI_ENTER(ctx);
+  if (!q_out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, wb, w_qkv);
+  MI_BUF(ctx, cb, cos_table);
+  MI_BUF(ctx, sb, sin_table);
+  MI_BUF(ctx, kb, k_cache);
+  MI_BUF(ctx, vb, v_cache);
+  const Buffer *gb = nullptr;
+  if (gamma) {
+    gb = lookup(ctx, gamma);
+    if (!gb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)gamma);
+  }
+  int s = check_common(ctx, xb, wb, gb, "norm_qkv_rope");
+  if (s) return s;
+  const int64_t M = xb->rows, D = kb->cols;
+  if (heads < 1 || kv_heads < 1 || D < 2 || D % 2)
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: heads %lld, kv heads %lld, head width %lld", (long long)heads,
+                (long long)kv_heads, (long long)D);
+  if (wb->rows != (heads + 2 * kv_heads) * D)
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: weight has %lld rows, want (heads + 2 kv_heads) * %lld = %lld",
+                (long long)wb->rows, (long long)D, (long long)((heads + 2 * kv_heads) * D));
+  if (kb->elem != MI_F32 || vb->elem != MI_F32 || vb->cols != D || vb->rows != kb->rows ||
+      kb->rows % (M * kv_heads))
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: caches must both be [rows * kv_heads * max_ctx, %lld] F32", (long long)D);
+  const int64_t maxc = kb->rows / (M * kv_heads);
+  if (pos < 0 || pos >= maxc) return fail(ctx, MI_E_ARG, "norm_qkv_rope: position %lld beyond the cache's %lld", (long long)pos, (long long)maxc);
+  if (cb->elem != MI_F32 || sb->elem != MI_F32 || cb->cols != D || sb->cols != D || cb->rows <= pos || sb->rows <= pos)
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: rotary tables must be [> %lld, %lld] F32", (long long)pos, (long long)D);
+  mi_id id;
+  Buffer *ob;
+  s = new_buffer(ctx, M, heads * D, MI_F32, &id, &ob);
+  if (s) return s;
+  DecodeArgs g{};
+  g.x = static_cast<const float *>(xb->ptr);
+  g.ldx = xb->cols;
+  g.K = xb->cols;
+  g.gamma = gb ? static_cast<const float *>(gb->ptr) : nullptr;
+  g.eps = eps;
+  g.w = static_cast<const uint16_t *>(wb->ptr);
+  g.N = wb->rows;
+  g.npairs = wb->rows / 2;
+  g.out = static_cast<float *>(ob->ptr);
+  g.ldo = heads * D;
+  g.d = static_cast<int>(D);
+  g.H = static_cast<int>(heads);
+  g.KVH = static_cast<int>(kv_heads);
+  g.pos = pos;
+  g.maxc = maxc;
+  g.cos = static_cast<const float *>(cb->ptr);
+  g.sin = static_cast<const float *>(sb->ptr);
+  g.kc = static_cast<float *>(kb->ptr);
+  g.vc = static_cast<float *>(vb->ptr);
+  launch_decode<DM_QKV>(M, g, ctx->stream);
+  s = check_launch(ctx, "norm_qkv_rope");
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *q_out = id;
+  return MI_OK;
+}

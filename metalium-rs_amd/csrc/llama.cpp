@@ -9,7 +9,12 @@
 // Layout on the device.  Activations are F32 [batch * t, hidden], row
 // (sequence, position).  Projection weights are BF16 stored [out, in], so
 // every product reads its weight k-contiguous: the decode GEMV streams each
-// weight row once; prefill runs the MFMA kernels.  The KV cache of a layer is
+// weight row once; prefill runs the MFMA kernels.  Each layer's q|k|v and
+// gate|up weights are one matrix each (the reference's `Llama::fused`,
+// llama.rs:655-672): prefill multiplies by row blocks of them, and a decode
+// step of at most 8 sequences runs six fused launches a layer -- RMSNorm +
+// q|k|v + RoPE + cache write, attention (two), o + residual, RMSNorm +
+// gate|up + SiLU-mul, down + residual.  The KV cache of a layer is
 // F32 [batch * kv_heads * max_ctx, head_dim], item (sequence, kv head), so the
 // attention of a query group is one product over a block of the cache:
 // queries regrouped to [batch * kv_heads, t * group, head_dim] (row
@@ -30,7 +35,7 @@ thread_local std::string g_model_error;
 using burn::Tensor;
 
 struct Layer {
-  Tensor attn_norm, wq, wk, wv, wo, mlp_norm, wgate, wup, wdown;
+  Tensor attn_norm, wqkv, wo, mlp_norm, wgu, wdown;  // wqkv = [wq; wk; wv], wgu = [gate; up]
   Tensor cache_k, cache_v;
 };
 
@@ -61,11 +66,13 @@ Tensor weight(mi_ctx *ctx, int64_t rows, int64_t cols, float stdv, uint64_t base
 
 // Largest number of new positions per sequence that take the fused attention.
 constexpr int64_t kFusedAttentionMaxT = 16;
+// Largest batch whose decode step takes the fused projections.
+constexpr int64_t kDecodeMaxBatch = 8;
 
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
 // The forward of `t` positions per sequence at cache length m->len; returns
-// the final-norm hidden states [batch * t, hidden].
+// the hidden states [batch * t, hidden] before the final norm.
 Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t) {
   mi_ctx *ctx = m->ctx;
   const mi_llama_config &c = m->cfg;
@@ -92,11 +99,27 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
   }
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
 
+  const int64_t qd = H * D, kvd = KVH * D, hid = c.hidden, I = c.intermediate;
+  if (t == 1 && batch <= kDecodeMaxBatch && fused && hid % 8 == 0 && I % 8 == 0) {
+    // Decode: six fused launches a layer.
+    for (Layer &L : m->layers) {
+      Tensor q = burn::norm_qkv_rope(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos0, L.cache_k,
+                                     L.cache_v);
+      Tensor o = burn::attention_rows(q, L.cache_k, L.cache_v, batch, 1, H, KVH, pos0, scale);
+      x = burn::norm_matvec(o, nullptr, 0.0f, L.wo, &x, false);
+      Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, L.wgu, nullptr, true);
+      x = burn::norm_matvec(h, nullptr, 0.0f, L.wdown, &x, false);
+    }
+    m->len = ctxlen;
+    return x;
+  }
   for (Layer &L : m->layers) {
     Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps);
-    Tensor q = burn::float_matmul(xn, false, L.wq, true).reshape({rows * H, D});
-    Tensor k = burn::float_matmul(xn, false, L.wk, true).reshape({rows * KVH, D});
-    Tensor v = burn::float_matmul(xn, false, L.wv, true).reshape({rows * KVH, D});
+    // Row blocks of the fused q|k|v weight.
+    Tensor q = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, qd, 0, 0, 0, 0).reshape({rows * H, D});
+    Tensor k = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, kvd, 0, 0, qd * hid, 0).reshape({rows * KVH, D});
+    Tensor v = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, kvd, 0, 0, (qd + kvd) * hid, 0)
+                   .reshape({rows * KVH, D});
     q = burn::rope(q, m->rope_cos, m->rope_sin, H, t, pos0);
     k = burn::rope(k, m->rope_cos, m->rope_sin, KVH, t, pos0);
     // Append k, v at positions pos0.. of each (sequence, kv head) item.
@@ -132,20 +155,30 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
     }
     x = burn::float_add(x, burn::float_matmul(oh, false, L.wo, true));
     Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps);
-    Tensor gate = burn::float_matmul(hn, false, L.wgate, true);
-    Tensor up = burn::float_matmul(hn, false, L.wup, true);
+    Tensor gate = burn::matmul_blocks(hn, false, L.wgu, true, 1, rows, hid, I, 0, 0, 0, 0);
+    Tensor up = burn::matmul_blocks(hn, false, L.wgu, true, 1, rows, hid, I, 0, 0, I * hid, 0);
     x = burn::float_add(x, burn::float_matmul(burn::silu_mul(gate, up), false, L.wdown, true));
   }
   m->len = ctxlen;
-  return burn::rms_norm(x, m->final_norm, c.eps);
+  return x;
 }
 
-// The tied head over the last position of each sequence: [batch, vocab].
+// The final norm and the tied head over the last position of each sequence:
+// [batch, vocab].  One position per sequence and at most 8 sequences: one
+// fused norm + GEMV launch over the embedding table.
 Tensor head_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
-  const int64_t dims[4] = {1, 1, batch, m->cfg.hidden};
-  const int64_t st[4] = {0, 0, t * m->cfg.hidden, 1};
-  Tensor last = burn::copy4(hidden, dims, (t - 1) * m->cfg.hidden, st);
-  return burn::float_matmul(last, false, m->embed, true);
+  const mi_llama_config &c = m->cfg;
+  if (t == 1 && batch <= kDecodeMaxBatch && c.hidden % 8 == 0)
+    return burn::norm_matvec(hidden, &m->final_norm, c.eps, m->embed, nullptr, false);
+  const int64_t dims[4] = {1, 1, batch, c.hidden};
+  const int64_t st[4] = {0, 0, t * c.hidden, 1};
+  Tensor last = burn::copy4(hidden, dims, (t - 1) * c.hidden, st);
+  return burn::float_matmul(burn::rms_norm(last, m->final_norm, c.eps), false, m->embed, true);
+}
+
+// Every position's logits: [batch * t, vocab].
+Tensor head_all(mi_llama *m, const Tensor &hidden) {
+  return burn::float_matmul(burn::rms_norm(hidden, m->final_norm, m->cfg.eps), false, m->embed, true);
 }
 
 void ensure_cache(mi_llama *m, int64_t batch) {
@@ -186,13 +219,10 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
     m->layers.resize(c.layers);
     for (Layer &L : m->layers) {
       L.attn_norm = ones(ctx, c.hidden);
-      L.wq = weight(ctx, qd, c.hidden, init_std, next());
-      L.wk = weight(ctx, kvd, c.hidden, init_std, next());
-      L.wv = weight(ctx, kvd, c.hidden, init_std, next());
+      L.wqkv = weight(ctx, qd + 2 * kvd, c.hidden, init_std, next());
       L.wo = weight(ctx, c.hidden, qd, init_std, next());
       L.mlp_norm = ones(ctx, c.hidden);
-      L.wgate = weight(ctx, c.intermediate, c.hidden, init_std, next());
-      L.wup = weight(ctx, c.intermediate, c.hidden, init_std, next());
+      L.wgu = weight(ctx, 2 * static_cast<int64_t>(c.intermediate), c.hidden, init_std, next());
       L.wdown = weight(ctx, c.hidden, c.intermediate, init_std, next());
     }
     // Rotary tables (rope.rs:14-60): angle = position * theta^(-2i / d), the
@@ -227,24 +257,44 @@ int mi_llama_destroy(mi_llama *m) {
 
 int mi_llama_param(mi_llama *m, int layer, int which, mi_id *out) {
   if (!m || !out) return MI_E_ARG;
+  const mi_llama_config &c = m->cfg;
+  const int64_t qd = static_cast<int64_t>(c.heads) * c.head_dim,
+                kvd = static_cast<int64_t>(c.kv_heads) * c.head_dim, I = c.intermediate;
   const Tensor *t = nullptr;
+  int64_t row0 = 0, nrows = -1;  // a row block of a fused matrix
   if (which == 0) t = &m->embed;
   else if (which == 1) t = &m->final_norm;
   else if (layer >= 0 && layer < static_cast<int>(m->layers.size())) {
     Layer &L = m->layers[layer];
-    const Tensor *w[] = {&L.attn_norm, &L.wq, &L.wk, &L.wv, &L.wo, &L.mlp_norm, &L.wgate, &L.wup, &L.wdown};
-    if (which >= 2 && which <= 10) t = w[which - 2];
+    switch (which) {
+      case 2: t = &L.attn_norm; break;
+      case 3: t = &L.wqkv; row0 = 0; nrows = qd; break;
+      case 4: t = &L.wqkv; row0 = qd; nrows = kvd; break;
+      case 5: t = &L.wqkv; row0 = qd + kvd; nrows = kvd; break;
+      case 6: t = &L.wo; break;
+      case 7: t = &L.mlp_norm; break;
+      case 8: t = &L.wgu; row0 = 0; nrows = I; break;
+      case 9: t = &L.wgu; row0 = I; nrows = I; break;
+      case 10: t = &L.wdown; break;
+      default: break;
+    }
   }
   if (!t) {
     g_model_error = "no such parameter";
     return MI_E_ARG;
   }
   try {
-    t->use();
+    // A copy (of the whole weight or of its row block) the caller frees.
+    mi_id id;
+    const int64_t cols = t->cols();
+    const int64_t n = nrows < 0 ? t->rows() : nrows;
+    const int64_t dims[4] = {1, 1, n, cols};
+    const int64_t st[4] = {0, 0, cols, 1};
+    burn::check(m->ctx, mi_copy_strided4(m->ctx, t->use(), dims, row0 * cols, st, &id), "param");
+    *out = id;
   } catch (const std::exception &e) {
     return fail_model(e);
   }
-  *out = t->id();
   return MI_OK;
 }
 
@@ -261,7 +311,7 @@ int mi_llama_forward(mi_llama *m, const int32_t *ids, int32_t batch, int32_t t, 
     if (batch > m->cfg.max_batch || m->len + t > m->cfg.max_ctx) throw burn::Error(MI_E_ARG, "batch or context too large");
     ensure_cache(m, batch);
     Tensor h = forward_hidden(m, ids, batch, t);
-    Tensor out = all_positions ? burn::float_matmul(h, false, m->embed, true) : head_last(m, h, batch, t);
+    Tensor out = all_positions ? head_all(m, h) : head_last(m, h, batch, t);
     // Hand the buffer to the caller: it owns (and frees) the id.
     mi_id id;
     burn::check(m->ctx, mi_cast(m->ctx, out.use(), MI_F32, &id), "logits");

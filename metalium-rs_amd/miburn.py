@@ -100,6 +100,8 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
         "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
+        "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
+        "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
         "mi_reduce": [P, U64, c_int, c_int, Ip],
         "mi_reduce_all": [P, U64, c_int, Ip],
@@ -266,6 +268,16 @@ class Engine:
 
     def rope(self, x: int, cos: int, sin: int, heads: int, seq: int, pos0: int) -> int:
         return self._out(self._lib.mi_rope, x, cos, sin, heads, seq, pos0)
+
+    def norm_matvec(self, x: int, gamma: int, eps: float, w: int, residual: int = 0, silu_mul: bool = False) -> int:
+        """Fused decode projection: residual + rmsnorm(x) w^T, or silu(g) * u."""
+        return self._out(self._lib.mi_norm_matvec, x, gamma, eps, w, residual, int(silu_mul))
+
+    def norm_qkv_rope(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
+                      kv_heads: int, pos: int, k_cache: int, v_cache: int) -> int:
+        """Fused decode q|k|v projection with RoPE and the KV-cache write; returns q."""
+        return self._out(self._lib.mi_norm_qkv_rope, x, gamma, eps, w_qkv, cos, sin, heads, kv_heads, pos,
+                         k_cache, v_cache)
 
     def attention_rows(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int, kv_heads: int,
                        pos0: int, scale: float) -> int:
@@ -451,6 +463,7 @@ class Llama:
             pass
 
     def param(self, name: str, layer: int = 0) -> int:
+        """A copy of the weight: a new id the caller frees."""
         out = ctypes.c_uint64()
         self._check(self.L.mi_llama_param(self.h, layer, LLAMA_PARAMS[name], ctypes.byref(out)))
         return out.value

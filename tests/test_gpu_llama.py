@@ -23,8 +23,10 @@ TINY = dict(vocab=512, hidden=64, layers=2, heads=4, kv_heads=2, head_dim=16, in
 
 def weights(eng, model, cfg):
     def get(name, layer=0):
-        r, c, e = eng.metadata(model.param(name, layer))
-        x = eng.download(model.param(name, layer))
+        pid = model.param(name, layer)
+        r, c, e = eng.metadata(pid)
+        x = eng.download(pid)
+        eng.free(pid)
         return torch.from_numpy(miburn.bf16_to_f32(x) if e == miburn.BF16 else x.astype(np.float32))
     W = {"embed": get("embed"), "final_norm": get("final_norm").reshape(-1), "layers": []}
     for l in range(cfg["layers"]):
@@ -81,7 +83,7 @@ def ref_logits(W, cfg, ids):
 
 @pytest.fixture(scope="module")
 def tiny(engine):
-    m = miburn.Llama(engine, TINY, max_ctx=64, max_batch=4, seed=3, init_std=0.2)
+    m = miburn.Llama(engine, TINY, max_ctx=64, max_batch=10, seed=3, init_std=0.2)
     return m, weights(engine, m, TINY)
 
 
@@ -100,12 +102,13 @@ def test_prefill_logits_all_positions(engine, tiny, t):
     close_logits(got, ref_logits(W, TINY, ids))
 
 
-def test_incremental_decode_matches_full_forward(engine, tiny):
+@pytest.mark.parametrize("batch", [3, 9])  # fused decode launches; the composition (over 8 sequences)
+def test_incremental_decode_matches_full_forward(engine, tiny, batch):
     """Prefill 9 tokens, then 5 single-token steps through the KV cache: each
     step's logits equal the full-sequence forward's at that position."""
     m, W = tiny
     rng = np.random.default_rng(6)
-    ids = rng.integers(0, TINY["vocab"], (3, 14)).astype(np.int32)
+    ids = rng.integers(0, TINY["vocab"], (batch, 14)).astype(np.int32)
     want = ref_logits(W, TINY, ids)
     m.reset()
     got = engine.download(m.forward(ids[:, :9]))  # last position of the prefill

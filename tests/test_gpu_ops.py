@@ -600,6 +600,100 @@ def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
 
 
+# ------------------------------------------------------ fused decode projections
+def decode_inputs(M, K, N):
+    x = rnd(M, K)
+    g = rnd(1, K) + np.float32(1.0)
+    w = orc.to_bf16(rnd(N, K, scale=0.05))
+    return x, g, w
+
+
+def rms_ref(x, g, eps):
+    x64 = x.astype(np.float64)
+    return x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + eps) * g.astype(np.float64)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("N", [576, 577])
+def test_norm_matvec_residual(engine, M, N):
+    K, eps = 576, 1e-5
+    x, g, wb = decode_inputs(M, K, N)
+    res = rnd(M, N)
+    w = orc.from_bf16(wb).astype(np.float64)
+    got = engine.download(engine.norm_matvec(engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb),
+                                             engine.upload(res)))
+    xn = rms_ref(x, g, eps)
+    want = res + xn @ w.T
+    assert np.abs(got - want).max() <= 1e-5 * (np.abs(xn) @ np.abs(w).T).max() + 1e-6 * np.abs(res).max()
+    # Without a gain: the plain product.
+    got = engine.download(engine.norm_matvec(engine.upload(x), 0, 0.0, engine.upload_bf16(wb)))
+    assert np.abs(got - x @ w.T).max() <= 1e-5 * (np.abs(x) @ np.abs(w).T).max()
+
+
+def test_norm_matvec_silu_mul(engine):
+    M, K, I, eps = 4, 576, 1536, 1e-5
+    x, g, wb = decode_inputs(M, K, 2 * I)
+    w = orc.from_bf16(wb).astype(np.float64)
+    got = engine.download(engine.norm_matvec(engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb),
+                                             silu_mul=True))
+    y = rms_ref(x, g, eps) @ w.T
+    gate, up = y[:, :I], y[:, I:]
+    want = gate / (1 + np.exp(-gate)) * up
+    assert got.shape == (M, I)
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_norm_qkv_rope_writes_cache(engine, M):
+    H, KVH, D, K, maxc, pos, eps = 9, 3, 64, 576, 40, 17, 1e-5
+    x, g, wb = decode_inputs(M, K, (H + 2 * KVH) * D)
+    w = orc.from_bf16(wb).astype(np.float64)
+    ang = pos * (1e5 ** (-2.0 * np.arange(D // 2) / D))
+    cos = np.tile(np.concatenate([np.cos(ang), np.cos(ang)]), (maxc, 1)).astype(np.float32)
+    sin = np.tile(np.concatenate([-np.sin(ang), np.sin(ang)]), (maxc, 1)).astype(np.float32)
+    kc0 = rnd(M * KVH * maxc, D)
+    vc0 = rnd(M * KVH * maxc, D)
+    kc, vc = engine.upload(kc0), engine.upload(vc0)
+    q = engine.download(engine.norm_qkv_rope(engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb),
+                                             engine.upload(cos), engine.upload(sin), H, KVH, pos, kc, vc))
+    y = rms_ref(x, g, eps) @ w.T  # [M, (H + 2 KVH) D]
+
+    def rope(h):  # h [M, heads, D]
+        rot = np.concatenate([h[..., D // 2:], h[..., :D // 2]], -1)
+        return h * cos[pos] + rot * sin[pos]
+    scale = (np.abs(rms_ref(x, g, eps)) @ np.abs(w).T).max()
+    want_q = rope(y[:, :H * D].reshape(M, H, D)).reshape(M, H * D)
+    assert np.abs(q - want_q).max() <= 2e-5 * scale
+    kc1 = engine.download(kc).reshape(M, KVH, maxc, D)
+    vc1 = engine.download(vc).reshape(M, KVH, maxc, D)
+    want_k = rope(y[:, H * D:(H + KVH) * D].reshape(M, KVH, D))
+    want_v = y[:, (H + KVH) * D:].reshape(M, KVH, D)
+    assert np.abs(kc1[:, :, pos] - want_k).max() <= 2e-5 * scale
+    assert np.abs(vc1[:, :, pos] - want_v).max() <= 2e-5 * scale
+    # Every other cache row is untouched.
+    keep = np.ones(maxc, bool)
+    keep[pos] = False
+    assert np.array_equal(kc1[:, :, keep], kc0.reshape(M, KVH, maxc, D)[:, :, keep])
+    assert np.array_equal(vc1[:, :, keep], vc0.reshape(M, KVH, maxc, D)[:, :, keep])
+
+
+def test_decode_projection_errors(engine):
+    w = engine.upload_bf16(orc.to_bf16(rnd(64, 576)))
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_matvec(engine.upload(rnd(9, 576)), 0, 0.0, w)  # nine rows
+    assert e.value.kind == "UNSUPPORTED"
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_matvec(engine.upload(rnd(2, 576)), 0, 0.0, engine.upload(rnd(64, 576)))  # F32 weight
+    assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_matvec(engine.upload(rnd(2, 572)), 0, 0.0, engine.upload_bf16(orc.to_bf16(rnd(64, 572))))
+    assert e.value.kind == "UNSUPPORTED"  # width not a multiple of 8
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_matvec(engine.upload(rnd(2, 576)), 0, 0.0, engine.upload_bf16(orc.to_bf16(rnd(63, 576))),
+                           silu_mul=True)  # odd gate|up rows
+    assert e.value.kind == "ARG"
+
+
 def test_attention_rows_errors(engine):
     q = engine.upload(rnd(2, 10 * 64))
     k = engine.upload(rnd(2 * 1 * 16, 64))
