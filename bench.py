@@ -37,6 +37,12 @@ sys.path.insert(0, os.path.join(ROOT, "metalium-rs_amd"))
 
 PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}  # MI355X dense MFMA (AMD published)
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the bf16 4096^3 NN product, from two rocprofv3 --pmc
+# passes over `bench.py --no-cpu --no-models --steps 5 --warmup 1` (FETCH_SIZE,
+# then WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
+# a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,703 KiB
+# read + 65,536 KiB written.  Only that configuration was measured.
+GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268527710}
 
 
 def cpu_baseline(n: int = 1024) -> dict:
@@ -270,7 +276,7 @@ def main() -> int:
         "config": {"workload": f"matmul {args.dtype}-in/f32-acc C=A.B {n}^3, A and B row-major (NN)",
                    "m": n, "n": n, "k": n},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": None,
+                     "frac": round(achieved / peak, 4), "traffic": GEMM_TRAFFIC_BYTES.get((args.dtype, n)),
                      "kernel_ms": round(kernel_ms, 5), "min_hbm_bytes": traffic_min},
     }
     if not args.no_cpu:

@@ -8,8 +8,8 @@
 //
 // MI355X design.  The cache of one (sequence, kv head) item is F32 [max_ctx,
 // D], position-major, so a key or value row is one contiguous D-float read.
-// A block of 256 threads (4 wavefronts) takes one (item, query position,
-// key chunk); the group's G query heads share every key and value row read.
+// A block of 4 wavefronts takes one (item, query position, key chunk); the
+// group's G query heads share every key and value row read.
 // D/4 lanes read a row as float4s (a wavefront covers 64/(D/4) rows per
 // access, coalesced), dot products fold over those lanes with xor shuffles,
 // the scores [G, chunk] stay in LDS, each softmax row is one wavefront's, and
@@ -21,7 +21,9 @@
 // blocks (split-K over the context): each chunk writes its own max, exp-sum
 // and unnormalised P V to scratch, and a combine pass rescales them by
 // exp(max_s - max) and divides.  One chunk writes the normalised result
-// directly, the composition's exact formula order.
+// directly, the composition's exact formula order.  A block loads the value
+// rows of its first pass before computing the scores (one HBM round trip
+// less on a short chunk).
 #include "common.hpp"
 #include "wave.hpp"
 
@@ -33,6 +35,7 @@ constexpr int ATT_MAX_GROUP = 8;       // query heads per kv head
 constexpr int64_t ATT_MAX_CHUNK = 1024;
 constexpr int64_t ATT_MIN_CHUNK = 64;
 constexpr int64_t ATT_TARGET_BLOCKS = 512;
+constexpr int ATT_WAVES = 4;  // wavefronts per chunk block
 
 // scores[g] = q[g] . k for one key row per lane group, folded over the row's
 // D/4 lanes.
@@ -48,15 +51,16 @@ __device__ __forceinline__ void dots(const float4 (&qv)[G], float4 kv, float (&p
 
 // One (item, position, chunk).  DIRECT: the only chunk -- write normalised
 // rows of `out`.  Else write part[(item * S + s)] = {m[G], l[G], o[G][D]}.
-template <int D, int G>
-__global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, const float *kc, const float *vc,
+template <int D, int G, int NW>
+__global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q, const float *kc, const float *vc,
                                                               float *out, float *part, int64_t T, int64_t H,
                                                               int64_t KVH, int64_t pos0, int64_t maxc, int64_t chunk,
                                                               float scale, int direct) {
   constexpr int LPR = D / 4;     // lanes per row
   constexpr int KPW = 64 / LPR;  // rows per wavefront access
-  constexpr int U = 4;           // accesses in flight per wavefront
-  constexpr int STEP = 4 * KPW;  // rows per block access
+  constexpr int U = 4;            // accesses in flight per wavefront
+  constexpr int STEP = NW * KPW;  // rows per block access
+  constexpr int NT = NW * 64;
   extern __shared__ float sm[];
   const int s = blockIdx.y;
   const int64_t item = blockIdx.x;  // (sequence, kv head, position), position fastest
@@ -68,17 +72,26 @@ __global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, co
   const float *K = kc + ((bj)*maxc + lo) * D;
   const float *V = vc + ((bj)*maxc + lo) * D;
   float *scores = sm;                     // [G][chunk]
-  float *red = sm + G * chunk;            // [4][G][D]
-  float *stat = red + 4 * G * D;          // [G] max, [G] sum
+  float *red = sm + G * chunk;            // [NW][G][D]
+  float *stat = red + NW * G * D;         // [G] max, [G] sum
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sl = lane % LPR, kk = lane / LPR;
   const float *qrow = q + (b * T + p) * H * D + j * G * D;
   float4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const float4 *>(qrow + g * D + 4 * sl);
+  // The value rows of the first P V pass are independent of the scores:
+  // their loads are issued now and land while the scores and softmax run.
+  const int64_t first = static_cast<int64_t>(wave) * KPW + kk;
+  float4 vv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t c = first + u * STEP;
+    vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 
   // Scores, U accesses in flight per wavefront.
-  for (int64_t c0 = static_cast<int64_t>(wave) * KPW + kk; c0 < len + kk; c0 += STEP * U) {
+  for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
     float4 kv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -98,7 +111,7 @@ __global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, co
   __syncthreads();
 
   // Softmax statistics of each row (one wavefront per row).
-  for (int g = wave; g < G; g += 4) {
+  for (int g = wave; g < G; g += NW) {
     float *row = scores + g * chunk;
     float m = -INFINITY;
     for (int64_t c = lane; c < len; c += 64) m = max_nan(m, row[c]);
@@ -126,12 +139,13 @@ __global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, co
   float4 acc[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t c0 = static_cast<int64_t>(wave) * KPW + kk; c0 < len + kk; c0 += STEP * U) {
-    float4 vv[U];
+  for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
+    if (c0 != first) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + u * STEP;
-      vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + u * STEP;
+        vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -170,53 +184,76 @@ __global__ void __launch_bounds__(256) attention_chunk_kernel(const float *q, co
     if (tid < 2 * G) pb[tid] = stat[tid];
     dst = pb + 2 * G;
   }
-  for (int e = tid; e < G * D; e += 256) {
-    const int g = e / D, d = e % D;
-    dst[e] = ((red[g * D + d] + red[(G + g) * D + d]) + red[(2 * G + g) * D + d]) + red[(3 * G + g) * D + d];
+  for (int e = tid; e < G * D; e += NT) {
+    float t = red[e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w * G * D + e];
+    dst[e] = t;
   }
 }
 
 // Combine the chunks of one (item, position): out = sum_s w_s o_s / sum_s w_s
-// l_s with w_s = exp(m_s - max_s m_s), the sum clamped below at FLT_MIN.
+// l_s with w_s = exp(m_s - max_s m_s), the sum clamped below at FLT_MIN.  The
+// chunks' statistics go to LDS in one pass and the weights are formed there,
+// so each output element then issues its S loads back to back.
 template <int D, int G>
 __global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, float *out, int64_t T, int64_t H,
                                                                 int64_t KVH, int S) {
+  extern __shared__ float st[];  // [S][2G] statistics, then [S][G] weights, [G] denominators
   const int64_t item = blockIdx.x;
   const int64_t p = item % T, bj = item / T;
   const int64_t j = bj % KVH, b = bj / KVH;
-  const float *pb = part + item * S * static_cast<int64_t>(G * (D + 2));
+  constexpr int PS = G * (D + 2);  // floats per chunk partial
+  const float *pb = part + item * S * static_cast<int64_t>(PS);
+  float *w = st + 2 * G * S;
+  float *den = w + G * S;
+  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + g]);
+    float l = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float ws = expf(st[s * 2 * G + g] - M);
+      w[s * G + g] = ws;
+      l += ws * st[s * 2 * G + G + g];
+    }
+    den[g] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
+  }
+  __syncthreads();
   float *dst = out + (b * T + p) * H * D + j * G * D;
   for (int e = threadIdx.x; e < G * D; e += 256) {
     const int g = e / D;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = max_nan(M, pb[s * G * (D + 2) + g]);
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float *ps = pb + s * G * (D + 2);
-      const float w = expf(ps[g] - M);
-      den += w * ps[G + g];
-      num += w * ps[2 * G + e];
-    }
-    den = isnan(den) ? den : (den > FLT_MIN ? den : FLT_MIN);
-    dst[e] = num / den;
+    float num = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
+    dst[e] = num / den[g];
   }
+}
+
+// LDS bytes of a chunk kernel with `nw` wavefronts.
+inline size_t attention_smem(int64_t G, int64_t D, int64_t chunk, int nw) {
+  return static_cast<size_t>(G * chunk + nw * G * D + 2 * G) * sizeof(float);
 }
 
 template <int D, int G>
 void launch_attention(hipStream_t st, const float *q, const float *k, const float *v, float *out, float *part,
                       int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
                       int64_t chunk, float scale) {
-  const size_t smem = static_cast<size_t>(G * chunk + 4 * G * D + 2 * G) * sizeof(float);
-  attention_chunk_kernel<D, G><<<dim3(static_cast<unsigned>(items), static_cast<unsigned>(S)), 256, smem, st>>>(
-      q, k, v, out, part, T, H, KVH, pos0, maxc, chunk, scale, S == 1);
+  const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(S));
+  const size_t smem = attention_smem(G, D, chunk, ATT_WAVES);
+  attention_chunk_kernel<D, G, ATT_WAVES><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pos0, maxc,
+                                                                            chunk, scale, S == 1);
   if (S > 1)
-    attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, 0, st>>>(part, out, T, H, KVH, S);
+    attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, static_cast<size_t>(3 * G * S + G) * sizeof(float),
+                                     st>>>(part, out, T, H, KVH, S);
 }
 
 template <int D>
 bool dispatch_group(int64_t G, hipStream_t st, const float *q, const float *k, const float *v, float *out,
-                    float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
-                    int64_t chunk, float scale) {
+                    float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0,
+                    int64_t maxc, int64_t chunk, float scale) {
   switch (G) {
 #define MI_ATT_G(g)                                                                                   \
   case g:                                                                                             \
@@ -261,18 +298,22 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
     return fail(ctx, MI_E_ARG, "attention_rows: positions %lld..%lld beyond the cache's %lld", (long long)pos0,
                 (long long)(pos0 + t), (long long)maxc);
   // Chunks: at least enough that none exceeds ATT_MAX_CHUNK keys, more (down
-  // to ATT_MIN_CHUNK keys each) until the grid has ATT_TARGET_BLOCKS blocks.
+  // to ATT_MIN_CHUNK keys each) until the grid has ATT_TARGET_BLOCKS blocks --
+  // decode has only batch * kv_heads query groups, and one block's chain of
+  // dependent loads over a long context is slower than several short chains
+  // and a combine pass.  Chunks are a multiple of 4 keys, so the LDS fold area
+  // after the scores stays 16-byte aligned for its float4 stores.
   const int64_t items = batch * kv_heads * t, nmax = pos0 + t;
   int64_t S = (nmax + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
   const int64_t want = (ATT_TARGET_BLOCKS + items - 1) / items;
   const int64_t cap = (nmax + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
   if (want > S) S = want < cap ? want : cap;
   if (S < 1) S = 1;
-  // Chunks are a multiple of 4 keys, so the LDS fold area after the scores
-  // stays 16-byte aligned for its float4 stores.
   const int64_t chunk = ((nmax + S - 1) / S + 3) / 4 * 4;
   S = (nmax + chunk - 1) / chunk;
   if (items > INT32_MAX || S > 65535) return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: grid too large");
+  if (static_cast<size_t>(3 * G * S + G) * sizeof(float) > 65536)
+    return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: context of %lld keys too long", (long long)nmax);
   float *part = nullptr;
   if (S > 1) {
     part = static_cast<float *>(scratch(ctx, static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float)));

@@ -86,6 +86,22 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   }
   const bool has1 = r1 < g.N;
 
+  // The weight rows are independent of the norm: with K <= 2048 (four
+  // 16-byte chunks a lane) all of them are requested first, so the norm's
+  // loads and reduction overlap the weights' HBM latency.
+  constexpr int PRE = 4;
+  uint4 pw0[PRE], pw1[PRE];
+  if (g.K <= 512 * PRE) {
+#pragma unroll
+    for (int c = 0; c < PRE; ++c) {
+      const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
+      if (k < g.K) {
+        pw0[c] = *reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k);
+        pw1[c] = has1 ? *reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k) : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+
   // RMSNorm of the activation rows: sqrt(mean(x x) + eps).
   float rms[M];
 #pragma unroll
@@ -108,13 +124,8 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   float acc[M][2];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
-  for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
-    float w0[8], w1[8];
-    bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
-    if (has1) bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k), w1);
-    else
-#pragma unroll
-      for (int e = 0; e < 8; ++e) w1[e] = 0.0f;
+  // One 8-wide k step: activations (normalised on the fly) times both rows.
+  auto step = [&](int64_t k, const float (&w0)[8], const float (&w1)[8]) {
     float gm[8];
     if (g.gamma) {
       const float4 g0 = *reinterpret_cast<const float4 *>(g.gamma + k);
@@ -138,6 +149,28 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
       }
       acc[m][0] = t0;
       acc[m][1] = t1;
+    }
+  };
+  if (g.K <= 512 * PRE) {
+#pragma unroll
+    for (int c = 0; c < PRE; ++c) {
+      const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
+      if (k < g.K) {
+        float w0[8], w1[8];
+        bf16x8(pw0[c], w0);
+        bf16x8(pw1[c], w1);
+        step(k, w0, w1);
+      }
+    }
+  } else {
+    for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
+      float w0[8], w1[8];
+      bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
+      if (has1) bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k), w1);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w1[e] = 0.0f;
+      step(k, w0, w1);
     }
   }
 #pragma unroll

@@ -138,17 +138,31 @@ __global__ void __launch_bounds__(256) argmax_rows_kernel(const void *x, int ele
   if (lane == 0) out[row] = best.i == INT32_MAX ? 0 : best.i;
 }
 
-// Long rows (a vocabulary's logits): one 256-thread block per row, each
-// thread a strided share, folded by the same (value, index) rule in a fixed
-// order through LDS.
-__global__ void __launch_bounds__(256) argmax_block_kernel(const void *x, int elem, int64_t cols, int32_t *out) {
-  const int64_t row = blockIdx.x;
+// Long rows (a vocabulary's logits): blocks of 256 threads over column
+// chunks of a row, eight loads per thread in flight, folded by the same
+// (value, index) rule -- a total order, so the fold order does not matter.
+// One chunk per row writes the index; several write (value, index) partials
+// that argmax_fold_kernel folds, one wavefront per row.
+__global__ void __launch_bounds__(256) argmax_chunk_kernel(const void *x, int elem, int64_t cols, int64_t ch,
+                                                           int32_t *out, float *pv, int32_t *pi) {
+  const int64_t row = blockIdx.y, chunk = blockIdx.x, nch = gridDim.x;
+  const int64_t lo = chunk * ch, hi = lo + ch < cols ? lo + ch : cols;
   const int64_t base = row * cols;
   ArgBest best{-INFINITY, INT32_MAX};
-  for (int64_t j = threadIdx.x; j < cols; j += 256) {
-    float v = elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[base + j])
-                              : static_cast<const float *>(x)[base + j];
-    best = better(best, ArgBest{v, static_cast<int32_t>(j)});
+  for (int64_t j0 = lo + threadIdx.x; j0 < hi; j0 += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t j = j0 + 256 * u;
+      v[u] = j < hi ? (elem == MI_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[base + j])
+                                       : static_cast<const float *>(x)[base + j])
+                    : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t j = j0 + 256 * u;
+      if (j < hi) best = better(best, ArgBest{v[u], static_cast<int32_t>(j)});
+    }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -162,8 +176,28 @@ __global__ void __launch_bounds__(256) argmax_block_kernel(const void *x, int el
   if (threadIdx.x == 0) {
     ArgBest b{rv[0], ri[0]};
     for (int w = 1; w < 4; ++w) b = better(b, ArgBest{rv[w], ri[w]});
-    out[row] = b.i == INT32_MAX ? 0 : b.i;
+    if (nch == 1) {
+      out[row] = b.i == INT32_MAX ? 0 : b.i;
+    } else {
+      pv[row * nch + chunk] = b.v;
+      pi[row * nch + chunk] = b.i;
+    }
   }
+}
+
+__global__ void __launch_bounds__(256) argmax_fold_kernel(const float *pv, const int32_t *pi, int64_t nch,
+                                                          int64_t rows, int32_t *out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  ArgBest best{-INFINITY, INT32_MAX};
+  for (int64_t c = lane; c < nch; c += 64) best = better(best, ArgBest{pv[row * nch + c], pi[row * nch + c]});
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ArgBest other{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)};
+    best = better(best, other);
+  }
+  if (lane == 0) out[row] = best.i == INT32_MAX ? 0 : best.i;
 }
 
 }  // namespace mi
@@ -323,9 +357,26 @@ extern "C" int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out) {
   int s = new_buffer(ctx, R, 1, MI_I32, &id, &ob);
   if (s) return s;
   if (R > 0) {
-    if (C > 2048 && R <= INT32_MAX)
-      argmax_block_kernel<<<static_cast<unsigned>(R), 256, 0, ctx->stream>>>(xp, xe, C, static_cast<int32_t *>(ob->ptr));
-    else
+    if (C > 2048 && R <= 65535) {
+      // Chunks of at least 2048 columns, enough of them for ~256 blocks.
+      int64_t nch = (256 + R - 1) / R;
+      const int64_t cap = (C + 2047) / 2048;
+      if (nch > cap) nch = cap;
+      const int64_t ch = (C + nch - 1) / nch;
+      nch = (C + ch - 1) / ch;
+      float *pv = nullptr;
+      int32_t *pi = nullptr;
+      if (nch > 1) {
+        char *sc = static_cast<char *>(scratch(ctx, static_cast<size_t>(R * nch) * 8));
+        if (!sc) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "argmax scratch"); }
+        pv = reinterpret_cast<float *>(sc);
+        pi = reinterpret_cast<int32_t *>(sc + static_cast<size_t>(R * nch) * 4);
+      }
+      int32_t *o = static_cast<int32_t *>(ob->ptr);
+      argmax_chunk_kernel<<<dim3(static_cast<unsigned>(nch), static_cast<unsigned>(R)), 256, 0, ctx->stream>>>(
+          xp, xe, C, ch, o, pv, pi);
+      if (nch > 1) argmax_fold_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(pv, pi, nch, R, o);
+    } else
       argmax_rows_kernel<<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, R, C, static_cast<int32_t *>(ob->ptr));
     s = check_launch(ctx, "argmax_rows");
     if (s) { mi_free(ctx, id); return s; }
