@@ -84,11 +84,13 @@ def _time_op(eng, fn, reps: int, warm: int = 3) -> float:
     return ms
 
 
-def suite(steps: int) -> int:
+def suite(steps: int, matmul_mode=None) -> int:
     """HBM-bound kernels on [8192, 8192] F32 and the
     matmul cube sweep: one JSON line per kernel."""
     import miburn
     eng = miburn.Engine(0)
+    if matmul_mode:
+        eng.set_matmul_mode(miburn.MATMUL_FAST if matmul_mode == "fast" else miburn.MATMUL_ACCURATE)
     R = C = 8192
     n = R * C
     x = eng.random_dram(R, C, miburn.DRAW_NORMAL, 0.0, 1.0, base=21)
@@ -211,16 +213,20 @@ def main() -> int:
     ap.add_argument("--only", choices=["decoder", "mlp", "transformer"],
                     help="run one model harness alone (for profiling) and print its JSON")
     ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
+    ap.add_argument("--matmul-mode", choices=["fast", "accurate"], default=None,
+                    help="how products with an F32 operand run (default: the engine's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(sharding is described in DESIGN.md, not run)", file=sys.stderr)
         return 2
     if args.suite:
-        return suite(args.steps)
+        return suite(args.steps, args.matmul_mode)
 
     import miburn
     eng = miburn.Engine(0)
+    if args.matmul_mode:
+        eng.set_matmul_mode(miburn.MATMUL_FAST if args.matmul_mode == "fast" else miburn.MATMUL_ACCURATE)
     if args.only:
         out = {"decoder": lambda: decoder_bench(eng, args.batch), "mlp": lambda: mlp_bench(eng),
                "transformer": lambda: transformer_bench(eng)}[args.only]()

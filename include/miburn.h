@@ -119,6 +119,25 @@ int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
                      int64_t b_offset, int64_t b_stride, int out_elem,
                      mi_id *out);
 
+/* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
+ * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as
+ * TtConfig::matmul fixes it per attachment.  Applies to products with an F32
+ * operand; BF16 x BF16 products are the same in both.
+ *  FAST (the default, as the reference's): where a product is large enough to
+ *   be bound by the matrix cores (>= 2^33 multiply-adds over >= 128 tiles of
+ *   128 x 128), each F32 operand element is split as bf16 hi + bf16 lo and
+ *   a b = hi hi + hi lo + lo hi runs on the BF16 matrix cores with F32
+ *   accumulation; error per product <= 3 * 2^-18 |a||b| (the reference's
+ *   fast mode rounds operands to TF32, 2^-11).  Smaller products run as in
+ *   ACCURATE.  A non-finite operand element gives NaN in its row or column
+ *   where F32 arithmetic could give an infinity.
+ *  ACCURATE: F32 products on the F32 matrix cores, F32 accumulation.
+ * The reference's EXACT mode (k-ordered sequential F32 sums) is not offered:
+ * MI_E_UNSUPPORTED. ---- */
+enum mi_matmul_mode { MI_MATMUL_FAST = 0, MI_MATMUL_ACCURATE = 1 };
+int mi_set_matmul_mode(mi_ctx *ctx, int mode);
+int mi_get_matmul_mode(mi_ctx *ctx, int *mode);
+
 /* ---- element-wise: Engine::eltwise_op_as (server.rs:519) ----
  * `kind` is one of the MI_K_* ids below (the reference's op ids,
  * crates/tt-kernels/src/kind.rs:11-27 and sfpu/ops.rs:24-250).  `b` and `c`

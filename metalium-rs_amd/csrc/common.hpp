@@ -133,6 +133,8 @@ struct Ctx {
 
   mi_report report{};
 
+  int matmul_mode = MI_MATMUL_FAST;  // how F32 products run (mi_set_matmul_mode)
+
   // Scratch for multi-pass kernels (reductions' partials), grown on demand.
   void *scratch = nullptr;
   size_t scratch_bytes = 0;

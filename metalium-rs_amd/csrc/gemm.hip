@@ -35,6 +35,7 @@
 namespace mi {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Element types: uint16_t carries BF16 bits, float is F32.
@@ -340,6 +341,277 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
     }
     __syncthreads();
     if (more) read_frags(nxt, nxt + A_BYTES, 0, 0);
+  }
+
+  // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        if (!GUARD || (row < g.M && col < g.N)) {
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
+          else C[row * g.ldc + col] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------- F32 operands on the BF16 matrix cores
+// The fast matmul mode for F32 operands.  Each F32 element a is split as
+// a = hi + lo + e with hi = bf16(a) and lo = bf16(a - hi) (a - hi is exact,
+// |e| <= 2^-18 |a|), and a product a b is taken as hi_a hi_b + hi_a lo_b +
+// lo_a hi_b on v_mfma_f32_32x32x16_bf16, accumulated in F32; a BF16 operand
+// has no lo part (two products, error <= 2^-18 |a||b|).  Per product the error
+// is at most 3 * 2^-18 |a||b| -- far inside the reference's own fast mode
+// (TF32 operands, crates/burn-tt/src/matmul_mode.rs:1-8) -- and the matrix
+// cores run 16x the F32 rate, so 3 (2) products cost 5.3x (8x) less than
+// v_mfma_f32_32x32x2f32.  The split happens in registers between the global
+// load and the LDS write: no pass over HBM, no extra launch.
+
+__device__ __forceinline__ void split_bf16(float a, uint16_t &hi, uint16_t &lo) {
+  hi = f32_to_bf16_bits(a);
+  // A finite value above the largest BF16 would round to infinity: keep the
+  // truncated head instead (its remainder is still exact in F32).
+  if (((hi & 0x7fffu) == 0x7f80u) && ((__float_as_uint(a) & 0x7f800000u) != 0x7f800000u))
+    hi = static_cast<uint16_t>(__float_as_uint(a) >> 16);
+  const float r = a - bf16_bits_to_f32(hi);
+  lo = (r == r) ? f32_to_bf16_bits(r) : 0;  // inf - inf: the head carries it
+}
+
+// Tile loader of the split kernel: ROWS rows x 64 k of an F32 (split into hi
+// and lo planes) or BF16 (hi plane only) operand, into swizzled 128-byte LDS
+// rows.  KCONTIG: source element (r, k) at src[r * ld + k], a unit is 8
+// consecutive k of one row; otherwise at src[k * ld + r], a unit is an 8 x 8
+// block (8 k x 8 rows) transposed in registers.  A thread whose index runs
+// past the last unit idles.
+template <typename S, int ROWS, int NT, bool KCONTIG, bool GUARD>
+struct SplitLoader {
+  static constexpr bool SPLIT = sizeof(S) == 4;
+  static constexpr int UNITS = KCONTIG ? ROWS * 8 : (ROWS / 8) * 8;
+  static constexpr int NU = (UNITS + NT - 1) / NT;
+  static constexpr bool EVEN = UNITS % NT == 0;
+  static constexpr int RAW = KCONTIG ? 8 : 64;
+  static_assert(ROWS % 8 == 0, "tile rows a multiple of 8");
+  S raw[NU][RAW];
+
+  __device__ __forceinline__ void load(const S *src, int64_t ld, int64_t r0, int64_t k0, int64_t rows_total,
+                                       int64_t k_total, int tid) {
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      const int q = tid + i * NT;
+      if (!EVEN && q >= UNITS) break;
+      if constexpr (KCONTIG) {
+        const int r = q / 8, c = q % 8;
+        const int64_t gr = r0 + r, gk = k0 + c * 8;
+        const S *p = src + gr * ld + gk;
+        int valid = 8;
+        if constexpr (GUARD) {
+          valid = (gr < rows_total) ? static_cast<int>(k_total - gk) : 0;
+          valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
+        }
+        fetch(p, valid, raw[i], 0);
+      } else {
+        const int kb = q % 8, rb = q / 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t gk = k0 + kb * 8 + e, gr = r0 + rb * 8;
+          const S *p = src + gk * ld + gr;
+          int valid = 8;
+          if constexpr (GUARD) {
+            valid = (gk < k_total) ? static_cast<int>(rows_total - gr) : 0;
+            valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
+          }
+          fetch(p, valid, raw[i], 8 * e);
+        }
+      }
+    }
+  }
+
+  // Eight elements at p into raw[o .. o + 7]: vector loads when all are in
+  // range and aligned, else element by element (zero past `valid`).
+  __device__ __forceinline__ static void fetch(const S *p, int valid, S *dst, int o) {
+    if (valid == 8 && (!GUARD || (reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+      if constexpr (sizeof(S) == 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+        dst[o + 0] = a.x; dst[o + 1] = a.y; dst[o + 2] = a.z; dst[o + 3] = a.w;
+        dst[o + 4] = b.x; dst[o + 5] = b.y; dst[o + 6] = b.z; dst[o + 7] = b.w;
+      } else {
+        Chunk c;
+        c.u = *reinterpret_cast<const uint4 *>(p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[o + e] = c.h[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[o + e] = e < valid ? p[e] : S(0);
+    }
+  }
+
+  // One chunk (8 k of one row) into the hi plane, and its remainders into the
+  // lo plane for an F32 source.  The narrowing is v_cvt_pk_bf16_f32 (round to
+  // nearest even, two values an instruction); a finite value whose head
+  // would round to infinity keeps its truncated head instead.
+  __device__ __forceinline__ static void put(char *hi_plane, char *lo_plane, int r, int c, const S (&v)[8]) {
+    Chunk h, l;
+    if constexpr (SPLIT) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2 hv = {static_cast<__bf16>(v[2 * e]), static_cast<__bf16>(v[2 * e + 1])};
+        uint32_t hb = __builtin_bit_cast(uint32_t, hv);
+        // Overflow to infinity from a finite value: rare, fixed up per pair.
+        if (__builtin_expect((hb & 0x7f80u) == 0x7f80u || (hb & 0x7f800000u) == 0x7f800000u, 0)) {
+          uint16_t h0, l0, h1, l1;
+          split_bf16(v[2 * e], h0, l0);
+          split_bf16(v[2 * e + 1], h1, l1);
+          hw[e] = uint32_t(h0) | (uint32_t(h1) << 16);
+          lw[e] = uint32_t(l0) | (uint32_t(l1) << 16);
+          continue;
+        }
+        const float r0 = v[2 * e] - __uint_as_float(hb << 16);
+        const float r1 = v[2 * e + 1] - __uint_as_float(hb & 0xffff0000u);
+        const bf16x2 lv = {static_cast<__bf16>(r0), static_cast<__bf16>(r1)};
+        hw[e] = hb;
+        lw[e] = __builtin_bit_cast(uint32_t, lv);
+      }
+      h.u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      l.u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h.h[e] = v[e];
+    }
+    *reinterpret_cast<uint4 *>(hi_plane + lds_off(r, c)) = h.u;
+    if constexpr (SPLIT) *reinterpret_cast<uint4 *>(lo_plane + lds_off(r, c)) = l.u;
+  }
+
+  __device__ __forceinline__ void store(char *hi_plane, char *lo_plane, int tid) const {
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+      const int q = tid + i * NT;
+      if (!EVEN && q >= UNITS) break;
+      if constexpr (KCONTIG) {
+        S v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = raw[i][e];
+        put(hi_plane, lo_plane, q / 8, q % 8, v);
+      } else {
+        const int kb = q % 8, rb = q / 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          S v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = raw[i][8 * e + j];  // k = e of row rb * 8 + j
+          put(hi_plane, lo_plane, rb * 8 + j, kb, v);
+        }
+      }
+    }
+  }
+};
+
+template <typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD>
+__global__ void __launch_bounds__(WM *WN * 64) gemm_split_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 64;
+  constexpr bool LA = sizeof(SA) == 4, LB = sizeof(SB) == 4;  // operands with a lo plane
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile");
+  constexpr int A_PLANE = BM * 128, B_PLANE = BN * 128;
+  constexpr int A_BYTES = A_PLANE * (LA ? 2 : 1), B_BYTES = B_PLANE * (LB ? 2 : 1);
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t z = blockIdx.y;
+  const SA *A = static_cast<const SA *>(g.a) + z * g.sa;
+  const SB *B = static_cast<const SB *>(g.b) + z * g.sb;
+  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+  int64_t Kz = g.K;
+  if (g.kc > 0) {
+    const int64_t ks = static_cast<int64_t>(blockIdx.z) * g.kc;
+    Kz = g.K - ks < g.kc ? g.K - ks : g.kc;
+    A += AK ? ks : ks * g.lda;
+    B += BKC ? ks : ks * g.ldb;
+    C += static_cast<int64_t>(blockIdx.z) * g.M * g.ldc;
+  }
+
+  SplitLoader<SA, BM, NT, AK, GUARD> la;
+  SplitLoader<SB, BN, NT, BKC, GUARD> lb;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int64_t ktiles = (Kz + BK - 1) / BK;
+  la.load(A, g.lda, m0, 0, g.M, Kz, tid);
+  lb.load(B, g.ldb, n0, 0, g.N, Kz, tid);
+  la.store(smem, smem + A_PLANE, tid);
+  lb.store(smem + A_BYTES, smem + A_BYTES + B_PLANE, tid);
+  __syncthreads();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      la.load(A, g.lda, m0, (kt + 1) * BK, g.M, Kz, tid);
+      lb.load(B, g.ldb, n0, (kt + 1) * BK, g.N, Kz, tid);
+    }
+    const char *a_s = smem + cur * STAGE;
+    const char *b_s = a_s + A_BYTES;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int c = 2 * p + lhalf;
+      Chunk ah[TM], al[TM], bh[TN], bl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int off = lds_off(wm * WTM + i * 32 + lrow, c);
+        ah[i].u = *reinterpret_cast<const uint4 *>(a_s + off);
+        if constexpr (LA) al[i].u = *reinterpret_cast<const uint4 *>(a_s + A_PLANE + off);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int off = lds_off(wn * WTN + j * 32 + lrow, c);
+        bh[j].u = *reinterpret_cast<const uint4 *>(b_s + off);
+        if constexpr (LB) bl[j].u = *reinterpret_cast<const uint4 *>(b_s + B_PLANE + off);
+      }
+      // The small cross terms first, then the head product.
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (LA)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al[i].u),
+                                                                __builtin_bit_cast(bf16x8, bh[j].u), acc[i][j], 0, 0, 0);
+          if constexpr (LB)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[i].u),
+                                                                __builtin_bit_cast(bf16x8, bl[j].u), acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[i].u),
+                                                              __builtin_bit_cast(bf16x8, bh[j].u), acc[i][j], 0, 0, 0);
+        }
+    }
+    if (more) {
+      // The other stage was last read before the previous barrier.
+      char *nxt = smem + (cur ^ 1) * STAGE;
+      la.store(nxt, nxt + A_PLANE, tid);
+      lb.store(nxt + A_BYTES, nxt + A_BYTES + B_PLANE, tid);
+    }
+    __syncthreads();
   }
 
   // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
@@ -718,6 +990,7 @@ struct Plan {
   int64_t lda, ldb;   // row pitch of each operand's storage
   int64_t kc = 0;     // split-K slice length (register kernel only)
   int splits = 1;
+  bool fast = true;   // F32 operands split into BF16 parts (the fast matmul mode)
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -796,6 +1069,55 @@ static bool tiles_exactly(const Plan &p, int bm, int bn, int bk, int64_t align_e
   return true;
 }
 
+template <typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD>
+static hipError_t launch_split_cfg(const Plan &p, hipStream_t st) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int SMEM = 2 * (BM * 128 * (sizeof(SA) == 4 ? 2 : 1) + BN * 128 * (sizeof(SB) == 4 ? 2 : 1));
+  auto kern = gemm_split_kernel<SA, SB, TO, BM, BN, WM, WN, AK, BKC, GUARD>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  GemmArgs g;
+  g.a = p.a; g.b = p.b; g.c = p.c;
+  g.M = p.M; g.N = p.N; g.K = p.K;
+  g.lda = p.lda;
+  g.ldb = p.ldb;
+  g.ldc = p.N;
+  g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.kc = p.kc;
+  g.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
+  g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
+  dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch),
+            static_cast<unsigned>(p.splits));
+  kern<<<grid, NT, SMEM, st>>>(g);
+  return hipGetLastError();
+}
+
+template <typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool GUARD>
+static hipError_t launch_split_orient(const Plan &p, hipStream_t st) {
+  const bool ak = !p.ta, bk = p.tb;
+  if (ak && bk) return launch_split_cfg<SA, SB, TO, BM, BN, WM, WN, true, true, GUARD>(p, st);
+  if (ak && !bk) return launch_split_cfg<SA, SB, TO, BM, BN, WM, WN, true, false, GUARD>(p, st);
+  if (!ak && bk) return launch_split_cfg<SA, SB, TO, BM, BN, WM, WN, false, true, GUARD>(p, st);
+  return launch_split_cfg<SA, SB, TO, BM, BN, WM, WN, false, false, GUARD>(p, st);
+}
+
+// F32 (or mixed) operands in the fast mode: the split kernel, 128 x 128 tiles
+// when they give at least half the CUs a tile, else 64 x 64.
+template <typename SA, typename SB, typename TO>
+static hipError_t run_split(const Plan &p, hipStream_t st) {
+  const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
+  if (tiles128 >= 128) {
+    if (tiles_exactly(p, 128, 128, 64, 8)) return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, false>(p, st);
+    return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, true>(p, st);
+  }
+  if (tiles_exactly(p, 64, 64, 64, 8)) return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, false>(p, st);
+  return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, true>(p, st);
+}
+
 template <typename TO>
 static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   using T = uint16_t;
@@ -829,6 +1151,20 @@ static hipError_t run_plan(const Plan &p, hipStream_t st) {
   const bool bf = p.eo == MI_BF16;
   if (p.ea == MI_BF16 && p.eb == MI_BF16)
     return bf ? run_bf16<uint16_t>(p, st) : run_bf16<float>(p, st);
+  // The fast mode splits F32 operands where the product is large enough to be
+  // bound by the matrix cores (at least 2^33 multiply-adds over at least 128
+  // tiles of 128 x 128): below that the kernels are bound by load latency and
+  // the split's conversions only add work, so the F32 kernel runs (more
+  // accurate, and faster there).
+  const bool split_pays =
+      p.M * p.N * p.K * p.batch >= (int64_t(1) << 33) && ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch >= 128;
+  if (p.fast && split_pays) {
+    if (p.ea == MI_F32 && p.eb == MI_F32)
+      return bf ? run_split<float, float, uint16_t>(p, st) : run_split<float, float, float>(p, st);
+    if (p.ea == MI_F32)
+      return bf ? run_split<float, uint16_t, uint16_t>(p, st) : run_split<float, uint16_t, float>(p, st);
+    return bf ? run_split<uint16_t, float, uint16_t>(p, st) : run_split<uint16_t, float, float>(p, st);
+  }
   if (p.ea == MI_F32 && p.eb == MI_F32)
     return bf ? run_f32<float, float, uint16_t>(p, st) : run_f32<float, float, float>(p, st);
   if (p.ea == MI_F32 && p.eb == MI_BF16)
@@ -943,6 +1279,7 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "matmul result kind %s", elem_name(out_elem));
   Plan p;
   p.ta = ta != 0; p.tb = tb != 0;
+  p.fast = ctx->matmul_mode == MI_MATMUL_FAST;
   p.ea = A->elem; p.eb = B->elem; p.eo = out_elem;
   p.a = A->ptr; p.b = B->ptr;
   if (mode == 0) {
@@ -1024,6 +1361,22 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
 extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out);
+}
+
+extern "C" int mi_set_matmul_mode(mi_ctx *ctx, int mode) {
+  MI_ENTER(ctx);
+  if (mode != MI_MATMUL_FAST && mode != MI_MATMUL_ACCURATE)
+    return fail(ctx, MI_E_UNSUPPORTED, "matmul mode %d (fast %d, accurate %d)", mode, MI_MATMUL_FAST,
+                MI_MATMUL_ACCURATE);
+  ctx->matmul_mode = mode;
+  return MI_OK;
+}
+
+extern "C" int mi_get_matmul_mode(mi_ctx *ctx, int *mode) {
+  MI_ENTER(ctx);
+  if (!mode) return fail(ctx, MI_E_ARG, "null out pointer");
+  *mode = ctx->matmul_mode;
+  return MI_OK;
 }
 
 extern "C" int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int64_t batch,

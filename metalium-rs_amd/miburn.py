@@ -29,6 +29,7 @@ F32, I32, BOOL, BF16 = 0, 1, 2, 3
 _NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}
 
 AXIS_ROWS, AXIS_COLS = 0, 1
+MATMUL_FAST, MATMUL_ACCURATE = 0, 1
 R_SUM, R_MAX, R_MEAN, R_MIN = 0, 1, 2, 3
 DRAW_UNIT, DRAW_UNIFORM, DRAW_NORMAL, DRAW_BERNOULLI, DRAW_INT_RANGE = 0, 1, 2, 3, 4
 
@@ -112,6 +113,8 @@ def _load() -> ctypes.CDLL:
         "mi_softmax_backward": [P, U64, U64, c_float, Ip],
         "mi_sgd_update": [P, I64, ctypes.POINTER(U64), ctypes.POINTER(U64), c_float],
         "mi_argmax_rows": [P, U64, Ip],
+        "mi_set_matmul_mode": [P, c_int],
+        "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_pick_columns": [P, U64, U64, Ip],
         "mi_scatter_add_columns": [P, U64, U64, U64, Ip],
@@ -322,6 +325,15 @@ class Engine:
 
     def softmax_backward(self, p: int, dp: int, scale: float = 1.0) -> int:
         return self._out(self._lib.mi_softmax_backward, p, dp, scale)
+
+    def set_matmul_mode(self, mode: int) -> None:
+        """MATMUL_FAST (F32 operands split into BF16 parts) or MATMUL_ACCURATE (F32 matrix cores)."""
+        self._check(self._lib.mi_set_matmul_mode(self.ctx, mode))
+
+    def matmul_mode(self) -> int:
+        m = ctypes.c_int()
+        self._check(self._lib.mi_get_matmul_mode(self.ctx, ctypes.byref(m)))
+        return m.value
 
     def argmax_row(self, a: int) -> int:
         return self._out(self._lib.mi_argmax_rows, a)

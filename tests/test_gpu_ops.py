@@ -337,17 +337,36 @@ def mm_tol(a, b, ta, tb, rel):
     return rel * (aa @ bb)
 
 
+@pytest.fixture(params=["fast", "accurate"])
+def mode(request, engine):
+    """Run the test in each matmul mode, restoring the default after."""
+    engine.set_matmul_mode(miburn.MATMUL_FAST if request.param == "fast" else miburn.MATMUL_ACCURATE)
+    yield request.param
+    engine.set_matmul_mode(miburn.MATMUL_FAST)
+
+
+def test_matmul_mode_api(engine):
+    assert engine.matmul_mode() == miburn.MATMUL_FAST  # the reference's default is its fast mode
+    engine.set_matmul_mode(miburn.MATMUL_ACCURATE)
+    assert engine.matmul_mode() == miburn.MATMUL_ACCURATE
+    with pytest.raises(miburn.MiError) as e:
+        engine.set_matmul_mode(2)  # an exact (k-ordered) mode is not offered
+    assert e.value.kind == "UNSUPPORTED"
+    engine.set_matmul_mode(miburn.MATMUL_FAST)
+
+
 @pytest.mark.parametrize("ta", [False, True])
 @pytest.mark.parametrize("tb", [False, True])
 @pytest.mark.parametrize("mnk", [(64, 128, 784), (64, 10, 128), (100, 70, 33), (256, 256, 256), (1, 576, 1536),
-                                 (513, 129, 77)])
-def test_matmul_f32(engine, ta, tb, mnk):
+                                 (513, 129, 77), (2048, 256, 256), (1024, 1024, 64), (2048, 2048, 2048),
+                                 (2000, 2100, 2050)])
+def test_matmul_f32(engine, mode, ta, tb, mnk):
     m, n, k = mnk
     a = rnd(k, m) if ta else rnd(m, k)
     b = rnd(n, k) if tb else rnd(k, n)
     ia, ib = engine.upload(a), engine.upload(b)
     got = engine.download(engine.matmul_dram(ia, ta, ib, tb))
-    want = orc.matmul(a, b, ta, tb)
+    want = orc.matmul(a, b, ta, tb, threads=16)
     assert got.shape == (m, n)
     assert np.all(np.abs(got - want) <= mm_tol(a, b, ta, tb, 1e-5) + 1e-30)
 
@@ -381,15 +400,36 @@ def test_matmul_bf16_out(engine):
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + mm_tol(af, bf, False, False, 1e-5))
 
 
-def test_matmul_mixed_f32_bf16(engine):
-    a, b = rnd(64, 96), orc.to_bf16(rnd(96, 48))
-    got = engine.download(engine.matmul_dram(engine.upload(a), False, engine.upload_bf16(b), False))
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("mnk", [(64, 48, 96), (512, 576, 576), (300, 200, 136), (2048, 2048, 2048)])
+def test_matmul_mixed_f32_bf16(engine, mode, tb, mnk):
+    m, n, k = mnk
+    a, b = rnd(m, k), orc.to_bf16(rnd(n, k) if tb else rnd(k, n))
+    got = engine.download(engine.matmul_dram(engine.upload(a), False, engine.upload_bf16(b), tb))
     bf = orc.from_bf16(b)
-    assert np.all(np.abs(got - orc.matmul(a, bf)) <= mm_tol(a, bf, False, False, 1e-5) + 1e-30)
+    assert np.all(np.abs(got - orc.matmul(a, bf, False, tb, threads=16)) <= mm_tol(a, bf, False, tb, 1e-5) + 1e-30)
 
 
-@pytest.mark.parametrize("dtype,n", [("f32", 1024), ("bf16", 1024), ("bf16", 2048), ("bf16", 4096)])
-def test_matmul_integer_exact_big(engine, dtype, n):
+def test_matmul_fast_split_keeps_large_finite_values(engine, mode):
+    """Values near FLT_MAX stay finite through the split (the BF16 head of a
+    value above the largest BF16 would round to infinity, so it is truncated).
+    Its remainder is then up to 2^-8 |a|: the split's error reaches 2^-17 |a|
+    and the dropped lo x lo term 2^-17 |a||b|, hence the looser bound for this
+    case (measured 2.4e-5).  2048^3 takes the split."""
+    a = rnd(2048, 2048)
+    a[3, 5] = np.float32(3.4e38)
+    a[7, 1] = np.float32(-3.39e38)
+    b = (rnd(2048, 2048) * np.float32(1e-3)).astype(np.float32)
+    got = engine.download(engine.matmul_dram(engine.upload(a), False, engine.upload(b), False))
+    want = orc.matmul(a, b, threads=16)
+    assert np.all(np.isfinite(got))
+    ratio = np.abs(got - want) / (mm_tol(a, b, False, False, 1.0) + 1e-30)
+    worst = np.unravel_index(np.argmax(ratio), ratio.shape)
+    assert ratio.max() <= 5e-5, (ratio.max(), worst, got[worst], want[worst])
+
+
+@pytest.mark.parametrize("dtype,n", [("f32", 1024), ("f32", 2048), ("bf16", 1024), ("bf16", 2048), ("bf16", 4096)])
+def test_matmul_integer_exact_big(engine, mode, dtype, n):
     """The reference's step11 trick: small-integer operands make every
     summation order exact, so the device must equal the float64 product bit
     for bit -- for each kernel the shape selects (bf16: 64x64 tiles at 1024,
