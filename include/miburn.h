@@ -326,6 +326,28 @@ int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);
 
+/* ---- traces: Engine::begin_trace / end_trace / run_trace /
+ * run_generic_trace / release_trace (server.rs:591-660, 746), the reference's
+ * TracedTrainingStep (crates/burn-tt/src/trace.rs:989-1010), as HIP graphs
+ * captured from the context's stream.  Between begin and end, ops are
+ * recorded, not run; host transfers, waits and event timing are refused
+ * (MI_E_UNSUPPORTED), as is an embedding backward of more than 8192 indices.
+ * Memory a capture allocates or frees stays reserved for the trace until it
+ * is released, so replays never touch memory handed to other work; buffers
+ * the trace reads that existed before the capture must outlive it.  A replay
+ * overwrites each input buffer with the host bytes given (its whole size),
+ * launches the graph and reads each output buffer back whole. ---- */
+int mi_trace_begin(mi_ctx *ctx);
+int mi_trace_end(mi_ctx *ctx, uint64_t *trace);
+int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs,
+                 const mi_id *inputs, const void *const *values,
+                 int64_t n_outputs, const mi_id *outputs,
+                 void *const *out_values);
+int mi_trace_release(mi_ctx *ctx, uint64_t trace);
+/* Engine::copy_into (server.rs:742): src's bytes into dst (equal byte size),
+ * no allocation. */
+int mi_copy_into(mi_ctx *ctx, mi_id src, mi_id dst);
+
 /* ---- random: Engine::random_dram (server.rs:768) with the draw's 64-bit
  * base (crates/burn-tt/src/random.rs:42-56) ---- */
 enum mi_draw {

@@ -98,6 +98,7 @@ struct Buffer {
   size_t bytes = 0;  // bytes the allocator handed out (>= datum bytes)
   int64_t rows = 0, cols = 0;
   int elem = MI_F32;
+  uint64_t trace = 0;  // the trace whose capture allocated it (its memory is the trace's until released)
   int64_t numel() const { return rows * cols; }
 };
 
@@ -135,6 +136,20 @@ struct Ctx {
 
   int matmul_mode = MI_MATMUL_FAST;  // how F32 products run (mi_set_matmul_mode)
 
+  // Traces (HIP graphs captured from the stream).  Memory a capture's kernels
+  // touch must not be handed to other work while the trace can replay: the
+  // buffers a capture allocates go back to the trace, not to the allocator,
+  // when freed, and scratch that grows while any trace lives is retired, not
+  // freed.
+  struct Trace {
+    hipGraphExec_t exec = nullptr;
+    std::vector<std::pair<void *, size_t>> held;
+  };
+  std::map<uint64_t, Trace> traces;
+  bool capturing = false;
+  uint64_t capture_id = 0, next_trace = 1;
+  std::vector<void *> retired_scratch;
+
   // Scratch for multi-pass kernels (reductions' partials), grown on demand.
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -154,6 +169,12 @@ int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id,
 void *device_alloc(Ctx *ctx, size_t bytes, size_t *got);
 void device_release(Ctx *ctx, void *p, size_t bytes);
 void *scratch(Ctx *ctx, size_t bytes);
+// Zero `bytes` (a multiple of 2) at p with a kernel: safe inside a captured
+// trace, where a memset node is not.
+int fill_zero(Ctx *ctx, void *p, size_t bytes);
+// MI_E_UNSUPPORTED if a trace is being captured (host transfers and waits
+// cannot be part of one).
+int refuse_if_capturing(Ctx *ctx, const char *what);
 
 // Kernel-side flag word for the context.
 inline uint32_t *flags(Ctx *ctx) { return ctx->dev_flags; }

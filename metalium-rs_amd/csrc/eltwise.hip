@@ -390,6 +390,18 @@ __global__ void fill16(uint16_t *p, int64_t n, uint16_t bits) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = bits;
 }
+
+int fill_zero(Ctx *ctx, void *p, size_t bytes) {
+  if (bytes == 0) return MI_OK;
+  if (bytes % 4 == 0) {
+    const int64_t n = static_cast<int64_t>(bytes / 4);
+    fill32<<<grid_for(n, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(static_cast<uint32_t *>(p), n, 0u);
+  } else {
+    const int64_t n = static_cast<int64_t>(bytes / 2);
+    fill16<<<grid_for(n, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(static_cast<uint16_t *>(p), n, uint16_t(0));
+  }
+  return check_launch(ctx, "fill");
+}
 }  // namespace mi
 
 extern "C" int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits, mi_id *out) {

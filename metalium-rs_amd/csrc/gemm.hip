@@ -1335,7 +1335,7 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   if (p.M > 0 && p.N > 0) {
     hipError_t e = hipSuccess;
     if (p.K == 0) {
-      e = hipMemsetAsync(cb->ptr, 0, p.batch * p.M * p.N * elem_size(out_elem), ctx->stream);
+      if (fill_zero(ctx, cb->ptr, p.batch * p.M * p.N * elem_size(out_elem))) e = hipErrorLaunchFailure;
     } else if (gemv_fits(p)) {
       launch_gemv(p, ctx->stream);
       e = hipGetLastError();

@@ -105,6 +105,42 @@ __global__ void __launch_bounds__(256) select_add_segments(float *out, int64_t v
   }
 }
 
+// Up to SORT_BLOCK_MAX indices: one block sorts the (index, position) pairs
+// in LDS with a bitonic network -- as 64-bit keys (index bits above position
+// bits), so equal indices keep position order and negative (invalid) indices
+// group above every valid one.  No library sort and no memset: the path a
+// captured trace can hold.
+constexpr int SORT_BLOCK_MAX = 8192;
+
+__global__ void __launch_bounds__(1024) sort_pairs_block(const int32_t *idx, int64_t n, int32_t *keys_out,
+                                                         int32_t *pos_out) {
+  __shared__ uint64_t k[SORT_BLOCK_MAX];
+  int np = 1;
+  while (np < n) np <<= 1;
+  for (int i = threadIdx.x; i < np; i += 1024)
+    k[i] = i < n ? (static_cast<uint64_t>(static_cast<uint32_t>(idx[i])) << 32) | static_cast<uint32_t>(i) : ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < np / 2; t += 1024) {
+        const int lo = 2 * t - (t & (stride - 1));  // first element of the pair
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = k[lo], b = k[hi];
+        if ((a > b) == up) {
+          k[lo] = b;
+          k[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    keys_out[i] = static_cast<int32_t>(k[i] >> 32);
+    pos_out[i] = static_cast<int32_t>(k[i] & 0xffffffffu);
+  }
+}
+
 // --------------------------------------------------------------- argmax
 struct ArgBest { float v; int32_t i; };
 __device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
@@ -317,7 +353,22 @@ extern "C" int mi_select_add_rows(mi_ctx *ctx, mi_id t, mi_id idx, mi_id value, 
   int s = new_buffer(ctx, V, D, MI_F32, &id, &ob);
   if (s) return s;
   if (V * D > 0) (void)hipMemcpyAsync(ob->ptr, tp, V * D * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
-  if (n > 0 && D > 0) {
+  if (n > 0 && D > 0 && n <= SORT_BLOCK_MAX) {
+    const size_t arr = (static_cast<size_t>(n) * 4 + 255) & ~size_t(255);
+    char *sc = static_cast<char *>(scratch(ctx, 2 * arr));
+    if (!sc) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "select_add_rows scratch"); }
+    int32_t *keys_out = reinterpret_cast<int32_t *>(sc);
+    int32_t *pos_out = reinterpret_cast<int32_t *>(sc + arr);
+    sort_pairs_block<<<1, 1024, 0, ctx->stream>>>(ip, n, keys_out, pos_out);
+    select_add_segments<<<grid_for(n, 4, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<float *>(ob->ptr), V, D, keys_out,
+                                                                           pos_out, n, vp, flags(ctx));
+  } else if (n > 0 && D > 0) {
+    // The library radix sort clears its counters with memsets, which a
+    // captured trace cannot replay correctly.
+    if (int r = refuse_if_capturing(ctx, "select_add_rows of more than 8192 indices")) {
+      mi_free(ctx, id);
+      return r;
+    }
     const int ni = static_cast<int>(n);
     size_t temp_bytes = 0;
     (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, static_cast<const int32_t *>(nullptr),

@@ -512,7 +512,7 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
   float *o = static_cast<float *>(ob->ptr);
   if (axis == MI_AXIS_COLS) {
     if (R > 0) {
-      if (C == 0) (void)hipMemsetAsync(o, 0, R * sizeof(float), ctx->stream);
+      if (C == 0) fill_zero(ctx, o, R * sizeof(float));
       else if (R * C * 4 >= kStreamBytes)
         reduce_cols_kernel<true><<<grid_for(R, 4, INT32_MAX), 256, 0, ctx->stream>>>(xp, xe, o, R, C, op);
       else
@@ -520,7 +520,7 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
     }
   } else if (C > 0) {
     if (R == 0) {
-      (void)hipMemsetAsync(o, 0, C * sizeof(float), ctx->stream);
+      fill_zero(ctx, o, C * sizeof(float));
     } else {
       const bool vec = (xe == MI_F32) && (C % 4 == 0);
       const bool wide = vec && C >= 1024;
@@ -845,8 +845,8 @@ extern "C" int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id d
   s = new_buffer(ctx, 1, C, MI_F32, &ids[2], &bb);
   if (s) { mi_free(ctx, ids[0]); mi_free(ctx, ids[1]); return s; }
   if (R == 0) {
-    (void)hipMemsetAsync(bg->ptr, 0, C * sizeof(float), ctx->stream);
-    (void)hipMemsetAsync(bb->ptr, 0, C * sizeof(float), ctx->stream);
+    fill_zero(ctx, bg->ptr, C * sizeof(float));
+    fill_zero(ctx, bb->ptr, C * sizeof(float));
   } else {
     const float *xp = static_cast<const float *>(xb->ptr), *dp = static_cast<const float *>(db->ptr);
     const float *gp = gb ? static_cast<const float *>(gb->ptr) : nullptr;

@@ -77,6 +77,10 @@ void *device_alloc(Ctx *ctx, size_t bytes, size_t *got) {
   }
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess && ctx->capturing) {
+    (void)hipGetLastError();  // no wait is possible inside a capture
+    return nullptr;
+  }
   if (e != hipSuccess) {
     // Give the cache back to the device and try once more.
     (void)hipGetLastError();
@@ -103,6 +107,7 @@ int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id, Buffer
   if (!elem_valid(elem)) return fail(ctx, MI_E_ARG, "unknown element kind %d", elem);
   Buffer b;
   b.rows = rows; b.cols = cols; b.elem = elem;
+  b.trace = ctx->capturing ? ctx->capture_id : 0;
   size_t want = static_cast<size_t>(rows) * static_cast<size_t>(cols) * elem_size(elem);
   b.ptr = device_alloc(ctx, want, &b.bytes);
   if (!b.ptr) return fail(ctx, MI_E_OOM, "device allocation of %zu bytes failed", want);
@@ -114,9 +119,14 @@ int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id, Buffer
 void *scratch(Ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return ctx->scratch;
   if (ctx->scratch) {
-    // Earlier work on the stream may still read the old scratch.
-    hipStreamSynchronize(ctx->stream);
-    hipFree(ctx->scratch);
+    if (ctx->capturing || !ctx->traces.empty()) {
+      // A trace may replay kernels that use it: keep it until the context ends.
+      ctx->retired_scratch.push_back(ctx->scratch);
+    } else {
+      // Earlier work on the stream may still read the old scratch.
+      hipStreamSynchronize(ctx->stream);
+      hipFree(ctx->scratch);
+    }
   }
   size_t sz = round_size(bytes);
   if (hipMalloc(&ctx->scratch, sz) != hipSuccess) {
@@ -137,6 +147,11 @@ static int stage_slot(Ctx *ctx) {
     ctx->stage_pending[s] = false;
   }
   return s;
+}
+
+int refuse_if_capturing(Ctx *ctx, const char *what) {
+  if (!ctx->capturing) return MI_OK;
+  return fail(ctx, MI_E_UNSUPPORTED, "%s while a trace is being captured", what);
 }
 
 // Collect the device flags and stream errors into the sticky status.
@@ -218,6 +233,18 @@ int mi_ctx_destroy(mi_ctx *ctx) {
     for (auto &kv : ctx->free_blocks)
       for (void *p : kv.second) hipFree(p);
     ctx->free_blocks.clear();
+    if (ctx->capturing) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(ctx->stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      (void)hipGetLastError();
+    }
+    for (auto &kv : ctx->traces) {
+      if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+      for (auto &h : kv.second.held) (void)hipFree(h.first);
+    }
+    ctx->traces.clear();
+    for (void *p : ctx->retired_scratch) (void)hipFree(p);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->dev_flags) hipFree(ctx->dev_flags);
     for (int i = 0; i < Ctx::kStageSlots; ++i) {
@@ -238,6 +265,7 @@ const char *mi_last_error(const mi_ctx *ctx) {
 
 int mi_sync(mi_ctx *ctx) {
   MI_ENTER(ctx);
+  if (int r = refuse_if_capturing(ctx, "sync")) return r;
   collect(ctx);
   return take_sticky(ctx);
 }
@@ -249,13 +277,8 @@ int mi_stream(mi_ctx *ctx, void **stream) {
   return MI_OK;
 }
 
-static int upload_raw(mi_ctx *ctx, const void *src, int64_t rows, int64_t cols, int elem, mi_id *out) {
-  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
-  if (!src && rows * cols > 0) return fail(ctx, MI_E_ARG, "null host pointer");
-  mi_id id; Buffer *b;
-  int s = new_buffer(ctx, rows, cols, elem, &id, &b);
-  if (s) return s;
-  size_t bytes = static_cast<size_t>(rows * cols) * elem_size(elem);
+// Host bytes into an existing buffer through the pinned staging ring.
+static int write_into(mi_ctx *ctx, Buffer *b, const void *src, size_t bytes) {
   const char *p = static_cast<const char *>(src);
   char *d = static_cast<char *>(b->ptr);
   for (size_t off = 0; off < bytes; off += Ctx::kStageBytes) {
@@ -269,6 +292,21 @@ static int upload_raw(mi_ctx *ctx, const void *src, int64_t rows, int64_t cols, 
   }
   ctx->report.uploads++;
   ctx->report.bytes_up += bytes;
+  return MI_OK;
+}
+
+static int upload_raw(mi_ctx *ctx, const void *src, int64_t rows, int64_t cols, int elem, mi_id *out) {
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  if (!src && rows * cols > 0) return fail(ctx, MI_E_ARG, "null host pointer");
+  if (int r = refuse_if_capturing(ctx, "upload")) return r;
+  mi_id id; Buffer *b;
+  int s = new_buffer(ctx, rows, cols, elem, &id, &b);
+  if (s) return s;
+  s = write_into(ctx, b, src, static_cast<size_t>(rows * cols) * elem_size(elem));
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
   *out = id;
   return MI_OK;
 }
@@ -290,6 +328,7 @@ int mi_upload_bf16(mi_ctx *ctx, const uint16_t *bits, int64_t rows, int64_t cols
 }
 
 static int download_raw(mi_ctx *ctx, mi_id id, void *dst, int64_t n, int want_elem_size, const char *what) {
+  if (int r = refuse_if_capturing(ctx, what)) return r;
   MI_BUF(ctx, b, id);
   if (static_cast<int>(elem_size(b->elem)) != want_elem_size)
     return fail(ctx, MI_E_ARG, "%s of a %s buffer", what, elem_name(b->elem));
@@ -335,7 +374,14 @@ int mi_free(mi_ctx *ctx, mi_id id) {
   auto it = ctx->bufs.find(id);
   if (it == ctx->bufs.end()) return fail(ctx, MI_E_ID, "free of unknown buffer id %llu", (unsigned long long)id);
   ctx->live_bytes -= it->second.bytes;
-  device_release(ctx, it->second.ptr, it->second.bytes);
+  // While capturing, any freed memory may be referenced by the capture's
+  // kernels: it is the capture's until the trace is released.
+  const uint64_t owner = ctx->capturing ? ctx->capture_id : it->second.trace;
+  auto tr = owner ? ctx->traces.find(owner) : ctx->traces.end();
+  if (tr != ctx->traces.end())
+    tr->second.held.emplace_back(it->second.ptr, it->second.bytes);  // the trace's until released
+  else
+    device_release(ctx, it->second.ptr, it->second.bytes);
   ctx->bufs.erase(it);
   return MI_OK;
 }
@@ -362,6 +408,7 @@ int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols) {
 
 int mi_event_record(mi_ctx *ctx, int slot) {
   MI_ENTER(ctx);
+  if (int r = refuse_if_capturing(ctx, "event record")) return r;
   if (slot < 0 || slot >= 16) return fail(ctx, MI_E_ARG, "event slot %d", slot);
   hipError_t e = hipEventRecord(ctx->events[slot], ctx->stream);
   return e == hipSuccess ? MI_OK : fail(ctx, MI_E_HIP, "event record: %s", hipGetErrorString(e));
@@ -369,10 +416,99 @@ int mi_event_record(mi_ctx *ctx, int slot) {
 
 int mi_event_elapsed_ms(mi_ctx *ctx, int from, int to, float *ms) {
   MI_ENTER(ctx);
+  if (int r = refuse_if_capturing(ctx, "event wait")) return r;
   if (from < 0 || from >= 16 || to < 0 || to >= 16 || !ms) return fail(ctx, MI_E_ARG, "event slots %d %d", from, to);
   hipError_t e = hipEventSynchronize(ctx->events[to]);
   if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->events[from], ctx->events[to]);
   return e == hipSuccess ? MI_OK : fail(ctx, MI_E_HIP, "event elapsed: %s", hipGetErrorString(e));
+}
+
+int mi_copy_into(mi_ctx *ctx, mi_id src, mi_id dst) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, sb, src);
+  MI_BUF(ctx, db, dst);
+  const size_t n = static_cast<size_t>(sb->numel()) * elem_size(sb->elem);
+  if (n != static_cast<size_t>(db->numel()) * elem_size(db->elem))
+    return fail(ctx, MI_E_ARG, "copy_into: %zu bytes into %zu", n, static_cast<size_t>(db->numel()) * elem_size(db->elem));
+  if (n > 0 && sb->ptr != db->ptr) {
+    hipError_t e = hipMemcpyAsync(db->ptr, sb->ptr, n, hipMemcpyDeviceToDevice, ctx->stream);
+    if (e != hipSuccess) return fail(ctx, MI_E_HIP, "copy_into: %s", hipGetErrorString(e));
+  }
+  return MI_OK;
+}
+
+int mi_trace_begin(mi_ctx *ctx) {
+  MI_ENTER(ctx);
+  if (ctx->capturing) return fail(ctx, MI_E_ARG, "a trace is already being captured");
+  // Earlier asynchronous failures surface before the capture starts.
+  collect(ctx);
+  if (int s = take_sticky(ctx)) return s;
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) return fail(ctx, MI_E_HIP, "begin capture: %s", hipGetErrorString(e));
+  ctx->capture_id = ctx->next_trace++;
+  ctx->traces[ctx->capture_id] = Ctx::Trace{};
+  ctx->capturing = true;
+  return MI_OK;
+}
+
+int mi_trace_end(mi_ctx *ctx, uint64_t *trace) {
+  MI_ENTER(ctx);
+  if (!ctx->capturing) return fail(ctx, MI_E_ARG, "no trace is being captured");
+  ctx->capturing = false;
+  const uint64_t id = ctx->capture_id;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+  hipGraphExec_t exec = nullptr;
+  if (e == hipSuccess) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    mi_trace_release(ctx, id);
+    return fail(ctx, MI_E_HIP, "end capture: %s", hipGetErrorString(e));
+  }
+  ctx->traces[id].exec = exec;
+  if (trace) *trace = id;
+  return MI_OK;
+}
+
+int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs, const mi_id *inputs, const void *const *values,
+                 int64_t n_outputs, const mi_id *outputs, void *const *out_values) {
+  MI_ENTER(ctx);
+  if (int r = refuse_if_capturing(ctx, "trace replay")) return r;
+  auto it = ctx->traces.find(trace);
+  if (it == ctx->traces.end() || !it->second.exec) return fail(ctx, MI_E_ID, "unknown trace %llu", (unsigned long long)trace);
+  if (n_inputs < 0 || n_outputs < 0 || (n_inputs && (!inputs || !values)) || (n_outputs && (!outputs || !out_values)))
+    return fail(ctx, MI_E_ARG, "trace_run: input or output lists");
+  for (int64_t i = 0; i < n_inputs; ++i) {
+    MI_BUF(ctx, b, inputs[i]);
+    if (!values[i]) return fail(ctx, MI_E_ARG, "trace_run: null values for input %lld", (long long)i);
+    if (int s = write_into(ctx, b, values[i], static_cast<size_t>(b->numel()) * elem_size(b->elem))) return s;
+  }
+  hipError_t e = hipGraphLaunch(it->second.exec, ctx->stream);
+  if (e != hipSuccess) return fail(ctx, MI_E_HIP, "trace launch: %s", hipGetErrorString(e));
+  ctx->report.ops++;
+  for (int64_t i = 0; i < n_outputs; ++i) {
+    MI_BUF(ctx, b, outputs[i]);
+    if (int s = download_raw(ctx, outputs[i], out_values[i], b->numel(), static_cast<int>(elem_size(b->elem)),
+                             "trace output"))
+      return s;
+  }
+  return MI_OK;
+}
+
+int mi_trace_release(mi_ctx *ctx, uint64_t trace) {
+  MI_ENTER(ctx);
+  auto it = ctx->traces.find(trace);
+  if (it == ctx->traces.end()) return fail(ctx, MI_E_ID, "unknown trace %llu", (unsigned long long)trace);
+  if (ctx->capturing && ctx->capture_id == trace) return fail(ctx, MI_E_ARG, "the trace is still being captured");
+  // A replay may still be running: wait, then hand the memory back.
+  hipStreamSynchronize(ctx->stream);
+  if (it->second.exec) (void)hipGraphExecDestroy(it->second.exec);
+  for (auto &h : it->second.held) device_release(ctx, h.first, h.second);
+  ctx->traces.erase(it);
+  for (auto &kv : ctx->bufs)
+    if (kv.second.trace == trace) kv.second.trace = 0;
+  return MI_OK;
 }
 
 int mi_get_report(mi_ctx *ctx, mi_report *out) {

@@ -114,6 +114,12 @@ def _load() -> ctypes.CDLL:
         "mi_sgd_update": [P, I64, ctypes.POINTER(U64), ctypes.POINTER(U64), c_float],
         "mi_argmax_rows": [P, U64, Ip],
         "mi_set_matmul_mode": [P, c_int],
+        "mi_trace_begin": [P],
+        "mi_trace_end": [P, ctypes.POINTER(U64)],
+        "mi_trace_run": [P, U64, I64, ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p), I64,
+                         ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p)],
+        "mi_trace_release": [P, U64],
+        "mi_copy_into": [P, U64, U64],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_pick_columns": [P, U64, U64, Ip],
@@ -325,6 +331,38 @@ class Engine:
 
     def softmax_backward(self, p: int, dp: int, scale: float = 1.0) -> int:
         return self._out(self._lib.mi_softmax_backward, p, dp, scale)
+
+    # -- traces (server.rs:591-660) ---------------------------------------
+    def begin_trace(self) -> None:
+        self._check(self._lib.mi_trace_begin(self.ctx))
+
+    def end_trace(self) -> int:
+        t = ctypes.c_uint64()
+        self._check(self._lib.mi_trace_end(self.ctx, ctypes.byref(t)))
+        return t.value
+
+    def run_trace(self, trace: int, inputs=None, outputs=()):
+        """Overwrite each input id with its array's bytes, replay, and return
+        the outputs' contents (arrays of each buffer's kind and shape)."""
+        inputs = inputs or {}
+        keep = [np.ascontiguousarray(v) for v in inputs.values()]
+        ids_in = (ctypes.c_uint64 * max(len(keep), 1))(*inputs.keys())
+        vals_in = (ctypes.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
+        outs = []
+        for o in outputs:
+            r, c, e = self.metadata(o)
+            dt = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}[e]
+            outs.append(np.empty((r, c), dt))
+        ids_out = (ctypes.c_uint64 * max(len(outs), 1))(*outputs)
+        vals_out = (ctypes.c_void_p * max(len(outs), 1))(*[a.ctypes.data for a in outs])
+        self._check(self._lib.mi_trace_run(self.ctx, trace, len(keep), ids_in, vals_in, len(outs), ids_out, vals_out))
+        return outs
+
+    def release_trace(self, trace: int) -> None:
+        self._check(self._lib.mi_trace_release(self.ctx, trace))
+
+    def copy_into(self, src: int, dst: int) -> None:
+        self._check(self._lib.mi_copy_into(self.ctx, src, dst))
 
     def set_matmul_mode(self, mode: int) -> None:
         """MATMUL_FAST (F32 operands split into BF16 parts) or MATMUL_ACCURATE (F32 matrix cores)."""
@@ -555,6 +593,12 @@ class Mlp:
             self.eng.free(i)
         return loss
 
+    def train_step_ids(self, x: int, labels: int, lr: float) -> int:
+        """One step on resident x / label ids; returns the loss id."""
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_mlp_train_step(self.h, x, labels, lr, ctypes.byref(out)))
+        return out.value
+
     def train_synthetic(self, batch: int, steps: int, lr: float, data_seed: int = 0):
         losses = np.zeros(steps, np.float32)
         ms = ctypes.c_double()
@@ -636,6 +680,13 @@ class Transformer:
         for i in (ti, yi, out.value):
             self.eng.free(i)
         return loss
+
+    def train_step_ids(self, tokens: int, targets: int, batch: int, seq: int, lr: float) -> int:
+        """One step on resident token / target ids; returns the loss id (the
+        form a captured trace records)."""
+        out = ctypes.c_uint64()
+        self._check(self.L.mi_transformer_train_step(self.h, tokens, targets, batch, seq, lr, ctypes.byref(out)))
+        return out.value
 
     def train_synthetic(self, batch: int, seq: int, steps: int, lr: float, data_seed: int = 0):
         losses = np.zeros(steps, np.float32)
