@@ -170,15 +170,52 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128) -> dict:
             "decode_tokens_per_s": round(batch * (new - 1) / (dc_ms / 1e3), 1)}
 
 
+def traced_steps(eng, step_ids, inputs, batches):
+    """Capture one training step (`step_ids()` on the resident `inputs`), then
+    replay it once per host batch, each overwriting the inputs (the reference's
+    traced training loop, crates/tt-mnist/src/transformer.rs:177-230): ms per
+    step with the batches uploaded inside the timed region, and ms per replay
+    of the graph alone (inputs left resident)."""
+    eng.begin_trace()
+    loss = step_ids()
+    trace = eng.end_trace()
+    eng.run_trace(trace, dict(zip(inputs, batches[0])))  # warm
+    eng.sync()
+    t0 = time.perf_counter()
+    for b in batches:
+        eng.run_trace(trace, dict(zip(inputs, b)))
+    eng.sync()
+    t1 = time.perf_counter()
+    for _ in batches:
+        eng.run_trace(trace)
+    eng.sync()
+    t2 = time.perf_counter()
+    eng.release_trace(trace)
+    eng.free(loss)
+    return (t1 - t0) * 1e3 / len(batches), (t2 - t1) * 1e3 / len(batches)
+
+
 def mlp_bench(eng, steps: int = 100) -> dict:
-    """MLP 784->128->10 training, batch 64, SGD lr 0.01."""
+    """MLP 784->128->10 training, batch 64, SGD lr 0.01:
+    eager steps on device-drawn batches, and the step captured as a trace
+    replayed on host batches."""
     import miburn
     m = miburn.Mlp(eng)
     m.train_synthetic(64, 5, 0.01, data_seed=2)
     losses, ms = m.train_synthetic(64, steps, 0.01, data_seed=3)
     m.close()
-    return {"steps": steps, "ms_per_step": round(ms / steps, 4), "first_loss": round(float(losses[0]), 5),
-            "last_loss": round(float(losses[-1]), 5)}
+    rng = np.random.default_rng(4)
+    batches = [(rng.random((64, 784), dtype=np.float32), rng.integers(0, 10, (64, 1)).astype(np.int32))
+               for _ in range(steps)]
+    mt = miburn.Mlp(eng)
+    x, lab = eng.upload(batches[0][0]), eng.upload_i32(batches[0][1])
+    traced, replay = traced_steps(eng, lambda: mt.train_step_ids(x, lab, 0.01), (x, lab), batches)
+    mt.close()
+    eng.free(x)
+    eng.free(lab)
+    return {"steps": steps, "ms_per_step": round(ms / steps, 4), "traced_ms_per_step": round(traced, 4),
+            "trace_replay_ms": round(replay, 4),
+            "first_loss": round(float(losses[0]), 5), "last_loss": round(float(losses[-1]), 5)}
 
 
 def transformer_bench(eng, steps: int = 20) -> dict:
@@ -195,8 +232,17 @@ def transformer_bench(eng, steps: int = 20) -> dict:
     losses, ms = m.train_synthetic(B, S, steps, 0.05, data_seed=2)
     m.close()
     step_ms = ms / steps
+    rng = np.random.default_rng(5)
+    batches = [tuple(rng.integers(0, V, (B * S, 1)).astype(np.int32) for _ in range(2)) for _ in range(steps)]
+    mt = miburn.Transformer(eng, cfg, seed=0)
+    tok, tgt = eng.upload_i32(batches[0][0]), eng.upload_i32(batches[0][1])
+    traced, replay = traced_steps(eng, lambda: mt.train_step_ids(tok, tgt, B, S, 0.05), (tok, tgt), batches)
+    mt.close()
+    eng.free(tok)
+    eng.free(tgt)
     return {"steps": steps, "batch": B, "seq": S, "ms_per_step": round(step_ms, 3),
-            "flop_per_step": 3 * fwd, "tflops": round(3 * fwd / (step_ms * 1e-3) / 1e12, 2),
+            "traced_ms_per_step": round(traced, 3), "trace_replay_ms": round(replay, 3), "flop_per_step": 3 * fwd,
+            "tflops": round(3 * fwd / (step_ms * 1e-3) / 1e12, 2),
             "first_loss": round(float(losses[0]), 4), "last_loss": round(float(losses[-1]), 4)}
 
 
