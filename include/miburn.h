@@ -307,7 +307,7 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
  * ops around them in a decode step -- Engine::rms_norm_as (server.rs:449),
  * rope_blocks (server.rs:566), the KV-cache slice_assign (llama.rs:415-435),
  * the residual add and silu_mul (crates/burn-tt/src/ops.rs:2622-2651).  x is
- * [M, K] F32 with 1 <= M <= 8 (one row per sequence), K a multiple of 8; w is
+ * [M, K] F32 with 1 <= M <= 32 (one row per sequence), K a multiple of 8; w is
  * BF16 [N, K] (each output row's weights k-contiguous, as the projections are
  * stored); gamma a [1, K] F32 RMSNorm gain or 0 for no norm. ---- */
 /* out = residual + rmsnorm(x) w^T ([M, N]; residual [M, N] or 0), or with

@@ -26,7 +26,7 @@
 namespace mi {
 
 enum DecodeMode { DM_PLAIN = 0, DM_SILU_MUL = 1, DM_QKV = 2 };
-constexpr int DECODE_MAX_M = 8;
+constexpr int DECODE_MAX_M = 32;
 
 struct DecodeArgs {
   const float *x;  // [M, K] F32, rows ldx apart
@@ -64,27 +64,66 @@ __device__ __forceinline__ float silu2(float a) {
   return a * s;
 }
 
+// The two weight rows of pair p, chosen so the epilogue is local.
+struct PairRows {
+  int64_t r0, r1, head, hi;
+  bool has1;
+};
+template <int MODE>
+__device__ __forceinline__ PairRows pair_rows(const DecodeArgs &g, int64_t p) {
+  PairRows q{0, 0, 0, 0, true};
+  if constexpr (MODE == DM_PLAIN) {
+    q.r0 = 2 * p;
+    q.r1 = 2 * p + 1;
+  } else if constexpr (MODE == DM_SILU_MUL) {
+    q.r0 = p;
+    q.r1 = p + g.inter;
+  } else {
+    const int half = g.d / 2;
+    q.head = p / half;
+    q.hi = p % half;
+    q.r0 = q.head * g.d + q.hi;
+    q.r1 = q.r0 + half;
+  }
+  q.has1 = q.r1 < g.N;
+  return q;
+}
+
+// Activation row m's outputs of the pair: y0, y1 its two products.
+template <int MODE>
+__device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &q, int64_t m, float y0, float y1) {
+  if constexpr (MODE == DM_PLAIN) {
+    float *o = g.out + m * g.ldo;
+    o[q.r0] = g.resid ? __fadd_rn(g.resid[m * g.ldo + q.r0], y0) : y0;
+    if (q.has1) o[q.r1] = g.resid ? __fadd_rn(g.resid[m * g.ldo + q.r1], y1) : y1;
+  } else if constexpr (MODE == DM_SILU_MUL) {
+    g.out[m * g.ldo + q.r0] = silu2(y0) * y1;
+  } else {
+    const int64_t half = g.d / 2, hi = q.hi, head = q.head;
+    if (head < g.H + g.KVH) {
+      const float *cs = g.cos + g.pos * g.d, *sn = g.sin + g.pos * g.d;
+      const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
+      const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
+      float *o = head < g.H ? g.out + m * g.ldo + head * g.d
+                            : g.kc + ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d;
+      o[hi] = o0;
+      o[hi + half] = o1;
+    } else {
+      float *o = g.vc + ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d;
+      o[hi] = y0;
+      o[hi + half] = y1;
+    }
+  }
+}
+
 template <int M, int MODE>
 __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
   if (p >= g.npairs) return;  // whole wavefronts
-  int64_t r0, r1;
-  int64_t head = 0, hi = 0;
-  if constexpr (MODE == DM_PLAIN) {
-    r0 = 2 * p;
-    r1 = 2 * p + 1;
-  } else if constexpr (MODE == DM_SILU_MUL) {
-    r0 = p;
-    r1 = p + g.inter;
-  } else {
-    const int half = g.d / 2;
-    head = p / half;
-    hi = p % half;
-    r0 = head * g.d + hi;
-    r1 = r0 + half;
-  }
-  const bool has1 = r1 < g.N;
+  const PairRows q = pair_rows<MODE>(g, p);
+  const int64_t r0 = q.r0, r1 = q.r1;
+  const bool has1 = q.has1;
 
   // The weight rows are independent of the norm: with K <= 2048 (four
   // 16-byte chunks a lane) all of them are requested first, so the norm's
@@ -180,42 +219,114 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   }
   // Lane m writes activation row m's outputs.
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    if (lane != m) continue;
-    const float y0 = acc[m][0], y1 = acc[m][1];
-    if constexpr (MODE == DM_PLAIN) {
-      float *o = g.out + m * g.ldo;
-      o[r0] = g.resid ? __fadd_rn(g.resid[m * g.ldo + r0], y0) : y0;
-      if (has1) o[r1] = g.resid ? __fadd_rn(g.resid[m * g.ldo + r1], y1) : y1;
-    } else if constexpr (MODE == DM_SILU_MUL) {
-      g.out[m * g.ldo + r0] = silu2(y0) * y1;
-    } else {
-      const int64_t half = g.d / 2;
-      if (head < g.H + g.KVH) {
-        const float *cs = g.cos + g.pos * g.d, *sn = g.sin + g.pos * g.d;
-        const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
-        const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
-        if (head < g.H) {
-          float *o = g.out + m * g.ldo + head * g.d;
-          o[hi] = o0;
-          o[hi + half] = o1;
-        } else {
-          float *o = g.kc + ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d;
-          o[hi] = o0;
-          o[hi + half] = o1;
+  for (int m = 0; m < M; ++m)
+    if (lane == m) pair_write<MODE>(g, q, m, acc[m][0], acc[m][1]);
+}
+
+// 9 to 32 activation rows: a block's 4 wavefronts (8 weight rows) share each
+// 256-wide k chunk of the (normalised) rows through LDS, read from cache once
+// per block instead of once per wavefront.  Lane l takes 4 k of the chunk (8
+// bytes of each weight row, 512 contiguous bytes a wavefront), accumulates the
+// 2 x 32 products, and a halving butterfly leaves lane l holding product l
+// (row l / 2, weight row l % 2) after 63 shuffles.
+constexpr int WIDE_M = 32;
+constexpr int WIDE_KC = 256;
+
+template <int MODE>
+__global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, int M) {
+  __shared__ float4 xs[WIDE_M][WIDE_KC / 4];
+  __shared__ float rms_s[WIDE_M];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const bool live = p < g.npairs;  // a wavefront past the last pair still stages and syncs
+  const PairRows q = pair_rows<MODE>(g, live ? p : 0);
+
+  // Row norms: wave w folds rows w, w + 4, ...
+  if (g.gamma) {
+    for (int m = wave; m < M; m += 4) {
+      float ss = 0.0f;
+      for (int64_t k = static_cast<int64_t>(lane) * 4; k < g.K; k += 256) {
+        const float4 a = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) rms_s[m] = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
+    }
+  }
+
+  float acc[2 * WIDE_M];
+#pragma unroll
+  for (int i = 0; i < 2 * WIDE_M; ++i) acc[i] = 0.0f;
+  for (int64_t k0 = 0; k0 < g.K; k0 += WIDE_KC) {
+    __syncthreads();  // the previous chunk's reads (and the norms) are done
+    // Stage the chunk: M x 64 float4, normalised on the fly.
+    for (int e = tid; e < WIDE_M * (WIDE_KC / 4); e += 256) {
+      const int m = e / (WIDE_KC / 4), c = e % (WIDE_KC / 4);
+      const int64_t k = k0 + 4 * c;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M && k < g.K) {
+        v = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
+        if (g.gamma) {
+          const float4 gm = *reinterpret_cast<const float4 *>(g.gamma + k);
+          const float r = rms_s[m];
+          v.x = (v.x / r) * gm.x; v.y = (v.y / r) * gm.y; v.z = (v.z / r) * gm.z; v.w = (v.w / r) * gm.w;
         }
+      }
+      xs[m][c] = v;
+    }
+    __syncthreads();
+    const int64_t k = k0 + 4 * lane;
+    if (live && k < g.K) {
+      float w0[4], w1[4];
+      {
+        const uint2 a = *reinterpret_cast<const uint2 *>(g.w + q.r0 * g.K + k);
+        w0[0] = __uint_as_float(a.x << 16); w0[1] = __uint_as_float(a.x & 0xffff0000u);
+        w0[2] = __uint_as_float(a.y << 16); w0[3] = __uint_as_float(a.y & 0xffff0000u);
+      }
+      if (q.has1) {
+        const uint2 b = *reinterpret_cast<const uint2 *>(g.w + q.r1 * g.K + k);
+        w1[0] = __uint_as_float(b.x << 16); w1[1] = __uint_as_float(b.x & 0xffff0000u);
+        w1[2] = __uint_as_float(b.y << 16); w1[3] = __uint_as_float(b.y & 0xffff0000u);
       } else {
-        float *o = g.vc + ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d;
-        o[hi] = y0;
-        o[hi + half] = y1;
+        w1[0] = w1[1] = w1[2] = w1[3] = 0.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < WIDE_M; ++m) {
+        const float4 v = xs[m][lane];
+        acc[2 * m] += v.x * w0[0] + v.y * w0[1] + v.z * w0[2] + v.w * w0[3];
+        acc[2 * m + 1] += v.x * w1[0] + v.y * w1[1] + v.z * w1[2] + v.w * w1[3];
       }
     }
   }
+  // Halving butterfly: after the step with offset o each lane keeps the half
+  // of its values whose index bit matches its own lane bit, plus the
+  // partner's matching half; lane l ends with the full sum of value l.
+#pragma unroll
+  for (int o = 32, n = 64; o >= 1; o >>= 1, n >>= 1) {
+    const bool upper = (lane & o) != 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i < n / 2) {
+        const float keep = upper ? acc[i + n / 2] : acc[i];
+        const float send = upper ? acc[i] : acc[i + n / 2];
+        acc[i] = keep + __shfl_xor(send, o, 64);
+      }
+    }
+  }
+  // Lane l: row l / 2, weight row l % 2; the pair's other product from lane l ^ 1.
+  const float y = acc[0];
+  const float other = __shfl_xor(y, 1, 64);
+  const int m = lane >> 1;
+  if (live && m < M && (lane & 1) == 0) pair_write<MODE>(g, q, m, y, other);
 }
 
 template <int MODE>
 static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
+  if (M > 8) {
+    decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
+    return;
+  }
   switch (M) {
 #define MI_DEC(m) case m: decode_matvec_kernel<m, MODE><<<grid, 256, 0, st>>>(g); break;
     MI_DEC(1) MI_DEC(2) MI_DEC(3) MI_DEC(4) MI_DEC(5) MI_DEC(6) MI_DEC(7) MI_DEC(8)
@@ -225,7 +336,7 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Shared checks: x [M <= 8, K] F32, w [N, K] BF16, K % 8 == 0, gamma [1, K].
+// Shared checks: x [M <= 32, K] F32, w [N, K] BF16, K % 8 == 0, gamma [1, K].
 static int check_common(mi_ctx *ctx, const Buffer *xb, const Buffer *wb, const Buffer *gb, const char *what) {
   if (xb->elem != MI_F32) return fail(ctx, MI_E_ARG, "%s: activations are %s, not F32", what, elem_name(xb->elem));
   if (wb->elem != MI_BF16) return fail(ctx, MI_E_ARG, "%s: weight is %s, not BF16", what, elem_name(wb->elem));

@@ -12,7 +12,7 @@
 // weight row once; prefill runs the MFMA kernels.  Each layer's q|k|v and
 // gate|up weights are one matrix each (the reference's `Llama::fused`,
 // llama.rs:655-672): prefill multiplies by row blocks of them, and a decode
-// step of at most 8 sequences runs six fused launches a layer -- RMSNorm +
+// step of at most 32 sequences runs six fused launches a layer -- RMSNorm +
 // q|k|v + RoPE + cache write, attention (two), o + residual, RMSNorm +
 // gate|up + SiLU-mul, down + residual.  The KV cache of a layer is
 // F32 [batch * kv_heads * max_ctx, head_dim], item (sequence, kv head), so the
@@ -66,8 +66,11 @@ Tensor weight(mi_ctx *ctx, int64_t rows, int64_t cols, float stdv, uint64_t base
 
 // Largest number of new positions per sequence that take the fused attention.
 constexpr int64_t kFusedAttentionMaxT = 16;
-// Largest batch whose decode step takes the fused projections.
-constexpr int64_t kDecodeMaxBatch = 8;
+// Largest batch whose decode step takes the fused projections, and whose
+// head is one fused norm + GEMV launch (beyond it the head is a product on the
+// matrix cores: the GEMV would re-read the activation rows per block).
+constexpr int64_t kDecodeMaxBatch = 32;
+constexpr int64_t kFusedHeadMaxBatch = 8;
 
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
@@ -168,7 +171,7 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
 // fused norm + GEMV launch over the embedding table.
 Tensor head_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
   const mi_llama_config &c = m->cfg;
-  if (t == 1 && batch <= kDecodeMaxBatch && c.hidden % 8 == 0)
+  if (t == 1 && batch <= kFusedHeadMaxBatch && c.hidden % 8 == 0)
     return burn::norm_matvec(hidden, &m->final_norm, c.eps, m->embed, nullptr, false);
   const int64_t dims[4] = {1, 1, batch, c.hidden};
   const int64_t st[4] = {0, 0, t * c.hidden, 1};

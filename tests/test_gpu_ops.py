@@ -653,7 +653,7 @@ def rms_ref(x, g, eps):
     return x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + eps) * g.astype(np.float64)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 17, 32])  # one GEMV wavefront per row pair; LDS-staged rows above 8
 @pytest.mark.parametrize("N", [576, 577])
 def test_norm_matvec_residual(engine, M, N):
     K, eps = 576, 1e-5
@@ -670,8 +670,9 @@ def test_norm_matvec_residual(engine, M, N):
     assert np.abs(got - x @ w.T).max() <= 1e-5 * (np.abs(x) @ np.abs(w).T).max()
 
 
-def test_norm_matvec_silu_mul(engine):
-    M, K, I, eps = 4, 576, 1536, 1e-5
+@pytest.mark.parametrize("M", [4, 20])
+def test_norm_matvec_silu_mul(engine, M):
+    K, I, eps = 1536, 1536, 1e-5
     x, g, wb = decode_inputs(M, K, 2 * I)
     w = orc.from_bf16(wb).astype(np.float64)
     got = engine.download(engine.norm_matvec(engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb),
@@ -683,7 +684,7 @@ def test_norm_matvec_silu_mul(engine):
     assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("M", [1, 5])
+@pytest.mark.parametrize("M", [1, 5, 32])
 def test_norm_qkv_rope_writes_cache(engine, M):
     H, KVH, D, K, maxc, pos, eps = 9, 3, 64, 576, 40, 17, 1e-5
     x, g, wb = decode_inputs(M, K, (H + 2 * KVH) * D)
@@ -720,7 +721,7 @@ def test_norm_qkv_rope_writes_cache(engine, M):
 def test_decode_projection_errors(engine):
     w = engine.upload_bf16(orc.to_bf16(rnd(64, 576)))
     with pytest.raises(miburn.MiError) as e:
-        engine.norm_matvec(engine.upload(rnd(9, 576)), 0, 0.0, w)  # nine rows
+        engine.norm_matvec(engine.upload(rnd(33, 576)), 0, 0.0, w)  # 33 rows
     assert e.value.kind == "UNSUPPORTED"
     with pytest.raises(miburn.MiError) as e:
         engine.norm_matvec(engine.upload(rnd(2, 576)), 0, 0.0, engine.upload(rnd(64, 576)))  # F32 weight
