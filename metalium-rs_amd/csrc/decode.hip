@@ -224,13 +224,19 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
 }
 
 // 9 to 32 activation rows: a block's 4 wavefronts (8 weight rows) share each
-// 256-wide k chunk of the (normalised) rows through LDS, read from cache once
-// per block instead of once per wavefront.  Lane l takes 4 k of the chunk (8
-// bytes of each weight row, 512 contiguous bytes a wavefront), accumulates the
-// 2 x 32 products, and a halving butterfly leaves lane l holding product l
-// (row l / 2, weight row l % 2) after 63 shuffles.
+// 256-wide k chunk of the rows (times the gain) through LDS, read from cache
+// once per block instead of once per wavefront.  Lane l takes 4 k of the chunk
+// (8 bytes of each weight row, 512 contiguous bytes a wavefront) and
+// accumulates the 2 x 32 products; a halving butterfly leaves lane l holding
+// product l (row l / 2, weight row l % 2) after 63 shuffles.  Latency is
+// hidden rather than waited for: a wavefront requests all its weight chunks
+// (K <= 2048) at the start, and the next chunk of rows is loaded into
+// registers while the current one is multiplied.  The RMSNorm divides the
+// finished products -- sum_k x g w / rms -- with the sums of squares folded
+// from the staged values, so no pass over the rows precedes the products.
 constexpr int WIDE_M = 32;
 constexpr int WIDE_KC = 256;
+constexpr int WIDE_PRE = 8;  // weight chunks requested up front (K <= 2048)
 
 template <int MODE>
 __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, int M) {
@@ -240,62 +246,84 @@ __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, i
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + wave;
   const bool live = p < g.npairs;  // a wavefront past the last pair still stages and syncs
   const PairRows q = pair_rows<MODE>(g, live ? p : 0);
+  const int nch = static_cast<int>((g.K + WIDE_KC - 1) / WIDE_KC);
+  const bool pre = nch <= WIDE_PRE;
 
-  // Row norms: wave w folds rows w, w + 4, ...
-  if (g.gamma) {
-    for (int m = wave; m < M; m += 4) {
-      float ss = 0.0f;
-      for (int64_t k = static_cast<int64_t>(lane) * 4; k < g.K; k += 256) {
-        const float4 a = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
-        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) rms_s[m] = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
+  uint2 pw0[WIDE_PRE], pw1[WIDE_PRE];
+  auto wload = [&](int c, uint2 &a, uint2 &b) {
+    const int64_t k = static_cast<int64_t>(c) * WIDE_KC + 4 * lane;
+    a = make_uint2(0u, 0u);
+    b = make_uint2(0u, 0u);
+    if (live && k < g.K) {
+      a = *reinterpret_cast<const uint2 *>(g.w + q.r0 * g.K + k);
+      if (q.has1) b = *reinterpret_cast<const uint2 *>(g.w + q.r1 * g.K + k);
     }
+  };
+  if (pre) {
+#pragma unroll
+    for (int c = 0; c < WIDE_PRE; ++c)
+      if (c < nch) wload(c, pw0[c], pw1[c]);
   }
+
+  // Staging: thread (wave w, lane l) owns rows w + 4 i (i < 8) at float4 l.
+  float4 xr[8];
+  float ssq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ssq[i] = 0.0f;
+  auto xload = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = wave + 4 * i;
+      const int64_t k = static_cast<int64_t>(c) * WIDE_KC + 4 * lane;
+      xr[i] = (m < M && k < g.K) ? *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  xload(0);
 
   float acc[2 * WIDE_M];
 #pragma unroll
   for (int i = 0; i < 2 * WIDE_M; ++i) acc[i] = 0.0f;
-  for (int64_t k0 = 0; k0 < g.K; k0 += WIDE_KC) {
-    __syncthreads();  // the previous chunk's reads (and the norms) are done
-    // Stage the chunk: M x 64 float4, normalised on the fly.
-    for (int e = tid; e < WIDE_M * (WIDE_KC / 4); e += 256) {
-      const int m = e / (WIDE_KC / 4), c = e % (WIDE_KC / 4);
-      const int64_t k = k0 + 4 * c;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (m < M && k < g.K) {
-        v = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
-        if (g.gamma) {
-          const float4 gm = *reinterpret_cast<const float4 *>(g.gamma + k);
-          const float r = rms_s[m];
-          v.x = (v.x / r) * gm.x; v.y = (v.y / r) * gm.y; v.z = (v.z / r) * gm.z; v.w = (v.w / r) * gm.w;
-        }
-      }
-      xs[m][c] = v;
+  for (int c = 0; c < nch; ++c) {
+    const int64_t k = static_cast<int64_t>(c) * WIDE_KC + 4 * lane;
+    float4 gm = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (g.gamma && k < g.K) gm = *reinterpret_cast<const float4 *>(g.gamma + k);
+    __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = xr[i];
+      ssq[i] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      xs[wave + 4 * i][lane] = make_float4(v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w);
     }
     __syncthreads();
-    const int64_t k = k0 + 4 * lane;
-    if (live && k < g.K) {
-      float w0[4], w1[4];
-      {
-        const uint2 a = *reinterpret_cast<const uint2 *>(g.w + q.r0 * g.K + k);
-        w0[0] = __uint_as_float(a.x << 16); w0[1] = __uint_as_float(a.x & 0xffff0000u);
-        w0[2] = __uint_as_float(a.y << 16); w0[3] = __uint_as_float(a.y & 0xffff0000u);
-      }
-      if (q.has1) {
-        const uint2 b = *reinterpret_cast<const uint2 *>(g.w + q.r1 * g.K + k);
-        w1[0] = __uint_as_float(b.x << 16); w1[1] = __uint_as_float(b.x & 0xffff0000u);
-        w1[2] = __uint_as_float(b.y << 16); w1[3] = __uint_as_float(b.y & 0xffff0000u);
-      } else {
-        w1[0] = w1[1] = w1[2] = w1[3] = 0.0f;
-      }
+    if (c + 1 < nch) xload(c + 1);  // lands while this chunk is multiplied
+    uint2 a, b;
+    if (pre) {
+      a = pw0[0];
+      b = pw1[0];
 #pragma unroll
-      for (int m = 0; m < WIDE_M; ++m) {
-        const float4 v = xs[m][lane];
-        acc[2 * m] += v.x * w0[0] + v.y * w0[1] + v.z * w0[2] + v.w * w0[3];
-        acc[2 * m + 1] += v.x * w1[0] + v.y * w1[1] + v.z * w1[2] + v.w * w1[3];
-      }
+      for (int j = 1; j < WIDE_PRE; ++j)
+        if (j == c) { a = pw0[j]; b = pw1[j]; }
+    } else {
+      wload(c, a, b);
+    }
+    const float w0[4] = {__uint_as_float(a.x << 16), __uint_as_float(a.x & 0xffff0000u),
+                         __uint_as_float(a.y << 16), __uint_as_float(a.y & 0xffff0000u)};
+    const float w1[4] = {__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u),
+                         __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xffff0000u)};
+#pragma unroll
+    for (int m = 0; m < WIDE_M; ++m) {
+      const float4 v = xs[m][lane];
+      acc[2 * m] += v.x * w0[0] + v.y * w0[1] + v.z * w0[2] + v.w * w0[3];
+      acc[2 * m + 1] += v.x * w1[0] + v.y * w1[1] + v.z * w1[2] + v.w * w1[3];
+    }
+  }
+  if (g.gamma) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float s = wave_sum(ssq[i]);
+      const int m = wave + 4 * i;
+      if (lane == 0 && m < M) rms_s[m] = __fsqrt_rn(s / static_cast<float>(g.K) + g.eps);
     }
   }
   // Halving butterfly: after the step with offset o each lane keeps the half
@@ -313,10 +341,12 @@ __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, i
       }
     }
   }
+  __syncthreads();  // the norms are visible
   // Lane l: row l / 2, weight row l % 2; the pair's other product from lane l ^ 1.
-  const float y = acc[0];
-  const float other = __shfl_xor(y, 1, 64);
   const int m = lane >> 1;
+  float y = acc[0];
+  if (g.gamma && m < M) y = y / rms_s[m];
+  const float other = __shfl_xor(y, 1, 64);
   if (live && m < M && (lane & 1) == 0) pair_write<MODE>(g, q, m, y, other);
 }
 
