@@ -1221,11 +1221,11 @@ static void launch_gemv(const Plan &p, hipStream_t st) {
 static int splitk_slices(const Plan &p) {
   if (p.batch != 1) return 1;
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
-  if (tiles >= 128 || p.K < 512) return 1;
-  int64_t s = (192 + tiles - 1) / tiles;
-  const int64_t smax = p.K / 256;
+  if (tiles >= 512 || p.K < 256) return 1;
+  int64_t s = (1024 + tiles - 1) / tiles;
+  const int64_t smax = p.K / 128;
   if (s > smax) s = smax;
-  if (s > 64) s = 64;
+  if (s > 32) s = 32;
   return s < 2 ? 1 : static_cast<int>(s);
 }
 
