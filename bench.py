@@ -195,7 +195,7 @@ def traced_steps(eng, step_ids, inputs, batches):
     return (t1 - t0) * 1e3 / len(batches), (t2 - t1) * 1e3 / len(batches)
 
 
-def mlp_bench(eng, steps: int = 100) -> dict:
+def mlp_bench(eng, steps: int = 100, traces: bool = True) -> dict:
     """MLP 784->128->10 training, batch 64, SGD lr 0.01:
     eager steps on device-drawn batches, and the step captured as a trace
     replayed on host batches."""
@@ -204,6 +204,10 @@ def mlp_bench(eng, steps: int = 100) -> dict:
     m.train_synthetic(64, 5, 0.01, data_seed=2)
     losses, ms = m.train_synthetic(64, steps, 0.01, data_seed=3)
     m.close()
+    out = {"steps": steps, "ms_per_step": round(ms / steps, 4), "first_loss": round(float(losses[0]), 5),
+           "last_loss": round(float(losses[-1]), 5)}
+    if not traces:
+        return out
     rng = np.random.default_rng(4)
     batches = [(rng.random((64, 784), dtype=np.float32), rng.integers(0, 10, (64, 1)).astype(np.int32))
                for _ in range(steps)]
@@ -213,12 +217,11 @@ def mlp_bench(eng, steps: int = 100) -> dict:
     mt.close()
     eng.free(x)
     eng.free(lab)
-    return {"steps": steps, "ms_per_step": round(ms / steps, 4), "traced_ms_per_step": round(traced, 4),
-            "trace_replay_ms": round(replay, 4),
-            "first_loss": round(float(losses[0]), 5), "last_loss": round(float(losses[-1]), 5)}
+    out.update(traced_ms_per_step=round(traced, 4), trace_replay_ms=round(replay, 4))
+    return out
 
 
-def transformer_bench(eng, steps: int = 20) -> dict:
+def transformer_bench(eng, steps: int = 20, traces: bool = True) -> dict:
     """4 layers, d_model 256, 4 heads, FFN 1024 GELU,
     LayerNorm, vocab 8192, seq 128, batch 16, fp32; uniform random tokens and
     targets; forward, cross-entropy, backward and SGD each step."""
@@ -232,6 +235,11 @@ def transformer_bench(eng, steps: int = 20) -> dict:
     losses, ms = m.train_synthetic(B, S, steps, 0.05, data_seed=2)
     m.close()
     step_ms = ms / steps
+    out = {"steps": steps, "batch": B, "seq": S, "ms_per_step": round(step_ms, 3), "flop_per_step": 3 * fwd,
+           "tflops": round(3 * fwd / (step_ms * 1e-3) / 1e12, 2),
+           "first_loss": round(float(losses[0]), 4), "last_loss": round(float(losses[-1]), 4)}
+    if not traces:
+        return out
     rng = np.random.default_rng(5)
     batches = [tuple(rng.integers(0, V, (B * S, 1)).astype(np.int32) for _ in range(2)) for _ in range(steps)]
     mt = miburn.Transformer(eng, cfg, seed=0)
@@ -240,10 +248,8 @@ def transformer_bench(eng, steps: int = 20) -> dict:
     mt.close()
     eng.free(tok)
     eng.free(tgt)
-    return {"steps": steps, "batch": B, "seq": S, "ms_per_step": round(step_ms, 3),
-            "traced_ms_per_step": round(traced, 3), "trace_replay_ms": round(replay, 3), "flop_per_step": 3 * fwd,
-            "tflops": round(3 * fwd / (step_ms * 1e-3) / 1e12, 2),
-            "first_loss": round(float(losses[0]), 4), "last_loss": round(float(losses[-1]), 4)}
+    out.update(traced_ms_per_step=round(traced, 3), trace_replay_ms=round(replay, 3))
+    return out
 
 
 def main() -> int:
@@ -259,6 +265,9 @@ def main() -> int:
     ap.add_argument("--only", choices=["decoder", "mlp", "transformer"],
                     help="run one model harness alone (for profiling) and print its JSON")
     ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
+    ap.add_argument("--no-traces", action="store_true",
+                    help="skip the traced (HIP-graph) training steps (rocprofv3's kernel trace does not follow "
+                         "graph replays)")
     ap.add_argument("--matmul-mode", choices=["fast", "accurate"], default=None,
                     help="how products with an F32 operand run (default: the engine's)")
     args = ap.parse_args()
@@ -274,8 +283,9 @@ def main() -> int:
     if args.matmul_mode:
         eng.set_matmul_mode(miburn.MATMUL_FAST if args.matmul_mode == "fast" else miburn.MATMUL_ACCURATE)
     if args.only:
-        out = {"decoder": lambda: decoder_bench(eng, args.batch), "mlp": lambda: mlp_bench(eng),
-               "transformer": lambda: transformer_bench(eng)}[args.only]()
+        out = {"decoder": lambda: decoder_bench(eng, args.batch),
+               "mlp": lambda: mlp_bench(eng, traces=not args.no_traces),
+               "transformer": lambda: transformer_bench(eng, traces=not args.no_traces)}[args.only]()
         print(json.dumps({"harness": args.only, **out}), flush=True)
         eng.close()
         return 0
@@ -335,8 +345,8 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline()
     if not args.no_models:
         line["decoder"] = [decoder_bench(eng, 1), decoder_bench(eng, 32)]
-        line["mlp_train"] = mlp_bench(eng)
-        line["transformer_train"] = transformer_bench(eng)
+        line["mlp_train"] = mlp_bench(eng, traces=not args.no_traces)
+        line["transformer_train"] = transformer_bench(eng, traces=not args.no_traces)
     print(json.dumps(line), flush=True)
     eng.close()
     return 0

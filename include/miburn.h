@@ -90,6 +90,10 @@ int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols);
  * `bits` (the low 16 bits for BF16): Engine::zeros_dram (server.rs:285). */
 int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits,
             mi_id *out);
+/* A fresh `[rows, cols]` buffer of `elem` whose contents are unspecified
+ * until written (Burn's float_empty, crates/burn-tt/src/generated/ops.rs:130):
+ * the destination of in-place writers such as mi_matmul_items. */
+int mi_empty(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *out);
 
 /* ---- products: Engine::matmul_dram / matmul_dram_bf16 (server.rs:178-204)
  * `op(A) @ op(B)`: `a` is `[m, k]` or, transposed, `[k, m]`; `b` is `[k, n]`
@@ -118,6 +122,35 @@ int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
                      int64_t n, int64_t a_offset, int64_t a_stride,
                      int64_t b_offset, int64_t b_stride, int out_elem,
                      mi_id *out);
+
+/* Products over strided items, the result written in place: what Burn's
+ * multi-head attention runs as reshape + swap_dims + batched matmul (the
+ * reference's batched_matmul, crates/burn-tt/src/ops.rs:2981-3052, after
+ * float_swap_dims, ops.rs:3168), without materialising the head-split
+ * operands.  There are groups x per_group items; item (g, i) of each operand
+ * is the `[rows, cols]` block at element at[0] + g * at[1] + i * at[2] of its
+ * buffer, read with the buffer's row pitch (its cols) -- e.g. head i of
+ * sequence g inside a `[batch * seq, heads * d_head]` projection.  The result
+ * item (g, i), `[m, n]`, is written likewise into the existing buffer `out`
+ * (F32 or BF16, not `a` or `b`); the rest of `out` is left as it was.  Items
+ * of the result must not overlap.  m, k, n >= 1; at most 65535 items. */
+int mi_matmul_items(mi_ctx *ctx, mi_id a, int a_transposed,
+                    const int64_t a_at[3], mi_id b, int b_transposed,
+                    const int64_t b_at[3], int64_t groups, int64_t per_group,
+                    int64_t m, int64_t k, int64_t n, mi_id out,
+                    const int64_t out_at[3]);
+
+/* A linear layer's forward with its residual add in the product's epilogue:
+ * out = residual + (x @ op(w) + bias), each sum rounded to F32 in that order,
+ * so the result is bit-identical to mi_matmul followed by the two broadcast
+ * adds.  No single Engine call corresponds: the reference runs burn's
+ * nn::Linear as float_matmul (crates/burn-tt/src/generated/ops.rs:532) then
+ * float_add (ops.rs:159), and a residual connection as another float_add.
+ * `x` is `[m, k]` (F32 or BF16), `w` is `[k, n]` or, transposed, `[n, k]`;
+ * `bias` (F32, n elements) and `residual` (F32 `[m, n]`) may each be 0 for
+ * none.  The result is F32, or BF16 rounded once after both adds. */
+int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias,
+              mi_id residual, int out_elem, mi_id *out);
 
 /* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
  * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as

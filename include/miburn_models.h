@@ -97,7 +97,9 @@ int mi_transformer_destroy(mi_transformer *m);
 /* layer < 0: which 0 embedding [vocab, d], 1 head weight [d, vocab], 2 head
  * bias [1, vocab].  layer >= 0: which 0 ln1 gamma, 1 ln1 beta, 2 wq, 3 bq,
  * 4 wk, 5 bk, 6 wv, 7 bv, 8 wo, 9 bo (weights [d, d], biases [1, d]),
- * 10 ln2 gamma, 11 ln2 beta, 12 w1 [d, d_ff], 13 b1, 14 w2 [d_ff, d], 15 b2. */
+ * 10 ln2 gamma, 11 ln2 beta, 12 w1 [d, d_ff], 13 b1, 14 w2 [d_ff, d], 15 b2.
+ * The result is a copy, a new id the caller frees (q, k and v are column
+ * blocks of one fused weight inside the model). */
 int mi_transformer_param(mi_transformer *m, int layer, int which, mi_id *out);
 /* One step on resident tokens and targets (batch * seq I32 each, row-major
  * [batch, seq]): forward, mean cross-entropy over all positions, backward,

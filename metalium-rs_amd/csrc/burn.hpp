@@ -145,6 +145,16 @@ inline Tensor fill(mi_ctx *ctx, std::vector<int64_t> shape, int elem, uint32_t b
   return Tensor(ctx, id, std::move(shape));
 }
 
+// float_empty: contents unspecified until written.
+inline Tensor empty(mi_ctx *ctx, std::vector<int64_t> shape, int elem = MI_F32) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  const int64_t cols = shape.empty() ? 1 : shape.back();
+  mi_id id;
+  check(ctx, mi_empty(ctx, cols ? n / cols : 0, cols, elem, &id), "empty");
+  return Tensor(ctx, id, std::move(shape));
+}
+
 inline Tensor float_cast(const Tensor &a, int elem) {
   mi_id id;
   check(a.ctx(), mi_cast(a.ctx(), a.use(), elem, &id), "float_cast");
@@ -191,6 +201,30 @@ inline Tensor float_matmul(const Tensor &a, bool ta, const Tensor &b, bool tb, i
     shape = {m, n};
   }
   return Tensor(a.ctx(), id, shape);
+}
+
+// A Linear forward with an optional residual: residual + (x @ op(w) + bias),
+// the adds in the product's epilogue (null pointers omit a term).
+inline Tensor linear(const Tensor &x, const Tensor &w, bool tw, const Tensor *bias, const Tensor *residual,
+                     int out_elem = MI_F32) {
+  mi_id id;
+  check(x.ctx(), mi_linear(x.ctx(), x.use(), w.use(), tw, bias ? bias->use() : 0, residual ? residual->use() : 0,
+                           out_elem, &id), "linear");
+  return Tensor(x.ctx(), id, {x.rows(), tw ? w.rows() : w.cols()});
+}
+
+// Grouped strided products written into `out` in place (item (g, i) of an
+// operand at at[0] + g * at[1] + i * at[2], read with its row pitch).
+struct Items {
+  int64_t offset, group_stride, item_stride;
+};
+inline void matmul_items(const Tensor &a, bool ta, Items a_at, const Tensor &b, bool tb, Items b_at, int64_t groups,
+                         int64_t per_group, int64_t m, int64_t k, int64_t n, const Tensor &out, Items out_at) {
+  const int64_t aa[3] = {a_at.offset, a_at.group_stride, a_at.item_stride};
+  const int64_t bb[3] = {b_at.offset, b_at.group_stride, b_at.item_stride};
+  const int64_t oo[3] = {out_at.offset, out_at.group_stride, out_at.item_stride};
+  check(a.ctx(), mi_matmul_items(a.ctx(), a.use(), ta, aa, b.use(), tb, bb, groups, per_group, m, k, n, out.use(), oo),
+        "matmul_items");
 }
 
 // Products over item blocks of resident buffers (batched_matmul,

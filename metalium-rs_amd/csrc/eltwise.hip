@@ -422,6 +422,16 @@ extern "C" int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32
   return MI_OK;
 }
 
+extern "C" int mi_empty(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  mi_id id; Buffer *b;
+  int s = new_buffer(ctx, rows, cols, elem, &id, &b);
+  if (s) return s;
+  *out = id;
+  return MI_OK;
+}
+
 // ------------------------------------------------------------------ casts
 namespace mi {
 __global__ void cast_kernel(const void *src, int se, void *dst, int de, int64_t n) {

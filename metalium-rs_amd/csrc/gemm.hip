@@ -215,9 +215,24 @@ struct GemmArgs {
   int64_t M, N, K;
   int64_t lda, ldb, ldc;
   int64_t sa, sb, sc;  // batch strides in elements (0 = broadcast)
+  // Items come in groups: item z = (z / per_group, z % per_group) starts at
+  // (z / per_group) * s?2 + (z % per_group) * s? (one group: per_group = batch).
+  int64_t per_group;
+  int64_t sa2, sb2, sc2;
   int tiles_m, tiles_n;
   int64_t kc;          // split-K: k per slice (blockIdx.z), 0 for none
+  // Epilogue of a linear layer (batch 1): C = resid + (A B + bias), each sum
+  // rounded in that order; null pointers skip the term.
+  const float *bias;   // [N]
+  const float *resid;  // [M, N], row pitch ldr
+  int64_t ldr;
 };
+
+__device__ __forceinline__ float epilogue(const GemmArgs &g, int64_t row, int64_t col, float v) {
+  if (g.bias) v = __fadd_rn(v, g.bias[col]);
+  if (g.resid) v = __fadd_rn(g.resid[row * g.ldr + col], v);
+  return v;
+}
 
 // Map a linear workgroup id to an output tile (tm, tn), grouping the tiles
 // each XCD receives.  Workgroup w runs on XCD w % 8.
@@ -255,9 +270,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t z = blockIdx.y;
-  const SA *A = static_cast<const SA *>(g.a) + z * g.sa;
-  const SB *B = static_cast<const SB *>(g.b) + z * g.sb;
-  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+  const int64_t zo = z / g.per_group, zi = z - zo * g.per_group;
+  const SA *A = static_cast<const SA *>(g.a) + zo * g.sa2 + zi * g.sa;
+  const SB *B = static_cast<const SB *>(g.b) + zo * g.sb2 + zi * g.sb;
+  TO *C = static_cast<TO *>(g.c) + zo * g.sc2 + zi * g.sc;
   int64_t Kz = g.K;
   if (g.kc > 0) {
     // Split-K slice blockIdx.z: k in [ks, ks + Kz), its partial product
@@ -353,8 +369,9 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
         if (!GUARD || (row < g.M && col < g.N)) {
-          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
-          else C[row * g.ldc + col] = acc[i][j][r];
+          const float v = epilogue(g, row, col, acc[i][j][r]);
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
+          else C[row * g.ldc + col] = v;
         }
       }
     }
@@ -534,9 +551,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_split_kernel(GemmArgs g) {
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t z = blockIdx.y;
-  const SA *A = static_cast<const SA *>(g.a) + z * g.sa;
-  const SB *B = static_cast<const SB *>(g.b) + z * g.sb;
-  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+  const int64_t zo = z / g.per_group, zi = z - zo * g.per_group;
+  const SA *A = static_cast<const SA *>(g.a) + zo * g.sa2 + zi * g.sa;
+  const SB *B = static_cast<const SB *>(g.b) + zo * g.sb2 + zi * g.sb;
+  TO *C = static_cast<TO *>(g.c) + zo * g.sc2 + zi * g.sc;
   int64_t Kz = g.K;
   if (g.kc > 0) {
     const int64_t ks = static_cast<int64_t>(blockIdx.z) * g.kc;
@@ -624,8 +642,9 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_split_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
         if (!GUARD || (row < g.M && col < g.N)) {
-          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
-          else C[row * g.ldc + col] = acc[i][j][r];
+          const float v = epilogue(g, row, col, acc[i][j][r]);
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
+          else C[row * g.ldc + col] = v;
         }
       }
     }
@@ -838,9 +857,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, &tm, &tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t z = blockIdx.y;
-  const uint16_t *A = static_cast<const uint16_t *>(g.a) + z * g.sa;
-  const uint16_t *B = static_cast<const uint16_t *>(g.b) + z * g.sb;
-  TO *C = static_cast<TO *>(g.c) + z * g.sc;
+  const int64_t zo = z / g.per_group, zi = z - zo * g.per_group;
+  const uint16_t *A = static_cast<const uint16_t *>(g.a) + zo * g.sa2 + zi * g.sa;
+  const uint16_t *B = static_cast<const uint16_t *>(g.b) + zo * g.sb2 + zi * g.sb;
+  TO *C = static_cast<TO *>(g.c) + zo * g.sc2 + zi * g.sc;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -880,8 +900,9 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(acc[i][j][r]);
-        else C[row * g.ldc + col] = acc[i][j][r];
+        const float v = epilogue(g, row, col, acc[i][j][r]);
+        if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
+        else C[row * g.ldc + col] = v;
       }
     }
   }
@@ -902,7 +923,8 @@ __device__ __forceinline__ float gemv_wave_sum(float v) {
 
 template <int M, typename SB, typename TO>
 __global__ void __launch_bounds__(256) gemv_kernel(const float *A, int64_t lda, const SB *B, int64_t ldb, TO *C,
-                                                   int64_t ldc, int64_t N, int64_t K) {
+                                                   int64_t ldc, int64_t N, int64_t K, const float *bias,
+                                                   const float *resid, int64_t ldr) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
   const int64_t n0 = wave * GEMV_NR;
@@ -961,22 +983,31 @@ __global__ void __launch_bounds__(256) gemv_kernel(const float *A, int64_t lda, 
 #pragma unroll
       for (int r = 0; r < GEMV_NR; ++r) {
         if (n0 + r < N) {
-          if constexpr (sizeof(TO) == 2) C[m * ldc + n0 + r] = f32_to_bf16_bits(acc[m][r]);
-          else C[m * ldc + n0 + r] = acc[m][r];
+          float v = acc[m][r];
+          if (bias) v = __fadd_rn(v, bias[n0 + r]);
+          if (resid) v = __fadd_rn(resid[m * ldr + n0 + r], v);
+          if constexpr (sizeof(TO) == 2) C[m * ldc + n0 + r] = f32_to_bf16_bits(v);
+          else C[m * ldc + n0 + r] = v;
         }
       }
   }
 }
 
 // Split-K: the S partial products [S, M, N] added in slice order.
+// The linear epilogue (bias over n, residual with row pitch ldr) applies to
+// the sum.
 template <typename TO>
-__global__ void splitk_reduce(const float *part, int S, int64_t mn, TO *C) {
+__global__ void splitk_reduce(const float *part, int S, int64_t mn, int64_t n, TO *C, int64_t ldc, const float *bias,
+                              const float *resid, int64_t ldr) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= mn) return;
   float s = part[i];
   for (int z = 1; z < S; ++z) s += part[z * mn + i];
-  if constexpr (sizeof(TO) == 2) C[i] = f32_to_bf16_bits(s);
-  else C[i] = s;
+  const int64_t row = i / n, col = i - row * n;
+  if (bias) s = __fadd_rn(s, bias[col]);
+  if (resid) s = __fadd_rn(resid[row * ldr + col], s);
+  if constexpr (sizeof(TO) == 2) C[row * ldc + col] = f32_to_bf16_bits(s);
+  else C[row * ldc + col] = s;
 }
 
 // ----------------------------------------------------------- launching
@@ -991,6 +1022,12 @@ struct Plan {
   int64_t kc = 0;     // split-K slice length (register kernel only)
   int splits = 1;
   bool fast = true;   // F32 operands split into BF16 parts (the fast matmul mode)
+  const float *bias = nullptr;   // linear epilogue (batch 1): C = resid + (A B + bias)
+  const float *resid = nullptr;
+  int64_t ldr = 0;
+  int64_t ldc = 0;                // result row pitch (0: N)
+  int64_t per_group = 0;          // items per group (0: one group of `batch`)
+  int64_t sa2 = 0, sb2 = 0, sc2 = 0;  // group strides
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1010,9 +1047,12 @@ static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   g.M = p.M; g.N = p.N; g.K = p.K;
   g.lda = p.lda;  // A is [m, k] or [k, m]
   g.ldb = p.ldb;  // B is [k, n] or [n, k]
-  g.ldc = p.N;
+  g.ldc = p.ldc > 0 ? p.ldc : p.N;
   g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.per_group = p.per_group > 0 ? p.per_group : p.batch;
+  g.sa2 = p.sa2; g.sb2 = p.sb2; g.sc2 = p.sc2;
   g.kc = p.kc;
+  g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch),
@@ -1029,9 +1069,12 @@ static hipError_t launch_dma_cfg(const Plan &p, hipStream_t st) {
   g.M = p.M; g.N = p.N; g.K = p.K;
   g.lda = p.lda;
   g.ldb = p.ldb;
-  g.ldc = p.N;
+  g.ldc = p.ldc > 0 ? p.ldc : p.N;
   g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.per_group = p.per_group > 0 ? p.per_group : p.batch;
+  g.sa2 = p.sa2; g.sb2 = p.sb2; g.sc2 = p.sc2;
   g.kc = 0;
+  g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>(p.N / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
@@ -1064,7 +1107,7 @@ static bool tiles_exactly(const Plan &p, int bm, int bn, int bk, int64_t align_e
   if (p.M % bm || p.N % bn || p.K % bk) return false;
   const int64_t lda = p.lda, ldb = p.ldb;
   if (lda % align_elems || ldb % align_elems) return false;
-  if (p.sa % align_elems || p.sb % align_elems) return false;
+  if (p.sa % align_elems || p.sb % align_elems || p.sa2 % align_elems || p.sb2 % align_elems) return false;
   if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.b) & 15)) return false;
   return true;
 }
@@ -1085,9 +1128,12 @@ static hipError_t launch_split_cfg(const Plan &p, hipStream_t st) {
   g.M = p.M; g.N = p.N; g.K = p.K;
   g.lda = p.lda;
   g.ldb = p.ldb;
-  g.ldc = p.N;
+  g.ldc = p.ldc > 0 ? p.ldc : p.N;
   g.sa = p.sa; g.sb = p.sb; g.sc = p.sc;
+  g.per_group = p.per_group > 0 ? p.per_group : p.batch;
+  g.sa2 = p.sa2; g.sb2 = p.sb2; g.sc2 = p.sc2;
   g.kc = p.kc;
+  g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch),
@@ -1184,12 +1230,16 @@ static void launch_gemv_m(const Plan &p, hipStream_t st) {
   const float *A = static_cast<const float *>(p.a);
   if (p.eb == MI_BF16) {
     const uint16_t *B = static_cast<const uint16_t *>(p.b);
-    if (p.eo == MI_BF16) gemv_kernel<M, uint16_t, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.N, p.N, p.K);
-    else gemv_kernel<M, uint16_t, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.N, p.N, p.K);
+    if (p.eo == MI_BF16) gemv_kernel<M, uint16_t, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.ldc > 0 ? p.ldc : p.N, p.N, p.K, p.bias,
+                                                                  p.resid, p.ldr);
+    else gemv_kernel<M, uint16_t, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.ldc > 0 ? p.ldc : p.N, p.N, p.K, p.bias,
+                                                                  p.resid, p.ldr);
   } else {
     const float *B = static_cast<const float *>(p.b);
-    if (p.eo == MI_BF16) gemv_kernel<M, float, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.N, p.N, p.K);
-    else gemv_kernel<M, float, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.N, p.N, p.K);
+    if (p.eo == MI_BF16) gemv_kernel<M, float, uint16_t><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<uint16_t *>(p.c), p.ldc > 0 ? p.ldc : p.N, p.N, p.K, p.bias,
+                                                                  p.resid, p.ldr);
+    else gemv_kernel<M, float, float><<<grid, 256, 0, st>>>(A, p.lda, B, p.ldb, static_cast<float *>(p.c), p.ldc > 0 ? p.ldc : p.N, p.N, p.K, p.bias,
+                                                                  p.resid, p.ldr);
   }
 }
 
@@ -1241,8 +1291,12 @@ static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
   p.splits = static_cast<int>((p.K + p.kc - 1) / p.kc);
   void *final_c = p.c;
   const int eo = p.eo;
+  const float *bias = p.bias, *resid = p.resid;
+  const int64_t ldc = p.ldc > 0 ? p.ldc : p.N;
   p.c = part;
   p.eo = MI_F32;
+  p.bias = p.resid = nullptr;  // the slices write raw partial products, [S, M, N] packed
+  p.ldc = 0;
   hipError_t e;
   if (p.ea == MI_BF16 && p.eb == MI_BF16) e = run_splitk_kernels<uint16_t, uint16_t, uint16_t>(p, st);
   else if (p.ea == MI_F32 && p.eb == MI_F32) e = run_splitk_kernels<float, float, float>(p, st);
@@ -1251,8 +1305,12 @@ static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int64_t mn = p.M * p.N;
   const unsigned g = static_cast<unsigned>((mn + 255) / 256);
-  if (eo == MI_BF16) splitk_reduce<uint16_t><<<g, 256, 0, st>>>(part, p.splits, mn, static_cast<uint16_t *>(final_c));
-  else splitk_reduce<float><<<g, 256, 0, st>>>(part, p.splits, mn, static_cast<float *>(final_c));
+  if (eo == MI_BF16)
+    splitk_reduce<uint16_t><<<g, 256, 0, st>>>(part, p.splits, mn, p.N, static_cast<uint16_t *>(final_c), ldc, bias,
+                                                resid, p.ldr);
+  else
+    splitk_reduce<float><<<g, 256, 0, st>>>(part, p.splits, mn, p.N, static_cast<float *>(final_c), ldc, bias, resid,
+                                             p.ldr);
   return hipGetLastError();
 }
 
@@ -1265,10 +1323,48 @@ static bool items_in(const Buffer *x, int64_t batch, int64_t rows, int64_t cols,
   return last < x->numel() && (stride >= 0);
 }
 
+// Check that item (g, i) of groups x per_group, `rows x cols` at
+// at[0] + g * at[1] + i * at[2] with row pitch x->cols, lies in x for all g, i.
+static bool grouped_items_in(const Buffer *x, int64_t groups, int64_t per_group, int64_t rows, int64_t cols,
+                             const int64_t *at) {
+  const int64_t n = x->numel(), ld = x->cols;
+  if (at[0] < 0 || at[1] < 0 || at[2] < 0 || at[1] > n || at[2] > n || cols > ld) return false;
+  const int64_t last = at[0] + (groups - 1) * at[1] + (per_group - 1) * at[2] + (rows - 1) * ld + cols - 1;
+  return last < n;
+}
+
+// Launch a planned product (M, N, K >= 1) into p.c: the GEMV for a few rows
+// against a k-contiguous weight, split-K for few tiles over a long k, else
+// the tiled kernels.
+static int run_product(mi_ctx *ctx, Plan &p) {
+  hipError_t e;
+  if (gemv_fits(p)) {
+    launch_gemv(p, ctx->stream);
+    e = hipGetLastError();
+  } else if ((p.splits = splitk_slices(p)) > 1) {
+    float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(p.splits) * p.M * p.N * sizeof(float)));
+    if (!part) return fail(ctx, MI_E_OOM, "split-K scratch");
+    e = run_splitk(p, part, ctx->stream);
+  } else {
+    p.splits = 1;
+    e = run_plan(p, ctx->stream);
+  }
+  if (e != hipSuccess) return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
+  return check_launch(ctx, "matmul");
+}
+
 }  // namespace mi
 
+// The epilogue operands of mi_linear (absent for plain products).
+struct LinearTerms {
+  const float *bias = nullptr;
+  const float *resid = nullptr;
+  int64_t ldr = 0;
+};
+
 static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t batch, int64_t m, int64_t k,
-                         int64_t n, int mode, const int64_t *blk, int out_elem, mi_id *out) {
+                         int64_t n, int mode, const int64_t *blk, int out_elem, mi_id *out,
+                         const LinearTerms &lin = LinearTerms()) {
   // mode 0: plain; 1: stacked batch; 2: explicit item offsets/strides (blk =
   // {a_off, a_stride, b_off, b_stride}), items read with the operand's row pitch.
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
@@ -1328,24 +1424,31 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
     p.sa = blk[1]; p.sb = blk[3]; p.sc = m * n;
   }
   if (p.batch > 65535) return fail(ctx, MI_E_ARG, "batched matmul: batch %lld above 65535", (long long)p.batch);
+  p.bias = lin.bias; p.resid = lin.resid; p.ldr = lin.ldr;
   mi_id id; Buffer *cb;
   int s = new_buffer(ctx, p.batch * p.M, p.N, out_elem, &id, &cb);
   if (s) return s;
   p.c = cb->ptr;
   if (p.M > 0 && p.N > 0) {
     hipError_t e = hipSuccess;
-    if (p.K == 0) {
+    if (p.K == 0 && (p.bias || p.resid)) {
+      // Empty sums: the epilogue alone, through a one-slice reduce of zeros.
+      float *zeros = static_cast<float *>(scratch(ctx, static_cast<size_t>(p.M * p.N) * sizeof(float)));
+      if (!zeros) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "linear scratch"); }
+      if (fill_zero(ctx, zeros, static_cast<size_t>(p.M * p.N) * sizeof(float))) e = hipErrorLaunchFailure;
+      const unsigned g = static_cast<unsigned>((p.M * p.N + 255) / 256);
+      if (e == hipSuccess && out_elem == MI_BF16)
+        splitk_reduce<uint16_t><<<g, 256, 0, ctx->stream>>>(zeros, 1, p.M * p.N, p.N, static_cast<uint16_t *>(cb->ptr),
+                                                             p.N, p.bias, p.resid, p.ldr);
+      else if (e == hipSuccess)
+        splitk_reduce<float><<<g, 256, 0, ctx->stream>>>(zeros, 1, p.M * p.N, p.N, static_cast<float *>(cb->ptr), p.N,
+                                                          p.bias, p.resid, p.ldr);
+      if (e == hipSuccess) e = hipGetLastError();
+    } else if (p.K == 0) {
       if (fill_zero(ctx, cb->ptr, p.batch * p.M * p.N * elem_size(out_elem))) e = hipErrorLaunchFailure;
-    } else if (gemv_fits(p)) {
-      launch_gemv(p, ctx->stream);
-      e = hipGetLastError();
-    } else if ((p.splits = splitk_slices(p)) > 1) {
-      float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(p.splits) * p.M * p.N * sizeof(float)));
-      if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "split-K scratch"); }
-      e = run_splitk(p, part, ctx->stream);
     } else {
-      p.splits = 1;
-      e = run_plan(p, ctx->stream);
+      s = run_product(ctx, p);
+      if (s) { mi_free(ctx, id); return s; }
     }
     if (e != hipSuccess) {
       mi_free(ctx, id);
@@ -1361,6 +1464,80 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
 extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out);
+}
+
+extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias, mi_id residual, int out_elem,
+                         mi_id *out) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, X, x);
+  MI_BUF(ctx, W, w);
+  const int64_t m = X->rows, n = w_transposed ? W->rows : W->cols;
+  LinearTerms lin;
+  if (bias) {
+    MI_BUF(ctx, Bb, bias);
+    if (Bb->elem != MI_F32 || Bb->numel() != n)
+      return fail(ctx, MI_E_ARG, "linear: bias is %s [%lld, %lld], want F32 with %lld elements", elem_name(Bb->elem),
+                  (long long)Bb->rows, (long long)Bb->cols, (long long)n);
+    lin.bias = static_cast<const float *>(Bb->ptr);
+  }
+  if (residual) {
+    MI_BUF(ctx, R, residual);
+    if (R->elem != MI_F32 || R->rows != m || R->cols != n)
+      return fail(ctx, MI_E_ARG, "linear: residual is %s [%lld, %lld], want F32 [%lld, %lld]", elem_name(R->elem),
+                  (long long)R->rows, (long long)R->cols, (long long)m, (long long)n);
+    lin.resid = static_cast<const float *>(R->ptr);
+    lin.ldr = n;
+  }
+  return matmul_common(ctx, x, 0, w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
+}
+
+extern "C" int mi_matmul_items(mi_ctx *ctx, mi_id a, int a_transposed, const int64_t *a_at, mi_id b,
+                               int b_transposed, const int64_t *b_at, int64_t groups, int64_t per_group, int64_t m,
+                               int64_t k, int64_t n, mi_id out, const int64_t *out_at) {
+  MI_ENTER(ctx);
+  if (!a_at || !b_at || !out_at) return fail(ctx, MI_E_ARG, "null item placement");
+  MI_BUF(ctx, A, a);
+  MI_BUF(ctx, B, b);
+  MI_BUF(ctx, C, out);
+  if (out == a || out == b) return fail(ctx, MI_E_ARG, "matmul_items: the result buffer is also an operand");
+  if (!elem_float(A->elem) || !elem_float(B->elem) || !elem_float(C->elem))
+    return fail(ctx, MI_E_ARG, "matmul_items of %s and %s into %s", elem_name(A->elem), elem_name(B->elem),
+                elem_name(C->elem));
+  if (groups < 1 || per_group < 1 || m < 1 || k < 1 || n < 1)
+    return fail(ctx, MI_E_ARG, "matmul_items: %lld x %lld items of [%lld, %lld] x [%lld, %lld]", (long long)groups,
+                (long long)per_group, (long long)m, (long long)k, (long long)k, (long long)n);
+  if (groups > 65535 || per_group > 65535 || groups * per_group > 65535)
+    return fail(ctx, MI_E_ARG, "matmul_items: %lld x %lld items, above 65535", (long long)groups,
+                (long long)per_group);
+  const int ta = a_transposed != 0, tb = b_transposed != 0;
+  const int64_t a_rows = ta ? k : m, a_cols = ta ? m : k;
+  const int64_t b_rows = tb ? n : k, b_cols = tb ? k : n;
+  if (!grouped_items_in(A, groups, per_group, a_rows, a_cols, a_at))
+    return fail(ctx, MI_E_ARG, "matmul_items: A items [%lld, %lld] at %lld + g * %lld + i * %lld exceed [%lld, %lld]",
+                (long long)a_rows, (long long)a_cols, (long long)a_at[0], (long long)a_at[1], (long long)a_at[2],
+                (long long)A->rows, (long long)A->cols);
+  if (!grouped_items_in(B, groups, per_group, b_rows, b_cols, b_at))
+    return fail(ctx, MI_E_ARG, "matmul_items: B items [%lld, %lld] at %lld + g * %lld + i * %lld exceed [%lld, %lld]",
+                (long long)b_rows, (long long)b_cols, (long long)b_at[0], (long long)b_at[1], (long long)b_at[2],
+                (long long)B->rows, (long long)B->cols);
+  if (!grouped_items_in(C, groups, per_group, m, n, out_at))
+    return fail(ctx, MI_E_ARG,
+                "matmul_items: result items [%lld, %lld] at %lld + g * %lld + i * %lld exceed [%lld, %lld]",
+                (long long)m, (long long)n, (long long)out_at[0], (long long)out_at[1], (long long)out_at[2],
+                (long long)C->rows, (long long)C->cols);
+  Plan p;
+  p.ta = ta; p.tb = tb;
+  p.fast = ctx->matmul_mode == MI_MATMUL_FAST;
+  p.ea = A->elem; p.eb = B->elem; p.eo = C->elem;
+  p.M = m; p.K = k; p.N = n; p.batch = groups * per_group;
+  p.a = static_cast<const char *>(A->ptr) + a_at[0] * elem_size(A->elem);
+  p.b = static_cast<const char *>(B->ptr) + b_at[0] * elem_size(B->elem);
+  p.c = static_cast<char *>(C->ptr) + out_at[0] * elem_size(C->elem);
+  p.lda = A->cols; p.ldb = B->cols; p.ldc = C->cols;
+  p.per_group = per_group;
+  p.sa = a_at[2]; p.sb = b_at[2]; p.sc = out_at[2];
+  p.sa2 = a_at[1]; p.sb2 = b_at[1]; p.sc2 = out_at[1];
+  return run_product(ctx, p);
 }
 
 extern "C" int mi_set_matmul_mode(mi_ctx *ctx, int mode) {

@@ -16,9 +16,12 @@
 //
 // The backward restates burn-autodiff's rules per op (the same as the MLP
 // harness for Linear, cross-entropy and SGD), with two fused engine kernels:
-// LayerNorm's gradient and softmax's.  Attention's products run per
-// (sequence, head) item over the head-split activations; the split and merge
-// are strided copies (swap_dims materialised).
+// LayerNorm's gradient and softmax's.  The q, k and v Linears are one product
+// against a [d, 3d] weight (columns q | k | v); attention's products run per
+// (sequence, head) item straight out of that [rows, 3d] projection and write
+// their results into place (the head split and merge, swap_dims in Burn, are
+// item strides, never copies).  Linear biases and the residual adds ride in
+// the products' epilogues.
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -33,12 +36,9 @@ thread_local std::string g_tf_error;
 using burn::Tensor;
 
 struct TLayer {
-  Tensor ln1_g, ln1_b, wq, bq, wk, bk, wv, bv, wo, bo, ln2_g, ln2_b, w1, b1, w2, b2;
-  // Parameter `which` in the order of the members above.
-  Tensor *at(int which) {
-    Tensor *p[] = {&ln1_g, &ln1_b, &wq, &bq, &wk, &bk, &wv, &bv, &wo, &bo, &ln2_g, &ln2_b, &w1, &b1, &w2, &b2};
-    return p[which];
-  }
+  Tensor ln1_g, ln1_b;
+  Tensor wqkv, bqkv;  // [d, 3d] and [1, 3d]: columns q | k | v
+  Tensor wo, bo, ln2_g, ln2_b, w1, b1, w2, b2;
 };
 constexpr int kLayerParams = 16;
 }  // namespace
@@ -65,27 +65,15 @@ Tensor scalar(mi_ctx *ctx, float v) {
   return burn::fill(ctx, {1, 1}, MI_F32, bits);
 }
 
-// [B * S, H * dk] rows (sequence, position), heads along the row ->
-// [B * H * S, dk] items (sequence, head).
-Tensor split_heads(const Tensor &x, int64_t B, int64_t S, int64_t H, int64_t dk) {
-  const int64_t dims[4] = {B, H, S, dk};
-  const int64_t st[4] = {S * H * dk, dk, H * dk, 1};
-  return burn::copy4(x, dims, 0, st);
-}
-
-Tensor merge_heads(const Tensor &x, int64_t B, int64_t S, int64_t H, int64_t dk) {
-  const int64_t dims[4] = {B, S, H, dk};
-  const int64_t st[4] = {H * S * dk, dk, S * dk, 1};
-  return burn::copy4(x, dims, 0, st).reshape({B * S, H * dk});
-}
-
-// Linear forward: x W + b (Burn's `Linear`, weight [d_in, d_out]).
-Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
-  return burn::float_add(burn::float_matmul(x, false, w, false), b);
+// Linear forward, x W + b (Burn's `Linear`, weight [d_in, d_out]), plus an
+// optional residual: residual + (x W + b), as Burn's float_add(residual,
+// linear(x)) rounds it.
+Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b, const Tensor *residual = nullptr) {
+  return burn::linear(x, w, false, &b, residual);
 }
 
 struct Saved {
-  Tensor x_in, n1, qh, kh, vh, p, om, x_mid, n2, h1, g;
+  Tensor x_in, n1, qkv, p, om, x_mid, n2, h1, g;
 };
 
 // One training step on tokens / targets [B * S] I32; returns the loss [1, 1].
@@ -95,7 +83,12 @@ Tensor step(mi_transformer *m, const Tensor &tokens, const Tensor &targets, int6
   const int64_t R = B * S, d = c.d_model, H = c.heads, dk = d / H, V = c.vocab;
   const float scale = 1.0f / std::sqrt(static_cast<float>(dk));
   const float eps = c.eps;
-  const int64_t items = B * H;
+  const int64_t items = B * H, W = 3 * d;
+  // Item (sequence b, head h) of each operand: q, k, v inside the [R, 3d]
+  // projection, the head's output columns inside [R, d], and the [S, S]
+  // scores, stored item after item.
+  const burn::Items q_at{0, S * W, dk}, k_at{d, S * W, dk}, v_at{2 * d, S * W, dk};
+  const burn::Items o_at{0, S * d, dk}, s_at{0, H * S * S, S * S};
 
   // Forward.
   Tensor x = burn::select_rows(m->embed, tokens).reshape({R, d});
@@ -105,19 +98,18 @@ Tensor step(mi_transformer *m, const Tensor &tokens, const Tensor &targets, int6
     Saved &sv = saved[l];
     sv.x_in = x;
     sv.n1 = burn::layer_norm(x, L.ln1_g, L.ln1_b, eps);
-    sv.qh = split_heads(linear(sv.n1, L.wq, L.bq), B, S, H, dk);
-    sv.kh = split_heads(linear(sv.n1, L.wk, L.bk), B, S, H, dk);
-    sv.vh = split_heads(linear(sv.n1, L.wv, L.bv), B, S, H, dk);
-    Tensor sc = burn::matmul_blocks(sv.qh, false, sv.kh, true, items, S, dk, S, 0, S * dk, 0, S * dk);
+    sv.qkv = linear(sv.n1, L.wqkv, L.bqkv);  // [R, 3d]
+    Tensor sc = burn::empty(ctx, {items * S, S});
+    burn::matmul_items(sv.qkv, false, q_at, sv.qkv, true, k_at, B, H, S, dk, S, sc, s_at);
     sv.p = burn::softmax_rows(sc, nullptr, scale, false);
-    Tensor oh = burn::matmul_blocks(sv.p, false, sv.vh, false, items, S, S, dk, 0, S * S, 0, S * dk);
-    sv.om = merge_heads(oh, B, S, H, dk);
-    x = burn::float_add(x, linear(sv.om, L.wo, L.bo));
+    sv.om = burn::empty(ctx, {R, d});
+    burn::matmul_items(sv.p, false, s_at, sv.qkv, false, v_at, B, H, S, S, dk, sv.om, o_at);
+    x = linear(sv.om, L.wo, L.bo, &x);
     sv.x_mid = x;
     sv.n2 = burn::layer_norm(x, L.ln2_g, L.ln2_b, eps);
     sv.h1 = linear(sv.n2, L.w1, L.b1);
     sv.g = burn::gelu(sv.h1);
-    x = burn::float_add(x, linear(sv.g, L.w2, L.b2));
+    x = linear(sv.g, L.w2, L.b2, &x);
   }
   Tensor z = linear(x, m->head_w, m->head_b);                       // [R, V]
   Tensor logp = burn::softmax_rows(z, nullptr, 1.0f, true);
@@ -164,17 +156,18 @@ Tensor step(mi_transformer *m, const Tensor &tokens, const Tensor &targets, int6
     sgd(L.ln2_g, n2g.dgamma);
     sgd(L.ln2_b, n2g.dbeta);
     Tensor dx2 = n2g.dx;
-    // Attention block.
+    // Attention block: d scores = d o v^T, dv = p^T d o, then through the
+    // softmax, dq = ds k and dk = ds^T q, each written into its columns of
+    // the [R, 3d] gradient of the fused projection.
     Tensor dom = linear_back(sv.om, dx2, L.wo, L.bo);
-    Tensor doh = split_heads(dom, B, S, H, dk);
-    Tensor dp = burn::matmul_blocks(doh, false, sv.vh, true, items, S, dk, S, 0, S * dk, 0, S * dk);
-    Tensor dvh = burn::matmul_blocks(sv.p, true, doh, false, items, S, S, dk, 0, S * S, 0, S * dk);
+    Tensor dp = burn::empty(ctx, {items * S, S});
+    burn::matmul_items(dom, false, o_at, sv.qkv, true, v_at, B, H, S, dk, S, dp, s_at);
+    Tensor dqkv = burn::empty(ctx, {R, W});
+    burn::matmul_items(sv.p, true, s_at, dom, false, o_at, B, H, S, S, dk, dqkv, v_at);
     Tensor ds = burn::softmax_backward(sv.p, dp, scale);
-    Tensor dqh = burn::matmul_blocks(ds, false, sv.kh, false, items, S, S, dk, 0, S * S, 0, S * dk);
-    Tensor dkh = burn::matmul_blocks(ds, true, sv.qh, false, items, S, S, dk, 0, S * S, 0, S * dk);
-    Tensor dn1 = linear_back(sv.n1, merge_heads(dqh, B, S, H, dk), L.wq, L.bq);
-    dn1 = burn::float_add(dn1, linear_back(sv.n1, merge_heads(dkh, B, S, H, dk), L.wk, L.bk));
-    dn1 = burn::float_add(dn1, linear_back(sv.n1, merge_heads(dvh, B, S, H, dk), L.wv, L.bv));
+    burn::matmul_items(ds, false, s_at, sv.qkv, false, k_at, B, H, S, S, dk, dqkv, q_at);
+    burn::matmul_items(ds, true, s_at, sv.qkv, false, q_at, B, H, S, S, dk, dqkv, k_at);
+    Tensor dn1 = linear_back(sv.n1, dqkv, L.wqkv, L.bqkv);
     burn::NormGrads n1g = burn::layer_norm_backward(sv.x_in, L.ln1_g, dn1, dx2, eps);
     sgd(L.ln1_g, n1g.dgamma);
     sgd(L.ln1_b, n1g.dbeta);
@@ -224,12 +217,18 @@ int mi_transformer_create(mi_ctx *ctx, const mi_transformer_config *cfg, uint64_
     for (TLayer &L : m->layers) {
       L.ln1_g = burn::fill(ctx, {1, d}, MI_F32, one);
       L.ln1_b = burn::fill(ctx, {1, d}, MI_F32, 0);
-      L.wq = kaiming(ctx, d, d, next());
-      L.bq = bias(ctx, d, d, next());
-      L.wk = kaiming(ctx, d, d, next());
-      L.bk = bias(ctx, d, d, next());
-      L.wv = kaiming(ctx, d, d, next());
-      L.bv = bias(ctx, d, d, next());
+      // q, k and v drawn one after another, as three Linears, then placed
+      // side by side.
+      L.wqkv = burn::empty(ctx, {d, 3 * d});
+      L.bqkv = burn::empty(ctx, {1, 3 * d});
+      for (int64_t part = 0; part < 3; ++part) {
+        const Tensor w = kaiming(ctx, d, d, next());
+        const Tensor b = bias(ctx, d, d, next());
+        const int64_t dst_st[4] = {0, 0, 3 * d, 1}, src_st[4] = {0, 0, d, 1};
+        const int64_t wdims[4] = {1, 1, d, d}, bdims[4] = {1, 1, 1, d};
+        burn::copy_into4(L.wqkv, part * d, dst_st, w, 0, src_st, wdims);
+        burn::copy_into4(L.bqkv, part * d, dst_st, b, 0, src_st, bdims);
+      }
       L.wo = kaiming(ctx, d, d, next());
       L.bo = bias(ctx, d, d, next());
       L.ln2_g = burn::fill(ctx, {1, d}, MI_F32, one);
@@ -257,22 +256,36 @@ int mi_transformer_destroy(mi_transformer *m) {
 int mi_transformer_param(mi_transformer *m, int layer, int which, mi_id *out) {
   if (!m || !out) return MI_E_ARG;
   const Tensor *t = nullptr;
+  int64_t col0 = 0, ncols = -1;  // a column block of the fused q | k | v
   if (layer < 0) {
     const Tensor *g[] = {&m->embed, &m->head_w, &m->head_b};
     if (which >= 0 && which < 3) t = g[which];
   } else if (layer < static_cast<int>(m->layers.size()) && which >= 0 && which < kLayerParams) {
-    t = m->layers[layer].at(which);
+    TLayer &L = m->layers[layer];
+    const Tensor *p[] = {&L.ln1_g, &L.ln1_b, &L.wqkv, &L.bqkv, &L.wqkv, &L.bqkv, &L.wqkv, &L.bqkv,
+                         &L.wo,    &L.bo,    &L.ln2_g, &L.ln2_b, &L.w1,  &L.b1,   &L.w2,   &L.b2};
+    t = p[which];
+    if (which >= 2 && which < 8) {
+      ncols = m->cfg.d_model;
+      col0 = (which - 2) / 2 * ncols;
+    }
   }
   if (!t) {
     g_tf_error = "no such parameter";
     return MI_E_ARG;
   }
   try {
-    t->use();
+    // A copy (of the whole parameter or of its column block) the caller frees.
+    const int64_t rows = t->rows(), cols = t->cols();
+    const int64_t n = ncols < 0 ? cols : ncols;
+    const int64_t dims[4] = {1, 1, rows, n};
+    const int64_t st[4] = {0, 0, cols, 1};
+    mi_id id;
+    burn::check(m->ctx, mi_copy_strided4(m->ctx, t->use(), dims, col0, st, &id), "param");
+    *out = id;
   } catch (const std::exception &e) {
     return fail_tf(e);
   }
-  *out = t->id();
   return MI_OK;
 }
 

@@ -94,9 +94,13 @@ def _load() -> ctypes.CDLL:
         "mi_free": [P, U64],
         "mi_metadata": [P, U64, ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(c_int)],
         "mi_fill": [P, I64, I64, c_int, c_u32, Ip],
+        "mi_empty": [P, I64, I64, c_int, Ip],
         "mi_reshape": [P, U64, I64, I64],
         "mi_matmul": [P, U64, c_int, U64, c_int, c_int, Ip],
         "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
+        "mi_linear": [P, U64, U64, c_int, U64, U64, c_int, Ip],
+        "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
+                            I64, U64, ctypes.POINTER(I64)],
         "mi_matmul_blocks": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, I64, I64, c_int, Ip],
         "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
@@ -245,6 +249,10 @@ class Engine:
     def fill(self, rows: int, cols: int, elem: int, bits: int) -> int:
         return self._out(self._lib.mi_fill, rows, cols, elem, bits)
 
+    def empty(self, rows: int, cols: int, elem: int = F32) -> int:
+        """A buffer whose contents are unspecified until written."""
+        return self._out(self._lib.mi_empty, rows, cols, elem)
+
     def sync(self) -> None:
         self._check(self._lib.mi_sync(self.ctx))
 
@@ -256,6 +264,18 @@ class Engine:
     # -- ops ---------------------------------------------------------------
     def matmul_dram(self, a: int, a_t: bool, b: int, b_t: bool, out_elem: int = F32) -> int:
         return self._out(self._lib.mi_matmul, a, int(a_t), b, int(b_t), out_elem)
+
+    def linear(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, out_elem: int = F32) -> int:
+        """residual + (x @ op(w) + bias) in one product; 0 omits a term."""
+        return self._out(self._lib.mi_linear, x, w, int(w_t), bias, residual, out_elem)
+
+    def matmul_items(self, a: int, a_t: bool, a_at, b: int, b_t: bool, b_at, groups: int, per_group: int, m: int,
+                     k: int, n: int, out: int, out_at) -> None:
+        """Grouped strided products written in place into `out`; each `*_at`
+        is (offset, group_stride, item_stride) in elements."""
+        A3 = ctypes.c_int64 * 3
+        self._check(self._lib.mi_matmul_items(self.ctx, a, int(a_t), A3(*a_at), b, int(b_t), A3(*b_at), groups,
+                                              per_group, m, k, n, out, A3(*out_at)))
 
     def matmul_dram_bf16(self, a: int, a_t: bool, b: int, b_t: bool) -> int:
         return self.matmul_dram(a, a_t, b, b_t, BF16)
@@ -666,7 +686,10 @@ class Transformer:
         which = ("embed", "head_w", "head_b").index(name) if layer < 0 else TRANSFORMER_LAYER_PARAMS.index(name)
         out = ctypes.c_uint64()
         self._check(self.L.mi_transformer_param(self.h, layer, which, ctypes.byref(out)))
-        return self.eng.download(out.value)
+        try:
+            return self.eng.download(out.value)
+        finally:
+            self.eng.free(out.value)
 
     def train_step(self, tokens: np.ndarray, targets: np.ndarray, lr: float) -> float:
         """One step on host tokens / targets [batch, seq]."""

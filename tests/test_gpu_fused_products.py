@@ -1,0 +1,247 @@
+"""Device parity of the fused product entry points.
+
+mi_linear (residual + (x op(w) + bias), the adds in the product's epilogue):
+bit-identical to the engine's own product followed by the two F32 adds (the
+product itself is pinned against the oracle by the matmul tests), for every
+kernel a shape selects -- the GEMV, split-K, the 64x64 tiles guarded and
+exact, the fast mode's split kernel, both direct-to-LDS BF16 kernels -- and
+within the matmul bound of the oracle.
+
+mi_matmul_items (grouped strided items written in place): each item within
+the F32 accumulation bound of the oracle's product of the same blocks, the
+rest of the result buffer untouched, on the transformer's head layout and on
+single strided items that take the GEMV and split-K paths.
+"""
+import numpy as np
+import pytest
+
+import miburn
+import oracle_lib as orc
+from miburn import BF16, F32
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(7_2024)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def same_bits(a, b, view=np.uint32):
+    a = np.ascontiguousarray(a).view(view)
+    b = np.ascontiguousarray(b).view(view)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    bad = np.flatnonzero(a.ravel() != b.ravel())
+    assert bad.size == 0, f"{bad.size} datums differ, first at {bad[0]}: {a.ravel()[bad[0]]:#x} vs {b.ravel()[bad[0]]:#x}"
+
+
+def mm_tol(a, b, rel):
+    return rel * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+
+
+@pytest.fixture(params=["fast", "accurate"])
+def mode(request, engine):
+    engine.set_matmul_mode(miburn.MATMUL_FAST if request.param == "fast" else miburn.MATMUL_ACCURATE)
+    yield request.param
+    engine.set_matmul_mode(miburn.MATMUL_FAST)
+
+
+# (m, n, k, w transposed, operand kind, the kernel it selects)
+LINEAR_SHAPES = [
+    (4, 576, 1536, True, "f32", "gemv"),
+    (3, 576, 1536, True, "w_bf16", "gemv bf16 weight"),
+    (64, 256, 2048, False, "f32", "split-K"),
+    (2048, 256, 256, False, "f32", "64x64 exact"),
+    (100, 70, 33, False, "f32", "64x64 guarded"),
+    (2048, 2048, 2048, False, "f32", "fast: split kernel"),
+    (2048, 2048, 512, True, "bf16", "direct 128x128"),
+    (4096, 4096, 256, False, "bf16", "direct 256x256"),
+    (5, 7, 0, False, "f32", "empty sums"),
+]
+
+
+@pytest.mark.parametrize("m,n,k,tw,kind,path", LINEAR_SHAPES, ids=[s[-1] for s in LINEAR_SHAPES])
+@pytest.mark.parametrize("terms", ["bias", "residual", "both", "none"])
+def test_linear_equals_product_then_adds(engine, mode, m, n, k, tw, kind, path, terms):
+    x = rnd(m, k)
+    w = rnd(n, k) if tw else rnd(k, n)
+    if kind == "bf16":
+        ix, iw = engine.upload_bf16(orc.to_bf16(x)), engine.upload_bf16(orc.to_bf16(w))
+    elif kind == "w_bf16":
+        ix, iw = engine.upload(x), engine.upload_bf16(orc.to_bf16(w))
+    else:
+        ix, iw = engine.upload(x), engine.upload(w)
+    bias = rnd(1, n)
+    resid = rnd(m, n)
+    ib = engine.upload(bias) if terms in ("bias", "both") else 0
+    ir = engine.upload(resid) if terms in ("residual", "both") else 0
+    got = engine.download(engine.linear(ix, iw, tw, ib, ir))
+    mm = engine.download(engine.matmul_dram(ix, False, iw, tw)) if k else np.zeros((m, n), np.float32)
+    want = mm
+    if ib:
+        want = want + bias
+    if ir:
+        want = resid + want
+    same_bits(got, want.astype(np.float32))
+    if k and kind == "f32":
+        wf = w.T if tw else w
+        ref = orc.matmul(x, wf, threads=16).astype(np.float64)
+        if ib:
+            ref = ref + bias
+        if ir:
+            ref = resid + ref
+        assert np.all(np.abs(got - ref) <= mm_tol(x, wf, 1e-5) + 1e-6 * (np.abs(ref) + 1e-30))
+
+
+def test_linear_bf16_result_rounds_once_after_the_adds(engine):
+    x, w, bias, resid = rnd(300, 200), rnd(200, 136), rnd(1, 136), rnd(300, 136)
+    ix, iw, ib, ir = engine.upload(x), engine.upload(w), engine.upload(bias), engine.upload(resid)
+    f32 = engine.download(engine.linear(ix, iw, False, ib, ir))
+    bf = engine.download(engine.linear(ix, iw, False, ib, ir, BF16))
+    same_bits(bf, orc.to_bf16(f32), np.uint16)
+
+
+def test_linear_argument_errors(engine):
+    ix, iw = engine.upload(rnd(8, 16)), engine.upload(rnd(16, 32))
+    for bad in (engine.upload(rnd(1, 31)), engine.upload_bf16(orc.to_bf16(rnd(1, 32)))):
+        with pytest.raises(miburn.MiError) as e:
+            engine.linear(ix, iw, False, bad, 0)
+        assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:
+        engine.linear(ix, iw, False, 0, engine.upload(rnd(8, 31)))
+    assert e.value.kind == "ARG"
+
+
+# ------------------------------------------------------------ strided items
+SENTINEL = np.float32(-1234.5)
+
+
+def head_layout(B, H, S, dk):
+    """The transformer's placements: q | k | v inside [B*S, 3d], the heads'
+    outputs inside [B*S, d], scores stored item after item."""
+    d, W = H * dk, 3 * H * dk
+    return dict(q=(0, S * W, dk), k=(d, S * W, dk), v=(2 * d, S * W, dk), o=(0, S * d, dk),
+                s=(0, H * S * S, S * S))
+
+
+def block(buf, at, g, i, rows, cols):
+    flat = buf.ravel()
+    ld = buf.shape[1]
+    start = at[0] + g * at[1] + i * at[2]
+    return np.stack([flat[start + r * ld:start + r * ld + cols] for r in range(rows)])
+
+
+def check_items(got, before, at, groups, per_group, want_fn, m, n, tol_fn):
+    """Each result item against want_fn(g, i); everything else unchanged."""
+    touched = np.zeros(got.size, bool)
+    ld = got.shape[1]
+    for g in range(groups):
+        for i in range(per_group):
+            start = at[0] + g * at[1] + i * at[2]
+            for r in range(m):
+                touched[start + r * ld:start + r * ld + n] = True
+            want = want_fn(g, i)
+            item = block(got, at, g, i, m, n)
+            assert np.all(np.abs(item - want) <= tol_fn(g, i) + 1e-30), (g, i)
+    same_bits(got.ravel()[~touched], before.ravel()[~touched])
+
+
+@pytest.mark.parametrize("B,H,S,dk", [(3, 4, 40, 16), (2, 4, 128, 64)])
+def test_matmul_items_attention_products(engine, mode, B, H, S, dk):
+    """The four attention products of the transformer's forward and backward
+    straight out of the fused projection, results written into place."""
+    d, W = H * dk, 3 * H * dk
+    R = B * S
+    at = head_layout(B, H, S, dk)
+    qkv, dom, p = rnd(R, W), rnd(R, d), rnd(B * H * S, S)
+    iqkv, idom, ip = engine.upload(qkv), engine.upload(dom), engine.upload(p)
+
+    def run(a, ta, a_at, b, tb, b_at, m, k, n, out_shape, out_at, A, Bm):
+        before = np.full(out_shape, SENTINEL, np.float32)
+        before.ravel()[::7] = rnd(before.size // 7 + 1)[: before.ravel()[::7].size]
+        io = engine.upload(before)
+        engine.matmul_items(a, ta, a_at, b, tb, b_at, B, H, m, k, n, io, out_at)
+        got = engine.download(io)
+
+        def operand(buf, at_, g, i, trans, rows, cols):
+            blk = block(buf, at_, g, i, cols if trans else rows, rows if trans else cols)
+            return blk.T if trans else blk
+
+        def want(g, i):
+            return orc.matmul(operand(A, a_at, g, i, ta, m, k), operand(Bm, b_at, g, i, tb, k, n))
+
+        def tol(g, i):
+            return mm_tol(operand(A, a_at, g, i, ta, m, k), operand(Bm, b_at, g, i, tb, k, n), 1e-5)
+
+        check_items(got, before, out_at, B, H, want, m, n, tol)
+
+    # scores = q k^T
+    run(iqkv, False, at["q"], iqkv, True, at["k"], S, dk, S, (B * H * S, S), at["s"], qkv, qkv)
+    # o = p v, merged into [R, d]
+    run(ip, False, at["s"], iqkv, False, at["v"], S, S, dk, (R, d), at["o"], p, qkv)
+    # dv = p^T do, into the v columns of [R, 3d]
+    run(ip, True, at["s"], idom, False, at["o"], S, S, dk, (R, W), at["v"], p, dom)
+    # dp = do v^T
+    run(idom, False, at["o"], iqkv, True, at["v"], S, dk, S, (B * H * S, S), at["s"], dom, qkv)
+
+
+def test_matmul_items_bf16_operands_into_bf16(engine):
+    B, H, S, dk = 2, 2, 64, 64
+    at = head_layout(B, H, S, dk)
+    qkv = orc.to_bf16(rnd(B * S, 3 * H * dk))
+    iq = engine.upload_bf16(qkv)
+    io = engine.fill(B * H * S, S, BF16, 0)
+    engine.matmul_items(iq, False, at["q"], iq, True, at["k"], B, H, S, dk, S, io, at["s"])
+    got = miburn.bf16_to_f32(engine.download(io))
+    qf = orc.from_bf16(qkv)
+    for g in range(B):
+        for i in range(H):
+            q = block(qf, at["q"], g, i, S, dk)
+            k = block(qf, at["k"], g, i, S, dk)
+            want = q.astype(np.float64) @ k.T.astype(np.float64)
+            item = block(got, at["s"], g, i, S, S)
+            tol = 2.0 ** -8 * np.abs(want) + mm_tol(q, k.T, 1e-5)
+            assert np.all(np.abs(item - want) <= tol), (g, i)
+
+
+@pytest.mark.parametrize("m,k,n,tb,path", [(4, 1536, 96, True, "gemv"), (64, 2048, 128, False, "split-K"),
+                                           (96, 80, 72, False, "tiled")])
+def test_matmul_items_single_strided_item(engine, m, k, n, tb, path):
+    """One item (groups = per_group = 1) written at an offset inside a wider
+    buffer: the result pitch is the buffer's, on every path."""
+    a = rnd(m, k)
+    b = rnd(n, k) if tb else rnd(k, n)
+    out_shape = (m + 3, n + 40)
+    before = rnd(*out_shape)
+    io = engine.upload(before)
+    at = (2 * out_shape[1] + 17, 0, 0)
+    engine.matmul_items(engine.upload(a), False, (0, 0, 0), engine.upload(b), tb, (0, 0, 0), 1, 1, m, k, n, io, at)
+    got = engine.download(io)
+    bb = b.T if tb else b
+    check_items(got, before, at, 1, 1, lambda g, i: orc.matmul(a, bb, threads=16), m, n,
+                lambda g, i: mm_tol(a, bb, 1e-5))
+
+
+def test_matmul_items_argument_errors(engine):
+    a = engine.upload(rnd(64, 64))
+    out = engine.empty(64, 64)
+    z = (0, 0, 0)
+    cases = [
+        lambda: engine.matmul_items(a, False, z, a, False, z, 1, 1, 64, 64, 64, a, z),          # result is an operand
+        lambda: engine.matmul_items(a, False, (1, 0, 0), a, False, z, 1, 1, 64, 64, 64, out, z),  # A past the end
+        lambda: engine.matmul_items(a, False, z, a, False, z, 2, 1, 64, 64, 64, out, (0, 4096, 0)),  # result past
+        lambda: engine.matmul_items(a, False, z, a, False, z, 1, 1, 64, 0, 64, out, z),          # k = 0
+        lambda: engine.matmul_items(a, False, z, a, False, z, 1, 1, 65, 64, 64, out, z),         # m > rows
+        lambda: engine.matmul_items(a, False, (0, -1, 0), a, False, z, 2, 1, 8, 8, 8, out, z),   # negative stride
+    ]
+    for c in cases:
+        with pytest.raises(miburn.MiError) as e:
+            c()
+        assert e.value.kind == "ARG"
+
+
+def test_empty_has_shape_and_kind(engine):
+    i = engine.empty(7, 9, BF16)
+    assert engine.metadata(i) == (7, 9, BF16)
+    engine.free(i)
