@@ -762,71 +762,11 @@ struct DmaOperand {
   }
 };
 
-// Scheduling directive for one k step: MF MFMAs, each followed by its share
-// of the NR LDS reads of the next step (compile-time group sizes).
-template <int Q, int MF, int NR>
-__device__ __forceinline__ void interleave_mfma_reads() {
-  if constexpr (Q < MF) {
-    constexpr int per = (NR + MF - 1) / MF;
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (Q * per < NR) __builtin_amdgcn_sched_group_barrier(0x100, (NR - Q * per) < per ? (NR - Q * per) : per, 0);
-    interleave_mfma_reads<Q + 1, MF, NR>();
-  }
-}
-
 // `s_waitcnt vmcnt(N)`, the other counters left alone.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// One k-tile of the direct path on stage `cur` (a static LDS array, so that
-// the compiler's LDS alias scopes keep the other stages' in-flight DMA from
-// forcing a wait before these reads), refilling stage `nxt` -- the stage read
-// one tile ago -- with the tile at k_next.
-template <typename OA, typename OB, int BK, int NW, int TM, int TN, int WTM, int WTN, int INFLIGHT>
-__device__ __forceinline__ void dma_tile(f32x16 (&acc)[TM][TN], const char *cur, char *nxt, const uint16_t *A,
-                                         const uint16_t *B, const GemmArgs &g, int64_t m0, int64_t n0, int64_t k_next,
-                                         int wm, int wn, int wave, int lane) {
-  constexpr int PER_TILE = (OA::BLOCKS + OB::BLOCKS) / NW;  // this thread's DMA instructions per tile
-  constexpr int STEPS = BK / 16;                            // MFMA k steps per tile
-  // This thread's DMA of the current tile has landed (the INFLIGHT younger
-  // tiles' may still be in flight); the barrier makes every thread's visible
-  // and ends every wave's reads of the stage about to be refilled.
-  // A bare s_barrier: a __syncthreads() fence would wait for every DMA in
-  // flight, including the younger tiles'.  LDS reads need no fence: the
-  // wave's own reads have all returned (lgkmcnt 0) before it arrives.
-  wait_vmcnt<INFLIGHT * PER_TILE>();
-  __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00 | (0 << 8));  // lgkmcnt(0) (vmcnt field at its maximum)
-  __builtin_amdgcn_s_barrier();
-  OA::template load<NW>(A, g.lda, m0, k_next, nxt, wave, lane);
-  OB::template load<NW>(B, g.ldb, n0, k_next, nxt + OA::BYTES, wave, lane);
-  const char *a_s = cur, *b_s = cur + OA::BYTES;
-  uint4 fa[2][TM], fb[2][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) fa[0][i] = OA::frag(a_s, wm * WTM + i * 32, 0, lane);
-#pragma unroll
-  for (int j = 0; j < TN; ++j) fb[0][j] = OB::frag(b_s, wn * WTN + j * 32, 0, lane);
-  constexpr int MF = TM * TN;
-  constexpr int NR = TM * OA::READS + TN * OB::READS;  // LDS reads per k step
-#pragma unroll
-  for (int p = 0; p < STEPS; ++p) {
-    const int cb = p & 1;
-    if (p + 1 < STEPS) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[cb ^ 1][i] = OA::frag(a_s, wm * WTM + i * 32, p + 1, lane);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[cb ^ 1][j] = OB::frag(b_s, wn * WTN + j * 32, p + 1, lane);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[cb][i]),
-                                                            __builtin_bit_cast(bf16x8, fb[cb][j]), acc[i][j], 0, 0, 0);
-    if (p + 1 < STEPS) interleave_mfma_reads<0, MF, NR>();
-  }
 }
 
 // The static LDS stage S of NS (unused stages collapse to 16 bytes).
@@ -838,15 +778,47 @@ __device__ __forceinline__ void dma_tile(f32x16 (&acc)[TM][TN], const char *cur,
   __shared__ __attribute__((aligned(1024))) char st4[(NS) > 4 ? (STAGE) : 16];               \
   char *const stages[5] = {st0, st1, st2, st3, st4};
 
-template <typename TO, int BM, int BN, int BK, int NS, bool AK, bool BKC, int WM = 2, int WN = 2>
-__global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
+// ------------------------------------- BF16: pipelined direct path
+// The direct path with the waits taken off the MFMA stream.  k-tiles of 32
+// (two MFMA k steps) in NS >= 3 LDS stages; every step's fragments are read
+// one step ahead into the other of two register buffers, across tile
+// boundaries too, so an MFMA never waits on an LDS read issued just before
+// it.  The one barrier per tile sits before the tile's last step: by then
+// every wave has finished the previous tile (so its stage can be refilled)
+// and this thread's DMA of the next tile has landed (so, after the barrier,
+// every wave's has), which lets the last step's MFMAs cover the first reads
+// of the next tile.  Scheduling fences keep the compiler from sinking the
+// reads back down to their uses.
+template <typename OA, typename OB, int TM, int TN, int WTM, int WTN>
+__device__ __forceinline__ void pipe_reads(uint4 (&fa)[TM], uint4 (&fb)[TN], const char *stage, int p, int wm, int wn,
+                                           int lane) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[i] = OA::frag(stage, wm * WTM + i * 32, p, lane);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[j] = OB::frag(stage + OA::BYTES, wn * WTN + j * 32, p, lane);
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void pipe_mfma(f32x16 (&acc)[TM][TN], const uint4 (&fa)[TM], const uint4 (&fb)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i]),
+                                                          __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
+}
+
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+__device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
+  constexpr int BK = 32;  // two MFMA k steps per tile
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   using OA = DmaOperand<BM, AK, BK>;
   using OB = DmaOperand<BN, BKC, BK>;
   constexpr int STAGE = OA::BYTES + OB::BYTES;
-  static_assert(NS >= 2 && NS <= 5, "stages");
+  constexpr int PER_TILE = (OA::BLOCKS + OB::BLOCKS) / NW;  // this thread's DMA instructions per tile
+  static_assert(NS >= 3 && NS <= 5, "stages");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
   MI_DMA_STAGES(STAGE, NS)
 
@@ -872,20 +844,43 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
 
   const int64_t ktiles = g.K / BK;
   // Tiles past the last reload the last into a stage nobody reads again, so
-  // every thread issues the same number of DMA instructions per tile and the
-  // counted waits stay exact.
+  // every thread issues PER_TILE DMA instructions per tile and the counted
+  // waits stay exact.
   auto kclamp = [&](int64_t t) { return (t < ktiles ? t : ktiles - 1) * BK; };
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) {
     OA::template load<NW>(A, g.lda, m0, kclamp(s), stages[s], wave, lane);
     OB::template load<NW>(B, g.ldb, n0, kclamp(s), stages[s] + OA::BYTES, wave, lane);
   }
+  // Tile 0 landed everywhere (tiles 1 .. NS-2 may be in flight).
+  wait_vmcnt<(NS - 2) * PER_TILE>();
+  __builtin_amdgcn_s_barrier();
+  uint4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa0, fb0, stages[0], 0, wm, wn, lane);
   for (int64_t kt = 0; kt < ktiles; kt += NS) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      if (s == 0 || kt + s < ktiles)
-        dma_tile<OA, OB, BK, NW, TM, TN, WTM, WTN, NS - 2>(acc, stages[s], stages[(s + NS - 1) % NS], A, B, g, m0, n0,
-                                                       kclamp(kt + s + NS - 1), wm, wn, wave, lane);
+      if (s == 0 || kt + s < ktiles) {
+        // Step 0 of tile kt + s (stage s): read step 1 ahead.
+        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa1, fb1, stages[s], 1, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        pipe_mfma<TM, TN>(acc, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Step 1: the next tile has landed here (NS - 3 younger tiles may be
+        // in flight); after the barrier it has landed everywhere and no wave
+        // reads the previous tile's stage, which is refilled with tile
+        // kt + s + NS - 1.  Then step 0 of the next tile is read ahead (past
+        // the last tile this reads a stage holding a reload, unused).
+        wait_vmcnt<(NS - 3) * PER_TILE>();
+        __builtin_amdgcn_s_barrier();
+        char *refill = stages[(s + NS - 1) % NS];
+        OA::template load<NW>(A, g.lda, m0, kclamp(kt + s + NS - 1), refill, wave, lane);
+        OB::template load<NW>(B, g.ldb, n0, kclamp(kt + s + NS - 1), refill + OA::BYTES, wave, lane);
+        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa0, fb0, stages[(s + 1) % NS], 0, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        pipe_mfma<TM, TN>(acc, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   // No DMA may still be writing this workgroup's LDS when its waves end.
@@ -906,6 +901,20 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_dma_kernel(GemmArgs g) {
       }
     }
   }
+}
+
+// Two waves per SIMD (8 per workgroup): at most 256 registers a wave.
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+__global__ void __launch_bounds__(WM *WN * 64) gemm_pipe_kernel(GemmArgs g) {
+  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN>(g);
+}
+
+// One wave per SIMD (4 per workgroup): the whole 512-entry register file, so
+// a 128 x 128 wave tile keeps its accumulators in the AGPRs.
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+__global__ void __launch_bounds__(WM *WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_pipe1_kernel(GemmArgs g) {
+  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN>(g);
 }
 
 // ------------------------------------------------- small-M products
@@ -1061,9 +1070,8 @@ static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename TO, int BM, int BN, int BK, int NS, bool AK, bool BKC, int WM = 2, int WN = 2>
-static hipError_t launch_dma_cfg(const Plan &p, hipStream_t st) {
-  auto kern = gemm_dma_kernel<TO, BM, BN, BK, NS, AK, BKC, WM, WN>;
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   GemmArgs g;
   g.a = p.a; g.b = p.b; g.c = p.c;
   g.M = p.M; g.N = p.N; g.K = p.K;
@@ -1078,18 +1086,20 @@ static hipError_t launch_dma_cfg(const Plan &p, hipStream_t st) {
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>(p.N / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
-  kern<<<grid, WM * WN * 64, 0, st>>>(g);
+  if constexpr (WM * WN == 4) gemm_pipe1_kernel<TO, BM, BN, NS, AK, BKC, WM, WN><<<grid, 256, 0, st>>>(g);
+  else gemm_pipe_kernel<TO, BM, BN, NS, AK, BKC, WM, WN><<<grid, WM * WN * 64, 0, st>>>(g);
   return hipGetLastError();
 }
 
-template <typename TO, int BM, int BN, int BK, int NS, int WM = 2, int WN = 2>
-static hipError_t launch_dma(const Plan &p, hipStream_t st) {
+template <typename TO, int BM, int BN, int NS, int WM, int WN>
+static hipError_t launch_pipe(const Plan &p, hipStream_t st) {
   const bool ak = !p.ta, bk = p.tb;
-  if (ak && bk) return launch_dma_cfg<TO, BM, BN, BK, NS, true, true, WM, WN>(p, st);
-  if (ak && !bk) return launch_dma_cfg<TO, BM, BN, BK, NS, true, false, WM, WN>(p, st);
-  if (!ak && bk) return launch_dma_cfg<TO, BM, BN, BK, NS, false, true, WM, WN>(p, st);
-  return launch_dma_cfg<TO, BM, BN, BK, NS, false, false, WM, WN>(p, st);
+  if (ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, true, true, WM, WN>(p, st);
+  if (ak && !bk) return launch_pipe_cfg<TO, BM, BN, NS, true, false, WM, WN>(p, st);
+  if (!ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, false, true, WM, WN>(p, st);
+  return launch_pipe_cfg<TO, BM, BN, NS, false, false, WM, WN>(p, st);
 }
+
 
 // Operand orientation: A k-contiguous unless transposed; B k-contiguous when transposed.
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool GUARD>
@@ -1168,14 +1178,12 @@ template <typename TO>
 static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   using T = uint16_t;
   auto tiles = [&](int64_t bm, int64_t bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.batch; };
-  // Exactly tiled shapes take the direct HBM -> LDS kernel: 256 x 256 tiles
-  // (8 waves, each 128 x 64 or 64 x 128, two k-tiles of 64 in LDS) when they
-  // give most of the 256 CUs a tile, else 128 x 128 tiles (4 waves, four
-  // stages).
-  if (tiles_exactly(p, 256, 256, 64, 8) && tiles(256, 256) >= 192)
-    return p.tb ? launch_dma<TO, 256, 256, 64, 2, 4, 2>(p, st) : launch_dma<TO, 256, 256, 64, 2, 2, 4>(p, st);
-  if (tiles_exactly(p, 128, 128, 64, 8) && tiles(128, 128) >= 96)
-    return launch_dma<TO, 128, 128, 64, 4>(p, st);
+  // Exactly tiled shapes take the pipelined direct HBM -> LDS kernel: 256 x
+  // 256 tiles (8 waves of 128 x 64, two per SIMD) when they give most of the
+  // 256 CUs a tile, else 128 x 128 tiles (4 waves of 64 x 64); five LDS
+  // stages of k 32 either way.
+  if (tiles_exactly(p, 256, 256, 32, 8) && tiles(256, 256) >= 192) return launch_pipe<TO, 256, 256, 5, 2, 4>(p, st);
+  if (tiles_exactly(p, 128, 128, 32, 8) && tiles(128, 128) >= 96) return launch_pipe<TO, 128, 128, 5, 2, 2>(p, st);
   if (tiles_exactly(p, 64, 64, 64, 8))
     return launch_orient<T, T, T, TO, 64, 64, 2, 2, false>(p, st);
   return launch_orient<T, T, T, TO, 64, 64, 2, 2, true>(p, st);
