@@ -798,6 +798,20 @@ __device__ __forceinline__ void pipe_reads(uint4 (&fa)[TM], uint4 (&fb)[TN], con
   for (int j = 0; j < TN; ++j) fb[j] = OB::frag(stage + OA::BYTES, wn * WTN + j * 32, p, lane);
 }
 
+// Scheduling directive for one step: the MFMAs in order, the first ones
+// each followed by PER of the NR LDS reads of the next step, so every read
+// is issued early in the step (and lands before the next one) while no more
+// reads are in flight at the step's first MFMA than its own operands.
+template <int Q, int MF, int NR, int PER>
+__device__ __forceinline__ void mfma_then_reads() {
+  if constexpr (Q < MF) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    if constexpr (Q * PER < NR)
+      __builtin_amdgcn_sched_group_barrier(0x100, (NR - Q * PER) < PER ? (NR - Q * PER) : PER, 0);  // LDS reads
+    mfma_then_reads<Q + 1, MF, NR, PER>();
+  }
+}
+
 template <int TM, int TN>
 __device__ __forceinline__ void pipe_mfma(f32x16 (&acc)[TM][TN], const uint4 (&fa)[TM], const uint4 (&fb)[TN]) {
 #pragma unroll
@@ -820,6 +834,8 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   constexpr int PER_TILE = (OA::BLOCKS + OB::BLOCKS) / NW;  // this thread's DMA instructions per tile
   static_assert(NS >= 3 && NS <= 5, "stages");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
+  constexpr int MF = TM * TN;                          // MFMAs per step
+  constexpr int NR = TM * OA::READS + TN * OB::READS;  // LDS reads per step
   MI_DMA_STAGES(STAGE, NS)
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -861,10 +877,11 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if (s == 0 || kt + s < ktiles) {
-        // Step 0 of tile kt + s (stage s): read step 1 ahead.
-        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa1, fb1, stages[s], 1, wm, wn, lane);
+        // Step 0 of tile kt + s (stage s), reading step 1 ahead.
         __builtin_amdgcn_sched_barrier(0);
+        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa1, fb1, stages[s], 1, wm, wn, lane);
         pipe_mfma<TM, TN>(acc, fa0, fb0);
+        mfma_then_reads<0, MF, NR, 2>();
         __builtin_amdgcn_sched_barrier(0);
         // Step 1: the next tile has landed here (NS - 3 younger tiles may be
         // in flight); after the barrier it has landed everywhere and no wave
@@ -876,9 +893,10 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
         char *refill = stages[(s + NS - 1) % NS];
         OA::template load<NW>(A, g.lda, m0, kclamp(kt + s + NS - 1), refill, wave, lane);
         OB::template load<NW>(B, g.ldb, n0, kclamp(kt + s + NS - 1), refill + OA::BYTES, wave, lane);
-        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa0, fb0, stages[(s + 1) % NS], 0, wm, wn, lane);
         __builtin_amdgcn_sched_barrier(0);
+        pipe_reads<OA, OB, TM, TN, WTM, WTN>(fa0, fb0, stages[(s + 1) % NS], 0, wm, wn, lane);
         pipe_mfma<TM, TN>(acc, fa1, fb1);
+        mfma_then_reads<0, MF, NR, 2>();
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -886,18 +904,25 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   // No DMA may still be writing this workgroup's LDS when its waves end.
   wait_vmcnt<0>();
 
+  // Fragment (i, j), value r: row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4,
+  // column 32 j + lane % 32 of the wave's tile.  One base pointer per
+  // fragment and 16 row offsets shared by all, so the addressing stays small
+  // next to the accumulators.
   const int lrow = lane & 31, lhalf = lane >> 5;
+  const int64_t row0 = m0 + wm * WTM + 4 * lhalf, col0 = n0 + wn * WTN + lrow;
+  const bool plain = g.bias == nullptr && g.resid == nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+      TO *cij = C + (row0 + i * 32) * g.ldc + col0 + j * 32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        const float v = epilogue(g, row, col, acc[i][j][r]);
-        if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
-        else C[row * g.ldc + col] = v;
+        const int dr = 8 * (r >> 2) + (r & 3);
+        float v = acc[i][j][r];
+        if (!plain) v = epilogue(g, row0 + i * 32 + dr, col0 + j * 32, v);
+        if constexpr (sizeof(TO) == 2) cij[dr * g.ldc] = f32_to_bf16_bits(v);
+        else cij[dr * g.ldc] = v;
       }
     }
   }
