@@ -44,6 +44,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// The logistic function in its two-branch form, so neither exponential
+// overflows: 1 / (1 + e^-x) for x >= 0 and e^x / (1 + e^x) below.  Both
+// quotients share t = e^-|x| (which is e^-x above zero and e^x below), so it
+// is computed branch-free as (x >= 0 ? 1 : t) / (1 + t): the same bits as the
+// branches, one exponential, and no divergence within a wavefront.
+__device__ __forceinline__ float sigmoid2(float x) {
+  const float t = expf(-fabsf(x));
+  return (x >= 0.0f ? 1.0f : t) / (1.0f + t);
+}
+
 // Streaming (non-temporal) 16-byte accesses: the line is not kept in the
 // caches.  On an MI355X a stream of them moves ~80% of the 8 TB/s peak
 // against ~70% for ordinary accesses; they suit operands far larger than the

@@ -60,7 +60,7 @@ __device__ __forceinline__ void bf16x8(uint4 q, float (&w)[8]) {
 
 __device__ __forceinline__ float silu2(float a) {
   // a * sigmoid(a), the sigmoid in the two-branch form of the element-wise op.
-  const float s = a >= 0.0f ? 1.0f / (1.0f + expf(-a)) : expf(a) / (1.0f + expf(a));
+  const float s = sigmoid2(a);
   return a * s;
 }
 

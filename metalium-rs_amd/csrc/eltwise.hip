@@ -35,13 +35,6 @@ __device__ __forceinline__ float load_elem(const Opnd &o, int64_t idx) {
   }
 }
 
-__device__ __forceinline__ float sigmoid2(float x) {
-  // Two branches, so neither exponential overflows for large |x|.
-  if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
-  float e = expf(x);
-  return e / (1.0f + e);
-}
-
 __device__ __forceinline__ float clamp_min_flex(float a, float s) {
   if (isnan(s)) return a;
   return a > s ? a : s;  // a NaN `a` gives the scalar, equal values the scalar

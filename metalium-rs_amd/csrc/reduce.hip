@@ -13,6 +13,10 @@
 // wavefront: lanes stride the row with coalesced loads, keep it in registers
 // when it fits (softmax reads its row from HBM once and writes it once), and
 // fold across lanes with a fixed butterfly, so results are deterministic.
+// Softmax takes each quotient by the row sum as a product with the sum's
+// reciprocal (one division per row instead of one per element, which would
+// make the kernel VALU-bound): at most one rounding more than a division,
+// relative error < 2^-22.
 // Column sums (over rows) split the rows over a 2-D grid, each block summing a
 // strip of 256 columns over a range of rows as float4 lanes, and a second
 // pass folds the row ranges' partials in a fixed order (16 interleaved
@@ -155,27 +159,93 @@ __global__ void __launch_bounds__(256) reduce_rows_wide(const float *x, float *p
   };
   const float *p = x + c;
   int64_t r = r_begin;
-  for (; r + 8 <= r_end; r += 8) {
-    float4 v[8];
+  // Software-pipelined: the next eight rows' loads are issued before the
+  // current eight are folded, so sixteen rows are in flight.
+  if (r + 8 <= r_end) {
+    float4 v[8], w[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) v[u] = ld4<NT>(p + (r + u) * cols);
+    for (; r + 16 <= r_end; r += 16) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) fold(acc, v[u]);
+      for (int u = 0; u < 8; ++u) w[u] = ld4<NT>(p + (r + 8 + u) * cols);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold(acc, v[u]);
+      if (r + 24 <= r_end) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ld4<NT>(p + (r + 16 + u) * cols);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold(acc, w[u]);
+    }
+    // Here v holds rows r .. r + 7 exactly when r + 8 <= r_end.
+    if (r + 8 <= r_end) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold(acc, v[u]);
+      r += 8;
+    }
   }
   for (; r < r_end; ++r) fold(acc, ld4<NT>(p + r * cols));
   *reinterpret_cast<float4 *>(part + split * cols + c) = acc;
 }
 
-// Fold the partial rows [nb, n] of a split reduction into [1, n].  A block of
-// 16 wavefronts takes 64 columns; wavefront w folds partial rows w, w + 16,
-// ... (four loads in flight), and the 16 results fold in wave order through
-// LDS -- a fixed order, so the result is deterministic.  Columns below
-// `split_at` go to out0, the rest to out1 (two reductions in one pass).
-__global__ void __launch_bounds__(1024) fold_partials_kernel(const float *part, int64_t nb, int64_t n, int op,
-                                                             float div, float *out0, int64_t split_at, float *out1) {
-  __shared__ float red[16][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+// F32 rows of Q * 1024 columns (Q <= 8) summed over rows: a block reads
+// whole rows -- each a contiguous run of Q * 4 KiB -- over its range of rows,
+// thread t folding columns 4 t + 1024 q (q < Q) in row order, the next row's
+// loads issued before the current row is folded.
+template <bool NT, int Q>
+__global__ void __launch_bounds__(256) reduce_rows_full(const float *x, float *part, int64_t rows, int64_t cols,
+                                                        int64_t rows_per_split, int op) {
+  const int64_t split = blockIdx.x;
+  const int64_t r_begin = split * rows_per_split;
+  const int64_t r_end = r_begin + rows_per_split < rows ? r_begin + rows_per_split : rows;
+  const float init = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
+  float4 acc[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) acc[q] = make_float4(init, init, init, init);
+  auto fold = [op](float4 &a, float4 v) {
+    if (op == MI_R_MAX) { a.x = max_nan(a.x, v.x); a.y = max_nan(a.y, v.y); a.z = max_nan(a.z, v.z); a.w = max_nan(a.w, v.w); }
+    else if (op == MI_R_MIN) { a.x = min_nan(a.x, v.x); a.y = min_nan(a.y, v.y); a.z = min_nan(a.z, v.z); a.w = min_nan(a.w, v.w); }
+    else { a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w; }
+  };
+  const float *p = x + threadIdx.x * 4;
+  if (r_begin < r_end) {
+    float4 v[Q], w[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) v[q] = ld4<NT>(p + r_begin * cols + 1024 * q);
+    int64_t r = r_begin;
+    for (; r + 2 <= r_end; r += 2) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) w[q] = ld4<NT>(p + (r + 1) * cols + 1024 * q);
+#pragma unroll
+      for (int q = 0; q < Q; ++q) fold(acc[q], v[q]);
+      if (r + 2 < r_end) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) v[q] = ld4<NT>(p + (r + 2) * cols + 1024 * q);
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) fold(acc[q], w[q]);
+    }
+    if (r < r_end) {  // one row left, already in v
+#pragma unroll
+      for (int q = 0; q < Q; ++q) fold(acc[q], v[q]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    *reinterpret_cast<float4 *>(part + split * cols + threadIdx.x * 4 + 1024 * q) = acc[q];
+}
+
+// Fold the partial rows [nb, n] of a split reduction into [1, n].  A block
+// of 512 threads takes 32 columns: thread t folds column t % 32 over partial
+// rows w, w + 16, w + 32, ... (chain w = t / 32, sixteen loads in flight),
+// and the 16 chains fold in chain order through LDS -- a fixed order, so the
+// result is deterministic.  Columns below `split_at` go to out0, the rest to
+// out1 (two reductions in one pass).
+__global__ void __launch_bounds__(512) fold_partials_kernel(const float *part, int64_t nb, int64_t n, int op,
+                                                            float div, float *out0, int64_t split_at, float *out1) {
+  __shared__ float red[16][32];
+  const int col = threadIdx.x & 31, w = threadIdx.x >> 5;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 32 + col;
   auto fold = [op](float a, float b) {
     if (op == MI_R_MAX) return max_nan(a, b);
     if (op == MI_R_MIN) return min_nan(a, b);
@@ -183,20 +253,21 @@ __global__ void __launch_bounds__(1024) fold_partials_kernel(const float *part, 
   };
   float acc = (op == MI_R_MAX) ? -INFINITY : (op == MI_R_MIN ? INFINITY : 0.0f);
   if (c < n) {
-    int64_t k = w;
-    for (; k + 48 < nb; k += 64) {
-      const float v0 = part[k * n + c], v1 = part[(k + 16) * n + c];
-      const float v2 = part[(k + 32) * n + c], v3 = part[(k + 48) * n + c];
-      acc = fold(fold(fold(fold(acc, v0), v1), v2), v3);
+    for (int64_t k = w; k < nb; k += 256) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = (k + 16 * u < nb) ? part[(k + 16 * u) * n + c] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (k + 16 * u < nb) acc = fold(acc, v[u]);
     }
-    for (; k < nb; k += 16) acc = fold(acc, part[k * n + c]);
   }
-  red[w][lane] = acc;
+  red[w][col] = acc;
   __syncthreads();
   if (w == 0 && c < n) {
-    float s = red[0][lane];
+    float s = red[0][col];
 #pragma unroll
-    for (int k = 1; k < 16; ++k) s = fold(s, red[k][lane]);
+    for (int k = 1; k < 16; ++k) s = fold(s, red[k][col]);
     if (op == MI_R_MEAN) s = s / div;
     if (c < split_at) out0[c] = s;
     else out1[c - split_at] = s;
@@ -282,10 +353,11 @@ __global__ void __launch_bounds__(256) softmax_kernel(const void *x, int elem, c
   s = wave_sum(s);
   if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
   const float ls = log_mode ? logf(s) : 0.0f;
+  const float inv = 1.0f / s;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
-    if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] / s);
+    if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] * inv);
   }
 }
 
@@ -309,10 +381,18 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return s;
 }
 
-template <int VPT, bool VEC, bool NT>
-__global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
-                                                            int64_t mask_rows, float scale, int log_mode, void *out,
+// FULL: the row is exactly 1024 VPT long (F32, VEC), so no column check.
+// LOG: 0 softmax, 1 log-softmax, -1 as `log_mode` says.
+// Up to 8192 columns the registers are held to 64, so eight rows' blocks
+// share a CU: the 32 rows a CU gets of an 8192-row input then run in four
+// full rounds instead of five and a third.
+template <int VPT, bool VEC, bool NT, bool FULL = false, int LOG = -1>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(VPT <= 8 ? 8 : 4)))
+softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
+                                                            int64_t mask_rows, float scale, int log_mode_arg, void *out,
                                                             int out_elem, int64_t cols) {
+  static_assert(!FULL || VEC, "full rows are read as float4");
+  const bool log_mode = LOG < 0 ? log_mode_arg != 0 : LOG == 1;
   constexpr int T = 4 * VPT;  // elements per thread
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -328,8 +408,8 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
       const int64_t j4 = tid + 256 * u;
-      float4 q = (j4 * 4 < cols) ? ld4<NT>(reinterpret_cast<const float *>(p + j4))
-                                 : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      float4 q = (FULL || j4 * 4 < cols) ? ld4<NT>(reinterpret_cast<const float *>(p + j4))
+                                         : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
       v[4 * u] = q.x; v[4 * u + 1] = q.y; v[4 * u + 2] = q.z; v[4 * u + 3] = q.w;
     }
   } else {
@@ -343,7 +423,7 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = col_of(t);
-    if (j < cols) {
+    if (FULL || j < cols) {
       if (scale != 1.0f) v[t] = v[t] * scale;
       if (mrow && mrow[j]) v[t] = -INFINITY;
     }
@@ -356,24 +436,25 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
   for (int t = 0; t < T; ++t) {
     const int64_t j = col_of(t);
     const float sh = v[t] - m;
-    const float e = j < cols ? expf(sh) : 0.0f;
+    const float e = (FULL || j < cols) ? expf(sh) : 0.0f;
     v[t] = log_mode ? sh : e;
     s += e;
   }
   s = block_sum(s, red);
   if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
   const float ls = log_mode ? logf(s) : 0.0f;
+  const float inv = 1.0f / s;
   if (VEC && out_elem == MI_F32) {
     float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + base);
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
       const int64_t j4 = tid + 256 * u;
-      if (j4 * 4 < cols) {
+      if (FULL || j4 * 4 < cols) {
         float4 r;
-        r.x = log_mode ? v[4 * u] - ls : v[4 * u] / s;
-        r.y = log_mode ? v[4 * u + 1] - ls : v[4 * u + 1] / s;
-        r.z = log_mode ? v[4 * u + 2] - ls : v[4 * u + 2] / s;
-        r.w = log_mode ? v[4 * u + 3] - ls : v[4 * u + 3] / s;
+        r.x = log_mode ? v[4 * u] - ls : v[4 * u] * inv;
+        r.y = log_mode ? v[4 * u + 1] - ls : v[4 * u + 1] * inv;
+        r.z = log_mode ? v[4 * u + 2] - ls : v[4 * u + 2] * inv;
+        r.w = log_mode ? v[4 * u + 3] - ls : v[4 * u + 3] * inv;
         st4<NT>(reinterpret_cast<float *>(o + j4), r);
       }
     }
@@ -381,7 +462,7 @@ __global__ void __launch_bounds__(256) softmax_block_kernel(const void *x, int e
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const int64_t j = col_of(t);
-      if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] / s);
+      if (j < cols) st(out, out_elem, base + j, log_mode ? v[t] - ls : v[t] * inv);
     }
   }
 }
@@ -410,9 +491,10 @@ __global__ void __launch_bounds__(256) softmax_long_kernel(const void *x, int el
   s = wave_sum(s);
   if (mrow) s = s > FLT_MIN ? s : (isnan(s) ? s : FLT_MIN);
   const float ls = log_mode ? logf(s) : 0.0f;
+  const float inv = 1.0f / s;
   for (int64_t j = lane; j < cols; j += 64) {
     float sh = val(j) - m;
-    st(out, out_elem, base + j, log_mode ? sh - ls : expf(sh) / s);
+    st(out, out_elem, base + j, log_mode ? sh - ls : expf(sh) * inv);
   }
 }
 
@@ -523,19 +605,43 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
       fill_zero(ctx, o, C * sizeof(float));
     } else {
       const bool vec = (xe == MI_F32) && (C % 4 == 0);
+      const bool full = vec && C % 1024 == 0 && C <= 8192 && R >= 1024;
       const bool wide = vec && C >= 1024;
       const int64_t cw = wide ? 1024 : (vec ? 256 : 64);
       const int64_t tiles = (C + cw - 1) / cw;
-      // About 2048 blocks (512 for the wide kernel, whose blocks read 4 KB a
-      // row step and fold 8 rows at a time: fewer, longer row ranges keep
-      // the partials -- written and re-read by the fold -- small).
-      const int64_t target = wide ? 512 : 2048;
+      // About 2048 blocks, eight a CU, so the row ranges' loads keep HBM
+      // busy; the partials (written and re-read by the fold) stay a few
+      // percent of the input.
+      const int64_t target = 2048;
       int64_t splits = (target + tiles - 1) / tiles;
       int64_t max_splits = (R + 15) / 16;
       if (splits > max_splits) splits = max_splits;
       if (splits < 1) splits = 1;
       const int64_t rps = (R + splits - 1) / splits;
       splits = (R + rps - 1) / rps;
+      if (full) {
+        // Whole-row blocks: 256 row ranges (one block a CU).
+        splits = R < 256 ? R : 256;
+        const int64_t r2 = (R + splits - 1) / splits;
+        splits = (R + r2 - 1) / r2;
+        float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(splits * C) * sizeof(float)));
+        if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "reduce scratch"); }
+        const float *xf = static_cast<const float *>(xp);
+        const bool nt = R * C * 4 >= kStreamBytes;
+        const unsigned g = static_cast<unsigned>(splits);
+        switch (C / 1024) {
+#define MI_RF(Q) case Q: if (nt) reduce_rows_full<true, Q><<<g, 256, 0, ctx->stream>>>(xf, part, R, C, r2, op); \
+                         else reduce_rows_full<false, Q><<<g, 256, 0, ctx->stream>>>(xf, part, R, C, r2, op); break;
+          MI_RF(1) MI_RF(2) MI_RF(3) MI_RF(4) MI_RF(5) MI_RF(6) MI_RF(7) MI_RF(8)
+#undef MI_RF
+        }
+        fold_partials_kernel<<<static_cast<unsigned>((C + 31) / 32), 512, 0, ctx->stream>>>(
+            part, splits, C, op, static_cast<float>(R), o, C, nullptr);
+        s = check_launch(ctx, "reduce");
+        if (s) { mi_free(ctx, id); return s; }
+        *out = id;
+        return MI_OK;
+      }
       float *part = static_cast<float *>(scratch(ctx, static_cast<size_t>(splits * C) * sizeof(float)));
       if (!part) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "reduce scratch"); }
       dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
@@ -544,7 +650,7 @@ extern "C" int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out) {
       else if (wide) reduce_rows_wide<false><<<grid, 256, 0, ctx->stream>>>(xf, part, R, C, rps, op);
       else if (vec) reduce_rows_part<true><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
       else reduce_rows_part<false><<<grid, 256, 0, ctx->stream>>>(xp, xe, part, R, C, rps, op);
-      fold_partials_kernel<<<static_cast<unsigned>((C + 63) / 64), 1024, 0, ctx->stream>>>(
+      fold_partials_kernel<<<static_cast<unsigned>((C + 31) / 32), 512, 0, ctx->stream>>>(
           part, splits, C, op, static_cast<float>(R), o, C, nullptr);
     }
   }
@@ -620,7 +726,9 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
       // Stream rows the size of the last-level cache and beyond.
       const bool nt = vec && R * C * 8 >= kStreamBytes;
       switch (vpt) {
-#define MI_SB(V) case V: if (nt) softmax_block_kernel<V, true, true><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+#define MI_SB(V) case V: if (nt && C == 1024 * V && log) softmax_block_kernel<V, true, true, true, 1><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+                         else if (nt && C == 1024 * V) softmax_block_kernel<V, true, true, true, 0><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
+                         else if (nt) softmax_block_kernel<V, true, true><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
                          else if (vec) softmax_block_kernel<V, true, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
                          else softmax_block_kernel<V, false, false><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); break;
         MI_SB(1) MI_SB(2) MI_SB(4) MI_SB(8) MI_SB(16)
@@ -858,7 +966,7 @@ extern "C" int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id d
       MI_LNB(1) MI_LNB(2) MI_LNB(4) MI_LNB(8) MI_LNB(16)
 #undef MI_LNB
     }
-    fold_partials_kernel<<<static_cast<unsigned>((2 * C + 63) / 64), 1024, 0, ctx->stream>>>(
+    fold_partials_kernel<<<static_cast<unsigned>((2 * C + 31) / 32), 512, 0, ctx->stream>>>(
         part, nb, 2 * C, MI_R_SUM, 1.0f, static_cast<float *>(bg->ptr), C, static_cast<float *>(bb->ptr));
   }
   s = check_launch(ctx, "layer_norm_backward");
