@@ -41,9 +41,9 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the bf16 4096^3 NN product, from two rocprofv3 --pmc
 # passes over `bench.py --no-cpu --no-models --steps 5 --warmup 1` (FETCH_SIZE,
 # then WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
-# a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,703 KiB
+# a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,922 KiB
 # read + 65,536 KiB written.  Only that configuration was measured.
-GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268527710}
+GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268756687}
 
 
 def cpu_baseline(n: int = 4096, seconds: float = 10.0) -> dict:
