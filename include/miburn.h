@@ -260,6 +260,19 @@ int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id dy,
  * ds = scale * p * (dp - sum_row(p * dp)).  F32 [rows, cols]. */
 int mi_softmax_backward(mi_ctx *ctx, mi_id p, mi_id dp, float scale,
                         mi_id *out);
+/* Cross-entropy against integer targets and its gradient in one pass over
+ * the logits: burn-nn's CrossEntropyLoss as the reference runs it --
+ * log_softmax (crates/burn-tt/src/ops.rs:5133-5166), the target's value
+ * gathered (pick_columns_native, ops.rs:1001), and under autodiff the
+ * gradient exp(logp) * s plus the one-hot -s scattered at the target
+ * (scatter_add_columns_native, ops.rs:1043), s = grad_scale (1 / rows for a
+ * mean).  logits F32 [rows, cols], cols <= 16384; targets I32, one per row.
+ * picked [rows, 1] = logp[row, target]; dlogits [rows, cols], the same bits
+ * as the composition (log-softmax, exp, MUL_ADD against the scattered
+ * one-hot).  A target outside [0, cols) is MI_E_DOMAIN at the next wait
+ * (picked 0, no one-hot term), as the gather and scatter report it. */
+int mi_log_softmax_ce(mi_ctx *ctx, mi_id logits, mi_id targets,
+                      float grad_scale, mi_id *picked, mi_id *dlogits);
 
 /* The optimizer step `param <- param - grad * lr` (burn-optim `Sgd`, no
  * momentum or decay; the reference applies it per parameter, and its traced

@@ -203,6 +203,19 @@ inline Tensor float_matmul(const Tensor &a, bool ta, const Tensor &b, bool tb, i
   return Tensor(a.ctx(), id, shape);
 }
 
+// Cross-entropy against integer targets and its gradient in one pass:
+// picked = logp at each row's target ([rows, 1]), dlogits = exp(logp) * s
+// minus s at the target.
+struct CrossEntropy {
+  Tensor picked, dlogits;
+};
+inline CrossEntropy log_softmax_ce(const Tensor &logits, const Tensor &targets, float grad_scale) {
+  mi_id p, d;
+  check(logits.ctx(), mi_log_softmax_ce(logits.ctx(), logits.use(), targets.use(), grad_scale, &p, &d),
+        "log_softmax_ce");
+  return {Tensor(logits.ctx(), p, {logits.rows(), 1}), Tensor(logits.ctx(), d, {logits.rows(), logits.cols()})};
+}
+
 // A Linear forward with an optional residual: residual + (x @ op(w) + bias),
 // the adds in the product's epilogue (null pointers omit a term).
 inline Tensor linear(const Tensor &x, const Tensor &w, bool tw, const Tensor *bias, const Tensor *residual,

@@ -1187,11 +1187,11 @@ static hipError_t launch_split_orient(const Plan &p, hipStream_t st) {
 }
 
 // F32 (or mixed) operands in the fast mode: the split kernel, 128 x 128 tiles
-// when they give at least half the CUs a tile, else 64 x 64.
+// when they give every CU a tile, else 64 x 64.
 template <typename SA, typename SB, typename TO>
 static hipError_t run_split(const Plan &p, hipStream_t st) {
   const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
-  if (tiles128 >= 128) {
+  if (tiles128 >= 256) {
     if (tiles_exactly(p, 128, 128, 64, 8)) return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, false>(p, st);
     return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, true>(p, st);
   }
@@ -1218,8 +1218,11 @@ template <typename SA, typename SB, typename TO>
 static hipError_t run_f32(const Plan &p, hipStream_t st) {
   using T = float;
   const int64_t al = (sizeof(SA) == 2 || sizeof(SB) == 2) ? 4 : 4;
+  // 128 x 128 tiles once they fill every CU; below that 64 x 64 tiles (four
+  // times the blocks) finish first -- e.g. a [256, 8192] product over k 2048
+  // in 117 us against 167 us on 128 tiles of 128 x 128.
   const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
-  if (tiles128 >= 128 && tiles_exactly(p, 128, 128, 32, al))
+  if (tiles128 >= 256 && tiles_exactly(p, 128, 128, 32, al))
     return launch_orient<T, SA, SB, TO, 128, 128, 2, 2, false>(p, st);
   if (tiles_exactly(p, 64, 64, 32, al))
     return launch_orient<T, SA, SB, TO, 64, 64, 2, 2, false>(p, st);

@@ -467,6 +467,125 @@ softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
   }
 }
 
+// Cross-entropy over a row of logits and its gradient in one pass: the row's
+// log-softmax logp_j = (z_j - m) - ln(sum_k e^(z_k - m)) exactly as the
+// log-softmax kernel forms it, the target's value logp_t written to
+// picked[row], and dz_j = e^(logp_j) * gscale + (j == t ? -gscale : 0) -- the
+// same two roundings as exp, then MUL_ADD against the scattered one-hot --
+// written to dz.  A target outside [0, cols) raises the index flag, picks 0
+// bits and adds no one-hot term (as pick_columns and scatter_add_columns).
+template <int VPT, bool VEC, bool NT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(VPT <= 8 ? 8 : 4)))
+log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gscale, float *picked, float *dz,
+                      uint32_t *flags) {
+  constexpr int T = 4 * VPT;
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * cols;
+  const int tid = threadIdx.x;
+  float v[T];
+  auto col_of = [&](int t) -> int64_t {
+    return VEC ? (static_cast<int64_t>(tid + 256 * (t >> 2)) * 4 + (t & 3)) : static_cast<int64_t>(tid + 256 * t);
+  };
+  if constexpr (VEC) {
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int64_t j4 = tid + 256 * u;
+      const float4 q = (j4 * 4 < cols) ? ld4<NT>(z + base + j4 * 4)
+                                       : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      v[4 * u] = q.x; v[4 * u + 1] = q.y; v[4 * u + 2] = q.z; v[4 * u + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = col_of(t);
+      v[t] = j < cols ? z[base + j] : -INFINITY;
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < T; ++t) m = max_nan(m, v[t]);
+  m = block_max(m, red);
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const float sh = v[t] - m;
+    s += col_of(t) < cols ? expf(sh) : 0.0f;
+    v[t] = sh;
+  }
+  s = block_sum(s, red);
+  const float ls = logf(s);
+  const int32_t target = tgt[row];
+  const bool in_range = target >= 0 && target < cols;
+  if (tid == 0 && !in_range) {
+    atomicOr(flags, FLAG_INDEX_RANGE);
+    picked[row] = 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = col_of(t);
+    v[t] = v[t] - ls;  // logp_j
+    if (j == target) picked[row] = v[t];
+    v[t] = __fadd_rn(j == target ? -gscale : 0.0f, __fmul_rn(expf(v[t]), gscale));
+  }
+  if constexpr (VEC) {
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int64_t j4 = tid + 256 * u;
+      if (j4 * 4 < cols) st4<NT>(dz + base + j4 * 4, make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]));
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t j = col_of(t);
+      if (j < cols) dz[base + j] = v[t];
+    }
+  }
+}
+
+// The same for rows of at most 1024 logits, a wavefront per row (lane l
+// holds columns l + 64 t), in the order of the wavefront softmax.
+template <int T>
+__global__ void __launch_bounds__(256) log_softmax_ce_wave_kernel(const float *z, const int32_t *tgt, int64_t rows,
+                                                                  int64_t cols, float gscale, float *picked, float *dz,
+                                                                  uint32_t *flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float v[T];
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    v[t] = j < cols ? z[base + j] : -INFINITY;
+    m = max_nan(m, v[t]);
+  }
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    const float sh = v[t] - m;
+    s += (j < cols) ? expf(sh) : 0.0f;
+    v[t] = sh;
+  }
+  s = wave_sum(s);
+  const float ls = logf(s);
+  const int32_t target = tgt[row];
+  if (lane == 0 && !(target >= 0 && target < cols)) {
+    atomicOr(flags, FLAG_INDEX_RANGE);
+    picked[row] = 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    const float lp = v[t] - ls;
+    if (j == target) picked[row] = lp;
+    if (j < cols) dz[base + j] = __fadd_rn(j == target ? -gscale : 0.0f, __fmul_rn(expf(lp), gscale));
+  }
+}
+
 // Rows too long for registers: three passes over the row (from L2).
 __global__ void __launch_bounds__(256) softmax_long_kernel(const void *x, int elem, const uint32_t *mask, int64_t mask_rows,
                                                            float scale, int log_mode, void *out, int out_elem,
@@ -972,6 +1091,58 @@ extern "C" int mi_layer_norm_backward(mi_ctx *ctx, mi_id x, mi_id gamma, mi_id d
   s = check_launch(ctx, "layer_norm_backward");
   if (s) { for (mi_id i : ids) mi_free(ctx, i); return s; }
   *dx = ids[0]; *dgamma = ids[1]; *dbeta = ids[2];
+  return MI_OK;
+}
+
+extern "C" int mi_log_softmax_ce(mi_ctx *ctx, mi_id logits, mi_id targets, float grad_scale, mi_id *picked,
+                                 mi_id *dlogits) {
+  MI_ENTER(ctx);
+  if (!picked || !dlogits) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, zb, logits);
+  MI_BUF(ctx, tb, targets);
+  if (zb->elem != MI_F32) return fail(ctx, MI_E_ARG, "log_softmax_ce of a %s buffer", elem_name(zb->elem));
+  const int64_t R = zb->rows, C = zb->cols;
+  if (tb->elem != MI_I32 || tb->numel() != R)
+    return fail(ctx, MI_E_ARG, "log_softmax_ce: targets must be %lld I32 values", (long long)R);
+  if (C < 1 || C > 16384)
+    return fail(ctx, MI_E_UNSUPPORTED, "log_softmax_ce: rows of %lld logits (1 to 16384)", (long long)C);
+  mi_id pid, did;
+  Buffer *pb, *db;
+  int s = new_buffer(ctx, R, 1, MI_F32, &pid, &pb);
+  if (s) return s;
+  s = new_buffer(ctx, R, C, MI_F32, &did, &db);
+  if (s) { mi_free(ctx, pid); return s; }
+  const float *zp = static_cast<const float *>(zb->ptr);
+  const int32_t *tp = static_cast<const int32_t *>(tb->ptr);
+  float *pp = static_cast<float *>(pb->ptr), *dp = static_cast<float *>(db->ptr);
+  if (R > 0 && C <= 1024) {
+    // The row lengths the log-softmax runs a wavefront per row on.
+    const unsigned g = grid_for(R, 4, INT32_MAX);
+    switch (pick_t(C)) {
+#define MI_CEW(T) case T: log_softmax_ce_wave_kernel<T><<<g, 256, 0, ctx->stream>>>(zp, tp, R, C, grad_scale, pp, dp, flags(ctx)); break;
+      MI_CEW(1) MI_CEW(2) MI_CEW(4) MI_CEW(8) MI_CEW(16)
+#undef MI_CEW
+    }
+    s = check_launch(ctx, "log_softmax_ce");
+    if (s) { mi_free(ctx, pid); mi_free(ctx, did); return s; }
+  } else if (R > 0) {
+    int vpt = 1;
+    while (1024 * vpt < C) vpt *= 2;
+    const bool vec = C % 4 == 0;
+    const bool nt = vec && R * C * 8 >= kStreamBytes;
+    const unsigned g = static_cast<unsigned>(R);
+    switch (vpt) {
+#define MI_CE(V) case V: if (nt) log_softmax_ce_kernel<V, true, true><<<g, 256, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); \
+                         else if (vec) log_softmax_ce_kernel<V, true, false><<<g, 256, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); \
+                         else log_softmax_ce_kernel<V, false, false><<<g, 256, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); break;
+      MI_CE(1) MI_CE(2) MI_CE(4) MI_CE(8) MI_CE(16)
+#undef MI_CE
+    }
+    s = check_launch(ctx, "log_softmax_ce");
+    if (s) { mi_free(ctx, pid); mi_free(ctx, did); return s; }
+  }
+  *picked = pid;
+  *dlogits = did;
   return MI_OK;
 }
 

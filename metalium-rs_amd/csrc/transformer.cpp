@@ -58,13 +58,6 @@ int fail_tf(const std::exception &e) {
   return MI_E_ARG;
 }
 
-// A [1, 1] F32 value (broadcast by the element-wise ops).
-Tensor scalar(mi_ctx *ctx, float v) {
-  uint32_t bits;
-  std::memcpy(&bits, &v, 4);
-  return burn::fill(ctx, {1, 1}, MI_F32, bits);
-}
-
 // Linear forward, x W + b (Burn's `Linear`, weight [d_in, d_out]), plus an
 // optional residual: residual + (x W + b), as Burn's float_add(residual,
 // linear(x)) rounds it.
@@ -112,20 +105,16 @@ Tensor step(mi_transformer *m, const Tensor &tokens, const Tensor &targets, int6
     x = linear(sv.g, L.w2, L.b2, &x);
   }
   Tensor z = linear(x, m->head_w, m->head_b);                       // [R, V]
-  Tensor logp = burn::softmax_rows(z, nullptr, 1.0f, true);
-  Tensor loss = burn::float_neg(burn::reduce_all(burn::pick_columns(logp, targets), MI_R_MEAN));
-
-  // Backward.  Cross-entropy through log_softmax: d logp = -1/R at each
-  // row's target (negation, mean and gather); dz = d logp - exp(logp) *
-  // rowsum(d logp), the row sum being -1/R exactly.
+  // Cross-entropy through log_softmax: the loss is -mean(logp[target]); its
+  // gradient d logp = -1/R at each row's target (negation, mean and gather)
+  // gives dz = d logp - exp(logp) * rowsum(d logp) = exp(logp) / R - onehot / R,
+  // formed in the same pass over the logits.
   const float inv = 1.0f / static_cast<float>(R);
-  uint32_t minus_inv;
-  const float mi = -inv;
-  std::memcpy(&minus_inv, &mi, 4);
-  Tensor onehot =
-      burn::scatter_add_columns(burn::fill(ctx, {R, V}, MI_F32, 0), targets, burn::fill(ctx, {R, 1}, MI_F32, minus_inv));
-  Tensor inv_t = scalar(ctx, inv);  // dz = onehot + exp(logp) * (1/R)
-  Tensor dz = burn::eltwise(MI_K_MUL_ADD, burn::float_exp(logp), &inv_t, &onehot);
+  burn::CrossEntropy ce = burn::log_softmax_ce(z, targets, inv);
+  Tensor loss = burn::float_neg(burn::reduce_all(ce.picked, MI_R_MEAN));
+
+  // Backward.
+  Tensor dz = ce.dlogits;
   // SGD (p <- p - grad * lr) runs once, in place, after the backward: the
   // gradients are collected here.
   std::vector<const Tensor *> upd_p;

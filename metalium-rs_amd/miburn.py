@@ -115,6 +115,7 @@ def _load() -> ctypes.CDLL:
         "mi_layer_norm": [P, U64, U64, U64, c_float, Ip],
         "mi_layer_norm_backward": [P, U64, U64, U64, U64, c_float, Ip, Ip, Ip],
         "mi_softmax_backward": [P, U64, U64, c_float, Ip],
+        "mi_log_softmax_ce": [P, U64, U64, c_float, Ip, Ip],
         "mi_sgd_update": [P, I64, ctypes.POINTER(U64), ctypes.POINTER(U64), c_float],
         "mi_argmax_rows": [P, U64, Ip],
         "mi_set_matmul_mode": [P, c_int],
@@ -268,6 +269,13 @@ class Engine:
     def linear(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, out_elem: int = F32) -> int:
         """residual + (x @ op(w) + bias) in one product; 0 omits a term."""
         return self._out(self._lib.mi_linear, x, w, int(w_t), bias, residual, out_elem)
+
+    def log_softmax_ce(self, logits: int, targets: int, grad_scale: float):
+        """(picked, dlogits): logp at each row's target and the cross-entropy
+        gradient exp(logp) * grad_scale - grad_scale * onehot, in one pass."""
+        a, b = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(self._lib.mi_log_softmax_ce(self.ctx, logits, targets, grad_scale, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
 
     def matmul_items(self, a: int, a_t: bool, a_at, b: int, b_t: bool, b_at, groups: int, per_group: int, m: int,
                      k: int, n: int, out: int, out_at) -> None:

@@ -245,3 +245,50 @@ def test_empty_has_shape_and_kind(engine):
     i = engine.empty(7, 9, BF16)
     assert engine.metadata(i) == (7, 9, BF16)
     engine.free(i)
+
+
+# ------------------------------------------------------ fused cross-entropy
+def ce_composition(engine, iz, it, rows, cols, inv):
+    """The composition the fused kernel replaces, op by op on the engine:
+    log-softmax, gather at the target, exp, one-hot scattered, MUL_ADD."""
+    logp = engine.softmax_rows(iz, 0, 1.0, True)
+    picked = engine.download(engine.pick_columns(logp, it))
+    minus = np.full((rows, 1), -inv, np.float32)
+    onehot = engine.scatter_add_columns(engine.fill(rows, cols, F32, 0), it, engine.upload(minus))
+    scale = engine.upload(np.full((1, 1), inv, np.float32))
+    dz = engine.download(engine.eltwise_op_as("MUL_ADD", engine.eltwise_op_as("EXP", logp), scale, onehot))
+    return picked, dz
+
+
+@pytest.mark.parametrize("rows,cols", [(2048, 8192), (64, 10), (37, 1001), (16, 16384), (5, 1024)])
+def test_log_softmax_ce_equals_composition(engine, rows, cols):
+    z = rnd(rows, cols, scale=3.0)
+    tgt = RNG.integers(0, cols, (rows, 1)).astype(np.int32)
+    iz, it = engine.upload(z), engine.upload_i32(tgt)
+    inv = np.float32(1.0 / rows)
+    ip, idz = engine.log_softmax_ce(iz, it, float(inv))
+    got_p, got_dz = engine.download(ip), engine.download(idz)
+    want_p, want_dz = ce_composition(engine, iz, it, rows, cols, float(inv))
+    same_bits(got_p, want_p)
+    same_bits(got_dz, want_dz)
+    # And against float64: logp at the target, softmax / rows minus the one-hot.
+    z64 = z.astype(np.float64)
+    lse = np.log(np.exp(z64 - z64.max(1, keepdims=True)).sum(1, keepdims=True)) + z64.max(1, keepdims=True)
+    logp = z64 - lse
+    assert np.allclose(got_p[:, 0], logp[np.arange(rows), tgt[:, 0]], rtol=1e-5, atol=1e-5)
+    ref = np.exp(logp) / rows
+    ref[np.arange(rows), tgt[:, 0]] -= 1.0 / rows
+    assert np.all(np.abs(got_dz - ref) <= 1e-5 * np.abs(ref) + 1e-6 / rows)
+
+
+def test_log_softmax_ce_target_out_of_range_is_domain(engine):
+    engine.sync()
+    iz = engine.upload(rnd(4, 64))
+    it = engine.upload_i32(np.array([[1], [64], [3], [-1]], np.int32))
+    ip, idz = engine.log_softmax_ce(iz, it, 0.25)
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()
+    p = engine.download(ip)
+    assert p[1, 0] == 0.0 and p[3, 0] == 0.0
