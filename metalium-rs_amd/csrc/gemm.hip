@@ -1303,13 +1303,18 @@ static void launch_gemv(const Plan &p, hipStream_t st) {
 }
 
 // Split-K for few output tiles over a long k: enough (tile, slice) pairs to
-// give most CUs work, each slice at least 256 deep.
+// give most CUs work.  Measured on the training steps' products: with 64 or
+// more tiles, slicing a k below 1024 costs more (the reduce launch) than it
+// gains and slices of 256 suit k = 1024; k >= 2048, or a handful of tiles,
+// takes slices down to 128 (a [256, 256] x k 2048 product: 72 us unsliced,
+// 16 us in 16 slices; the MLP's [64, 784] x [784, 128] gains from 6).
 static int splitk_slices(const Plan &p) {
   if (p.batch != 1) return 1;
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
   if (tiles >= 512 || p.K < 256) return 1;
+  if (p.K < 1024 && tiles >= 64) return 1;
   int64_t s = (1024 + tiles - 1) / tiles;
-  const int64_t smax = p.K / 128;
+  const int64_t smax = (p.K >= 2048 || tiles < 64) ? p.K / 128 : p.K / 256;
   if (s > smax) s = smax;
   if (s > 32) s = 32;
   return s < 2 ? 1 : static_cast<int>(s);
