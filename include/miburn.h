@@ -140,6 +140,14 @@ int mi_matmul_items(mi_ctx *ctx, mi_id a, int a_transposed,
                     int64_t m, int64_t k, int64_t n, mi_id out,
                     const int64_t out_at[3]);
 
+/* op(A) @ op(B) left as the engine's split-K slices: `out` is [S * m, n], S
+ * partial products over consecutive k ranges (S = 1: the product itself),
+ * whose sum in slice order is what mi_matmul returns.  For a consumer that
+ * folds the slices itself (mi_sgd_update: a weight gradient x^T dy over many
+ * rows), so no reduce launch runs.  No Engine counterpart; F32 result. */
+int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
+                     int b_transposed, mi_id *out, int64_t *slices);
+
 /* A linear layer's forward with its residual add in the product's epilogue:
  * out = residual + (x @ op(w) + bias), each sum rounded to F32 in that order,
  * so the result is bit-identical to mi_matmul followed by the two broadcast
@@ -278,8 +286,10 @@ int mi_log_softmax_ce(mi_ctx *ctx, mi_id logits, mi_id targets,
  * momentum or decay; the reference applies it per parameter, and its traced
  * training step writes the weights in place, crates/burn-tt/src/trace.rs:
  * 989-1010) for `count` parameters in place, in one launch per 48.  params[i]
- * and grads[i] are F32 buffers of equal element count (grads[i] may have any
- * [rows, cols] folding); the same bits as the two-op form. */
+ * and grads[i] are F32 buffers; grads[i] holds the parameter's element count
+ * (any [rows, cols] folding) or S <= 64 times it -- S stacked slices, as
+ * mi_matmul_slices returns them, whose sum in slice order is the gradient.
+ * The same bits as the reduce-then-two-op form. */
 int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params,
                   const mi_id *grads, float lr);
 

@@ -216,6 +216,15 @@ inline CrossEntropy log_softmax_ce(const Tensor &logits, const Tensor &targets, 
   return {Tensor(logits.ctx(), p, {logits.rows(), 1}), Tensor(logits.ctx(), d, {logits.rows(), logits.cols()})};
 }
 
+// A product left as its split-K slices ([S * m, n]; S = 1: the product),
+// for mi_sgd_update to fold.
+inline Tensor matmul_slices(const Tensor &a, bool ta, const Tensor &b, bool tb) {
+  mi_id id;
+  int64_t S = 1;
+  check(a.ctx(), mi_matmul_slices(a.ctx(), a.use(), ta, b.use(), tb, &id, &S), "matmul_slices");
+  return Tensor(a.ctx(), id, {S * (ta ? a.cols() : a.rows()), tb ? b.rows() : b.cols()});
+}
+
 // A Linear forward with an optional residual: residual + (x @ op(w) + bias),
 // the adds in the product's epilogue (null pointers omit a term).
 inline Tensor linear(const Tensor &x, const Tensor &w, bool tw, const Tensor *bias, const Tensor *residual,

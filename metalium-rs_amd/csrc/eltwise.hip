@@ -680,6 +680,8 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
 // run of blocks; a block finds its parameter by a scan of the (at most
 // SGD_MAX_PARAMS) block offsets in the kernel argument, then updates 4 float4
 // per thread.  Bits equal the two-op form: grad * lr rounded, then subtracted.
+// A gradient of S stacked slices (a split-K product's partials) is their sum
+// in slice order first -- the bits split-K's own reduce gives.
 namespace mi {
 constexpr int SGD_MAX_PARAMS = 48;
 constexpr int SGD_BLOCK_ELEMS = 256 * 16;
@@ -688,6 +690,7 @@ struct SgdList {
   float *p[SGD_MAX_PARAMS];
   const float *g[SGD_MAX_PARAMS];
   int64_t n[SGD_MAX_PARAMS];
+  int S[SGD_MAX_PARAMS];
   int64_t first_block[SGD_MAX_PARAMS + 1];
   int count;
 };
@@ -698,20 +701,29 @@ __global__ void __launch_bounds__(256) sgd_kernel(SgdList L, float lr) {
   float *p = L.p[i];
   const float *g = L.g[i];
   const int64_t n = L.n[i];
+  const int S = L.S[i];
   const int64_t base = (static_cast<int64_t>(blockIdx.x) - L.first_block[i]) * SGD_BLOCK_ELEMS;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int64_t e = base + (static_cast<int64_t>(u) * 256 + threadIdx.x) * 4;
-    if (e + 3 < n) {
+    if (e + 3 < n && (S == 1 || (n & 3) == 0)) {  // slices 16-byte aligned too
       float4 pv = *reinterpret_cast<const float4 *>(p + e);
-      const float4 gv = *reinterpret_cast<const float4 *>(g + e);
+      float4 gv = *reinterpret_cast<const float4 *>(g + e);
+      for (int z = 1; z < S; ++z) {
+        const float4 q = *reinterpret_cast<const float4 *>(g + z * n + e);
+        gv.x += q.x; gv.y += q.y; gv.z += q.z; gv.w += q.w;
+      }
       pv.x = __fsub_rn(pv.x, __fmul_rn(gv.x, lr));
       pv.y = __fsub_rn(pv.y, __fmul_rn(gv.y, lr));
       pv.z = __fsub_rn(pv.z, __fmul_rn(gv.z, lr));
       pv.w = __fsub_rn(pv.w, __fmul_rn(gv.w, lr));
       *reinterpret_cast<float4 *>(p + e) = pv;
     } else {
-      for (int64_t k = e; k < n && k < e + 4; ++k) p[k] = __fsub_rn(p[k], __fmul_rn(g[k], lr));
+      for (int64_t k = e; k < n && k < e + 4; ++k) {
+        float gk = g[k];
+        for (int z = 1; z < S; ++z) gk += g[z * n + k];
+        p[k] = __fsub_rn(p[k], __fmul_rn(gk, lr));
+      }
     }
   }
 }
@@ -736,10 +748,12 @@ extern "C" int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params, co
     const Buffer *gb = lookup(ctx, grads[i]);
     if (!pb || !gb) return fail(ctx, MI_E_ID, "sgd_update: unknown id in entry %lld", (long long)i);
     if (pb->elem != MI_F32 || gb->elem != MI_F32) return fail(ctx, MI_E_ARG, "sgd_update: entry %lld is not F32", (long long)i);
-    const int64_t n = pb->rows * pb->cols;
-    if (gb->rows * gb->cols != n)
-      return fail(ctx, MI_E_ARG, "sgd_update: entry %lld: %lld parameters, %lld gradients", (long long)i, (long long)n,
-                  (long long)(gb->rows * gb->cols));
+    const int64_t n = pb->rows * pb->cols, ng = gb->rows * gb->cols;
+    if (n > 0 && (ng % n || ng / n < 1 || ng / n > 64))
+      return fail(ctx, MI_E_ARG, "sgd_update: entry %lld: %lld parameters, %lld gradients (1 to 64 slices)",
+                  (long long)i, (long long)n, (long long)ng);
+    if (n == 0 && ng != 0)
+      return fail(ctx, MI_E_ARG, "sgd_update: entry %lld: no parameters, %lld gradients", (long long)i, (long long)ng);
     if (params[i] == grads[i]) return fail(ctx, MI_E_ARG, "sgd_update: entry %lld updates a buffer by itself", (long long)i);
     if (n == 0) continue;
     const int64_t nb = (n + SGD_BLOCK_ELEMS - 1) / SGD_BLOCK_ELEMS;
@@ -750,6 +764,7 @@ extern "C" int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params, co
     L.p[L.count] = static_cast<float *>(pb->ptr);
     L.g[L.count] = static_cast<const float *>(gb->ptr);
     L.n[L.count] = n;
+    L.S[L.count] = static_cast<int>(ng / n);
     L.first_block[L.count] = blocks;
     ++L.count;
     blocks += nb;

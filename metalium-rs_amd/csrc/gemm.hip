@@ -1325,24 +1325,35 @@ static hipError_t run_splitk_kernels(const Plan &p, hipStream_t st) {
   return launch_orient<T, SA, SB, float, 64, 64, 2, 2, true>(p, st);
 }
 
-static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
+// Slice length (on k-tile boundaries of both precisions) and the slice count
+// it gives for p.splits requested slices.
+static void plan_slices(Plan &p) {
   const int S = p.splits;
-  const int64_t align = 64;  // slice boundaries on k-tile boundaries of both precisions
+  const int64_t align = 64;
   p.kc = ((p.K + S - 1) / S + align - 1) / align * align;
   p.splits = static_cast<int>((p.K + p.kc - 1) / p.kc);
+}
+
+// The slices' raw partial products, [S, M, N] packed at part.
+static hipError_t run_slices(const Plan &p, float *part, hipStream_t st) {
+  Plan q = p;
+  q.c = part;
+  q.eo = MI_F32;
+  q.bias = q.resid = nullptr;
+  q.ldc = 0;
+  if (q.ea == MI_BF16 && q.eb == MI_BF16) return run_splitk_kernels<uint16_t, uint16_t, uint16_t>(q, st);
+  if (q.ea == MI_F32 && q.eb == MI_F32) return run_splitk_kernels<float, float, float>(q, st);
+  if (q.ea == MI_F32) return run_splitk_kernels<float, float, uint16_t>(q, st);
+  return run_splitk_kernels<float, uint16_t, float>(q, st);
+}
+
+static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
+  plan_slices(p);
   void *final_c = p.c;
   const int eo = p.eo;
   const float *bias = p.bias, *resid = p.resid;
   const int64_t ldc = p.ldc > 0 ? p.ldc : p.N;
-  p.c = part;
-  p.eo = MI_F32;
-  p.bias = p.resid = nullptr;  // the slices write raw partial products, [S, M, N] packed
-  p.ldc = 0;
-  hipError_t e;
-  if (p.ea == MI_BF16 && p.eb == MI_BF16) e = run_splitk_kernels<uint16_t, uint16_t, uint16_t>(p, st);
-  else if (p.ea == MI_F32 && p.eb == MI_F32) e = run_splitk_kernels<float, float, float>(p, st);
-  else if (p.ea == MI_F32) e = run_splitk_kernels<float, float, uint16_t>(p, st);
-  else e = run_splitk_kernels<float, uint16_t, float>(p, st);
+  hipError_t e = run_slices(p, part, st);
   if (e != hipSuccess) return e;
   const int64_t mn = p.M * p.N;
   const unsigned g = static_cast<unsigned>((mn + 255) / 256);
@@ -1505,6 +1516,49 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
 extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out);
+}
+
+extern "C" int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, mi_id *out,
+                                int64_t *slices) {
+  MI_ENTER(ctx);
+  if (!out || !slices) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, A, a);
+  MI_BUF(ctx, B, b);
+  if (!elem_float(A->elem) || !elem_float(B->elem))
+    return fail(ctx, MI_E_ARG, "matmul_slices of %s and %s", elem_name(A->elem), elem_name(B->elem));
+  Plan p;
+  p.ta = a_transposed != 0; p.tb = b_transposed != 0;
+  p.fast = ctx->matmul_mode == MI_MATMUL_FAST;
+  p.ea = A->elem; p.eb = B->elem; p.eo = MI_F32;
+  p.a = A->ptr; p.b = B->ptr;
+  p.M = p.ta ? A->cols : A->rows;
+  p.K = p.ta ? A->rows : A->cols;
+  const int64_t kb = p.tb ? B->cols : B->rows;
+  p.N = p.tb ? B->rows : B->cols;
+  if (kb != p.K)
+    return fail(ctx, MI_E_ARG, "matmul_slices: op(A) is [%lld, %lld], op(B) is [%lld, %lld]", (long long)p.M,
+                (long long)p.K, (long long)kb, (long long)p.N);
+  p.batch = 1; p.sa = p.sb = p.sc = 0;
+  p.lda = A->cols; p.ldb = B->cols;
+  p.splits = (p.M > 0 && p.N > 0 && p.K > 0 && !gemv_fits(p)) ? splitk_slices(p) : 1;
+  if (p.splits <= 1) {
+    *slices = 1;
+    return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, MI_F32, out);
+  }
+  plan_slices(p);
+  mi_id id; Buffer *cb;
+  int s = new_buffer(ctx, p.splits * p.M, p.N, MI_F32, &id, &cb);
+  if (s) return s;
+  hipError_t e = run_slices(p, static_cast<float *>(cb->ptr), ctx->stream);
+  if (e != hipSuccess) {
+    mi_free(ctx, id);
+    return fail(ctx, MI_E_HIP, "matmul_slices launch: %s", hipGetErrorString(e));
+  }
+  s = check_launch(ctx, "matmul_slices");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  *slices = p.splits;
+  return MI_OK;
 }
 
 extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias, mi_id residual, int out_elem,

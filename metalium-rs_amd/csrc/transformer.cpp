@@ -124,9 +124,9 @@ Tensor step(mi_transformer *m, const Tensor &tokens, const Tensor &targets, int6
     upd_g.push_back(grad);
   };
   // Linear's backward (ops.rs:5006-5029): dW = x^T dy, db = sum_rows(dy),
-  // dx = dy W^T.
+  // dx = dy W^T.  dW is left as its split-K slices: the SGD step folds them.
   auto linear_back = [&](const Tensor &xin, const Tensor &dy, const Tensor &w, const Tensor &b) {
-    Tensor dw = burn::float_matmul(xin, true, dy, false);
+    Tensor dw = burn::matmul_slices(xin, true, dy, false);
     Tensor db = burn::reduce(dy, MI_R_SUM, MI_AXIS_ROWS);
     Tensor dx = burn::float_matmul(dy, false, w, true);
     sgd(w, dw);

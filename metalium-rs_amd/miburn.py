@@ -99,6 +99,7 @@ def _load() -> ctypes.CDLL:
         "mi_matmul": [P, U64, c_int, U64, c_int, c_int, Ip],
         "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
         "mi_linear": [P, U64, U64, c_int, U64, U64, c_int, Ip],
+        "mi_matmul_slices": [P, U64, c_int, U64, c_int, Ip, ctypes.POINTER(I64)],
         "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
                             I64, U64, ctypes.POINTER(I64)],
         "mi_matmul_blocks": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, I64, I64, c_int, Ip],
@@ -265,6 +266,13 @@ class Engine:
     # -- ops ---------------------------------------------------------------
     def matmul_dram(self, a: int, a_t: bool, b: int, b_t: bool, out_elem: int = F32) -> int:
         return self._out(self._lib.mi_matmul, a, int(a_t), b, int(b_t), out_elem)
+
+    def matmul_slices(self, a: int, a_t: bool, b: int, b_t: bool):
+        """(id, S): the product as S stacked split-K slices [S * m, n]."""
+        out, sl = ctypes.c_uint64(), ctypes.c_int64()
+        self._check(self._lib.mi_matmul_slices(self.ctx, a, int(a_t), b, int(b_t), ctypes.byref(out),
+                                               ctypes.byref(sl)))
+        return out.value, sl.value
 
     def linear(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, out_elem: int = F32) -> int:
         """residual + (x @ op(w) + bias) in one product; 0 omits a term."""

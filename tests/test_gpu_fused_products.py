@@ -292,3 +292,45 @@ def test_log_softmax_ce_target_out_of_range_is_domain(engine):
     engine.sync()
     p = engine.download(ip)
     assert p[1, 0] == 0.0 and p[3, 0] == 0.0
+
+
+# --------------------------------------------- split-K slices folded by SGD
+@pytest.mark.parametrize("m,n,k,ta,sliced", [(256, 256, 2048, True, True), (1024, 256, 2048, True, True),
+                                             (256, 768, 2048, True, True), (64, 128, 784, False, True),
+                                             (2048, 1024, 256, False, False)])
+def test_matmul_slices_sum_to_the_product(engine, m, n, k, ta, sliced):
+    a = rnd(k, m) if ta else rnd(m, k)
+    b = rnd(k, n)
+    ia, ib = engine.upload(a), engine.upload(b)
+    sid, S = engine.matmul_slices(ia, ta, ib, False)
+    parts = engine.download(sid)
+    assert parts.shape == (S * m, n)
+    total = parts[:m].copy()
+    for z in range(1, S):  # slice order, F32 adds: split-K's own reduce
+        total = (total + parts[z * m:(z + 1) * m]).astype(np.float32)
+    same_bits(total, engine.download(engine.matmul_dram(ia, ta, ib, False)))
+    # Long-k weight-gradient shapes are sliced; a full wave of tiles is one slice.
+    assert (S > 1) == sliced
+
+
+def test_sgd_folds_stacked_slices(engine):
+    lr = np.float32(0.05)
+    # A weight gradient from slices, against the same update from the reduced product.
+    x, dy = rnd(2048, 256), rnd(2048, 256)
+    ix, idy = engine.upload(x), engine.upload(dy)
+    sid, S = engine.matmul_slices(ix, True, idy, False)
+    assert S > 1
+    p = rnd(256, 256)
+    p1, p2 = engine.upload(p), engine.upload(p)
+    engine.sgd_update([p1], [sid], float(lr))
+    engine.sgd_update([p2], [engine.matmul_dram(ix, True, idy, False)], float(lr))
+    same_bits(engine.download(p1), engine.download(p2))
+    # Widths that are not a multiple of 4 take the scalar path.
+    q = rnd(1, 7)
+    g = rnd(3, 7)
+    iq = engine.upload(q)
+    engine.sgd_update([iq], [engine.upload(g)], float(lr))
+    gsum = ((g[0] + g[1]).astype(np.float32) + g[2]).astype(np.float32)
+    same_bits(engine.download(iq), (q - gsum * lr).astype(np.float32))
+    with pytest.raises(miburn.MiError):
+        engine.sgd_update([iq], [engine.upload(rnd(1, 10))], 0.1)  # 10 gradients for 7 parameters
