@@ -467,6 +467,74 @@ softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
   }
 }
 
+// One row of exactly 1024 VPT F32 columns held in registers (thread t holds
+// float4 lanes t + 256 u), unmasked: the softmax_block_kernel<VPT, true, true,
+// true, LOG> arithmetic in the same order, so the same bits for every row
+// without a NaN.  The row's max ignores NaN (v_max / v_max3, one instruction
+// per element or two instead of six for the NaN-ranking max): a NaN makes the
+// sum NaN and so every output of its row NaN, as when the max is NaN.  The
+// max and the sum fold through separate LDS slots, one barrier each.
+template <int VPT, int LOG>
+__device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float scale, float *o, float (&red)[2][4]) {
+  constexpr int T = 4 * VPT;
+  const int tid = threadIdx.x, w = tid >> 6;
+  float v[T];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    v[4 * u] = q[u].x; v[4 * u + 1] = q[u].y; v[4 * u + 2] = q[u].z; v[4 * u + 3] = q[u].w;
+  }
+  if (scale != 1.0f) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) v[t] = v[t] * scale;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < T; t += 2) m = fmaxf(fmaxf(m, v[t]), v[t + 1]);
+  m = wave_max(m);
+  if ((tid & 63) == 0) red[0][w] = m;
+  __syncthreads();
+  m = max_nan(max_nan(red[0][0], red[0][1]), max_nan(red[0][2], red[0][3]));
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const float sh = v[t] - m;
+    const float e = expf(sh);
+    v[t] = LOG ? sh : e;
+    s += e;
+  }
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[1][w] = s;
+  __syncthreads();
+  s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  const float ls = LOG ? logf(s) : 0.0f;
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    float4 r;
+    r.x = LOG ? v[4 * u] - ls : v[4 * u] * inv;
+    r.y = LOG ? v[4 * u + 1] - ls : v[4 * u + 1] * inv;
+    r.z = LOG ? v[4 * u + 2] - ls : v[4 * u + 2] * inv;
+    r.w = LOG ? v[4 * u + 3] - ls : v[4 * u + 3] * inv;
+    st4<true>(o + static_cast<int64_t>(tid + 256 * u) * 4, r);
+  }
+}
+
+// Unmasked F32 rows of exactly 1024 VPT columns, one block per row, eight
+// blocks to a CU.  (Blocks that walk several rows with the next row's loads
+// in flight under the current row's folds measured the same.)
+template <int VPT, int LOG>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
+softmax_row_kernel(const float *x, float scale, float *out) {
+  constexpr int64_t C = 1024 * VPT;
+  __shared__ float red[2][4];
+  const int64_t lane = static_cast<int64_t>(threadIdx.x) * 4;
+  const int64_t row = blockIdx.x;
+  float4 a[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) a[u] = ld4<true>(x + row * C + lane + 1024 * u);
+  softmax_row_regs<VPT, LOG>(a, scale, out + row * C, red);
+}
+
 // Cross-entropy over a row of logits and its gradient in one pass: the row's
 // log-softmax logp_j = (z_j - m) - ln(sum_k e^(z_k - m)) exactly as the
 // log-softmax kernel forms it, the target's value logp_t written to
@@ -502,9 +570,11 @@ log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gs
       v[t] = j < cols ? z[base + j] : -INFINITY;
     }
   }
+  // The max ignores NaN (two elements an instruction): a NaN logit makes the
+  // sum, and so every value of its row, NaN, as a NaN max would.
   float m = -INFINITY;
 #pragma unroll
-  for (int t = 0; t < T; ++t) m = max_nan(m, v[t]);
+  for (int t = 0; t < T; t += 2) m = fmaxf(fmaxf(m, v[t]), v[t + 1]);
   m = block_max(m, red);
   float s = 0.0f;
 #pragma unroll
@@ -844,6 +914,16 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
       const unsigned rows = static_cast<unsigned>(R);
       // Stream rows the size of the last-level cache and beyond.
       const bool nt = vec && R * C * 8 >= kStreamBytes;
+      if (nt && C == 1024 * vpt && vpt >= 2 && vpt <= 8 && !mp && out_elem == MI_F32) {
+        const float *xf = static_cast<const float *>(xp);
+        float *of = static_cast<float *>(ob->ptr);
+        switch (vpt * 2 + (log ? 1 : 0)) {
+#define MI_SL(V) case 2 * V: softmax_row_kernel<V, 0><<<rows, 256, 0, ctx->stream>>>(xf, scale, of); break; \
+                 case 2 * V + 1: softmax_row_kernel<V, 1><<<rows, 256, 0, ctx->stream>>>(xf, scale, of); break;
+          MI_SL(2) MI_SL(4) MI_SL(8)
+#undef MI_SL
+        }
+      } else
       switch (vpt) {
 #define MI_SB(V) case V: if (nt && C == 1024 * V && log) softmax_block_kernel<V, true, true, true, 1><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \
                          else if (nt && C == 1024 * V) softmax_block_kernel<V, true, true, true, 0><<<rows, 256, 0, ctx->stream>>>(xp, xe, mp, mrows, scale, log, ob->ptr, out_elem, C); \

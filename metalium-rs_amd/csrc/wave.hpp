@@ -10,16 +10,16 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// NaN ranks above every number, so it propagates (a NaN `a` first, then a NaN
+// `b`); of two equal numbers `a` is kept.  Written as selects: early returns
+// compile to a divergent branch per call.
 __device__ __forceinline__ float max_nan(float a, float b) {
-  // NaN ranks above every number, so it propagates.
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  return b > a ? b : a;
+  const float m = b > a ? b : a;
+  return isnan(a) ? a : (isnan(b) ? b : m);
 }
 __device__ __forceinline__ float min_nan(float a, float b) {
-  if (isnan(a)) return a;
-  if (isnan(b)) return b;
-  return b < a ? b : a;
+  const float m = b < a ? b : a;
+  return isnan(a) ? a : (isnan(b) ? b : m);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -281,6 +281,26 @@ def test_log_softmax_ce_equals_composition(engine, rows, cols):
     assert np.all(np.abs(got_dz - ref) <= 1e-5 * np.abs(ref) + 1e-6 / rows)
 
 
+@pytest.mark.parametrize("rows,cols", [(2048, 8192), (16, 16384)])
+def test_log_softmax_ce_nan_rows(engine, rows, cols):
+    # A NaN or +inf logit makes its row's loss and gradient NaN, as in the
+    # composition; the other rows keep their bits.
+    z = rnd(rows, cols, scale=3.0)
+    z[1, 3], z[2, 9] = np.nan, np.inf
+    tgt = RNG.integers(0, cols, (rows, 1)).astype(np.int32)
+    iz, it = engine.upload(z), engine.upload_i32(tgt)
+    inv = float(np.float32(1.0 / rows))
+    ip, idz = engine.log_softmax_ce(iz, it, inv)
+    got_p, got_dz = engine.download(ip), engine.download(idz)
+    want_p, want_dz = ce_composition(engine, iz, it, rows, cols, inv)
+    bad = np.zeros(rows, bool)
+    bad[1:3] = True
+    assert np.isnan(got_p[bad]).all() and np.isnan(got_dz[bad]).all()
+    assert np.isnan(want_p[bad]).all() and np.isnan(want_dz[bad]).all()
+    same_bits(got_p[~bad], want_p[~bad])
+    same_bits(got_dz[~bad], want_dz[~bad])
+
+
 def test_log_softmax_ce_target_out_of_range_is_domain(engine):
     engine.sync()
     iz = engine.upload(rnd(4, 64))

@@ -254,6 +254,27 @@ def test_softmax(engine, cols, log):
         assert np.allclose(got.sum(axis=1), 1.0, atol=cols * 6e-8 + 1e-6)
 
 
+@pytest.mark.parametrize("rows,cols", [(2600, 8192), (4100, 4096), (8200, 2048)])
+@pytest.mark.parametrize("log,scale", [(False, 1.0), (True, 1.0), (False, 0.125)])
+def test_softmax_streamed_rows(engine, rows, cols, log, scale):
+    # Inputs past the streaming threshold (2 x 4 x rows x cols >= 128 MiB) with
+    # more rows than one block per row covers in a round: each block walks
+    # rows with the next row's loads in flight.  Rows are independent, so a
+    # subset run through the one-block-per-row kernel has the same bits.
+    x = rnd(rows, cols, scale=3.0)
+    x[1, 5] = np.nan      # a NaN makes its whole row NaN
+    x[2, 7] = np.inf      # so does +inf (inf - inf)
+    x[3, :] = -np.inf     # and a row of -inf
+    full = engine.download(engine.softmax_rows(engine.upload(x), log=log, scale=scale))
+    sel = np.r_[0:40, rows // 2:rows // 2 + 40, rows - 40:rows]
+    part = engine.download(engine.softmax_rows(engine.upload(np.ascontiguousarray(x[sel])), log=log, scale=scale))
+    finite = np.isfinite(x[sel]).all(axis=1)
+    same_bits(full[sel][finite], part[finite])
+    assert np.isnan(full[1:4]).all()
+    want = orc.softmax_rows(x[sel], log=log, scale=scale)
+    close(full[sel], want, rtol=1e-5, atol=1e-6 if log else 1e-12)
+
+
 def test_softmax_masked_scaled(engine):
     R, C = 36, 200
     x = rnd(R, C)
