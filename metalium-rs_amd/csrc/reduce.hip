@@ -474,9 +474,21 @@ softmax_block_kernel(const void *x, int elem, const uint32_t *mask,
 // per element or two instead of six for the NaN-ranking max): a NaN makes the
 // sum NaN and so every output of its row NaN, as when the max is NaN.  The
 // max and the sum fold through separate LDS slots, one barrier each.
-template <int VPT, int LOG>
-__device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float scale, float *o, float (&red)[2][4]) {
-  constexpr int T = 4 * VPT;
+template <int N>
+__device__ __forceinline__ float tree_sum(const float *r) {
+  if constexpr (N == 1) return r[0];
+  else return tree_sum<N / 2>(r) + tree_sum<N / 2>(r + N / 2);
+}
+template <int N>
+__device__ __forceinline__ float tree_max(const float *r) {
+  if constexpr (N == 1) return r[0];
+  else return fmaxf(tree_max<N / 2>(r), tree_max<N / 2>(r + N / 2));
+}
+
+template <int VPT, int LOG, int NTH, bool NT>
+__device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float scale, float *o,
+                                                 float (&red)[2][NTH / 64]) {
+  constexpr int T = 4 * VPT, NW = NTH / 64;
   const int tid = threadIdx.x, w = tid >> 6;
   float v[T];
 #pragma unroll
@@ -493,7 +505,7 @@ __device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float s
   m = wave_max(m);
   if ((tid & 63) == 0) red[0][w] = m;
   __syncthreads();
-  m = max_nan(max_nan(red[0][0], red[0][1]), max_nan(red[0][2], red[0][3]));
+  m = tree_max<NW>(red[0]);
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -505,7 +517,7 @@ __device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float s
   s = wave_sum(s);
   if ((tid & 63) == 0) red[1][w] = s;
   __syncthreads();
-  s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  s = tree_sum<NW>(red[1]);
   const float ls = LOG ? logf(s) : 0.0f;
   const float inv = 1.0f / s;
 #pragma unroll
@@ -515,24 +527,28 @@ __device__ __forceinline__ void softmax_row_regs(const float4 (&q)[VPT], float s
     r.y = LOG ? v[4 * u + 1] - ls : v[4 * u + 1] * inv;
     r.z = LOG ? v[4 * u + 2] - ls : v[4 * u + 2] * inv;
     r.w = LOG ? v[4 * u + 3] - ls : v[4 * u + 3] * inv;
-    st4<true>(o + static_cast<int64_t>(tid + 256 * u) * 4, r);
+    st4<NT>(o + static_cast<int64_t>(tid + NTH * u) * 4, r);
   }
 }
 
-// Unmasked F32 rows of exactly 1024 VPT columns, one block per row, eight
-// blocks to a CU.  (Blocks that walk several rows with the next row's loads
-// in flight under the current row's folds measured the same.)
-template <int VPT, int LOG>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
+// Unmasked F32 rows of exactly 4 NTH VPT columns, one block of NTH threads
+// per row, eight waves to a SIMD; NT streams the accesses (large inputs).  Eight values a thread (VPT = 2; 1024
+// threads for 8192 columns): on [8192, 8192] 0.78 of HBM peak against 0.75
+// with 16 values a thread and 0.73 with 32 -- short-lived waves keep more of
+// the chip's loads in flight while others fold and exponentiate.  (Blocks
+// that walk several rows with the next row's loads in flight under the
+// current row's folds measured no better.)
+template <int VPT, int LOG, int NTH, bool NT>
+__global__ void __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(8)))
 softmax_row_kernel(const float *x, float scale, float *out) {
-  constexpr int64_t C = 1024 * VPT;
-  __shared__ float red[2][4];
+  constexpr int64_t C = 4 * NTH * VPT;
+  __shared__ float red[2][NTH / 64];
   const int64_t lane = static_cast<int64_t>(threadIdx.x) * 4;
   const int64_t row = blockIdx.x;
   float4 a[VPT];
 #pragma unroll
-  for (int u = 0; u < VPT; ++u) a[u] = ld4<true>(x + row * C + lane + 1024 * u);
-  softmax_row_regs<VPT, LOG>(a, scale, out + row * C, red);
+  for (int u = 0; u < VPT; ++u) a[u] = ld4<NT>(x + row * C + lane + 4 * NTH * u);
+  softmax_row_regs<VPT, LOG, NTH, NT>(a, scale, out + row * C, red);
 }
 
 // Cross-entropy over a row of logits and its gradient in one pass: the row's
@@ -542,23 +558,27 @@ softmax_row_kernel(const float *x, float scale, float *out) {
 // same two roundings as exp, then MUL_ADD against the scattered one-hot --
 // written to dz.  A target outside [0, cols) raises the index flag, picks 0
 // bits and adds no one-hot term (as pick_columns and scatter_add_columns).
-template <int VPT, bool VEC, bool NT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(VPT <= 8 ? 8 : 4)))
+// NTH threads a row: thread t holds float4 lanes t + NTH u (VEC) or values
+// t + NTH u, folded as the softmax kernel that runs the log-softmax of the
+// same row folds (softmax_row_kernel, NTH = columns / 8, for rows of 2048,
+// 4096 or 8192 columns; softmax_block_kernel, NTH = 256, otherwise).
+template <int VPT, bool VEC, bool NT, int NTH = 256>
+__global__ void __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(VPT <= 8 ? 8 : 4)))
 log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gscale, float *picked, float *dz,
                       uint32_t *flags) {
-  constexpr int T = 4 * VPT;
-  __shared__ float red[4];
+  constexpr int T = 4 * VPT, NW = NTH / 64;
+  __shared__ float red[2][NW];
   const int64_t row = blockIdx.x;
   const int64_t base = row * cols;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6;
   float v[T];
   auto col_of = [&](int t) -> int64_t {
-    return VEC ? (static_cast<int64_t>(tid + 256 * (t >> 2)) * 4 + (t & 3)) : static_cast<int64_t>(tid + 256 * t);
+    return VEC ? (static_cast<int64_t>(tid + NTH * (t >> 2)) * 4 + (t & 3)) : static_cast<int64_t>(tid + NTH * t);
   };
   if constexpr (VEC) {
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      const int64_t j4 = tid + 256 * u;
+      const int64_t j4 = tid + NTH * u;
       const float4 q = (j4 * 4 < cols) ? ld4<NT>(z + base + j4 * 4)
                                        : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
       v[4 * u] = q.x; v[4 * u + 1] = q.y; v[4 * u + 2] = q.z; v[4 * u + 3] = q.w;
@@ -575,7 +595,10 @@ log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gs
   float m = -INFINITY;
 #pragma unroll
   for (int t = 0; t < T; t += 2) m = fmaxf(fmaxf(m, v[t]), v[t + 1]);
-  m = block_max(m, red);
+  m = wave_max(m);
+  if ((tid & 63) == 0) red[0][w] = m;
+  __syncthreads();
+  m = tree_max<NW>(red[0]);
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -583,7 +606,10 @@ log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gs
     s += col_of(t) < cols ? expf(sh) : 0.0f;
     v[t] = sh;
   }
-  s = block_sum(s, red);
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[1][w] = s;
+  __syncthreads();
+  s = tree_sum<NW>(red[1]);
   const float ls = logf(s);
   const int32_t target = tgt[row];
   const bool in_range = target >= 0 && target < cols;
@@ -601,7 +627,7 @@ log_softmax_ce_kernel(const float *z, const int32_t *tgt, int64_t cols, float gs
   if constexpr (VEC) {
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      const int64_t j4 = tid + 256 * u;
+      const int64_t j4 = tid + NTH * u;
       if (j4 * 4 < cols) st4<NT>(dz + base + j4 * 4, make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]));
     }
   } else {
@@ -914,12 +940,15 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
       const unsigned rows = static_cast<unsigned>(R);
       // Stream rows the size of the last-level cache and beyond.
       const bool nt = vec && R * C * 8 >= kStreamBytes;
-      if (nt && C == 1024 * vpt && vpt >= 2 && vpt <= 8 && !mp && out_elem == MI_F32) {
+      if (xe == MI_F32 && C == 1024 * vpt && vpt >= 2 && vpt <= 8 && !mp && out_elem == MI_F32) {
+        // Unmasked F32 rows of 2048, 4096, 8192: the same folds at any size.
         const float *xf = static_cast<const float *>(xp);
         float *of = static_cast<float *>(ob->ptr);
-        switch (vpt * 2 + (log ? 1 : 0)) {
-#define MI_SL(V) case 2 * V: softmax_row_kernel<V, 0><<<rows, 256, 0, ctx->stream>>>(xf, scale, of); break; \
-                 case 2 * V + 1: softmax_row_kernel<V, 1><<<rows, 256, 0, ctx->stream>>>(xf, scale, of); break;
+        switch (vpt * 4 + (log ? 2 : 0) + (nt ? 1 : 0)) {
+#define MI_SL(V) case 4 * V: softmax_row_kernel<2, 0, 128 * V, false><<<rows, 128 * V, 0, ctx->stream>>>(xf, scale, of); break; \
+                 case 4 * V + 1: softmax_row_kernel<2, 0, 128 * V, true><<<rows, 128 * V, 0, ctx->stream>>>(xf, scale, of); break; \
+                 case 4 * V + 2: softmax_row_kernel<2, 1, 128 * V, false><<<rows, 128 * V, 0, ctx->stream>>>(xf, scale, of); break; \
+                 case 4 * V + 3: softmax_row_kernel<2, 1, 128 * V, true><<<rows, 128 * V, 0, ctx->stream>>>(xf, scale, of); break;
           MI_SL(2) MI_SL(4) MI_SL(8)
 #undef MI_SL
         }
@@ -1211,6 +1240,15 @@ extern "C" int mi_log_softmax_ce(mi_ctx *ctx, mi_id logits, mi_id targets, float
     const bool vec = C % 4 == 0;
     const bool nt = vec && R * C * 8 >= kStreamBytes;
     const unsigned g = static_cast<unsigned>(R);
+    // Rows of 2048, 4096 or 8192: the layout of softmax_row_kernel.
+    if (C == 1024 * vpt && vpt >= 2 && vpt <= 8) {
+      switch (vpt * 2 + (nt ? 1 : 0)) {
+#define MI_CER(V) case 2 * V: log_softmax_ce_kernel<2, true, false, 128 * V><<<g, 128 * V, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); break; \
+                  case 2 * V + 1: log_softmax_ce_kernel<2, true, true, 128 * V><<<g, 128 * V, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); break;
+        MI_CER(2) MI_CER(4) MI_CER(8)
+#undef MI_CER
+      }
+    } else
     switch (vpt) {
 #define MI_CE(V) case V: if (nt) log_softmax_ce_kernel<V, true, true><<<g, 256, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); \
                          else if (vec) log_softmax_ce_kernel<V, true, false><<<g, 256, 0, ctx->stream>>>(zp, tp, C, grad_scale, pp, dp, flags(ctx)); \

@@ -260,7 +260,8 @@ def ce_composition(engine, iz, it, rows, cols, inv):
     return picked, dz
 
 
-@pytest.mark.parametrize("rows,cols", [(2048, 8192), (64, 10), (37, 1001), (16, 16384), (5, 1024)])
+@pytest.mark.parametrize("rows,cols", [(2048, 8192), (300, 8192), (4100, 4096), (8200, 2048), (64, 10), (37, 1001),
+                                       (16, 16384), (5, 1024), (7, 3000)])
 def test_log_softmax_ce_equals_composition(engine, rows, cols):
     z = rnd(rows, cols, scale=3.0)
     tgt = RNG.integers(0, cols, (rows, 1)).astype(np.int32)

@@ -257,10 +257,9 @@ def test_softmax(engine, cols, log):
 @pytest.mark.parametrize("rows,cols", [(2600, 8192), (4100, 4096), (8200, 2048)])
 @pytest.mark.parametrize("log,scale", [(False, 1.0), (True, 1.0), (False, 0.125)])
 def test_softmax_streamed_rows(engine, rows, cols, log, scale):
-    # Inputs past the streaming threshold (2 x 4 x rows x cols >= 128 MiB) with
-    # more rows than one block per row covers in a round: each block walks
-    # rows with the next row's loads in flight.  Rows are independent, so a
-    # subset run through the one-block-per-row kernel has the same bits.
+    # Inputs past the streaming threshold (2 x 4 x rows x cols >= 128 MiB):
+    # nontemporal accesses.  Rows are independent and fold alike at any size,
+    # so a subset of rows (cached accesses) has the same bits.
     x = rnd(rows, cols, scale=3.0)
     x[1, 5] = np.nan      # a NaN makes its whole row NaN
     x[2, 7] = np.inf      # so does +inf (inf - inf)
