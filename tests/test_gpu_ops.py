@@ -195,7 +195,8 @@ def reduce_tol(x, axis):
     return 1e-5 * np.abs(x.astype(np.float64)).sum(axis=1 - axis if axis in (0, 1) else None, keepdims=True)
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (7, 3), (64, 10), (130, 1000), (1000, 130), (2048, 512), (5, 9000)])
+@pytest.mark.parametrize("shape", [(1, 1), (7, 3), (64, 10), (130, 1000), (1000, 130), (2048, 512), (5, 9000),
+                                   (1024, 8192), (1500, 8224), (4096, 8192)])
 @pytest.mark.parametrize("axis", [AXIS_ROWS, AXIS_COLS])
 def test_sum_mean(engine, shape, axis):
     x = rnd(*shape)
@@ -211,11 +212,12 @@ def test_sum_mean(engine, shape, axis):
         assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * scale + 1e-30)
 
 
-@pytest.mark.parametrize("shape", [(3, 5), (64, 10), (300, 700)])
+@pytest.mark.parametrize("shape", [(3, 5), (64, 10), (300, 700), (1500, 8224)])
 @pytest.mark.parametrize("axis", [AXIS_ROWS, AXIS_COLS])
 def test_max_min_exact(engine, shape, axis):
     x = rnd(*shape)
     x[0, 0] = np.nan
+    x[-1, -1] = np.nan  # the last row of a column
     a = engine.upload(x)
     for op in (R_MAX, R_MIN):
         same_bits(engine.download(engine.reduce(a, op, axis)), orc.reduce(x, op, axis))
