@@ -1205,10 +1205,11 @@ static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.batch; };
   // Exactly tiled shapes take the pipelined direct HBM -> LDS kernel: 256 x
   // 256 tiles (8 waves of 128 x 64, two per SIMD) when they give most of the
-  // 256 CUs a tile, else 128 x 128 tiles (4 waves of 64 x 64); five LDS
+  // 256 CUs a tile, else 128 x 128 tiles (4 waves of 64 x 64) from 16 tiles
+  // up (512^3 in 7.5 us against 8.9 on 64 x 64 register tiles); five LDS
   // stages of k 32 either way.
   if (tiles_exactly(p, 256, 256, 32, 8) && tiles(256, 256) >= 192) return launch_pipe<TO, 256, 256, 5, 2, 4>(p, st);
-  if (tiles_exactly(p, 128, 128, 32, 8) && tiles(128, 128) >= 96) return launch_pipe<TO, 128, 128, 5, 2, 2>(p, st);
+  if (tiles_exactly(p, 128, 128, 32, 8) && tiles(128, 128) >= 16) return launch_pipe<TO, 128, 128, 5, 2, 2>(p, st);
   if (tiles_exactly(p, 64, 64, 64, 8))
     return launch_orient<T, T, T, TO, 64, 64, 2, 2, false>(p, st);
   return launch_orient<T, T, T, TO, 64, 64, 2, 2, true>(p, st);
@@ -1310,6 +1311,15 @@ static void launch_gemv(const Plan &p, hipStream_t st) {
 // 16 us in 16 slices; the MLP's [64, 784] x [784, 128] gains from 6).
 static int splitk_slices(const Plan &p) {
   if (p.batch != 1) return 1;
+  // BF16 operands tiled exactly by 128 run the pipelined kernel whole once
+  // its tiles (16 or more) cover the k loop, tiles x 128 >= k: 1024^3 in
+  // 11 us against 26 us split four ways on the register kernel, 768 x 768
+  // over k 2048 in 18 against 26; 512 x 512 over k 4096 stays split (27 us
+  // against 32).
+  if (p.ea == MI_BF16 && p.eb == MI_BF16 && tiles_exactly(p, 128, 128, 32, 8)) {
+    const int64_t t128 = (p.M / 128) * (p.N / 128);
+    if (t128 >= 16 && t128 * 128 >= p.K) return 1;
+  }
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
   if (tiles >= 512 || p.K < 256) return 1;
   if (p.K < 1024 && tiles >= 64) return 1;

@@ -396,7 +396,8 @@ def test_matmul_f32(engine, mode, ta, tb, mnk):
 @pytest.mark.parametrize("ta", [False, True])
 @pytest.mark.parametrize("tb", [False, True])
 @pytest.mark.parametrize("mnk", [(512, 512, 512), (256, 512, 192), (128, 64, 64), (100, 70, 33), (1, 576, 1536),
-                                 (2048, 256, 1024)])
+                                 (2048, 256, 1024), (1024, 1024, 1024), (768, 768, 2048), (384, 1024, 2048),
+                                 (512, 512, 4096)])
 def test_matmul_bf16(engine, ta, tb, mnk):
     m, n, k = mnk
     a = rnd(k, m) if ta else rnd(m, k)
@@ -506,6 +507,20 @@ def test_matmul_batched_bf16_integer_exact_256_tiles(engine, tb):
     bb = b.transpose(0, 2, 1) if tb else b
     want = np.matmul(a.astype(np.float64), bb.astype(np.float64)).astype(np.float32)
     same_bits(got, want)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True)])
+@pytest.mark.parametrize("mnk", [(512, 512, 512), (768, 768, 2048), (384, 1024, 2048)])
+def test_matmul_bf16_integer_exact_few_tiles(engine, ta, tb, mnk):
+    """16 to 36 tiles of 128 x 128: the pipelined kernel over the whole k
+    loop (no split), exact with small-integer operands."""
+    m, n, k = mnk
+    a = RNG.integers(-3, 4, (k, m) if ta else (m, k)).astype(np.float32)
+    b = RNG.integers(-3, 4, (n, k) if tb else (k, n)).astype(np.float32)
+    got = engine.download(engine.matmul_dram(engine.upload_bf16(orc.to_bf16(a)), ta,
+                                             engine.upload_bf16(orc.to_bf16(b)), tb))
+    aa, bb = (a.T if ta else a), (b.T if tb else b)
+    same_bits(got, (aa.astype(np.float64) @ bb.astype(np.float64)).astype(np.float32))
 
 
 def test_matmul_bf16_out_direct_kernel(engine):
