@@ -1239,8 +1239,16 @@ static hipError_t run_plan(const Plan &p, hipStream_t st) {
   // tiles of 128 x 128): below that the kernels are bound by load latency and
   // the split's conversions only add work, so the F32 kernel runs (more
   // accurate, and faster there).
+  // F32 activations against BF16 weights over at least 256 rows are the
+  // exception below 2^31 multiply-adds: split, only the activations take two
+  // BF16 parts, and a 64 x 64 tile's k loop runs on the BF16 matrix cores
+  // instead of the F32 ones (a 512-token prefill of the SmolLM2-shaped decoder
+  // 8.7 -> 7.5 ms); between 2^31 and 2^33 (a batch-32 prefill's products) the
+  // F32 kernel's 128 x 128 tiles stay ahead.
+  const int64_t macs = p.M * p.N * p.K * p.batch;
   const bool split_pays =
-      p.M * p.N * p.K * p.batch >= (int64_t(1) << 33) && ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch >= 128;
+      (macs >= (int64_t(1) << 33) && ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch >= 128) ||
+      (p.ea == MI_F32 && p.eb == MI_BF16 && p.M >= 256 && macs < (int64_t(1) << 31));
   if (p.fast && split_pays) {
     if (p.ea == MI_F32 && p.eb == MI_F32)
       return bf ? run_split<float, float, uint16_t>(p, st) : run_split<float, float, float>(p, st);

@@ -424,7 +424,8 @@ def test_matmul_bf16_out(engine):
 
 
 @pytest.mark.parametrize("tb", [False, True])
-@pytest.mark.parametrize("mnk", [(64, 48, 96), (512, 576, 576), (300, 200, 136), (2048, 2048, 2048)])
+@pytest.mark.parametrize("mnk", [(64, 48, 96), (512, 576, 576), (300, 200, 136), (2048, 2048, 2048), (512, 192, 576),
+                                 (256, 1536, 576), (512, 576, 1536)])
 def test_matmul_mixed_f32_bf16(engine, mode, tb, mnk):
     m, n, k = mnk
     a, b = rnd(m, k), orc.to_bf16(rnd(n, k) if tb else rnd(k, n))
