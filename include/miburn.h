@@ -378,6 +378,26 @@ int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
                      mi_id w_qkv, mi_id cos_table, mi_id sin_table,
                      int64_t heads, int64_t kv_heads, int64_t pos,
                      mi_id k_cache, mi_id v_cache, mi_id *q_out);
+/* silu(gate) * up over the halves of a fused gate|up product: gate_up
+ * [rows, 2 i] F32 -> [rows, i] (the reference's MLP, crates/tt-models/src/
+ * llama.rs:494-498, on the two row blocks of its gate|up weight); no Engine
+ * counterpart.  Bit-identical to MI_K_SILU_MUL of the two halves. */
+int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, mi_id *out);
+/* The q|k|v tail of a prefill in one launch: the composition the reference's
+ * attention block makes of RoPE on the query and key heads, the key/value
+ * cache write and the queries' grouping per kv head (crates/tt-models/src/
+ * llama.rs:403-446; crates/tt-models/src/rope.rs:1-140), with no Engine
+ * counterpart.  qkv: [batch * seq, (heads + 2 kv_heads) * d] F32 rows
+ * (sequence, position) of the fused q|k|v projection; RoPE as mi_rope at
+ * positions pos0 + p; keys and values written into the caches ([batch *
+ * kv_heads * max_ctx, d] F32, item (sequence, kv head)) at positions pos0 ..
+ * pos0 + seq - 1; q_out [batch * seq * heads, d]: rows (sequence, position,
+ * head), or with `grouped` rows (sequence, kv head j, position, g) for head
+ * j * heads / kv_heads + g.  Bit-identical to mi_rope + mi_copy_into4 +
+ * mi_copy_strided4. */
+int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id sin_table,
+                      int64_t seq, int64_t heads, int64_t kv_heads, int64_t pos0,
+                      mi_id k_cache, mi_id v_cache, int grouped, mi_id *q_out);
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);

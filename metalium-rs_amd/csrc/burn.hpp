@@ -373,6 +373,23 @@ inline Tensor rope(const Tensor &x, const Tensor &cos, const Tensor &sin, int64_
   return Tensor(x.ctx(), id, x.shape());
 }
 
+// silu(gate) * up of a fused gate|up product's halves (mi_silu_mul_halves).
+inline Tensor silu_mul_halves(const Tensor &gate_up) {
+  mi_id id;
+  check(gate_up.ctx(), mi_silu_mul_halves(gate_up.ctx(), gate_up.use(), &id), "silu_mul_halves");
+  return Tensor(gate_up.ctx(), id, {gate_up.rows(), gate_up.cols() / 2});
+}
+
+// The prefill's q|k|v tail (mi_qkv_rope_cache): RoPE, cache writes, q out.
+inline Tensor qkv_rope_cache(const Tensor &qkv, const Tensor &cos, const Tensor &sin, int64_t seq, int64_t heads,
+                             int64_t kv_heads, int64_t pos0, const Tensor &k_cache, const Tensor &v_cache,
+                             bool grouped) {
+  mi_id id;
+  check(qkv.ctx(), mi_qkv_rope_cache(qkv.ctx(), qkv.use(), cos.use(), sin.use(), seq, heads, kv_heads, pos0,
+                                     k_cache.use(), v_cache.use(), grouped ? 1 : 0, &id), "qkv_rope_cache");
+  return Tensor(qkv.ctx(), id, {qkv.rows() * heads, k_cache.cols()});
+}
+
 inline Tensor attention_rows(const Tensor &q, const Tensor &k_cache, const Tensor &v_cache, int64_t batch, int64_t t,
                              int64_t heads, int64_t kv_heads, int64_t pos0, float scale) {
   mi_id id;

@@ -620,6 +620,65 @@ __global__ void rope_kernel(const float *x, const float *cosp, const float *sinp
     out[e] = __fadd_rn(c, __fmul_rn(rv, sinp[pos * d + j]));
   }
 }
+
+// silu(gate) * up over the two halves of a fused gate|up product's rows,
+// gu [rows, 2 i] -> [rows, i], with SILU_MUL's arithmetic; four columns a
+// thread when i is a multiple of 4.
+template <bool VEC>
+__global__ void silu_mul_halves_kernel(const float *gu, float *out, int64_t rows, int64_t inner) {
+  const int64_t per = VEC ? inner / 4 : inner, n = rows * per;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int64_t r = e / per, c = e - r * per;
+    if constexpr (VEC) {
+      const float4 g = *reinterpret_cast<const float4 *>(gu + r * 2 * inner + 4 * c);
+      const float4 u = *reinterpret_cast<const float4 *>(gu + r * 2 * inner + inner + 4 * c);
+      float4 y;
+      y.x = op<MI_K_SILU_MUL>(g.x, u.x, 0.f, 0.f, 0.f);
+      y.y = op<MI_K_SILU_MUL>(g.y, u.y, 0.f, 0.f, 0.f);
+      y.z = op<MI_K_SILU_MUL>(g.z, u.z, 0.f, 0.f, 0.f);
+      y.w = op<MI_K_SILU_MUL>(g.w, u.w, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4 *>(out + r * inner + 4 * c) = y;
+    } else {
+      out[r * inner + c] = op<MI_K_SILU_MUL>(gu[r * 2 * inner + c], gu[r * 2 * inner + inner + c], 0.f, 0.f, 0.f);
+    }
+  }
+}
+
+// The q|k|v tail of a prefill in one pass over the fused projection's rows
+// qkv [batch * seq, (heads + 2 kv) * d], row (sequence b, position p): RoPE
+// on the q and k heads at position pos0 + p (rope_kernel's arithmetic), k and
+// v written into the caches [batch * kv * maxc, d] at row (b kv + j) maxc +
+// pos0 + p, q written to row (b seq + p) heads + h (natural order) or, with
+// `grouped`, to row ((b kv + j) seq + p) G + g for head h = j G + g (the
+// queries regrouped per kv head, G = heads / kv).
+__global__ void qkv_rope_cache_kernel(const float *qkv, const float *cosp, const float *sinp, float *q, float *kc,
+                                      float *vc, int64_t rows, int64_t seq, int64_t heads, int64_t kv, int64_t d,
+                                      int64_t maxc, int64_t pos0, int grouped) {
+  const int64_t w = (heads + 2 * kv) * d, n = rows * w, half = d / 2, G = heads / kv;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int64_t r = e / w, c = e - r * w;
+    const int64_t b = r / seq, p = r - b * seq, pos = pos0 + p;
+    const int64_t h = c / d, j = c - h * d;  // head index across q, k, v
+    const float xv = qkv[e];
+    float y = xv;
+    if (h < heads + kv) {  // q or k: rotate
+      const float rv = qkv[r * w + h * d + (j < half ? j + half : j - half)];
+      const float cv = __fmul_rn(xv, cosp[pos * d + j]);
+      y = __fadd_rn(cv, __fmul_rn(rv, sinp[pos * d + j]));
+    }
+    if (h < heads) {
+      const int64_t kvh = h / G, g = h - kvh * G;
+      const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
+      q[row * d + j] = y;
+    } else if (h < heads + kv) {
+      kc[((b * kv + (h - heads)) * maxc + pos) * d + j] = y;
+    } else {
+      vc[((b * kv + (h - heads - kv)) * maxc + pos) * d + j] = y;
+    }
+  }
+}
 }  // namespace mi
 
 extern "C" int mi_copy_into4(mi_ctx *ctx, mi_id dst, int64_t dst_offset, const int64_t dst_strides[4], mi_id src,
@@ -674,6 +733,77 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
     if (s) { mi_free(ctx, id); return s; }
   }
   *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, gb, gate_up);
+  if (gb->elem != MI_F32 || gb->cols % 2)
+    return fail(ctx, MI_E_ARG, "silu_mul_halves of %s [%lld, %lld]: want F32 with an even width", elem_name(gb->elem),
+                (long long)gb->rows, (long long)gb->cols);
+  const int64_t R = gb->rows, I = gb->cols / 2;
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R, I, MI_F32, &id, &ob);
+  if (s) return s;
+  if (R * I > 0) {
+    const float *gp = static_cast<const float *>(gb->ptr);
+    float *op_ = static_cast<float *>(ob->ptr);
+    if (I % 4 == 0)
+      silu_mul_halves_kernel<true><<<grid_for(R * I / 4, 256 * 2, 256 * 128), 256, 0, ctx->stream>>>(gp, op_, R, I);
+    else
+      silu_mul_halves_kernel<false><<<grid_for(R * I, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(gp, op_, R, I);
+    s = check_launch(ctx, "silu_mul_halves");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id sin_table, int64_t seq,
+                                 int64_t heads, int64_t kv_heads, int64_t pos0, mi_id k_cache, mi_id v_cache,
+                                 int grouped, mi_id *q_out) {
+  MI_ENTER(ctx);
+  if (!q_out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, qkv);
+  MI_BUF(ctx, cb, cos_table);
+  MI_BUF(ctx, sb, sin_table);
+  MI_BUF(ctx, kb, k_cache);
+  MI_BUF(ctx, vb, v_cache);
+  if (xb->elem != MI_F32 || cb->elem != MI_F32 || sb->elem != MI_F32 || kb->elem != MI_F32 || vb->elem != MI_F32)
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache takes F32");
+  const int64_t D = kb->cols, R = xb->rows;
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads || D < 2 || D % 2)
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache: %lld heads over %lld kv heads of width %lld", (long long)heads,
+                (long long)kv_heads, (long long)D);
+  if (xb->cols != (heads + 2 * kv_heads) * D)
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache: rows of %lld, want (heads + 2 kv_heads) * %lld = %lld",
+                (long long)xb->cols, (long long)D, (long long)((heads + 2 * kv_heads) * D));
+  if (seq < 1 || R % seq) return fail(ctx, MI_E_ARG, "qkv_rope_cache: %lld rows are not sequences of %lld", (long long)R, (long long)seq);
+  const int64_t batch = R / seq;
+  if (vb->cols != D || vb->rows != kb->rows || kb->rows % (batch * kv_heads))
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache: caches must both be [%lld * %lld * max_ctx, %lld]", (long long)batch,
+                (long long)kv_heads, (long long)D);
+  const int64_t maxc = kb->rows / (batch * kv_heads);
+  if (pos0 < 0 || pos0 + seq > maxc)
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache: positions [%lld, %lld) beyond the cache's %lld", (long long)pos0,
+                (long long)(pos0 + seq), (long long)maxc);
+  if (cb->cols != D || sb->cols != D || cb->rows != sb->rows || pos0 + seq > cb->rows)
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache: rope tables [%lld, %lld] for positions below %lld", (long long)cb->rows,
+                (long long)cb->cols, (long long)(pos0 + seq));
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R * heads, D, MI_F32, &id, &ob);
+  if (s) return s;
+  if (R > 0) {
+    qkv_rope_cache_kernel<<<grid_for(R * xb->cols, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(
+        static_cast<const float *>(xb->ptr), static_cast<const float *>(cb->ptr), static_cast<const float *>(sb->ptr),
+        static_cast<float *>(ob->ptr), static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), R, seq, heads,
+        kv_heads, D, maxc, pos0, grouped ? 1 : 0);
+    s = check_launch(ctx, "qkv_rope_cache");
+    if (s) { mi_free(ctx, id); return s; }
+  }
+  *q_out = id;
   return MI_OK;
 }
 

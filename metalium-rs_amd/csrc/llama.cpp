@@ -102,7 +102,7 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
   }
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
 
-  const int64_t qd = H * D, kvd = KVH * D, hid = c.hidden, I = c.intermediate;
+  const int64_t hid = c.hidden, I = c.intermediate;
   if (t == 1 && batch <= kDecodeMaxBatch && fused && hid % 8 == 0 && I % 8 == 0) {
     // Decode: six fused launches a layer.
     for (Layer &L : m->layers) {
@@ -118,32 +118,18 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
   }
   for (Layer &L : m->layers) {
     Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps);
-    // Row blocks of the fused q|k|v weight.
-    Tensor q = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, qd, 0, 0, 0, 0).reshape({rows * H, D});
-    Tensor k = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, kvd, 0, 0, qd * hid, 0).reshape({rows * KVH, D});
-    Tensor v = burn::matmul_blocks(xn, false, L.wqkv, true, 1, rows, hid, kvd, 0, 0, (qd + kvd) * hid, 0)
-                   .reshape({rows * KVH, D});
-    q = burn::rope(q, m->rope_cos, m->rope_sin, H, t, pos0);
-    k = burn::rope(k, m->rope_cos, m->rope_sin, KVH, t, pos0);
-    // Append k, v at positions pos0.. of each (sequence, kv head) item.
-    {
-      const int64_t dims[4] = {batch, KVH, t, D};
-      const int64_t dst[4] = {KVH * maxc * D, maxc * D, D, 1};
-      const int64_t src[4] = {t * KVH * D, D, KVH * D, 1};
-      burn::copy_into4(L.cache_k, pos0 * D, dst, k, 0, src, dims);
-      burn::copy_into4(L.cache_v, pos0 * D, dst, v, 0, src, dims);
-    }
+    // One product against the fused q|k|v weight, then RoPE on q and k, k and
+    // v appended to the caches at positions pos0.. of each (sequence, kv head)
+    // item, and q laid out for the attention, in one launch: rows (sequence,
+    // position, head) for the fused kernel, else regrouped per kv head, rows
+    // (sequence, kv head, position, g).
+    Tensor qkv = burn::float_matmul(xn, false, L.wqkv, true);
+    Tensor q = burn::qkv_rope_cache(qkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k, L.cache_v, !fused);
     Tensor oh;
     if (fused) {
       oh = burn::attention_rows(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0, scale);
     } else {
-      // Queries regrouped per kv head: [batch * KVH * t, G * D] = rows (p, g).
-      Tensor qg;
-      {
-        const int64_t dims[4] = {batch, KVH, t, G * D};
-        const int64_t st[4] = {t * H * D, G * D, H * D, 1};
-        qg = burn::copy4(q, dims, 0, st).reshape({batch * KVH * t * G, D});
-      }
+      const Tensor &qg = q;  // [batch * KVH * t * G, D], rows (p, g) of each (sequence, kv head)
       Tensor scores = burn::matmul_blocks(qg, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
                                           maxc * D);
       Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
@@ -156,11 +142,11 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
         oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
       }
     }
-    x = burn::float_add(x, burn::float_matmul(oh, false, L.wo, true));
+    x = burn::linear(oh, L.wo, true, nullptr, &x);  // x + oh wo^T, the add in the product's epilogue
     Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps);
-    Tensor gate = burn::matmul_blocks(hn, false, L.wgu, true, 1, rows, hid, I, 0, 0, 0, 0);
-    Tensor up = burn::matmul_blocks(hn, false, L.wgu, true, 1, rows, hid, I, 0, 0, I * hid, 0);
-    x = burn::float_add(x, burn::float_matmul(burn::silu_mul(gate, up), false, L.wdown, true));
+    // One product against the fused gate|up weight, silu(gate) * up of its halves.
+    Tensor h = burn::silu_mul_halves(burn::float_matmul(hn, false, L.wgu, true));
+    x = burn::linear(h, L.wdown, true, nullptr, &x);
   }
   m->len = ctxlen;
   return x;

@@ -108,6 +108,8 @@ def _load() -> ctypes.CDLL:
         "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
+        "mi_qkv_rope_cache": [P, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
+        "mi_silu_mul_halves": [P, U64, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
         "mi_reduce": [P, U64, c_int, c_int, Ip],
         "mi_reduce_all": [P, U64, c_int, Ip],
@@ -317,6 +319,16 @@ class Engine:
     def norm_matvec(self, x: int, gamma: int, eps: float, w: int, residual: int = 0, silu_mul: bool = False) -> int:
         """Fused decode projection: residual + rmsnorm(x) w^T, or silu(g) * u."""
         return self._out(self._lib.mi_norm_matvec, x, gamma, eps, w, residual, int(silu_mul))
+
+    def silu_mul_halves(self, gate_up: int) -> int:
+        """silu(gate) * up over the two column halves of a fused gate|up product."""
+        return self._out(self._lib.mi_silu_mul_halves, gate_up)
+
+    def qkv_rope_cache(self, qkv: int, cos: int, sin: int, seq: int, heads: int, kv_heads: int, pos0: int,
+                       k_cache: int, v_cache: int, grouped: bool = False) -> int:
+        """Prefill q|k|v tail: RoPE on q and k, k and v into the caches; returns q."""
+        return self._out(self._lib.mi_qkv_rope_cache, qkv, cos, sin, seq, heads, kv_heads, pos0, k_cache, v_cache,
+                         int(grouped))
 
     def norm_qkv_rope(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
                       kv_heads: int, pos: int, k_cache: int, v_cache: int) -> int:

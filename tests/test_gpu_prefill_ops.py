@@ -1,0 +1,107 @@
+"""Device parity of the prefill's fused tails.
+
+mi_qkv_rope_cache (RoPE on the q and k heads of the fused q|k|v rows, the
+cache writes, q in either layout): bit-identical to the engine's own
+composition -- mi_rope on the q and k blocks, mi_copy_into4 of k and v into
+the caches, mi_copy_strided4 for the regrouped queries (each pinned against
+the oracle by its own tests) -- with every cache row outside the written
+positions left as it was.
+
+mi_silu_mul_halves: bit-identical to MI_K_SILU_MUL of the two halves, on the
+vector and the scalar paths.
+"""
+import numpy as np
+import pytest
+
+import miburn
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(31_2024)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def same_bits(a, b):
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    bad = np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} datums differ, first at {bad[0]}"
+
+
+@pytest.fixture(scope="module")
+def engine():
+    e = miburn.Engine(0)
+    yield e
+    e.close()
+
+
+def rope_tables(n, d, theta=1e5):
+    inv = theta ** (-np.arange(0, d, 2, dtype=np.float64) / d)
+    ang = np.arange(n)[:, None] * inv[None, :]
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], 1).astype(np.float32)
+    sin = np.concatenate([-np.sin(ang), np.sin(ang)], 1).astype(np.float32)
+    return cos, sin
+
+
+@pytest.mark.parametrize("batch,seq,heads,kv,d,pos0,maxc", [(2, 5, 9, 3, 64, 3, 16), (1, 33, 4, 4, 32, 0, 40),
+                                                           (3, 7, 8, 2, 16, 9, 20)])
+def test_qkv_rope_cache_equals_composition(engine, batch, seq, heads, kv, d, pos0, maxc):
+    rows, w = batch * seq, (heads + 2 * kv) * d
+    qkv = rnd(rows, w)
+    cos, sin = rope_tables(maxc, d)
+    ic, isn = engine.upload(cos), engine.upload(sin)
+    kc0, vc0 = rnd(batch * kv * maxc, d), rnd(batch * kv * maxc, d)
+    iq = engine.upload(qkv)
+    # The fused tail, both layouts (the second call rewrites the same cache rows).
+    k1, v1 = engine.upload(kc0), engine.upload(vc0)
+    q_nat = engine.download(engine.qkv_rope_cache(iq, ic, isn, seq, heads, kv, pos0, k1, v1, grouped=False))
+    q_grp = engine.download(engine.qkv_rope_cache(iq, ic, isn, seq, heads, kv, pos0, k1, v1, grouped=True))
+    # The composition.
+    qd, kvd = heads * d, kv * d
+    q = engine.rope(engine.upload(np.ascontiguousarray(qkv[:, :qd]).reshape(rows * heads, d)), ic, isn, heads, seq, pos0)
+    k = engine.rope(engine.upload(np.ascontiguousarray(qkv[:, qd:qd + kvd]).reshape(rows * kv, d)), ic, isn, kv, seq,
+                    pos0)
+    v = engine.upload(np.ascontiguousarray(qkv[:, qd + kvd:]).reshape(rows * kv, d))
+    k2, v2 = engine.upload(kc0), engine.upload(vc0)
+    dims, dst, src = (batch, kv, seq, d), (kv * maxc * d, maxc * d, d, 1), (seq * kv * d, d, kv * d, 1)
+    engine.copy_into4(k2, pos0 * d, dst, k, 0, src, dims)
+    engine.copy_into4(v2, pos0 * d, dst, v, 0, src, dims)
+    G = heads // kv
+    qg = engine.copy_strided4(q, (batch, kv, seq, G * d), 0, (seq * heads * d, G * d, heads * d, 1))
+    same_bits(q_nat, engine.download(q))
+    same_bits(q_grp, engine.download(qg).reshape(rows * heads, d))
+    same_bits(engine.download(k1), engine.download(k2))
+    same_bits(engine.download(v1), engine.download(v2))
+    # Rows outside positions pos0 .. pos0 + seq - 1 are untouched.
+    kk = engine.download(k1).reshape(batch * kv, maxc, d)
+    keep = np.ones(maxc, bool)
+    keep[pos0:pos0 + seq] = False
+    same_bits(kk[:, keep], kc0.reshape(batch * kv, maxc, d)[:, keep])
+
+
+def test_qkv_rope_cache_argument_errors(engine):
+    cos, sin = rope_tables(8, 16)
+    ic, isn = engine.upload(cos), engine.upload(sin)
+    kc, vc = engine.upload(rnd(2 * 8, 16)), engine.upload(rnd(2 * 8, 16))
+    good = engine.upload(rnd(4, 4 * 16))  # 2 heads + 2 x 1 kv head
+    engine.qkv_rope_cache(good, ic, isn, 4, 2, 1, 0, kc, vc)  # 1 sequence, 2 x 1 x 8 cache rows: max_ctx 16
+    for args in [(engine.upload(rnd(4, 3 * 16)), 4, 2, 1, 0),  # width is not (heads + 2 kv) d
+                 (good, 3, 2, 1, 0),                            # 4 rows are not sequences of 3
+                 (good, 4, 3, 2, 0),                            # heads not a multiple of kv heads
+                 (good, 4, 2, 1, 6)]:                           # positions beyond the rope table
+        with pytest.raises(miburn.MiError) as e:
+            engine.qkv_rope_cache(args[0], ic, isn, args[1], args[2], args[3], args[4], kc, vc)
+        assert e.value.kind == "ARG"
+
+
+@pytest.mark.parametrize("rows,inner", [(512, 1536), (7, 13), (3, 4)])
+def test_silu_mul_halves_equals_silu_mul(engine, rows, inner):
+    gu = rnd(rows, 2 * inner, scale=3.0)
+    got = engine.download(engine.silu_mul_halves(engine.upload(gu)))
+    g, u = engine.upload(np.ascontiguousarray(gu[:, :inner])), engine.upload(np.ascontiguousarray(gu[:, inner:]))
+    same_bits(got, engine.download(engine.eltwise_op_as("SILU_MUL", g, u)))
+    with pytest.raises(miburn.MiError):
+        engine.silu_mul_halves(engine.upload(rnd(2, 5)))  # odd width
