@@ -736,6 +736,45 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
   return MI_OK;
 }
 
+// qkv_rope_cache_kernel's work, one block per row and four columns a thread
+// (d a multiple of 8, so a float4 of one half of a head has its rotation
+// partner at the same place in the other half).  The head, sequence and
+// position come from one small division per thread and one per block, not
+// four 64-bit divisions per element.
+__global__ void __launch_bounds__(256) qkv_rope_cache_row_kernel(const float *qkv, const float *cosp,
+                                                                 const float *sinp, float *q, float *kc, float *vc,
+                                                                 int64_t seq, int heads, int kv, int d, int64_t maxc,
+                                                                 int64_t pos0, int grouped) {
+  const int w = (heads + 2 * kv) * d, half = d / 2, G = heads / kv;
+  const int64_t r = blockIdx.x;
+  const int64_t b = r / seq, p = r - b * seq, pos = pos0 + p;
+  const float *xr = qkv + r * w;
+  for (int c = 4 * threadIdx.x; c < w; c += 4 * 256) {
+    const int h = c / d, j = c - h * d;
+    float4 y = *reinterpret_cast<const float4 *>(xr + c);
+    if (h < heads + kv) {
+      const float4 rv = *reinterpret_cast<const float4 *>(xr + h * d + (j < half ? j + half : j - half));
+      const float4 cv = *reinterpret_cast<const float4 *>(cosp + pos * d + j);
+      const float4 sv = *reinterpret_cast<const float4 *>(sinp + pos * d + j);
+      y.x = __fadd_rn(__fmul_rn(y.x, cv.x), __fmul_rn(rv.x, sv.x));
+      y.y = __fadd_rn(__fmul_rn(y.y, cv.y), __fmul_rn(rv.y, sv.y));
+      y.z = __fadd_rn(__fmul_rn(y.z, cv.z), __fmul_rn(rv.z, sv.z));
+      y.w = __fadd_rn(__fmul_rn(y.w, cv.w), __fmul_rn(rv.w, sv.w));
+    }
+    float *dst;
+    if (h < heads) {
+      const int kvh = h / G, g = h - kvh * G;
+      const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
+      dst = q + row * d + j;
+    } else if (h < heads + kv) {
+      dst = kc + ((b * kv + (h - heads)) * maxc + pos) * d + j;
+    } else {
+      dst = vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j;
+    }
+    *reinterpret_cast<float4 *>(dst) = y;
+  }
+}
+
 extern "C" int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
@@ -795,7 +834,17 @@ extern "C" int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id 
   mi_id id; Buffer *ob;
   int s = new_buffer(ctx, R * heads, D, MI_F32, &id, &ob);
   if (s) return s;
-  if (R > 0) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(xb->ptr) | reinterpret_cast<uintptr_t>(ob->ptr) |
+                        reinterpret_cast<uintptr_t>(kb->ptr) | reinterpret_cast<uintptr_t>(vb->ptr) |
+                        reinterpret_cast<uintptr_t>(cb->ptr) | reinterpret_cast<uintptr_t>(sb->ptr)) % 16 == 0;
+  if (R > 0 && D % 8 == 0 && aligned && R <= INT32_MAX && xb->cols <= INT32_MAX) {
+    qkv_rope_cache_row_kernel<<<static_cast<unsigned>(R), 256, 0, ctx->stream>>>(
+        static_cast<const float *>(xb->ptr), static_cast<const float *>(cb->ptr), static_cast<const float *>(sb->ptr),
+        static_cast<float *>(ob->ptr), static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), seq,
+        static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(D), maxc, pos0, grouped ? 1 : 0);
+    s = check_launch(ctx, "qkv_rope_cache");
+    if (s) { mi_free(ctx, id); return s; }
+  } else if (R > 0) {
     qkv_rope_cache_kernel<<<grid_for(R * xb->cols, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(
         static_cast<const float *>(xb->ptr), static_cast<const float *>(cb->ptr), static_cast<const float *>(sb->ptr),
         static_cast<float *>(ob->ptr), static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), R, seq, heads,

@@ -288,6 +288,22 @@ def test_softmax_masked_scaled(engine):
     assert np.all(got[3] == 0.0) and np.all(got[15] == 0.0)
 
 
+@pytest.mark.parametrize("cols", [4, 36, 512, 1000, 1024])
+@pytest.mark.parametrize("log", [False, True])
+def test_softmax_masked_vector_rows(engine, cols, log):
+    # F32 rows of a multiple of 4 up to 1024 columns with a mask: float4 loads.
+    R = 24
+    x = rnd(R, cols, scale=2.0)
+    mask = (RNG.random((8, cols)) < 0.3).astype(np.uint32)
+    mask[5, :] = 1            # rows 5, 13, 21 fully masked
+    x[2, 1] = np.nan          # row 2: NaN unless masked
+    mask[2, 1] = 0
+    got = engine.download(engine.softmax_rows(engine.upload(x), engine.upload_bool(mask), scale=0.25, log=log))
+    want = orc.softmax_rows(x, mask=mask, scale=0.25, log=log)
+    close(got, want, rtol=1e-5, atol=1e-6 if log else 1e-12)
+    assert np.isnan(got[2]).all()
+
+
 def test_softmax_shift_invariance(engine):
     x = rnd(8, 512)
     a, b = engine.upload(x), engine.upload(x + np.float32(4.0))

@@ -1,7 +1,8 @@
 """Device parity of the prefill's fused tails.
 
 mi_qkv_rope_cache (RoPE on the q and k heads of the fused q|k|v rows, the
-cache writes, q in either layout): bit-identical to the engine's own
+cache writes, q in either layout; float4 rows for head widths of a multiple
+of 8, the element-wise form otherwise): bit-identical to the engine's own
 composition -- mi_rope on the q and k blocks, mi_copy_into4 of k and v into
 the caches, mi_copy_strided4 for the regrouped queries (each pinned against
 the oracle by its own tests) -- with every cache row outside the written
@@ -47,7 +48,7 @@ def rope_tables(n, d, theta=1e5):
 
 
 @pytest.mark.parametrize("batch,seq,heads,kv,d,pos0,maxc", [(2, 5, 9, 3, 64, 3, 16), (1, 33, 4, 4, 32, 0, 40),
-                                                           (3, 7, 8, 2, 16, 9, 20)])
+                                                           (3, 7, 8, 2, 16, 9, 20), (2, 3, 2, 1, 12, 1, 8)])
 def test_qkv_rope_cache_equals_composition(engine, batch, seq, heads, kv, d, pos0, maxc):
     rows, w = batch * seq, (heads + 2 * kv) * d
     qkv = rnd(rows, w)
