@@ -350,10 +350,218 @@ __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, i
   if (live && m < M && (lane & 1) == 0) pair_write<MODE>(g, q, m, y, other);
 }
 
+// ------------------------------------ 9 to 32 rows on the matrix cores
+// One 512-thread block per tile of weight rows -- 32 consecutive rows
+// (DM_PLAIN), or two blocks of 32 whose rows pair up lane by lane: gate rows
+// and their up rows (DM_SILU_MUL), the two halves of one 64-wide head
+// (DM_QKV) -- against all M <= 32 activation rows, on
+// v_mfma_f32_32x32x16_bf16 (A: the activation rows times the gain, B: the
+// weight rows; lane l holds row l % 32, k group l / 32 of both).  Each F32
+// activation is split into three BF16 parts (hi + mid + lo = a to within
+// 2^-26 |a|, each remainder exact in F32), so the products keep F32
+// accuracy.  The block's eight wavefronts take the k16 steps w, w + 8, ...;
+// each lane issues all its weight, activation and gain loads before any
+// arithmetic (STEPS steps a wavefront, fixed at compile time), then the
+// eight partial accumulators and the rows' sums of squares fold through LDS
+// in wavefront order and the pair epilogue writes.  Against the LDS-staged
+// VALU form, which re-reads every activation row from LDS for every weight
+// pair, a 32-row step does one MFMA per 16K multiply-adds.
+typedef __bf16 dm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float dm_f32x16 __attribute__((ext_vector_type(16)));
+constexpr int DMFMA_WAVES = 8;
+
+// Three BF16 parts of eight F32 values: the head truncated (it cannot
+// overflow, and a - head is exact), the two remainders rounded to nearest by
+// the hardware conversion; |a - hi - mid - lo| <= 2^-25 |a|.  An infinite or
+// NaN value leaves a NaN remainder: its head carries it alone.
+__device__ __forceinline__ void split3x8(const float (&v)[8], dm_bf16x8 &hi, dm_bf16x8 &mid, dm_bf16x8 &lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t hb = __float_as_uint(v[e]) & 0xffff0000u;
+    const float r1 = v[e] - __uint_as_float(hb);
+    const bool fin = r1 == r1;
+    const __bf16 m = static_cast<__bf16>(fin ? r1 : 0.0f);
+    const float r2 = fin ? r1 - static_cast<float>(m) : 0.0f;
+    hi[e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(hb >> 16));
+    mid[e] = m;
+    lo[e] = static_cast<__bf16>(r2);
+  }
+}
+
+template <int MODE, int STEPS, int NB, bool GAMMA>
+__global__ void __launch_bounds__(64 * DMFMA_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+decode_mfma_kernel(DecodeArgs g, int M) {
+  constexpr int NW = DMFMA_WAVES;
+  __shared__ float red[NW][NB * 16][64];
+  __shared__ float sq[NW][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t = blockIdx.x;
+  const int n = lane & 31, kg = lane >> 5;
+  // The weight row of column n in each block, and whether it exists.
+  int64_t row[NB];
+  bool rv[NB];
+  if constexpr (MODE == DM_PLAIN) {
+    row[0] = 32 * t + n;
+    rv[0] = row[0] < g.N;
+  } else if constexpr (MODE == DM_SILU_MUL) {
+    row[0] = 32 * t + n;
+    row[1] = g.inter + row[0];
+    rv[0] = rv[1] = row[0] < g.inter;
+  } else {
+    row[0] = t * g.d + n;  // g.d == 64: the head's two halves
+    row[1] = row[0] + 32;
+    rv[0] = rv[1] = true;
+  }
+  const int m = lane & 31;
+  const bool mv = m < M;
+  const int64_t nsteps = g.K / 16;
+
+  // Every load is unconditional from an address inside its buffer (the last
+  // step, row 0 of the weight, row 0 of the activations): a load under a
+  // condition compiles to a load through a selected pointer, one that may
+  // point at a private zero.  Steps past the end are skipped below, missing
+  // weight rows and activation rows zeroed.
+  uint4 wb[STEPS][NB];
+  float4 xa[STEPS][2], ga[GAMMA ? STEPS : 1][2];
+  const int64_t mc = mv ? m : 0;
+  int64_t rowc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) rowc[b] = rv[b] ? row[b] : 0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int64_t step = w + NW * s;
+    const int64_t k = (step < nsteps ? step : nsteps - 1) * 16 + 8 * kg;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) wb[s][b] = *reinterpret_cast<const uint4 *>(g.w + rowc[b] * g.K + k);
+    xa[s][0] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k);
+    xa[s][1] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k + 4);
+    if constexpr (GAMMA) {
+      ga[s][0] = *reinterpret_cast<const float4 *>(g.gamma + k);
+      ga[s][1] = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
+    }
+  }
+  dm_f32x16 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
+  float ssq = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    if (w + NW * s < nsteps) {
+      float v[8] = {xa[s][0].x, xa[s][0].y, xa[s][0].z, xa[s][0].w, xa[s][1].x, xa[s][1].y, xa[s][1].z, xa[s][1].w};
+      if (!mv) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+      }
+      if constexpr (GAMMA) {
+        const float gm[8] = {ga[s][0].x, ga[s][0].y, ga[s][0].z, ga[s][0].w,
+                             ga[s][1].x, ga[s][1].y, ga[s][1].z, ga[s][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ssq += v[e] * v[e];
+          v[e] = v[e] * gm[e];
+        }
+      }
+      dm_bf16x8 hi, mid, lo;
+      split3x8(v, hi, mid, lo);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? wb[s][b] : make_uint4(0, 0, 0, 0));
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wv, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, wv, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wv, acc[b], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[w][b * 16 + r][lane] = acc[b][r];
+  sq[w][lane] = ssq;
+  __syncthreads();
+  // Wavefront w finishes values r = 2w, 2w + 1 of every block: rows
+  // m = 8 (r / 4) + 4 (lane / 32) + r % 4, column n = lane % 32.
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * w + rr;
+    const int mo = 8 * (r >> 2) + 4 * kg + (r & 3);
+    if (mo >= M) continue;
+    float y[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float a = red[0][b * 16 + r][lane];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) a += red[v][b * 16 + r][lane];
+      y[b] = a;
+    }
+    if constexpr (GAMMA) {
+      float ss = sq[0][mo] + sq[0][mo + 32];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) ss += sq[v][mo] + sq[v][mo + 32];
+      const float rms = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) y[b] = y[b] / rms;
+    }
+    if constexpr (MODE == DM_PLAIN) {
+      if (rv[0]) {
+        float *o = g.out + mo * g.ldo + row[0];
+        *o = g.resid ? __fadd_rn(g.resid[mo * g.ldo + row[0]], y[0]) : y[0];
+      }
+    } else if constexpr (MODE == DM_SILU_MUL) {
+      if (rv[0]) g.out[mo * g.ldo + row[0]] = silu2(y[0]) * y[1];
+    } else {
+      PairRows q{row[0], row[1], t, n, true};
+      pair_write<MODE>(g, q, mo, y[0], y[1]);
+    }
+  }
+}
+
+// Steps a wavefront takes for k = 16 * nsteps, rounded up to an instance,
+// or 0 past what the registers hold without spilling (the loads of every
+// step are in flight at once: 4 NB + 8 + (gain) 8 registers a step).
+static int dmfma_steps(int64_t K, int nb, bool gamma) {
+  const int64_t need = (K / 16 + DMFMA_WAVES - 1) / DMFMA_WAVES;
+  const int most = nb == 1 ? (gamma ? 10 : 16) : (gamma ? 6 : 8);
+  static const int inst[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+  for (int v : inst)
+    if (v >= need) return v <= most ? v : 0;
+  return 0;  // longer rows: the LDS-staged kernel
+}
+
+template <int MODE, int NB, bool GAMMA>
+static void launch_dmfma(int steps, unsigned grid, const DecodeArgs &g, int M, hipStream_t st) {
+  switch (steps) {
+#define MI_DMF(S) case S: decode_mfma_kernel<MODE, S, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+    MI_DMF(1) MI_DMF(2) MI_DMF(3) MI_DMF(4) MI_DMF(5) MI_DMF(6)
+#undef MI_DMF
+    case 8: if constexpr (!(NB == 2 && GAMMA)) decode_mfma_kernel<MODE, 8, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+    case 10: if constexpr (NB == 1) decode_mfma_kernel<MODE, 10, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+    case 12: if constexpr (NB == 1 && !GAMMA) decode_mfma_kernel<MODE, 12, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+    case 16: if constexpr (NB == 1 && !GAMMA) decode_mfma_kernel<MODE, 16, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+  }
+}
+
+// The matrix-core form for 9 to 32 rows; false when the shape does not fit it.
+template <int MODE>
+static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
+  if (g.K % 16) return false;
+  constexpr int NB = MODE == DM_PLAIN ? 1 : 2;
+  if (MODE == DM_QKV && g.d != 64) return false;
+  const int steps = dmfma_steps(g.K, NB, g.gamma != nullptr);
+  if (!steps) return false;
+  const int64_t tiles = MODE == DM_PLAIN ? (g.N + 31) / 32 : (MODE == DM_SILU_MUL ? (g.inter + 31) / 32 : g.H + 2 * g.KVH);
+  const unsigned grid = static_cast<unsigned>(tiles);
+  if (g.gamma) launch_dmfma<MODE, NB, true>(steps, grid, g, static_cast<int>(M), st);
+  else launch_dmfma<MODE, NB, false>(steps, grid, g, static_cast<int>(M), st);
+  return true;
+}
+
 template <int MODE>
 static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
   if (M > 8) {
+    if (launch_dmfma_mode<MODE>(M, g, st)) return;
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
     return;
   }
