@@ -358,17 +358,17 @@ __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, i
 // v_mfma_f32_32x32x16_bf16 (A: the activation rows times the gain, B: the
 // weight rows; lane l holds row l % 32, k group l / 32 of both).  Each F32
 // activation is split into three BF16 parts (hi + mid + lo = a to within
-// 2^-26 |a|, each remainder exact in F32), so the products keep F32
-// accuracy.  The block's eight wavefronts take the k16 steps w, w + 8, ...;
+// 2^-25 |a|, each remainder exact in F32), so the products keep F32
+// accuracy.  The block's sixteen wavefronts take the k16 steps w, w + 16, ...;
 // each lane issues all its weight, activation and gain loads before any
 // arithmetic (STEPS steps a wavefront, fixed at compile time), then the
-// eight partial accumulators and the rows' sums of squares fold through LDS
+// sixteen partial accumulators and the rows' sums of squares fold through LDS
 // in wavefront order and the pair epilogue writes.  Against the LDS-staged
 // VALU form, which re-reads every activation row from LDS for every weight
 // pair, a 32-row step does one MFMA per 16K multiply-adds.
 typedef __bf16 dm_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float dm_f32x16 __attribute__((ext_vector_type(16)));
-constexpr int DMFMA_WAVES = 8;
+constexpr int DMFMA_WAVES = 16;
 
 // Three BF16 parts of eight F32 values: the head truncated (it cannot
 // overflow, and a - head is exact), the two remainders rounded to nearest by
@@ -389,7 +389,7 @@ __device__ __forceinline__ void split3x8(const float (&v)[8], dm_bf16x8 &hi, dm_
 }
 
 template <int MODE, int STEPS, int NB, bool GAMMA>
-__global__ void __launch_bounds__(64 * DMFMA_WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(64 * DMFMA_WAVES)
 decode_mfma_kernel(DecodeArgs g, int M) {
   constexpr int NW = DMFMA_WAVES;
   __shared__ float red[NW][NB * 16][64];
@@ -480,13 +480,13 @@ decode_mfma_kernel(DecodeArgs g, int M) {
     for (int r = 0; r < 16; ++r) red[w][b * 16 + r][lane] = acc[b][r];
   sq[w][lane] = ssq;
   __syncthreads();
-  // Wavefront w finishes values r = 2w, 2w + 1 of every block: rows
+  // Wavefront w finishes value r = w of every block: rows
   // m = 8 (r / 4) + 4 (lane / 32) + r % 4, column n = lane % 32.
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = 2 * w + rr;
+  static_assert(NW == 16, "one accumulator value a wavefront");
+  {
+    const int r = w;
     const int mo = 8 * (r >> 2) + 4 * kg + (r & 3);
-    if (mo >= M) continue;
+    if (mo >= M) return;
     float y[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -517,28 +517,35 @@ decode_mfma_kernel(DecodeArgs g, int M) {
   }
 }
 
-// Steps a wavefront takes for k = 16 * nsteps, rounded up to an instance,
-// or 0 past what the registers hold without spilling (the loads of every
-// step are in flight at once: 4 NB + 8 + (gain) 8 registers a step).
+// Steps a wavefront takes for k = 16 * nsteps, or 0 past what the registers
+// hold without spilling: the loads of every step are in flight at once (4 NB
+// + 8, plus 8 with a gain, registers a step) within the 128 registers of four
+// wavefronts a SIMD -- k up to 1536 plain, 768 for paired rows with a gain.
+template <int NB, bool GAMMA>
+constexpr int dmfma_most() { return NB == 1 ? (GAMMA ? 5 : 6) : (GAMMA ? 3 : 5); }
+
 static int dmfma_steps(int64_t K, int nb, bool gamma) {
   const int64_t need = (K / 16 + DMFMA_WAVES - 1) / DMFMA_WAVES;
-  const int most = nb == 1 ? (gamma ? 10 : 16) : (gamma ? 6 : 8);
-  static const int inst[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
-  for (int v : inst)
-    if (v >= need) return v <= most ? v : 0;
-  return 0;  // longer rows: the LDS-staged kernel
+  const int most = nb == 1 ? (gamma ? dmfma_most<1, true>() : dmfma_most<1, false>())
+                           : (gamma ? dmfma_most<2, true>() : dmfma_most<2, false>());
+  return need <= most ? static_cast<int>(need) : 0;  // longer rows: the LDS-staged kernel
+}
+
+template <int MODE, int NB, bool GAMMA, int S>
+static void launch_dmfma_s(unsigned grid, const DecodeArgs &g, int M, hipStream_t st) {
+  if constexpr (S <= dmfma_most<NB, GAMMA>())
+    decode_mfma_kernel<MODE, S, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M);
 }
 
 template <int MODE, int NB, bool GAMMA>
 static void launch_dmfma(int steps, unsigned grid, const DecodeArgs &g, int M, hipStream_t st) {
   switch (steps) {
-#define MI_DMF(S) case S: decode_mfma_kernel<MODE, S, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
-    MI_DMF(1) MI_DMF(2) MI_DMF(3) MI_DMF(4) MI_DMF(5) MI_DMF(6)
-#undef MI_DMF
-    case 8: if constexpr (!(NB == 2 && GAMMA)) decode_mfma_kernel<MODE, 8, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
-    case 10: if constexpr (NB == 1) decode_mfma_kernel<MODE, 10, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
-    case 12: if constexpr (NB == 1 && !GAMMA) decode_mfma_kernel<MODE, 12, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
-    case 16: if constexpr (NB == 1 && !GAMMA) decode_mfma_kernel<MODE, 16, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M); break;
+    case 1: launch_dmfma_s<MODE, NB, GAMMA, 1>(grid, g, M, st); break;
+    case 2: launch_dmfma_s<MODE, NB, GAMMA, 2>(grid, g, M, st); break;
+    case 3: launch_dmfma_s<MODE, NB, GAMMA, 3>(grid, g, M, st); break;
+    case 4: launch_dmfma_s<MODE, NB, GAMMA, 4>(grid, g, M, st); break;
+    case 5: launch_dmfma_s<MODE, NB, GAMMA, 5>(grid, g, M, st); break;
+    case 6: launch_dmfma_s<MODE, NB, GAMMA, 6>(grid, g, M, st); break;
   }
 }
 
