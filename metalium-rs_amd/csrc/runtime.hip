@@ -339,14 +339,33 @@ static int download_raw(mi_ctx *ctx, mi_id id, void *dst, int64_t n, int want_el
   size_t bytes = static_cast<size_t>(b->numel()) * elem_size(b->elem);
   const char *d = static_cast<const char *>(b->ptr);
   char *o = static_cast<char *>(dst);
-  for (size_t off = 0; off < bytes; off += Ctx::kStageBytes) {
-    size_t m = std::min(Ctx::kStageBytes, bytes - off);
-    int slot = stage_slot(ctx);
+  // Up to kStageSlots chunks in flight: the copy of chunk k + slots is issued
+  // as soon as chunk k has left its slot, so the device-to-host copies overlap
+  // the host copies out of the staging memory.
+  constexpr int S = Ctx::kStageSlots;
+  const size_t nch = (bytes + Ctx::kStageBytes - 1) / Ctx::kStageBytes;
+  int slot_of[S] = {};
+  auto issue = [&](size_t k) -> hipError_t {
+    const size_t off = k * Ctx::kStageBytes, m = std::min(Ctx::kStageBytes, bytes - off);
+    const int slot = stage_slot(ctx);  // waits for the slot's previous copy
+    slot_of[k % S] = slot;
     hipError_t e = hipMemcpyAsync(ctx->stage[slot], d + off, m, hipMemcpyDeviceToHost, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return fail(ctx, MI_E_HIP, "%s: %s", what, hipGetErrorString(e));
-    std::memcpy(o + off, ctx->stage[slot], m);
+    if (e == hipSuccess) e = hipEventRecord(ctx->stage_done[slot], ctx->stream);
+    if (e == hipSuccess) ctx->stage_pending[slot] = true;
+    return e;
+  };
+  hipError_t e = hipSuccess;
+  for (size_t k = 0; k < nch && k < static_cast<size_t>(S) && e == hipSuccess; ++k) e = issue(k);
+  for (size_t k = 0; k < nch && e == hipSuccess; ++k) {
+    const int slot = slot_of[k % S];
+    e = hipEventSynchronize(ctx->stage_done[slot]);
+    if (e != hipSuccess) break;
+    ctx->stage_pending[slot] = false;
+    const size_t off = k * Ctx::kStageBytes;
+    std::memcpy(o + off, ctx->stage[slot], std::min(Ctx::kStageBytes, bytes - off));
+    if (k + S < nch) e = issue(k + S);
   }
+  if (e != hipSuccess) return fail(ctx, MI_E_HIP, "%s: %s", what, hipGetErrorString(e));
   ctx->report.downloads++;
   ctx->report.bytes_down += bytes;
   return MI_OK;

@@ -189,6 +189,24 @@ def test_large_vector_path(engine):
     close(engine.download(engine.eltwise_op_as("EXP", a)), orc.eltwise(K["EXP"], x), rtol=1e-5)
 
 
+@pytest.mark.parametrize("n", [5 * (8 << 20) + 123, 3 * (8 << 20), 1000])
+def test_transfer_round_trip_chunks(engine, n):
+    # More 32 MiB staging chunks than slots (downloads keep four in flight),
+    # sizes that are not a chunk multiple, F32, BF16 and raw 32-bit datums.
+    x = RNG.standard_normal(n).astype(np.float32).reshape(1, n)
+    ix = engine.upload(x)
+    same_bits(engine.download(ix), x)
+    b = (x.view(np.uint32) >> 16).astype(np.uint16)
+    ib = engine.upload_bf16(b)
+    assert np.array_equal(engine.download(ib), b)
+    bits = x.view(np.uint32)
+    iu = engine.upload_bits(bits, I32)
+    assert np.array_equal(engine.download(iu).view(np.uint32), bits)
+    same_bits(engine.download(ix), x)  # again, after the slots were reused by the uploads
+    for i in (ix, ib, iu):
+        engine.free(i)
+
+
 # ------------------------------------------------------------------ reductions
 def reduce_tol(x, axis):
     # Normwise: rel 1e-5 of the sum of magnitudes along the reduced axis.
