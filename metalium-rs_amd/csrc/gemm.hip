@@ -1186,13 +1186,43 @@ static hipError_t launch_split_orient(const Plan &p, hipStream_t st) {
   return launch_split_cfg<SA, SB, TO, BM, BN, WM, WN, false, false, GUARD>(p, st);
 }
 
+// Columns [n0, n0 + n) of a single product (no batch, no split-K) as a plan
+// of its own: B, the result, the bias and the residual start n0 columns in,
+// the result and residual keep their full row pitch.
+static Plan column_block(const Plan &p, int64_t n0, int64_t n) {
+  Plan q = p;
+  const size_t esb = p.eb == MI_BF16 ? 2 : 4, eso = p.eo == MI_BF16 ? 2 : 4;
+  q.N = n;
+  q.b = static_cast<const char *>(p.b) + static_cast<size_t>(p.tb ? n0 * p.ldb : n0) * esb;
+  q.c = static_cast<char *>(p.c) + static_cast<size_t>(n0) * eso;
+  q.ldc = p.ldc > 0 ? p.ldc : p.N;
+  if (p.bias) q.bias = p.bias + n0;
+  if (p.resid) q.resid = p.resid + n0;
+  return q;
+}
+
 // F32 (or mixed) operands in the fast mode: the split kernel, 128 x 128 tiles
-// when they give every CU a tile, else 64 x 64.
+// when they give every CU a tile, else 64 x 64.  A width that is not a
+// multiple of 128 (a 960-wide q|k|v or 576-wide down projection) runs its
+// 128-aligned columns on unguarded tiles and only the rest on the guarded
+// form: the guarded loads slow every tile, not just the edge ones (a
+// 16384 x 960 x 576 product 257 us guarded against 251 us for an exact one
+// three times its size).
 template <typename SA, typename SB, typename TO>
 static hipError_t run_split(const Plan &p, hipStream_t st) {
   const int64_t tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
   if (tiles128 >= 256) {
     if (tiles_exactly(p, 128, 128, 64, 8)) return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, false>(p, st);
+    if (p.batch == 1 && p.kc == 0 && p.N > 128) {
+      const int64_t ni = p.N / 128 * 128;
+      const Plan in = column_block(p, 0, ni), edge = column_block(p, ni, p.N - ni);
+      if (tiles_exactly(in, 128, 128, 64, 8)) {
+        hipError_t e = launch_split_orient<SA, SB, TO, 128, 128, 2, 2, false>(in, st);
+        if (e != hipSuccess) return e;
+        if (tiles_exactly(edge, 64, 64, 64, 8)) return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, false>(edge, st);
+        return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, true>(edge, st);
+      }
+    }
     return launch_split_orient<SA, SB, TO, 128, 128, 2, 2, true>(p, st);
   }
   if (tiles_exactly(p, 64, 64, 64, 8)) return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, false>(p, st);

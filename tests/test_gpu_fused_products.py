@@ -57,6 +57,7 @@ LINEAR_SHAPES = [
     (2048, 2048, 2048, False, "f32", "fast: split kernel"),
     (2048, 2048, 512, True, "bf16", "direct 128x128"),
     (4096, 4096, 256, False, "bf16", "direct 256x256"),
+    (16384, 960, 576, True, "w_bf16", "fast: split kernel, 128-aligned columns + edge"),
     (5, 7, 0, False, "f32", "empty sums"),
 ]
 
@@ -92,6 +93,21 @@ def test_linear_equals_product_then_adds(engine, mode, m, n, k, tw, kind, path, 
         if ir:
             ref = resid + ref
         assert np.all(np.abs(got - ref) <= mm_tol(x, wf, 1e-5) + 1e-6 * (np.abs(ref) + 1e-30))
+
+
+@pytest.mark.parametrize("m,n,k", [(16384, 960, 576), (16384, 576, 1536)])
+def test_split_kernel_column_blocks_against_oracle(engine, m, n, k):
+    """Widths that are not a multiple of 128 on the fast mode's split kernel:
+    the 128-aligned columns and the rest run as two launches.  Rows sampled
+    against float64 within the normwise F32 bound."""
+    x = rnd(m, k)
+    wb = orc.to_bf16(rnd(n, k))
+    got = engine.download(engine.matmul_dram(engine.upload(x), False, engine.upload_bf16(wb), True))
+    w = orc.from_bf16(wb).astype(np.float64)
+    sel = np.r_[0:64, m // 2:m // 2 + 64, m - 64:m]
+    xs = x[sel].astype(np.float64)
+    ref = xs @ w.T
+    assert np.all(np.abs(got[sel] - ref) <= 1e-5 * (np.abs(xs) @ np.abs(w).T) + 1e-30)
 
 
 def test_linear_bf16_result_rounds_once_after_the_adds(engine):
