@@ -76,14 +76,15 @@ Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3
 
 // The forward of `t` positions per sequence at cache length m->len; returns
 // the hidden states [batch * t, hidden] before the final norm.
-Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t) {
+// The hidden rows of token ids already on the device ([batch * t] I32, rows
+// (sequence, position)).
+Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   mi_ctx *ctx = m->ctx;
   const mi_llama_config &c = m->cfg;
   const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim, G = H / KVH;
   const int64_t pos0 = m->len, ctxlen = pos0 + t, maxc = c.max_ctx;
   const int64_t rows = batch * t;
 
-  Tensor idx = burn::int_from_data(ctx, ids, {rows});
   Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
   x = x.reshape({rows, c.hidden});
 
@@ -150,6 +151,10 @@ Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t)
   }
   m->len = ctxlen;
   return x;
+}
+
+Tensor forward_hidden(mi_llama *m, const int32_t *ids, int64_t batch, int64_t t) {
+  return forward_ids(m, burn::int_from_data(m->ctx, ids, {batch * t}), batch, t);
 }
 
 // The final norm and the tied head over the last position of each sequence:
@@ -326,9 +331,18 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
     std::vector<int32_t> tok = burn::int_into_data(next);  // waits for the prefill
     auto t1 = clock::now();
     for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
+    // Each step's tokens stay on the device and feed the next step's
+    // embedding gather: no host round trip (and no drained queue) between
+    // steps; the tokens are read back once at the end.
+    std::vector<Tensor> steps;
+    steps.reserve(n_new > 0 ? n_new - 1 : 0);
     for (int32_t s = 1; s < n_new; ++s) {
-      Tensor hs = forward_hidden(m, tok.data(), batch, 1);
-      tok = burn::int_into_data(burn::argmax_rows(head_last(m, hs, batch, 1)));
+      Tensor hs = forward_ids(m, next.reshape({batch}), batch, 1);
+      next = burn::argmax_rows(head_last(m, hs, batch, 1));
+      steps.push_back(next);
+    }
+    for (int32_t s = 1; s < n_new; ++s) {
+      tok = burn::int_into_data(steps[s - 1]);
       for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
     }
     auto t2 = clock::now();
