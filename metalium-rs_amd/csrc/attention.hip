@@ -306,7 +306,11 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   const int64_t items = batch * kv_heads * t, nmax = pos0 + t;
   int64_t S = (nmax + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
   const int64_t want = (ATT_TARGET_BLOCKS + items - 1) / items;
-  const int64_t cap = (nmax + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
+  // With many items (a batch of sequences) longer chunks: fewer blocks and
+  // partials to combine (batch-32 decode 1.94 -> 1.89 ms a step at 128 keys;
+  // batch 1 is fastest at 64).
+  const int64_t min_chunk = items >= 64 ? 2 * ATT_MIN_CHUNK : ATT_MIN_CHUNK;
+  const int64_t cap = (nmax + min_chunk - 1) / min_chunk;
   if (want > S) S = want < cap ? want : cap;
   if (S < 1) S = 1;
   const int64_t chunk = ((nmax + S - 1) / S + 3) / 4 * 4;
