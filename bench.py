@@ -275,7 +275,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(the path would shard by output columns or rows with RCCL; nothing multi-GPU is built)",
+              file=sys.stderr)
         return 2
     if args.suite:
         return suite(args.steps, args.matmul_mode)
