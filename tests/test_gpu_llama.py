@@ -92,13 +92,15 @@ def close_logits(got, want, rel=2e-3):
     assert np.abs(got - want).max() <= rel * scale, (np.abs(got - want).max(), scale)
 
 
-@pytest.mark.parametrize("t", [12, 24])  # fused attention kernel; product composition (over 16 positions)
-def test_prefill_logits_all_positions(engine, tiny, t):
+# Fused attention kernel (up to 16 new positions, or a long prompt of up to 4
+# sequences); the product composition (a long prompt of more sequences).
+@pytest.mark.parametrize("batch,t", [(2, 12), (2, 24), (6, 24)])
+def test_prefill_logits_all_positions(engine, tiny, batch, t):
     m, W = tiny
     rng = np.random.default_rng(5)
-    ids = rng.integers(0, TINY["vocab"], (2, t)).astype(np.int32)
+    ids = rng.integers(0, TINY["vocab"], (batch, t)).astype(np.int32)
     m.reset()
-    got = engine.download(m.forward(ids, all_positions=True)).reshape(2, t, -1)
+    got = engine.download(m.forward(ids, all_positions=True)).reshape(batch, t, -1)
     close_logits(got, ref_logits(W, TINY, ids))
 
 
