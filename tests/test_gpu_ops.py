@@ -699,6 +699,8 @@ def attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale):
     (3, 16, 8, 1, 128, 30, 64),      # 8 query heads per kv head
     (2, 3, 4, 4, 32, 2000, 2304),    # no grouping, context over one chunk's limit
     (1, 2, 6, 2, 64, 0, 8),          # whole cache, one chunk, direct write
+    (1, 512, 9, 3, 64, 0, 640),      # a 512-token prompt at batch 1 (prefill takes the fused kernel)
+    (4, 100, 9, 3, 64, 28, 160),     # prompts of 4 sequences after 28 cached positions
 ])
 def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     q = rnd(batch * t, heads * D)
