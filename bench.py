@@ -166,10 +166,31 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128) -> dict:
     m.generate(ids[:, :32], 4)  # warm the kernels
     out, pf_ms, dc_ms = m.generate(ids, new)
     m.close()
+    # Rooflines (algorithmic work): a decode step reads every BF16 weight once
+    # (134.48 M parameters, the tied table included) plus each sequence's F32
+    # key/value cache (2 x 30 layers x 3 kv heads x 64 x 4 B a position, at the
+    # steps' mean context); a prefill's FLOP are 2 x tokens x the layers'
+    # 106.17 M weights plus causal attention (2 t (t + 1) x 64 x 9 heads x 30
+    # layers a sequence) and the last position's head.
+    cfg = miburn.SMOLLM2_135M
+    per_layer = ((cfg["heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"] * cfg["hidden"] + cfg["hidden"] ** 2
+                 + 3 * cfg["intermediate"] * cfg["hidden"])
+    layer_params = cfg["layers"] * per_layer
+    params = layer_params + cfg["vocab"] * cfg["hidden"]
+    kv_per_pos = 2 * cfg["layers"] * cfg["kv_heads"] * cfg["head_dim"] * 4
+    mean_ctx = prompt + new / 2
+    step_bytes = 2 * params + batch * kv_per_pos * mean_ctx
+    dc_step_ms = dc_ms / max(new - 1, 1)
+    attn = 2 * prompt * (prompt + 1) * cfg["head_dim"] * cfg["heads"] * cfg["layers"]
+    pf_flop = batch * (2 * prompt * layer_params + attn + 2 * cfg["hidden"] * cfg["vocab"])
     return {"batch": batch, "prompt": prompt, "new_tokens": new,
             "prefill_ms": round(pf_ms, 2), "prefill_tokens_per_s": round(batch * prompt / (pf_ms / 1e3), 1),
-            "decode_ms_per_step": round(dc_ms / max(new - 1, 1), 3),
-            "decode_tokens_per_s": round(batch * (new - 1) / (dc_ms / 1e3), 1)}
+            "prefill_gflop": round(pf_flop / 1e9, 1),
+            "prefill_mfma_frac": round(pf_flop / (pf_ms * 1e-3) / (PEAK_TFLOPS["bf16"] * 1e12), 4),
+            "decode_ms_per_step": round(dc_step_ms, 3),
+            "decode_tokens_per_s": round(batch * (new - 1) / (dc_ms / 1e3), 1),
+            "decode_hbm_mb_per_step": round(step_bytes / 1e6, 1),
+            "decode_hbm_frac": round(step_bytes / (dc_step_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
 
 
 def traced_steps(eng, step_ids, inputs, batches):

@@ -11,8 +11,9 @@
 // residual add, and silu(gate) * up (ops.rs:2622-2651).
 //
 // MI355X design.  Decode reads every weight once per step: the kernels are
-// HBM-latency-bound GEMVs.  A wavefront owns two output rows of the weight
-// and all M (<= 8) activation rows; each lane streams 16 bytes (8 BF16) of
+// HBM-latency-bound GEMVs.  Up to 2 activation rows (up to 8 where the
+// matrix-core form below does not fit the shape) a wavefront owns two output
+// rows of the weight and all M activation rows; each lane streams 16 bytes (8 BF16) of
 // both weight rows per step, so a 576-wide row is read by the wavefront in two
 // coalesced passes.  The activation rows (a few KB) are re-read from cache by
 // every wavefront; when a gain is given each wavefront first folds its rows'
@@ -128,16 +129,21 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   // The weight rows are independent of the norm: with K <= 2048 (four
   // 16-byte chunks a lane) all of them are requested first, so the norm's
   // loads and reduction overlap the weights' HBM latency.
+  // The loads are unconditional, from clamped rows and columns: a load under
+  // a condition compiles to a branch that waits for it before the next is
+  // issued (0.956 -> 0.922 ms a batch-1 SmolLM2 decode step).  Without a
+  // second row (a lone last row) the first is read twice and the second
+  // product is discarded by pair_write.
   constexpr int PRE = 4;
   uint4 pw0[PRE], pw1[PRE];
+  const int64_t r1c = has1 ? r1 : r0;
   if (g.K <= 512 * PRE) {
 #pragma unroll
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
-      if (k < g.K) {
-        pw0[c] = *reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k);
-        pw1[c] = has1 ? *reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k) : make_uint4(0u, 0u, 0u, 0u);
-      }
+      const int64_t kc = k < g.K ? k : g.K - 8;
+      pw0[c] = *reinterpret_cast<const uint4 *>(g.w + r0 * g.K + kc);
+      pw1[c] = *reinterpret_cast<const uint4 *>(g.w + r1c * g.K + kc);
     }
   }
 
@@ -205,10 +211,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
       float w0[8], w1[8];
       bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
-      if (has1) bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1 * g.K + k), w1);
-      else
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w1[e] = 0.0f;
+      bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1c * g.K + k), w1);
       step(k, w0, w1);
     }
   }
@@ -350,7 +353,7 @@ __global__ void __launch_bounds__(256) decode_matvec_wide_kernel(DecodeArgs g, i
   if (live && m < M && (lane & 1) == 0) pair_write<MODE>(g, q, m, y, other);
 }
 
-// ------------------------------------ 9 to 32 rows on the matrix cores
+// ------------------------------------ 3 to 32 rows on the matrix cores
 // One 512-thread block per tile of weight rows -- 32 consecutive rows
 // (DM_PLAIN), or two blocks of 32 whose rows pair up lane by lane: gate rows
 // and their up rows (DM_SILU_MUL), the two halves of one 64-wide head
@@ -549,7 +552,7 @@ static void launch_dmfma(int steps, unsigned grid, const DecodeArgs &g, int M, h
   }
 }
 
-// The matrix-core form for 9 to 32 rows; false when the shape does not fit it.
+// The matrix-core form for 3 to 32 rows; false when the shape does not fit it.
 template <int MODE>
 static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   if (g.K % 16) return false;
@@ -564,11 +567,16 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   return true;
 }
 
+// Rows up to which the GEMV beats the matrix-core form (SmolLM2 decode step,
+// ms: batch 2 1.12 against 1.28, batch 3 1.32 against 1.31, batch 4 1.54
+// against 1.34, batch 8 2.43 against 1.38).
+constexpr int64_t DECODE_GEMV_MAX_M = 2;
+
 template <int MODE>
 static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
+  if (M > DECODE_GEMV_MAX_M && launch_dmfma_mode<MODE>(M, g, st)) return;
   if (M > 8) {
-    if (launch_dmfma_mode<MODE>(M, g, st)) return;
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
     return;
   }

@@ -72,8 +72,9 @@ constexpr int64_t kFusedAttentionMaxT = 16;
 // the composition's matrix-core products win (37 against 43.5 ms).
 constexpr int64_t kFusedAttentionLongMaxBatch = 4;
 // Largest batch whose decode step takes the fused projections, and whose
-// head is one fused norm + GEMV launch (beyond it the head is a product on the
-// matrix cores: the GEMV would re-read the activation rows per block).
+// head is one fused norm + projection launch (mi_norm_matvec: the GEMV up to 2
+// rows, the matrix-core form above; beyond kFusedHeadMaxBatch the head is a
+// plain product on the matrix cores).
 constexpr int64_t kDecodeMaxBatch = 32;
 constexpr int64_t kFusedHeadMaxBatch = 8;
 

@@ -727,10 +727,10 @@ def rms_ref(x, g, eps):
     return x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + eps) * g.astype(np.float64)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 9, 17, 32])  # one GEMV wavefront per row pair; matrix cores above 8
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 9, 17, 32])  # one GEMV wavefront per row pair; matrix cores above 2
 @pytest.mark.parametrize("N,K", [(576, 576), (577, 576), (576, 1536), (100, 2056)])
 def test_norm_matvec_residual(engine, M, N, K):
-    # k 2056 is not a multiple of 16: the LDS-staged form above 8 rows.
+    # k 2056 is not a multiple of 16: the GEMV up to 8 rows, the LDS-staged form above.
     eps = 1e-5
     x, g, wb = decode_inputs(M, K, N)
     res = rnd(M, N)
@@ -747,7 +747,7 @@ def test_norm_matvec_residual(engine, M, N, K):
 
 @pytest.mark.parametrize("M,K", [(4, 1536), (20, 1536), (9, 576), (20, 576), (32, 576), (32, 64)])
 def test_norm_matvec_silu_mul(engine, M, K):
-    # Above 8 rows and up to k 768 with a gain: the matrix-core form.
+    # Above 2 rows and up to k 768 with a gain: the matrix-core form.
     I, eps = 1536, 1e-5
     x, g, wb = decode_inputs(M, K, 2 * I)
     w = orc.from_bf16(wb).astype(np.float64)
