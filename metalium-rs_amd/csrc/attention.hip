@@ -82,12 +82,17 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
   for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const float4 *>(qrow + g * D + 4 * sl);
   // The value rows of the first P V pass are independent of the scores:
   // their loads are issued now and land while the scores and softmax run.
+  // Key and value rows are loaded unconditionally, rows past the chunk's end
+  // clamped to its last (row lo when the chunk is empty, still below the
+  // context): a load under a condition compiles to a branch that waits for
+  // it.  Those lanes' scores are never written and their values never used.
   const int64_t first = static_cast<int64_t>(wave) * KPW + kk;
+  const int64_t last = len > 0 ? len - 1 : 0;
   float4 vv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t c = first + u * STEP;
-    vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+    vv[u] = *reinterpret_cast<const float4 *>(V + (c < len ? c : last) * D + 4 * sl);
   }
 
   // Scores, U accesses in flight per wavefront.
@@ -96,7 +101,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + u * STEP;
-      kv[u] = c < len ? *reinterpret_cast<const float4 *>(K + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+      kv[u] = *reinterpret_cast<const float4 *>(K + (c < len ? c : last) * D + 4 * sl);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -144,7 +149,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t c = c0 + u * STEP;
-        vv[u] = c < len ? *reinterpret_cast<const float4 *>(V + c * D + 4 * sl) : make_float4(0.f, 0.f, 0.f, 0.f);
+        vv[u] = *reinterpret_cast<const float4 *>(V + (c < len ? c : last) * D + 4 * sl);
       }
     }
 #pragma unroll
