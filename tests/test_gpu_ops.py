@@ -728,7 +728,7 @@ def rms_ref(x, g, eps):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 8, 9, 17, 32])  # one GEMV wavefront per row pair; matrix cores above 2
-@pytest.mark.parametrize("N,K", [(576, 576), (577, 576), (576, 1536), (100, 2056)])
+@pytest.mark.parametrize("N,K", [(576, 576), (577, 576), (576, 1536), (100, 2056), (16400, 576)])
 def test_norm_matvec_residual(engine, M, N, K):
     # k 2056 is not a multiple of 16: the GEMV up to 8 rows, the LDS-staged form above.
     eps = 1e-5
