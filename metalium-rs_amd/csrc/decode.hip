@@ -571,15 +571,11 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
 // ms: batch 2 1.12 against 1.28, batch 3 1.32 against 1.31, batch 4 1.54
 // against 1.34, batch 8 2.43 against 1.38).
 constexpr int64_t DECODE_GEMV_MAX_M = 2;
-// Output rows from which the matrix-core form takes even 1 or 2 activation
-// rows: a tall weight (a vocabulary head) as 32-row tiles instead of one
-// wavefront, with its own norm pass, per row pair.
-constexpr int64_t DECODE_TALL_N = 16384;
 
 template <int MODE>
 static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
-  if ((M > DECODE_GEMV_MAX_M || g.N >= DECODE_TALL_N) && launch_dmfma_mode<MODE>(M, g, st)) return;
+  if (M > DECODE_GEMV_MAX_M && launch_dmfma_mode<MODE>(M, g, st)) return;
   if (M > 8) {
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
     return;
