@@ -597,7 +597,8 @@ static int check_common(mi_ctx *ctx, const Buffer *xb, const Buffer *wb, const B
     return fail(ctx, MI_E_UNSUPPORTED, "%s: %lld activation rows (1 to %d)", what, (long long)xb->rows, DECODE_MAX_M);
   if (wb->cols != xb->cols) return fail(ctx, MI_E_ARG, "%s: weight is [%lld, %lld], activations [%lld, %lld]", what,
                                         (long long)wb->rows, (long long)wb->cols, (long long)xb->rows, (long long)xb->cols);
-  if (xb->cols % 8) return fail(ctx, MI_E_UNSUPPORTED, "%s: width %lld is not a multiple of 8", what, (long long)xb->cols);
+  if (xb->cols < 8 || xb->cols % 8)
+    return fail(ctx, MI_E_UNSUPPORTED, "%s: width %lld is not a positive multiple of 8", what, (long long)xb->cols);
   if (gb && (gb->elem != MI_F32 || gb->rows * gb->cols != xb->cols))
     return fail(ctx, MI_E_ARG, "%s: gain must be [1, %lld] F32", what, (long long)xb->cols);
   if (!aligned16(xb->ptr) || !aligned16(wb->ptr) || (gb && !aligned16(gb->ptr)))

@@ -325,7 +325,9 @@ int mi_llama_forward(mi_llama *m, const int32_t *ids, int32_t batch, int32_t t, 
 
 int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t t_prompt, int32_t n_new,
                       int32_t *out, double *prefill_ms, double *decode_ms) {
-  if (!m || !prompt || !out || batch <= 0 || t_prompt <= 0 || n_new < 0) return MI_E_ARG;
+  // At least one new token, as the reference's generate_with asserts
+  // (crates/tt-models/src/llama.rs:1155): `out` holds batch * n_new tokens.
+  if (!m || !prompt || !out || batch <= 0 || t_prompt <= 0 || n_new < 1) return MI_E_ARG;
   using clock = std::chrono::steady_clock;
   try {
     if (batch > m->cfg.max_batch || t_prompt + n_new > m->cfg.max_ctx) throw burn::Error(MI_E_ARG, "batch or context too large");
@@ -342,7 +344,7 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
     // embedding gather: no host round trip (and no drained queue) between
     // steps; the tokens are read back once at the end.
     std::vector<Tensor> steps;
-    steps.reserve(n_new > 0 ? n_new - 1 : 0);
+    steps.reserve(n_new - 1);
     for (int32_t s = 1; s < n_new; ++s) {
       Tensor hs = forward_ids(m, next.reshape({batch}), batch, 1);
       next = burn::argmax_rows(head_last(m, hs, batch, 1));

@@ -188,8 +188,11 @@ static float opf(uint32_t k, float a, float b, float c, float s1, float s2) {
     case MI_K_SIGMOID_BACKWARD: return (b * a) * (1.0f - a);
     case MI_K_TANH: return (float)tanh(ad);
     case MI_K_ERF: return (float)erf(ad);
-    /* sfpu/ops.rs:124-128: 0.5 a (1 + erf(a / sqrt 2)). */
-    case MI_K_GELU: return (float)(0.5 * ad * (1.0 + erf(ad * 0.70710678118654752440)));
+    /* sfpu/ops.rs:135-137: 0.5 a (1 + erf(a / sqrt 2)), as 0.5 a erfc(-a / sqrt 2)
+     * -- the same value without the cancellation of 1 + erf below a = -5
+     * (the reference's own device program takes the erfc form there,
+     * gelu_program, sfpu/ops.rs:2113-2150). */
+    case MI_K_GELU: return (float)(0.5 * ad * erfc(-ad * 0.70710678118654752440));
     /* sfpu/ops.rs:128-131: g (Phi(a) + a phi(a)). */
     case MI_K_GELU_BACKWARD: {
       double cdf = 0.5 * (1.0 + erf(ad * 0.70710678118654752440));
@@ -221,6 +224,9 @@ static float at(const float *x, int64_t xr, int64_t xc, int64_t i, int64_t j) {
 void or_eltwise(uint32_t kind, float s1, float s2, const float *a, int64_t ar, int64_t ac, const float *b,
                 int64_t br, int64_t bc, const float *c, int64_t cr, int64_t cc, float *out, int64_t R,
                 int64_t C) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (R * C > (1 << 20))
+#endif
   for (int64_t i = 0; i < R; ++i)
     for (int64_t j = 0; j < C; ++j) {
       float x = at(a, ar, ac, i, j);
@@ -247,6 +253,9 @@ static float min_nan(float a, float b) {
  * 24-28); mean = sum / n (ops.rs:3456-3469). */
 void or_reduce(const float *x, int64_t R, int64_t C, int op, int axis, float *out) {
   const int64_t outer = axis == MI_AXIS_COLS ? R : C, inner = axis == MI_AXIS_COLS ? C : R;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (R * C > (1 << 20))
+#endif
   for (int64_t o = 0; o < outer; ++o) {
     double s = 0.0;
     float m = op == MI_R_MAX ? -INFINITY : INFINITY;

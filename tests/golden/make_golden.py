@@ -63,7 +63,7 @@ def main():
     g["ew_exp"] = f32(np.exp(xd))
     g["ew_tanh"] = f32(np.tanh(xd))
     g["ew_erf"] = f32(special.erf(xd))
-    g["ew_gelu"] = f32(0.5 * xd * (1.0 + special.erf(xd / np.sqrt(2.0))))
+    g["ew_gelu"] = f32(0.5 * xd * special.erfc(-xd / np.sqrt(2.0)))  # 1 + erf without cancellation
     g["ew_sigmoid"] = f32(special.expit(xd))
     g["ew_silu"] = f32(xd * special.expit(xd))  # reference: x * rounded sigmoid
     pos = np.abs(x) + np.float32(1e-3)
@@ -76,6 +76,36 @@ def main():
     cdf = 0.5 * (1.0 + special.erf(xd / np.sqrt(2.0)))
     pdf = np.exp(-0.5 * xd * xd) / np.sqrt(2.0 * np.pi)
     g["ew_gelu_bwd"] = f32(gb.astype(np.float64) * (cdf + xd * pdf))
+    # GELU's negative tail, where 1 + erf(x / sqrt 2) cancels in float32
+    gt = values(19, 512, -12.0, -4.0, specials=False)
+    g["ew_gelu_tail_x"] = gt
+    g["ew_gelu_tail"] = f32(0.5 * gt.astype(np.float64) * special.erfc(-gt.astype(np.float64) / np.sqrt(2.0)))
+    # more transcendental kinds, float64 closed forms rounded once
+    g["ew_log1p_x"] = lx = values(15, 4096, -0.9, 8.0, specials=False)
+    g["ew_log1p"] = f32(np.log1p(lx.astype(np.float64)))
+    g["ew_expm1"] = f32(np.expm1(xd))
+    tw = values(16, 4096, -100.0, 100.0, specials=False)
+    g["ew_trig_x"] = tw
+    g["ew_sin"] = f32(np.sin(tw.astype(np.float64)))
+    g["ew_cos"] = f32(np.cos(tw.astype(np.float64)))
+    g["ew_pow"] = f32(np.power(pos.astype(np.float64), gb.astype(np.float64)))
+    g["ew_pow_s25"] = f32(np.power(pos.astype(np.float64), 2.5))
+    g["ew_pow_sm05"] = f32(np.power(pos.astype(np.float64), -0.5))
+    g["ew_recip"] = f32(1.0 / xd)
+    g["ew_div_s3"] = f32(xd / np.float64(np.float32(3.0)))
+    # rsqrt(|x| + 1e-6) as Burn composes it (abs, add_scalar in F32, then the
+    # root and reciprocal), with values small enough for the 1e-6 to matter
+    ra = np.concatenate([x[:3000], values(17, 1096, -1e-5, 1e-5, specials=False)])
+    ra[-4:] = [0.0, -0.0, 1e-30, -1e-6]
+    g["ew_rsq_x"] = ra
+    t = (np.abs(ra) + np.float32(1e-6)).astype(np.float32)
+    g["ew_rsqrt_abs_add"] = f32(1.0 / np.sqrt(t.astype(np.float64)))
+    # sigmoid's backward g * s * (1 - s) in Flex's order, two F32 roundings
+    # (sfpu/ops.rs:128-130), from a sigmoid output s in (0, 1)
+    sg = f32(special.expit(xd))
+    g["ew_sig_s"] = sg
+    g["ew_sig_bwd"] = ((gb * sg).astype(np.float32) * (np.float32(1.0) - sg)).astype(np.float32)
+    g["ew_sig_bwd64"] = f32(gb.astype(np.float64) * sg.astype(np.float64) * (1.0 - sg.astype(np.float64)))
     # exact element-wise ops on special values
     sp = values(13, 1024)
     sq = values(14, 1024)
@@ -89,6 +119,22 @@ def main():
         g["sp_relu_bwd"] = np.where(sp > 0, sq, np.float32(0.0)).astype(np.float32)
         g["sp_gt"] = (sp > sq).astype(np.float32)
         g["sp_eq"] = (sp == sq).astype(np.float32)
+        g["sp_neg"] = (sp.view(np.uint32) ^ np.uint32(0x80000000)).view(np.float32)
+        g["sp_abs"] = (sp.view(np.uint32) & np.uint32(0x7FFFFFFF)).view(np.float32)
+        g["sp_sign"] = np.where(np.isnan(sp), sp, np.where(sp > 0, np.float32(1), np.where(
+            sp < 0, np.float32(-1), np.float32(0)))).astype(np.float32)
+        # leaky_relu (sfpu/ops.rs:61-62): a >= 0 ? a : slope * a
+        g["sp_leaky"] = np.where(sp >= 0, sp, np.float32(0.01) * sp).astype(np.float32)
+        # hard_sigmoid (sfpu/ops.rs:63-64): (alpha a + beta).clamp(0, 1), two roundings
+        hs = (np.float32(0.2) * sp).astype(np.float32) + np.float32(0.5)
+        g["sp_hard_sigmoid"] = np.where(np.isnan(hs), hs, np.minimum(np.maximum(hs, np.float32(0)),
+                                                                     np.float32(1))).astype(np.float32)
+        # scale_mask_fill (sfpu/ops.rs:246-251): mask ? fill : a * scale
+        mk = (lcg_stream(18, 1024) & np.uint64(1)).astype(np.float32)
+        g["sp_mask"] = mk
+        g["sp_scale_mask_fill"] = np.where(mk != 0, np.float32(-np.inf),
+                                           (sp * np.float32(0.125)).astype(np.float32)).astype(np.float32)
+        g["sp_div_s0"] = (sp / np.float32(0.0)).astype(np.float32)
     # ---- products: integer-valued (exact) and general (float64 reference)
     ai = ints(21, 37 * 53, 4).reshape(37, 53)
     bi = ints(22, 53 * 29, 4).reshape(53, 29)
@@ -105,6 +151,8 @@ def main():
     g["red_sum1"] = f32(r.astype(np.float64).sum(axis=1, keepdims=True))
     g["red_max0"] = r.max(axis=0, keepdims=True)
     g["red_max1"] = r.max(axis=1, keepdims=True)
+    g["red_min0"] = r.min(axis=0, keepdims=True)
+    g["red_min1"] = r.min(axis=1, keepdims=True)
     g["red_mean_all"] = np.array([f32(r.astype(np.float64).sum()) / np.float32(r.size)], np.float32)
     # ---- softmax / log-softmax, including rows that overflow exp unshifted
     s = values(41, 9 * 130, -30.0, 30.0, specials=False).reshape(9, 130)

@@ -6,8 +6,14 @@ Bars: logits within rel 2e-2 of the CPU model --
 checked here at 2e-3 of the logits' scale -- and greedy tokens equal to the
 CPU model's where its top-2 margin exceeds that tolerance (teacher-forced
 top-1 agreement, the reference's own criterion, step167_smollm2.rs:14-21).
-Full SmolLM2 size: determinism and batch consistency (every row of a batch
-of one repeated prompt decodes the same tokens as batch 1).
+At the full SmolLM2-135M shape the same bars hold at
+batch 1 and batch 32 -- the two batch sizes take different kernels (the
+fused attention against the product composition at prefill; the decode GEMV
+against the matrix-core decode projections and 128-key attention chunks) --
+on a 40-token prompt and four decoded positions, and the tokens of greedy
+generation agree with the CPU model teacher-forced on them; determinism and
+batch consistency are checked too (every row of a batch of one repeated
+prompt decodes the same tokens as batch 1).
 """
 import numpy as np
 import pytest
@@ -47,6 +53,11 @@ def rope_tables(cfg, n):
 
 def ref_logits(W, cfg, ids):
     """Full-sequence float32 forward from position 0: [B, T, vocab]."""
+    return (ref_hidden(W, cfg, ids) @ W["embed"].T).numpy()
+
+
+def ref_hidden(W, cfg, ids):
+    """The final RMSNorm's output of the full-sequence forward: [B, T, hidden]."""
     B, T = ids.shape
     H, KVH, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
     G = H // KVH
@@ -77,8 +88,7 @@ def ref_logits(W, cfg, ids):
         x = x + o @ L["wo"].T
         hn = rms(x, L["mlp_norm"])
         x = x + (torch.nn.functional.silu(hn @ L["wgate"].T) * (hn @ L["wup"].T)) @ L["wdown"].T
-    x = rms(x, W["final_norm"])
-    return (x @ W["embed"].T).numpy()
+    return rms(x, W["final_norm"])
 
 
 @pytest.fixture(scope="module")
@@ -148,3 +158,86 @@ def test_smollm2_shape_batch_consistency_and_determinism(engine):
     assert np.array_equal(four, np.repeat(one, 4, 0))
     m.close()
     m2.close()
+
+
+# ------------------------------------------------------------ SmolLM2 shape
+SMOL_PROMPT, SMOL_STEPS = 40, 4
+
+
+@pytest.fixture(scope="module")
+def smol(engine):
+    cfg = miburn.SMOLLM2_135M
+    m = miburn.Llama(engine, cfg, max_ctx=64, max_batch=32, seed=11)
+    yield m, weights(engine, m, cfg)
+    m.close()
+
+
+def top1_agrees(got, want, err):
+    """Teacher-forced top-1 agreement (step167_smollm2.rs:14-21) over rows
+    whose CPU top-2 margin exceeds twice the largest logit difference seen;
+    returns how many rows were margin-clear."""
+    top2 = np.sort(want, -1)[..., -2:]
+    clear = (top2[..., 1] - top2[..., 0]) > 2 * err
+    assert np.array_equal(np.argmax(got, -1)[clear], np.argmax(want, -1)[clear])
+    return int(clear.sum())
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_smollm2_shape_logits_within_tolerance(engine, smol, batch):
+    """All 30 layers at SmolLM2-135M's shape: the prefill's logits at every
+    prompt position, then four single-token steps through the KV cache,
+    against the CPU model fed the same tokens.  Logits within rel 2e-2 of
+    their scale (the north star's bar) and top-1 agreement wherever the CPU
+    model's margin is clear of the difference."""
+    m, W = smol
+    cfg = miburn.SMOLLM2_135M
+    T = SMOL_PROMPT + SMOL_STEPS
+    ids = np.random.default_rng(100 + batch).integers(0, cfg["vocab"], (batch, T)).astype(np.int32)
+    want = ref_logits(W, cfg, ids)  # [B, T, vocab]
+    scale = np.abs(want).max()
+    m.reset()
+    lid = m.forward(ids[:, :SMOL_PROMPT], all_positions=True)
+    got = engine.download(lid).reshape(batch, SMOL_PROMPT, -1)
+    engine.free(lid)
+    err = np.abs(got - want[:, :SMOL_PROMPT]).max()
+    print(f"batch {batch} prefill: max |diff| {err:.3g} of logit scale {scale:.3g}")
+    assert err <= 2e-2 * scale
+    clear = top1_agrees(got, want[:, :SMOL_PROMPT], err)
+    for p in range(SMOL_PROMPT, T):
+        lid = m.forward(ids[:, p:p + 1])
+        got = engine.download(lid)
+        engine.free(lid)
+        e = np.abs(got - want[:, p]).max()
+        print(f"batch {batch} decode position {p}: max |diff| {e:.3g}")
+        assert e <= 2e-2 * scale
+        clear += top1_agrees(got, want[:, p], e)
+    # The agreement check must have covered most positions.
+    assert clear >= 0.8 * batch * T, (clear, batch * T)
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_smollm2_shape_greedy_generation(engine, smol, batch):
+    """Greedy generation (the device's argmax feeding the next step's
+    embedding gather) at both batch sizes: each token is the CPU model's
+    top-1 teacher-forced on the device's earlier tokens, wherever the CPU
+    model's margin is clear of 5e-3 of the logit scale."""
+    m, W = smol
+    cfg = miburn.SMOLLM2_135M
+    prompt = np.random.default_rng(200 + batch).integers(0, cfg["vocab"], (batch, SMOL_PROMPT)).astype(np.int32)
+    out, _, _ = m.generate(prompt, SMOL_STEPS)
+    assert out.shape == (batch, SMOL_STEPS)
+    hid = ref_hidden(W, cfg, np.concatenate([prompt, out[:, :-1]], 1))
+    want = (hid[:, SMOL_PROMPT - 1:] @ W["embed"].T).numpy()  # predicts tokens 0 .. steps-1
+    tol = 5e-3 * np.abs(want).max()
+    top2 = np.sort(want, -1)[..., -2:]
+    clear = (top2[..., 1] - top2[..., 0]) > tol
+    assert np.array_equal(out[clear], np.argmax(want, -1)[clear])
+    if batch >= 8:  # enough tokens for the check to have covered most of them
+        assert clear.mean() >= 0.7, clear.mean()
+
+
+def test_generate_rejects_zero_new_tokens(engine, smol):
+    m, _ = smol
+    with pytest.raises(miburn.MiError) as e:
+        m.generate(np.zeros((1, 4), np.int32), 0)
+    assert e.value.kind == "ARG"

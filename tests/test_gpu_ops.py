@@ -119,6 +119,19 @@ def test_scalar_ops_exact(engine, kind, s1, s2):
         same_bits(got, want)
 
 
+def test_gelu_negative_tail(engine):
+    """Below a = -5.3, 1 + erf(a / sqrt 2) cancels to zero in F32; GELU stays
+    within rel 1e-5 down to a = -13 (the erfc form)."""
+    x = np.linspace(-13.0, -4.0, 4099, dtype=np.float32).reshape(1, -1)
+    close(engine.download(engine.eltwise_op_as("GELU", engine.upload(x))), orc.eltwise(K["GELU"], x), rtol=1e-5)
+    # Special values: +inf stays, -inf and NaN give NaN (inf * 0), signed
+    # zeros keep their sign; below -13 the value is under F32's normal range.
+    sp = np.array([[np.inf, -np.inf, np.nan, 0.0, -0.0, -14.0, -40.0, 13.2, 20.0, 1e30]], np.float32)
+    got = engine.download(engine.eltwise_op_as("GELU", engine.upload(sp)))
+    close(got, orc.eltwise(K["GELU"], sp), rtol=1e-5, atol=1e-37)
+    assert np.signbit(got[0, 4]) and not np.signbit(got[0, 3])
+
+
 def test_rsqrt_abs_add_fused(engine):
     x = rnd(128, 128)
     a = engine.upload(x)
@@ -701,6 +714,8 @@ def attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale):
     (1, 2, 6, 2, 64, 0, 8),          # whole cache, one chunk, direct write
     (1, 512, 9, 3, 64, 0, 640),      # a 512-token prompt at batch 1 (prefill takes the fused kernel)
     (4, 100, 9, 3, 64, 28, 160),     # prompts of 4 sequences after 28 cached positions
+    (1, 300, 2, 1, 64, 0, 300),      # two key chunks: early positions' second chunk is empty
+    (1, 1100, 9, 3, 64, 0, 1100),    # a prompt past one chunk at SmolLM2's heads: empty chunks too
 ])
 def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     q = rnd(batch * t, heads * D)
@@ -809,6 +824,9 @@ def test_decode_projection_errors(engine):
         engine.norm_matvec(engine.upload(rnd(2, 576)), 0, 0.0, engine.upload_bf16(orc.to_bf16(rnd(63, 576))),
                            silu_mul=True)  # odd gate|up rows
     assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_matvec(engine.empty(2, 0), 0, 0.0, engine.empty(64, 0, BF16))  # no columns
+    assert e.value.kind == "UNSUPPORTED"
 
 
 def test_attention_rows_errors(engine):

@@ -1,11 +1,19 @@
 """Device parity of the prefill's fused tails.
 
+mi_rope and mi_copy_into4 on their own, against numpy: RoPE bit for bit
+against the reference's composition `x cos + rotate_half(x) sin` in F32
+(crates/tt-models/src/rope.rs:6-60, 128-135; two products and a sum, each
+rounded) and within 1e-6 of the float64 rotation of each pair (i, i + d/2)
+by the angle pos * theta^(-2i/d); the strided 4-D copy bit for bit against a
+numpy strided assignment, the rest of the destination untouched.
+
 mi_qkv_rope_cache (RoPE on the q and k heads of the fused q|k|v rows, the
 cache writes, q in either layout; float4 rows for head widths of a multiple
 of 8, the element-wise form otherwise): bit-identical to the engine's own
 composition -- mi_rope on the q and k blocks, mi_copy_into4 of k and v into
-the caches, mi_copy_strided4 for the regrouped queries (each pinned against
-the oracle by its own tests) -- with every cache row outside the written
+the caches, mi_copy_strided4 for the regrouped queries (mi_rope and
+mi_copy_into4 checked against numpy above, mi_copy_strided4 against the
+oracle in test_gpu_ops.py) -- with every cache row outside the written
 positions left as it was.
 
 mi_silu_mul_halves: bit-identical to MI_K_SILU_MUL of the two halves, on the
@@ -45,6 +53,52 @@ def rope_tables(n, d, theta=1e5):
     cos = np.concatenate([np.cos(ang), np.cos(ang)], 1).astype(np.float32)
     sin = np.concatenate([-np.sin(ang), np.sin(ang)], 1).astype(np.float32)
     return cos, sin
+
+
+@pytest.mark.parametrize("heads,seq,d,pos0", [(9, 40, 64, 0), (3, 7, 64, 25), (4, 5, 16, 3), (2, 3, 12, 1)])
+def test_rope_against_numpy(engine, heads, seq, d, pos0):
+    batch, theta = 2, 1e5
+    maxc = pos0 + seq
+    x = rnd(batch * seq * heads, d)  # rows (sequence, position, head)
+    # The tables as the reference builds them: F32 angles pos * freq, then
+    # cos and sin, sin's first half negated.
+    freq = (theta ** (-np.arange(0, d, 2, dtype=np.float64) / d)).astype(np.float32)
+    ang = (np.arange(maxc, dtype=np.float32)[:, None] * freq[None, :]).astype(np.float32)
+    cos = np.concatenate([np.cos(ang.astype(np.float64))] * 2, 1).astype(np.float32)
+    s_ = np.sin(ang.astype(np.float64)).astype(np.float32)
+    sin = np.concatenate([-s_, s_], 1)
+    got = engine.download(engine.rope(engine.upload(x), engine.upload(cos), engine.upload(sin), heads, seq, pos0))
+    pos = pos0 + (np.arange(x.shape[0]) // heads) % seq
+    rot = np.concatenate([x[:, d // 2:], x[:, :d // 2]], 1)
+    want = ((x * cos[pos]).astype(np.float32) + (rot * sin[pos]).astype(np.float32)).astype(np.float32)
+    same_bits(got, want)
+    # The rotation it stands for, in float64: pair (i, i + d/2) turned by the angle.
+    a = ang[pos].astype(np.float64)
+    x1, x2 = x[:, :d // 2].astype(np.float64), x[:, d // 2:].astype(np.float64)
+    exact = np.concatenate([x1 * np.cos(a) - x2 * np.sin(a), x2 * np.cos(a) + x1 * np.sin(a)], 1)
+    assert np.abs(got - exact).max() <= 1e-6 * np.abs(x).max() * 4
+
+
+@pytest.mark.parametrize("dims,dst_off,dst_st,src_off,src_st", [
+    ((2, 3, 5, 64), 7 * 64, (3 * 20 * 64, 20 * 64, 64, 1), 0, (5 * 3 * 64, 64, 3 * 64, 1)),  # KV-cache append
+    ((1, 4, 6, 3), 5, (0, 40, 2, 7), 11, (0, 1, 4, 24)),                                     # arbitrary strides
+])
+def test_copy_into4_against_numpy(engine, dims, dst_off, dst_st, src_off, src_st):
+    def span(off, st):
+        return off + sum((n - 1) * s for n, s in zip(dims, st)) + 1
+    dst0 = rnd(span(dst_off, dst_st) + 9)
+    src = rnd(span(src_off, src_st) + 3)
+    idst = engine.upload(dst0.reshape(1, -1))
+    engine.copy_into4(idst, dst_off, dst_st, engine.upload(src.reshape(1, -1)), src_off, src_st, dims)
+    want = dst0.copy()
+    it = np.stack(np.meshgrid(*[np.arange(n) for n in dims], indexing="ij"), -1).reshape(-1, 4)
+    want[dst_off + it @ np.array(dst_st)] = src[src_off + it @ np.array(src_st)]
+    same_bits(engine.download(idst).reshape(-1), want)
+    # A destination range past the buffer is refused and writes nothing.
+    with pytest.raises(miburn.MiError) as e:
+        engine.copy_into4(idst, dst0.size, dst_st, engine.upload(src.reshape(1, -1)), src_off, src_st, dims)
+    assert e.value.kind == "ARG"
+    same_bits(engine.download(idst).reshape(-1), want)
 
 
 @pytest.mark.parametrize("batch,seq,heads,kv,d,pos0,maxc", [(2, 5, 9, 3, 64, 3, 16), (1, 33, 4, 4, 32, 0, 40),

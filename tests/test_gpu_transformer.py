@@ -7,8 +7,11 @@ Bars: each step's loss within rel 1e-4 of the CPU model and every parameter
 after the steps within 1e-4 of its scale (the reference's own criterion is
 the first loss within rel 1e-3, step59_burn_transformer.rs:18-22); on the
 reference's learnable task (arithmetic progressions mod the vocabulary,
-transformer.rs:99-113) the loss falls.  Config-4 shape: finite losses,
-bit-identical reruns.
+transformer.rs:99-113) the loss falls.  At BASELINE config 4's shape (4
+layers, d 256, 4 heads, FFN 1024, vocab 8192, batch 16 x 128 tokens): two
+steps' losses within rel 1e-3 of the CPU model (the reference's bar) and the
+parameters after them within 1e-4 of their scale; finite losses and
+bit-identical reruns over three steps.
 """
 import math
 
@@ -126,3 +129,35 @@ def test_config4_shape_finite_and_deterministic(engine):
     assert np.all(np.isfinite(runs[0]))
     assert 8.0 < runs[0][0] < 12.0, runs[0]  # about ln(8192) = 9.01 plus the init's logit spread
     assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+
+
+def test_config4_shape_two_steps_match_torch_autograd(engine):
+    cfg = miburn.TRANSFORMER_CONFIG4
+    lr = 0.05
+    m = miburn.Transformer(engine, cfg, seed=9)
+    P, layers = params(m, cfg)
+    everything = list(P.values()) + [t for L in layers for t in L.values()]
+    rng = np.random.default_rng(44)
+    for step in range(2):
+        x = rng.integers(0, cfg["vocab"], (16, 128)).astype(np.int32)
+        y = rng.integers(0, cfg["vocab"], (16, 128)).astype(np.int32)
+        got = m.train_step(x, y, lr)
+        loss = torch_loss(P, layers, cfg, x, y)
+        loss.backward()
+        sgd(everything, lr)
+        print(f"config 4 step {step}: device loss {got!r}, CPU {loss.item()!r}")
+        assert abs(got - loss.item()) <= 1e-3 * abs(loss.item()), (step, got, loss.item())
+    worst = 0.0
+    for name in ("embed", "head_w", "head_b"):
+        want = P[name].detach().numpy()
+        err = np.abs(m.param(name) - want).max() / np.abs(want).max()
+        worst = max(worst, err)
+        assert err <= 1e-4, (name, err)
+    for l in range(cfg["layers"]):
+        for name in miburn.TRANSFORMER_LAYER_PARAMS:
+            want = layers[l][name].detach().numpy()
+            err = np.abs(m.param(name, l) - want).max() / max(np.abs(want).max(), 1e-3)
+            worst = max(worst, err)
+            assert err <= 1e-4, (l, name, err)
+    print(f"config 4 parameters: worst relative difference {worst:.3g}")
+    m.close()

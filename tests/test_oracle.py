@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as orc
-from miburn import AXIS_COLS, AXIS_ROWS, K, R_MAX, R_MEAN, R_SUM
+from miburn import AXIS_COLS, AXIS_ROWS, K, R_MAX, R_MEAN, R_MIN, R_SUM
 
 G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_v1.npz"))
 ULP = 2.0 ** -23
@@ -44,7 +44,7 @@ def assert_ulps(got, want, n_ulp):
 # ------------------------------------------------------------ element-wise
 @pytest.mark.parametrize("kind,key,src,n_ulp", [
     ("EXP", "ew_exp", "ew_x", 1), ("TANH", "ew_tanh", "ew_x", 1), ("ERF", "ew_erf", "ew_x", 1),
-    ("GELU", "ew_gelu", "ew_x", 1), ("SIGMOID", "ew_sigmoid", "ew_x", 1), ("SILU", "ew_silu", "ew_x", 2),
+    ("GELU", "ew_gelu", "ew_x", 1), ("GELU", "ew_gelu_tail", "ew_gelu_tail_x", 1), ("SIGMOID", "ew_sigmoid", "ew_x", 1), ("SILU", "ew_silu", "ew_x", 2),
     ("LOG", "ew_log", "ew_pos", 1), ("SQRT", "ew_sqrt", "ew_pos", 0), ("RSQRT", "ew_rsqrt", "ew_pos", 1),
 ])
 def test_unary_against_float64_golden(kind, key, src, n_ulp):
@@ -53,6 +53,47 @@ def test_unary_against_float64_golden(kind, key, src, n_ulp):
         assert_bits(got, G[key])
     else:
         assert_ulps(got, G[key], n_ulp)
+
+
+@pytest.mark.parametrize("kind,key,src,s1,n_ulp", [
+    ("LOG1P", "ew_log1p", "ew_log1p_x", 0.0, 1), ("EXPM1", "ew_expm1", "ew_x", 0.0, 1),
+    ("SIN", "ew_sin", "ew_trig_x", 0.0, 1), ("COS", "ew_cos", "ew_trig_x", 0.0, 1),
+    ("POW_S", "ew_pow_s25", "ew_pos", 2.5, 1), ("POW_S", "ew_pow_sm05", "ew_pos", -0.5, 1),
+    ("RECIP", "ew_recip", "ew_x", 0.0, 0), ("DIV_SCALAR", "ew_div_s3", "ew_x", 3.0, 0),
+    ("RSQRT_ABS_ADD", "ew_rsqrt_abs_add", "ew_rsq_x", 1e-6, 1),
+])
+def test_more_unary_against_float64_golden(kind, key, src, s1, n_ulp):
+    got = orc.eltwise(K[kind], G[src], s1=s1).ravel()
+    if n_ulp == 0:
+        assert_bits(got, G[key])
+    else:
+        assert_ulps(got, G[key], n_ulp)
+
+
+def test_pow_against_float64_golden():
+    assert_ulps(orc.eltwise(K["POW"], G["ew_pos"], G["ew_g"]).ravel(), G["ew_pow"], 1)
+
+
+def test_sigmoid_backward_golden():
+    s, g = G["ew_sig_s"], G["ew_g"]
+    got = orc.eltwise(K["SIGMOID_BACKWARD"], s, g).ravel()
+    # Flex's order, (g s)(1 - s), bit for bit; and within 2 ulps of the exact value.
+    assert_bits(got, G["ew_sig_bwd"])
+    assert_ulps(got, G["ew_sig_bwd64"], 2)
+
+
+@pytest.mark.parametrize("kind,key,s1,s2", [
+    ("NEG", "sp_neg", 0.0, 0.0), ("ABS", "sp_abs", 0.0, 0.0), ("SIGN", "sp_sign", 0.0, 0.0),
+    ("LEAKY_RELU", "sp_leaky", 0.01, 0.0), ("HARD_SIGMOID", "sp_hard_sigmoid", 0.2, 0.5),
+    ("DIV_SCALAR", "sp_div_s0", 0.0, 0.0),
+])
+def test_exact_unary_with_special_values(kind, key, s1, s2):
+    assert_bits(orc.eltwise(K[kind], G["sp_a"], s1=s1, s2=s2).ravel(), G[key])
+
+
+def test_scale_mask_fill_golden():
+    got = orc.eltwise(K["SCALE_MASK_FILL"], G["sp_a"], G["sp_mask"], s1=0.125, s2=-np.inf).ravel()
+    assert_bits(got, G["sp_scale_mask_fill"])
 
 
 def test_gelu_backward_golden():
@@ -107,6 +148,8 @@ def test_scalar_forms_and_clamps():
     c = orc.eltwise(K["CLAMP"], x, s1=-1.0, s2=1.0).ravel()
     assert_bits(c[:5], np.array([-1, -0.0, 0, 0.5, 1], np.float32))
     assert np.isnan(c[5])
+    # FILL (sfpu/ops.rs:90-91): the scalar everywhere, whatever the datum.
+    assert_bits(orc.eltwise(K["FILL"], x, s1=1.5), np.full((1, 6), 1.5, np.float32))
 
 
 def test_mask_fill_and_where():
@@ -167,6 +210,8 @@ def test_reductions_against_float64():
     assert_bits(orc.reduce(x, R_SUM, AXIS_COLS), G["red_sum1"])
     assert_bits(orc.reduce(x, R_MAX, AXIS_ROWS), G["red_max0"])
     assert_bits(orc.reduce(x, R_MAX, AXIS_COLS), G["red_max1"])
+    assert_bits(orc.reduce(x, R_MIN, AXIS_ROWS), G["red_min0"])
+    assert_bits(orc.reduce(x, R_MIN, AXIS_COLS), G["red_min1"])
     assert_bits(np.array([orc.reduce_all(x, R_MEAN)]), G["red_mean_all"])
 
 
@@ -180,6 +225,8 @@ def test_max_propagates_nan_and_sum_keeps_exact_values():
     x = np.array([[1.0, np.nan, 3.0], [-1.0, -2.0, -0.5]], np.float32)
     m = orc.reduce(x, R_MAX, AXIS_COLS).ravel()
     assert np.isnan(m[0]) and m[1] == -0.5
+    m = orc.reduce(x, R_MIN, AXIS_COLS).ravel()
+    assert np.isnan(m[0]) and m[1] == -2.0
     y = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
     assert orc.reduce(y, R_SUM, AXIS_COLS)[0, 0] == 10.0
 
@@ -316,3 +363,57 @@ def test_softmax_backward_matches_finite_differences():
     assert np.allclose(ds, f, atol=1e-3, rtol=1e-3)
     # Rows of the gradient sum to zero (softmax is shift-invariant).
     assert np.abs(ds.astype(np.float64).sum(1)).max() < 1e-6
+
+
+# ------------------------------------------------------------------- guard
+# Where each element-wise kind and reduction the device tests grade against
+# the oracle is pinned in this file (a golden vector, a known answer or a
+# composition of pinned kinds).
+PINNED = {
+    "ADD": "sp_add", "SUB": "sp_sub", "MUL": "sp_mul", "DIV": "sp_div", "RELU": "sp_relu",
+    "RELU_BACKWARD": "sp_relu_bwd", "GT": "sp_gt", "EQ": "sp_eq", "NEG": "sp_neg", "ABS": "sp_abs",
+    "SIGN": "sp_sign", "LEAKY_RELU": "sp_leaky", "HARD_SIGMOID": "sp_hard_sigmoid",
+    "SCALE_MASK_FILL": "sp_scale_mask_fill", "EXP": "ew_exp", "TANH": "ew_tanh", "ERF": "ew_erf",
+    "GELU": "ew_gelu", "SIGMOID": "ew_sigmoid", "SILU": "ew_silu", "LOG": "ew_log", "SQRT": "ew_sqrt",
+    "RSQRT": "ew_rsqrt", "LOG1P": "ew_log1p", "EXPM1": "ew_expm1", "SIN": "ew_sin", "COS": "ew_cos",
+    "POW": "ew_pow", "POW_S": "ew_pow_s25", "RECIP": "ew_recip", "DIV_SCALAR": "ew_div_s3",
+    "RSQRT_ABS_ADD": "ew_rsqrt_abs_add", "SIGMOID_BACKWARD": "ew_sig_bwd", "GELU_BACKWARD": "ew_gelu_bwd",
+    # known answers and compositions above
+    "SILU_MUL": "test_fused_kinds_equal_their_compositions", "ADD_RELU": "test_fused_kinds_equal_their_compositions",
+    "MUL_ADD": "test_fused_kinds_equal_their_compositions", "SUB_EXP": "test_fused_kinds_equal_their_compositions",
+    "ADD_SCALAR": "test_scalar_forms_and_clamps", "MUL_SCALAR": "test_scalar_forms_and_clamps",
+    "CLAMP": "test_scalar_forms_and_clamps", "CLAMP_MIN": "test_scalar_forms_and_clamps",
+    "CLAMP_MAX": "test_scalar_forms_and_clamps", "FILL": "test_scalar_forms_and_clamps", "MASK_FILL": "test_mask_fill_and_where",
+    "MASK_WHERE": "test_mask_fill_and_where", "NE": "test_comparisons_known_answers",
+    "GE": "test_comparisons_known_answers", "LT": "test_comparisons_known_answers",
+    "LE": "test_comparisons_known_answers",
+    "R_SUM": "red_sum0", "R_MAX": "red_max0", "R_MIN": "red_min0", "R_MEAN": "red_mean_all",
+}
+
+
+def test_comparisons_known_answers():
+    # IEEE comparisons (sfpu/ops.rs:66-72): -0 == +0, a NaN unordered (only NE true).
+    a = np.array([1.0, -0.0, np.nan, 2.0, -np.inf], np.float32)
+    b = np.array([1.0, 0.0, np.nan, 3.0, -np.inf], np.float32)
+    want = {"EQ": [1, 1, 0, 0, 1], "NE": [0, 0, 1, 1, 0], "GT": [0, 0, 0, 0, 0], "GE": [1, 1, 0, 0, 1],
+            "LT": [0, 0, 0, 1, 0], "LE": [1, 1, 0, 1, 1]}
+    for kind, w in want.items():
+        assert_bits(orc.eltwise(K[kind], a, b).ravel(), np.array(w, np.float32))
+
+
+def test_every_kind_the_device_is_graded_on_is_pinned():
+    """Fails when a device test grades against an oracle function that no
+    check in this file pins."""
+    import glob
+    import re
+    here = os.path.dirname(os.path.abspath(__file__))
+    used = set()
+    for path in glob.glob(os.path.join(here, "test_gpu_*.py")):
+        text = open(path).read()
+        used |= {m for m in re.findall(r'"([A-Z][A-Z0-9_]*)"', text) if m in K}
+        used |= set(re.findall(r"\b(R_(?:SUM|MAX|MIN|MEAN))\b", text))
+    missing = sorted(used - set(PINNED))
+    assert not missing, missing
+    me = open(os.path.abspath(__file__)).read()
+    for kind, where in PINNED.items():
+        assert where in G.files or f"def {where}(" in me, (kind, where)
