@@ -358,6 +358,22 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
                       int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, int64_t pos0, float scale,
                       mi_id *out);
+/* mi_attention_rows writing into an existing F32 `[batch * t, heads * d]`
+ * buffer `out` (not one of the inputs), with no allocation of any kind: no
+ * device or host memory is allocated, freed or grown, so callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation -- can call it.  No counterpart in the reference
+ * (its attention_rows returns a new buffer).  The key-chunk partials live in
+ * a fixed 4 MiB device array per GPU, held until the process ends; a call
+ * whose partials need more (items * chunks * G * (d + 2) floats: long
+ * prompts of many sequences) is refused with MI_E_UNSUPPORTED.  Every call on
+ * one GPU shares that array: calls from different contexts or streams that
+ * overlap in time on one GPU race; calls on one context's stream never do.
+ * Same kernels and chunking as mi_attention_rows, so the same bits. */
+int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
+                           int64_t batch, int64_t t, int64_t heads,
+                           int64_t kv_heads, int64_t pos0, float scale,
+                           mi_id out);
 /* ---- fused decode projections: the fused q|k|v and gate|up matrices of
  * crates/tt-models/src/llama.rs:655-672 (`Llama::fused`) composed with the
  * ops around them in a decode step -- Engine::rms_norm_as (server.rs:449),

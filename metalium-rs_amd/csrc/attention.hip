@@ -27,7 +27,9 @@
 #include "common.hpp"
 #include "wave.hpp"
 
+#include <atomic>
 #include <cfloat>
+#include <mutex>
 
 namespace mi {
 
@@ -273,12 +275,54 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const float *k, c
 
 }  // namespace mi
 
-using namespace mi;
+// The no-allocation form's partials (mi_attention_rows_into): a file-scope
+// device array, one copy per GPU the library runs on, held until the process
+// ends.  Host code never passes the array's name to a kernel (in host code it
+// is a stand-in, not a device address): attention_scratch_setup looks up each
+// device's address once, with that device current, and the entry point uses
+// that address.
+constexpr size_t ATT_NOALLOC_BYTES = size_t(4) << 20;  // 1 Mi floats
+static __device__ __align__(256) float scratch[ATT_NOALLOC_BYTES / sizeof(float)];
 
-extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
-                                 int64_t heads, int64_t kv_heads, int64_t pos0, float scale, mi_id *out) {
-  MI_ENTER(ctx);
-  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+namespace mi {
+
+constexpr int ATT_MAX_DEVICES = 64;
+static std::atomic<float *> g_att_scratch[ATT_MAX_DEVICES];
+static std::mutex g_att_scratch_mu;
+
+// At context creation (mi_ctx_create), once per device: the address of this
+// device's copy of `scratch`.  A failure is kept and reported by
+// mi_attention_rows_into, which cannot run without it.
+int attention_scratch_setup(Ctx *ctx) {
+  if (ctx->device < 0 || ctx->device >= ATT_MAX_DEVICES) return MI_OK;
+  std::lock_guard<std::mutex> lk(g_att_scratch_mu);
+  if (g_att_scratch[ctx->device].load()) return MI_OK;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return fail(ctx, MI_E_HIP, "attention scratch: no current device");
+  if (cur != ctx->device && hipSetDevice(ctx->device) != hipSuccess)
+    return fail(ctx, MI_E_HIP, "attention scratch: hipSetDevice(%d)", ctx->device);
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch));
+  if (cur != ctx->device) (void)hipSetDevice(cur);
+  if (e != hipSuccess || !p)
+    return fail(ctx, MI_E_HIP, "attention scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+  g_att_scratch[ctx->device].store(static_cast<float *>(p));
+  return MI_OK;
+}
+
+namespace {
+
+// A checked attention call: shapes, the key-chunk split and the partials'
+// size, shared by the allocating and the no-allocation entry points so both
+// run the same kernels on the same chunks.
+struct AttPlan {
+  const float *q, *k, *v;
+  int64_t D, G, maxc, items, S, chunk;
+  size_t part_bytes;
+};
+
+int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t, int64_t heads,
+                   int64_t kv_heads, int64_t pos0, AttPlan *P) {
   MI_BUF(ctx, qb, q);
   MI_BUF(ctx, kb, k_cache);
   MI_BUF(ctx, vb, v_cache);
@@ -323,25 +367,48 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   if (items > INT32_MAX || S > 65535) return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: grid too large");
   if (static_cast<size_t>(3 * G * S + G) * sizeof(float) > 65536)
     return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: context of %lld keys too long", (long long)nmax);
+  P->q = static_cast<const float *>(qb->ptr);
+  P->k = static_cast<const float *>(kb->ptr);
+  P->v = static_cast<const float *>(vb->ptr);
+  P->D = D; P->G = G; P->maxc = maxc; P->items = items; P->S = S; P->chunk = chunk;
+  P->part_bytes = S > 1 ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
+  return MI_OK;
+}
+
+void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t t, int64_t heads,
+                      int64_t kv_heads, int64_t pos0, float scale) {
+  const int Si = static_cast<int>(P.S);
+  switch (P.D) {
+    case 16: dispatch_group<16>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 32: dispatch_group<32>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 64: dispatch_group<64>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    default: dispatch_group<128>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+  }
+}
+
+}  // namespace
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
+                                 int64_t heads, int64_t kv_heads, int64_t pos0, float scale, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  AttPlan P;
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, &P);
+  if (s) return s;
   float *part = nullptr;
-  if (S > 1) {
-    part = static_cast<float *>(scratch(ctx, static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float)));
+  if (P.part_bytes) {
+    part = static_cast<float *>(mi::scratch(ctx, P.part_bytes));
     if (!part) return fail(ctx, MI_E_OOM, "attention_rows scratch");
   }
   mi_id id;
   Buffer *ob;
-  int s = new_buffer(ctx, batch * t, heads * D, MI_F32, &id, &ob);
+  s = new_buffer(ctx, batch * t, heads * P.D, MI_F32, &id, &ob);
   if (s) return s;
-  const float *qp = static_cast<const float *>(qb->ptr), *kp = static_cast<const float *>(kb->ptr),
-              *vp = static_cast<const float *>(vb->ptr);
-  float *op = static_cast<float *>(ob->ptr);
-  const int Si = static_cast<int>(S);
-  switch (D) {
-    case 16: dispatch_group<16>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
-    case 32: dispatch_group<32>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
-    case 64: dispatch_group<64>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
-    default: dispatch_group<128>(G, ctx->stream, qp, kp, vp, op, part, items, Si, t, heads, kv_heads, pos0, maxc, chunk, scale); break;
-  }
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, t, heads, kv_heads, pos0, scale);
   s = check_launch(ctx, "attention_rows");
   if (s) {
     mi_free(ctx, id);
@@ -349,4 +416,30 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   }
   *out = id;
   return MI_OK;
+}
+
+extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
+                                      int64_t heads, int64_t kv_heads, int64_t pos0, float scale, mi_id out) {
+  MI_ENTER(ctx);
+  AttPlan P;
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, &P);
+  if (s) return s;
+  MI_BUF(ctx, ob, out);
+  if (out == q || out == k_cache || out == v_cache)
+    return fail(ctx, MI_E_ARG, "attention_rows_into: the output is one of the inputs");
+  if (ob->elem != MI_F32 || ob->rows != batch * t || ob->cols != heads * P.D)
+    return fail(ctx, MI_E_ARG, "attention_rows_into: output is [%lld, %lld] %s, want [%lld, %lld] F32",
+                (long long)ob->rows, (long long)ob->cols, elem_name(ob->elem), (long long)(batch * t),
+                (long long)(heads * P.D));
+  if (P.part_bytes > ATT_NOALLOC_BYTES)
+    return fail(ctx, MI_E_UNSUPPORTED,
+                "attention_rows_into: %zu bytes of key-chunk partials, beyond the %zu the no-allocation form holds",
+                P.part_bytes, ATT_NOALLOC_BYTES);
+  float *part = nullptr;
+  if (P.part_bytes) {
+    part = ctx->device >= 0 && ctx->device < ATT_MAX_DEVICES ? g_att_scratch[ctx->device].load() : nullptr;
+    if (!part) return fail(ctx, MI_E_HIP, "attention_rows_into: no scratch address for device %d", ctx->device);
+  }
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, t, heads, kv_heads, pos0, scale);
+  return check_launch(ctx, "attention_rows_into");
 }

@@ -179,6 +179,10 @@ int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id,
 void *device_alloc(Ctx *ctx, size_t bytes, size_t *got);
 void device_release(Ctx *ctx, void *p, size_t bytes);
 void *scratch(Ctx *ctx, size_t bytes);
+// Looks up, once per device, the device address of the no-allocation
+// attention form's file-scope partials (attention.hip); called at context
+// creation.
+int attention_scratch_setup(Ctx *ctx);
 // Zero `bytes` (a multiple of 2) at p with a kernel: safe inside a captured
 // trace, where a memset node is not.
 int fill_zero(Ctx *ctx, void *p, size_t bytes);

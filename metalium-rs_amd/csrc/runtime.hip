@@ -205,6 +205,9 @@ int mi_ctx_create(int device, mi_ctx **out) {
   mi_ctx *c = new (std::nothrow) mi_ctx();
   if (!c) return fail(nullptr, MI_E_OOM, "context allocation");
   c->device = device;
+  // Messages up to fail()'s 512 bytes never allocate after this.
+  c->last_error.reserve(512);
+  c->sticky_msg.reserve(512);
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&c->dev_flags, 256);
   if (e == hipSuccess) e = hipMemset(c->dev_flags, 0, 256);
@@ -218,6 +221,8 @@ int mi_ctx_create(int device, mi_ctx **out) {
     mi_ctx_destroy(c);
     return code;
   }
+  // A failure here only disables mi_attention_rows_into, which reports it.
+  (void)attention_scratch_setup(c);
   *out = c;
   return MI_OK;
 }

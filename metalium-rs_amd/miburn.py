@@ -106,6 +106,7 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
         "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
+        "mi_attention_rows_into": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, U64],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_qkv_rope_cache": [P, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
@@ -341,6 +342,13 @@ class Engine:
         """Engine::attention_rows (server.rs:255-265): causal GQA of `t` new
         positions against the first pos0 + t rows of each cache item."""
         return self._out(self._lib.mi_attention_rows, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, scale)
+
+    def attention_rows_into(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int,
+                            kv_heads: int, pos0: int, scale: float, out: int) -> None:
+        """attention_rows into the existing F32 buffer `out`, allocating
+        nothing (the partials in a fixed per-GPU device array)."""
+        self._check(self._lib.mi_attention_rows_into(self.ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0,
+                                                     scale, out))
 
     def eltwise_op_as(self, kind, a: int, b: int = 0, c: int = 0, scalar: float = 0.0, scalar2: float = 0.0,
                       out_elem: int = F32) -> int:
