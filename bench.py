@@ -47,14 +47,14 @@ GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268756687}
 
 
 def cpu_baseline(n: int = 4096, seconds: float = 10.0) -> dict:
-    """The oracle's F32 product (k ascending, F32 accumulation, OpenMP over
-    rows) on this host's cores: the CPU restatement standing in for burn-flex,
-    which cannot be built here.  The sample is the headline's own shape,
-    repeated for about `seconds` of CPU work."""
+    """The oracle's F32 product (k ascending, F32 accumulation; register tiles
+    of 4 x 32, AVX-512 / AVX2 clones, OpenMP over column strips) on this
+    host's cores: the CPU restatement standing in for burn-flex, which cannot
+    be built here.  The sample is the headline's own shape, repeated for
+    about `seconds` of CPU work."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as orc
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, 16)  # the GPU box's CPU share
+    cores = _cpu_cores()
     rng = np.random.default_rng(1)
     a = rng.standard_normal((n, n)).astype(np.float32)
     b = rng.standard_normal((n, n)).astype(np.float32)
@@ -68,7 +68,89 @@ def cpu_baseline(n: int = 4096, seconds: float = 10.0) -> dict:
             break
     tflops = 2.0 * n ** 3 * reps / el / 1e12
     return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"oracle F32 product {n}^3 (k-ascending F32 accumulation, OpenMP rows), {reps} reps in {el:.2f} s"}
+            "sample": f"oracle F32 product {n}^3 (k-ascending F32 sums, 4x32 register tiles, vector ISA "
+                      f"clones, OpenMP column strips), {reps} reps in {el:.2f} s"}
+
+
+def _cpu_cores() -> int:
+    return min(len(os.sched_getaffinity(0)), 16)  # the GPU box's CPU share
+
+
+def cpu_models_baseline() -> dict:
+    """The reference's model workloads on this host's cores, in the float32
+    torch restatements the device harnesses are checked against
+    (oracle/models_cpu.py), standing in for burn-flex (not buildable here).
+    Bounded samples of each workload, 10 to 30 s of CPU work in all."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch
+    import models_cpu as mc
+    import miburn
+    cores = _cpu_cores()
+    torch.set_num_threads(cores)
+    out = {}
+    kind = {"unit": "ms", "cores": cores, "kind": "port"}
+    # Config 1: MLP 784-128-10, batch 64, SGD lr 0.01, fresh batches.
+    g = torch.Generator().manual_seed(0)
+    ps = [torch.empty(784, 128).uniform_(-1 / 28, 1 / 28, generator=g).requires_grad_(),
+          torch.empty(128).uniform_(-1 / 28, 1 / 28, generator=g).requires_grad_(),
+          torch.empty(128, 10).uniform_(-0.088, 0.088, generator=g).requires_grad_(),
+          torch.empty(10).uniform_(-0.088, 0.088, generator=g).requires_grad_()]
+    data = [(torch.rand(64, 784, generator=g), torch.randint(0, 10, (64,), generator=g)) for _ in range(110)]
+    for i, (x, y) in enumerate(data):
+        if i == 10:
+            t0 = time.perf_counter()
+        mc.mlp_loss(ps, x, y).backward()
+        mc.sgd(ps, 0.01)
+    ms = (time.perf_counter() - t0) * 1e3 / 100
+    out["mlp_train"] = dict(value=round(ms, 4), **kind, sample="torch CPU float32 restatement, 100 SGD steps "
+                            "(after 10 warm), batch 64")
+    # Config 4: the transformer training step at its shape.
+    cfg = miburn.TRANSFORMER_CONFIG4
+    P, layers = mc.transformer_init(cfg, seed=0)
+    every = list(P.values()) + [t for L in layers for t in L.values()]
+    toks = [(torch.randint(0, cfg["vocab"], (16, 128), generator=g).numpy(),
+             torch.randint(0, cfg["vocab"], (16, 128), generator=g).numpy()) for _ in range(3)]
+    for i, (x, y) in enumerate(toks):
+        if i == 1:
+            t0 = time.perf_counter()
+        mc.transformer_loss(P, layers, cfg, x, y).backward()
+        mc.sgd(every, 0.05)
+    ms = (time.perf_counter() - t0) * 1e3 / 2
+    out["transformer_train"] = dict(value=round(ms, 2), **kind, sample="torch CPU float32 restatement, 2 "
+                                    "forward + backward + SGD steps (after 1 warm), batch 16 x 128 tokens")
+    # Config 5: the SmolLM2-shaped decoder (BF16-rounded N(0, 0.02) weights
+    # held in F32), greedy decoding through a KV cache.
+    lc = miburn.SMOLLM2_135M
+    W = mc.llama_random_weights(lc, seed=0)
+    with torch.no_grad():
+        ids = torch.randint(0, lc["vocab"], (32, 512), generator=g).numpy()
+        mc.llama_generate(W, lc, ids[:1, :16], 2)  # warm
+        _, pf1, dc1 = mc.llama_generate(W, lc, ids[:1], 17, max_ctx=640)
+        # Batch 32: the prefill of 2 of the 32 sequences (a CPU at full width
+        # already: tokens/s scale with the batch), and decode steps at batch
+        # 32 after a 512-position cache (its contents do not change the time).
+        t0 = time.perf_counter()
+        mc.llama_step(W, lc, mc.LlamaCache(lc, 2, 513), ids[:2])
+        pf2 = (time.perf_counter() - t0) * 1e3
+        cache = mc.LlamaCache(lc, 32, 640)
+        cache.len = 512
+        nxt = ids[:, :1]
+        mc.llama_step(W, lc, cache, nxt)  # warm
+        t0 = time.perf_counter()
+        for _ in range(4):
+            h = mc.llama_step(W, lc, cache, nxt)
+            nxt = mc.argmax_first(h[:, -1] @ W["embed"].T)[:, None].numpy()
+        dc32 = (time.perf_counter() - t0) * 1e3 / 4
+    out["decoder_b1"] = {"prefill_tokens_per_s": round(512 / (pf1 / 1e3), 1),
+                         "decode_ms_per_step": round(dc1 / 16, 3), "decode_tokens_per_s": round(16 / (dc1 / 1e3), 1),
+                         "cores": cores, "kind": "port",
+                         "sample": "torch CPU float32 restatement: 512-token prefill, 16 greedy steps"}
+    out["decoder_b32"] = {"prefill_tokens_per_s": round(2 * 512 / (pf2 / 1e3), 1),
+                          "decode_ms_per_step": round(dc32, 3), "decode_tokens_per_s": round(32 / (dc32 / 1e3), 1),
+                          "cores": cores, "kind": "port",
+                          "sample": "torch CPU float32 restatement: 512-token prefill of 2 sequences, 4 greedy "
+                                    "steps at batch 32 after 512 cached positions"}
+    return out
 
 
 def _time_op(eng, fn, reps: int, warm: int = 3) -> float:
@@ -371,6 +453,12 @@ def main() -> int:
         line["decoder"] = [decoder_bench(eng, 1), decoder_bench(eng, 32)]
         line["mlp_train"] = mlp_bench(eng, traces=not args.no_traces)
         line["transformer_train"] = transformer_bench(eng, traces=not args.no_traces)
+        if not args.no_cpu:
+            cm = cpu_models_baseline()
+            line["decoder"][0]["cpu_baseline"] = cm["decoder_b1"]
+            line["decoder"][1]["cpu_baseline"] = cm["decoder_b32"]
+            line["mlp_train"]["cpu_baseline"] = cm["mlp_train"]
+            line["transformer_train"]["cpu_baseline"] = cm["transformer_train"]
     print(json.dumps(line), flush=True)
     eng.close()
     return 0

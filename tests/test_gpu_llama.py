@@ -1,6 +1,6 @@
-"""The SmolLM2-shaped decoder harness on the device against a float32 CPU
-restatement of the reference's Llama (crates/tt-models/src/llama.rs:140-520,
-1030-1178; rope.rs:1-60) fed the same (BF16) weights.
+"""The SmolLM2-shaped decoder harness on the device against the float32 CPU
+restatement of the reference's Llama (oracle/models_cpu.py: crates/tt-models/
+src/llama.rs:140-520, 1030-1178; rope.rs:1-60) fed the same (BF16) weights.
 
 Bars: logits within rel 2e-2 of the CPU model --
 checked here at 2e-3 of the logits' scale -- and greedy tokens equal to the
@@ -20,6 +20,7 @@ import pytest
 import torch
 
 import miburn
+import models_cpu as mc
 
 pytestmark = pytest.mark.gpu
 
@@ -41,54 +42,12 @@ def weights(eng, model, cfg):
     return W
 
 
-def rope_tables(cfg, n):
-    D = cfg["head_dim"]
-    half = D // 2
-    freq = np.array([np.float32(cfg["rope_theta"] ** (-2.0 * i / D)) for i in range(half)], np.float32)
-    ang = (np.arange(n, dtype=np.float32)[:, None] * freq[None, :]).astype(np.float32)
-    cos = np.cos(ang.astype(np.float64)).astype(np.float32)
-    sin = np.sin(ang.astype(np.float64)).astype(np.float32)
-    return torch.from_numpy(np.concatenate([cos, cos], 1)), torch.from_numpy(np.concatenate([-sin, sin], 1))
-
-
 def ref_logits(W, cfg, ids):
     """Full-sequence float32 forward from position 0: [B, T, vocab]."""
-    return (ref_hidden(W, cfg, ids) @ W["embed"].T).numpy()
+    return mc.llama_logits(W, cfg, ids).numpy()
 
 
-def ref_hidden(W, cfg, ids):
-    """The final RMSNorm's output of the full-sequence forward: [B, T, hidden]."""
-    B, T = ids.shape
-    H, KVH, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
-    G = H // KVH
-    eps = cfg["eps"]
-    cos, sin = rope_tables(cfg, T)
-
-    def rms(x, g):
-        return x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * g.reshape(-1)
-
-    def rope(x):  # x [B, T, heads, D]
-        x1, x2 = x[..., : D // 2], x[..., D // 2:]
-        rot = torch.cat([x2, x1], -1)
-        return x * cos[None, :, None, :] + rot * sin[None, :, None, :]
-
-    x = W["embed"][torch.from_numpy(ids.astype(np.int64))]
-    causal = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
-    for L in W["layers"]:
-        xn = rms(x, L["attn_norm"])
-        q = rope((xn @ L["wq"].T).reshape(B, T, H, D))
-        k = rope((xn @ L["wk"].T).reshape(B, T, KVH, D))
-        v = (xn @ L["wv"].T).reshape(B, T, KVH, D)
-        k = k.repeat_interleave(G, dim=2)
-        v = v.repeat_interleave(G, dim=2)
-        s = torch.einsum("bthd,bshd->bhts", q, k) / np.sqrt(D)
-        s = s.masked_fill(causal, float("-inf"))
-        p = torch.softmax(s, -1)
-        o = torch.einsum("bhts,bshd->bthd", p, v).reshape(B, T, H * D)
-        x = x + o @ L["wo"].T
-        hn = rms(x, L["mlp_norm"])
-        x = x + (torch.nn.functional.silu(hn @ L["wgate"].T) * (hn @ L["wup"].T)) @ L["wdown"].T
-    return rms(x, W["final_norm"])
+ref_hidden = mc.llama_hidden  # the final RMSNorm's output: [B, T, hidden]
 
 
 @pytest.fixture(scope="module")

@@ -1,6 +1,6 @@
-"""The transformer training harness on the device against a float32 torch
-autograd restatement of the reference's model (crates/tt-mnist/src/
-transformer.rs:36-166: Embedding, pre-norm encoder layers without a mask,
+"""The transformer training harness on the device against the float32 torch
+autograd restatement of the reference's model (oracle/models_cpu.py;
+crates/tt-mnist/src/transformer.rs:36-166: Embedding, pre-norm encoder layers without a mask,
 Linear head, CrossEntropyLoss, Sgd) started from the same weights.
 
 Bars: each step's loss within rel 1e-4 of the CPU model and every parameter
@@ -13,13 +13,13 @@ steps' losses within rel 1e-3 of the CPU model (the reference's bar) and the
 parameters after them within 1e-4 of their scale; finite losses and
 bit-identical reruns over three steps.
 """
-import math
 
 import numpy as np
 import pytest
 import torch
 
 import miburn
+import models_cpu as mc
 
 pytestmark = pytest.mark.gpu
 
@@ -48,38 +48,8 @@ def params(model, cfg):
     return P, layers
 
 
-def torch_loss(P, layers, cfg, tokens, targets):
-    B, S = tokens.shape
-    d, H = cfg["d_model"], cfg["heads"]
-    dk = d // H
-    eps = cfg["eps"]
-
-    def ln(x, g, b):
-        mu = x.mean(-1, keepdim=True)
-        var = ((x - mu) ** 2).mean(-1, keepdim=True)
-        return (x - mu) / torch.sqrt(var + eps) * g + b
-
-    def heads(t):
-        return t.reshape(B, S, H, dk).transpose(1, 2)
-
-    x = P["embed"][torch.from_numpy(tokens.reshape(-1).astype(np.int64))]
-    for L in layers:
-        n1 = ln(x, L["ln1_g"], L["ln1_b"])
-        q, k, v = (heads(n1 @ L[w] + L[b]) for w, b in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
-        s = (q @ k.transpose(-1, -2).contiguous()) / math.sqrt(dk)
-        o = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B * S, d)
-        x = x + o @ L["wo"] + L["bo"]
-        n2 = ln(x, L["ln2_g"], L["ln2_b"])
-        x = x + torch.nn.functional.gelu(n2 @ L["w1"] + L["b1"]) @ L["w2"] + L["b2"]
-    z = x @ P["head_w"] + P["head_b"]
-    return torch.nn.functional.cross_entropy(z, torch.from_numpy(targets.reshape(-1).astype(np.int64)))
-
-
-def sgd(tensors, lr):
-    with torch.no_grad():
-        for t in tensors:
-            t -= lr * t.grad
-            t.grad = None
+torch_loss = mc.transformer_loss
+sgd = mc.sgd
 
 
 def test_three_steps_match_torch_autograd(engine):
