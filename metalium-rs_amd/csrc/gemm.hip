@@ -226,6 +226,10 @@ struct GemmArgs {
   const float *bias;   // [N]
   const float *resid;  // [M, N], row pitch ldr
   int64_t ldr;
+  // Direct BF16 kernel only: B's own k extent when A's k loop runs over
+  // several copies of it (A = [hi | lo] parts of an F32 operand against one
+  // B: B's k wraps modulo kb; 0 for none).
+  int64_t kb = 0;
 };
 
 __device__ __forceinline__ float epilogue(const GemmArgs &g, int64_t row, int64_t col, float v) {
@@ -698,6 +702,13 @@ struct DmaOperand {
     uint32_t voff;
     const char *base;
     int64_t ustep;
+    // Rows past `limit` (an edge tile of a k-contiguous operand whose row
+    // count is not a multiple of the tile, and a multiple of RPB): such a
+    // block is read from `clamp` (the last whole block of rows) instead, so
+    // no read leaves the operand; those rows only feed results that are not
+    // stored.  limit = 0: no edge.
+    int64_t first_row, limit;
+    const char *clamp;
   };
   template <int NW>
   __device__ __forceinline__ static Src src_of(const uint16_t *src, int64_t ld, int64_t r0, int64_t k0, int wave,
@@ -722,7 +733,19 @@ struct DmaOperand {
       base_off = ((k0 + RPB * wave) * ld + r0) * 2;
     }
     ustep = static_cast<int64_t>(RPB) * NW * ld * 2;
-    return Src{voff, reinterpret_cast<const char *>(src) + base_off, ustep};
+    return Src{voff, reinterpret_cast<const char *>(src) + base_off, ustep, 0, 0, nullptr};
+  }
+  // src_of for a k-contiguous operand of `rows` rows (a multiple of RPB) whose
+  // last tile runs past them.
+  template <int NW>
+  __device__ __forceinline__ static Src src_edge(const uint16_t *src, int64_t ld, int64_t r0, int64_t k0, int wave,
+                                                 int lane, int64_t rows) {
+    Src sr = src_of<NW>(src, ld, r0, k0, wave, lane);
+    if constexpr (!KCONTIG) return sr;  // only k-contiguous operands take an edge
+    sr.first_row = r0 + RPB * wave;
+    sr.limit = rows;
+    sr.clamp = reinterpret_cast<const char *>(src) + ((rows - RPB) * ld + k0) * 2;
+    return sr;
   }
 
   // The DMA instruction of this wave's block i of the tile into `lds`.
@@ -732,6 +755,7 @@ struct DmaOperand {
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(lds)));
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds0 + b * 1024);
     const char *p = sr.base + i * sr.ustep;
+    if (sr.limit && sr.first_row + static_cast<int64_t>(i) * RPB * NW >= sr.limit) p = sr.clamp;
     const char *gb = reinterpret_cast<const char *>(
         static_cast<uint64_t>(static_cast<uint32_t>(
             __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>(p))))) |
@@ -749,8 +773,8 @@ struct DmaOperand {
   // Issue this wave's share of the tile's 1 KiB blocks (all of them).
   template <int NW>
   __device__ __forceinline__ static void load(const uint16_t *src, int64_t ld, int64_t r0, int64_t k0, char *lds,
-                                              int wave, int lane) {
-    const Src sr = src_of<NW>(src, ld, r0, k0, wave, lane);
+                                              int wave, int lane, int64_t rows = 0) {
+    const Src sr = rows ? src_edge<NW>(src, ld, r0, k0, wave, lane, rows) : src_of<NW>(src, ld, r0, k0, wave, lane);
 #pragma unroll
     for (int i = 0; i < BLOCKS / NW; ++i) issue<NW>(sr, i, lds, wave);
   }
@@ -841,7 +865,7 @@ __device__ __forceinline__ void pipe_mfma(f32x16 (&acc)[TM][TN], const uint4 (&f
                                                           __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
 }
 
-template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN, bool GN>
 __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   constexpr int BK = 32;  // two MFMA k steps per tile
   constexpr int NW = WM * WN;
@@ -883,10 +907,16 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   // every thread issues PER_TILE DMA instructions per tile and the counted
   // waits stay exact.
   auto kclamp = [&](int64_t t) { return (t < ktiles ? t : ktiles - 1) * BK; };
+  // B's k of tile t: wrapped modulo its own extent when A repeats it.
+  auto kbof = [&](int64_t t) { return g.kb ? kclamp(t) % g.kb : kclamp(t); };
+  // GN: the last column tile runs past N (B k-contiguous, N a multiple of
+  // its block rows): those B rows are read from the last whole block, their
+  // results not stored.
+  const int64_t brows = GN ? g.N : 0;
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) {
     OA::template load<NW>(A, g.lda, m0, kclamp(s), stages[s], wave, lane);
-    OB::template load<NW>(B, g.ldb, n0, kclamp(s), stages[s] + OA::BYTES, wave, lane);
+    OB::template load<NW>(B, g.ldb, n0, kbof(s), stages[s] + OA::BYTES, wave, lane, brows);
   }
   // Tile 0 landed everywhere (tiles 1 .. NS-2 may be in flight).
   wait_vmcnt<(NS - 2) * PER_TILE>();
@@ -910,29 +940,33 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
         // the last tile this reads a stage holding a reload, unused).
         wait_vmcnt<(NS - 3) * PER_TILE>();
         __builtin_amdgcn_s_barrier();
-        // The refill's DMA instructions and the next step's fragment reads
-        // are spread over the step's MFMAs -- one DMA instruction after each
-        // of the first MFMAs, one fragment read after each MFMA from the
-        // third -- so the MFMA pipe is not left idle while a wave issues a
-        // burst of them (0.75 -> 0.83 of the MFMA cycles in the main loop at
+        // The next step's fragment reads and the refill's DMA instructions
+        // are spread over the step's MFMAs -- one fragment read after each
+        // MFMA, in the order the next step's MFMAs use them (A's first
+        // fragment, B's, then A's others), and one DMA instruction after each
+        // MFMA from the third -- so the MFMA pipe is not left idle while a
+        // wave issues a burst of them and the first reads land well before
+        // their use (0.75 -> 0.85 of the MFMA cycles in the main loop at
         // 4096^3); whatever the step has no MFMA left for follows it.
         char *refill = stages[(s + NS - 1) % NS];
         const auto sa = OA::template src_of<NW>(A, g.lda, m0, kclamp(kt + s + NS - 1), wave, lane);
-        const auto sb = OB::template src_of<NW>(B, g.ldb, n0, kclamp(kt + s + NS - 1), wave, lane);
+        const auto sb = GN ? OB::template src_edge<NW>(B, g.ldb, n0, kbof(kt + s + NS - 1), wave, lane, brows)
+                           : OB::template src_of<NW>(B, g.ldb, n0, kbof(kt + s + NS - 1), wave, lane);
         const char *nst = stages[(s + 1) % NS];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < MF || q < PER_TILE || q < TM + TN + 2; ++q) {
+        for (int q = 0; q < MF || q < PER_TILE + 2 || q < TM + TN; ++q) {
           if (q < MF) {
             const int i = q / TN, j = q % TN;
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa1[i]),
                                                                 __builtin_bit_cast(bf16x8, fb1[j]), acc[i][j], 0, 0, 0);
           }
-          if (q < PA) OA::template issue<NW>(sa, q, refill, wave);
-          else if (q < PER_TILE) OB::template issue<NW>(sb, q - PA, refill + OA::BYTES, wave);
-          const int r = q - 2;
-          if (r >= 0 && r < TM) fa0[r] = OA::frag(nst, wm * WTM + r * 32, 0, lane);
-          else if (r >= TM && r < TM + TN) fb0[r - TM] = OB::frag(nst + OA::BYTES, wn * WTN + (r - TM) * 32, 0, lane);
+          if (q == 0) fa0[0] = OA::frag(nst, wm * WTM, 0, lane);
+          else if (q <= TN) fb0[q - 1] = OB::frag(nst + OA::BYTES, wn * WTN + (q - 1) * 32, 0, lane);
+          else if (q < TN + TM) fa0[q - TN] = OA::frag(nst, wm * WTM + (q - TN) * 32, 0, lane);
+          const int d = q - 2;
+          if (d >= 0 && d < PA) OA::template issue<NW>(sa, d, refill, wave);
+          else if (d >= PA && d < PER_TILE) OB::template issue<NW>(sb, d - PA, refill + OA::BYTES, wave);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -952,6 +986,7 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      if (GN && col0 + j * 32 >= g.N) continue;
       TO *cij = C + (row0 + i * 32) * g.ldc + col0 + j * 32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -966,17 +1001,17 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
 }
 
 // Two waves per SIMD (8 per workgroup): at most 256 registers a wave.
-template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN, bool GN>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_pipe_kernel(GemmArgs g) {
-  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN>(g);
+  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN, GN>(g);
 }
 
 // One wave per SIMD (4 per workgroup): the whole 512-entry register file, so
 // a 128 x 128 wave tile keeps its accumulators in the AGPRs.
-template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN, bool GN>
 __global__ void __launch_bounds__(WM *WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_pipe1_kernel(GemmArgs g) {
-  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN>(g);
+  gemm_pipe_body<TO, BM, BN, NS, AK, BKC, WM, WN, GN>(g);
 }
 
 // ------------------------------------------------- small-M products
@@ -1099,6 +1134,7 @@ struct Plan {
   int64_t ldc = 0;                // result row pitch (0: N)
   int64_t per_group = 0;          // items per group (0: one group of `batch`)
   int64_t sa2 = 0, sb2 = 0, sc2 = 0;  // group strides
+  int64_t kb = 0;  // direct BF16 kernel: B's k extent when A's k repeats it (see GemmArgs)
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1132,7 +1168,7 @@ static hipError_t launch_cfg(const Plan &p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN>
+template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN, bool GN>
 static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   GemmArgs g;
   g.a = p.a; g.b = p.b; g.c = p.c;
@@ -1145,21 +1181,29 @@ static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   g.sa2 = p.sa2; g.sb2 = p.sb2; g.sc2 = p.sc2;
   g.kc = 0;
   g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
+  g.kb = p.kb;
   g.tiles_m = static_cast<int>(p.M / BM);
-  g.tiles_n = static_cast<int>(p.N / BN);
+  g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
-  if constexpr (WM * WN == 4) gemm_pipe1_kernel<TO, BM, BN, NS, AK, BKC, WM, WN><<<grid, 256, 0, st>>>(g);
-  else gemm_pipe_kernel<TO, BM, BN, NS, AK, BKC, WM, WN><<<grid, WM * WN * 64, 0, st>>>(g);
+  if constexpr (WM * WN == 4) gemm_pipe1_kernel<TO, BM, BN, NS, AK, BKC, WM, WN, GN><<<grid, 256, 0, st>>>(g);
+  else gemm_pipe_kernel<TO, BM, BN, NS, AK, BKC, WM, WN, GN><<<grid, WM * WN * 64, 0, st>>>(g);
   return hipGetLastError();
 }
 
 template <typename TO, int BM, int BN, int NS, int WM, int WN>
 static hipError_t launch_pipe(const Plan &p, hipStream_t st) {
   const bool ak = !p.ta, bk = p.tb;
-  if (ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, true, true, WM, WN>(p, st);
-  if (ak && !bk) return launch_pipe_cfg<TO, BM, BN, NS, true, false, WM, WN>(p, st);
-  if (!ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, false, true, WM, WN>(p, st);
-  return launch_pipe_cfg<TO, BM, BN, NS, false, false, WM, WN>(p, st);
+  if (ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, true, true, WM, WN, false>(p, st);
+  if (ak && !bk) return launch_pipe_cfg<TO, BM, BN, NS, true, false, WM, WN, false>(p, st);
+  if (!ak && bk) return launch_pipe_cfg<TO, BM, BN, NS, false, true, WM, WN, false>(p, st);
+  return launch_pipe_cfg<TO, BM, BN, NS, false, false, WM, WN, false>(p, st);
+}
+
+// A width that is not a multiple of the tile: B k-contiguous ([N, K] as the
+// weights are stored), N a multiple of 16, A k-contiguous.
+template <typename TO, int BM, int BN, int NS, int WM, int WN>
+static hipError_t launch_pipe_edge(const Plan &p, hipStream_t st) {
+  return launch_pipe_cfg<TO, BM, BN, NS, true, true, WM, WN, true>(p, st);
 }
 
 
@@ -1476,8 +1520,81 @@ static bool grouped_items_in(const Buffer *x, int64_t groups, int64_t per_group,
 // Launch a planned product (M, N, K >= 1) into p.c: the GEMV for a few rows
 // against a k-contiguous weight, split-K for few tiles over a long k, else
 // the tiled kernels.
+// F32 rows [M, K] -> BF16 [M, 2 K]: each row's hi parts then its lo parts
+// (split_bf16), eight elements a thread.
+__global__ void __launch_bounds__(256) split_rows_kernel(const float *a, int64_t lda, uint16_t *out, int64_t M,
+                                                         int64_t K) {
+  const int64_t per_row = K / 8;
+  const int64_t n = M * per_row;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; u < n;
+       u += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = u / per_row, c = (u - r * per_row) * 8;
+    const float4 v0 = *reinterpret_cast<const float4 *>(a + r * lda + c);
+    const float4 v1 = *reinterpret_cast<const float4 *>(a + r * lda + c + 4);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint16_t h[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_bf16(v[e], h[e], l[e]);
+    uint4 hv, lv;
+    hv.x = h[0] | (uint32_t(h[1]) << 16); hv.y = h[2] | (uint32_t(h[3]) << 16);
+    hv.z = h[4] | (uint32_t(h[5]) << 16); hv.w = h[6] | (uint32_t(h[7]) << 16);
+    lv.x = l[0] | (uint32_t(l[1]) << 16); lv.y = l[2] | (uint32_t(l[3]) << 16);
+    lv.z = l[4] | (uint32_t(l[5]) << 16); lv.w = l[6] | (uint32_t(l[7]) << 16);
+    *reinterpret_cast<uint4 *>(out + r * 2 * K + c) = hv;
+    *reinterpret_cast<uint4 *>(out + r * 2 * K + K + c) = lv;
+  }
+}
+
+// The fast mode's F32 x BF16 product as one BF16 product on the direct
+// kernel: A's rows split once into their BF16 hi and lo parts, side by side
+// ([M, 2 K]: A = hi + lo to 2^-17 relative, the same split the split kernel
+// makes in registers), against B whose k wraps every K -- so the k loop
+// accumulates hi . b then lo . b in F32.  The split costs one pass over A;
+// the product then runs at the BF16 kernel's rate instead of the split
+// kernel's (whose per-tile conversions hold it to a fraction of it).  For
+// products big enough to fill the chip with 256 x 256 tiles.
+static bool stacked_split_pays(const Plan &p) {
+  if (!p.fast || p.ea != MI_F32 || p.eb != MI_BF16 || p.ta || p.batch != 1 || p.kc != 0) return false;
+  if (p.K % 32 || p.M % 256 || p.lda % 4 || (reinterpret_cast<uintptr_t>(p.a) & 15) ||
+      (reinterpret_cast<uintptr_t>(p.b) & 15) || p.ldb % 8)
+    return false;
+  if (p.N % 256 && !(p.tb && p.N % 16 == 0)) return false;
+  const int64_t tiles = (p.M / 256) * ((p.N + 255) / 256);
+  return tiles >= 128 && p.M * p.N * p.K >= (int64_t(1) << 32);
+}
+
+static int run_stacked_split(mi_ctx *ctx, const Plan &p) {
+  mi_id tid;
+  Buffer *tb;
+  int s = new_buffer(ctx, p.M, 2 * p.K, MI_BF16, &tid, &tb);
+  if (s) return s;
+  const int64_t units = p.M * (p.K / 8);
+  const unsigned g = static_cast<unsigned>(units / 256 + 1 < 65536 ? units / 256 + 1 : 65536);
+  split_rows_kernel<<<g, 256, 0, ctx->stream>>>(static_cast<const float *>(p.a), p.lda,
+                                                static_cast<uint16_t *>(tb->ptr), p.M, p.K);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) {
+    Plan q = p;
+    q.a = tb->ptr;
+    q.ea = MI_BF16;
+    q.lda = 2 * p.K;
+    q.K = 2 * p.K;
+    q.kb = p.K;
+    const bool bf = p.eo == MI_BF16;
+    if (p.N % 256 == 0)
+      e = bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, ctx->stream) : launch_pipe<float, 256, 256, 5, 2, 4>(q, ctx->stream);
+    else
+      e = bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, ctx->stream)
+             : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, ctx->stream);
+  }
+  mi_free(ctx, tid);  // stream-ordered: the block is reused only by later work
+  if (e != hipSuccess) return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
+  return check_launch(ctx, "matmul");
+}
+
 static int run_product(mi_ctx *ctx, Plan &p) {
   hipError_t e;
+  if (stacked_split_pays(p)) return run_stacked_split(ctx, p);
   if (gemv_fits(p)) {
     launch_gemv(p, ctx->stream);
     e = hipGetLastError();

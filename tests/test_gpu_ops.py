@@ -481,6 +481,30 @@ def test_matmul_mixed_f32_bf16(engine, mode, tb, mnk):
     assert np.all(np.abs(got - orc.matmul(a, bf, False, tb, threads=16)) <= mm_tol(a, bf, False, tb, 1e-5) + 1e-30)
 
 
+@pytest.mark.parametrize("mnk", [(4096, 2048, 576), (8192, 960, 576), (16384, 576, 576), (4096, 3072, 1536)])
+def test_matmul_mixed_stacked_split(engine, mode, mnk):
+    """F32 activations x BF16 weights [n, k] at the prefill's sizes: in the
+    fast mode the activations are split once into BF16 hi | lo parts and the
+    product runs on the direct BF16 kernel with the weight's k wrapping (widths
+    960 and 576 take its edge tiles).  Random operands within the F32 bound;
+    small integers bit for bit; a linear layer's bias and residual too."""
+    m, n, k = mnk
+    a, b = rnd(m, k), orc.to_bf16(rnd(n, k))
+    bf = orc.from_bf16(b)
+    ib = engine.upload_bf16(b)
+    got = engine.download(engine.matmul_dram(engine.upload(a), False, ib, True))
+    assert np.all(np.abs(got - orc.matmul(a, bf, False, True, threads=16)) <= mm_tol(a, bf, False, True, 1e-5) + 1e-30)
+    ai = RNG.integers(-8, 9, (m, k)).astype(np.float32)
+    bi = orc.to_bf16(RNG.integers(-8, 9, (n, k)).astype(np.float32))
+    got = engine.download(engine.matmul_dram(engine.upload(ai), False, engine.upload_bf16(bi), True))
+    same_bits(got, (ai.astype(np.float64) @ orc.from_bf16(bi).astype(np.float64).T).astype(np.float32))
+    bias, res = rnd(1, n), rnd(m, n)
+    got = engine.download(engine.linear(engine.upload(ai), engine.upload_bf16(bi), True, engine.upload(bias),
+                                        engine.upload(res)))
+    want = (ai.astype(np.float64) @ orc.from_bf16(bi).astype(np.float64).T).astype(np.float32)
+    same_bits(got, (res + (want + bias)).astype(np.float32))
+
+
 def test_matmul_fast_split_keeps_large_finite_values(engine, mode):
     """Values near FLT_MAX stay finite through the split (the BF16 head of a
     value above the largest BF16 would round to infinity, so it is truncated).
