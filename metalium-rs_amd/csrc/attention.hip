@@ -239,6 +239,217 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
   }
 }
 
+// ------------------------------------------- long prompts: matrix cores
+// Causal attention of many new positions (a prefill) on the F32 matrix cores
+// (v_mfma_f32_32x32x2f32), flash style: one block per (sequence, kv head,
+// two runs of 32 query positions), one wavefront per query head of the group; the
+// scores never leave registers.  Per block of 32 keys (staged in LDS, shared
+// by the group's heads) a wavefront forms S^T = K Q^T -- keys as the rows of
+// its 32 x 32 accumulator, its lane's query as the column, so each query's
+// keys sit in one lane and its partner (lane ^ 32) -- scales and masks it,
+// takes the running softmax (max clamped as the composition's; the sum of a
+// causal row is never empty; exponentials in base 2, v_exp_f32, within a few
+// ulps), and adds V^T P^T to its 64 x 32 output
+// accumulator: P^T's accumulator registers are the B operand as they lie,
+// once the value rows are read in the order the accumulator holds the keys
+// (register r: keys 8 (r / 4) + r % 4 and that + 4, one per half-wave).  The
+// contraction over d pairs d with d + 32 across the half-waves, so a lane's
+// query values and key row segments are contiguous (float4 reads).  F32
+// products and sums; only the order of the sums differs from the
+// composition.  D = 64.
+constexpr int FLASH_MIN_T = 64;  // new positions per sequence that take it
+constexpr int64_t FLASH_MIN_BLOCKS = 256;
+constexpr int FLASH_KS = 68;     // LDS row pitch (floats) of the key block
+constexpr int FLASH_VS = 72;     // ... and the value block
+
+typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
+
+template <int G>
+__global__ void __launch_bounds__(G * 64) __attribute__((amdgpu_waves_per_eu(3)))
+flash_prefill_kernel(const float *q, const float *kc, const float *vc, float *out, int64_t T, int64_t H, int64_t KVH,
+                     int64_t pos0, int64_t maxc, float scale) {
+  constexpr int D = 64, NT = G * 64;
+  __shared__ __attribute__((aligned(16))) float ks[2 * 32 * FLASH_KS];
+  __shared__ __attribute__((aligned(16))) float vs[2 * 32 * FLASH_VS];
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int64_t bj = blockIdx.y;  // (sequence, kv head)
+  const int64_t j = bj % KVH, b = bj / KVH;
+  const int n = lane & 31, half = lane >> 5;
+  const int64_t ctx = pos0 + T;
+  const int64_t h = j * G + g;
+  const float scale2 = scale * 1.4426950408889634f;
+  const float *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
+  const int ctx32 = static_cast<int>(ctx);  // the host keeps a cache item below 2^31 / D rows
+  // A block takes query blocks x and nqb - 1 - x in turn: a long and a short
+  // run of keys, so every block has about the same work (causal attention's
+  // blocks otherwise range from 1 to nqb key blocks) and the grid runs as one
+  // even wave.
+  const int64_t nqb = (T + 31) / 32;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int64_t qb = pass == 0 ? static_cast<int64_t>(blockIdx.x) : nqb - 1 - blockIdx.x;
+    if (pass == 1 && qb == static_cast<int64_t>(blockIdx.x)) break;
+    const int64_t p0 = qb * 32, p = p0 + n;
+    const bool live = p < T;
+    const int64_t pq = live ? p : T - 1;
+    const int64_t qpos = pos0 + pq;  // the lane's query position in the cache
+    // Q^T as the B operand: step s holds q[p][s + 32 half].
+    float qv[32];
+    {
+      const float *qrow = q + (b * T + pq) * H * D + h * D + 32 * half;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float4 v = *reinterpret_cast<const float4 *>(qrow + 4 * c);
+        qv[4 * c] = v.x; qv[4 * c + 1] = v.y; qv[4 * c + 2] = v.z; qv[4 * c + 3] = v.w;
+      }
+    }
+    flash_f32x16 o0, o1;  // O^T: d 0..31 and 32..63 (rows) by the 32 queries (columns)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o0[r] = 0.0f; o1[r] = 0.0f; }
+    float m = -INFINITY, l = 0.0f;  // running max (base 2) and sum
+    const int64_t kend = pos0 + (p0 + 32 < T ? p0 + 32 : T);  // keys this block's queries can see
+    // Key and value blocks go through registers into two LDS buffers in turn:
+    // the next block's loads are in flight while the current one is used.
+    constexpr int PER = (32 * 16 + NT - 1) / NT;  // float4 of a block per thread
+    float4 kr[PER], vr[PER];
+    // Loads are unconditional (a conditional load compiles to a branch whose
+    // join waits for it): rows past the context read the context's last row
+    // instead -- their scores are masked to -inf, so their values meet only
+    // zero weights -- and a thread's surplus slots reload a row it also loads
+    // and are not staged.
+    auto fetch = [&](int64_t j0) {
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int e0 = tid + u * NT, e = e0 < 32 * 16 ? e0 : tid;
+        const int r = static_cast<int>(j0) + (e >> 4) < ctx32 ? static_cast<int>(j0) + (e >> 4) : ctx32 - 1;
+        const int off = r * D + (e & 15) * 4;
+        kr[u] = *reinterpret_cast<const float4 *>(K + off);
+        vr[u] = *reinterpret_cast<const float4 *>(V + off);
+      }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int e = tid + u * NT;
+        const int r = e >> 4, c4 = (e & 15) * 4;
+        if (e < 32 * 16) {
+          *reinterpret_cast<float4 *>(ks + buf * 32 * FLASH_KS + r * FLASH_KS + c4) = kr[u];
+          *reinterpret_cast<float4 *>(vs + buf * 32 * FLASH_VS + r * FLASH_VS + c4) = vr[u];
+        }
+      }
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int64_t j0 = 0, it = 0; j0 < kend; j0 += 32, ++it) {
+      const int buf = static_cast<int>(it & 1);
+      const bool more = j0 + 32 < kend;
+      if (more) fetch(j0 + 32);
+
+      // S^T = K Q^T over d (step s: d = s for the first half-wave, s + 32 for
+      // the second).
+      flash_f32x16 st;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+      const float *krow = ks + buf * 32 * FLASH_KS + n * FLASH_KS + 32 * half;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv[4 * c], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv[4 * c + 1], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv[4 * c + 2], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv[4 * c + 3], st, 0, 0, 0);
+      }
+      // Scale and mask (keys after the query's position, or past the context:
+      // only a block reaching past the block's first query has any), then the
+      // running softmax of the lane's query over its keys.  The scores are
+      // kept in base 2 (scale * log2 e folded into one product), so each
+      // exponential is one exp2.
+      float mx = -INFINITY;
+      if (j0 + 31 <= pos0 + p0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          st[r] *= scale2;
+          mx = max_nan(mx, st[r]);
+        }
+      } else {
+        const int lim = static_cast<int>((qpos < ctx - 1 ? qpos : ctx - 1) - j0);  // last visible key offset
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kofs = 8 * (r >> 2) + 4 * half + (r & 3);
+          st[r] = kofs > lim ? -INFINITY : st[r] * scale2;
+          mx = max_nan(mx, st[r]);
+        }
+      }
+      mx = max_nan(mx, __shfl_xor(mx, 32, 64));
+      // The exponentials are taken against a reference m that trails the
+      // running max by less than 8 (weights up to 2^8, far from F32's range):
+      // the accumulated sums are rescaled only when the max outruns it, which
+      // after the first block is rare -- the same quotient, without a rescale
+      // of the output accumulators every block.
+      if (__any(!(mx <= m + 8.0f))) {
+        float mnew = max_nan(m, mx);
+        mnew = isnan(mnew) ? mnew : (mnew > -FLT_MAX ? mnew : -FLT_MAX);
+        const float corr = __builtin_amdgcn_exp2f(m - mnew);
+        l *= corr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o0[r] *= corr; o1[r] *= corr; }
+        m = mnew;
+      }
+      float ls = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = __builtin_amdgcn_exp2f(st[r] - m);
+        st[r] = e;
+        ls += e;
+      }
+      ls += __shfl_xor(ls, 32, 64);
+      l += ls;
+      // O^T += V^T P^T: step r contracts keys 8 (r / 4) + r % 4 (first
+      // half-wave) and that + 4 (second), P^T's register r as it lies.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float *vrow = vs + buf * 32 * FLASH_VS + (8 * (r >> 2) + 4 * half + (r & 3)) * FLASH_VS + n;
+        o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[0], st[r], o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32], st[r], o1, 0, 0, 0);
+      }
+      // The other buffer was last read before the previous barrier.
+      if (more) stage(buf ^ 1);
+      __syncthreads();
+    }
+    if (live) {
+      const float den = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
+      // Lane (n, half), register r of tile t: d = 32 t + 8 (r / 4) + 4 half + r % 4.
+      float *orow = out + (b * T + p) * H * D + h * D + 4 * half;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        *reinterpret_cast<float4 *>(orow + 8 * c) =
+            make_float4(o0[4 * c] / den, o0[4 * c + 1] / den, o0[4 * c + 2] / den, o0[4 * c + 3] / den);
+        *reinterpret_cast<float4 *>(orow + 32 + 8 * c) =
+            make_float4(o1[4 * c] / den, o1[4 * c + 1] / den, o1[4 * c + 2] / den, o1[4 * c + 3] / den);
+      }
+    }
+  }
+}
+
+template <int G>
+void launch_flash(hipStream_t st, const float *q, const float *k, const float *v, float *out, int64_t batch, int64_t T,
+                  int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
+  const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
+  flash_prefill_kernel<G><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
+}
+
+inline bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const float *k, const float *v, float *out,
+                           int64_t batch, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
+  switch (G) {
+#define MI_FLASH_G(gg) \
+  case gg: launch_flash<gg>(st, q, k, v, out, batch, T, H, KVH, pos0, maxc, scale); return true;
+    MI_FLASH_G(1) MI_FLASH_G(2) MI_FLASH_G(3) MI_FLASH_G(4) MI_FLASH_G(5) MI_FLASH_G(6) MI_FLASH_G(7) MI_FLASH_G(8)
+#undef MI_FLASH_G
+    default:
+      return false;
+  }
+}
+
 // LDS bytes of a chunk kernel with `nw` wavefronts.
 inline size_t attention_smem(int64_t G, int64_t D, int64_t chunk, int nw) {
   return static_cast<size_t>(G * chunk + nw * G * D + 2 * G) * sizeof(float);
@@ -319,6 +530,7 @@ struct AttPlan {
   const float *q, *k, *v;
   int64_t D, G, maxc, items, S, chunk;
   size_t part_bytes;
+  bool flash;  // many new positions: the matrix-core kernel, no chunk partials
 };
 
 int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t, int64_t heads,
@@ -371,12 +583,21 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   P->k = static_cast<const float *>(kb->ptr);
   P->v = static_cast<const float *>(vb->ptr);
   P->D = D; P->G = G; P->maxc = maxc; P->items = items; P->S = S; P->chunk = chunk;
-  P->part_bytes = S > 1 ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
+  // The matrix-core kernel once its (32 positions, sequence, kv head) blocks
+  // fill the chip; fewer sequences keep the key-chunked kernel (a 512-token
+  // prompt at batch 1: 48 blocks, slower than 30 key chunks a position).
+  P->flash = D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535 &&
+             (t + 31) / 32 * batch * kv_heads >= FLASH_MIN_BLOCKS;
+  P->part_bytes = S > 1 && !P->flash ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
   return MI_OK;
 }
 
-void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t t, int64_t heads,
+void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, int64_t pos0, float scale) {
+  if (P.flash) {
+    flash_dispatch(P.G, ctx->stream, P.q, P.k, P.v, out, batch, t, heads, kv_heads, pos0, P.maxc, scale);
+    return;
+  }
   const int Si = static_cast<int>(P.S);
   switch (P.D) {
     case 16: dispatch_group<16>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
@@ -408,7 +629,7 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   Buffer *ob;
   s = new_buffer(ctx, batch * t, heads * P.D, MI_F32, &id, &ob);
   if (s) return s;
-  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, t, heads, kv_heads, pos0, scale);
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, pos0, scale);
   s = check_launch(ctx, "attention_rows");
   if (s) {
     mi_free(ctx, id);
@@ -440,6 +661,6 @@ extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id
     part = ctx->device >= 0 && ctx->device < ATT_MAX_DEVICES ? g_att_scratch[ctx->device].load() : nullptr;
     if (!part) return fail(ctx, MI_E_HIP, "attention_rows_into: no scratch address for device %d", ctx->device);
   }
-  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, t, heads, kv_heads, pos0, scale);
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, pos0, scale);
   return check_launch(ctx, "attention_rows_into");
 }

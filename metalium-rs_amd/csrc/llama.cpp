@@ -71,6 +71,10 @@ constexpr int64_t kFusedAttentionMaxT = 16;
 // (scores, masked softmax, P V and the regroup never touch HBM); at batch 32
 // the composition's matrix-core products win (37 against 43.5 ms).
 constexpr int64_t kFusedAttentionLongMaxBatch = 4;
+// New positions (and blocks of 32 positions x sequences x kv heads) from
+// which mi_attention_rows runs 64-wide heads on the matrix cores (its flash
+// kernel).
+constexpr int64_t kFlashMinT = 64, kFlashMinBlocks = 256;
 // Largest batch whose decode step takes the fused projections, and whose
 // head is one fused norm + projection launch (mi_norm_matvec: the GEMV up to 2
 // rows, the matrix-core form above; beyond kFusedHeadMaxBatch the head is a
@@ -94,9 +98,12 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
   x = x.reshape({rows, c.hidden});
 
-  // A few new positions (decode) take the fused attention kernel; a long
-  // prefill takes the product composition, whose MFMA products pay off there.
-  const bool fused = (t <= kFusedAttentionMaxT || batch <= kFusedAttentionLongMaxBatch) &&
+  // A few new positions (decode) take the fused attention kernel, and so does
+  // a long prompt with 64-wide heads (the matrix-core flash kernel behind
+  // mi_attention_rows) or of a few sequences; other long prompts take the
+  // product composition.
+  const bool fused = (t <= kFusedAttentionMaxT || batch <= kFusedAttentionLongMaxBatch ||
+                      (D == 64 && t >= kFlashMinT && (t + 31) / 32 * batch * KVH >= kFlashMinBlocks)) &&
                      (D == 16 || D == 32 || D == 64 || D == 128) && G <= 8;
   // The composition's causal mask for t > 1, rows (position, group) of one
   // item: row p * G + g attends to cache columns <= pos0 + p.

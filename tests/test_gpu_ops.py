@@ -740,6 +740,10 @@ def attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale):
     (4, 100, 9, 3, 64, 28, 160),     # prompts of 4 sequences after 28 cached positions
     (1, 300, 2, 1, 64, 0, 300),      # two key chunks: early positions' second chunk is empty
     (1, 1100, 9, 3, 64, 0, 1100),    # a prompt past one chunk at SmolLM2's heads: empty chunks too
+    (1, 63, 9, 3, 64, 0, 64),        # just below the matrix-core kernel: the chunk kernel
+    (32, 96, 9, 3, 64, 32, 160),     # 64+ positions filling the chip: the matrix-core (flash) kernel
+    (40, 70, 8, 1, 64, 5, 80),       # flash: 8 heads a group, a partial last query block
+    (64, 64, 2, 2, 64, 0, 64),       # flash: no grouping, the whole cache
 ])
 def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     q = rnd(batch * t, heads * D)

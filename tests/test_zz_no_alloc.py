@@ -39,8 +39,9 @@ def footprint(eng):
 
 # SmolLM2 decode at batch 32 (96 key-chunk items of several chunks each),
 # then batch 1 at a shorter context (fewer, smaller partials): the second call
-# reads an array the first one left full.
-CASES = [(32, 1, 9, 3, 64, 600, 640), (1, 1, 9, 3, 64, 300, 320)]
+# reads an array the first one left full; then a prompt long enough for the
+# matrix-core kernel (no partials).
+CASES = [(32, 1, 9, 3, 64, 600, 640), (1, 1, 9, 3, 64, 300, 320), (32, 96, 9, 3, 64, 0, 96)]
 
 
 def test_into_equals_allocating_entry_twice(eng):
@@ -58,13 +59,13 @@ def test_into_equals_allocating_entry_twice(eng):
         want = eng.download(eng.attention_rows(q, k, v, batch, t, heads, kvh, pos0, scale))
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (batch, pos0)
         outs.append(got)
-    assert outs[1].shape == (1, 9 * 64)
+    assert outs[1].shape == (1, 9 * 64) and outs[2].shape == (3072, 9 * 64)
 
 
 def test_into_refuses_partials_beyond_its_array_and_bad_outputs(eng):
-    # 4 sequences x 3 kv heads x 256 new positions after 1792 cached ones:
-    # 3072 items x 2 key chunks x 3 heads x (64 + 2) floats is 4.6 MiB.
-    batch, t, heads, kvh, D, pos0, maxc = 4, 256, 9, 3, 64, 1792, 2048
+    # 16 sequences x 3 kv heads x 48 new positions after 4000 cached ones:
+    # 2304 items x 4 key chunks x 3 heads x (64 + 2) floats is 7 MiB.
+    batch, t, heads, kvh, D, pos0, maxc = 16, 48, 9, 3, 64, 4000, 4048
     q, k, v = inputs(eng, batch, t, heads, kvh, D, maxc)
     out = eng.fill(batch * t, heads * D, miburn.F32, 0x3F800000)
     with pytest.raises(miburn.MiError) as e:
@@ -72,7 +73,7 @@ def test_into_refuses_partials_beyond_its_array_and_bad_outputs(eng):
     assert e.value.kind == "UNSUPPORTED"
     assert np.all(eng.download(out) == 1.0)
     # The same call through the allocating entry point runs.
-    assert eng.download(eng.attention_rows(q, k, v, batch, t, heads, kvh, pos0, 0.125)).shape == (1024, 576)
+    assert eng.download(eng.attention_rows(q, k, v, batch, t, heads, kvh, pos0, 0.125)).shape == (768, 576)
     small = eng.fill(batch * t, heads * D - 64, miburn.F32, 0)
     with pytest.raises(miburn.MiError) as e:
         eng.attention_rows_into(q, k, v, batch, t, heads, kvh, 0, 0.125, small)  # wrong output shape
