@@ -18,6 +18,10 @@ SmolLM2-135M-shaped decoder (config 5) at batch 1 and 32 -- prefill 512 tokens,
 greedy-decode 128, tokens/s -- and `mlp_train`, the MLP training step
 (config 1), ms/step over 100 steps.
 
+Before the timed steps the product runs untimed for the W warm-up steps and
+at least two seconds (the GPU's clocks ramp up under sustained load; the
+timed steps measure the steady state).
+
 Flags: --gpus N (only 1: this build runs on one GPU), --steps K, --warmup W,
 --n (cube size, default 4096), --dtype bf16|f32, --no-cpu, --no-models.  `--suite` instead
 prints one JSON line per kernel of the HBM-bound suite (BASELINE.json
@@ -44,6 +48,7 @@ HBM_PEAK_GBS = 8000.0
 # a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,922 KiB
 # read + 65,536 KiB written.  Only that configuration was measured.
 GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268756687}
+WARM_S = 2.0  # seconds of untimed product before the timed steps (clock ramp-up)
 
 
 def cpu_baseline(n: int = 4096, seconds: float = 10.0) -> dict:
@@ -408,9 +413,17 @@ def main() -> int:
         a, b = a32, b32
     eng.sync()
 
-    for _ in range(args.warmup):
-        eng.free(eng.matmul_dram(a, False, b, False))
-    eng.sync()
+    # Untimed warm-up: the W steps asked for, and at least WARM_S seconds of
+    # the same product -- MI355X raises its clocks over a second or two of
+    # sustained load (4096^3: ~1000-1080 TF/s in the first steps from idle,
+    # ~1180 at steady state), and the timed steps measure the steady state.
+    t_warm = time.perf_counter()
+    done = 0
+    while done < args.warmup or time.perf_counter() - t_warm < WARM_S:
+        for _ in range(10):
+            eng.free(eng.matmul_dram(a, False, b, False))
+        done += 10
+        eng.sync()
 
     eng.event_record(0)
     t0 = time.perf_counter()

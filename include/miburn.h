@@ -123,6 +123,19 @@ int mi_matmul_blocks(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
                      int64_t b_offset, int64_t b_stride, int out_elem,
                      mi_id *out);
 
+/* Engine::matmul_dram_batched (server.rs:229-237) over an arbitrary list of
+ * operand blocks (the trait's `&[(Block, Block)]`; Block,
+ * crates/tt-kernels/src/tensor.rs:3479-3483): item i multiplies the block of
+ * `a` whose top-left element is (a_at[2i], a_at[2i + 1]), `[m, k]` or,
+ * transposed (a_transposed[i]), `[k, m]`, by the block of `b` at
+ * (b_at[2i], b_at[2i + 1]), `[k, n]` or `[n, k]`.  Result `[items * m, n]`,
+ * item i in rows i m .. i m + m - 1.  Runs of items stepping by constant
+ * offsets are one launch. */
+int mi_matmul_pairs(mi_ctx *ctx, mi_id a, mi_id b, int64_t items,
+                    const int64_t *a_at, const int *a_transposed,
+                    const int64_t *b_at, const int *b_transposed, int64_t m,
+                    int64_t k, int64_t n, int out_elem, mi_id *out);
+
 /* Products over strided items, the result written in place: what Burn's
  * multi-head attention runs as reshape + swap_dims + batched matmul (the
  * reference's batched_matmul, crates/burn-tt/src/ops.rs:2981-3052, after
@@ -231,6 +244,12 @@ enum mi_axis { MI_AXIS_ROWS = 0, MI_AXIS_COLS = 1 };
 int mi_reduce(mi_ctx *ctx, mi_id a, int op, int axis, mi_id *out);
 /* The whole buffer to `[1, 1]` (float_sum / float_mean, ops.rs:3246-3400). */
 int mi_reduce_all(mi_ctx *ctx, mi_id a, int op, mi_id *out);
+/* Engine::reduce with its `then` (server.rs:404-412; ReduceThen,
+ * crates/tt-kernels/src/tensor.rs:6038): the reduction, then the unary kind
+ * `then_kind` (0 for none) with scalar `then_scalar` applied to its result --
+ * a softmax's clamp_min of a row max, say -- bit for bit the two ops. */
+int mi_reduce_then(mi_ctx *ctx, mi_id a, int op, int axis, uint32_t then_kind,
+                   float then_scalar, mi_id *out);
 
 /* ---- softmax: Engine::softmax_rows (server.rs:428) and the
  * softmax/log_softmax composition (ops.rs:5133-5166) ----
@@ -247,6 +266,10 @@ int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, int log,
  * row or 0. */
 int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem,
                 mi_id *out);
+/* Engine::add_rms_norm (server.rs:466-475): `sum = a + b` and
+ * rms_norm(sum, gamma, eps), both new buffers; bit for bit the two ops. */
+int mi_add_rms_norm(mi_ctx *ctx, mi_id a, mi_id b, mi_id gamma, float eps,
+                    mi_id *sum, mi_id *norm);
 /* LayerNorm over each row, `(a - mean) / sqrt(var + eps) * gamma + beta`
  * (Burn's `LayerNorm`, biased variance); gamma/beta `[1, cols]` or 0. */
 int mi_layer_norm(mi_ctx *ctx, mi_id a, mi_id gamma, mi_id beta, float eps,

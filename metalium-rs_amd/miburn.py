@@ -107,6 +107,10 @@ def _load() -> ctypes.CDLL:
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
         "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
         "mi_attention_rows_into": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, U64],
+        "mi_reduce_then": [P, U64, c_int, c_int, c_u32, c_float, Ip],
+        "mi_add_rms_norm": [P, U64, U64, U64, c_float, Ip, Ip],
+        "mi_matmul_pairs": [P, U64, U64, I64, ctypes.POINTER(I64), ctypes.POINTER(c_int), ctypes.POINTER(I64),
+                            ctypes.POINTER(c_int), I64, I64, I64, c_int, Ip],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_qkv_rope_cache": [P, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
@@ -357,6 +361,27 @@ class Engine:
 
     def reduce(self, a: int, op: int, axis: int) -> int:
         return self._out(self._lib.mi_reduce, a, op, axis)
+
+    def reduce_then(self, a: int, op: int, axis: int, then_kind=0, then_scalar: float = 0.0) -> int:
+        """Engine::reduce with `then`: an exact unary kind on the result."""
+        k = K[then_kind] if isinstance(then_kind, str) else int(then_kind)
+        return self._out(self._lib.mi_reduce_then, a, op, axis, k, then_scalar)
+
+    def add_rms_norm(self, a: int, b: int, gamma: int = 0, eps: float = 1e-5):
+        """Engine::add_rms_norm: (a + b, rms_norm(a + b) * gamma)."""
+        s, nrm = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(self._lib.mi_add_rms_norm(self.ctx, a, b, gamma, eps, ctypes.byref(s), ctypes.byref(nrm)))
+        return s.value, nrm.value
+
+    def matmul_pairs(self, a: int, b: int, a_blocks, b_blocks, m: int, k: int, n: int, out_elem: int = F32) -> int:
+        """Engine::matmul_dram_batched over (Block, Block) pairs: each block
+        ((row, col), transposed)."""
+        items = len(a_blocks)
+        aat = (ctypes.c_int64 * (2 * items))(*[v for (rc, _) in a_blocks for v in rc])
+        bat = (ctypes.c_int64 * (2 * items))(*[v for (rc, _) in b_blocks for v in rc])
+        at_ = (ctypes.c_int * items)(*[int(t) for (_, t) in a_blocks])
+        bt_ = (ctypes.c_int * items)(*[int(t) for (_, t) in b_blocks])
+        return self._out(self._lib.mi_matmul_pairs, a, b, items, aat, at_, bat, bt_, m, k, n, out_elem)
 
     def reduce_all(self, a: int, op: int) -> int:
         return self._out(self._lib.mi_reduce_all, a, op)

@@ -254,6 +254,48 @@ def test_max_min_exact(engine, shape, axis):
         same_bits(engine.download(engine.reduce(a, op, axis)), orc.reduce(x, op, axis))
 
 
+def test_reduce_then_is_reduce_then_op(engine):
+    """Engine::reduce's `then`: the exact unary kind on the reduction, bit for
+    bit the two ops (a softmax's clamp_min of its row max)."""
+    x = rnd(37, 300)
+    x[5] = -np.inf
+    ix = engine.upload(x)
+    for op, axis, kind, sc in [(R_MAX, AXIS_COLS, "CLAMP_MIN", -3.4028235e38), (R_SUM, AXIS_ROWS, "MUL_SCALAR", 0.5),
+                               (R_MEAN, AXIS_COLS, 0, 0.0)]:
+        got = engine.download(engine.reduce_then(ix, op, axis, kind, sc))
+        r = engine.reduce(ix, op, axis)
+        want = engine.download(engine.eltwise_op_as(kind, r, scalar=sc)) if kind else engine.download(r)
+        same_bits(got, want)
+        if kind:
+            same_bits(got, orc.eltwise(K[kind], orc.reduce(x, op, axis), s1=sc))
+
+
+def test_add_rms_norm(engine):
+    a, b, g = rnd(9, 576), rnd(9, 576), rnd(1, 576) + np.float32(1.0)
+    s, n = engine.add_rms_norm(engine.upload(a), engine.upload(b), engine.upload(g), 1e-5)
+    same_bits(engine.download(s), a + b)
+    close(engine.download(n), orc.rms_norm(a + b, g, 1e-5), rtol=1e-5, atol=1e-30)
+
+
+def test_matmul_pairs_arbitrary_blocks(engine):
+    """matmul_dram_batched over (Block, Block) items: a constant-stride run,
+    then items in any order, transposed blocks among them."""
+    A, B = rnd(96, 80), rnd(120, 64)
+    m, k, n = 16, 24, 32
+    a_blocks = [((0, 0), False), ((16, 0), False), ((32, 0), False), ((8, 40), False), ((40, 8), True), ((0, 56), True)]
+    b_blocks = [((0, 0), False), ((24, 0), False), ((48, 0), False), ((96, 32), False), ((3, 5), True), ((60, 30), True)]
+    got = engine.download(engine.matmul_pairs(engine.upload(A), engine.upload(B), a_blocks, b_blocks, m, k, n))
+    assert got.shape == (6 * m, n)
+    for i, (((ar, ac), at), ((br, bc), bt)) in enumerate(zip(a_blocks, b_blocks)):
+        ab = A[ar:ar + (k if at else m), ac:ac + (m if at else k)]
+        bb = B[br:br + (n if bt else k), bc:bc + (k if bt else n)]
+        want = orc.matmul(ab.copy(), bb.copy(), at, bt)
+        assert np.all(np.abs(got[i * m:(i + 1) * m] - want) <= mm_tol(ab, bb, at, bt, 1e-5) + 1e-30), i
+    with pytest.raises(miburn.MiError) as e:
+        engine.matmul_pairs(engine.upload(A), engine.upload(B), [((90, 0), False)], [((0, 0), False)], m, k, n)
+    assert e.value.kind == "ARG"  # the A block leaves its buffer
+
+
 def test_reduce_all(engine):
     x = rnd(333, 777)
     a = engine.upload(x)
