@@ -15,7 +15,8 @@ about 10 s).
 
 The same line carries BASELINE.json's other measured configs: `decoder`, the
 SmolLM2-135M-shaped decoder (config 5) at batch 1 and 32 -- prefill 512 tokens,
-greedy-decode 128, tokens/s -- and `mlp_train`, the MLP training step
+greedy-decode 128, tokens/s, under the reference numeric contract and (in
+`decoder_performance_numerics`) the performance one -- and `mlp_train`, the MLP training step
 (config 1), ms/step over 100 steps.
 
 Before the timed steps the product runs untimed for the W warm-up steps and
@@ -242,21 +243,24 @@ def suite(steps: int, matmul_mode=None) -> int:
     return 0
 
 
-def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128) -> dict:
+def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: str = "reference") -> dict:
     """the SmolLM2-135M-shaped decoder (random N(0, 0.02)
     BF16 weights), prefill `prompt` random tokens per sequence, then greedy
-    decode `new` tokens; tokens/s of the prefill and of the decode steps."""
+    decode `new` tokens; tokens/s of the prefill and of the decode steps.
+    `numerics`: the reference contract (F32 KV cache and activations) or the
+    performance one (BF16 KV cache, BF16 prefill activation operands)."""
     import miburn
-    m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt + new, max_batch=batch, seed=5)
+    m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt + new, max_batch=batch, seed=5, numerics=numerics)
     rng = np.random.default_rng(9)
     ids = rng.integers(0, 49152, (batch, prompt)).astype(np.int32)
     m.generate(ids[:, :32], 4)  # warm the kernels
     out, pf_ms, dc_ms = m.generate(ids, new)
     m.close()
     # Rooflines (algorithmic work): a decode step reads every BF16 weight once
-    # (134.48 M parameters, the tied table included) plus each sequence's F32
-    # key/value cache (2 x 30 layers x 3 kv heads x 64 x 4 B a position, at the
-    # steps' mean context); a prefill's FLOP are 2 x tokens x the layers'
+    # (134.48 M parameters, the tied table included) plus each sequence's
+    # key/value cache (2 x 30 layers x 3 kv heads x 64 x 4 B a position for
+    # F32, 2 B for BF16, at the steps' mean context); a prefill's FLOP are
+    # 2 x tokens x the layers'
     # 106.17 M weights plus causal attention (2 t (t + 1) x 64 x 9 heads x 30
     # layers a sequence) and the last position's head.
     cfg = miburn.SMOLLM2_135M
@@ -264,13 +268,13 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128) -> dict:
                  + 3 * cfg["intermediate"] * cfg["hidden"])
     layer_params = cfg["layers"] * per_layer
     params = layer_params + cfg["vocab"] * cfg["hidden"]
-    kv_per_pos = 2 * cfg["layers"] * cfg["kv_heads"] * cfg["head_dim"] * 4
+    kv_per_pos = 2 * cfg["layers"] * cfg["kv_heads"] * cfg["head_dim"] * (2 if numerics == "performance" else 4)
     mean_ctx = prompt + new / 2
     step_bytes = 2 * params + batch * kv_per_pos * mean_ctx
     dc_step_ms = dc_ms / max(new - 1, 1)
     attn = 2 * prompt * (prompt + 1) * cfg["head_dim"] * cfg["heads"] * cfg["layers"]
     pf_flop = batch * (2 * prompt * layer_params + attn + 2 * cfg["hidden"] * cfg["vocab"])
-    return {"batch": batch, "prompt": prompt, "new_tokens": new,
+    return {"batch": batch, "numerics": numerics, "prompt": prompt, "new_tokens": new,
             "prefill_ms": round(pf_ms, 2), "prefill_tokens_per_s": round(batch * prompt / (pf_ms / 1e3), 1),
             "prefill_gflop": round(pf_flop / 1e9, 1),
             "prefill_mfma_frac": round(pf_flop / (pf_ms * 1e-3) / (PEAK_TFLOPS["bf16"] * 1e12), 4),
@@ -375,6 +379,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["decoder", "mlp", "transformer"],
                     help="run one model harness alone (for profiling) and print its JSON")
     ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
+    ap.add_argument("--numerics", choices=["reference", "performance"], default="reference",
+                    help="decoder numeric contract for --only decoder")
     ap.add_argument("--no-traces", action="store_true",
                     help="skip the traced (HIP-graph) training steps (rocprofv3's kernel trace does not follow "
                          "graph replays)")
@@ -394,7 +400,7 @@ def main() -> int:
     if args.matmul_mode:
         eng.set_matmul_mode(miburn.MATMUL_FAST if args.matmul_mode == "fast" else miburn.MATMUL_ACCURATE)
     if args.only:
-        out = {"decoder": lambda: decoder_bench(eng, args.batch),
+        out = {"decoder": lambda: decoder_bench(eng, args.batch, numerics=args.numerics),
                "mlp": lambda: mlp_bench(eng, traces=not args.no_traces),
                "transformer": lambda: transformer_bench(eng, traces=not args.no_traces)}[args.only]()
         print(json.dumps({"harness": args.only, **out}), flush=True)
@@ -464,6 +470,8 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline()
     if not args.no_models:
         line["decoder"] = [decoder_bench(eng, 1), decoder_bench(eng, 32)]
+        line["decoder_performance_numerics"] = [decoder_bench(eng, 1, numerics="performance"),
+                                                decoder_bench(eng, 32, numerics="performance")]
         line["mlp_train"] = mlp_bench(eng, traces=not args.no_traces)
         line["transformer_train"] = transformer_bench(eng, traces=not args.no_traces)
         if not args.no_cpu:

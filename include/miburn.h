@@ -418,10 +418,12 @@ int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
                      int64_t heads, int64_t kv_heads, int64_t pos,
                      mi_id k_cache, mi_id v_cache, mi_id *q_out);
 /* silu(gate) * up over the halves of a fused gate|up product: gate_up
- * [rows, 2 i] F32 -> [rows, i] (the reference's MLP, crates/tt-models/src/
- * llama.rs:494-498, on the two row blocks of its gate|up weight); no Engine
- * counterpart.  Bit-identical to MI_K_SILU_MUL of the two halves. */
-int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, mi_id *out);
+ * [rows, 2 i] F32 -> [rows, i] of out_elem (the reference's MLP, crates/
+ * tt-models/src/llama.rs:494-498, on the two row blocks of its gate|up
+ * weight); no Engine counterpart.  F32: bit-identical to MI_K_SILU_MUL of the
+ * two halves; BF16: that value rounded once (the performance contract's
+ * activation operand, llama.rs:1270-1274). */
+int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, int out_elem, mi_id *out);
 /* The q|k|v tail of a prefill in one launch: the composition the reference's
  * attention block makes of RoPE on the query and key heads, the key/value
  * cache write and the queries' grouping per kv head (crates/tt-models/src/

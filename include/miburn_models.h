@@ -19,10 +19,23 @@ extern "C" {
 /* ---- Llama / SmolLM2 decoder (crates/tt-models/src/llama.rs:40-71,
  * 140-520, 1030-1178): pre-norm GQA attention with RoPE, SwiGLU MLP, RMSNorm,
  * tied embedding head, BF16 weights and F32 activations. ---- */
+
+/* The two numeric contracts inference runs under (llama.rs:1252-1282, the
+ * reference's `Numerics`): REFERENCE keeps the KV cache and every
+ * activation F32; PERFORMANCE stores the KV cache BF16 (half its bytes) and
+ * rounds each activation a prefill's product reads to BF16 once, where it is
+ * made (the attention and MLP norms, the attention output, the SiLU-mul, the
+ * final norm).  A decode step's fused projections read F32 activations under
+ * both: their traffic is the weights'.  The reference's BFP8 weights are a
+ * Tensix block format with no counterpart here; weights are BF16 under both. */
+#define MI_NUMERICS_REFERENCE 0
+#define MI_NUMERICS_PERFORMANCE 1
+
 typedef struct mi_llama_config {
   int32_t vocab, hidden, layers, heads, kv_heads, head_dim, intermediate;
   float rope_theta, eps;
   int32_t max_ctx, max_batch;
+  int32_t numerics; /* MI_NUMERICS_* */
 } mi_llama_config;
 
 typedef struct mi_llama mi_llama;

@@ -6,8 +6,11 @@
 // above the causal diagonal, max clamped below at -FLT_MAX, exp(x - max), sum
 // clamped below at FLT_MIN, divide, then P V.
 //
-// MI355X design.  The cache of one (sequence, kv head) item is F32 [max_ctx,
-// D], position-major, so a key or value row is one contiguous D-float read.
+// MI355X design.  The cache of one (sequence, kv head) item is [max_ctx, D],
+// position-major, so a key or value row is one contiguous read; its elements
+// are F32 (the reference numeric contract) or BF16 (the performance
+// contract's cache, llama.rs:1276-1278: half the bytes), widened to F32 as
+// they are loaded -- every product and sum is F32 either way.
 // A block of 4 wavefronts takes one (item, query position, key chunk); the
 // group's G query heads share every key and value row read.
 // D/4 lanes read a row as float4s (a wavefront covers 64/(D/4) rows per
@@ -53,8 +56,8 @@ __device__ __forceinline__ void dots(const float4 (&qv)[G], float4 kv, float (&p
 
 // One (item, position, chunk).  DIRECT: the only chunk -- write normalised
 // rows of `out`.  Else write part[(item * S + s)] = {m[G], l[G], o[G][D]}.
-template <int D, int G, int NW>
-__global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q, const float *kc, const float *vc,
+template <int D, int G, int NW, typename KV>
+__global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q, const KV *kc, const KV *vc,
                                                               float *out, float *part, int64_t T, int64_t H,
                                                               int64_t KVH, int64_t pos0, int64_t maxc, int64_t chunk,
                                                               float scale, int direct) {
@@ -71,8 +74,8 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
   const int64_t n = pos0 + p + 1;  // causal: cache positions 0 .. pos0 + p
   const int64_t lo = static_cast<int64_t>(s) * chunk;
   const int64_t len = n > lo ? (n - lo < chunk ? n - lo : chunk) : 0;
-  const float *K = kc + ((bj)*maxc + lo) * D;
-  const float *V = vc + ((bj)*maxc + lo) * D;
+  const KV *K = kc + ((bj)*maxc + lo) * D;
+  const KV *V = vc + ((bj)*maxc + lo) * D;
   float *scores = sm;                     // [G][chunk]
   float *red = sm + G * chunk;            // [NW][G][D]
   float *stat = red + NW * G * D;         // [G] max, [G] sum
@@ -94,7 +97,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t c = first + u * STEP;
-    vv[u] = *reinterpret_cast<const float4 *>(V + (c < len ? c : last) * D + 4 * sl);
+    vv[u] = f32x4_get(V + (c < len ? c : last) * D + 4 * sl);
   }
 
   // Scores, U accesses in flight per wavefront.
@@ -103,7 +106,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + u * STEP;
-      kv[u] = *reinterpret_cast<const float4 *>(K + (c < len ? c : last) * D + 4 * sl);
+      kv[u] = f32x4_get(K + (c < len ? c : last) * D + 4 * sl);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -151,7 +154,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t c = c0 + u * STEP;
-        vv[u] = *reinterpret_cast<const float4 *>(V + (c < len ? c : last) * D + 4 * sl);
+        vv[u] = f32x4_get(V + (c < len ? c : last) * D + 4 * sl);
       }
     }
 #pragma unroll
@@ -264,9 +267,9 @@ constexpr int FLASH_VS = 72;     // ... and the value block
 
 typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
 
-template <int G>
+template <int G, typename KV>
 __global__ void __launch_bounds__(G * 64) __attribute__((amdgpu_waves_per_eu(3)))
-flash_prefill_kernel(const float *q, const float *kc, const float *vc, float *out, int64_t T, int64_t H, int64_t KVH,
+flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int64_t T, int64_t H, int64_t KVH,
                      int64_t pos0, int64_t maxc, float scale) {
   constexpr int D = 64, NT = G * 64;
   __shared__ __attribute__((aligned(16))) float ks[2 * 32 * FLASH_KS];
@@ -278,7 +281,7 @@ flash_prefill_kernel(const float *q, const float *kc, const float *vc, float *ou
   const int64_t ctx = pos0 + T;
   const int64_t h = j * G + g;
   const float scale2 = scale * 1.4426950408889634f;
-  const float *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
+  const KV *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
   const int ctx32 = static_cast<int>(ctx);  // the host keeps a cache item below 2^31 / D rows
   // A block takes query blocks x and nqb - 1 - x in turn: a long and a short
   // run of keys, so every block has about the same work (causal attention's
@@ -322,8 +325,8 @@ flash_prefill_kernel(const float *q, const float *kc, const float *vc, float *ou
         const int e0 = tid + u * NT, e = e0 < 32 * 16 ? e0 : tid;
         const int r = static_cast<int>(j0) + (e >> 4) < ctx32 ? static_cast<int>(j0) + (e >> 4) : ctx32 - 1;
         const int off = r * D + (e & 15) * 4;
-        kr[u] = *reinterpret_cast<const float4 *>(K + off);
-        vr[u] = *reinterpret_cast<const float4 *>(V + off);
+        kr[u] = f32x4_get(K + off);
+        vr[u] = f32x4_get(V + off);
       }
     };
     auto stage = [&](int buf) {
@@ -431,18 +434,19 @@ flash_prefill_kernel(const float *q, const float *kc, const float *vc, float *ou
   }
 }
 
-template <int G>
-void launch_flash(hipStream_t st, const float *q, const float *k, const float *v, float *out, int64_t batch, int64_t T,
+template <int G, typename KV>
+void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch, int64_t T,
                   int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
   const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
-  flash_prefill_kernel<G><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
+  flash_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
 }
 
-inline bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const float *k, const float *v, float *out,
-                           int64_t batch, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
+template <typename KV>
+bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch,
+                    int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
   switch (G) {
 #define MI_FLASH_G(gg) \
-  case gg: launch_flash<gg>(st, q, k, v, out, batch, T, H, KVH, pos0, maxc, scale); return true;
+  case gg: launch_flash<gg, KV>(st, q, k, v, out, batch, T, H, KVH, pos0, maxc, scale); return true;
     MI_FLASH_G(1) MI_FLASH_G(2) MI_FLASH_G(3) MI_FLASH_G(4) MI_FLASH_G(5) MI_FLASH_G(6) MI_FLASH_G(7) MI_FLASH_G(8)
 #undef MI_FLASH_G
     default:
@@ -455,27 +459,27 @@ inline size_t attention_smem(int64_t G, int64_t D, int64_t chunk, int nw) {
   return static_cast<size_t>(G * chunk + nw * G * D + 2 * G) * sizeof(float);
 }
 
-template <int D, int G>
-void launch_attention(hipStream_t st, const float *q, const float *k, const float *v, float *out, float *part,
+template <int D, int G, typename KV>
+void launch_attention(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, float *part,
                       int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
                       int64_t chunk, float scale) {
   const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(S));
   const size_t smem = attention_smem(G, D, chunk, ATT_WAVES);
-  attention_chunk_kernel<D, G, ATT_WAVES><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pos0, maxc,
+  attention_chunk_kernel<D, G, ATT_WAVES, KV><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pos0, maxc,
                                                                             chunk, scale, S == 1);
   if (S > 1)
     attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, static_cast<size_t>(3 * G * S + G) * sizeof(float),
                                      st>>>(part, out, T, H, KVH, S);
 }
 
-template <int D>
-bool dispatch_group(int64_t G, hipStream_t st, const float *q, const float *k, const float *v, float *out,
+template <int D, typename KV>
+bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, float *out,
                     float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0,
                     int64_t maxc, int64_t chunk, float scale) {
   switch (G) {
 #define MI_ATT_G(g)                                                                                   \
   case g:                                                                                             \
-    launch_attention<D, g>(st, q, k, v, out, part, items, S, T, H, KVH, pos0, maxc, chunk, scale); \
+    launch_attention<D, g, KV>(st, q, k, v, out, part, items, S, T, H, KVH, pos0, maxc, chunk, scale); \
     return true;
     MI_ATT_G(1) MI_ATT_G(2) MI_ATT_G(3) MI_ATT_G(4) MI_ATT_G(5) MI_ATT_G(6) MI_ATT_G(7) MI_ATT_G(8)
 #undef MI_ATT_G
@@ -527,7 +531,9 @@ namespace {
 // size, shared by the allocating and the no-allocation entry points so both
 // run the same kernels on the same chunks.
 struct AttPlan {
-  const float *q, *k, *v;
+  const float *q;
+  const void *k, *v;
+  bool kv16;  // BF16 caches (else F32)
   int64_t D, G, maxc, items, S, chunk;
   size_t part_bytes;
   bool flash;  // many new positions: the matrix-core kernel, no chunk partials
@@ -538,8 +544,9 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   MI_BUF(ctx, qb, q);
   MI_BUF(ctx, kb, k_cache);
   MI_BUF(ctx, vb, v_cache);
-  if (qb->elem != MI_F32 || kb->elem != MI_F32 || vb->elem != MI_F32)
-    return fail(ctx, MI_E_ARG, "attention_rows takes F32 queries and caches");
+  if (qb->elem != MI_F32 || kb->elem != vb->elem || !elem_float(kb->elem))
+    return fail(ctx, MI_E_ARG, "attention_rows takes F32 queries and two F32 or two BF16 caches (q %s, k %s, v %s)",
+                elem_name(qb->elem), elem_name(kb->elem), elem_name(vb->elem));
   if (batch < 1 || t < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads)
     return fail(ctx, MI_E_ARG, "attention_rows: batch %lld, t %lld, heads %lld, kv heads %lld", (long long)batch,
                 (long long)t, (long long)heads, (long long)kv_heads);
@@ -580,8 +587,9 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   if (static_cast<size_t>(3 * G * S + G) * sizeof(float) > 65536)
     return fail(ctx, MI_E_UNSUPPORTED, "attention_rows: context of %lld keys too long", (long long)nmax);
   P->q = static_cast<const float *>(qb->ptr);
-  P->k = static_cast<const float *>(kb->ptr);
-  P->v = static_cast<const float *>(vb->ptr);
+  P->k = kb->ptr;
+  P->v = vb->ptr;
+  P->kv16 = kb->elem == MI_BF16;
   P->D = D; P->G = G; P->maxc = maxc; P->items = items; P->S = S; P->chunk = chunk;
   // The matrix-core kernel once its (32 positions, sequence, kv head) blocks
   // fill the chip; fewer sequences keep the key-chunked kernel (a 512-token
@@ -592,19 +600,29 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   return MI_OK;
 }
 
-void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t, int64_t heads,
-                      int64_t kv_heads, int64_t pos0, float scale) {
+template <typename KV>
+void attention_launch_kv(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t,
+                         int64_t heads, int64_t kv_heads, int64_t pos0, float scale) {
+  const KV *k = static_cast<const KV *>(P.k), *v = static_cast<const KV *>(P.v);
   if (P.flash) {
-    flash_dispatch(P.G, ctx->stream, P.q, P.k, P.v, out, batch, t, heads, kv_heads, pos0, P.maxc, scale);
+    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, pos0, P.maxc, scale);
     return;
   }
   const int Si = static_cast<int>(P.S);
   switch (P.D) {
-    case 16: dispatch_group<16>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    case 32: dispatch_group<32>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    case 64: dispatch_group<64>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    default: dispatch_group<128>(P.G, ctx->stream, P.q, P.k, P.v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 16: dispatch_group<16, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 32: dispatch_group<32, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 64: dispatch_group<64, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    default: dispatch_group<128, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
   }
+}
+
+void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t, int64_t heads,
+                      int64_t kv_heads, int64_t pos0, float scale) {
+  if (P.kv16)
+    attention_launch_kv<uint16_t>(ctx, P, out, part, batch, t, heads, kv_heads, pos0, scale);
+  else
+    attention_launch_kv<float>(ctx, P, out, part, batch, t, heads, kv_heads, pos0, scale);
 }
 
 }  // namespace

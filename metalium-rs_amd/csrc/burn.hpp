@@ -276,9 +276,9 @@ inline Tensor softmax_rows(const Tensor &x, const Tensor *mask, float scale, boo
   return Tensor(x.ctx(), id, x.shape());
 }
 
-inline Tensor rms_norm(const Tensor &x, const Tensor &gamma, float eps) {
+inline Tensor rms_norm(const Tensor &x, const Tensor &gamma, float eps, int out_elem = MI_F32) {
   mi_id id;
-  check(x.ctx(), mi_rms_norm(x.ctx(), x.use(), gamma.use(), eps, MI_F32, &id), "rms_norm");
+  check(x.ctx(), mi_rms_norm(x.ctx(), x.use(), gamma.use(), eps, out_elem, &id), "rms_norm");
   return Tensor(x.ctx(), id, x.shape());
 }
 
@@ -373,10 +373,11 @@ inline Tensor rope(const Tensor &x, const Tensor &cos, const Tensor &sin, int64_
   return Tensor(x.ctx(), id, x.shape());
 }
 
-// silu(gate) * up of a fused gate|up product's halves (mi_silu_mul_halves).
-inline Tensor silu_mul_halves(const Tensor &gate_up) {
+// silu(gate) * up of a fused gate|up product's halves (mi_silu_mul_halves),
+// F32 or rounded to BF16.
+inline Tensor silu_mul_halves(const Tensor &gate_up, int out_elem = MI_F32) {
   mi_id id;
-  check(gate_up.ctx(), mi_silu_mul_halves(gate_up.ctx(), gate_up.use(), &id), "silu_mul_halves");
+  check(gate_up.ctx(), mi_silu_mul_halves(gate_up.ctx(), gate_up.use(), out_elem, &id), "silu_mul_halves");
   return Tensor(gate_up.ctx(), id, {gate_up.rows(), gate_up.cols() / 2});
 }
 

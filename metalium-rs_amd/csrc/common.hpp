@@ -44,6 +44,25 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// F32 values in F32 or BF16 (uint16_t bits) storage -- a KV cache under the
+// reference or the performance numeric contract, an activation stored for a
+// product's operand: four consecutive values widened to F32, and F32 values
+// stored (BF16 rounded to nearest, ties to even).
+__device__ __forceinline__ float4 f32x4_get(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ float4 f32x4_get(const uint16_t *p) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(p);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                     __uint_as_float(u.y & 0xffff0000u));
+}
+__device__ __forceinline__ void f32x4_put(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+__device__ __forceinline__ void f32x4_put(uint16_t *p, float4 v) {
+  const uint32_t a = f32_to_bf16_bits(v.x) | (static_cast<uint32_t>(f32_to_bf16_bits(v.y)) << 16);
+  const uint32_t b = f32_to_bf16_bits(v.z) | (static_cast<uint32_t>(f32_to_bf16_bits(v.w)) << 16);
+  *reinterpret_cast<uint2 *>(p) = make_uint2(a, b);
+}
+__device__ __forceinline__ void f32_put(float *p, float v) { *p = v; }
+__device__ __forceinline__ void f32_put(uint16_t *p, float v) { *p = f32_to_bf16_bits(v); }
+
 // The logistic function in its two-branch form, so neither exponential
 // overflows: 1 / (1 + e^-x) for x >= 0 and e^x / (1 + e^x) below.  Both
 // quotients share t = e^-|x| (which is e^-x above zero and e^x below), so it

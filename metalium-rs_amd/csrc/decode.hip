@@ -43,12 +43,28 @@ struct DecodeArgs {
   int64_t ldo, inter;
   // DM_QKV: pair p = rows (h d + i, h d + i + d / 2) of head h = p / (d / 2)
   // over heads q 0..H-1, k H..H+KVH-1, v H+KVH..H+2KVH-1; q to `out`, k and v
-  // into the caches at position pos of item (row m, kv head).
+  // into the caches at position pos of item (row m, kv head): F32, or BF16
+  // (kv16; rounded to nearest even as stored).
   int d, H, KVH;
   int64_t pos, maxc;
   const float *cos, *sin;
-  float *kc, *vc;
+  void *kc, *vc;
+  int kv16;
 };
+
+// Two values of one cache row, elements hi and hi + half of the row at `at`.
+__device__ __forceinline__ void cache_pair(const DecodeArgs &g, void *base, int64_t at, int64_t hi, int64_t half,
+                                           float a, float b) {
+  if (g.kv16) {
+    uint16_t *o = static_cast<uint16_t *>(base) + at;
+    o[hi] = f32_to_bf16_bits(a);
+    o[hi + half] = f32_to_bf16_bits(b);
+  } else {
+    float *o = static_cast<float *>(base) + at;
+    o[hi] = a;
+    o[hi + half] = b;
+  }
+}
 
 __device__ __forceinline__ void bf16x8(uint4 q, float (&w)[8]) {
   const uint32_t u[4] = {q.x, q.y, q.z, q.w};
@@ -105,14 +121,15 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
       const float *cs = g.cos + g.pos * g.d, *sn = g.sin + g.pos * g.d;
       const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
       const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
-      float *o = head < g.H ? g.out + m * g.ldo + head * g.d
-                            : g.kc + ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d;
-      o[hi] = o0;
-      o[hi + half] = o1;
+      if (head < g.H) {
+        float *o = g.out + m * g.ldo + head * g.d;
+        o[hi] = o0;
+        o[hi + half] = o1;
+      } else {
+        cache_pair(g, g.kc, ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d, hi, half, o0, o1);
+      }
     } else {
-      float *o = g.vc + ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d;
-      o[hi] = y0;
-      o[hi + half] = y1;
+      cache_pair(g, g.vc, ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d, hi, half, y0, y1);
     }
   }
 }
@@ -692,9 +709,10 @@ extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi
   if (wb->rows != (heads + 2 * kv_heads) * D)
     return fail(ctx, MI_E_ARG, "norm_qkv_rope: weight has %lld rows, want (heads + 2 kv_heads) * %lld = %lld",
                 (long long)wb->rows, (long long)D, (long long)((heads + 2 * kv_heads) * D));
-  if (kb->elem != MI_F32 || vb->elem != MI_F32 || vb->cols != D || vb->rows != kb->rows ||
+  if (kb->elem != vb->elem || !elem_float(kb->elem) || vb->cols != D || vb->rows != kb->rows ||
       kb->rows % (M * kv_heads))
-    return fail(ctx, MI_E_ARG, "norm_qkv_rope: caches must both be [rows * kv_heads * max_ctx, %lld] F32", (long long)D);
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: caches must both be [rows * kv_heads * max_ctx, %lld], both F32 or both BF16",
+                (long long)D);
   const int64_t maxc = kb->rows / (M * kv_heads);
   if (pos < 0 || pos >= maxc) return fail(ctx, MI_E_ARG, "norm_qkv_rope: position %lld beyond the cache's %lld", (long long)pos, (long long)maxc);
   if (cb->elem != MI_F32 || sb->elem != MI_F32 || cb->cols != D || sb->cols != D || cb->rows <= pos || sb->rows <= pos)
@@ -721,8 +739,9 @@ extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi
   g.maxc = maxc;
   g.cos = static_cast<const float *>(cb->ptr);
   g.sin = static_cast<const float *>(sb->ptr);
-  g.kc = static_cast<float *>(kb->ptr);
-  g.vc = static_cast<float *>(vb->ptr);
+  g.kc = kb->ptr;
+  g.vc = vb->ptr;
+  g.kv16 = kb->elem == MI_BF16 ? 1 : 0;
   launch_decode<DM_QKV>(M, g, ctx->stream);
   s = check_launch(ctx, "norm_qkv_rope");
   if (s) {

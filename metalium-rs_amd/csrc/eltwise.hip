@@ -656,9 +656,10 @@ __global__ void rope_kernel(const float *x, const float *cosp, const float *sinp
 
 // silu(gate) * up over the two halves of a fused gate|up product's rows,
 // gu [rows, 2 i] -> [rows, i], with SILU_MUL's arithmetic; four columns a
-// thread when i is a multiple of 4.
-template <bool VEC>
-__global__ void silu_mul_halves_kernel(const float *gu, float *out, int64_t rows, int64_t inner) {
+// thread when i is a multiple of 4.  TO: F32, or BF16 (the result rounded once
+// as stored, for a product that reads BF16 activations).
+template <bool VEC, typename TO>
+__global__ void silu_mul_halves_kernel(const float *gu, TO *out, int64_t rows, int64_t inner) {
   const int64_t per = VEC ? inner / 4 : inner, n = rows * per;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
@@ -671,9 +672,9 @@ __global__ void silu_mul_halves_kernel(const float *gu, float *out, int64_t rows
       y.y = op<MI_K_SILU_MUL>(g.y, u.y, 0.f, 0.f, 0.f);
       y.z = op<MI_K_SILU_MUL>(g.z, u.z, 0.f, 0.f, 0.f);
       y.w = op<MI_K_SILU_MUL>(g.w, u.w, 0.f, 0.f, 0.f);
-      *reinterpret_cast<float4 *>(out + r * inner + 4 * c) = y;
+      f32x4_put(out + r * inner + 4 * c, y);
     } else {
-      out[r * inner + c] = op<MI_K_SILU_MUL>(gu[r * 2 * inner + c], gu[r * 2 * inner + inner + c], 0.f, 0.f, 0.f);
+      f32_put(out + r * inner + c, op<MI_K_SILU_MUL>(gu[r * 2 * inner + c], gu[r * 2 * inner + inner + c], 0.f, 0.f, 0.f));
     }
   }
 }
@@ -684,9 +685,11 @@ __global__ void silu_mul_halves_kernel(const float *gu, float *out, int64_t rows
 // v written into the caches [batch * kv * maxc, d] at row (b kv + j) maxc +
 // pos0 + p, q written to row (b seq + p) heads + h (natural order) or, with
 // `grouped`, to row ((b kv + j) seq + p) G + g for head h = j G + g (the
-// queries regrouped per kv head, G = heads / kv).
-__global__ void qkv_rope_cache_kernel(const float *qkv, const float *cosp, const float *sinp, float *q, float *kc,
-                                      float *vc, int64_t rows, int64_t seq, int64_t heads, int64_t kv, int64_t d,
+// queries regrouped per kv head, G = heads / kv).  The caches are F32 or BF16
+// (KV; k and v rounded to nearest even as they are stored).
+template <typename KV>
+__global__ void qkv_rope_cache_kernel(const float *qkv, const float *cosp, const float *sinp, float *q, KV *kc,
+                                      KV *vc, int64_t rows, int64_t seq, int64_t heads, int64_t kv, int64_t d,
                                       int64_t maxc, int64_t pos0, int grouped) {
   const int64_t w = (heads + 2 * kv) * d, n = rows * w, half = d / 2, G = heads / kv;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -706,9 +709,9 @@ __global__ void qkv_rope_cache_kernel(const float *qkv, const float *cosp, const
       const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
       q[row * d + j] = y;
     } else if (h < heads + kv) {
-      kc[((b * kv + (h - heads)) * maxc + pos) * d + j] = y;
+      f32_put(kc + ((b * kv + (h - heads)) * maxc + pos) * d + j, y);
     } else {
-      vc[((b * kv + (h - heads - kv)) * maxc + pos) * d + j] = y;
+      f32_put(vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j, y);
     }
   }
 }
@@ -774,8 +777,9 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
 // partner at the same place in the other half).  The head, sequence and
 // position come from one small division per thread and one per block, not
 // four 64-bit divisions per element.
+template <typename KV>
 __global__ void __launch_bounds__(256) qkv_rope_cache_row_kernel(const float *qkv, const float *cosp,
-                                                                 const float *sinp, float *q, float *kc, float *vc,
+                                                                 const float *sinp, float *q, KV *kc, KV *vc,
                                                                  int64_t seq, int heads, int kv, int d, int64_t maxc,
                                                                  int64_t pos0, int grouped) {
   const int w = (heads + 2 * kv) * d, half = d / 2, G = heads / kv;
@@ -794,38 +798,47 @@ __global__ void __launch_bounds__(256) qkv_rope_cache_row_kernel(const float *qk
       y.z = __fadd_rn(__fmul_rn(y.z, cv.z), __fmul_rn(rv.z, sv.z));
       y.w = __fadd_rn(__fmul_rn(y.w, cv.w), __fmul_rn(rv.w, sv.w));
     }
-    float *dst;
     if (h < heads) {
       const int kvh = h / G, g = h - kvh * G;
       const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
-      dst = q + row * d + j;
+      *reinterpret_cast<float4 *>(q + row * d + j) = y;
     } else if (h < heads + kv) {
-      dst = kc + ((b * kv + (h - heads)) * maxc + pos) * d + j;
+      f32x4_put(kc + ((b * kv + (h - heads)) * maxc + pos) * d + j, y);
     } else {
-      dst = vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j;
+      f32x4_put(vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j, y);
     }
-    *reinterpret_cast<float4 *>(dst) = y;
   }
 }
 
-extern "C" int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, mi_id *out) {
+extern "C" int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, gb, gate_up);
   if (gb->elem != MI_F32 || gb->cols % 2)
     return fail(ctx, MI_E_ARG, "silu_mul_halves of %s [%lld, %lld]: want F32 with an even width", elem_name(gb->elem),
                 (long long)gb->rows, (long long)gb->cols);
+  if (out_elem != MI_F32 && out_elem != MI_BF16)
+    return fail(ctx, MI_E_ARG, "silu_mul_halves result kind %s", elem_name(out_elem));
   const int64_t R = gb->rows, I = gb->cols / 2;
   mi_id id; Buffer *ob;
-  int s = new_buffer(ctx, R, I, MI_F32, &id, &ob);
+  int s = new_buffer(ctx, R, I, out_elem, &id, &ob);
   if (s) return s;
   if (R * I > 0) {
     const float *gp = static_cast<const float *>(gb->ptr);
-    float *op_ = static_cast<float *>(ob->ptr);
-    if (I % 4 == 0)
-      silu_mul_halves_kernel<true><<<grid_for(R * I / 4, 256 * 2, 256 * 128), 256, 0, ctx->stream>>>(gp, op_, R, I);
-    else
-      silu_mul_halves_kernel<false><<<grid_for(R * I, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(gp, op_, R, I);
+    const unsigned gv = grid_for(R * I / 4, 256 * 2, 256 * 128), gs = grid_for(R * I, 256 * 4, 256 * 64);
+    if (out_elem == MI_BF16) {
+      uint16_t *op_ = static_cast<uint16_t *>(ob->ptr);
+      if (I % 4 == 0)
+        silu_mul_halves_kernel<true, uint16_t><<<gv, 256, 0, ctx->stream>>>(gp, op_, R, I);
+      else
+        silu_mul_halves_kernel<false, uint16_t><<<gs, 256, 0, ctx->stream>>>(gp, op_, R, I);
+    } else {
+      float *op_ = static_cast<float *>(ob->ptr);
+      if (I % 4 == 0)
+        silu_mul_halves_kernel<true, float><<<gv, 256, 0, ctx->stream>>>(gp, op_, R, I);
+      else
+        silu_mul_halves_kernel<false, float><<<gs, 256, 0, ctx->stream>>>(gp, op_, R, I);
+    }
     s = check_launch(ctx, "silu_mul_halves");
     if (s) { mi_free(ctx, id); return s; }
   }
@@ -843,8 +856,9 @@ extern "C" int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id 
   MI_BUF(ctx, sb, sin_table);
   MI_BUF(ctx, kb, k_cache);
   MI_BUF(ctx, vb, v_cache);
-  if (xb->elem != MI_F32 || cb->elem != MI_F32 || sb->elem != MI_F32 || kb->elem != MI_F32 || vb->elem != MI_F32)
-    return fail(ctx, MI_E_ARG, "qkv_rope_cache takes F32");
+  if (xb->elem != MI_F32 || cb->elem != MI_F32 || sb->elem != MI_F32 || kb->elem != vb->elem ||
+      !elem_float(kb->elem))
+    return fail(ctx, MI_E_ARG, "qkv_rope_cache takes F32 rows and tables and two F32 or two BF16 caches");
   const int64_t D = kb->cols, R = xb->rows;
   if (heads < 1 || kv_heads < 1 || heads % kv_heads || D < 2 || D % 2)
     return fail(ctx, MI_E_ARG, "qkv_rope_cache: %lld heads over %lld kv heads of width %lld", (long long)heads,
@@ -870,18 +884,33 @@ extern "C" int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id 
   const bool aligned = (reinterpret_cast<uintptr_t>(xb->ptr) | reinterpret_cast<uintptr_t>(ob->ptr) |
                         reinterpret_cast<uintptr_t>(kb->ptr) | reinterpret_cast<uintptr_t>(vb->ptr) |
                         reinterpret_cast<uintptr_t>(cb->ptr) | reinterpret_cast<uintptr_t>(sb->ptr)) % 16 == 0;
+  const float *xp = static_cast<const float *>(xb->ptr), *cp = static_cast<const float *>(cb->ptr),
+              *sp = static_cast<const float *>(sb->ptr);
+  float *qp = static_cast<float *>(ob->ptr);
+  const bool kv16 = kb->elem == MI_BF16;
   if (R > 0 && D % 8 == 0 && aligned && R <= INT32_MAX && xb->cols <= INT32_MAX) {
-    qkv_rope_cache_row_kernel<<<static_cast<unsigned>(R), 256, 0, ctx->stream>>>(
-        static_cast<const float *>(xb->ptr), static_cast<const float *>(cb->ptr), static_cast<const float *>(sb->ptr),
-        static_cast<float *>(ob->ptr), static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), seq,
-        static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(D), maxc, pos0, grouped ? 1 : 0);
+    const unsigned grid = static_cast<unsigned>(R);
+    const int hi = static_cast<int>(heads), kvi = static_cast<int>(kv_heads), di = static_cast<int>(D);
+    if (kv16)
+      qkv_rope_cache_row_kernel<uint16_t><<<grid, 256, 0, ctx->stream>>>(
+          xp, cp, sp, qp, static_cast<uint16_t *>(kb->ptr), static_cast<uint16_t *>(vb->ptr), seq, hi, kvi, di, maxc,
+          pos0, grouped ? 1 : 0);
+    else
+      qkv_rope_cache_row_kernel<float><<<grid, 256, 0, ctx->stream>>>(
+          xp, cp, sp, qp, static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), seq, hi, kvi, di, maxc, pos0,
+          grouped ? 1 : 0);
     s = check_launch(ctx, "qkv_rope_cache");
     if (s) { mi_free(ctx, id); return s; }
   } else if (R > 0) {
-    qkv_rope_cache_kernel<<<grid_for(R * xb->cols, 256 * 4, 256 * 64), 256, 0, ctx->stream>>>(
-        static_cast<const float *>(xb->ptr), static_cast<const float *>(cb->ptr), static_cast<const float *>(sb->ptr),
-        static_cast<float *>(ob->ptr), static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), R, seq, heads,
-        kv_heads, D, maxc, pos0, grouped ? 1 : 0);
+    const unsigned grid = grid_for(R * xb->cols, 256 * 4, 256 * 64);
+    if (kv16)
+      qkv_rope_cache_kernel<uint16_t><<<grid, 256, 0, ctx->stream>>>(
+          xp, cp, sp, qp, static_cast<uint16_t *>(kb->ptr), static_cast<uint16_t *>(vb->ptr), R, seq, heads, kv_heads,
+          D, maxc, pos0, grouped ? 1 : 0);
+    else
+      qkv_rope_cache_kernel<float><<<grid, 256, 0, ctx->stream>>>(
+          xp, cp, sp, qp, static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), R, seq, heads, kv_heads, D,
+          maxc, pos0, grouped ? 1 : 0);
     s = check_launch(ctx, "qkv_rope_cache");
     if (s) { mi_free(ctx, id); return s; }
   }

@@ -15,7 +15,9 @@
 // step of at most 32 sequences runs six fused launches a layer -- RMSNorm +
 // q|k|v + RoPE + cache write, attention (two), o + residual, RMSNorm +
 // gate|up + SiLU-mul, down + residual.  The KV cache of a layer is
-// F32 [batch * kv_heads * max_ctx, head_dim], item (sequence, kv head), so the
+// [batch * kv_heads * max_ctx, head_dim], item (sequence, kv head), F32 under
+// the reference numeric contract and BF16 under the performance one (which
+// also rounds a prefill product's activation operand to BF16), so the
 // attention of a query group is one product over a block of the cache:
 // queries regrouped to [batch * kv_heads, t * group, head_dim] (row
 // t * group + g) multiply the first ctx rows of their cache item.
@@ -95,6 +97,8 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   const int64_t pos0 = m->len, ctxlen = pos0 + t, maxc = c.max_ctx;
   const int64_t rows = batch * t;
 
+  // The element type of a prefill product's activation operand.
+  const int act = c.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
   Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
   x = x.reshape({rows, c.hidden});
 
@@ -132,7 +136,7 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
     return x;
   }
   for (Layer &L : m->layers) {
-    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps);
+    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps, act);
     // One product against the fused q|k|v weight, then RoPE on q and k, k and
     // v appended to the caches at positions pos0.. of each (sequence, kv head)
     // item, and q laid out for the attention, in one launch: rows (sequence,
@@ -157,10 +161,11 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
         oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
       }
     }
+    if (act != MI_F32) oh = burn::float_cast(oh, act);
     x = burn::linear(oh, L.wo, true, nullptr, &x);  // x + oh wo^T, the add in the product's epilogue
-    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps);
+    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps, act);
     // One product against the fused gate|up weight, silu(gate) * up of its halves.
-    Tensor h = burn::silu_mul_halves(burn::float_matmul(hn, false, L.wgu, true));
+    Tensor h = burn::silu_mul_halves(burn::float_matmul(hn, false, L.wgu, true), act);
     x = burn::linear(h, L.wdown, true, nullptr, &x);
   }
   m->len = ctxlen;
@@ -181,20 +186,26 @@ Tensor head_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
   const int64_t dims[4] = {1, 1, batch, c.hidden};
   const int64_t st[4] = {0, 0, t * c.hidden, 1};
   Tensor last = burn::copy4(hidden, dims, (t - 1) * c.hidden, st);
-  return burn::float_matmul(burn::rms_norm(last, m->final_norm, c.eps), false, m->embed, true);
+  const int act = c.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
+  return burn::float_matmul(burn::rms_norm(last, m->final_norm, c.eps, act), false, m->embed, true);
 }
 
 // Every position's logits: [batch * t, vocab].
 Tensor head_all(mi_llama *m, const Tensor &hidden) {
-  return burn::float_matmul(burn::rms_norm(hidden, m->final_norm, m->cfg.eps), false, m->embed, true);
+  const int act = m->cfg.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
+  return burn::float_matmul(burn::rms_norm(hidden, m->final_norm, m->cfg.eps, act), false, m->embed, true);
 }
 
 void ensure_cache(mi_llama *m, int64_t batch) {
   if (m->len == 0 && m->cache_batch != batch) {
     const mi_llama_config &c = m->cfg;
+    const int kv = c.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
     for (Layer &L : m->layers) {
-      L.cache_k = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, MI_F32, 0);
-      L.cache_v = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, MI_F32, 0);
+      // The old caches go before the new ones are made, so their memory is reused.
+      L.cache_k = Tensor();
+      L.cache_v = Tensor();
+      L.cache_k = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, kv, 0);
+      L.cache_v = burn::fill(m->ctx, {batch * c.kv_heads * c.max_ctx, c.head_dim}, kv, 0);
     }
     m->cache_batch = batch;
   }
@@ -211,7 +222,7 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
   if (!ctx || !cfg || !out) return MI_E_ARG;
   const mi_llama_config &c = *cfg;
   if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 2 || c.layers < 0 || c.max_ctx <= 0 ||
-      c.max_batch <= 0) {
+      c.max_batch <= 0 || (c.numerics != MI_NUMERICS_REFERENCE && c.numerics != MI_NUMERICS_PERFORMANCE)) {
     g_model_error = "invalid llama config";
     return MI_E_ARG;
   }

@@ -114,7 +114,7 @@ def _load() -> ctypes.CDLL:
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_qkv_rope_cache": [P, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
-        "mi_silu_mul_halves": [P, U64, Ip],
+        "mi_silu_mul_halves": [P, U64, c_int, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
         "mi_reduce": [P, U64, c_int, c_int, Ip],
         "mi_reduce_all": [P, U64, c_int, Ip],
@@ -325,9 +325,9 @@ class Engine:
         """Fused decode projection: residual + rmsnorm(x) w^T, or silu(g) * u."""
         return self._out(self._lib.mi_norm_matvec, x, gamma, eps, w, residual, int(silu_mul))
 
-    def silu_mul_halves(self, gate_up: int) -> int:
-        """silu(gate) * up over the two column halves of a fused gate|up product."""
-        return self._out(self._lib.mi_silu_mul_halves, gate_up)
+    def silu_mul_halves(self, gate_up: int, out_elem: int = F32) -> int:
+        """silu(gate) * up over the two column halves of a fused gate|up product (F32, or rounded to BF16)."""
+        return self._out(self._lib.mi_silu_mul_halves, gate_up, out_elem)
 
     def qkv_rope_cache(self, qkv: int, cos: int, sin: int, seq: int, heads: int, kv_heads: int, pos0: int,
                        k_cache: int, v_cache: int, grouped: bool = False) -> int:
@@ -531,7 +531,11 @@ class LlamaConfig(ctypes.Structure):
     _fields_ = [("vocab", ctypes.c_int32), ("hidden", ctypes.c_int32), ("layers", ctypes.c_int32),
                 ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("intermediate", ctypes.c_int32), ("rope_theta", ctypes.c_float), ("eps", ctypes.c_float),
-                ("max_ctx", ctypes.c_int32), ("max_batch", ctypes.c_int32)]
+                ("max_ctx", ctypes.c_int32), ("max_batch", ctypes.c_int32), ("numerics", ctypes.c_int32)]
+
+
+# Numeric contracts (include/miburn_models.h MI_NUMERICS_*; the reference's burn_tt::Numerics).
+NUMERICS = {"reference": 0, "performance": 1}
 
 
 # SmolLM2-135M's shape (crates/tt-models/src/llama.rs:60-71).
@@ -566,13 +570,15 @@ def _models_lib():
 class Llama:
     """The SmolLM2-shaped decoder harness (crates/tt-models/src/llama.rs) on an Engine."""
 
-    def __init__(self, eng: Engine, cfg: dict, max_ctx: int, max_batch: int, seed: int = 0, init_std: float = 0.02):
+    def __init__(self, eng: Engine, cfg: dict, max_ctx: int, max_batch: int, seed: int = 0, init_std: float = 0.02,
+                 numerics: str = "reference"):
         self.eng = eng
         self.L = _models_lib()
         c = LlamaConfig(**{k: cfg[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "head_dim",
                                                "intermediate")},
-                        rope_theta=cfg["rope_theta"], eps=cfg["eps"], max_ctx=max_ctx, max_batch=max_batch)
-        self.cfg = dict(cfg, max_ctx=max_ctx, max_batch=max_batch)
+                        rope_theta=cfg["rope_theta"], eps=cfg["eps"], max_ctx=max_ctx, max_batch=max_batch,
+                        numerics=NUMERICS[numerics])
+        self.cfg = dict(cfg, max_ctx=max_ctx, max_batch=max_batch, numerics=numerics)
         h = ctypes.c_void_p()
         self._check(self.L.mi_llama_create(eng.ctx, ctypes.byref(c), seed, init_std, ctypes.byref(h)))
         self.h = h

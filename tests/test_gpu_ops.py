@@ -714,10 +714,12 @@ def test_pick_and_scatter_add_columns(engine):
     same_bits(got, orc.scatter_add_columns(xf, idx, v))
 
 
-def test_select_add_rows_duplicates_in_order(engine):
-    V, D, n = 300, 64, 2048
+@pytest.mark.parametrize("V,D,n,hot", [(300, 64, 2048, 40),  # one-block sort
+                                       (49152, 64, 20000, 49152),  # library radix sort above 8192 ids
+                                       (1000, 576, 9000, 30)])
+def test_select_add_rows_duplicates_in_order(engine, V, D, n, hot):
     t = rnd(V, D)
-    idx = RNG.integers(0, 40, n).astype(np.int32)  # many duplicates
+    idx = RNG.integers(0, hot, n).astype(np.int32)  # duplicates (many when hot is small)
     val = rnd(n, D)
     got = engine.download(engine.select_add_rows(engine.upload(t), engine.upload_i32(idx), engine.upload(val)))
     same_bits(got, orc.select_add_rows(t, idx, val))
@@ -799,6 +801,37 @@ def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("batch,t,heads,kvh,D,pos0,maxc", [
+    (1, 1, 9, 3, 64, 639, 640),      # decode, many key chunks
+    (32, 1, 9, 3, 64, 200, 640),     # batch 32 decode
+    (2, 5, 4, 2, 16, 7, 64),         # 16-wide heads
+    (3, 16, 8, 1, 128, 30, 64),      # 128-wide heads, 8 a group
+    (1, 512, 9, 3, 64, 0, 640),      # a 512-token prompt at batch 1
+    (32, 96, 9, 3, 64, 32, 160),     # the matrix-core (flash) kernel
+    (40, 70, 8, 1, 64, 5, 80),       # flash, a partial last query block
+])
+def test_attention_rows_bf16_caches(engine, batch, t, heads, kvh, D, pos0, maxc):
+    # The performance contract's BF16 caches: widened exactly as loaded, so
+    # the float64 reference on the BF16 values holds to the F32 bound.
+    q = rnd(batch * t, heads * D)
+    kb = orc.to_bf16(rnd(batch * kvh * maxc, D))
+    vb = orc.to_bf16(rnd(batch * kvh * maxc, D))
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    got = engine.download(engine.attention_rows(engine.upload(q), engine.upload_bf16(kb), engine.upload_bf16(vb),
+                                                batch, t, heads, kvh, pos0, scale))
+    want = attention_ref(q, orc.from_bf16(kb), orc.from_bf16(vb), batch, t, heads, kvh, pos0, scale)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
+
+
+def test_attention_rows_mixed_caches_refused(engine):
+    q = engine.upload(rnd(1, 2 * 64))
+    kf = engine.upload(rnd(8, 64))
+    kb = engine.upload_bf16(orc.to_bf16(rnd(8, 64)))
+    with pytest.raises(miburn.MiError) as e:
+        engine.attention_rows(q, kf, kb, 1, 1, 2, 1, 0, 0.125)
+    assert e.value.kind == "ARG"
+
+
 # ------------------------------------------------------ fused decode projections
 def decode_inputs(M, K, N):
     x = rnd(M, K)
@@ -877,6 +910,29 @@ def test_norm_qkv_rope_writes_cache(engine, M):
     keep[pos] = False
     assert np.array_equal(kc1[:, :, keep], kc0.reshape(M, KVH, maxc, D)[:, :, keep])
     assert np.array_equal(vc1[:, :, keep], vc0.reshape(M, KVH, maxc, D)[:, :, keep])
+
+
+@pytest.mark.parametrize("M", [1, 5, 32])
+def test_norm_qkv_rope_bf16_caches(engine, M):
+    # The same kernel into BF16 caches: q unchanged, the new cache row the F32
+    # form's rounded to nearest even, every other row untouched.
+    H, KVH, D, K, maxc, pos, eps = 9, 3, 64, 576, 40, 17, 1e-5
+    x, g, wb = decode_inputs(M, K, (H + 2 * KVH) * D)
+    cos, sin = rnd(maxc, D), rnd(maxc, D)
+    kc0 = orc.to_bf16(rnd(M * KVH * maxc, D))
+    vc0 = orc.to_bf16(rnd(M * KVH * maxc, D))
+    args = (engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb), engine.upload(cos), engine.upload(sin),
+            H, KVH, pos)
+    kf, vf = engine.upload(orc.from_bf16(kc0)), engine.upload(orc.from_bf16(vc0))
+    kb, vb = engine.upload_bf16(kc0), engine.upload_bf16(vc0)
+    qf = engine.download(engine.norm_qkv_rope(*args, kf, vf))
+    qb = engine.download(engine.norm_qkv_rope(*args, kb, vb))
+    same_bits(qb, qf)
+    assert np.array_equal(engine.download(kb), orc.to_bf16(engine.download(kf)))
+    assert np.array_equal(engine.download(vb), orc.to_bf16(engine.download(vf)))
+    with pytest.raises(miburn.MiError) as e:
+        engine.norm_qkv_rope(*args, kb, vf)
+    assert e.value.kind == "ARG"
 
 
 def test_decode_projection_errors(engine):

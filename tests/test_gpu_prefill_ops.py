@@ -18,11 +18,17 @@ positions left as it was.
 
 mi_silu_mul_halves: bit-identical to MI_K_SILU_MUL of the two halves, on the
 vector and the scalar paths.
+
+BF16 storage (the performance numeric contract's KV cache and activation
+operands): mi_qkv_rope_cache into BF16 caches writes exactly the F32 form's
+values rounded to nearest even (the oracle's pinned cast) and the same q;
+mi_silu_mul_halves to BF16 is its F32 result so rounded.
 """
 import numpy as np
 import pytest
 
 import miburn
+import oracle_lib as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -137,6 +143,27 @@ def test_qkv_rope_cache_equals_composition(engine, batch, seq, heads, kv, d, pos
     same_bits(kk[:, keep], kc0.reshape(batch * kv, maxc, d)[:, keep])
 
 
+@pytest.mark.parametrize("batch,seq,heads,kv,d,pos0,maxc", [(2, 5, 9, 3, 64, 3, 16), (1, 70, 9, 3, 64, 0, 80),
+                                                           (2, 3, 2, 1, 12, 1, 8)])
+def test_qkv_rope_cache_bf16_caches(engine, batch, seq, heads, kv, d, pos0, maxc):
+    rows, w = batch * seq, (heads + 2 * kv) * d
+    iq = engine.upload(rnd(rows, w))
+    cos, sin = rope_tables(maxc, d)
+    ic, isn = engine.upload(cos), engine.upload(sin)
+    kc0, vc0 = orc.to_bf16(rnd(batch * kv * maxc, d)), orc.to_bf16(rnd(batch * kv * maxc, d))
+    kf, vf = engine.upload(orc.from_bf16(kc0)), engine.upload(orc.from_bf16(vc0))
+    kb, vb = engine.upload_bf16(kc0), engine.upload_bf16(vc0)
+    for grouped in (False, True):
+        qf = engine.download(engine.qkv_rope_cache(iq, ic, isn, seq, heads, kv, pos0, kf, vf, grouped=grouped))
+        qb = engine.download(engine.qkv_rope_cache(iq, ic, isn, seq, heads, kv, pos0, kb, vb, grouped=grouped))
+        same_bits(qb, qf)
+    assert np.array_equal(engine.download(kb), orc.to_bf16(engine.download(kf)))
+    assert np.array_equal(engine.download(vb), orc.to_bf16(engine.download(vf)))
+    with pytest.raises(miburn.MiError) as e:  # one cache of each kind
+        engine.qkv_rope_cache(iq, ic, isn, seq, heads, kv, pos0, kf, vb)
+    assert e.value.kind == "ARG"
+
+
 def test_qkv_rope_cache_argument_errors(engine):
     cos, sin = rope_tables(8, 16)
     ic, isn = engine.upload(cos), engine.upload(sin)
@@ -158,5 +185,9 @@ def test_silu_mul_halves_equals_silu_mul(engine, rows, inner):
     got = engine.download(engine.silu_mul_halves(engine.upload(gu)))
     g, u = engine.upload(np.ascontiguousarray(gu[:, :inner])), engine.upload(np.ascontiguousarray(gu[:, inner:]))
     same_bits(got, engine.download(engine.eltwise_op_as("SILU_MUL", g, u)))
+    got16 = engine.download(engine.silu_mul_halves(engine.upload(gu), miburn.BF16))
+    assert got16.dtype == np.uint16 and np.array_equal(got16, orc.to_bf16(got))
     with pytest.raises(miburn.MiError):
         engine.silu_mul_halves(engine.upload(rnd(2, 5)))  # odd width
+    with pytest.raises(miburn.MiError):
+        engine.silu_mul_halves(engine.upload(gu), miburn.I32)
