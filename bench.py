@@ -248,14 +248,22 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     BF16 weights), prefill `prompt` random tokens per sequence, then greedy
     decode `new` tokens; tokens/s of the prefill and of the decode steps.
     `numerics`: the reference contract (F32 KV cache and activations) or the
-    performance one (BF16 KV cache, BF16 prefill activation operands)."""
+    performance one (BF16 KV cache, BF16 prefill activation operands).  The
+    generation runs eagerly, then traced (each decode step a replay of a step
+    captured per 64-position span, token ids in and out through the host:
+    the reference's TracedGenerator); the traced run's steps are captured by
+    an untimed first traced generation and must give the eager tokens."""
     import miburn
     m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt + new, max_batch=batch, seed=5, numerics=numerics)
     rng = np.random.default_rng(9)
     ids = rng.integers(0, 49152, (batch, prompt)).astype(np.int32)
     m.generate(ids[:, :32], 4)  # warm the kernels
     out, pf_ms, dc_ms = m.generate(ids, new)
+    m.generate(ids, new, traced=True)  # captures every span's step
+    tr_out, _, tr_ms = m.generate(ids, new, traced=True)
     m.close()
+    if not np.array_equal(tr_out, out):
+        raise RuntimeError("traced generation's tokens differ from the eager loop's")
     # Rooflines (algorithmic work): a decode step reads every BF16 weight once
     # (134.48 M parameters, the tied table included) plus each sequence's
     # key/value cache (2 x 30 layers x 3 kv heads x 64 x 4 B a position for
@@ -279,6 +287,7 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
             "prefill_gflop": round(pf_flop / 1e9, 1),
             "prefill_mfma_frac": round(pf_flop / (pf_ms * 1e-3) / (PEAK_TFLOPS["bf16"] * 1e12), 4),
             "decode_ms_per_step": round(dc_step_ms, 3),
+            "decode_traced_ms_per_step": round(tr_ms / max(new - 1, 1), 3),
             "decode_tokens_per_s": round(batch * (new - 1) / (dc_ms / 1e3), 1),
             "decode_hbm_mb_per_step": round(step_bytes / 1e6, 1),
             "decode_hbm_frac": round(step_bytes / (dc_step_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}

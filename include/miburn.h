@@ -371,7 +371,9 @@ int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table,
  * attention.rs:1-20; the composition of crates/burn-tt/src/ops.rs:4520-4595):
  * causal grouped-query attention of `t` new positions per sequence against a
  * KV cache.  q: [batch * t, heads * d] F32, rows (sequence, position), head h
- * reading kv head h / (heads / kv_heads).  k_cache, v_cache: F32
+ * reading kv head h / (heads / kv_heads).  k_cache, v_cache: both F32 or
+ * both BF16 (the performance contract's cache, crates/tt-models/src/
+ * llama.rs:1276-1278; widened exactly, F32 arithmetic either way)
  * [batch * kv_heads * max_ctx, d], item (sequence, kv head), the new
  * positions already written at pos0 .. pos0 + t - 1.  Query position p sees
  * cache positions 0 .. pos0 + p.  out: [batch * t, heads * d] =
@@ -381,6 +383,22 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
                       int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, int64_t pos0, float scale,
                       mi_id *out);
+/* mi_attention_rows for a traced decode step, whose positions are device
+ * data (the reference's position tensors and its step traced per attended
+ * length, crates/tt-models/src/generate.rs:1-22, 770-790): pos0 read on the
+ * device from `pos` ([1, 1] I32) when `pos` is nonzero, else the immediate
+ * pos0; the key chunks planned for `span` positions (pos0 + t <= span <=
+ * max_ctx), so every call with one span runs the same launches whatever the
+ * position and a graph captured once replays at any position of its span.
+ * The same results as mi_attention_rows up to the order of the chunk sums,
+ * and bit for bit the same between an immediate and a device pos0 of one
+ * value and span.  A device pos0 with pos0 < 0 or pos0 + t > span attends
+ * from position 0 and raises MI_E_DOMAIN at the next wait.  The prompt's
+ * matrix-core kernel is not used. */
+int mi_attention_rows_at(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
+                         int64_t batch, int64_t t, int64_t heads,
+                         int64_t kv_heads, mi_id pos, int64_t pos0,
+                         int64_t span, float scale, mi_id *out);
 /* mi_attention_rows writing into an existing F32 `[batch * t, heads * d]`
  * buffer `out` (not one of the inputs), with no allocation of any kind: no
  * device or host memory is allocated, freed or grown, so callers that cannot
@@ -411,12 +429,22 @@ int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w,
                    mi_id residual, int silu_mul, mi_id *out);
 /* w_qkv = [wq; wk; wv] ([(heads + 2 kv_heads) * d, K]): q = rope(rmsnorm(x)
  * wq^T) returned [M, heads * d]; k = rope(.. wk^T) and v = .. wv^T written
- * into the caches ([M * kv_heads * max_ctx, d] F32, item (row, kv head)) at
+ * into the caches ([M * kv_heads * max_ctx, d], both F32 or both BF16
+ * (rounded to nearest even), item (row, kv head)) at
  * position `pos`; the rotary tables as mi_rope's, read at row `pos`. */
 int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
                      mi_id w_qkv, mi_id cos_table, mi_id sin_table,
                      int64_t heads, int64_t kv_heads, int64_t pos,
                      mi_id k_cache, mi_id v_cache, mi_id *q_out);
+/* mi_norm_qkv_rope with the position read on the device from `pos` ([1, 1]
+ * I32; a traced decode step's input, as mi_attention_rows_at's), the rotary
+ * tables covering every position below max_ctx.  Bit for bit
+ * mi_norm_qkv_rope at the position's value; a position outside [0, max_ctx)
+ * writes no cache row and no q and raises MI_E_DOMAIN at the next wait. */
+int mi_norm_qkv_rope_at(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
+                        mi_id w_qkv, mi_id cos_table, mi_id sin_table,
+                        int64_t heads, int64_t kv_heads, mi_id pos,
+                        mi_id k_cache, mi_id v_cache, mi_id *q_out);
 /* silu(gate) * up over the halves of a fused gate|up product: gate_up
  * [rows, 2 i] F32 -> [rows, i] of out_elem (the reference's MLP, crates/
  * tt-models/src/llama.rs:494-498, on the two row blocks of its gate|up

@@ -42,6 +42,26 @@ constexpr int64_t ATT_MIN_CHUNK = 64;
 constexpr int64_t ATT_TARGET_BLOCKS = 512;
 constexpr int ATT_WAVES = 4;  // wavefronts per chunk block
 
+// The first new position of the queries: an immediate value, or (a traced
+// decode step's) read from the device, where it must keep pos0 + T <= span
+// (the positions the key chunks were planned for, at most the cache's);
+// outside that the rows attend from position 0 -- every read stays in the
+// cache -- and the range flag is raised for the next wait.
+struct AttPos {
+  int64_t pos0;
+  const int32_t *dev;
+  int64_t span;
+  uint32_t *flags;
+};
+
+__device__ __forceinline__ int64_t att_pos0(const AttPos &pa, int64_t T) {
+  if (!pa.dev) return pa.pos0;
+  const int64_t v = *pa.dev;
+  const bool ok = v >= 0 && v + T <= pa.span;
+  if (!ok && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0) atomicOr(pa.flags, FLAG_INDEX_RANGE);
+  return ok ? v : 0;
+}
+
 // scores[g] = q[g] . k for one key row per lane group, folded over the row's
 // D/4 lanes.
 template <int G, int LPR>
@@ -59,7 +79,7 @@ __device__ __forceinline__ void dots(const float4 (&qv)[G], float4 kv, float (&p
 template <int D, int G, int NW, typename KV>
 __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q, const KV *kc, const KV *vc,
                                                               float *out, float *part, int64_t T, int64_t H,
-                                                              int64_t KVH, int64_t pos0, int64_t maxc, int64_t chunk,
+                                                              int64_t KVH, AttPos pa, int64_t maxc, int64_t chunk,
                                                               float scale, int direct) {
   constexpr int LPR = D / 4;     // lanes per row
   constexpr int KPW = 64 / LPR;  // rows per wavefront access
@@ -71,7 +91,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
   const int64_t item = blockIdx.x;  // (sequence, kv head, position), position fastest
   const int64_t p = item % T, bj = item / T;
   const int64_t j = bj % KVH, b = bj / KVH;
-  const int64_t n = pos0 + p + 1;  // causal: cache positions 0 .. pos0 + p
+  const int64_t n = att_pos0(pa, T) + p + 1;  // causal: cache positions 0 .. pos0 + p
   const int64_t lo = static_cast<int64_t>(s) * chunk;
   const int64_t len = n > lo ? (n - lo < chunk ? n - lo : chunk) : 0;
   const KV *K = kc + ((bj)*maxc + lo) * D;
@@ -461,11 +481,11 @@ inline size_t attention_smem(int64_t G, int64_t D, int64_t chunk, int nw) {
 
 template <int D, int G, typename KV>
 void launch_attention(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, float *part,
-                      int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc,
+                      int64_t items, int S, int64_t T, int64_t H, int64_t KVH, const AttPos &pa, int64_t maxc,
                       int64_t chunk, float scale) {
   const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(S));
   const size_t smem = attention_smem(G, D, chunk, ATT_WAVES);
-  attention_chunk_kernel<D, G, ATT_WAVES, KV><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pos0, maxc,
+  attention_chunk_kernel<D, G, ATT_WAVES, KV><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pa, maxc,
                                                                             chunk, scale, S == 1);
   if (S > 1)
     attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, static_cast<size_t>(3 * G * S + G) * sizeof(float),
@@ -474,12 +494,12 @@ void launch_attention(hipStream_t st, const float *q, const KV *k, const KV *v, 
 
 template <int D, typename KV>
 bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, float *out,
-                    float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, int64_t pos0,
+                    float *part, int64_t items, int S, int64_t T, int64_t H, int64_t KVH, const AttPos &pa,
                     int64_t maxc, int64_t chunk, float scale) {
   switch (G) {
 #define MI_ATT_G(g)                                                                                   \
   case g:                                                                                             \
-    launch_attention<D, g, KV>(st, q, k, v, out, part, items, S, T, H, KVH, pos0, maxc, chunk, scale); \
+    launch_attention<D, g, KV>(st, q, k, v, out, part, items, S, T, H, KVH, pa, maxc, chunk, scale); \
     return true;
     MI_ATT_G(1) MI_ATT_G(2) MI_ATT_G(3) MI_ATT_G(4) MI_ATT_G(5) MI_ATT_G(6) MI_ATT_G(7) MI_ATT_G(8)
 #undef MI_ATT_G
@@ -537,10 +557,13 @@ struct AttPlan {
   int64_t D, G, maxc, items, S, chunk;
   size_t part_bytes;
   bool flash;  // many new positions: the matrix-core kernel, no chunk partials
+  AttPos pos;
 };
 
+// pos_dev null: the immediate pos0, chunks planned for span = pos0 + t when
+// span is 0.  pos_dev set: pos0 read on the device, chunks for `span`.
 int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t, int64_t heads,
-                   int64_t kv_heads, int64_t pos0, AttPlan *P) {
+                   int64_t kv_heads, int64_t pos0, const int32_t *pos_dev, int64_t span, AttPlan *P) {
   MI_BUF(ctx, qb, q);
   MI_BUF(ctx, kb, k_cache);
   MI_BUF(ctx, vb, v_cache);
@@ -562,16 +585,26 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   if (vb->cols != D || vb->rows != kb->rows || kb->rows % (batch * kv_heads))
     return fail(ctx, MI_E_ARG, "attention_rows: caches must both be [batch * kv_heads * max_ctx, %lld]", (long long)D);
   const int64_t maxc = kb->rows / (batch * kv_heads);
-  if (pos0 < 0 || pos0 + t > maxc)
-    return fail(ctx, MI_E_ARG, "attention_rows: positions %lld..%lld beyond the cache's %lld", (long long)pos0,
-                (long long)(pos0 + t), (long long)maxc);
+  if (pos_dev) {
+    if (span < t || span > maxc)
+      return fail(ctx, MI_E_ARG, "attention_rows: span %lld for %lld new positions in a cache of %lld", (long long)span,
+                  (long long)t, (long long)maxc);
+  } else {
+    if (pos0 < 0 || pos0 + t > maxc)
+      return fail(ctx, MI_E_ARG, "attention_rows: positions %lld..%lld beyond the cache's %lld", (long long)pos0,
+                  (long long)(pos0 + t), (long long)maxc);
+    if (span == 0) span = pos0 + t;
+    if (span < pos0 + t || span > maxc)
+      return fail(ctx, MI_E_ARG, "attention_rows: span %lld for positions %lld..%lld in a cache of %lld",
+                  (long long)span, (long long)pos0, (long long)(pos0 + t), (long long)maxc);
+  }
   // Chunks: at least enough that none exceeds ATT_MAX_CHUNK keys, more (down
   // to ATT_MIN_CHUNK keys each) until the grid has ATT_TARGET_BLOCKS blocks --
   // decode has only batch * kv_heads query groups, and one block's chain of
   // dependent loads over a long context is slower than several short chains
   // and a combine pass.  Chunks are a multiple of 4 keys, so the LDS fold area
   // after the scores stays 16-byte aligned for its float4 stores.
-  const int64_t items = batch * kv_heads * t, nmax = pos0 + t;
+  const int64_t items = batch * kv_heads * t, nmax = span;
   int64_t S = (nmax + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
   const int64_t want = (ATT_TARGET_BLOCKS + items - 1) / items;
   // With many items (a batch of sequences) longer chunks: fewer blocks and
@@ -594,35 +627,59 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   // The matrix-core kernel once its (32 positions, sequence, kv head) blocks
   // fill the chip; fewer sequences keep the key-chunked kernel (a 512-token
   // prompt at batch 1: 48 blocks, slower than 30 key chunks a position).
-  P->flash = D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535 &&
+  P->flash = !pos_dev && span == pos0 + t && D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535 &&
              (t + 31) / 32 * batch * kv_heads >= FLASH_MIN_BLOCKS;
+  P->pos = AttPos{pos0, pos_dev, span, flags(ctx)};
   P->part_bytes = S > 1 && !P->flash ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
   return MI_OK;
 }
 
 template <typename KV>
 void attention_launch_kv(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t,
-                         int64_t heads, int64_t kv_heads, int64_t pos0, float scale) {
+                         int64_t heads, int64_t kv_heads, float scale) {
   const KV *k = static_cast<const KV *>(P.k), *v = static_cast<const KV *>(P.v);
   if (P.flash) {
-    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, pos0, P.maxc, scale);
+    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, P.pos.pos0, P.maxc, scale);
     return;
   }
   const int Si = static_cast<int>(P.S);
   switch (P.D) {
-    case 16: dispatch_group<16, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    case 32: dispatch_group<32, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    case 64: dispatch_group<64, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
-    default: dispatch_group<128, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, pos0, P.maxc, P.chunk, scale); break;
+    case 16: dispatch_group<16, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, P.pos, P.maxc, P.chunk, scale); break;
+    case 32: dispatch_group<32, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, P.pos, P.maxc, P.chunk, scale); break;
+    case 64: dispatch_group<64, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, P.pos, P.maxc, P.chunk, scale); break;
+    default: dispatch_group<128, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, P.pos, P.maxc, P.chunk, scale); break;
   }
 }
 
 void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t, int64_t heads,
-                      int64_t kv_heads, int64_t pos0, float scale) {
+                      int64_t kv_heads, float scale) {
   if (P.kv16)
-    attention_launch_kv<uint16_t>(ctx, P, out, part, batch, t, heads, kv_heads, pos0, scale);
+    attention_launch_kv<uint16_t>(ctx, P, out, part, batch, t, heads, kv_heads, scale);
   else
-    attention_launch_kv<float>(ctx, P, out, part, batch, t, heads, kv_heads, pos0, scale);
+    attention_launch_kv<float>(ctx, P, out, part, batch, t, heads, kv_heads, scale);
+}
+
+// The result of a planned call into a new buffer (partials in the context's
+// scratch).
+int attention_new(mi_ctx *ctx, const AttPlan &P, int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, float scale,
+                  const char *what, mi_id *out) {
+  float *part = nullptr;
+  if (P.part_bytes) {
+    part = static_cast<float *>(mi::scratch(ctx, P.part_bytes));
+    if (!part) return fail(ctx, MI_E_OOM, "%s scratch", what);
+  }
+  mi_id id;
+  Buffer *ob;
+  int s = new_buffer(ctx, batch * t, heads * P.D, MI_F32, &id, &ob);
+  if (s) return s;
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, scale);
+  s = check_launch(ctx, what);
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *out = id;
+  return MI_OK;
 }
 
 }  // namespace
@@ -636,32 +693,36 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   AttPlan P;
-  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, &P);
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, nullptr, 0, &P);
   if (s) return s;
-  float *part = nullptr;
-  if (P.part_bytes) {
-    part = static_cast<float *>(mi::scratch(ctx, P.part_bytes));
-    if (!part) return fail(ctx, MI_E_OOM, "attention_rows scratch");
+  return attention_new(ctx, P, batch, t, heads, kv_heads, scale, "attention_rows", out);
+}
+
+extern "C" int mi_attention_rows_at(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
+                                    int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0, int64_t span,
+                                    float scale, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  const int32_t *pos_dev = nullptr;
+  if (pos) {
+    MI_BUF(ctx, pb, pos);
+    if (pb->elem != MI_I32 || pb->numel() != 1)
+      return fail(ctx, MI_E_ARG, "attention_rows_at: the position is %s [%lld, %lld], want I32 [1, 1]",
+                  elem_name(pb->elem), (long long)pb->rows, (long long)pb->cols);
+    pos_dev = static_cast<const int32_t *>(pb->ptr);
   }
-  mi_id id;
-  Buffer *ob;
-  s = new_buffer(ctx, batch * t, heads * P.D, MI_F32, &id, &ob);
+  if (span < 1) return fail(ctx, MI_E_ARG, "attention_rows_at: span %lld", (long long)span);
+  AttPlan P;
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, pos_dev, span, &P);
   if (s) return s;
-  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, pos0, scale);
-  s = check_launch(ctx, "attention_rows");
-  if (s) {
-    mi_free(ctx, id);
-    return s;
-  }
-  *out = id;
-  return MI_OK;
+  return attention_new(ctx, P, batch, t, heads, kv_heads, scale, "attention_rows_at", out);
 }
 
 extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
                                       int64_t heads, int64_t kv_heads, int64_t pos0, float scale, mi_id out) {
   MI_ENTER(ctx);
   AttPlan P;
-  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, &P);
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, nullptr, 0, &P);
   if (s) return s;
   MI_BUF(ctx, ob, out);
   if (out == q || out == k_cache || out == v_cache)
@@ -679,6 +740,6 @@ extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id
     part = ctx->device >= 0 && ctx->device < ATT_MAX_DEVICES ? g_att_scratch[ctx->device].load() : nullptr;
     if (!part) return fail(ctx, MI_E_HIP, "attention_rows_into: no scratch address for device %d", ctx->device);
   }
-  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, pos0, scale);
+  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, scale);
   return check_launch(ctx, "attention_rows_into");
 }

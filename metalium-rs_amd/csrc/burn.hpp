@@ -400,6 +400,18 @@ inline Tensor attention_rows(const Tensor &q, const Tensor &k_cache, const Tenso
   return Tensor(q.ctx(), id, {q.rows(), q.cols()});
 }
 
+// attention_rows with the key chunks planned for `span` positions and pos0
+// read on the device from `pos` when it is given (mi_attention_rows_at).
+inline Tensor attention_rows_at(const Tensor &q, const Tensor &k_cache, const Tensor &v_cache, int64_t batch,
+                                int64_t t, int64_t heads, int64_t kv_heads, const Tensor *pos, int64_t pos0,
+                                int64_t span, float scale) {
+  mi_id id;
+  check(q.ctx(), mi_attention_rows_at(q.ctx(), q.use(), k_cache.use(), v_cache.use(), batch, t, heads, kv_heads,
+                                      pos ? pos->use() : 0, pos0, span, scale, &id),
+        "attention_rows_at");
+  return Tensor(q.ctx(), id, {q.rows(), q.cols()});
+}
+
 // Fused decode projections (one row per sequence, at most 8 rows).
 inline Tensor norm_matvec(const Tensor &x, const Tensor *gamma, float eps, const Tensor &w, const Tensor *residual,
                           bool silu_mul) {
@@ -418,6 +430,17 @@ inline Tensor norm_qkv_rope(const Tensor &x, const Tensor &gamma, float eps, con
   check(x.ctx(), mi_norm_qkv_rope(x.ctx(), x.use(), gamma.use(), eps, w_qkv.use(), cos.use(), sin.use(), heads,
                                   kv_heads, pos, k_cache.use(), v_cache.use(), &id),
         "norm_qkv_rope");
+  return Tensor(x.ctx(), id, {x.rows(), heads * k_cache.cols()});
+}
+
+// norm_qkv_rope at the position held on the device in `pos` ([1, 1] I32).
+inline Tensor norm_qkv_rope_at(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv, const Tensor &cos,
+                               const Tensor &sin, int64_t heads, int64_t kv_heads, const Tensor &pos,
+                               const Tensor &k_cache, const Tensor &v_cache) {
+  mi_id id;
+  check(x.ctx(), mi_norm_qkv_rope_at(x.ctx(), x.use(), gamma.use(), eps, w_qkv.use(), cos.use(), sin.use(), heads,
+                                     kv_heads, pos.use(), k_cache.use(), v_cache.use(), &id),
+        "norm_qkv_rope_at");
   return Tensor(x.ctx(), id, {x.rows(), heads * k_cache.cols()});
 }
 

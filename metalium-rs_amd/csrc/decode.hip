@@ -44,12 +44,16 @@ struct DecodeArgs {
   // DM_QKV: pair p = rows (h d + i, h d + i + d / 2) of head h = p / (d / 2)
   // over heads q 0..H-1, k H..H+KVH-1, v H+KVH..H+2KVH-1; q to `out`, k and v
   // into the caches at position pos of item (row m, kv head): F32, or BF16
-  // (kv16; rounded to nearest even as stored).
+  // (kv16; rounded to nearest even as stored).  pos_dev set: the position is
+  // read on the device (a traced decode step's input); outside [0, maxc) the
+  // step writes no cache row and no q, and raises the range flag.
   int d, H, KVH;
   int64_t pos, maxc;
   const float *cos, *sin;
   void *kc, *vc;
   int kv16;
+  const int32_t *pos_dev;
+  uint32_t *flags;
 };
 
 // Two values of one cache row, elements hi and hi + half of the row at `at`.
@@ -117,8 +121,16 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
     g.out[m * g.ldo + q.r0] = silu2(y0) * y1;
   } else {
     const int64_t half = g.d / 2, hi = q.hi, head = q.head;
+    int64_t pos = g.pos;
+    if (g.pos_dev) {
+      pos = *g.pos_dev;
+      if (pos < 0 || pos >= g.maxc) {
+        if (m == 0 && hi == 0 && head == 0) atomicOr(g.flags, FLAG_INDEX_RANGE);
+        return;
+      }
+    }
     if (head < g.H + g.KVH) {
-      const float *cs = g.cos + g.pos * g.d, *sn = g.sin + g.pos * g.d;
+      const float *cs = g.cos + pos * g.d, *sn = g.sin + pos * g.d;
       const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
       const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
       if (head < g.H) {
@@ -126,10 +138,10 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
         o[hi] = o0;
         o[hi + half] = o1;
       } else {
-        cache_pair(g, g.kc, ((m * g.KVH + (head - g.H)) * g.maxc + g.pos) * g.d, hi, half, o0, o1);
+        cache_pair(g, g.kc, ((m * g.KVH + (head - g.H)) * g.maxc + pos) * g.d, hi, half, o0, o1);
       }
     } else {
-      cache_pair(g, g.vc, ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + g.pos) * g.d, hi, half, y0, y1);
+      cache_pair(g, g.vc, ((m * g.KVH + (head - g.H - g.KVH)) * g.maxc + pos) * g.d, hi, half, y0, y1);
     }
   }
 }
@@ -684,10 +696,10 @@ extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_i
   return MI_OK;
 }
 
-extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
-                                mi_id sin_table, int64_t heads, int64_t kv_heads, int64_t pos, mi_id k_cache,
-                                mi_id v_cache, mi_id *q_out) {
-  MI_ENTER(ctx);
+// pos_dev null: the immediate position `pos`; else read on the device.
+static int norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table, mi_id sin_table,
+                         int64_t heads, int64_t kv_heads, int64_t pos, const int32_t *pos_dev, mi_id k_cache,
+                         mi_id v_cache, mi_id *q_out) {
   if (!q_out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, xb, x);
   MI_BUF(ctx, wb, w_qkv);
@@ -714,9 +726,13 @@ extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi
     return fail(ctx, MI_E_ARG, "norm_qkv_rope: caches must both be [rows * kv_heads * max_ctx, %lld], both F32 or both BF16",
                 (long long)D);
   const int64_t maxc = kb->rows / (M * kv_heads);
-  if (pos < 0 || pos >= maxc) return fail(ctx, MI_E_ARG, "norm_qkv_rope: position %lld beyond the cache's %lld", (long long)pos, (long long)maxc);
-  if (cb->elem != MI_F32 || sb->elem != MI_F32 || cb->cols != D || sb->cols != D || cb->rows <= pos || sb->rows <= pos)
-    return fail(ctx, MI_E_ARG, "norm_qkv_rope: rotary tables must be [> %lld, %lld] F32", (long long)pos, (long long)D);
+  // A position read on the device may be any below max_ctx: the tables must
+  // cover them all.
+  const int64_t need = pos_dev ? maxc - 1 : pos;
+  if (!pos_dev && (pos < 0 || pos >= maxc))
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: position %lld beyond the cache's %lld", (long long)pos, (long long)maxc);
+  if (cb->elem != MI_F32 || sb->elem != MI_F32 || cb->cols != D || sb->cols != D || cb->rows <= need || sb->rows <= need)
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope: rotary tables must be [> %lld, %lld] F32", (long long)need, (long long)D);
   mi_id id;
   Buffer *ob;
   s = new_buffer(ctx, M, heads * D, MI_F32, &id, &ob);
@@ -742,6 +758,8 @@ extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi
   g.kc = kb->ptr;
   g.vc = vb->ptr;
   g.kv16 = kb->elem == MI_BF16 ? 1 : 0;
+  g.pos_dev = pos_dev;
+  g.flags = flags(ctx);
   launch_decode<DM_QKV>(M, g, ctx->stream);
   s = check_launch(ctx, "norm_qkv_rope");
   if (s) {
@@ -750,4 +768,24 @@ extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi
   }
   *q_out = id;
   return MI_OK;
+}
+
+extern "C" int mi_norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                mi_id sin_table, int64_t heads, int64_t kv_heads, int64_t pos, mi_id k_cache,
+                                mi_id v_cache, mi_id *q_out) {
+  MI_ENTER(ctx);
+  return norm_qkv_rope(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos, nullptr, k_cache,
+                       v_cache, q_out);
+}
+
+extern "C" int mi_norm_qkv_rope_at(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                   mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, mi_id k_cache,
+                                   mi_id v_cache, mi_id *q_out) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, pb, pos);
+  if (pb->elem != MI_I32 || pb->numel() != 1)
+    return fail(ctx, MI_E_ARG, "norm_qkv_rope_at: the position is %s [%lld, %lld], want I32 [1, 1]", elem_name(pb->elem),
+                (long long)pb->rows, (long long)pb->cols);
+  return norm_qkv_rope(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, 0,
+                       static_cast<const int32_t *>(pb->ptr), k_cache, v_cache, q_out);
 }

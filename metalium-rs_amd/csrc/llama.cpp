@@ -21,9 +21,11 @@
 // attention of a query group is one product over a block of the cache:
 // queries regrouped to [batch * kv_heads, t * group, head_dim] (row
 // t * group + g) multiply the first ctx rows of their cache item.
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -43,6 +45,13 @@ struct Layer {
 
 }  // namespace
 
+// A decode step captured as a trace (mi_llama_generate_traced): its span and
+// the buffer its replays leave the next token ids in.
+struct StepTrace {
+  uint64_t id = 0;
+  Tensor next;  // [batch, 1] I32, allocated by the capture
+};
+
 struct mi_llama {
   mi_ctx *ctx;
   mi_llama_config cfg;
@@ -51,6 +60,10 @@ struct mi_llama {
   Tensor rope_cos, rope_sin;  // [max_ctx, head_dim]
   int64_t len = 0;            // positions in the cache
   int64_t cache_batch = 0;    // sequences the cache holds
+  // Traced decode steps over the current caches, by span; their inputs: the
+  // token ids [batch, 1] and the position [1, 1] (I32).
+  std::map<int64_t, StepTrace> traces;
+  Tensor step_ids, step_pos;
 };
 
 namespace {
@@ -83,6 +96,44 @@ constexpr int64_t kFlashMinT = 64, kFlashMinBlocks = 256;
 // plain product on the matrix cores).
 constexpr int64_t kDecodeMaxBatch = 32;
 constexpr int64_t kFusedHeadMaxBatch = 8;
+// A decode step's attention plans its key chunks for its span: the attended
+// positions rounded up to a multiple of kSpanStep (at most max_ctx).  Every
+// step of one span runs the same launches, so a step captured once replays
+// at each of its positions, and an eager step computes the same bits.
+constexpr int64_t kSpanStep = 64;
+
+int64_t decode_span(const mi_llama *m, int64_t ctxlen) {
+  return std::min<int64_t>(m->cfg.max_ctx, (ctxlen + kSpanStep - 1) / kSpanStep * kSpanStep);
+}
+
+// Whether a single-position step of `batch` sequences takes the fused decode
+// launches (and so can be traced).
+bool decode_fused(const mi_llama *m, int64_t batch) {
+  const mi_llama_config &c = m->cfg;
+  const int64_t D = c.head_dim, G = c.heads / c.kv_heads;
+  return batch <= kDecodeMaxBatch && (D == 16 || D == 32 || D == 64 || D == 128) && G <= 8 && c.hidden % 8 == 0 &&
+         c.intermediate % 8 == 0;
+}
+
+// The layers of a decode step, six fused launches each, on the hidden rows
+// x [batch, hidden]: the new position pos0 (immediate) or held on the device
+// in `pos`, the attention planned for `span` positions.
+Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, int64_t pos0, int64_t span) {
+  const mi_llama_config &c = m->cfg;
+  const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+  for (Layer &L : m->layers) {
+    Tensor q = pos ? burn::norm_qkv_rope_at(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, *pos,
+                                            L.cache_k, L.cache_v)
+                   : burn::norm_qkv_rope(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos0,
+                                         L.cache_k, L.cache_v);
+    Tensor o = burn::attention_rows_at(q, L.cache_k, L.cache_v, batch, 1, H, KVH, pos, pos0, span, scale);
+    x = burn::norm_matvec(o, nullptr, 0.0f, L.wo, &x, false);
+    Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, L.wgu, nullptr, true);
+    x = burn::norm_matvec(h, nullptr, 0.0f, L.wdown, &x, false);
+  }
+  return x;
+}
 
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
@@ -121,17 +172,8 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   }
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
 
-  const int64_t hid = c.hidden, I = c.intermediate;
-  if (t == 1 && batch <= kDecodeMaxBatch && fused && hid % 8 == 0 && I % 8 == 0) {
-    // Decode: six fused launches a layer.
-    for (Layer &L : m->layers) {
-      Tensor q = burn::norm_qkv_rope(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos0, L.cache_k,
-                                     L.cache_v);
-      Tensor o = burn::attention_rows(q, L.cache_k, L.cache_v, batch, 1, H, KVH, pos0, scale);
-      x = burn::norm_matvec(o, nullptr, 0.0f, L.wo, &x, false);
-      Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, L.wgu, nullptr, true);
-      x = burn::norm_matvec(h, nullptr, 0.0f, L.wdown, &x, false);
-    }
+  if (t == 1 && decode_fused(m, batch)) {
+    x = decode_layers(m, x, batch, nullptr, pos0, decode_span(m, ctxlen));
     m->len = ctxlen;
     return x;
   }
@@ -196,8 +238,15 @@ Tensor head_all(mi_llama *m, const Tensor &hidden) {
   return burn::float_matmul(burn::rms_norm(hidden, m->final_norm, m->cfg.eps, act), false, m->embed, true);
 }
 
+// Release every captured decode step (they read the current caches).
+void drop_traces(mi_llama *m) {
+  for (auto &kv : m->traces) (void)mi_trace_release(m->ctx, kv.second.id);
+  m->traces.clear();
+}
+
 void ensure_cache(mi_llama *m, int64_t batch) {
   if (m->len == 0 && m->cache_batch != batch) {
+    drop_traces(m);
     const mi_llama_config &c = m->cfg;
     const int kv = c.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
     for (Layer &L : m->layers) {
@@ -270,6 +319,7 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
 }
 
 int mi_llama_destroy(mi_llama *m) {
+  if (m) drop_traces(m);
   delete m;
   return MI_OK;
 }
@@ -382,3 +432,71 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
 }
 
 }  // extern "C"
+
+namespace {
+
+// The decode step of `span`, captured on first use: the token ids and the
+// position come from m->step_ids and m->step_pos, the next ids go to the
+// trace's own buffer.  Capture records the launches without running them:
+// the caches are not touched.
+StepTrace &step_trace(mi_llama *m, int64_t batch, int64_t span) {
+  auto it = m->traces.find(span);
+  if (it != m->traces.end()) return it->second;
+  mi_ctx *ctx = m->ctx;
+  if (!m->step_ids.defined() || m->step_ids.rows() != batch) m->step_ids = burn::fill(ctx, {batch, 1}, MI_I32, 0);
+  if (!m->step_pos.defined()) m->step_pos = burn::fill(ctx, {1, 1}, MI_I32, 0);
+  burn::check(ctx, mi_trace_begin(ctx), "trace_begin");
+  StepTrace st;
+  try {
+    Tensor x = burn::float_cast(burn::select_rows(m->embed, m->step_ids.reshape({batch})), MI_F32);
+    x = decode_layers(m, x.reshape({batch, m->cfg.hidden}), batch, &m->step_pos, 0, span);
+    st.next = burn::argmax_rows(head_last(m, x, batch, 1));
+  } catch (...) {
+    uint64_t dead = 0;
+    if (mi_trace_end(ctx, &dead) == MI_OK) (void)mi_trace_release(ctx, dead);
+    throw;
+  }
+  burn::check(ctx, mi_trace_end(ctx, &st.id), "trace_end");
+  return m->traces[span] = std::move(st);
+}
+
+}  // namespace
+
+extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t t_prompt,
+                                        int32_t n_new, int32_t *out, double *prefill_ms, double *decode_ms) {
+  if (!m || !prompt || !out || batch <= 0 || t_prompt <= 0 || n_new < 1) return MI_E_ARG;
+  if (!decode_fused(m, batch))  // no fused decode step to capture: the eager loop
+    return mi_llama_generate(m, prompt, batch, t_prompt, n_new, out, prefill_ms, decode_ms);
+  using clock = std::chrono::steady_clock;
+  try {
+    if (batch > m->cfg.max_batch || t_prompt + n_new > m->cfg.max_ctx) throw burn::Error(MI_E_ARG, "batch or context too large");
+    m->len = 0;
+    ensure_cache(m, batch);
+    burn::check(m->ctx, mi_sync(m->ctx), "sync");
+    auto t0 = clock::now();
+    Tensor h = forward_hidden(m, prompt, batch, t_prompt);
+    std::vector<int32_t> tok = burn::int_into_data(burn::argmax_rows(head_last(m, h, batch, t_prompt)));
+    auto t1 = clock::now();
+    for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
+    // Each step: the ids and the position written into the trace's inputs,
+    // one replay, the next ids read back (the reference's traced step:
+    // token ids in, the next token out).
+    for (int32_t s = 1; s < n_new; ++s) {
+      StepTrace &st = step_trace(m, batch, decode_span(m, m->len + 1));
+      const int32_t pos = static_cast<int32_t>(m->len);
+      const mi_id in_ids[2] = {m->step_ids.id(), m->step_pos.id()};
+      const void *in_vals[2] = {tok.data(), &pos};
+      const mi_id out_ids[1] = {st.next.id()};
+      void *out_vals[1] = {tok.data()};
+      burn::check(m->ctx, mi_trace_run(m->ctx, st.id, 2, in_ids, in_vals, 1, out_ids, out_vals), "trace_run");
+      m->len += 1;
+      for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
+    }
+    auto t2 = clock::now();
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+  } catch (const std::exception &e) {
+    return fail_model(e);
+  }
+  return MI_OK;
+}

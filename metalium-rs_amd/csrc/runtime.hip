@@ -84,9 +84,9 @@ void *device_alloc(Ctx *ctx, size_t bytes, size_t *got) {
   if (e != hipSuccess) {
     // Give the cache back to the device and try once more.
     (void)hipGetLastError();
-    hipStreamSynchronize(ctx->stream);
+    (void)hipStreamSynchronize(ctx->stream);
     for (auto &kv : ctx->free_blocks)
-      for (void *q : kv.second) hipFree(q);
+      for (void *q : kv.second) (void)hipFree(q);
     ctx->free_blocks.clear();
     ctx->cached_bytes = 0;
     e = hipMalloc(&p, sz);
@@ -124,8 +124,8 @@ void *scratch(Ctx *ctx, size_t bytes) {
       ctx->retired_scratch.push_back(ctx->scratch);
     } else {
       // Earlier work on the stream may still read the old scratch.
-      hipStreamSynchronize(ctx->stream);
-      hipFree(ctx->scratch);
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipFree(ctx->scratch);
     }
   }
   size_t sz = round_size(bytes);
@@ -143,7 +143,7 @@ static int stage_slot(Ctx *ctx) {
   int s = ctx->stage_next;
   ctx->stage_next = (s + 1) % Ctx::kStageSlots;
   if (ctx->stage_pending[s]) {
-    hipEventSynchronize(ctx->stage_done[s]);
+    (void)hipEventSynchronize(ctx->stage_done[s]);
     ctx->stage_pending[s] = false;
   }
   return s;
@@ -166,7 +166,7 @@ static int collect(Ctx *ctx) {
   e = hipMemcpy(&f, ctx->dev_flags, sizeof f, hipMemcpyDeviceToHost);
   if (e == hipSuccess && f != 0) {
     uint32_t zero = 0;
-    hipMemcpy(ctx->dev_flags, &zero, sizeof zero, hipMemcpyHostToDevice);
+    (void)hipMemcpy(ctx->dev_flags, &zero, sizeof zero, hipMemcpyHostToDevice);
     if (ctx->sticky == MI_OK) {
       ctx->sticky = MI_E_DOMAIN;
       fail(ctx, MI_E_DOMAIN, "an index was out of range (DOMAIN)");
@@ -231,12 +231,12 @@ int mi_ctx_destroy(mi_ctx *ctx) {
   if (!ctx) return MI_OK;
   {
     std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    hipSetDevice(ctx->device);
-    if (ctx->stream) hipStreamSynchronize(ctx->stream);
-    for (auto &kv : ctx->bufs) hipFree(kv.second.ptr);
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->bufs) (void)hipFree(kv.second.ptr);
     ctx->bufs.clear();
     for (auto &kv : ctx->free_blocks)
-      for (void *p : kv.second) hipFree(p);
+      for (void *p : kv.second) (void)hipFree(p);
     ctx->free_blocks.clear();
     if (ctx->capturing) {
       hipGraph_t g = nullptr;
@@ -250,15 +250,15 @@ int mi_ctx_destroy(mi_ctx *ctx) {
     }
     ctx->traces.clear();
     for (void *p : ctx->retired_scratch) (void)hipFree(p);
-    if (ctx->scratch) hipFree(ctx->scratch);
-    if (ctx->dev_flags) hipFree(ctx->dev_flags);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->dev_flags) (void)hipFree(ctx->dev_flags);
     for (int i = 0; i < Ctx::kStageSlots; ++i) {
-      if (ctx->stage[i]) hipHostFree(ctx->stage[i]);
-      if (ctx->stage_done[i]) hipEventDestroy(ctx->stage_done[i]);
+      if (ctx->stage[i]) (void)hipHostFree(ctx->stage[i]);
+      if (ctx->stage_done[i]) (void)hipEventDestroy(ctx->stage_done[i]);
     }
     for (int i = 0; i < 16; ++i)
-      if (ctx->events[i]) hipEventDestroy(ctx->events[i]);
-    if (ctx->stream) hipStreamDestroy(ctx->stream);
+      if (ctx->events[i]) (void)hipEventDestroy(ctx->events[i]);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
   return MI_OK;
@@ -526,7 +526,7 @@ int mi_trace_release(mi_ctx *ctx, uint64_t trace) {
   if (it == ctx->traces.end()) return fail(ctx, MI_E_ID, "unknown trace %llu", (unsigned long long)trace);
   if (ctx->capturing && ctx->capture_id == trace) return fail(ctx, MI_E_ARG, "the trace is still being captured");
   // A replay may still be running: wait, then hand the memory back.
-  hipStreamSynchronize(ctx->stream);
+  (void)hipStreamSynchronize(ctx->stream);
   if (it->second.exec) (void)hipGraphExecDestroy(it->second.exec);
   for (auto &h : it->second.held) device_release(ctx, h.first, h.second);
   ctx->traces.erase(it);

@@ -113,6 +113,8 @@ def _load() -> ctypes.CDLL:
                             ctypes.POINTER(c_int), I64, I64, I64, c_int, Ip],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
+        "mi_norm_qkv_rope_at": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, U64, U64, Ip],
+        "mi_attention_rows_at": [P, U64, U64, U64, I64, I64, I64, I64, U64, I64, I64, c_float, Ip],
         "mi_qkv_rope_cache": [P, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
         "mi_silu_mul_halves": [P, U64, c_int, Ip],
         "mi_eltwise": [P, c_u32, c_float, c_float, U64, U64, U64, c_int, Ip],
@@ -347,6 +349,19 @@ class Engine:
         positions against the first pos0 + t rows of each cache item."""
         return self._out(self._lib.mi_attention_rows, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, scale)
 
+    def attention_rows_at(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int, kv_heads: int,
+                          pos: int, pos0: int, span: int, scale: float) -> int:
+        """attention_rows with the key chunks planned for `span` positions and
+        pos0 read on the device from the [1, 1] I32 buffer `pos` (if nonzero)."""
+        return self._out(self._lib.mi_attention_rows_at, q, k_cache, v_cache, batch, t, heads, kv_heads, pos, pos0,
+                         span, scale)
+
+    def norm_qkv_rope_at(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
+                         kv_heads: int, pos: int, k_cache: int, v_cache: int) -> int:
+        """norm_qkv_rope at the position held on the device in `pos` ([1, 1] I32)."""
+        return self._out(self._lib.mi_norm_qkv_rope_at, x, gamma, eps, w_qkv, cos, sin, heads, kv_heads, pos,
+                         k_cache, v_cache)
+
     def attention_rows_into(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int,
                             kv_heads: int, pos0: int, scale: float, out: int) -> None:
         """attention_rows into the existing F32 buffer `out`, allocating
@@ -558,8 +573,9 @@ def _models_lib():
     L.mi_llama_forward.argtypes = [P, P, I32, I32, I32, ctypes.POINTER(U64)]
     L.mi_llama_generate.argtypes = [P, P, I32, I32, I32, P, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double)]
+    L.mi_llama_generate_traced.argtypes = L.mi_llama_generate.argtypes
     for f in (L.mi_llama_create, L.mi_llama_destroy, L.mi_llama_param, L.mi_llama_reset, L.mi_llama_forward,
-              L.mi_llama_generate):
+              L.mi_llama_generate, L.mi_llama_generate_traced):
         f.restype = ctypes.c_int
     L.mi_models_last_error.argtypes = []
     L.mi_models_last_error.restype = ctypes.c_char_p
@@ -615,13 +631,15 @@ class Llama:
         self._check(self.L.mi_llama_forward(self.h, ids.ctypes.data, b, t, int(all_positions), ctypes.byref(out)))
         return out.value
 
-    def generate(self, prompt: np.ndarray, n_new: int):
+    def generate(self, prompt: np.ndarray, n_new: int, traced: bool = False):
+        """Greedy generation: ([batch, n_new] ids, prefill ms, decode ms); `traced` replays a captured
+        decode step per token (mi_llama_generate_traced)."""
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         b, t = prompt.shape
         out = np.zeros((b, n_new), np.int32)
         pf, dc = ctypes.c_double(), ctypes.c_double()
-        self._check(self.L.mi_llama_generate(self.h, prompt.ctypes.data, b, t, n_new, out.ctypes.data,
-                                             ctypes.byref(pf), ctypes.byref(dc)))
+        fn = self.L.mi_llama_generate_traced if traced else self.L.mi_llama_generate
+        self._check(fn(self.h, prompt.ctypes.data, b, t, n_new, out.ctypes.data, ctypes.byref(pf), ctypes.byref(dc)))
         return out, pf.value, dc.value
 
 

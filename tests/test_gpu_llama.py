@@ -243,6 +243,20 @@ def test_smollm2_shape_greedy_generation(engine, smol, batch):
         assert clear.mean() >= 0.7, clear.mean()
 
 
+@pytest.mark.parametrize("batch,numerics", [(1, "reference"), (32, "reference"), (32, "performance")])
+def test_traced_generation_equals_eager(engine, smol, smol_perf, batch, numerics):
+    """The decode step captured once per 64-position span and replayed per
+    token (the reference's TracedGenerator) gives the eager loop's tokens;
+    the 20 steps from a 56-token prompt cross from the 64 span into the 128."""
+    m = smol[0] if numerics == "reference" else smol_perf
+    prompt = np.random.default_rng(300 + batch).integers(0, 49152, (batch, 56)).astype(np.int32)
+    eager, _, _ = m.generate(prompt, 20)
+    traced, _, _ = m.generate(prompt, 20, traced=True)
+    assert np.array_equal(traced, eager)
+    again, _, _ = m.generate(prompt, 20, traced=True)  # the captured steps replayed again
+    assert np.array_equal(again, eager)
+
+
 def test_generate_rejects_zero_new_tokens(engine, smol):
     m, _ = smol
     with pytest.raises(miburn.MiError) as e:

@@ -823,6 +823,52 @@ def test_attention_rows_bf16_caches(engine, batch, t, heads, kvh, D, pos0, maxc)
     assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("batch,t,heads,kvh,D,pos0,span,maxc", [
+    (1, 1, 9, 3, 64, 575, 576, 640),    # decode: span = the attended length
+    (1, 1, 9, 3, 64, 513, 576, 640),    # span past the context: trailing chunks empty
+    (32, 1, 9, 3, 64, 100, 128, 640),   # batch 32
+    (2, 5, 4, 2, 16, 7, 64, 64),        # several new positions
+    (1, 1, 9, 3, 64, 0, 64, 64),        # the first position
+])
+def test_attention_rows_at_device_position(engine, batch, t, heads, kvh, D, pos0, span, maxc):
+    # Planned for `span`: within the F32 bound of the float64 reference; the
+    # device-held position gives the immediate one's bits.
+    q = rnd(batch * t, heads * D)
+    kc = rnd(batch * kvh * maxc, D)
+    vc = rnd(batch * kvh * maxc, D)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    iq, ik, iv = engine.upload(q), engine.upload(kc), engine.upload(vc)
+    imm = engine.download(engine.attention_rows_at(iq, ik, iv, batch, t, heads, kvh, 0, pos0, span, scale))
+    pos = engine.upload_bits(np.array([[pos0]], np.int32), I32)
+    dev = engine.download(engine.attention_rows_at(iq, ik, iv, batch, t, heads, kvh, pos, 0, span, scale))
+    same_bits(dev, imm)
+    want = attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale)
+    assert np.abs(imm - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    if span == pos0 + t:  # the plain call's plan
+        same_bits(imm, engine.download(engine.attention_rows(iq, ik, iv, batch, t, heads, kvh, pos0, scale)))
+
+
+def test_attention_rows_at_errors(engine):
+    q = engine.upload(rnd(1, 2 * 64))
+    k = engine.upload(rnd(64, 64))
+    with pytest.raises(miburn.MiError) as e:
+        engine.attention_rows_at(q, k, k, 1, 1, 2, 1, 0, 60, 32, 0.125)  # span below pos0 + t
+    assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:
+        engine.attention_rows_at(q, k, k, 1, 1, 2, 1, 0, 0, 65, 0.125)  # span beyond the cache
+    assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:  # a position buffer that is not [1, 1] I32
+        engine.attention_rows_at(q, k, k, 1, 1, 2, 1, engine.upload(rnd(1, 1)), 0, 32, 0.125)
+    assert e.value.kind == "ARG"
+    # A device position past the span: attended from 0 (in bounds), reported at the next wait.
+    bad = engine.upload_bits(np.array([[40]], np.int32), I32)
+    engine.attention_rows_at(q, k, k, 1, 1, 2, 1, bad, 0, 32, 0.125)
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()
+
+
 def test_attention_rows_mixed_caches_refused(engine):
     q = engine.upload(rnd(1, 2 * 64))
     kf = engine.upload(rnd(8, 64))
@@ -932,6 +978,36 @@ def test_norm_qkv_rope_bf16_caches(engine, M):
     assert np.array_equal(engine.download(vb), orc.to_bf16(engine.download(vf)))
     with pytest.raises(miburn.MiError) as e:
         engine.norm_qkv_rope(*args, kb, vf)
+    assert e.value.kind == "ARG"
+
+
+@pytest.mark.parametrize("M", [1, 5, 32])
+def test_norm_qkv_rope_at_device_position(engine, M):
+    # The position read on the device: the immediate call's q and cache bits.
+    H, KVH, D, K, maxc, pos, eps = 9, 3, 64, 576, 40, 23, 1e-5
+    x, g, wb = decode_inputs(M, K, (H + 2 * KVH) * D)
+    cos, sin = rnd(maxc, D), rnd(maxc, D)
+    kc0, vc0 = rnd(M * KVH * maxc, D), rnd(M * KVH * maxc, D)
+    args = (engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb), engine.upload(cos), engine.upload(sin),
+            H, KVH)
+    k1, v1 = engine.upload(kc0), engine.upload(vc0)
+    k2, v2 = engine.upload(kc0), engine.upload(vc0)
+    q1 = engine.download(engine.norm_qkv_rope(*args, pos, k1, v1))
+    ipos = engine.upload_bits(np.array([[pos]], np.int32), I32)
+    q2 = engine.download(engine.norm_qkv_rope_at(*args, ipos, k2, v2))
+    same_bits(q2, q1)
+    same_bits(engine.download(k2), engine.download(k1))
+    same_bits(engine.download(v2), engine.download(v1))
+    # Outside the cache: nothing written, reported at the next wait.
+    bad = engine.upload_bits(np.array([[maxc]], np.int32), I32)
+    engine.norm_qkv_rope_at(*args, bad, k2, v2)
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()
+    same_bits(engine.download(k2), engine.download(k1))
+    with pytest.raises(miburn.MiError) as e:  # tables shorter than the cache
+        engine.norm_qkv_rope_at(*args[:4], engine.upload(cos[:30]), engine.upload(sin[:30]), H, KVH, ipos, k2, v2)
     assert e.value.kind == "ARG"
 
 
