@@ -243,6 +243,21 @@ def test_sum_mean(engine, shape, axis):
         assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * scale + 1e-30)
 
 
+@pytest.mark.parametrize("shape", [(4096, 8192), (1500, 8224), (100, 3000), (70, 1024)])
+def test_column_sum_repeatable(engine, shape):
+    # The one-launch column reduction resets its arrival counters: calls in a
+    # row, and interleaved with other shapes, give the same bits.
+    x = rnd(*shape)
+    a = engine.upload(x)
+    other = engine.upload(rnd(300, 2048))
+    first = engine.download(engine.reduce(a, R_SUM, AXIS_ROWS))
+    for _ in range(3):
+        engine.free(engine.reduce(other, R_MEAN, AXIS_ROWS))
+        same_bits(engine.download(engine.reduce(a, R_SUM, AXIS_ROWS)), first)
+    absx = np.abs(x.astype(np.float64)).sum(axis=0, keepdims=True)
+    assert np.all(np.abs(first.astype(np.float64) - orc.reduce(x, R_SUM, AXIS_ROWS)) <= 1e-5 * absx + 1e-30)
+
+
 @pytest.mark.parametrize("shape", [(3, 5), (64, 10), (300, 700), (1500, 8224)])
 @pytest.mark.parametrize("axis", [AXIS_ROWS, AXIS_COLS])
 def test_max_min_exact(engine, shape, axis):
