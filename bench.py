@@ -256,10 +256,11 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     decode `new` tokens; tokens/s of the prefill and of the decode steps.
     `numerics`: the reference contract (F32 KV cache and activations) or the
     performance one (BF16 KV cache, BF16 prefill activation operands).  The
-    generation runs eagerly, then traced (each decode step a replay of a step
-    captured per 64-position span, token ids in and out through the host:
-    the reference's TracedGenerator); the traced run's steps are captured by
-    an untimed first traced generation and must give the eager tokens.
+    generation runs eagerly, then traced (the prompt's prefill and each decode
+    step replays of captures -- the step per 64-position span -- token ids in
+    and out through the host: the reference's TracedGenerator); the traced
+    run's captures are made by an untimed first traced generation, and its
+    tokens must be the eager ones.
     `traced` False skips the traced runs (profiling: rocprofv3's kernel
     trace has ended in a host segmentation fault inside hipGraphLaunch)."""
     import miburn
@@ -268,10 +269,10 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     ids = rng.integers(0, 49152, (batch, prompt)).astype(np.int32)
     m.generate(ids[:, :32], 4)  # warm the kernels
     out, pf_ms, dc_ms = m.generate(ids, new)
-    tr_ms = None
+    tr_ms = tr_pf = None
     if traced:
-        m.generate(ids, new, traced=True)  # captures every span's step
-        tr_out, _, tr_ms = m.generate(ids, new, traced=True)
+        m.generate(ids, new, traced=True)  # captures the prompt's prefill and every span's step
+        tr_out, tr_pf, tr_ms = m.generate(ids, new, traced=True)
         if not np.array_equal(tr_out, out):
             raise RuntimeError("traced generation's tokens differ from the eager loop's")
     m.close()
@@ -294,7 +295,8 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     attn = 2 * prompt * (prompt + 1) * cfg["head_dim"] * cfg["heads"] * cfg["layers"]
     pf_flop = batch * (2 * prompt * layer_params + attn + 2 * cfg["hidden"] * cfg["vocab"])
     return {"batch": batch, "numerics": numerics, "prompt": prompt, "new_tokens": new,
-            "prefill_ms": round(pf_ms, 2), "prefill_tokens_per_s": round(batch * prompt / (pf_ms / 1e3), 1),
+            "prefill_ms": round(pf_ms, 2), "prefill_traced_ms": round(tr_pf, 2) if traced else None,
+            "prefill_tokens_per_s": round(batch * prompt / (pf_ms / 1e3), 1),
             "prefill_gflop": round(pf_flop / 1e9, 1),
             "prefill_mfma_frac": round(pf_flop / (pf_ms * 1e-3) / (PEAK_TFLOPS["bf16"] * 1e12), 4),
             "decode_ms_per_step": round(dc_step_ms, 3),

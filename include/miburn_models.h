@@ -67,15 +67,18 @@ int mi_llama_forward(mi_llama *m, const int32_t *ids, int32_t batch,
 int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch,
                       int32_t t_prompt, int32_t n_new, int32_t *out,
                       double *prefill_ms, double *decode_ms);
-/* mi_llama_generate with each decode step a trace replay (the reference's
- * TracedGenerator, crates/tt-models/src/generate.rs:1-22, 770-790): the
- * prompt runs eagerly; the decode step is captured once per span of 64
- * attended positions over the model's caches and replayed per token, the
- * token ids and the position written into the trace's inputs and the next
- * ids read back.  The tokens equal mi_llama_generate's bit for bit (the
- * eager step runs the same launches).  Traces live until the caches are
- * reallocated (a new batch size) or the model is destroyed.  A batch the
- * fused decode step does not take runs mi_llama_generate. */
+/* mi_llama_generate with the prompt and each decode step trace replays
+ * (the reference's TracedGenerator, crates/tt-models/src/generate.rs:1-22,
+ * 770-790): the prefill is captured once per (batch, prompt length), token
+ * ids in and the first new ids out (eager where its path cannot be captured:
+ * the composition's causal mask is an upload); the decode step is captured
+ * once per span of 64 attended positions over the model's caches and
+ * replayed per token, the token ids and the position written into the
+ * trace's inputs and the next ids read back.  The tokens equal
+ * mi_llama_generate's bit for bit (the eager steps run the same launches).
+ * Traces live until the caches are reallocated (a new batch size) or the
+ * model is destroyed.  A batch the fused decode step does not take runs
+ * mi_llama_generate. */
 int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int32_t batch,
                              int32_t t_prompt, int32_t n_new, int32_t *out,
                              double *prefill_ms, double *decode_ms);

@@ -175,6 +175,11 @@ struct Ctx {
     std::vector<std::pair<void *, size_t>> held;
   };
   std::map<uint64_t, Trace> traces;
+  // Blocks freed during the current capture: the capture records one
+  // stream's launches in order, so a later allocation of the same capture
+  // may take one (its graph runs the freeing kernels first); they stay the
+  // trace's.
+  std::map<size_t, std::vector<void *>> capture_free;
   bool capturing = false;
   uint64_t capture_id = 0, next_trace = 1;
   std::vector<void *> retired_scratch;

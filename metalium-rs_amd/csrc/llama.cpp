@@ -52,6 +52,15 @@ struct StepTrace {
   Tensor next;  // [batch, 1] I32, allocated by the capture
 };
 
+// A prompt's prefill from position 0 captured as a trace, per (batch,
+// length): its token ids input and the buffer its replays leave the first new
+// ids in.  id 0: the prefill could not be captured (its path uploads, as the
+// composition's causal mask does) and runs eagerly.
+struct PromptTrace {
+  uint64_t id = 0;
+  Tensor ids, next;  // [batch * t] and [batch, 1] I32
+};
+
 struct mi_llama {
   mi_ctx *ctx;
   mi_llama_config cfg;
@@ -64,6 +73,7 @@ struct mi_llama {
   // token ids [batch, 1] and the position [1, 1] (I32).
   std::map<int64_t, StepTrace> traces;
   Tensor step_ids, step_pos;
+  std::map<std::pair<int64_t, int64_t>, PromptTrace> prompt_traces;
 };
 
 namespace {
@@ -242,6 +252,9 @@ Tensor head_all(mi_llama *m, const Tensor &hidden) {
 void drop_traces(mi_llama *m) {
   for (auto &kv : m->traces) (void)mi_trace_release(m->ctx, kv.second.id);
   m->traces.clear();
+  for (auto &kv : m->prompt_traces)
+    if (kv.second.id) (void)mi_trace_release(m->ctx, kv.second.id);
+  m->prompt_traces.clear();
 }
 
 void ensure_cache(mi_llama *m, int64_t batch) {
@@ -460,6 +473,40 @@ StepTrace &step_trace(mi_llama *m, int64_t batch, int64_t span) {
   return m->traces[span] = std::move(st);
 }
 
+// The prefill of `t` tokens per sequence into the empty caches, captured on
+// first use (the reference's traced prompt chunk): embedding gather, the
+// layers, the head on each sequence's last position and the argmax.  A path
+// that cannot be captured leaves a record with id 0.
+PromptTrace &prompt_trace(mi_llama *m, int64_t batch, int64_t t) {
+  const auto key = std::make_pair(batch, t);
+  auto it = m->prompt_traces.find(key);
+  if (it != m->prompt_traces.end()) return it->second;
+  mi_ctx *ctx = m->ctx;
+  PromptTrace pt;
+  pt.ids = burn::fill(ctx, {batch * t}, MI_I32, 0);
+  burn::check(ctx, mi_trace_begin(ctx), "trace_begin");
+  try {
+    m->len = 0;
+    Tensor h = forward_ids(m, pt.ids, batch, t);
+    pt.next = burn::argmax_rows(head_last(m, h, batch, t));
+    m->len = 0;  // the capture ran nothing
+  } catch (const burn::Error &e) {
+    m->len = 0;
+    uint64_t dead = 0;
+    if (mi_trace_end(ctx, &dead) == MI_OK) (void)mi_trace_release(ctx, dead);
+    if (e.status != MI_E_UNSUPPORTED) throw;
+    PromptTrace eager;
+    return m->prompt_traces[key] = std::move(eager);
+  } catch (...) {
+    m->len = 0;
+    uint64_t dead = 0;
+    if (mi_trace_end(ctx, &dead) == MI_OK) (void)mi_trace_release(ctx, dead);
+    throw;
+  }
+  burn::check(ctx, mi_trace_end(ctx, &pt.id), "trace_end");
+  return m->prompt_traces[key] = std::move(pt);
+}
+
 }  // namespace
 
 extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t t_prompt,
@@ -473,9 +520,22 @@ extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int3
     m->len = 0;
     ensure_cache(m, batch);
     burn::check(m->ctx, mi_sync(m->ctx), "sync");
+    // The prompt: a replay of its captured prefill (ids in, the first new
+    // ids out), or eagerly where the prefill cannot be captured.
+    PromptTrace &pt = prompt_trace(m, batch, t_prompt);
     auto t0 = clock::now();
-    Tensor h = forward_hidden(m, prompt, batch, t_prompt);
-    std::vector<int32_t> tok = burn::int_into_data(burn::argmax_rows(head_last(m, h, batch, t_prompt)));
+    std::vector<int32_t> tok(static_cast<size_t>(batch));
+    if (pt.id) {
+      const mi_id in_ids[1] = {pt.ids.id()};
+      const void *in_vals[1] = {prompt};
+      const mi_id out_ids[1] = {pt.next.id()};
+      void *out_vals[1] = {tok.data()};
+      burn::check(m->ctx, mi_trace_run(m->ctx, pt.id, 1, in_ids, in_vals, 1, out_ids, out_vals), "trace_run");
+      m->len = t_prompt;
+    } else {
+      Tensor h = forward_hidden(m, prompt, batch, t_prompt);
+      tok = burn::int_into_data(burn::argmax_rows(head_last(m, h, batch, t_prompt)));
+    }
     auto t1 = clock::now();
     for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
     // Each step: the ids and the position written into the trace's inputs,

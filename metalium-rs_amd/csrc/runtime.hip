@@ -67,6 +67,24 @@ static size_t round_size(size_t bytes) {
 
 void *device_alloc(Ctx *ctx, size_t bytes, size_t *got) {
   size_t sz = round_size(bytes);
+  if (ctx->capturing) {
+    // A block this capture freed: it leaves the trace's held list while the
+    // capture's new buffer has it (mi_free returns it there).
+    auto cf = ctx->capture_free.find(sz);
+    if (cf != ctx->capture_free.end() && !cf->second.empty()) {
+      void *p = cf->second.back();
+      cf->second.pop_back();
+      auto &held = ctx->traces[ctx->capture_id].held;
+      for (size_t i = 0; i < held.size(); ++i)
+        if (held[i].first == p) {
+          held[i] = held.back();
+          held.pop_back();
+          break;
+        }
+      *got = sz;
+      return p;
+    }
+  }
   auto it = ctx->free_blocks.find(sz);
   if (it != ctx->free_blocks.end() && !it->second.empty()) {
     void *p = it->second.back();
@@ -402,10 +420,12 @@ int mi_free(mi_ctx *ctx, mi_id id) {
   // kernels: it is the capture's until the trace is released.
   const uint64_t owner = ctx->capturing ? ctx->capture_id : it->second.trace;
   auto tr = owner ? ctx->traces.find(owner) : ctx->traces.end();
-  if (tr != ctx->traces.end())
+  if (tr != ctx->traces.end()) {
     tr->second.held.emplace_back(it->second.ptr, it->second.bytes);  // the trace's until released
-  else
+    if (ctx->capturing) ctx->capture_free[it->second.bytes].push_back(it->second.ptr);
+  } else {
     device_release(ctx, it->second.ptr, it->second.bytes);
+  }
   ctx->bufs.erase(it);
   return MI_OK;
 }
@@ -471,6 +491,7 @@ int mi_trace_begin(mi_ctx *ctx) {
   if (e != hipSuccess) return fail(ctx, MI_E_HIP, "begin capture: %s", hipGetErrorString(e));
   ctx->capture_id = ctx->next_trace++;
   ctx->traces[ctx->capture_id] = Ctx::Trace{};
+  ctx->capture_free.clear();
   ctx->capturing = true;
   return MI_OK;
 }
@@ -479,6 +500,7 @@ int mi_trace_end(mi_ctx *ctx, uint64_t *trace) {
   MI_ENTER(ctx);
   if (!ctx->capturing) return fail(ctx, MI_E_ARG, "no trace is being captured");
   ctx->capturing = false;
+  ctx->capture_free.clear();
   const uint64_t id = ctx->capture_id;
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(ctx->stream, &g);
