@@ -54,6 +54,10 @@ struct DecodeArgs {
   int kv16;
   const int32_t *pos_dev;
   uint32_t *flags;
+  // Split-k matrix-core form: S partial sums per output and each activation
+  // row's partial sum of squares (see decode_mfma_split_kernel).
+  float *part;
+  int split;
 };
 
 // Two values of one cache row, elements hi and hi + half of the row at `at`.
@@ -549,6 +553,173 @@ decode_mfma_kernel(DecodeArgs g, int M) {
   }
 }
 
+// The same products split over k for grids of few tiles (the q|k|v heads and
+// the down projection: 15 and 18 tiles of a 256-CU chip, each block pulling
+// every activation row and its weight rows through one CU): block (tile, s)
+// takes k16 steps [s per, (s + 1) per) on four wavefronts and writes its raw
+// sums -- no RMS, no epilogue -- to part[(s M + m) N + weight row], and,
+// from the first tile's blocks, each activation row's sum of squares over
+// its steps to part[S M N + s M + m].  decode_fold_kernel adds the S
+// partials in split order and runs the mode's epilogue.  In a batch-32
+// SmolLM2 decode step the down projection takes 6.9 + 3.6 us (split, fold)
+// against 13.6, the q|k|v heads 6.7 + 3.8 against 11.1: 1.88 -> 1.755 ms a
+// step.
+constexpr int DSPLIT_WAVES = 4;
+
+template <int MODE, int STEPS, int NB, bool GAMMA>
+__global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(DecodeArgs g, int M) {
+  constexpr int NW = DSPLIT_WAVES;
+  __shared__ float red[NW][NB * 16][64];
+  __shared__ float sq[NW][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
+  const int n = lane & 31, kg = lane >> 5;
+  int64_t row[NB];
+  bool rv[NB];
+  if constexpr (MODE == DM_PLAIN) {
+    row[0] = 32 * t + n;
+    rv[0] = row[0] < g.N;
+  } else if constexpr (MODE == DM_SILU_MUL) {
+    row[0] = 32 * t + n;
+    row[1] = g.inter + row[0];
+    rv[0] = rv[1] = row[0] < g.inter;
+  } else {
+    row[0] = t * g.d + n;
+    row[1] = row[0] + 32;
+    rv[0] = rv[1] = true;
+  }
+  const int m = lane & 31;
+  const bool mv = m < M;
+  const int64_t nsteps = g.K / 16, per = (nsteps + S - 1) / S;
+  const int64_t s0 = sp * per, s1 = s0 + per < nsteps ? s0 + per : nsteps;  // s0 < s1: the host keeps S <= nsteps / per
+  // Unconditional loads from addresses inside the buffers, as the unsplit
+  // kernel's: steps past the split's end reread its last step.
+  uint4 wb[STEPS][NB];
+  float4 xa[STEPS][2], ga[GAMMA ? STEPS : 1][2];
+  const int64_t mc = mv ? m : 0;
+  int64_t rowc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) rowc[b] = rv[b] ? row[b] : 0;
+#pragma unroll
+  for (int si = 0; si < STEPS; ++si) {
+    const int64_t step = s0 + w + NW * si;
+    const int64_t k = (step < s1 ? step : s1 - 1) * 16 + 8 * kg;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) wb[si][b] = *reinterpret_cast<const uint4 *>(g.w + rowc[b] * g.K + k);
+    xa[si][0] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k);
+    xa[si][1] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k + 4);
+    if constexpr (GAMMA) {
+      ga[si][0] = *reinterpret_cast<const float4 *>(g.gamma + k);
+      ga[si][1] = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
+    }
+  }
+  dm_f32x16 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
+  float ssq = 0.0f;
+#pragma unroll
+  for (int si = 0; si < STEPS; ++si) {
+    if (s0 + w + NW * si < s1) {
+      float v[8] = {xa[si][0].x, xa[si][0].y, xa[si][0].z, xa[si][0].w, xa[si][1].x, xa[si][1].y, xa[si][1].z,
+                    xa[si][1].w};
+      if (!mv) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+      }
+      if constexpr (GAMMA) {
+        const float gm[8] = {ga[si][0].x, ga[si][0].y, ga[si][0].z, ga[si][0].w,
+                             ga[si][1].x, ga[si][1].y, ga[si][1].z, ga[si][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ssq += v[e] * v[e];
+          v[e] = v[e] * gm[e];
+        }
+      }
+      dm_bf16x8 hi, mid, lo;
+      split3x8(v, hi, mid, lo);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? wb[si][b] : make_uint4(0, 0, 0, 0));
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wv, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, wv, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wv, acc[b], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[w][b * 16 + r][lane] = acc[b][r];
+  sq[w][lane] = ssq;
+  __syncthreads();
+  // Wavefront w finishes values r = w, w + 4, ... of every block: rows
+  // m = 8 (r / 4) + 4 (lane / 32) + r % 4, weight row row[b].
+  for (int r = w; r < 16; r += NW) {
+    const int mo = 8 * (r >> 2) + 4 * kg + (r & 3);
+    if (mo >= M) continue;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float a = red[0][b * 16 + r][lane];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) a += red[v][b * 16 + r][lane];
+      if (rv[b]) g.part[(sp * M + mo) * g.N + row[b]] = a;
+    }
+  }
+  if (GAMMA && t == 0 && tid < M) {
+    float ss = sq[0][tid] + sq[0][tid + 32];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) ss += sq[v][tid] + sq[v][tid + 32];
+    g.part[S * M * g.N + sp * M + tid] = ss;
+  }
+}
+
+// The split products' partials added in split order, then the mode's
+// epilogue (RMS, residual, SiLU-mul, RoPE and the cache write): one thread
+// per (activation row, output pair).
+template <int MODE>
+__global__ void __launch_bounds__(256) decode_fold_kernel(DecodeArgs g, int M) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= M * g.npairs) return;
+  const int64_t m = i / g.npairs, p = i - m * g.npairs;
+  const PairRows q = pair_rows<MODE>(g, p);
+  const int S = g.split;
+  float y0 = g.part[m * g.N + q.r0], y1 = q.has1 ? g.part[m * g.N + q.r1] : 0.0f;
+  for (int s = 1; s < S; ++s) {
+    y0 += g.part[(s * M + m) * g.N + q.r0];
+    if (q.has1) y1 += g.part[(s * M + m) * g.N + q.r1];
+  }
+  if (g.gamma) {
+    const float *ssq = g.part + static_cast<int64_t>(S) * M * g.N;
+    float ss = ssq[m];
+    for (int s = 1; s < S; ++s) ss += ssq[s * M + m];
+    const float rms = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
+    y0 = y0 / rms;
+    y1 = y1 / rms;
+  }
+  pair_write<MODE>(g, q, m, y0, y1);
+}
+
+// Splits for the split-k form, or 1: grids of fewer than 32 tiles whose
+// blocks carry paired rows (the q|k|v heads) or long rows (k >= 1024); each
+// split at most four wavefronts' STEPS steps.  (Splitting the o and gate|up
+// products too: batch-32 decode 1.755 -> 1.735 ms a step, batch 8 1.371 ->
+// 1.419.)
+template <int MODE>
+static int dsplit_count(int64_t M, const DecodeArgs &g) {
+  if (M <= 2 || g.K % 16) return 1;
+  if (MODE == DM_QKV && g.d != 64) return 1;
+  constexpr int NB = MODE == DM_PLAIN ? 1 : 2;
+  const int64_t tiles = MODE == DM_PLAIN ? (g.N + 31) / 32 : (MODE == DM_SILU_MUL ? (g.inter + 31) / 32 : g.H + 2 * g.KVH);
+  if (tiles >= 32 || !(NB == 2 || g.K >= 1024)) return 1;
+  const int64_t nsteps = g.K / 16, per = DSPLIT_WAVES * (NB == 1 ? 6 : 3);
+  int64_t S = (nsteps + per - 1) / per;
+  if (S < 2) return 1;
+  if (S > 8) S = 8;
+  return static_cast<int>(S);
+}
+
 // Steps a wavefront takes for k = 16 * nsteps, or 0 past what the registers
 // hold without spilling: the loads of every step are in flight at once (4 NB
 // + 8, plus 8 with a gain, registers a step) within the 128 registers of four
@@ -590,6 +761,23 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   const int steps = dmfma_steps(g.K, NB, g.gamma != nullptr);
   if (!steps) return false;
   const int64_t tiles = MODE == DM_PLAIN ? (g.N + 31) / 32 : (MODE == DM_SILU_MUL ? (g.inter + 31) / 32 : g.H + 2 * g.KVH);
+  if (g.split > 1 && g.part) {
+    // Per split: four wavefronts of STEPS steps cover ceil(nsteps / S) steps.
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(g.split));
+    const int per = static_cast<int>((g.K / 16 + g.split - 1) / g.split);
+    const int Mi = static_cast<int>(M);
+    if constexpr (NB == 1) {
+      if (per > DSPLIT_WAVES * 6) return false;
+      if (g.gamma) decode_mfma_split_kernel<MODE, 6, 1, true><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      else decode_mfma_split_kernel<MODE, 6, 1, false><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+    } else {
+      if (per > DSPLIT_WAVES * 3) return false;
+      if (g.gamma) decode_mfma_split_kernel<MODE, 3, 2, true><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      else decode_mfma_split_kernel<MODE, 3, 2, false><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+    }
+    decode_fold_kernel<MODE><<<static_cast<unsigned>((M * g.npairs + 255) / 256), 256, 0, st>>>(g, Mi);
+    return true;
+  }
   const unsigned grid = static_cast<unsigned>(tiles);
   if (g.gamma) launch_dmfma<MODE, NB, true>(steps, grid, g, static_cast<int>(M), st);
   else launch_dmfma<MODE, NB, false>(steps, grid, g, static_cast<int>(M), st);
@@ -617,6 +805,19 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The split-k form's partials in the context's scratch, when the shape takes
+// it (without scratch the unsplit form runs).
+template <int MODE>
+static void split_setup(Ctx *ctx, int64_t M, DecodeArgs &g) {
+  g.split = dsplit_count<MODE>(M, g);
+  g.part = nullptr;
+  if (g.split > 1) {
+    const size_t bytes = (static_cast<size_t>(g.split) * M * g.N + static_cast<size_t>(g.split) * M) * sizeof(float);
+    g.part = static_cast<float *>(scratch(ctx, bytes));
+    if (!g.part) g.split = 1;
+  }
+}
 
 // Shared checks: x [M <= 32, K] F32, w [N, K] BF16, K % 8 == 0, gamma [1, K].
 static int check_common(mi_ctx *ctx, const Buffer *xb, const Buffer *wb, const Buffer *gb, const char *what) {
@@ -681,9 +882,11 @@ extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_i
     if (silu_mul) {
       g.inter = ncols;
       g.npairs = ncols;
+      split_setup<DM_SILU_MUL>(ctx, M, g);
       launch_decode<DM_SILU_MUL>(M, g, ctx->stream);
     } else {
       g.npairs = (N + 1) / 2;
+      split_setup<DM_PLAIN>(ctx, M, g);
       launch_decode<DM_PLAIN>(M, g, ctx->stream);
     }
   }
@@ -760,6 +963,7 @@ static int norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_q
   g.kv16 = kb->elem == MI_BF16 ? 1 : 0;
   g.pos_dev = pos_dev;
   g.flags = flags(ctx);
+  split_setup<DM_QKV>(ctx, M, g);
   launch_decode<DM_QKV>(M, g, ctx->stream);
   s = check_launch(ctx, "norm_qkv_rope");
   if (s) {
