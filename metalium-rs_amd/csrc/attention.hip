@@ -33,6 +33,7 @@
 #include <atomic>
 #include <cfloat>
 #include <mutex>
+#include <type_traits>
 
 namespace mi {
 
@@ -263,37 +264,79 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
 }
 
 // ------------------------------------------- long prompts: matrix cores
-// Causal attention of many new positions (a prefill) on the F32 matrix cores
-// (v_mfma_f32_32x32x2f32), flash style: one block per (sequence, kv head,
-// two runs of 32 query positions), one wavefront per query head of the group; the
-// scores never leave registers.  Per block of 32 keys (staged in LDS, shared
-// by the group's heads) a wavefront forms S^T = K Q^T -- keys as the rows of
-// its 32 x 32 accumulator, its lane's query as the column, so each query's
-// keys sit in one lane and its partner (lane ^ 32) -- scales and masks it,
-// takes the running softmax (max clamped as the composition's; the sum of a
-// causal row is never empty; exponentials in base 2, v_exp_f32, within a few
-// ulps), and adds V^T P^T to its 64 x 32 output
-// accumulator: P^T's accumulator registers are the B operand as they lie,
-// once the value rows are read in the order the accumulator holds the keys
-// (register r: keys 8 (r / 4) + r % 4 and that + 4, one per half-wave).  The
-// contraction over d pairs d with d + 32 across the half-waves, so a lane's
-// query values and key row segments are contiguous (float4 reads).  F32
-// products and sums; only the order of the sums differs from the
-// composition.  D = 64.
+// Causal attention of many new positions (a prefill) flash style on the
+// matrix cores: one block per (sequence, kv head, two runs of 32 query
+// positions -- a long and a short run of keys paired, so causal blocks carry
+// equal work), one wavefront per query head of the group; the scores never
+// leave registers.  Per block of 32 keys (staged in LDS, shared by the
+// group's heads, the next block's loads in flight under the current one) a
+// wavefront forms S^T = K Q^T -- keys as the rows of its 32 x 32
+// accumulator, its lane's query as the column, so each query's keys sit in
+// one lane and its partner (lane ^ 32) -- scales and masks it, takes the
+// running softmax (max clamped as the composition's; the sum of a causal row
+// is never empty; exponentials in base 2, v_exp_f32, within a few ulps,
+// against a reference max allowed to trail the running max by < 8, so the
+// accumulators are rescaled only when the max outruns it), and adds V^T P^T
+// to its 64 x 32 output accumulator.  Only the order of the sums differs from
+// the composition.  D = 64.
 constexpr int FLASH_MIN_T = 64;  // new positions per sequence that take it
 constexpr int64_t FLASH_MIN_BLOCKS = 256;
-constexpr int FLASH_KS = 68;     // LDS row pitch (floats) of the key block
-constexpr int FLASH_VS = 72;     // ... and the value block
 
 typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
 
+// The products run on the BF16 matrix cores (v_mfma_f32_32x32x16_bf16:
+// 16 K multiply-adds a 32-cycle instruction, against 2 K a 64-cycle one on
+// F32: 138.5 -> 122.5 us a layer for the batch-32 prompt, the rest being the
+// staging, the splits and the softmax).  Every F32 operand is split into three BF16 parts (head truncated,
+// remainders rounded to nearest: |a - hi - mid - lo| <= 2^-25 |a|) and each
+// product taken as the part products down to 2^-16 of its size -- hi hi, hi
+// mid, mid hi, hi lo, mid mid, lo hi -- so the scores and P V keep the F32
+// products' accuracy; a BF16 cache holds its keys and values exactly: one
+// part, three products.  The key and value blocks are split as they are
+// staged into LDS (keys [32 keys][64 d], values transposed [64 d][32 keys],
+// one array per part), the queries once per run into registers, P^T from
+// its accumulator registers after the softmax.  The contraction over keys
+// for V^T P^T takes k slots in the order P^T's registers hold the keys
+// (slot i of half-wave h: key 16 j + 8 (i / 4) + 4 h + i % 4), so P^T is
+// the B operand as it lies; the value fragments are read in that order.
+// D = 64.
+typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 fl_bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int FL3_KS = 72;  // LDS row pitch (bf16) of a key part [32][64]
+constexpr int FL3_VS = 40;  // ... of a value part, transposed [64][32]
+
+__device__ __forceinline__ void fl_split(float v, __bf16 &hi, __bf16 &mid, __bf16 &lo) {
+  const uint32_t hb = __float_as_uint(v) & 0xffff0000u;
+  const float r1 = v - __uint_as_float(hb);
+  const bool fin = r1 == r1;  // an infinite or NaN value: its head carries it alone
+  const __bf16 m = static_cast<__bf16>(fin ? r1 : 0.0f);
+  const float r2 = fin ? r1 - static_cast<float>(m) : 0.0f;
+  hi = __builtin_bit_cast(__bf16, static_cast<uint16_t>(hb >> 16));
+  mid = m;
+  lo = static_cast<__bf16>(r2);
+}
+
+// The part products of one k step: A parts a[], B parts b[] (NA and NB of them).
+template <int NA, int NB>
+__device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const fl_bf16x8 (&b)[NB], flash_f32x16 c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], c, 0, 0, 0);
+  if constexpr (NB > 1) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], c, 0, 0, 0);
+  if constexpr (NA > 1) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], c, 0, 0, 0);
+  if constexpr (NB > 2) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], c, 0, 0, 0);
+  if constexpr (NA > 1 && NB > 1) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], c, 0, 0, 0);
+  if constexpr (NA > 2) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], c, 0, 0, 0);
+  return c;
+}
+
 template <int G, typename KV>
-__global__ void __launch_bounds__(G * 64) __attribute__((amdgpu_waves_per_eu(3)))
-flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int64_t T, int64_t H, int64_t KVH,
-                     int64_t pos0, int64_t maxc, float scale) {
+__global__ void __launch_bounds__(G * 64)
+flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int64_t T, int64_t H, int64_t KVH,
+                      int64_t pos0, int64_t maxc, float scale) {
   constexpr int D = 64, NT = G * 64;
-  __shared__ __attribute__((aligned(16))) float ks[2 * 32 * FLASH_KS];
-  __shared__ __attribute__((aligned(16))) float vs[2 * 32 * FLASH_VS];
+  constexpr bool EXACT = sizeof(KV) == 2;  // a BF16 cache: one part
+  constexpr int KP = EXACT ? 1 : 3;
+  __shared__ __attribute__((aligned(16))) __bf16 ks[2][KP][32 * FL3_KS];
+  __shared__ __attribute__((aligned(16))) __bf16 vs[2][KP][64 * FL3_VS];
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
   const int64_t bj = blockIdx.y;  // (sequence, kv head)
   const int64_t j = bj % KVH, b = bj / KVH;
@@ -303,10 +346,6 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
   const float scale2 = scale * 1.4426950408889634f;
   const KV *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
   const int ctx32 = static_cast<int>(ctx);  // the host keeps a cache item below 2^31 / D rows
-  // A block takes query blocks x and nqb - 1 - x in turn: a long and a short
-  // run of keys, so every block has about the same work (causal attention's
-  // blocks otherwise range from 1 to nqb key blocks) and the grid runs as one
-  // even wave.
   const int64_t nqb = (T + 31) / 32;
   for (int pass = 0; pass < 2; ++pass) {
     const int64_t qb = pass == 0 ? static_cast<int64_t>(blockIdx.x) : nqb - 1 - blockIdx.x;
@@ -314,49 +353,76 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
     const int64_t p0 = qb * 32, p = p0 + n;
     const bool live = p < T;
     const int64_t pq = live ? p : T - 1;
-    const int64_t qpos = pos0 + pq;  // the lane's query position in the cache
-    // Q^T as the B operand: step s holds q[p][s + 32 half].
-    float qv[32];
+    const int64_t qpos = pos0 + pq;
+    // Q^T as the B operand of step s: q[p][16 s + 8 half .. + 7], three parts.
+    fl_bf16x8 qp[4][3];
     {
-      const float *qrow = q + (b * T + pq) * H * D + h * D + 32 * half;
+      const float *qrow = q + (b * T + pq) * H * D + h * D + 8 * half;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float4 v = *reinterpret_cast<const float4 *>(qrow + 4 * c);
-        qv[4 * c] = v.x; qv[4 * c + 1] = v.y; qv[4 * c + 2] = v.z; qv[4 * c + 3] = v.w;
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const float4 v0 = *reinterpret_cast<const float4 *>(qrow + 16 * s2);
+        const float4 v1 = *reinterpret_cast<const float4 *>(qrow + 16 * s2 + 4);
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          __bf16 a0, a1, a2;
+          fl_split(vv[e], a0, a1, a2);
+          qp[s2][0][e] = a0;
+          qp[s2][1][e] = a1;
+          qp[s2][2][e] = a2;
+        }
       }
     }
-    flash_f32x16 o0, o1;  // O^T: d 0..31 and 32..63 (rows) by the 32 queries (columns)
+    flash_f32x16 o0, o1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) { o0[r] = 0.0f; o1[r] = 0.0f; }
-    float m = -INFINITY, l = 0.0f;  // running max (base 2) and sum
-    const int64_t kend = pos0 + (p0 + 32 < T ? p0 + 32 : T);  // keys this block's queries can see
-    // Key and value blocks go through registers into two LDS buffers in turn:
-    // the next block's loads are in flight while the current one is used.
-    constexpr int PER = (32 * 16 + NT - 1) / NT;  // float4 of a block per thread
-    float4 kr[PER], vr[PER];
-    // Loads are unconditional (a conditional load compiles to a branch whose
-    // join waits for it): rows past the context read the context's last row
-    // instead -- their scores are masked to -inf, so their values meet only
-    // zero weights -- and a thread's surplus slots reload a row it also loads
-    // and are not staged.
+    float m = -INFINITY, l = 0.0f;
+    const int64_t kend = pos0 + (p0 + 32 < T ? p0 + 32 : T);
+    // Key and value blocks: 512 groups of 4 values each (key e / 16, d 4 (e % 16)),
+    // loaded into registers for the next block while the current one is used.
+    constexpr int PER = (32 * 16 + NT - 1) / NT;
+    using Raw = typename std::conditional<EXACT, uint2, float4>::type;
+    Raw kr[PER], vr[PER];
     auto fetch = [&](int64_t j0) {
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int e0 = tid + u * NT, e = e0 < 32 * 16 ? e0 : tid;
         const int r = static_cast<int>(j0) + (e >> 4) < ctx32 ? static_cast<int>(j0) + (e >> 4) : ctx32 - 1;
         const int off = r * D + (e & 15) * 4;
-        kr[u] = f32x4_get(K + off);
-        vr[u] = f32x4_get(V + off);
+        kr[u] = *reinterpret_cast<const Raw *>(K + off);
+        vr[u] = *reinterpret_cast<const Raw *>(V + off);
       }
     };
     auto stage = [&](int buf) {
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int e = tid + u * NT;
-        const int r = e >> 4, c4 = (e & 15) * 4;
         if (e < 32 * 16) {
-          *reinterpret_cast<float4 *>(ks + buf * 32 * FLASH_KS + r * FLASH_KS + c4) = kr[u];
-          *reinterpret_cast<float4 *>(vs + buf * 32 * FLASH_VS + r * FLASH_VS + c4) = vr[u];
+          const int r = e >> 4, c4 = (e & 15) * 4;
+          if constexpr (EXACT) {
+            *reinterpret_cast<uint2 *>(&ks[buf][0][r * FL3_KS + c4]) = kr[u];
+            const uint16_t v4[4] = {static_cast<uint16_t>(vr[u].x & 0xffffu), static_cast<uint16_t>(vr[u].x >> 16),
+                                    static_cast<uint16_t>(vr[u].y & 0xffffu), static_cast<uint16_t>(vr[u].y >> 16)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vs[buf][0][(c4 + i) * FL3_VS + r] = __builtin_bit_cast(__bf16, v4[i]);
+          } else {
+            const float k4[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+            const float v4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+            fl_bf16x4 kp0, kp1, kp2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              __bf16 a0, a1, a2;
+              fl_split(k4[i], a0, a1, a2);
+              kp0[i] = a0; kp1[i] = a1; kp2[i] = a2;
+              fl_split(v4[i], a0, a1, a2);
+              vs[buf][0][(c4 + i) * FL3_VS + r] = a0;
+              vs[buf][1 % KP][(c4 + i) * FL3_VS + r] = a1;
+              vs[buf][2 % KP][(c4 + i) * FL3_VS + r] = a2;
+            }
+            *reinterpret_cast<fl_bf16x4 *>(&ks[buf][0][r * FL3_KS + c4]) = kp0;
+            *reinterpret_cast<fl_bf16x4 *>(&ks[buf][1 % KP][r * FL3_KS + c4]) = kp1;
+            *reinterpret_cast<fl_bf16x4 *>(&ks[buf][2 % KP][r * FL3_KS + c4]) = kp2;
+          }
         }
       }
     };
@@ -368,25 +434,19 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
       const bool more = j0 + 32 < kend;
       if (more) fetch(j0 + 32);
 
-      // S^T = K Q^T over d (step s: d = s for the first half-wave, s + 32 for
-      // the second).
+      // S^T = K Q^T over d: step s takes d 16 s .. 16 s + 15, half-wave h
+      // supplying d 16 s + 8 h .. + 7.
       flash_f32x16 st;
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[r] = 0.0f;
-      const float *krow = ks + buf * 32 * FLASH_KS + n * FLASH_KS + 32 * half;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
-        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv[4 * c], st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv[4 * c + 1], st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv[4 * c + 2], st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv[4 * c + 3], st, 0, 0, 0);
+      for (int s2 = 0; s2 < 4; ++s2) {
+        fl_bf16x8 ka[KP];
+#pragma unroll
+        for (int pp = 0; pp < KP; ++pp)
+          ka[pp] = *reinterpret_cast<const fl_bf16x8 *>(&ks[buf][pp][n * FL3_KS + 16 * s2 + 8 * half]);
+        st = fl_mfma<KP, 3>(ka, qp[s2], st);
       }
-      // Scale and mask (keys after the query's position, or past the context:
-      // only a block reaching past the block's first query has any), then the
-      // running softmax of the lane's query over its keys.  The scores are
-      // kept in base 2 (scale * log2 e folded into one product), so each
-      // exponential is one exp2.
       float mx = -INFINITY;
       if (j0 + 31 <= pos0 + p0) {
 #pragma unroll
@@ -395,7 +455,7 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
           mx = max_nan(mx, st[r]);
         }
       } else {
-        const int lim = static_cast<int>((qpos < ctx - 1 ? qpos : ctx - 1) - j0);  // last visible key offset
+        const int lim = static_cast<int>((qpos < ctx - 1 ? qpos : ctx - 1) - j0);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kofs = 8 * (r >> 2) + 4 * half + (r & 3);
@@ -404,11 +464,6 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
         }
       }
       mx = max_nan(mx, __shfl_xor(mx, 32, 64));
-      // The exponentials are taken against a reference m that trails the
-      // running max by less than 8 (weights up to 2^8, far from F32's range):
-      // the accumulated sums are rescaled only when the max outruns it, which
-      // after the first block is rare -- the same quotient, without a rescale
-      // of the output accumulators every block.
       if (__any(!(mx <= m + 8.0f))) {
         float mnew = max_nan(m, mx);
         mnew = isnan(mnew) ? mnew : (mnew > -FLT_MAX ? mnew : -FLT_MAX);
@@ -419,29 +474,40 @@ flash_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int
         m = mnew;
       }
       float ls = 0.0f;
+      fl_bf16x8 pb[2][3];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = __builtin_amdgcn_exp2f(st[r] - m);
-        st[r] = e;
         ls += e;
+        __bf16 a0, a1, a2;
+        fl_split(e, a0, a1, a2);
+        pb[r >> 3][0][r & 7] = a0;
+        pb[r >> 3][1][r & 7] = a1;
+        pb[r >> 3][2][r & 7] = a2;
       }
       ls += __shfl_xor(ls, 32, 64);
       l += ls;
-      // O^T += V^T P^T: step r contracts keys 8 (r / 4) + r % 4 (first
-      // half-wave) and that + 4 (second), P^T's register r as it lies.
+      // O^T += V^T P^T: step s2 contracts the keys of P^T's registers 8 s2 .. 8 s2 + 7.
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float *vrow = vs + buf * 32 * FLASH_VS + (8 * (r >> 2) + 4 * half + (r & 3)) * FLASH_VS + n;
-        o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[0], st[r], o0, 0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32], st[r], o1, 0, 0, 0);
+      for (int s2 = 0; s2 < 2; ++s2) {
+        fl_bf16x8 va0[KP], va1[KP];
+#pragma unroll
+        for (int pp = 0; pp < KP; ++pp) {
+          const __bf16 *v0 = &vs[buf][pp][n * FL3_VS + 16 * s2 + 4 * half];
+          const __bf16 *v1 = &vs[buf][pp][(32 + n) * FL3_VS + 16 * s2 + 4 * half];
+          const fl_bf16x4 a = *reinterpret_cast<const fl_bf16x4 *>(v0), c = *reinterpret_cast<const fl_bf16x4 *>(v0 + 8);
+          const fl_bf16x4 a1 = *reinterpret_cast<const fl_bf16x4 *>(v1), c1 = *reinterpret_cast<const fl_bf16x4 *>(v1 + 8);
+          va0[pp] = fl_bf16x8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+          va1[pp] = fl_bf16x8{a1[0], a1[1], a1[2], a1[3], c1[0], c1[1], c1[2], c1[3]};
+        }
+        o0 = fl_mfma<KP, 3>(va0, pb[s2], o0);
+        o1 = fl_mfma<KP, 3>(va1, pb[s2], o1);
       }
-      // The other buffer was last read before the previous barrier.
       if (more) stage(buf ^ 1);
       __syncthreads();
     }
     if (live) {
       const float den = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
-      // Lane (n, half), register r of tile t: d = 32 t + 8 (r / 4) + 4 half + r % 4.
       float *orow = out + (b * T + p) * H * D + h * D + 4 * half;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -458,7 +524,7 @@ template <int G, typename KV>
 void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch, int64_t T,
                   int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
   const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
-  flash_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
+  flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
 }
 
 template <typename KV>
