@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
 // to its 64 x 32 output accumulator.  Only the order of the sums differs from
 // the composition.  D = 64.
 constexpr int FLASH_MIN_T = 64;  // new positions per sequence that take it
-constexpr int64_t FLASH_MIN_BLOCKS = 256;
+constexpr int64_t FLASH_MIN_BLOCKS = 128;
 
 typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -690,9 +690,10 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   P->v = vb->ptr;
   P->kv16 = kb->elem == MI_BF16;
   P->D = D; P->G = G; P->maxc = maxc; P->items = items; P->S = S; P->chunk = chunk;
-  // The matrix-core kernel once its (32 positions, sequence, kv head) blocks
-  // fill the chip; fewer sequences keep the key-chunked kernel (a 512-token
-  // prompt at batch 1: 48 blocks, slower than 30 key chunks a position).
+  // The matrix-core kernel from 128 (32 positions, sequence, kv head)
+  // blocks; fewer keep the key-chunked kernel (512-token prompts: batch 1,
+  // 48 blocks, 4.27 ms against 3.92 on the chunked kernel; batch 4, 192
+  // blocks, 8.0 against 10.9).
   P->flash = !pos_dev && span == pos0 + t && D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535 &&
              (t + 31) / 32 * batch * kv_heads >= FLASH_MIN_BLOCKS;
   P->pos = AttPos{pos0, pos_dev, span, flags(ctx)};

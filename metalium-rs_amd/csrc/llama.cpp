@@ -99,7 +99,7 @@ constexpr int64_t kFusedAttentionLongMaxBatch = 4;
 // New positions (and blocks of 32 positions x sequences x kv heads) from
 // which mi_attention_rows runs 64-wide heads on the matrix cores (its flash
 // kernel).
-constexpr int64_t kFlashMinT = 64, kFlashMinBlocks = 256;
+constexpr int64_t kFlashMinT = 64, kFlashMinBlocks = 128;
 // Largest batch whose decode step takes the fused projections, and whose
 // head is one fused norm + projection launch (mi_norm_matvec: the GEMV up to 2
 // rows, the matrix-core form above; beyond kFusedHeadMaxBatch the head is a

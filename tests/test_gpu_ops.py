@@ -801,7 +801,7 @@ def attention_ref(q, kc, vc, batch, t, heads, kvh, pos0, scale):
     (1, 1100, 9, 3, 64, 0, 1100),    # a prompt past one chunk at SmolLM2's heads: empty chunks too
     (1, 63, 9, 3, 64, 0, 64),        # just below the matrix-core kernel: the chunk kernel
     (32, 96, 9, 3, 64, 32, 160),     # 64+ positions filling the chip: the matrix-core (flash) kernel
-    (40, 70, 8, 1, 64, 5, 80),       # flash: 8 heads a group, a partial last query block
+    (48, 70, 8, 1, 64, 5, 80),       # flash: 8 heads a group, a partial last query block
     (64, 64, 2, 2, 64, 0, 64),       # flash: no grouping, the whole cache
 ])
 def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
@@ -823,7 +823,7 @@ def test_attention_rows(engine, batch, t, heads, kvh, D, pos0, maxc):
     (3, 16, 8, 1, 128, 30, 64),      # 128-wide heads, 8 a group
     (1, 512, 9, 3, 64, 0, 640),      # a 512-token prompt at batch 1
     (32, 96, 9, 3, 64, 32, 160),     # the matrix-core (flash) kernel
-    (40, 70, 8, 1, 64, 5, 80),       # flash, a partial last query block
+    (48, 70, 8, 1, 64, 5, 80),       # flash, a partial last query block
 ])
 def test_attention_rows_bf16_caches(engine, batch, t, heads, kvh, D, pos0, maxc):
     # The performance contract's BF16 caches: widened exactly as loaded, so
