@@ -445,6 +445,23 @@ int mi_norm_qkv_rope_at(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
                         mi_id w_qkv, mi_id cos_table, mi_id sin_table,
                         int64_t heads, int64_t kv_heads, mi_id pos,
                         mi_id k_cache, mi_id v_cache, mi_id *q_out);
+/* A decode step's attention up to its rows, in one call: mi_norm_qkv_rope
+ * (or _at; the new key and value stored into the caches at the position)
+ * then mi_attention_rows_at over the keys up to and including it (t = 1),
+ * returning the attention rows [M, heads * d] F32 -- the reference's
+ * attention block from its normed input to the attention output (crates/
+ * tt-models/src/llama.rs:380-470), no Engine counterpart.  pos: a [1, 1]
+ * I32 device position, or 0 for the immediate pos0; span as
+ * mi_attention_rows_at's.  Up to 2 sequences with 64-wide heads, a gain and
+ * k a multiple of 32 up to 1024: one launch forms each head's queries, the
+ * new key and value rows and the key chunks' partials over the earlier
+ * positions, and a combine adds the new key as one more chunk -- the two
+ * calls' values up to the order of the sums.  Otherwise those two calls. */
+int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
+                          mi_id w_qkv, mi_id cos_table, mi_id sin_table,
+                          int64_t heads, int64_t kv_heads, mi_id pos,
+                          int64_t pos0, int64_t span, mi_id k_cache,
+                          mi_id v_cache, float scale, mi_id *out);
 /* silu(gate) * up over the halves of a fused gate|up product: gate_up
  * [rows, 2 i] F32 -> [rows, i] of out_elem (the reference's MLP, crates/
  * tt-models/src/llama.rs:494-498, on the two row blocks of its gate|up

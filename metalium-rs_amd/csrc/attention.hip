@@ -70,9 +70,7 @@ __device__ __forceinline__ void dots(const float4 (&qv)[G], float4 kv, float (&p
 #pragma unroll
   for (int g = 0; g < G; ++g) part[g] = (qv[g].x * kv.x + qv[g].y * kv.y) + (qv[g].z * kv.z + qv[g].w * kv.w);
 #pragma unroll
-  for (int o = LPR / 2; o >= 1; o >>= 1)
-#pragma unroll
-    for (int g = 0; g < G; ++g) part[g] += __shfl_xor(part[g], o, 64);
+  for (int g = 0; g < G; ++g) part[g] = fold_sum<LPR>(part[g]);
 }
 
 // One (item, position, chunk).  DIRECT: the only chunk -- write normalised
@@ -146,7 +144,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
     float *row = scores + g * chunk;
     float m = -INFINITY;
     for (int64_t c = lane; c < len; c += 64) m = max_nan(m, row[c]);
-    m = wave_max(m);
+    m = fold_max<64>(m);
     m = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
     float sum = 0.0f;
     for (int64_t c = lane; c < len; c += 64) {
@@ -154,7 +152,7 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
       row[c] = e;
       sum += e;
     }
-    sum = wave_sum(sum);
+    sum = fold_sum<64>(sum);
     if (direct) {
       sum = isnan(sum) ? sum : (sum > FLT_MIN ? sum : FLT_MIN);
       for (int64_t c = lane; c < len; c += 64) row[c] = row[c] / sum;
@@ -195,14 +193,12 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
   }
   // Fold the row groups of a wavefront (lanes with equal sl), then the waves.
 #pragma unroll
-  for (int o = LPR; o < 64; o <<= 1)
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      acc[g].x += __shfl_xor(acc[g].x, o, 64);
-      acc[g].y += __shfl_xor(acc[g].y, o, 64);
-      acc[g].z += __shfl_xor(acc[g].z, o, 64);
-      acc[g].w += __shfl_xor(acc[g].w, o, 64);
-    }
+  for (int g = 0; g < G; ++g) {
+    acc[g].x = fold_columns<LPR>(acc[g].x);
+    acc[g].y = fold_columns<LPR>(acc[g].y);
+    acc[g].z = fold_columns<LPR>(acc[g].z);
+    acc[g].w = fold_columns<LPR>(acc[g].w);
+  }
   if (kk == 0)
 #pragma unroll
     for (int g = 0; g < G; ++g) *reinterpret_cast<float4 *>(red + (wave * G + g) * D + 4 * sl) = acc[g];
@@ -574,6 +570,371 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, cons
   }
 }
 
+
+// ------------------------------ a decode step's q|k|v and attention, fused
+// One new position per sequence (a decode step) of up to 2 sequences with
+// 64-wide heads: the RMSNorm of the hidden row, the q|k|v projection, RoPE,
+// the cache write and the attention's key chunks in one launch (the
+// composition mi_norm_qkv_rope then mi_attention_rows_at runs as two, the
+// second waiting for the first's queries and cache row).  Two kinds of block:
+//   - (sequence, query head, key chunk): the block forms its head's 64 query
+//     values itself -- the norm into LDS, a 64-row GEMV, RoPE -- and attends
+//     over its chunk of the keys before the new position, whose rows are
+//     requested at the start so they land under the GEMV;
+//   - (sequence, kv head, k or v): 64 rows of the new key (rotated) or value,
+//     stored into the cache at the position.
+// The new key itself is one more chunk, added by the combine pass: score
+// q . k_new (read back from the cache, as stored), weight 1, value v_new.
+// So every block of the launch is independent; the queries of the head's
+// first chunk block go to memory for the combine.  The 9 chunk blocks of a
+// head read the same 64 weight rows (74 KB for k = 576): the repeats come
+// from the caches.
+constexpr int DQA_MAX_CH = 32;  // 16-byte weight chunks a thread: k <= 1024 (CH: 8, 16, 24 or 32)
+constexpr int DQA_D = 64;
+
+struct DqaArgs {
+  const float *x;  // [B, K] F32 hidden rows
+  int64_t K;
+  const float *gamma;  // [1, K] RMSNorm gain
+  float eps;
+  const uint16_t *w;       // [(H + 2 KVH) 64, K] BF16: q, k, v heads
+  const float *cos, *sin;  // rotary tables, rows by position
+  void *kc, *vc;           // caches [B KVH maxc, 64], F32 or BF16
+  int64_t maxc;
+  int H, KVH, G, B;
+  AttPos pa;  // the new position
+  int64_t S, chunk;
+  float scale;
+  float *q;     // [B, H 64] rotated queries, for the combine
+  float *part;  // [B KVH][S][G (64 + 2)] chunk partials
+};
+
+// Block (256 threads): 64 rows (w0, each K BF16) times the normalised row in
+// LDS xn; thread t takes row t / 4 and the 16-byte chunks t % 4, + 4, ...;
+// the four partial sums fold over the row's lanes.  wr: the chunks, loaded
+// by dqa_wload.
+template <int CH>
+__device__ __forceinline__ void dqa_wload(const uint16_t *w0, int64_t K, uint4 (&wr)[CH]) {
+  const int tid = threadIdx.x, r = tid >> 2, kq = tid & 3;
+  const int64_t nch = K / 8;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int64_t c = kq + 4 * i;
+    wr[i] = *reinterpret_cast<const uint4 *>(w0 + r * K + 8 * (c < nch ? c : nch - 1));
+  }
+}
+template <int CH>
+__device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4 (&wr)[CH]) {
+  const int kq = threadIdx.x & 3;
+  const int64_t nch = K / 8;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int64_t c = kq + 4 * i;
+    if (c < nch) {
+      const float4 a0 = *reinterpret_cast<const float4 *>(xn + 8 * c);
+      const float4 a1 = *reinterpret_cast<const float4 *>(xn + 8 * c + 4);
+      const uint32_t u[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc += av[2 * e] * __uint_as_float(u[e] << 16);
+        acc += av[2 * e + 1] * __uint_as_float(u[e] & 0xffff0000u);
+      }
+    }
+  }
+  return fold_sum<4>(acc);
+}
+
+// A thread's operands of the norm and the rotation, requested with the
+// weights so neither phase waits for a round trip of its own: the float4 of
+// the hidden row b and of the gain at 4 tid (k <= 1024: one a thread), and
+// for tid < 32 the rotary table entries of pair (tid, tid + 32) at pos.
+struct DqaPre {
+  float4 x, gm;
+  float cs0, cs1, sn0, sn1;
+};
+__device__ __forceinline__ DqaPre dqa_pre(const DqaArgs &g, int64_t b, int64_t pos) {
+  const int tid = threadIdx.x;
+  constexpr int half = DQA_D / 2;
+  const int64_t k = 4 * tid < g.K ? 4 * tid : g.K - 4;
+  const int i = tid & (half - 1);
+  const float *cs = g.cos + pos * DQA_D, *sn = g.sin + pos * DQA_D;
+  return DqaPre{*reinterpret_cast<const float4 *>(g.x + b * g.K + k), *reinterpret_cast<const float4 *>(g.gamma + k),
+                cs[i], cs[i + half], sn[i], sn[i + half]};
+}
+
+// The hidden row normalised into LDS: xn[k] = (x[k] / rms) * gamma[k],
+// rms = sqrt(mean(x x) + eps) (the norm kernel's formula).
+__device__ __forceinline__ void dqa_norm(const DqaArgs &g, const DqaPre &pre, float *xn, float *red4) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool mine = 4 * tid < g.K;
+  const float4 v = pre.x;
+  float ss = mine ? v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w : 0.0f;
+  ss = fold_sum<64>(ss);
+  if (lane == 0) red4[wave] = ss;
+  __syncthreads();
+  const float rms = __fsqrt_rn((red4[0] + red4[1] + red4[2] + red4[3]) / static_cast<float>(g.K) + g.eps);
+  if (mine) {
+    const float4 gm = pre.gm;
+    *reinterpret_cast<float4 *>(xn + 4 * tid) =
+        make_float4((v.x / rms) * gm.x, (v.y / rms) * gm.y, (v.z / rms) * gm.z, (v.w / rms) * gm.w);
+  }
+  __syncthreads();
+}
+
+// RoPE of a 64-wide head in LDS (raw -> rot): the rotation of pair (i, i +
+// 32) as the decode projections apply it, the table entries from dqa_pre.
+__device__ __forceinline__ void dqa_rope(const DqaPre &pre, const float *raw, float *rot) {
+  const int tid = threadIdx.x;
+  constexpr int half = DQA_D / 2;
+  if (tid < half) {
+    const float y0 = raw[tid], y1 = raw[tid + half];
+    rot[tid] = __fadd_rn(__fmul_rn(y0, pre.cs0), __fmul_rn(y1, pre.sn0));
+    rot[tid + half] = __fadd_rn(__fmul_rn(y1, pre.cs1), __fmul_rn(y0, pre.sn1));
+  }
+}
+
+template <typename KV, int CH>
+__global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
+  constexpr int D = DQA_D, NW = 4, LPR = D / 4, KPW = 64 / LPR, U = 4, STEP = NW * KPW;
+  extern __shared__ float dqa_sm[];
+  float *xn = dqa_sm;            // [K]
+  float *qraw = xn + g.K;        // [64]
+  float *qrot = qraw + D;        // [64]
+  float *red4 = qrot + D;        // [4] (+4 pad)
+  float *scores = red4 + 8;      // [chunk]
+  float *red = scores + g.chunk; // [NW][D]
+  float *stat = red + NW * D;    // max, sum
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t natt = static_cast<int64_t>(g.B) * g.H * g.S;
+  const int64_t bid = blockIdx.x;
+
+  if (bid >= natt) {  // the new key or value row of (sequence, kv head)
+    const int64_t kb = bid - natt, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
+    uint4 wr[CH];
+    dqa_wload<CH>(g.w + ((g.H + which * g.KVH + j) * D) * g.K, g.K, wr);
+    int64_t pos = g.pa.pos0;
+    bool ok = true;
+    if (g.pa.dev) {
+      pos = *g.pa.dev;
+      ok = pos >= 0 && pos + 1 <= g.pa.span;
+      pos = ok ? pos : 0;
+    }
+    const DqaPre pre = dqa_pre(g, b, pos);
+    dqa_norm(g, pre, xn, red4);
+    const float y = dqa_dot<CH>(xn, g.K, wr);
+    if ((tid & 3) == 0) qraw[tid >> 2] = y;
+    __syncthreads();
+    if (!ok) return;  // refused position: no cache row (flag raised by the chunk blocks)
+    KV *dst = static_cast<KV *>(which ? g.vc : g.kc) + (bj * g.maxc + pos) * D;
+    if (which == 0) {
+      dqa_rope(pre, qraw, qrot);
+      __syncthreads();
+      if (tid < D) f32_put(dst + tid, qrot[tid]);
+    } else if (tid < D) {
+      f32_put(dst + tid, qraw[tid]);
+    }
+    return;
+  }
+
+  // (sequence, query head, key chunk)
+  const int64_t s = bid % g.S, bh = bid / g.S, hq = bh % g.H, b = bh / g.H;
+  const int64_t j = hq / g.G, gg = hq % g.G, bj = b * g.KVH + j;
+  const int64_t pos = att_pos0(g.pa, 1);
+  const int64_t lo = s * g.chunk, len = pos > lo ? (pos - lo < g.chunk ? pos - lo : g.chunk) : 0;
+  const int64_t PS = static_cast<int64_t>(g.G) * (D + 2);
+  float *pb = g.part + (bj * g.S + s) * PS;
+  if (len == 0 && s != 0) {  // past the keys: the empty chunk's statistics
+    if (tid == 0) {
+      pb[gg] = -FLT_MAX;
+      pb[g.G + gg] = 0.0f;
+    }
+    if (tid < D) pb[2 * g.G + gg * D + tid] = 0.0f;
+    return;
+  }
+  const KV *Kc = static_cast<const KV *>(g.kc) + (bj * g.maxc + lo) * D;
+  const KV *Vc = static_cast<const KV *>(g.vc) + (bj * g.maxc + lo) * D;
+  const int sl = lane % LPR, kk = lane / LPR;
+  const int64_t first = static_cast<int64_t>(wave) * KPW + kk, last = len > 0 ? len - 1 : 0;
+  // The first pass's key and value rows, then the weights: all in flight
+  // before the norm waits.
+  float4 kpre[U], vv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t c = first + u * STEP;
+    kpre[u] = f32x4_get(Kc + (c < len ? c : last) * D + 4 * sl);
+    vv[u] = f32x4_get(Vc + (c < len ? c : last) * D + 4 * sl);
+  }
+  uint4 wr[CH];
+  dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
+  const DqaPre pre = dqa_pre(g, b, pos);
+  dqa_norm(g, pre, xn, red4);
+  {
+    const float y = dqa_dot<CH>(xn, g.K, wr);
+    if ((tid & 3) == 0) qraw[tid >> 2] = y;
+  }
+  __syncthreads();
+  dqa_rope(pre, qraw, qrot);
+  __syncthreads();
+  if (s == 0 && tid < D) g.q[(b * g.H + hq) * D + tid] = qrot[tid];
+
+  // Scores, softmax statistics and P V of the chunk: the key-chunked
+  // kernel's steps for one query head.
+  const float4 qv[1] = {*reinterpret_cast<const float4 *>(qrot + 4 * sl)};
+  for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
+    float4 kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      kv[u] = c0 == first ? kpre[u] : f32x4_get(Kc + (c < len ? c : last) * D + 4 * sl);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      float pr[1];
+      dots<1, LPR>(qv, kv[u], pr);
+      if (sl == 0 && c < len) scores[c] = pr[0] * g.scale;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float m = -INFINITY;
+    for (int64_t c = lane; c < len; c += 64) m = max_nan(m, scores[c]);
+    m = fold_max<64>(m);
+    m = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
+    float sum = 0.0f;
+    for (int64_t c = lane; c < len; c += 64) {
+      const float e = expf(scores[c] - m);
+      scores[c] = e;
+      sum += e;
+    }
+    sum = fold_sum<64>(sum);
+    if (lane == 0) {
+      stat[0] = m;
+      stat[1] = sum;
+    }
+  }
+  __syncthreads();
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
+    if (c0 != first) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + u * STEP;
+        vv[u] = f32x4_get(Vc + (c < len ? c : last) * D + 4 * sl);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + u * STEP;
+      if (c < len) {
+        const float pg = scores[c];
+        acc.x += pg * vv[u].x;
+        acc.y += pg * vv[u].y;
+        acc.z += pg * vv[u].z;
+        acc.w += pg * vv[u].w;
+      }
+    }
+  }
+  acc.x = fold_columns<LPR>(acc.x);
+  acc.y = fold_columns<LPR>(acc.y);
+  acc.z = fold_columns<LPR>(acc.z);
+  acc.w = fold_columns<LPR>(acc.w);
+  if (kk == 0) *reinterpret_cast<float4 *>(red + wave * D + 4 * sl) = acc;
+  __syncthreads();
+  if (tid == 0) {
+    pb[gg] = stat[0];
+    pb[g.G + gg] = stat[1];
+  }
+  if (tid < D) {
+    float t = red[tid];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w * D + tid];
+    pb[2 * g.G + gg * D + tid] = t;
+  }
+}
+
+// The combine of a fused step: the S chunks of each (sequence, kv head) and
+// the new key as one more -- score scale (q . k_new) over the 64 lanes of a
+// wavefront, weight exp(score - max), value row v_new -- with the key-chunked
+// combine's formula: out = (sum_s w_s o_s + w_new v_new) / max(sum_s w_s
+// l_s + w_new, FLT_MIN), w_s = exp(m_s - max).
+template <int G, typename KV>
+__global__ void __launch_bounds__(256) attention_combine_new_kernel(const float *part, const float *q, const KV *kc,
+                                                                    const KV *vc, float *out, int64_t H, int64_t KVH,
+                                                                    int S, AttPos pa, int64_t maxc, float scale) {
+  constexpr int D = DQA_D;
+  extern __shared__ float st[];  // [S][2G] statistics, [S][G] weights, [G] den, [G] new score, [G] new weight
+  const int64_t bj = blockIdx.x, b = bj / KVH, j = bj % KVH;
+  constexpr int PS = G * (D + 2);
+  const float *pb = part + bj * S * static_cast<int64_t>(PS);
+  float *w = st + 2 * G * S;
+  float *den = w + G * S;
+  float *snew = den + G;
+  float *wnew = snew + G;
+  int64_t pos = pa.pos0;
+  if (pa.dev) {
+    const int64_t v = *pa.dev;
+    pos = v >= 0 && v + 1 <= pa.span ? v : 0;
+  }
+  const KV *kn = kc + (bj * maxc + pos) * D, *vn = vc + (bj * maxc + pos) * D;
+  // A thread's output elements e = tid + 256 i: their first CS chunks' values
+  // and the new value row's, requested with the statistics (one round trip
+  // for all but very long contexts).
+  constexpr int EP = (G * D + 255) / 256, CS = 16;
+  float ov[EP][CS], vd[EP];
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) ov[i][s] = pb[(s < S ? s : S - 1) * PS + 2 * G + ec];
+    if constexpr (sizeof(KV) == 2) vd[i] = bf16_bits_to_f32(vn[ec % D]);
+    else vd[i] = vn[ec % D];
+  }
+  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int g = wave; g < G; g += 4) {
+    float kd;
+    if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
+    else kd = kn[lane];
+    const float sc = fold_sum<64>(q[(b * H + j * G + g) * D + lane] * kd);
+    if (lane == 0) snew[g] = sc * scale;
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float M = snew[g];
+    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + g]);
+    float l = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float ws = expf(st[s * 2 * G + g] - M);
+      w[s * G + g] = ws;
+      l += ws * st[s * 2 * G + G + g];
+    }
+    const float wn = expf(snew[g] - M);
+    wnew[g] = wn;
+    l += wn;
+    den[g] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
+  }
+  __syncthreads();
+  float *dst = out + b * H * D + j * G * D;
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    if (e < G * D) {
+      const int g = e / D;
+      float num = 0.0f;
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+        if (s < S) num += w[s * G + g] * ov[i][s];
+      for (int s = CS; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
+      num += wnew[g] * vd[i];
+      dst[e] = num / den[g];
+    }
+  }
+}
+
 }  // namespace mi
 
 // The no-allocation form's partials (mi_attention_rows_into): a file-scope
@@ -809,4 +1170,152 @@ extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id
   }
   attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, scale);
   return check_launch(ctx, "attention_rows_into");
+}
+
+namespace mi {
+namespace {
+
+template <typename KV>
+void launch_dqa(hipStream_t st, const DqaArgs &g) {
+  const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.H * g.S + 2 * static_cast<int64_t>(g.B) * g.KVH);
+  const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + 8 + g.chunk + 4 * DQA_D + 2) * sizeof(float);
+  const int64_t ch = (g.K / 8 + 3) / 4;  // chunks a thread
+  if (ch <= 8) decode_qkv_attention_kernel<KV, 8><<<blocks, 256, lds, st>>>(g);
+  else if (ch <= 16) decode_qkv_attention_kernel<KV, 16><<<blocks, 256, lds, st>>>(g);
+  else if (ch <= 24) decode_qkv_attention_kernel<KV, 24><<<blocks, 256, lds, st>>>(g);
+  else decode_qkv_attention_kernel<KV, 32><<<blocks, 256, lds, st>>>(g);
+}
+
+template <typename KV>
+bool launch_combine_new(int64_t G, hipStream_t st, const DqaArgs &g, float *out) {
+  const unsigned items = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH);
+  const size_t lds = static_cast<size_t>(3 * G * g.S + 3 * G) * sizeof(float);
+  const KV *k = static_cast<const KV *>(g.kc), *v = static_cast<const KV *>(g.vc);
+  const int S = static_cast<int>(g.S);
+  switch (G) {
+#define MI_CN_G(gg)                                                                                          \
+  case gg:                                                                                                   \
+    attention_combine_new_kernel<gg, KV><<<items, 256, lds, st>>>(g.part, g.q, k, v, out, g.H, g.KVH, S, g.pa, \
+                                                                  g.maxc, g.scale);                          \
+    return true;
+    MI_CN_G(1) MI_CN_G(2) MI_CN_G(3) MI_CN_G(4) MI_CN_G(5) MI_CN_G(6) MI_CN_G(7) MI_CN_G(8)
+#undef MI_CN_G
+    default:
+      return false;
+  }
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                     mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0,
+                                     int64_t span, mi_id k_cache, mi_id v_cache, float scale, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, wb, w_qkv);
+  MI_BUF(ctx, cb, cos_table);
+  MI_BUF(ctx, sb, sin_table);
+  MI_BUF(ctx, kb, k_cache);
+  MI_BUF(ctx, vb, v_cache);
+  const Buffer *gb = nullptr;
+  if (gamma) {
+    gb = lookup(ctx, gamma);
+    if (!gb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)gamma);
+  }
+  const int32_t *pos_dev = nullptr;
+  if (pos) {
+    MI_BUF(ctx, pb, pos);
+    if (pb->elem != MI_I32 || pb->numel() != 1)
+      return fail(ctx, MI_E_ARG, "norm_qkv_attention: the position is %s [%lld, %lld], want I32 [1, 1]",
+                  elem_name(pb->elem), (long long)pb->rows, (long long)pb->cols);
+    pos_dev = static_cast<const int32_t *>(pb->ptr);
+  }
+  const int64_t B = xb->rows, K = xb->cols, D = kb->cols;
+  const int64_t G = kv_heads > 0 ? heads / kv_heads : 0;
+  const int64_t maxc = B > 0 && kv_heads > 0 ? kb->rows / (B * kv_heads) : 0;
+  // The fused launch: up to 2 sequences, 64-wide heads, k a multiple of 32
+  // up to 1024, a gain, aligned operands; else the two calls composed (which
+  // check every argument themselves).
+  const bool fused = B >= 1 && B <= 2 && D == DQA_D && K % 32 == 0 && K <= 32 * DQA_MAX_CH && gb &&
+                     xb->elem == MI_F32 && wb->elem == MI_BF16 && wb->cols == K && heads >= 1 && kv_heads >= 1 &&
+                     heads % kv_heads == 0 && G <= ATT_MAX_GROUP && wb->rows == (heads + 2 * kv_heads) * D &&
+                     kb->elem == vb->elem && elem_float(kb->elem) && vb->cols == D && vb->rows == kb->rows &&
+                     kb->rows % (B * kv_heads) == 0 && gb->elem == MI_F32 && gb->rows * gb->cols == K &&
+                     cb->elem == MI_F32 && sb->elem == MI_F32 && cb->cols == D && sb->cols == D &&
+                     cb->rows >= maxc && sb->rows >= maxc &&
+                     ((reinterpret_cast<uintptr_t>(xb->ptr) | reinterpret_cast<uintptr_t>(wb->ptr) |
+                       reinterpret_cast<uintptr_t>(gb->ptr)) & 15) == 0;
+  if (!fused) {
+    mi_id q = 0;
+    int s = pos_dev ? mi_norm_qkv_rope_at(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos,
+                                          k_cache, v_cache, &q)
+                    : mi_norm_qkv_rope(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos0,
+                                       k_cache, v_cache, &q);
+    if (s) return s;
+    s = mi_attention_rows_at(ctx, q, k_cache, v_cache, B, 1, heads, kv_heads, pos, pos0, span, scale, out);
+    mi_free(ctx, q);
+    return s;
+  }
+  if (span < 1 || span > maxc)
+    return fail(ctx, MI_E_ARG, "norm_qkv_attention: span %lld in a cache of %lld", (long long)span, (long long)maxc);
+  if (!pos_dev && (pos0 < 0 || pos0 + 1 > span))
+    return fail(ctx, MI_E_ARG, "norm_qkv_attention: position %lld beyond the span %lld", (long long)pos0,
+                (long long)span);
+  // The key chunks as mi_attention_rows_at plans them for one new position.
+  const int64_t items = B * kv_heads;
+  int64_t S = (span + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
+  const int64_t want = (ATT_TARGET_BLOCKS + items - 1) / items;
+  const int64_t min_chunk = items >= 64 ? 2 * ATT_MIN_CHUNK : ATT_MIN_CHUNK;
+  const int64_t cap = (span + min_chunk - 1) / min_chunk;
+  if (want > S) S = want < cap ? want : cap;
+  if (S < 1) S = 1;
+  const int64_t chunk = ((span + S - 1) / S + 3) / 4 * 4;
+  S = (span + chunk - 1) / chunk;
+  if (static_cast<size_t>(3 * G * S + 3 * G) * sizeof(float) > 65536 || B * heads * S + 2 * items > INT32_MAX)
+    return fail(ctx, MI_E_UNSUPPORTED, "norm_qkv_attention: context of %lld keys too long", (long long)span);
+  const size_t part_floats = static_cast<size_t>(items * S * G * (D + 2));
+  float *sc = static_cast<float *>(mi::scratch(ctx, (part_floats + static_cast<size_t>(B * heads * D)) * sizeof(float)));
+  if (!sc) return fail(ctx, MI_E_OOM, "norm_qkv_attention scratch");
+  mi_id id;
+  Buffer *ob;
+  int s = new_buffer(ctx, B, heads * D, MI_F32, &id, &ob);
+  if (s) return s;
+  DqaArgs g{};
+  g.x = static_cast<const float *>(xb->ptr);
+  g.K = K;
+  g.gamma = static_cast<const float *>(gb->ptr);
+  g.eps = eps;
+  g.w = static_cast<const uint16_t *>(wb->ptr);
+  g.cos = static_cast<const float *>(cb->ptr);
+  g.sin = static_cast<const float *>(sb->ptr);
+  g.kc = kb->ptr;
+  g.vc = vb->ptr;
+  g.maxc = maxc;
+  g.H = static_cast<int>(heads);
+  g.KVH = static_cast<int>(kv_heads);
+  g.G = static_cast<int>(G);
+  g.B = static_cast<int>(B);
+  g.pa = AttPos{pos0, pos_dev, span, flags(ctx)};
+  g.S = S;
+  g.chunk = chunk;
+  g.scale = scale;
+  g.part = sc;
+  g.q = sc + part_floats;
+  float *o = static_cast<float *>(ob->ptr);
+  if (kb->elem == MI_BF16) {
+    launch_dqa<uint16_t>(ctx->stream, g);
+    launch_combine_new<uint16_t>(G, ctx->stream, g, o);
+  } else {
+    launch_dqa<float>(ctx->stream, g);
+    launch_combine_new<float>(G, ctx->stream, g, o);
+  }
+  s = check_launch(ctx, "norm_qkv_attention");
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *out = id;
+  return MI_OK;
 }

@@ -423,6 +423,20 @@ inline Tensor norm_matvec(const Tensor &x, const Tensor *gamma, float eps, const
   return Tensor(x.ctx(), id, {x.rows(), n});
 }
 
+// The attention rows of one new position per sequence from the hidden rows
+// (mi_norm_qkv_attention): q|k|v, RoPE, the cache write and the attention.
+inline Tensor norm_qkv_attention(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv,
+                                 const Tensor &cos, const Tensor &sin, int64_t heads, int64_t kv_heads,
+                                 const Tensor *pos, int64_t pos0, int64_t span, const Tensor &k_cache,
+                                 const Tensor &v_cache, float scale) {
+  mi_id id;
+  check(x.ctx(), mi_norm_qkv_attention(x.ctx(), x.use(), gamma.use(), eps, w_qkv.use(), cos.use(), sin.use(), heads,
+                                       kv_heads, pos ? pos->use() : 0, pos0, span, k_cache.use(), v_cache.use(),
+                                       scale, &id),
+        "norm_qkv_attention");
+  return Tensor(x.ctx(), id, {x.rows(), heads * k_cache.cols()});
+}
+
 inline Tensor norm_qkv_rope(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv, const Tensor &cos,
                             const Tensor &sin, int64_t heads, int64_t kv_heads, int64_t pos, const Tensor &k_cache,
                             const Tensor &v_cache) {

@@ -114,29 +114,59 @@ __device__ __forceinline__ PairRows pair_rows(const DecodeArgs &g, int64_t p) {
   return q;
 }
 
-// Activation row m's outputs of the pair: y0, y1 its two products.
+// The epilogue's operands of activation row m, requested with the weights so
+// they have landed by the time the sums are folded: the residual values
+// (DM_PLAIN; without a residual a harmless read of the output), or the
+// rotary table entries at the position (DM_QKV; a position read on the
+// device and out of range reads row 0 and is refused at the write).
+struct PairPre {
+  float v0, v1, v2, v3;
+  int64_t pos;
+  bool ok;
+};
 template <int MODE>
-__device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &q, int64_t m, float y0, float y1) {
+__device__ __forceinline__ PairPre pair_pre(const DecodeArgs &g, const PairRows &q, int64_t m) {
+  PairPre e{0.0f, 0.0f, 0.0f, 0.0f, g.pos, true};
+  if constexpr (MODE == DM_PLAIN) {
+    const float *rp = g.resid ? g.resid : g.out;
+    e.v0 = rp[m * g.ldo + q.r0];
+    e.v1 = rp[m * g.ldo + (q.has1 ? q.r1 : q.r0)];
+  } else if constexpr (MODE == DM_QKV) {
+    if (g.pos_dev) {
+      const int64_t v = *g.pos_dev;
+      e.ok = v >= 0 && v < g.maxc;
+      e.pos = e.ok ? v : 0;
+    }
+    const int64_t half = g.d / 2;
+    const float *cs = g.cos + e.pos * g.d, *sn = g.sin + e.pos * g.d;
+    e.v0 = cs[q.hi];
+    e.v1 = cs[q.hi + half];
+    e.v2 = sn[q.hi];
+    e.v3 = sn[q.hi + half];
+  }
+  return e;
+}
+
+// Activation row m's outputs of the pair: y0, y1 its two products, the
+// epilogue's operands e from pair_pre.
+template <int MODE>
+__device__ __forceinline__ void pair_write_pre(const DecodeArgs &g, const PairRows &q, int64_t m, float y0, float y1,
+                                               const PairPre &e) {
   if constexpr (MODE == DM_PLAIN) {
     float *o = g.out + m * g.ldo;
-    o[q.r0] = g.resid ? __fadd_rn(g.resid[m * g.ldo + q.r0], y0) : y0;
-    if (q.has1) o[q.r1] = g.resid ? __fadd_rn(g.resid[m * g.ldo + q.r1], y1) : y1;
+    o[q.r0] = g.resid ? __fadd_rn(e.v0, y0) : y0;
+    if (q.has1) o[q.r1] = g.resid ? __fadd_rn(e.v1, y1) : y1;
   } else if constexpr (MODE == DM_SILU_MUL) {
     g.out[m * g.ldo + q.r0] = silu2(y0) * y1;
   } else {
-    const int64_t half = g.d / 2, hi = q.hi, head = q.head;
-    int64_t pos = g.pos;
-    if (g.pos_dev) {
-      pos = *g.pos_dev;
-      if (pos < 0 || pos >= g.maxc) {
-        if (m == 0 && hi == 0 && head == 0) atomicOr(g.flags, FLAG_INDEX_RANGE);
-        return;
-      }
+    const int64_t half = g.d / 2, hi = q.hi, head = q.head, pos = e.pos;
+    if (!e.ok) {
+      if (m == 0 && hi == 0 && head == 0) atomicOr(g.flags, FLAG_INDEX_RANGE);
+      return;
     }
     if (head < g.H + g.KVH) {
-      const float *cs = g.cos + pos * g.d, *sn = g.sin + pos * g.d;
-      const float o0 = __fadd_rn(__fmul_rn(y0, cs[hi]), __fmul_rn(y1, sn[hi]));
-      const float o1 = __fadd_rn(__fmul_rn(y1, cs[hi + half]), __fmul_rn(y0, sn[hi + half]));
+      const float o0 = __fadd_rn(__fmul_rn(y0, e.v0), __fmul_rn(y1, e.v2));
+      const float o1 = __fadd_rn(__fmul_rn(y1, e.v1), __fmul_rn(y0, e.v3));
       if (head < g.H) {
         float *o = g.out + m * g.ldo + head * g.d;
         o[hi] = o0;
@@ -150,7 +180,13 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
   }
 }
 
-template <int M, int MODE>
+template <int MODE>
+__device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &q, int64_t m, float y0, float y1) {
+  pair_write_pre<MODE>(g, q, m, y0, y1, pair_pre<MODE>(g, q, m));
+}
+
+// PRE: 16-byte chunks a lane requested up front (k <= 512 PRE), 2 or 4.
+template <int M, int MODE, int PRE = 4>
 __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
@@ -161,24 +197,52 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
 
   // The weight rows are independent of the norm: with K <= 2048 (four
   // 16-byte chunks a lane) all of them are requested first, so the norm's
-  // loads and reduction overlap the weights' HBM latency.
+  // loads and reduction overlap the weights' HBM latency.  Up to 2 rows the
+  // activation rows and the gain are requested with them into registers, so
+  // the norm and the products wait for one round trip instead of three.
   // The loads are unconditional, from clamped rows and columns: a load under
   // a condition compiles to a branch that waits for it before the next is
   // issued (0.956 -> 0.922 ms a batch-1 SmolLM2 decode step).  Without a
   // second row (a lone last row) the first is read twice and the second
   // product is discarded by pair_write.
-  constexpr int PRE = 4;
+  constexpr bool XPRE = M <= 2;
+  constexpr int XM = XPRE ? M : 1, XC = XPRE ? PRE : 1;
   uint4 pw0[PRE], pw1[PRE];
+  float4 px[XM][XC][2], pg[XC][2];
   const int64_t r1c = has1 ? r1 : r0;
-  if (g.K <= 512 * PRE) {
+  const bool pre_k = g.K <= 512 * PRE;
+  if (pre_k) {
+    const float *gp = g.gamma ? g.gamma : g.x;  // without a gain: read, never used
 #pragma unroll
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
       const int64_t kc = k < g.K ? k : g.K - 8;
       pw0[c] = *reinterpret_cast<const uint4 *>(g.w + r0 * g.K + kc);
       pw1[c] = *reinterpret_cast<const uint4 *>(g.w + r1c * g.K + kc);
+      if constexpr (XPRE) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          px[m][c][0] = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + kc);
+          px[m][c][1] = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + kc + 4);
+        }
+        pg[c][0] = *reinterpret_cast<const float4 *>(gp + kc);
+        pg[c][1] = *reinterpret_cast<const float4 *>(gp + kc + 4);
+      }
     }
   }
+  const PairPre pre = pair_pre<MODE>(g, q, lane < M ? lane : 0);
+  const bool inreg = XPRE && pre_k;
+
+  // Activation row m at k (chunk c of the prefetch): its 8 values.
+  auto xrow = [&](int m, int c, int64_t k, float4 &a0, float4 &a1) {
+    if (inreg) {
+      a0 = px[XPRE ? m : 0][XPRE ? c : 0][0];
+      a1 = px[XPRE ? m : 0][XPRE ? c : 0][1];
+    } else {
+      a0 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
+      a1 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k + 4);
+    }
+  };
 
   // RMSNorm of the activation rows: sqrt(mean(x x) + eps).
   float rms[M];
@@ -188,13 +252,22 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float ss = 0.0f;
-      for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
-        const float4 a0 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
-        const float4 a1 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k + 4);
+      auto sq = [&](int c, int64_t k) {
+        float4 a0, a1;
+        xrow(m, c, k, a0, a1);
         ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w;
         ss += a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
+      };
+      if (inreg) {
+#pragma unroll
+        for (int c = 0; c < PRE; ++c) {
+          const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
+          if (k < g.K) sq(c, k);
+        }
+      } else {
+        for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) sq(0, k);
       }
-      ss = wave_sum(ss);
+      ss = fold_sum<64>(ss);
       rms[m] = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
     }
   }
@@ -203,19 +276,29 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
   // One 8-wide k step: activations (normalised on the fly) times both rows.
-  auto step = [&](int64_t k, const float (&w0)[8], const float (&w1)[8]) {
+  auto step = [&](int c, int64_t k, const float (&w0)[8], const float (&w1)[8]) {
     float gm[8];
     if (g.gamma) {
-      const float4 g0 = *reinterpret_cast<const float4 *>(g.gamma + k);
-      const float4 g1 = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
+      float4 g0, g1;
+      if (inreg) {
+        g0 = pg[XPRE ? c : 0][0];
+        g1 = pg[XPRE ? c : 0][1];
+      } else {
+        g0 = *reinterpret_cast<const float4 *>(g.gamma + k);
+        g1 = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
+      }
       gm[0] = g0.x; gm[1] = g0.y; gm[2] = g0.z; gm[3] = g0.w;
       gm[4] = g1.x; gm[5] = g1.y; gm[6] = g1.z; gm[7] = g1.w;
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float4 a0 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k);
-      const float4 a1 = *reinterpret_cast<const float4 *>(g.x + m * g.ldx + k + 4);
-      float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      float av[8];
+      {
+        float4 a0, a1;
+        xrow(m, c, k, a0, a1);
+        av[0] = a0.x; av[1] = a0.y; av[2] = a0.z; av[3] = a0.w;
+        av[4] = a1.x; av[5] = a1.y; av[6] = a1.z; av[7] = a1.w;
+      }
       if (g.gamma)
 #pragma unroll
         for (int e = 0; e < 8; ++e) av[e] = (av[e] / rms[m]) * gm[e];
@@ -229,7 +312,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
       acc[m][1] = t1;
     }
   };
-  if (g.K <= 512 * PRE) {
+  if (pre_k) {
 #pragma unroll
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
@@ -237,7 +320,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
         float w0[8], w1[8];
         bf16x8(pw0[c], w0);
         bf16x8(pw1[c], w1);
-        step(k, w0, w1);
+        step(c, k, w0, w1);
       }
     }
   } else {
@@ -245,18 +328,18 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
       float w0[8], w1[8];
       bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
       bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1c * g.K + k), w1);
-      step(k, w0, w1);
+      step(0, k, w0, w1);
     }
   }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    acc[m][0] = wave_sum(acc[m][0]);
-    acc[m][1] = wave_sum(acc[m][1]);
+    acc[m][0] = fold_sum<64>(acc[m][0]);
+    acc[m][1] = fold_sum<64>(acc[m][1]);
   }
   // Lane m writes activation row m's outputs.
 #pragma unroll
   for (int m = 0; m < M; ++m)
-    if (lane == m) pair_write<MODE>(g, q, m, acc[m][0], acc[m][1]);
+    if (lane == m) pair_write_pre<MODE>(g, q, m, acc[m][0], acc[m][1], pre);
 }
 
 // 9 to 32 activation rows: a block's 4 wavefronts (8 weight rows) share each
@@ -797,6 +880,11 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
     return;
   }
+  if (M <= 2 && g.K <= 1024) {  // two chunks a lane: half the registers of four
+    if (M == 1) decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
+    else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+    return;
+  }
   switch (M) {
 #define MI_DEC(m) case m: decode_matvec_kernel<m, MODE><<<grid, 256, 0, st>>>(g); break;
     MI_DEC(1) MI_DEC(2) MI_DEC(3) MI_DEC(4) MI_DEC(5) MI_DEC(6) MI_DEC(7) MI_DEC(8)
@@ -993,3 +1081,4 @@ extern "C" int mi_norm_qkv_rope_at(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
   return norm_qkv_rope(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, 0,
                        static_cast<const int32_t *>(pb->ptr), k_cache, v_cache, q_out);
 }
+

@@ -125,19 +125,17 @@ bool decode_fused(const mi_llama *m, int64_t batch) {
          c.intermediate % 8 == 0;
 }
 
-// The layers of a decode step, six fused launches each, on the hidden rows
-// x [batch, hidden]: the new position pos0 (immediate) or held on the device
-// in `pos`, the attention planned for `span` positions.
+// The layers of a decode step on the hidden rows x [batch, hidden]: the new
+// position pos0 (immediate) or held on the device in `pos`, the attention
+// planned for `span` positions.  Five launches a layer up to 2 sequences
+// (q|k|v and the attention's chunks in one), six above.
 Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, int64_t pos0, int64_t span) {
   const mi_llama_config &c = m->cfg;
   const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim;
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
   for (Layer &L : m->layers) {
-    Tensor q = pos ? burn::norm_qkv_rope_at(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, *pos,
-                                            L.cache_k, L.cache_v)
-                   : burn::norm_qkv_rope(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos0,
-                                         L.cache_k, L.cache_v);
-    Tensor o = burn::attention_rows_at(q, L.cache_k, L.cache_v, batch, 1, H, KVH, pos, pos0, span, scale);
+    Tensor o = burn::norm_qkv_attention(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos, pos0,
+                                        span, L.cache_k, L.cache_v, scale);
     x = burn::norm_matvec(o, nullptr, 0.0f, L.wo, &x, false);
     Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, L.wgu, nullptr, true);
     x = burn::norm_matvec(h, nullptr, 0.0f, L.wdown, &x, false);

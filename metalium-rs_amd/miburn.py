@@ -112,6 +112,8 @@ def _load() -> ctypes.CDLL:
         "mi_matmul_pairs": [P, U64, U64, I64, ctypes.POINTER(I64), ctypes.POINTER(c_int), ctypes.POINTER(I64),
                             ctypes.POINTER(c_int), I64, I64, I64, c_int, Ip],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
+        "mi_norm_qkv_attention": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, I64, I64, U64, U64, c_float,
+                                  Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_norm_qkv_rope_at": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, U64, U64, Ip],
         "mi_attention_rows_at": [P, U64, U64, U64, I64, I64, I64, I64, U64, I64, I64, c_float, Ip],
@@ -355,6 +357,14 @@ class Engine:
         pos0 read on the device from the [1, 1] I32 buffer `pos` (if nonzero)."""
         return self._out(self._lib.mi_attention_rows_at, q, k_cache, v_cache, batch, t, heads, kv_heads, pos, pos0,
                          span, scale)
+
+    def norm_qkv_attention(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
+                           kv_heads: int, pos: int, pos0: int, span: int, k_cache: int, v_cache: int,
+                           scale: float) -> int:
+        """norm_qkv_rope(_at) then attention_rows_at (t = 1) in one call: the
+        attention rows of one new position per sequence (llama.rs:380-470)."""
+        return self._out(self._lib.mi_norm_qkv_attention, x, gamma, eps, w_qkv, cos, sin, heads, kv_heads, pos,
+                         pos0, span, k_cache, v_cache, scale)
 
     def norm_qkv_rope_at(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
                          kv_heads: int, pos: int, k_cache: int, v_cache: int) -> int:

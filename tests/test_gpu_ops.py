@@ -973,6 +973,93 @@ def test_norm_qkv_rope_writes_cache(engine, M):
     assert np.array_equal(vc1[:, :, keep], vc0.reshape(M, KVH, maxc, D)[:, :, keep])
 
 
+def qkv_attention_case(engine, M, kv16, pos0, maxc, seed=0):
+    rng = np.random.default_rng(seed)
+    H, KVH, D, K, eps = 9, 3, 64, 576, 1e-5
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    g = (rng.standard_normal((1, K)) * 0.1 + 1.0).astype(np.float32)
+    wb = orc.to_bf16((rng.standard_normal(((H + 2 * KVH) * D, K)) * 0.05).astype(np.float32))
+    ang = np.arange(maxc)[:, None] * (1e5 ** (-2.0 * np.arange(D // 2) / D))[None, :]
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], 1).astype(np.float32)
+    sin = np.concatenate([-np.sin(ang), np.sin(ang)], 1).astype(np.float32)
+    kc0 = rng.standard_normal((M * KVH * maxc, D)).astype(np.float32)
+    vc0 = rng.standard_normal((M * KVH * maxc, D)).astype(np.float32)
+    if kv16:
+        kc0, vc0 = orc.to_bf16(kc0), orc.to_bf16(vc0)
+    up = engine.upload_bf16 if kv16 else engine.upload
+    args = (engine.upload(x), engine.upload(g), eps, engine.upload_bf16(wb), engine.upload(cos), engine.upload(sin),
+            H, KVH)
+    return dict(H=H, KVH=KVH, D=D, K=K, eps=eps, x=x, g=g, wb=wb, cos=cos, sin=sin, kc0=kc0, vc0=vc0, up=up,
+                args=args, scale=float(np.float32(1.0 / np.sqrt(D))))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])  # one launch and a combine up to 2 sequences, the two calls above
+@pytest.mark.parametrize("kv16", [False, True])
+@pytest.mark.parametrize("pos0,span,maxc", [(575, 576, 640), (100, 192, 640), (40, 64, 64), (0, 64, 64)])
+def test_norm_qkv_attention(engine, M, kv16, pos0, span, maxc):
+    # Against the two calls it fuses, on the same inputs: the attention rows
+    # within the F32 bound, the new cache row within the projection's bound
+    # (exact in BF16 up to one rounding), every other row untouched; and
+    # against float64 over the caches as written.  The device position gives
+    # the immediate one's bits.
+    c = qkv_attention_case(engine, M, kv16, pos0, maxc)
+    H, KVH, D = c["H"], c["KVH"], c["D"]
+    k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    got = engine.download(engine.norm_qkv_attention(*c["args"], 0, pos0, span, k1, v1, c["scale"]))
+    k2, v2 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    q = engine.norm_qkv_rope(*c["args"], pos0, k2, v2)
+    want = engine.download(engine.attention_rows_at(q, k2, v2, M, 1, H, KVH, 0, pos0, span, c["scale"]))
+    dl = (lambda b: orc.from_bf16(engine.download(b))) if kv16 else engine.download
+    kc1, vc1, kc2, vc2 = (dl(b).reshape(M, KVH, maxc, D) for b in (k1, v1, k2, v2))
+    x64 = rms_ref(c["x"], c["g"], c["eps"])
+    w = orc.from_bf16(c["wb"]).astype(np.float64)
+    bound = (np.abs(x64) @ np.abs(w).T).max()
+    tol_row = 2e-5 * bound + (2.0 ** -8 * np.abs(kc2[:, :, pos0]).max() if kv16 else 0.0)
+    assert np.abs(kc1[:, :, pos0] - kc2[:, :, pos0]).max() <= tol_row
+    assert np.abs(vc1[:, :, pos0] - vc2[:, :, pos0]).max() <= tol_row
+    keep = np.ones(maxc, bool)
+    keep[pos0] = False
+    assert np.array_equal(kc1[:, :, keep], kc2[:, :, keep])
+    assert np.array_equal(vc1[:, :, keep], vc2[:, :, keep])
+    # float64 attention over this call's caches and queries, the queries from float64 too.
+    y = x64 @ w.T
+    qh = y[:, :H * D].reshape(M, H, D)
+    rot = np.concatenate([qh[..., D // 2:], qh[..., :D // 2]], -1)
+    q64 = (qh * c["cos"][pos0] + rot * c["sin"][pos0]).reshape(M, H * D)
+    a64 = attention_ref(q64.astype(np.float32), kc1.reshape(-1, D), vc1.reshape(-1, D), M, 1, H, KVH, pos0,
+                        c["scale"])
+    vmax = np.abs(vc1).max()
+    assert np.abs(got - a64).max() <= 1e-4 * vmax * max(1.0, bound * c["scale"] * np.abs(kc1).max())
+    assert np.abs(got - want).max() <= 1e-4 * vmax * max(1.0, bound * c["scale"] * np.abs(kc1).max())
+    if M > 2:  # the two calls themselves
+        same_bits(got, want)
+    ipos = engine.upload_bits(np.array([[pos0]], np.int32), I32)
+    k3, v3 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    same_bits(engine.download(engine.norm_qkv_attention(*c["args"], ipos, 0, span, k3, v3, c["scale"])), got)
+    same_bits(engine.download(k3), engine.download(k1))
+    same_bits(engine.download(v3), engine.download(v1))
+
+
+def test_norm_qkv_attention_refuses_bad_positions(engine):
+    c = qkv_attention_case(engine, 1, False, 10, 64)
+    k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    with pytest.raises(miburn.MiError) as e:  # immediate position past the span
+        engine.norm_qkv_attention(*c["args"], 0, 64, 64, k1, v1, c["scale"])
+    assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:  # span beyond the cache
+        engine.norm_qkv_attention(*c["args"], 0, 10, 65, k1, v1, c["scale"])
+    assert e.value.kind == "ARG"
+    # A device position past the span: no cache row written, reported at the next wait.
+    bad = engine.upload_bits(np.array([[64]], np.int32), I32)
+    engine.norm_qkv_attention(*c["args"], bad, 0, 64, k1, v1, c["scale"])
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()
+    same_bits(engine.download(k1), c["kc0"])
+    same_bits(engine.download(v1), c["vc0"])
+
+
 @pytest.mark.parametrize("M", [1, 5, 32])
 def test_norm_qkv_rope_bf16_caches(engine, M):
     # The same kernel into BF16 caches: q unchanged, the new cache row the F32
