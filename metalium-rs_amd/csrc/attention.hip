@@ -609,7 +609,7 @@ struct DqaArgs {
   float *part;  // [B KVH][S][G (64 + 2)] chunk partials
 };
 
-// Block (256 threads): 64 rows (w0, each K BF16) times the normalised row in
+// Block (256 threads): 64 rows (w0, each K BF16) times the staged row in
 // LDS xn; thread t takes row t / 4 and the 16-byte chunks t % 4, + 4, ...;
 // the four partial sums fold over the row's lanes.  wr: the chunks, loaded
 // by dqa_wload.
@@ -638,8 +638,8 @@ __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4
       const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc += av[2 * e] * __uint_as_float(u[e] << 16);
-        acc += av[2 * e + 1] * __uint_as_float(u[e] & 0xffff0000u);
+        acc = fmaf(av[2 * e], __uint_as_float(u[e] << 16), acc);
+        acc = fmaf(av[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u), acc);
       }
     }
   }
@@ -664,23 +664,19 @@ __device__ __forceinline__ DqaPre dqa_pre(const DqaArgs &g, int64_t b, int64_t p
                 cs[i], cs[i + half], sn[i], sn[i + half]};
 }
 
-// The hidden row normalised into LDS: xn[k] = (x[k] / rms) * gamma[k],
-// rms = sqrt(mean(x x) + eps) (the norm kernel's formula).
-__device__ __forceinline__ void dqa_norm(const DqaArgs &g, const DqaPre &pre, float *xn, float *red4) {
+// The hidden row times the gain into LDS, xg[k] = x[k] gamma[k], and the
+// RMSNorm's rms = sqrt(mean(x x) + eps), which divides the finished
+// products (sum_k x g w / rms: the GEMV need not wait for the norm's fold).
+__device__ __forceinline__ float dqa_stage(const DqaArgs &g, const DqaPre &pre, float *xg, float *red4) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool mine = 4 * tid < g.K;
-  const float4 v = pre.x;
-  float ss = mine ? v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w : 0.0f;
+  const float4 v = pre.x, gm = pre.gm;
+  float ss = mine ? fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w))) : 0.0f;
+  if (mine) *reinterpret_cast<float4 *>(xg + 4 * tid) = make_float4(v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w);
   ss = fold_sum<64>(ss);
   if (lane == 0) red4[wave] = ss;
   __syncthreads();
-  const float rms = __fsqrt_rn((red4[0] + red4[1] + red4[2] + red4[3]) / static_cast<float>(g.K) + g.eps);
-  if (mine) {
-    const float4 gm = pre.gm;
-    *reinterpret_cast<float4 *>(xn + 4 * tid) =
-        make_float4((v.x / rms) * gm.x, (v.y / rms) * gm.y, (v.z / rms) * gm.z, (v.w / rms) * gm.w);
-  }
-  __syncthreads();
+  return __fsqrt_rn((red4[0] + red4[1] + red4[2] + red4[3]) / static_cast<float>(g.K) + g.eps);
 }
 
 // RoPE of a 64-wide head in LDS (raw -> rot): the rotation of pair (i, i +
@@ -722,8 +718,8 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
       pos = ok ? pos : 0;
     }
     const DqaPre pre = dqa_pre(g, b, pos);
-    dqa_norm(g, pre, xn, red4);
-    const float y = dqa_dot<CH>(xn, g.K, wr);
+    const float rms = dqa_stage(g, pre, xn, red4);
+    const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
     __syncthreads();
     if (!ok) return;  // refused position: no cache row (flag raised by the chunk blocks)
@@ -769,9 +765,9 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
   uint4 wr[CH];
   dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
   const DqaPre pre = dqa_pre(g, b, pos);
-  dqa_norm(g, pre, xn, red4);
+  const float rms = dqa_stage(g, pre, xn, red4);
   {
-    const float y = dqa_dot<CH>(xn, g.K, wr);
+    const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
   }
   __syncthreads();

@@ -192,24 +192,22 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
   if (p >= g.npairs) return;  // whole wavefronts
   const PairRows q = pair_rows<MODE>(g, p);
-  const int64_t r0 = q.r0, r1 = q.r1;
-  const bool has1 = q.has1;
+  const int64_t r1c = q.has1 ? q.r1 : q.r0;
 
-  // The weight rows are independent of the norm: with K <= 2048 (four
-  // 16-byte chunks a lane) all of them are requested first, so the norm's
-  // loads and reduction overlap the weights' HBM latency.  Up to 2 rows the
-  // activation rows and the gain are requested with them into registers, so
-  // the norm and the products wait for one round trip instead of three.
-  // The loads are unconditional, from clamped rows and columns: a load under
-  // a condition compiles to a branch that waits for it before the next is
-  // issued (0.956 -> 0.922 ms a batch-1 SmolLM2 decode step).  Without a
-  // second row (a lone last row) the first is read twice and the second
-  // product is discarded by pair_write.
+  // The weight rows are independent of the norm: with K <= 512 PRE all of
+  // them are requested first, and up to 2 rows the activation rows and the
+  // gain with them into registers, so the products wait for one round trip.
+  // The norm scales the finished sums -- sum_k x g w / rms -- so the
+  // products do not wait for its fold either.  The loads are unconditional,
+  // from clamped rows and columns: a load under a condition compiles to a
+  // branch that waits for it before the next is issued (0.956 -> 0.922 ms a
+  // batch-1 SmolLM2 decode step).  Without a second row (a lone last row)
+  // the first is read twice and the second product is discarded by
+  // pair_write.
   constexpr bool XPRE = M <= 2;
   constexpr int XM = XPRE ? M : 1, XC = XPRE ? PRE : 1;
   uint4 pw0[PRE], pw1[PRE];
   float4 px[XM][XC][2], pg[XC][2];
-  const int64_t r1c = has1 ? r1 : r0;
   const bool pre_k = g.K <= 512 * PRE;
   if (pre_k) {
     const float *gp = g.gamma ? g.gamma : g.x;  // without a gain: read, never used
@@ -217,7 +215,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
       const int64_t kc = k < g.K ? k : g.K - 8;
-      pw0[c] = *reinterpret_cast<const uint4 *>(g.w + r0 * g.K + kc);
+      pw0[c] = *reinterpret_cast<const uint4 *>(g.w + q.r0 * g.K + kc);
       pw1[c] = *reinterpret_cast<const uint4 *>(g.w + r1c * g.K + kc);
       if constexpr (XPRE) {
 #pragma unroll
@@ -244,38 +242,14 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     }
   };
 
-  // RMSNorm of the activation rows: sqrt(mean(x x) + eps).
-  float rms[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) rms[m] = 1.0f;
-  if (g.gamma) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      float ss = 0.0f;
-      auto sq = [&](int c, int64_t k) {
-        float4 a0, a1;
-        xrow(m, c, k, a0, a1);
-        ss += a0.x * a0.x + a0.y * a0.y + a0.z * a0.z + a0.w * a0.w;
-        ss += a1.x * a1.x + a1.y * a1.y + a1.z * a1.z + a1.w * a1.w;
-      };
-      if (inreg) {
-#pragma unroll
-        for (int c = 0; c < PRE; ++c) {
-          const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
-          if (k < g.K) sq(c, k);
-        }
-      } else {
-        for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) sq(0, k);
-      }
-      ss = fold_sum<64>(ss);
-      rms[m] = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
-    }
-  }
-
   float acc[M][2];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
-  // One 8-wide k step: activations (normalised on the fly) times both rows.
+  float ss[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) ss[m] = 0.0f;
+  // One 8-wide k step: the activations times the gain, times both rows; and
+  // the rows' sums of squares for the norm.
   auto step = [&](int c, int64_t k, const float (&w0)[8], const float (&w1)[8]) {
     float gm[8];
     if (g.gamma) {
@@ -299,14 +273,19 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
         av[0] = a0.x; av[1] = a0.y; av[2] = a0.z; av[3] = a0.w;
         av[4] = a1.x; av[5] = a1.y; av[6] = a1.z; av[7] = a1.w;
       }
-      if (g.gamma)
+      if (g.gamma) {
+        float t = ss[m];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) av[e] = (av[e] / rms[m]) * gm[e];
+        for (int e = 0; e < 8; ++e) t = fmaf(av[e], av[e], t);
+        ss[m] = t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[e] *= gm[e];
+      }
       float t0 = acc[m][0], t1 = acc[m][1];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        t0 += av[e] * w0[e];
-        t1 += av[e] * w1[e];
+        t0 = fmaf(av[e], w0[e], t0);
+        t1 = fmaf(av[e], w1[e], t1);
       }
       acc[m][0] = t0;
       acc[m][1] = t1;
@@ -326,20 +305,26 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   } else {
     for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
       float w0[8], w1[8];
-      bf16x8(*reinterpret_cast<const uint4 *>(g.w + r0 * g.K + k), w0);
+      bf16x8(*reinterpret_cast<const uint4 *>(g.w + q.r0 * g.K + k), w0);
       bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1c * g.K + k), w1);
       step(0, k, w0, w1);
     }
   }
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    acc[m][0] = fold_sum<64>(acc[m][0]);
-    acc[m][1] = fold_sum<64>(acc[m][1]);
-  }
-  // Lane m writes activation row m's outputs.
+  // RMSNorm: rms = sqrt(mean(x x) + eps), dividing the finished sums.
+  float rms[M];
 #pragma unroll
   for (int m = 0; m < M; ++m)
-    if (lane == m) pair_write_pre<MODE>(g, q, m, acc[m][0], acc[m][1], pre);
+    rms[m] = g.gamma ? __fsqrt_rn(fold_sum<64>(ss[m]) / static_cast<float>(g.K) + g.eps) : 1.0f;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float y0 = fold_sum<64>(acc[m][0]), y1 = fold_sum<64>(acc[m][1]);
+    if (g.gamma) {
+      y0 = y0 / rms[m];
+      y1 = y1 / rms[m];
+    }
+    // Lane m writes activation row m's outputs.
+    if (lane == m) pair_write_pre<MODE>(g, q, m, y0, y1, pre);
+  }
 }
 
 // 9 to 32 activation rows: a block's 4 wavefronts (8 weight rows) share each
@@ -881,8 +866,11 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     return;
   }
   if (M <= 2 && g.K <= 1024) {  // two chunks a lane: half the registers of four
-    if (M == 1) decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
-    else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+    if (M == 1) {
+      decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
+    } else {
+      decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+    }
     return;
   }
   switch (M) {
