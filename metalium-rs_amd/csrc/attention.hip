@@ -691,10 +691,98 @@ __device__ __forceinline__ void dqa_rope(const DqaPre &pre, const float *raw, fl
   }
 }
 
+// The combine of a fused step: the S chunks of each (sequence, kv head) and
+// the new key as one more -- score scale (q . k_new) over the 64 lanes of a
+// wavefront, weight exp(score - max), value row v_new -- with the key-chunked
+// combine's formula: out = (sum_s w_s o_s + w_new v_new) / max(sum_s w_s
+// l_s + w_new, FLT_MIN), w_s = exp(m_s - max).
+// Item bj (sequence, kv head) of a fused step's combine, by one block of 256
+// threads; st: 3 G S + 3 G floats of LDS.
+template <typename KV>
+__device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, float *out, float *st) {
+  constexpr int D = DQA_D;
+  const int G = g.G, S = static_cast<int>(g.S);
+  const int64_t b = bj / g.KVH, j = bj % g.KVH, PS = static_cast<int64_t>(G) * (D + 2);
+  const float *pb = g.part + bj * S * PS;
+  float *w = st + 2 * G * S;
+  float *den = w + G * S;
+  float *snew = den + G;
+  float *wnew = snew + G;
+  // A thread's output elements e = tid + 256 i (G D <= 512): their first CS
+  // chunks' values, requested with the statistics before the position (read
+  // on the device, a traced step's) that the new rows' loads wait for; one
+  // round trip for all but very long contexts.
+  constexpr int EP = 2, CS = 16;
+  float ov[EP][CS], vd[EP];
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) ov[i][s] = pb[(s < S ? s : S - 1) * PS + 2 * G + ec];
+  }
+  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
+  int64_t pos = g.pa.pos0;
+  if (g.pa.dev) {
+    const int64_t v = *g.pa.dev;
+    pos = v >= 0 && v + 1 <= g.pa.span ? v : 0;
+  }
+  const KV *kn = static_cast<const KV *>(g.kc) + (bj * g.maxc + pos) * D;
+  const KV *vn = static_cast<const KV *>(g.vc) + (bj * g.maxc + pos) * D;
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
+    if constexpr (sizeof(KV) == 2) vd[i] = bf16_bits_to_f32(vn[ec % D]);
+    else vd[i] = vn[ec % D];
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int gg = wave; gg < G; gg += 4) {
+    float kd;
+    if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
+    else kd = kn[lane];
+    const float sc = fold_sum<64>(g.q[(b * g.H + j * G + gg) * D + lane] * kd);
+    if (lane == 0) snew[gg] = sc * g.scale;
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int gg = threadIdx.x;
+    float M = snew[gg];
+    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + gg]);
+    float l = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float ws = expf(st[s * 2 * G + gg] - M);
+      w[s * G + gg] = ws;
+      l += ws * st[s * 2 * G + G + gg];
+    }
+    const float wn = expf(snew[gg] - M);
+    wnew[gg] = wn;
+    l += wn;
+    den[gg] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
+  }
+  __syncthreads();
+  float *dst = out + b * g.H * D + j * G * D;
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    if (e < G * D) {
+      const int gg = e / D;
+      float num = 0.0f;
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+        if (s < S) num += w[s * G + gg] * ov[i][s];
+      for (int s = CS; s < S; ++s) num += w[s * G + gg] * pb[s * PS + 2 * G + e];
+      num += wnew[gg] * vd[i];
+      dst[e] = num / den[gg];
+    }
+  }
+}
+
+// The block's part of the launch (its item, sequence and kv head, is
+// returned).  (Counting the blocks in and letting the last of an item combine -- device
+// fences before and after the count -- costs more than the combine's own
+// launch: batch-1 SmolLM2 decode 0.694 -> 0.938 ms a step.)
 template <typename KV, int CH>
-__global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
+__device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   constexpr int D = DQA_D, NW = 4, LPR = D / 4, KPW = 64 / LPR, U = 4, STEP = NW * KPW;
-  extern __shared__ float dqa_sm[];
   float *xn = dqa_sm;            // [K]
   float *qraw = xn + g.K;        // [64]
   float *qrot = qraw + D;        // [64]
@@ -722,7 +810,7 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
     const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
     __syncthreads();
-    if (!ok) return;  // refused position: no cache row (flag raised by the chunk blocks)
+    if (!ok) return bj;  // refused position: no cache row (flag raised by the chunk blocks)
     KV *dst = static_cast<KV *>(which ? g.vc : g.kc) + (bj * g.maxc + pos) * D;
     if (which == 0) {
       dqa_rope(pre, qraw, qrot);
@@ -731,12 +819,15 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
     } else if (tid < D) {
       f32_put(dst + tid, qraw[tid]);
     }
-    return;
+    return bj;
   }
 
   // (sequence, query head, key chunk)
   const int64_t s = bid % g.S, bh = bid / g.S, hq = bh % g.H, b = bh / g.H;
   const int64_t j = hq / g.G, gg = hq % g.G, bj = b * g.KVH + j;
+  // The weights first: they do not wait for a position read on the device.
+  uint4 wr[CH];
+  dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
   const int64_t pos = att_pos0(g.pa, 1);
   const int64_t lo = s * g.chunk, len = pos > lo ? (pos - lo < g.chunk ? pos - lo : g.chunk) : 0;
   const int64_t PS = static_cast<int64_t>(g.G) * (D + 2);
@@ -747,14 +838,14 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
       pb[g.G + gg] = 0.0f;
     }
     if (tid < D) pb[2 * g.G + gg * D + tid] = 0.0f;
-    return;
+    return bj;
   }
   const KV *Kc = static_cast<const KV *>(g.kc) + (bj * g.maxc + lo) * D;
   const KV *Vc = static_cast<const KV *>(g.vc) + (bj * g.maxc + lo) * D;
   const int sl = lane % LPR, kk = lane / LPR;
   const int64_t first = static_cast<int64_t>(wave) * KPW + kk, last = len > 0 ? len - 1 : 0;
-  // The first pass's key and value rows, then the weights: all in flight
-  // before the norm waits.
+  // The first pass's key and value rows: in flight with the weights before
+  // the norm waits.
   float4 kpre[U], vv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -762,8 +853,6 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
     kpre[u] = f32x4_get(Kc + (c < len ? c : last) * D + 4 * sl);
     vv[u] = f32x4_get(Vc + (c < len ? c : last) * D + 4 * sl);
   }
-  uint4 wr[CH];
-  dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
   const DqaPre pre = dqa_pre(g, b, pos);
   const float rms = dqa_stage(g, pre, xn, red4);
   {
@@ -849,86 +938,20 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
     for (int w = 1; w < NW; ++w) t += red[w * D + tid];
     pb[2 * g.G + gg * D + tid] = t;
   }
+  return bj;
 }
 
-// The combine of a fused step: the S chunks of each (sequence, kv head) and
-// the new key as one more -- score scale (q . k_new) over the 64 lanes of a
-// wavefront, weight exp(score - max), value row v_new -- with the key-chunked
-// combine's formula: out = (sum_s w_s o_s + w_new v_new) / max(sum_s w_s
-// l_s + w_new, FLT_MIN), w_s = exp(m_s - max).
-template <int G, typename KV>
-__global__ void __launch_bounds__(256) attention_combine_new_kernel(const float *part, const float *q, const KV *kc,
-                                                                    const KV *vc, float *out, int64_t H, int64_t KVH,
-                                                                    int S, AttPos pa, int64_t maxc, float scale) {
-  constexpr int D = DQA_D;
-  extern __shared__ float st[];  // [S][2G] statistics, [S][G] weights, [G] den, [G] new score, [G] new weight
-  const int64_t bj = blockIdx.x, b = bj / KVH, j = bj % KVH;
-  constexpr int PS = G * (D + 2);
-  const float *pb = part + bj * S * static_cast<int64_t>(PS);
-  float *w = st + 2 * G * S;
-  float *den = w + G * S;
-  float *snew = den + G;
-  float *wnew = snew + G;
-  int64_t pos = pa.pos0;
-  if (pa.dev) {
-    const int64_t v = *pa.dev;
-    pos = v >= 0 && v + 1 <= pa.span ? v : 0;
-  }
-  const KV *kn = kc + (bj * maxc + pos) * D, *vn = vc + (bj * maxc + pos) * D;
-  // A thread's output elements e = tid + 256 i: their first CS chunks' values
-  // and the new value row's, requested with the statistics (one round trip
-  // for all but very long contexts).
-  constexpr int EP = (G * D + 255) / 256, CS = 16;
-  float ov[EP][CS], vd[EP];
-#pragma unroll
-  for (int i = 0; i < EP; ++i) {
-    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
-#pragma unroll
-    for (int s = 0; s < CS; ++s) ov[i][s] = pb[(s < S ? s : S - 1) * PS + 2 * G + ec];
-    if constexpr (sizeof(KV) == 2) vd[i] = bf16_bits_to_f32(vn[ec % D]);
-    else vd[i] = vn[ec % D];
-  }
-  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int g = wave; g < G; g += 4) {
-    float kd;
-    if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
-    else kd = kn[lane];
-    const float sc = fold_sum<64>(q[(b * H + j * G + g) * D + lane] * kd);
-    if (lane == 0) snew[g] = sc * scale;
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int g = threadIdx.x;
-    float M = snew[g];
-    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + g]);
-    float l = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float ws = expf(st[s * 2 * G + g] - M);
-      w[s * G + g] = ws;
-      l += ws * st[s * 2 * G + G + g];
-    }
-    const float wn = expf(snew[g] - M);
-    wnew[g] = wn;
-    l += wn;
-    den[g] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
-  }
-  __syncthreads();
-  float *dst = out + b * H * D + j * G * D;
-#pragma unroll
-  for (int i = 0; i < EP; ++i) {
-    const int e = threadIdx.x + 256 * i;
-    if (e < G * D) {
-      const int g = e / D;
-      float num = 0.0f;
-#pragma unroll
-      for (int s = 0; s < CS; ++s)
-        if (s < S) num += w[s * G + g] * ov[i][s];
-      for (int s = CS; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
-      num += wnew[g] * vd[i];
-      dst[e] = num / den[g];
-    }
-  }
+template <typename KV, int CH>
+__global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
+  extern __shared__ float dqa_sm[];
+  dqa_work<KV, CH>(g, dqa_sm);
+}
+
+// The combine: one block an item, the launch after the fused one.
+template <typename KV>
+__global__ void __launch_bounds__(256) attention_combine_new_kernel(DqaArgs g, float *out) {
+  extern __shared__ float st[];
+  combine_new_item<KV>(g, blockIdx.x, out, st);
 }
 
 }  // namespace mi
@@ -1171,8 +1194,9 @@ extern "C" int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id
 namespace mi {
 namespace {
 
+// The fused launch, then the combine's.
 template <typename KV>
-void launch_dqa(hipStream_t st, const DqaArgs &g) {
+void launch_dqa(hipStream_t st, const DqaArgs &g, float *out) {
   const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.H * g.S + 2 * static_cast<int64_t>(g.B) * g.KVH);
   const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + 8 + g.chunk + 4 * DQA_D + 2) * sizeof(float);
   const int64_t ch = (g.K / 8 + 3) / 4;  // chunks a thread
@@ -1180,25 +1204,8 @@ void launch_dqa(hipStream_t st, const DqaArgs &g) {
   else if (ch <= 16) decode_qkv_attention_kernel<KV, 16><<<blocks, 256, lds, st>>>(g);
   else if (ch <= 24) decode_qkv_attention_kernel<KV, 24><<<blocks, 256, lds, st>>>(g);
   else decode_qkv_attention_kernel<KV, 32><<<blocks, 256, lds, st>>>(g);
-}
-
-template <typename KV>
-bool launch_combine_new(int64_t G, hipStream_t st, const DqaArgs &g, float *out) {
-  const unsigned items = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH);
-  const size_t lds = static_cast<size_t>(3 * G * g.S + 3 * G) * sizeof(float);
-  const KV *k = static_cast<const KV *>(g.kc), *v = static_cast<const KV *>(g.vc);
-  const int S = static_cast<int>(g.S);
-  switch (G) {
-#define MI_CN_G(gg)                                                                                          \
-  case gg:                                                                                                   \
-    attention_combine_new_kernel<gg, KV><<<items, 256, lds, st>>>(g.part, g.q, k, v, out, g.H, g.KVH, S, g.pa, \
-                                                                  g.maxc, g.scale);                          \
-    return true;
-    MI_CN_G(1) MI_CN_G(2) MI_CN_G(3) MI_CN_G(4) MI_CN_G(5) MI_CN_G(6) MI_CN_G(7) MI_CN_G(8)
-#undef MI_CN_G
-    default:
-      return false;
-  }
+  const size_t comb = static_cast<size_t>(3 * g.G * g.S + 3 * g.G) * sizeof(float);
+  attention_combine_new_kernel<KV><<<static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH), 256, comb, st>>>(g, out);
 }
 
 }  // namespace
@@ -1300,13 +1307,8 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   g.part = sc;
   g.q = sc + part_floats;
   float *o = static_cast<float *>(ob->ptr);
-  if (kb->elem == MI_BF16) {
-    launch_dqa<uint16_t>(ctx->stream, g);
-    launch_combine_new<uint16_t>(G, ctx->stream, g, o);
-  } else {
-    launch_dqa<float>(ctx->stream, g);
-    launch_combine_new<float>(G, ctx->stream, g, o);
-  }
+  if (kb->elem == MI_BF16) launch_dqa<uint16_t>(ctx->stream, g, o);
+  else launch_dqa<float>(ctx->stream, g, o);
   s = check_launch(ctx, "norm_qkv_attention");
   if (s) {
     mi_free(ctx, id);

@@ -186,7 +186,11 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
 }
 
 // PRE: 16-byte chunks a lane requested up front (k <= 512 PRE), 2 or 4.
-template <int M, int MODE, int PRE = 4>
+// NTW: the weights streamed (non-temporal loads), for a weight larger than
+// the caches keep between steps -- the vocabulary head -- so it does not
+// displace the layers' weights from the last-level cache (batch-1 SmolLM2
+// decode 0.713 -> 0.697 ms a step).
+template <int M, int MODE, int PRE = 4, bool NTW = false>
 __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
@@ -215,8 +219,8 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
       const int64_t kc = k < g.K ? k : g.K - 8;
-      pw0[c] = *reinterpret_cast<const uint4 *>(g.w + q.r0 * g.K + kc);
-      pw1[c] = *reinterpret_cast<const uint4 *>(g.w + r1c * g.K + kc);
+      pw0[c] = ldu4<NTW>(g.w + q.r0 * g.K + kc);
+      pw1[c] = ldu4<NTW>(g.w + r1c * g.K + kc);
       if constexpr (XPRE) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -856,6 +860,8 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
 // ms: batch 2 1.12 against 1.28, batch 3 1.32 against 1.31, batch 4 1.54
 // against 1.34, batch 8 2.43 against 1.38).
 constexpr int64_t DECODE_GEMV_MAX_M = 2;
+// Weights of at least this many bytes are streamed (NTW).
+constexpr int64_t DECODE_STREAM_BYTES = int64_t(32) << 20;
 
 template <int MODE>
 static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
@@ -866,10 +872,13 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     return;
   }
   if (M <= 2 && g.K <= 1024) {  // two chunks a lane: half the registers of four
+    const bool nt = g.N * g.K * 2 >= DECODE_STREAM_BYTES;
     if (M == 1) {
-      decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
+      if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
+      else decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
     } else {
-      decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+      if (nt) decode_matvec_kernel<2, MODE, 2, true><<<grid, 256, 0, st>>>(g);
+      else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
     }
     return;
   }
