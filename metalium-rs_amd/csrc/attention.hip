@@ -627,7 +627,9 @@ template <int CH>
 __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4 (&wr)[CH]) {
   const int kq = threadIdx.x & 3;
   const int64_t nch = K / 8;
-  float acc = 0.0f;
+  // Four independent sums (one wavefront a SIMD: nothing else hides an FMA's
+  // latency), added at the end.
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int64_t c = kq + 4 * i;
@@ -638,12 +640,12 @@ __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4
       const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc = fmaf(av[2 * e], __uint_as_float(u[e] << 16), acc);
-        acc = fmaf(av[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u), acc);
+        acc[e] = fmaf(av[2 * e], __uint_as_float(u[e] << 16), acc[e]);
+        acc[e] = fmaf(av[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u), acc[e]);
       }
     }
   }
-  return fold_sum<4>(acc);
+  return fold_sum<4>((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
 // A thread's operands of the norm and the rotation, requested with the
