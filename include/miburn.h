@@ -452,7 +452,7 @@ int mi_norm_qkv_rope_at(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
  * attention block from its normed input to the attention output (crates/
  * tt-models/src/llama.rs:380-470), no Engine counterpart.  pos: a [1, 1]
  * I32 device position, or 0 for the immediate pos0; span as
- * mi_attention_rows_at's.  Up to 2 sequences with 64-wide heads, a gain and
+ * mi_attention_rows_at's.  Up to 6 sequences with 64-wide heads, a gain and
  * k a multiple of 32 up to 1024: one launch forms each head's queries, the
  * new key and value rows and the key chunks' partials over the earlier
  * positions, and a combine adds the new key as one more chunk -- the two

@@ -591,6 +591,11 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, cons
 // from the caches.
 constexpr int DQA_MAX_CH = 32;  // 16-byte weight chunks a thread: k <= 1024 (CH: 8, 16, 24 or 32)
 constexpr int DQA_D = 64;
+// Sequences up to which the fused launch serves a decode step: beyond, its
+// blocks' query GEMVs (each (sequence, head, chunk) block its own) cost more
+// than the composition's one matrix-core product (batch 8: 1.34 ms a
+// SmolLM2 step either way).
+constexpr int64_t DQA_MAX_B = 6;
 
 struct DqaArgs {
   const float *x;  // [B, K] F32 hidden rows
@@ -1240,10 +1245,10 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   const int64_t B = xb->rows, K = xb->cols, D = kb->cols;
   const int64_t G = kv_heads > 0 ? heads / kv_heads : 0;
   const int64_t maxc = B > 0 && kv_heads > 0 ? kb->rows / (B * kv_heads) : 0;
-  // The fused launch: up to 2 sequences, 64-wide heads, k a multiple of 32
-  // up to 1024, a gain, aligned operands; else the two calls composed (which
-  // check every argument themselves).
-  const bool fused = B >= 1 && B <= 2 && D == DQA_D && K % 32 == 0 && K <= 32 * DQA_MAX_CH && gb &&
+  // The fused launch: up to DQA_MAX_B sequences, 64-wide heads, k a
+  // multiple of 32 up to 1024, a gain, aligned operands; else the two calls
+  // composed (which check every argument themselves).
+  const bool fused = B >= 1 && B <= DQA_MAX_B && D == DQA_D && K % 32 == 0 && K <= 32 * DQA_MAX_CH && gb &&
                      xb->elem == MI_F32 && wb->elem == MI_BF16 && wb->cols == K && heads >= 1 && kv_heads >= 1 &&
                      heads % kv_heads == 0 && G <= ATT_MAX_GROUP && wb->rows == (heads + 2 * kv_heads) * D &&
                      kb->elem == vb->elem && elem_float(kb->elem) && vb->cols == D && vb->rows == kb->rows &&

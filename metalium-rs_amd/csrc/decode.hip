@@ -11,14 +11,15 @@
 // residual add, and silu(gate) * up (ops.rs:2622-2651).
 //
 // MI355X design.  Decode reads every weight once per step: the kernels are
-// HBM-latency-bound GEMVs.  Up to 2 activation rows (up to 8 where the
+// HBM-latency-bound GEMVs.  Up to 6 activation rows (up to 8 where the
 // matrix-core form below does not fit the shape) a wavefront owns two output
-// rows of the weight and all M activation rows; each lane streams 16 bytes (8 BF16) of
-// both weight rows per step, so a 576-wide row is read by the wavefront in two
-// coalesced passes.  The activation rows (a few KB) are re-read from cache by
-// every wavefront; when a gain is given each wavefront first folds its rows'
-// sum of squares and normalises on the fly (x / rms * gamma, the norm
-// kernel's formula), so the normalised rows never touch HBM.  The two rows a
+// rows of the weight and all M activation rows; each lane streams 16 bytes
+// (8 BF16) of both weight rows per step, so a 576-wide row is read by the
+// wavefront in two coalesced passes.  The activation rows (a few KB) are
+// re-read from cache by every wavefront; when a gain is given each wavefront
+// multiplies the rows by it on the fly and divides its finished sums by the
+// rows' rms (folded from the same values), so the normalised rows never touch
+// HBM.  The two rows a
 // wavefront owns are chosen so that the epilogue is local: a RoPE pair
 // (i, i + d/2) of one head, or a gate row and its up row.
 #include "common.hpp"
@@ -199,7 +200,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int64_t r1c = q.has1 ? q.r1 : q.r0;
 
   // The weight rows are independent of the norm: with K <= 512 PRE all of
-  // them are requested first, and up to 2 rows the activation rows and the
+  // them are requested first, and up to 4 rows the activation rows and the
   // gain with them into registers, so the products wait for one round trip.
   // The norm scales the finished sums -- sum_k x g w / rms -- so the
   // products do not wait for its fold either.  The loads are unconditional,
@@ -208,7 +209,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   // batch-1 SmolLM2 decode step).  Without a second row (a lone last row)
   // the first is read twice and the second product is discarded by
   // pair_write.
-  constexpr bool XPRE = M <= 2;
+  constexpr bool XPRE = M <= 4;
   constexpr int XM = XPRE ? M : 1, XC = XPRE ? PRE : 1;
   uint4 pw0[PRE], pw1[PRE];
   float4 px[XM][XC][2], pg[XC][2];
@@ -773,6 +774,12 @@ __global__ void __launch_bounds__(256) decode_fold_kernel(DecodeArgs g, int M) {
   pair_write<MODE>(g, q, m, y0, y1);
 }
 
+// Rows up to which the GEMV beats the matrix-core form (SmolLM2 decode step
+// with the fused q|k|v attention up to the same batch, ms: batch 3 0.89
+// against 1.26, batch 4 0.99 against 1.29, batch 6 1.22 against 1.32, batch
+// 8 1.40 against 1.33).
+constexpr int64_t DECODE_GEMV_MAX_M = 6;
+
 // Splits for the split-k form, or 1: grids of fewer than 32 tiles whose
 // blocks carry paired rows (the q|k|v heads) or long rows (k >= 1024); each
 // split at most four wavefronts' STEPS steps.  (Splitting the o and gate|up
@@ -780,7 +787,7 @@ __global__ void __launch_bounds__(256) decode_fold_kernel(DecodeArgs g, int M) {
 // 1.419.)
 template <int MODE>
 static int dsplit_count(int64_t M, const DecodeArgs &g) {
-  if (M <= 2 || g.K % 16) return 1;
+  if (M <= DECODE_GEMV_MAX_M || g.K % 16) return 1;
   if (MODE == DM_QKV && g.d != 64) return 1;
   constexpr int NB = MODE == DM_PLAIN ? 1 : 2;
   const int64_t tiles = MODE == DM_PLAIN ? (g.N + 31) / 32 : (MODE == DM_SILU_MUL ? (g.inter + 31) / 32 : g.H + 2 * g.KVH);
@@ -856,10 +863,6 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   return true;
 }
 
-// Rows up to which the GEMV beats the matrix-core form (SmolLM2 decode step,
-// ms: batch 2 1.12 against 1.28, batch 3 1.32 against 1.31, batch 4 1.54
-// against 1.34, batch 8 2.43 against 1.38).
-constexpr int64_t DECODE_GEMV_MAX_M = 2;
 // Weights of at least this many bytes are streamed (NTW).
 constexpr int64_t DECODE_STREAM_BYTES = int64_t(32) << 20;
 
@@ -871,14 +874,21 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
     return;
   }
-  if (M <= 2 && g.K <= 1024) {  // two chunks a lane: half the registers of four
+  if (M <= DECODE_GEMV_MAX_M && g.K <= 1024) {  // two chunks a lane: half the registers of four
     const bool nt = g.N * g.K * 2 >= DECODE_STREAM_BYTES;
-    if (M == 1) {
-      if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-      else decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
-    } else {
-      if (nt) decode_matvec_kernel<2, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-      else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+    switch (M) {
+      case 1:
+        if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
+        else decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
+        break;
+      case 2:
+        if (nt) decode_matvec_kernel<2, MODE, 2, true><<<grid, 256, 0, st>>>(g);
+        else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+        break;
+      case 3: decode_matvec_kernel<3, MODE, 2><<<grid, 256, 0, st>>>(g); break;
+      case 4: decode_matvec_kernel<4, MODE, 2><<<grid, 256, 0, st>>>(g); break;
+      case 5: decode_matvec_kernel<5, MODE, 2><<<grid, 256, 0, st>>>(g); break;
+      default: decode_matvec_kernel<6, MODE, 2><<<grid, 256, 0, st>>>(g); break;
     }
     return;
   }

@@ -127,7 +127,7 @@ bool decode_fused(const mi_llama *m, int64_t batch) {
 
 // The layers of a decode step on the hidden rows x [batch, hidden]: the new
 // position pos0 (immediate) or held on the device in `pos`, the attention
-// planned for `span` positions.  Five launches a layer up to 2 sequences
+// planned for `span` positions.  Five launches a layer up to 6 sequences
 // (q|k|v and the attention's chunks in one), six above.
 Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, int64_t pos0, int64_t span) {
   const mi_llama_config &c = m->cfg;
