@@ -144,7 +144,7 @@ def top1_agrees(got, want, err):
     return int(clear.sum())
 
 
-@pytest.mark.parametrize("batch", [1, 32])
+@pytest.mark.parametrize("batch", [1, 5, 32])  # the fused decode step up to 6 sequences, the matrix cores above
 def test_smollm2_shape_logits_within_tolerance(engine, smol, batch):
     """All 30 layers at SmolLM2-135M's shape: the prefill's logits at every
     prompt position, then four single-token steps through the KV cache,
@@ -243,7 +243,8 @@ def test_smollm2_shape_greedy_generation(engine, smol, batch):
         assert clear.mean() >= 0.7, clear.mean()
 
 
-@pytest.mark.parametrize("batch,numerics", [(1, "reference"), (32, "reference"), (32, "performance")])
+@pytest.mark.parametrize("batch,numerics", [(1, "reference"), (5, "performance"), (32, "reference"),
+                                            (32, "performance")])
 def test_traced_generation_equals_eager(engine, smol, smol_perf, batch, numerics):
     """The decode step captured once per 64-position span and replayed per
     token (the reference's TracedGenerator) gives the eager loop's tokens;
