@@ -256,7 +256,8 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     decode `new` tokens; tokens/s of the prefill and of the decode steps.
     `numerics`: the reference contract (F32 KV cache and activations) or the
     performance one (BF16 KV cache, BF16 prefill activation operands).  The
-    generation runs eagerly, then traced (the prompt's prefill and each decode
+    generation runs eagerly (after an untimed one of the same prompt, so the
+    allocator's blocks exist), then traced (the prompt's prefill and each decode
     step replays of captures -- the step per 64-position span -- token ids in
     and out through the host: the reference's TracedGenerator); the traced
     run's captures are made by an untimed first traced generation, and its
@@ -267,7 +268,7 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt + new, max_batch=batch, seed=5, numerics=numerics)
     rng = np.random.default_rng(9)
     ids = rng.integers(0, 49152, (batch, prompt)).astype(np.int32)
-    m.generate(ids[:, :32], 4)  # warm the kernels
+    m.generate(ids, 4)  # warm the kernels and the allocator at the measured shapes
     out, pf_ms, dc_ms = m.generate(ids, new)
     tr_ms = tr_pf = None
     if traced:

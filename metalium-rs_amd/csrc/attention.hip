@@ -276,7 +276,12 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
 // to its 64 x 32 output accumulator.  Only the order of the sums differs from
 // the composition.  D = 64.
 constexpr int FLASH_MIN_T = 64;  // new positions per sequence that take it
-constexpr int64_t FLASH_MIN_BLOCKS = 128;
+// Below FLASH_MIN_BLOCKS (run, sequence, kv head) blocks the kernel splits
+// its keys into ranges of 128 -- 64 where that still leaves fewer than
+// FLASH_MIN_BLOCKS (run, item, range) blocks -- and the combine pass adds
+// the ranges (512-token prompts, ms: batch 1 2.98 -> 2.74 at 64 keys,
+// batch 2 3.98 -> 3.59 and batch 4 6.69 -> 6.52 at 128).
+constexpr int64_t FLASH_MIN_BLOCKS = 256;
 
 typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -327,7 +332,7 @@ __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const 
 template <int G, typename KV>
 __global__ void __launch_bounds__(G * 64)
 flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int64_t T, int64_t H, int64_t KVH,
-                      int64_t pos0, int64_t maxc, float scale) {
+                      int64_t pos0, int64_t maxc, float scale, int64_t kchunk, float *part) {
   constexpr int D = 64, NT = G * 64;
   constexpr bool EXACT = sizeof(KV) == 2;  // a BF16 cache: one part
   constexpr int KP = EXACT ? 1 : 3;
@@ -343,7 +348,12 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
   const KV *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
   const int ctx32 = static_cast<int>(ctx);  // the host keeps a cache item below 2^31 / D rows
   const int64_t nqb = (T + 31) / 32;
-  for (int pass = 0; pass < 2; ++pass) {
+  // Split over keys (kchunk > 0): block (query run x, item y, key range z)
+  // takes keys [z kchunk, (z + 1) kchunk) of its run's and writes the
+  // range's partials (max, sum, unnormalised P V) for the combine pass;
+  // one run a block, no pairing.
+  const bool split = kchunk > 0;
+  for (int pass = 0; pass < (split ? 1 : 2); ++pass) {
     const int64_t qb = pass == 0 ? static_cast<int64_t>(blockIdx.x) : nqb - 1 - blockIdx.x;
     if (pass == 1 && qb == static_cast<int64_t>(blockIdx.x)) break;
     const int64_t p0 = qb * 32, p = p0 + n;
@@ -373,7 +383,9 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
 #pragma unroll
     for (int r = 0; r < 16; ++r) { o0[r] = 0.0f; o1[r] = 0.0f; }
     float m = -INFINITY, l = 0.0f;
-    const int64_t kend = pos0 + (p0 + 32 < T ? p0 + 32 : T);
+    const int64_t kend_run = pos0 + (p0 + 32 < T ? p0 + 32 : T);
+    const int64_t kbeg = split ? static_cast<int64_t>(blockIdx.z) * kchunk : 0;
+    const int64_t kend = split ? (kbeg + kchunk < kend_run ? kbeg + kchunk : kend_run) : kend_run;
     // Key and value blocks: 512 groups of 4 values each (key e / 16, d 4 (e % 16)),
     // loaded into registers for the next block while the current one is used.
     constexpr int PER = (32 * 16 + NT - 1) / NT;
@@ -422,10 +434,10 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
         }
       }
     };
-    fetch(0);
+    fetch(kbeg < kend ? kbeg : 0);
     stage(0);
     __syncthreads();
-    for (int64_t j0 = 0, it = 0; j0 < kend; j0 += 32, ++it) {
+    for (int64_t j0 = kbeg, it = 0; j0 < kend; j0 += 32, ++it) {
       const int buf = static_cast<int>(it & 1);
       const bool more = j0 + 32 < kend;
       if (more) fetch(j0 + 32);
@@ -502,7 +514,26 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
       if (more) stage(buf ^ 1);
       __syncthreads();
     }
-    if (live) {
+    if (split) {
+      if (live) {
+        // The combine's layout: item (sequence, kv head, position), range z;
+        // the max in natural units (the scores here are in base 2).
+        float *pbk = part + (((b * KVH + j) * T + p) * gridDim.z + blockIdx.z) * static_cast<int64_t>(G * (D + 2));
+        if (half == 0) {
+          const float mc = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
+          pbk[g] = mc > -FLT_MAX ? mc * 0.6931471805599453f : mc;
+          pbk[G + g] = l;
+        }
+        float *orow = pbk + 2 * G + g * D + 4 * half;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            orow[8 * c + i] = o0[4 * c + i];
+            orow[32 + 8 * c + i] = o1[4 * c + i];
+          }
+      }
+    } else if (live) {
       const float den = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
       float *orow = out + (b * T + p) * H * D + h * D + 4 * half;
 #pragma unroll
@@ -518,17 +549,27 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
 
 template <int G, typename KV>
 void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch, int64_t T,
-                  int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
+                  int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale, int64_t kchunk, int S,
+                  float *part) {
+  if (kchunk > 0) {
+    const dim3 grid(static_cast<unsigned>((T + 31) / 32), static_cast<unsigned>(batch * KVH), static_cast<unsigned>(S));
+    flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk, part);
+    attention_combine_kernel<64, G><<<static_cast<unsigned>(batch * KVH * T), 256,
+                                         static_cast<size_t>(3 * G * S + G) * sizeof(float), st>>>(part, out, T, H, KVH,
+                                                                                                   S);
+    return;
+  }
   const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
-  flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale);
+  flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
 }
 
 template <typename KV>
 bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch,
-                    int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale) {
+                    int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale, int64_t kchunk,
+                    int S, float *part) {
   switch (G) {
 #define MI_FLASH_G(gg) \
-  case gg: launch_flash<gg, KV>(st, q, k, v, out, batch, T, H, KVH, pos0, maxc, scale); return true;
+  case gg: launch_flash<gg, KV>(st, q, k, v, out, batch, T, H, KVH, pos0, maxc, scale, kchunk, S, part); return true;
     MI_FLASH_G(1) MI_FLASH_G(2) MI_FLASH_G(3) MI_FLASH_G(4) MI_FLASH_G(5) MI_FLASH_G(6) MI_FLASH_G(7) MI_FLASH_G(8)
 #undef MI_FLASH_G
     default:
@@ -1009,7 +1050,8 @@ struct AttPlan {
   bool kv16;  // BF16 caches (else F32)
   int64_t D, G, maxc, items, S, chunk;
   size_t part_bytes;
-  bool flash;  // many new positions: the matrix-core kernel, no chunk partials
+  bool flash;  // many new positions: the matrix-core kernel
+  int64_t fchunk, fS;  // its key ranges when split (fchunk 0: whole runs, no partials)
   AttPos pos;
 };
 
@@ -1077,14 +1119,22 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
   P->v = vb->ptr;
   P->kv16 = kb->elem == MI_BF16;
   P->D = D; P->G = G; P->maxc = maxc; P->items = items; P->S = S; P->chunk = chunk;
-  // The matrix-core kernel from 128 (32 positions, sequence, kv head)
-  // blocks; fewer keep the key-chunked kernel (512-token prompts: batch 1,
-  // 48 blocks, 4.27 ms against 3.92 on the chunked kernel; batch 4, 192
-  // blocks, 8.0 against 10.9).
-  P->flash = !pos_dev && span == pos0 + t && D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535 &&
-             (t + 31) / 32 * batch * kv_heads >= FLASH_MIN_BLOCKS;
+  // The matrix-core kernel for 64+ new positions with 64-wide heads, its
+  // keys split into ranges on small grids (whole, paired runs of a 512-token
+  // prompt at batch 1 took 4.27 ms against 3.92 on the key-chunked kernel).
+  P->flash = !pos_dev && span == pos0 + t && D == 64 && t >= FLASH_MIN_T && batch * kv_heads <= 65535;
+  P->fchunk = P->fS = 0;
+  const int64_t runs = (t + 31) / 32 * batch * kv_heads;
+  if (P->flash && runs < FLASH_MIN_BLOCKS) {
+    P->fchunk = runs * ((pos0 + t + 127) / 128) >= FLASH_MIN_BLOCKS ? 128 : 64;
+    P->fS = (pos0 + t + P->fchunk - 1) / P->fchunk;
+    if (P->fS > 65535 || static_cast<size_t>(3 * G * P->fS + G) * sizeof(float) > 65536) P->flash = false;
+  }
   P->pos = AttPos{pos0, pos_dev, span, flags(ctx)};
-  P->part_bytes = S > 1 && !P->flash ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
+  if (P->flash)
+    P->part_bytes = P->fchunk ? static_cast<size_t>(items * P->fS * G * (D + 2)) * sizeof(float) : 0;
+  else
+    P->part_bytes = S > 1 ? static_cast<size_t>(items * S * G * (D + 2)) * sizeof(float) : 0;
   return MI_OK;
 }
 
@@ -1093,7 +1143,8 @@ void attention_launch_kv(Ctx *ctx, const AttPlan &P, float *out, float *part, in
                          int64_t heads, int64_t kv_heads, float scale) {
   const KV *k = static_cast<const KV *>(P.k), *v = static_cast<const KV *>(P.v);
   if (P.flash) {
-    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, P.pos.pos0, P.maxc, scale);
+    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, P.pos.pos0, P.maxc, scale,
+                       P.fchunk, static_cast<int>(P.fS), part);
     return;
   }
   const int Si = static_cast<int>(P.S);

@@ -96,12 +96,11 @@ constexpr int64_t kFusedAttentionMaxT = 16;
 // (scores, masked softmax, P V and the regroup never touch HBM); at batch 32
 // the composition's matrix-core products win (37 against 43.5 ms).
 constexpr int64_t kFusedAttentionLongMaxBatch = 4;
-// New positions (and blocks of 32 positions x sequences x kv heads) from
-// which mi_attention_rows runs 64-wide heads on the matrix cores (its flash
-// kernel).
-constexpr int64_t kFlashMinT = 64, kFlashMinBlocks = 128;
+// New positions from which mi_attention_rows runs 64-wide heads on the
+// matrix cores (its flash kernel, keys split into ranges on small grids).
+constexpr int64_t kFlashMinT = 64;
 // Largest batch whose decode step takes the fused projections, and whose
-// head is one fused norm + projection launch (mi_norm_matvec: the GEMV up to 2
+// head is one fused norm + projection launch (mi_norm_matvec: the GEMV up to 6
 // rows, the matrix-core form above; beyond kFusedHeadMaxBatch the head is a
 // plain product on the matrix cores).
 constexpr int64_t kDecodeMaxBatch = 32;
@@ -166,7 +165,7 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   // mi_attention_rows) or of a few sequences; other long prompts take the
   // product composition.
   const bool fused = (t <= kFusedAttentionMaxT || batch <= kFusedAttentionLongMaxBatch ||
-                      (D == 64 && t >= kFlashMinT && (t + 31) / 32 * batch * KVH >= kFlashMinBlocks)) &&
+                      (D == 64 && t >= kFlashMinT)) &&
                      (D == 16 || D == 32 || D == 64 || D == 128) && G <= 8;
   // The composition's causal mask for t > 1, rows (position, group) of one
   // item: row p * G + g attends to cache columns <= pos0 + p.
