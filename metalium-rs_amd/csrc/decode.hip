@@ -194,7 +194,7 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
 template <int M, int MODE, int PRE = 4, bool NTW = false>
 __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int lane = threadIdx.x & 63;
-  const int64_t p = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const int64_t p = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
   if (p >= g.npairs) return;  // whole wavefronts
   const PairRows q = pair_rows<MODE>(g, p);
   const int64_t r1c = q.has1 ? q.r1 : q.r0;
@@ -875,20 +875,24 @@ static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     return;
   }
   if (M <= DECODE_GEMV_MAX_M && g.K <= 1024) {  // two chunks a lane: half the registers of four
+    // One wavefront a block (a pair each): the few hundred pairs of a layer's
+    // products spread over that many CUs (batch-1 SmolLM2 step 0.703 ->
+    // 0.695 ms); the streamed head keeps four.
     const bool nt = g.N * g.K * 2 >= DECODE_STREAM_BYTES;
+    const unsigned g1 = static_cast<unsigned>(g.npairs);
     switch (M) {
       case 1:
         if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-        else decode_matvec_kernel<1, MODE, 2><<<grid, 256, 0, st>>>(g);
+        else decode_matvec_kernel<1, MODE, 2><<<g1, 64, 0, st>>>(g);
         break;
       case 2:
         if (nt) decode_matvec_kernel<2, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-        else decode_matvec_kernel<2, MODE, 2><<<grid, 256, 0, st>>>(g);
+        else decode_matvec_kernel<2, MODE, 2><<<g1, 64, 0, st>>>(g);
         break;
-      case 3: decode_matvec_kernel<3, MODE, 2><<<grid, 256, 0, st>>>(g); break;
-      case 4: decode_matvec_kernel<4, MODE, 2><<<grid, 256, 0, st>>>(g); break;
-      case 5: decode_matvec_kernel<5, MODE, 2><<<grid, 256, 0, st>>>(g); break;
-      default: decode_matvec_kernel<6, MODE, 2><<<grid, 256, 0, st>>>(g); break;
+      case 3: decode_matvec_kernel<3, MODE, 2><<<g1, 64, 0, st>>>(g); break;
+      case 4: decode_matvec_kernel<4, MODE, 2><<<g1, 64, 0, st>>>(g); break;
+      case 5: decode_matvec_kernel<5, MODE, 2><<<g1, 64, 0, st>>>(g); break;
+      default: decode_matvec_kernel<6, MODE, 2><<<g1, 64, 0, st>>>(g); break;
     }
     return;
   }
