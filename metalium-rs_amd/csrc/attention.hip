@@ -696,20 +696,27 @@ __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4
 
 // A thread's operands of the norm and the rotation, requested with the
 // weights so neither phase waits for a round trip of its own: the float4 of
-// the hidden row b and of the gain at 4 tid (k <= 1024: one a thread), and
-// for tid < 32 the rotary table entries of pair (tid, tid + 32) at pos.
+// the hidden row b and of the gain at 4 tid (k <= 1024: one a thread) --
+// requested before a device-held position is read, so the norm does not wait
+// for that read -- and for tid < 32 the rotary table entries of pair (tid,
+// tid + 32) at the position.
 struct DqaPre {
   float4 x, gm;
   float cs0, cs1, sn0, sn1;
 };
-__device__ __forceinline__ DqaPre dqa_pre(const DqaArgs &g, int64_t b, int64_t pos) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void dqa_pre_x(const DqaArgs &g, int64_t b, DqaPre &e) {
+  const int64_t k = 4 * threadIdx.x < g.K ? 4 * threadIdx.x : g.K - 4;
+  e.x = *reinterpret_cast<const float4 *>(g.x + b * g.K + k);
+  e.gm = *reinterpret_cast<const float4 *>(g.gamma + k);
+}
+__device__ __forceinline__ void dqa_pre_rot(const DqaArgs &g, int64_t pos, DqaPre &e) {
   constexpr int half = DQA_D / 2;
-  const int64_t k = 4 * tid < g.K ? 4 * tid : g.K - 4;
-  const int i = tid & (half - 1);
+  const int i = threadIdx.x & (half - 1);
   const float *cs = g.cos + pos * DQA_D, *sn = g.sin + pos * DQA_D;
-  return DqaPre{*reinterpret_cast<const float4 *>(g.x + b * g.K + k), *reinterpret_cast<const float4 *>(g.gamma + k),
-                cs[i], cs[i + half], sn[i], sn[i + half]};
+  e.cs0 = cs[i];
+  e.cs1 = cs[i + half];
+  e.sn0 = sn[i];
+  e.sn1 = sn[i + half];
 }
 
 // The hidden row times the gain into LDS, xg[k] = x[k] gamma[k], and the
@@ -728,7 +735,7 @@ __device__ __forceinline__ float dqa_stage(const DqaArgs &g, const DqaPre &pre, 
 }
 
 // RoPE of a 64-wide head in LDS (raw -> rot): the rotation of pair (i, i +
-// 32) as the decode projections apply it, the table entries from dqa_pre.
+// 32) as the decode projections apply it, the table entries from dqa_pre_rot.
 __device__ __forceinline__ void dqa_rope(const DqaPre &pre, const float *raw, float *rot) {
   const int tid = threadIdx.x;
   constexpr int half = DQA_D / 2;
@@ -846,6 +853,8 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     const int64_t kb = bid - natt, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
     uint4 wr[CH];
     dqa_wload<CH>(g.w + ((g.H + which * g.KVH + j) * D) * g.K, g.K, wr);
+    DqaPre pre;
+    dqa_pre_x(g, b, pre);
     int64_t pos = g.pa.pos0;
     bool ok = true;
     if (g.pa.dev) {
@@ -853,7 +862,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
       ok = pos >= 0 && pos + 1 <= g.pa.span;
       pos = ok ? pos : 0;
     }
-    const DqaPre pre = dqa_pre(g, b, pos);
+    dqa_pre_rot(g, pos, pre);
     const float rms = dqa_stage(g, pre, xn, red4);
     const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
@@ -876,6 +885,8 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   // The weights first: they do not wait for a position read on the device.
   uint4 wr[CH];
   dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
+  DqaPre pre;
+  dqa_pre_x(g, b, pre);
   const int64_t pos = att_pos0(g.pa, 1);
   const int64_t lo = s * g.chunk, len = pos > lo ? (pos - lo < g.chunk ? pos - lo : g.chunk) : 0;
   const int64_t PS = static_cast<int64_t>(g.G) * (D + 2);
@@ -901,7 +912,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     kpre[u] = f32x4_get(Kc + (c < len ? c : last) * D + 4 * sl);
     vv[u] = f32x4_get(Vc + (c < len ? c : last) * D + 4 * sl);
   }
-  const DqaPre pre = dqa_pre(g, b, pos);
+  dqa_pre_rot(g, pos, pre);
   const float rms = dqa_stage(g, pre, xn, red4);
   {
     const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
