@@ -232,10 +232,31 @@ struct GemmArgs {
   int64_t kb = 0;
 };
 
-__device__ __forceinline__ float epilogue(const GemmArgs &g, int64_t row, int64_t col, float v) {
-  if (g.bias) v = __fadd_rn(v, g.bias[col]);
-  if (g.resid) v = __fadd_rn(g.resid[row * g.ldr + col], v);
-  return v;
+// The epilogue over one 32 x 32 accumulator fragment, whose lane holds column
+// `col` at rows row0 + 8 (r / 4) + r % 4: the fragment's 16 residual values
+// and its bias are all requested before any result is stored.  The result
+// may be the residual itself (an in-place update), so a residual load issued
+// after a store the compiler cannot prove disjoint waits for that store; per
+// value, that chain made the write-out latency-bound.  Out-of-range values
+// (GUARD) are not read.
+template <bool GUARD>
+__device__ __forceinline__ void fragment_epilogue(const GemmArgs &g, int64_t row0, int64_t col, float (&v)[16]) {
+  float e[16];
+  if (g.resid) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + 8 * (r >> 2) + (r & 3);
+      e[r] = (!GUARD || (row < g.M && col < g.N)) ? g.resid[row * g.ldr + col] : 0.f;
+    }
+  }
+  const float b = (g.bias && (!GUARD || col < g.N)) ? g.bias[col] : 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = v[r];
+    if (g.bias) x = __fadd_rn(x, b);
+    if (g.resid) x = __fadd_rn(e[r], x);
+    v[r] = x;
+  }
 }
 
 // Map a linear workgroup id to an output tile (tm, tn), grouping the tiles
@@ -364,18 +385,23 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
   }
 
   // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
+  const bool epi = g.bias != nullptr || g.resid != nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+      const int64_t rb = m0 + wm * WTM + i * 32 + 4 * lhalf;
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = acc[i][j][r];
+      if (epi) fragment_epilogue<GUARD>(g, rb, col, v);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        const int64_t row = rb + 8 * (r >> 2) + (r & 3);
         if (!GUARD || (row < g.M && col < g.N)) {
-          const float v = epilogue(g, row, col, acc[i][j][r]);
-          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
-          else C[row * g.ldc + col] = v;
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v[r]);
+          else C[row * g.ldc + col] = v[r];
         }
       }
     }
@@ -637,18 +663,23 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_split_kernel(GemmArgs g) {
   }
 
   // Epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4.
+  const bool epi = g.bias != nullptr || g.resid != nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+      const int64_t rb = m0 + wm * WTM + i * 32 + 4 * lhalf;
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = acc[i][j][r];
+      if (epi) fragment_epilogue<GUARD>(g, rb, col, v);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        const int64_t row = rb + 8 * (r >> 2) + (r & 3);
         if (!GUARD || (row < g.M && col < g.N)) {
-          const float v = epilogue(g, row, col, acc[i][j][r]);
-          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v);
-          else C[row * g.ldc + col] = v;
+          if constexpr (sizeof(TO) == 2) C[row * g.ldc + col] = f32_to_bf16_bits(v[r]);
+          else C[row * g.ldc + col] = v[r];
         }
       }
     }
@@ -988,13 +1019,15 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
     for (int j = 0; j < TN; ++j) {
       if (GN && col0 + j * 32 >= g.N) continue;
       TO *cij = C + (row0 + i * 32) * g.ldc + col0 + j * 32;
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = acc[i][j][r];
+      if (!plain) fragment_epilogue<false>(g, row0 + i * 32, col0 + j * 32, v);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dr = 8 * (r >> 2) + (r & 3);
-        float v = acc[i][j][r];
-        if (!plain) v = epilogue(g, row0 + i * 32 + dr, col0 + j * 32, v);
-        if constexpr (sizeof(TO) == 2) cij[dr * g.ldc] = f32_to_bf16_bits(v);
-        else cij[dr * g.ldc] = v;
+        if constexpr (sizeof(TO) == 2) cij[dr * g.ldc] = f32_to_bf16_bits(v[r]);
+        else cij[dr * g.ldc] = v[r];
       }
     }
   }
