@@ -42,6 +42,18 @@ typedef uint64_t mi_id;
  * 32-bit words (a Bool is 0 or 1), BF16 two-byte slots. */
 enum mi_elem { MI_F32 = 0, MI_I32 = 1, MI_BOOL = 2, MI_BF16 = 3 };
 
+/* A result form, not a buffer kind: an F32 result [rows, cols] delivered as
+ * its two BF16 parts in a BF16 buffer [rows, 2 cols], each row's heads (the
+ * values rounded to nearest even; a finite value that would round to
+ * infinity keeps its truncated head) then its remainders (value - head,
+ * exact in F32, rounded to nearest even; 0 for an infinite or NaN value):
+ * head + remainder is within 2^-17 relative of the value.  It is the operand
+ * form of the fast matmul mode's split of F32 activations (a product taken as
+ * head . w + remainder . w); mi_rms_norm and mi_silu_mul_halves produce it as
+ * their `out_elem`, mi_linear_parts reads it, so a producer's F32 result
+ * reaches the product with no separate split pass.  No Engine counterpart. */
+enum mi_result_form { MI_BF16_PARTS = 4 };
+
 /* Status codes.  `MI_E_DOMAIN` is the reference's DOMAIN error for an index
  * out of range (crates/burn-tt/src/ops.rs:995-1000). */
 enum mi_status {
@@ -172,6 +184,18 @@ int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
  * none.  The result is F32, or BF16 rounded once after both adds. */
 int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias,
               mi_id residual, int out_elem, mi_id *out);
+/* mi_linear of an F32 `x` [m, k] given as its parts (MI_BF16_PARTS, a BF16
+ * `x_parts` [m, 2 k]) against a BF16 `w`: the product runs as head . op(w) +
+ * remainder . op(w), accumulated in F32 over the 2 k parts in that order --
+ * what the fast matmul mode computes from `x` itself where it splits it (F32
+ * x BF16 products filling the chip: m a multiple of 256, k of 32), and then
+ * bit for bit the same result; in either matmul mode.  Other shapes run the
+ * same sums on the plain BF16 product against `w` repeated along k.  Bias,
+ * residual and result as mi_linear.  No Engine counterpart: the reference
+ * fuses operation chains in its fusion runtime (crates/burn-tt/src/fusion/
+ * mod.rs:1-12) instead. */
+int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed,
+                    mi_id bias, mi_id residual, int out_elem, mi_id *out);
 
 /* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
  * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as
@@ -263,7 +287,8 @@ int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, int log,
 
 /* ---- RMSNorm: Engine::rms_norm_as (server.rs:449) ----
  * `a / sqrt(mean(a * a) + eps) * gamma` over each row; `gamma` a `[1, cols]`
- * row or 0. */
+ * row or 0.  `out_elem` MI_F32, MI_BF16 or MI_BF16_PARTS (the F32 result's
+ * parts, [rows, 2 cols] BF16). */
 int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem,
                 mi_id *out);
 /* Engine::add_rms_norm (server.rs:466-475): `sum = a + b` and
@@ -467,7 +492,8 @@ int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
  * tt-models/src/llama.rs:494-498, on the two row blocks of its gate|up
  * weight); no Engine counterpart.  F32: bit-identical to MI_K_SILU_MUL of the
  * two halves; BF16: that value rounded once (the performance contract's
- * activation operand, llama.rs:1270-1274). */
+ * activation operand, llama.rs:1270-1274); MI_BF16_PARTS: the F32 value's
+ * parts ([rows, 2 i] BF16). */
 int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, int out_elem, mi_id *out);
 /* The q|k|v tail of a prefill in one launch: the composition the reference's
  * attention block makes of RoPE on the query and key heads, the key/value

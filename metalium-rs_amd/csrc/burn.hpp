@@ -235,6 +235,16 @@ inline Tensor linear(const Tensor &x, const Tensor &w, bool tw, const Tensor *bi
   return Tensor(x.ctx(), id, {x.rows(), tw ? w.rows() : w.cols()});
 }
 
+// linear() of an F32 operand given as its BF16 parts ([m, 2 k], MI_BF16_PARTS
+// from rms_norm or silu_mul_halves): mi_linear_parts.
+inline Tensor linear_parts(const Tensor &x_parts, const Tensor &w, bool tw, const Tensor *bias, const Tensor *residual,
+                           int out_elem = MI_F32) {
+  mi_id id;
+  check(x_parts.ctx(), mi_linear_parts(x_parts.ctx(), x_parts.use(), w.use(), tw, bias ? bias->use() : 0,
+                                       residual ? residual->use() : 0, out_elem, &id), "linear_parts");
+  return Tensor(x_parts.ctx(), id, {x_parts.rows(), tw ? w.rows() : w.cols()});
+}
+
 // Grouped strided products written into `out` in place (item (g, i) of an
 // operand at at[0] + g * at[1] + i * at[2], read with its row pitch).
 struct Items {
@@ -276,9 +286,12 @@ inline Tensor softmax_rows(const Tensor &x, const Tensor *mask, float scale, boo
   return Tensor(x.ctx(), id, x.shape());
 }
 
+// RMSNorm over rows: F32, rounded to BF16, or as its BF16 parts ([rows,
+// 2 cols]).
 inline Tensor rms_norm(const Tensor &x, const Tensor &gamma, float eps, int out_elem = MI_F32) {
   mi_id id;
   check(x.ctx(), mi_rms_norm(x.ctx(), x.use(), gamma.use(), eps, out_elem, &id), "rms_norm");
+  if (out_elem == MI_BF16_PARTS) return Tensor(x.ctx(), id, {x.rows(), 2 * x.cols()});
   return Tensor(x.ctx(), id, x.shape());
 }
 
@@ -374,11 +387,11 @@ inline Tensor rope(const Tensor &x, const Tensor &cos, const Tensor &sin, int64_
 }
 
 // silu(gate) * up of a fused gate|up product's halves (mi_silu_mul_halves),
-// F32 or rounded to BF16.
+// F32, rounded to BF16, or as its BF16 parts (twice as many columns).
 inline Tensor silu_mul_halves(const Tensor &gate_up, int out_elem = MI_F32) {
   mi_id id;
   check(gate_up.ctx(), mi_silu_mul_halves(gate_up.ctx(), gate_up.use(), out_elem, &id), "silu_mul_halves");
-  return Tensor(gate_up.ctx(), id, {gate_up.rows(), gate_up.cols() / 2});
+  return Tensor(gate_up.ctx(), id, {gate_up.rows(), out_elem == MI_BF16_PARTS ? gate_up.cols() : gate_up.cols() / 2});
 }
 
 // The prefill's q|k|v tail (mi_qkv_rope_cache): RoPE, cache writes, q out.

@@ -44,6 +44,32 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// An F32 value as two BF16 parts, hi + lo within 2^-17 relative of it: hi
+// rounded to nearest even, lo the BF16 of the exact F32 remainder a - hi.  A
+// finite value above the largest BF16 would round to infinity: it keeps the
+// truncated head instead (its remainder is still exact in F32).  An infinite
+// or NaN value is carried by its head alone.
+__device__ __forceinline__ void split_bf16(float a, uint16_t &hi, uint16_t &lo) {
+  hi = f32_to_bf16_bits(a);
+  if (((hi & 0x7fffu) == 0x7f80u) && ((__float_as_uint(a) & 0x7f800000u) != 0x7f800000u))
+    hi = static_cast<uint16_t>(__float_as_uint(a) >> 16);
+  const float r = a - bf16_bits_to_f32(hi);
+  lo = (r == r) ? f32_to_bf16_bits(r) : 0;
+}
+
+// Four consecutive F32 values of a row as parts: their heads at hp, their
+// remainders at lp (a row of MI_BF16_PARTS keeps its heads, then its
+// remainders).
+__device__ __forceinline__ void parts4_put(uint16_t *hp, uint16_t *lp, float4 v) {
+  uint16_t h[4], l[4];
+  split_bf16(v.x, h[0], l[0]);
+  split_bf16(v.y, h[1], l[1]);
+  split_bf16(v.z, h[2], l[2]);
+  split_bf16(v.w, h[3], l[3]);
+  *reinterpret_cast<uint2 *>(hp) = make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
+  *reinterpret_cast<uint2 *>(lp) = make_uint2(l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16));
+}
+
 // F32 values in F32 or BF16 (uint16_t bits) storage -- a KV cache under the
 // reference or the performance numeric contract, an activation stored for a
 // product's operand: four consecutive values widened to F32, and F32 values

@@ -549,6 +549,15 @@ decode_mfma_kernel(DecodeArgs g, int M) {
       ga[s][1] = *reinterpret_cast<const float4 *>(g.gamma + k + 4);
     }
   }
+  // The residual value this thread's epilogue adds (row mo below), requested
+  // with the weights rather than after the fold.
+  float rpre = 0.0f;
+  if constexpr (MODE == DM_PLAIN) {
+    if (g.resid) {
+      const int mo = 8 * (w >> 2) + 4 * kg + (w & 3);
+      rpre = g.resid[(mo < M ? mo : 0) * g.ldo + rowc[0]];
+    }
+  }
   dm_f32x16 acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -615,7 +624,7 @@ decode_mfma_kernel(DecodeArgs g, int M) {
     if constexpr (MODE == DM_PLAIN) {
       if (rv[0]) {
         float *o = g.out + mo * g.ldo + row[0];
-        *o = g.resid ? __fadd_rn(g.resid[mo * g.ldo + row[0]], y[0]) : y[0];
+        *o = g.resid ? __fadd_rn(rpre, y[0]) : y[0];
       }
     } else if constexpr (MODE == DM_SILU_MUL) {
       if (rv[0]) g.out[mo * g.ldo + row[0]] = silu2(y[0]) * y[1];

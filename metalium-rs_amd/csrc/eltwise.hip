@@ -657,9 +657,12 @@ __global__ void rope_kernel(const float *x, const float *cosp, const float *sinp
 // silu(gate) * up over the two halves of a fused gate|up product's rows,
 // gu [rows, 2 i] -> [rows, i], with SILU_MUL's arithmetic; four columns a
 // thread when i is a multiple of 4.  TO: F32, or BF16 (the result rounded once
-// as stored, for a product that reads BF16 activations).
-template <bool VEC, typename TO>
+// as stored, for a product that reads BF16 activations); PARTS (TO = BF16):
+// the F32 result's parts, row r's heads at out[2 r i ...] and its remainders
+// i further.
+template <bool VEC, typename TO, bool PARTS = false>
 __global__ void silu_mul_halves_kernel(const float *gu, TO *out, int64_t rows, int64_t inner) {
+  static_assert(!PARTS || sizeof(TO) == 2, "parts are BF16");
   const int64_t per = VEC ? inner / 4 : inner, n = rows * per;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
@@ -672,9 +675,18 @@ __global__ void silu_mul_halves_kernel(const float *gu, TO *out, int64_t rows, i
       y.y = op<MI_K_SILU_MUL>(g.y, u.y, 0.f, 0.f, 0.f);
       y.z = op<MI_K_SILU_MUL>(g.z, u.z, 0.f, 0.f, 0.f);
       y.w = op<MI_K_SILU_MUL>(g.w, u.w, 0.f, 0.f, 0.f);
-      f32x4_put(out + r * inner + 4 * c, y);
+      if constexpr (PARTS) parts4_put(out + r * 2 * inner + 4 * c, out + r * 2 * inner + inner + 4 * c, y);
+      else f32x4_put(out + r * inner + 4 * c, y);
     } else {
-      f32_put(out + r * inner + c, op<MI_K_SILU_MUL>(gu[r * 2 * inner + c], gu[r * 2 * inner + inner + c], 0.f, 0.f, 0.f));
+      const float y = op<MI_K_SILU_MUL>(gu[r * 2 * inner + c], gu[r * 2 * inner + inner + c], 0.f, 0.f, 0.f);
+      if constexpr (PARTS) {
+        uint16_t h, l;
+        split_bf16(y, h, l);
+        out[r * 2 * inner + c] = h;
+        out[r * 2 * inner + inner + c] = l;
+      } else {
+        f32_put(out + r * inner + c, y);
+      }
     }
   }
 }
@@ -817,16 +829,23 @@ extern "C" int mi_silu_mul_halves(mi_ctx *ctx, mi_id gate_up, int out_elem, mi_i
   if (gb->elem != MI_F32 || gb->cols % 2)
     return fail(ctx, MI_E_ARG, "silu_mul_halves of %s [%lld, %lld]: want F32 with an even width", elem_name(gb->elem),
                 (long long)gb->rows, (long long)gb->cols);
-  if (out_elem != MI_F32 && out_elem != MI_BF16)
-    return fail(ctx, MI_E_ARG, "silu_mul_halves result kind %s", elem_name(out_elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16 && out_elem != MI_BF16_PARTS)
+    return fail(ctx, MI_E_ARG, "silu_mul_halves result kind %d", out_elem);
   const int64_t R = gb->rows, I = gb->cols / 2;
+  const bool parts = out_elem == MI_BF16_PARTS;
   mi_id id; Buffer *ob;
-  int s = new_buffer(ctx, R, I, out_elem, &id, &ob);
+  int s = new_buffer(ctx, R, parts ? 2 * I : I, parts ? MI_BF16 : out_elem, &id, &ob);
   if (s) return s;
   if (R * I > 0) {
     const float *gp = static_cast<const float *>(gb->ptr);
     const unsigned gv = grid_for(R * I / 4, 256 * 2, 256 * 128), gs = grid_for(R * I, 256 * 4, 256 * 64);
-    if (out_elem == MI_BF16) {
+    if (parts) {
+      uint16_t *op_ = static_cast<uint16_t *>(ob->ptr);
+      if (I % 4 == 0)
+        silu_mul_halves_kernel<true, uint16_t, true><<<gv, 256, 0, ctx->stream>>>(gp, op_, R, I);
+      else
+        silu_mul_halves_kernel<false, uint16_t, true><<<gs, 256, 0, ctx->stream>>>(gp, op_, R, I);
+    } else if (out_elem == MI_BF16) {
       uint16_t *op_ = static_cast<uint16_t *>(ob->ptr);
       if (I % 4 == 0)
         silu_mul_halves_kernel<true, uint16_t><<<gv, 256, 0, ctx->stream>>>(gp, op_, R, I);

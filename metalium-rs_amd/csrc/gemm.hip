@@ -420,16 +420,6 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmArgs g) {
 // v_mfma_f32_32x32x2f32.  The split happens in registers between the global
 // load and the LDS write: no pass over HBM, no extra launch.
 
-__device__ __forceinline__ void split_bf16(float a, uint16_t &hi, uint16_t &lo) {
-  hi = f32_to_bf16_bits(a);
-  // A finite value above the largest BF16 would round to infinity: keep the
-  // truncated head instead (its remainder is still exact in F32).
-  if (((hi & 0x7fffu) == 0x7f80u) && ((__float_as_uint(a) & 0x7f800000u) != 0x7f800000u))
-    hi = static_cast<uint16_t>(__float_as_uint(a) >> 16);
-  const float r = a - bf16_bits_to_f32(hi);
-  lo = (r == r) ? f32_to_bf16_bits(r) : 0;  // inf - inf: the head carries it
-}
-
 // Tile loader of the split kernel: ROWS rows x 64 k of an F32 (split into hi
 // and lo planes) or BF16 (hi plane only) operand, into swizzled 128-byte LDS
 // rows.  KCONTIG: source element (r, k) at src[r * ld + k], a unit is 8
@@ -1599,14 +1589,37 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const float *a, int64_t
 // the product then runs at the BF16 kernel's rate instead of the split
 // kernel's (whose per-tile conversions hold it to a fraction of it).  For
 // products big enough to fill the chip with 256 x 256 tiles.
+static bool parts_direct_fits(const Plan &p);
 static bool stacked_split_pays(const Plan &p) {
-  if (!p.fast || p.ea != MI_F32 || p.eb != MI_BF16 || p.ta || p.batch != 1 || p.kc != 0) return false;
-  if (p.K % 32 || p.M % 256 || p.lda % 4 || (reinterpret_cast<uintptr_t>(p.a) & 15) ||
-      (reinterpret_cast<uintptr_t>(p.b) & 15) || p.ldb % 8)
-    return false;
-  if (p.N % 256 && !(p.tb && p.N % 16 == 0)) return false;
+  if (!p.fast || p.ea != MI_F32 || p.kc != 0 || p.lda % 4 || (reinterpret_cast<uintptr_t>(p.a) & 15)) return false;
+  if (!parts_direct_fits(p)) return false;
   const int64_t tiles = (p.M / 256) * ((p.N + 255) / 256);
   return tiles >= 128 && p.M * p.N * p.K >= (int64_t(1) << 32);
+}
+
+// Whether the direct kernel takes an F32 x BF16 product of plan p from A's
+// parts: 256-row tiles, whole k-tiles on each side of the wrap, B's width
+// tiled by 256 or (k-contiguous B) a multiple of 16 for the edge tiles.
+static bool parts_direct_fits(const Plan &p) {
+  if (p.eb != MI_BF16 || p.ta || p.batch != 1 || p.K % 32 || p.M % 256) return false;
+  if ((reinterpret_cast<uintptr_t>(p.b) & 15) || p.ldb % 8) return false;
+  return p.N % 256 == 0 || (p.tb && p.N % 16 == 0);
+}
+
+// The product of plan p (A F32 [M, K]) from A's parts at `parts` ([M, 2 K]
+// BF16: each row's heads, then its remainders) on the direct kernel, B's k
+// wrapping every K.
+static hipError_t launch_parts(const Plan &p, const void *parts, hipStream_t st) {
+  Plan q = p;
+  q.a = parts;
+  q.ea = MI_BF16;
+  q.lda = 2 * p.K;
+  q.K = 2 * p.K;
+  q.kb = p.K;
+  const bool bf = p.eo == MI_BF16;
+  if (p.N % 256 == 0)
+    return bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe<float, 256, 256, 5, 2, 4>(q, st);
+  return bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, st);
 }
 
 static int run_stacked_split(mi_ctx *ctx, const Plan &p) {
@@ -1619,20 +1632,7 @@ static int run_stacked_split(mi_ctx *ctx, const Plan &p) {
   split_rows_kernel<<<g, 256, 0, ctx->stream>>>(static_cast<const float *>(p.a), p.lda,
                                                 static_cast<uint16_t *>(tb->ptr), p.M, p.K);
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) {
-    Plan q = p;
-    q.a = tb->ptr;
-    q.ea = MI_BF16;
-    q.lda = 2 * p.K;
-    q.K = 2 * p.K;
-    q.kb = p.K;
-    const bool bf = p.eo == MI_BF16;
-    if (p.N % 256 == 0)
-      e = bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, ctx->stream) : launch_pipe<float, 256, 256, 5, 2, 4>(q, ctx->stream);
-    else
-      e = bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, ctx->stream)
-             : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, ctx->stream);
-  }
+  if (e == hipSuccess) e = launch_parts(p, tb->ptr, ctx->stream);
   mi_free(ctx, tid);  // stream-ordered: the block is reused only by later work
   if (e != hipSuccess) return fail(ctx, MI_E_HIP, "matmul launch: %s", hipGetErrorString(e));
   return check_launch(ctx, "matmul");
@@ -1812,6 +1812,26 @@ extern "C" int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
   return MI_OK;
 }
 
+// A linear layer's bias (n elements) and residual ([m, n]), F32, each 0 for none.
+static int linear_terms(mi_ctx *ctx, mi_id bias, mi_id residual, int64_t m, int64_t n, LinearTerms *lin) {
+  if (bias) {
+    MI_BUF(ctx, Bb, bias);
+    if (Bb->elem != MI_F32 || Bb->numel() != n)
+      return fail(ctx, MI_E_ARG, "linear: bias is %s [%lld, %lld], want F32 with %lld elements", elem_name(Bb->elem),
+                  (long long)Bb->rows, (long long)Bb->cols, (long long)n);
+    lin->bias = static_cast<const float *>(Bb->ptr);
+  }
+  if (residual) {
+    MI_BUF(ctx, R, residual);
+    if (R->elem != MI_F32 || R->rows != m || R->cols != n)
+      return fail(ctx, MI_E_ARG, "linear: residual is %s [%lld, %lld], want F32 [%lld, %lld]", elem_name(R->elem),
+                  (long long)R->rows, (long long)R->cols, (long long)m, (long long)n);
+    lin->resid = static_cast<const float *>(R->ptr);
+    lin->ldr = n;
+  }
+  return MI_OK;
+}
+
 extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias, mi_id residual, int out_elem,
                          mi_id *out) {
   MI_ENTER(ctx);
@@ -1819,22 +1839,76 @@ extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id 
   MI_BUF(ctx, W, w);
   const int64_t m = X->rows, n = w_transposed ? W->rows : W->cols;
   LinearTerms lin;
-  if (bias) {
-    MI_BUF(ctx, Bb, bias);
-    if (Bb->elem != MI_F32 || Bb->numel() != n)
-      return fail(ctx, MI_E_ARG, "linear: bias is %s [%lld, %lld], want F32 with %lld elements", elem_name(Bb->elem),
-                  (long long)Bb->rows, (long long)Bb->cols, (long long)n);
-    lin.bias = static_cast<const float *>(Bb->ptr);
-  }
-  if (residual) {
-    MI_BUF(ctx, R, residual);
-    if (R->elem != MI_F32 || R->rows != m || R->cols != n)
-      return fail(ctx, MI_E_ARG, "linear: residual is %s [%lld, %lld], want F32 [%lld, %lld]", elem_name(R->elem),
-                  (long long)R->rows, (long long)R->cols, (long long)m, (long long)n);
-    lin.resid = static_cast<const float *>(R->ptr);
-    lin.ldr = n;
-  }
+  int s = linear_terms(ctx, bias, residual, m, n, &lin);
+  if (s) return s;
   return matmul_common(ctx, x, 0, w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
+}
+
+extern "C" int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed, mi_id bias, mi_id residual,
+                               int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, X, x_parts);
+  MI_BUF(ctx, W, w);
+  if (X->elem != MI_BF16 || X->cols % 2)
+    return fail(ctx, MI_E_ARG, "linear_parts: parts are %s [%lld, %lld], want BF16 [m, 2 k]", elem_name(X->elem),
+                (long long)X->rows, (long long)X->cols);
+  if (W->elem != MI_BF16) return fail(ctx, MI_E_ARG, "linear_parts: weight is %s, want BF16", elem_name(W->elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16)
+    return fail(ctx, MI_E_ARG, "linear_parts result kind %s", elem_name(out_elem));
+  const int64_t m = X->rows, k = X->cols / 2, wk = w_transposed ? W->cols : W->rows, n = w_transposed ? W->rows : W->cols;
+  if (wk != k)
+    return fail(ctx, MI_E_ARG, "linear_parts: x is [%lld, %lld] (parts [%lld, %lld]), op(w) is [%lld, %lld]",
+                (long long)m, (long long)k, (long long)m, (long long)(2 * k), (long long)wk, (long long)n);
+  LinearTerms lin;
+  int s = linear_terms(ctx, bias, residual, m, n, &lin);
+  if (s) return s;
+  Plan p;
+  p.ta = false; p.tb = w_transposed != 0;
+  p.fast = true;
+  p.ea = MI_F32; p.eb = MI_BF16; p.eo = out_elem;
+  p.a = nullptr; p.b = W->ptr;
+  p.M = m; p.K = k; p.N = n;
+  p.batch = 1; p.sa = p.sb = p.sc = 0;
+  p.lda = k; p.ldb = W->cols;
+  p.bias = lin.bias; p.resid = lin.resid; p.ldr = lin.ldr;
+  if (k == 0 || !parts_direct_fits(p)) {
+    // Any other shape: the weight repeated along k ([w | w] rows, or w over
+    // w), then the plain BF16 product over 2 k -- the same sums.
+    mi_id did; Buffer *db;
+    s = new_buffer(ctx, p.tb ? n : 2 * k, p.tb ? 2 * k : n, MI_BF16, &did, &db);
+    if (s) return s;
+    hipError_t e = hipSuccess;
+    for (int h = 0; h < 2 && e == hipSuccess && n > 0 && k > 0; ++h) {
+      if (p.tb)
+        e = hipMemcpy2DAsync(static_cast<uint16_t *>(db->ptr) + h * k, 2 * k * sizeof(uint16_t), W->ptr,
+                             k * sizeof(uint16_t), k * sizeof(uint16_t), n, hipMemcpyDeviceToDevice, ctx->stream);
+      else
+        e = hipMemcpyAsync(static_cast<uint16_t *>(db->ptr) + h * k * n, W->ptr, k * n * sizeof(uint16_t),
+                           hipMemcpyDeviceToDevice, ctx->stream);
+    }
+    if (e != hipSuccess) {
+      mi_free(ctx, did);
+      return fail(ctx, MI_E_HIP, "linear_parts copy: %s", hipGetErrorString(e));
+    }
+    s = matmul_common(ctx, x_parts, 0, did, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
+    mi_free(ctx, did);  // stream-ordered
+    return s;
+  }
+  mi_id id; Buffer *cb;
+  s = new_buffer(ctx, m, n, out_elem, &id, &cb);
+  if (s) return s;
+  p.c = cb->ptr;
+  hipError_t e = hipSuccess;
+  if (m > 0 && n > 0) e = launch_parts(p, X->ptr, ctx->stream);
+  if (e != hipSuccess) {
+    mi_free(ctx, id);
+    return fail(ctx, MI_E_HIP, "linear_parts launch: %s", hipGetErrorString(e));
+  }
+  s = check_launch(ctx, "linear_parts");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
 }
 
 extern "C" int mi_matmul_items(mi_ctx *ctx, mi_id a, int a_transposed, const int64_t *a_at, mi_id b,

@@ -144,6 +144,20 @@ Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, in
 
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
+// Whether the fast matmul mode runs a prefill product of `rows` F32
+// activation rows against a BF16 weight [n, k] from the activations' BF16
+// parts on the direct kernel (rows in 256-row tiles, at least 128 tiles of
+// 256 x 256 and 2^32 multiply-adds, as the library plans it): then the
+// producer (RMSNorm, the SiLU-mul) writes the parts itself (MI_BF16_PARTS)
+// and mi_linear_parts takes them -- the same result with no split pass over
+// the activations in between.
+static bool parts_pay(mi_ctx *ctx, int64_t rows, int64_t k, int64_t n) {
+  int mode = MI_MATMUL_ACCURATE;
+  if (mi_get_matmul_mode(ctx, &mode) != MI_OK || mode != MI_MATMUL_FAST) return false;
+  if (rows % 256 || k % 32 || n % 16) return false;
+  return (rows / 256) * ((n + 255) / 256) >= 128 && rows * n * k >= (int64_t(1) << 32);
+}
+
 // The forward of `t` positions per sequence at cache length m->len; returns
 // the hidden states [batch * t, hidden] before the final norm.
 // The hidden rows of token ids already on the device ([batch * t] I32, rows
@@ -184,14 +198,21 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
     m->len = ctxlen;
     return x;
   }
+  // Under the reference contract, the products the fast mode would split
+  // take their activations' parts from the producers.
+  const int64_t nqkv = (H + 2 * KVH) * D;
+  const bool parts_qkv = act == MI_F32 && parts_pay(ctx, rows, c.hidden, nqkv);
+  const bool parts_gu = act == MI_F32 && parts_pay(ctx, rows, c.hidden, 2 * c.intermediate);
+  const bool parts_down = act == MI_F32 && parts_pay(ctx, rows, c.intermediate, c.hidden);
   for (Layer &L : m->layers) {
-    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps, act);
+    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps, parts_qkv ? MI_BF16_PARTS : act);
     // One product against the fused q|k|v weight, then RoPE on q and k, k and
     // v appended to the caches at positions pos0.. of each (sequence, kv head)
     // item, and q laid out for the attention, in one launch: rows (sequence,
     // position, head) for the fused kernel, else regrouped per kv head, rows
     // (sequence, kv head, position, g).
-    Tensor qkv = burn::float_matmul(xn, false, L.wqkv, true);
+    Tensor qkv = parts_qkv ? burn::linear_parts(xn, L.wqkv, true, nullptr, nullptr)
+                           : burn::float_matmul(xn, false, L.wqkv, true);
     Tensor q = burn::qkv_rope_cache(qkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k, L.cache_v, !fused);
     Tensor oh;
     if (fused) {
@@ -212,10 +233,12 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
     }
     if (act != MI_F32) oh = burn::float_cast(oh, act);
     x = burn::linear(oh, L.wo, true, nullptr, &x);  // x + oh wo^T, the add in the product's epilogue
-    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps, act);
+    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps, parts_gu ? MI_BF16_PARTS : act);
     // One product against the fused gate|up weight, silu(gate) * up of its halves.
-    Tensor h = burn::silu_mul_halves(burn::float_matmul(hn, false, L.wgu, true), act);
-    x = burn::linear(h, L.wdown, true, nullptr, &x);
+    Tensor gu = parts_gu ? burn::linear_parts(hn, L.wgu, true, nullptr, nullptr)
+                         : burn::float_matmul(hn, false, L.wgu, true);
+    Tensor h = burn::silu_mul_halves(gu, parts_down ? MI_BF16_PARTS : act);
+    x = parts_down ? burn::linear_parts(h, L.wdown, true, nullptr, &x) : burn::linear(h, L.wdown, true, nullptr, &x);
   }
   m->len = ctxlen;
   return x;

@@ -755,7 +755,15 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, 
     if (j < cols) {
       float y = v[t] / rms;
       if (gamma) y = y * ld(gamma, gelem, j);
-      st(out, out_elem, base + j, y);
+      if (out_elem == MI_BF16_PARTS) {
+        uint16_t h, l;
+        split_bf16(y, h, l);
+        uint16_t *o = static_cast<uint16_t *>(out) + 2 * base;
+        o[j] = h;
+        o[cols + j] = l;
+      } else {
+        st(out, out_elem, base + j, y);
+      }
     }
   }
 }
@@ -982,7 +990,8 @@ extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, xb, a);
   if (!elem_float(xb->elem)) return fail(ctx, MI_E_ARG, "rms_norm of a %s buffer", elem_name(xb->elem));
-  if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "rms_norm result kind %s", elem_name(out_elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16 && out_elem != MI_BF16_PARTS)
+    return fail(ctx, MI_E_ARG, "rms_norm result kind %d", out_elem);
   const void *gp = nullptr;
   int ge = MI_F32;
   if (gamma) {
@@ -996,7 +1005,8 @@ extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out
   const void *xp = xb->ptr;
   const int xe = xb->elem;
   mi_id id; Buffer *ob;
-  int s = new_buffer(ctx, R, C, out_elem, &id, &ob);
+  const bool parts = out_elem == MI_BF16_PARTS;
+  int s = new_buffer(ctx, R, parts ? 2 * C : C, parts ? MI_BF16 : out_elem, &id, &ob);
   if (s) return s;
   if (R > 0 && C > 0) {
     unsigned g = grid_for(R, 4, INT32_MAX);

@@ -26,6 +26,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmiburn.so")
 
 F32, I32, BOOL, BF16 = 0, 1, 2, 3
+# A result form of mi_rms_norm / mi_silu_mul_halves: the F32 result as its
+# BF16 parts, [rows, 2 cols] (heads, then remainders), read by linear_parts.
+BF16_PARTS = 4
 _NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}
 
 AXIS_ROWS, AXIS_COLS = 0, 1
@@ -99,6 +102,7 @@ def _load() -> ctypes.CDLL:
         "mi_matmul": [P, U64, c_int, U64, c_int, c_int, Ip],
         "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
         "mi_linear": [P, U64, U64, c_int, U64, U64, c_int, Ip],
+        "mi_linear_parts": [P, U64, U64, c_int, U64, U64, c_int, Ip],
         "mi_matmul_slices": [P, U64, c_int, U64, c_int, Ip, ctypes.POINTER(I64)],
         "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
                             I64, U64, ctypes.POINTER(I64)],
@@ -288,6 +292,11 @@ class Engine:
     def linear(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, out_elem: int = F32) -> int:
         """residual + (x @ op(w) + bias) in one product; 0 omits a term."""
         return self._out(self._lib.mi_linear, x, w, int(w_t), bias, residual, out_elem)
+
+    def linear_parts(self, x_parts: int, w: int, w_t: bool, bias: int = 0, residual: int = 0,
+                     out_elem: int = F32) -> int:
+        """linear() of an F32 operand given as its BF16 parts [m, 2k] (BF16_PARTS)."""
+        return self._out(self._lib.mi_linear_parts, x_parts, w, int(w_t), bias, residual, out_elem)
 
     def log_softmax_ce(self, logits: int, targets: int, grad_scale: float):
         """(picked, dlogits): logp at each row's target and the cross-entropy

@@ -7,6 +7,13 @@ kernel a shape selects -- the GEMV, split-K, the 64x64 tiles guarded and
 exact, the fast mode's split kernel, both direct-to-LDS BF16 kernels -- and
 within the matmul bound of the oracle.
 
+mi_linear_parts (an F32 operand given as its BF16 parts, MI_BF16_PARTS): bit
+for bit the fast mode's own linear where that splits the operand itself,
+and within the F32 bound of float64 on the other shapes; the parts that
+mi_rms_norm and mi_silu_mul_halves produce are bit for bit the split of
+their F32 results (the split restated here in numpy and checked on
+hand-worked values).
+
 mi_matmul_items (grouped strided items written in place): each item within
 the F32 accumulation bound of the oracle's product of the same blocks, the
 rest of the result buffer untouched, on the transformer's head layout and on
@@ -126,6 +133,113 @@ def test_linear_argument_errors(engine):
         assert e.value.kind == "ARG"
     with pytest.raises(miburn.MiError) as e:
         engine.linear(ix, iw, False, 0, engine.upload(rnd(8, 31)))
+    assert e.value.kind == "ARG"
+
+
+# ------------------------------------------------ F32 operands as BF16 parts
+def split_parts(y):
+    """[rows, cols] F32 -> [rows, 2 cols] BF16 bits: each row's heads (round to
+    nearest even through the oracle's cast; a finite value that would round to
+    infinity keeps its truncated head), then the BF16 of the exact remainders
+    (0 where the remainder is NaN: an infinite value)."""
+    y = np.ascontiguousarray(y, np.float32)
+    u = y.view(np.uint32)
+    hi = orc.to_bf16(y)
+    ovf = ((hi & 0x7FFF) == 0x7F80) & ((u & 0x7F800000) != 0x7F800000)
+    hi = np.where(ovf, (u >> 16).astype(np.uint16), hi)
+    with np.errstate(invalid="ignore"):
+        r = (y.astype(np.float64) - orc.from_bf16(hi).astype(np.float64)).astype(np.float32)
+    lo = np.where(np.isnan(r), np.uint16(0), orc.to_bf16(np.nan_to_num(r)))
+    return np.concatenate([hi, lo], axis=1)
+
+
+def test_split_parts_reference_cases():
+    """The test's own split against hand-worked values: an exact BF16 value
+    has no remainder; 1 + 2^-9 rounds its head to 1 (ties to even) and keeps
+    2^-9; the largest F32 keeps its truncated head 0x7f7f, its remainder
+    (2^16 - 1) 2^104 rounding up to 2^120; infinity is its head alone."""
+    y = np.array([[1.5, 1 + 2.0 ** -9, np.finfo(np.float32).max, np.inf]], np.float32)
+    p = split_parts(y)
+    assert list(p[0, :4]) == [0x3FC0, 0x3F80, 0x7F7F, 0x7F80]
+    lo = orc.from_bf16(p[:, 4:])[0]
+    assert lo[0] == 0 and lo[1] == 2.0 ** -9 and lo[3] == 0
+    assert lo[2] == 2.0 ** 120
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 576), (300, 1000), (5, 8192)])
+def test_rms_norm_parts_split_its_f32_result(engine, rows, cols):
+    x = rnd(rows, cols)
+    gamma = rnd(1, cols)
+    gamma[0, :3] = [3.4e38, -3.39e38, 1e38]  # heads past the largest BF16, infinities
+    ix, ig = engine.upload(x), engine.upload(gamma)
+    f32 = engine.download(engine.rms_norm(ix, ig, 1e-5))
+    parts = engine.download(engine.rms_norm(ix, ig, 1e-5, miburn.BF16_PARTS))
+    same_bits(parts, split_parts(f32), np.uint16)
+
+
+@pytest.mark.parametrize("rows,inner", [(64, 1536), (33, 7), (4, 4)])
+def test_silu_mul_halves_parts_split_its_f32_result(engine, rows, inner):
+    gu = rnd(rows, 2 * inner, scale=4.0)
+    ig = engine.upload(gu)
+    f32 = engine.download(engine.silu_mul_halves(ig))
+    parts = engine.download(engine.silu_mul_halves(ig, miburn.BF16_PARTS))
+    same_bits(parts, split_parts(f32), np.uint16)
+
+
+# (m, n, k): shapes the fast mode splits into stacked parts for F32 x.
+@pytest.mark.parametrize("m,n,k,terms", [(16384, 960, 576, "none"), (16384, 576, 1536, "residual"),
+                                         (16384, 3072, 576, "both")])
+def test_linear_parts_equals_the_fast_linear(engine, m, n, k, terms):
+    """Where the fast mode's mi_linear splits F32 activations itself, the
+    product from parts made elsewhere is the same, bit for bit."""
+    x = rnd(m, k)
+    w = orc.to_bf16(rnd(n, k))
+    ix, iw = engine.upload(x), engine.upload_bf16(w)
+    ip = engine.upload_bf16(split_parts(x))
+    ib = engine.upload(rnd(1, n)) if terms == "both" else 0
+    ir = engine.upload(rnd(m, n)) if terms != "none" else 0
+    want = engine.download(engine.linear(ix, iw, True, ib, ir))
+    got = engine.download(engine.linear_parts(ip, iw, True, ib, ir))
+    same_bits(got, want)
+    engine.set_matmul_mode(miburn.MATMUL_ACCURATE)
+    try:
+        again = engine.download(engine.linear_parts(ip, iw, True, ib, ir))
+    finally:
+        engine.set_matmul_mode(miburn.MATMUL_FAST)
+    same_bits(again, want)
+
+
+@pytest.mark.parametrize("m,n,k,tw", [(100, 70, 48, True), (512, 256, 64, False), (256, 300, 32, False),
+                                      (512, 512, 40, True), (3, 576, 1536, True), (7, 5, 0, True)])
+def test_linear_parts_other_shapes(engine, m, n, k, tw):
+    """Shapes outside the direct kernel's tiling: the sums head . w +
+    remainder . w within the F32 accumulation bound of float64."""
+    x = rnd(m, k)
+    wb = orc.to_bf16(rnd(n, k) if tw else rnd(k, n))
+    p = split_parts(x)
+    bias, resid = rnd(1, n), rnd(m, n)
+    got = engine.download(engine.linear_parts(engine.upload_bf16(p), engine.upload_bf16(wb), tw,
+                                              engine.upload(bias), engine.upload(resid)))
+    w = orc.from_bf16(wb).astype(np.float64)
+    w = w.T if tw else w
+    a = orc.from_bf16(p).astype(np.float64)
+    xs = a[:, :k] + a[:, k:]
+    ref = resid + (xs @ w + bias)
+    tol = 1e-5 * (np.abs(xs) @ np.abs(w)) + 1e-6 * (np.abs(ref) + np.abs(bias) + np.abs(resid)) + 1e-30
+    assert got.shape == (m, n)
+    assert np.all(np.abs(got - ref) <= tol)
+
+
+def test_linear_parts_argument_errors(engine):
+    iw = engine.upload_bf16(orc.to_bf16(rnd(32, 16)))
+    for bad in (engine.upload_bf16(orc.to_bf16(rnd(8, 31))),   # odd width
+                engine.upload(rnd(8, 32)),                      # F32, not parts
+                engine.upload_bf16(orc.to_bf16(rnd(8, 48)))):   # k 24 against the weight's 16
+        with pytest.raises(miburn.MiError) as e:
+            engine.linear_parts(bad, iw, True)
+        assert e.value.kind == "ARG"
+    with pytest.raises(miburn.MiError) as e:  # an F32 weight
+        engine.linear_parts(engine.upload_bf16(orc.to_bf16(rnd(8, 32))), engine.upload(rnd(32, 16)), True)
     assert e.value.kind == "ARG"
 
 
