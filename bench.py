@@ -46,9 +46,9 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the bf16 4096^3 NN product, from two rocprofv3 --pmc
 # passes over `bench.py --no-cpu --no-models --steps 5 --warmup 1` (FETCH_SIZE,
 # then WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for
-# a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,922 KiB
+# a plain copy of 256 MiB (FETCH_SIZE x 1.9998, WRITE_SIZE x 1.0): 196,904 KiB
 # read + 65,536 KiB written.  Only that configuration was measured.
-GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268756687}
+GEMM_TRAFFIC_BYTES = {("bf16", 4096): 268738874}
 WARM_S = 2.0  # seconds of untimed product before the timed steps (clock ramp-up)
 
 
@@ -332,6 +332,53 @@ def traced_steps(eng, step_ids, inputs, batches):
     return (t1 - t0) * 1e3 / len(batches), (t2 - t1) * 1e3 / len(batches)
 
 
+def decode_layer_bench(eng, batch: int = 1, ctx: int = 576, steps: int = 200) -> dict:
+    """One SmolLM2-135M layer's decode launches alone, for counter profiles
+    (rocprofv3 --pmc of the whole decoder harness has ended in host
+    segmentation faults inside the profiler): the fused norm + q|k|v +
+    attention step at a `ctx`-position context (mi_norm_qkv_attention: its
+    chunk kernel and its combine), then the o, gate|up and down GEMVs
+    (mi_norm_matvec) -- the five launches of a decode layer
+    (crates/tt-models/src/llama.rs:380-520) -- `steps` times over one layer's
+    random BF16 weights and a random F32 cache."""
+    import miburn
+    H, KVH, D, hid, inter, maxc = 9, 3, 64, 576, 1536, 1024
+
+    def bf(r, c, base):
+        t = eng.random_dram(r, c, miburn.DRAW_NORMAL, 0.0, 0.02, base=base)
+        y = eng.cast_float(t, miburn.BF16)
+        eng.free(t)
+        return y
+    x = eng.random_dram(batch, hid, miburn.DRAW_NORMAL, 0.0, 1.0, base=1)
+    gamma = eng.fill(1, hid, miburn.F32, 0x3F800000)
+    wqkv, wo, wgu, wdn = bf((H + 2 * KVH) * D, hid, 2), bf(hid, H * D, 3), bf(2 * inter, hid, 4), bf(hid, inter, 5)
+    cos = eng.random_dram(maxc, D, miburn.DRAW_UNIFORM, -1.0, 1.0, base=6)
+    sin = eng.random_dram(maxc, D, miburn.DRAW_UNIFORM, -1.0, 1.0, base=7)
+    kc = eng.random_dram(batch * KVH * maxc, D, miburn.DRAW_NORMAL, 0.0, 1.0, base=8)
+    vc = eng.random_dram(batch * KVH * maxc, D, miburn.DRAW_NORMAL, 0.0, 1.0, base=9)
+    span = (ctx + 1 + 63) // 64 * 64
+
+    def layer():
+        o = eng.norm_qkv_attention(x, gamma, 1e-5, wqkv, cos, sin, H, KVH, 0, ctx, span, kc, vc, D ** -0.5)
+        x1 = eng.norm_matvec(o, 0, 0.0, wo, x, False)
+        h = eng.norm_matvec(x1, gamma, 1e-5, wgu, 0, True)
+        x2 = eng.norm_matvec(h, 0, 0.0, wdn, x1, False)
+        for t in (o, x1, h, x2):
+            eng.free(t)
+    for _ in range(20):
+        layer()
+    eng.sync()
+    eng.event_record(0)
+    for _ in range(steps):
+        layer()
+    eng.event_record(1)
+    eng.sync()
+    us = eng.event_elapsed_ms(0, 1) * 1e3 / steps
+    for t in (x, gamma, wqkv, wo, wgu, wdn, cos, sin, kc, vc):
+        eng.free(t)
+    return dict(batch=batch, ctx=ctx, steps=steps, us_per_layer=round(us, 2))
+
+
 def mlp_bench(eng, steps: int = 100, traces: bool = True) -> dict:
     """MLP 784->128->10 training, batch 64, SGD lr 0.01:
     eager steps on device-drawn batches, and the step captured as a trace
@@ -399,9 +446,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true")
     ap.add_argument("--no-models", action="store_true")
-    ap.add_argument("--only", choices=["decoder", "mlp", "transformer"],
-                    help="run one model harness alone (for profiling) and print its JSON")
-    ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder")
+    ap.add_argument("--only", choices=["decoder", "decode_layer", "mlp", "transformer"],
+                    help="run one model harness (or one decoder layer's decode launches) alone, for profiling, "
+                         "and print its JSON")
+    ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder / decode_layer")
     ap.add_argument("--numerics", choices=["reference", "performance"], default="reference",
                     help="decoder numeric contract for --only decoder")
     ap.add_argument("--no-traces", action="store_true",
@@ -424,6 +472,7 @@ def main() -> int:
         eng.set_matmul_mode(miburn.MATMUL_FAST if args.matmul_mode == "fast" else miburn.MATMUL_ACCURATE)
     if args.only:
         out = {"decoder": lambda: decoder_bench(eng, args.batch, numerics=args.numerics, traced=not args.no_traces),
+               "decode_layer": lambda: decode_layer_bench(eng, args.batch),
                "mlp": lambda: mlp_bench(eng, traces=not args.no_traces),
                "transformer": lambda: transformer_bench(eng, traces=not args.no_traces)}[args.only]()
         print(json.dumps({"harness": args.only, **out}), flush=True)
