@@ -303,8 +303,12 @@ typedef float flash_f32x16 __attribute__((ext_vector_type(16)));
 // D = 64.
 typedef __bf16 fl_bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 fl_bf16x4 __attribute__((ext_vector_type(4)));
-constexpr int FL3_KS = 72;  // LDS row pitch (bf16) of a key part [32][64]
-constexpr int FL3_VS = 40;  // ... of a value part, transposed [64][32]
+// LDS row pitches (bf16): a key part [32 keys][64 d] at 72 (a lane's 16-byte
+// fragment reads of one 16-lane group start 36 dwords apart: no two share a
+// bank), a value part transposed [64 d][32 keys] at 36 (a half-wave's 8-byte
+// reads start 18 dwords apart: none shared).
+constexpr int FL3_KS = 72;
+constexpr int FL3_VS = 36;
 
 __device__ __forceinline__ void fl_split(float v, __bf16 &hi, __bf16 &mid, __bf16 &lo) {
   const uint32_t hb = __float_as_uint(v) & 0xffff0000u;
@@ -386,19 +390,24 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
     const int64_t kend_run = pos0 + (p0 + 32 < T ? p0 + 32 : T);
     const int64_t kbeg = split ? static_cast<int64_t>(blockIdx.z) * kchunk : 0;
     const int64_t kend = split ? (kbeg + kchunk < kend_run ? kbeg + kchunk : kend_run) : kend_run;
-    // Key and value blocks: 512 groups of 4 values each (key e / 16, d 4 (e % 16)),
-    // loaded into registers for the next block while the current one is used.
+    // Key and value blocks as 512 groups of 4 values, loaded into registers
+    // for the next block while the current one is used: key group e is key
+    // e / 16, d 4 (e % 16) .. + 3 (a 16-byte load); value group e is d e % 64
+    // of keys 4 (e / 64) .. + 3 (four loads, each a half-wave's row segment),
+    // so that it is stored transposed as one 8-byte run a part.
     constexpr int PER = (32 * 16 + NT - 1) / NT;
     using Raw = typename std::conditional<EXACT, uint2, float4>::type;
-    Raw kr[PER], vr[PER];
+    Raw kr[PER];
+    KV vr[PER][4];
     auto fetch = [&](int64_t j0) {
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int e0 = tid + u * NT, e = e0 < 32 * 16 ? e0 : tid;
         const int r = static_cast<int>(j0) + (e >> 4) < ctx32 ? static_cast<int>(j0) + (e >> 4) : ctx32 - 1;
-        const int off = r * D + (e & 15) * 4;
-        kr[u] = *reinterpret_cast<const Raw *>(K + off);
-        vr[u] = *reinterpret_cast<const Raw *>(V + off);
+        kr[u] = *reinterpret_cast<const Raw *>(K + r * D + (e & 15) * 4);
+        const int d = e & 63, k4 = static_cast<int>(j0) + 4 * (e >> 6);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[u][i] = V[(k4 + i < ctx32 ? k4 + i : ctx32 - 1) * D + d];
       }
     };
     auto stage = [&](int buf) {
@@ -407,29 +416,29 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
         const int e = tid + u * NT;
         if (e < 32 * 16) {
           const int r = e >> 4, c4 = (e & 15) * 4;
+          const int vofs = (e & 63) * FL3_VS + 4 * (e >> 6);
           if constexpr (EXACT) {
             *reinterpret_cast<uint2 *>(&ks[buf][0][r * FL3_KS + c4]) = kr[u];
-            const uint16_t v4[4] = {static_cast<uint16_t>(vr[u].x & 0xffffu), static_cast<uint16_t>(vr[u].x >> 16),
-                                    static_cast<uint16_t>(vr[u].y & 0xffffu), static_cast<uint16_t>(vr[u].y >> 16)};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vs[buf][0][(c4 + i) * FL3_VS + r] = __builtin_bit_cast(__bf16, v4[i]);
+            const fl_bf16x4 v4 = {__builtin_bit_cast(__bf16, vr[u][0]), __builtin_bit_cast(__bf16, vr[u][1]),
+                                  __builtin_bit_cast(__bf16, vr[u][2]), __builtin_bit_cast(__bf16, vr[u][3])};
+            *reinterpret_cast<fl_bf16x4 *>(&vs[buf][0][vofs]) = v4;
           } else {
             const float k4[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-            const float v4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-            fl_bf16x4 kp0, kp1, kp2;
+            fl_bf16x4 kp0, kp1, kp2, vp0, vp1, vp2;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               __bf16 a0, a1, a2;
               fl_split(k4[i], a0, a1, a2);
               kp0[i] = a0; kp1[i] = a1; kp2[i] = a2;
-              fl_split(v4[i], a0, a1, a2);
-              vs[buf][0][(c4 + i) * FL3_VS + r] = a0;
-              vs[buf][1 % KP][(c4 + i) * FL3_VS + r] = a1;
-              vs[buf][2 % KP][(c4 + i) * FL3_VS + r] = a2;
+              fl_split(vr[u][i], a0, a1, a2);
+              vp0[i] = a0; vp1[i] = a1; vp2[i] = a2;
             }
             *reinterpret_cast<fl_bf16x4 *>(&ks[buf][0][r * FL3_KS + c4]) = kp0;
             *reinterpret_cast<fl_bf16x4 *>(&ks[buf][1 % KP][r * FL3_KS + c4]) = kp1;
             *reinterpret_cast<fl_bf16x4 *>(&ks[buf][2 % KP][r * FL3_KS + c4]) = kp2;
+            *reinterpret_cast<fl_bf16x4 *>(&vs[buf][0][vofs]) = vp0;
+            *reinterpret_cast<fl_bf16x4 *>(&vs[buf][1 % KP][vofs]) = vp1;
+            *reinterpret_cast<fl_bf16x4 *>(&vs[buf][2 % KP][vofs]) = vp2;
           }
         }
       }
