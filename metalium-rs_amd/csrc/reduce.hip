@@ -739,22 +739,32 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, 
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
-  float v[T];
+  // Rows of up to 2048 columns request the gain with the row, so the scaling
+  // does not wait for a second memory round trip after the fold; the fold
+  // runs on the DPP lane paths.
+  constexpr bool GPRE = T <= 32;
+  float v[T], gm[GPRE ? T : 1];
   float ss = 0.0f;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
     v[t] = j < cols ? ld(x, elem, base + j) : 0.0f;
-    ss += v[t] * v[t];
+    if constexpr (GPRE) gm[t] = (gamma && j < cols) ? ld(gamma, gelem, j) : 1.0f;
   }
-  ss = wave_sum(ss);
+#pragma unroll
+  for (int t = 0; t < T; ++t) ss += v[t] * v[t];
+  ss = fold_sum<64>(ss);
   const float rms = __fsqrt_rn(ss / static_cast<float>(cols) + eps);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
     if (j < cols) {
       float y = v[t] / rms;
-      if (gamma) y = y * ld(gamma, gelem, j);
+      if constexpr (GPRE) {
+        if (gamma) y = y * gm[t];
+      } else {
+        if (gamma) y = y * ld(gamma, gelem, j);
+      }
       if (out_elem == MI_BF16_PARTS) {
         uint16_t h, l;
         split_bf16(y, h, l);
@@ -775,15 +785,23 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const float *x, const f
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
-  float v[T];
+  // As rms_norm_kernel: the gain and bias requested with the row (up to
+  // 1024 columns), the folds on the DPP lane paths.
+  constexpr bool GPRE = T <= 16;
+  float v[T], gm[GPRE ? T : 1], bt[GPRE ? T : 1];
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
     v[t] = j < cols ? x[base + j] : 0.0f;
-    s += v[t];
+    if constexpr (GPRE) {
+      gm[t] = (gamma && j < cols) ? gamma[j] : 1.0f;
+      bt[t] = (beta && j < cols) ? beta[j] : 0.0f;
+    }
   }
-  const float mean = wave_sum(s) / static_cast<float>(cols);
+#pragma unroll
+  for (int t = 0; t < T; ++t) s += v[t];
+  const float mean = fold_sum<64>(s) / static_cast<float>(cols);
   float q = 0.0f;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -791,15 +809,20 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const float *x, const f
     float d = j < cols ? v[t] - mean : 0.0f;
     q += d * d;
   }
-  const float var = wave_sum(q) / static_cast<float>(cols);
+  const float var = fold_sum<64>(q) / static_cast<float>(cols);
   const float den = __fsqrt_rn(var + eps);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int64_t j = lane + 64 * t;
     if (j < cols) {
       float y = (v[t] - mean) / den;
-      if (gamma) y = y * gamma[j];
-      if (beta) y = y + beta[j];
+      if constexpr (GPRE) {
+        if (gamma) y = y * gm[t];
+        if (beta) y = y + bt[t];
+      } else {
+        if (gamma) y = y * gamma[j];
+        if (beta) y = y + beta[j];
+      }
       out[base + j] = y;
     }
   }
