@@ -1374,15 +1374,15 @@ static hipError_t run_plan(const Plan &p, hipStream_t st) {
   // the split's conversions only add work, so the F32 kernel runs (more
   // accurate, and faster there).
   // F32 activations against BF16 weights over at least 256 rows are the
-  // exception below 2^31 multiply-adds: split, only the activations take two
-  // BF16 parts, and a 64 x 64 tile's k loop runs on the BF16 matrix cores
-  // instead of the F32 ones (a 512-token prefill of the SmolLM2-shaped decoder
-  // 8.7 -> 7.5 ms); between 2^31 and 2^33 (a batch-32 prefill's products) the
-  // F32 kernel's 128 x 128 tiles stay ahead.
+  // exception at any size: split, only the activations take two BF16 parts,
+  // and the k loop runs on the BF16 matrix cores instead of the F32 ones (a
+  // 512-token prefill of the SmolLM2-shaped decoder 8.7 -> 7.5 ms; its
+  // products at 2048 - 8192 rows, us: gate|up at 2048 rows 86.6 -> 42.0, down
+  // at 4096 98.7 -> 39.8, down at 8192 167.7 -> 81.7, o at 8192 66.9 -> 38.0).
   const int64_t macs = p.M * p.N * p.K * p.batch;
   const bool split_pays =
       (macs >= (int64_t(1) << 33) && ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch >= 128) ||
-      (p.ea == MI_F32 && p.eb == MI_BF16 && p.M >= 256 && macs < (int64_t(1) << 31));
+      (p.ea == MI_F32 && p.eb == MI_BF16 && p.M >= 256);
   if (p.fast && split_pays) {
     if (p.ea == MI_F32 && p.eb == MI_F32)
       return bf ? run_split<float, float, uint16_t>(p, st) : run_split<float, float, float>(p, st);
@@ -1592,18 +1592,26 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const float *a, int64_t
 static bool parts_direct_fits(const Plan &p);
 static bool stacked_split_pays(const Plan &p) {
   if (!p.fast || p.ea != MI_F32 || p.kc != 0 || p.lda % 4 || (reinterpret_cast<uintptr_t>(p.a) & 15)) return false;
-  if (!parts_direct_fits(p)) return false;
+  if (p.M % 256 || !parts_direct_fits(p)) return false;
   const int64_t tiles = (p.M / 256) * ((p.N + 255) / 256);
   return tiles >= 128 && p.M * p.N * p.K >= (int64_t(1) << 32);
 }
 
 // Whether the direct kernel takes an F32 x BF16 product of plan p from A's
-// parts: 256-row tiles, whole k-tiles on each side of the wrap, B's width
-// tiled by 256 or (k-contiguous B) a multiple of 16 for the edge tiles.
+// parts: rows in 128-row tiles (256-row tiles where they fill the chip),
+// whole k-tiles on each side of the wrap, B's width a multiple of the tile or
+// (k-contiguous B) of 16 for the edge tiles.
 static bool parts_direct_fits(const Plan &p) {
-  if (p.eb != MI_BF16 || p.ta || p.batch != 1 || p.K % 32 || p.M % 256) return false;
+  if (p.eb != MI_BF16 || p.ta || p.batch != 1 || p.K % 32 || p.M % 128) return false;
   if ((reinterpret_cast<uintptr_t>(p.b) & 15) || p.ldb % 8) return false;
-  return p.N % 256 == 0 || (p.tb && p.N % 16 == 0);
+  if (p.M % 256 && p.N % 128 && !p.tb) return false;
+  return p.N % 256 == 0 || (p.tb && p.N % 16 == 0) || (p.M % 256 && p.N % 128 == 0);
+}
+
+// Products of fewer than 192 tiles of 256 x 256 (or 128-row multiples) take
+// the 128 x 128 tiles.
+static bool parts_small_tiles(const Plan &p) {
+  return p.M % 256 || (p.M / 256) * ((p.N + 255) / 256) < 192;
 }
 
 // The product of plan p (A F32 [M, K]) from A's parts at `parts` ([M, 2 K]
@@ -1617,6 +1625,11 @@ static hipError_t launch_parts(const Plan &p, const void *parts, hipStream_t st)
   q.K = 2 * p.K;
   q.kb = p.K;
   const bool bf = p.eo == MI_BF16;
+  if (parts_small_tiles(p)) {
+    if (p.N % 128 == 0)
+      return bf ? launch_pipe<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe<float, 128, 128, 5, 2, 2>(q, st);
+    return bf ? launch_pipe_edge<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe_edge<float, 128, 128, 5, 2, 2>(q, st);
+  }
   if (p.N % 256 == 0)
     return bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe<float, 256, 256, 5, 2, 4>(q, st);
   return bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, st);

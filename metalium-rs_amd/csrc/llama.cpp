@@ -144,18 +144,20 @@ Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, in
 
 Tensor ones(mi_ctx *ctx, int64_t n) { return burn::fill(ctx, {1, n}, MI_F32, 0x3f800000u); }
 
-// Whether the fast matmul mode runs a prefill product of `rows` F32
-// activation rows against a BF16 weight [n, k] from the activations' BF16
-// parts on the direct kernel (rows in 256-row tiles, at least 128 tiles of
-// 256 x 256 and 2^32 multiply-adds, as the library plans it): then the
-// producer (RMSNorm, the SiLU-mul) writes the parts itself (MI_BF16_PARTS)
-// and mi_linear_parts takes them -- the same result with no split pass over
-// the activations in between.
+// Whether a prefill product of `rows` F32 activation rows against a BF16
+// weight [n, k] takes the activations' BF16 parts from their producer
+// (RMSNorm, the SiLU-mul write MI_BF16_PARTS) into mi_linear_parts: in the
+// fast matmul mode, from 4096 rows in 128-row tiles.  Where the library
+// would split the activations itself into parts for its direct kernel
+// (rows in 256-row tiles over at least 128 tiles of 256 x 256) the result is
+// the same with no split pass between; from 4096 rows the direct kernel on
+// parts also beats the split kernel (SmolLM2 shapes at 4096 rows, us: q|k|v
+// 33.7 -> 17.8, gate|up 51.2 -> 44.4, down 39.8 -> 38.1; at 2048 rows and
+// below the split kernel stays ahead).
 static bool parts_pay(mi_ctx *ctx, int64_t rows, int64_t k, int64_t n) {
   int mode = MI_MATMUL_ACCURATE;
   if (mi_get_matmul_mode(ctx, &mode) != MI_OK || mode != MI_MATMUL_FAST) return false;
-  if (rows % 256 || k % 32 || n % 16) return false;
-  return (rows / 256) * ((n + 255) / 256) >= 128 && rows * n * k >= (int64_t(1) << 32);
+  return rows >= 4096 && rows % 128 == 0 && k % 32 == 0 && n % 16 == 0;
 }
 
 // The forward of `t` positions per sequence at cache length m->len; returns

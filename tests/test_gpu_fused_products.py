@@ -210,10 +210,12 @@ def test_linear_parts_equals_the_fast_linear(engine, m, n, k, terms):
 
 
 @pytest.mark.parametrize("m,n,k,tw", [(100, 70, 48, True), (512, 256, 64, False), (256, 300, 32, False),
-                                      (512, 512, 40, True), (3, 576, 1536, True), (7, 5, 0, True)])
+                                      (512, 512, 40, True), (3, 576, 1536, True), (7, 5, 0, True),
+                                      (384, 960, 576, True), (4096, 576, 1536, True), (2048, 3072, 576, True)])
 def test_linear_parts_other_shapes(engine, m, n, k, tw):
-    """Shapes outside the direct kernel's tiling: the sums head . w +
-    remainder . w within the F32 accumulation bound of float64."""
+    """The direct kernel's 128 x 128 tiles (edge tiles for widths of 16s) and
+    shapes outside its tiling (the weight repeated along k): the sums head . w
+    + remainder . w within the F32 accumulation bound of float64."""
     x = rnd(m, k)
     wb = orc.to_bf16(rnd(n, k) if tw else rnd(k, n))
     p = split_parts(x)

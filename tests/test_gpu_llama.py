@@ -76,20 +76,21 @@ def test_prefill_logits_all_positions(engine, tiny, batch, t):
     close_logits(got, ref_logits(W, TINY, ids))
 
 
-# 32 prompts of 512 positions at hidden 512: 16384 rows in 256-row tiles that
-# fill the chip, so under the reference contract the q|k|v, gate|up and down
-# products take their F32 operands' BF16 parts straight from the norms and
-# the SiLU-mul (MI_BF16_PARTS into mi_linear_parts).
+# 8 or 32 prompts of 512 positions at hidden 512 (4096 or 16384 rows): under
+# the reference contract the q|k|v, gate|up and down products take their F32
+# operands' BF16 parts straight from the norms and the SiLU-mul
+# (MI_BF16_PARTS into mi_linear_parts).
 WIDE = dict(vocab=512, hidden=512, layers=2, heads=8, kv_heads=4, head_dim=64, intermediate=1024,
             rope_theta=10000.0, eps=1e-5)
 
 
-def test_prefill_logits_with_operand_parts(engine):
-    m = miburn.Llama(engine, WIDE, max_ctx=512, max_batch=32, seed=11, init_std=0.05)
+@pytest.mark.parametrize("batch", [8, 32])  # 4096 rows: 128 x 128 tiles; 16384: 256 x 256
+def test_prefill_logits_with_operand_parts(engine, batch):
+    m = miburn.Llama(engine, WIDE, max_ctx=512, max_batch=batch, seed=11, init_std=0.05)
     W = weights(engine, m, WIDE)
-    ids = np.random.default_rng(8).integers(0, WIDE["vocab"], (32, 512)).astype(np.int32)
+    ids = np.random.default_rng(8).integers(0, WIDE["vocab"], (batch, 512)).astype(np.int32)
     m.reset()
-    got = engine.download(m.forward(ids, all_positions=True)).reshape(32, 512, -1)
+    got = engine.download(m.forward(ids, all_positions=True)).reshape(batch, 512, -1)
     m.close()
     close_logits(got, ref_logits(W, WIDE, ids))
 
