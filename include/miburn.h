@@ -203,12 +203,13 @@ int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed,
  * operand; BF16 x BF16 products are the same in both.
  *  FAST (the default, as the reference's): where a product is large enough to
  *   be bound by the matrix cores (>= 2^33 multiply-adds over >= 128 tiles of
- *   128 x 128), each F32 operand element is split as bf16 hi + bf16 lo and
+ *   128 x 128), and for F32 activations (>= 256 rows) against BF16 weights at
+ *   any size, each F32 operand element is split as bf16 hi + bf16 lo and
  *   a b = hi hi + hi lo + lo hi runs on the BF16 matrix cores with F32
- *   accumulation; error per product <= 3 * 2^-18 |a||b| (the reference's
- *   fast mode rounds operands to TF32, 2^-11).  Smaller products run as in
- *   ACCURATE.  A non-finite operand element gives NaN in its row or column
- *   where F32 arithmetic could give an infinity.
+ *   accumulation (hi b + lo b for a BF16 b); error per product <= 3 * 2^-18
+ *   |a||b| (the reference's fast mode rounds operands to TF32, 2^-11).  Other
+ *   products run as in ACCURATE.  A non-finite operand element gives NaN in
+ *   its row or column where F32 arithmetic could give an infinity.
  *  ACCURATE: F32 products on the F32 matrix cores, F32 accumulation.
  * The reference's EXACT mode (k-ordered sequential F32 sums) is not offered:
  * MI_E_UNSUPPORTED. ---- */
