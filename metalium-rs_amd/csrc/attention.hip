@@ -784,6 +784,15 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
 #pragma unroll
     for (int s = 0; s < CS; ++s) ov[i][s] = pb[(s < S ? s : S - 1) * PS + 2 * G + ec];
   }
+  // The queries the new key's scores take (wavefront w: heads w, w + 4),
+  // requested with them too.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float qv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int gg = wave + 4 * u;
+    qv[u] = g.q[(b * g.H + j * G + (gg < G ? gg : 0)) * D + lane];
+  }
   for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
   int64_t pos = g.pa.pos0;
   if (g.pa.dev) {
@@ -798,13 +807,16 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
     if constexpr (sizeof(KV) == 2) vd[i] = bf16_bits_to_f32(vn[ec % D]);
     else vd[i] = vn[ec % D];
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int gg = wave; gg < G; gg += 4) {
-    float kd;
-    if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
-    else kd = kn[lane];
-    const float sc = fold_sum<64>(g.q[(b * g.H + j * G + gg) * D + lane] * kd);
-    if (lane == 0) snew[gg] = sc * g.scale;
+  float kd;
+  if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
+  else kd = kn[lane];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int gg = wave + 4 * u;
+    if (gg < G) {
+      const float sc = fold_sum<64>(qv[u] * kd);
+      if (lane == 0) snew[gg] = sc * g.scale;
+    }
   }
   __syncthreads();
   if (threadIdx.x < G) {
