@@ -622,7 +622,7 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, cons
 
 
 // ------------------------------ a decode step's q|k|v and attention, fused
-// One new position per sequence (a decode step) of up to 2 sequences with
+// One new position per sequence (a decode step) of up to 6 sequences with
 // 64-wide heads: the RMSNorm of the hidden row, the q|k|v projection, RoPE,
 // the cache write and the attention's key chunks in one launch (the
 // composition mi_norm_qkv_rope then mi_attention_rows_at runs as two, the
@@ -637,8 +637,10 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, cons
 // q . k_new (read back from the cache, as stored), weight 1, value v_new.
 // So every block of the launch is independent; the queries of the head's
 // first chunk block go to memory for the combine.  The 9 chunk blocks of a
-// head read the same 64 weight rows (74 KB for k = 576): the repeats come
-// from the caches.
+// head read the same 64 weight rows (74 KB for k = 576); they run on
+// different XCDs, each with its own L2, so the repeats are fetched from the
+// fabric (8.7 MB a SmolLM2 launch against 2.0 MB of weights and cache), at a
+// rate that does not bound the launch.
 constexpr int DQA_MAX_CH = 32;  // 16-byte weight chunks a thread: k <= 1024 (CH: 8, 16, 24 or 32)
 constexpr int DQA_D = 64;
 // Sequences up to which the fused launch serves a decode step: beyond, its
