@@ -759,7 +759,10 @@ __global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(De
 
 // The split products' partials added in split order, then the mode's
 // epilogue (RMS, residual, SiLU-mul, RoPE and the cache write): one thread
-// per (activation row, output pair).
+// per (activation row, output pair).  Every partial, sum of squares and
+// epilogue operand is requested before the first add (the split count is at
+// most DSPLIT_MAX), so the fold is one memory round trip, not one per split.
+constexpr int DSPLIT_MAX = 8;
 template <int MODE>
 __global__ void __launch_bounds__(256) decode_fold_kernel(DecodeArgs g, int M) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -767,20 +770,35 @@ __global__ void __launch_bounds__(256) decode_fold_kernel(DecodeArgs g, int M) {
   const int64_t m = i / g.npairs, p = i - m * g.npairs;
   const PairRows q = pair_rows<MODE>(g, p);
   const int S = g.split;
-  float y0 = g.part[m * g.N + q.r0], y1 = q.has1 ? g.part[m * g.N + q.r1] : 0.0f;
-  for (int s = 1; s < S; ++s) {
-    y0 += g.part[(s * M + m) * g.N + q.r0];
-    if (q.has1) y1 += g.part[(s * M + m) * g.N + q.r1];
+  const float *ssq = g.part + static_cast<int64_t>(S) * M * g.N;
+  float p0[DSPLIT_MAX], p1[DSPLIT_MAX], sq[DSPLIT_MAX];
+#pragma unroll
+  for (int s = 0; s < DSPLIT_MAX; ++s) {
+    if (s < S) {
+      p0[s] = g.part[(s * M + m) * g.N + q.r0];
+      p1[s] = q.has1 ? g.part[(s * M + m) * g.N + q.r1] : 0.0f;
+      sq[s] = g.gamma ? ssq[s * M + m] : 0.0f;
+    }
+  }
+  const PairPre e = pair_pre<MODE>(g, q, m);
+  float y0 = p0[0], y1 = p1[0];
+#pragma unroll
+  for (int s = 1; s < DSPLIT_MAX; ++s) {
+    if (s < S) {
+      y0 += p0[s];
+      y1 += p1[s];
+    }
   }
   if (g.gamma) {
-    const float *ssq = g.part + static_cast<int64_t>(S) * M * g.N;
-    float ss = ssq[m];
-    for (int s = 1; s < S; ++s) ss += ssq[s * M + m];
+    float ss = sq[0];
+#pragma unroll
+    for (int s = 1; s < DSPLIT_MAX; ++s)
+      if (s < S) ss += sq[s];
     const float rms = __fsqrt_rn(ss / static_cast<float>(g.K) + g.eps);
     y0 = y0 / rms;
     y1 = y1 / rms;
   }
-  pair_write<MODE>(g, q, m, y0, y1);
+  pair_write_pre<MODE>(g, q, m, y0, y1, e);
 }
 
 // Rows up to which the GEMV beats the matrix-core form (SmolLM2 decode step
@@ -804,7 +822,7 @@ static int dsplit_count(int64_t M, const DecodeArgs &g) {
   const int64_t nsteps = g.K / 16, per = DSPLIT_WAVES * (NB == 1 ? 6 : 3);
   int64_t S = (nsteps + per - 1) / per;
   if (S < 2) return 1;
-  if (S > 8) S = 8;
+  if (S > DSPLIT_MAX) S = DSPLIT_MAX;
   return static_cast<int>(S);
 }
 
