@@ -234,6 +234,17 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
   const float *pb = part + item * S * static_cast<int64_t>(PS);
   float *w = st + 2 * G * S;
   float *den = w + G * S;
+  // A thread's output elements e = tid + 256 i: their first CS chunks'
+  // values requested with the statistics, so the combine is one round trip
+  // for up to CS chunks.
+  constexpr int EP = (G * D + 255) / 256, CS = EP <= 2 ? 16 : 8;
+  float ov[EP][CS];
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) ov[i][s] = s < S ? pb[s * PS + 2 * G + ec] : 0.0f;
+  }
   for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
   __syncthreads();
   if (threadIdx.x < G) {
@@ -250,12 +261,18 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
   }
   __syncthreads();
   float *dst = out + (b * T + p) * H * D + j * G * D;
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int g = e / D;
-    float num = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
-    dst[e] = num / den[g];
+#pragma unroll
+  for (int i = 0; i < EP; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    if (e < G * D) {
+      const int g = e / D;
+      float num = 0.0f;
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+        if (s < S) num += w[s * G + g] * ov[i][s];
+      for (int s = CS; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
+      dst[e] = num / den[g];
+    }
   }
 }
 

@@ -972,9 +972,16 @@ __global__ void __launch_bounds__(256) sgd_kernel(SgdList L, float lr) {
     if (e + 3 < n && (S == 1 || (n & 3) == 0)) {  // slices 16-byte aligned too
       float4 pv = *reinterpret_cast<const float4 *>(p + e);
       float4 gv = *reinterpret_cast<const float4 *>(g + e);
-      for (int z = 1; z < S; ++z) {
-        const float4 q = *reinterpret_cast<const float4 *>(g + z * n + e);
-        gv.x += q.x; gv.y += q.y; gv.z += q.z; gv.w += q.w;
+      for (int z0 = 1; z0 < S; z0 += 4) {  // four slices' loads before their adds
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (z0 + u < S) q[u] = *reinterpret_cast<const float4 *>(g + (z0 + u) * n + e);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (z0 + u < S) {
+            gv.x += q[u].x; gv.y += q[u].y; gv.z += q[u].z; gv.w += q[u].w;
+          }
       }
       pv.x = __fsub_rn(pv.x, __fmul_rn(gv.x, lr));
       pv.y = __fsub_rn(pv.y, __fmul_rn(gv.y, lr));

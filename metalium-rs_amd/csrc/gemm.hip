@@ -1130,11 +1130,22 @@ __global__ void splitk_reduce(const float *part, int S, int64_t mn, int64_t n, T
                               const float *resid, int64_t ldr) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= mn) return;
-  float s = part[i];
-  for (int z = 1; z < S; ++z) s += part[z * mn + i];
   const int64_t row = i / n, col = i - row * n;
-  if (bias) s = __fadd_rn(s, bias[col]);
-  if (resid) s = __fadd_rn(resid[row * ldr + col], s);
+  // The epilogue operands and eight slices at a time requested before their
+  // adds (in slice order), so the reduce is not one round trip per slice.
+  const float bv = bias ? bias[col] : 0.0f, rv = resid ? resid[row * ldr + col] : 0.0f;
+  float s = part[i];
+  for (int z0 = 1; z0 < S; z0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < S) v[u] = part[(z0 + u) * mn + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < S) s += v[u];
+  }
+  if (bias) s = __fadd_rn(s, bv);
+  if (resid) s = __fadd_rn(rv, s);
   if constexpr (sizeof(TO) == 2) C[row * ldc + col] = f32_to_bf16_bits(s);
   else C[row * ldc + col] = s;
 }
