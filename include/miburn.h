@@ -196,6 +196,19 @@ int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias,
  * mod.rs:1-12) instead. */
 int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed,
                     mi_id bias, mi_id residual, int out_elem, mi_id *out);
+/* A SwiGLU MLP's first half from an F32 `x` [m, k] given as its parts: with
+ * the gate and up weights' rows interleaved in 32-row groups (`w_pairs`
+ * [2 i, k] BF16: gate rows 0..31, up rows 0..31, gate rows 32..63, ...), the
+ * result is silu(x gate^T) * (x up^T) ([m, i]) as its parts (MI_BF16_PARTS,
+ * [m, 2 i] BF16), each product as mi_linear_parts computes it and
+ * silu * up as MI_K_SILU_MUL does -- the same bits as mi_linear_parts against
+ * the [gate; up] weight followed by mi_silu_mul_halves to parts, without the
+ * F32 [m, 2 i] product between them.  Whole tiles only: m a multiple of
+ * 128, k of 32, i of 128 (else MI_E_UNSUPPORTED).  No Engine counterpart
+ * (the reference's MLP, crates/tt-models/src/llama.rs:494-498, runs the two
+ * products and the SwiGLU as separate ops). */
+int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
+                           mi_id *out);
 
 /* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
  * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as

@@ -245,6 +245,14 @@ inline Tensor linear_parts(const Tensor &x_parts, const Tensor &w, bool tw, cons
   return Tensor(x_parts.ctx(), id, {x_parts.rows(), tw ? w.rows() : w.cols()});
 }
 
+// silu(x gate^T) * (x up^T) as BF16 parts from x's parts and the gate|up
+// weight interleaved in 32-row groups: mi_linear_swiglu_parts.
+inline Tensor linear_swiglu_parts(const Tensor &x_parts, const Tensor &w_pairs) {
+  mi_id id;
+  check(x_parts.ctx(), mi_linear_swiglu_parts(x_parts.ctx(), x_parts.use(), w_pairs.use(), &id), "linear_swiglu_parts");
+  return Tensor(x_parts.ctx(), id, {x_parts.rows(), w_pairs.rows()});
+}
+
 // Grouped strided products written into `out` in place (item (g, i) of an
 // operand at at[0] + g * at[1] + i * at[2], read with its row pitch).
 struct Items {

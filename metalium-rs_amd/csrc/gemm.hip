@@ -230,6 +230,11 @@ struct GemmArgs {
   // several copies of it (A = [hi | lo] parts of an F32 operand against one
   // B: B's k wraps modulo kb; 0 for none).
   int64_t kb = 0;
+  // Direct BF16 kernel only: B's rows are gate|up pairs (32 gate rows, then
+  // the 32 up rows of the same outputs, ...), and C receives silu(gate) * up
+  // as its BF16 parts ([M, N] BF16 for N / 2 outputs: a row's heads, then its
+  // remainders); 0 for a plain product.
+  int swiglu = 0;
 };
 
 // The epilogue over one 32 x 32 accumulator fragment, whose lane holds column
@@ -1002,6 +1007,32 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   // next to the accumulators.
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t row0 = m0 + wm * WTM + 4 * lhalf, col0 = n0 + wn * WTN + lrow;
+  if constexpr (TN % 2 == 0 && !GN) {
+    if (g.swiglu) {
+      // Fragments (i, 2 jp) and (i, 2 jp + 1) are the gate and up columns of
+      // outputs (n0 + wn WTN) / 2 + 32 jp + lane % 32: silu(gate) * up as the
+      // element-wise SILU_MUL computes it, stored as its BF16 parts.
+      uint16_t *P = static_cast<uint16_t *>(g.c);
+      const int64_t I = g.N / 2;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int jp = 0; jp < TN / 2; ++jp) {
+          const int64_t oc = (n0 + wn * WTN) / 2 + 32 * jp + lrow;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+            const float gt = acc[i][2 * jp][r], up = acc[i][2 * jp + 1][r];
+            uint16_t h, l;
+            split_bf16((gt * sigmoid2(gt)) * up, h, l);
+            P[row * 2 * I + oc] = h;
+            P[row * 2 * I + I + oc] = l;
+          }
+        }
+      }
+      return;
+    }
+  }
   const bool plain = g.bias == nullptr && g.resid == nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -1169,6 +1200,7 @@ struct Plan {
   int64_t per_group = 0;          // items per group (0: one group of `batch`)
   int64_t sa2 = 0, sb2 = 0, sc2 = 0;  // group strides
   int64_t kb = 0;  // direct BF16 kernel: B's k extent when A's k repeats it (see GemmArgs)
+  bool swiglu = false;  // direct BF16 kernel: gate|up pairs into silu(gate) * up parts (see GemmArgs)
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1216,6 +1248,7 @@ static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   g.kc = 0;
   g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.kb = p.kb;
+  g.swiglu = p.swiglu ? 1 : 0;
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
@@ -1930,6 +1963,47 @@ extern "C" int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transp
     return fail(ctx, MI_E_HIP, "linear_parts launch: %s", hipGetErrorString(e));
   }
   s = check_launch(ctx, "linear_parts");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, X, x_parts);
+  MI_BUF(ctx, W, w_pairs);
+  if (X->elem != MI_BF16 || X->cols % 2 || W->elem != MI_BF16)
+    return fail(ctx, MI_E_ARG, "linear_swiglu_parts: parts %s [%lld, %lld] and weight %s, want BF16 [m, 2 k] and BF16",
+                elem_name(X->elem), (long long)X->rows, (long long)X->cols, elem_name(W->elem));
+  const int64_t m = X->rows, k = X->cols / 2, n = W->rows;
+  if (W->cols != k)
+    return fail(ctx, MI_E_ARG, "linear_swiglu_parts: x is [%lld, %lld], the weight [%lld, %lld]", (long long)m,
+                (long long)k, (long long)n, (long long)W->cols);
+  Plan p;
+  p.ta = false; p.tb = true;
+  p.fast = true;
+  p.ea = MI_F32; p.eb = MI_BF16; p.eo = MI_F32;
+  p.a = nullptr; p.b = W->ptr;
+  p.M = m; p.K = k; p.N = n;
+  p.batch = 1; p.sa = p.sb = p.sc = 0;
+  p.lda = k; p.ldb = W->cols;
+  p.swiglu = true;
+  // Whole tiles only (the pairs' epilogue has no edge form): 128-row tiles,
+  // k a multiple of 32, 256 weight rows (128 outputs) a tile column.
+  if (m < 1 || k < 1 || n % 256 || !parts_direct_fits(p))
+    return fail(ctx, MI_E_UNSUPPORTED, "linear_swiglu_parts: [%lld, %lld] x [%lld, %lld] (m a multiple of 128, k of 32, "
+                "the weight's rows of 256)", (long long)m, (long long)k, (long long)n, (long long)k);
+  mi_id id; Buffer *cb;
+  int s = new_buffer(ctx, m, n, MI_BF16, &id, &cb);
+  if (s) return s;
+  p.c = cb->ptr;
+  const hipError_t e = launch_parts(p, X->ptr, ctx->stream);
+  if (e != hipSuccess) {
+    mi_free(ctx, id);
+    return fail(ctx, MI_E_HIP, "linear_swiglu_parts launch: %s", hipGetErrorString(e));
+  }
+  s = check_launch(ctx, "linear_swiglu_parts");
   if (s) { mi_free(ctx, id); return s; }
   *out = id;
   return MI_OK;

@@ -40,6 +40,10 @@ using burn::Tensor;
 
 struct Layer {
   Tensor attn_norm, wqkv, wo, mlp_norm, wgu, wdown;  // wqkv = [wq; wk; wv], wgu = [gate; up]
+  // wgu's rows interleaved in 32-row groups (gate 0..31, up 0..31, gate
+  // 32..63, ...) for mi_linear_swiglu_parts (intermediate a multiple of 128;
+  // weights do not change after creation).
+  Tensor wgu_pairs;
   Tensor cache_k, cache_v;
 };
 
@@ -237,9 +241,17 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
     x = burn::linear(oh, L.wo, true, nullptr, &x);  // x + oh wo^T, the add in the product's epilogue
     Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps, parts_gu ? MI_BF16_PARTS : act);
     // One product against the fused gate|up weight, silu(gate) * up of its halves.
-    Tensor gu = parts_gu ? burn::linear_parts(hn, L.wgu, true, nullptr, nullptr)
-                         : burn::float_matmul(hn, false, L.wgu, true);
-    Tensor h = burn::silu_mul_halves(gu, parts_down ? MI_BF16_PARTS : act);
+    // With parts for both the gate|up and the down product, one launch forms
+    // silu(gate) * up's parts from the interleaved weight (no F32 [rows,
+    // 2 inter] product in between).
+    Tensor h;
+    if (parts_gu && parts_down && L.wgu_pairs.defined()) {
+      h = burn::linear_swiglu_parts(hn, L.wgu_pairs);
+    } else {
+      Tensor gu = parts_gu ? burn::linear_parts(hn, L.wgu, true, nullptr, nullptr)
+                           : burn::float_matmul(hn, false, L.wgu, true);
+      h = burn::silu_mul_halves(gu, parts_down ? MI_BF16_PARTS : act);
+    }
     x = parts_down ? burn::linear_parts(h, L.wdown, true, nullptr, &x) : burn::linear(h, L.wdown, true, nullptr, &x);
   }
   m->len = ctxlen;
@@ -327,6 +339,11 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
       L.mlp_norm = ones(ctx, c.hidden);
       L.wgu = weight(ctx, 2 * static_cast<int64_t>(c.intermediate), c.hidden, init_std, next());
       L.wdown = weight(ctx, c.hidden, c.intermediate, init_std, next());
+      if (c.intermediate % 128 == 0 && c.hidden % 32 == 0) {
+        const int64_t I = c.intermediate, Hd = c.hidden;
+        const int64_t dims[4] = {I / 32, 2, 32, Hd}, st[4] = {32 * Hd, I * Hd, Hd, 1};
+        L.wgu_pairs = burn::copy4(L.wgu, dims, 0, st);
+      }
     }
     // Rotary tables (rope.rs:14-60): angle = position * theta^(-2i / d), the
     // first half repeated as the second, sin's first half negated.

@@ -103,6 +103,7 @@ def _load() -> ctypes.CDLL:
         "mi_matmul_batched": [P, U64, c_int, U64, c_int, I64, I64, I64, I64, c_int, Ip],
         "mi_linear": [P, U64, U64, c_int, U64, U64, c_int, Ip],
         "mi_linear_parts": [P, U64, U64, c_int, U64, U64, c_int, Ip],
+        "mi_linear_swiglu_parts": [P, U64, U64, Ip],
         "mi_matmul_slices": [P, U64, c_int, U64, c_int, Ip, ctypes.POINTER(I64)],
         "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
                             I64, U64, ctypes.POINTER(I64)],
@@ -297,6 +298,11 @@ class Engine:
                      out_elem: int = F32) -> int:
         """linear() of an F32 operand given as its BF16 parts [m, 2k] (BF16_PARTS)."""
         return self._out(self._lib.mi_linear_parts, x_parts, w, int(w_t), bias, residual, out_elem)
+
+    def linear_swiglu_parts(self, x_parts: int, w_pairs: int) -> int:
+        """silu(x gate^T) * (x up^T) as BF16 parts, from x's parts and a gate|up
+        weight whose rows interleave in 32-row groups."""
+        return self._out(self._lib.mi_linear_swiglu_parts, x_parts, w_pairs)
 
     def log_softmax_ce(self, logits: int, targets: int, grad_scale: float):
         """(picked, dlogits): logp at each row's target and the cross-entropy

@@ -12,7 +12,8 @@ for bit the fast mode's own linear where that splits the operand itself,
 and within the F32 bound of float64 on the other shapes; the parts that
 mi_rms_norm and mi_silu_mul_halves produce are bit for bit the split of
 their F32 results (the split restated here in numpy and checked on
-hand-worked values).
+hand-worked values); mi_linear_swiglu_parts is bit for bit that product
+against [gate; up] followed by the SiLU-mul to parts.
 
 mi_matmul_items (grouped strided items written in place): each item within
 the F32 accumulation bound of the oracle's product of the same blocks, the
@@ -230,6 +231,39 @@ def test_linear_parts_other_shapes(engine, m, n, k, tw):
     tol = 1e-5 * (np.abs(xs) @ np.abs(w)) + 1e-6 * (np.abs(ref) + np.abs(bias) + np.abs(resid)) + 1e-30
     assert got.shape == (m, n)
     assert np.all(np.abs(got - ref) <= tol)
+
+
+def pairs_of(gu, inter):
+    """[gate; up] rows [2 i, k] -> rows interleaved in 32-row groups."""
+    k = gu.shape[1]
+    return np.ascontiguousarray(gu.reshape(2, inter // 32, 32, k).transpose(1, 0, 2, 3).reshape(2 * inter, k))
+
+
+@pytest.mark.parametrize("m,k,inter", [(16384, 576, 1536), (4096, 576, 1536), (512, 576, 1536), (256, 64, 128)])
+def test_linear_swiglu_parts_equals_composition(engine, m, k, inter):
+    """The fused SwiGLU half from interleaved weights: bit for bit the
+    product from parts against [gate; up] then the SiLU-mul to parts (256 x
+    256 tiles at 4096+ rows, 128 x 128 below)."""
+    x = rnd(m, k)
+    gu = orc.to_bf16(rnd(2 * inter, k, scale=0.05))
+    ip = engine.upload_bf16(split_parts(x))
+    want = engine.download(engine.silu_mul_halves(engine.linear_parts(ip, engine.upload_bf16(gu), True),
+                                                  miburn.BF16_PARTS))
+    got = engine.download(engine.linear_swiglu_parts(ip, engine.upload_bf16(pairs_of(gu, inter))))
+    assert got.shape == (m, 2 * inter)
+    same_bits(got, want, np.uint16)
+
+
+def test_linear_swiglu_parts_refuses_partial_tiles(engine):
+    w = engine.upload_bf16(orc.to_bf16(rnd(256, 64)))
+    for rows, cols, kind in ((200, 128, "UNSUPPORTED"), (256, 127, "ARG")):
+        with pytest.raises(miburn.MiError) as e:
+            engine.linear_swiglu_parts(engine.upload_bf16(orc.to_bf16(rnd(rows, cols))), w)
+        assert e.value.kind == kind
+    with pytest.raises(miburn.MiError) as e:  # 192 weight rows: 96 outputs, not a whole tile column
+        engine.linear_swiglu_parts(engine.upload_bf16(orc.to_bf16(rnd(256, 128))),
+                                   engine.upload_bf16(orc.to_bf16(rnd(192, 64))))
+    assert e.value.kind == "UNSUPPORTED"
 
 
 def test_linear_parts_argument_errors(engine):
