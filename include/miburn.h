@@ -209,6 +209,13 @@ int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed,
  * products and the SwiGLU as separate ops). */
 int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
                            mi_id *out);
+/* The same for BF16 activations `x` [m, k] (the performance numeric
+ * contract's operands): silu(x gate^T) * (x up^T) [m, i] as F32, or rounded
+ * once to BF16 (`out_elem`) -- the same bits as the BF16 product against
+ * [gate; up] on the direct kernel followed by mi_silu_mul_halves.  Whole
+ * tiles only, as mi_linear_swiglu_parts. */
+int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_elem,
+                     mi_id *out);
 
 /* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
  * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as

@@ -253,6 +253,13 @@ inline Tensor linear_swiglu_parts(const Tensor &x_parts, const Tensor &w_pairs) 
   return Tensor(x_parts.ctx(), id, {x_parts.rows(), w_pairs.rows()});
 }
 
+// The same from BF16 activations, F32 or rounded to BF16: mi_linear_swiglu.
+inline Tensor linear_swiglu(const Tensor &x, const Tensor &w_pairs, int out_elem) {
+  mi_id id;
+  check(x.ctx(), mi_linear_swiglu(x.ctx(), x.use(), w_pairs.use(), out_elem, &id), "linear_swiglu");
+  return Tensor(x.ctx(), id, {x.rows(), w_pairs.rows() / 2});
+}
+
 // Grouped strided products written into `out` in place (item (g, i) of an
 // operand at at[0] + g * at[1] + i * at[2], read with its row pitch).
 struct Items {

@@ -208,6 +208,7 @@ struct TileLoader {
   }
 };
 
+enum { SWIGLU_PARTS = 1, SWIGLU_BF16 = 2, SWIGLU_F32 = 3 };
 struct GemmArgs {
   const void *a;
   const void *b;
@@ -232,8 +233,9 @@ struct GemmArgs {
   int64_t kb = 0;
   // Direct BF16 kernel only: B's rows are gate|up pairs (32 gate rows, then
   // the 32 up rows of the same outputs, ...), and C receives silu(gate) * up
-  // as its BF16 parts ([M, N] BF16 for N / 2 outputs: a row's heads, then its
-  // remainders); 0 for a plain product.
+  // for the N / 2 outputs -- SWIGLU_PARTS: as its BF16 parts ([M, N] BF16: a
+  // row's heads, then its remainders); SWIGLU_BF16 / SWIGLU_F32: [M, N / 2]
+  // rounded once to BF16, or F32; 0 for a plain product.
   int swiglu = 0;
 };
 
@@ -1011,8 +1013,9 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
     if (g.swiglu) {
       // Fragments (i, 2 jp) and (i, 2 jp + 1) are the gate and up columns of
       // outputs (n0 + wn WTN) / 2 + 32 jp + lane % 32: silu(gate) * up as the
-      // element-wise SILU_MUL computes it, stored as its BF16 parts.
+      // element-wise SILU_MUL computes it, stored in the asked form.
       uint16_t *P = static_cast<uint16_t *>(g.c);
+      float *Pf = static_cast<float *>(g.c);
       const int64_t I = g.N / 2;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -1023,10 +1026,17 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
           for (int r = 0; r < 16; ++r) {
             const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
             const float gt = acc[i][2 * jp][r], up = acc[i][2 * jp + 1][r];
-            uint16_t h, l;
-            split_bf16((gt * sigmoid2(gt)) * up, h, l);
-            P[row * 2 * I + oc] = h;
-            P[row * 2 * I + I + oc] = l;
+            const float y = (gt * sigmoid2(gt)) * up;
+            if (g.swiglu == SWIGLU_PARTS) {
+              uint16_t h, l;
+              split_bf16(y, h, l);
+              P[row * 2 * I + oc] = h;
+              P[row * 2 * I + I + oc] = l;
+            } else if (g.swiglu == SWIGLU_BF16) {
+              P[row * I + oc] = f32_to_bf16_bits(y);
+            } else {
+              Pf[row * I + oc] = y;
+            }
           }
         }
       }
@@ -1200,7 +1210,7 @@ struct Plan {
   int64_t per_group = 0;          // items per group (0: one group of `batch`)
   int64_t sa2 = 0, sb2 = 0, sc2 = 0;  // group strides
   int64_t kb = 0;  // direct BF16 kernel: B's k extent when A's k repeats it (see GemmArgs)
-  bool swiglu = false;  // direct BF16 kernel: gate|up pairs into silu(gate) * up parts (see GemmArgs)
+  int swiglu = 0;  // direct BF16 kernel: gate|up pairs into silu(gate) * up (see GemmArgs)
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1248,7 +1258,7 @@ static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   g.kc = 0;
   g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.kb = p.kb;
-  g.swiglu = p.swiglu ? 1 : 0;
+  g.swiglu = p.swiglu;
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
@@ -1988,7 +1998,7 @@ extern "C" int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
   p.M = m; p.K = k; p.N = n;
   p.batch = 1; p.sa = p.sb = p.sc = 0;
   p.lda = k; p.ldb = W->cols;
-  p.swiglu = true;
+  p.swiglu = SWIGLU_PARTS;
   // Whole tiles only (the pairs' epilogue has no edge form): 128-row tiles,
   // k a multiple of 32, 256 weight rows (128 outputs) a tile column.
   if (m < 1 || k < 1 || n % 256 || !parts_direct_fits(p))
@@ -2004,6 +2014,48 @@ extern "C" int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
     return fail(ctx, MI_E_HIP, "linear_swiglu_parts launch: %s", hipGetErrorString(e));
   }
   s = check_launch(ctx, "linear_swiglu_parts");
+  if (s) { mi_free(ctx, id); return s; }
+  *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, X, x);
+  MI_BUF(ctx, W, w_pairs);
+  if (X->elem != MI_BF16 || W->elem != MI_BF16)
+    return fail(ctx, MI_E_ARG, "linear_swiglu: x %s and weight %s, want BF16", elem_name(X->elem), elem_name(W->elem));
+  if (out_elem != MI_F32 && out_elem != MI_BF16)
+    return fail(ctx, MI_E_ARG, "linear_swiglu result kind %d", out_elem);
+  const int64_t m = X->rows, k = X->cols, n = W->rows;
+  if (W->cols != k)
+    return fail(ctx, MI_E_ARG, "linear_swiglu: x is [%lld, %lld], the weight [%lld, %lld]", (long long)m, (long long)k,
+                (long long)n, (long long)W->cols);
+  Plan p;
+  p.ta = false; p.tb = true;
+  p.fast = true;
+  p.ea = MI_BF16; p.eb = MI_BF16; p.eo = MI_F32;
+  p.a = X->ptr; p.b = W->ptr;
+  p.M = m; p.K = k; p.N = n;
+  p.batch = 1; p.sa = p.sb = p.sc = 0;
+  p.lda = k; p.ldb = W->cols;
+  p.swiglu = out_elem == MI_BF16 ? SWIGLU_BF16 : SWIGLU_F32;
+  if (m < 1 || k < 1 || n % 256 || !parts_direct_fits(p) || k % 8 || (reinterpret_cast<uintptr_t>(p.a) & 15))
+    return fail(ctx, MI_E_UNSUPPORTED, "linear_swiglu: [%lld, %lld] x [%lld, %lld] (m a multiple of 128, k of 32, "
+                "the weight's rows of 256)", (long long)m, (long long)k, (long long)n, (long long)k);
+  mi_id id; Buffer *cb;
+  int s = new_buffer(ctx, m, n / 2, out_elem, &id, &cb);
+  if (s) return s;
+  p.c = cb->ptr;
+  hipError_t e;
+  if (parts_small_tiles(p)) e = launch_pipe<float, 128, 128, 5, 2, 2>(p, ctx->stream);
+  else e = launch_pipe<float, 256, 256, 5, 2, 4>(p, ctx->stream);
+  if (e != hipSuccess) {
+    mi_free(ctx, id);
+    return fail(ctx, MI_E_HIP, "linear_swiglu launch: %s", hipGetErrorString(e));
+  }
+  s = check_launch(ctx, "linear_swiglu");
   if (s) { mi_free(ctx, id); return s; }
   *out = id;
   return MI_OK;

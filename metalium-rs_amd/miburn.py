@@ -104,6 +104,7 @@ def _load() -> ctypes.CDLL:
         "mi_linear": [P, U64, U64, c_int, U64, U64, c_int, Ip],
         "mi_linear_parts": [P, U64, U64, c_int, U64, U64, c_int, Ip],
         "mi_linear_swiglu_parts": [P, U64, U64, Ip],
+        "mi_linear_swiglu": [P, U64, U64, c_int, Ip],
         "mi_matmul_slices": [P, U64, c_int, U64, c_int, Ip, ctypes.POINTER(I64)],
         "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
                             I64, U64, ctypes.POINTER(I64)],
@@ -303,6 +304,11 @@ class Engine:
         """silu(x gate^T) * (x up^T) as BF16 parts, from x's parts and a gate|up
         weight whose rows interleave in 32-row groups."""
         return self._out(self._lib.mi_linear_swiglu_parts, x_parts, w_pairs)
+
+    def linear_swiglu(self, x: int, w_pairs: int, out_elem: int = BF16) -> int:
+        """silu(x gate^T) * (x up^T) from BF16 activations and the interleaved
+        gate|up weight, F32 or rounded to BF16."""
+        return self._out(self._lib.mi_linear_swiglu, x, w_pairs, out_elem)
 
     def log_softmax_ce(self, logits: int, targets: int, grad_scale: float):
         """(picked, dlogits): logp at each row's target and the cross-entropy

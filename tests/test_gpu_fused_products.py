@@ -254,6 +254,21 @@ def test_linear_swiglu_parts_equals_composition(engine, m, k, inter):
     same_bits(got, want, np.uint16)
 
 
+@pytest.mark.parametrize("m,k,inter", [(16384, 576, 1536), (512, 576, 1536), (256, 64, 128)])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_linear_swiglu_equals_composition(engine, m, k, inter, out):
+    """BF16 activations: bit for bit the BF16 product against [gate; up]
+    (the direct kernel at these shapes) then the SiLU-mul, F32 or rounded to
+    BF16."""
+    oe = BF16 if out == "bf16" else F32
+    ix = engine.upload_bf16(orc.to_bf16(rnd(m, k)))
+    gu = orc.to_bf16(rnd(2 * inter, k, scale=0.05))
+    want = engine.download(engine.silu_mul_halves(engine.matmul_dram(ix, False, engine.upload_bf16(gu), True), oe))
+    got = engine.download(engine.linear_swiglu(ix, engine.upload_bf16(pairs_of(gu, inter)), oe))
+    assert got.shape == (m, inter)
+    same_bits(got, want, np.uint16 if oe == BF16 else np.uint32)
+
+
 def test_linear_swiglu_parts_refuses_partial_tiles(engine):
     w = engine.upload_bf16(orc.to_bf16(rnd(256, 64)))
     for rows, cols, kind in ((200, 128, "UNSUPPORTED"), (256, 127, "ARG")):
@@ -264,6 +279,10 @@ def test_linear_swiglu_parts_refuses_partial_tiles(engine):
         engine.linear_swiglu_parts(engine.upload_bf16(orc.to_bf16(rnd(256, 128))),
                                    engine.upload_bf16(orc.to_bf16(rnd(192, 64))))
     assert e.value.kind == "UNSUPPORTED"
+    for x, kind in ((engine.upload_bf16(orc.to_bf16(rnd(200, 64))), "UNSUPPORTED"), (engine.upload(rnd(256, 64)), "ARG")):
+        with pytest.raises(miburn.MiError) as e:
+            engine.linear_swiglu(x, w)
+        assert e.value.kind == kind
 
 
 def test_linear_parts_argument_errors(engine):
