@@ -216,6 +216,21 @@ int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
  * tiles only, as mi_linear_swiglu_parts. */
 int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_elem,
                      mi_id *out);
+/* The q|k|v product and mi_qkv_rope_cache in one launch: `x` BF16 [rows, k]
+ * activations, or with `x_parts` an F32 operand's parts ([rows, 2 k],
+ * MI_BF16_PARTS), against `w_qkv` [(heads + 2 kv_heads) 64, k] BF16; RoPE,
+ * the cache writes and q's layout as mi_qkv_rope_cache (its q returned), on
+ * the product's accumulators -- the same bits as the product (mi_matmul /
+ * mi_linear_parts) followed by mi_qkv_rope_cache, without the F32 q|k|v
+ * rows between them.  64-wide heads, rows a multiple of 128 and k of 32
+ * (else MI_E_UNSUPPORTED).  No Engine counterpart (the reference's
+ * attention block, crates/tt-models/src/llama.rs:403-446, runs the
+ * projection, RoPE and the cache writes as separate ops). */
+int mi_linear_qkv_rope_cache(mi_ctx *ctx, mi_id x, int x_parts, mi_id w_qkv,
+                             mi_id cos_table, mi_id sin_table, int64_t seq,
+                             int64_t heads, int64_t kv_heads, int64_t pos0,
+                             mi_id k_cache, mi_id v_cache, int grouped,
+                             mi_id *q_out);
 
 /* ---- matmul mode: Engine::matmul_mode (server.rs:48) and the reference's
  * MatmulMode (crates/burn-tt/src/matmul_mode.rs:1-43), fixed per context as

@@ -260,6 +260,18 @@ inline Tensor linear_swiglu(const Tensor &x, const Tensor &w_pairs, int out_elem
   return Tensor(x.ctx(), id, {x.rows(), w_pairs.rows() / 2});
 }
 
+// The q|k|v product and the prefill's q|k|v tail in one launch
+// (mi_linear_qkv_rope_cache): q out, as qkv_rope_cache.
+inline Tensor linear_qkv_rope_cache(const Tensor &x, bool x_parts, const Tensor &w_qkv, const Tensor &cos,
+                                    const Tensor &sin, int64_t seq, int64_t heads, int64_t kv_heads, int64_t pos0,
+                                    const Tensor &k_cache, const Tensor &v_cache, bool grouped) {
+  mi_id id;
+  check(x.ctx(), mi_linear_qkv_rope_cache(x.ctx(), x.use(), x_parts ? 1 : 0, w_qkv.use(), cos.use(), sin.use(), seq,
+                                          heads, kv_heads, pos0, k_cache.use(), v_cache.use(), grouped ? 1 : 0, &id),
+        "linear_qkv_rope_cache");
+  return Tensor(x.ctx(), id, {x.rows() * heads, k_cache.cols()});
+}
+
 // Grouped strided products written into `out` in place (item (g, i) of an
 // operand at at[0] + g * at[1] + i * at[2], read with its row pitch).
 struct Items {

@@ -209,6 +209,21 @@ struct TileLoader {
 };
 
 enum { SWIGLU_PARTS = 1, SWIGLU_BF16 = 2, SWIGLU_F32 = 3 };
+// A prefill's q|k|v tail in the direct kernel's epilogue (64-wide heads, the
+// product's columns (heads + 2 kv heads) x 64, its rows (sequence,
+// position)): RoPE on the q and k heads at position pos0 + p, q written to
+// row (b seq + p) heads + h or, grouped, ((b kv + j) seq + p) G + g, k and v
+// to cache row (b kv + j) maxc + pos0 + p -- mi_qkv_rope_cache's layout and
+// arithmetic.  mode 0: none; QKV_F32 / QKV_BF16: the caches' element.
+enum { QKV_F32 = 1, QKV_BF16 = 2 };
+struct QkvTail {
+  int mode = 0;
+  const float *cos = nullptr, *sin = nullptr;
+  float *q = nullptr;
+  void *kc = nullptr, *vc = nullptr;
+  int64_t seq = 1, pos0 = 0, maxc = 0;
+  int heads = 0, kvh = 1, grouped = 0;
+};
 struct GemmArgs {
   const void *a;
   const void *b;
@@ -237,6 +252,7 @@ struct GemmArgs {
   // row's heads, then its remainders); SWIGLU_BF16 / SWIGLU_F32: [M, N / 2]
   // rounded once to BF16, or F32; 0 for a plain product.
   int swiglu = 0;
+  QkvTail qkv;  // direct BF16 kernel only: the q|k|v tail instead of C
 };
 
 // The epilogue over one 32 x 32 accumulator fragment, whose lane holds column
@@ -893,6 +909,81 @@ __device__ __forceinline__ void pipe_mfma(f32x16 (&acc)[TM][TN], const uint4 (&f
                                                           __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
 }
 
+// The q|k|v tail of a wavefront whose 64 columns are head hb / 64: fragment
+// 0 holds its columns j = lane % 32, fragment 1 columns j + 32 -- each
+// other's RoPE partners -- at rows row0 + 32 i + 8 (r / 4) + r % 4.  Each
+// fragment's rotary entries are requested before its rows are written.
+template <int TM>
+__device__ __forceinline__ void qkv_tail(const GemmArgs &g, const f32x16 (&acc)[TM][2], int64_t row0, int64_t hb,
+                                         int j) {
+  const QkvTail &t = g.qkv;
+  if (hb >= g.N) return;  // an edge tile's columns past the last head
+  const int h = static_cast<int>(hb >> 6), G = t.heads / t.kvh;
+  const bool rope = h < t.heads + t.kvh;
+  // A fragment's 32 rows (32-aligned) lie in one sequence when seq is a
+  // multiple of 32: one division a fragment, not two a value.
+  const bool whole = (t.seq & 31) == 0;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t fb = (row0 + i * 32) & ~static_cast<int64_t>(31);
+    const int64_t fbs = whole ? fb / t.seq : 0, fps = fb - fbs * t.seq;
+    auto seq_of = [&](int64_t row, int64_t &b, int64_t &p) {
+      if (whole) {
+        b = fbs;
+        p = fps + (row - fb);
+      } else {
+        b = row / t.seq;
+        p = row - b * t.seq;
+      }
+    };
+    float c0[16], c1[16], s0[16], s1[16];
+    if (rope) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+        int64_t b, p;
+        seq_of(row, b, p);
+        const int64_t pos = t.pos0 + p;
+        c0[r] = t.cos[pos * 64 + j];
+        c1[r] = t.cos[pos * 64 + j + 32];
+        s0[r] = t.sin[pos * 64 + j];
+        s1[r] = t.sin[pos * 64 + j + 32];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
+      int64_t b, p;
+      seq_of(row, b, p);
+      const int64_t pos = t.pos0 + p;
+      const float x0 = acc[i][0][r], x1 = acc[i][1][r];
+      float y0 = x0, y1 = x1;
+      if (rope) {
+        y0 = __fadd_rn(__fmul_rn(x0, c0[r]), __fmul_rn(x1, s0[r]));
+        y1 = __fadd_rn(__fmul_rn(x1, c1[r]), __fmul_rn(x0, s1[r]));
+      }
+      if (h < t.heads) {
+        const int kvh = h / G, gg = h - kvh * G;
+        const int64_t qrow = t.grouped ? ((b * t.kvh + kvh) * t.seq + p) * G + gg : row * t.heads + h;
+        t.q[qrow * 64 + j] = y0;
+        t.q[qrow * 64 + j + 32] = y1;
+      } else {
+        const bool isk = rope;
+        const int64_t crow = (b * t.kvh + (isk ? h - t.heads : h - t.heads - t.kvh)) * t.maxc + pos;
+        if (t.mode == QKV_BF16) {
+          uint16_t *c = static_cast<uint16_t *>(isk ? t.kc : t.vc) + crow * 64;
+          c[j] = f32_to_bf16_bits(y0);
+          c[j + 32] = f32_to_bf16_bits(y1);
+        } else {
+          float *c = static_cast<float *>(isk ? t.kc : t.vc) + crow * 64;
+          c[j] = y0;
+          c[j + 32] = y1;
+        }
+      }
+    }
+  }
+}
+
 template <typename TO, int BM, int BN, int NS, bool AK, bool BKC, int WM, int WN, bool GN>
 __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   constexpr int BK = 32;  // two MFMA k steps per tile
@@ -1009,6 +1100,12 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   // next to the accumulators.
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t row0 = m0 + wm * WTM + 4 * lhalf, col0 = n0 + wn * WTN + lrow;
+  if constexpr (TN == 2) {
+    if (g.qkv.mode) {
+      qkv_tail<TM>(g, acc, row0, n0 + wn * WTN, lrow);
+      return;
+    }
+  }
   if constexpr (TN % 2 == 0 && !GN) {
     if (g.swiglu) {
       // Fragments (i, 2 jp) and (i, 2 jp + 1) are the gate and up columns of
@@ -1211,6 +1308,7 @@ struct Plan {
   int64_t sa2 = 0, sb2 = 0, sc2 = 0;  // group strides
   int64_t kb = 0;  // direct BF16 kernel: B's k extent when A's k repeats it (see GemmArgs)
   int swiglu = 0;  // direct BF16 kernel: gate|up pairs into silu(gate) * up (see GemmArgs)
+  QkvTail qkv;     // direct BF16 kernel: the q|k|v tail (see QkvTail)
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1259,6 +1357,7 @@ static hipError_t launch_pipe_cfg(const Plan &p, hipStream_t st) {
   g.bias = p.bias; g.resid = p.resid; g.ldr = p.ldr;
   g.kb = p.kb;
   g.swiglu = p.swiglu;
+  g.qkv = p.qkv;
   g.tiles_m = static_cast<int>(p.M / BM);
   g.tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n), static_cast<unsigned>(p.batch));
@@ -1387,6 +1486,7 @@ static hipError_t run_split(const Plan &p, hipStream_t st) {
   return launch_split_orient<SA, SB, TO, 64, 64, 2, 2, true>(p, st);
 }
 
+static bool parts_small_tiles(const Plan &p);
 template <typename TO>
 static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   using T = uint16_t;
@@ -1398,6 +1498,18 @@ static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   // stages of k 32 either way.
   if (tiles_exactly(p, 256, 256, 32, 8) && tiles(256, 256) >= 192) return launch_pipe<TO, 256, 256, 5, 2, 4>(p, st);
   if (tiles_exactly(p, 128, 128, 32, 8) && tiles(128, 128) >= 16) return launch_pipe<TO, 128, 128, 5, 2, 2>(p, st);
+  // Widths of 16s that the tiles do not divide, against a k-contiguous B (a
+  // weight stored [n, k]): the direct kernel's edge tiles, where its rows and
+  // k tile, over at least 128 tiles of 128 x 128 (a batch-32 prefill's o,
+  // down and q|k|v products at 576 and 960 columns: the performance-contract
+  // prefill 12.1 -> 11.3 ms; at 512 rows the 64 x 64 register tiles stay
+  // ahead, 2.36 against 2.56 ms for that prefill).
+  if (p.batch == 1 && !p.ta && p.tb && p.N % 16 == 0 && p.M % 128 == 0 && p.K % 32 == 0 && p.lda % 8 == 0 &&
+      p.ldb % 8 == 0 && !(reinterpret_cast<uintptr_t>(p.a) & 15) && !(reinterpret_cast<uintptr_t>(p.b) & 15) &&
+      tiles(128, 128) >= 128) {
+    if (!parts_small_tiles(p)) return launch_pipe_edge<TO, 256, 256, 5, 2, 4>(p, st);
+    return launch_pipe_edge<TO, 128, 128, 5, 2, 2>(p, st);
+  }
   if (tiles_exactly(p, 64, 64, 64, 8))
     return launch_orient<T, T, T, TO, 64, 64, 2, 2, false>(p, st);
   return launch_orient<T, T, T, TO, 64, 64, 2, 2, true>(p, st);
@@ -1671,6 +1783,20 @@ static bool parts_small_tiles(const Plan &p) {
 // The product of plan p (A F32 [M, K]) from A's parts at `parts` ([M, 2 K]
 // BF16: each row's heads, then its remainders) on the direct kernel, B's k
 // wrapping every K.
+// A BF16 x BF16 product on the direct kernel, tiled as parts_small_tiles
+// and parts_direct_fits plan it.
+static hipError_t launch_direct(const Plan &q, hipStream_t st) {
+  const bool bf = q.eo == MI_BF16;
+  if (parts_small_tiles(q)) {
+    if (q.N % 128 == 0)
+      return bf ? launch_pipe<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe<float, 128, 128, 5, 2, 2>(q, st);
+    return bf ? launch_pipe_edge<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe_edge<float, 128, 128, 5, 2, 2>(q, st);
+  }
+  if (q.N % 256 == 0)
+    return bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe<float, 256, 256, 5, 2, 4>(q, st);
+  return bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, st);
+}
+
 static hipError_t launch_parts(const Plan &p, const void *parts, hipStream_t st) {
   Plan q = p;
   q.a = parts;
@@ -1678,15 +1804,7 @@ static hipError_t launch_parts(const Plan &p, const void *parts, hipStream_t st)
   q.lda = 2 * p.K;
   q.K = 2 * p.K;
   q.kb = p.K;
-  const bool bf = p.eo == MI_BF16;
-  if (parts_small_tiles(p)) {
-    if (p.N % 128 == 0)
-      return bf ? launch_pipe<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe<float, 128, 128, 5, 2, 2>(q, st);
-    return bf ? launch_pipe_edge<uint16_t, 128, 128, 5, 2, 2>(q, st) : launch_pipe_edge<float, 128, 128, 5, 2, 2>(q, st);
-  }
-  if (p.N % 256 == 0)
-    return bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe<float, 256, 256, 5, 2, 4>(q, st);
-  return bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, st);
+  return launch_direct(q, st);
 }
 
 static int run_stacked_split(mi_ctx *ctx, const Plan &p) {
@@ -2058,6 +2176,78 @@ extern "C" int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_ele
   s = check_launch(ctx, "linear_swiglu");
   if (s) { mi_free(ctx, id); return s; }
   *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_linear_qkv_rope_cache(mi_ctx *ctx, mi_id x, int x_parts, mi_id w_qkv, mi_id cos_table,
+                                        mi_id sin_table, int64_t seq, int64_t heads, int64_t kv_heads, int64_t pos0,
+                                        mi_id k_cache, mi_id v_cache, int grouped, mi_id *q_out) {
+  MI_ENTER(ctx);
+  if (!q_out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, X, x);
+  MI_BUF(ctx, W, w_qkv);
+  MI_BUF(ctx, cb, cos_table);
+  MI_BUF(ctx, sb, sin_table);
+  MI_BUF(ctx, kb, k_cache);
+  MI_BUF(ctx, vb, v_cache);
+  if (X->elem != MI_BF16 || W->elem != MI_BF16 || (x_parts && X->cols % 2))
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: x %s [%lld, %lld] (%s) and weight %s, want BF16",
+                elem_name(X->elem), (long long)X->rows, (long long)X->cols, x_parts ? "parts" : "values",
+                elem_name(W->elem));
+  if (cb->elem != MI_F32 || sb->elem != MI_F32 || kb->elem != vb->elem || !elem_float(kb->elem))
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache takes F32 tables and two F32 or two BF16 caches");
+  const int64_t R = X->rows, K = x_parts ? X->cols / 2 : X->cols, D = kb->cols;
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: %lld heads over %lld kv heads", (long long)heads,
+                (long long)kv_heads);
+  const int64_t N = (heads + 2 * kv_heads) * D;
+  if (W->rows != N || W->cols != K)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: weight [%lld, %lld], want [(heads + 2 kv_heads) %lld, %lld]",
+                (long long)W->rows, (long long)W->cols, (long long)D, (long long)K);
+  if (seq < 1 || R % seq)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: %lld rows are not sequences of %lld", (long long)R, (long long)seq);
+  const int64_t batch = R / seq;
+  if (vb->cols != D || vb->rows != kb->rows || kb->rows % (batch * kv_heads))
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: caches must both be [%lld * %lld * max_ctx, %lld]",
+                (long long)batch, (long long)kv_heads, (long long)D);
+  const int64_t maxc = kb->rows / (batch * kv_heads);
+  if (pos0 < 0 || pos0 + seq > maxc)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: positions [%lld, %lld) beyond the cache's %lld", (long long)pos0,
+                (long long)(pos0 + seq), (long long)maxc);
+  if (cb->cols != D || sb->cols != D || cb->rows != sb->rows || pos0 + seq > cb->rows)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: rope tables [%lld, %lld] for positions below %lld",
+                (long long)cb->rows, (long long)cb->cols, (long long)(pos0 + seq));
+  Plan p;
+  p.ta = false; p.tb = true;
+  p.fast = true;
+  p.ea = x_parts ? MI_F32 : MI_BF16; p.eb = MI_BF16; p.eo = MI_F32;
+  p.a = X->ptr; p.b = W->ptr; p.c = nullptr;
+  p.M = R; p.K = K; p.N = N;
+  p.batch = 1; p.sa = p.sb = p.sc = 0;
+  p.lda = X->cols; p.ldb = W->cols;
+  if (D != 64 || R < 1 || !parts_direct_fits(p) || (reinterpret_cast<uintptr_t>(X->ptr) & 15))
+    return fail(ctx, MI_E_UNSUPPORTED, "linear_qkv_rope_cache: [%lld, %lld] x [%lld, %lld], head width %lld (64-wide "
+                "heads, rows a multiple of 128, k of 32)", (long long)R, (long long)K, (long long)N, (long long)K,
+                (long long)D);
+  mi_id id; Buffer *ob;
+  int s = new_buffer(ctx, R * heads, D, MI_F32, &id, &ob);
+  if (s) return s;
+  p.qkv.mode = kb->elem == MI_BF16 ? QKV_BF16 : QKV_F32;
+  p.qkv.cos = static_cast<const float *>(cb->ptr);
+  p.qkv.sin = static_cast<const float *>(sb->ptr);
+  p.qkv.q = static_cast<float *>(ob->ptr);
+  p.qkv.kc = kb->ptr;
+  p.qkv.vc = vb->ptr;
+  p.qkv.seq = seq; p.qkv.pos0 = pos0; p.qkv.maxc = maxc;
+  p.qkv.heads = static_cast<int>(heads); p.qkv.kvh = static_cast<int>(kv_heads); p.qkv.grouped = grouped != 0;
+  const hipError_t e = x_parts ? launch_parts(p, X->ptr, ctx->stream) : launch_direct(p, ctx->stream);
+  if (e != hipSuccess) {
+    mi_free(ctx, id);
+    return fail(ctx, MI_E_HIP, "linear_qkv_rope_cache launch: %s", hipGetErrorString(e));
+  }
+  s = check_launch(ctx, "linear_qkv_rope_cache");
+  if (s) { mi_free(ctx, id); return s; }
+  *q_out = id;
   return MI_OK;
 }
 

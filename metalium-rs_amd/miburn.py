@@ -105,6 +105,7 @@ def _load() -> ctypes.CDLL:
         "mi_linear_parts": [P, U64, U64, c_int, U64, U64, c_int, Ip],
         "mi_linear_swiglu_parts": [P, U64, U64, Ip],
         "mi_linear_swiglu": [P, U64, U64, c_int, Ip],
+        "mi_linear_qkv_rope_cache": [P, U64, c_int, U64, U64, U64, I64, I64, I64, I64, U64, U64, c_int, Ip],
         "mi_matmul_slices": [P, U64, c_int, U64, c_int, Ip, ctypes.POINTER(I64)],
         "mi_matmul_items": [P, U64, c_int, ctypes.POINTER(I64), U64, c_int, ctypes.POINTER(I64), I64, I64, I64, I64,
                             I64, U64, ctypes.POINTER(I64)],
@@ -309,6 +310,13 @@ class Engine:
         """silu(x gate^T) * (x up^T) from BF16 activations and the interleaved
         gate|up weight, F32 or rounded to BF16."""
         return self._out(self._lib.mi_linear_swiglu, x, w_pairs, out_elem)
+
+    def linear_qkv_rope_cache(self, x: int, x_parts: bool, w_qkv: int, cos: int, sin: int, seq: int, heads: int,
+                              kv_heads: int, pos0: int, k_cache: int, v_cache: int, grouped: bool = False) -> int:
+        """The q|k|v product (BF16 activations, or an F32 operand's parts) and
+        qkv_rope_cache in one launch; returns q."""
+        return self._out(self._lib.mi_linear_qkv_rope_cache, x, int(x_parts), w_qkv, cos, sin, seq, heads, kv_heads,
+                         pos0, k_cache, v_cache, int(grouped))
 
     def log_softmax_ce(self, logits: int, targets: int, grad_scale: float):
         """(picked, dlogits): logp at each row's target and the cross-entropy

@@ -13,7 +13,8 @@ and within the F32 bound of float64 on the other shapes; the parts that
 mi_rms_norm and mi_silu_mul_halves produce are bit for bit the split of
 their F32 results (the split restated here in numpy and checked on
 hand-worked values); mi_linear_swiglu_parts is bit for bit that product
-against [gate; up] followed by the SiLU-mul to parts.
+against [gate; up] followed by the SiLU-mul to parts, mi_linear_qkv_rope_cache
+the q|k|v product followed by mi_qkv_rope_cache (q and both caches).
 
 mi_matmul_items (grouped strided items written in place): each item within
 the F32 accumulation bound of the oracle's product of the same blocks, the
@@ -267,6 +268,62 @@ def test_linear_swiglu_equals_composition(engine, m, k, inter, out):
     got = engine.download(engine.linear_swiglu(ix, engine.upload_bf16(pairs_of(gu, inter)), oe))
     assert got.shape == (m, inter)
     same_bits(got, want, np.uint16 if oe == BF16 else np.uint32)
+
+
+QKV_CASES = [  # (batch, seq, heads, kv heads, hidden, pos0, grouped, cache)
+    (32, 512, 9, 3, 576, 0, False, "f32"),   # the SmolLM2 batch-32 prompt: 256 x 256 tiles, an edge tile column
+    (8, 512, 9, 3, 576, 0, True, "bf16"),    # 4096 rows, grouped queries, a BF16 cache
+    (2, 256, 4, 2, 256, 64, False, "f32"),   # 512 rows on 128 x 128 tiles, positions after cached ones
+]
+
+
+@pytest.mark.parametrize("batch,seq,heads,kvh,hidden,pos0,grouped,cache", QKV_CASES)
+@pytest.mark.parametrize("parts", [True, False])
+def test_linear_qkv_rope_cache_equals_composition(engine, batch, seq, heads, kvh, hidden, pos0, grouped, cache, parts):
+    """The q|k|v product with RoPE, cache writes and q's layout in its
+    epilogue: q and both caches (every row, the untouched ones included) bit
+    for bit the product followed by mi_qkv_rope_cache."""
+    D, maxc = 64, pos0 + seq + 32
+    rows = batch * seq
+    n = (heads + 2 * kvh) * D
+    x = rnd(rows, hidden)
+    w = engine.upload_bf16(orc.to_bf16(rnd(n, hidden, scale=0.05)))
+    ang = np.arange(maxc)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], 1).astype(np.float32)
+    sin = np.concatenate([-np.sin(ang), np.sin(ang)], 1).astype(np.float32)
+    ic, is_ = engine.upload(cos), engine.upload(sin)
+    if parts:
+        ix = engine.upload_bf16(split_parts(x))
+        qkv = engine.linear_parts(ix, w, True)
+    else:
+        ix = engine.upload_bf16(orc.to_bf16(x))
+        qkv = engine.matmul_dram(ix, False, w, True)
+    init = rnd(batch * kvh * maxc, D)
+    def caches():
+        if cache == "bf16":
+            return engine.upload_bf16(orc.to_bf16(init)), engine.upload_bf16(orc.to_bf16(init))
+        return engine.upload(init), engine.upload(init)
+    k1, v1 = caches()
+    q1 = engine.download(engine.qkv_rope_cache(qkv, ic, is_, seq, heads, kvh, pos0, k1, v1, grouped))
+    k2, v2 = caches()
+    q2 = engine.download(engine.linear_qkv_rope_cache(ix, parts, w, ic, is_, seq, heads, kvh, pos0, k2, v2, grouped))
+    same_bits(q2, q1)
+    view = np.uint16 if cache == "bf16" else np.uint32
+    same_bits(engine.download(k2), engine.download(k1), view)
+    same_bits(engine.download(v2), engine.download(v1), view)
+
+
+def test_linear_qkv_rope_cache_refuses(engine):
+    w = engine.upload_bf16(orc.to_bf16(rnd(8 * 64, 128)))
+    ic = engine.upload(rnd(64, 64))
+    k, v = engine.upload(rnd(2 * 2 * 64, 64)), engine.upload(rnd(2 * 2 * 64, 64))
+    with pytest.raises(miburn.MiError) as e:  # 100 rows: not whole 128-row tiles
+        engine.linear_qkv_rope_cache(engine.upload_bf16(orc.to_bf16(rnd(100, 128))), False, w, ic, ic, 50, 4, 2, 0, k, v)
+    assert e.value.kind == "UNSUPPORTED"
+    with pytest.raises(miburn.MiError) as e:  # the weight's rows are not (heads + 2 kv heads) x 64
+        engine.linear_qkv_rope_cache(engine.upload_bf16(orc.to_bf16(rnd(128, 128))), False, w, ic, ic, 64, 2, 1, 0,
+                                     k, v)
+    assert e.value.kind == "ARG"
 
 
 def test_linear_swiglu_parts_refuses_partial_tiles(engine):

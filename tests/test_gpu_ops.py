@@ -562,6 +562,28 @@ def test_matmul_mixed_stacked_split(engine, mode, mnk):
     same_bits(got, (res + (want + bias)).astype(np.float32))
 
 
+@pytest.mark.parametrize("mnk", [(4096, 576, 1536), (16384, 960, 576), (16384, 576, 576)])
+def test_matmul_bf16_edge_tiles(engine, mnk):
+    """BF16 x BF16 [n, k] products whose width the tiles do not divide (the
+    performance contract's prefill products): the direct kernel's edge tiles
+    (128 x 128 at 4096 rows, 256 x 256 at 16384), small integers bit for bit
+    against float64, random operands within the F32 bound of the oracle fed
+    the same BF16 values, and a linear layer's residual bit for bit."""
+    m, n, k = mnk
+    ai = orc.to_bf16(RNG.integers(-8, 9, (m, k)).astype(np.float32))
+    bi = orc.to_bf16(RNG.integers(-8, 9, (n, k)).astype(np.float32))
+    got = engine.download(engine.matmul_dram(engine.upload_bf16(ai), False, engine.upload_bf16(bi), True))
+    want = (orc.from_bf16(ai).astype(np.float64) @ orc.from_bf16(bi).astype(np.float64).T).astype(np.float32)
+    same_bits(got, want)
+    res = rnd(m, n)
+    got = engine.download(engine.linear(engine.upload_bf16(ai), engine.upload_bf16(bi), True, 0, engine.upload(res)))
+    same_bits(got, (res + want).astype(np.float32))
+    a, b = orc.to_bf16(rnd(m, k)), orc.to_bf16(rnd(n, k))
+    af, bf = orc.from_bf16(a), orc.from_bf16(b)
+    got = engine.download(engine.matmul_dram(engine.upload_bf16(a), False, engine.upload_bf16(b), True))
+    assert np.all(np.abs(got - orc.matmul(af, bf, False, True, threads=16)) <= mm_tol(af, bf, False, True, 1e-5) + 1e-30)
+
+
 def test_matmul_fast_split_keeps_large_finite_values(engine, mode):
     """Values near FLT_MAX stay finite through the split (the BF16 head of a
     value above the largest BF16 would round to infinity, so it is truncated).
