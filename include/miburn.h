@@ -385,6 +385,14 @@ int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out);
  * bits; `idx` an I32 buffer of any dims, read in row-major order.  An index
  * outside `[0, table rows)` is an MI_E_DOMAIN failure. */
 int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out);
+/* mi_select_rows then mi_cast to `out_elem` (F32 or BF16) in one call: a
+ * BF16 table's rows are widened as they are gathered (one launch; rows of a
+ * multiple of 8 columns), other pairs run the two ops.  The gathered values
+ * are those of the two ops.  No Engine counterpart (the reference's
+ * embedding is the gather then a cast of the rows to the stream's dtype,
+ * crates/tt-models/src/llama.rs:756-764). */
+int mi_select_rows_as(mi_ctx *ctx, mi_id table, mi_id idx, int out_elem,
+                      mi_id *out);
 /* Engine::pick_columns (server.rs:349): `out[r] = x[r, idx[r]]`, raw bits,
  * `[r, 1]`. */
 int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out);

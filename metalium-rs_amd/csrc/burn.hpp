@@ -376,6 +376,17 @@ inline Tensor select_rows(const Tensor &table, const Tensor &idx) {
   return Tensor(table.ctx(), id, shape);
 }
 
+// select_rows then float_cast to out_elem (mi_select_rows_as: one launch for
+// a BF16 table widened to F32).
+inline Tensor select_rows_as(const Tensor &table, const Tensor &idx, int out_elem) {
+  mi_id id;
+  check(table.ctx(), mi_select_rows_as(table.ctx(), table.use(), idx.use(), out_elem, &id), "select_rows_as");
+  std::vector<int64_t> shape = idx.shape();
+  if (shape.size() >= 2 && shape.back() == 1) shape.pop_back();
+  shape.push_back(table.cols());
+  return Tensor(table.ctx(), id, shape);
+}
+
 inline Tensor pick_columns(const Tensor &x, const Tensor &idx) {
   mi_id id;
   check(x.ctx(), mi_pick_columns(x.ctx(), x.use(), idx.use(), &id), "pick_columns");

@@ -141,6 +141,36 @@ __global__ void __launch_bounds__(1024) sort_pairs_block(const int32_t *idx, int
   }
 }
 
+// BF16 table rows gathered and widened to F32 (exact) in one pass: a wave a
+// row, eight columns a lane per access; an index outside the table raises
+// the range flag and gives a zero row, as select_rows_kernel does.
+__global__ void __launch_bounds__(256) select_rows_widen_kernel(const uint16_t *table, int64_t vrows, int64_t cols,
+                                                                const int32_t *idx, int64_t n, float *out,
+                                                                uint32_t *flags) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t waves = (static_cast<int64_t>(gridDim.x) * blockDim.x) >> 6;
+  for (int64_t i = wave; i < n; i += waves) {
+    const int32_t r = idx[i];
+    float *dst = out + i * cols;
+    if (r < 0 || r >= vrows) {
+      if (lane == 0) atomicOr(flags, FLAG_INDEX_RANGE);
+      for (int64_t j = lane; j < cols; j += 64) dst[j] = 0.0f;
+      continue;
+    }
+    const uint16_t *src = table + static_cast<int64_t>(r) * cols;
+    for (int64_t j = 8 * lane; j < cols; j += 512) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(src + j);
+      *reinterpret_cast<float4 *>(dst + j) = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                                                         __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+      *reinterpret_cast<float4 *>(dst + j + 4) = make_float4(__uint_as_float(u.z << 16),
+                                                             __uint_as_float(u.z & 0xffff0000u),
+                                                             __uint_as_float(u.w << 16),
+                                                             __uint_as_float(u.w & 0xffff0000u));
+    }
+  }
+}
+
 // --------------------------------------------------------------- argmax
 struct ArgBest { float v; int32_t i; };
 __device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
@@ -278,6 +308,39 @@ extern "C" int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out) {
   }
   *out = id;
   return MI_OK;
+}
+
+extern "C" int mi_select_rows_as(mi_ctx *ctx, mi_id table, mi_id idx, int out_elem, mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, t, table);
+  MI_BUF(ctx, ix, idx);
+  if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "select_rows_as indices are %s, not I32", elem_name(ix->elem));
+  if (!elem_float(t->elem) || (out_elem != MI_F32 && out_elem != MI_BF16))
+    return fail(ctx, MI_E_ARG, "select_rows_as of a %s table to %d", elem_name(t->elem), out_elem);
+  const int64_t n = ix->numel(), D = t->cols;
+  if (out_elem == t->elem) return mi_select_rows(ctx, table, idx, out);
+  if (t->elem == MI_BF16 && D % 8 == 0 && n > 0) {
+    // BF16 rows widened (exactly) as they are gathered: one launch.
+    mi_id id; Buffer *ob;
+    int s = new_buffer(ctx, n, D, MI_F32, &id, &ob);
+    if (s) return s;
+    const unsigned g = grid_for(n, 4, 256 * 64);
+    select_rows_widen_kernel<<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(t->ptr), t->rows, D,
+                                                          static_cast<const int32_t *>(ix->ptr), n,
+                                                          static_cast<float *>(ob->ptr), flags(ctx));
+    s = check_launch(ctx, "select_rows_as");
+    if (s) { mi_free(ctx, id); return s; }
+    *out = id;
+    return MI_OK;
+  }
+  // Any other pair: the gather, then the cast.
+  mi_id g;
+  int s = mi_select_rows(ctx, table, idx, &g);
+  if (s) return s;
+  s = mi_cast(ctx, g, out_elem, out);
+  mi_free(ctx, g);
+  return s;
 }
 
 extern "C" int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out) {

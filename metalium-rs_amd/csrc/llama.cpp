@@ -181,7 +181,7 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
 
   // The element type of a prefill product's activation operand.
   const int act = c.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
-  Tensor x = burn::float_cast(burn::select_rows(m->embed, idx), MI_F32);  // [rows, hidden]
+  Tensor x = burn::select_rows_as(m->embed, idx, MI_F32);  // [rows, hidden], the BF16 rows widened
   x = x.reshape({rows, c.hidden});
 
   // A few new positions (decode) take the fused attention kernel, and so does
@@ -524,7 +524,7 @@ StepTrace &step_trace(mi_llama *m, int64_t batch, int64_t span) {
   burn::check(ctx, mi_trace_begin(ctx), "trace_begin");
   StepTrace st;
   try {
-    Tensor x = burn::float_cast(burn::select_rows(m->embed, m->step_ids.reshape({batch})), MI_F32);
+    Tensor x = burn::select_rows_as(m->embed, m->step_ids.reshape({batch}), MI_F32);
     x = decode_layers(m, x.reshape({batch, m->cfg.hidden}), batch, &m->step_pos, 0, span);
     st.next = burn::argmax_rows(head_last(m, x, batch, 1));
   } catch (...) {

@@ -146,6 +146,7 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into": [P, U64, U64],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
+        "mi_select_rows_as": [P, U64, U64, c_int, Ip],
         "mi_pick_columns": [P, U64, U64, Ip],
         "mi_scatter_add_columns": [P, U64, U64, U64, Ip],
         "mi_select_add_rows": [P, U64, U64, U64, Ip],
@@ -513,6 +514,10 @@ class Engine:
 
     def select_rows(self, table: int, idx: int) -> int:
         return self._out(self._lib.mi_select_rows, table, idx)
+
+    def select_rows_as(self, table: int, idx: int, out_elem: int) -> int:
+        """select_rows then the cast to out_elem, in one launch for BF16 rows widened to F32."""
+        return self._out(self._lib.mi_select_rows_as, table, idx, out_elem)
 
     def pick_columns(self, x: int, idx: int) -> int:
         return self._out(self._lib.mi_pick_columns, x, idx)

@@ -775,9 +775,42 @@ def test_argmax_first_and_nan(engine, cols):
     assert got[1, 0] == 5 and got[2, 0] == 7 and got[3, 0] == 0
 
 
-def test_argmax_vocab_rows(engine):
-    x = rnd(32, 49152)
-    assert np.array_equal(engine.download(engine.argmax_row(engine.upload(x))), orc.argmax_rows(x))
+@pytest.mark.parametrize("rows", [32, 100])  # column chunks and their fold
+def test_argmax_vocab_rows(engine, rows):
+    x = rnd(rows, 49152)
+    x[rows - 1, 30000] = x[rows - 1, 20000] = 60.0  # a tie across chunks: the first wins
+    x[0, 45000] = np.nan
+    got = engine.download(engine.argmax_row(engine.upload(x)))
+    assert np.array_equal(got, orc.argmax_rows(x))
+    assert got[rows - 1, 0] == 20000 and got[0, 0] == 45000
+
+
+@pytest.mark.parametrize("n,cols", [(1, 576), (32, 576), (5, 12)])
+def test_select_rows_as_equals_gather_then_cast(engine, n, cols):
+    """The gather with its cast: BF16 rows widened in one launch (widths of
+    8s), other pairs through the two ops -- bit for bit select_rows then
+    cast either way."""
+    tb = orc.to_bf16(rnd(300, cols))
+    idx = RNG.integers(0, 300, n).astype(np.int32)
+    it, ii = engine.upload_bf16(tb), engine.upload_i32(idx)
+    want = engine.download(engine.cast_float(engine.select_rows(it, ii), miburn.F32))
+    got = engine.download(engine.select_rows_as(it, ii, miburn.F32))
+    assert got.dtype == np.float32 and got.shape == want.shape
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got, orc.from_bf16(tb[idx]))
+    tf = rnd(300, cols)
+    got = engine.download(engine.select_rows_as(engine.upload(tf), ii, miburn.BF16))
+    assert np.array_equal(got, orc.to_bf16(tf[idx]))
+
+
+def test_select_rows_as_out_of_range_is_domain(engine):
+    engine.sync()
+    it = engine.upload_bf16(orc.to_bf16(rnd(10, 64)))
+    engine.select_rows_as(it, engine.upload_i32(np.array([3, 10], np.int32)), miburn.F32)  # deferred
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    engine.sync()
 
 
 def test_argmax_bf16_long_rows(engine):
