@@ -681,6 +681,7 @@ struct DqaArgs {
   float scale;
   float *q;     // [B, H 64] rotated queries, for the combine
   float *part;  // [B KVH][S][G (64 + 2)] chunk partials
+  float *kvn;   // [B KVH][2][64] the new key and value rows as stored, for the combine
 };
 
 // Block (256 threads): 64 rows (w0, each K BF16) times the staged row in
@@ -792,8 +793,7 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
   float *snew = den + G;
   float *wnew = snew + G;
   // A thread's output elements e = tid + 256 i (G D <= 512): their first CS
-  // chunks' values, requested with the statistics before the position (read
-  // on the device, a traced step's) that the new rows' loads wait for; one
+  // chunks' values, requested with the statistics and the new rows; one
   // round trip for all but very long contexts.
   constexpr int EP = 2, CS = 16;
   float ov[EP][CS], vd[EP];
@@ -813,22 +813,15 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
     qv[u] = g.q[(b * g.H + j * G + (gg < G ? gg : 0)) * D + lane];
   }
   for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
-  int64_t pos = g.pa.pos0;
-  if (g.pa.dev) {
-    const int64_t v = *g.pa.dev;
-    pos = v >= 0 && v + 1 <= g.pa.span ? v : 0;
-  }
-  const KV *kn = static_cast<const KV *>(g.kc) + (bj * g.maxc + pos) * D;
-  const KV *vn = static_cast<const KV *>(g.vc) + (bj * g.maxc + pos) * D;
+  // The new key and value rows as the cache holds them, from where the
+  // launch's key/value blocks left them: no position read before them.
+  const float *kn = g.kvn + bj * 2 * D, *vn = kn + D;
 #pragma unroll
   for (int i = 0; i < EP; ++i) {
     const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
-    if constexpr (sizeof(KV) == 2) vd[i] = bf16_bits_to_f32(vn[ec % D]);
-    else vd[i] = vn[ec % D];
+    vd[i] = vn[ec % D];
   }
-  float kd;
-  if constexpr (sizeof(KV) == 2) kd = bf16_bits_to_f32(kn[lane]);
-  else kd = kn[lane];
+  const float kd = kn[lane];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int gg = wave + 4 * u;
@@ -909,12 +902,20 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     __syncthreads();
     if (!ok) return bj;  // refused position: no cache row (flag raised by the chunk blocks)
     KV *dst = static_cast<KV *>(which ? g.vc : g.kc) + (bj * g.maxc + pos) * D;
+    // The row as the cache holds it, also where the combine reads it
+    // without the position.
+    auto put = [&](float y) {
+      f32_put(dst + tid, y);
+      float held = y;
+      if constexpr (sizeof(KV) == 2) held = bf16_bits_to_f32(f32_to_bf16_bits(y));
+      g.kvn[(bj * 2 + which) * D + tid] = held;
+    };
     if (which == 0) {
       dqa_rope(pre, qraw, qrot);
       __syncthreads();
-      if (tid < D) f32_put(dst + tid, qrot[tid]);
+      if (tid < D) put(qrot[tid]);
     } else if (tid < D) {
-      f32_put(dst + tid, qraw[tid]);
+      put(qraw[tid]);
     }
     return bj;
   }
@@ -1388,7 +1389,8 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   if (static_cast<size_t>(3 * G * S + 3 * G) * sizeof(float) > 65536 || B * heads * S + 2 * items > INT32_MAX)
     return fail(ctx, MI_E_UNSUPPORTED, "norm_qkv_attention: context of %lld keys too long", (long long)span);
   const size_t part_floats = static_cast<size_t>(items * S * G * (D + 2));
-  float *sc = static_cast<float *>(mi::scratch(ctx, (part_floats + static_cast<size_t>(B * heads * D)) * sizeof(float)));
+  const size_t q_floats = static_cast<size_t>(B * heads * D), kvn_floats = static_cast<size_t>(items * 2 * D);
+  float *sc = static_cast<float *>(mi::scratch(ctx, (part_floats + q_floats + kvn_floats) * sizeof(float)));
   if (!sc) return fail(ctx, MI_E_OOM, "norm_qkv_attention scratch");
   mi_id id;
   Buffer *ob;
@@ -1415,6 +1417,7 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   g.scale = scale;
   g.part = sc;
   g.q = sc + part_floats;
+  g.kvn = g.q + q_floats;
   float *o = static_cast<float *>(ob->ptr);
   if (kb->elem == MI_BF16) launch_dqa<uint16_t>(ctx->stream, g, o);
   else launch_dqa<float>(ctx->stream, g, o);
