@@ -19,13 +19,23 @@ reference's models compute, op by op, with torch's float32 CPU kernels:
   `llama_step` (incremental, with a KV cache), `llama_generate`.
 
 How they are pinned (tests/test_oracle_models.py, CPU): every op is a torch
-library routine; the compositions are checked against invariants the models
-fix -- incremental decoding through the KV cache equals the full-sequence
-forward position by position, causality (a later token never changes an
-earlier position's logits), RoPE turning each (i, i + d/2) pair by the angle
-pos * theta^(-2i/d) (norms kept, relative rotation of two positions depends on
-their distance only), the first-maximum / NaN rule of greedy argmax, and the
-training losses' gradients against central differences in float64.
+library routine, and each model's forward is checked against an independent
+implementation of the same architecture with the same weights copied in --
+the Llama decoder against Hugging Face `transformers`' LlamaForCausalLM (the
+implementation the reference pins its own host model against,
+crates/tt-tests/tests/step167_smollm2.rs:4-7, crates/tt-models/tests/
+llama_host.rs:1-3), the transformer against torch.nn.TransformerEncoderLayer
+(norm_first, GELU, no dropout: burn-nn's TransformerEncoderConfig
+.with_norm_first(true).with_dropout(0.0), transformer.rs:44-52), the MLP
+against torch.nn.Linear / ReLU / CrossEntropyLoss and torch.optim.SGD.  The
+attention scale, the feed-forward activation and SwiGLU are module-level
+functions (`score_divisor`, `ffn_activation`, `swiglu`), so the tests plant a
+wrong scale, ReLU for GELU or gate and up swapped and show each caught.  On
+top of that, invariants the models fix: incremental decoding through the KV
+cache equals the full-sequence forward position by position, causality,
+RoPE turning each (i, i + d/2) pair by the angle pos * theta^(-2i/d), the
+first-maximum / NaN rule of greedy argmax, and the training losses'
+gradients against central differences in float64.
 """
 from __future__ import annotations
 
@@ -34,6 +44,28 @@ import time
 
 import numpy as np
 import torch
+
+# ------------------------------------------------ shared model pieces
+
+
+def score_divisor(head_dim):
+    """Attention scores are q.k / sqrt(d_head): Burn's default scale
+    1/sqrt(d_head) (crates/burn-tt/src/ops.rs:4481), the one burn-nn's
+    MultiHeadAttention and the Llama attention use."""
+    return math.sqrt(head_dim)
+
+
+def ffn_activation(x):
+    """burn-nn's PositionWiseFeedForward activation in the transformer:
+    erf GELU 0.5 x (1 + erf(x / sqrt 2)) (crates/burn-tt/src/ops.rs:5297-5301)."""
+    return torch.nn.functional.gelu(x)
+
+
+def swiglu(hn, L):
+    """Llama MLP's SwiGLU: silu(x Wgate^T) * (x Wup^T), the gate through SiLU
+    (crates/tt-models/src/llama.rs:482-500)."""
+    return torch.nn.functional.silu(hn @ L["wgate"].T) * (hn @ L["wup"].T)
+
 
 # ----------------------------------------------------------------- MLP
 
@@ -79,11 +111,11 @@ def transformer_loss(P, layers, cfg, tokens, targets):
     for L in layers:
         n1 = ln(x, L["ln1_g"], L["ln1_b"])
         q, k, v = (heads(n1 @ L[w] + L[b]) for w, b in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
-        s = (q @ k.transpose(-1, -2).contiguous()) / math.sqrt(dk)
+        s = (q @ k.transpose(-1, -2).contiguous()) / score_divisor(dk)
         o = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B * S, d)
         x = x + o @ L["wo"] + L["bo"]
         n2 = ln(x, L["ln2_g"], L["ln2_b"])
-        x = x + torch.nn.functional.gelu(n2 @ L["w1"] + L["b1"]) @ L["w2"] + L["b2"]
+        x = x + ffn_activation(n2 @ L["w1"] + L["b1"]) @ L["w2"] + L["b2"]
     z = x @ P["head_w"] + P["head_b"]
     return torch.nn.functional.cross_entropy(z, torch.as_tensor(np.asarray(targets).reshape(-1), dtype=torch.int64))
 
@@ -153,12 +185,12 @@ def llama_hidden(W, cfg, ids):
         q = _rope((xn @ L["wq"].T).reshape(B, T, H, D), cos, sin, D)
         k = _rope((xn @ L["wk"].T).reshape(B, T, KVH, D), cos, sin, D).repeat_interleave(G, dim=2)
         v = (xn @ L["wv"].T).reshape(B, T, KVH, D).repeat_interleave(G, dim=2)
-        s = torch.einsum("bthd,bshd->bhts", q, k) / np.sqrt(D)
+        s = torch.einsum("bthd,bshd->bhts", q, k) / score_divisor(D)
         p = torch.softmax(s.masked_fill(causal, float("-inf")), -1)
         o = torch.einsum("bhts,bshd->bthd", p, v).reshape(B, T, H * D)
         x = x + o @ L["wo"].T
         hn = _rms(x, L["mlp_norm"], eps)
-        x = x + (torch.nn.functional.silu(hn @ L["wgate"].T) * (hn @ L["wup"].T)) @ L["wdown"].T
+        x = x + swiglu(hn, L) @ L["wdown"].T
     return _rms(x, W["final_norm"], eps)
 
 
@@ -202,12 +234,12 @@ def llama_step(W, cfg, cache, ids):
         # of a kv head stacked over its rows: [B, KVH, G t, D] against the
         # cache's [B, KVH, n, D], no copy of the cache.
         qg = q.reshape(B, t, KVH, G, D).permute(0, 2, 3, 1, 4).reshape(B, KVH, G * t, D)
-        s = (qg @ cache.k[li][:, :, :n].transpose(-1, -2)) / np.sqrt(D)  # [B, KVH, G t, n]
+        s = (qg @ cache.k[li][:, :, :n].transpose(-1, -2)) / score_divisor(D)  # [B, KVH, G t, n]
         pr = torch.softmax(s.masked_fill(mask.repeat(G, 1), float("-inf")), -1)
         o = (pr @ cache.v[li][:, :, :n]).reshape(B, KVH, G, t, D).permute(0, 3, 1, 2, 4).reshape(B, t, H * D)
         x = x + o @ L["wo"].T
         hn = _rms(x, L["mlp_norm"], eps)
-        x = x + (torch.nn.functional.silu(hn @ L["wgate"].T) * (hn @ L["wup"].T)) @ L["wdown"].T
+        x = x + swiglu(hn, L) @ L["wdown"].T
     cache.len = n
     return _rms(x, W["final_norm"], eps)
 
