@@ -567,14 +567,20 @@ int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);
  * Memory a capture allocates or frees stays reserved for the trace until it
  * is released, so replays never touch memory handed to other work; buffers
  * the trace reads that existed before the capture must outlive it.  A replay
- * overwrites each input buffer with the host bytes given (its whole size),
- * launches the graph and reads each output buffer back whole. ---- */
+ * overwrites each input buffer with the host bytes given, launches the graph
+ * and reads each output buffer back whole.  The host slices' lengths are
+ * passed as the reference passes its slices (`values: &[f32]`, server.rs:
+ * 650-656; the payloads of run_generic_trace, 746-751): value_bytes[i] must
+ * be input i's buffer size in bytes exactly, out_bytes[i] the room at
+ * out_values[i], at least output i's buffer size; any mismatch is MI_E_ARG
+ * before anything is written or launched. ---- */
 int mi_trace_begin(mi_ctx *ctx);
 int mi_trace_end(mi_ctx *ctx, uint64_t *trace);
 int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs,
                  const mi_id *inputs, const void *const *values,
-                 int64_t n_outputs, const mi_id *outputs,
-                 void *const *out_values);
+                 const int64_t *value_bytes, int64_t n_outputs,
+                 const mi_id *outputs, void *const *out_values,
+                 const int64_t *out_bytes);
 int mi_trace_release(mi_ctx *ctx, uint64_t trace);
 /* Engine::copy_into (server.rs:742): src's bytes into dst (equal byte size),
  * no allocation. */

@@ -900,7 +900,19 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
     __syncthreads();
-    if (!ok) return bj;  // refused position: no cache row (flag raised by the chunk blocks)
+    if (!ok) {
+      // Refused position (the chunk blocks raise the flag): no cache row is
+      // written, and the step attends from position 0, so the combine's new
+      // row is the cache's row at position 0 as stored.
+      const KV *row0 = static_cast<const KV *>(which ? g.vc : g.kc) + bj * g.maxc * D;
+      if (tid < D) {
+        float held;
+        if constexpr (sizeof(KV) == 2) held = bf16_bits_to_f32(row0[tid]);
+        else held = row0[tid];
+        g.kvn[(bj * 2 + which) * D + tid] = held;
+      }
+      return bj;
+    }
     KV *dst = static_cast<KV *>(which ? g.vc : g.kc) + (bj * g.maxc + pos) * D;
     // The row as the cache holds it, also where the combine reads it
     // without the position.

@@ -593,7 +593,10 @@ extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int3
       const void *in_vals[1] = {prompt};
       const mi_id out_ids[1] = {pt.next.id()};
       void *out_vals[1] = {tok.data()};
-      burn::check(m->ctx, mi_trace_run(m->ctx, pt.id, 1, in_ids, in_vals, 1, out_ids, out_vals), "trace_run");
+      const int64_t in_len[1] = {static_cast<int64_t>(batch) * t_prompt * 4};
+      const int64_t out_len[1] = {static_cast<int64_t>(tok.size()) * 4};
+      burn::check(m->ctx, mi_trace_run(m->ctx, pt.id, 1, in_ids, in_vals, in_len, 1, out_ids, out_vals, out_len),
+                  "trace_run");
       m->len = t_prompt;
     } else {
       Tensor h = forward_hidden(m, prompt, batch, t_prompt);
@@ -611,7 +614,10 @@ extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int3
       const void *in_vals[2] = {tok.data(), &pos};
       const mi_id out_ids[1] = {st.next.id()};
       void *out_vals[1] = {tok.data()};
-      burn::check(m->ctx, mi_trace_run(m->ctx, st.id, 2, in_ids, in_vals, 1, out_ids, out_vals), "trace_run");
+      const int64_t in_len[2] = {static_cast<int64_t>(tok.size()) * 4, 4};
+      const int64_t out_len[1] = {static_cast<int64_t>(tok.size()) * 4};
+      burn::check(m->ctx, mi_trace_run(m->ctx, st.id, 2, in_ids, in_vals, in_len, 1, out_ids, out_vals, out_len),
+                  "trace_run");
       m->len += 1;
       for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
     }

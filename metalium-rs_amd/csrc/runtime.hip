@@ -518,26 +518,45 @@ int mi_trace_end(mi_ctx *ctx, uint64_t *trace) {
 }
 
 int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs, const mi_id *inputs, const void *const *values,
-                 int64_t n_outputs, const mi_id *outputs, void *const *out_values) {
+                 const int64_t *value_bytes, int64_t n_outputs, const mi_id *outputs, void *const *out_values,
+                 const int64_t *out_bytes) {
   MI_ENTER(ctx);
   if (int r = refuse_if_capturing(ctx, "trace replay")) return r;
   auto it = ctx->traces.find(trace);
   if (it == ctx->traces.end() || !it->second.exec) return fail(ctx, MI_E_ID, "unknown trace %llu", (unsigned long long)trace);
-  if (n_inputs < 0 || n_outputs < 0 || (n_inputs && (!inputs || !values)) || (n_outputs && (!outputs || !out_values)))
+  if (n_inputs < 0 || n_outputs < 0 || (n_inputs && (!inputs || !values || !value_bytes)) ||
+      (n_outputs && (!outputs || !out_values || !out_bytes)))
     return fail(ctx, MI_E_ARG, "trace_run: input or output lists");
+  // Every input's length and every output's room are checked before any
+  // byte is written: an input's host bytes are its buffer's size exactly,
+  // an output's room at least its buffer's size.
   for (int64_t i = 0; i < n_inputs; ++i) {
     MI_BUF(ctx, b, inputs[i]);
+    const int64_t bytes = b->numel() * static_cast<int64_t>(elem_size(b->elem));
     if (!values[i]) return fail(ctx, MI_E_ARG, "trace_run: null values for input %lld", (long long)i);
-    if (int s = write_into(ctx, b, values[i], static_cast<size_t>(b->numel()) * elem_size(b->elem))) return s;
+    if (value_bytes[i] != bytes)
+      return fail(ctx, MI_E_ARG, "trace_run: input %lld is %lld bytes, its buffer %lld", (long long)i,
+                  (long long)value_bytes[i], (long long)bytes);
+  }
+  for (int64_t i = 0; i < n_outputs; ++i) {
+    MI_BUF(ctx, b, outputs[i]);
+    const int64_t bytes = b->numel() * static_cast<int64_t>(elem_size(b->elem));
+    if (!out_values[i]) return fail(ctx, MI_E_ARG, "trace_run: null destination for output %lld", (long long)i);
+    if (out_bytes[i] < bytes)
+      return fail(ctx, MI_E_ARG, "trace_run: output %lld has room for %lld bytes of %lld", (long long)i,
+                  (long long)out_bytes[i], (long long)bytes);
+  }
+  for (int64_t i = 0; i < n_inputs; ++i) {
+    MI_BUF(ctx, b, inputs[i]);
+    if (int s = write_into(ctx, b, values[i], static_cast<size_t>(value_bytes[i]))) return s;
   }
   hipError_t e = hipGraphLaunch(it->second.exec, ctx->stream);
   if (e != hipSuccess) return fail(ctx, MI_E_HIP, "trace launch: %s", hipGetErrorString(e));
   ctx->report.ops++;
   for (int64_t i = 0; i < n_outputs; ++i) {
     MI_BUF(ctx, b, outputs[i]);
-    if (int s = download_raw(ctx, outputs[i], out_values[i], b->numel(), static_cast<int>(elem_size(b->elem)),
-                             "trace output"))
-      return s;
+    const int esz = static_cast<int>(elem_size(b->elem));
+    if (int s = download_raw(ctx, outputs[i], out_values[i], out_bytes[i] / esz, esz, "trace output")) return s;
   }
   return MI_OK;
 }

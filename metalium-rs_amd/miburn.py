@@ -140,8 +140,8 @@ def _load() -> ctypes.CDLL:
         "mi_set_matmul_mode": [P, c_int],
         "mi_trace_begin": [P],
         "mi_trace_end": [P, ctypes.POINTER(U64)],
-        "mi_trace_run": [P, U64, I64, ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p), I64,
-                         ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p)],
+        "mi_trace_run": [P, U64, I64, ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64), I64,
+                         ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64)],
         "mi_trace_release": [P, U64],
         "mi_copy_into": [P, U64, U64],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
@@ -477,21 +477,31 @@ class Engine:
         self._check(self._lib.mi_trace_end(self.ctx, ctypes.byref(t)))
         return t.value
 
-    def run_trace(self, trace: int, inputs=None, outputs=()):
+    def run_trace(self, trace: int, inputs=None, outputs=(), out_arrays=None):
         """Overwrite each input id with its array's bytes, replay, and return
-        the outputs' contents (arrays of each buffer's kind and shape)."""
+        the outputs' contents (arrays of each buffer's kind and shape, or the
+        caller's `out_arrays`).  Each array's byte length goes with it (the
+        library refuses an input whose length is not its buffer's size, or an
+        output array with less room than its buffer)."""
         inputs = inputs or {}
         keep = [np.ascontiguousarray(v) for v in inputs.values()]
         ids_in = (ctypes.c_uint64 * max(len(keep), 1))(*inputs.keys())
         vals_in = (ctypes.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
-        outs = []
-        for o in outputs:
-            r, c, e = self.metadata(o)
-            dt = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}[e]
-            outs.append(np.empty((r, c), dt))
+        lens_in = (ctypes.c_int64 * max(len(keep), 1))(*[k.nbytes for k in keep])
+        if out_arrays is None:
+            outs = []
+            for o in outputs:
+                r, c, e = self.metadata(o)
+                dt = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}[e]
+                outs.append(np.empty((r, c), dt))
+        else:
+            outs = list(out_arrays)
+            assert all(a.flags.c_contiguous for a in outs) and len(outs) == len(outputs)
         ids_out = (ctypes.c_uint64 * max(len(outs), 1))(*outputs)
         vals_out = (ctypes.c_void_p * max(len(outs), 1))(*[a.ctypes.data for a in outs])
-        self._check(self._lib.mi_trace_run(self.ctx, trace, len(keep), ids_in, vals_in, len(outs), ids_out, vals_out))
+        lens_out = (ctypes.c_int64 * max(len(outs), 1))(*[a.nbytes for a in outs])
+        self._check(self._lib.mi_trace_run(self.ctx, trace, len(keep), ids_in, vals_in, lens_in, len(outs), ids_out,
+                                           vals_out, lens_out))
         return outs
 
     def release_trace(self, trace: int) -> None:

@@ -274,6 +274,9 @@ QKV_CASES = [  # (batch, seq, heads, kv heads, hidden, pos0, grouped, cache)
     (32, 512, 9, 3, 576, 0, False, "f32"),   # the SmolLM2 batch-32 prompt: 256 x 256 tiles, an edge tile column
     (8, 512, 9, 3, 576, 0, True, "bf16"),    # 4096 rows, grouped queries, a BF16 cache
     (2, 256, 4, 2, 256, 64, False, "f32"),   # 512 rows on 128 x 128 tiles, positions after cached ones
+    # 4608 rows of 144-token sequences: 32-row fragments straddle two
+    # sequences, so the epilogue finds each row's sequence and position itself
+    (32, 144, 9, 3, 576, 8, True, "bf16"),
 ]
 
 

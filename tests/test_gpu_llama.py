@@ -84,15 +84,29 @@ WIDE = dict(vocab=512, hidden=512, layers=2, heads=8, kv_heads=4, head_dim=64, i
             rope_theta=10000.0, eps=1e-5)
 
 
+@pytest.mark.parametrize("numerics", ["reference", "performance"])
 @pytest.mark.parametrize("batch", [8, 32])  # 4096 rows: 128 x 128 tiles; 16384: 256 x 256
-def test_prefill_logits_with_operand_parts(engine, batch):
-    m = miburn.Llama(engine, WIDE, max_ctx=512, max_batch=batch, seed=11, init_std=0.05)
+def test_prefill_logits_with_operand_parts(engine, batch, numerics):
+    """Under the performance contract the same prompts take, from 4096 rows,
+    mi_linear_qkv_rope_cache and mi_linear_swiglu on BF16 activations: held
+    to the north star's 2e-2 and the contract's 0.995 correlation floor."""
+    m = miburn.Llama(engine, WIDE, max_ctx=512, max_batch=batch, seed=11, init_std=0.05, numerics=numerics)
     W = weights(engine, m, WIDE)
     ids = np.random.default_rng(8).integers(0, WIDE["vocab"], (batch, 512)).astype(np.int32)
     m.reset()
-    got = engine.download(m.forward(ids, all_positions=True)).reshape(batch, 512, -1)
+    lid = m.forward(ids, all_positions=True)
+    got = engine.download(lid).reshape(batch, 512, -1)
+    engine.free(lid)
     m.close()
-    close_logits(got, ref_logits(W, WIDE, ids))
+    want = ref_logits(W, WIDE, ids)
+    if numerics == "reference":
+        close_logits(got, want)
+    else:
+        close_logits(got, want, rel=2e-2)
+        pcc = pcc_rows(got, want)
+        print(f"WIDE performance batch {batch}: max |diff| {np.abs(got - want).max():.3g} of "
+              f"{np.abs(want).max():.3g}; correlation mean {pcc.mean():.6f}")
+        assert pcc.mean() >= 0.995, pcc.mean()
 
 
 @pytest.mark.parametrize("batch", [3, 9])  # fused decode launches; the composition (over 8 sequences)
@@ -209,36 +223,108 @@ def pcc_rows(got, want):
     return (g * w).sum(1) / np.sqrt((g * g).sum(1) * (w * w).sum(1))
 
 
-def check_smol_logits(engine, m, W, batch, label, cover=0.8, min_pcc=0.99999):
+def check_smol_logits(engine, m, W, batch, label, cover=0.8, min_pcc=0.99999, prompt=SMOL_PROMPT,
+                      steps=SMOL_STEPS, seqs=None, seed=None):
+    """The prefill's logits at every prompt position, then `steps`
+    single-token steps through the KV cache (teacher-forced), against the CPU
+    model fed the same tokens.  `seqs` names the sequences of the batch the
+    CPU model runs (sequences are independent; None: all of them)."""
     cfg = miburn.SMOLLM2_135M
-    T = SMOL_PROMPT + SMOL_STEPS
-    ids = np.random.default_rng(100 + batch).integers(0, cfg["vocab"], (batch, T)).astype(np.int32)
-    want = ref_logits(W, cfg, ids)  # [B, T, vocab]
+    V = cfg["vocab"]
+    T = prompt + steps
+    ids = np.random.default_rng(100 + batch if seed is None else seed).integers(0, V, (batch, T)).astype(np.int32)
+    rows = list(range(batch)) if seqs is None else list(seqs)
+    want = ref_logits(W, cfg, ids[rows])  # [len(rows), T, vocab]
     scale = np.abs(want).max()
     m.reset()
-    lid = m.forward(ids[:, :SMOL_PROMPT], all_positions=True)
-    got = engine.download(lid).reshape(batch, SMOL_PROMPT, -1)
+    lid = m.forward(ids[:, :prompt], all_positions=True)
+    if seqs is None:
+        got = engine.download(lid).reshape(batch, prompt, -1)
+    else:  # only the checked sequences' rows leave the device
+        got = []
+        for b in rows:
+            sub = engine.copy_strided(lid, prompt, V, b * prompt * V, V, 1)
+            got.append(engine.download(sub))
+            engine.free(sub)
+        got = np.stack(got)
     engine.free(lid)
-    err = np.abs(got - want[:, :SMOL_PROMPT]).max()
-    print(f"{label} batch {batch} prefill: max |diff| {err:.3g} of logit scale {scale:.3g}")
+    err = np.abs(got - want[:, :prompt]).max()
+    print(f"{label} batch {batch} prefill of {prompt}: max |diff| {err:.3g} of logit scale {scale:.3g}")
     assert err <= 2e-2 * scale
-    clear = top1_agrees(got, want[:, :SMOL_PROMPT], err)
-    pcc = [pcc_rows(got, want[:, :SMOL_PROMPT])]
-    for p in range(SMOL_PROMPT, T):
+    clear = top1_agrees(got, want[:, :prompt], err)
+    pcc = [pcc_rows(got, want[:, :prompt])]
+    worst = 0.0
+    for p in range(prompt, T):
         lid = m.forward(ids[:, p:p + 1])
-        got = engine.download(lid)
+        got = engine.download(lid)[rows]
         engine.free(lid)
         e = np.abs(got - want[:, p]).max()
-        print(f"{label} batch {batch} decode position {p}: max |diff| {e:.3g}")
-        assert e <= 2e-2 * scale
+        worst = max(worst, e)
+        assert e <= 2e-2 * scale, (p, e, scale)
         clear += top1_agrees(got, want[:, p], e)
         pcc.append(pcc_rows(got, want[:, p]))
+    print(f"{label} batch {batch} decode positions {prompt}..{T - 1}: max |diff| {worst:.3g}")
     pcc = np.concatenate(pcc)
     print(f"{label} batch {batch}: logit correlation mean {pcc.mean():.6f} (least {pcc.min():.6f}); "
-          f"top-1 checked on {clear} of {batch * T} positions")
+          f"top-1 checked on {clear} of {len(rows) * T} positions")
     assert pcc.mean() >= min_pcc, pcc.mean()
     # The agreement check must have covered most positions.
-    assert clear >= cover * batch * T, (clear, batch * T)
+    assert clear >= cover * len(rows) * T, (clear, len(rows) * T)
+
+
+# ---------------------------------------- config 5 at its own lengths
+# A 512-token prompt, then decoding to position 639 (BASELINE config 5: 512
+# prefilled, 128 generated).  At batch 32 the prefill is 16,384 rows -- the
+# 256 x 256 direct tiles on the norms' BF16 parts, the SwiGLU and q|k|v
+# epilogues, the edge tiles at widths 576 and 960, the flash attention over
+# 512 keys -- and the CPU model runs two of the 32 sequences.
+FULL_PROMPT, FULL_STEPS = 512, 128
+
+
+@pytest.fixture(scope="module")
+def smol_full(engine):
+    cfg = miburn.SMOLLM2_135M
+    m = miburn.Llama(engine, cfg, max_ctx=FULL_PROMPT + FULL_STEPS, max_batch=32, seed=17)
+    yield m, weights(engine, m, cfg)
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def smol_full_perf(engine, smol_full):
+    m = miburn.Llama(engine, miburn.SMOLLM2_135M, max_ctx=FULL_PROMPT + FULL_STEPS, max_batch=32, seed=17,
+                     numerics="performance")
+    yield m
+    m.close()
+
+
+@pytest.mark.parametrize("batch,numerics", [(1, "reference"), (1, "performance"), (32, "reference"),
+                                            (32, "performance")])
+def test_smollm2_config5_lengths(engine, smol_full, smol_full_perf, batch, numerics):
+    """BASELINE config 5's own lengths: every logit of the 512-token prefill
+    and of the 128 decode steps after it (positions 512..639) within rel 2e-2
+    of the CPU model's scale, top-1 agreement where the margin is clear, and
+    the mean logit correlation at the contract's floor."""
+    m, W = smol_full
+    seqs = None if batch == 1 else (0, 31)
+    if numerics == "reference":
+        check_smol_logits(engine, m, W, batch, "config5 reference", prompt=FULL_PROMPT, steps=FULL_STEPS,
+                          seqs=seqs, seed=500 + batch)
+    else:
+        check_smol_logits(engine, smol_full_perf, W, batch, "config5 performance", cover=0.6, min_pcc=0.995,
+                          prompt=FULL_PROMPT, steps=FULL_STEPS, seqs=seqs, seed=500 + batch)
+
+
+@pytest.mark.parametrize("batch,numerics", [(1, "reference"), (32, "reference"), (1, "performance"),
+                                            (32, "performance")])
+def test_smollm2_config5_traced_equals_eager(engine, smol_full, smol_full_perf, batch, numerics):
+    """Greedy generation of 128 tokens after a 512-token prompt: the traced
+    generator's tokens equal the eager loop's (decode spans 512..639)."""
+    m = smol_full[0] if numerics == "reference" else smol_full_perf
+    prompt = np.random.default_rng(600 + batch).integers(0, 49152, (batch, FULL_PROMPT)).astype(np.int32)
+    eager, _, _ = m.generate(prompt, FULL_STEPS)
+    traced, _, _ = m.generate(prompt, FULL_STEPS, traced=True)
+    assert eager.shape == (batch, FULL_STEPS)
+    assert np.array_equal(traced, eager)
 
 
 @pytest.mark.parametrize("batch", [1, 32])

@@ -1095,8 +1095,10 @@ def test_norm_qkv_attention(engine, M, kv16, pos0, span, maxc):
     same_bits(engine.download(v3), engine.download(v1))
 
 
-def test_norm_qkv_attention_refuses_bad_positions(engine):
-    c = qkv_attention_case(engine, 1, False, 10, 64)
+@pytest.mark.parametrize("M,kv16", [(1, False), (2, True)])
+def test_norm_qkv_attention_refuses_bad_positions(engine, M, kv16):
+    c = qkv_attention_case(engine, M, kv16, 10, 64)
+    H, KVH, D = c["H"], c["KVH"], c["D"]
     k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
     with pytest.raises(miburn.MiError) as e:  # immediate position past the span
         engine.norm_qkv_attention(*c["args"], 0, 64, 64, k1, v1, c["scale"])
@@ -1105,14 +1107,23 @@ def test_norm_qkv_attention_refuses_bad_positions(engine):
         engine.norm_qkv_attention(*c["args"], 0, 10, 65, k1, v1, c["scale"])
     assert e.value.kind == "ARG"
     # A device position past the span: no cache row written, reported at the next wait.
+    # The step then attends from position 0: its only key is the cache's
+    # position-0 row as stored, weight 1, so every query head's output is its
+    # kv head's position-0 value row exactly -- the same on every call.
     bad = engine.upload_bits(np.array([[64]], np.int32), I32)
-    engine.norm_qkv_attention(*c["args"], bad, 0, 64, k1, v1, c["scale"])
-    with pytest.raises(miburn.MiError) as e:
+    v0 = (orc.from_bf16(c["vc0"]) if kv16 else c["vc0"]).reshape(M, KVH, 64, D)[:, :, 0]
+    want = np.repeat(v0, H // KVH, axis=1).reshape(M * H, D)
+    for _ in range(2):
+        out = engine.norm_qkv_attention(*c["args"], bad, 0, 64, k1, v1, c["scale"])
+        with pytest.raises(miburn.MiError) as e:
+            engine.sync()
+        assert e.value.kind == "DOMAIN"
         engine.sync()
-    assert e.value.kind == "DOMAIN"
-    engine.sync()
-    same_bits(engine.download(k1), c["kc0"])
-    same_bits(engine.download(v1), c["vc0"])
+        got = engine.download(out).reshape(M * H, D)
+        assert np.all(np.isfinite(got))
+        same_bits(got, want)
+        same_bits(engine.download(k1), c["kc0"])
+        same_bits(engine.download(v1), c["vc0"])
 
 
 @pytest.mark.parametrize("M", [1, 5, 32])

@@ -55,6 +55,38 @@ def test_trace_replays_equal_eager(engine):
         engine.free(i)
 
 
+def test_trace_run_checks_host_lengths(engine):
+    """An input whose host bytes are not its buffer's size, or an output
+    array with less room than its buffer, is refused (MI_E_ARG) before
+    anything is written or replayed: the input buffer, the output buffer and
+    the caller's array keep their contents."""
+    b = engine.upload(rnd(128, 96))
+    x = engine.upload(rnd(64, 128))
+    engine.begin_trace()
+    out = ops(engine, x, b)
+    trace = engine.end_trace()
+    x0 = rnd(64, 128)
+    first, = engine.run_trace(trace, {x: x0}, [out])
+    for bad in (rnd(64, 100), rnd(65, 128), np.zeros(0, np.float32)):  # short, long, empty
+        with pytest.raises(miburn.MiError) as e:
+            engine.run_trace(trace, {x: bad}, [out])
+        assert e.value.kind == "ARG"
+    small = np.full((10, 10), 7.0, np.float32)
+    with pytest.raises(miburn.MiError) as e:  # a fresh input with an undersized output
+        engine.run_trace(trace, {x: rnd(64, 128)}, [out], out_arrays=[small])
+    assert e.value.kind == "ARG"
+    assert np.all(small == 7.0)
+    assert np.array_equal(bits(engine.download(x)), bits(x0))
+    assert np.array_equal(bits(engine.download(out)), bits(first))
+    # Room to spare is accepted; the buffer's bytes land at the front.
+    roomy = np.full(64 * 96 + 5, 3.0, np.float32)
+    engine.run_trace(trace, {x: x0}, [out], out_arrays=[roomy])
+    assert np.array_equal(bits(roomy[:64 * 96].reshape(64, 96)), bits(first)) and np.all(roomy[-5:] == 3.0)
+    engine.release_trace(trace)
+    for i in (b, x, out):
+        engine.free(i)
+
+
 def test_trace_memory_is_reserved(engine):
     """A buffer the capture freed keeps its memory: an allocation after the
     capture never receives it, so a replay cannot overwrite eager data."""
