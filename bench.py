@@ -79,7 +79,12 @@ def cpu_baseline(n: int = 4096, seconds: float = 10.0) -> dict:
 
 
 def _cpu_cores() -> int:
-    return min(len(os.sched_getaffinity(0)), 16)  # the GPU box's CPU share
+    """The host cores this process may run on (sched_getaffinity), within the
+    CPU share its environment grants (OMP_NUM_THREADS, when set: 16 on the
+    MI355X boxes these numbers come from)."""
+    n = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(share)) if share.isdigit() and int(share) > 0 else n
 
 
 def cpu_models_baseline() -> dict:
