@@ -260,13 +260,14 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     BF16 weights), prefill `prompt` random tokens per sequence, then greedy
     decode `new` tokens; tokens/s of the prefill and of the decode steps.
     `numerics`: the reference contract (F32 KV cache and activations) or the
-    performance one (BF16 KV cache, BF16 prefill activation operands).  The
-    generation runs eagerly (after an untimed one of the same prompt, so the
-    allocator's blocks exist), then traced (the prompt's prefill and each decode
-    step replays of captures -- the step per 64-position span -- token ids in
-    and out through the host: the reference's TracedGenerator); the traced
-    run's captures are made by an untimed first traced generation, and its
-    tokens must be the eager ones.
+    performance one (BFP8 projection weights, BF16 KV cache, BF16 prefill
+    activation operands).  The generation runs eagerly (after an untimed one
+    of the same prompt, so the allocator's blocks exist), then traced (the
+    prompt's prefill and each decode step replays of captures -- the step per
+    64-position span, chained on the device: each replay's tokens are the
+    next one's input, read back once at the end -- the reference's
+    TracedGenerator); the traced run's captures are made by an untimed first
+    traced generation, and its tokens must be the eager ones.
     `traced` False skips the traced runs (profiling: rocprofv3's kernel
     trace has ended in a host segmentation fault inside hipGraphLaunch)."""
     import miburn
@@ -282,8 +283,10 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
         if not np.array_equal(tr_out, out):
             raise RuntimeError("traced generation's tokens differ from the eager loop's")
     m.close()
-    # Rooflines (algorithmic work): a decode step reads every BF16 weight once
-    # (134.48 M parameters, the tied table included) plus each sequence's
+    # Rooflines (algorithmic work): a decode step reads every weight once
+    # (134.48 M parameters, the tied table included: BF16, 2 B each; under
+    # the performance contract the layers' 106.17 M are BFP8, 1 + 1/16 B
+    # each, and the table stays BF16) plus each sequence's
     # key/value cache (2 x 30 layers x 3 kv heads x 64 x 4 B a position for
     # F32, 2 B for BF16, at the steps' mean context); a prefill's FLOP are
     # 2 x tokens x the layers'
@@ -296,7 +299,9 @@ def decoder_bench(eng, batch: int, prompt: int = 512, new: int = 128, numerics: 
     params = layer_params + cfg["vocab"] * cfg["hidden"]
     kv_per_pos = 2 * cfg["layers"] * cfg["kv_heads"] * cfg["head_dim"] * (2 if numerics == "performance" else 4)
     mean_ctx = prompt + new / 2
-    step_bytes = 2 * params + batch * kv_per_pos * mean_ctx
+    weight_bytes = (layer_params * 17 / 16 + 2 * cfg["vocab"] * cfg["hidden"]) if numerics == "performance" \
+        else 2 * params
+    step_bytes = weight_bytes + batch * kv_per_pos * mean_ctx
     dc_step_ms = dc_ms / max(new - 1, 1)
     attn = 2 * prompt * (prompt + 1) * cfg["head_dim"] * cfg["heads"] * cfg["layers"]
     pf_flop = batch * (2 * prompt * layer_params + attn + 2 * cfg["hidden"] * cfg["vocab"])

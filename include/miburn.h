@@ -39,8 +39,18 @@ typedef struct mi_ctx mi_ctx;
 typedef uint64_t mi_id;
 
 /* Element kinds: the trait's `Elem` (server.rs:862 ff.).  I32 and Bool are
- * 32-bit words (a Bool is 0 or 1), BF16 two-byte slots. */
-enum mi_elem { MI_F32 = 0, MI_I32 = 1, MI_BOOL = 2, MI_BF16 = 3 };
+ * 32-bit words (a Bool is 0 or 1), BF16 two-byte slots.  MI_BFP8 is the
+ * reference's block floating point storage StorageFormat::Bfp8
+ * (crates/burn-tt/src/storage.rs:24-40): a logical F32 [rows, cols] whose
+ * rows are blocks of 16 consecutive columns (the last may be shorter)
+ * sharing one exponent byte E, each value q * 2^(E - 133) with an integer
+ * |q| <= 127 -- 1 + 1/16 bytes a value.  It is made by mi_cast_bfp, read
+ * back decoded (mi_download, mi_cast_bfp to F32), and taken as the weight
+ * operand of mi_matmul, mi_linear, mi_norm_matvec, mi_norm_qkv_rope(_at) and
+ * mi_norm_qkv_attention; other ops refuse it.  Layout: q as [rows, cols]
+ * two's-complement bytes, then, from the first multiple of 256 bytes after
+ * them, E as [rows, ceil(cols / 16)] bytes. */
+enum mi_elem { MI_F32 = 0, MI_I32 = 1, MI_BOOL = 2, MI_BF16 = 3, MI_BFP8 = 5 };
 
 /* A result form, not a buffer kind: an F32 result [rows, cols] delivered as
  * its two BF16 parts in a BF16 buffer [rows, 2 cols], each row's heads (the
@@ -381,6 +391,17 @@ int mi_sgd_update(mi_ctx *ctx, int64_t count, const mi_id *params,
 /* Engine::argmax_row (server.rs:477) over every row: `[r, c] -> [r, 1]` I32,
  * the first maximum, a NaN ranking above every number. */
 int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out);
+/* A decode step's tail for a caller that chains steps on the device: with
+ * p the device position of the step's input tokens, `ids[b] = next[b]` (the
+ * next step's input), `log[b, p + 1] = next[b]` and the position becomes
+ * p + 1.  next, ids: I32 with B elements; pos: I32 [1, 1]; log: I32 [B,
+ * cols].  A position with p + 1 outside [0, cols) writes no log entry,
+ * leaves the position and raises MI_E_DOMAIN at the next wait.  No
+ * counterpart in the reference, whose generator hands each step's token to
+ * the host (crates/tt-models/src/generate.rs:12-22): this one lets a traced
+ * decode step be replayed token after token with no host transfer between,
+ * the tokens read back once. */
+int mi_decode_advance(mi_ctx *ctx, mi_id next, mi_id ids, mi_id pos, mi_id log);
 /* Engine::select_rows (server.rs:300): `out[i, :] = table[idx[i], :]`, raw
  * bits; `idx` an I32 buffer of any dims, read in row-major order.  An index
  * outside `[0, table rows)` is an MI_E_DOMAIN failure. */
@@ -557,6 +578,16 @@ int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id sin_table,
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
  * a NaN; and I32 -> F32 (`as f32`). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);
+/* Engine::cast_bfp (server.rs:141-147, 1035-1050; Session::store_bfp and
+ * bfp_to_f32): `format` MI_BFP8 stores an F32 or BF16 buffer as BFP8 by the
+ * reference's packer rule (crates/tt-models/src/quant.rs:185-235): each
+ * value's BF16 truncation in quanta of 2^(E - 133), E the largest biased
+ * exponent of its block, rounded half away from zero and clamped to 127
+ * quanta (a zero or subnormal value is 0).  The reference refuses a
+ * non-finite value; here one raises MI_E_DOMAIN at the next wait and its
+ * block is held as zeros.  `format` 0 decodes a BFP8 buffer to F32 (exact).
+ * A new buffer either way. */
+int mi_cast_bfp(mi_ctx *ctx, mi_id a, int format, mi_id *out);
 
 /* ---- traces: Engine::begin_trace / end_trace / run_trace /
  * run_generic_trace / release_trace (server.rs:591-660, 746), the reference's

@@ -672,6 +672,8 @@ struct DqaArgs {
   const float *gamma;  // [1, K] RMSNorm gain
   float eps;
   const uint16_t *w;       // [(H + 2 KVH) 64, K] BF16: q, k, v heads
+  const int8_t *wq;        // or BFP8: datums [(H + 2 KVH) 64, K] and
+  const uint8_t *we;       //   block exponents [(H + 2 KVH) 64, K / 16]
   const float *cos, *sin;  // rotary tables, rows by position
   void *kc, *vc;           // caches [B KVH maxc, 64], F32 or BF16
   int64_t maxc;
@@ -684,22 +686,64 @@ struct DqaArgs {
   float *kvn;   // [B KVH][2][64] the new key and value rows as stored, for the combine
 };
 
-// Block (256 threads): 64 rows (w0, each K BF16) times the staged row in
-// LDS xn; thread t takes row t / 4 and the 16-byte chunks t % 4, + 4, ...;
-// the four partial sums fold over the row's lanes.  wr: the chunks, loaded
-// by dqa_wload.
-template <int CH>
-__device__ __forceinline__ void dqa_wload(const uint16_t *w0, int64_t K, uint4 (&wr)[CH]) {
+// How the fused step reads eight consecutive q|k|v weights of row r from k
+// (a multiple of 8): a BF16 weight as one 16-byte load, a BFP8 weight as its
+// 8 datum bytes and the block's exponent byte -- decoded exactly to the
+// values a BF16 weight holding them gives, so the step's bits are the same.
+struct DqaBf16 {
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw load(const DqaArgs &g, int64_t r, int64_t k) {
+    return *reinterpret_cast<const uint4 *>(g.w + r * g.K + k);
+  }
+  static __device__ __forceinline__ void f32(const Raw &q, float (&w)[8]) {
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[2 * e] = __uint_as_float(u[e] << 16);
+      w[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+    }
+  }
+};
+struct DqaBfp8 {
+  struct Raw {
+    uint2 d;
+    int e;
+  };
+  static __device__ __forceinline__ Raw load(const DqaArgs &g, int64_t r, int64_t k) {
+    Raw q;
+    q.d = *reinterpret_cast<const uint2 *>(g.wq + r * g.K + k);
+    q.e = g.we[r * (g.K >> 4) + (k >> 4)];
+    return q;
+  }
+  static __device__ __forceinline__ void f32(const Raw &q, float (&w)[8]) { bfp8x8(q.d, q.e, w); }
+};
+
+// Ids of the fused step's chunk blocks in the XCD-aware order (dqa_work): 8
+// XCDs times ceil(heads / 8) heads' S chunks.  (Measured against the plain
+// order and against all G S blocks of a (sequence, kv head) on one XCD: the
+// same batch-1 and batch-4 step times, 0.703 / 0.705 / 0.714 ms at batch 1;
+// this order halves the launch's fetched bytes, 8.7 -> 4.1 MB.)
+__host__ __device__ __forceinline__ int64_t dqa_chunk_ids(const DqaArgs &g) {
+  const int64_t nh = static_cast<int64_t>(g.B) * g.H;
+  return 8 * ((nh + 7) / 8) * g.S;
+}
+
+// Block (256 threads): 64 rows (from row0, each K weights) times the staged
+// row in LDS xn; thread t takes row t / 4 and the 8-weight chunks t % 4,
+// + 4, ...; the four partial sums fold over the row's lanes.  wr: the chunks,
+// loaded by dqa_wload.
+template <int CH, typename WT>
+__device__ __forceinline__ void dqa_wload(const DqaArgs &g, int64_t row0, typename WT::Raw (&wr)[CH]) {
   const int tid = threadIdx.x, r = tid >> 2, kq = tid & 3;
-  const int64_t nch = K / 8;
+  const int64_t nch = g.K / 8;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int64_t c = kq + 4 * i;
-    wr[i] = *reinterpret_cast<const uint4 *>(w0 + r * K + 8 * (c < nch ? c : nch - 1));
+    wr[i] = WT::load(g, row0 + r, 8 * (c < nch ? c : nch - 1));
   }
 }
-template <int CH>
-__device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4 (&wr)[CH]) {
+template <int CH, typename WT>
+__device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const typename WT::Raw (&wr)[CH]) {
   const int kq = threadIdx.x & 3;
   const int64_t nch = K / 8;
   // Four independent sums (one wavefront a SIMD: nothing else hides an FMA's
@@ -711,12 +755,13 @@ __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const uint4
     if (c < nch) {
       const float4 a0 = *reinterpret_cast<const float4 *>(xn + 8 * c);
       const float4 a1 = *reinterpret_cast<const float4 *>(xn + 8 * c + 4);
-      const uint32_t u[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+      float w[8];
+      WT::f32(wr[i], w);
       const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[e] = fmaf(av[2 * e], __uint_as_float(u[e] << 16), acc[e]);
-        acc[e] = fmaf(av[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u), acc[e]);
+        acc[e] = fmaf(av[2 * e], w[2 * e], acc[e]);
+        acc[e] = fmaf(av[2 * e + 1], w[2 * e + 1], acc[e]);
       }
     }
   }
@@ -868,7 +913,7 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
 // returned).  (Counting the blocks in and letting the last of an item combine -- device
 // fences before and after the count -- costs more than the combine's own
 // launch: batch-1 SmolLM2 decode 0.694 -> 0.938 ms a step.)
-template <typename KV, int CH>
+template <typename KV, int CH, typename WT>
 __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   constexpr int D = DQA_D, NW = 4, LPR = D / 4, KPW = 64 / LPR, U = 4, STEP = NW * KPW;
   float *xn = dqa_sm;            // [K]
@@ -879,13 +924,19 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   float *red = scores + g.chunk; // [NW][D]
   float *stat = red + NW * D;    // max, sum
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t natt = static_cast<int64_t>(g.B) * g.H * g.S;
+  // Block order, XCD-aware: workgroup p runs on XCD p % 8, and the S chunk
+  // blocks of query head u (u = sequence H + head) take the ids p = u % 8 +
+  // 8 (slot), slot = (u / 8) S + chunk, so every block that reads the head's
+  // 64 weight rows runs on one XCD and the rows come once into its L2
+  // (ids with u past the last head are empty blocks).  Then the key / value
+  // blocks.
+  const int64_t nchunk = dqa_chunk_ids(g);
   const int64_t bid = blockIdx.x;
 
-  if (bid >= natt) {  // the new key or value row of (sequence, kv head)
-    const int64_t kb = bid - natt, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
-    uint4 wr[CH];
-    dqa_wload<CH>(g.w + ((g.H + which * g.KVH + j) * D) * g.K, g.K, wr);
+  if (bid >= nchunk) {  // the new key or value row of (sequence, kv head)
+    const int64_t kb = bid - nchunk, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
+    typename WT::Raw wr[CH];
+    dqa_wload<CH, WT>(g, (g.H + which * g.KVH + j) * D, wr);
     DqaPre pre;
     dqa_pre_x(g, b, pre);
     int64_t pos = g.pa.pos0;
@@ -897,7 +948,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     }
     dqa_pre_rot(g, pos, pre);
     const float rms = dqa_stage(g, pre, xn, red4);
-    const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
+    const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
     __syncthreads();
     if (!ok) {
@@ -933,11 +984,13 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   }
 
   // (sequence, query head, key chunk)
-  const int64_t s = bid % g.S, bh = bid / g.S, hq = bh % g.H, b = bh / g.H;
+  const int64_t slot = bid >> 3, bh = (bid & 7) + 8 * (slot / g.S), s = slot % g.S;
+  if (bh >= static_cast<int64_t>(g.B) * g.H) return 0;  // an empty id of the XCD-aware order
+  const int64_t hq = bh % g.H, b = bh / g.H;
   const int64_t j = hq / g.G, gg = hq % g.G, bj = b * g.KVH + j;
   // The weights first: they do not wait for a position read on the device.
-  uint4 wr[CH];
-  dqa_wload<CH>(g.w + (hq * D) * g.K, g.K, wr);
+  typename WT::Raw wr[CH];
+  dqa_wload<CH, WT>(g, hq * D, wr);
   DqaPre pre;
   dqa_pre_x(g, b, pre);
   const int64_t pos = att_pos0(g.pa, 1);
@@ -968,7 +1021,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   dqa_pre_rot(g, pos, pre);
   const float rms = dqa_stage(g, pre, xn, red4);
   {
-    const float y = dqa_dot<CH>(xn, g.K, wr) / rms;
+    const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
     if ((tid & 3) == 0) qraw[tid >> 2] = y;
   }
   __syncthreads();
@@ -1053,10 +1106,10 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   return bj;
 }
 
-template <typename KV, int CH>
+template <typename KV, int CH, typename WT>
 __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
   extern __shared__ float dqa_sm[];
-  dqa_work<KV, CH>(g, dqa_sm);
+  dqa_work<KV, CH, WT>(g, dqa_sm);
 }
 
 // The combine: one block an item, the launch after the fused one.
@@ -1317,15 +1370,21 @@ namespace mi {
 namespace {
 
 // The fused launch, then the combine's.
+template <typename KV, typename WT>
+void launch_dqa_w(hipStream_t st, const DqaArgs &g, unsigned blocks, size_t lds) {
+  const int64_t ch = (g.K / 8 + 3) / 4;  // chunks a thread
+  if (ch <= 8) decode_qkv_attention_kernel<KV, 8, WT><<<blocks, 256, lds, st>>>(g);
+  else if (ch <= 16) decode_qkv_attention_kernel<KV, 16, WT><<<blocks, 256, lds, st>>>(g);
+  else if (ch <= 24) decode_qkv_attention_kernel<KV, 24, WT><<<blocks, 256, lds, st>>>(g);
+  else decode_qkv_attention_kernel<KV, 32, WT><<<blocks, 256, lds, st>>>(g);
+}
+
 template <typename KV>
 void launch_dqa(hipStream_t st, const DqaArgs &g, float *out) {
-  const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.H * g.S + 2 * static_cast<int64_t>(g.B) * g.KVH);
+  const unsigned blocks = static_cast<unsigned>(dqa_chunk_ids(g) + 2 * static_cast<int64_t>(g.B) * g.KVH);
   const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + 8 + g.chunk + 4 * DQA_D + 2) * sizeof(float);
-  const int64_t ch = (g.K / 8 + 3) / 4;  // chunks a thread
-  if (ch <= 8) decode_qkv_attention_kernel<KV, 8><<<blocks, 256, lds, st>>>(g);
-  else if (ch <= 16) decode_qkv_attention_kernel<KV, 16><<<blocks, 256, lds, st>>>(g);
-  else if (ch <= 24) decode_qkv_attention_kernel<KV, 24><<<blocks, 256, lds, st>>>(g);
-  else decode_qkv_attention_kernel<KV, 32><<<blocks, 256, lds, st>>>(g);
+  if (g.wq) launch_dqa_w<KV, DqaBfp8>(st, g, blocks, lds);
+  else launch_dqa_w<KV, DqaBf16>(st, g, blocks, lds);
   const size_t comb = static_cast<size_t>(3 * g.G * g.S + 3 * g.G) * sizeof(float);
   attention_combine_new_kernel<KV><<<static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH), 256, comb, st>>>(g, out);
 }
@@ -1364,7 +1423,8 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   // multiple of 32 up to 1024, a gain, aligned operands; else the two calls
   // composed (which check every argument themselves).
   const bool fused = B >= 1 && B <= DQA_MAX_B && D == DQA_D && K % 32 == 0 && K <= 32 * DQA_MAX_CH && gb &&
-                     xb->elem == MI_F32 && wb->elem == MI_BF16 && wb->cols == K && heads >= 1 && kv_heads >= 1 &&
+                     xb->elem == MI_F32 && (wb->elem == MI_BF16 || (wb->elem == MI_BFP8 && K % 16 == 0)) &&
+                     wb->cols == K && heads >= 1 && kv_heads >= 1 &&
                      heads % kv_heads == 0 && G <= ATT_MAX_GROUP && wb->rows == (heads + 2 * kv_heads) * D &&
                      kb->elem == vb->elem && elem_float(kb->elem) && vb->cols == D && vb->rows == kb->rows &&
                      kb->rows % (B * kv_heads) == 0 && gb->elem == MI_F32 && gb->rows * gb->cols == K &&
@@ -1398,7 +1458,7 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   if (S < 1) S = 1;
   const int64_t chunk = ((span + S - 1) / S + 3) / 4 * 4;
   S = (span + chunk - 1) / chunk;
-  if (static_cast<size_t>(3 * G * S + 3 * G) * sizeof(float) > 65536 || B * heads * S + 2 * items > INT32_MAX)
+  if (static_cast<size_t>(3 * G * S + 3 * G) * sizeof(float) > 65536 || 8 * (B * heads + 8 * G) * S + 2 * items > INT32_MAX)
     return fail(ctx, MI_E_UNSUPPORTED, "norm_qkv_attention: context of %lld keys too long", (long long)span);
   const size_t part_floats = static_cast<size_t>(items * S * G * (D + 2));
   const size_t q_floats = static_cast<size_t>(B * heads * D), kvn_floats = static_cast<size_t>(items * 2 * D);
@@ -1413,7 +1473,12 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   g.K = K;
   g.gamma = static_cast<const float *>(gb->ptr);
   g.eps = eps;
-  g.w = static_cast<const uint16_t *>(wb->ptr);
+  if (wb->elem == MI_BFP8) {
+    g.wq = static_cast<const int8_t *>(wb->ptr);
+    g.we = static_cast<const uint8_t *>(wb->ptr) + bfp8_exp_offset(wb->rows, wb->cols);
+  } else {
+    g.w = static_cast<const uint16_t *>(wb->ptr);
+  }
   g.cos = static_cast<const float *>(cb->ptr);
   g.sin = static_cast<const float *>(sb->ptr);
   g.kc = kb->ptr;

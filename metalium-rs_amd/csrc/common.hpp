@@ -27,8 +27,19 @@
 namespace mi {
 
 // ---------------------------------------------------------------- elements
-inline size_t elem_size(int elem) { return elem == MI_BF16 ? 2 : 4; }
-inline bool elem_valid(int elem) { return elem >= MI_F32 && elem <= MI_BF16; }
+inline size_t elem_size(int elem) { return elem == MI_BF16 ? 2 : elem == MI_BFP8 ? 1 : 4; }
+// BFP8 storage: rows x cols datum bytes, then from the next multiple of 256
+// bytes the block exponents, rows x ceil(cols / 16) bytes.
+inline int64_t bfp_blocks(int64_t cols) { return (cols + 15) / 16; }
+inline size_t bfp8_exp_offset(int64_t rows, int64_t cols) {
+  return (static_cast<size_t>(rows) * static_cast<size_t>(cols) + 255) & ~static_cast<size_t>(255);
+}
+// Bytes a buffer of `elem` [rows, cols] holds.
+inline size_t storage_bytes(int elem, int64_t rows, int64_t cols) {
+  if (elem == MI_BFP8) return bfp8_exp_offset(rows, cols) + static_cast<size_t>(rows) * bfp_blocks(cols);
+  return static_cast<size_t>(rows) * static_cast<size_t>(cols) * elem_size(elem);
+}
+inline bool elem_valid(int elem) { return (elem >= MI_F32 && elem <= MI_BF16) || elem == MI_BFP8; }
 inline bool elem_float(int elem) { return elem == MI_F32 || elem == MI_BF16; }
 const char *elem_name(int elem);
 
@@ -142,6 +153,23 @@ __device__ __forceinline__ void stu4(void *p, uint4 v) {
     *static_cast<uint4 *>(p) = v;
   }
 }
+// BFP8 values (MI_BFP8): datum q, a signed byte, under its block's exponent
+// byte e is q * 2^(e - 133) -- at most 7 significant bits, so exact in F32
+// and in BF16 (the F32 value's top half).  ldexp keeps it exact for every e,
+// including the blocks of tiny values whose factor 2^(e - 133) alone would
+// be subnormal.
+__device__ __forceinline__ float bfp8_val(uint32_t word, int byte, int e) {
+  return ldexpf(static_cast<float>(static_cast<int8_t>(word >> (8 * byte))), e - 133);
+}
+// Eight consecutive datums (one 8-byte load) of one block.
+__device__ __forceinline__ void bfp8x8(uint2 d, int e, float (&w)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w[j] = bfp8_val(d.x, j, e);
+    w[4 + j] = bfp8_val(d.y, j, e);
+  }
+}
+
 // Host side: stream an operation's accesses when it moves at least this many
 // bytes -- beyond what the 256 MB last-level cache would keep for the next
 // kernel to re-read.
@@ -155,10 +183,11 @@ struct Buffer {
   int elem = MI_F32;
   uint64_t trace = 0;  // the trace whose capture allocated it (its memory is the trace's until released)
   int64_t numel() const { return rows * cols; }
+  size_t storage() const { return storage_bytes(elem, rows, cols); }
 };
 
 // Device error flags a kernel may raise; read back at the next wait.
-enum DeviceFlag : uint32_t { FLAG_INDEX_RANGE = 1u };
+enum DeviceFlag : uint32_t { FLAG_INDEX_RANGE = 1u, FLAG_NOT_FINITE = 2u };
 
 struct Ctx {
   int device = 0;
@@ -236,6 +265,10 @@ int attention_scratch_setup(Ctx *ctx);
 // Zero `bytes` (a multiple of 2) at p with a kernel: safe inside a captured
 // trace, where a memset node is not.
 int fill_zero(Ctx *ctx, void *p, size_t bytes);
+// A new buffer holding the decoded values of BFP8 buffer `src` as `elem`
+// (MI_F32, or MI_BF16: exact either way); what a consumer without a BFP8
+// read of its own takes instead.  The caller frees it.
+int bfp8_decode_to(Ctx *ctx, const Buffer *src, int elem, mi_id *id, Buffer **out);
 // MI_E_UNSUPPORTED if a trace is being captured (host transfers and waits
 // cannot be part of one).
 int refuse_if_capturing(Ctx *ctx, const char *what);
@@ -266,3 +299,8 @@ struct mi_ctx : mi::Ctx {};
   if (var == nullptr)                                                  \
     return mi::fail((ctx), MI_E_ID, "unknown or freed buffer id %llu", \
                     (unsigned long long)(id))
+
+// Ops that read a buffer's datums as plain slots refuse BFP8 storage.
+#define MI_NO_BFP8(ctx, var, what)                                                                     \
+  if ((var)->elem == MI_BFP8)                                                                          \
+  return mi::fail((ctx), MI_E_ARG, "%s does not take a BFP8 buffer (mi_cast_bfp decodes it)", (what))

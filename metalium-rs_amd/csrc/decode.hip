@@ -22,6 +22,8 @@
 // HBM.  The two rows a
 // wavefront owns are chosen so that the epilogue is local: a RoPE pair
 // (i, i + d/2) of one head, or a gate row and its up row.
+#include <type_traits>
+
 #include "common.hpp"
 #include "wave.hpp"
 
@@ -36,6 +38,10 @@ struct DecodeArgs {
   const float *gamma;  // [1, K] RMSNorm gain, or null for no norm
   float eps;
   const uint16_t *w;  // [N, K] BF16, k-contiguous
+  // Or a BFP8 weight (WBfp8 below): datums [N, K] signed bytes and block
+  // exponents [N, K / 16] bytes, K a multiple of 16.
+  const int8_t *wq;
+  const uint8_t *we;
   int64_t N, npairs;
   // DM_PLAIN: pair p = rows (2p, 2p + 1), out [M, N] (+ resid [M, N]).
   // DM_SILU_MUL: pair p = rows (p, p + inter), out [M, inter].
@@ -83,6 +89,45 @@ __device__ __forceinline__ void bf16x8(uint4 q, float (&w)[8]) {
     w[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
   }
 }
+
+// How a kernel reads eight consecutive weights of row r from k (a multiple
+// of 8): a BF16 weight as one 16-byte load; a BFP8 weight as its 8 datum
+// bytes and the block's exponent byte, decoded exactly to the values the
+// BF16 weight holding them would give -- so a product over BFP8 weights has
+// the BF16 kernel's bits.  Raw is what is held in registers between the
+// load and the use.
+struct WBf16 {
+  using Raw = uint4;
+  template <bool NT>
+  static __device__ __forceinline__ Raw load(const DecodeArgs &g, int64_t r, int64_t k) {
+    return ldu4<NT>(g.w + r * g.K + k);
+  }
+  static __device__ __forceinline__ void f32(const Raw &q, float (&w)[8]);
+  static __device__ __forceinline__ uint4 bf16(const Raw &q) { return q; }
+};
+struct WBfp8 {
+  struct Raw {
+    uint2 d;
+    int e;
+  };
+  template <bool NT>
+  static __device__ __forceinline__ Raw load(const DecodeArgs &g, int64_t r, int64_t k) {
+    Raw q;
+    q.d = *reinterpret_cast<const uint2 *>(g.wq + r * g.K + k);
+    q.e = g.we[r * (g.K >> 4) + (k >> 4)];
+    return q;
+  }
+  static __device__ __forceinline__ void f32(const Raw &q, float (&w)[8]) { bfp8x8(q.d, q.e, w); }
+  static __device__ __forceinline__ uint4 bf16(const Raw &q) {
+    float w[8];
+    bfp8x8(q.d, q.e, w);
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = (__float_as_uint(w[2 * i]) >> 16) | (__float_as_uint(w[2 * i + 1]) & 0xffff0000u);
+    return make_uint4(h[0], h[1], h[2], h[3]);
+  }
+};
+__device__ __forceinline__ void WBf16::f32(const Raw &q, float (&w)[8]) { bf16x8(q, w); }
 
 __device__ __forceinline__ float silu2(float a) {
   // a * sigmoid(a), the sigmoid in the two-branch form of the element-wise op.
@@ -191,7 +236,7 @@ __device__ __forceinline__ void pair_write(const DecodeArgs &g, const PairRows &
 // the caches keep between steps -- the vocabulary head -- so it does not
 // displace the layers' weights from the last-level cache (batch-1 SmolLM2
 // decode 0.713 -> 0.697 ms a step).
-template <int M, int MODE, int PRE = 4, bool NTW = false>
+template <int M, int MODE, int PRE = 4, bool NTW = false, typename WT = WBf16>
 __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
@@ -211,7 +256,7 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   // pair_write.
   constexpr bool XPRE = M <= 4;
   constexpr int XM = XPRE ? M : 1, XC = XPRE ? PRE : 1;
-  uint4 pw0[PRE], pw1[PRE];
+  typename WT::Raw pw0[PRE], pw1[PRE];
   float4 px[XM][XC][2], pg[XC][2];
   const bool pre_k = g.K <= 512 * PRE;
   if (pre_k) {
@@ -220,8 +265,8 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     for (int c = 0; c < PRE; ++c) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
       const int64_t kc = k < g.K ? k : g.K - 8;
-      pw0[c] = ldu4<NTW>(g.w + q.r0 * g.K + kc);
-      pw1[c] = ldu4<NTW>(g.w + r1c * g.K + kc);
+      pw0[c] = WT::template load<NTW>(g, q.r0, kc);
+      pw1[c] = WT::template load<NTW>(g, r1c, kc);
       if constexpr (XPRE) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -302,16 +347,16 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
       const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
       if (k < g.K) {
         float w0[8], w1[8];
-        bf16x8(pw0[c], w0);
-        bf16x8(pw1[c], w1);
+        WT::f32(pw0[c], w0);
+        WT::f32(pw1[c], w1);
         step(c, k, w0, w1);
       }
     }
   } else {
     for (int64_t k = static_cast<int64_t>(lane) * 8; k < g.K; k += 512) {
       float w0[8], w1[8];
-      bf16x8(*reinterpret_cast<const uint4 *>(g.w + q.r0 * g.K + k), w0);
-      bf16x8(*reinterpret_cast<const uint4 *>(g.w + r1c * g.K + k), w1);
+      WT::f32(WT::template load<false>(g, q.r0, k), w0);
+      WT::f32(WT::template load<false>(g, r1c, k), w1);
       step(0, k, w0, w1);
     }
   }
@@ -497,7 +542,7 @@ __device__ __forceinline__ void split3x8(const float (&v)[8], dm_bf16x8 &hi, dm_
   }
 }
 
-template <int MODE, int STEPS, int NB, bool GAMMA>
+template <int MODE, int STEPS, int NB, bool GAMMA, typename WT = WBf16>
 __global__ void __launch_bounds__(64 * DMFMA_WAVES)
 decode_mfma_kernel(DecodeArgs g, int M) {
   constexpr int NW = DMFMA_WAVES;
@@ -530,7 +575,7 @@ decode_mfma_kernel(DecodeArgs g, int M) {
   // condition compiles to a load through a selected pointer, one that may
   // point at a private zero.  Steps past the end are skipped below, missing
   // weight rows and activation rows zeroed.
-  uint4 wb[STEPS][NB];
+  typename WT::Raw wb[STEPS][NB];
   float4 xa[STEPS][2], ga[GAMMA ? STEPS : 1][2];
   const int64_t mc = mv ? m : 0;
   int64_t rowc[NB];
@@ -541,7 +586,7 @@ decode_mfma_kernel(DecodeArgs g, int M) {
     const int64_t step = w + NW * s;
     const int64_t k = (step < nsteps ? step : nsteps - 1) * 16 + 8 * kg;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) wb[s][b] = *reinterpret_cast<const uint4 *>(g.w + rowc[b] * g.K + k);
+    for (int b = 0; b < NB; ++b) wb[s][b] = WT::template load<false>(g, rowc[b], k);
     xa[s][0] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k);
     xa[s][1] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k + 4);
     if constexpr (GAMMA) {
@@ -585,7 +630,7 @@ decode_mfma_kernel(DecodeArgs g, int M) {
       split3x8(v, hi, mid, lo);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? wb[s][b] : make_uint4(0, 0, 0, 0));
+        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? WT::bf16(wb[s][b]) : make_uint4(0, 0, 0, 0));
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wv, acc[b], 0, 0, 0);
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, wv, acc[b], 0, 0, 0);
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wv, acc[b], 0, 0, 0);
@@ -648,7 +693,7 @@ decode_mfma_kernel(DecodeArgs g, int M) {
 // step.
 constexpr int DSPLIT_WAVES = 4;
 
-template <int MODE, int STEPS, int NB, bool GAMMA>
+template <int MODE, int STEPS, int NB, bool GAMMA, typename WT = WBf16>
 __global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(DecodeArgs g, int M) {
   constexpr int NW = DSPLIT_WAVES;
   __shared__ float red[NW][NB * 16][64];
@@ -676,7 +721,7 @@ __global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(De
   const int64_t s0 = sp * per, s1 = s0 + per < nsteps ? s0 + per : nsteps;  // s0 < s1: the host keeps S <= nsteps / per
   // Unconditional loads from addresses inside the buffers, as the unsplit
   // kernel's: steps past the split's end reread its last step.
-  uint4 wb[STEPS][NB];
+  typename WT::Raw wb[STEPS][NB];
   float4 xa[STEPS][2], ga[GAMMA ? STEPS : 1][2];
   const int64_t mc = mv ? m : 0;
   int64_t rowc[NB];
@@ -687,7 +732,7 @@ __global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(De
     const int64_t step = s0 + w + NW * si;
     const int64_t k = (step < s1 ? step : s1 - 1) * 16 + 8 * kg;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) wb[si][b] = *reinterpret_cast<const uint4 *>(g.w + rowc[b] * g.K + k);
+    for (int b = 0; b < NB; ++b) wb[si][b] = WT::template load<false>(g, rowc[b], k);
     xa[si][0] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k);
     xa[si][1] = *reinterpret_cast<const float4 *>(g.x + mc * g.ldx + k + 4);
     if constexpr (GAMMA) {
@@ -723,7 +768,7 @@ __global__ void __launch_bounds__(64 * DSPLIT_WAVES) decode_mfma_split_kernel(De
       split3x8(v, hi, mid, lo);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? wb[si][b] : make_uint4(0, 0, 0, 0));
+        const dm_bf16x8 wv = __builtin_bit_cast(dm_bf16x8, rv[b] ? WT::bf16(wb[si][b]) : make_uint4(0, 0, 0, 0));
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, wv, acc[b], 0, 0, 0);
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, wv, acc[b], 0, 0, 0);
         acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, wv, acc[b], 0, 0, 0);
@@ -840,26 +885,26 @@ static int dmfma_steps(int64_t K, int nb, bool gamma) {
   return need <= most ? static_cast<int>(need) : 0;  // longer rows: the LDS-staged kernel
 }
 
-template <int MODE, int NB, bool GAMMA, int S>
+template <int MODE, int NB, bool GAMMA, int S, typename WT>
 static void launch_dmfma_s(unsigned grid, const DecodeArgs &g, int M, hipStream_t st) {
   if constexpr (S <= dmfma_most<NB, GAMMA>())
-    decode_mfma_kernel<MODE, S, NB, GAMMA><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M);
+    decode_mfma_kernel<MODE, S, NB, GAMMA, WT><<<grid, 64 * DMFMA_WAVES, 0, st>>>(g, M);
 }
 
-template <int MODE, int NB, bool GAMMA>
+template <int MODE, int NB, bool GAMMA, typename WT>
 static void launch_dmfma(int steps, unsigned grid, const DecodeArgs &g, int M, hipStream_t st) {
   switch (steps) {
-    case 1: launch_dmfma_s<MODE, NB, GAMMA, 1>(grid, g, M, st); break;
-    case 2: launch_dmfma_s<MODE, NB, GAMMA, 2>(grid, g, M, st); break;
-    case 3: launch_dmfma_s<MODE, NB, GAMMA, 3>(grid, g, M, st); break;
-    case 4: launch_dmfma_s<MODE, NB, GAMMA, 4>(grid, g, M, st); break;
-    case 5: launch_dmfma_s<MODE, NB, GAMMA, 5>(grid, g, M, st); break;
-    case 6: launch_dmfma_s<MODE, NB, GAMMA, 6>(grid, g, M, st); break;
+    case 1: launch_dmfma_s<MODE, NB, GAMMA, 1, WT>(grid, g, M, st); break;
+    case 2: launch_dmfma_s<MODE, NB, GAMMA, 2, WT>(grid, g, M, st); break;
+    case 3: launch_dmfma_s<MODE, NB, GAMMA, 3, WT>(grid, g, M, st); break;
+    case 4: launch_dmfma_s<MODE, NB, GAMMA, 4, WT>(grid, g, M, st); break;
+    case 5: launch_dmfma_s<MODE, NB, GAMMA, 5, WT>(grid, g, M, st); break;
+    case 6: launch_dmfma_s<MODE, NB, GAMMA, 6, WT>(grid, g, M, st); break;
   }
 }
 
 // The matrix-core form for 3 to 32 rows; false when the shape does not fit it.
-template <int MODE>
+template <int MODE, typename WT>
 static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
   if (g.K % 16) return false;
   constexpr int NB = MODE == DM_PLAIN ? 1 : 2;
@@ -874,60 +919,88 @@ static bool launch_dmfma_mode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     const int Mi = static_cast<int>(M);
     if constexpr (NB == 1) {
       if (per > DSPLIT_WAVES * 6) return false;
-      if (g.gamma) decode_mfma_split_kernel<MODE, 6, 1, true><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
-      else decode_mfma_split_kernel<MODE, 6, 1, false><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      if (g.gamma) decode_mfma_split_kernel<MODE, 6, 1, true, WT><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      else decode_mfma_split_kernel<MODE, 6, 1, false, WT><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
     } else {
       if (per > DSPLIT_WAVES * 3) return false;
-      if (g.gamma) decode_mfma_split_kernel<MODE, 3, 2, true><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
-      else decode_mfma_split_kernel<MODE, 3, 2, false><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      if (g.gamma) decode_mfma_split_kernel<MODE, 3, 2, true, WT><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
+      else decode_mfma_split_kernel<MODE, 3, 2, false, WT><<<grid, 64 * DSPLIT_WAVES, 0, st>>>(g, Mi);
     }
     decode_fold_kernel<MODE><<<static_cast<unsigned>((M * g.npairs + 255) / 256), 256, 0, st>>>(g, Mi);
     return true;
   }
   const unsigned grid = static_cast<unsigned>(tiles);
-  if (g.gamma) launch_dmfma<MODE, NB, true>(steps, grid, g, static_cast<int>(M), st);
-  else launch_dmfma<MODE, NB, false>(steps, grid, g, static_cast<int>(M), st);
+  if (g.gamma) launch_dmfma<MODE, NB, true, WT>(steps, grid, g, static_cast<int>(M), st);
+  else launch_dmfma<MODE, NB, false, WT>(steps, grid, g, static_cast<int>(M), st);
   return true;
 }
 
 // Weights of at least this many bytes are streamed (NTW).
 constexpr int64_t DECODE_STREAM_BYTES = int64_t(32) << 20;
 
-template <int MODE>
-static void launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
+// false: a BFP8 weight of a shape only the LDS-staged kernel takes (the
+// caller runs it on the weight decoded to BF16 instead).
+template <int MODE, typename WT = WBf16>
+static bool launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
+  constexpr bool Q = !std::is_same<WT, WBf16>::value;
   const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
-  if (M > DECODE_GEMV_MAX_M && launch_dmfma_mode<MODE>(M, g, st)) return;
+  if (M > DECODE_GEMV_MAX_M && launch_dmfma_mode<MODE, WT>(M, g, st)) return true;
   if (M > 8) {
+    if constexpr (Q) return false;
     decode_matvec_wide_kernel<MODE><<<grid, 256, 0, st>>>(g, static_cast<int>(M));
-    return;
+    return true;
   }
   if (M <= DECODE_GEMV_MAX_M && g.K <= 1024) {  // two chunks a lane: half the registers of four
     // One wavefront a block (a pair each): the few hundred pairs of a layer's
     // products spread over that many CUs (batch-1 SmolLM2 step 0.703 ->
     // 0.695 ms); the streamed head keeps four.
-    const bool nt = g.N * g.K * 2 >= DECODE_STREAM_BYTES;
+    // (The streamed form is for the BF16 head; a BFP8 weight is a layer's.)
+    const bool nt = !Q && g.N * g.K * 2 >= DECODE_STREAM_BYTES;
     const unsigned g1 = static_cast<unsigned>(g.npairs);
     switch (M) {
       case 1:
         if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-        else decode_matvec_kernel<1, MODE, 2><<<g1, 64, 0, st>>>(g);
+        else decode_matvec_kernel<1, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g);
         break;
       case 2:
         if (nt) decode_matvec_kernel<2, MODE, 2, true><<<grid, 256, 0, st>>>(g);
-        else decode_matvec_kernel<2, MODE, 2><<<g1, 64, 0, st>>>(g);
+        else decode_matvec_kernel<2, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g);
         break;
-      case 3: decode_matvec_kernel<3, MODE, 2><<<g1, 64, 0, st>>>(g); break;
-      case 4: decode_matvec_kernel<4, MODE, 2><<<g1, 64, 0, st>>>(g); break;
-      case 5: decode_matvec_kernel<5, MODE, 2><<<g1, 64, 0, st>>>(g); break;
-      default: decode_matvec_kernel<6, MODE, 2><<<g1, 64, 0, st>>>(g); break;
+      case 3: decode_matvec_kernel<3, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g); break;
+      case 4: decode_matvec_kernel<4, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g); break;
+      case 5: decode_matvec_kernel<5, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g); break;
+      default: decode_matvec_kernel<6, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g); break;
     }
-    return;
+    return true;
   }
   switch (M) {
-#define MI_DEC(m) case m: decode_matvec_kernel<m, MODE><<<grid, 256, 0, st>>>(g); break;
+#define MI_DEC(m) case m: decode_matvec_kernel<m, MODE, 4, false, WT><<<grid, 256, 0, st>>>(g); break;
     MI_DEC(1) MI_DEC(2) MI_DEC(3) MI_DEC(4) MI_DEC(5) MI_DEC(6) MI_DEC(7) MI_DEC(8)
 #undef MI_DEC
   }
+  return true;
+}
+
+// A projection's launch for its weight: BF16, or BFP8 read as such where
+// the kernels take it, else decoded to BF16 into a buffer freed after the
+// launch (stream-ordered: no later op gets the memory before the launch
+// has run).
+template <int MODE>
+static int launch_weight(Ctx *ctx, int64_t M, DecodeArgs &g, const Buffer *wb) {
+  if (wb->elem != MI_BFP8) {
+    launch_decode<MODE>(M, g, ctx->stream);
+    return MI_OK;
+  }
+  g.wq = static_cast<const int8_t *>(wb->ptr);
+  g.we = static_cast<const uint8_t *>(wb->ptr) + bfp8_exp_offset(wb->rows, wb->cols);
+  if (launch_decode<MODE, WBfp8>(M, g, ctx->stream)) return MI_OK;
+  mi_id t;
+  Buffer *tb;
+  if (int s = bfp8_decode_to(ctx, wb, MI_BF16, &t, &tb)) return s;
+  g.w = static_cast<const uint16_t *>(tb->ptr);
+  launch_decode<MODE>(M, g, ctx->stream);
+  mi_free(static_cast<mi_ctx *>(ctx), t);
+  return MI_OK;
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -948,7 +1021,11 @@ static void split_setup(Ctx *ctx, int64_t M, DecodeArgs &g) {
 // Shared checks: x [M <= 32, K] F32, w [N, K] BF16, K % 8 == 0, gamma [1, K].
 static int check_common(mi_ctx *ctx, const Buffer *xb, const Buffer *wb, const Buffer *gb, const char *what) {
   if (xb->elem != MI_F32) return fail(ctx, MI_E_ARG, "%s: activations are %s, not F32", what, elem_name(xb->elem));
-  if (wb->elem != MI_BF16) return fail(ctx, MI_E_ARG, "%s: weight is %s, not BF16", what, elem_name(wb->elem));
+  if (wb->elem != MI_BF16 && wb->elem != MI_BFP8)
+    return fail(ctx, MI_E_ARG, "%s: weight is %s, not BF16 or BFP8", what, elem_name(wb->elem));
+  if (wb->elem == MI_BFP8 && xb->cols % 16)
+    return fail(ctx, MI_E_UNSUPPORTED, "%s: a BFP8 weight of width %lld (a multiple of 16 is read)", what,
+                (long long)xb->cols);
   if (xb->rows < 1 || xb->rows > DECODE_MAX_M)
     return fail(ctx, MI_E_UNSUPPORTED, "%s: %lld activation rows (1 to %d)", what, (long long)xb->rows, DECODE_MAX_M);
   if (wb->cols != xb->cols) return fail(ctx, MI_E_ARG, "%s: weight is [%lld, %lld], activations [%lld, %lld]", what,
@@ -1000,7 +1077,7 @@ extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_i
     g.K = K;
     g.gamma = gb ? static_cast<const float *>(gb->ptr) : nullptr;
     g.eps = eps;
-    g.w = static_cast<const uint16_t *>(wb->ptr);
+    g.w = wb->elem == MI_BF16 ? static_cast<const uint16_t *>(wb->ptr) : nullptr;
     g.N = N;
     g.resid = rb ? static_cast<const float *>(rb->ptr) : nullptr;
     g.out = static_cast<float *>(ob->ptr);
@@ -1009,11 +1086,15 @@ extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_i
       g.inter = ncols;
       g.npairs = ncols;
       split_setup<DM_SILU_MUL>(ctx, M, g);
-      launch_decode<DM_SILU_MUL>(M, g, ctx->stream);
+      s = launch_weight<DM_SILU_MUL>(ctx, M, g, wb);
     } else {
       g.npairs = (N + 1) / 2;
       split_setup<DM_PLAIN>(ctx, M, g);
-      launch_decode<DM_PLAIN>(M, g, ctx->stream);
+      s = launch_weight<DM_PLAIN>(ctx, M, g, wb);
+    }
+    if (s) {
+      mi_free(ctx, id);
+      return s;
     }
   }
   s = check_launch(ctx, "norm_matvec");
@@ -1072,7 +1153,7 @@ static int norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_q
   g.K = xb->cols;
   g.gamma = gb ? static_cast<const float *>(gb->ptr) : nullptr;
   g.eps = eps;
-  g.w = static_cast<const uint16_t *>(wb->ptr);
+  g.w = wb->elem == MI_BF16 ? static_cast<const uint16_t *>(wb->ptr) : nullptr;
   g.N = wb->rows;
   g.npairs = wb->rows / 2;
   g.out = static_cast<float *>(ob->ptr);
@@ -1090,7 +1171,11 @@ static int norm_qkv_rope(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_q
   g.pos_dev = pos_dev;
   g.flags = flags(ctx);
   split_setup<DM_QKV>(ctx, M, g);
-  launch_decode<DM_QKV>(M, g, ctx->stream);
+  s = launch_weight<DM_QKV>(ctx, M, g, wb);
+  if (s) {
+    mi_free(ctx, id);
+    return s;
+  }
   s = check_launch(ctx, "norm_qkv_rope");
   if (s) {
     mi_free(ctx, id);

@@ -436,6 +436,7 @@ int fill_zero(Ctx *ctx, void *p, size_t bytes) {
 extern "C" int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32_t bits, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  if (elem == MI_BFP8) return fail(ctx, MI_E_ARG, "fill of a BFP8 buffer (mi_cast_bfp makes one)");
   mi_id id; Buffer *b;
   int s = new_buffer(ctx, rows, cols, elem, &id, &b);
   if (s) return s;
@@ -454,6 +455,7 @@ extern "C" int mi_fill(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, uint32
 extern "C" int mi_empty(mi_ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  if (elem == MI_BFP8) return fail(ctx, MI_E_ARG, "empty BFP8 buffer (mi_cast_bfp makes one)");
   mi_id id; Buffer *b;
   int s = new_buffer(ctx, rows, cols, elem, &id, &b);
   if (s) return s;
@@ -492,6 +494,13 @@ extern "C" int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out) {
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, src, a);
   if (!elem_valid(out_elem)) return fail(ctx, MI_E_ARG, "cast to unknown kind %d", out_elem);
+  // BFP8 storage: packed or decoded (the reference's cast_bfp).
+  if (out_elem == MI_BFP8) return mi_cast_bfp(ctx, a, MI_BFP8, out);
+  if (src->elem == MI_BFP8) {
+    if (out_elem != MI_F32 && out_elem != MI_BF16)
+      return fail(ctx, MI_E_ARG, "cast of BFP8 to %s", elem_name(out_elem));
+    return bfp8_decode_to(ctx, src, out_elem, out, nullptr);
+  }
   int64_t rows = src->rows, cols = src->cols;
   int se = src->elem;
   const void *sp = src->ptr;
@@ -529,6 +538,7 @@ __global__ void copy4_kernel(const T *src, T *dst, int64_t d1, int64_t d2, int64
 static int copy4(Ctx *ctx, mi_id srcid, const int64_t dims[4], int64_t offset, const int64_t strides[4], mi_id *out) {
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, src, srcid);
+  MI_NO_BFP8(ctx, src, "copy_strided");
   int64_t n = 1;
   for (int i = 0; i < 4; ++i) {
     if (dims[i] < 0) return fail(ctx, MI_E_ARG, "negative copy extent");
@@ -595,6 +605,7 @@ extern "C" int mi_assign_block(mi_ctx *ctx, mi_id dst, mi_id src, int64_t row0, 
   MI_ENTER(ctx);
   MI_BUF(ctx, d, dst);
   MI_BUF(ctx, s, src);
+  MI_NO_BFP8(ctx, d, "assign_block");
   if (d->elem != s->elem) return fail(ctx, MI_E_ARG, "assign of %s into %s", elem_name(s->elem), elem_name(d->elem));
   if (row0 < 0 || col0 < 0 || row0 + s->rows > d->rows || col0 + s->cols > d->cols)
     return fail(ctx, MI_E_ARG, "block [%lld, %lld] at (%lld, %lld) outside [%lld, %lld]", (long long)s->rows,
@@ -735,6 +746,8 @@ extern "C" int mi_copy_into4(mi_ctx *ctx, mi_id dst, int64_t dst_offset, const i
   if (!dst_strides || !src_strides || !dims) return fail(ctx, MI_E_ARG, "null dims or strides");
   MI_BUF(ctx, d, dst);
   MI_BUF(ctx, sb, src);
+  MI_NO_BFP8(ctx, d, "copy_into4");
+  MI_NO_BFP8(ctx, sb, "copy_into4");
   if (elem_size(d->elem) != elem_size(sb->elem)) return fail(ctx, MI_E_ARG, "copy of %s into %s", elem_name(sb->elem), elem_name(d->elem));
   int64_t n = 1;
   for (int i = 0; i < 4; ++i) {

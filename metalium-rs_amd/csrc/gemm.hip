@@ -1949,9 +1949,31 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   return MI_OK;
 }
 
+// A BFP8 operand of a product is decoded to BF16 first (exact), so the
+// product is the BF16 product of the same values; *tmp receives the decoded
+// buffer's id (0 when `id` is not BFP8), for the caller to free.  The decode
+// step's projections read BFP8 weights themselves (mi_norm_matvec,
+// mi_norm_qkv_rope, mi_norm_qkv_attention).
+static int bfp8_operand(mi_ctx *ctx, mi_id id, mi_id *tmp) {
+  *tmp = 0;
+  Buffer *b = lookup(ctx, id);
+  if (!b || b->elem != MI_BFP8) return MI_OK;  // an unknown id is reported by the product
+  return bfp8_decode_to(ctx, b, MI_BF16, tmp, nullptr);
+}
+
 extern "C" int mi_matmul(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
-  return matmul_common(ctx, a, a_transposed, b, b_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out);
+  mi_id da, db;
+  if (int s = bfp8_operand(ctx, a, &da)) return s;
+  if (int s = bfp8_operand(ctx, b, &db)) {
+    if (da) mi_free(ctx, da);
+    return s;
+  }
+  const int s = matmul_common(ctx, da ? da : a, a_transposed, db ? db : b, b_transposed, 1, 0, 0, 0, 0, nullptr,
+                              out_elem, out);
+  if (da) mi_free(ctx, da);
+  if (db) mi_free(ctx, db);
+  return s;
 }
 
 extern "C" int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b, int b_transposed, mi_id *out,
@@ -2026,7 +2048,11 @@ extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id 
   LinearTerms lin;
   int s = linear_terms(ctx, bias, residual, m, n, &lin);
   if (s) return s;
-  return matmul_common(ctx, x, 0, w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
+  mi_id dw;
+  if ((s = bfp8_operand(ctx, w, &dw))) return s;
+  s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
+  if (dw) mi_free(ctx, dw);
+  return s;
 }
 
 extern "C" int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed, mi_id bias, mi_id residual,

@@ -275,6 +275,7 @@ extern "C" int mi_select_rows(mi_ctx *ctx, mi_id table, mi_id idx, mi_id *out) {
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, t, table);
   MI_BUF(ctx, ix, idx);
+  MI_NO_BFP8(ctx, t, "select_rows");
   if (ix->elem != MI_I32) return fail(ctx, MI_E_ARG, "select_rows indices are %s, not I32", elem_name(ix->elem));
   const int64_t n = ix->numel(), V = t->rows, D = t->cols;
   const void *tp = t->ptr;
@@ -455,6 +456,45 @@ extern "C" int mi_select_add_rows(mi_ctx *ctx, mi_id t, mi_id idx, mi_id value, 
   if (s) { mi_free(ctx, id); return s; }
   *out = id;
   return MI_OK;
+}
+
+namespace mi {
+// One block: every thread reads the position before thread 0 advances it.
+__global__ void __launch_bounds__(1024) decode_advance_kernel(const int32_t *next, int32_t *ids, int32_t *pos,
+                                                                int32_t *log, int64_t B, int64_t cols,
+                                                                uint32_t *flags) {
+  const int32_t p = *pos;
+  const bool ok = p >= 0 && static_cast<int64_t>(p) + 1 < cols;
+  for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
+    const int32_t v = next[b];
+    ids[b] = v;
+    if (ok) log[b * cols + p + 1] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (ok) *pos = p + 1;
+    else atomicOr(flags, FLAG_INDEX_RANGE);
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_decode_advance(mi_ctx *ctx, mi_id next, mi_id ids, mi_id pos, mi_id log) {
+  MI_ENTER(ctx);
+  MI_BUF(ctx, nb, next);
+  MI_BUF(ctx, ib, ids);
+  MI_BUF(ctx, pb, pos);
+  MI_BUF(ctx, lb, log);
+  const int64_t B = nb->numel();
+  if (nb->elem != MI_I32 || ib->elem != MI_I32 || lb->elem != MI_I32 || pb->elem != MI_I32 || pb->numel() != 1 ||
+      ib->numel() != B || lb->rows != B || B < 1)
+    return fail(ctx, MI_E_ARG, "decode_advance: next [%lld] %s, ids [%lld] %s, position %s [%lld], log %s [%lld, %lld]; "
+                "want I32 with ids and log rows matching next and one position", (long long)B, elem_name(nb->elem),
+                (long long)ib->numel(), elem_name(ib->elem), elem_name(pb->elem), (long long)pb->numel(),
+                elem_name(lb->elem), (long long)lb->rows, (long long)lb->cols);
+  decode_advance_kernel<<<1, 256, 0, ctx->stream>>>(static_cast<const int32_t *>(nb->ptr), static_cast<int32_t *>(ib->ptr),
+                                                    static_cast<int32_t *>(pb->ptr), static_cast<int32_t *>(lb->ptr), B,
+                                                    lb->cols, flags(ctx));
+  return check_launch(ctx, "decode_advance");
 }
 
 extern "C" int mi_argmax_rows(mi_ctx *ctx, mi_id a, mi_id *out) {

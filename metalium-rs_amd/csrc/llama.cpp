@@ -44,6 +44,13 @@ struct Layer {
   // 32..63, ...) for mi_linear_swiglu_parts (intermediate a multiple of 128;
   // weights do not change after creation).
   Tensor wgu_pairs;
+  // Under the performance contract the four projection weights are BFP8
+  // (the reference's Numerics::Performance weight plan, crates/tt-models/src/
+  // quant.rs:154-175: every matrix but the embedding table).  A decode step
+  // reads these as stored (1 + 1/16 bytes a weight); the BF16 tensors above
+  // then hold the same values decoded (exact), for the prefill's matrix-core
+  // products, whose time is arithmetic, not weight bytes.
+  Tensor q_wqkv, q_wo, q_wgu, q_wdown;
   Tensor cache_k, cache_v;
 };
 
@@ -77,6 +84,9 @@ struct mi_llama {
   // token ids [batch, 1] and the position [1, 1] (I32).
   std::map<int64_t, StepTrace> traces;
   Tensor step_ids, step_pos;
+  // [batch, max_ctx] I32: the token each chained step chose, at the
+  // position it goes to (mi_decode_advance), read back once a generation.
+  Tensor step_log;
   std::map<std::pair<int64_t, int64_t>, PromptTrace> prompt_traces;
 };
 
@@ -141,11 +151,12 @@ Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, in
   const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim;
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
   for (Layer &L : m->layers) {
-    Tensor o = burn::norm_qkv_attention(x, L.attn_norm, c.eps, L.wqkv, m->rope_cos, m->rope_sin, H, KVH, pos, pos0,
-                                        span, L.cache_k, L.cache_v, scale);
-    x = burn::norm_matvec(o, nullptr, 0.0f, L.wo, &x, false);
-    Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, L.wgu, nullptr, true);
-    x = burn::norm_matvec(h, nullptr, 0.0f, L.wdown, &x, false);
+    const bool q = L.q_wqkv.defined();  // BFP8 weights
+    Tensor o = burn::norm_qkv_attention(x, L.attn_norm, c.eps, q ? L.q_wqkv : L.wqkv, m->rope_cos, m->rope_sin, H,
+                                        KVH, pos, pos0, span, L.cache_k, L.cache_v, scale);
+    x = burn::norm_matvec(o, nullptr, 0.0f, q ? L.q_wo : L.wo, &x, false);
+    Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, q ? L.q_wgu : L.wgu, nullptr, true);
+    x = burn::norm_matvec(h, nullptr, 0.0f, q ? L.q_wdown : L.wdown, &x, false);
   }
   return x;
 }
@@ -363,6 +374,18 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
       L.mlp_norm = ones(ctx, c.hidden);
       L.wgu = weight(ctx, 2 * static_cast<int64_t>(c.intermediate), c.hidden, init_std, next());
       L.wdown = weight(ctx, c.hidden, c.intermediate, init_std, next());
+      if (c.numerics == MI_NUMERICS_PERFORMANCE) {
+        // BFP8 (mi_cast_bfp); the BF16 copies become the values it holds.  The
+        // decode kernels read BFP8 rows whose width is a multiple of 16; other
+        // shapes keep only the BF16 copies of the same values.
+        const bool native = c.hidden % 16 == 0 && c.intermediate % 16 == 0 && qd % 16 == 0;
+        for (auto wp : {std::make_pair(&L.wqkv, &L.q_wqkv), std::make_pair(&L.wo, &L.q_wo),
+                        std::make_pair(&L.wgu, &L.q_wgu), std::make_pair(&L.wdown, &L.q_wdown)}) {
+          Tensor held = burn::float_cast(*wp.first, MI_BFP8);
+          *wp.first = burn::float_cast(held, MI_BF16);
+          if (native) *wp.second = held;
+        }
+      }
       if (c.intermediate % 128 == 0 && c.hidden % 32 == 0) {
         const int64_t I = c.intermediate, Hd = c.hidden;
         const int64_t dims[4] = {I / 32, 2, 32, Hd}, st[4] = {32 * Hd, I * Hd, Hd, 1};
@@ -511,22 +534,35 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
 
 namespace {
 
+// The chained decode step's device buffers for `batch` sequences: the input
+// token ids, the position of those tokens, the token log.
+void step_buffers(mi_llama *m, int64_t batch) {
+  mi_ctx *ctx = m->ctx;
+  if (!m->step_ids.defined() || m->step_ids.rows() != batch) m->step_ids = burn::fill(ctx, {batch, 1}, MI_I32, 0);
+  if (!m->step_pos.defined()) m->step_pos = burn::fill(ctx, {1, 1}, MI_I32, 0);
+  if (!m->step_log.defined() || m->step_log.rows() != batch)
+    m->step_log = burn::fill(ctx, {batch, m->cfg.max_ctx}, MI_I32, 0);
+}
+
 // The decode step of `span`, captured on first use: the token ids and the
-// position come from m->step_ids and m->step_pos, the next ids go to the
-// trace's own buffer.  Capture records the launches without running them:
-// the caches are not touched.
+// position come from m->step_ids and m->step_pos; the step ends with
+// mi_decode_advance, which makes its chosen ids the next step's input, logs
+// them at the next position and advances the position -- so replays chain
+// on the device, with no host transfer between tokens.  Capture records the
+// launches without running them: the caches are not touched.
 StepTrace &step_trace(mi_llama *m, int64_t batch, int64_t span) {
   auto it = m->traces.find(span);
   if (it != m->traces.end()) return it->second;
   mi_ctx *ctx = m->ctx;
-  if (!m->step_ids.defined() || m->step_ids.rows() != batch) m->step_ids = burn::fill(ctx, {batch, 1}, MI_I32, 0);
-  if (!m->step_pos.defined()) m->step_pos = burn::fill(ctx, {1, 1}, MI_I32, 0);
+  step_buffers(m, batch);
   burn::check(ctx, mi_trace_begin(ctx), "trace_begin");
   StepTrace st;
   try {
     Tensor x = burn::select_rows_as(m->embed, m->step_ids.reshape({batch}), MI_F32);
     x = decode_layers(m, x.reshape({batch, m->cfg.hidden}), batch, &m->step_pos, 0, span);
     st.next = burn::argmax_rows(head_last(m, x, batch, 1));
+    burn::check(ctx, mi_decode_advance(ctx, st.next.use(), m->step_ids.use(), m->step_pos.use(), m->step_log.use()),
+                "decode_advance");
   } catch (...) {
     uint64_t dead = 0;
     if (mi_trace_end(ctx, &dead) == MI_OK) (void)mi_trace_release(ctx, dead);
@@ -583,44 +619,45 @@ extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int3
     m->len = 0;
     ensure_cache(m, batch);
     burn::check(m->ctx, mi_sync(m->ctx), "sync");
-    // The prompt: a replay of its captured prefill (ids in, the first new
-    // ids out), or eagerly where the prefill cannot be captured.
+    // The prompt: a replay of its captured prefill (ids in), or eagerly where
+    // the prefill cannot be captured; its first new ids start the chain.
     PromptTrace &pt = prompt_trace(m, batch, t_prompt);
+    step_buffers(m, batch);
+    mi_ctx *ctx = m->ctx;
+    const Tensor start = burn::fill(ctx, {1, 1}, MI_I32, static_cast<uint32_t>(t_prompt - 1));
     auto t0 = clock::now();
-    std::vector<int32_t> tok(static_cast<size_t>(batch));
+    Tensor first;
     if (pt.id) {
       const mi_id in_ids[1] = {pt.ids.id()};
       const void *in_vals[1] = {prompt};
-      const mi_id out_ids[1] = {pt.next.id()};
-      void *out_vals[1] = {tok.data()};
       const int64_t in_len[1] = {static_cast<int64_t>(batch) * t_prompt * 4};
-      const int64_t out_len[1] = {static_cast<int64_t>(tok.size()) * 4};
-      burn::check(m->ctx, mi_trace_run(m->ctx, pt.id, 1, in_ids, in_vals, in_len, 1, out_ids, out_vals, out_len),
+      burn::check(ctx, mi_trace_run(ctx, pt.id, 1, in_ids, in_vals, in_len, 0, nullptr, nullptr, nullptr),
                   "trace_run");
-      m->len = t_prompt;
+      first = pt.next;
     } else {
       Tensor h = forward_hidden(m, prompt, batch, t_prompt);
-      tok = burn::int_into_data(burn::argmax_rows(head_last(m, h, batch, t_prompt)));
+      first = burn::argmax_rows(head_last(m, h, batch, t_prompt));
     }
+    m->len = t_prompt;
+    // The first ids are the input at position t_prompt: the chain starts one
+    // before it, and mi_decode_advance logs them there and moves on.
+    burn::check(ctx, mi_copy_into(ctx, start.use(), m->step_pos.use()), "copy_into");
+    burn::check(ctx, mi_decode_advance(ctx, first.use(), m->step_ids.use(), m->step_pos.use(), m->step_log.use()),
+                "decode_advance");
+    burn::check(ctx, mi_sync(ctx), "sync");
     auto t1 = clock::now();
-    for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
-    // Each step: the ids and the position written into the trace's inputs,
-    // one replay, the next ids read back (the reference's traced step:
-    // token ids in, the next token out).
+    // Each later token: one replay of the step for its span, queued behind
+    // the last with no transfer; the tokens come back once, at the end.
     for (int32_t s = 1; s < n_new; ++s) {
       StepTrace &st = step_trace(m, batch, decode_span(m, m->len + 1));
-      const int32_t pos = static_cast<int32_t>(m->len);
-      const mi_id in_ids[2] = {m->step_ids.id(), m->step_pos.id()};
-      const void *in_vals[2] = {tok.data(), &pos};
-      const mi_id out_ids[1] = {st.next.id()};
-      void *out_vals[1] = {tok.data()};
-      const int64_t in_len[2] = {static_cast<int64_t>(tok.size()) * 4, 4};
-      const int64_t out_len[1] = {static_cast<int64_t>(tok.size()) * 4};
-      burn::check(m->ctx, mi_trace_run(m->ctx, st.id, 2, in_ids, in_vals, in_len, 1, out_ids, out_vals, out_len),
+      burn::check(ctx, mi_trace_run(ctx, st.id, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr),
                   "trace_run");
       m->len += 1;
-      for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
     }
+    const std::vector<int32_t> log = burn::int_into_data(m->step_log);  // waits for the last step
+    const int64_t cols = m->cfg.max_ctx;
+    for (int32_t b = 0; b < batch; ++b)
+      for (int32_t s = 0; s < n_new; ++s) out[b * n_new + s] = log[static_cast<size_t>(b * cols + t_prompt + s)];
     auto t2 = clock::now();
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();

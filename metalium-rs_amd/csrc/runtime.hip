@@ -22,6 +22,7 @@ const char *elem_name(int elem) {
     case MI_I32: return "I32";
     case MI_BOOL: return "Bool";
     case MI_BF16: return "BF16";
+    case MI_BFP8: return "BFP8";
     default: return "?";
   }
 }
@@ -126,7 +127,7 @@ int new_buffer(Ctx *ctx, int64_t rows, int64_t cols, int elem, mi_id *id, Buffer
   Buffer b;
   b.rows = rows; b.cols = cols; b.elem = elem;
   b.trace = ctx->capturing ? ctx->capture_id : 0;
-  size_t want = static_cast<size_t>(rows) * static_cast<size_t>(cols) * elem_size(elem);
+  size_t want = storage_bytes(elem, rows, cols);
   b.ptr = device_alloc(ctx, want, &b.bytes);
   if (!b.ptr) return fail(ctx, MI_E_OOM, "device allocation of %zu bytes failed", want);
   *id = insert(ctx, b);
@@ -187,7 +188,8 @@ static int collect(Ctx *ctx) {
     (void)hipMemcpy(ctx->dev_flags, &zero, sizeof zero, hipMemcpyHostToDevice);
     if (ctx->sticky == MI_OK) {
       ctx->sticky = MI_E_DOMAIN;
-      fail(ctx, MI_E_DOMAIN, "an index was out of range (DOMAIN)");
+      fail(ctx, MI_E_DOMAIN, (f & FLAG_INDEX_RANGE) ? "an index was out of range (DOMAIN)"
+                                                    : "a value stored as BFP8 was not finite (DOMAIN)");
       ctx->sticky_msg = ctx->last_error;
     }
   }
@@ -322,6 +324,7 @@ static int upload_raw(mi_ctx *ctx, const void *src, int64_t rows, int64_t cols, 
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   if (!src && rows * cols > 0) return fail(ctx, MI_E_ARG, "null host pointer");
   if (int r = refuse_if_capturing(ctx, "upload")) return r;
+  if (elem == MI_BFP8) return fail(ctx, MI_E_ARG, "a BFP8 buffer is made on the device by mi_cast_bfp, not uploaded");
   mi_id id; Buffer *b;
   int s = new_buffer(ctx, rows, cols, elem, &id, &b);
   if (s) return s;
@@ -397,6 +400,16 @@ static int download_raw(mi_ctx *ctx, mi_id id, void *dst, int64_t n, int want_el
 int mi_download(mi_ctx *ctx, mi_id id, float *out, int64_t n) {
   MI_ENTER(ctx);
   MI_BUF(ctx, b, id);
+  if (b->elem == MI_BFP8) {  // its decoded values, as the reference's download_bfp
+    if (int r = refuse_if_capturing(ctx, "download")) return r;
+    if (n < b->numel())
+      return fail(ctx, MI_E_ARG, "download: room for %lld of %lld datums", (long long)n, (long long)b->numel());
+    mi_id t;
+    if (int s = bfp8_decode_to(ctx, b, MI_F32, &t, nullptr)) return s;
+    const int s = download_raw(ctx, t, out, n, 4, "download");
+    mi_free(ctx, t);
+    return s;
+  }
   if (b->elem != MI_F32) return fail(ctx, MI_E_ARG, "download of a %s buffer as F32", elem_name(b->elem));
   return download_raw(ctx, id, out, n, 4, "download");
 }
@@ -442,9 +455,9 @@ int mi_metadata(mi_ctx *ctx, mi_id id, int64_t *rows, int64_t *cols, int *elem) 
 int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols) {
   MI_ENTER(ctx);
   MI_BUF(ctx, b, id);
-  if (rows < 0 || cols < 0 || rows * cols != b->numel())
-    return fail(ctx, MI_E_ARG, "reshape of [%lld, %lld] to [%lld, %lld]", (long long)b->rows, (long long)b->cols,
-                (long long)rows, (long long)cols);
+  if (rows < 0 || cols < 0 || rows * cols != b->numel() || (b->elem == MI_BFP8 && cols != b->cols))
+    return fail(ctx, MI_E_ARG, "reshape of %s [%lld, %lld] to [%lld, %lld]", elem_name(b->elem), (long long)b->rows,
+                (long long)b->cols, (long long)rows, (long long)cols);
   b->rows = rows;
   b->cols = cols;
   return MI_OK;
@@ -471,9 +484,12 @@ int mi_copy_into(mi_ctx *ctx, mi_id src, mi_id dst) {
   MI_ENTER(ctx);
   MI_BUF(ctx, sb, src);
   MI_BUF(ctx, db, dst);
-  const size_t n = static_cast<size_t>(sb->numel()) * elem_size(sb->elem);
-  if (n != static_cast<size_t>(db->numel()) * elem_size(db->elem))
-    return fail(ctx, MI_E_ARG, "copy_into: %zu bytes into %zu", n, static_cast<size_t>(db->numel()) * elem_size(db->elem));
+  const size_t n = sb->storage();
+  if ((sb->elem == MI_BFP8) != (db->elem == MI_BFP8) ||
+      (sb->elem == MI_BFP8 && (sb->rows != db->rows || sb->cols != db->cols)))
+    return fail(ctx, MI_E_ARG, "copy_into: %s [%lld, %lld] into %s [%lld, %lld]", elem_name(sb->elem),
+                (long long)sb->rows, (long long)sb->cols, elem_name(db->elem), (long long)db->rows, (long long)db->cols);
+  if (n != db->storage()) return fail(ctx, MI_E_ARG, "copy_into: %zu bytes into %zu", n, db->storage());
   if (n > 0 && sb->ptr != db->ptr) {
     hipError_t e = hipMemcpyAsync(db->ptr, sb->ptr, n, hipMemcpyDeviceToDevice, ctx->stream);
     if (e != hipSuccess) return fail(ctx, MI_E_HIP, "copy_into: %s", hipGetErrorString(e));
@@ -534,6 +550,7 @@ int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs, const mi_id *inp
     MI_BUF(ctx, b, inputs[i]);
     const int64_t bytes = b->numel() * static_cast<int64_t>(elem_size(b->elem));
     if (!values[i]) return fail(ctx, MI_E_ARG, "trace_run: null values for input %lld", (long long)i);
+    if (b->elem == MI_BFP8) return fail(ctx, MI_E_ARG, "trace_run: input %lld is a BFP8 buffer", (long long)i);
     if (value_bytes[i] != bytes)
       return fail(ctx, MI_E_ARG, "trace_run: input %lld is %lld bytes, its buffer %lld", (long long)i,
                   (long long)value_bytes[i], (long long)bytes);
@@ -542,6 +559,7 @@ int mi_trace_run(mi_ctx *ctx, uint64_t trace, int64_t n_inputs, const mi_id *inp
     MI_BUF(ctx, b, outputs[i]);
     const int64_t bytes = b->numel() * static_cast<int64_t>(elem_size(b->elem));
     if (!out_values[i]) return fail(ctx, MI_E_ARG, "trace_run: null destination for output %lld", (long long)i);
+    if (b->elem == MI_BFP8) return fail(ctx, MI_E_ARG, "trace_run: output %lld is a BFP8 buffer", (long long)i);
     if (out_bytes[i] < bytes)
       return fail(ctx, MI_E_ARG, "trace_run: output %lld has room for %lld bytes of %lld", (long long)i,
                   (long long)out_bytes[i], (long long)bytes);

@@ -25,11 +25,11 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmiburn.so")
 
-F32, I32, BOOL, BF16 = 0, 1, 2, 3
+F32, I32, BOOL, BF16, BFP8 = 0, 1, 2, 3, 5
 # A result form of mi_rms_norm / mi_silu_mul_halves: the F32 result as its
 # BF16 parts, [rows, 2 cols] (heads, then remainders), read by linear_parts.
 BF16_PARTS = 4
-_NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16}
+_NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16, BFP8: np.float32}
 
 AXIS_ROWS, AXIS_COLS = 0, 1
 MATMUL_FAST, MATMUL_ACCURATE = 0, 1
@@ -144,6 +144,8 @@ def _load() -> ctypes.CDLL:
                          ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64)],
         "mi_trace_release": [P, U64],
         "mi_copy_into": [P, U64, U64],
+        "mi_cast_bfp": [P, U64, c_int, ctypes.POINTER(U64)],
+        "mi_decode_advance": [P, U64, U64, U64, U64],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_select_rows_as": [P, U64, U64, c_int, Ip],
@@ -253,7 +255,7 @@ class Engine:
     def download(self, id_: int) -> np.ndarray:
         r, c, e = self.metadata(id_)
         out = np.empty((r, c), dtype=_NP[e])
-        if e == F32:
+        if e in (F32, BFP8):  # a BFP8 buffer reads back decoded (F32)
             self._check(self._lib.mi_download(self.ctx, id_, out.ctypes.data, out.size))
         elif e == BF16:
             self._check(self._lib.mi_download_bf16(self.ctx, id_, out.ctypes.data, out.size))
@@ -551,6 +553,16 @@ class Engine:
 
     def cast_float(self, a: int, out_elem: int) -> int:
         return self._out(self._lib.mi_cast, a, out_elem)
+
+    def decode_advance(self, next_ids: int, ids: int, pos: int, log: int) -> None:
+        """A chained decode step's tail: ids <- next_ids, log[:, pos + 1] <-
+        next_ids, pos <- pos + 1 (all on the device)."""
+        self._check(self._lib.mi_decode_advance(self.ctx, next_ids, ids, pos, log))
+
+    def cast_bfp(self, a: int, fmt: int = BFP8) -> int:
+        """Engine::cast_bfp: an F32 or BF16 buffer stored as BFP8 (fmt
+        BFP8), or a BFP8 buffer decoded to F32 (fmt 0)."""
+        return self._out(self._lib.mi_cast_bfp, a, fmt)
 
     def random_dram(self, rows: int, cols: int, draw: int, p1: float = 0.0, p2: float = 1.0,
                     base: int = 0) -> int:

@@ -20,7 +20,10 @@
  *    (ops.rs:4572-4590);
  *  - gather / select / scatter-add, argmax (ops.rs:1001-1240, 2389-2490;
  *    ops/index.rs:27-30; crates/tt-models/src/generate.rs:176-183);
- *  - RMSNorm (crates/burn-tt/src/ops/norm.rs:1-5, ops.rs:2686-2693).
+ *  - RMSNorm (crates/burn-tt/src/ops/norm.rs:1-5, ops.rs:2686-2693);
+ *  - block floating point storage: the performance contract's BFP8 weights
+ *    (crates/tt-models/src/quant.rs:185-235 bfp_round_trip, crates/tt-isa/
+ *    src/tile.rs:619-650 the unpacker's decode).
  * Where Flex's exact bits depend on its libm and its summation order, this
  * oracle computes the better answer instead: transcendental functions in
  * double precision rounded once to f32, and every sum or dot product
@@ -535,4 +538,86 @@ int or_max_threads(void) {
 #else
   return 1;
 #endif
+}
+
+/* ------------------------------------------------- block floating point */
+/* crates/tt-isa/src/tile.rs:619-636 bfp8_to_bf16: the unpacker's decode of
+ * one BFP8 datum (sign bit 7, magnitude bits 6..0) under its block's shared
+ * exponent byte, to a BF16 bit pattern.  The magnitude shifted left once is
+ * normalised by its leading zeros, which come off the exponent byte with
+ * uint8 wrap-around; a zero magnitude decodes to +0, or to 0xff80 (-inf)
+ * when the sign bit is set (FloatBitPatterns.md:98, tile.rs:1158-1167). */
+uint16_t or_bfp8_to_bf16(uint8_t datum, uint8_t exp) {
+  const uint16_t sign = (uint16_t)(datum >> 7);
+  uint8_t mag = (uint8_t)(datum << 1);
+  if (mag == 0) return sign ? 0xff80u : 0u;
+  int lz = 0;
+  while (!(mag & 0x80u)) {
+    mag = (uint8_t)(mag << 1);
+    ++lz;
+  }
+  const uint8_t e = (uint8_t)(exp - (uint8_t)lz);
+  return (uint16_t)((sign << 15) | ((uint16_t)e << 7) | (mag & 0x7eu));
+}
+
+/* crates/tt-models/src/quant.rs:185-235 bfp_round_trip: `values`, rows of
+ * `cols`, held in a block floating point format of `width` datum bits (8:
+ * BFP8, 4: BFP4, 2: BFP2) and read back.  Blocks of 16 consecutive columns
+ * (the last of a row may be shorter) share the largest biased exponent E of
+ * their values; each value truncated to BF16 is scaled by 2^-(E - 133)
+ * (double precision), rounded half away from zero, clamped to 127, its low
+ * 8 - width bits dropped; a zero magnitude is datum 0, else the sign joins
+ * it; the datum decodes through the unpacker (BFP4 / BFP2 datums shifted to
+ * the top of the byte first, tile.rs:640-650) and a decoded exponent field
+ * of 0 reads as 0.0.  The reference asserts finite values; a non-finite
+ * value here gives a NaN output and a return of 1 (0 otherwise).  `exps`,
+ * if not null, receives each block's E ([rows, ceil(cols / 16)]). */
+int or_bfp_round_trip(const float *x, int64_t rows, int64_t cols, int width, float *out, uint8_t *exps) {
+  const int64_t nb = (cols + 15) / 16;
+  int bad = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t b = 0; b < nb; ++b) {
+      const int64_t c0 = b * 16, c1 = c0 + 16 < cols ? c0 + 16 : cols;
+      uint8_t E = 0;
+      int finite = 1;
+      for (int64_t c = c0; c < c1; ++c) {
+        uint32_t u;
+        memcpy(&u, &x[r * cols + c], 4);
+        const uint8_t e = (uint8_t)(u >> 23);
+        if (e > E) E = e;
+        if ((u & 0x7f800000u) == 0x7f800000u) finite = 0;
+      }
+      if (exps) exps[r * nb + b] = E;
+      const double quantum = ldexp(1.0, (int)E - 127 - 6);
+      for (int64_t c = c0; c < c1; ++c) {
+        float *dst = &out[r * cols + c];
+        if (!finite) {
+          *dst = NAN;
+          bad = 1;
+          continue;
+        }
+        uint32_t u;
+        memcpy(&u, &x[r * cols + c], 4);
+        const uint32_t bits = u & 0xffff0000u;
+        double scaled = 0.0;
+        if (bits & 0x7f800000u) {
+          float t;
+          memcpy(&t, &bits, 4);
+          scaled = fabs((double)t) / quantum;
+        }
+        double rd = round(scaled); /* half away from zero, as Rust's f64::round */
+        if (rd > 127.0) rd = 127.0;
+        const uint8_t magnitude = (uint8_t)((uint8_t)rd >> (8 - width));
+        const uint8_t datum = magnitude == 0 ? 0 : (uint8_t)(magnitude | ((bits >> 31) << (width - 1)));
+        const uint16_t dec = or_bfp8_to_bf16((uint8_t)(datum << (8 - width)), E);
+        if ((dec & 0x7f80u) == 0) {
+          *dst = 0.0f;
+        } else {
+          const uint32_t v = (uint32_t)dec << 16;
+          memcpy(dst, &v, 4);
+        }
+      }
+    }
+  }
+  return bad;
 }

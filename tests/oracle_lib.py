@@ -46,6 +46,10 @@ def lib():
         L.or_cast_to_bf16.argtypes = [P, I64, P]
         L.or_cast_from_bf16.argtypes = [P, I64, P]
         L.or_max_threads.restype = I
+        L.or_bfp8_to_bf16.argtypes = [ctypes.c_uint8, ctypes.c_uint8]
+        L.or_bfp8_to_bf16.restype = ctypes.c_uint16
+        L.or_bfp_round_trip.argtypes = [P, I64, I64, I, P, P]
+        L.or_bfp_round_trip.restype = I
         _lib = L
     return _lib
 
@@ -219,3 +223,19 @@ def from_bf16(h):
 
 def max_threads():
     return lib().or_max_threads()
+
+
+def bfp8_to_bf16(datum: int, exp: int) -> int:
+    """The unpacker's decode of one BFP8 datum under its exponent byte."""
+    return int(lib().or_bfp8_to_bf16(datum, exp))
+
+
+def bfp_round_trip(x, width: int = 8):
+    """(values held in BFP8 / BFP4 / BFP2 and read back [rows, cols], block
+    exponents [rows, ceil(cols / 16)] uint8, 1 if a value was not finite)."""
+    x = f32(np.atleast_2d(x))
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    exps = np.empty((rows, (cols + 15) // 16), np.uint8)
+    bad = lib().or_bfp_round_trip(_p(x), rows, cols, width, _p(out), _p(exps))
+    return out, exps, bad

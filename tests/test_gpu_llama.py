@@ -16,7 +16,12 @@ batch consistency are checked too (every row of a batch of one repeated
 prompt decodes the same tokens as batch 1).  Under the performance numeric
 contract (BF16 KV cache, BF16 activation operands in the prefill's products;
 llama.rs:1270-1280) the same model's logits meet the same 2e-2 bar against
-the F32 CPU model, with the same top-1 agreement.
+the F32 CPU model holding the BFP8-rounded weights (the contract's
+specification model), with the same top-1 agreement; those weights are
+checked bit for bit against the oracle's BFP8 round trip of the reference
+model's draws.  BASELINE config 5's own lengths -- a 512-token prompt, then
+decoding to position 639 -- run at batch 1 and 32 under both contracts, and
+the traced generator's 128 tokens equal the eager loop's.
 """
 import numpy as np
 import pytest
@@ -24,6 +29,7 @@ import torch
 
 import miburn
 import models_cpu as mc
+import oracle_lib as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -188,16 +194,30 @@ def test_smollm2_shape_logits_within_tolerance(engine, smol, batch):
     check_smol_logits(engine, m, W, batch, "reference")
 
 
+def check_bfp8_weights(engine, ref_model, perf_model, W_perf):
+    """The performance contract's weights are the reference model's (same
+    seed) held as BFP8: every projection the oracle's bfp_round_trip of the
+    BF16 draw, bit for bit; the embedding table unchanged (BF16)."""
+    for name, layer in (("embed", 0), ("wq", 0), ("wk", 7), ("wv", 13), ("wo", 21), ("wgate", 3), ("wup", 17),
+                        ("wdown", 29)):
+        pid = ref_model.param(name, layer)
+        base = miburn.bf16_to_f32(engine.download(pid))
+        engine.free(pid)
+        got = W_perf["embed"] if name == "embed" else W_perf["layers"][layer][name]
+        want = base if name == "embed" else orc.bfp_round_trip(base)[0]
+        assert np.array_equal(got.numpy().view(np.uint32), want.view(np.uint32)), name
+
+
 @pytest.fixture(scope="module")
 def smol_perf(engine, smol):
-    """The same weights (same seed) under the performance numeric contract."""
+    """The same draws (same seed) under the performance numeric contract:
+    BFP8 projection weights; the CPU model holds the BFP8-rounded values
+    (the reference's specification model for this contract, crates/burn-tt/
+    src/numerics.rs:14-17)."""
     m = miburn.Llama(engine, miburn.SMOLLM2_135M, max_ctx=96, max_batch=32, seed=11, numerics="performance")
-    for name, layer in (("embed", 0), ("wq", 0), ("wdown", 29)):
-        a, b = smol[0].param(name, layer), m.param(name, layer)
-        assert np.array_equal(engine.download(a), engine.download(b)), name
-        engine.free(a)
-        engine.free(b)
-    yield m
+    W = weights(engine, m, miburn.SMOLLM2_135M)
+    check_bfp8_weights(engine, smol[0], m, W)
+    yield m, W
     m.close()
 
 
@@ -211,7 +231,7 @@ def test_smollm2_shape_performance_numerics(engine, smol, smol_perf, batch):
     least 0.995 -- the reference's own floor for this contract, its
     reference-contract baseline (1.0 here) less 0.005
     (step269_performance_contract.rs:21-24)."""
-    check_smol_logits(engine, smol_perf, smol[1], batch, "performance", cover=0.6, min_pcc=0.995)
+    check_smol_logits(engine, smol_perf[0], smol_perf[1], batch, "performance", cover=0.6, min_pcc=0.995)
 
 
 def pcc_rows(got, want):
@@ -293,7 +313,9 @@ def smol_full(engine):
 def smol_full_perf(engine, smol_full):
     m = miburn.Llama(engine, miburn.SMOLLM2_135M, max_ctx=FULL_PROMPT + FULL_STEPS, max_batch=32, seed=17,
                      numerics="performance")
-    yield m
+    W = weights(engine, m, miburn.SMOLLM2_135M)
+    check_bfp8_weights(engine, smol_full[0], m, W)
+    yield m, W
     m.close()
 
 
@@ -310,8 +332,8 @@ def test_smollm2_config5_lengths(engine, smol_full, smol_full_perf, batch, numer
         check_smol_logits(engine, m, W, batch, "config5 reference", prompt=FULL_PROMPT, steps=FULL_STEPS,
                           seqs=seqs, seed=500 + batch)
     else:
-        check_smol_logits(engine, smol_full_perf, W, batch, "config5 performance", cover=0.6, min_pcc=0.995,
-                          prompt=FULL_PROMPT, steps=FULL_STEPS, seqs=seqs, seed=500 + batch)
+        check_smol_logits(engine, smol_full_perf[0], smol_full_perf[1], batch, "config5 performance", cover=0.6,
+                          min_pcc=0.995, prompt=FULL_PROMPT, steps=FULL_STEPS, seqs=seqs, seed=500 + batch)
 
 
 @pytest.mark.parametrize("batch,numerics", [(1, "reference"), (32, "reference"), (1, "performance"),
@@ -319,7 +341,7 @@ def test_smollm2_config5_lengths(engine, smol_full, smol_full_perf, batch, numer
 def test_smollm2_config5_traced_equals_eager(engine, smol_full, smol_full_perf, batch, numerics):
     """Greedy generation of 128 tokens after a 512-token prompt: the traced
     generator's tokens equal the eager loop's (decode spans 512..639)."""
-    m = smol_full[0] if numerics == "reference" else smol_full_perf
+    m = smol_full[0] if numerics == "reference" else smol_full_perf[0]
     prompt = np.random.default_rng(600 + batch).integers(0, 49152, (batch, FULL_PROMPT)).astype(np.int32)
     eager, _, _ = m.generate(prompt, FULL_STEPS)
     traced, _, _ = m.generate(prompt, FULL_STEPS, traced=True)
@@ -354,7 +376,7 @@ def test_traced_generation_equals_eager(engine, smol, smol_perf, batch, numerics
     """The decode step captured once per 64-position span and replayed per
     token (the reference's TracedGenerator) gives the eager loop's tokens;
     the 20 steps from a 56-token prompt cross from the 64 span into the 128."""
-    m = smol[0] if numerics == "reference" else smol_perf
+    m = smol[0] if numerics == "reference" else smol_perf[0]
     prompt = np.random.default_rng(300 + batch).integers(0, 49152, (batch, 56)).astype(np.int32)
     eager, _, _ = m.generate(prompt, 20)
     traced, _, _ = m.generate(prompt, 20, traced=True)

@@ -1287,3 +1287,31 @@ def test_stale_id_and_report(engine):
         engine.eltwise_op_as("EXP", a)
     r = engine.report()
     assert r["uploads"] > 0 and r["ops"] > 0
+
+
+def test_decode_advance_chains_on_the_device(engine):
+    """mi_decode_advance: ids <- next, log[:, pos + 1] <- next, pos <- pos + 1;
+    a position whose log column is past the log writes no entry, keeps the
+    position and raises MI_E_DOMAIN at the next wait."""
+    B, cols = 5, 12
+    nxt = engine.upload_bits(np.arange(100, 100 + B, dtype=np.int32).reshape(B, 1), I32)
+    ids = engine.upload_bits(np.zeros((B, 1), np.int32), I32)
+    pos = engine.upload_bits(np.array([[3]], np.int32), I32)
+    log = engine.upload_bits(np.full((B, cols), -1, np.int32), I32)
+    engine.decode_advance(nxt, ids, pos, log)
+    engine.decode_advance(ids, ids, pos, log)  # next is this step's input: logged again one further
+    assert engine.download(pos)[0, 0] == 5
+    want = np.full((B, cols), -1, np.int32)
+    want[:, 4] = want[:, 5] = np.arange(100, 100 + B)
+    assert np.array_equal(engine.download(log), want)
+    assert np.array_equal(engine.download(ids).ravel(), np.arange(100, 100 + B))
+    end = engine.upload_bits(np.array([[cols - 1]], np.int32), I32)
+    engine.decode_advance(nxt, ids, end, log)
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    assert engine.download(end)[0, 0] == cols - 1
+    assert np.array_equal(engine.download(log), want)
+    with pytest.raises(miburn.MiError) as e:  # mismatched rows are refused at the call
+        engine.decode_advance(nxt, ids, pos, engine.upload_bits(np.zeros((B + 1, cols), np.int32), I32))
+    assert e.value.kind == "ARG"

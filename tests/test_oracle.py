@@ -12,6 +12,8 @@ and brute-force loops on tiny inputs.  No GPU is needed.
 """
 import os
 
+import math
+
 import numpy as np
 import pytest
 
@@ -417,3 +419,111 @@ def test_every_kind_the_device_is_graded_on_is_pinned():
     me = open(os.path.abspath(__file__)).read()
     for kind, where in PINNED.items():
         assert where in G.files or f"def {where}(" in me, (kind, where)
+
+
+# ------------------------------------------------------------ BFP8 / BFP4
+# oracle/oracle.c's restatement of crates/tt-isa/src/tile.rs:619 (the
+# unpacker's BFP8 decode) and crates/tt-models/src/quant.rs:185-235
+# (bfp_round_trip), pinned by the mathematics rather than by its procedure.
+
+def _bf16_value(h):
+    return float(orc.from_bf16(np.array([h], np.uint16))[0])
+
+
+def test_bfp8_decode_every_datum_and_exponent():
+    """All 65536 (datum, exponent) pairs.  Where the normalised exponent
+    stays in 1..254 the BF16 value is the closed form +-mag * 2^(exp - 133);
+    a zero magnitude is +0, or -inf with the sign set (tile.rs:1158-1167's
+    known answers); past the range the exponent field wraps modulo 256 with
+    the significand still the normalised magnitude."""
+    for datum in range(256):
+        sign, mag = datum >> 7, datum & 0x7F
+        for exp in range(256):
+            h = orc.bfp8_to_bf16(datum, exp)
+            if mag == 0:
+                assert h == (0xFF80 if sign else 0), (datum, exp)
+                continue
+            nb = mag.bit_length()
+            dexp = exp - (7 - nb)  # leading zeros of the magnitude's 8-bit form
+            assert (h >> 15) == sign
+            if 1 <= dexp <= 254:
+                assert _bf16_value(h) == (-1) ** sign * math.ldexp(mag, exp - 133), (datum, exp)
+            else:
+                assert (h >> 7) & 0xFF == dexp % 256, (datum, exp)
+                assert 1 + (h & 0x7F) / 128 == mag / 2 ** (nb - 1), (datum, exp)
+
+
+def test_bfp_round_trip_hand_worked_block():
+    # Block exponent 127 (from 1.0): quantum 2^-6.
+    v = np.zeros(16, np.float32)
+    v[:10] = [1.0, 0.3, -0.3, 0.5, 2.0 ** -7, 1.5 * 2.0 ** -8, 0.0, -0.0, 1.9921875, -3 * 2.0 ** -7]
+    out, exps, bad = orc.bfp_round_trip(v.reshape(1, 16))
+    assert bad == 0 and exps[0, 0] == 127
+    # 0.3 truncates to BF16 0.298828125 = 19.125 quanta -> 19; 2^-7 is half a
+    # quantum -> 1 (half away from zero); 1.5 * 2^-8 is 0.375 quanta -> 0;
+    # 1.9921875 is 127.5 quanta -> 128, clamped to 127; -3 * 2^-7 is -1.5
+    # quanta -> -2.  -0.0 comes back +0.0 (datum 0).
+    want = [1.0, 19 / 64, -19 / 64, 0.5, 1 / 64, 0.0, 0.0, 0.0, 127 / 64, -2 / 64] + [0.0] * 6
+    assert out[0].tolist() == want
+    assert not np.signbit(out[0, 7])
+    # BFP4 keeps the top 3 magnitude bits: 19 -> 16 quanta (0.25), 64 -> 1.0,
+    # 32 -> 0.5, 127 -> 112 quanta (1.75), 1 and 2 -> 0.
+    out4, _, _ = orc.bfp_round_trip(v.reshape(1, 16), width=4)
+    assert out4[0, :10].tolist() == [1.0, 0.25, -0.25, 0.5, 0.0, 0.0, 0.0, 0.0, 1.75, 0.0]
+
+
+def test_bfp_round_trip_is_the_nearest_block_value():
+    """Each value is the nearest of the 255 values k * 2^(E - 133), |k| <=
+    127, to its BF16 truncation (ties away from zero; beyond 127 quanta the
+    largest), E the block's largest biased exponent: a brute-force search,
+    not the rounding the oracle does.  Rows of mixed scales, a partial last
+    block, the reference's own step92 pattern."""
+    rng = np.random.default_rng(41)
+    scale = 2.0 ** rng.integers(-30, 30, (24, 1))
+    x = (rng.standard_normal((24, 40)) * scale).astype(np.float32)
+    x[3, 5] = 0.0
+    x[4, 17:19] = [-0.0, 1e-39]  # a signed zero and a subnormal: zero magnitude
+    i = np.arange(1024)
+    step92 = (((i % 16) - 8 + np.where(i % 3 == 0, 65 / 1024, 0)) * 2.0 ** ((i // 16 % 9) - 4)).astype(np.float32)
+    for data in (x, step92.reshape(16, 64)):
+        out, exps, bad = orc.bfp_round_trip(data)
+        assert bad == 0
+        rows, cols = data.shape
+        t = (data.view(np.uint32) & 0xFFFF0000).view(np.float32).astype(np.float64)
+        k = np.arange(-127, 128, dtype=np.float64)
+        for r in range(rows):
+            for b in range((cols + 15) // 16):
+                blk = slice(16 * b, min(16 * b + 16, cols))
+                E = int(np.max(data[r, blk].view(np.uint32) >> 23 & 0xFF))
+                assert exps[r, b] == E
+                cand = k * math.ldexp(1.0, E - 133)
+                for c in range(blk.start, blk.stop):
+                    tv = t[r, c] if (data[r, c].view(np.uint32) >> 23) & 0xFF else 0.0
+                    d = np.abs(cand - tv)
+                    best = np.flatnonzero(d == d.min())
+                    j = best[np.argmax(np.abs(k[best]))]  # a tie goes away from zero
+                    assert out[r, c] == cand[j], (r, c, data[r, c], out[r, c], cand[j])
+
+
+def test_bfp_round_trip_invariants():
+    rng = np.random.default_rng(43)
+    x = (rng.standard_normal((64, 96)) * 0.02).astype(np.float32)
+    out, exps, _ = orc.bfp_round_trip(x)
+    again, exps2, _ = orc.bfp_round_trip(out)
+    assert np.array_equal(again, out)  # held values are held exactly
+    neg, _, _ = orc.bfp_round_trip(-x)
+    assert np.array_equal(neg, -out)  # odd (zeros aside: +0 either way)
+    # Every held value is a BF16 value (at most 7 significant bits), within
+    # half a quantum of the BF16 truncation, and exact in BFP8's 1 + 1/16
+    # bytes a value: sign, 7 magnitude bits, the block's exponent byte.
+    assert np.array_equal(orc.from_bf16(orc.to_bf16(out)), out)
+    q = np.ldexp(1.0, exps.astype(np.int64) - 133).repeat(16, 1)[:, :96]
+    m = out.astype(np.float64) / q
+    assert np.array_equal(m, np.round(m)) and np.abs(m).max() <= 127
+    t = (x.view(np.uint32) & 0xFFFF0000).view(np.float32).astype(np.float64)
+    assert np.all(np.abs(out - t) <= 0.5 * q)
+    # A non-finite value is refused (the reference asserts finite values).
+    y = x.copy()
+    y[2, 3] = np.inf
+    _, _, bad = orc.bfp_round_trip(y)
+    assert bad == 1
