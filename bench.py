@@ -389,6 +389,30 @@ def decode_layer_bench(eng, batch: int = 1, ctx: int = 576, steps: int = 200) ->
     return dict(batch=batch, ctx=ctx, steps=steps, us_per_layer=round(us, 2))
 
 
+def prefill_bench(eng, batch: int = 1, prompt: int = 512, numerics: str = "reference", reps: int = 3) -> dict:
+    """The SmolLM2-135M-shaped decoder's prefill alone (config 5's 512-token
+    prompt, last-position logits), `reps` times after one warm run: a short
+    run of few dispatches, for kernel traces and counters of the prefill's
+    kernels (the whole decoder harness under rocprofv3 --pmc has ended in a
+    fault inside the profiler)."""
+    import miburn
+    m = miburn.Llama(eng, miburn.SMOLLM2_135M, max_ctx=prompt, max_batch=batch, seed=5, numerics=numerics)
+    ids = np.random.default_rng(9).integers(0, 49152, (batch, prompt)).astype(np.int32)
+
+    def once():
+        m.reset()
+        eng.free(m.forward(ids))
+    once()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        once()
+    eng.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    m.close()
+    return dict(batch=batch, prompt=prompt, numerics=numerics, reps=reps, prefill_ms=round(ms, 3))
+
+
 def mlp_bench(eng, steps: int = 100, traces: bool = True) -> dict:
     """MLP 784->128->10 training, batch 64, SGD lr 0.01:
     eager steps on device-drawn batches, and the step captured as a trace
@@ -456,7 +480,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true")
     ap.add_argument("--no-models", action="store_true")
-    ap.add_argument("--only", choices=["decoder", "decode_layer", "mlp", "transformer"],
+    ap.add_argument("--only", choices=["decoder", "decode_layer", "prefill", "mlp", "transformer"],
                     help="run one model harness (or one decoder layer's decode launches) alone, for profiling, "
                          "and print its JSON")
     ap.add_argument("--batch", type=int, default=1, help="decoder batch for --only decoder / decode_layer")
@@ -483,6 +507,7 @@ def main() -> int:
     if args.only:
         out = {"decoder": lambda: decoder_bench(eng, args.batch, numerics=args.numerics, traced=not args.no_traces),
                "decode_layer": lambda: decode_layer_bench(eng, args.batch),
+               "prefill": lambda: prefill_bench(eng, args.batch, numerics=args.numerics),
                "mlp": lambda: mlp_bench(eng, traces=not args.no_traces),
                "transformer": lambda: transformer_bench(eng, traces=not args.no_traces)}[args.only]()
         print(json.dumps({"harness": args.only, **out}), flush=True)
