@@ -417,6 +417,19 @@ int mi_select_rows_as(mi_ctx *ctx, mi_id table, mi_id idx, int out_elem,
 /* Engine::pick_columns (server.rs:349): `out[r] = x[r, idx[r]]`, raw bits,
  * `[r, 1]`. */
 int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out);
+/* Burn's float_gather along any dim of a rank <= 4 tensor (ops.rs:1102-1160,
+ * gather_native): `x` holds the row-major tensor of dims `dims[0..3]`
+ * (leading dims 1 for a lower rank), `idx` an I32 buffer of the same
+ * element count as dims `idims` (equal to `dims` except along `dim`);
+ * `out[i] = x[i with its coordinate along dim replaced by idx[i]]`, raw
+ * bits (4- or 2-byte elements), as [idims[0] idims[1] idims[2], idims[3]].
+ * An index outside [0, dims[dim]) writes zero bits and is an MI_E_DOMAIN
+ * failure at the next wait (ops.rs:995-1000).  The reference stages each
+ * output element's candidates as a row (its repack, 32 rows at a time) and
+ * picks with Engine::gather_indexed (server.rs:293), which is this
+ * library's mi_pick_columns; here one launch reads the candidates in place. */
+int mi_gather(mi_ctx *ctx, mi_id x, const int64_t dims[4], int dim, mi_id idx,
+              const int64_t idims[4], mi_id *out);
 /* The gather's backward (ops.rs:1043-1100): a copy of `x` with `v[r]` added
  * at `[r, idx[r]]`. */
 int mi_scatter_add_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id v,

@@ -368,6 +368,84 @@ extern "C" int mi_pick_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id *out) {
   return MI_OK;
 }
 
+namespace mi {
+// One thread an output element: its coordinates from its flat position in
+// the index tensor's dims, the source with the gathered dim replaced.
+template <typename T>
+__global__ void __launch_bounds__(256) gather_dim_kernel(const T *x, int64_t d1, int64_t d2, int64_t d3, int dim,
+                                                         int64_t ddim, const int32_t *idx, int64_t i1, int64_t i2,
+                                                         int64_t i3, int64_t n, T *out, uint32_t *flags) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    int64_t c[4];
+    int64_t r = e;
+    c[3] = r % i3; r /= i3;
+    c[2] = r % i2; r /= i2;
+    c[1] = r % i1; r /= i1;
+    c[0] = r;
+    const int32_t k = idx[e];
+    if (k < 0 || k >= ddim) {
+      atomicOr(flags, FLAG_INDEX_RANGE);
+      out[e] = T(0);
+      continue;
+    }
+    c[dim] = k;
+    out[e] = x[((c[0] * d1 + c[1]) * d2 + c[2]) * d3 + c[3]];
+  }
+}
+}  // namespace mi
+
+extern "C" int mi_gather(mi_ctx *ctx, mi_id x, const int64_t dims[4], int dim, mi_id idx, const int64_t idims[4],
+                         mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out || !dims || !idims) return fail(ctx, MI_E_ARG, "null pointer argument");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, ib, idx);
+  MI_NO_BFP8(ctx, xb, "gather");
+  if (ib->elem != MI_I32) return fail(ctx, MI_E_ARG, "gather indices are %s, not I32", elem_name(ib->elem));
+  if (dim < 0 || dim > 3) return fail(ctx, MI_E_ARG, "gather dim %d (0 to 3)", dim);
+  int64_t nx = 1, ni = 1;
+  for (int d = 0; d < 4; ++d) {
+    if (dims[d] < 1 || idims[d] < 0 || (d != dim && idims[d] != dims[d]))
+      return fail(ctx, MI_E_ARG, "gather: dims [%lld, %lld, %lld, %lld], index dims [%lld, %lld, %lld, %lld] along %d",
+                  (long long)dims[0], (long long)dims[1], (long long)dims[2], (long long)dims[3], (long long)idims[0],
+                  (long long)idims[1], (long long)idims[2], (long long)idims[3], dim);
+    nx *= dims[d];
+    ni *= idims[d];
+  }
+  if (nx != xb->numel() || ni != ib->numel())
+    return fail(ctx, MI_E_ARG, "gather: %lld and %lld elements for dims of %lld and %lld", (long long)xb->numel(),
+                (long long)ib->numel(), (long long)nx, (long long)ni);
+  if (dims[dim] > INT32_MAX) return fail(ctx, MI_E_ARG, "gather: dim of %lld", (long long)dims[dim]);
+  const size_t es = elem_size(xb->elem);
+  if (es != 4 && es != 2) return fail(ctx, MI_E_ARG, "gather of a %s buffer", elem_name(xb->elem));
+  const int64_t rows = idims[0] * idims[1] * idims[2], cols = idims[3];
+  const void *xp = xb->ptr;
+  const int32_t *ip = static_cast<const int32_t *>(ib->ptr);
+  mi_id id;
+  Buffer *ob;
+  int s = new_buffer(ctx, rows, cols, xb->elem, &id, &ob);
+  if (s) return s;
+  if (ni > 0) {
+    const unsigned g = grid_for(ni, 256, 256 * 64);
+    if (es == 4)
+      gather_dim_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint32_t *>(xp), dims[1], dims[2], dims[3],
+                                                               dim, dims[dim], ip, idims[1], idims[2], idims[3], ni,
+                                                               static_cast<uint32_t *>(ob->ptr), flags(ctx));
+    else
+      gather_dim_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>(static_cast<const uint16_t *>(xp), dims[1], dims[2], dims[3],
+                                                               dim, dims[dim], ip, idims[1], idims[2], idims[3], ni,
+                                                               static_cast<uint16_t *>(ob->ptr), flags(ctx));
+    s = check_launch(ctx, "gather");
+    if (s) {
+      mi_free(ctx, id);
+      return s;
+    }
+  }
+  *out = id;
+  return MI_OK;
+}
+
 extern "C" int mi_scatter_add_columns(mi_ctx *ctx, mi_id x, mi_id idx, mi_id v, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");

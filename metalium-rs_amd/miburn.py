@@ -146,6 +146,7 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into": [P, U64, U64],
         "mi_cast_bfp": [P, U64, c_int, ctypes.POINTER(U64)],
         "mi_decode_advance": [P, U64, U64, U64, U64],
+        "mi_gather": [P, U64, ctypes.POINTER(I64), c_int, U64, ctypes.POINTER(I64), Ip],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_select_rows_as": [P, U64, U64, c_int, Ip],
@@ -553,6 +554,13 @@ class Engine:
 
     def cast_float(self, a: int, out_elem: int) -> int:
         return self._out(self._lib.mi_cast, a, out_elem)
+
+    def gather(self, x: int, dims, dim: int, idx: int, idims) -> int:
+        """Burn's float_gather along `dim` of a rank <= 4 tensor (dims and the
+        index tensor's dims padded with leading 1s to four)."""
+        d = (ctypes.c_int64 * 4)(*dims)
+        di = (ctypes.c_int64 * 4)(*idims)
+        return self._out(self._lib.mi_gather, x, d, dim, idx, di)
 
     def decode_advance(self, next_ids: int, ids: int, pos: int, log: int) -> None:
         """A chained decode step's tail: ids <- next_ids, log[:, pos + 1] <-

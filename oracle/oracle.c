@@ -621,3 +621,28 @@ int or_bfp_round_trip(const float *x, int64_t rows, int64_t cols, int width, flo
   }
   return bad;
 }
+
+/* crates/burn-tt/src/ops.rs:1102-1160 (gather_native): Burn's float_gather
+ * along `dim` of a rank <= 4 row-major tensor of dims[4], raw 32-bit
+ * payloads; the output has the index tensor's dims idims[4].  Returns 1 if
+ * an index is out of range (its output is zero bits), 0 otherwise. */
+int or_gather(const uint32_t *x, const int64_t dims[4], int dim, const int32_t *idx, const int64_t idims[4],
+              uint32_t *out) {
+  int bad = 0;
+  for (int64_t a = 0; a < idims[0]; ++a)
+    for (int64_t b = 0; b < idims[1]; ++b)
+      for (int64_t c = 0; c < idims[2]; ++c)
+        for (int64_t d = 0; d < idims[3]; ++d) {
+          const int64_t e = ((a * idims[1] + b) * idims[2] + c) * idims[3] + d;
+          int64_t co[4] = {a, b, c, d};
+          const int32_t k = idx[e];
+          if (k < 0 || k >= dims[dim]) {
+            out[e] = 0;
+            bad = 1;
+            continue;
+          }
+          co[dim] = k;
+          out[e] = x[((co[0] * dims[1] + co[1]) * dims[2] + co[2]) * dims[3] + co[3]];
+        }
+  return bad;
+}

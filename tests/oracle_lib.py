@@ -50,6 +50,8 @@ def lib():
         L.or_bfp8_to_bf16.restype = ctypes.c_uint16
         L.or_bfp_round_trip.argtypes = [P, I64, I64, I, P, P]
         L.or_bfp_round_trip.restype = I
+        L.or_gather.argtypes = [P, ctypes.POINTER(I64), I, P, ctypes.POINTER(I64), P]
+        L.or_gather.restype = I
         _lib = L
     return _lib
 
@@ -239,3 +241,17 @@ def bfp_round_trip(x, width: int = 8):
     exps = np.empty((rows, (cols + 15) // 16), np.uint8)
     bad = lib().or_bfp_round_trip(_p(x), rows, cols, width, _p(out), _p(exps))
     return out, exps, bad
+
+
+def gather(x, dim: int, idx):
+    """Burn's gather along `dim` (rank <= 4), raw 32-bit payloads: (out with
+    idx's shape, 1 if an index was out of range)."""
+    x = np.ascontiguousarray(x)
+    assert x.dtype.itemsize == 4
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    pad = 4 - x.ndim
+    dims = (ctypes.c_int64 * 4)(*([1] * pad + list(x.shape)))
+    idims = (ctypes.c_int64 * 4)(*([1] * pad + list(idx.shape)))
+    out = np.empty(idx.shape, np.uint32)
+    bad = lib().or_gather(_p(x.view(np.uint32)), dims, dim + pad, _p(idx), idims, _p(out))
+    return out.view(x.dtype), bad

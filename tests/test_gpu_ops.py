@@ -1315,3 +1315,50 @@ def test_decode_advance_chains_on_the_device(engine):
     with pytest.raises(miburn.MiError) as e:  # mismatched rows are refused at the call
         engine.decode_advance(nxt, ids, pos, engine.upload_bits(np.zeros((B + 1, cols), np.int32), I32))
     assert e.value.kind == "ARG"
+
+
+@pytest.mark.parametrize("shape", [(7,), (5, 9), (3, 4, 6), (2, 3, 4, 5), (64, 3, 128)])
+def test_gather_along_any_dim(engine, shape):
+    """mi_gather (Burn's float_gather, ops.rs:1102-1160) along every dim
+    against the oracle, bit for bit, NaN / -0.0 / infinity payloads kept;
+    BF16 payloads gathered as they lie."""
+    rng = np.random.default_rng(len(shape) * 10 + shape[0])
+    x = rng.standard_normal(shape).astype(np.float32)
+    flat = x.reshape(-1)
+    flat[::7] = np.nan
+    flat[1::11] = -0.0
+    flat[2::13] = np.inf
+    pad = 4 - len(shape)
+    dims = [1] * pad + list(shape)
+    xid = engine.upload(x.reshape(-1, shape[-1]))
+    xb = engine.upload_bf16(orc.to_bf16(x.reshape(-1, shape[-1])))
+    for dim in range(len(shape)):
+        ishape = list(shape)
+        ishape[dim] = 3 + 2 * dim
+        idx = rng.integers(0, shape[dim], ishape).astype(np.int32)
+        iid = engine.upload_bits(idx.reshape(-1, ishape[-1]), I32)
+        idims = [1] * pad + ishape
+        got = engine.download(engine.gather(xid, dims, dim + pad, iid, idims))
+        want, bad = orc.gather(x, dim, idx)
+        assert bad == 0
+        assert np.array_equal(got.reshape(ishape).view(np.uint32), want.view(np.uint32)), dim
+        gb = engine.download(engine.gather(xb, dims, dim + pad, iid, idims))
+        wb = np.take_along_axis(orc.to_bf16(x), idx.astype(np.int64), dim)
+        assert np.array_equal(gb.reshape(ishape), wb), dim
+    engine.sync()
+
+
+def test_gather_errors(engine):
+    x = engine.upload(rnd(4, 5))
+    idx = np.zeros((4, 2), np.int32)
+    idx[2, 1] = 5
+    out = engine.gather(x, [1, 1, 4, 5], 3, engine.upload_bits(idx, I32), [1, 1, 4, 2])
+    with pytest.raises(miburn.MiError) as e:
+        engine.sync()
+    assert e.value.kind == "DOMAIN"
+    assert engine.download(out).view(np.uint32)[2, 1] == 0
+    for dims, dim, idims in (([1, 1, 4, 5], 4, [1, 1, 4, 2]), ([1, 1, 4, 5], 3, [1, 1, 3, 2]),
+                             ([1, 1, 4, 6], 3, [1, 1, 4, 2])):
+        with pytest.raises(miburn.MiError) as e:
+            engine.gather(x, dims, dim, engine.upload_bits(np.zeros((4, 2), np.int32), I32), idims)
+        assert e.value.kind == "ARG"
