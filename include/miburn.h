@@ -194,6 +194,17 @@ int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
  * none.  The result is F32, or BF16 rounded once after both adds. */
 int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias,
               mi_id residual, int out_elem, mi_id *out);
+/* mi_linear then mi_rms_norm of its result, in one call and bit for bit the
+ * two: `y` = residual + x op(w) + bias (F32 [m, n]) and `y_norm` =
+ * rms_norm(y) * gamma (eps; gamma F32 [1, n] or 0 for none) as `norm_elem`
+ * (MI_F32, MI_BF16 or MI_BF16_PARTS), n <= 8192.  Where the product splits
+ * over k (few output tiles: a short prompt's o and down projections) the
+ * split's reduce forms the norm as it writes y: one launch and one pass over
+ * y fewer.  The reference's Engine::add_rms_norm (server.rs:466-475) on a
+ * Linear's output and its residual; the fusion has no Engine counterpart. */
+int mi_linear_add_rms_norm(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed,
+                           mi_id bias, mi_id residual, mi_id gamma, float eps,
+                           int norm_elem, mi_id *y, mi_id *y_norm);
 /* mi_linear of an F32 `x` [m, k] given as its parts (MI_BF16_PARTS, a BF16
  * `x_parts` [m, 2 k]) against a BF16 `w`: the product runs as head . op(w) +
  * remainder . op(w), accumulated in F32 over the 2 k parts in that order --

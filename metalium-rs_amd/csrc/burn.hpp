@@ -13,6 +13,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/miburn.h"
@@ -233,6 +234,20 @@ inline Tensor linear(const Tensor &x, const Tensor &w, bool tw, const Tensor *bi
   check(x.ctx(), mi_linear(x.ctx(), x.use(), w.use(), tw, bias ? bias->use() : 0, residual ? residual->use() : 0,
                            out_elem, &id), "linear");
   return Tensor(x.ctx(), id, {x.rows(), tw ? w.rows() : w.cols()});
+}
+
+// linear() then rms_norm() of its result in one call: (y, rms_norm(y) gamma
+// as norm_elem).
+inline std::pair<Tensor, Tensor> linear_add_rms_norm(const Tensor &x, const Tensor &w, bool tw, const Tensor *bias,
+                                                     const Tensor *residual, const Tensor &gamma, float eps,
+                                                     int norm_elem) {
+  mi_id y, yn;
+  check(x.ctx(), mi_linear_add_rms_norm(x.ctx(), x.use(), w.use(), tw, bias ? bias->use() : 0,
+                                        residual ? residual->use() : 0, gamma.use(), eps, norm_elem, &y, &yn),
+        "linear_add_rms_norm");
+  const int64_t n = tw ? w.rows() : w.cols();
+  return {Tensor(x.ctx(), y, {x.rows(), n}),
+          Tensor(x.ctx(), yn, {x.rows(), norm_elem == MI_BF16_PARTS ? 2 * n : n})};
 }
 
 // linear() of an F32 operand given as its BF16 parts ([m, 2 k], MI_BF16_PARTS

@@ -265,6 +265,11 @@ int attention_scratch_setup(Ctx *ctx);
 // Zero `bytes` (a multiple of 2) at p with a kernel: safe inside a captured
 // trace, where a memset node is not.
 int fill_zero(Ctx *ctx, void *p, size_t bytes);
+// RMSNorm of R rows of C <= 8192 columns (x of kind xe, gain of kind ge or
+// null) into `out` as out_elem (F32, BF16 or MI_BF16_PARTS): mi_rms_norm's
+// launch.
+void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, float eps, void *out, int out_elem,
+                     int64_t R, int64_t C);
 // A new buffer holding the decoded values of BFP8 buffer `src` as `elem`
 // (MI_F32, or MI_BF16: exact either way); what a consumer without a BFP8
 // read of its own takes instead.  The caller frees it.

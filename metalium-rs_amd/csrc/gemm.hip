@@ -31,6 +31,7 @@
 //  * Shapes that are not multiples of the tile take a guarded variant
 //    (zero-filled loads, masked stores) of the same kernel.
 #include "common.hpp"
+#include "wave.hpp"
 
 namespace mi {
 
@@ -1288,6 +1289,86 @@ __global__ void splitk_reduce(const float *part, int S, int64_t mn, int64_t n, T
   else C[row * ldc + col] = s;
 }
 
+// splitk_reduce then mi_rms_norm's row kernel in one pass, bit for bit the
+// two: a wavefront a row, lane l owning columns l + 64 t; each value is the
+// slices added in slice order, then the bias, then the residual (stored as
+// the F32 result), and the row's sum of squares folds in the norm kernel's
+// order before each value is divided by the RMS and scaled by the gain.
+template <int T>
+__global__ void __launch_bounds__(256) splitk_reduce_norm(const float *part, int S, int64_t M, int64_t n, float *C,
+                                                          const float *bias, const float *resid, int64_t ldr,
+                                                          const float *gamma, float eps, void *yn, int yn_elem) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t mn = M * n;
+  // Every operand of the lane's columns is requested before the first add:
+  // the slices four at a time across all columns (clamped addresses, so the
+  // loads are unconditional), the gain, bias and residual with the first.
+  float v[T], gm[T], bv[T], rv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t, jc = j < n ? j : n - 1, i = row * n + jc;
+    v[t] = part[i];
+    gm[t] = gamma ? gamma[jc] : 1.0f;
+    bv[t] = bias ? bias[jc] : 0.0f;
+    rv[t] = resid ? resid[row * ldr + jc] : 0.0f;
+  }
+  for (int z0 = 1; z0 < S; z0 += 4) {
+    float p4[4][T];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int64_t j = lane + 64 * t, jc = j < n ? j : n - 1;
+        const int z = z0 + u < S ? z0 + u : S - 1;
+        p4[u][t] = part[z * mn + row * n + jc];
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (z0 + u < S) v[t] += p4[u][t];
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < n) {
+      float s = v[t];
+      if (bias) s = __fadd_rn(s, bv[t]);
+      if (resid) s = __fadd_rn(rv[t], s);
+      v[t] = s;
+      C[row * n + j] = s;
+    } else {
+      v[t] = 0.0f;
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < T; ++t) ss += v[t] * v[t];
+  ss = fold_sum<64>(ss);
+  const float rms = __fsqrt_rn(ss / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t j = lane + 64 * t;
+    if (j < n) {
+      float y = v[t] / rms;
+      if (gamma) y = y * gm[t];
+      if (yn_elem == MI_BF16_PARTS) {
+        uint16_t h, l;
+        split_bf16(y, h, l);
+        uint16_t *o = static_cast<uint16_t *>(yn) + 2 * row * n;
+        o[j] = h;
+        o[n + j] = l;
+      } else if (yn_elem == MI_BF16) {
+        static_cast<uint16_t *>(yn)[row * n + j] = f32_to_bf16_bits(y);
+      } else {
+        static_cast<float *>(yn)[row * n + j] = y;
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------- launching
 struct Plan {
   int64_t M, N, K, batch;
@@ -1309,6 +1390,14 @@ struct Plan {
   int64_t kb = 0;  // direct BF16 kernel: B's k extent when A's k repeats it (see GemmArgs)
   int swiglu = 0;  // direct BF16 kernel: gate|up pairs into silu(gate) * up (see GemmArgs)
   QkvTail qkv;     // direct BF16 kernel: the q|k|v tail (see QkvTail)
+  // The RMSNorm of the F32 result's rows (mi_linear_add_rms_norm): taken by
+  // the split-K reduce when the product splits over k (*norm_done set),
+  // else run after the product by the caller.
+  const float *norm_gamma = nullptr;
+  float norm_eps = 0.0f;
+  void *norm_out = nullptr;
+  int norm_elem = MI_F32;
+  bool *norm_done = nullptr;
 };
 
 template <typename T, typename SA, typename SB, typename TO, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool GUARD,
@@ -1691,6 +1780,29 @@ static hipError_t run_splitk(Plan p, float *part, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int64_t mn = p.M * p.N;
   const unsigned g = static_cast<unsigned>((mn + 255) / 256);
+  if (p.norm_out && eo == MI_F32 && ldc == p.N && p.N <= 2048 && p.batch == 1) {
+    const unsigned gr = static_cast<unsigned>((p.M + 3) / 4);
+    float *y = static_cast<float *>(final_c);
+    const int64_t n = p.N;
+#define MI_SRN(T) splitk_reduce_norm<T><<<gr, 256, 0, st>>>(part, p.splits, p.M, n, y, bias, resid, p.ldr, \
+                                                            p.norm_gamma, p.norm_eps, p.norm_out, p.norm_elem)
+    // T = ceil(n / 64) where instantiated (576, 768, 960, 1536 columns: 9,
+    // 12, 15, 24), else the next size up: no lane loads padded columns.
+    const int64_t t = (n + 63) / 64;
+    if (t <= 1) MI_SRN(1);
+    else if (t <= 2) MI_SRN(2);
+    else if (t <= 4) MI_SRN(4);
+    else if (t <= 8) MI_SRN(8);
+    else if (t <= 9) MI_SRN(9);
+    else if (t <= 12) MI_SRN(12);
+    else if (t <= 15) MI_SRN(15);
+    else if (t <= 16) MI_SRN(16);
+    else if (t <= 24) MI_SRN(24);
+    else MI_SRN(32);
+#undef MI_SRN
+    if (p.norm_done) *p.norm_done = true;
+    return hipGetLastError();
+  }
   if (eo == MI_BF16)
     splitk_reduce<uint16_t><<<g, 256, 0, st>>>(part, p.splits, mn, p.N, static_cast<uint16_t *>(final_c), ldc, bias,
                                                 resid, p.ldr);
@@ -1848,6 +1960,12 @@ struct LinearTerms {
   const float *bias = nullptr;
   const float *resid = nullptr;
   int64_t ldr = 0;
+  // mi_linear_add_rms_norm: the result rows' RMSNorm into norm_out (see Plan).
+  const float *norm_gamma = nullptr;
+  float norm_eps = 0.0f;
+  void *norm_out = nullptr;
+  int norm_elem = MI_F32;
+  bool *norm_done = nullptr;
 };
 
 static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t batch, int64_t m, int64_t k,
@@ -1913,6 +2031,8 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   }
   if (p.batch > 65535) return fail(ctx, MI_E_ARG, "batched matmul: batch %lld above 65535", (long long)p.batch);
   p.bias = lin.bias; p.resid = lin.resid; p.ldr = lin.ldr;
+  p.norm_gamma = lin.norm_gamma; p.norm_eps = lin.norm_eps; p.norm_out = lin.norm_out; p.norm_elem = lin.norm_elem;
+  p.norm_done = lin.norm_done;
   mi_id id; Buffer *cb;
   int s = new_buffer(ctx, p.batch * p.M, p.N, out_elem, &id, &cb);
   if (s) return s;
@@ -2053,6 +2173,61 @@ extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id 
   s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
   if (dw) mi_free(ctx, dw);
   return s;
+}
+
+extern "C" int mi_linear_add_rms_norm(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias, mi_id residual,
+                                      mi_id gamma, float eps, int norm_elem, mi_id *y, mi_id *y_norm) {
+  MI_ENTER(ctx);
+  if (!y || !y_norm) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, X, x);
+  MI_BUF(ctx, W, w);
+  if (norm_elem != MI_F32 && norm_elem != MI_BF16 && norm_elem != MI_BF16_PARTS)
+    return fail(ctx, MI_E_ARG, "linear_add_rms_norm: norm result kind %d", norm_elem);
+  const int64_t m = X->rows, n = w_transposed ? W->rows : W->cols;
+  const float *gp = nullptr;
+  if (gamma) {
+    MI_BUF(ctx, G, gamma);
+    if (G->elem != MI_F32 || G->numel() != n)
+      return fail(ctx, MI_E_ARG, "linear_add_rms_norm: gain is %s [%lld, %lld], want F32 with %lld elements",
+                  elem_name(G->elem), (long long)G->rows, (long long)G->cols, (long long)n);
+    gp = static_cast<const float *>(G->ptr);
+  }
+  if (n > 8192) return fail(ctx, MI_E_UNSUPPORTED, "linear_add_rms_norm: rows of %lld (at most 8192)", (long long)n);
+  LinearTerms lin;
+  int s = linear_terms(ctx, bias, residual, m, n, &lin);
+  if (s) return s;
+  const bool parts = norm_elem == MI_BF16_PARTS;
+  mi_id nid;
+  Buffer *nb;
+  if ((s = new_buffer(ctx, m, parts ? 2 * n : n, parts ? MI_BF16 : norm_elem, &nid, &nb))) return s;
+  bool done = false;
+  lin.norm_gamma = gp;
+  lin.norm_eps = eps;
+  lin.norm_out = nb->ptr;
+  lin.norm_elem = norm_elem;
+  lin.norm_done = &done;
+  mi_id dw, yid = 0;
+  if ((s = bfp8_operand(ctx, w, &dw))) {
+    mi_free(ctx, nid);
+    return s;
+  }
+  s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, MI_F32, &yid, lin);
+  if (dw) mi_free(ctx, dw);
+  if (s) {
+    mi_free(ctx, nid);
+    return s;
+  }
+  if (!done && m > 0 && n > 0) {  // the product did not split over k: the norm's own launch
+    rms_norm_launch(ctx, lookup(ctx, yid)->ptr, MI_F32, gp, MI_F32, eps, nb->ptr, norm_elem, m, n);
+    if ((s = check_launch(ctx, "linear_add_rms_norm"))) {
+      mi_free(ctx, yid);
+      mi_free(ctx, nid);
+      return s;
+    }
+  }
+  *y = yid;
+  *y_norm = nid;
+  return MI_OK;
 }
 
 extern "C" int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transposed, mi_id bias, mi_id residual,

@@ -27,6 +27,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/miburn_models.h"
@@ -225,8 +226,14 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   const bool parts_qkv = act == MI_F32 && parts_pay(ctx, rows, c.hidden, nqkv);
   const bool parts_gu = act == MI_F32 && parts_pay(ctx, rows, c.hidden, 2 * c.intermediate);
   const bool parts_down = act == MI_F32 && parts_pay(ctx, rows, c.intermediate, c.hidden);
-  for (Layer &L : m->layers) {
-    Tensor xn = burn::rms_norm(x, L.attn_norm, c.eps, parts_qkv ? MI_BF16_PARTS : act);
+  // A layer's attention norm comes with the previous layer's down product
+  // (mi_linear_add_rms_norm: where that product splits over k, a short
+  // prompt's, its reduce forms the norm; bit for bit the two calls).
+  Tensor xn_next;
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    Layer &L = m->layers[li];
+    Tensor xn = xn_next.defined() ? xn_next : burn::rms_norm(x, L.attn_norm, c.eps, parts_qkv ? MI_BF16_PARTS : act);
+    xn_next = Tensor();
     // One product against the fused q|k|v weight, then RoPE on q and k, k and
     // v appended to the caches at positions pos0.. of each (sequence, kv head)
     // item, and q laid out for the attention, in one launch: rows (sequence,
@@ -265,8 +272,10 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
       }
     }
     if (act != MI_F32) oh = burn::float_cast(oh, act);
-    x = burn::linear(oh, L.wo, true, nullptr, &x);  // x + oh wo^T, the add in the product's epilogue
-    Tensor hn = burn::rms_norm(x, L.mlp_norm, c.eps, parts_gu ? MI_BF16_PARTS : act);
+    // x + oh wo^T (the add in the product's epilogue), and its MLP norm.
+    Tensor hn;
+    std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.wo, true, nullptr, &x, L.mlp_norm, c.eps,
+                                                parts_gu ? MI_BF16_PARTS : act);
     // One product against the fused gate|up weight, silu(gate) * up of its halves.
     // With parts for both the gate|up and the down product, one launch forms
     // silu(gate) * up's parts from the interleaved weight (no F32 [rows,
@@ -285,7 +294,14 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
                            : burn::float_matmul(hn, false, L.wgu, true);
       h = burn::silu_mul_halves(gu, parts_down ? MI_BF16_PARTS : act);
     }
-    x = parts_down ? burn::linear_parts(h, L.wdown, true, nullptr, &x) : burn::linear(h, L.wdown, true, nullptr, &x);
+    if (parts_down) {
+      x = burn::linear_parts(h, L.wdown, true, nullptr, &x);
+    } else if (li + 1 < m->layers.size()) {
+      std::tie(x, xn_next) = burn::linear_add_rms_norm(h, L.wdown, true, nullptr, &x, m->layers[li + 1].attn_norm, c.eps,
+                                                       parts_qkv ? MI_BF16_PARTS : act);
+    } else {
+      x = burn::linear(h, L.wdown, true, nullptr, &x);
+    }
   }
   m->len = ctxlen;
   return x;

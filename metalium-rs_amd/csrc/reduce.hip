@@ -1008,6 +1008,18 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
   return MI_OK;
 }
 
+namespace mi {
+void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, float eps, void *out, int out_elem,
+                     int64_t R, int64_t C) {
+  const unsigned g = grid_for(R, 4, INT32_MAX);
+  switch (pick_t(C)) {
+#define MI_RN(T) case T: rms_norm_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
+    MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16) MI_RN(32) MI_RN(64) MI_RN(128)
+#undef MI_RN
+  }
+}
+}  // namespace mi
+
 extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
@@ -1031,14 +1043,7 @@ extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out
   const bool parts = out_elem == MI_BF16_PARTS;
   int s = new_buffer(ctx, R, parts ? 2 * C : C, parts ? MI_BF16 : out_elem, &id, &ob);
   if (s) return s;
-  if (R > 0 && C > 0) {
-    unsigned g = grid_for(R, 4, INT32_MAX);
-    switch (t) {
-#define MI_RN(T) case T: rms_norm_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, gp, ge, eps, ob->ptr, out_elem, R, C); break;
-      MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16) MI_RN(32) MI_RN(64) MI_RN(128)
-#undef MI_RN
-    }
-  }
+  if (R > 0 && C > 0) rms_norm_launch(ctx, xp, xe, gp, ge, eps, ob->ptr, out_elem, R, C);
   s = check_launch(ctx, "rms_norm");
   if (s) { mi_free(ctx, id); return s; }
   *out = id;

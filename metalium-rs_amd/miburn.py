@@ -147,6 +147,7 @@ def _load() -> ctypes.CDLL:
         "mi_cast_bfp": [P, U64, c_int, ctypes.POINTER(U64)],
         "mi_decode_advance": [P, U64, U64, U64, U64],
         "mi_gather": [P, U64, ctypes.POINTER(I64), c_int, U64, ctypes.POINTER(I64), Ip],
+        "mi_linear_add_rms_norm": [P, U64, U64, c_int, U64, U64, U64, c_float, c_int, Ip, Ip],
         "mi_get_matmul_mode": [P, ctypes.POINTER(c_int)],
         "mi_select_rows": [P, U64, U64, Ip],
         "mi_select_rows_as": [P, U64, U64, c_int, Ip],
@@ -299,6 +300,14 @@ class Engine:
     def linear(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, out_elem: int = F32) -> int:
         """residual + (x @ op(w) + bias) in one product; 0 omits a term."""
         return self._out(self._lib.mi_linear, x, w, int(w_t), bias, residual, out_elem)
+
+    def linear_add_rms_norm(self, x: int, w: int, w_t: bool, bias: int = 0, residual: int = 0, gamma: int = 0,
+                            eps: float = 1e-5, norm_elem: int = F32):
+        """mi_linear then mi_rms_norm of its result in one call: (y, y_norm)."""
+        y, yn = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(self._lib.mi_linear_add_rms_norm(self.ctx, x, w, int(w_t), bias, residual, gamma, eps, norm_elem,
+                                                     ctypes.byref(y), ctypes.byref(yn)))
+        return y.value, yn.value
 
     def linear_parts(self, x_parts: int, w: int, w_t: bool, bias: int = 0, residual: int = 0,
                      out_elem: int = F32) -> int:

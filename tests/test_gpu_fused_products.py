@@ -600,3 +600,32 @@ def test_sgd_folds_stacked_slices(engine):
     same_bits(engine.download(iq), (q - gsum * lr).astype(np.float32))
     with pytest.raises(miburn.MiError):
         engine.sgd_update([iq], [engine.upload(rnd(1, 10))], 0.1)  # 10 gradients for 7 parameters
+
+
+# (m, k, n, x kind): a short prompt's o and down projections (the product
+# splits over k, so the reduce forms the norm), and shapes that do not split.
+LIN_NORM_CASES = [(512, 576, 576, "f32"), (512, 1536, 576, "f32"), (512, 1536, 576, "bf16"), (64, 512, 1000, "f32"),
+                  (4096, 576, 576, "f32"), (4096, 1536, 576, "bf16"), (3, 576, 576, "f32")]
+
+
+@pytest.mark.parametrize("m,k,n,xk", LIN_NORM_CASES)
+@pytest.mark.parametrize("norm_elem", ["f32", "bf16", "parts"])
+def test_linear_add_rms_norm_equals_linear_then_norm(engine, m, k, n, xk, norm_elem):
+    """mi_linear_add_rms_norm: y and its RMSNorm bit for bit mi_linear then
+    mi_rms_norm, with and without bias and gain."""
+    ne = {"f32": miburn.F32, "bf16": miburn.BF16, "parts": miburn.BF16_PARTS}[norm_elem]
+    x32 = rnd(m, k)
+    x = engine.upload(x32) if xk == "f32" else engine.upload_bf16(orc.to_bf16(x32))
+    w = engine.upload_bf16(orc.to_bf16(rnd(n, k, scale=0.05)))
+    r = engine.upload(rnd(m, n))
+    g = engine.upload(rnd(1, n) + np.float32(1.0))
+    b = engine.upload(rnd(1, n, scale=0.1))
+    for bias, gamma in ((0, g), (b, 0)):
+        y, yn = engine.linear_add_rms_norm(x, w, True, bias=bias, residual=r, gamma=gamma, eps=1e-5, norm_elem=ne)
+        y2 = engine.linear(x, w, True, bias=bias, residual=r)
+        yn2 = engine.rms_norm(y2, gamma, 1e-5, ne)
+        same_bits(engine.download(y), engine.download(y2))
+        assert np.array_equal(engine.download(yn).view(np.uint32) if ne == miburn.F32 else engine.download(yn),
+                              engine.download(yn2).view(np.uint32) if ne == miburn.F32 else engine.download(yn2))
+        for t in (y, yn, y2, yn2):
+            engine.free(t)
