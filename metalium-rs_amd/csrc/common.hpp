@@ -43,16 +43,24 @@ inline bool elem_valid(int elem) { return (elem >= MI_F32 && elem <= MI_BF16) ||
 inline bool elem_float(int elem) { return elem == MI_F32 || elem == MI_BF16; }
 const char *elem_name(int elem);
 
-// BF16 <-> F32 on the device.  Narrowing rounds to nearest, ties to even, and
-// keeps a NaN a (quiet) NaN; widening is exact.
+// BF16 <-> F32 on the device.  Narrowing rounds to nearest, ties to even,
+// keeps subnormals (F32 denormals are on) and keeps a NaN a quiet NaN with
+// its sign and top payload bits: gfx950's v_cvt_pk_bf16_f32, whose result
+// for every one of the 2^32 F32 bit patterns u was checked on the device to
+// equal the integer form the host oracle uses -- (u >> 16) | 0x40 for a NaN,
+// else (u + 0x7fff + ((u >> 16) & 1)) >> 16.  Widening is exact.
+typedef __bf16 mi_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float mi_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
+// Two values narrowed in one instruction: a in the low half, b in the high.
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  const mi_f32x2 f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, mi_bf16x2));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>(bf16x2_bits(f, 0.0f));
 }
 
 // An F32 value as two BF16 parts, hi + lo within 2^-17 relative of it: hi
@@ -67,18 +75,33 @@ __device__ __forceinline__ void split_bf16(float a, uint16_t &hi, uint16_t &lo) 
   const float r = a - bf16_bits_to_f32(hi);
   lo = (r == r) ? f32_to_bf16_bits(r) : 0;
 }
+// split_bf16 of two values, their heads and remainders packed in pairs (a in
+// the low halves).  A head with an all-ones exponent (an infinity or NaN
+// input, or a finite one rounding to infinity) is rare: such a pair takes
+// split_bf16 per value.
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  const uint32_t h = bf16x2_bits(a, b);
+  if (__builtin_expect((h & 0x7f80u) == 0x7f80u || (h & 0x7f800000u) == 0x7f800000u, 0)) {
+    uint16_t h0, l0, h1, l1;
+    split_bf16(a, h0, l0);
+    split_bf16(b, h1, l1);
+    hi = uint32_t(h0) | (uint32_t(h1) << 16);
+    lo = uint32_t(l0) | (uint32_t(l1) << 16);
+    return;
+  }
+  hi = h;
+  lo = bf16x2_bits(a - __uint_as_float(h << 16), b - __uint_as_float(h & 0xffff0000u));
+}
 
 // Four consecutive F32 values of a row as parts: their heads at hp, their
 // remainders at lp (a row of MI_BF16_PARTS keeps its heads, then its
 // remainders).
 __device__ __forceinline__ void parts4_put(uint16_t *hp, uint16_t *lp, float4 v) {
-  uint16_t h[4], l[4];
-  split_bf16(v.x, h[0], l[0]);
-  split_bf16(v.y, h[1], l[1]);
-  split_bf16(v.z, h[2], l[2]);
-  split_bf16(v.w, h[3], l[3]);
-  *reinterpret_cast<uint2 *>(hp) = make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
-  *reinterpret_cast<uint2 *>(lp) = make_uint2(l[0] | (uint32_t(l[1]) << 16), l[2] | (uint32_t(l[3]) << 16));
+  uint32_t h0, l0, h1, l1;
+  split_bf16x2(v.x, v.y, h0, l0);
+  split_bf16x2(v.z, v.w, h1, l1);
+  *reinterpret_cast<uint2 *>(hp) = make_uint2(h0, h1);
+  *reinterpret_cast<uint2 *>(lp) = make_uint2(l0, l1);
 }
 
 // F32 values in F32 or BF16 (uint16_t bits) storage -- a KV cache under the
@@ -93,9 +116,7 @@ __device__ __forceinline__ float4 f32x4_get(const uint16_t *p) {
 }
 __device__ __forceinline__ void f32x4_put(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 __device__ __forceinline__ void f32x4_put(uint16_t *p, float4 v) {
-  const uint32_t a = f32_to_bf16_bits(v.x) | (static_cast<uint32_t>(f32_to_bf16_bits(v.y)) << 16);
-  const uint32_t b = f32_to_bf16_bits(v.z) | (static_cast<uint32_t>(f32_to_bf16_bits(v.w)) << 16);
-  *reinterpret_cast<uint2 *>(p) = make_uint2(a, b);
+  *reinterpret_cast<uint2 *>(p) = make_uint2(bf16x2_bits(v.x, v.y), bf16x2_bits(v.z, v.w));
 }
 __device__ __forceinline__ void f32_put(float *p, float v) { *p = v; }
 __device__ __forceinline__ void f32_put(uint16_t *p, float v) { *p = f32_to_bf16_bits(v); }

@@ -189,10 +189,7 @@ __device__ __forceinline__ void store4(void *out, int out_elem, int64_t flat, fl
   if (out_elem == MI_F32) {
     st4<NT>(static_cast<float *>(out) + flat, r);
   } else if (out_elem == MI_BF16) {
-    uint2 h;
-    h.x = uint32_t(f32_to_bf16_bits(r.x)) | (uint32_t(f32_to_bf16_bits(r.y)) << 16);
-    h.y = uint32_t(f32_to_bf16_bits(r.z)) | (uint32_t(f32_to_bf16_bits(r.w)) << 16);
-    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = h;
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + flat) = make_uint2(bf16x2_bits(r.x, r.y), bf16x2_bits(r.z, r.w));
   } else {
     uint4 m = make_uint4(r.x != 0.f, r.y != 0.f, r.z != 0.f, r.w != 0.f);
     stu4<NT>(static_cast<uint32_t *>(out) + flat, m);

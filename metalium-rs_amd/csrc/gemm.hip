@@ -515,32 +515,13 @@ struct SplitLoader {
   }
 
   // One chunk (8 k of one row) into the hi plane, and its remainders into the
-  // lo plane for an F32 source.  The narrowing is v_cvt_pk_bf16_f32 (round to
-  // nearest even, two values an instruction); a finite value whose head
-  // would round to infinity keeps its truncated head instead.
+  // lo plane for an F32 source (split_bf16x2: two values an instruction).
   __device__ __forceinline__ static void put(char *hi_plane, char *lo_plane, int r, int c, const S (&v)[8]) {
     Chunk h, l;
     if constexpr (SPLIT) {
       uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bf16x2 hv = {static_cast<__bf16>(v[2 * e]), static_cast<__bf16>(v[2 * e + 1])};
-        uint32_t hb = __builtin_bit_cast(uint32_t, hv);
-        // Overflow to infinity from a finite value: rare, fixed up per pair.
-        if (__builtin_expect((hb & 0x7f80u) == 0x7f80u || (hb & 0x7f800000u) == 0x7f800000u, 0)) {
-          uint16_t h0, l0, h1, l1;
-          split_bf16(v[2 * e], h0, l0);
-          split_bf16(v[2 * e + 1], h1, l1);
-          hw[e] = uint32_t(h0) | (uint32_t(h1) << 16);
-          lw[e] = uint32_t(l0) | (uint32_t(l1) << 16);
-          continue;
-        }
-        const float r0 = v[2 * e] - __uint_as_float(hb << 16);
-        const float r1 = v[2 * e + 1] - __uint_as_float(hb & 0xffff0000u);
-        const bf16x2 lv = {static_cast<__bf16>(r0), static_cast<__bf16>(r1)};
-        hw[e] = hb;
-        lw[e] = __builtin_bit_cast(uint32_t, lv);
-      }
+      for (int e = 0; e < 4; ++e) split_bf16x2(v[2 * e], v[2 * e + 1], hw[e], lw[e]);
       h.u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
       l.u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     } else {
@@ -1846,14 +1827,11 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const float *a, int64_t
     const float4 v0 = *reinterpret_cast<const float4 *>(a + r * lda + c);
     const float4 v1 = *reinterpret_cast<const float4 *>(a + r * lda + c + 4);
     const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    uint16_t h[8], l[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) split_bf16(v[e], h[e], l[e]);
     uint4 hv, lv;
-    hv.x = h[0] | (uint32_t(h[1]) << 16); hv.y = h[2] | (uint32_t(h[3]) << 16);
-    hv.z = h[4] | (uint32_t(h[5]) << 16); hv.w = h[6] | (uint32_t(h[7]) << 16);
-    lv.x = l[0] | (uint32_t(l[1]) << 16); lv.y = l[2] | (uint32_t(l[3]) << 16);
-    lv.z = l[4] | (uint32_t(l[5]) << 16); lv.w = l[6] | (uint32_t(l[7]) << 16);
+    split_bf16x2(v[0], v[1], hv.x, lv.x);
+    split_bf16x2(v[2], v[3], hv.y, lv.y);
+    split_bf16x2(v[4], v[5], hv.z, lv.z);
+    split_bf16x2(v[6], v[7], hv.w, lv.w);
     *reinterpret_cast<uint4 *>(out + r * 2 * K + c) = hv;
     *reinterpret_cast<uint4 *>(out + r * 2 * K + K + c) = lv;
   }
