@@ -61,8 +61,23 @@ enum mi_elem { MI_F32 = 0, MI_I32 = 1, MI_BOOL = 2, MI_BF16 = 3, MI_BFP8 = 5 };
  * form of the fast matmul mode's split of F32 activations (a product taken as
  * head . w + remainder . w); mi_rms_norm and mi_silu_mul_halves produce it as
  * their `out_elem`, mi_linear_parts reads it, so a producer's F32 result
- * reaches the product with no separate split pass.  No Engine counterpart. */
-enum mi_result_form { MI_BF16_PARTS = 4 };
+ * reaches the product with no separate split pass.  No Engine counterpart.
+ *
+ * MI_TILES_BF16 / MI_TILES_PARTS: an [r, c] operand (r a multiple of 32, c of
+ * 16) in the matrix cores' operand order ("tiles"), the form mi_linear's
+ * short-row path reads: blocks of 32 rows x 16 columns, block (t, s) at
+ * element ((t (c / 16) + s) 64 + l) 8, its lane l holding row 32 t + l % 32,
+ * columns 16 s + 8 (l / 32) .. + 7 -- the registers of one
+ * v_mfma_f32_32x32x16_bf16 step, so each step's operand is one contiguous
+ * KiB.  MI_TILES_BF16: the BF16 values (an F32 source rounded to nearest
+ * even), a BF16 buffer [r, c]; MI_TILES_PARTS: an F32 value's two parts (as
+ * MI_BF16_PARTS) in two planes, the heads' tiles then the remainders', a
+ * BF16 buffer [r, 2 c].  A buffer holding tiles is marked so: mi_linear,
+ * mi_linear_swiglu and mi_linear_qkv_rope_cache read a tiled weight (and
+ * tiled activations) with it, mi_matmul and mi_reshape refuse it, and other
+ * ops see its datums as BF16 values in that order.  No Engine counterpart
+ * (the reference's weights are tiled for its cores by tt-layout). */
+enum mi_result_form { MI_BF16_PARTS = 4, MI_TILES_BF16 = 6, MI_TILES_PARTS = 7 };
 
 /* Status codes.  `MI_E_DOMAIN` is the reference's DOMAIN error for an index
  * out of range (crates/burn-tt/src/ops.rs:995-1000). */
@@ -191,9 +206,27 @@ int mi_matmul_slices(mi_ctx *ctx, mi_id a, int a_transposed, mi_id b,
  * float_add (ops.rs:159), and a residual connection as another float_add.
  * `x` is `[m, k]` (F32 or BF16), `w` is `[k, n]` or, transposed, `[n, k]`;
  * `bias` (F32, n elements) and `residual` (F32 `[m, n]`) may each be 0 for
- * none.  The result is F32, or BF16 rounded once after both adds. */
+ * none.  The result is F32, or BF16 rounded once after both adds.
+ *
+ * A weight in tiles (mi_tile of a BF16 [n, k] weight; w_transposed 1) takes
+ * the short-row path (a batch-1 prefill's products: few output tiles, so the
+ * k range is split over the waves of a block instead of over launches):
+ * each wave loads its k steps of both operands straight into the matrix
+ * cores' registers, sums its range in k order, and the block adds the
+ * ranges in order -- one fixed order for a given (m, n, k), not the other
+ * kernels'.  `x` is then F32 [m, k] (its parts' products, as the fast
+ * matmul mode splits it; the accurate mode refuses it), BF16 [m, k], or
+ * tiles of an [m, k] operand (MI_TILES_PARTS: the parts' products;
+ * MI_TILES_BF16).  m a multiple of 32, n of 32, k of 16 and at most 3072
+ * (else MI_E_UNSUPPORTED). */
 int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id bias,
               mi_id residual, int out_elem, mi_id *out);
+/* A row-major F32 or BF16 `a` [r, c] (r a multiple of 32, c of 16) in tiles:
+ * `form` MI_TILES_BF16 (BF16 values; F32 rounded to nearest even) or
+ * MI_TILES_PARTS (an F32 source's parts).  A weight is tiled once, where it
+ * is made; activations come in tiles from their producers (mi_rms_norm,
+ * mi_linear_swiglu).  No Engine counterpart. */
+int mi_tile(mi_ctx *ctx, mi_id a, int form, mi_id *out);
 /* mi_linear then mi_rms_norm of its result, in one call and bit for bit the
  * two: `y` = residual + x op(w) + bias (F32 [m, n]) and `y_norm` =
  * rms_norm(y) * gamma (eps; gamma F32 [1, n] or 0 for none) as `norm_elem`
@@ -234,7 +267,14 @@ int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
  * contract's operands): silu(x gate^T) * (x up^T) [m, i] as F32, or rounded
  * once to BF16 (`out_elem`) -- the same bits as the BF16 product against
  * [gate; up] on the direct kernel followed by mi_silu_mul_halves.  Whole
- * tiles only, as mi_linear_swiglu_parts. */
+ * tiles only, as mi_linear_swiglu_parts.
+ *
+ * With `w_pairs` in tiles (mi_tile of the interleaved weight), mi_linear's
+ * short-row path: `x` F32, BF16 or tiles as there, each product's sums as
+ * mi_linear forms them against the same tiled weight, silu * up as
+ * MI_K_SILU_MUL; `out_elem` MI_F32, MI_BF16, MI_BF16_PARTS, or tiles of the
+ * [m, i] result (MI_TILES_BF16 / MI_TILES_PARTS: the down product's operand
+ * as it reads it).  m a multiple of 32, i of 32. */
 int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_elem,
                      mi_id *out);
 /* The q|k|v product and mi_qkv_rope_cache in one launch: `x` BF16 [rows, k]
@@ -244,7 +284,10 @@ int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_elem,
  * the product's accumulators -- the same bits as the product (mi_matmul /
  * mi_linear_parts) followed by mi_qkv_rope_cache, without the F32 q|k|v
  * rows between them.  64-wide heads, rows a multiple of 128 and k of 32
- * (else MI_E_UNSUPPORTED).  No Engine counterpart (the reference's
+ * (else MI_E_UNSUPPORTED).  With `w_qkv` in tiles, mi_linear's short-row
+ * path (`x` F32, BF16 or tiles as there, `x_parts` 0; rows a multiple of
+ * 32): the same bits as mi_linear against that tiled weight followed by
+ * mi_qkv_rope_cache.  No Engine counterpart (the reference's
  * attention block, crates/tt-models/src/llama.rs:403-446, runs the
  * projection, RoPE and the cache writes as separate ops). */
 int mi_linear_qkv_rope_cache(mi_ctx *ctx, mi_id x, int x_parts, mi_id w_qkv,
@@ -344,8 +387,9 @@ int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, int log,
 
 /* ---- RMSNorm: Engine::rms_norm_as (server.rs:449) ----
  * `a / sqrt(mean(a * a) + eps) * gamma` over each row; `gamma` a `[1, cols]`
- * row or 0.  `out_elem` MI_F32, MI_BF16 or MI_BF16_PARTS (the F32 result's
- * parts, [rows, 2 cols] BF16). */
+ * row or 0.  `out_elem` MI_F32, MI_BF16, MI_BF16_PARTS (the F32 result's
+ * parts, [rows, 2 cols] BF16), or tiles of the result (MI_TILES_BF16 /
+ * MI_TILES_PARTS; rows a multiple of 32, cols of 16). */
 int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out_elem,
                 mi_id *out);
 /* Engine::add_rms_norm (server.rs:466-475): `sum = a + b` and

@@ -156,6 +156,16 @@ inline Tensor empty(mi_ctx *ctx, std::vector<int64_t> shape, int elem = MI_F32) 
   return Tensor(ctx, id, std::move(shape));
 }
 
+// Result forms holding an F32 result's two BF16 parts ([rows, 2 cols]).
+inline bool two_parts(int form) { return form == MI_BF16_PARTS || form == MI_TILES_PARTS; }
+
+// A row-major [r, c] operand in the matrix cores' operand order (mi_tile).
+inline Tensor tile(const Tensor &a, int form) {
+  mi_id id;
+  check(a.ctx(), mi_tile(a.ctx(), a.use(), form, &id), "tile");
+  return Tensor(a.ctx(), id, {a.rows(), form == MI_TILES_PARTS ? 2 * a.cols() : a.cols()});
+}
+
 inline Tensor float_cast(const Tensor &a, int elem) {
   mi_id id;
   check(a.ctx(), mi_cast(a.ctx(), a.use(), elem, &id), "float_cast");
@@ -246,8 +256,7 @@ inline std::pair<Tensor, Tensor> linear_add_rms_norm(const Tensor &x, const Tens
                                         residual ? residual->use() : 0, gamma.use(), eps, norm_elem, &y, &yn),
         "linear_add_rms_norm");
   const int64_t n = tw ? w.rows() : w.cols();
-  return {Tensor(x.ctx(), y, {x.rows(), n}),
-          Tensor(x.ctx(), yn, {x.rows(), norm_elem == MI_BF16_PARTS ? 2 * n : n})};
+  return {Tensor(x.ctx(), y, {x.rows(), n}), Tensor(x.ctx(), yn, {x.rows(), two_parts(norm_elem) ? 2 * n : n})};
 }
 
 // linear() of an F32 operand given as its BF16 parts ([m, 2 k], MI_BF16_PARTS
@@ -272,7 +281,7 @@ inline Tensor linear_swiglu_parts(const Tensor &x_parts, const Tensor &w_pairs) 
 inline Tensor linear_swiglu(const Tensor &x, const Tensor &w_pairs, int out_elem) {
   mi_id id;
   check(x.ctx(), mi_linear_swiglu(x.ctx(), x.use(), w_pairs.use(), out_elem, &id), "linear_swiglu");
-  return Tensor(x.ctx(), id, {x.rows(), w_pairs.rows() / 2});
+  return Tensor(x.ctx(), id, {x.rows(), two_parts(out_elem) ? w_pairs.rows() : w_pairs.rows() / 2});
 }
 
 // The q|k|v product and the prefill's q|k|v tail in one launch
@@ -333,7 +342,7 @@ inline Tensor softmax_rows(const Tensor &x, const Tensor *mask, float scale, boo
 inline Tensor rms_norm(const Tensor &x, const Tensor &gamma, float eps, int out_elem = MI_F32) {
   mi_id id;
   check(x.ctx(), mi_rms_norm(x.ctx(), x.use(), gamma.use(), eps, out_elem, &id), "rms_norm");
-  if (out_elem == MI_BF16_PARTS) return Tensor(x.ctx(), id, {x.rows(), 2 * x.cols()});
+  if (two_parts(out_elem)) return Tensor(x.ctx(), id, {x.rows(), 2 * x.cols()});
   return Tensor(x.ctx(), id, x.shape());
 }
 

@@ -121,6 +121,13 @@ __device__ __forceinline__ void f32x4_put(uint16_t *p, float4 v) {
 __device__ __forceinline__ void f32_put(float *p, float v) { *p = v; }
 __device__ __forceinline__ void f32_put(uint16_t *p, float v) { *p = f32_to_bf16_bits(v); }
 
+// Element (r, k) of an [R, K] operand in tiles (MI_TILES_BF16 / one plane of
+// MI_TILES_PARTS): block (r / 32, k / 16) of 64 lanes x 8 values, lane
+// r % 32 + 32 ((k / 8) % 2), value k % 8.
+__device__ __host__ __forceinline__ int64_t tile_offset(int64_t r, int64_t k, int64_t K) {
+  return (((r >> 5) * (K >> 4) + (k >> 4)) * 64 + (r & 31) + 32 * ((k >> 3) & 1)) * 8 + (k & 7);
+}
+
 // The logistic function in its two-branch form, so neither exponential
 // overflows: 1 / (1 + e^-x) for x >= 0 and e^x / (1 + e^x) below.  Both
 // quotients share t = e^-|x| (which is e^-x above zero and e^x below), so it
@@ -203,6 +210,7 @@ struct Buffer {
   int64_t rows = 0, cols = 0;
   int elem = MI_F32;
   uint64_t trace = 0;  // the trace whose capture allocated it (its memory is the trace's until released)
+  int tiles = 0;       // MI_TILES_BF16 / MI_TILES_PARTS: datums in the matrix cores' operand order; 0 row-major
   int64_t numel() const { return rows * cols; }
   size_t storage() const { return storage_bytes(elem, rows, cols); }
 };

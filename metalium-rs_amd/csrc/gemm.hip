@@ -31,6 +31,7 @@
 //  * Shapes that are not multiples of the tile take a guarded variant
 //    (zero-filled loads, masked stores) of the same kernel.
 #include "common.hpp"
+#include "tails.hpp"
 #include "wave.hpp"
 
 namespace mi {
@@ -209,22 +210,6 @@ struct TileLoader {
   }
 };
 
-enum { SWIGLU_PARTS = 1, SWIGLU_BF16 = 2, SWIGLU_F32 = 3 };
-// A prefill's q|k|v tail in the direct kernel's epilogue (64-wide heads, the
-// product's columns (heads + 2 kv heads) x 64, its rows (sequence,
-// position)): RoPE on the q and k heads at position pos0 + p, q written to
-// row (b seq + p) heads + h or, grouped, ((b kv + j) seq + p) G + g, k and v
-// to cache row (b kv + j) maxc + pos0 + p -- mi_qkv_rope_cache's layout and
-// arithmetic.  mode 0: none; QKV_F32 / QKV_BF16: the caches' element.
-enum { QKV_F32 = 1, QKV_BF16 = 2 };
-struct QkvTail {
-  int mode = 0;
-  const float *cos = nullptr, *sin = nullptr;
-  float *q = nullptr;
-  void *kc = nullptr, *vc = nullptr;
-  int64_t seq = 1, pos0 = 0, maxc = 0;
-  int heads = 0, kvh = 1, grouped = 0;
-};
 struct GemmArgs {
   const void *a;
   const void *b;
@@ -900,7 +885,7 @@ __device__ __forceinline__ void qkv_tail(const GemmArgs &g, const f32x16 (&acc)[
                                          int j) {
   const QkvTail &t = g.qkv;
   if (hb >= g.N) return;  // an edge tile's columns past the last head
-  const int h = static_cast<int>(hb >> 6), G = t.heads / t.kvh;
+  const int h = static_cast<int>(hb >> 6);
   const bool rope = h < t.heads + t.kvh;
   // A fragment's 32 rows (32-aligned) lie in one sequence when seq is a
   // multiple of 32: one division a fragment, not two a value.
@@ -937,31 +922,9 @@ __device__ __forceinline__ void qkv_tail(const GemmArgs &g, const f32x16 (&acc)[
       const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
       int64_t b, p;
       seq_of(row, b, p);
-      const int64_t pos = t.pos0 + p;
-      const float x0 = acc[i][0][r], x1 = acc[i][1][r];
-      float y0 = x0, y1 = x1;
-      if (rope) {
-        y0 = __fadd_rn(__fmul_rn(x0, c0[r]), __fmul_rn(x1, s0[r]));
-        y1 = __fadd_rn(__fmul_rn(x1, c1[r]), __fmul_rn(x0, s1[r]));
-      }
-      if (h < t.heads) {
-        const int kvh = h / G, gg = h - kvh * G;
-        const int64_t qrow = t.grouped ? ((b * t.kvh + kvh) * t.seq + p) * G + gg : row * t.heads + h;
-        t.q[qrow * 64 + j] = y0;
-        t.q[qrow * 64 + j + 32] = y1;
-      } else {
-        const bool isk = rope;
-        const int64_t crow = (b * t.kvh + (isk ? h - t.heads : h - t.heads - t.kvh)) * t.maxc + pos;
-        if (t.mode == QKV_BF16) {
-          uint16_t *c = static_cast<uint16_t *>(isk ? t.kc : t.vc) + crow * 64;
-          c[j] = f32_to_bf16_bits(y0);
-          c[j + 32] = f32_to_bf16_bits(y1);
-        } else {
-          float *c = static_cast<float *>(isk ? t.kc : t.vc) + crow * 64;
-          c[j] = y0;
-          c[j + 32] = y1;
-        }
-      }
+      float y0 = acc[i][0][r], y1 = acc[i][1][r];
+      if (rope) rope_pair(acc[i][0][r], acc[i][1][r], c0[r], c1[r], s0[r], s1[r], y0, y1);
+      qkv_put(t, row, b, p, h, j, y0, y1);
     }
   }
 }
@@ -1105,7 +1068,7 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
           for (int r = 0; r < 16; ++r) {
             const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
             const float gt = acc[i][2 * jp][r], up = acc[i][2 * jp + 1][r];
-            const float y = (gt * sigmoid2(gt)) * up;
+            const float y = swiglu_value(gt, up);
             if (g.swiglu == SWIGLU_PARTS) {
               uint16_t h, l;
               split_bf16(y, h, l);
@@ -1956,6 +1919,7 @@ static int matmul_common(mi_ctx *ctx, mi_id a, int ta, mi_id b, int tb, int64_t 
   MI_BUF(ctx, B, b);
   if (!elem_float(A->elem) || !elem_float(B->elem))
     return fail(ctx, MI_E_ARG, "matmul of %s and %s", elem_name(A->elem), elem_name(B->elem));
+  if (A->tiles || B->tiles) return fail(ctx, MI_E_ARG, "matmul of an operand in tiles (mi_linear reads them)");
   if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "matmul result kind %s", elem_name(out_elem));
   Plan p;
   p.ta = ta != 0; p.tb = tb != 0;
@@ -2146,6 +2110,11 @@ extern "C" int mi_linear(mi_ctx *ctx, mi_id x, mi_id w, int w_transposed, mi_id 
   LinearTerms lin;
   int s = linear_terms(ctx, bias, residual, m, n, &lin);
   if (s) return s;
+  if (W->tiles) {
+    if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+    if (!w_transposed) return fail(ctx, MI_E_ARG, "linear: a weight in tiles is [n, k] (w_transposed 1)");
+    return tiles_linear(ctx, x, w, lin.bias, lin.resid, out_elem, out);
+  }
   mi_id dw;
   if ((s = bfp8_operand(ctx, w, &dw))) return s;
   s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, out_elem, out, lin);
@@ -2159,7 +2128,8 @@ extern "C" int mi_linear_add_rms_norm(mi_ctx *ctx, mi_id x, mi_id w, int w_trans
   if (!y || !y_norm) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, X, x);
   MI_BUF(ctx, W, w);
-  if (norm_elem != MI_F32 && norm_elem != MI_BF16 && norm_elem != MI_BF16_PARTS)
+  if (norm_elem != MI_F32 && norm_elem != MI_BF16 && norm_elem != MI_BF16_PARTS && norm_elem != MI_TILES_BF16 &&
+      norm_elem != MI_TILES_PARTS)
     return fail(ctx, MI_E_ARG, "linear_add_rms_norm: norm result kind %d", norm_elem);
   const int64_t m = X->rows, n = w_transposed ? W->rows : W->cols;
   const float *gp = nullptr;
@@ -2174,22 +2144,35 @@ extern "C" int mi_linear_add_rms_norm(mi_ctx *ctx, mi_id x, mi_id w, int w_trans
   LinearTerms lin;
   int s = linear_terms(ctx, bias, residual, m, n, &lin);
   if (s) return s;
-  const bool parts = norm_elem == MI_BF16_PARTS;
+  const bool tiled = norm_elem == MI_TILES_BF16 || norm_elem == MI_TILES_PARTS;
+  const bool parts = norm_elem == MI_BF16_PARTS || norm_elem == MI_TILES_PARTS;
+  if (tiled && (m % 32 || n % 16))
+    return fail(ctx, MI_E_ARG, "linear_add_rms_norm: tiles of [%lld, %lld] (rows a multiple of 32, columns of 16)",
+                (long long)m, (long long)n);
+  if (W->tiles && !w_transposed)
+    return fail(ctx, MI_E_ARG, "linear_add_rms_norm: a weight in tiles is [n, k] (w_transposed 1)");
   mi_id nid;
   Buffer *nb;
-  if ((s = new_buffer(ctx, m, parts ? 2 * n : n, parts ? MI_BF16 : norm_elem, &nid, &nb))) return s;
+  if ((s = new_buffer(ctx, m, parts ? 2 * n : n, parts || tiled ? MI_BF16 : norm_elem, &nid, &nb))) return s;
+  nb->tiles = tiled ? norm_elem : 0;
   bool done = false;
-  lin.norm_gamma = gp;
-  lin.norm_eps = eps;
-  lin.norm_out = nb->ptr;
-  lin.norm_elem = norm_elem;
-  lin.norm_done = &done;
-  mi_id dw, yid = 0;
-  if ((s = bfp8_operand(ctx, w, &dw))) {
-    mi_free(ctx, nid);
-    return s;
+  if (!tiled) {  // the split-K reduce forms the row-major forms
+    lin.norm_gamma = gp;
+    lin.norm_eps = eps;
+    lin.norm_out = nb->ptr;
+    lin.norm_elem = norm_elem;
+    lin.norm_done = &done;
   }
-  s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, MI_F32, &yid, lin);
+  mi_id dw = 0, yid = 0;
+  if (W->tiles) {
+    s = tiles_linear(ctx, x, w, lin.bias, lin.resid, MI_F32, &yid);
+  } else {
+    if ((s = bfp8_operand(ctx, w, &dw))) {
+      mi_free(ctx, nid);
+      return s;
+    }
+    s = matmul_common(ctx, x, 0, dw ? dw : w, w_transposed, 1, 0, 0, 0, 0, nullptr, MI_F32, &yid, lin);
+  }
   if (dw) mi_free(ctx, dw);
   if (s) {
     mi_free(ctx, nid);
@@ -2214,9 +2197,9 @@ extern "C" int mi_linear_parts(mi_ctx *ctx, mi_id x_parts, mi_id w, int w_transp
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, X, x_parts);
   MI_BUF(ctx, W, w);
-  if (X->elem != MI_BF16 || X->cols % 2)
-    return fail(ctx, MI_E_ARG, "linear_parts: parts are %s [%lld, %lld], want BF16 [m, 2 k]", elem_name(X->elem),
-                (long long)X->rows, (long long)X->cols);
+  if (X->elem != MI_BF16 || X->cols % 2 || X->tiles || W->tiles)
+    return fail(ctx, MI_E_ARG, "linear_parts: parts are %s [%lld, %lld]%s, want BF16 [m, 2 k] rows (tiles go to mi_linear)",
+                elem_name(X->elem), (long long)X->rows, (long long)X->cols, X->tiles || W->tiles ? " in tiles" : "");
   if (W->elem != MI_BF16) return fail(ctx, MI_E_ARG, "linear_parts: weight is %s, want BF16", elem_name(W->elem));
   if (out_elem != MI_F32 && out_elem != MI_BF16)
     return fail(ctx, MI_E_ARG, "linear_parts result kind %s", elem_name(out_elem));
@@ -2280,8 +2263,8 @@ extern "C" int mi_linear_swiglu_parts(mi_ctx *ctx, mi_id x_parts, mi_id w_pairs,
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, X, x_parts);
   MI_BUF(ctx, W, w_pairs);
-  if (X->elem != MI_BF16 || X->cols % 2 || W->elem != MI_BF16)
-    return fail(ctx, MI_E_ARG, "linear_swiglu_parts: parts %s [%lld, %lld] and weight %s, want BF16 [m, 2 k] and BF16",
+  if (X->elem != MI_BF16 || X->cols % 2 || W->elem != MI_BF16 || X->tiles || W->tiles)
+    return fail(ctx, MI_E_ARG, "linear_swiglu_parts: parts %s [%lld, %lld] and weight %s, want BF16 [m, 2 k] and BF16 rows",
                 elem_name(X->elem), (long long)X->rows, (long long)X->cols, elem_name(W->elem));
   const int64_t m = X->rows, k = X->cols / 2, n = W->rows;
   if (W->cols != k)
@@ -2321,7 +2304,8 @@ extern "C" int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_ele
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, X, x);
   MI_BUF(ctx, W, w_pairs);
-  if (X->elem != MI_BF16 || W->elem != MI_BF16)
+  if (W->tiles) return tiles_swiglu(ctx, x, w_pairs, out_elem, out);
+  if (X->elem != MI_BF16 || W->elem != MI_BF16 || X->tiles)
     return fail(ctx, MI_E_ARG, "linear_swiglu: x %s and weight %s, want BF16", elem_name(X->elem), elem_name(W->elem));
   if (out_elem != MI_F32 && out_elem != MI_BF16)
     return fail(ctx, MI_E_ARG, "linear_swiglu result kind %d", out_elem);
@@ -2358,6 +2342,55 @@ extern "C" int mi_linear_swiglu(mi_ctx *ctx, mi_id x, mi_id w_pairs, int out_ele
   return MI_OK;
 }
 
+// mi_linear_qkv_rope_cache against a weight in tiles: the same checks of
+// the tables and caches, then the short-row kernel with the tail.
+static int linear_qkv_tiles(mi_ctx *ctx, const Buffer *X, const Buffer *W, const Buffer *cb, const Buffer *sb, int64_t seq,
+                            int64_t heads, int64_t kv_heads, int64_t pos0, const Buffer *kb, const Buffer *vb,
+                            int grouped, mi_id x, mi_id w_qkv, mi_id *q_out) {
+  if (cb->elem != MI_F32 || sb->elem != MI_F32 || kb->elem != vb->elem || !elem_float(kb->elem))
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache takes F32 tables and two F32 or two BF16 caches");
+  const int64_t R = X->rows, D = kb->cols;
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: %lld heads over %lld kv heads", (long long)heads,
+                (long long)kv_heads);
+  if (D != 64)
+    return fail(ctx, MI_E_UNSUPPORTED, "linear_qkv_rope_cache: head width %lld (64-wide heads)", (long long)D);
+  if (W->rows != (heads + 2 * kv_heads) * D)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: weight [%lld, %lld], want [(heads + 2 kv_heads) %lld, k]",
+                (long long)W->rows, (long long)W->cols, (long long)D);
+  if (seq < 1 || R % seq)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: %lld rows are not sequences of %lld", (long long)R, (long long)seq);
+  const int64_t batch = R / seq;
+  if (vb->cols != D || vb->rows != kb->rows || kb->rows % (batch * kv_heads))
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: caches must both be [%lld * %lld * max_ctx, %lld]",
+                (long long)batch, (long long)kv_heads, (long long)D);
+  const int64_t maxc = kb->rows / (batch * kv_heads);
+  if (pos0 < 0 || pos0 + seq > maxc)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: positions [%lld, %lld) beyond the cache's %lld", (long long)pos0,
+                (long long)(pos0 + seq), (long long)maxc);
+  if (cb->cols != D || sb->cols != D || cb->rows != sb->rows || pos0 + seq > cb->rows)
+    return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: rope tables [%lld, %lld] for positions below %lld",
+                (long long)cb->rows, (long long)cb->cols, (long long)(pos0 + seq));
+  mi_id id;
+  Buffer *ob;
+  if (int s = new_buffer(ctx, R * heads, D, MI_F32, &id, &ob)) return s;
+  QkvTail t;
+  t.mode = kb->elem == MI_BF16 ? QKV_BF16 : QKV_F32;
+  t.cos = static_cast<const float *>(cb->ptr);
+  t.sin = static_cast<const float *>(sb->ptr);
+  t.q = static_cast<float *>(ob->ptr);
+  t.kc = kb->ptr;
+  t.vc = vb->ptr;
+  t.seq = seq; t.pos0 = pos0; t.maxc = maxc;
+  t.heads = static_cast<int>(heads); t.kvh = static_cast<int>(kv_heads); t.grouped = grouped != 0;
+  if (int s = tiles_qkv(ctx, x, w_qkv, t)) {
+    mi_free(ctx, id);
+    return s;
+  }
+  *q_out = id;
+  return MI_OK;
+}
+
 extern "C" int mi_linear_qkv_rope_cache(mi_ctx *ctx, mi_id x, int x_parts, mi_id w_qkv, mi_id cos_table,
                                         mi_id sin_table, int64_t seq, int64_t heads, int64_t kv_heads, int64_t pos0,
                                         mi_id k_cache, mi_id v_cache, int grouped, mi_id *q_out) {
@@ -2369,7 +2402,8 @@ extern "C" int mi_linear_qkv_rope_cache(mi_ctx *ctx, mi_id x, int x_parts, mi_id
   MI_BUF(ctx, sb, sin_table);
   MI_BUF(ctx, kb, k_cache);
   MI_BUF(ctx, vb, v_cache);
-  if (X->elem != MI_BF16 || W->elem != MI_BF16 || (x_parts && X->cols % 2))
+  if (W->tiles) return linear_qkv_tiles(ctx, X, W, cb, sb, seq, heads, kv_heads, pos0, kb, vb, grouped, x, w_qkv, q_out);
+  if (X->elem != MI_BF16 || W->elem != MI_BF16 || (x_parts && X->cols % 2) || X->tiles)
     return fail(ctx, MI_E_ARG, "linear_qkv_rope_cache: x %s [%lld, %lld] (%s) and weight %s, want BF16",
                 elem_name(X->elem), (long long)X->rows, (long long)X->cols, x_parts ? "parts" : "values",
                 elem_name(W->elem));

@@ -52,6 +52,10 @@ struct Layer {
   // then hold the same values decoded (exact), for the prefill's matrix-core
   // products, whose time is arithmetic, not weight bytes.
   Tensor q_wqkv, q_wo, q_wgu, q_wdown;
+  // The four projection weights again in the matrix cores' operand order
+  // (mi_tile; gate|up interleaved as wgu_pairs), for the products of a prompt
+  // of up to kTilesMaxRows rows (mi_linear's short-row path).
+  Tensor t_wqkv, t_wo, t_wgu_pairs, t_wdown;
   Tensor cache_k, cache_v;
 };
 
@@ -129,6 +133,11 @@ constexpr int64_t kFusedHeadMaxBatch = 8;
 // step of one span runs the same launches, so a step captured once replays
 // at each of its positions, and an eager step computes the same bits.
 constexpr int64_t kSpanStep = 64;
+// Prompts of up to this many rows (sequences x positions, a multiple of 32)
+// run their projections against the tiled weights: one block a 32 x 32 (or
+// 32 x 64) output tile with k split over its waves, the activations handed
+// over in tiles by the norms and the SwiGLU.
+constexpr int64_t kTilesMaxRows = 2048;
 
 int64_t decode_span(const mi_llama *m, int64_t ctxlen) {
   return std::min<int64_t>(m->cfg.max_ctx, (ctxlen + kSpanStep - 1) / kSpanStep * kSpanStep);
@@ -184,11 +193,31 @@ static bool parts_pay(mi_ctx *ctx, int64_t rows, int64_t k, int64_t n) {
 // the hidden states [batch * t, hidden] before the final norm.
 // The hidden rows of token ids already on the device ([batch * t] I32, rows
 // (sequence, position)).
+// A prefill's attention over q from the q|k|v tail (rows (sequence,
+// position, head) for the fused kernel, else regrouped per kv head): the
+// output rows (sequence, position) of heads x head_dim.
+Tensor attention_of(mi_llama *m, Layer &L, const Tensor &q, int64_t batch, int64_t t, int64_t pos0, int64_t ctxlen,
+                    bool fused, const Tensor &mask, float scale) {
+  const mi_llama_config &c = m->cfg;
+  const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim, G = H / KVH, maxc = c.max_ctx, rows = batch * t;
+  if (fused) return burn::attention_rows(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0, scale);
+  // [batch * KVH * t * G, D], rows (p, g) of each (sequence, kv head)
+  Tensor scores = burn::matmul_blocks(q, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
+                                      maxc * D);
+  Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
+  Tensor o = burn::matmul_blocks(p, false, L.cache_v, false, batch * KVH, t * G, ctxlen, D, 0, t * G * ctxlen, 0,
+                                 maxc * D);
+  // Back to rows (sequence, position), heads in order h = j * G + g.
+  const int64_t dims[4] = {batch, t, KVH, G * D};
+  const int64_t st[4] = {KVH * t * G * D, G * D, t * G * D, 1};
+  return burn::copy4(o, dims, 0, st).reshape({rows, H * D});
+}
+
 Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   mi_ctx *ctx = m->ctx;
   const mi_llama_config &c = m->cfg;
   const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim, G = H / KVH;
-  const int64_t pos0 = m->len, ctxlen = pos0 + t, maxc = c.max_ctx;
+  const int64_t pos0 = m->len, ctxlen = pos0 + t;
   const int64_t rows = batch * t;
 
   // The element type of a prefill product's activation operand.
@@ -230,6 +259,35 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   // (mi_linear_add_rms_norm: where that product splits over k, a short
   // prompt's, its reduce forms the norm; bit for bit the two calls).
   Tensor xn_next;
+  // A short prompt's products against the tiled weights, their activations in
+  // tiles: the F32 values' parts under the reference contract, BF16 values
+  // under the performance one (the attention output goes in as rows).
+  int mode = MI_MATMUL_FAST;
+  (void)mi_get_matmul_mode(ctx, &mode);
+  const bool tiles = !m->layers.empty() && m->layers[0].t_wqkv.defined() && rows % 32 == 0 &&
+                     rows <= kTilesMaxRows && (act == MI_BF16 || mode == MI_MATMUL_FAST);
+  if (tiles) {
+    const int tform = act == MI_F32 ? MI_TILES_PARTS : MI_TILES_BF16;
+    for (size_t li = 0; li < m->layers.size(); ++li) {
+      Layer &L = m->layers[li];
+      Tensor xn = xn_next.defined() ? xn_next : burn::rms_norm(x, L.attn_norm, c.eps, tform);
+      xn_next = Tensor();
+      Tensor q = burn::linear_qkv_rope_cache(xn, false, L.t_wqkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k,
+                                             L.cache_v, !fused);
+      Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
+      if (act != MI_F32) oh = burn::float_cast(oh, act);
+      Tensor hn;
+      std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.t_wo, true, nullptr, &x, L.mlp_norm, c.eps, tform);
+      Tensor h = burn::linear_swiglu(hn, L.t_wgu_pairs, tform);
+      if (li + 1 < m->layers.size())
+        std::tie(x, xn_next) = burn::linear_add_rms_norm(h, L.t_wdown, true, nullptr, &x, m->layers[li + 1].attn_norm,
+                                                         c.eps, tform);
+      else
+        x = burn::linear(h, L.t_wdown, true, nullptr, &x);
+    }
+    m->len = ctxlen;
+    return x;
+  }
   for (size_t li = 0; li < m->layers.size(); ++li) {
     Layer &L = m->layers[li];
     Tensor xn = xn_next.defined() ? xn_next : burn::rms_norm(x, L.attn_norm, c.eps, parts_qkv ? MI_BF16_PARTS : act);
@@ -254,23 +312,7 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
                              : burn::float_matmul(xn, false, L.wqkv, true);
       q = burn::qkv_rope_cache(qkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k, L.cache_v, !fused);
     }
-    Tensor oh;
-    if (fused) {
-      oh = burn::attention_rows(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0, scale);
-    } else {
-      const Tensor &qg = q;  // [batch * KVH * t * G, D], rows (p, g) of each (sequence, kv head)
-      Tensor scores = burn::matmul_blocks(qg, false, L.cache_k, true, batch * KVH, t * G, D, ctxlen, 0, t * G * D, 0,
-                                          maxc * D);
-      Tensor p = burn::softmax_rows(scores, mask.defined() ? &mask : nullptr, scale, false);
-      Tensor o = burn::matmul_blocks(p, false, L.cache_v, false, batch * KVH, t * G, ctxlen, D, 0, t * G * ctxlen, 0,
-                                     maxc * D);
-      // Back to rows (sequence, position), heads in order h = j * G + g.
-      {
-        const int64_t dims[4] = {batch, t, KVH, G * D};
-        const int64_t st[4] = {KVH * t * G * D, G * D, t * G * D, 1};
-        oh = burn::copy4(o, dims, 0, st).reshape({rows, H * D});
-      }
-    }
+    Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
     if (act != MI_F32) oh = burn::float_cast(oh, act);
     // x + oh wo^T (the add in the product's epilogue), and its MLP norm.
     Tensor hn;
@@ -402,10 +444,21 @@ int mi_llama_create(mi_ctx *ctx, const mi_llama_config *cfg, uint64_t seed, floa
           if (native) *wp.second = held;
         }
       }
-      if (c.intermediate % 128 == 0 && c.hidden % 32 == 0) {
+      Tensor pairs;
+      if (c.intermediate % 32 == 0 && c.hidden % 32 == 0) {
         const int64_t I = c.intermediate, Hd = c.hidden;
         const int64_t dims[4] = {I / 32, 2, 32, Hd}, st[4] = {32 * Hd, I * Hd, Hd, 1};
-        L.wgu_pairs = burn::copy4(L.wgu, dims, 0, st);
+        pairs = burn::copy4(L.wgu, dims, 0, st);
+        if (I % 128 == 0) L.wgu_pairs = pairs;
+      }
+      // Tiles: k (hidden, heads x 64, intermediate) a multiple of 16 up to
+      // 1536, output widths of 32 (pairs and 64-wide heads of 64).
+      if (c.head_dim == 64 && pairs.defined() && qd % 16 == 0 && c.hidden <= 1536 && qd <= 1536 &&
+          c.intermediate <= 1536) {
+        L.t_wqkv = burn::tile(L.wqkv, MI_TILES_BF16);
+        L.t_wo = burn::tile(L.wo, MI_TILES_BF16);
+        L.t_wgu_pairs = burn::tile(pairs, MI_TILES_BF16);
+        L.t_wdown = burn::tile(L.wdown, MI_TILES_BF16);
       }
     }
     // Rotary tables (rope.rs:14-60): angle = position * theta^(-2i / d), the

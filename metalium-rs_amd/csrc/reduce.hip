@@ -771,6 +771,14 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, 
         uint16_t *o = static_cast<uint16_t *>(out) + 2 * base;
         o[j] = h;
         o[cols + j] = l;
+      } else if (out_elem == MI_TILES_PARTS) {
+        uint16_t h, l;
+        split_bf16(y, h, l);
+        uint16_t *o = static_cast<uint16_t *>(out) + tile_offset(row, j, cols);
+        o[0] = h;
+        o[rows * cols] = l;
+      } else if (out_elem == MI_TILES_BF16) {
+        static_cast<uint16_t *>(out)[tile_offset(row, j, cols)] = f32_to_bf16_bits(y);
       } else {
         st(out, out_elem, base + j, y);
       }
@@ -1024,9 +1032,15 @@ extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, xb, a);
-  if (!elem_float(xb->elem)) return fail(ctx, MI_E_ARG, "rms_norm of a %s buffer", elem_name(xb->elem));
-  if (out_elem != MI_F32 && out_elem != MI_BF16 && out_elem != MI_BF16_PARTS)
+  if (!elem_float(xb->elem) || xb->tiles)
+    return fail(ctx, MI_E_ARG, "rms_norm of a %s buffer%s", elem_name(xb->elem), xb->tiles ? " in tiles" : "");
+  if (out_elem != MI_F32 && out_elem != MI_BF16 && out_elem != MI_BF16_PARTS && out_elem != MI_TILES_BF16 &&
+      out_elem != MI_TILES_PARTS)
     return fail(ctx, MI_E_ARG, "rms_norm result kind %d", out_elem);
+  const bool tiled = out_elem == MI_TILES_BF16 || out_elem == MI_TILES_PARTS;
+  if (tiled && (xb->rows % 32 || xb->cols % 16))
+    return fail(ctx, MI_E_ARG, "rms_norm: tiles of [%lld, %lld] (rows a multiple of 32, columns of 16)",
+                (long long)xb->rows, (long long)xb->cols);
   const void *gp = nullptr;
   int ge = MI_F32;
   if (gamma) {
@@ -1040,9 +1054,10 @@ extern "C" int mi_rms_norm(mi_ctx *ctx, mi_id a, mi_id gamma, float eps, int out
   const void *xp = xb->ptr;
   const int xe = xb->elem;
   mi_id id; Buffer *ob;
-  const bool parts = out_elem == MI_BF16_PARTS;
-  int s = new_buffer(ctx, R, parts ? 2 * C : C, parts ? MI_BF16 : out_elem, &id, &ob);
+  const bool parts = out_elem == MI_BF16_PARTS || out_elem == MI_TILES_PARTS;
+  int s = new_buffer(ctx, R, parts ? 2 * C : C, parts || tiled ? MI_BF16 : out_elem, &id, &ob);
   if (s) return s;
+  ob->tiles = tiled ? out_elem : 0;
   if (R > 0 && C > 0) rms_norm_launch(ctx, xp, xe, gp, ge, eps, ob->ptr, out_elem, R, C);
   s = check_launch(ctx, "rms_norm");
   if (s) { mi_free(ctx, id); return s; }

@@ -455,9 +455,10 @@ int mi_metadata(mi_ctx *ctx, mi_id id, int64_t *rows, int64_t *cols, int *elem) 
 int mi_reshape(mi_ctx *ctx, mi_id id, int64_t rows, int64_t cols) {
   MI_ENTER(ctx);
   MI_BUF(ctx, b, id);
-  if (rows < 0 || cols < 0 || rows * cols != b->numel() || (b->elem == MI_BFP8 && cols != b->cols))
-    return fail(ctx, MI_E_ARG, "reshape of %s [%lld, %lld] to [%lld, %lld]", elem_name(b->elem), (long long)b->rows,
-                (long long)b->cols, (long long)rows, (long long)cols);
+  if (rows < 0 || cols < 0 || rows * cols != b->numel() || ((b->elem == MI_BFP8 || b->tiles) && cols != b->cols) ||
+      (b->tiles && rows != b->rows))
+    return fail(ctx, MI_E_ARG, "reshape of %s [%lld, %lld]%s to [%lld, %lld]", elem_name(b->elem), (long long)b->rows,
+                (long long)b->cols, b->tiles ? " in tiles" : "", (long long)rows, (long long)cols);
   b->rows = rows;
   b->cols = cols;
   return MI_OK;

@@ -29,6 +29,8 @@ F32, I32, BOOL, BF16, BFP8 = 0, 1, 2, 3, 5
 # A result form of mi_rms_norm / mi_silu_mul_halves: the F32 result as its
 # BF16 parts, [rows, 2 cols] (heads, then remainders), read by linear_parts.
 BF16_PARTS = 4
+TILES_BF16 = 6   # an operand in the matrix cores' operand order (mi_tile)
+TILES_PARTS = 7
 _NP = {F32: np.float32, I32: np.int32, BOOL: np.uint32, BF16: np.uint16, BFP8: np.float32}
 
 AXIS_ROWS, AXIS_COLS = 0, 1
@@ -145,6 +147,7 @@ def _load() -> ctypes.CDLL:
         "mi_trace_release": [P, U64],
         "mi_copy_into": [P, U64, U64],
         "mi_cast_bfp": [P, U64, c_int, ctypes.POINTER(U64)],
+        "mi_tile": [P, U64, c_int, ctypes.POINTER(U64)],
         "mi_decode_advance": [P, U64, U64, U64, U64],
         "mi_gather": [P, U64, ctypes.POINTER(I64), c_int, U64, ctypes.POINTER(I64), Ip],
         "mi_linear_add_rms_norm": [P, U64, U64, c_int, U64, U64, U64, c_float, c_int, Ip, Ip],
@@ -575,6 +578,10 @@ class Engine:
         """A chained decode step's tail: ids <- next_ids, log[:, pos + 1] <-
         next_ids, pos <- pos + 1 (all on the device)."""
         self._check(self._lib.mi_decode_advance(self.ctx, next_ids, ids, pos, log))
+
+    def tile(self, a: int, form: int = TILES_BF16) -> int:
+        """A row-major F32/BF16 [r, c] buffer in tiles (TILES_BF16 / TILES_PARTS)."""
+        return self._out(self._lib.mi_tile, a, form)
 
     def cast_bfp(self, a: int, fmt: int = BFP8) -> int:
         """Engine::cast_bfp: an F32 or BF16 buffer stored as BFP8 (fmt

@@ -183,6 +183,21 @@ def test_special_values_relu_and_neg(engine):
     same_bits(engine.download(engine.eltwise_op_as("ABS", a)), orc.eltwise(K["ABS"], x))
 
 
+def test_bf16_narrowing_over_every_head(engine):
+    """F32 -> BF16 on the device (gfx950's conversion instruction) against the
+    oracle's integer rounding: every sign/exponent/7-bit-mantissa head with
+    low halves at the rounding boundaries (exact, just below and at the tie,
+    past it, the largest) and random ones -- NaN payloads, infinities,
+    subnormals, overflow to infinity and ties to even included."""
+    heads = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    u = (heads[:, None] | lows[None, :]).ravel()
+    u = np.concatenate([u, heads | RNG.integers(0, 1 << 16, heads.size, dtype=np.uint32)])
+    x = u.view(np.float32).reshape(-1, 1024)
+    got = engine.download(engine.cast_float(engine.upload_bits(u.reshape(-1, 1024), F32), BF16))
+    assert np.array_equal(got, orc.to_bf16(x))
+
+
 def test_bf16_in_and_out(engine):
     x = rnd(64, 128)
     xb = orc.to_bf16(x)
