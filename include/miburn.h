@@ -541,6 +541,17 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
                       int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, int64_t pos0, float scale,
                       mi_id *out);
+/* mi_attention_rows with its result in `out_form`: MI_F32 (mi_attention_rows
+ * itself), MI_BF16 (each value rounded once), or tiles of the [batch t,
+ * heads d] result (MI_TILES_BF16 / MI_TILES_PARTS; batch t a multiple of 32)
+ * -- the operand an o projection against a tiled weight reads, stored by the
+ * matrix-core (many new positions) kernel itself; other paths convert their
+ * F32 rows.  The same values as mi_attention_rows, then rounded or split.
+ * No Engine counterpart. */
+int mi_attention_rows_as(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
+                         int64_t batch, int64_t t, int64_t heads,
+                         int64_t kv_heads, int64_t pos0, float scale,
+                         int out_form, mi_id *out);
 /* mi_attention_rows for a traced decode step, whose positions are device
  * data (the reference's position tensors and its step traced per attended
  * length, crates/tt-models/src/generate.rs:1-22, 770-790): pos0 read on the

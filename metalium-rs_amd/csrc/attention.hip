@@ -219,12 +219,49 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
   }
 }
 
+// Where an attention result value (row, col) of [R, C] goes: F32 rows (the
+// plain form), BF16 rows rounded once, or the tiles an o projection reads
+// (MI_TILES_BF16, or MI_TILES_PARTS: heads' plane then remainders').
+struct AttOut {
+  void *p = nullptr;
+  int form = MI_F32;
+  int64_t R = 0, C = 0;
+};
+__device__ __forceinline__ void att_put(const AttOut &o, int64_t r, int64_t c, float v) {
+  uint16_t *h = static_cast<uint16_t *>(o.p);
+  switch (o.form) {
+    case MI_F32: static_cast<float *>(o.p)[r * o.C + c] = v; break;
+    case MI_BF16: h[r * o.C + c] = f32_to_bf16_bits(v); break;
+    case MI_TILES_BF16: h[tile_offset(r, c, o.C)] = f32_to_bf16_bits(v); break;
+    default: {
+      uint16_t hi, lo;
+      split_bf16(v, hi, lo);
+      const int64_t t = tile_offset(r, c, o.C);
+      h[t] = hi;
+      h[o.R * o.C + t] = lo;
+    }
+  }
+}
+// Four consecutive values (c a multiple of 4) of one row.
+__device__ __forceinline__ void att_put4(const AttOut &o, int64_t r, int64_t c, float4 v) {
+  uint16_t *h = static_cast<uint16_t *>(o.p);
+  switch (o.form) {
+    case MI_F32: *reinterpret_cast<float4 *>(static_cast<float *>(o.p) + r * o.C + c) = v; break;
+    case MI_BF16: f32x4_put(h + r * o.C + c, v); break;
+    case MI_TILES_BF16: f32x4_put(h + tile_offset(r, c, o.C), v); break;
+    default: {
+      const int64_t t = tile_offset(r, c, o.C);
+      parts4_put(h + t, h + o.R * o.C + t, v);
+    }
+  }
+}
+
 // Combine the chunks of one (item, position): out = sum_s w_s o_s / sum_s w_s
 // l_s with w_s = exp(m_s - max_s m_s), the sum clamped below at FLT_MIN.  The
 // chunks' statistics go to LDS in one pass and the weights are formed there,
 // so each output element then issues its S loads back to back.
-template <int D, int G>
-__global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, float *out, int64_t T, int64_t H,
+template <int D, int G, bool FORMS = false>
+__global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, AttOut out, int64_t T, int64_t H,
                                                                 int64_t KVH, int S) {
   extern __shared__ float st[];  // [S][2G] statistics, then [S][G] weights, [G] denominators
   const int64_t item = blockIdx.x;
@@ -260,7 +297,7 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
     den[g] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
   }
   __syncthreads();
-  float *dst = out + (b * T + p) * H * D + j * G * D;
+  const int64_t orow = b * T + p, ocol = j * G * D;
 #pragma unroll
   for (int i = 0; i < EP; ++i) {
     const int e = threadIdx.x + 256 * i;
@@ -271,7 +308,8 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
       for (int s = 0; s < CS; ++s)
         if (s < S) num += w[s * G + g] * ov[i][s];
       for (int s = CS; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
-      dst[e] = num / den[g];
+      if constexpr (FORMS) att_put(out, orow, ocol + e, num / den[g]);
+      else static_cast<float *>(out.p)[orow * out.C + ocol + e] = num / den[g];
     }
   }
 }
@@ -350,9 +388,11 @@ __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const 
   return c;
 }
 
-template <int G, typename KV>
+// FORMS: the result may be stored in another form than F32 rows (the
+// store's form switch is compiled in only then).
+template <int G, typename KV, bool FORMS>
 __global__ void __launch_bounds__(G * 64)
-flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, int64_t T, int64_t H, int64_t KVH,
+flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, int64_t T, int64_t H, int64_t KVH,
                       int64_t pos0, int64_t maxc, float scale, int64_t kchunk, float *part) {
   constexpr int D = 64, NT = G * 64;
   constexpr bool EXACT = sizeof(KV) == 2;  // a BF16 cache: one part
@@ -561,36 +601,49 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, float *out, in
       }
     } else if (live) {
       const float den = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
-      float *orow = out + (b * T + p) * H * D + h * D + 4 * half;
+      const int64_t orow = b * T + p, ocol = h * D + 4 * half;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        *reinterpret_cast<float4 *>(orow + 8 * c) =
-            make_float4(o0[4 * c] / den, o0[4 * c + 1] / den, o0[4 * c + 2] / den, o0[4 * c + 3] / den);
-        *reinterpret_cast<float4 *>(orow + 32 + 8 * c) =
-            make_float4(o1[4 * c] / den, o1[4 * c + 1] / den, o1[4 * c + 2] / den, o1[4 * c + 3] / den);
+        const float4 y0 = make_float4(o0[4 * c] / den, o0[4 * c + 1] / den, o0[4 * c + 2] / den, o0[4 * c + 3] / den);
+        const float4 y1 = make_float4(o1[4 * c] / den, o1[4 * c + 1] / den, o1[4 * c + 2] / den, o1[4 * c + 3] / den);
+        if constexpr (FORMS) {
+          att_put4(out, orow, ocol + 8 * c, y0);
+          att_put4(out, orow, ocol + 32 + 8 * c, y1);
+        } else {
+          float *orp = static_cast<float *>(out.p) + orow * out.C + ocol;
+          *reinterpret_cast<float4 *>(orp + 8 * c) = y0;
+          *reinterpret_cast<float4 *>(orp + 32 + 8 * c) = y1;
+        }
       }
     }
   }
 }
 
 template <int G, typename KV>
-void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch, int64_t T,
+void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, const AttOut &out, int64_t batch, int64_t T,
                   int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale, int64_t kchunk, int S,
                   float *part) {
   if (kchunk > 0) {
     const dim3 grid(static_cast<unsigned>((T + 31) / 32), static_cast<unsigned>(batch * KVH), static_cast<unsigned>(S));
-    flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk, part);
-    attention_combine_kernel<64, G><<<static_cast<unsigned>(batch * KVH * T), 256,
-                                         static_cast<size_t>(3 * G * S + G) * sizeof(float), st>>>(part, out, T, H, KVH,
-                                                                                                   S);
+    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk,
+                                                                   part);
+    const unsigned items = static_cast<unsigned>(batch * KVH * T);
+    const size_t smem = static_cast<size_t>(3 * G * S + G) * sizeof(float);
+    if (out.form == MI_F32)
+      attention_combine_kernel<64, G, false><<<items, 256, smem, st>>>(part, out, T, H, KVH, S);
+    else
+      attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S);
     return;
   }
   const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
-  flash3_prefill_kernel<G, KV><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
+  if (out.form == MI_F32)
+    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
+  else
+    flash3_prefill_kernel<G, KV, true><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
 }
 
 template <typename KV>
-bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, float *out, int64_t batch,
+bool flash_dispatch(int64_t G, hipStream_t st, const float *q, const KV *k, const KV *v, const AttOut &out, int64_t batch,
                     int64_t T, int64_t H, int64_t KVH, int64_t pos0, int64_t maxc, float scale, int64_t kchunk,
                     int S, float *part) {
   switch (G) {
@@ -616,9 +669,13 @@ void launch_attention(hipStream_t st, const float *q, const KV *k, const KV *v, 
   const size_t smem = attention_smem(G, D, chunk, ATT_WAVES);
   attention_chunk_kernel<D, G, ATT_WAVES, KV><<<grid, ATT_WAVES * 64, smem, st>>>(q, k, v, out, part, T, H, KVH, pa, maxc,
                                                                             chunk, scale, S == 1);
-  if (S > 1)
+  if (S > 1) {
+    AttOut o;  // F32 rows of H D columns (the form reads no row count)
+    o.p = out;
+    o.C = H * D;
     attention_combine_kernel<D, G><<<static_cast<unsigned>(items), 256, static_cast<size_t>(3 * G * S + G) * sizeof(float),
-                                     st>>>(part, out, T, H, KVH, S);
+                                     st>>>(part, o, T, H, KVH, S);
+  }
 }
 
 template <int D, typename KV>
@@ -1256,14 +1313,15 @@ int attention_plan(Ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batc
 }
 
 template <typename KV>
-void attention_launch_kv(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t,
+void attention_launch_kv(Ctx *ctx, const AttPlan &P, const AttOut &ao, float *part, int64_t batch, int64_t t,
                          int64_t heads, int64_t kv_heads, float scale) {
   const KV *k = static_cast<const KV *>(P.k), *v = static_cast<const KV *>(P.v);
   if (P.flash) {
-    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, out, batch, t, heads, kv_heads, P.pos.pos0, P.maxc, scale,
+    flash_dispatch<KV>(P.G, ctx->stream, P.q, k, v, ao, batch, t, heads, kv_heads, P.pos.pos0, P.maxc, scale,
                        P.fchunk, static_cast<int>(P.fS), part);
     return;
   }
+  float *out = static_cast<float *>(ao.p);  // the chunk kernels write F32 rows
   const int Si = static_cast<int>(P.S);
   switch (P.D) {
     case 16: dispatch_group<16, KV>(P.G, ctx->stream, P.q, k, v, out, part, P.items, Si, t, heads, kv_heads, P.pos, P.maxc, P.chunk, scale); break;
@@ -1273,18 +1331,41 @@ void attention_launch_kv(Ctx *ctx, const AttPlan &P, float *out, float *part, in
   }
 }
 
+// The result in `ao`: any form on the matrix-core (flash) path, F32 rows on
+// the chunk kernels'.
+void attention_launch(Ctx *ctx, const AttPlan &P, const AttOut &ao, float *part, int64_t batch, int64_t t,
+                      int64_t heads, int64_t kv_heads, float scale) {
+  if (P.kv16)
+    attention_launch_kv<uint16_t>(ctx, P, ao, part, batch, t, heads, kv_heads, scale);
+  else
+    attention_launch_kv<float>(ctx, P, ao, part, batch, t, heads, kv_heads, scale);
+}
 void attention_launch(Ctx *ctx, const AttPlan &P, float *out, float *part, int64_t batch, int64_t t, int64_t heads,
                       int64_t kv_heads, float scale) {
-  if (P.kv16)
-    attention_launch_kv<uint16_t>(ctx, P, out, part, batch, t, heads, kv_heads, scale);
-  else
-    attention_launch_kv<float>(ctx, P, out, part, batch, t, heads, kv_heads, scale);
+  AttOut o;
+  o.p = out;
+  o.R = batch * t;
+  o.C = heads * P.D;
+  attention_launch(ctx, P, o, part, batch, t, heads, kv_heads, scale);
 }
 
 // The result of a planned call into a new buffer (partials in the context's
 // scratch).
 int attention_new(mi_ctx *ctx, const AttPlan &P, int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, float scale,
-                  const char *what, mi_id *out) {
+                  const char *what, mi_id *out, int form = MI_F32) {
+  const int64_t R = batch * t, C = heads * P.D;
+  const bool tiled = form == MI_TILES_BF16 || form == MI_TILES_PARTS;
+  if (tiled && (R % 32 || C % 16))
+    return fail(ctx, MI_E_ARG, "%s: tiles of [%lld, %lld] (rows a multiple of 32, columns of 16)", what, (long long)R,
+                (long long)C);
+  // The chunk kernels write F32 rows: another form from them is converted.
+  if (form != MI_F32 && !P.flash) {
+    mi_id f;
+    if (int s = attention_new(ctx, P, batch, t, heads, kv_heads, scale, what, &f)) return s;
+    const int s = tiled ? mi_tile(ctx, f, form, out) : mi_cast(ctx, f, form, out);
+    mi_free(ctx, f);  // stream-ordered
+    return s;
+  }
   float *part = nullptr;
   if (P.part_bytes) {
     part = static_cast<float *>(mi::scratch(ctx, P.part_bytes));
@@ -1292,9 +1373,15 @@ int attention_new(mi_ctx *ctx, const AttPlan &P, int64_t batch, int64_t t, int64
   }
   mi_id id;
   Buffer *ob;
-  int s = new_buffer(ctx, batch * t, heads * P.D, MI_F32, &id, &ob);
+  int s = new_buffer(ctx, R, form == MI_TILES_PARTS ? 2 * C : C, form == MI_F32 ? MI_F32 : MI_BF16, &id, &ob);
   if (s) return s;
-  attention_launch(ctx, P, static_cast<float *>(ob->ptr), part, batch, t, heads, kv_heads, scale);
+  ob->tiles = tiled ? form : 0;
+  AttOut o;
+  o.p = ob->ptr;
+  o.form = form;
+  o.R = R;
+  o.C = C;
+  attention_launch(ctx, P, o, part, batch, t, heads, kv_heads, scale);
   s = check_launch(ctx, what);
   if (s) {
     mi_free(ctx, id);
@@ -1318,6 +1405,19 @@ extern "C" int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_ca
   int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, nullptr, 0, &P);
   if (s) return s;
   return attention_new(ctx, P, batch, t, heads, kv_heads, scale, "attention_rows", out);
+}
+
+extern "C" int mi_attention_rows_as(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,
+                                    int64_t heads, int64_t kv_heads, int64_t pos0, float scale, int out_form,
+                                    mi_id *out) {
+  MI_ENTER(ctx);
+  if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  if (out_form != MI_F32 && out_form != MI_BF16 && out_form != MI_TILES_BF16 && out_form != MI_TILES_PARTS)
+    return fail(ctx, MI_E_ARG, "attention_rows_as: result form %d", out_form);
+  AttPlan P;
+  int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, nullptr, 0, &P);
+  if (s) return s;
+  return attention_new(ctx, P, batch, t, heads, kv_heads, scale, "attention_rows_as", out, out_form);
 }
 
 extern "C" int mi_attention_rows_at(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache, int64_t batch, int64_t t,

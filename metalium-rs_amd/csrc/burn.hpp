@@ -474,6 +474,16 @@ inline Tensor attention_rows(const Tensor &q, const Tensor &k_cache, const Tenso
         "attention_rows");
   return Tensor(q.ctx(), id, {q.rows(), q.cols()});
 }
+// The same with its result in `form` (mi_attention_rows_as: rounded to BF16,
+// or tiles for an o projection against a tiled weight).
+inline Tensor attention_rows_as(const Tensor &q, const Tensor &k_cache, const Tensor &v_cache, int64_t batch, int64_t t,
+                                int64_t heads, int64_t kv_heads, int64_t pos0, float scale, int form) {
+  mi_id id;
+  check(q.ctx(), mi_attention_rows_as(q.ctx(), q.use(), k_cache.use(), v_cache.use(), batch, t, heads, kv_heads, pos0,
+                                      scale, form, &id),
+        "attention_rows_as");
+  return Tensor(q.ctx(), id, {q.rows(), two_parts(form) ? 2 * q.cols() : q.cols()});
+}
 
 // attention_rows with the key chunks planned for `span` positions and pos0
 // read on the device from `pos` when it is given (mi_attention_rows_at).

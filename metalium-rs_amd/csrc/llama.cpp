@@ -274,8 +274,11 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
       xn_next = Tensor();
       Tensor q = burn::linear_qkv_rope_cache(xn, false, L.t_wqkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k,
                                              L.cache_v, !fused);
-      Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
-      if (act != MI_F32) oh = burn::float_cast(oh, act);
+      // The attention hands its result to the o projection in tiles (the
+      // matrix-core kernel stores them itself).
+      Tensor oh = fused ? burn::attention_rows_as(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0,
+                                                  scale, tform)
+                        : burn::tile(attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale), tform);
       Tensor hn;
       std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.t_wo, true, nullptr, &x, L.mlp_norm, c.eps, tform);
       Tensor h = burn::linear_swiglu(hn, L.t_wgu_pairs, tform);

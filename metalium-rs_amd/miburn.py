@@ -115,6 +115,7 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into4": [P, U64, I64, ctypes.POINTER(I64), U64, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)],
         "mi_rope": [P, U64, U64, U64, I64, I64, I64, Ip],
         "mi_attention_rows": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, Ip],
+        "mi_attention_rows_as": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, c_int, Ip],
         "mi_attention_rows_into": [P, U64, U64, U64, I64, I64, I64, I64, I64, c_float, U64],
         "mi_reduce_then": [P, U64, c_int, c_int, c_u32, c_float, Ip],
         "mi_add_rms_norm": [P, U64, U64, U64, c_float, Ip, Ip],
@@ -395,6 +396,12 @@ class Engine:
         """Engine::attention_rows (server.rs:255-265): causal GQA of `t` new
         positions against the first pos0 + t rows of each cache item."""
         return self._out(self._lib.mi_attention_rows, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, scale)
+
+    def attention_rows_as(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int, kv_heads: int,
+                          pos0: int, scale: float, out_form: int) -> int:
+        """attention_rows with its result in out_form (F32, BF16, TILES_BF16, TILES_PARTS)."""
+        return self._out(self._lib.mi_attention_rows_as, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, scale,
+                         out_form)
 
     def attention_rows_at(self, q: int, k_cache: int, v_cache: int, batch: int, t: int, heads: int, kv_heads: int,
                           pos: int, pos0: int, span: int, scale: float) -> int:

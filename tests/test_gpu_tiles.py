@@ -241,3 +241,26 @@ def test_tiles_refusals(engine):
     finally:
         engine.set_matmul_mode(miburn.MATMUL_FAST)
     engine.sync()
+
+
+@pytest.mark.parametrize("batch,t,pos0,kv16", [(1, 512, 0, False), (1, 512, 0, True), (2, 128, 64, False),
+                                               (2, 16, 8, False)])  # the last on the key-chunk kernels
+@pytest.mark.parametrize("form", [BF16, TILES_BF16, TILES_PARTS])
+def test_attention_rows_as_equals_rows_then_form(engine, batch, t, pos0, kv16, form):
+    H, KVH, D = 9, 3, 64
+    maxc = pos0 + t + 8
+    q = engine.upload(rnd(batch * t, H * D))
+    kc, vc = rnd(batch * KVH * maxc, D), rnd(batch * KVH * maxc, D)
+    if kv16:
+        k, v = engine.upload_bf16(orc.to_bf16(kc)), engine.upload_bf16(orc.to_bf16(vc))
+    else:
+        k, v = engine.upload(kc), engine.upload(vc)
+    scale = float(np.float32(1 / 8))
+    y = engine.download(engine.attention_rows(q, k, v, batch, t, H, KVH, pos0, scale))
+    got = engine.download(engine.attention_rows_as(q, k, v, batch, t, H, KVH, pos0, scale, form))
+    if form == BF16:
+        same_bits(got, orc.to_bf16(y), np.uint16)
+    elif form == TILES_BF16:
+        same_bits(got.reshape(-1), tiled(orc.to_bf16(y)), np.uint16)
+    else:
+        same_bits(got.reshape(-1), tiled_parts(y), np.uint16)
