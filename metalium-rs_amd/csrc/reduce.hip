@@ -736,7 +736,7 @@ template <int T>
 __global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, const void *gamma, int gelem, float eps,
                                                        void *out, int out_elem, int64_t rows, int64_t cols) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t base = row * cols;
   // Rows of up to 2048 columns request the gain with the row, so the scaling
@@ -1019,9 +1019,13 @@ extern "C" int mi_softmax_rows(mi_ctx *ctx, mi_id x, mi_id mask, float scale, in
 namespace mi {
 void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, float eps, void *out, int out_elem,
                      int64_t R, int64_t C) {
-  const unsigned g = grid_for(R, 4, INT32_MAX);
+  // One wavefront a row; below 4096 rows one a block, so the rows spread
+  // over every CU (a 512-row prompt's norms: 128 blocks of four rows left
+  // half the chip idle).
+  const int per = R < 4096 ? 1 : 4;
+  const unsigned g = grid_for(R, per, INT32_MAX);
   switch (pick_t(C)) {
-#define MI_RN(T) case T: rms_norm_kernel<T><<<g, 256, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
+#define MI_RN(T) case T: rms_norm_kernel<T><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
     MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16) MI_RN(32) MI_RN(64) MI_RN(128)
 #undef MI_RN
   }

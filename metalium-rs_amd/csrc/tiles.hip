@@ -360,7 +360,13 @@ int tiles_linear(mi_ctx *ctx, mi_id x, mi_id w, const float *bias, const float *
   if (out_elem != MI_F32 && out_elem != MI_BF16) return fail(ctx, MI_E_ARG, "linear: result kind %d", out_elem);
   TileArgs g;
   int am;
-  if (int s = tiles_operands(ctx, "linear", X, W, 0, &g, &am)) return s;
+  // 32 x 64 tiles for long k where 32 x 32 ones would take more than a round
+  // of the chip's 256 CUs and the wider ones fit in one (a 512-row prompt's
+  // down product: 288 blocks -> 144, 11.3 -> 10.1 us; its o product, k 576,
+  // measured slower so); the k ranges, hence the sums, are the same either way.
+  const int64_t tiles32 = (X->rows / 32) * (W->rows / 32);
+  const bool wide = W->rows % 64 == 0 && W->cols > 768 && tiles32 > 256 && tiles32 / 2 <= 256;
+  if (int s = tiles_operands(ctx, "linear", X, W, wide, &g, &am)) return s;
   mi_id id;
   Buffer *ob;
   if (int s = new_buffer(ctx, g.M, g.N, out_elem, &id, &ob)) return s;
@@ -369,7 +375,7 @@ int tiles_linear(mi_ctx *ctx, mi_id x, mi_id w, const float *bias, const float *
   g.bias = bias;
   g.resid = resid;
   g.ldr = g.N;
-  const hipError_t e = launch_tiles<1, TE_STORE>(am, g, ctx->stream);
+  const hipError_t e = wide ? launch_tiles<2, TE_STORE>(am, g, ctx->stream) : launch_tiles<1, TE_STORE>(am, g, ctx->stream);
   if (e != hipSuccess) {
     mi_free(ctx, id);
     return fail(ctx, MI_E_HIP, "linear (tiles) launch: %s", hipGetErrorString(e));
