@@ -13,9 +13,10 @@
 // its range sets the context's device flag (reported as MI_E_DOMAIN at the
 // next wait) and the element is written as zero bits, never read out of
 // bounds.
+#include <utility>
+
 #include "common.hpp"
 
-#include <hipcub/device/device_radix_sort.hpp>
 
 namespace mi {
 
@@ -139,6 +140,70 @@ __global__ void __launch_bounds__(1024) sort_pairs_block(const int32_t *idx, int
     keys_out[i] = static_cast<int32_t>(k[i] >> 32);
     pos_out[i] = static_cast<int32_t>(k[i] & 0xffffffffu);
   }
+}
+
+// More indices: each block sorts a chunk of SORT_BLOCK_MAX keys in LDS with
+// the same network, then merge passes double the sorted runs.  The keys are
+// unique (the position is part of each), so an element's place in the merged
+// run is its place in its own run plus the number of the other run's keys
+// below it (a binary search): no ties, no atomics, one order.
+__global__ void __launch_bounds__(1024) sort_keys_chunks(const int32_t *idx, int64_t n, uint64_t *out) {
+  __shared__ uint64_t k[SORT_BLOCK_MAX];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * SORT_BLOCK_MAX;
+  const int64_t m = n - base < SORT_BLOCK_MAX ? n - base : SORT_BLOCK_MAX;
+  int np = 1;
+  while (np < m) np <<= 1;
+  for (int i = threadIdx.x; i < np; i += 1024)
+    k[i] = i < m ? (static_cast<uint64_t>(static_cast<uint32_t>(idx[base + i])) << 32) |
+                       static_cast<uint32_t>(base + i)
+                 : ~0ull;
+  __syncthreads();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < np / 2; t += 1024) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = k[lo], b = k[hi];
+        if ((a > b) == up) {
+          k[lo] = b;
+          k[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < m; i += 1024) out[base + i] = k[i];
+}
+
+// Keys of [lo, hi) below `key`: a binary search over a sorted run.
+__device__ __forceinline__ int64_t keys_below(const uint64_t *k, int64_t lo, int64_t hi, uint64_t key) {
+  int64_t a = lo, b = hi;
+  while (a < b) {
+    const int64_t mid = a + ((b - a) >> 1);
+    if (k[mid] < key) a = mid + 1;
+    else b = mid;
+  }
+  return a - lo;
+}
+
+// One merge pass: sorted runs of `run` keys pairwise into runs of 2 run.
+__global__ void __launch_bounds__(256) merge_runs(const uint64_t *src, uint64_t *dst, int64_t n, int64_t run) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t a0 = i / (2 * run) * (2 * run);
+  const int64_t b0 = a0 + run < n ? a0 + run : n, b1 = b0 + run < n ? b0 + run : n;
+  const uint64_t key = src[i];
+  const int64_t at = i < b0 ? a0 + (i - a0) + keys_below(src, b0, b1, key)
+                            : a0 + (i - b0) + keys_below(src, a0, b0, key);
+  dst[at] = key;
+}
+
+__global__ void __launch_bounds__(256) split_keys(const uint64_t *k, int64_t n, int32_t *keys, int32_t *pos) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  keys[i] = static_cast<int32_t>(k[i] >> 32);
+  pos[i] = static_cast<int32_t>(k[i] & 0xffffffffu);
 }
 
 // BF16 table rows gathered and widened to F32 (exact) in one pass: a wave a
@@ -505,28 +570,21 @@ extern "C" int mi_select_add_rows(mi_ctx *ctx, mi_id t, mi_id idx, mi_id value, 
     select_add_segments<<<grid_for(n, 4, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<float *>(ob->ptr), V, D, keys_out,
                                                                            pos_out, n, vp, flags(ctx));
   } else if (n > 0 && D > 0) {
-    // The library radix sort clears its counters with memsets, which a
-    // captured trace cannot replay correctly.
-    if (int r = refuse_if_capturing(ctx, "select_add_rows of more than 8192 indices")) {
-      mi_free(ctx, id);
-      return r;
-    }
-    const int ni = static_cast<int>(n);
-    size_t temp_bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, static_cast<const int32_t *>(nullptr),
-                                       static_cast<int32_t *>(nullptr), static_cast<const int32_t *>(nullptr),
-                                       static_cast<int32_t *>(nullptr), ni, 0, 32, ctx->stream);
     const size_t arr = (static_cast<size_t>(n) * 4 + 255) & ~size_t(255);
-    char *sc = static_cast<char *>(scratch(ctx, 3 * arr + temp_bytes + 256));
+    const size_t arr8 = (static_cast<size_t>(n) * 8 + 255) & ~size_t(255);
+    char *sc = static_cast<char *>(scratch(ctx, 2 * arr + 2 * arr8));
     if (!sc) { mi_free(ctx, id); return fail(ctx, MI_E_OOM, "select_add_rows scratch"); }
-    int32_t *pos_in = reinterpret_cast<int32_t *>(sc);
-    int32_t *keys_out = reinterpret_cast<int32_t *>(sc + arr);
-    int32_t *pos_out = reinterpret_cast<int32_t *>(sc + 2 * arr);
-    void *temp = sc + 3 * arr;
-    iota_kernel<<<grid_for(n, 256, INT32_MAX), 256, 0, ctx->stream>>>(pos_in, n);
-    // Keys as unsigned bits keep negative (invalid) indices grouped; the
-    // segment kernel flags them.
-    (void)hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, ip, keys_out, pos_in, pos_out, ni, 0, 32, ctx->stream);
+    int32_t *keys_out = reinterpret_cast<int32_t *>(sc);
+    int32_t *pos_out = reinterpret_cast<int32_t *>(sc + arr);
+    uint64_t *ka = reinterpret_cast<uint64_t *>(sc + 2 * arr), *kb = reinterpret_cast<uint64_t *>(sc + 2 * arr + arr8);
+    sort_keys_chunks<<<static_cast<unsigned>((n + SORT_BLOCK_MAX - 1) / SORT_BLOCK_MAX), 1024, 0, ctx->stream>>>(ip, n,
+                                                                                                                ka);
+    const unsigned g = grid_for(n, 256, INT32_MAX);
+    for (int64_t run = SORT_BLOCK_MAX; run < n; run *= 2) {
+      merge_runs<<<g, 256, 0, ctx->stream>>>(ka, kb, n, run);
+      std::swap(ka, kb);
+    }
+    split_keys<<<g, 256, 0, ctx->stream>>>(ka, n, keys_out, pos_out);
     select_add_segments<<<grid_for(n, 4, INT32_MAX), 256, 0, ctx->stream>>>(static_cast<float *>(ob->ptr), V, D, keys_out,
                                                                            pos_out, n, vp, flags(ctx));
   }

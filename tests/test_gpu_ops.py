@@ -767,8 +767,9 @@ def test_pick_and_scatter_add_columns(engine):
 
 
 @pytest.mark.parametrize("V,D,n,hot", [(300, 64, 2048, 40),  # one-block sort
-                                       (49152, 64, 20000, 49152),  # library radix sort above 8192 ids
-                                       (1000, 576, 9000, 30)])
+                                       (49152, 64, 20000, 49152),  # chunk sorts and merge passes above 8192 ids
+                                       (1000, 576, 9000, 30),
+                                       (49152, 16, 70001, 700)])   # four merge passes, a partial last run
 def test_select_add_rows_duplicates_in_order(engine, V, D, n, hot):
     t = rnd(V, D)
     idx = RNG.integers(0, hot, n).astype(np.int32)  # duplicates (many when hot is small)
