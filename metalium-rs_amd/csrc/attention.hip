@@ -260,11 +260,20 @@ __device__ __forceinline__ void att_put4(const AttOut &o, int64_t r, int64_t c, 
 // l_s with w_s = exp(m_s - max_s m_s), the sum clamped below at FLT_MIN.  The
 // chunks' statistics go to LDS in one pass and the weights are formed there,
 // so each output element then issues its S loads back to back.
+// RUNS: the matrix-core kernel's split wrote the partials, its 32-position
+// runs on XCD (run % 8) (T a multiple of 256): block c takes an item whose
+// run lies on c's own XCD (c % 8), so the partials are read from the L2 they
+// were written to.
 template <int D, int G, bool FORMS = false>
 __global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, AttOut out, int64_t T, int64_t H,
-                                                                int64_t KVH, int S) {
+                                                                int64_t KVH, int S, int runs = 0) {
   extern __shared__ float st[];  // [S][2G] statistics, then [S][G] weights, [G] denominators
-  const int64_t item = blockIdx.x;
+  int64_t item = blockIdx.x;
+  if (runs) {
+    const int64_t x = item & 7, sl = item >> 3, per = T >> 3;  // items of one XCD per (sequence, kv head)
+    const int64_t bjx = sl / per, r = sl - bjx * per;
+    item = bjx * T + 32 * (x + 8 * (r >> 5)) + (r & 31);
+  }
   const int64_t p = item % T, bj = item / T;
   const int64_t j = bj % KVH, b = bj / KVH;
   constexpr int PS = G * (D + 2);  // floats per chunk partial
@@ -393,14 +402,18 @@ __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const 
 template <int G, typename KV, bool FORMS>
 __global__ void __launch_bounds__(G * 64)
 flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, int64_t T, int64_t H, int64_t KVH,
-                      int64_t pos0, int64_t maxc, float scale, int64_t kchunk, float *part) {
+                      int64_t pos0, int64_t maxc, float scale, int64_t kchunk, float *part, int item_major) {
   constexpr int D = 64, NT = G * 64;
   constexpr bool EXACT = sizeof(KV) == 2;  // a BF16 cache: one part
   constexpr int KP = EXACT ? 1 : 3;
   __shared__ __attribute__((aligned(16))) __bf16 ks[2][KP][32 * FL3_KS];
   __shared__ __attribute__((aligned(16))) __bf16 vs[2][KP][64 * FL3_VS];
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
-  const int64_t bj = blockIdx.y;  // (sequence, kv head)
+  // Block (run x, item y) -- or, item-major (many items), the grid's x the
+  // item, so every block of an item is on one XCD (workgroup w runs on XCD
+  // w % 8) and its keys and values are read into one L2.
+  const int64_t bx = item_major ? blockIdx.y : blockIdx.x;
+  const int64_t bj = item_major ? blockIdx.x : blockIdx.y;  // (sequence, kv head)
   const int64_t j = bj % KVH, b = bj / KVH;
   const int n = lane & 31, half = lane >> 5;
   const int64_t ctx = pos0 + T;
@@ -415,8 +428,8 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
   // one run a block, no pairing.
   const bool split = kchunk > 0;
   for (int pass = 0; pass < (split ? 1 : 2); ++pass) {
-    const int64_t qb = pass == 0 ? static_cast<int64_t>(blockIdx.x) : nqb - 1 - blockIdx.x;
-    if (pass == 1 && qb == static_cast<int64_t>(blockIdx.x)) break;
+    const int64_t qb = pass == 0 ? bx : nqb - 1 - bx;
+    if (pass == 1 && qb == bx) break;
     const int64_t p0 = qb * 32, p = p0 + n;
     const bool live = p < T;
     const int64_t pq = live ? p : T - 1;
@@ -626,20 +639,28 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
   if (kchunk > 0) {
     const dim3 grid(static_cast<unsigned>((T + 31) / 32), static_cast<unsigned>(batch * KVH), static_cast<unsigned>(S));
     flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk,
-                                                                   part);
+                                                                   part, 0);
+    // With the runs a multiple of 8 the split's blocks of a run share an XCD
+    // (run % 8): the combine reads each item's partials there.
+    const int runs = T % 256 == 0 ? 1 : 0;
     const unsigned items = static_cast<unsigned>(batch * KVH * T);
     const size_t smem = static_cast<size_t>(3 * G * S + G) * sizeof(float);
     if (out.form == MI_F32)
-      attention_combine_kernel<64, G, false><<<items, 256, smem, st>>>(part, out, T, H, KVH, S);
+      attention_combine_kernel<64, G, false><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs);
     else
-      attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S);
+      attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs);
     return;
   }
-  const dim3 grid(static_cast<unsigned>(((T + 31) / 32 + 1) / 2), static_cast<unsigned>(batch * KVH));
+  // Many items (a multiple of 8): item-major, each item's blocks on one XCD.
+  const int64_t pairs = ((T + 31) / 32 + 1) / 2, items = batch * KVH;
+  const int im = items % 8 == 0 ? 1 : 0;
+  const dim3 grid(static_cast<unsigned>(im ? items : pairs), static_cast<unsigned>(im ? pairs : items));
   if (out.form == MI_F32)
-    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
+    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr,
+                                                                   im);
   else
-    flash3_prefill_kernel<G, KV, true><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr);
+    flash3_prefill_kernel<G, KV, true><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr,
+                                                                  im);
 }
 
 template <typename KV>
