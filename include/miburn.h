@@ -542,7 +542,8 @@ int mi_attention_rows(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
                       int64_t kv_heads, int64_t pos0, float scale,
                       mi_id *out);
 /* mi_attention_rows with its result in `out_form`: MI_F32 (mi_attention_rows
- * itself), MI_BF16 (each value rounded once), or tiles of the [batch t,
+ * itself), MI_BF16 (each value rounded once), MI_BF16_PARTS (the F32
+ * values' parts, [batch t, 2 heads d]), or tiles of the [batch t,
  * heads d] result (MI_TILES_BF16 / MI_TILES_PARTS; batch t a multiple of 32)
  * -- the operand an o projection against a tiled weight reads, stored by the
  * matrix-core (many new positions) kernel itself; other paths convert their
@@ -655,7 +656,8 @@ int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id sin_table,
                       int64_t seq, int64_t heads, int64_t kv_heads, int64_t pos0,
                       mi_id k_cache, mi_id v_cache, int grouped, mi_id *q_out);
 /* Engine::cast_float (server.rs:128): F32 <-> BF16, ties to even, NaN kept
- * a NaN; and I32 -> F32 (`as f32`). */
+ * a NaN; and I32 -> F32 (`as f32`).  `out_elem` MI_BF16_PARTS: an F32
+ * buffer's parts (columns a multiple of 4). */
 int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out);
 /* Engine::cast_bfp (server.rs:141-147, 1035-1050; Session::store_bfp and
  * bfp_to_f32): `format` MI_BFP8 stores an F32 or BF16 buffer as BFP8 by the

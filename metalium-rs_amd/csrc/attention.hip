@@ -220,8 +220,10 @@ __global__ void __launch_bounds__(NW * 64) attention_chunk_kernel(const float *q
 }
 
 // Where an attention result value (row, col) of [R, C] goes: F32 rows (the
-// plain form), BF16 rows rounded once, or the tiles an o projection reads
-// (MI_TILES_BF16, or MI_TILES_PARTS: heads' plane then remainders').
+// plain form), BF16 rows rounded once, an F32 value's BF16 parts in rows
+// (MI_BF16_PARTS: a row's heads, then its remainders), or the tiles an o
+// projection reads (MI_TILES_BF16, or MI_TILES_PARTS: heads' plane then
+// remainders').
 struct AttOut {
   void *p = nullptr;
   int form = MI_F32;
@@ -233,6 +235,13 @@ __device__ __forceinline__ void att_put(const AttOut &o, int64_t r, int64_t c, f
     case MI_F32: static_cast<float *>(o.p)[r * o.C + c] = v; break;
     case MI_BF16: h[r * o.C + c] = f32_to_bf16_bits(v); break;
     case MI_TILES_BF16: h[tile_offset(r, c, o.C)] = f32_to_bf16_bits(v); break;
+    case MI_BF16_PARTS: {
+      uint16_t hi, lo;
+      split_bf16(v, hi, lo);
+      h[r * 2 * o.C + c] = hi;
+      h[r * 2 * o.C + o.C + c] = lo;
+      break;
+    }
     default: {
       uint16_t hi, lo;
       split_bf16(v, hi, lo);
@@ -249,6 +258,7 @@ __device__ __forceinline__ void att_put4(const AttOut &o, int64_t r, int64_t c, 
     case MI_F32: *reinterpret_cast<float4 *>(static_cast<float *>(o.p) + r * o.C + c) = v; break;
     case MI_BF16: f32x4_put(h + r * o.C + c, v); break;
     case MI_TILES_BF16: f32x4_put(h + tile_offset(r, c, o.C), v); break;
+    case MI_BF16_PARTS: parts4_put(h + r * 2 * o.C + c, h + r * 2 * o.C + o.C + c, v); break;
     default: {
       const int64_t t = tile_offset(r, c, o.C);
       parts4_put(h + t, h + o.R * o.C + t, v);
@@ -397,9 +407,10 @@ __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const 
   return c;
 }
 
-// FORMS: the result may be stored in another form than F32 rows (the
-// store's form switch is compiled in only then).
-template <int G, typename KV, bool FORMS>
+// FORMS: the result's form -- 0 F32 rows, 1 BF16 parts in rows, 2 any
+// (the store's form switch); each compiles only its own store, so the F32
+// and parts kernels keep two waves a SIMD.
+template <int G, typename KV, int FORMS>
 __global__ void __launch_bounds__(G * 64)
 flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, int64_t T, int64_t H, int64_t KVH,
                       int64_t pos0, int64_t maxc, float scale, int64_t kchunk, float *part, int item_major) {
@@ -619,7 +630,11 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
       for (int c = 0; c < 4; ++c) {
         const float4 y0 = make_float4(o0[4 * c] / den, o0[4 * c + 1] / den, o0[4 * c + 2] / den, o0[4 * c + 3] / den);
         const float4 y1 = make_float4(o1[4 * c] / den, o1[4 * c + 1] / den, o1[4 * c + 2] / den, o1[4 * c + 3] / den);
-        if constexpr (FORMS) {
+        if constexpr (FORMS == 1) {
+          uint16_t *h = static_cast<uint16_t *>(out.p) + orow * 2 * out.C + ocol;
+          parts4_put(h + 8 * c, h + out.C + 8 * c, y0);
+          parts4_put(h + 32 + 8 * c, h + out.C + 32 + 8 * c, y1);
+        } else if constexpr (FORMS == 2) {
           att_put4(out, orow, ocol + 8 * c, y0);
           att_put4(out, orow, ocol + 32 + 8 * c, y1);
         } else {
@@ -638,7 +653,7 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
                   float *part) {
   if (kchunk > 0) {
     const dim3 grid(static_cast<unsigned>((T + 31) / 32), static_cast<unsigned>(batch * KVH), static_cast<unsigned>(S));
-    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk,
+    flash3_prefill_kernel<G, KV, 0><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, kchunk,
                                                                    part, 0);
     // With the runs a multiple of 8 the split's blocks of a run share an XCD
     // (run % 8): the combine reads each item's partials there.
@@ -656,11 +671,11 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
   const int im = items % 8 == 0 ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(im ? items : pairs), static_cast<unsigned>(im ? pairs : items));
   if (out.form == MI_F32)
-    flash3_prefill_kernel<G, KV, false><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr,
-                                                                   im);
+    flash3_prefill_kernel<G, KV, 0><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
+  else if (out.form == MI_BF16_PARTS)
+    flash3_prefill_kernel<G, KV, 1><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
   else
-    flash3_prefill_kernel<G, KV, true><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr,
-                                                                  im);
+    flash3_prefill_kernel<G, KV, 2><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
 }
 
 template <typename KV>
@@ -1394,7 +1409,8 @@ int attention_new(mi_ctx *ctx, const AttPlan &P, int64_t batch, int64_t t, int64
   }
   mi_id id;
   Buffer *ob;
-  int s = new_buffer(ctx, R, form == MI_TILES_PARTS ? 2 * C : C, form == MI_F32 ? MI_F32 : MI_BF16, &id, &ob);
+  const bool parts = form == MI_TILES_PARTS || form == MI_BF16_PARTS;
+  int s = new_buffer(ctx, R, parts ? 2 * C : C, form == MI_F32 ? MI_F32 : MI_BF16, &id, &ob);
   if (s) return s;
   ob->tiles = tiled ? form : 0;
   AttOut o;
@@ -1433,7 +1449,8 @@ extern "C" int mi_attention_rows_as(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v
                                     mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
-  if (out_form != MI_F32 && out_form != MI_BF16 && out_form != MI_TILES_BF16 && out_form != MI_TILES_PARTS)
+  if (out_form != MI_F32 && out_form != MI_BF16 && out_form != MI_BF16_PARTS && out_form != MI_TILES_BF16 &&
+      out_form != MI_TILES_PARTS)
     return fail(ctx, MI_E_ARG, "attention_rows_as: result form %d", out_form);
   AttPlan P;
   int s = attention_plan(ctx, q, k_cache, v_cache, batch, t, heads, kv_heads, pos0, nullptr, 0, &P);

@@ -166,6 +166,13 @@ inline Tensor tile(const Tensor &a, int form) {
   return Tensor(a.ctx(), id, {a.rows(), form == MI_TILES_PARTS ? 2 * a.cols() : a.cols()});
 }
 
+// An F32 tensor's BF16 parts ([rows, 2 cols], MI_BF16_PARTS: mi_cast).
+inline Tensor parts(const Tensor &a) {
+  mi_id id;
+  check(a.ctx(), mi_cast(a.ctx(), a.use(), MI_BF16_PARTS, &id), "parts");
+  return Tensor(a.ctx(), id, {a.rows(), 2 * a.cols()});
+}
+
 inline Tensor float_cast(const Tensor &a, int elem) {
   mi_id id;
   check(a.ctx(), mi_cast(a.ctx(), a.use(), elem, &id), "float_cast");

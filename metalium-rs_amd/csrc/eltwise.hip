@@ -484,12 +484,41 @@ __global__ void cast_kernel(const void *src, int se, void *dst, int de, int64_t 
     }
   }
 }
+// F32 rows as their BF16 parts ([rows, 2 cols]: a row's heads, then its
+// remainders), four values a thread.
+__global__ void parts_kernel(const float *src, int64_t rows, int64_t cols, uint16_t *dst) {
+  const int64_t q = cols / 4, n = rows * q;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / q, c = (i - r * q) * 4;
+    parts4_put(dst + r * 2 * cols + c, dst + r * 2 * cols + cols + c,
+               *reinterpret_cast<const float4 *>(src + r * cols + c));
+  }
+}
 }  // namespace mi
 
 extern "C" int mi_cast(mi_ctx *ctx, mi_id a, int out_elem, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
   MI_BUF(ctx, src, a);
+  if (out_elem == MI_BF16_PARTS) {  // an F32 buffer's parts (a product's split operand)
+    if (src->elem != MI_F32 || src->tiles || src->cols % 4)
+      return fail(ctx, MI_E_ARG, "cast of %s [%lld, %lld] to parts: want F32 rows of a multiple of 4",
+                  elem_name(src->elem), (long long)src->rows, (long long)src->cols);
+    mi_id id; Buffer *b;
+    if (int s = new_buffer(ctx, src->rows, 2 * src->cols, MI_BF16, &id, &b)) return s;
+    const int64_t n = src->rows * src->cols / 4;
+    if (n > 0)
+      parts_kernel<<<grid_for(n, 256 * 4, 256 * 32), 256, 0, ctx->stream>>>(static_cast<const float *>(src->ptr),
+                                                                          src->rows, src->cols,
+                                                                          static_cast<uint16_t *>(b->ptr));
+    if (int s = check_launch(ctx, "cast")) {
+      mi_free(ctx, id);
+      return s;
+    }
+    *out = id;
+    return MI_OK;
+  }
   if (!elem_valid(out_elem)) return fail(ctx, MI_E_ARG, "cast to unknown kind %d", out_elem);
   // BFP8 storage: packed or decoded (the reference's cast_bfp).
   if (out_elem == MI_BFP8) return mi_cast_bfp(ctx, a, MI_BFP8, out);

@@ -255,6 +255,7 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
   const bool parts_qkv = act == MI_F32 && parts_pay(ctx, rows, c.hidden, nqkv);
   const bool parts_gu = act == MI_F32 && parts_pay(ctx, rows, c.hidden, 2 * c.intermediate);
   const bool parts_down = act == MI_F32 && parts_pay(ctx, rows, c.intermediate, c.hidden);
+  const bool parts_o = act == MI_F32 && parts_pay(ctx, rows, H * D, c.hidden);
   // A layer's attention norm comes with the previous layer's down product
   // (mi_linear_add_rms_norm: where that product splits over k, a short
   // prompt's, its reduce forms the norm; bit for bit the two calls).
@@ -315,12 +316,22 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
                              : burn::float_matmul(xn, false, L.wqkv, true);
       q = burn::qkv_rope_cache(qkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k, L.cache_v, !fused);
     }
-    Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
-    if (act != MI_F32) oh = burn::float_cast(oh, act);
     // x + oh wo^T (the add in the product's epilogue), and its MLP norm.
     Tensor hn;
-    std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.wo, true, nullptr, &x, L.mlp_norm, c.eps,
-                                                parts_gu ? MI_BF16_PARTS : act);
+    if (parts_o) {
+      // The attention's result as parts, stored by the attention kernels
+      // (no split pass before the o product).
+      Tensor ohp = fused ? burn::attention_rows_as(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH,
+                                                   pos0, scale, MI_BF16_PARTS)
+                         : burn::parts(attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale));
+      x = burn::linear_parts(ohp, L.wo, true, nullptr, &x);
+      hn = burn::rms_norm(x, L.mlp_norm, c.eps, parts_gu ? MI_BF16_PARTS : act);
+    } else {
+      Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
+      if (act != MI_F32) oh = burn::float_cast(oh, act);
+      std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.wo, true, nullptr, &x, L.mlp_norm, c.eps,
+                                                  parts_gu ? MI_BF16_PARTS : act);
+    }
     // One product against the fused gate|up weight, silu(gate) * up of its halves.
     // With parts for both the gate|up and the down product, one launch forms
     // silu(gate) * up's parts from the interleaved weight (no F32 [rows,

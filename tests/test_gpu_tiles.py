@@ -245,7 +245,7 @@ def test_tiles_refusals(engine):
 
 @pytest.mark.parametrize("batch,t,pos0,kv16", [(1, 512, 0, False), (1, 512, 0, True), (2, 128, 64, False),
                                                (2, 16, 8, False)])  # the last on the key-chunk kernels
-@pytest.mark.parametrize("form", [BF16, TILES_BF16, TILES_PARTS])
+@pytest.mark.parametrize("form", [BF16, miburn.BF16_PARTS, TILES_BF16, TILES_PARTS])
 def test_attention_rows_as_equals_rows_then_form(engine, batch, t, pos0, kv16, form):
     H, KVH, D = 9, 3, 64
     maxc = pos0 + t + 8
@@ -260,6 +260,10 @@ def test_attention_rows_as_equals_rows_then_form(engine, batch, t, pos0, kv16, f
     got = engine.download(engine.attention_rows_as(q, k, v, batch, t, H, KVH, pos0, scale, form))
     if form == BF16:
         same_bits(got, orc.to_bf16(y), np.uint16)
+    elif form == miburn.BF16_PARTS:
+        same_bits(got, split_parts(y), np.uint16)
+        # mi_cast's parts of the F32 rows: the same bits.
+        same_bits(engine.download(engine.cast_float(engine.upload(y), miburn.BF16_PARTS)), split_parts(y), np.uint16)
     elif form == TILES_BF16:
         same_bits(got.reshape(-1), tiled(orc.to_bf16(y)), np.uint16)
     else:
