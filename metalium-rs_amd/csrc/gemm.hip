@@ -721,10 +721,18 @@ struct DmaOperand {
     int64_t first_row, limit;
     const char *clamp;
   };
+  // A wave's DMA instructions per tile: its blocks wave, wave + NW, ...;
+  // where NW does not divide the blocks, a wave with one fewer repeats its
+  // last (the same bytes into the same LDS block), so every wave issues the
+  // same count and the counted waits stay exact.
+  template <int NW>
+  static constexpr int per_wave() {
+    return (BLOCKS + NW - 1) / NW;
+  }
   template <int NW>
   __device__ __forceinline__ static Src src_of(const uint16_t *src, int64_t ld, int64_t r0, int64_t k0, int wave,
                                                int lane) {
-    static_assert(BLOCKS % NW == 0, "blocks per wave");
+    static_assert(BLOCKS >= NW, "blocks per wave");
     const int lr = (lane * 16) / RB;          // row of this lane within its block
     const int pch = ((lane * 16) % RB) >> 4;  // physical chunk it fills
     uint32_t voff;
@@ -762,6 +770,9 @@ struct DmaOperand {
   // The DMA instruction of this wave's block i of the tile into `lds`.
   template <int NW>
   __device__ __forceinline__ static void issue(const Src &sr, int i, char *lds, int wave) {
+    if constexpr (BLOCKS % NW != 0) {
+      if (i * NW + wave >= BLOCKS) i -= 1;  // this wave's repeat of its last block
+    }
     const int b = i * NW + wave;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void *)(lds)));
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds0 + b * 1024);
@@ -787,7 +798,7 @@ struct DmaOperand {
                                               int wave, int lane, int64_t rows = 0) {
     const Src sr = rows ? src_edge<NW>(src, ld, r0, k0, wave, lane, rows) : src_of<NW>(src, ld, r0, k0, wave, lane);
 #pragma unroll
-    for (int i = 0; i < BLOCKS / NW; ++i) issue<NW>(sr, i, lds, wave);
+    for (int i = 0; i < per_wave<NW>(); ++i) issue<NW>(sr, i, lds, wave);
   }
 
   // The 8 BF16 of lane `lane` for the 32-row fragment at `row0`, k step p.
@@ -938,7 +949,7 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   using OA = DmaOperand<BM, AK, BK>;
   using OB = DmaOperand<BN, BKC, BK>;
   constexpr int STAGE = OA::BYTES + OB::BYTES;
-  constexpr int PA = OA::BLOCKS / NW, PB = OB::BLOCKS / NW;
+  constexpr int PA = OA::template per_wave<NW>(), PB = OB::template per_wave<NW>();
   constexpr int PER_TILE = PA + PB;  // this thread's DMA instructions per tile
   static_assert(NS >= 3 && NS <= 5, "stages");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
@@ -1520,6 +1531,20 @@ static hipError_t run_split(const Plan &p, hipStream_t st) {
 }
 
 static bool parts_small_tiles(const Plan &p);
+
+// A width of 192s that 256 does not divide (576: a 576-wide model's o and
+// down products), plain or with bias and residual, A and B k-contiguous, at
+// most a tile a CU: 256 x 192 tiles, eight waves of 64 x 96, where 256 x 256
+// ones would leave a quarter of every third column tile unused.  The q|k|v
+// and gate|up tails take column pairs of the 64-wide wave tiles, so those
+// keep the 256-wide ones.
+static bool pipe_192_fits(const Plan &p) {
+  return p.batch == 1 && !p.ta && p.tb && p.N % 256 && p.N % 192 == 0 && p.M % 256 == 0 && p.K % 32 == 0 &&
+         (p.M / 256) * (p.N / 192) <= 256 &&
+         p.lda % 8 == 0 && p.ldb % 8 == 0 && !(reinterpret_cast<uintptr_t>(p.a) & 15) &&
+         !(reinterpret_cast<uintptr_t>(p.b) & 15) && !p.swiglu && !p.qkv.mode;
+}
+
 template <typename TO>
 static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   using T = uint16_t;
@@ -1540,7 +1565,10 @@ static hipError_t run_bf16(const Plan &p, hipStream_t st) {
   if (p.batch == 1 && !p.ta && p.tb && p.N % 16 == 0 && p.M % 128 == 0 && p.K % 32 == 0 && p.lda % 8 == 0 &&
       p.ldb % 8 == 0 && !(reinterpret_cast<uintptr_t>(p.a) & 15) && !(reinterpret_cast<uintptr_t>(p.b) & 15) &&
       tiles(128, 128) >= 128) {
-    if (!parts_small_tiles(p)) return launch_pipe_edge<TO, 256, 256, 5, 2, 4>(p, st);
+    if (!parts_small_tiles(p)) {
+      if (pipe_192_fits(p)) return launch_pipe_cfg<TO, 256, 192, 5, true, true, 4, 2, false>(p, st);
+      return launch_pipe_edge<TO, 256, 256, 5, 2, 4>(p, st);
+    }
     return launch_pipe_edge<TO, 128, 128, 5, 2, 2>(p, st);
   }
   if (tiles_exactly(p, 64, 64, 64, 8))
@@ -1847,6 +1875,9 @@ static hipError_t launch_direct(const Plan &q, hipStream_t st) {
   }
   if (q.N % 256 == 0)
     return bf ? launch_pipe<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe<float, 256, 256, 5, 2, 4>(q, st);
+  if (pipe_192_fits(q))
+    return bf ? launch_pipe_cfg<uint16_t, 256, 192, 5, true, true, 4, 2, false>(q, st)
+              : launch_pipe_cfg<float, 256, 192, 5, true, true, 4, 2, false>(q, st);
   return bf ? launch_pipe_edge<uint16_t, 256, 256, 5, 2, 4>(q, st) : launch_pipe_edge<float, 256, 256, 5, 2, 4>(q, st);
 }
 

@@ -557,8 +557,8 @@ def test_matmul_mixed_f32_bf16(engine, mode, tb, mnk):
 def test_matmul_mixed_stacked_split(engine, mode, mnk):
     """F32 activations x BF16 weights [n, k] at the prefill's sizes: in the
     fast mode the activations are split once into BF16 hi | lo parts and the
-    product runs on the direct BF16 kernel with the weight's k wrapping (widths
-    960 and 576 take its edge tiles).  Random operands within the F32 bound;
+    product runs on the direct BF16 kernel with the weight's k wrapping (width
+    960 takes its edge tiles, 576 at 16384 rows its 256 x 192 tiles).  Random operands within the F32 bound;
     small integers bit for bit; a linear layer's bias and residual too."""
     m, n, k = mnk
     a, b = rnd(m, k), orc.to_bf16(rnd(n, k))
@@ -581,7 +581,8 @@ def test_matmul_mixed_stacked_split(engine, mode, mnk):
 def test_matmul_bf16_edge_tiles(engine, mnk):
     """BF16 x BF16 [n, k] products whose width the tiles do not divide (the
     performance contract's prefill products): the direct kernel's edge tiles
-    (128 x 128 at 4096 rows, 256 x 256 at 16384), small integers bit for bit
+    (128 x 128 at 4096 rows, 256 x 256 at 16384; 576 wide there, 256 x 192
+    tiles that divide it), small integers bit for bit
     against float64, random operands within the F32 bound of the oracle fed
     the same BF16 values, and a linear layer's residual bit for bit."""
     m, n, k = mnk
