@@ -407,9 +407,9 @@ __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const 
   return c;
 }
 
-// FORMS: the result's form -- 0 F32 rows, 1 BF16 parts in rows, 2 any
-// (the store's form switch); each compiles only its own store, so the F32
-// and parts kernels keep two waves a SIMD.
+// FORMS: the result's form -- 0 F32 rows, 1 BF16 parts in rows, 3 BF16
+// rows, 2 any (the store's form switch); each compiles only its own store,
+// so the row-form kernels keep two waves a SIMD.
 template <int G, typename KV, int FORMS>
 __global__ void __launch_bounds__(G * 64)
 flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, int64_t T, int64_t H, int64_t KVH,
@@ -634,6 +634,10 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
           uint16_t *h = static_cast<uint16_t *>(out.p) + orow * 2 * out.C + ocol;
           parts4_put(h + 8 * c, h + out.C + 8 * c, y0);
           parts4_put(h + 32 + 8 * c, h + out.C + 32 + 8 * c, y1);
+        } else if constexpr (FORMS == 3) {
+          uint16_t *h = static_cast<uint16_t *>(out.p) + orow * out.C + ocol;
+          f32x4_put(h + 8 * c, y0);
+          f32x4_put(h + 32 + 8 * c, y1);
         } else if constexpr (FORMS == 2) {
           att_put4(out, orow, ocol + 8 * c, y0);
           att_put4(out, orow, ocol + 32 + 8 * c, y1);
@@ -674,6 +678,8 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
     flash3_prefill_kernel<G, KV, 0><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
   else if (out.form == MI_BF16_PARTS)
     flash3_prefill_kernel<G, KV, 1><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
+  else if (out.form == MI_BF16)
+    flash3_prefill_kernel<G, KV, 3><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
   else
     flash3_prefill_kernel<G, KV, 2><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
 }

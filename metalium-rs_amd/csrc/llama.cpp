@@ -327,8 +327,15 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
       x = burn::linear_parts(ohp, L.wo, true, nullptr, &x);
       hn = burn::rms_norm(x, L.mlp_norm, c.eps, parts_gu ? MI_BF16_PARTS : act);
     } else {
-      Tensor oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
-      if (act != MI_F32) oh = burn::float_cast(oh, act);
+      // BF16 activations: the attention kernels store the result as BF16.
+      Tensor oh;
+      if (fused && act == MI_BF16) {
+        oh = burn::attention_rows_as(q.reshape({rows, H * D}), L.cache_k, L.cache_v, batch, t, H, KVH, pos0, scale,
+                                     MI_BF16);
+      } else {
+        oh = attention_of(m, L, q, batch, t, pos0, ctxlen, fused, mask, scale);
+        if (act != MI_F32) oh = burn::float_cast(oh, act);
+      }
       std::tie(x, hn) = burn::linear_add_rms_norm(oh, L.wo, true, nullptr, &x, L.mlp_norm, c.eps,
                                                   parts_gu ? MI_BF16_PARTS : act);
     }

@@ -243,8 +243,11 @@ def test_tiles_refusals(engine):
     engine.sync()
 
 
+# (1, 512): the matrix-core kernel split over keys, then the combine; (32,
+# 256): unsplit, item-major, each form stored by the kernel itself; (2, 16):
+# the key-chunk kernels.
 @pytest.mark.parametrize("batch,t,pos0,kv16", [(1, 512, 0, False), (1, 512, 0, True), (2, 128, 64, False),
-                                               (2, 16, 8, False)])  # the last on the key-chunk kernels
+                                               (32, 256, 0, False), (32, 256, 0, True), (2, 16, 8, False)])
 @pytest.mark.parametrize("form", [BF16, miburn.BF16_PARTS, TILES_BF16, TILES_PARTS])
 def test_attention_rows_as_equals_rows_then_form(engine, batch, t, pos0, kv16, form):
     H, KVH, D = 9, 3, 64
