@@ -823,40 +823,61 @@ extern "C" int mi_rope(mi_ctx *ctx, mi_id x, mi_id cos_table, mi_id sin_table, i
   return MI_OK;
 }
 
-// qkv_rope_cache_kernel's work, one block per row and four columns a thread
-// (d a multiple of 8, so a float4 of one half of a head has its rotation
-// partner at the same place in the other half).  The head, sequence and
-// position come from one small division per thread and one per block, not
-// four 64-bit divisions per element.
+// qkv_rope_cache_kernel's work, one wavefront per row (four a block) and
+// four columns a lane (d a multiple of 8, so a float4 of one half of a head
+// has its rotation partner at the same place in the other half).  A row's
+// loads are all issued before its first store (up to NQ float4 a lane: rows
+// of up to 256 NQ columns; wider ones loop).  The head, sequence and position
+// come from one small division per lane and one per row, not four 64-bit
+// divisions per element.
 template <typename KV>
 __global__ void __launch_bounds__(256) qkv_rope_cache_row_kernel(const float *qkv, const float *cosp,
                                                                  const float *sinp, float *q, KV *kc, KV *vc,
-                                                                 int64_t seq, int heads, int kv, int d, int64_t maxc,
-                                                                 int64_t pos0, int grouped) {
+                                                                 int64_t rows, int64_t seq, int heads, int kv, int d,
+                                                                 int64_t maxc, int64_t pos0, int grouped) {
+  constexpr int NQ = 4;
   const int w = (heads + 2 * kv) * d, half = d / 2, G = heads / kv;
-  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
   const int64_t b = r / seq, p = r - b * seq, pos = pos0 + p;
   const float *xr = qkv + r * w;
-  for (int c = 4 * threadIdx.x; c < w; c += 4 * 256) {
-    const int h = c / d, j = c - h * d;
-    float4 y = *reinterpret_cast<const float4 *>(xr + c);
-    if (h < heads + kv) {
-      const float4 rv = *reinterpret_cast<const float4 *>(xr + h * d + (j < half ? j + half : j - half));
-      const float4 cv = *reinterpret_cast<const float4 *>(cosp + pos * d + j);
-      const float4 sv = *reinterpret_cast<const float4 *>(sinp + pos * d + j);
-      y.x = __fadd_rn(__fmul_rn(y.x, cv.x), __fmul_rn(rv.x, sv.x));
-      y.y = __fadd_rn(__fmul_rn(y.y, cv.y), __fmul_rn(rv.y, sv.y));
-      y.z = __fadd_rn(__fmul_rn(y.z, cv.z), __fmul_rn(rv.z, sv.z));
-      y.w = __fadd_rn(__fmul_rn(y.w, cv.w), __fmul_rn(rv.w, sv.w));
+  for (int c0 = 4 * lane; c0 < w; c0 += 4 * 64 * NQ) {
+    float4 y[NQ], rv[NQ], cv[NQ], sv[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int c = c0 + 4 * 64 * u;
+      if (c < w) {
+        const int h = c / d, j = c - h * d;
+        y[u] = *reinterpret_cast<const float4 *>(xr + c);
+        if (h < heads + kv) {
+          rv[u] = *reinterpret_cast<const float4 *>(xr + h * d + (j < half ? j + half : j - half));
+          cv[u] = *reinterpret_cast<const float4 *>(cosp + pos * d + j);
+          sv[u] = *reinterpret_cast<const float4 *>(sinp + pos * d + j);
+        }
+      }
     }
-    if (h < heads) {
-      const int kvh = h / G, g = h - kvh * G;
-      const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
-      *reinterpret_cast<float4 *>(q + row * d + j) = y;
-    } else if (h < heads + kv) {
-      f32x4_put(kc + ((b * kv + (h - heads)) * maxc + pos) * d + j, y);
-    } else {
-      f32x4_put(vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j, y);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int c = c0 + 4 * 64 * u;
+      if (c >= w) break;
+      const int h = c / d, j = c - h * d;
+      float4 o = y[u];
+      if (h < heads + kv) {
+        o.x = __fadd_rn(__fmul_rn(y[u].x, cv[u].x), __fmul_rn(rv[u].x, sv[u].x));
+        o.y = __fadd_rn(__fmul_rn(y[u].y, cv[u].y), __fmul_rn(rv[u].y, sv[u].y));
+        o.z = __fadd_rn(__fmul_rn(y[u].z, cv[u].z), __fmul_rn(rv[u].z, sv[u].z));
+        o.w = __fadd_rn(__fmul_rn(y[u].w, cv[u].w), __fmul_rn(rv[u].w, sv[u].w));
+      }
+      if (h < heads) {
+        const int kvh = h / G, g = h - kvh * G;
+        const int64_t row = grouped ? ((b * kv + kvh) * seq + p) * G + g : r * heads + h;
+        *reinterpret_cast<float4 *>(q + row * d + j) = o;
+      } else if (h < heads + kv) {
+        f32x4_put(kc + ((b * kv + (h - heads)) * maxc + pos) * d + j, o);
+      } else {
+        f32x4_put(vc + ((b * kv + (h - heads - kv)) * maxc + pos) * d + j, o);
+      }
     }
   }
 }
@@ -947,16 +968,16 @@ extern "C" int mi_qkv_rope_cache(mi_ctx *ctx, mi_id qkv, mi_id cos_table, mi_id 
   float *qp = static_cast<float *>(ob->ptr);
   const bool kv16 = kb->elem == MI_BF16;
   if (R > 0 && D % 8 == 0 && aligned && R <= INT32_MAX && xb->cols <= INT32_MAX) {
-    const unsigned grid = static_cast<unsigned>(R);
+    const unsigned grid = static_cast<unsigned>((R + 3) / 4);
     const int hi = static_cast<int>(heads), kvi = static_cast<int>(kv_heads), di = static_cast<int>(D);
     if (kv16)
       qkv_rope_cache_row_kernel<uint16_t><<<grid, 256, 0, ctx->stream>>>(
-          xp, cp, sp, qp, static_cast<uint16_t *>(kb->ptr), static_cast<uint16_t *>(vb->ptr), seq, hi, kvi, di, maxc,
-          pos0, grouped ? 1 : 0);
+          xp, cp, sp, qp, static_cast<uint16_t *>(kb->ptr), static_cast<uint16_t *>(vb->ptr), R, seq, hi, kvi, di,
+          maxc, pos0, grouped ? 1 : 0);
     else
       qkv_rope_cache_row_kernel<float><<<grid, 256, 0, ctx->stream>>>(
-          xp, cp, sp, qp, static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), seq, hi, kvi, di, maxc, pos0,
-          grouped ? 1 : 0);
+          xp, cp, sp, qp, static_cast<float *>(kb->ptr), static_cast<float *>(vb->ptr), R, seq, hi, kvi, di, maxc,
+          pos0, grouped ? 1 : 0);
     s = check_launch(ctx, "qkv_rope_cache");
     if (s) { mi_free(ctx, id); return s; }
   } else if (R > 0) {

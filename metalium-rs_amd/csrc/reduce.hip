@@ -732,9 +732,17 @@ __global__ void __launch_bounds__(256) softmax_long_kernel(const void *x, int el
 }
 
 // ------------------------------------------------------- RMSNorm, LayerNorm
-template <int T>
+// XF: the input and the gain F32, fixed at compile time (else read from elem
+// and gelem); OE >= 0: the result's form, fixed likewise.  The fixed forms
+// carry no element switch around each load and store.
+template <int T, bool XF = false, int OE = -1>
 __global__ void __launch_bounds__(256) rms_norm_kernel(const void *x, int elem, const void *gamma, int gelem, float eps,
                                                        void *out, int out_elem, int64_t rows, int64_t cols) {
+  if constexpr (XF) {
+    elem = MI_F32;
+    gelem = MI_F32;
+  }
+  if constexpr (OE >= 0) out_elem = OE;
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -1024,7 +1032,20 @@ void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, f
   // half the chip idle).
   const int per = R < 4096 ? 1 : 4;
   const unsigned g = grid_for(R, per, INT32_MAX);
-  switch (pick_t(C)) {
+  const int t = pick_t(C);
+  if (xe == MI_F32 && (gp == nullptr || ge == MI_F32) && t >= 1 && t <= 16 &&
+      (out_elem == MI_F32 || out_elem == MI_BF16 || out_elem == MI_BF16_PARTS)) {
+    switch (t * 4 + (out_elem == MI_F32 ? 0 : out_elem == MI_BF16 ? 1 : 2)) {
+#define MI_RN(T)                                                                                                  \
+  case 4 * T: rms_norm_kernel<T, true, MI_F32><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 4 * T + 1: rms_norm_kernel<T, true, MI_BF16><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 4 * T + 2: rms_norm_kernel<T, true, MI_BF16_PARTS><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
+      MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16)
+#undef MI_RN
+    }
+    return;
+  }
+  switch (t) {
 #define MI_RN(T) case T: rms_norm_kernel<T><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
     MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16) MI_RN(32) MI_RN(64) MI_RN(128)
 #undef MI_RN

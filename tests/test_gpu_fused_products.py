@@ -168,7 +168,7 @@ def test_split_parts_reference_cases():
     assert lo[2] == 2.0 ** 120
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 576), (300, 1000), (5, 8192)])
+@pytest.mark.parametrize("rows,cols", [(64, 576), (300, 1000), (5, 8192), (8195, 576)])
 def test_rms_norm_parts_split_its_f32_result(engine, rows, cols):
     x = rnd(rows, cols)
     gamma = rnd(1, cols)

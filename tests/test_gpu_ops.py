@@ -414,9 +414,9 @@ def test_softmax_shift_invariance(engine):
 
 
 # ----------------------------------------------------------------------- norms
-@pytest.mark.parametrize("cols", [64, 576, 1000])
-def test_rms_norm(engine, cols):
-    x, g = rnd(50, cols), rnd(1, cols)
+@pytest.mark.parametrize("rows,cols", [(50, 64), (50, 576), (50, 1000), (8193, 576)])  # 8193: two rows a wavefront
+def test_rms_norm(engine, rows, cols):
+    x, g = rnd(rows, cols), rnd(1, cols)
     a, gb = engine.upload(x), engine.upload(g)
     close(engine.download(engine.rms_norm(a, gb, 1e-5)), orc.rms_norm(x, g, 1e-5), rtol=1e-5, atol=1e-7)
     close(engine.download(engine.rms_norm(a, 0, 1e-5)), orc.rms_norm(x, None, 1e-5), rtol=1e-5, atol=1e-7)

@@ -107,8 +107,10 @@ def test_copy_into4_against_numpy(engine, dims, dst_off, dst_st, src_off, src_st
     same_bits(engine.download(idst).reshape(-1), want)
 
 
+# (3, 7, 32, 8, 64): rows of 3072 columns, wider than one pass of a wavefront's loads.
 @pytest.mark.parametrize("batch,seq,heads,kv,d,pos0,maxc", [(2, 5, 9, 3, 64, 3, 16), (1, 33, 4, 4, 32, 0, 40),
-                                                           (3, 7, 8, 2, 16, 9, 20), (2, 3, 2, 1, 12, 1, 8)])
+                                                           (3, 7, 8, 2, 16, 9, 20), (2, 3, 2, 1, 12, 1, 8),
+                                                           (3, 7, 32, 8, 64, 2, 12)])
 def test_qkv_rope_cache_equals_composition(engine, batch, seq, heads, kv, d, pos0, maxc):
     rows, w = batch * seq, (heads + 2 * kv) * d
     qkv = rnd(rows, w)
