@@ -420,11 +420,18 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
   __shared__ __attribute__((aligned(16))) __bf16 ks[2][KP][32 * FL3_KS];
   __shared__ __attribute__((aligned(16))) __bf16 vs[2][KP][64 * FL3_VS];
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
-  // Block (run x, item y) -- or, item-major (many items), the grid's x the
-  // item, so every block of an item is on one XCD (workgroup w runs on XCD
-  // w % 8) and its keys and values are read into one L2.
-  const int64_t bx = item_major ? blockIdx.y : blockIdx.x;
-  const int64_t bj = item_major ? blockIdx.x : blockIdx.y;  // (sequence, kv head)
+  // item_major 0: block (pair of runs x, item y).  1 (many items): the
+  // grid's x the item, so every block of an item is on one XCD (workgroup w
+  // runs on XCD w % 8) and its keys and values are read into one L2.  2 (the
+  // items a multiple of 8): one run a block, blocks in order of falling work
+  // -- block w takes run nqb - 1 - w / items of item w % items -- so the
+  // dispatcher, handing blocks out in order as CUs free up, fills the last
+  // ones with the shortest runs (equal pairs left the chip's second round of
+  // blocks half empty), each item still on one XCD.
+  const int64_t nqb = (T + 31) / 32;
+  const int64_t nitems = static_cast<int64_t>(item_major == 2 ? gridDim.x / nqb : 0);
+  const int64_t bx = item_major == 2 ? nqb - 1 - blockIdx.x / nitems : item_major ? blockIdx.y : blockIdx.x;
+  const int64_t bj = item_major == 2 ? blockIdx.x % nitems : item_major ? blockIdx.x : blockIdx.y;  // (sequence, kv head)
   const int64_t j = bj % KVH, b = bj / KVH;
   const int n = lane & 31, half = lane >> 5;
   const int64_t ctx = pos0 + T;
@@ -432,13 +439,12 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
   const float scale2 = scale * 1.4426950408889634f;
   const KV *K = kc + bj * maxc * D, *V = vc + bj * maxc * D;
   const int ctx32 = static_cast<int>(ctx);  // the host keeps a cache item below 2^31 / D rows
-  const int64_t nqb = (T + 31) / 32;
   // Split over keys (kchunk > 0): block (query run x, item y, key range z)
   // takes keys [z kchunk, (z + 1) kchunk) of its run's and writes the
   // range's partials (max, sum, unnormalised P V) for the combine pass;
   // one run a block, no pairing.
   const bool split = kchunk > 0;
-  for (int pass = 0; pass < (split ? 1 : 2); ++pass) {
+  for (int pass = 0; pass < (split || item_major == 2 ? 1 : 2); ++pass) {
     const int64_t qb = pass == 0 ? bx : nqb - 1 - bx;
     if (pass == 1 && qb == bx) break;
     const int64_t p0 = qb * 32, p = p0 + n;
@@ -670,10 +676,11 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
       attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs);
     return;
   }
-  // Many items (a multiple of 8): item-major, each item's blocks on one XCD.
-  const int64_t pairs = ((T + 31) / 32 + 1) / 2, items = batch * KVH;
-  const int im = items % 8 == 0 ? 1 : 0;
-  const dim3 grid(static_cast<unsigned>(im ? items : pairs), static_cast<unsigned>(im ? pairs : items));
+  // Many items (a multiple of 8): one run a block, the longest first, each
+  // item's blocks on one XCD; else pairs of runs of equal total work.
+  const int64_t pairs = ((T + 31) / 32 + 1) / 2, items = batch * KVH, nqb = (T + 31) / 32;
+  const int im = items % 8 == 0 ? 2 : 0;
+  const dim3 grid = im ? dim3(static_cast<unsigned>(nqb * items)) : dim3(static_cast<unsigned>(pairs), static_cast<unsigned>(items));
   if (out.form == MI_F32)
     flash3_prefill_kernel<G, KV, 0><<<grid, G * 64, 0, st>>>(q, k, v, out, T, H, KVH, pos0, maxc, scale, 0, nullptr, im);
   else if (out.form == MI_BF16_PARTS)
