@@ -274,9 +274,13 @@ __device__ __forceinline__ void att_put4(const AttOut &o, int64_t r, int64_t c, 
 // runs on XCD (run % 8) (T a multiple of 256): block c takes an item whose
 // run lies on c's own XCD (c % 8), so the partials are read from the L2 they
 // were written to.
+// chunk > 0 (the matrix-core kernel's split, causal): position p's keys
+// reach only its first (pos0 + p) / chunk + 1 ranges, and only those are
+// read (the others carry no keys and were not written).
 template <int D, int G, bool FORMS = false>
 __global__ void __launch_bounds__(256) attention_combine_kernel(const float *part, AttOut out, int64_t T, int64_t H,
-                                                                int64_t KVH, int S, int runs = 0) {
+                                                                int64_t KVH, int S, int runs = 0, int64_t pos0 = 0,
+                                                                int64_t chunk = 0) {
   extern __shared__ float st[];  // [S][2G] statistics, then [S][G] weights, [G] denominators
   int64_t item = blockIdx.x;
   if (runs) {
@@ -288,6 +292,8 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
   const int64_t j = bj % KVH, b = bj / KVH;
   constexpr int PS = G * (D + 2);  // floats per chunk partial
   const float *pb = part + item * S * static_cast<int64_t>(PS);
+  const int64_t reach = chunk > 0 ? (pos0 + p) / chunk + 1 : S;
+  const int SR = static_cast<int>(reach < S ? reach : S);  // the ranges read
   float *w = st + 2 * G * S;
   float *den = w + G * S;
   // A thread's output elements e = tid + 256 i: their first CS chunks'
@@ -299,16 +305,16 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
   for (int i = 0; i < EP; ++i) {
     const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
 #pragma unroll
-    for (int s = 0; s < CS; ++s) ov[i][s] = s < S ? pb[s * PS + 2 * G + ec] : 0.0f;
+    for (int s = 0; s < CS; ++s) ov[i][s] = s < SR ? pb[s * PS + 2 * G + ec] : 0.0f;
   }
-  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
+  for (int e = threadIdx.x; e < 2 * G * SR; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
   __syncthreads();
   if (threadIdx.x < G) {
     const int g = threadIdx.x;
     float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + g]);
+    for (int s = 0; s < SR; ++s) M = max_nan(M, st[s * 2 * G + g]);
     float l = 0.0f;
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < SR; ++s) {
       const float ws = expf(st[s * 2 * G + g] - M);
       w[s * G + g] = ws;
       l += ws * st[s * 2 * G + G + g];
@@ -325,8 +331,8 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const float *par
       float num = 0.0f;
 #pragma unroll
       for (int s = 0; s < CS; ++s)
-        if (s < S) num += w[s * G + g] * ov[i][s];
-      for (int s = CS; s < S; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
+        if (s < SR) num += w[s * G + g] * ov[i][s];
+      for (int s = CS; s < SR; ++s) num += w[s * G + g] * pb[s * PS + 2 * G + e];
       if constexpr (FORMS) att_put(out, orow, ocol + e, num / den[g]);
       else static_cast<float *>(out.p)[orow * out.C + ocol + e] = num / den[g];
     }
@@ -477,6 +483,9 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
     const int64_t kend_run = pos0 + (p0 + 32 < T ? p0 + 32 : T);
     const int64_t kbeg = split ? static_cast<int64_t>(blockIdx.z) * kchunk : 0;
     const int64_t kend = split ? (kbeg + kchunk < kend_run ? kbeg + kchunk : kend_run) : kend_run;
+    // A key range past every position of the run: no partials (the combine
+    // reads only the ranges a position's keys reach).
+    if (split && kbeg >= kend_run) return;
     // Key and value blocks as 512 groups of 4 values, loaded into registers
     // for the next block while the current one is used: key group e is key
     // e / 16, d 4 (e % 16) .. + 3 (a 16-byte load); value group e is d e % 64
@@ -671,9 +680,9 @@ void launch_flash(hipStream_t st, const float *q, const KV *k, const KV *v, cons
     const unsigned items = static_cast<unsigned>(batch * KVH * T);
     const size_t smem = static_cast<size_t>(3 * G * S + G) * sizeof(float);
     if (out.form == MI_F32)
-      attention_combine_kernel<64, G, false><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs);
+      attention_combine_kernel<64, G, false><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs, pos0, kchunk);
     else
-      attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs);
+      attention_combine_kernel<64, G, true><<<items, 256, smem, st>>>(part, out, T, H, KVH, S, runs, pos0, kchunk);
     return;
   }
   // Many items (a multiple of 8): one run a block, the longest first, each

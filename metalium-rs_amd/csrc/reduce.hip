@@ -1033,13 +1033,16 @@ void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, f
   const int per = R < 4096 ? 1 : 4;
   const unsigned g = grid_for(R, per, INT32_MAX);
   const int t = pick_t(C);
-  if (xe == MI_F32 && (gp == nullptr || ge == MI_F32) && t >= 1 && t <= 16 &&
-      (out_elem == MI_F32 || out_elem == MI_BF16 || out_elem == MI_BF16_PARTS)) {
-    switch (t * 4 + (out_elem == MI_F32 ? 0 : out_elem == MI_BF16 ? 1 : 2)) {
+  const int form = out_elem == MI_F32 ? 0 : out_elem == MI_BF16 ? 1 : out_elem == MI_BF16_PARTS ? 2
+                 : out_elem == MI_TILES_BF16 ? 3 : out_elem == MI_TILES_PARTS ? 4 : -1;
+  if (xe == MI_F32 && (gp == nullptr || ge == MI_F32) && t >= 1 && t <= 16 && form >= 0) {
+    switch (t * 8 + form) {
 #define MI_RN(T)                                                                                                  \
-  case 4 * T: rms_norm_kernel<T, true, MI_F32><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
-  case 4 * T + 1: rms_norm_kernel<T, true, MI_BF16><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
-  case 4 * T + 2: rms_norm_kernel<T, true, MI_BF16_PARTS><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
+  case 8 * T: rms_norm_kernel<T, true, MI_F32><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 8 * T + 1: rms_norm_kernel<T, true, MI_BF16><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 8 * T + 2: rms_norm_kernel<T, true, MI_BF16_PARTS><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 8 * T + 3: rms_norm_kernel<T, true, MI_TILES_BF16><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break; \
+  case 8 * T + 4: rms_norm_kernel<T, true, MI_TILES_PARTS><<<g, 64 * per, 0, ctx->stream>>>(xp, xe, gp, ge, eps, out, out_elem, R, C); break;
       MI_RN(1) MI_RN(2) MI_RN(4) MI_RN(8) MI_RN(16)
 #undef MI_RN
     }
