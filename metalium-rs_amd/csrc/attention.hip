@@ -401,6 +401,19 @@ __device__ __forceinline__ void fl_split(float v, __bf16 &hi, __bf16 &mid, __bf1
   lo = static_cast<__bf16>(r2);
 }
 
+// fl_split of two exponentials (finite, < 2^8 here, or a quiet NaN) as
+// packed pairs: a quiet NaN's truncated head is itself NaN (its quiet bit is
+// in the head), so no finiteness check is needed -- a NaN gives NaN
+// products either way; the remainders rounded two at a time.
+__device__ __forceinline__ void fl_split2_exp(float a, float b, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+  const uint32_t ha = __float_as_uint(a) & 0xffff0000u, hb = __float_as_uint(b) & 0xffff0000u;
+  const float ra = a - __uint_as_float(ha), rb = b - __uint_as_float(hb);
+  mid = bf16x2_bits(ra, rb);
+  const float sa = ra - __uint_as_float(mid << 16), sb = rb - __uint_as_float(mid & 0xffff0000u);
+  lo = bf16x2_bits(sa, sb);
+  hi = (ha >> 16) | hb;
+}
+
 // The part products of one k step: A parts a[], B parts b[] (NA and NB of them).
 template <int NA, int NB>
 __device__ __forceinline__ flash_f32x16 fl_mfma(const fl_bf16x8 (&a)[NA], const fl_bf16x8 (&b)[NB], flash_f32x16 c) {
@@ -457,23 +470,16 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
     const bool live = p < T;
     const int64_t pq = live ? p : T - 1;
     const int64_t qpos = pos0 + pq;
-    // Q^T as the B operand of step s: q[p][16 s + 8 half .. + 7], three parts.
-    fl_bf16x8 qp[4][3];
+    // Q^T as the B operand of step s: q[p][16 s + 8 half .. + 7], three
+    // parts -- its loads issued here, split once the first key and value
+    // block's loads are in flight too.
+    float4 qv[4][2];
     {
       const float *qrow = q + (b * T + pq) * H * D + h * D + 8 * half;
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
-        const float4 v0 = *reinterpret_cast<const float4 *>(qrow + 16 * s2);
-        const float4 v1 = *reinterpret_cast<const float4 *>(qrow + 16 * s2 + 4);
-        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          __bf16 a0, a1, a2;
-          fl_split(vv[e], a0, a1, a2);
-          qp[s2][0][e] = a0;
-          qp[s2][1][e] = a1;
-          qp[s2][2][e] = a2;
-        }
+        qv[s2][0] = *reinterpret_cast<const float4 *>(qrow + 16 * s2);
+        qv[s2][1] = *reinterpret_cast<const float4 *>(qrow + 16 * s2 + 4);
       }
     }
     flash_f32x16 o0, o1;
@@ -540,6 +546,20 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
       }
     };
     fetch(kbeg < kend ? kbeg : 0);
+    fl_bf16x8 qp[4][3];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const float vv[8] = {qv[s2][0].x, qv[s2][0].y, qv[s2][0].z, qv[s2][0].w,
+                           qv[s2][1].x, qv[s2][1].y, qv[s2][1].z, qv[s2][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 a0, a1, a2;
+        fl_split(vv[e], a0, a1, a2);
+        qp[s2][0][e] = a0;
+        qp[s2][1][e] = a1;
+        qp[s2][2][e] = a2;
+      }
+    }
     stage(0);
     __syncthreads();
     for (int64_t j0 = kbeg, it = 0; j0 < kend; j0 += 32, ++it) {
@@ -587,17 +607,20 @@ flash3_prefill_kernel(const float *q, const KV *kc, const KV *vc, AttOut out, in
         m = mnew;
       }
       float ls = 0.0f;
+      uint32_t pw[2][3][4];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(st[r] - m), e1 = __builtin_amdgcn_exp2f(st[r + 1] - m);
+        ls += e0;
+        ls += e1;
+        fl_split2_exp(e0, e1, pw[r >> 3][0][(r & 7) >> 1], pw[r >> 3][1][(r & 7) >> 1], pw[r >> 3][2][(r & 7) >> 1]);
+      }
       fl_bf16x8 pb[2][3];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(st[r] - m);
-        ls += e;
-        __bf16 a0, a1, a2;
-        fl_split(e, a0, a1, a2);
-        pb[r >> 3][0][r & 7] = a0;
-        pb[r >> 3][1][r & 7] = a1;
-        pb[r >> 3][2][r & 7] = a2;
-      }
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp)
+          pb[i][pp] = __builtin_bit_cast(fl_bf16x8, make_uint4(pw[i][pp][0], pw[i][pp][1], pw[i][pp][2], pw[i][pp][3]));
       ls += __shfl_xor(ls, 32, 64);
       l += ls;
       // O^T += V^T P^T: step s2 contracts the keys of P^T's registers 8 s2 .. 8 s2 + 7.
