@@ -887,17 +887,77 @@ __device__ __forceinline__ void pipe_mfma(f32x16 (&acc)[TM][TN], const uint4 (&f
                                                           __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
 }
 
+// The rotary tables' rows of a block's BM result rows (cos, then sin), read
+// into the LDS stages once the main loop is done with them: row lr of a table
+// at stage (table (BM / RPS) + lr / RPS), RPS rows of 64 floats a stage.  One
+// request a thread per 16 bytes, all in flight together, instead of each
+// wavefront's 64 scalar loads a fragment.
+// Row lr of rotary table tbl (0 cos, 1 sin) among the stages (a select
+// between stages named at compile time, not an index into a pointer array,
+// which would live in scratch memory).
+template <int BM, int RPS>
+__device__ __forceinline__ char *qkv_table_row(char *const (&stages)[5], int tbl, int lr) {
+  static_assert(BM / RPS == 1 || BM / RPS == 2, "a table in one or two stages");
+  char *s0 = tbl ? stages[BM / RPS] : stages[0];
+  if constexpr (BM / RPS == 2) {
+    char *s1 = tbl ? stages[BM / RPS + 1] : stages[1];
+    s0 = lr < RPS ? s0 : s1;
+  }
+  return s0 + (lr % RPS) * 256;
+}
+
+template <int BM, int NS, int STAGE, int NT>
+__device__ __forceinline__ void qkv_tables(const QkvTail &t, int64_t m0, char *const (&stages)[5], int tid) {
+  constexpr int RPS = STAGE / 256;
+  static_assert(RPS >= 1 && 2 * BM <= NS * RPS, "rotary tables in the stages");
+  constexpr int PER = 2 * BM * 16 / NT, BATCH = PER < 8 ? PER : 8;  // 16-byte pieces a thread, in batches
+  static_assert(PER * NT == 2 * BM * 16 && PER % BATCH == 0, "table pieces a thread");
+  // The block's rows in one sequence (consecutive positions): no division a row.
+  const int64_t b0 = m0 / t.seq, p0 = m0 - b0 * t.seq;
+  const bool one = p0 + BM <= t.seq;
+  auto src = [&](int c) {
+    const int tbl = c / (BM * 16), rem = c - tbl * (BM * 16), lr = rem >> 4, q4 = rem & 15;
+    int64_t pos;
+    if (one) {
+      pos = t.pos0 + p0 + lr;
+    } else {
+      const int64_t row = m0 + lr, b = row / t.seq;
+      pos = t.pos0 + (row - b * t.seq);
+    }
+    return reinterpret_cast<const float4 *>((tbl ? t.sin : t.cos) + pos * 64 + 4 * q4);
+  };
+  auto dst = [&](int c) {
+    const int tbl = c / (BM * 16), rem = c - tbl * (BM * 16), lr = rem >> 4, q4 = rem & 15;
+    return reinterpret_cast<float4 *>(qkv_table_row<BM, RPS>(stages, tbl, lr) + 16 * q4);
+  };
+#pragma unroll
+  for (int u0 = 0; u0 < PER; u0 += BATCH) {
+    float4 v[BATCH];
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) v[u] = *src(tid + (u0 + u) * NT);
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) *dst(tid + (u0 + u) * NT) = v[u];
+  }
+}
+
 // The q|k|v tail of a wavefront whose 64 columns are head hb / 64: fragment
 // 0 holds its columns j = lane % 32, fragment 1 columns j + 32 -- each
-// other's RoPE partners -- at rows row0 + 32 i + 8 (r / 4) + r % 4.  Each
-// fragment's rotary entries are requested before its rows are written.
-template <int TM>
+// other's RoPE partners -- at rows row0 + 32 i + 8 (r / 4) + r % 4, the
+// block's rows from m0.  The rotary entries come from the LDS copy
+// qkv_tables made (RPS rows a stage).
+template <int TM, int BM, int RPS>
 __device__ __forceinline__ void qkv_tail(const GemmArgs &g, const f32x16 (&acc)[TM][2], int64_t row0, int64_t hb,
-                                         int j) {
+                                         int j, int64_t m0, char *const (&stages)[5]) {
   const QkvTail &t = g.qkv;
   if (hb >= g.N) return;  // an edge tile's columns past the last head
   const int h = static_cast<int>(hb >> 6);
   const bool rope = h < t.heads + t.kvh;
+  // The wavefront's head: a query head (its kv group and place in it), or
+  // kv head jj's key or value.
+  const int G = t.heads / t.kvh;
+  const bool isq = h < t.heads, isk = !isq && rope;
+  const int kvq = isq ? h / G : 0, gq = isq ? h - kvq * G : 0;
+  const int jj = isq ? 0 : (isk ? h - t.heads : h - t.heads - t.kvh);
   // A fragment's 32 rows (32-aligned) lie in one sequence when seq is a
   // multiple of 32: one division a fragment, not two a value.
   const bool whole = (t.seq & 31) == 0;
@@ -918,15 +978,49 @@ __device__ __forceinline__ void qkv_tail(const GemmArgs &g, const f32x16 (&acc)[
     if (rope) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = row0 + i * 32 + 8 * (r >> 2) + (r & 3);
-        int64_t b, p;
-        seq_of(row, b, p);
-        const int64_t pos = t.pos0 + p;
-        c0[r] = t.cos[pos * 64 + j];
-        c1[r] = t.cos[pos * 64 + j + 32];
-        s0[r] = t.sin[pos * 64 + j];
-        s1[r] = t.sin[pos * 64 + j + 32];
+        const int lr = static_cast<int>(row0 + i * 32 + 8 * (r >> 2) + (r & 3) - m0);
+        const float *cr = reinterpret_cast<const float *>(qkv_table_row<BM, RPS>(stages, 0, lr));
+        const float *sr = reinterpret_cast<const float *>(qkv_table_row<BM, RPS>(stages, 1, lr));
+        c0[r] = cr[j];
+        c1[r] = cr[j + 32];
+        s0[r] = sr[j];
+        s1[r] = sr[j + 32];
       }
+    }
+    if (whole) {
+      // The fragment's rows in one sequence: the wavefront's destination rows
+      // are base + p * stride for its head (q rows natural or grouped, or the
+      // k or v cache rows), so each value's address is a constant step from
+      // one base a fragment -- not qkv_put's divisions and products per value.
+      const int64_t b = fbs, p0 = fps + (row0 + i * 32 - fb);  // the position of value r = 0
+      int64_t base, stride;
+      if (isq) {
+        base = t.grouped ? ((b * t.kvh + kvq) * t.seq + p0) * G + gq : (b * t.seq + p0) * t.heads + h;
+        stride = t.grouped ? G : t.heads;
+      } else {
+        base = (b * t.kvh + jj) * t.maxc + t.pos0 + p0;
+        stride = 1;
+      }
+      float *qd = t.q + base * 64 + j;
+      float *cf = static_cast<float *>(isk ? t.kc : t.vc) + base * 64 + j;
+      uint16_t *ch = static_cast<uint16_t *>(isk ? t.kc : t.vc) + base * 64 + j;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t o = (8 * (r >> 2) + (r & 3)) * stride * 64;
+        float y0 = acc[i][0][r], y1 = acc[i][1][r];
+        if (rope) rope_pair(acc[i][0][r], acc[i][1][r], c0[r], c1[r], s0[r], s1[r], y0, y1);
+        if (isq) {
+          qd[o] = y0;
+          qd[o + 32] = y1;
+        } else if (t.mode == QKV_BF16) {
+          ch[o] = f32_to_bf16_bits(y0);
+          ch[o + 32] = f32_to_bf16_bits(y1);
+        } else {
+          cf[o] = y0;
+          cf[o + 32] = y1;
+        }
+      }
+      continue;
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1058,7 +1152,12 @@ __device__ __forceinline__ void gemm_pipe_body(const GemmArgs &g) {
   const int64_t row0 = m0 + wm * WTM + 4 * lhalf, col0 = n0 + wn * WTN + lrow;
   if constexpr (TN == 2) {
     if (g.qkv.mode) {
-      qkv_tail<TM>(g, acc, row0, n0 + wn * WTN, lrow);
+      __syncthreads();  // every wave past its last read of the stages
+      if (n0 < static_cast<int64_t>(g.qkv.heads + g.qkv.kvh) * 64) {  // a tile with RoPE heads
+        qkv_tables<BM, NS, STAGE, NW * 64>(g.qkv, m0, stages, tid);
+        __syncthreads();
+      }
+      qkv_tail<TM, BM, STAGE / 256>(g, acc, row0, n0 + wn * WTN, lrow, m0, stages);
       return;
     }
   }

@@ -301,15 +301,14 @@ Tensor forward_ids(mi_llama *m, const Tensor &idx, int64_t batch, int64_t t) {
     // item, and q laid out for the attention, in one launch: rows (sequence,
     // position, head) for the fused kernel, else regrouped per kv head, rows
     // (sequence, kv head, position, g).
-    // BF16 activations from 4096 rows with 64-wide heads: the product's
-    // epilogue runs that tail itself (mi_linear_qkv_rope_cache: no F32 q|k|v
-    // rows between them; batch-32 performance-contract prefill 12.1 -> 11.6
-    // ms).  From F32 activations' parts it measured slower than the product
-    // then the tail kernel (77.7 against 46.4 + 22.8 us a layer: the rotary
-    // entries' loads at the end of every wavefront), so those keep the two.
+    // From 4096 rows with 64-wide heads the product's epilogue runs that tail
+    // itself (mi_linear_qkv_rope_cache: no F32 q|k|v rows between them), from
+    // BF16 activations or the F32 activations' parts (batch 32, from the
+    // parts: 54 us a layer against 49 + 28 for the product then the tail
+    // kernel; from BF16 activations 35 us).
     Tensor q;
-    if (D == 64 && rows >= 4096 && rows % 128 == 0 && c.hidden % 32 == 0 && act == MI_BF16) {
-      q = burn::linear_qkv_rope_cache(xn, false, L.wqkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k,
+    if (D == 64 && rows >= 4096 && rows % 128 == 0 && c.hidden % 32 == 0 && (act == MI_BF16 || parts_qkv)) {
+      q = burn::linear_qkv_rope_cache(xn, parts_qkv, L.wqkv, m->rope_cos, m->rope_sin, t, H, KVH, pos0, L.cache_k,
                                       L.cache_v, !fused);
     } else {
       Tensor qkv = parts_qkv ? burn::linear_parts(xn, L.wqkv, true, nullptr, nullptr)
