@@ -130,12 +130,20 @@ __device__ __host__ __forceinline__ int64_t tile_offset(int64_t r, int64_t k, in
 
 // The logistic function in its two-branch form, so neither exponential
 // overflows: 1 / (1 + e^-x) for x >= 0 and e^x / (1 + e^x) below.  Both
-// quotients share t = e^-|x| (which is e^-x above zero and e^x below), so it
-// is computed branch-free as (x >= 0 ? 1 : t) / (1 + t): the same bits as the
-// branches, one exponential, and no divergence within a wavefront.
+// share t = e^-|x| (which is e^-x above zero and e^x below), so it is
+// computed branch-free: r = 1 / (1 + t), then r or t r -- one exponential,
+// no divergence within a wavefront.  t is the hardware 2^y (v_exp_f32) of
+// y = -|x| log2(e) and r the hardware reciprocal (v_rcp_f32), each within
+// 1 ulp; y's rounding and the F32 log2(e) (0.22 2^-24 below the true one)
+// add up to 1.23 |x| 2^-24 of relative error to t, so with the sum's and the
+// product's roundings the result is within (6 + 1.25 |x|) 2^-24 relative of
+// the exact logistic (for |x| < 87, where t is normal) -- 2-3x faster than
+// the library exponential and an IEEE division, which made it most of a
+// SwiGLU epilogue's cost.
 __device__ __forceinline__ float sigmoid2(float x) {
-  const float t = expf(-fabsf(x));
-  return (x >= 0.0f ? 1.0f : t) / (1.0f + t);
+  const float t = __builtin_amdgcn_exp2f(-fabsf(x) * 1.4426950408889634f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + t);
+  return x >= 0.0f ? r : t * r;
 }
 
 // Streaming (non-temporal) 16-byte accesses: the line is not kept in the

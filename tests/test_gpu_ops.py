@@ -90,6 +90,24 @@ def test_binary_broadcast_exact(engine, kind, bshape):
     same_bits(got, orc.eltwise(K[kind], x, y))
 
 
+def test_sigmoid_within_its_bound(engine):
+    """The logistic function (hardware 2^y of y = -|x| log2 e, hardware
+    reciprocal) against float64 over |x| < 87: relative error within
+    (6 + 1.25 |x|) 2^-24 (y's rounding and the F32 log2 e's 0.22 2^-24 scale
+    with |x|); beyond, the tails' limits; and the special values."""
+    x = np.concatenate([np.linspace(-86.9, 86.9, 200001), rnd(1, 4096).ravel() * np.float32(8)]).astype(np.float32)
+    got = engine.download(engine.eltwise_op_as("SIGMOID", engine.upload(x.reshape(1, -1)))).ravel()
+    xd = x.astype(np.float64)
+    want = np.where(xd >= 0, 1.0 / (1.0 + np.exp(-xd)), np.exp(xd) / (1.0 + np.exp(xd)))
+    rel = np.abs(got - want) / want
+    bound = (6 + 1.25 * np.abs(xd)) * 2.0 ** -24
+    assert np.all(rel <= bound), float(np.max(rel / bound))
+    sp = np.array([[0.0, -0.0, np.inf, -np.inf, np.nan, 100.0, -100.0, 88.0]], np.float32)
+    g = engine.download(engine.eltwise_op_as("SIGMOID", engine.upload(sp))).ravel()
+    assert g[0] == 0.5 and g[1] == 0.5 and g[2] == 1.0 and g[3] == 0.0 and np.isnan(g[4])
+    assert g[5] == 1.0 and 0.0 <= g[6] < 1e-40 and g[7] == 1.0
+
+
 @pytest.mark.parametrize("kind", ["SIGMOID_BACKWARD", "GELU_BACKWARD", "SILU_MUL", "SUB_EXP", "POW"])
 def test_binary_approx(engine, kind):
     R, C = 40, 200
