@@ -194,3 +194,32 @@ def test_mlp_training_step_trace(engine):
         engine.free(i)
     eager.close()
     traced.close()
+
+
+def test_mlp_trace_replays_back_to_back(engine):
+    """Replays on fresh host batches with nothing read back between them (each
+    batch staged ahead on the transfer stream, an input's two device copies
+    used in turn): the parameters after eight replays equal eight eager
+    steps' bit for bit."""
+    eager = miburn.Mlp(engine)
+    traced = miburn.Mlp(engine)
+    x = engine.upload(np.zeros((64, 784), np.float32))
+    lab = engine.upload_i32(np.zeros((64, 1), np.int32))
+    engine.begin_trace()
+    loss_id = traced.train_step_ids(x, lab, 0.01)
+    trace = engine.end_trace()
+    batches = [(RNG.random((64, 784)).astype(np.float32), RNG.integers(0, 10, (64, 1)).astype(np.int32))
+               for _ in range(8)]
+    for xv, yv in batches:
+        eager.train_step(xv, yv, 0.01)
+    for xv, yv in batches:
+        engine.run_trace(trace, {x: xv, lab: yv})
+    engine.sync()
+    for i in range(4):
+        assert np.array_equal(bits(eager.param(i)), bits(traced.param(i))), i
+    engine.release_trace(trace)
+    for i in (x, lab, loss_id):
+        engine.free(i)
+    eager.close()
+    traced.close()
+
