@@ -862,8 +862,8 @@ struct DqaBfp8 {
 // same batch-1 and batch-4 step times, 0.703 / 0.705 / 0.714 ms at batch 1;
 // this order halves the launch's fetched bytes, 8.7 -> 4.1 MB.)
 __host__ __device__ __forceinline__ int64_t dqa_chunk_ids(const DqaArgs &g) {
-  const int64_t nh = static_cast<int64_t>(g.B) * g.H;
-  return 8 * ((nh + 7) / 8) * g.S;
+  const int64_t ni = static_cast<int64_t>(g.B) * g.KVH;
+  return 8 * ((ni + 7) / 8) * g.G * g.S;
 }
 
 // Block (256 threads): 64 rows (from row0, each K weights) times the staged
@@ -1062,12 +1062,12 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   float *red = scores + g.chunk; // [NW][D]
   float *stat = red + NW * D;    // max, sum
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // Block order, XCD-aware: workgroup p runs on XCD p % 8, and the S chunk
-  // blocks of query head u (u = sequence H + head) take the ids p = u % 8 +
-  // 8 (slot), slot = (u / 8) S + chunk, so every block that reads the head's
-  // 64 weight rows runs on one XCD and the rows come once into its L2
-  // (ids with u past the last head are empty blocks).  Then the key / value
-  // blocks.
+  // Block order, XCD-aware: workgroup p runs on XCD p % 8, and the G S
+  // chunk blocks of kv item i (i = sequence KVH + kv head) take the ids p =
+  // i % 8 + 8 (slot), slot = (i / 8) G S + g S + chunk, so every block that
+  // reads the item's key and value chunks, and a query head's 64 weight
+  // rows, runs on one XCD and they come once into its L2 (ids with i past
+  // the last item are empty blocks).  Then the key / value blocks.
   const int64_t nchunk = dqa_chunk_ids(g);
   const int64_t bid = blockIdx.x;
 
@@ -1122,10 +1122,11 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   }
 
   // (sequence, query head, key chunk)
-  const int64_t slot = bid >> 3, bh = (bid & 7) + 8 * (slot / g.S), s = slot % g.S;
-  if (bh >= static_cast<int64_t>(g.B) * g.H) return 0;  // an empty id of the XCD-aware order
-  const int64_t hq = bh % g.H, b = bh / g.H;
-  const int64_t j = hq / g.G, gg = hq % g.G, bj = b * g.KVH + j;
+  const int64_t GS = static_cast<int64_t>(g.G) * g.S;
+  const int64_t slot = bid >> 3, bj = (bid & 7) + 8 * (slot / GS), rem = slot % GS;
+  if (bj >= static_cast<int64_t>(g.B) * g.KVH) return 0;  // an empty id of the XCD-aware order
+  const int64_t gg = rem / g.S, s = rem - gg * g.S;
+  const int64_t b = bj / g.KVH, j = bj % g.KVH, hq = j * g.G + gg;
   // The weights first: they do not wait for a position read on the device.
   typename WT::Raw wr[CH];
   dqa_wload<CH, WT>(g, hq * D, wr);
