@@ -346,11 +346,12 @@ def decode_layer_bench(eng, batch: int = 1, ctx: int = 576, steps: int = 200) ->
     """One SmolLM2-135M layer's decode launches alone, for counter profiles
     (rocprofv3 --pmc of the whole decoder harness has ended in host
     segmentation faults inside the profiler): the fused norm + q|k|v +
-    attention step at a `ctx`-position context (mi_norm_qkv_attention: its
-    chunk kernel and its combine), then the o, gate|up and down GEMVs
-    (mi_norm_matvec) -- the five launches of a decode layer
-    (crates/tt-models/src/llama.rs:380-520) -- `steps` times over one layer's
-    random BF16 weights and a random F32 cache."""
+    attention step at a `ctx`-position context through the o projection and
+    residual (mi_norm_qkv_attention_o: its chunk kernel, then the combine and
+    the o projection -- one launch for one sequence), then the gate|up and
+    down GEMVs (mi_norm_matvec) -- the launches of a decode layer as the model
+    runs them (crates/tt-models/src/llama.rs:380-520) -- `steps` times over
+    one layer's random BF16 weights and a random F32 cache."""
     import miburn
     H, KVH, D, hid, inter, maxc = 9, 3, 64, 576, 1536, 1024
 
@@ -369,11 +370,10 @@ def decode_layer_bench(eng, batch: int = 1, ctx: int = 576, steps: int = 200) ->
     span = (ctx + 1 + 63) // 64 * 64
 
     def layer():
-        o = eng.norm_qkv_attention(x, gamma, 1e-5, wqkv, cos, sin, H, KVH, 0, ctx, span, kc, vc, D ** -0.5)
-        x1 = eng.norm_matvec(o, 0, 0.0, wo, x, False)
+        x1 = eng.norm_qkv_attention_o(x, gamma, 1e-5, wqkv, cos, sin, H, KVH, 0, ctx, span, kc, vc, D ** -0.5, wo)
         h = eng.norm_matvec(x1, gamma, 1e-5, wgu, 0, True)
         x2 = eng.norm_matvec(h, 0, 0.0, wdn, x1, False)
-        for t in (o, x1, h, x2):
+        for t in (x1, h, x2):
             eng.free(t)
     for _ in range(20):
         layer()

@@ -632,6 +632,21 @@ int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
                           int64_t heads, int64_t kv_heads, mi_id pos,
                           int64_t pos0, int64_t span, mi_id k_cache,
                           mi_id v_cache, float scale, mi_id *out);
+/* A decode step's whole attention block: x + o w_o^T, o the attention rows
+ * mi_norm_qkv_attention returns for the same arguments, w_o the output
+ * projection [hidden, heads * d] (BF16 or BFP8) and x [M, hidden] the
+ * residual -- the reference's attention block through its output
+ * projection and residual add (crates/tt-models/src/llama.rs:380-478; the
+ * add at :478), no Engine counterpart.  Bit for bit mi_norm_qkv_attention then
+ * mi_norm_matvec(o, 0, 0, w_o, x).  For one sequence on the fused launch
+ * (up to 16 heads) the combine of the key chunks runs inside the
+ * projection's launch, one launch fewer a step; otherwise those two calls. */
+int mi_norm_qkv_attention_o(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
+                            mi_id w_qkv, mi_id cos_table, mi_id sin_table,
+                            int64_t heads, int64_t kv_heads, mi_id pos,
+                            int64_t pos0, int64_t span, mi_id k_cache,
+                            mi_id v_cache, float scale, mi_id w_o,
+                            mi_id *out);
 /* silu(gate) * up over the halves of a fused gate|up product: gate_up
  * [rows, 2 i] F32 -> [rows, i] of out_elem (the reference's MLP, crates/
  * tt-models/src/llama.rs:494-498, on the two row blocks of its gate|up

@@ -27,6 +27,7 @@
 // directly, the composition's exact formula order.  A block loads the value
 // rows of its first pass before computing the scores (one HBM round trip
 // less on a short chunk).
+#include "combine.hpp"
 #include "common.hpp"
 #include "wave.hpp"
 
@@ -959,92 +960,23 @@ __device__ __forceinline__ void dqa_rope(const DqaPre &pre, const float *raw, fl
 }
 
 // The combine of a fused step: the S chunks of each (sequence, kv head) and
-// the new key as one more -- score scale (q . k_new) over the 64 lanes of a
-// wavefront, weight exp(score - max), value row v_new -- with the key-chunked
-// combine's formula: out = (sum_s w_s o_s + w_new v_new) / max(sum_s w_s
-// l_s + w_new, FLT_MIN), w_s = exp(m_s - max).
-// Item bj (sequence, kv head) of a fused step's combine, by one block of 256
-// threads; st: 3 G S + 3 G floats of LDS.
-template <typename KV>
-__device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, float *out, float *st) {
+// the new key as one more -- score scale (q . k_new), weight exp(score -
+// max), value row v_new -- with the key-chunked combine's formula: out =
+// (sum_s w_s o_s + w_new v_new) / max(sum_s w_s l_s + w_new, FLT_MIN), w_s =
+// exp(m_s - max) (ChunkCombine).  Item bj, one block: its G query heads on
+// rows of 16 lanes (a row past the last head repeats the last and writes
+// nothing); wl: 16 S floats of LDS for each wavefront's rows.
+template <int CS>
+__device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, float *out, float *wl) {
   constexpr int D = DQA_D;
   const int G = g.G, S = static_cast<int>(g.S);
-  const int64_t b = bj / g.KVH, j = bj % g.KVH, PS = static_cast<int64_t>(G) * (D + 2);
-  const float *pb = g.part + bj * S * PS;
-  float *w = st + 2 * G * S;
-  float *den = w + G * S;
-  float *snew = den + G;
-  float *wnew = snew + G;
-  // A thread's output elements e = tid + 256 i (G D <= 512): their first CS
-  // chunks' values, requested with the statistics and the new rows; one
-  // round trip for all but very long contexts.
-  constexpr int EP = 2, CS = 16;
-  float ov[EP][CS], vd[EP];
-#pragma unroll
-  for (int i = 0; i < EP; ++i) {
-    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
-#pragma unroll
-    for (int s = 0; s < CS; ++s) ov[i][s] = pb[(s < S ? s : S - 1) * PS + 2 * G + ec];
-  }
-  // The queries the new key's scores take (wavefront w: heads w, w + 4),
-  // requested with them too.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float qv[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int gg = wave + 4 * u;
-    qv[u] = g.q[(b * g.H + j * G + (gg < G ? gg : 0)) * D + lane];
-  }
-  for (int e = threadIdx.x; e < 2 * G * S; e += 256) st[e] = pb[(e / (2 * G)) * PS + e % (2 * G)];
-  // The new key and value rows as the cache holds them, from where the
-  // launch's key/value blocks left them: no position read before them.
-  const float *kn = g.kvn + bj * 2 * D, *vn = kn + D;
-#pragma unroll
-  for (int i = 0; i < EP; ++i) {
-    const int e = threadIdx.x + 256 * i, ec = e < G * D ? e : 0;
-    vd[i] = vn[ec % D];
-  }
-  const float kd = kn[lane];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int gg = wave + 4 * u;
-    if (gg < G) {
-      const float sc = fold_sum<64>(qv[u] * kd);
-      if (lane == 0) snew[gg] = sc * g.scale;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int gg = threadIdx.x;
-    float M = snew[gg];
-    for (int s = 0; s < S; ++s) M = max_nan(M, st[s * 2 * G + gg]);
-    float l = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float ws = expf(st[s * 2 * G + gg] - M);
-      w[s * G + gg] = ws;
-      l += ws * st[s * 2 * G + G + gg];
-    }
-    const float wn = expf(snew[gg] - M);
-    wnew[gg] = wn;
-    l += wn;
-    den[gg] = isnan(l) ? l : (l > FLT_MIN ? l : FLT_MIN);
-  }
-  __syncthreads();
-  float *dst = out + b * g.H * D + j * G * D;
-#pragma unroll
-  for (int i = 0; i < EP; ++i) {
-    const int e = threadIdx.x + 256 * i;
-    if (e < G * D) {
-      const int gg = e / D;
-      float num = 0.0f;
-#pragma unroll
-      for (int s = 0; s < CS; ++s)
-        if (s < S) num += w[s * G + gg] * ov[i][s];
-      for (int s = CS; s < S; ++s) num += w[s * G + gg] * pb[s * PS + 2 * G + e];
-      num += wnew[gg] * vd[i];
-      dst[e] = num / den[gg];
-    }
-  }
+  const int row = threadIdx.x >> 4, r = threadIdx.x & 15, gg = row < G ? row : G - 1;
+  const int64_t b = bj / g.KVH, j = bj % g.KVH, h = j * G + gg;
+  const float *pitem = g.part + bj * S * dqa_part_stride(G);
+  ChunkCombine<CS> cc;
+  cc.load(pitem, G, gg, S, r, g.q + (b * g.H + h) * D, g.kvn + bj * 2 * D, g.kvn + bj * 2 * D + D);
+  const float4 o = cc.finish(pitem, G, gg, S, r, g.scale, wl + row * S);
+  if (row < G) *reinterpret_cast<float4 *>(out + (b * g.H + h) * D + 4 * r) = o;
 }
 
 // The block's part of the launch (its item, sequence and kv head, is
@@ -1134,14 +1066,14 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   dqa_pre_x(g, b, pre);
   const int64_t pos = att_pos0(g.pa, 1);
   const int64_t lo = s * g.chunk, len = pos > lo ? (pos - lo < g.chunk ? pos - lo : g.chunk) : 0;
-  const int64_t PS = static_cast<int64_t>(g.G) * (D + 2);
-  float *pb = g.part + (bj * g.S + s) * PS;
+  float *pb = g.part + (bj * g.S + s) * dqa_part_stride(g.G);
+  float *pacc = pb + dqa_part_acc0(g.G) + gg * D;
   if (len == 0 && s != 0) {  // past the keys: the empty chunk's statistics
     if (tid == 0) {
       pb[gg] = -FLT_MAX;
       pb[g.G + gg] = 0.0f;
     }
-    if (tid < D) pb[2 * g.G + gg * D + tid] = 0.0f;
+    if (tid < D) pacc[tid] = 0.0f;
     return bj;
   }
   const KV *Kc = static_cast<const KV *>(g.kc) + (bj * g.maxc + lo) * D;
@@ -1240,7 +1172,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     float t = red[tid];
 #pragma unroll
     for (int w = 1; w < NW; ++w) t += red[w * D + tid];
-    pb[2 * g.G + gg * D + tid] = t;
+    pacc[tid] = t;
   }
   return bj;
 }
@@ -1252,10 +1184,10 @@ __global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
 }
 
 // The combine: one block an item, the launch after the fused one.
-template <typename KV>
-__global__ void __launch_bounds__(256) attention_combine_new_kernel(DqaArgs g, float *out) {
-  extern __shared__ float st[];
-  combine_new_item<KV>(g, blockIdx.x, out, st);
+template <int CS>
+__global__ void __launch_bounds__(128) attention_combine_new_kernel(DqaArgs g, float *out) {
+  extern __shared__ float wl[];
+  combine_new_item<CS>(g, blockIdx.x, out, wl);
 }
 
 }  // namespace mi
@@ -1563,24 +1495,45 @@ void launch_dqa_w(hipStream_t st, const DqaArgs &g, unsigned blocks, size_t lds)
   else decode_qkv_attention_kernel<KV, 32, WT><<<blocks, 256, lds, st>>>(g);
 }
 
+// out null: the fused launch only (its combine is the caller's).
 template <typename KV>
 void launch_dqa(hipStream_t st, const DqaArgs &g, float *out) {
   const unsigned blocks = static_cast<unsigned>(dqa_chunk_ids(g) + 2 * static_cast<int64_t>(g.B) * g.KVH);
   const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + 8 + g.chunk + 4 * DQA_D + 2) * sizeof(float);
   if (g.wq) launch_dqa_w<KV, DqaBfp8>(st, g, blocks, lds);
   else launch_dqa_w<KV, DqaBf16>(st, g, blocks, lds);
-  const size_t comb = static_cast<size_t>(3 * g.G * g.S + 3 * g.G) * sizeof(float);
-  attention_combine_new_kernel<KV><<<static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH), 256, comb, st>>>(g, out);
+  if (!out) return;
+  const unsigned threads = g.G <= 4 ? 64 : 128, items = static_cast<unsigned>(static_cast<int64_t>(g.B) * g.KVH);
+  const size_t comb = static_cast<size_t>(threads / 16 * g.S) * sizeof(float);
+  switch (combine_cs(g.S)) {
+    case 4: attention_combine_new_kernel<4><<<items, threads, comb, st>>>(g, out); break;
+    case 8: attention_combine_new_kernel<8><<<items, threads, comb, st>>>(g, out); break;
+    case 12: attention_combine_new_kernel<12><<<items, threads, comb, st>>>(g, out); break;
+    default: attention_combine_new_kernel<16><<<items, threads, comb, st>>>(g, out); break;
+  }
 }
 
 }  // namespace
 }  // namespace mi
 
-extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
-                                     mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0,
-                                     int64_t span, mi_id k_cache, mi_id v_cache, float scale, mi_id *out) {
+// w_o 0: the attention rows (mi_norm_qkv_attention); else x + those rows
+// times w_o^T (mi_norm_qkv_attention_o).
+static int norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                              mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0, int64_t span,
+                              mi_id k_cache, mi_id v_cache, float scale, mi_id w_o, mi_id *out) {
   MI_ENTER(ctx);
   if (!out) return fail(ctx, MI_E_ARG, "null out pointer");
+  // With w_o and no launch of its own: the attention rows, then the
+  // projection (which checks w_o against them and x).
+  auto project = [&](int s, mi_id o) {
+    if (s || !w_o) {
+      if (!s) *out = o;
+      return s;
+    }
+    s = mi_norm_matvec(ctx, o, 0, 0.0f, w_o, x, 0, out);
+    mi_free(ctx, o);
+    return s;
+  };
   MI_BUF(ctx, xb, x);
   MI_BUF(ctx, wb, w_qkv);
   MI_BUF(ctx, cb, cos_table);
@@ -1603,6 +1556,16 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   const int64_t B = xb->rows, K = xb->cols, D = kb->cols;
   const int64_t G = kv_heads > 0 ? heads / kv_heads : 0;
   const int64_t maxc = B > 0 && kv_heads > 0 ? kb->rows / (B * kv_heads) : 0;
+  const Buffer *wob = nullptr;
+  if (w_o) {  // checked before anything is written
+    wob = lookup(ctx, w_o);
+    if (!wob) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)w_o);
+    if ((wob->elem != MI_BF16 && wob->elem != MI_BFP8) || wob->rows != K || wob->cols != heads * D ||
+        xb->elem != MI_F32)
+      return fail(ctx, MI_E_ARG, "norm_qkv_attention_o: the o weight is %s [%lld, %lld], want BF16 or BFP8 [%lld, %lld]",
+                  elem_name(wob->elem), (long long)wob->rows, (long long)wob->cols, (long long)K,
+                  (long long)(heads * D));
+  }
   // The fused launch: up to DQA_MAX_B sequences, 64-wide heads, k a
   // multiple of 32 up to 1024, a gain, aligned operands; else the two calls
   // composed (which check every argument themselves).
@@ -1617,15 +1580,15 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
                      ((reinterpret_cast<uintptr_t>(xb->ptr) | reinterpret_cast<uintptr_t>(wb->ptr) |
                        reinterpret_cast<uintptr_t>(gb->ptr)) & 15) == 0;
   if (!fused) {
-    mi_id q = 0;
+    mi_id q = 0, o = 0;
     int s = pos_dev ? mi_norm_qkv_rope_at(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos,
                                           k_cache, v_cache, &q)
                     : mi_norm_qkv_rope(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos0,
                                        k_cache, v_cache, &q);
     if (s) return s;
-    s = mi_attention_rows_at(ctx, q, k_cache, v_cache, B, 1, heads, kv_heads, pos, pos0, span, scale, out);
+    s = mi_attention_rows_at(ctx, q, k_cache, v_cache, B, 1, heads, kv_heads, pos, pos0, span, scale, &o);
     mi_free(ctx, q);
-    return s;
+    return project(s, o);
   }
   if (span < 1 || span > maxc)
     return fail(ctx, MI_E_ARG, "norm_qkv_attention: span %lld in a cache of %lld", (long long)span, (long long)maxc);
@@ -1642,15 +1605,20 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   if (S < 1) S = 1;
   const int64_t chunk = ((span + S - 1) / S + 3) / 4 * 4;
   S = (span + chunk - 1) / chunk;
-  if (static_cast<size_t>(3 * G * S + 3 * G) * sizeof(float) > 65536 || 8 * (B * heads + 8 * G) * S + 2 * items > INT32_MAX)
+  if (static_cast<size_t>(16 * S) * sizeof(float) > 65536 || 8 * (B * heads + 8 * G) * S + 2 * items > INT32_MAX)
     return fail(ctx, MI_E_UNSUPPORTED, "norm_qkv_attention: context of %lld keys too long", (long long)span);
-  const size_t part_floats = static_cast<size_t>(items * S * G * (D + 2));
+  const size_t part_floats = static_cast<size_t>(items * S * dqa_part_stride(G));
   const size_t q_floats = static_cast<size_t>(B * heads * D), kvn_floats = static_cast<size_t>(items * 2 * D);
   float *sc = static_cast<float *>(mi::scratch(ctx, (part_floats + q_floats + kvn_floats) * sizeof(float)));
   if (!sc) return fail(ctx, MI_E_OOM, "norm_qkv_attention scratch");
+  // One sequence, a BF16 or BFP8 o weight [K, heads 64]: the combine runs
+  // inside the o projection's launch.
+  const bool fuse_o = wob && B == 1 && (wob->elem == MI_BF16 || wob->elem == MI_BFP8) && wob->rows == K &&
+                      wob->cols == heads * D && attention_o_fits(heads, S) &&
+                      (reinterpret_cast<uintptr_t>(wob->ptr) & 15) == 0;
   mi_id id;
   Buffer *ob;
-  int s = new_buffer(ctx, B, heads * D, MI_F32, &id, &ob);
+  int s = new_buffer(ctx, B, fuse_o ? K : heads * D, MI_F32, &id, &ob);
   if (s) return s;
   DqaArgs g{};
   g.x = static_cast<const float *>(xb->ptr);
@@ -1680,6 +1648,20 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
   g.q = sc + part_floats;
   g.kvn = g.q + q_floats;
   float *o = static_cast<float *>(ob->ptr);
+  if (fuse_o) {
+    if (kb->elem == MI_BF16) launch_dqa<uint16_t>(ctx->stream, g, nullptr);
+    else launch_dqa<float>(ctx->stream, g, nullptr);
+    s = check_launch(ctx, "norm_qkv_attention");
+    if (!s)
+      s = attention_o_launch(ctx, AttnCombine{g.part, g.q, g.kvn, g.H, g.G, static_cast<int>(S), scale}, wob,
+                             static_cast<const float *>(xb->ptr), o);
+    if (s) {
+      mi_free(ctx, id);
+      return s;
+    }
+    *out = id;
+    return MI_OK;
+  }
   if (kb->elem == MI_BF16) launch_dqa<uint16_t>(ctx->stream, g, o);
   else launch_dqa<float>(ctx->stream, g, o);
   s = check_launch(ctx, "norm_qkv_attention");
@@ -1687,6 +1669,22 @@ extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float ep
     mi_free(ctx, id);
     return s;
   }
-  *out = id;
-  return MI_OK;
+  return project(MI_OK, id);
+}
+
+extern "C" int mi_norm_qkv_attention(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                     mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0,
+                                     int64_t span, mi_id k_cache, mi_id v_cache, float scale, mi_id *out) {
+  return norm_qkv_attention(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos, pos0, span,
+                            k_cache, v_cache, scale, 0, out);
+}
+
+extern "C" int mi_norm_qkv_attention_o(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w_qkv, mi_id cos_table,
+                                       mi_id sin_table, int64_t heads, int64_t kv_heads, mi_id pos, int64_t pos0,
+                                       int64_t span, mi_id k_cache, mi_id v_cache, float scale, mi_id w_o,
+                                       mi_id *out) {
+  MI_ENTER(ctx);
+  if (!w_o) return fail(ctx, MI_E_ARG, "norm_qkv_attention_o: no o weight");
+  return norm_qkv_attention(ctx, x, gamma, eps, w_qkv, cos_table, sin_table, heads, kv_heads, pos, pos0, span,
+                            k_cache, v_cache, scale, w_o, out);
 }

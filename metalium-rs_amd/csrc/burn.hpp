@@ -529,6 +529,20 @@ inline Tensor norm_qkv_attention(const Tensor &x, const Tensor &gamma, float eps
   return Tensor(x.ctx(), id, {x.rows(), heads * k_cache.cols()});
 }
 
+// x + the attention rows times w_o^T (mi_norm_qkv_attention_o): the
+// attention block through its output projection and residual.
+inline Tensor norm_qkv_attention_o(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv,
+                                   const Tensor &cos, const Tensor &sin, int64_t heads, int64_t kv_heads,
+                                   const Tensor *pos, int64_t pos0, int64_t span, const Tensor &k_cache,
+                                   const Tensor &v_cache, float scale, const Tensor &w_o) {
+  mi_id id;
+  check(x.ctx(), mi_norm_qkv_attention_o(x.ctx(), x.use(), gamma.use(), eps, w_qkv.use(), cos.use(), sin.use(),
+                                         heads, kv_heads, pos ? pos->use() : 0, pos0, span, k_cache.use(),
+                                         v_cache.use(), scale, w_o.use(), &id),
+        "norm_qkv_attention_o");
+  return Tensor(x.ctx(), id, {x.rows(), x.cols()});
+}
+
 inline Tensor norm_qkv_rope(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv, const Tensor &cos,
                             const Tensor &sin, int64_t heads, int64_t kv_heads, int64_t pos, const Tensor &k_cache,
                             const Tensor &v_cache) {

@@ -311,6 +311,22 @@ void rms_norm_launch(Ctx *ctx, const void *xp, int xe, const void *gp, int ge, f
 // (MI_F32, or MI_BF16: exact either way); what a consumer without a BFP8
 // read of its own takes instead.  The caller frees it.
 int bfp8_decode_to(Ctx *ctx, const Buffer *src, int elem, mi_id *id, Buffer **out);
+// What a one-sequence decode step's fused attention launch (attention.hip)
+// leaves for its combine: the key chunks' partials ([KVH][S], laid out as
+// combine.hpp states), the rotated queries [H, 64] and the new key and value
+// rows [KVH][2][64], F32; H query heads, G a kv head, 64-wide.
+struct AttnCombine {
+  const float *part, *q, *kvn;
+  int H, G, S;
+  float scale;
+};
+// Whether attention_o_launch takes H heads over S chunks (the row's LDS).
+bool attention_o_fits(int64_t H, int64_t S);
+// out [1, N] = resid + attention row w^T, the attention row the combine of
+// `c` (bit for bit attention.hip's combine_new_kernel) and w [N, H 64] BF16
+// or BFP8: the combine and the o projection in one launch.  Returns the
+// launch's status.
+int attention_o_launch(Ctx *ctx, const AttnCombine &c, const Buffer *w, const float *resid, float *out);
 // MI_E_UNSUPPORTED if a trace is being captured (host transfers and waits
 // cannot be part of one).
 int refuse_if_capturing(Ctx *ctx, const char *what);

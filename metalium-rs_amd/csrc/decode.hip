@@ -22,8 +22,10 @@
 // HBM.  The two rows a
 // wavefront owns are chosen so that the epilogue is local: a RoPE pair
 // (i, i + d/2) of one head, or a gate row and its up row.
+#include <cfloat>
 #include <type_traits>
 
+#include "combine.hpp"
 #include "common.hpp"
 #include "wave.hpp"
 
@@ -375,6 +377,113 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
     // Lane m writes activation row m's outputs.
     if (lane == m) pair_write_pre<MODE>(g, q, m, y0, y1, pre);
   }
+}
+
+// A one-sequence decode step's attention combine and o projection in one
+// launch.  The block's 16 rows of 16 lanes first form the whole attention row
+// into LDS -- row h query head h (ChunkCombine, the combine kernel's code, so
+// its bits) -- then its 4 wavefronts (output rows 8 b .. 8 b + 7, a pair
+// each) multiply it as decode_matvec_kernel<1, DM_PLAIN, 2> does (its bits
+// again).  The weight rows are requested first and the combine's partials,
+// queries and new rows after them with no wait between, so the launch waits
+// for one round trip as the plain product does, and the combine's own launch
+// is gone.  H <= 16 heads (a row past the last repeats it and writes
+// nothing); LDS: the row's H 64 floats, then 16 S chunk weights.
+template <typename WT, int CS>
+__global__ void __launch_bounds__(256) attention_o_kernel(DecodeArgs g, AttnCombine c) {
+  constexpr int D = 64, PRE = 2;
+  extern __shared__ float sm[];
+  const int H = c.H, G = c.G, S = c.S;
+  float *xs = sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const bool live = p < g.npairs;  // a wavefront past the last pair still combines and syncs
+  const int64_t r0 = live ? 2 * p : 0;
+  const bool has1 = live && r0 + 1 < g.N;
+  const int64_t r1 = has1 ? r0 + 1 : r0;
+
+  typename WT::Raw pw0[PRE], pw1[PRE];
+#pragma unroll
+  for (int cc = 0; cc < PRE; ++cc) {
+    const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * cc;
+    const int64_t kc = k < g.K ? k : g.K - 8;
+    pw0[cc] = WT::template load<false>(g, r0, kc);
+    pw1[cc] = WT::template load<false>(g, r1, kc);
+  }
+  const float *rp = g.resid ? g.resid : g.out;
+  const float e0 = rp[r0], e1 = rp[r1];
+  const int row = tid >> 4, r = tid & 15, h = row < H ? row : H - 1, j = h / G, gg = h - j * G;
+  const float *pitem = c.part + static_cast<int64_t>(j) * S * dqa_part_stride(G);
+  ChunkCombine<CS> comb;
+  comb.load(pitem, G, gg, S, r, c.q + h * D, c.kvn + j * 2 * D, c.kvn + j * 2 * D + D);
+  const float4 o = comb.finish(pitem, G, gg, S, r, c.scale, xs + H * D + row * S);
+  if (row < H) *reinterpret_cast<float4 *>(xs + h * D + 4 * r) = o;
+  __syncthreads();
+  float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < PRE; ++cc) {
+    const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * cc;
+    if (k < g.K) {
+      float w0[8], w1[8];
+      WT::f32(pw0[cc], w0);
+      WT::f32(pw1[cc], w1);
+      const float4 a0 = *reinterpret_cast<const float4 *>(xs + k);
+      const float4 a1 = *reinterpret_cast<const float4 *>(xs + k + 4);
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        t0 = fmaf(av[e], w0[e], t0);
+        t1 = fmaf(av[e], w1[e], t1);
+      }
+    }
+  }
+  const float y0 = fold_sum<64>(t0), y1 = fold_sum<64>(t1);
+  if (live && lane == 0) {
+    g.out[r0] = g.resid ? __fadd_rn(e0, y0) : y0;
+    if (has1) g.out[r1] = g.resid ? __fadd_rn(e1, y1) : y1;
+  }
+}
+
+// LDS of attention_o_kernel for H heads over S chunks, in floats.
+static int64_t attention_o_lds(int64_t H, int64_t S) { return H * 64 + 16 * S; }
+
+bool attention_o_fits(int64_t H, int64_t S) {
+  return H >= 1 && H <= 16 && S >= 1 && attention_o_lds(H, S) * 4 <= 65536;
+}
+
+template <typename WT>
+static void attention_o_cs(unsigned grid, size_t lds, hipStream_t st, const DecodeArgs &g, const AttnCombine &c) {
+  switch (combine_cs(c.S)) {
+    case 4: attention_o_kernel<WT, 4><<<grid, 256, lds, st>>>(g, c); break;
+    case 8: attention_o_kernel<WT, 8><<<grid, 256, lds, st>>>(g, c); break;
+    case 12: attention_o_kernel<WT, 12><<<grid, 256, lds, st>>>(g, c); break;
+    default: attention_o_kernel<WT, 16><<<grid, 256, lds, st>>>(g, c); break;
+  }
+}
+
+int attention_o_launch(Ctx *ctx, const AttnCombine &c, const Buffer *w, const float *resid, float *out) {
+  if (!attention_o_fits(c.H, c.S) || c.G < 1 || c.H % c.G || w->cols != c.H * 64 || w->rows < 1 ||
+      (w->elem != MI_BF16 && w->elem != MI_BFP8))
+    return fail(ctx, MI_E_ARG, "attention_o: %d heads over %d chunks against a %s [%lld, %lld] weight", c.H, c.S,
+                elem_name(w->elem), (long long)w->rows, (long long)w->cols);
+  DecodeArgs g{};
+  g.K = w->cols;
+  g.N = w->rows;
+  g.npairs = (w->rows + 1) / 2;
+  g.resid = resid;
+  g.out = out;
+  g.ldo = w->rows;
+  const unsigned grid = static_cast<unsigned>((g.npairs + 3) / 4);
+  const size_t lds = static_cast<size_t>(attention_o_lds(c.H, c.S)) * sizeof(float);
+  if (w->elem == MI_BFP8) {
+    g.wq = static_cast<const int8_t *>(w->ptr);
+    g.we = static_cast<const uint8_t *>(w->ptr) + bfp8_exp_offset(w->rows, w->cols);
+    attention_o_cs<WBfp8>(grid, lds, ctx->stream, g, c);
+  } else {
+    g.w = static_cast<const uint16_t *>(w->ptr);
+    attention_o_cs<WBf16>(grid, lds, ctx->stream, g, c);
+  }
+  return check_launch(ctx, "attention_o");
 }
 
 // 9 to 32 activation rows: a block's 4 wavefronts (8 weight rows) share each

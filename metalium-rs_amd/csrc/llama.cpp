@@ -154,17 +154,17 @@ bool decode_fused(const mi_llama *m, int64_t batch) {
 
 // The layers of a decode step on the hidden rows x [batch, hidden]: the new
 // position pos0 (immediate) or held on the device in `pos`, the attention
-// planned for `span` positions.  Five launches a layer up to 6 sequences
-// (q|k|v and the attention's chunks in one), six above.
+// planned for `span` positions.  Four launches a layer for one sequence (q|k|v
+// and the attention's chunks in one, their combine in the o projection's),
+// five up to 6 sequences, six above.
 Tensor decode_layers(mi_llama *m, Tensor x, int64_t batch, const Tensor *pos, int64_t pos0, int64_t span) {
   const mi_llama_config &c = m->cfg;
   const int64_t H = c.heads, KVH = c.kv_heads, D = c.head_dim;
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));
   for (Layer &L : m->layers) {
     const bool q = L.q_wqkv.defined();  // BFP8 weights
-    Tensor o = burn::norm_qkv_attention(x, L.attn_norm, c.eps, q ? L.q_wqkv : L.wqkv, m->rope_cos, m->rope_sin, H,
-                                        KVH, pos, pos0, span, L.cache_k, L.cache_v, scale);
-    x = burn::norm_matvec(o, nullptr, 0.0f, q ? L.q_wo : L.wo, &x, false);
+    x = burn::norm_qkv_attention_o(x, L.attn_norm, c.eps, q ? L.q_wqkv : L.wqkv, m->rope_cos, m->rope_sin, H, KVH,
+                                   pos, pos0, span, L.cache_k, L.cache_v, scale, q ? L.q_wo : L.wo);
     Tensor h = burn::norm_matvec(x, &L.mlp_norm, c.eps, q ? L.q_wgu : L.wgu, nullptr, true);
     x = burn::norm_matvec(h, nullptr, 0.0f, q ? L.q_wdown : L.wdown, &x, false);
   }

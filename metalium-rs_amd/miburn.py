@@ -124,6 +124,8 @@ def _load() -> ctypes.CDLL:
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
         "mi_norm_qkv_attention": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, I64, I64, U64, U64, c_float,
                                   Ip],
+        "mi_norm_qkv_attention_o": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, I64, I64, U64, U64,
+                                    c_float, U64, Ip],
         "mi_norm_qkv_rope": [P, U64, U64, c_float, U64, U64, U64, I64, I64, I64, U64, U64, Ip],
         "mi_norm_qkv_rope_at": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, U64, U64, Ip],
         "mi_attention_rows_at": [P, U64, U64, U64, I64, I64, I64, I64, U64, I64, I64, c_float, Ip],
@@ -417,6 +419,15 @@ class Engine:
         attention rows of one new position per sequence (llama.rs:380-470)."""
         return self._out(self._lib.mi_norm_qkv_attention, x, gamma, eps, w_qkv, cos, sin, heads, kv_heads, pos,
                          pos0, span, k_cache, v_cache, scale)
+
+    def norm_qkv_attention_o(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
+                             kv_heads: int, pos: int, pos0: int, span: int, k_cache: int, v_cache: int,
+                             scale: float, w_o: int) -> int:
+        """x + norm_qkv_attention(...) w_o^T: the attention block through its
+        output projection and residual (llama.rs:380-470), bit for bit the
+        two calls."""
+        return self._out(self._lib.mi_norm_qkv_attention_o, x, gamma, eps, w_qkv, cos, sin, heads, kv_heads, pos,
+                         pos0, span, k_cache, v_cache, scale, w_o)
 
     def norm_qkv_rope_at(self, x: int, gamma: int, eps: float, w_qkv: int, cos: int, sin: int, heads: int,
                          kv_heads: int, pos: int, k_cache: int, v_cache: int) -> int:

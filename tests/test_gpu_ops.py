@@ -1161,6 +1161,72 @@ def test_norm_qkv_attention_refuses_bad_positions(engine, M, kv16):
         same_bits(engine.download(v1), c["vc0"])
 
 
+@pytest.mark.parametrize("M", [1, 2])  # the combine inside the projection's launch for one sequence; the two calls
+@pytest.mark.parametrize("kv16", [False, True])
+@pytest.mark.parametrize("bfp", [False, True])
+@pytest.mark.parametrize("pos0,span,maxc", [(575, 576, 640), (40, 64, 64), (0, 64, 64), (2000, 2048, 2048)])
+def test_norm_qkv_attention_o(engine, M, kv16, bfp, pos0, span, maxc):
+    # The attention block through its o projection and residual: bit for bit
+    # norm_qkv_attention then norm_matvec(o, w_o, residual x) on copies of the
+    # caches, the caches written the same, at the immediate and the device
+    # position.  2048 keys: 32 chunks, past the 16 a thread holds in registers.
+    c = qkv_attention_case(engine, M, kv16, pos0, maxc)
+    H, KVH, D, K = c["H"], c["KVH"], c["D"], c["K"]
+    rng = np.random.default_rng(7)
+    wo32 = (rng.standard_normal((K, H * D)) * 0.05).astype(np.float32)
+    wo = engine.cast_bfp(engine.upload(wo32)) if bfp else engine.upload_bf16(orc.to_bf16(wo32))
+    x = c["args"][0]
+    k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    got = engine.download(engine.norm_qkv_attention_o(*c["args"], 0, pos0, span, k1, v1, c["scale"], wo))
+    k2, v2 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    o = engine.norm_qkv_attention(*c["args"], 0, pos0, span, k2, v2, c["scale"])
+    want = engine.download(engine.norm_matvec(o, 0, 0.0, wo, x))
+    assert got.shape == (M, K)
+    same_bits(got, want)
+    same_bits(engine.download(k1), engine.download(k2))
+    same_bits(engine.download(v1), engine.download(v2))
+    # Within the F32 bound of float64 x + o w_o^T over the two calls' attention rows.
+    wo64 = (engine.download(wo) if bfp else orc.from_bf16(orc.to_bf16(wo32))).astype(np.float64)  # BFP8 reads decoded
+    o64 = engine.download(o).astype(np.float64)
+    ref = c["x"].astype(np.float64) + o64 @ wo64.T
+    assert np.abs(got - ref).max() <= 1e-5 * (np.abs(c["x"]).max() + (np.abs(o64) @ np.abs(wo64).T).max())
+    ipos = engine.upload_bits(np.array([[pos0]], np.int32), I32)
+    k3, v3 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    same_bits(engine.download(engine.norm_qkv_attention_o(*c["args"], ipos, 0, span, k3, v3, c["scale"], wo)), got)
+    same_bits(engine.download(k3), engine.download(k1))
+
+
+def test_norm_qkv_attention_o_refuses(engine):
+    # A missing or mis-shaped o weight is refused before any cache row is written.
+    c = qkv_attention_case(engine, 1, False, 10, 64)
+    H, D, K = c["H"], c["D"], c["K"]
+    k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    for wo in (engine.upload_bf16(orc.to_bf16(np.zeros((K, H * D - 64), np.float32))),
+               engine.upload(np.zeros((K, H * D), np.float32)), 0):
+        with pytest.raises(miburn.MiError) as e:
+            engine.norm_qkv_attention_o(*c["args"], 0, 10, 64, k1, v1, c["scale"], wo)
+        assert e.value.kind == "ARG"
+    same_bits(engine.download(k1), c["kc0"])
+    same_bits(engine.download(v1), c["vc0"])
+    # A device position past the span: the same refusal and the same output as the two calls.
+    bad = engine.upload_bits(np.array([[64]], np.int32), I32)
+    wo = engine.upload_bf16(orc.to_bf16(np.full((K, H * D), 0.01, np.float32)))
+    outs = []
+    for fused in (True, False):
+        if fused:
+            out = engine.norm_qkv_attention_o(*c["args"], bad, 0, 64, k1, v1, c["scale"], wo)
+        else:
+            out = engine.norm_matvec(engine.norm_qkv_attention(*c["args"], bad, 0, 64, k1, v1, c["scale"]), 0, 0.0,
+                                     wo, c["args"][0])
+        with pytest.raises(miburn.MiError) as e:
+            engine.sync()
+        assert e.value.kind == "DOMAIN"
+        engine.sync()
+        outs.append(engine.download(out))
+    same_bits(outs[0], outs[1])
+    same_bits(engine.download(k1), c["kc0"])
+
+
 @pytest.mark.parametrize("M", [1, 5, 32])
 def test_norm_qkv_rope_bf16_caches(engine, M):
     # The same kernel into BF16 caches: q unchanged, the new cache row the F32
