@@ -797,7 +797,11 @@ bool dispatch_group(int64_t G, hipStream_t st, const float *q, const KV *k, cons
 // different XCDs, each with its own L2, so the repeats are fetched from the
 // fabric (8.7 MB a SmolLM2 launch against 2.0 MB of weights and cache), at a
 // rate that does not bound the launch.
-constexpr int DQA_MAX_CH = 32;  // 16-byte weight chunks a thread: k <= 1024 (CH: 8, 16, 24 or 32)
+constexpr int DQA_MAX_CH = 32;  // k <= 32 DQA_MAX_CH = 1024
+// Wavefronts a block of the fused step, and so the lanes of each of its 64
+// weight rows: 8 (two a SIMD: the GEMV's and the chunk passes' instruction
+// latencies hide behind the other wavefront's; 7.2 -> 6.4 us a SmolLM2 layer).
+constexpr int DQA_NW = 8, DQA_NT = 64 * DQA_NW, DQA_RL = DQA_NT / 64;
 constexpr int DQA_D = 64;
 // Sequences up to which the fused launch serves a decode step: beyond, its
 // blocks' query GEMVs (each (sequence, head, chunk) block its own) cost more
@@ -867,30 +871,30 @@ __host__ __device__ __forceinline__ int64_t dqa_chunk_ids(const DqaArgs &g) {
   return 8 * ((ni + 7) / 8) * g.G * g.S;
 }
 
-// Block (256 threads): 64 rows (from row0, each K weights) times the staged
-// row in LDS xn; thread t takes row t / 4 and the 8-weight chunks t % 4,
-// + 4, ...; the four partial sums fold over the row's lanes.  wr: the chunks,
-// loaded by dqa_wload.
+// Block (DQA_NT threads): 64 rows (from row0, each K weights) times the
+// staged row in LDS xn; thread t takes row t / RL and the 8-weight chunks t %
+// RL, + RL, ... (RL = DQA_RL); the partial sums fold over the row's lanes.
+// wr: the chunks, loaded by dqa_wload.
 template <int CH, typename WT>
 __device__ __forceinline__ void dqa_wload(const DqaArgs &g, int64_t row0, typename WT::Raw (&wr)[CH]) {
-  const int tid = threadIdx.x, r = tid >> 2, kq = tid & 3;
+  const int tid = threadIdx.x, r = tid / DQA_RL, kq = tid % DQA_RL;
   const int64_t nch = g.K / 8;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
-    const int64_t c = kq + 4 * i;
+    const int64_t c = kq + DQA_RL * i;
     wr[i] = WT::load(g, row0 + r, 8 * (c < nch ? c : nch - 1));
   }
 }
 template <int CH, typename WT>
 __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const typename WT::Raw (&wr)[CH]) {
-  const int kq = threadIdx.x & 3;
+  const int kq = threadIdx.x % DQA_RL;
   const int64_t nch = K / 8;
-  // Four independent sums (one wavefront a SIMD: nothing else hides an FMA's
-  // latency), added at the end.
+  // Four independent sums (an FMA's latency is not hidden by the SIMD's
+  // other wavefront alone), added at the end.
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
-    const int64_t c = kq + 4 * i;
+    const int64_t c = kq + DQA_RL * i;
     if (c < nch) {
       const float4 a0 = *reinterpret_cast<const float4 *>(xn + 8 * c);
       const float4 a1 = *reinterpret_cast<const float4 *>(xn + 8 * c + 4);
@@ -904,7 +908,7 @@ __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const typen
       }
     }
   }
-  return fold_sum<4>((acc[0] + acc[1]) + (acc[2] + acc[3]));
+  return fold_sum<DQA_RL>((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
 // A thread's operands of the norm and the rotation, requested with the
@@ -944,7 +948,10 @@ __device__ __forceinline__ float dqa_stage(const DqaArgs &g, const DqaPre &pre, 
   ss = fold_sum<64>(ss);
   if (lane == 0) red4[wave] = ss;
   __syncthreads();
-  return __fsqrt_rn((red4[0] + red4[1] + red4[2] + red4[3]) / static_cast<float>(g.K) + g.eps);
+  float t = red4[0];
+#pragma unroll
+  for (int w = 1; w < DQA_NW; ++w) t += red4[w];
+  return __fsqrt_rn(t / static_cast<float>(g.K) + g.eps);
 }
 
 // RoPE of a 64-wide head in LDS (raw -> rot): the rotation of pair (i, i +
@@ -985,12 +992,12 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
 // launch: batch-1 SmolLM2 decode 0.694 -> 0.938 ms a step.)
 template <typename KV, int CH, typename WT>
 __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
-  constexpr int D = DQA_D, NW = 4, LPR = D / 4, KPW = 64 / LPR, U = 4, STEP = NW * KPW;
+  constexpr int D = DQA_D, NW = DQA_NW, LPR = D / 4, KPW = 64 / LPR, U = 2, STEP = NW * KPW;
   float *xn = dqa_sm;            // [K]
   float *qraw = xn + g.K;        // [64]
   float *qrot = qraw + D;        // [64]
-  float *red4 = qrot + D;        // [4] (+4 pad)
-  float *scores = red4 + 8;      // [chunk]
+  float *red4 = qrot + D;        // [NW]
+  float *scores = red4 + NW;     // [chunk]
   float *red = scores + g.chunk; // [NW][D]
   float *stat = red + NW * D;    // max, sum
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1019,7 +1026,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     dqa_pre_rot(g, pos, pre);
     const float rms = dqa_stage(g, pre, xn, red4);
     const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
-    if ((tid & 3) == 0) qraw[tid >> 2] = y;
+    if (tid % DQA_RL == 0) qraw[tid / DQA_RL] = y;
     __syncthreads();
     if (!ok) {
       // Refused position (the chunk blocks raise the flag): no cache row is
@@ -1093,7 +1100,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   const float rms = dqa_stage(g, pre, xn, red4);
   {
     const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
-    if ((tid & 3) == 0) qraw[tid >> 2] = y;
+    if (tid % DQA_RL == 0) qraw[tid / DQA_RL] = y;
   }
   __syncthreads();
   dqa_rope(pre, qraw, qrot);
@@ -1178,7 +1185,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
 }
 
 template <typename KV, int CH, typename WT>
-__global__ void __launch_bounds__(256) decode_qkv_attention_kernel(DqaArgs g) {
+__global__ void __launch_bounds__(DQA_NT) decode_qkv_attention_kernel(DqaArgs g) {
   extern __shared__ float dqa_sm[];
   dqa_work<KV, CH, WT>(g, dqa_sm);
 }
@@ -1488,18 +1495,18 @@ namespace {
 // The fused launch, then the combine's.
 template <typename KV, typename WT>
 void launch_dqa_w(hipStream_t st, const DqaArgs &g, unsigned blocks, size_t lds) {
-  const int64_t ch = (g.K / 8 + 3) / 4;  // chunks a thread
-  if (ch <= 8) decode_qkv_attention_kernel<KV, 8, WT><<<blocks, 256, lds, st>>>(g);
-  else if (ch <= 16) decode_qkv_attention_kernel<KV, 16, WT><<<blocks, 256, lds, st>>>(g);
-  else if (ch <= 24) decode_qkv_attention_kernel<KV, 24, WT><<<blocks, 256, lds, st>>>(g);
-  else decode_qkv_attention_kernel<KV, 32, WT><<<blocks, 256, lds, st>>>(g);
+  const int64_t ch = (g.K / 8 + DQA_RL - 1) / DQA_RL;  // chunks a thread
+  if (ch <= 4) decode_qkv_attention_kernel<KV, 4, WT><<<blocks, DQA_NT, lds, st>>>(g);
+  else if (ch <= 8) decode_qkv_attention_kernel<KV, 8, WT><<<blocks, DQA_NT, lds, st>>>(g);
+  else if (ch <= 12) decode_qkv_attention_kernel<KV, 12, WT><<<blocks, DQA_NT, lds, st>>>(g);
+  else decode_qkv_attention_kernel<KV, DQA_MAX_CH * 4 / DQA_RL, WT><<<blocks, DQA_NT, lds, st>>>(g);
 }
 
 // out null: the fused launch only (its combine is the caller's).
 template <typename KV>
 void launch_dqa(hipStream_t st, const DqaArgs &g, float *out) {
   const unsigned blocks = static_cast<unsigned>(dqa_chunk_ids(g) + 2 * static_cast<int64_t>(g.B) * g.KVH);
-  const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + 8 + g.chunk + 4 * DQA_D + 2) * sizeof(float);
+  const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + DQA_NW + g.chunk + DQA_NW * DQA_D + 2) * sizeof(float);
   if (g.wq) launch_dqa_w<KV, DqaBfp8>(st, g, blocks, lds);
   else launch_dqa_w<KV, DqaBf16>(st, g, blocks, lds);
   if (!out) return;
