@@ -874,21 +874,22 @@ __host__ __device__ __forceinline__ int64_t dqa_chunk_ids(const DqaArgs &g) {
 // Block (DQA_NT threads): 64 rows (from row0, each K weights) times the
 // staged row in LDS xn; thread t takes row t / RL and the 8-weight chunks t %
 // RL, + RL, ... (RL = DQA_RL); the partial sums fold over the row's lanes.
-// wr: the chunks, loaded by dqa_wload.
-template <int CH, typename WT>
+// wr: the chunks, loaded by dqa_wload.  NCH > 0: K / 8 is NCH, known when
+// compiled (no chunk past the row to clamp or skip).
+template <int CH, typename WT, int NCH = 0>
 __device__ __forceinline__ void dqa_wload(const DqaArgs &g, int64_t row0, typename WT::Raw (&wr)[CH]) {
   const int tid = threadIdx.x, r = tid / DQA_RL, kq = tid % DQA_RL;
-  const int64_t nch = g.K / 8;
+  const int64_t nch = NCH > 0 ? NCH : g.K / 8;
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int64_t c = kq + DQA_RL * i;
     wr[i] = WT::load(g, row0 + r, 8 * (c < nch ? c : nch - 1));
   }
 }
-template <int CH, typename WT>
+template <int CH, typename WT, int NCH = 0>
 __device__ __forceinline__ float dqa_dot(const float *xn, int64_t K, const typename WT::Raw (&wr)[CH]) {
   const int kq = threadIdx.x % DQA_RL;
-  const int64_t nch = K / 8;
+  const int64_t nch = NCH > 0 ? NCH : K / 8;
   // Four independent sums (an FMA's latency is not hidden by the SIMD's
   // other wavefront alone), added at the end.
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -990,7 +991,7 @@ __device__ __forceinline__ void combine_new_item(const DqaArgs &g, int64_t bj, f
 // returned).  (Counting the blocks in and letting the last of an item combine -- device
 // fences before and after the count -- costs more than the combine's own
 // launch: batch-1 SmolLM2 decode 0.694 -> 0.938 ms a step.)
-template <typename KV, int CH, typename WT>
+template <typename KV, int CH, typename WT, int NCH>
 __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   constexpr int D = DQA_D, NW = DQA_NW, LPR = D / 4, KPW = 64 / LPR, U = 2, STEP = NW * KPW;
   float *xn = dqa_sm;            // [K]
@@ -999,7 +1000,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   float *red4 = qrot + D;        // [NW]
   float *scores = red4 + NW;     // [chunk]
   float *red = scores + g.chunk; // [NW][D]
-  float *stat = red + NW * D;    // max, sum
+  float *wsum = red + NW * D;    // [NW]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Block order, XCD-aware: workgroup p runs on XCD p % 8, and the G S
   // chunk blocks of kv item i (i = sequence KVH + kv head) take the ids p =
@@ -1013,7 +1014,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   if (bid >= nchunk) {  // the new key or value row of (sequence, kv head)
     const int64_t kb = bid - nchunk, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
     typename WT::Raw wr[CH];
-    dqa_wload<CH, WT>(g, (g.H + which * g.KVH + j) * D, wr);
+    dqa_wload<CH, WT, NCH>(g, (g.H + which * g.KVH + j) * D, wr);
     DqaPre pre;
     dqa_pre_x(g, b, pre);
     int64_t pos = g.pa.pos0;
@@ -1025,7 +1026,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     }
     dqa_pre_rot(g, pos, pre);
     const float rms = dqa_stage(g, pre, xn, red4);
-    const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
+    const float y = dqa_dot<CH, WT, NCH>(xn, g.K, wr) / rms;
     if (tid % DQA_RL == 0) qraw[tid / DQA_RL] = y;
     __syncthreads();
     if (!ok) {
@@ -1068,7 +1069,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   const int64_t b = bj / g.KVH, j = bj % g.KVH, hq = j * g.G + gg;
   // The weights first: they do not wait for a position read on the device.
   typename WT::Raw wr[CH];
-  dqa_wload<CH, WT>(g, hq * D, wr);
+  dqa_wload<CH, WT, NCH>(g, hq * D, wr);
   DqaPre pre;
   dqa_pre_x(g, b, pre);
   const int64_t pos = att_pos0(g.pa, 1);
@@ -1099,7 +1100,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   dqa_pre_rot(g, pos, pre);
   const float rms = dqa_stage(g, pre, xn, red4);
   {
-    const float y = dqa_dot<CH, WT>(xn, g.K, wr) / rms;
+    const float y = dqa_dot<CH, WT, NCH>(xn, g.K, wr) / rms;
     if (tid % DQA_RL == 0) qraw[tid / DQA_RL] = y;
   }
   __syncthreads();
@@ -1108,8 +1109,13 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   if (s == 0 && tid < D) g.q[(b * g.H + hq) * D + tid] = qrot[tid];
 
   // Scores, softmax statistics and P V of the chunk: the key-chunked
-  // kernel's steps for one query head.
+  // kernel's steps for one query head.  Each wavefront keeps the maximum of
+  // its own scores (every lane of a key's LPR lanes holds the key's score),
+  // so the block's maximum is a fold of NW values after the one barrier, and
+  // the P V pass forms exp(score - max) and the sums itself: no pass over
+  // the scores between.
   const float4 qv[1] = {*reinterpret_cast<const float4 *>(qrot + 4 * sl)};
+  float mx = -INFINITY;
   for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
     float4 kv[U];
 #pragma unroll
@@ -1122,29 +1128,22 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
       const int64_t c = c0 + u * STEP;
       float pr[1];
       dots<1, LPR>(qv, kv[u], pr);
-      if (sl == 0 && c < len) scores[c] = pr[0] * g.scale;
+      const float sc = pr[0] * g.scale;
+      if (c < len) {
+        mx = max_nan(mx, sc);
+        if (sl == 0) scores[c] = sc;
+      }
     }
   }
+  mx = fold_max<64>(mx);
+  if (lane == 0) red4[wave] = mx;  // the norm's sums are read before the q barriers
   __syncthreads();
-  if (wave == 0) {
-    float m = -INFINITY;
-    for (int64_t c = lane; c < len; c += 64) m = max_nan(m, scores[c]);
-    m = fold_max<64>(m);
-    m = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
-    float sum = 0.0f;
-    for (int64_t c = lane; c < len; c += 64) {
-      const float e = expf(scores[c] - m);
-      scores[c] = e;
-      sum += e;
-    }
-    sum = fold_sum<64>(sum);
-    if (lane == 0) {
-      stat[0] = m;
-      stat[1] = sum;
-    }
-  }
-  __syncthreads();
+  float m = red4[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = max_nan(m, red4[w]);
+  m = isnan(m) ? m : (m > -FLT_MAX ? m : -FLT_MAX);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.0f;
   for (int64_t c0 = first; c0 < len + kk; c0 += STEP * U) {
     if (c0 != first) {
 #pragma unroll
@@ -1157,7 +1156,8 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + u * STEP;
       if (c < len) {
-        const float pg = scores[c];
+        const float pg = expf(scores[c] - m);
+        if (sl == 0) lsum += pg;
         acc.x += pg * vv[u].x;
         acc.y += pg * vv[u].y;
         acc.z += pg * vv[u].z;
@@ -1169,11 +1169,16 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   acc.y = fold_columns<LPR>(acc.y);
   acc.z = fold_columns<LPR>(acc.z);
   acc.w = fold_columns<LPR>(acc.w);
+  lsum = fold_sum<64>(lsum);
   if (kk == 0) *reinterpret_cast<float4 *>(red + wave * D + 4 * sl) = acc;
+  if (lane == 0) wsum[wave] = lsum;
   __syncthreads();
   if (tid == 0) {
-    pb[gg] = stat[0];
-    pb[g.G + gg] = stat[1];
+    float l = wsum[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) l += wsum[w];
+    pb[gg] = m;
+    pb[g.G + gg] = l;
   }
   if (tid < D) {
     float t = red[tid];
@@ -1184,10 +1189,10 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   return bj;
 }
 
-template <typename KV, int CH, typename WT>
+template <typename KV, int CH, typename WT, int NCH = 0>
 __global__ void __launch_bounds__(DQA_NT) decode_qkv_attention_kernel(DqaArgs g) {
   extern __shared__ float dqa_sm[];
-  dqa_work<KV, CH, WT>(g, dqa_sm);
+  dqa_work<KV, CH, WT, NCH>(g, dqa_sm);
 }
 
 // The combine: one block an item, the launch after the fused one.
@@ -1496,7 +1501,9 @@ namespace {
 template <typename KV, typename WT>
 void launch_dqa_w(hipStream_t st, const DqaArgs &g, unsigned blocks, size_t lds) {
   const int64_t ch = (g.K / 8 + DQA_RL - 1) / DQA_RL;  // chunks a thread
-  if (ch <= 4) decode_qkv_attention_kernel<KV, 4, WT><<<blocks, DQA_NT, lds, st>>>(g);
+  if (g.K == 576)  // SmolLM2's width: 9 chunks a thread exactly
+    decode_qkv_attention_kernel<KV, 9, WT, 576 / 8><<<blocks, DQA_NT, lds, st>>>(g);
+  else if (ch <= 4) decode_qkv_attention_kernel<KV, 4, WT><<<blocks, DQA_NT, lds, st>>>(g);
   else if (ch <= 8) decode_qkv_attention_kernel<KV, 8, WT><<<blocks, DQA_NT, lds, st>>>(g);
   else if (ch <= 12) decode_qkv_attention_kernel<KV, 12, WT><<<blocks, DQA_NT, lds, st>>>(g);
   else decode_qkv_attention_kernel<KV, DQA_MAX_CH * 4 / DQA_RL, WT><<<blocks, DQA_NT, lds, st>>>(g);
@@ -1506,7 +1513,7 @@ void launch_dqa_w(hipStream_t st, const DqaArgs &g, unsigned blocks, size_t lds)
 template <typename KV>
 void launch_dqa(hipStream_t st, const DqaArgs &g, float *out) {
   const unsigned blocks = static_cast<unsigned>(dqa_chunk_ids(g) + 2 * static_cast<int64_t>(g.B) * g.KVH);
-  const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + DQA_NW + g.chunk + DQA_NW * DQA_D + 2) * sizeof(float);
+  const size_t lds = static_cast<size_t>(g.K + 2 * DQA_D + DQA_NW + g.chunk + DQA_NW * DQA_D + DQA_NW) * sizeof(float);
   if (g.wq) launch_dqa_w<KV, DqaBfp8>(st, g, blocks, lds);
   else launch_dqa_w<KV, DqaBf16>(st, g, blocks, lds);
   if (!out) return;
