@@ -597,6 +597,16 @@ int mi_attention_rows_into(mi_ctx *ctx, mi_id q, mi_id k_cache, mi_id v_cache,
  * silu_mul != 0 and w = [gate; up] ([2 I, K]): out = silu(g) * u, [M, I]. */
 int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w,
                    mi_id residual, int silu_mul, mi_id *out);
+/* A greedy decode step's head and pick in one call: logits = rmsnorm(x) w^T
+ * (mi_norm_matvec with no residual, its bits) and ids = mi_argmax_rows of
+ * them ([M, 1] I32, its rule) -- the reference's vocabulary head then the
+ * greedy argmax of its generation loop (crates/tt-models/src/generate.rs:
+ * 176-183), no Engine counterpart.  For one row against a weight of 32 MiB
+ * or more (BF16, k <= 1024: a vocabulary head) the head's launch also folds
+ * each block's logits to a best (value, index), and one block folds those:
+ * no pass over the logits afterwards.  Otherwise the two calls. */
+int mi_norm_matvec_argmax(mi_ctx *ctx, mi_id x, mi_id gamma, float eps,
+                          mi_id w, mi_id *logits, mi_id *ids);
 /* w_qkv = [wq; wk; wv] ([(heads + 2 kv_heads) * d, K]): q = rope(rmsnorm(x)
  * wq^T) returned [M, heads * d]; k = rope(.. wk^T) and v = .. wv^T written
  * into the caches ([M * kv_heads * max_ctx, d], both F32 or both BF16

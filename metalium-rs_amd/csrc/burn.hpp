@@ -515,6 +515,15 @@ inline Tensor norm_matvec(const Tensor &x, const Tensor *gamma, float eps, const
   return Tensor(x.ctx(), id, {x.rows(), n});
 }
 
+// The greedy pick of each row's logits rmsnorm(x) w^T
+// (mi_norm_matvec_argmax): [rows, 1] I32.
+inline Tensor norm_matvec_argmax(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w) {
+  mi_id lg, id;
+  check(x.ctx(), mi_norm_matvec_argmax(x.ctx(), x.use(), gamma.use(), eps, w.use(), &lg, &id), "norm_matvec_argmax");
+  Tensor logits(x.ctx(), lg, {x.rows(), w.rows()});  // freed here
+  return Tensor(x.ctx(), id, {x.rows(), 1});
+}
+
 // The attention rows of one new position per sequence from the hidden rows
 // (mi_norm_qkv_attention): q|k|v, RoPE, the cache write and the attention.
 inline Tensor norm_qkv_attention(const Tensor &x, const Tensor &gamma, float eps, const Tensor &w_qkv,

@@ -146,6 +146,21 @@ __device__ __forceinline__ float sigmoid2(float x) {
   return x >= 0.0f ? r : t * r;
 }
 
+// Argmax's rule (crates/burn-tt/src/ops.rs:2389-2490): the largest value,
+// a NaN above every number, the lowest index among equals -- a total order
+// on (value, index), so partial bests fold in any order.
+struct ArgBest { float v; int32_t i; };
+__device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
+  const bool an = isnan(a.v), bn = isnan(b.v);
+  if (an || bn) {
+    if (an && bn) return a.i <= b.i ? a : b;
+    return an ? a : b;
+  }
+  if (a.v > b.v) return a;
+  if (b.v > a.v) return b;
+  return a.i <= b.i ? a : b;
+}
+
 // Streaming (non-temporal) 16-byte accesses: the line is not kept in the
 // caches.  On an MI355X a stream of them moves ~80% of the 8 TB/s peak
 // against ~70% for ordinary accesses; they suit operands far larger than the

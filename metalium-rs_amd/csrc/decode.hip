@@ -379,6 +379,151 @@ __global__ void __launch_bounds__(256) decode_matvec_kernel(DecodeArgs g) {
   }
 }
 
+// The streamed product of one activation row (the vocabulary head at batch
+// 1): decode_matvec_kernel<1, DM_PLAIN, 2, true>'s arithmetic per pair (so
+// its bits), R pairs a wavefront.  That kernel reads the row and the gain
+// again for every pair, two thirds of what its CUs load, and the loads
+// through each CU's vector cache (64 bytes a clock), not HBM, bound it; here
+// the row, the gain and the norm's sum of squares serve R pairs, whose 4 R
+// weight chunks a lane are all requested first.  K <= 1024, BF16 weights.
+// ARG: also the block's best output by argmax's rule (better), written to
+// (pv, pi)[block] for argmax_partials_kernel -- the greedy pick's first
+// pass over the logits done where they are formed.
+template <int R, bool ARG = false>
+__global__ void __launch_bounds__(256) decode_head_kernel(DecodeArgs g, float *pv = nullptr, int32_t *pi = nullptr) {
+  constexpr int PRE = 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t p0 = ((static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6) * R;
+  if (!ARG && p0 >= g.npairs) return;  // whole wavefronts (with ARG: clamped, to reach the barrier)
+  uint4 pw[R][2][PRE];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t p = p0 + r < g.npairs ? p0 + r : g.npairs - 1;
+    const int64_t r0 = 2 * p, r1 = r0 + 1 < g.N ? r0 + 1 : r0;
+#pragma unroll
+    for (int c = 0; c < PRE; ++c) {
+      const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
+      const int64_t kc = k < g.K ? k : g.K - 8;
+      pw[r][0][c] = ldu4<true>(g.w + r0 * g.K + kc);
+      pw[r][1][c] = ldu4<true>(g.w + r1 * g.K + kc);
+    }
+  }
+  const float *gp = g.gamma ? g.gamma : g.x;  // without a gain: read, never used
+  float4 px[PRE][2], pg[PRE][2];
+#pragma unroll
+  for (int c = 0; c < PRE; ++c) {
+    const int64_t k = static_cast<int64_t>(lane) * 8 + 512 * c;
+    const int64_t kc = k < g.K ? k : g.K - 8;
+    px[c][0] = *reinterpret_cast<const float4 *>(g.x + kc);
+    px[c][1] = *reinterpret_cast<const float4 *>(g.x + kc + 4);
+    pg[c][0] = *reinterpret_cast<const float4 *>(gp + kc);
+    pg[c][1] = *reinterpret_cast<const float4 *>(gp + kc + 4);
+  }
+  float ev[R][2];
+  if (g.resid) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t p = p0 + r < g.npairs ? p0 + r : g.npairs - 1;
+      ev[r][0] = g.resid[2 * p];
+      ev[r][1] = g.resid[2 * p + 1 < g.N ? 2 * p + 1 : 2 * p];
+    }
+  }
+  // The row times the gain, and the norm's sum of squares, as the plain
+  // kernel forms them lane by lane.
+  float xg[PRE][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < PRE; ++c) {
+    const float av[8] = {px[c][0].x, px[c][0].y, px[c][0].z, px[c][0].w,
+                         px[c][1].x, px[c][1].y, px[c][1].z, px[c][1].w};
+    const float gm[8] = {pg[c][0].x, pg[c][0].y, pg[c][0].z, pg[c][0].w,
+                         pg[c][1].x, pg[c][1].y, pg[c][1].z, pg[c][1].w};
+    const bool in = static_cast<int64_t>(lane) * 8 + 512 * c < g.K;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (g.gamma) {
+        if (in) ss = fmaf(av[e], av[e], ss);
+        xg[c][e] = av[e] * gm[e];
+      } else {
+        xg[c][e] = av[e];
+      }
+    }
+  }
+  const float rms = g.gamma ? __fsqrt_rn(fold_sum<64>(ss) / static_cast<float>(g.K) + g.eps) : 1.0f;
+  ArgBest best{-INFINITY, INT32_MAX};
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < PRE; ++c) {
+      if (static_cast<int64_t>(lane) * 8 + 512 * c < g.K) {
+        float w0[8], w1[8];
+        bf16x8(pw[r][0][c], w0);
+        bf16x8(pw[r][1][c], w1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          t0 = fmaf(xg[c][e], w0[e], t0);
+          t1 = fmaf(xg[c][e], w1[e], t1);
+        }
+      }
+    }
+    float y0 = fold_sum<64>(t0), y1 = fold_sum<64>(t1);
+    if (g.gamma) {
+      y0 = y0 / rms;
+      y1 = y1 / rms;
+    }
+    const int64_t p = p0 + r;
+    const float o0 = g.resid ? __fadd_rn(ev[r][0], y0) : y0, o1 = g.resid ? __fadd_rn(ev[r][1], y1) : y1;
+    if (lane == r && p < g.npairs) {
+      g.out[2 * p] = o0;
+      if (2 * p + 1 < g.N) g.out[2 * p + 1] = o1;
+    }
+    if constexpr (ARG) {
+      if (p < g.npairs) best = better(best, ArgBest{o0, static_cast<int32_t>(2 * p)});
+      if (2 * p + 1 < g.N) best = better(best, ArgBest{o1, static_cast<int32_t>(2 * p + 1)});
+    }
+  }
+  if constexpr (ARG) {  // every lane holds the wavefront's best
+    __shared__ float bv[4];
+    __shared__ int32_t bi[4];
+    if (lane == 0) {
+      bv[wave] = best.v;
+      bi[wave] = best.i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      ArgBest b{bv[0], bi[0]};
+      for (int w = 1; w < 4; ++w) b = better(b, ArgBest{bv[w], bi[w]});
+      pv[blockIdx.x] = b.v;
+      pi[blockIdx.x] = b.i;
+    }
+  }
+}
+
+// The greedy pick's last pass: the n partial bests of one row, by argmax's
+// rule, into out[0] (0 when every partial is empty).
+__global__ void __launch_bounds__(256) argmax_partials_kernel(const float *pv, const int32_t *pi, int64_t n,
+                                                              int32_t *out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  ArgBest best{-INFINITY, INT32_MAX};
+  for (int64_t c = threadIdx.x; c < n; c += 256) best = better(best, ArgBest{pv[c], pi[c]});
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) best = better(best, ArgBest{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)});
+  __shared__ float bv[4];
+  __shared__ int32_t bi[4];
+  if (lane == 0) {
+    bv[wave] = best.v;
+    bi[wave] = best.i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgBest b{bv[0], bi[0]};
+    for (int w = 1; w < 4; ++w) b = better(b, ArgBest{bv[w], bi[w]});
+    out[0] = b.i == INT32_MAX ? 0 : b.i;
+  }
+}
+constexpr int HEAD_R = 4;  // pairs a wavefront of decode_head_kernel
+
 // A one-sequence decode step's attention combine and o projection in one
 // launch.  The block's 16 rows of 16 lanes first form the whole attention row
 // into LDS -- row h query head h (ChunkCombine, the combine kernel's code, so
@@ -1068,7 +1213,9 @@ static bool launch_decode(int64_t M, const DecodeArgs &g, hipStream_t st) {
     const unsigned g1 = static_cast<unsigned>(g.npairs);
     switch (M) {
       case 1:
-        if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
+        if (nt && MODE == DM_PLAIN && g.w)
+          decode_head_kernel<HEAD_R><<<static_cast<unsigned>((g.npairs + 4 * HEAD_R - 1) / (4 * HEAD_R)), 256, 0, st>>>(g);
+        else if (nt) decode_matvec_kernel<1, MODE, 2, true><<<grid, 256, 0, st>>>(g);
         else decode_matvec_kernel<1, MODE, 2, false, WT><<<g1, 64, 0, st>>>(g);
         break;
       case 2:
@@ -1212,6 +1359,75 @@ extern "C" int mi_norm_matvec(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_i
     return s;
   }
   *out = id;
+  return MI_OK;
+}
+
+extern "C" int mi_norm_matvec_argmax(mi_ctx *ctx, mi_id x, mi_id gamma, float eps, mi_id w, mi_id *logits,
+                                     mi_id *ids) {
+  MI_ENTER(ctx);
+  if (!logits || !ids) return fail(ctx, MI_E_ARG, "null out pointer");
+  MI_BUF(ctx, xb, x);
+  MI_BUF(ctx, wb, w);
+  const Buffer *gb = nullptr;
+  if (gamma) {
+    gb = lookup(ctx, gamma);
+    if (!gb) return fail(ctx, MI_E_ID, "unknown id %llu", (unsigned long long)gamma);
+  }
+  int s = check_common(ctx, xb, wb, gb, "norm_matvec_argmax");
+  if (s) return s;
+  const int64_t M = xb->rows, K = xb->cols, N = wb->rows;
+  // One row against a streamed BF16 weight: the head kernel with the pick's
+  // first pass, then one block over its partials.  Else the two calls.
+  const bool fused = M == 1 && N >= 1 && wb->elem == MI_BF16 && K <= 1024 && N * K * 2 >= DECODE_STREAM_BYTES &&
+                     N <= INT32_MAX;
+  if (!fused) {
+    mi_id lg = 0, id = 0;
+    s = mi_norm_matvec(ctx, x, gamma, eps, w, 0, 0, &lg);
+    if (s) return s;
+    s = mi_argmax_rows(ctx, lg, &id);
+    if (s) {
+      mi_free(ctx, lg);
+      return s;
+    }
+    *logits = lg;
+    *ids = id;
+    return MI_OK;
+  }
+  const int64_t npairs = (N + 1) / 2, blocks = (npairs + 4 * HEAD_R - 1) / (4 * HEAD_R);
+  char *sc = static_cast<char *>(scratch(ctx, static_cast<size_t>(blocks) * 8));
+  if (!sc) return fail(ctx, MI_E_OOM, "norm_matvec_argmax scratch");
+  mi_id lid, iid;
+  Buffer *lb, *ib;
+  s = new_buffer(ctx, 1, N, MI_F32, &lid, &lb);
+  if (s) return s;
+  s = new_buffer(ctx, 1, 1, MI_I32, &iid, &ib);
+  if (s) {
+    mi_free(ctx, lid);
+    return s;
+  }
+  DecodeArgs g{};
+  g.x = static_cast<const float *>(xb->ptr);
+  g.ldx = K;
+  g.K = K;
+  g.gamma = gb ? static_cast<const float *>(gb->ptr) : nullptr;
+  g.eps = eps;
+  g.w = static_cast<const uint16_t *>(wb->ptr);
+  g.N = N;
+  g.npairs = npairs;
+  g.out = static_cast<float *>(lb->ptr);
+  g.ldo = N;
+  float *pv = reinterpret_cast<float *>(sc);
+  int32_t *pi = reinterpret_cast<int32_t *>(sc + static_cast<size_t>(blocks) * 4);
+  decode_head_kernel<HEAD_R, true><<<static_cast<unsigned>(blocks), 256, 0, ctx->stream>>>(g, pv, pi);
+  argmax_partials_kernel<<<1, 256, 0, ctx->stream>>>(pv, pi, blocks, static_cast<int32_t *>(ib->ptr));
+  s = check_launch(ctx, "norm_matvec_argmax");
+  if (s) {
+    mi_free(ctx, lid);
+    mi_free(ctx, iid);
+    return s;
+  }
+  *logits = lid;
+  *ids = iid;
   return MI_OK;
 }
 

@@ -237,17 +237,6 @@ __global__ void __launch_bounds__(256) select_rows_widen_kernel(const uint16_t *
 }
 
 // --------------------------------------------------------------- argmax
-struct ArgBest { float v; int32_t i; };
-__device__ __forceinline__ ArgBest better(ArgBest a, ArgBest b) {
-  const bool an = isnan(a.v), bn = isnan(b.v);
-  if (an || bn) {
-    if (an && bn) return a.i <= b.i ? a : b;
-    return an ? a : b;
-  }
-  if (a.v > b.v) return a;
-  if (b.v > a.v) return b;
-  return a.i <= b.i ? a : b;
-}
 
 __global__ void __launch_bounds__(256) argmax_rows_kernel(const void *x, int elem, int64_t rows, int64_t cols,
                                                           int32_t *out) {

@@ -389,6 +389,17 @@ Tensor head_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
   return burn::float_matmul(burn::rms_norm(last, m->final_norm, c.eps, act), false, m->embed, true);
 }
 
+// The greedy pick of each sequence's last position: [batch, 1] I32 (the
+// reference's generation loop, crates/tt-models/src/generate.rs:176-183).
+// A decode step's head and pick are one call (mi_norm_matvec_argmax).
+Tensor greedy_last(mi_llama *m, const Tensor &hidden, int64_t batch, int64_t t) {
+  const mi_llama_config &c = m->cfg;
+  const int64_t fused_max = c.numerics == MI_NUMERICS_PERFORMANCE ? kFusedHeadMaxBatch : kDecodeMaxBatch;
+  if (t == 1 && batch <= fused_max && c.hidden % 8 == 0)
+    return burn::norm_matvec_argmax(hidden, m->final_norm, c.eps, m->embed);
+  return burn::argmax_rows(head_last(m, hidden, batch, t));
+}
+
 // Every position's logits: [batch * t, vocab].
 Tensor head_all(mi_llama *m, const Tensor &hidden) {
   const int act = m->cfg.numerics == MI_NUMERICS_PERFORMANCE ? MI_BF16 : MI_F32;
@@ -592,7 +603,7 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
     burn::check(m->ctx, mi_sync(m->ctx), "sync");
     auto t0 = clock::now();
     Tensor h = forward_hidden(m, prompt, batch, t_prompt);
-    Tensor next = burn::argmax_rows(head_last(m, h, batch, t_prompt));
+    Tensor next = greedy_last(m, h, batch, t_prompt);
     std::vector<int32_t> tok = burn::int_into_data(next);  // waits for the prefill
     auto t1 = clock::now();
     for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
@@ -603,7 +614,7 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
     steps.reserve(n_new - 1);
     for (int32_t s = 1; s < n_new; ++s) {
       Tensor hs = forward_ids(m, next.reshape({batch}), batch, 1);
-      next = burn::argmax_rows(head_last(m, hs, batch, 1));
+      next = greedy_last(m, hs, batch, 1);
       steps.push_back(next);
     }
     for (int32_t s = 1; s < n_new; ++s) {
@@ -649,7 +660,7 @@ StepTrace &step_trace(mi_llama *m, int64_t batch, int64_t span) {
   try {
     Tensor x = burn::select_rows_as(m->embed, m->step_ids.reshape({batch}), MI_F32);
     x = decode_layers(m, x.reshape({batch, m->cfg.hidden}), batch, &m->step_pos, 0, span);
-    st.next = burn::argmax_rows(head_last(m, x, batch, 1));
+    st.next = greedy_last(m, x, batch, 1);
     burn::check(ctx, mi_decode_advance(ctx, st.next.use(), m->step_ids.use(), m->step_pos.use(), m->step_log.use()),
                 "decode_advance");
   } catch (...) {
@@ -676,7 +687,7 @@ PromptTrace &prompt_trace(mi_llama *m, int64_t batch, int64_t t) {
   try {
     m->len = 0;
     Tensor h = forward_ids(m, pt.ids, batch, t);
-    pt.next = burn::argmax_rows(head_last(m, h, batch, t));
+    pt.next = greedy_last(m, h, batch, t);
     m->len = 0;  // the capture ran nothing
   } catch (const burn::Error &e) {
     m->len = 0;
@@ -725,7 +736,7 @@ extern "C" int mi_llama_generate_traced(mi_llama *m, const int32_t *prompt, int3
       first = pt.next;
     } else {
       Tensor h = forward_hidden(m, prompt, batch, t_prompt);
-      first = burn::argmax_rows(head_last(m, h, batch, t_prompt));
+      first = greedy_last(m, h, batch, t_prompt);
     }
     m->len = t_prompt;
     // The first ids are the input at position t_prompt: the chain starts one

@@ -122,6 +122,7 @@ def _load() -> ctypes.CDLL:
         "mi_matmul_pairs": [P, U64, U64, I64, ctypes.POINTER(I64), ctypes.POINTER(c_int), ctypes.POINTER(I64),
                             ctypes.POINTER(c_int), I64, I64, I64, c_int, Ip],
         "mi_norm_matvec": [P, U64, U64, c_float, U64, U64, c_int, Ip],
+        "mi_norm_matvec_argmax": [P, U64, U64, c_float, U64, Ip, Ip],
         "mi_norm_qkv_attention": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, I64, I64, U64, U64, c_float,
                                   Ip],
         "mi_norm_qkv_attention_o": [P, U64, U64, c_float, U64, U64, U64, I64, I64, U64, I64, I64, U64, U64,
@@ -376,6 +377,12 @@ class Engine:
     def norm_matvec(self, x: int, gamma: int, eps: float, w: int, residual: int = 0, silu_mul: bool = False) -> int:
         """Fused decode projection: residual + rmsnorm(x) w^T, or silu(g) * u."""
         return self._out(self._lib.mi_norm_matvec, x, gamma, eps, w, residual, int(silu_mul))
+
+    def norm_matvec_argmax(self, x: int, gamma: int, eps: float, w: int) -> Tuple[int, int]:
+        """(logits, ids): rmsnorm(x) w^T and the argmax of each row, in one call."""
+        lg, ids = ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(self._lib.mi_norm_matvec_argmax(self.ctx, x, gamma, eps, w, ctypes.byref(lg), ctypes.byref(ids)))
+        return lg.value, ids.value
 
     def silu_mul_halves(self, gate_up: int, out_elem: int = F32) -> int:
         """silu(gate) * up over the two column halves of a fused gate|up product (F32, or rounded to BF16)."""

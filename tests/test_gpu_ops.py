@@ -1014,6 +1014,56 @@ def test_norm_matvec_residual(engine, M, N, K):
     assert np.abs(got - x @ w.T).max() <= 1e-5 * (np.abs(x) @ np.abs(w).T).max()
 
 
+@pytest.mark.parametrize("N,K", [(30001, 576), (30000, 1024), (29200, 600)])
+def test_norm_matvec_streamed_head(engine, N, K):
+    # A weight of 32 MiB or more is streamed; one row takes the head kernel (4
+    # pairs a wavefront, the row and gain read once for them), two rows the
+    # plain streamed kernel: row 0's products are the same bits either way,
+    # with and without a gain and a residual; odd N leaves a lone last row.
+    eps = 1e-5
+    x, g, wb = decode_inputs(2, K, N)
+    res = rnd(2, N)
+    w = engine.upload_bf16(wb)
+    for gamma, r in ((engine.upload(g), 0), (0, engine.upload(res))):
+        one = engine.download(engine.norm_matvec(engine.upload(x[:1]), gamma, eps, w,
+                                                 engine.upload(res[:1]) if r else 0))
+        two = engine.download(engine.norm_matvec(engine.upload(x), gamma, eps, w, r))
+        same_bits(one[0], two[0])
+    xn = rms_ref(x[:1], g, eps)
+    w64 = orc.from_bf16(wb).astype(np.float64)
+    got = engine.download(engine.norm_matvec(engine.upload(x[:1]), engine.upload(g), eps, w))
+    assert np.abs(got - xn @ w64.T).max() <= 1e-5 * (np.abs(xn) @ np.abs(w64).T).max()
+
+
+@pytest.mark.parametrize("N,K,M", [(30001, 576, 1), (30000, 1024, 1), (30001, 576, 2)])
+def test_norm_matvec_argmax(engine, N, K, M):
+    # The head and the greedy pick in one call: the logits are norm_matvec's
+    # bits and the ids argmax_rows' pick of them -- a planted tie of two equal
+    # largest rows picks the first, NaN rows the first NaN.  One row takes the
+    # fused launch (the head's blocks fold their logits), two the two calls.
+    eps = 1e-5
+    x, g, wb = decode_inputs(M, K, N)
+    xd, gd = engine.upload(x), engine.upload(g)
+    y = rms_ref(x, g, eps) @ orc.from_bf16(wb).astype(np.float64).T
+    top = int(np.argmax(y[0]))
+    tie = wb.copy()
+    tie[[17, N - 2]] = orc.to_bf16(orc.from_bf16(wb[top]) * np.float32(4.0))
+    nan = wb.copy()
+    nan[[20000, 25000]] = 0x7FC0
+    for w, want_id in ((wb, None), (tie, 17), (nan, 20000)):
+        wd = engine.upload_bf16(w)
+        lg, ids = engine.norm_matvec_argmax(xd, gd, eps, wd)
+        ref = engine.norm_matvec(xd, gd, eps, wd)
+        same_bits(engine.download(lg), engine.download(ref))
+        got = engine.download(ids)
+        assert got.shape == (M, 1)
+        assert np.array_equal(got, engine.download(engine.argmax_row(ref)))
+        if want_id is not None:
+            assert got[0, 0] == want_id
+        else:
+            assert got[0, 0] == top
+
+
 @pytest.mark.parametrize("M,K", [(4, 1536), (20, 1536), (9, 576), (20, 576), (32, 576), (32, 64)])
 def test_norm_matvec_silu_mul(engine, M, K):
     # Above 2 rows and up to k 768 with a gain: the matrix-core form.
