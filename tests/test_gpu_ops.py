@@ -1113,9 +1113,9 @@ def test_norm_qkv_rope_writes_cache(engine, M):
     assert np.array_equal(vc1[:, :, keep], vc0.reshape(M, KVH, maxc, D)[:, :, keep])
 
 
-def qkv_attention_case(engine, M, kv16, pos0, maxc, seed=0):
+def qkv_attention_case(engine, M, kv16, pos0, maxc, seed=0, H=9, KVH=3):
     rng = np.random.default_rng(seed)
-    H, KVH, D, K, eps = 9, 3, 64, 576, 1e-5
+    D, K, eps = 64, 576, 1e-5
     x = rng.standard_normal((M, K)).astype(np.float32)
     g = (rng.standard_normal((1, K)) * 0.1 + 1.0).astype(np.float32)
     wb = orc.to_bf16((rng.standard_normal(((H + 2 * KVH) * D, K)) * 0.05).astype(np.float32))
@@ -1244,6 +1244,40 @@ def test_norm_qkv_attention_o(engine, M, kv16, bfp, pos0, span, maxc):
     k3, v3 = c["up"](c["kc0"]), c["up"](c["vc0"])
     same_bits(engine.download(engine.norm_qkv_attention_o(*c["args"], ipos, 0, span, k3, v3, c["scale"], wo)), got)
     same_bits(engine.download(k3), engine.download(k1))
+
+
+@pytest.mark.parametrize("H,KVH", [(16, 4), (8, 1), (4, 4), (6, 2)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_norm_qkv_attention_o_head_shapes(engine, H, KVH, M):
+    # Other head counts and groups (1 to 8 query heads a kv head, 4 to 16
+    # heads): the combine's rows past the last head, the 128-thread combine
+    # above 4 heads a group, o weights of 256 to 1024 columns -- still bit
+    # for bit the two calls, and near float64.
+    pos0, span, maxc = 300, 320, 384
+    c = qkv_attention_case(engine, M, False, pos0, maxc, seed=3, H=H, KVH=KVH)
+    D, K = c["D"], c["K"]
+    rng = np.random.default_rng(11)
+    wo32 = (rng.standard_normal((K, H * D)) * 0.05).astype(np.float32)
+    wo = engine.upload_bf16(orc.to_bf16(wo32))
+    k1, v1 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    got = engine.download(engine.norm_qkv_attention_o(*c["args"], 0, pos0, span, k1, v1, c["scale"], wo))
+    k2, v2 = c["up"](c["kc0"]), c["up"](c["vc0"])
+    o = engine.norm_qkv_attention(*c["args"], 0, pos0, span, k2, v2, c["scale"])
+    same_bits(got, engine.download(engine.norm_matvec(o, 0, 0.0, wo, c["args"][0])))
+    same_bits(engine.download(k1), engine.download(k2))
+    x64 = rms_ref(c["x"], c["g"], c["eps"])
+    w = orc.from_bf16(c["wb"]).astype(np.float64)
+    y = x64 @ w.T
+    qh = y[:, :H * D].reshape(M, H, D)
+    rot = np.concatenate([qh[..., D // 2:], qh[..., :D // 2]], -1)
+    q64 = (qh * c["cos"][pos0] + rot * c["sin"][pos0]).reshape(M, H * D)
+    kc1 = engine.download(k1).reshape(-1, D)
+    vc1 = engine.download(v1).reshape(-1, D)
+    a64 = attention_ref(q64.astype(np.float32), kc1, vc1, M, 1, H, KVH, pos0, c["scale"]).astype(np.float64)
+    wo64 = orc.from_bf16(orc.to_bf16(wo32)).astype(np.float64)
+    ref = c["x"].astype(np.float64) + a64 @ wo64.T
+    bound = (np.abs(a64) @ np.abs(wo64).T).max() + np.abs(c["x"]).max()
+    assert np.abs(got - ref).max() <= 1e-4 * bound
 
 
 def test_norm_qkv_attention_o_refuses(engine):
