@@ -58,7 +58,7 @@ struct AttPos {
 
 __device__ __forceinline__ int64_t att_pos0(const AttPos &pa, int64_t T) {
   if (!pa.dev) return pa.pos0;
-  const int64_t v = *pa.dev;
+  const int64_t v = scalar_read_i32(pa.dev);
   const bool ok = v >= 0 && v + T <= pa.span;
   if (!ok && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0) atomicOr(pa.flags, FLAG_INDEX_RANGE);
   return ok ? v : 0;
@@ -861,6 +861,12 @@ struct DqaBfp8 {
   static __device__ __forceinline__ void f32(const Raw &q, float (&w)[8]) { bfp8x8(q.d, q.e, w); }
 };
 
+// The fused step's device-held position (or, without one, the flags word:
+// read, never used) through the scalar cache (scalar_read_i32), unconditionally.
+__device__ __forceinline__ int32_t dqa_pos_read(const AttPos &pa) {
+  return scalar_read_i32(pa.dev ? pa.dev : reinterpret_cast<const int32_t *>(pa.flags));
+}
+
 // Ids of the fused step's chunk blocks in the XCD-aware order (dqa_work): 8
 // XCDs times ceil(heads / 8) heads' S chunks.  (Measured against the plain
 // order and against all G S blocks of a (sequence, kv head) on one XCD: the
@@ -1013,6 +1019,9 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
 
   if (bid >= nchunk) {  // the new key or value row of (sequence, kv head)
     const int64_t kb = bid - nchunk, which = kb & 1, bj = kb >> 1, b = bj / g.KVH, j = bj % g.KVH;
+    // A device-held position through the scalar cache (dqa_pos_read): its
+    // wait covers it alone, not the weights requested around it.
+    const int32_t pdev = dqa_pos_read(g.pa);
     typename WT::Raw wr[CH];
     dqa_wload<CH, WT, NCH>(g, (g.H + which * g.KVH + j) * D, wr);
     DqaPre pre;
@@ -1020,7 +1029,7 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
     int64_t pos = g.pa.pos0;
     bool ok = true;
     if (g.pa.dev) {
-      pos = *g.pa.dev;
+      pos = pdev;
       ok = pos >= 0 && pos + 1 <= g.pa.span;
       pos = ok ? pos : 0;
     }
@@ -1067,12 +1076,20 @@ __device__ __forceinline__ int64_t dqa_work(const DqaArgs &g, float *dqa_sm) {
   if (bj >= static_cast<int64_t>(g.B) * g.KVH) return 0;  // an empty id of the XCD-aware order
   const int64_t gg = rem / g.S, s = rem - gg * g.S;
   const int64_t b = bj / g.KVH, j = bj % g.KVH, hq = j * g.G + gg;
-  // The weights first: they do not wait for a position read on the device.
+  // A device-held position through the scalar cache (dqa_pos_read: its wait
+  // covers it alone), the weights and the hidden row, which do not wait for it.
+  const int32_t pdev = dqa_pos_read(g.pa);
   typename WT::Raw wr[CH];
   dqa_wload<CH, WT, NCH>(g, hq * D, wr);
   DqaPre pre;
   dqa_pre_x(g, b, pre);
-  const int64_t pos = att_pos0(g.pa, 1);
+  int64_t pos = g.pa.pos0;
+  if (g.pa.dev) {  // att_pos0's check for one new position
+    const int64_t v = pdev;
+    const bool ok = v >= 0 && v + 1 <= g.pa.span;
+    if (!ok && tid == 0 && blockIdx.x == 0) atomicOr(g.pa.flags, FLAG_INDEX_RANGE);
+    pos = ok ? v : 0;
+  }
   const int64_t lo = s * g.chunk, len = pos > lo ? (pos - lo < g.chunk ? pos - lo : g.chunk) : 0;
   float *pb = g.part + (bj * g.S + s) * dqa_part_stride(g.G);
   float *pacc = pb + dqa_part_acc0(g.G) + gg * D;

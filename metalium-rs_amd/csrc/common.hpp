@@ -146,6 +146,14 @@ __device__ __forceinline__ float sigmoid2(float x) {
   return x >= 0.0f ? r : t * r;
 }
 
+// A word written by an earlier launch and only read in this one (a decode
+// step's device-held position), read through the scalar cache: a scalar load
+// completes on its own counter, so what waits for it does not also wait for
+// the vector loads issued around it (those complete in order, and making a
+// vector-loaded value uniform waits for all of them).  p: a uniform address.
+typedef __attribute__((address_space(4))) const int32_t mi_const_i32;
+__device__ __forceinline__ int32_t scalar_read_i32(const int32_t *p) { return *(mi_const_i32 *)p; }
+
 // Argmax's rule (crates/burn-tt/src/ops.rs:2389-2490): the largest value,
 // a NaN above every number, the lowest index among equals -- a total order
 // on (value, index), so partial bests fold in any order.

@@ -181,7 +181,7 @@ __device__ __forceinline__ PairPre pair_pre(const DecodeArgs &g, const PairRows 
     e.v1 = rp[m * g.ldo + (q.has1 ? q.r1 : q.r0)];
   } else if constexpr (MODE == DM_QKV) {
     if (g.pos_dev) {
-      const int64_t v = *g.pos_dev;
+      const int64_t v = scalar_read_i32(g.pos_dev);
       e.ok = v >= 0 && v < g.maxc;
       e.pos = e.ok ? v : 0;
     }

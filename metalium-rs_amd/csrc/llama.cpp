@@ -609,17 +609,22 @@ int mi_llama_generate(mi_llama *m, const int32_t *prompt, int32_t batch, int32_t
     for (int32_t b = 0; b < batch; ++b) out[b * n_new + 0] = tok[b];
     // Each step's tokens stay on the device and feed the next step's
     // embedding gather: no host round trip (and no drained queue) between
-    // steps; the tokens are read back once at the end.
-    std::vector<Tensor> steps;
-    steps.reserve(n_new - 1);
+    // steps.
+    // Each step's tokens go to row s - 1 of one device log, read back with
+    // one wait (reading 127 steps' tokens one buffer at a time cost a host
+    // round trip each: batch-1 decode 0.564 -> 0.540 ms a step without them,
+    // performance contract).
+    Tensor log = n_new > 1 ? burn::fill(m->ctx, {n_new - 1, batch}, MI_I32, 0) : Tensor();
     for (int32_t s = 1; s < n_new; ++s) {
       Tensor hs = forward_ids(m, next.reshape({batch}), batch, 1);
       next = greedy_last(m, hs, batch, 1);
-      steps.push_back(next);
+      burn::check(m->ctx, mi_assign_block(m->ctx, log.use(), next.reshape({1, batch}).use(), s - 1, 0),
+                  "assign_block");
     }
-    for (int32_t s = 1; s < n_new; ++s) {
-      tok = burn::int_into_data(steps[s - 1]);
-      for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[b];
+    if (n_new > 1) {
+      tok = burn::int_into_data(log);
+      for (int32_t s = 1; s < n_new; ++s)
+        for (int32_t b = 0; b < batch; ++b) out[b * n_new + s] = tok[static_cast<size_t>(s - 1) * batch + b];
     }
     auto t2 = clock::now();
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
